@@ -1,0 +1,178 @@
+/*
+ * turboquant_hip.h -- C ABI of the MI355X (gfx950) TurboQuant kernels.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream (hipStream_t passed as void*; NULL = the null stream).  Nothing here
+ * allocates: scratch memory is passed in by the caller as (workspace,
+ * workspace_bytes), sized by the matching *_workspace_bytes() query.  Calls are
+ * asynchronous on `stream`; none synchronizes.  Return value: TQ_OK, or an
+ * error code with a message available from tq_last_error() (thread-local).
+ * Inputs are validated on the host before any launch; an invalid call launches
+ * nothing.
+ *
+ * Layouts follow the reference (turboquant_kv/reference.py:191-224):
+ *   packed row = b bit planes of bpp = ceil(d/8) bytes, plane i = bit i of
+ *   every code, dim j in byte j>>3 of its plane at bit 7-(j&7); pad bits 0.
+ *   QJL sign rows use the same layout with b = 1.
+ *
+ * The reference binds its kernels through torch.ops (csrc/registration.cpp:84-99);
+ * each entry point below names the schema or Python function it replaces.
+ */
+#ifndef TURBOQUANT_HIP_H
+#define TURBOQUANT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQ_OK 0
+#define TQ_EINVAL 1       /* bad argument: shape, bit width, null pointer, size */
+#define TQ_EHIP 2         /* a HIP runtime call failed */
+#define TQ_EUNSUPPORTED 3 /* valid request outside what these kernels cover */
+
+typedef enum tq_dtype { TQ_F32 = 0, TQ_F16 = 1, TQ_BF16 = 2 } tq_dtype;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* tq_last_error(void);
+/* Bumped whenever a signature below changes. */
+int tq_abi_version(void);
+
+/*
+ * Fused normalize -> rotate -> Lloyd-Max quantize -> bit-plane pack.
+ * Replaces schema `rotate_and_quantize(Tensor vectors, Tensor rotation,
+ * Tensor boundaries, int bit_width) -> (Tensor, Tensor)` (csrc/registration.cpp:86-88)
+ * with the arithmetic of quantize_mse (reference.py:263-317):
+ *   n = ||x||, u = x / max(n, 1e-10), y = u R^T, code = #{boundaries < y}.
+ * in_dtype: element type of `vectors`.  round_dtype: the type every
+ * intermediate is rounded to, as reference.py does for low-precision inputs
+ * (TQ_F32 = upcast and compute in fp32, which is what the reference's own
+ * torch op does).  norms are written as fp32 (holding the rounded value).
+ *   vectors [n, d], rotation [d, d] fp32 row-major, boundaries [2^b - 1] fp32,
+ *   packed [n, b*ceil(d/8)] u8, norms [n] fp32.   1 <= b <= 4, 1 <= d <= 256.
+ */
+int tq_rotate_and_quantize(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtype,
+                           int64_t n, int32_t d, const float* rotation,
+                           const float* boundaries, int32_t bit_width,
+                           uint8_t* packed, float* norms, void* stream);
+
+/*
+ * TurboQuant_prod quantize (reference.py:392-469): MSE at b-1 bits on the unit
+ * vector (normalized a second time inside, reference.py:441 -> 294-295), the
+ * residual r = u - c[codes] R, gamma = ||r||, and sign bits of r S^T (>= 0 -> 1).
+ *   boundaries [2^(b-1) - 1], centroids [2^(b-1)] (the b-1 bit codebook),
+ *   qjl [d, d] fp32 (S), mse_packed [n, (b-1)*ceil(d/8)], signs [n, ceil(d/8)],
+ *   res_norms [n] fp32, norms [n] fp32.   2 <= b <= 5.
+ */
+int tq_quantize_prod(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtype,
+                     int64_t n, int32_t d, const float* rotation, const float* boundaries,
+                     const float* centroids, const float* qjl, int32_t bit_width,
+                     uint8_t* mse_packed, uint8_t* signs, float* res_norms, float* norms,
+                     void* stream);
+
+/* Schema `pack_codes(Tensor codes, int bit_width) -> Tensor` (csrc/registration.cpp:98).
+ * codes [n, d] u8 (values < 2^b), packed [n, b*ceil(d/8)].  1 <= b <= 8. */
+int tq_pack_codes(const uint8_t* codes, int64_t n, int32_t d, int32_t bit_width,
+                  uint8_t* packed, void* stream);
+
+/* Schema `unpack_codes(Tensor packed, int bit_width, int dim) -> Tensor`
+ * (csrc/registration.cpp:99).  packed [n, b*ceil(d/8)], codes [n, d]. */
+int tq_unpack_codes(const uint8_t* packed, int64_t n, int32_t d, int32_t bit_width,
+                    uint8_t* codes, void* stream);
+
+/*
+ * dequantize_mse (reference.py:320-367): out = (c[codes] R) * n, computed in
+ * `out_dtype` rounding (the reference computes in norms.dtype).
+ *   packed [n, b*ceil(d/8)], norms [n] fp32 values, centroids [2^b], rotation [d, d],
+ *   out [n, d] of out_dtype.
+ */
+int tq_dequantize_mse(const uint8_t* packed, const float* norms, int64_t n, int32_t d,
+                      int32_t bit_width, const float* centroids, const float* rotation,
+                      tq_dtype out_dtype, void* out, void* stream);
+
+/*
+ * dequantize_prod (reference.py:472-533):
+ *   out = (c[codes] R + sqrt(pi/2)/d * gamma * (s S)) * n,  s = +-1 from the sign bits.
+ *   centroids: the (b-1)-bit codebook.
+ */
+int tq_dequantize_prod(const uint8_t* mse_packed, const uint8_t* signs, const float* res_norms,
+                       const float* norms, int64_t n, int32_t d, int32_t bit_width,
+                       const float* centroids, const float* rotation, const float* qjl,
+                       tq_dtype out_dtype, void* out, void* stream);
+
+/*
+ * Schema `attention_scores_packed(Tensor query, Tensor packed_keys, Tensor key_norms,
+ * Tensor centroids, Tensor rotation, int bit_width) -> Tensor`
+ * (csrc/registration.cpp:89-92; csrc/cpu/quant_cpu.cpp:125-192):
+ *   scores[q, t] = key_norms[t] * sum_j (R query_q)_j * centroids[code_tj]   (no 1/sqrt(d))
+ *   query [nq, d] (nq = batch*heads) of q_dtype, packed_keys [T, b*ceil(d/8)],
+ *   key_norms [T] fp32, scores [nq, T] fp32.  Needs tq_scan_workspace_bytes(nq, d, b, 0).
+ */
+int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                               const uint8_t* packed_keys, const float* key_norms, int64_t T,
+                               const float* centroids, const float* rotation, int32_t bit_width,
+                               float* scores, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/*
+ * Schema `attention_values_packed(Tensor attn_weights, Tensor packed_values,
+ * Tensor value_norms, Tensor centroids, Tensor rotation_T, int bit_width) -> Tensor`
+ * (csrc/registration.cpp:93-96; csrc/cpu/quant_cpu.cpp:199-266):
+ *   out[q] = (sum_t w[q, t] * value_norms[t] * centroids[code_t]) @ rotation_T
+ *   (pass R itself as rotation_T to invert y = x R^T).
+ *   attn_weights [nq, T] fp32, out [nq, d] fp32.
+ *   Needs tq_values_workspace_bytes(nq, d, T).
+ */
+size_t tq_values_workspace_bytes(int64_t nq, int32_t d, int64_t T);
+int tq_attention_values_packed(const float* attn_weights, int64_t nq, int64_t T,
+                               const uint8_t* packed_values, const float* value_norms,
+                               const float* centroids, const float* rotation_T, int32_t d,
+                               int32_t bit_width, float* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/*
+ * Inner-product top-k scan over packed codes: TurboQuantIndex.search / _search_mse
+ * (turboquant_kv/search.py:178-227) and _core.search_packed
+ * (csrc/core/turboquant_core.cpp:407-514):
+ *   score_i = norms[i] * sum_j LUT[j][code_ij],  LUT[j][l] = (R q)_j * centroids[l],
+ *   top k by score descending; equal scores keep the lower index first.
+ *   queries [nq, d] of q_dtype (fp16/bf16 are upcast to fp32 before rotation),
+ *   packed [N, b*ceil(d/8)], norms [N] fp32, out_scores [nq, k] fp32,
+ *   out_ids [nq, k] int64.  k > N pads with (-inf, -1).  2 <= b <= 4, d <= 256, k <= 32.
+ */
+size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N, int32_t k);
+int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                    const uint8_t* packed, const float* norms, int64_t N,
+                    const float* centroids, const float* rotation, int32_t bit_width, int32_t k,
+                    float* out_scores, int64_t* out_ids, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Fused GQA decode attention over a packed KV cache (new op: the semantics of
+ * QuantizedKVCache.attention_scores -> softmax -> attention_values,
+ * turboquant_kv/cache.py:282-339 with turboquant_kv/vllm_plugin/__init__.py:400,
+ * extended to grouped KV heads as HF repeat_kv does: q head h reads kv head
+ * h / (hq / hkv)):
+ *   s_t = scale * kn_t * sum_j (Rk q)_j ck[kcode_tj],  p = softmax_t(s),
+ *   out = (sum_t p_t vn_t cv[vcode_t]) Rv
+ *   q [B, hq, d] of q_dtype; kpacked [B, hkv, t_max, kb*ceil(d/8)], knorms
+ *   [B, hkv, t_max] fp32; vpacked/vnorms likewise with vb; seq_lens [B] int32 on
+ *   the device (tokens 0..seq_lens[b]-1 are attended); out [B, hq, d] of q_dtype.
+ *   d in {64, 128}; kb, vb in 2..4.  Needs tq_decode_workspace_bytes(...).
+ */
+size_t tq_decode_workspace_bytes(int32_t B, int32_t hq, int32_t d, int64_t t_max);
+int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
+                               int32_t hkv, int32_t d, const uint8_t* kpacked,
+                               const float* knorms, const uint8_t* vpacked, const float* vnorms,
+                               int64_t t_max, const int32_t* seq_lens, const float* kcentroids,
+                               const float* vcentroids, const float* krotation,
+                               const float* vrotation, int32_t kbits, int32_t vbits, float scale,
+                               void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOQUANT_HIP_H */

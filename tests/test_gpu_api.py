@@ -1,0 +1,189 @@
+"""GPU tests of the drop-in Python API (quantize_* functions, TurboQuantIndex,
+QuantizedKVCache, torch.ops schemas) against the reference's golden vectors,
+mirroring the reference's own tests (tests/test_reference.py, tests/test_cache.py)."""
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def test_native_library_is_what_runs():
+    from turboquant_kv import _lib
+    _lib.load()
+    maps = open("/proc/self/maps").read()
+    assert os.path.basename(_lib.HIP_LIB) in maps and os.path.basename(_lib.TORCH_LIB) in maps
+
+
+def test_quantize_mse_api_vs_reference(golden):
+    from turboquant_kv import quantize_mse, dequantize_mse
+    from turboquant_kv.reference import make_rotation_matrix, lloyd_max_codebook
+    m = golden("quant_mse")
+    x = m["d128_x"]
+    for b in (2, 3, 4):
+        packed, norms = quantize_mse(T(x), b)  # default rotation seed 42, default codebook
+        codes = O.unpack_codes(packed.cpu().numpy(), b, 128)
+        ref = O.unpack_codes(m[f"d128_b{b}_packed"], b, 128)
+        amb = O.code_margin(x, make_rotation_matrix(128, 42).numpy(), lloyd_max_codebook(b, 128)[0].numpy())
+        assert not ((codes != ref) & ~amb).any()
+        assert norms.dtype == torch.float32
+        rec = dequantize_mse(T(m[f"d128_b{b}_packed"][:64]), T(m[f"d128_b{b}_norms"][:64]), b, 128)
+        assert np.allclose(rec.cpu().numpy(), m[f"d128_b{b}_deq64"], rtol=1e-5, atol=2e-6)
+    # bf16 input keeps bf16 norms, as reference.py does
+    xb = torch.from_numpy(m["bf16_d64_x_u16"].view(np.int16)).to(DEV).view(torch.bfloat16)
+    packed, norms = quantize_mse(xb, 4)
+    assert norms.dtype == torch.bfloat16
+    assert np.array_equal(norms.float().cpu().numpy(), O.bf16_bits_to_f32(m["bf16_d64_b4_norms_u16"]))
+
+
+def test_quantize_prod_api_roundtrip(golden):
+    from turboquant_kv import quantize_prod, dequantize_prod
+    pr = golden("quant_prod")
+    x = pr["d128_x"]
+    mp, sg, rn, nm = quantize_prod(T(x), 4)
+    assert mp.shape == (1024, 48) and sg.shape == (1024, 16)
+    rec = dequantize_prod(T(pr["d128_mse_packed"][:64]), T(pr["d128_signs"][:64]),
+                          T(pr["d128_res_norms"][:64]), T(pr["d128_norms"][:64]), 4, 128)
+    ref = pr["d128_deq64"]
+    assert np.max(np.abs(rec.cpu().numpy() - ref)) <= 2e-5 * np.max(np.abs(ref))
+    with pytest.raises(ValueError):
+        quantize_prod(T(x), 1)
+
+
+def test_torch_ops_reference_schemas(golden):
+    ops = torch.ops.turboquant
+    m, rot = golden("quant_mse"), golden("rotation")
+    R = T(rot["R_d128_s42"])
+    bnd, cen = O.lloyd_max_codebook(4, 128)
+    packed, norms = ops.rotate_and_quantize(T(m["d128_x"]), R, T(bnd), 4)
+    assert packed.shape == (1024, 64) and norms.dtype == torch.float32
+    codes = ops.unpack_codes(packed, 4, 128)
+    assert torch.equal(ops.pack_codes(codes, 4), packed)
+    q = torch.randn(2, 3, 128, device=DEV)
+    s = ops.attention_scores_packed(q, packed, norms, T(cen), R, 4)
+    assert s.shape == (2, 3, 1024)
+    w = torch.softmax(s, -1)
+    o = ops.attention_values_packed(w, packed, norms, T(cen), R, 4)
+    assert o.shape == (2, 3, 128)
+    with pytest.raises(RuntimeError, match="bit_width"):
+        ops.rotate_and_quantize(T(m["d128_x"]), R, T(bnd), 7)
+    with pytest.raises(RuntimeError, match="packed dim mismatch"):
+        ops.unpack_codes(packed, 3, 128)
+
+
+def test_index_vs_reference(golden, tmp_path):
+    from turboquant_kv import TurboQuantIndex
+    ix, m = golden("index"), golden("quant_mse")
+    db = T(m["d128_x"])
+    for b in (2, 3, 4):
+        index = TurboQuantIndex.from_vectors(db, bit_width=b, mode="mse")
+        s, i = index.search(T(ix["queries"]), k=10)
+        assert np.array_equal(i.cpu().numpy(), ix[f"b{b}_ids"]), b
+        assert np.allclose(s.cpu().numpy(), ix[f"b{b}_scores"], rtol=1e-5, atol=1e-6)
+        path = str(tmp_path / f"idx{b}.tq")
+        index.save(path)
+        back = TurboQuantIndex.load(path)
+        assert back.n_vectors == 1024
+        s2, i2 = back.search(T(ix["queries"]), k=10)
+        assert torch.equal(i2, i)
+    # incremental add == one add; k > n clamps to n
+    inc = TurboQuantIndex(128, bit_width=4)
+    for c in range(0, 1024, 300):
+        inc.add(db[c:c + 300])
+    s3, i3 = inc.search(T(ix["queries"]), k=10)
+    assert np.array_equal(i3.cpu().numpy(), ix["b4_ids"])
+    small = TurboQuantIndex.from_vectors(db[:3], bit_width=4)
+    assert small.search(db[0], k=10)[1].shape == (1, 3)
+
+
+def test_index_top1_matches_brute_force():
+    # reference tests/test_reference.py:295-316
+    from turboquant_kv import TurboQuantIndex
+    torch.manual_seed(42)
+    db = torch.randn(500, 64, device=DEV)
+    q = torch.randn(10, 64, device=DEV)
+    exact = (q @ db.t()).argmax(-1)
+    idx = TurboQuantIndex.from_vectors(db, bit_width=4, mode="mse")
+    _, top = idx.search(q, k=1)
+    assert (top.squeeze(-1) == exact).float().mean().item() >= 0.5
+    prod = TurboQuantIndex.from_vectors(db, bit_width=4, mode="prod")
+    _, top = prod.search(q, k=1)
+    assert (top.squeeze(-1) == exact).float().mean().item() >= 0.5
+
+
+def test_cache_vs_reference(golden):
+    from turboquant_kv import QuantizedKVCache, TurboQuantConfig
+    c = golden("cache")
+    cfg = TurboQuantConfig(key_bits=4, value_bits=2, mode="mse")
+    kv = QuantizedKVCache(cfg, 1, 128, 4, 64, device=DEV)
+    kv.append(0, T(c["keys"][:, :100]), T(c["values"][:, :100]))
+    kv.append(0, T(c["keys"][:, 100:]), T(c["values"][:, 100:]))
+    assert kv.seq_lens[0].item() == 128
+    assert np.array_equal(kv._key_packed[0][0].cpu().numpy(), c["key_packed"])
+    assert np.array_equal(kv._val_packed[0][0].cpu().numpy(), c["val_packed"])
+    logits = kv.attention_scores(0, T(c["query"]))
+    assert np.max(np.abs(logits.cpu().numpy() - c["logits"])) <= 1e-5 * np.abs(c["logits"]).max()
+    w = torch.softmax(logits, -1)
+    out = kv.attention_values(0, w)
+    assert np.max(np.abs(out.cpu().numpy() - c["output"])) <= 1e-5 * np.abs(c["output"]).max()
+    fused = kv.decode_attention(0, T(c["query"][:, 0])[None])
+    assert np.max(np.abs(fused[0].cpu().numpy() - c["output"][:, 0])) <= 1e-4 * np.abs(c["output"]).max()
+    assert kv.memory_bytes() == int(c["memory_bytes"])
+
+
+def test_cache_reference_behaviours():
+    # reference tests/test_cache.py
+    from turboquant_kv import QuantizedKVCache, TurboQuantConfig
+    torch.manual_seed(0)
+    cfg = TurboQuantConfig(key_bits=4, value_bits=4, mode="mse")
+    cache = QuantizedKVCache(cfg, 2, 128, 4, 64, device=DEV)
+    keys, values = torch.randn(4, 32, 64, device=DEV), torch.randn(4, 32, 64, device=DEV)
+    cache.append(0, keys, values)
+    q = torch.randn(4, 1, 64, device=DEV)
+    logits = cache.attention_scores(0, q)
+    exact = torch.matmul(q, keys.transpose(-2, -1)) / 8.0
+    for h in range(4):
+        assert torch.corrcoef(torch.stack([logits[h, 0], exact[h, 0]]))[0, 1] > 0.8
+    ratio_cfg = TurboQuantConfig(key_bits=4, value_bits=2)
+    c2 = QuantizedKVCache(ratio_cfg, 1, 100, 1, 128, device=DEV)
+    c2.append(0, torch.randn(1, 50, 128, device=DEV), torch.randn(1, 50, 128, device=DEV))
+    assert 3.0 < c2.compression_ratio < 10.0
+    prot = QuantizedKVCache(TurboQuantConfig(protected_layers=2), 4, 64, 2, 32, device=DEV)
+    k, v = torch.randn(2, 8, 32, device=DEV), torch.randn(2, 8, 32, device=DEV)
+    prot.append(0, k, v)
+    prot.append(2, k, v)
+    qq = torch.randn(2, 1, 32, device=DEV)
+    lp = prot.attention_scores(0, qq)
+    ex = torch.matmul(qq, k.half().float().transpose(-2, -1)) / math.sqrt(32)
+    assert (lp - ex).abs().max().item() < 0.05
+    prodc = QuantizedKVCache(TurboQuantConfig(key_bits=4, value_bits=3, mode="prod"), 1, 64, 2, 64,
+                             device=DEV)
+    prodc.append(0, torch.randn(2, 20, 64, device=DEV), torch.randn(2, 20, 64, device=DEV))
+    w = torch.softmax(prodc.attention_scores(0, torch.randn(2, 1, 64, device=DEV)), -1)
+    assert prodc.attention_values(0, w).shape == (2, 1, 64)
+
+
+def test_cache_gqa_batched_decode_matches_composition():
+    from turboquant_kv import QuantizedKVCache, TurboQuantConfig
+    torch.manual_seed(1)
+    B, Hq, H, d, T_ = 2, 8, 2, 64, 700
+    kv = QuantizedKVCache(TurboQuantConfig(key_bits=4, value_bits=2), 1, 1024, H, d, device=DEV,
+                          batch_size=B)
+    kv.append(0, torch.randn(B, H, 500, d, device=DEV), torch.randn(B, H, 500, d, device=DEV))
+    kv.append(0, torch.randn(B, H, T_ - 500, d, device=DEV), torch.randn(B, H, T_ - 500, d, device=DEV))
+    q = torch.randn(B, Hq, d, device=DEV)
+    fused = kv.decode_attention(0, q)
+    logits = kv.attention_scores(0, q.unsqueeze(2))
+    ref = kv.attention_values(0, torch.softmax(logits, -1)).squeeze(2)
+    assert (fused - ref).abs().max().item() <= 1e-4 * ref.abs().max().item()

@@ -1,0 +1,346 @@
+"""GPU parity tests of the C ABI (include/turboquant_hip.h) against the oracle and the
+reference's golden vectors.  Tolerances are written in each test:
+
+* codes / sign bits / packed bytes / top-k ids: bit-exact, except codes whose fp64
+  distance to a decision point is inside the fp32 band of tq_oracle.code_margin
+  (those are counted and bounded);
+* ADC scores: bit-exact with the oracle's exact-float32 LUT evaluation (same order
+  of operations as the reference's C++ core);
+* float outputs (norms, dequantized vectors, values, attention): relative bounds.
+"""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import capi
+import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+L = capi.lib
+
+
+def T(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return t if dtype is None else t.to(dtype)
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ wrappers
+def k_quantize(x_t, R, bnd, bits, in_dt=capi.TQ_F32, rdt=capi.TQ_F32):
+    n, d = x_t.shape
+    packed = torch.empty(n, bits * ((d + 7) // 8), dtype=torch.uint8, device=DEV)
+    norms = torch.empty(n, dtype=torch.float32, device=DEV)
+    capi.check(L().tq_rotate_and_quantize(capi.p(x_t), in_dt, rdt, capi.i64(n), capi.i32(d),
+                                          capi.p(T(R)), capi.p(T(bnd)), capi.i32(bits),
+                                          capi.p(packed), capi.p(norms), capi.stream()))
+    sync()
+    return packed.cpu().numpy(), norms.cpu().numpy()
+
+
+def k_prod(x, R, bnd, cen, S, bits):
+    n, d = x.shape
+    bpp = (d + 7) // 8
+    mp = torch.empty(n, (bits - 1) * bpp, dtype=torch.uint8, device=DEV)
+    sg = torch.empty(n, bpp, dtype=torch.uint8, device=DEV)
+    rn = torch.empty(n, dtype=torch.float32, device=DEV)
+    nm = torch.empty(n, dtype=torch.float32, device=DEV)
+    capi.check(L().tq_quantize_prod(capi.p(T(x)), capi.TQ_F32, capi.TQ_F32, capi.i64(n), capi.i32(d),
+                                    capi.p(T(R)), capi.p(T(bnd)), capi.p(T(cen)), capi.p(T(S)),
+                                    capi.i32(bits), capi.p(mp), capi.p(sg), capi.p(rn), capi.p(nm),
+                                    capi.stream()))
+    sync()
+    return mp.cpu().numpy(), sg.cpu().numpy(), rn.cpu().numpy(), nm.cpu().numpy()
+
+
+def k_scan(q, packed, norms, cen, R, bits, k, q_dt=capi.TQ_F32):
+    qt = T(q)
+    Q, d = q.shape
+    N = packed.shape[0]
+    os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
+    oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
+    ws_bytes = L().tq_scan_workspace_bytes(Q, d, bits, N, k)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    pk = T(packed) if N else torch.empty(0, bits * ((d + 7) // 8), dtype=torch.uint8, device=DEV)
+    nt = T(norms) if N else torch.empty(0, dtype=torch.float32, device=DEV)
+    capi.check(L().tq_ip_scan_topk(capi.p(qt), q_dt, capi.i64(Q), capi.i32(d), capi.p(pk), capi.p(nt),
+                                   capi.i64(N), capi.p(T(cen)), capi.p(T(R)), capi.i32(bits),
+                                   capi.i32(k), capi.p(os_), capi.p(oi), capi.p(ws),
+                                   ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return os_.cpu().numpy(), oi.cpu().numpy()
+
+
+def k_scores(q, packed, norms, cen, R, bits):
+    Q, d = q.shape
+    N = packed.shape[0]
+    out = torch.empty(Q, N, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, bits, N, 0), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_attention_scores_packed(capi.p(T(q)), capi.TQ_F32, capi.i64(Q), capi.i32(d),
+                                              capi.p(T(packed)), capi.p(T(norms)), capi.i64(N),
+                                              capi.p(T(cen)), capi.p(T(R)), capi.i32(bits),
+                                              capi.p(out), capi.p(ws), ctypes.c_size_t(ws.numel()),
+                                              capi.stream()))
+    sync()
+    return out.cpu().numpy()
+
+
+def k_values(w, packed, norms, cen, M, bits):
+    Q, N = w.shape
+    d = M.shape[0]
+    out = torch.empty(Q, d, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_values_workspace_bytes(Q, d, N), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_attention_values_packed(capi.p(T(w)), capi.i64(Q), capi.i64(N),
+                                              capi.p(T(packed)), capi.p(T(norms)), capi.p(T(cen)),
+                                              capi.p(T(M)), capi.i32(d), capi.i32(bits), capi.p(out),
+                                              capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.cpu().numpy()
+
+
+def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
+    B, Hq, d = q_t.shape
+    Hkv, Tm = kp.shape[1], kp.shape[2]
+    out = torch.empty_like(q_t)
+    ws = torch.empty(max(L().tq_decode_workspace_bytes(B, Hq, d, Tm), 1), dtype=torch.uint8, device=DEV)
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
+    sl = T(np.asarray(seq_lens, np.int32))
+    capi.check(L().tq_decode_attention_packed(
+        capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(T(kp)),
+        capi.p(T(kn)), capi.p(T(vp)), capi.p(T(vn)), capi.i64(Tm), capi.p(sl), capi.p(T(kc)),
+        capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(kb), capi.i32(vb), ctypes.c_float(scale),
+        capi.p(out), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.float().cpu().numpy()
+
+
+CASES = {"d128": (128, (2, 3, 4)), "d200": (200, (3, 4)), "d64": (64, (2, 3, 4))}
+
+
+# ------------------------------------------------------------------ quantize
+def test_quantize_mse_fp32_vs_reference(golden):
+    m, rot = golden("quant_mse"), golden("rotation")
+    for name, (d, bl) in CASES.items():
+        x, R = m[f"{name}_x"], rot[f"R_d{d}_s42"]
+        for b in bl:
+            bnd, _ = O.lloyd_max_codebook(b, d)
+            packed, norms = k_quantize(T(x), R, bnd, b)
+            codes = O.unpack_codes(packed, b, d)
+            ref = O.unpack_codes(m[f"{name}_b{b}_packed"], b, d)
+            amb = O.code_margin(x, R, bnd)
+            bad = (codes != ref) & ~amb
+            print(f"{name} b={b}: {np.sum(codes != ref)} mismatches, all inside the band of {amb.sum()}")
+            assert not bad.any(), (name, b, np.argwhere(bad)[:5])
+            assert np.array_equal(O.pack_codes(codes, b), packed)  # pad bits zero
+            assert np.allclose(norms, m[f"{name}_b{b}_norms"], rtol=5e-7, atol=0)
+
+
+def test_quantize_mse_bf16_vs_reference(golden):
+    m, rot = golden("quant_mse"), golden("rotation")
+    xb = torch.from_numpy(m["bf16_d64_x_u16"].view(np.int16)).to(DEV).view(torch.bfloat16)
+    x = O.bf16_bits_to_f32(m["bf16_d64_x_u16"])
+    R = rot["R_d64_s42"]
+    for b in (2, 3, 4):
+        bnd, _ = O.lloyd_max_codebook(b, 64)
+        packed, norms = k_quantize(xb, R, bnd, b, capi.TQ_BF16, capi.TQ_BF16)
+        codes = O.unpack_codes(packed, b, 64)
+        ref = O.unpack_codes(m[f"bf16_d64_b{b}_packed"], b, 64)
+        amb = O.code_margin(x, R, bnd, "bf16")
+        assert not ((codes != ref) & ~amb).any()
+        assert np.array_equal(norms, O.bf16_bits_to_f32(m[f"bf16_d64_b{b}_norms_u16"]))
+
+
+def test_quantize_zero_tiny_and_empty_rows():
+    d, b = 128, 4
+    R = O.dense_qr_rotation(d, 42)
+    bnd, _ = O.lloyd_max_codebook(b, d)
+    x = np.zeros((3, d), np.float32)
+    x[1] = 1e-12
+    packed, norms = k_quantize(T(x), R, bnd, b)
+    _, n_o, c_o = O.quantize_mse(x, b, R, bnd)
+    assert np.array_equal(O.unpack_codes(packed, b, d), c_o)
+    assert norms[0] == 0.0
+    k_quantize(T(np.zeros((0, d), np.float32)), R, bnd, b)  # no launch, no error
+
+
+def test_quantize_prod_vs_reference(golden):
+    pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
+    for name, d in (("d128", 128), ("d200", 200)):
+        x, R, S = pr[f"{name}_x"], rot[f"R_d{d}_s42"], qj[f"S_d{d}_s42"]
+        bnd, cen = O.lloyd_max_codebook(3, d)
+        mp, sg, rn, nm = k_prod(x, R, bnd, cen, S, 4)
+        _, _, _, _, _, proj64 = O.quantize_prod(x, 4, R, bnd, cen, S)
+        u = x / np.maximum(np.linalg.norm(x.astype(np.float64), axis=1), 1e-10)[:, None]
+        amb = O.code_margin(u.astype(np.float32), R, bnd)
+        codes = O.unpack_codes(mp, 3, d)
+        ref = O.unpack_codes(pr[f"{name}_mse_packed"], 3, d)
+        assert not ((codes != ref) & ~amb).any(), name
+        same_rows = ~(codes != ref).any(axis=1)
+        sign_band = np.abs(proj64) <= 2.0 ** -16 * np.max(np.abs(proj64), axis=1, keepdims=True)
+        s_k = O.unpack_codes(sg, 1, d)
+        s_r = O.unpack_codes(pr[f"{name}_signs"], 1, d)
+        bad = (s_k != s_r) & ~sign_band & same_rows[:, None]
+        print(f"{name}: sign mismatches {np.sum(s_k != s_r)}; outside band {bad.sum()}")
+        assert not bad.any()
+        assert np.allclose(nm, pr[f"{name}_norms"], rtol=5e-7)
+        ok = same_rows
+        assert np.allclose(rn[ok], pr[f"{name}_res_norms"][ok], rtol=2e-5, atol=1e-7)
+
+
+# ------------------------------------------------------------------ pack / unpack
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("d", [1, 7, 64, 100, 128, 200, 256])
+def test_pack_unpack_vs_oracle(bits, d):
+    rs = np.random.RandomState(bits * 31 + d)
+    codes = rs.randint(0, 1 << bits, (333, d)).astype(np.uint8)
+    P = bits * ((d + 7) // 8)
+    packed = torch.empty(333, P, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_pack_codes(capi.p(T(codes)), capi.i64(333), capi.i32(d), capi.i32(bits),
+                                 capi.p(packed), capi.stream()))
+    back = torch.empty(333, d, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_unpack_codes(capi.p(packed), capi.i64(333), capi.i32(d), capi.i32(bits),
+                                   capi.p(back), capi.stream()))
+    sync()
+    assert np.array_equal(packed.cpu().numpy(), O.pack_codes(codes, bits))
+    assert np.array_equal(back.cpu().numpy(), codes)
+
+
+# ------------------------------------------------------------------ dequantize
+def test_dequantize_mse_vs_reference(golden):
+    m, rot = golden("quant_mse"), golden("rotation")
+    for name, (d, bl) in CASES.items():
+        R = rot[f"R_d{d}_s42"]
+        for b in bl:
+            _, cen = O.lloyd_max_codebook(b, d)
+            pk, nm = m[f"{name}_b{b}_packed"][:64], m[f"{name}_b{b}_norms"][:64]
+            out = torch.empty(64, d, dtype=torch.float32, device=DEV)
+            capi.check(L().tq_dequantize_mse(capi.p(T(pk)), capi.p(T(nm)), capi.i64(64), capi.i32(d),
+                                             capi.i32(b), capi.p(T(cen)), capi.p(T(R)), capi.TQ_F32,
+                                             capi.p(out), capi.stream()))
+            sync()
+            assert np.allclose(out.cpu().numpy(), m[f"{name}_b{b}_deq64"], rtol=1e-5, atol=2e-6)
+
+
+def test_dequantize_prod_vs_reference(golden):
+    pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
+    for name, d in (("d128", 128), ("d200", 200)):
+        R, S = rot[f"R_d{d}_s42"], qj[f"S_d{d}_s42"]
+        _, cen = O.lloyd_max_codebook(3, d)
+        args = [pr[f"{name}_{k}"][:64] for k in ("mse_packed", "signs", "res_norms", "norms")]
+        out = torch.empty(64, d, dtype=torch.float32, device=DEV)
+        capi.check(L().tq_dequantize_prod(*[capi.p(T(a)) for a in args], capi.i64(64), capi.i32(d),
+                                          capi.i32(4), capi.p(T(cen)), capi.p(T(R)), capi.p(T(S)),
+                                          capi.TQ_F32, capi.p(out), capi.stream()))
+        sync()
+        ref = pr[f"{name}_deq64"]
+        assert np.max(np.abs(out.cpu().numpy() - ref)) <= 2e-5 * np.max(np.abs(ref))
+
+
+# ------------------------------------------------------------------ scores / values
+def _db(rs, n, d, b, seed=42):
+    R = O.dense_qr_rotation(d, seed)
+    bnd, cen = O.lloyd_max_codebook(b, d)
+    x = rs.randn(n, d).astype(np.float32)
+    p, nm, _ = O.quantize_mse(x, b, R, bnd)
+    return R, cen, p, nm
+
+
+@pytest.mark.parametrize("d", [64, 128, 200])
+@pytest.mark.parametrize("b", [1, 2, 3, 4])
+def test_attention_scores_bit_exact(d, b):
+    rs = np.random.RandomState(d + b)
+    R, cen, p, nm = _db(rs, 1500, d, b)
+    for Q in (1, 3, 6):
+        q = rs.randn(Q, d).astype(np.float32)
+        got = k_scores(q, p, nm, cen, R, b)
+        want = O.lut_scores_f32(q, p, nm, cen, R, b)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (d, b, Q)
+
+
+@pytest.mark.parametrize("d,b", [(64, 2), (128, 4), (200, 3)])
+def test_attention_values_vs_f64(d, b):
+    rs = np.random.RandomState(7 * d + b)
+    R, cen, p, nm = _db(rs, 2500, d, b, seed=43)
+    w = rs.rand(5, 2500).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    got = k_values(w, p, nm, cen, R, b)
+    want = O.values_f64(w, p, nm, cen, R, b)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+# ------------------------------------------------------------------ top-k scan
+def test_scan_vs_reference_index(golden):
+    ix, m, rot = golden("index"), golden("quant_mse"), golden("rotation")
+    R, q = rot["R_d128_s42"], ix["queries"]
+    for b in (2, 3, 4):
+        _, cen = O.lloyd_max_codebook(b, 128)
+        s, i = k_scan(q, ix[f"b{b}_packed"], m[f"d128_b{b}_norms"], cen, R, b, 10)
+        assert np.array_equal(i, ix[f"b{b}_ids"]), b
+        assert np.allclose(s, ix[f"b{b}_scores"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("d", [64, 128, 200])
+@pytest.mark.parametrize("b", [2, 3, 4])
+def test_scan_topk_bit_exact(d, b):
+    rs = np.random.RandomState(3 * d + b)
+    R, cen, p, nm = _db(rs, 20000, d, b)
+    for Q, k in ((1, 10), (4, 1), (7, 32)):
+        q = rs.randn(Q, d).astype(np.float32)
+        s, i = k_scan(q, p, nm, cen, R, b, k)
+        so, io = O.search_topk(q, p, nm, cen, R, b, k)
+        assert np.array_equal(i, io), (d, b, Q, k)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+def test_scan_ties_padding_and_fp16_queries():
+    rs = np.random.RandomState(11)
+    d, b = 128, 4
+    R, cen, p, nm = _db(rs, 40, d, b)
+    p = np.concatenate([p, p[:7], p[:7]])  # duplicated rows tie exactly
+    nm = np.concatenate([nm, nm[:7], nm[:7]])
+    q = rs.randn(3, d).astype(np.float32)
+    s, i = k_scan(q, p, nm, cen, R, b, 30)
+    so, io = O.search_topk(q, p, nm, cen, R, b, 30)
+    assert np.array_equal(i, io)
+    s, i = k_scan(q, p[:5], nm[:5], cen, R, b, 8)  # k > N pads (-inf, -1)
+    assert (i[:, 5:] == -1).all() and np.isneginf(s[:, 5:]).all()
+    q16 = q.astype(np.float16)
+    s, i = k_scan(q16, p, nm, cen, R, b, 10, capi.TQ_F16)
+    so, io = O.search_topk(q16.astype(np.float32), p, nm, cen, R, b, 10)
+    assert np.array_equal(i, io)
+
+
+# ------------------------------------------------------------------ decode attention
+@pytest.mark.parametrize("d,kb,vb", [(64, 4, 2), (128, 3, 4), (64, 2, 3)])
+def test_decode_attention_vs_f64(d, kb, vb):
+    rs = np.random.RandomState(d + 10 * kb + vb)
+    B, Hq, Hkv, Tm = 3, 8, 2, 2600
+    seq = [37, 0, 2600]
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(kb, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    K = rs.randn(B * Hkv * Tm, d).astype(np.float32)
+    K[:, rs.choice(d, 4, replace=False)] *= 20.0
+    V = rs.randn(B * Hkv * Tm, d).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, kb, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kp, vp = kp.reshape(B, Hkv, Tm, -1), vp.reshape(B, Hkv, Tm, -1)
+    kn, vn = kn.reshape(B, Hkv, Tm), vn.reshape(B, Hkv, Tm)
+    q = rs.randn(B, Hq, d).astype(np.float32)
+    scale = 1.0 / math.sqrt(d)
+    want = O.decode_attention_f64(q, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
+    got = k_decode(T(q), kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
+    assert np.all(got[1] == 0)  # empty sequence -> zeros
+    assert np.max(np.abs(got - want)) <= 1e-3 * np.max(np.abs(want))
+    qb = torch.from_numpy(q).to(DEV).to(torch.bfloat16)
+    want_b = O.decode_attention_f64(qb.float().cpu().numpy(), kp, kn, vp, vn, seq, ck, cv, Rk, Rv,
+                                    kb, vb, scale)
+    got_b = k_decode(qb, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
+    assert np.max(np.abs(got_b - want_b)) <= 1e-2 * np.max(np.abs(want_b))

@@ -1,0 +1,430 @@
+// torch_ops.cpp -- registers the `turboquant` operator namespace with the PyTorch
+// dispatcher and forwards every op to the C ABI in include/turboquant_hip.h.
+//
+// It takes the place of csrc/registration.cpp: the five reference schemas
+// (registration.cpp:84-99) are kept verbatim, and the fused ops the reference's
+// signatures cannot express are added.  Ops are registered for the CUDA dispatch
+// key, which is where PyTorch-ROCm files HIP tensors.  There is no CPU
+// implementation and no fallback: a CPU tensor raises.
+//
+// Conventions (registration.cpp, quant_cpu.cpp, rotate_fused.cu): inputs are made
+// contiguous (and upcast to fp32 where the reference op does), outputs are freshly
+// allocated on the input's device, kernels run asynchronously on the current
+// stream under a device guard, errors raise RuntimeError with the kernel's message.
+
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include <cmath>
+
+#include "../../include/turboquant_hip.h"
+
+namespace {
+
+void check_rc(int rc) { TORCH_CHECK(rc == TQ_OK, "turboquant: ", tq_last_error()); }
+
+void* cur_stream(const at::Tensor& t) {
+  return reinterpret_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+tq_dtype to_tq(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat: return TQ_F32;
+    case at::kHalf: return TQ_F16;
+    case at::kBFloat16: return TQ_BF16;
+    default: TORCH_CHECK(false, "turboquant: unsupported dtype ", t);
+  }
+  return TQ_F32;
+}
+
+at::ScalarType from_tq(tq_dtype t) {
+  return t == TQ_F32 ? at::kFloat : t == TQ_F16 ? at::kHalf : at::kBFloat16;
+}
+
+void require_gpu(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), "turboquant: ", name,
+              " must be on a HIP device (this build has no CPU kernels)");
+}
+
+at::Tensor f32c(const at::Tensor& t, const at::Device& dev) {
+  return t.to(dev, at::kFloat).contiguous();
+}
+
+// Input of a supported float dtype, contiguous, on `dev`.
+at::Tensor floatc(const at::Tensor& t, const at::Device& dev) {
+  auto st = t.scalar_type();
+  if (st != at::kFloat && st != at::kHalf && st != at::kBFloat16) return t.to(dev, at::kFloat).contiguous();
+  return t.to(dev).contiguous();
+}
+
+at::Tensor workspace(size_t bytes, const at::Device& dev) {
+  return at::empty({(int64_t)(bytes > 0 ? bytes : 1)}, at::TensorOptions().dtype(at::kByte).device(dev));
+}
+
+int64_t packed_width(int64_t bits, int64_t d) { return bits * ((d + 7) / 8); }
+
+// ------------------------------------------------------------ reference schemas
+
+std::tuple<at::Tensor, at::Tensor> rotate_and_quantize(const at::Tensor& vectors,
+                                                       const at::Tensor& rotation,
+                                                       const at::Tensor& boundaries,
+                                                       int64_t bit_width) {
+  require_gpu(vectors, "vectors");
+  TORCH_CHECK(vectors.dim() == 2, "vectors must be [N, d]");
+  c10::DeviceGuard g(vectors.device());
+  const auto dev = vectors.device();
+  auto x = f32c(vectors, dev);  // the reference op upcasts (rotate_fused.cu:148)
+  auto R = f32c(rotation, dev);
+  auto bnd = f32c(boundaries, dev);
+  const int64_t n = x.size(0), d = x.size(1);
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "Rotation matrix must be [d, d]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4");
+  TORCH_CHECK(bnd.numel() == (1 << bit_width) - 1, "boundaries length must be 2^bit_width - 1");
+  auto packed = at::zeros({n, packed_width(bit_width, d)}, x.options().dtype(at::kByte));
+  auto norms = at::empty({n}, x.options());
+  check_rc(tq_rotate_and_quantize(x.data_ptr(), TQ_F32, TQ_F32, n, (int32_t)d, R.data_ptr<float>(),
+                                  bnd.data_ptr<float>(), (int32_t)bit_width,
+                                  packed.data_ptr<uint8_t>(), norms.data_ptr<float>(),
+                                  cur_stream(x)));
+  return {packed, norms};
+}
+
+at::Tensor attention_scores_packed(const at::Tensor& query, const at::Tensor& packed_keys,
+                                   const at::Tensor& key_norms, const at::Tensor& centroids,
+                                   const at::Tensor& rotation, int64_t bit_width) {
+  require_gpu(query, "query");
+  TORCH_CHECK(query.dim() == 3, "query must be [batch, heads, head_dim]");
+  TORCH_CHECK(packed_keys.dim() == 2, "packed_keys must be [seq_len, packed_dim]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4");
+  c10::DeviceGuard g(query.device());
+  const auto dev = query.device();
+  auto q = f32c(query, dev);
+  auto pk = packed_keys.to(dev).contiguous();
+  auto kn = f32c(key_norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t B = q.size(0), H = q.size(1), d = q.size(2), T = pk.size(0);
+  TORCH_CHECK(pk.scalar_type() == at::kByte, "packed_keys must be uint8");
+  TORCH_CHECK(pk.size(1) == packed_width(bit_width, d), "packed dim mismatch: expected ",
+              packed_width(bit_width, d), " got ", pk.size(1));
+  TORCH_CHECK(kn.numel() == T, "key_norms must have seq_len entries");
+  TORCH_CHECK(cen.numel() == (1 << bit_width), "centroids length must be 2^bit_width");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto scores = at::empty({B, H, T}, q.options());
+  if (B * H == 0 || T == 0) return scores;
+  auto ws = workspace(tq_scan_workspace_bytes(B * H, (int32_t)d, (int32_t)bit_width, T, 0), dev);
+  check_rc(tq_attention_scores_packed(q.data_ptr(), TQ_F32, B * H, (int32_t)d, pk.data_ptr<uint8_t>(),
+                                      kn.data_ptr<float>(), T, cen.data_ptr<float>(),
+                                      R.data_ptr<float>(), (int32_t)bit_width,
+                                      scores.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                                      cur_stream(q)));
+  return scores;
+}
+
+at::Tensor attention_values_packed(const at::Tensor& attn_weights, const at::Tensor& packed_values,
+                                   const at::Tensor& value_norms, const at::Tensor& centroids,
+                                   const at::Tensor& rotation_T, int64_t bit_width) {
+  require_gpu(attn_weights, "attn_weights");
+  TORCH_CHECK(attn_weights.dim() == 3, "attn_weights must be [batch, heads, seq_len]");
+  TORCH_CHECK(packed_values.dim() == 2, "packed_values must be [seq_len, packed_dim]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4");
+  c10::DeviceGuard g(attn_weights.device());
+  const auto dev = attn_weights.device();
+  auto w = f32c(attn_weights, dev);
+  auto pv = packed_values.to(dev).contiguous();
+  auto vn = f32c(value_norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto RT = f32c(rotation_T, dev);
+  const int64_t B = w.size(0), H = w.size(1), T = w.size(2), d = RT.size(0);
+  TORCH_CHECK(RT.dim() == 2 && RT.size(1) == d, "rotation_T must be [d, d]");
+  TORCH_CHECK(pv.scalar_type() == at::kByte, "packed_values must be uint8");
+  TORCH_CHECK(pv.size(0) == T, "packed_values must have seq_len rows");
+  TORCH_CHECK(pv.size(1) == packed_width(bit_width, d), "packed dim mismatch: expected ",
+              packed_width(bit_width, d), " got ", pv.size(1));
+  TORCH_CHECK(vn.numel() == T, "value_norms must have seq_len entries");
+  TORCH_CHECK(cen.numel() == (1 << bit_width), "centroids length must be 2^bit_width");
+  auto out = at::empty({B, H, d}, w.options());
+  if (B * H == 0) return out;
+  auto ws = workspace(tq_values_workspace_bytes(B * H, (int32_t)d, T), dev);
+  check_rc(tq_attention_values_packed(w.data_ptr<float>(), B * H, T, pv.data_ptr<uint8_t>(),
+                                      vn.data_ptr<float>(), cen.data_ptr<float>(),
+                                      RT.data_ptr<float>(), (int32_t)d, (int32_t)bit_width,
+                                      out.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                                      cur_stream(w)));
+  return out;
+}
+
+at::Tensor pack_codes(const at::Tensor& codes, int64_t bit_width) {
+  require_gpu(codes, "codes");
+  TORCH_CHECK(codes.scalar_type() == at::kByte, "codes must be uint8");
+  TORCH_CHECK(codes.dim() == 2, "codes must be 2D [N, d]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 8, "bit_width must be 1-8");
+  c10::DeviceGuard g(codes.device());
+  auto c = codes.contiguous();
+  const int64_t n = c.size(0), d = c.size(1);
+  auto packed = at::empty({n, packed_width(bit_width, d)}, c.options());
+  if (d == 0) return packed;
+  check_rc(tq_pack_codes(c.data_ptr<uint8_t>(), n, (int32_t)d, (int32_t)bit_width,
+                         packed.data_ptr<uint8_t>(), cur_stream(c)));
+  return packed;
+}
+
+at::Tensor unpack_codes(const at::Tensor& packed, int64_t bit_width, int64_t dim) {
+  require_gpu(packed, "packed");
+  TORCH_CHECK(packed.scalar_type() == at::kByte, "packed must be uint8");
+  TORCH_CHECK(packed.dim() == 2, "packed must be 2D");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 8, "bit_width must be 1-8");
+  TORCH_CHECK(dim >= 1, "dim must be >= 1");
+  c10::DeviceGuard g(packed.device());
+  auto p = packed.contiguous();
+  TORCH_CHECK(p.size(1) == packed_width(bit_width, dim), "packed dim mismatch: expected ",
+              packed_width(bit_width, dim), " got ", p.size(1));
+  auto codes = at::empty({p.size(0), dim}, p.options());
+  check_rc(tq_unpack_codes(p.data_ptr<uint8_t>(), p.size(0), (int32_t)dim, (int32_t)bit_width,
+                           codes.data_ptr<uint8_t>(), cur_stream(p)));
+  return codes;
+}
+
+// ------------------------------------------------------------ fused ops (new)
+
+// quantize_mse with the reference's rounding points: intermediates in vectors.dtype,
+// norms returned in vectors.dtype (reference.py:263-317).
+std::tuple<at::Tensor, at::Tensor> quantize_mse_packed(const at::Tensor& vectors,
+                                                       const at::Tensor& rotation,
+                                                       const at::Tensor& boundaries,
+                                                       int64_t bit_width) {
+  require_gpu(vectors, "vectors");
+  TORCH_CHECK(vectors.dim() == 2, "vectors must be [N, d]");
+  c10::DeviceGuard g(vectors.device());
+  const auto dev = vectors.device();
+  auto x = floatc(vectors, dev);
+  const tq_dtype dt = to_tq(x.scalar_type());
+  auto R = f32c(rotation, dev);
+  auto bnd = f32c(boundaries, dev);
+  const int64_t n = x.size(0), d = x.size(1);
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4");
+  TORCH_CHECK(bnd.numel() == (1 << bit_width) - 1, "boundaries length must be 2^bit_width - 1");
+  auto packed = at::empty({n, packed_width(bit_width, d)}, x.options().dtype(at::kByte));
+  auto norms = at::empty({n}, x.options().dtype(at::kFloat));
+  check_rc(tq_rotate_and_quantize(x.data_ptr(), dt, dt, n, (int32_t)d, R.data_ptr<float>(),
+                                  bnd.data_ptr<float>(), (int32_t)bit_width,
+                                  packed.data_ptr<uint8_t>(), norms.data_ptr<float>(),
+                                  cur_stream(x)));
+  return {packed, norms.to(x.scalar_type())};
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> quantize_prod_packed(
+    const at::Tensor& vectors, const at::Tensor& rotation, const at::Tensor& boundaries,
+    const at::Tensor& centroids, const at::Tensor& qjl, int64_t bit_width) {
+  require_gpu(vectors, "vectors");
+  TORCH_CHECK(vectors.dim() == 2, "vectors must be [N, d]");
+  TORCH_CHECK(bit_width >= 2, "Prod mode requires bits >= 2, got ", bit_width);
+  TORCH_CHECK(bit_width <= 5, "Prod mode supports bits <= 5");
+  c10::DeviceGuard g(vectors.device());
+  const auto dev = vectors.device();
+  auto x = floatc(vectors, dev);
+  const tq_dtype dt = to_tq(x.scalar_type());
+  auto R = f32c(rotation, dev);
+  auto bnd = f32c(boundaries, dev);
+  auto cen = f32c(centroids, dev);
+  auto S = f32c(qjl, dev);
+  const int64_t n = x.size(0), d = x.size(1);
+  const int64_t mb = bit_width - 1;
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  TORCH_CHECK(S.dim() == 2 && S.size(0) == d && S.size(1) == d, "S_matrix must be [d, d]");
+  TORCH_CHECK(bnd.numel() == (1 << mb) - 1, "boundaries length must be 2^(bits-1) - 1");
+  TORCH_CHECK(cen.numel() == (1 << mb), "centroids length must be 2^(bits-1)");
+  auto ob = x.options().dtype(at::kByte);
+  auto of = x.options().dtype(at::kFloat);
+  auto mp = at::empty({n, packed_width(mb, d)}, ob);
+  auto sg = at::empty({n, (d + 7) / 8}, ob);
+  auto rn = at::empty({n}, of);
+  auto nm = at::empty({n}, of);
+  check_rc(tq_quantize_prod(x.data_ptr(), dt, dt, n, (int32_t)d, R.data_ptr<float>(),
+                            bnd.data_ptr<float>(), cen.data_ptr<float>(), S.data_ptr<float>(),
+                            (int32_t)bit_width, mp.data_ptr<uint8_t>(), sg.data_ptr<uint8_t>(),
+                            rn.data_ptr<float>(), nm.data_ptr<float>(), cur_stream(x)));
+  return {mp, sg, rn.to(x.scalar_type()), nm.to(x.scalar_type())};
+}
+
+at::Tensor dequantize_mse_packed(const at::Tensor& packed, const at::Tensor& norms,
+                                 const at::Tensor& centroids, const at::Tensor& rotation,
+                                 int64_t bit_width, int64_t dim) {
+  require_gpu(packed, "packed_codes");
+  TORCH_CHECK(packed.scalar_type() == at::kByte && packed.dim() == 2, "packed must be uint8 [N, P]");
+  TORCH_CHECK(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4");
+  c10::DeviceGuard g(packed.device());
+  const auto dev = packed.device();
+  auto p = packed.contiguous();
+  const int64_t n = p.size(0);
+  TORCH_CHECK(p.size(1) == packed_width(bit_width, dim), "packed dim mismatch");
+  auto nf = norms.to(dev).contiguous();
+  const tq_dtype odt = to_tq(nf.scalar_type());
+  auto n32 = nf.to(at::kFloat).contiguous();
+  TORCH_CHECK(n32.numel() == n, "norms must have N entries");
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  TORCH_CHECK(cen.numel() == (1 << bit_width), "centroids length must be 2^bit_width");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == dim && R.size(1) == dim, "rotation must be [d, d]");
+  auto out = at::empty({n, dim}, p.options().dtype(from_tq(odt)));
+  check_rc(tq_dequantize_mse(p.data_ptr<uint8_t>(), n32.data_ptr<float>(), n, (int32_t)dim,
+                             (int32_t)bit_width, cen.data_ptr<float>(), R.data_ptr<float>(), odt,
+                             out.data_ptr(), cur_stream(p)));
+  return out;
+}
+
+at::Tensor dequantize_prod_packed(const at::Tensor& mse_packed, const at::Tensor& signs,
+                                  const at::Tensor& res_norms, const at::Tensor& norms,
+                                  const at::Tensor& centroids, const at::Tensor& rotation,
+                                  const at::Tensor& qjl, int64_t bit_width, int64_t dim) {
+  require_gpu(mse_packed, "mse_packed");
+  TORCH_CHECK(bit_width >= 2 && bit_width <= 5, "Prod mode requires bits in [2, 5]");
+  c10::DeviceGuard g(mse_packed.device());
+  const auto dev = mse_packed.device();
+  auto mp = mse_packed.contiguous();
+  auto sg = signs.to(dev).contiguous();
+  const int64_t n = mp.size(0);
+  TORCH_CHECK(norms.scalar_type() == at::kFloat,
+              "dequantize_prod computes in float32 (the reference's signs @ S needs fp32 S)");
+  TORCH_CHECK(mp.size(1) == packed_width(bit_width - 1, dim), "packed dim mismatch");
+  TORCH_CHECK(sg.scalar_type() == at::kByte && sg.size(0) == n && sg.size(1) == (dim + 7) / 8,
+              "signs must be uint8 [N, ceil(d/8)]");
+  auto rn = f32c(res_norms, dev);
+  auto nm = f32c(norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  auto S = f32c(qjl, dev);
+  TORCH_CHECK(rn.numel() == n && nm.numel() == n, "norms must have N entries");
+  TORCH_CHECK(cen.numel() == (1 << (bit_width - 1)), "centroids length must be 2^(bits-1)");
+  auto out = at::empty({n, dim}, mp.options().dtype(at::kFloat));
+  check_rc(tq_dequantize_prod(mp.data_ptr<uint8_t>(), sg.data_ptr<uint8_t>(), rn.data_ptr<float>(),
+                              nm.data_ptr<float>(), n, (int32_t)dim, (int32_t)bit_width,
+                              cen.data_ptr<float>(), R.data_ptr<float>(), S.data_ptr<float>(),
+                              TQ_F32, out.data_ptr(), cur_stream(mp)));
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk(const at::Tensor& queries, const at::Tensor& packed,
+                                                const at::Tensor& norms, const at::Tensor& centroids,
+                                                const at::Tensor& rotation, int64_t bit_width,
+                                                int64_t k) {
+  require_gpu(queries, "queries");
+  TORCH_CHECK(queries.dim() == 2, "queries must be [Q, d]");
+  TORCH_CHECK(packed.dim() == 2 && packed.scalar_type() == at::kByte, "packed must be uint8 [N, P]");
+  c10::DeviceGuard g(queries.device());
+  const auto dev = queries.device();
+  auto q = floatc(queries, dev);
+  auto p = packed.to(dev).contiguous();
+  auto nm = f32c(norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t Q = q.size(0), d = q.size(1), N = p.size(0);
+  TORCH_CHECK(p.size(1) == packed_width(bit_width, d), "packed dim mismatch");
+  TORCH_CHECK(nm.numel() == N, "norms must have N entries");
+  TORCH_CHECK(cen.numel() == (1 << bit_width), "centroids length must be 2^bit_width");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
+  auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
+  if (Q == 0) return {os, oi};
+  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
+  check_rc(tq_ip_scan_topk(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d, p.data_ptr<uint8_t>(),
+                           nm.data_ptr<float>(), N, cen.data_ptr<float>(), R.data_ptr<float>(),
+                           (int32_t)bit_width, (int32_t)k, os.data_ptr<float>(),
+                           oi.data_ptr<int64_t>(), ws.data_ptr(), ws.numel(), cur_stream(q)));
+  return {os, oi};
+}
+
+at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacked,
+                                   const at::Tensor& knorms, const at::Tensor& vpacked,
+                                   const at::Tensor& vnorms, const at::Tensor& seq_lens,
+                                   const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+                                   const at::Tensor& krotation, const at::Tensor& vrotation,
+                                   int64_t kbits, int64_t vbits, double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
+  TORCH_CHECK(kpacked.dim() == 4 && vpacked.dim() == 4, "packed K/V must be [B, Hkv, T, P]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  const int64_t B = qq.size(0), Hq = qq.size(1), d = qq.size(2);
+  const int64_t Hkv = kpacked.size(1), Tm = kpacked.size(2);
+  TORCH_CHECK(kpacked.scalar_type() == at::kByte && vpacked.scalar_type() == at::kByte,
+              "packed K/V must be uint8");
+  TORCH_CHECK(kpacked.is_contiguous() && vpacked.is_contiguous() && knorms.is_contiguous() &&
+                  vnorms.is_contiguous(),
+              "packed K/V and norms must be contiguous");
+  TORCH_CHECK(kpacked.device() == dev && vpacked.device() == dev && knorms.device() == dev &&
+                  vnorms.device() == dev,
+              "K/V must be on the query's device");
+  TORCH_CHECK(kpacked.size(0) == B && vpacked.size(0) == B && vpacked.size(1) == Hkv &&
+                  vpacked.size(2) == Tm,
+              "K/V batch/head/length mismatch");
+  TORCH_CHECK(kpacked.size(3) == packed_width(kbits, d), "packed key width mismatch");
+  TORCH_CHECK(vpacked.size(3) == packed_width(vbits, d), "packed value width mismatch");
+  TORCH_CHECK(knorms.scalar_type() == at::kFloat && vnorms.scalar_type() == at::kFloat,
+              "norms must be float32");
+  TORCH_CHECK(knorms.numel() == B * Hkv * Tm && vnorms.numel() == B * Hkv * Tm, "norms shape");
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "num_heads must be a multiple of num_kv_heads");
+  auto sl = seq_lens.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  auto kc = f32c(kcentroids, dev);
+  auto vc = f32c(vcentroids, dev);
+  auto Rk = f32c(krotation, dev);
+  auto Rv = f32c(vrotation, dev);
+  TORCH_CHECK(kc.numel() == (1 << kbits) && vc.numel() == (1 << vbits), "centroid lengths");
+  auto out = at::empty({B, Hq, d}, qq.options());
+  if (B == 0) return out;
+  auto ws = workspace(tq_decode_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)d, Tm), dev);
+  check_rc(tq_decode_attention_packed(
+      qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
+      kpacked.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vpacked.data_ptr<uint8_t>(),
+      vnorms.data_ptr<float>(), Tm, sl.data_ptr<int32_t>(), kc.data_ptr<float>(),
+      vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), (int32_t)kbits,
+      (int32_t)vbits, (float)scale, out.data_ptr(), ws.data_ptr(), ws.numel(), cur_stream(qq)));
+  return out;
+}
+
+}  // namespace
+
+TORCH_LIBRARY(turboquant, m) {
+  // The reference's schemas (csrc/registration.cpp:84-99), verbatim.
+  m.def("rotate_and_quantize(Tensor vectors, Tensor rotation, Tensor boundaries, int bit_width)"
+        " -> (Tensor, Tensor)");
+  m.def("attention_scores_packed(Tensor query, Tensor packed_keys, Tensor key_norms,"
+        " Tensor centroids, Tensor rotation, int bit_width) -> Tensor");
+  m.def("attention_values_packed(Tensor attn_weights, Tensor packed_values, Tensor value_norms,"
+        " Tensor centroids, Tensor rotation_T, int bit_width) -> Tensor");
+  m.def("pack_codes(Tensor codes, int bit_width) -> Tensor");
+  m.def("unpack_codes(Tensor packed, int bit_width, int dim) -> Tensor");
+  // Fused ops the reference's signatures cannot express.
+  m.def("quantize_mse_packed(Tensor vectors, Tensor rotation, Tensor boundaries, int bit_width)"
+        " -> (Tensor, Tensor)");
+  m.def("quantize_prod_packed(Tensor vectors, Tensor rotation, Tensor boundaries,"
+        " Tensor centroids, Tensor qjl, int bit_width) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("dequantize_mse_packed(Tensor packed, Tensor norms, Tensor centroids, Tensor rotation,"
+        " int bit_width, int dim) -> Tensor");
+  m.def("dequantize_prod_packed(Tensor mse_packed, Tensor signs, Tensor res_norms, Tensor norms,"
+        " Tensor centroids, Tensor rotation, Tensor qjl, int bit_width, int dim) -> Tensor");
+  m.def("ip_scan_topk(Tensor queries, Tensor packed, Tensor norms, Tensor centroids,"
+        " Tensor rotation, int bit_width, int k) -> (Tensor, Tensor)");
+  m.def("decode_attention_packed(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
+        " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
+        " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
+  m.impl("rotate_and_quantize", &rotate_and_quantize);
+  m.impl("attention_scores_packed", &attention_scores_packed);
+  m.impl("attention_values_packed", &attention_values_packed);
+  m.impl("pack_codes", &pack_codes);
+  m.impl("unpack_codes", &unpack_codes);
+  m.impl("quantize_mse_packed", &quantize_mse_packed);
+  m.impl("quantize_prod_packed", &quantize_prod_packed);
+  m.impl("dequantize_mse_packed", &dequantize_mse_packed);
+  m.impl("dequantize_prod_packed", &dequantize_prod_packed);
+  m.impl("ip_scan_topk", &ip_scan_topk);
+  m.impl("decode_attention_packed", &decode_attention_packed);
+}

@@ -1,0 +1,118 @@
+// tq_common.h -- shared host/device helpers for the gfx950 TurboQuant kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/turboquant_hip.h"
+
+namespace tq {
+
+// ---------------------------------------------------------------- errors
+// One message per host thread; entry points return a code and leave the text here.
+std::string& last_error();
+
+int fail(int code, const char* fmt, ...);
+
+#define TQ_REQUIRE(cond, ...)                                   \
+  do {                                                          \
+    if (!(cond)) return ::tq::fail(TQ_EINVAL, __VA_ARGS__);     \
+  } while (0)
+
+#define TQ_HIP_TRY(expr)                                                          \
+  do {                                                                            \
+    hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess)                                                         \
+      return ::tq::fail(TQ_EHIP, "%s: %s", #expr, hipGetErrorString(e_));         \
+  } while (0)
+
+// Checks the launch that was just issued on this thread.
+#define TQ_LAUNCH_CHECK(name)                                                     \
+  do {                                                                            \
+    hipError_t e_ = hipGetLastError();                                            \
+    if (e_ != hipSuccess)                                                         \
+      return ::tq::fail(TQ_EHIP, "launch of %s failed: %s", name,                 \
+                        hipGetErrorString(e_));                                   \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ---------------------------------------------------------------- dtype helpers
+// Round an fp32 value to the nearest bf16 / fp16 value (ties to even) and return it
+// widened back to fp32.  This is how the reference's torch ops round every
+// intermediate when the input tensor is bf16 or fp16.
+__device__ __forceinline__ float round_bf16(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7f800000u) == 0x7f800000u) {              // inf / nan: keep, quiet nan
+    return (u & 0x007fffffu) ? __uint_as_float(u | 0x00400000u) : v;
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(u & 0xffff0000u);
+}
+
+__device__ __forceinline__ float round_f16(float v) {
+  return __half2float(__float2half_rn(v));
+}
+
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == TQ_BF16) return round_bf16(v);
+  if (dt == TQ_F16) return round_f16(v);
+  return v;
+}
+
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dt) {
+  if (dt == TQ_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dt == TQ_BF16) {
+    uint32_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    return __uint_as_float(h << 16);
+  }
+  return __half2float(reinterpret_cast<const __half*>(p)[i]);
+}
+
+// Store an fp32 value that already holds a representable value of `dt`.
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v, int dt) {
+  if (dt == TQ_F32) {
+    reinterpret_cast<float*>(p)[i] = v;
+  } else if (dt == TQ_BF16) {
+    reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)(__float_as_uint(round_bf16(v)) >> 16);
+  } else {
+    reinterpret_cast<__half*>(p)[i] = __float2half_rn(v);
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// #{ bnd[i] < y } for sorted bnd of length 2^bits - 1 (torch.searchsorted, right=False).
+__device__ __forceinline__ int count_below(const float* bnd, int nlev, float y) {
+  int lo = 0;
+  for (int step = nlev >> 1; step >= 1; step >>= 1) {
+    if (y > bnd[lo + step - 1]) lo += step;
+  }
+  return lo;
+}
+
+inline bool valid_dtype(int dt) { return dt == TQ_F32 || dt == TQ_F16 || dt == TQ_BF16; }
+inline size_t dtype_size(int dt) { return dt == TQ_F32 ? 4 : 2; }
+
+}  // namespace tq

@@ -1,0 +1,513 @@
+// tq_quantize.hip -- quantize-on-write kernels for gfx950.
+//
+//   rotate_and_quantize : n = ||x||, u = x/max(n,1e-10), y = u R^T, code = #{bnd < y}, pack
+//                         (reference.py:263-317; registration.cpp:86-88)
+//   quantize_prod       : MSE at b-1 bits + 1-bit QJL sign residual (reference.py:392-469)
+//   pack / unpack       : bit-plane layout (reference.py:191-255)
+//   dequantize_mse/prod : c[codes] R * n (+ QJL correction) (reference.py:320-367, 472-533)
+//
+// Work decomposition.  A 256-thread workgroup owns a tile of ROWS=16 rows at a
+// time (grid-stride over tiles).  The tile's rows are staged in LDS as fp32, the
+// per-row reductions (norms, residual norms) are one wave per 4 rows, and every
+// d x d contraction is an item loop: item = (output column j, group of 8 rows);
+// the thread keeps 8 fp32 accumulators, streams row j of the matrix from L1/L2
+// in float4 pieces and reads the 8 staged rows as LDS broadcasts, summing k in
+// increasing order.  Codes land in an LDS byte tile and are packed to bit planes
+// by one thread per output byte, so the packed rows leave as contiguous stores.
+//
+// Rounding.  `rdt` is the element type every intermediate is rounded to; the
+// reference computes in the input tensor's dtype (bf16 inputs give bf16 norms,
+// bf16 unit vectors, a bf16 GEMM output and bf16 boundaries).  With rdt=F32 all
+// rounding helpers are the identity.
+
+#include "tq_common.h"
+
+namespace tq {
+
+std::string& last_error() {
+  static thread_local std::string msg;
+  return msg;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  last_error() = buf;
+  return code;
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+namespace {
+
+constexpr int kRows = 16;       // rows per tile
+constexpr int kThreads = 256;   // 4 waves
+constexpr int kRowsPerItem = 8; // accumulators per contraction item
+constexpr int kMaxD = 256;
+constexpr int kDPad = kMaxD + 4;  // LDS row stride (floats); keeps rows 16-byte aligned
+
+struct QuantArgs {
+  const void* x;
+  int in_dt;
+  int rdt;
+  int64_t n;
+  int d;
+  const float* rot;     // [d, d]
+  const float* bnd;     // [2^bits - 1]
+  const float* cen;     // [2^bits] (prod only)
+  const float* qjl;     // [d, d]   (prod only)
+  int bits;             // bits of the MSE codes written
+  uint8_t* packed;      // [n, bits*bpp]
+  uint8_t* signs;       // [n, bpp] (prod only)
+  float* res_norms;     // [n]     (prod only)
+  float* norms;         // [n]
+};
+
+// acc[i] = sum_k A[row0+i][k] * M[col][k] for i < 8, k ascending.  A rows in LDS
+// (stride kDPad), M row-major in global memory.  `rdt` rounds M's elements.
+__device__ __forceinline__ void contract_rows(const float (*A)[kDPad], int row0,
+                                              const float* __restrict__ M, int col, int d,
+                                              int rdt, float acc[kRowsPerItem]) {
+#pragma unroll
+  for (int i = 0; i < kRowsPerItem; ++i) acc[i] = 0.f;
+  const float* mrow = M + (size_t)col * d;
+  if ((d & 3) == 0) {
+    for (int k = 0; k < d; k += 4) {
+      float4 m4 = *reinterpret_cast<const float4*>(mrow + k);
+      if (rdt != TQ_F32) {
+        m4.x = round_to(m4.x, rdt); m4.y = round_to(m4.y, rdt);
+        m4.z = round_to(m4.z, rdt); m4.w = round_to(m4.w, rdt);
+      }
+#pragma unroll
+      for (int i = 0; i < kRowsPerItem; ++i) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&A[row0 + i][k]);
+        float s = acc[i];
+        s = fmaf(a4.x, m4.x, s);
+        s = fmaf(a4.y, m4.y, s);
+        s = fmaf(a4.z, m4.z, s);
+        s = fmaf(a4.w, m4.w, s);
+        acc[i] = s;
+      }
+    }
+  } else {
+    for (int k = 0; k < d; ++k) {
+      const float m = round_to(mrow[k], rdt);
+#pragma unroll
+      for (int i = 0; i < kRowsPerItem; ++i) acc[i] = fmaf(A[row0 + i][k], m, acc[i]);
+    }
+  }
+}
+
+// Same contraction with the matrix read down a column: acc[i] = sum_j C[row0+i][j] * M[j][col].
+// C holds centroid values already (fp32); j ascending.
+__device__ __forceinline__ void contract_cols(const float (*C)[kDPad], int row0,
+                                              const float* __restrict__ M, int col, int d,
+                                              int rdt, float acc[kRowsPerItem]) {
+#pragma unroll
+  for (int i = 0; i < kRowsPerItem; ++i) acc[i] = 0.f;
+  for (int j = 0; j < d; ++j) {
+    const float m = round_to(M[(size_t)j * d + col], rdt);
+#pragma unroll
+    for (int i = 0; i < kRowsPerItem; ++i) acc[i] = fmaf(C[row0 + i][j], m, acc[i]);
+  }
+}
+
+// Pack the LDS code tile rows [0, rows) into bit planes and store them.
+__device__ __forceinline__ void pack_tile(const uint8_t (*codes)[kDPad], int rows, int64_t row_base,
+                                          int d, int bits, uint8_t* __restrict__ out) {
+  const int bpp = (d + 7) >> 3;
+  const int P = bits * bpp;
+  for (int idx = threadIdx.x; idx < rows * P; idx += kThreads) {
+    const int r = idx / P;
+    const int byte = idx - r * P;
+    const int plane = byte / bpp;
+    const int kb = byte - plane * bpp;
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = kb * 8 + i;
+      if (j < d) v |= ((uint32_t)(codes[r][j] >> plane) & 1u) << (7 - i);
+    }
+    out[(row_base + r) * (int64_t)P + byte] = (uint8_t)v;
+  }
+}
+
+// Row norms of the staged tile: wave w reduces rows 4w..4w+3.  Returns nothing;
+// writes nrm[r] = round(sqrt(sum x^2)).
+__device__ __forceinline__ void tile_norms(const float (*X)[kDPad], int d, int rdt, float* nrm) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int rr = 0; rr < kRows / 4; ++rr) {
+    const int r = wave * (kRows / 4) + rr;
+    float s = 0.f;
+    for (int c = lane; c < d; c += 64) s = fmaf(X[r][c], X[r][c], s);
+    s = wave_sum(s);
+    if (lane == 0) nrm[r] = round_to(sqrtf(s), rdt);
+  }
+}
+
+template <bool kProd>
+__global__ __launch_bounds__(kThreads) void quantize_kernel(QuantArgs a) {
+  __shared__ __attribute__((aligned(16))) float xs[kRows][kDPad];   // x, then unit u
+  __shared__ __attribute__((aligned(16))) float us[kRows][kDPad];   // u / ||u||, then residual
+  __shared__ uint8_t cs[kRows][kDPad];                              // codes
+  __shared__ float bnd_s[32];
+  __shared__ float cen_s[32];
+  __shared__ float nrm_s[kRows];
+  __shared__ float nrm2_s[kRows];
+
+  const int d = a.d;
+  const int rdt = a.rdt;
+  const int nlev = 1 << a.bits;
+  if (threadIdx.x < nlev - 1) bnd_s[threadIdx.x] = round_to(a.bnd[threadIdx.x], rdt);
+  if (kProd && threadIdx.x < nlev) cen_s[threadIdx.x] = round_to(a.cen[threadIdx.x], rdt);
+  const float eps = round_to(1e-10f, rdt);
+  const int64_t ntiles = (a.n + kRows - 1) / kRows;
+  const int items = d * (kRows / kRowsPerItem);
+
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r0 = tile * kRows;
+    const int rows = (int)min<int64_t>(kRows, a.n - r0);
+    __syncthreads();  // previous tile fully consumed
+    for (int idx = threadIdx.x; idx < kRows * d; idx += kThreads) {
+      const int r = idx / d, c = idx - r * d;
+      xs[r][c] = (r < rows) ? load_as_f32(a.x, (r0 + r) * (int64_t)d + c, a.in_dt) : 0.f;
+    }
+    __syncthreads();
+    tile_norms(xs, d, rdt, nrm_s);
+    __syncthreads();
+    // unit = x / max(n, eps)
+    for (int idx = threadIdx.x; idx < kRows * d; idx += kThreads) {
+      const int r = idx / d, c = idx - r * d;
+      const float den = fmaxf(nrm_s[r], eps);
+      xs[r][c] = round_to(xs[r][c] / den, rdt);
+    }
+    if (threadIdx.x < rows) a.norms[r0 + threadIdx.x] = nrm_s[threadIdx.x];
+    __syncthreads();
+    if (kProd) {
+      // quantize_mse normalizes its (already unit) input again.
+      tile_norms(xs, d, rdt, nrm2_s);
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < kRows * d; idx += kThreads) {
+        const int r = idx / d, c = idx - r * d;
+        us[r][c] = round_to(xs[r][c] / fmaxf(nrm2_s[r], eps), rdt);
+      }
+      __syncthreads();
+    }
+    const float (*U)[kDPad] = kProd ? us : xs;
+    // y = u R^T and codes.
+    for (int it = threadIdx.x; it < items; it += kThreads) {
+      const int g = it / d, j = it - g * d;
+      float acc[kRowsPerItem];
+      contract_rows(U, g * kRowsPerItem, a.rot, j, d, rdt, acc);
+#pragma unroll
+      for (int i = 0; i < kRowsPerItem; ++i) {
+        const float y = round_to(acc[i], rdt);
+        cs[g * kRowsPerItem + i][j] = (uint8_t)count_below(bnd_s, nlev, y);
+      }
+    }
+    __syncthreads();
+    pack_tile(cs, rows, r0, d, a.bits, a.packed);
+    if (kProd) {
+      // us <- centroid values of the codes (reads cs, writes us: u/||u|| is dead now)
+      for (int idx = threadIdx.x; idx < kRows * d; idx += kThreads) {
+        const int r = idx / d, c = idx - r * d;
+        us[r][c] = cen_s[cs[r][c]];
+      }
+      __syncthreads();
+      // residual = u - round(c[codes] R); kept in registers until all reads of us end.
+      // items <= 2 * kMaxD = 2 * kThreads, so each thread owns at most two items.
+      float resv[2][kRowsPerItem];
+#pragma unroll
+      for (int rep = 0; rep < 2; ++rep) {
+        const int it = threadIdx.x + rep * kThreads;
+        if (it < items) {
+          const int g = it / d, k = it - g * d;
+          float acc[kRowsPerItem];
+          contract_cols(us, g * kRowsPerItem, a.rot, k, d, rdt, acc);
+#pragma unroll
+          for (int i = 0; i < kRowsPerItem; ++i)
+            resv[rep][i] = round_to(xs[g * kRowsPerItem + i][k] - round_to(acc[i], rdt), rdt);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rep = 0; rep < 2; ++rep) {
+        const int it = threadIdx.x + rep * kThreads;
+        if (it < items) {
+          const int g = it / d, k = it - g * d;
+#pragma unroll
+          for (int i = 0; i < kRowsPerItem; ++i) us[g * kRowsPerItem + i][k] = resv[rep][i];
+        }
+      }
+      __syncthreads();
+      tile_norms(us, d, rdt, nrm2_s);
+      // signs of residual S^T
+      for (int it = threadIdx.x; it < items; it += kThreads) {
+        const int g = it / d, j = it - g * d;
+        float acc[kRowsPerItem];
+        contract_rows(us, g * kRowsPerItem, a.qjl, j, d, rdt, acc);
+#pragma unroll
+        for (int i = 0; i < kRowsPerItem; ++i)
+          cs[g * kRowsPerItem + i][j] = (round_to(acc[i], rdt) >= 0.f) ? 1 : 0;
+      }
+      __syncthreads();
+      if (threadIdx.x < rows) a.res_norms[r0 + threadIdx.x] = nrm2_s[threadIdx.x];
+      pack_tile(cs, rows, r0, d, 1, a.signs);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- pack / unpack
+__global__ void pack_kernel(const uint8_t* __restrict__ codes, int64_t n, int d, int bits,
+                            uint8_t* __restrict__ packed) {
+  const int bpp = (d + 7) >> 3;
+  const int P = bits * bpp;
+  const int64_t total = n * (int64_t)P;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / P;
+    const int byte = (int)(idx - r * P);
+    const int plane = byte / bpp;
+    const int kb = byte - plane * bpp;
+    const uint8_t* crow = codes + r * d;
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = kb * 8 + i;
+      if (j < d) v |= ((uint32_t)(crow[j] >> plane) & 1u) << (7 - i);
+    }
+    packed[idx] = (uint8_t)v;
+  }
+}
+
+__global__ void unpack_kernel(const uint8_t* __restrict__ packed, int64_t n, int d, int bits,
+                              uint8_t* __restrict__ codes) {
+  const int bpp = (d + 7) >> 3;
+  const int P = bits * bpp;
+  const int64_t total = n * (int64_t)d;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / d;
+    const int j = (int)(idx - r * d);
+    const uint8_t* prow = packed + r * P;
+    uint32_t c = 0;
+    for (int p = 0; p < bits; ++p) c |= ((uint32_t)(prow[p * bpp + (j >> 3)] >> (7 - (j & 7))) & 1u) << p;
+    codes[idx] = (uint8_t)c;
+  }
+}
+
+// ---------------------------------------------------------------- dequantize
+struct DequantArgs {
+  const uint8_t* packed;
+  const uint8_t* signs;     // prod only
+  const float* res_norms;   // prod only
+  const float* norms;
+  int64_t n;
+  int d;
+  int bits;                 // bits of `packed`
+  const float* cen;
+  const float* rot;
+  const float* qjl;         // prod only
+  int out_dt;
+  void* out;
+};
+
+template <bool kProd>
+__global__ __launch_bounds__(kThreads) void dequant_kernel(DequantArgs a) {
+  __shared__ __attribute__((aligned(16))) float cv[kRows][kDPad];   // centroid values
+  __shared__ __attribute__((aligned(16))) float sv[kRows][kDPad];   // +-1 signs (prod)
+  __shared__ float cen_s[32];
+  const int d = a.d;
+  const int rdt = a.out_dt;
+  const int nlev = 1 << a.bits;
+  const int bpp = (d + 7) >> 3;
+  const int P = a.bits * bpp;
+  if (threadIdx.x < nlev) cen_s[threadIdx.x] = round_to(a.cen[threadIdx.x], rdt);
+  const int64_t ntiles = (a.n + kRows - 1) / kRows;
+  const int items = d * (kRows / kRowsPerItem);
+  const float qscale = 1.2533141373155003f / (float)d;  // sqrt(pi/2) / d
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r0 = tile * kRows;
+    const int rows = (int)min<int64_t>(kRows, a.n - r0);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kRows * d; idx += kThreads) {
+      const int r = idx / d, j = idx - r * d;
+      float v = 0.f, s = 0.f;
+      if (r < rows) {
+        const uint8_t* prow = a.packed + (r0 + r) * (int64_t)P;
+        uint32_t c = 0;
+        for (int p = 0; p < a.bits; ++p)
+          c |= ((uint32_t)(prow[p * bpp + (j >> 3)] >> (7 - (j & 7))) & 1u) << p;
+        v = cen_s[c];
+        if (kProd) {
+          const uint8_t sb = a.signs[(r0 + r) * (int64_t)bpp + (j >> 3)];
+          s = ((sb >> (7 - (j & 7))) & 1u) ? 1.f : -1.f;
+        }
+      }
+      cv[r][j] = v;
+      if (kProd) sv[r][j] = s;
+    }
+    __syncthreads();
+    for (int it = threadIdx.x; it < items; it += kThreads) {
+      const int g = it / d, k = it - g * d;
+      float acc[kRowsPerItem];
+      contract_cols(cv, g * kRowsPerItem, a.rot, k, d, rdt, acc);
+      float corr[kRowsPerItem];
+      if (kProd) contract_cols(sv, g * kRowsPerItem, a.qjl, k, d, TQ_F32, corr);
+#pragma unroll
+      for (int i = 0; i < kRowsPerItem; ++i) {
+        const int r = g * kRowsPerItem + i;
+        if (r >= rows) continue;
+        const int64_t row = r0 + r;
+        float v = round_to(acc[i], rdt);
+        if (kProd) {
+          const float t = qscale * a.res_norms[row];
+          v = v + t * corr[i];
+        }
+        v = round_to(v * a.norms[row], rdt);
+        store_from_f32(a.out, row * (int64_t)d + k, v, rdt);
+      }
+    }
+  }
+}
+
+int grid_for_tiles(int64_t n) {
+  const int64_t tiles = (n + kRows - 1) / kRows;
+  const int64_t cap = (int64_t)device_cu_count() * 6;
+  return (int)(tiles < cap ? tiles : cap);
+}
+
+int grid_for_elems(int64_t total, int threads) {
+  const int64_t blocks = (total + threads - 1) / threads;
+  const int64_t cap = (int64_t)device_cu_count() * 16;
+  return (int)(blocks < cap ? blocks : cap);
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+const char* tq_last_error(void) { return tq::last_error().c_str(); }
+
+int tq_abi_version(void) { return 1; }
+
+int tq_rotate_and_quantize(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtype, int64_t n,
+                           int32_t d, const float* rotation, const float* boundaries,
+                           int32_t bit_width, uint8_t* packed, float* norms, void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && d <= kMaxD, "dim must be in [1, %d], got %d", kMaxD, d);
+  TQ_REQUIRE(n >= 0, "n must be >= 0");
+  TQ_REQUIRE(valid_dtype(in_dtype) && valid_dtype(round_dtype), "unknown dtype");
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(vectors && rotation && boundaries && packed && norms, "null pointer argument");
+  QuantArgs a{vectors, in_dtype, round_dtype, n, d, rotation, boundaries, nullptr, nullptr,
+              bit_width, packed, nullptr, nullptr, norms};
+  hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
+                     as_stream(stream), a);
+  TQ_LAUNCH_CHECK("quantize_kernel<mse>");
+  return TQ_OK;
+}
+
+int tq_quantize_prod(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtype, int64_t n,
+                     int32_t d, const float* rotation, const float* boundaries,
+                     const float* centroids, const float* qjl, int32_t bit_width,
+                     uint8_t* mse_packed, uint8_t* signs, float* res_norms, float* norms,
+                     void* stream) {
+  TQ_REQUIRE(bit_width >= 2 && bit_width <= 5, "Prod mode requires bits in [2, 5], got %d",
+             bit_width);
+  TQ_REQUIRE(d >= 1 && d <= kMaxD, "dim must be in [1, %d], got %d", kMaxD, d);
+  TQ_REQUIRE(n >= 0, "n must be >= 0");
+  TQ_REQUIRE(valid_dtype(in_dtype) && valid_dtype(round_dtype), "unknown dtype");
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(vectors && rotation && boundaries && centroids && qjl && mse_packed && signs &&
+                 res_norms && norms,
+             "null pointer argument");
+  QuantArgs a{vectors, in_dtype, round_dtype, n, d, rotation, boundaries, centroids, qjl,
+              bit_width - 1, mse_packed, signs, res_norms, norms};
+  hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
+                     as_stream(stream), a);
+  TQ_LAUNCH_CHECK("quantize_kernel<prod>");
+  return TQ_OK;
+}
+
+int tq_pack_codes(const uint8_t* codes, int64_t n, int32_t d, int32_t bit_width, uint8_t* packed,
+                  void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 8, "bit_width must be 1-8, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && n >= 0, "bad shape");
+  const int64_t total = n * (int64_t)(bit_width * ((d + 7) / 8));
+  if (total == 0) return TQ_OK;
+  TQ_REQUIRE(codes && packed, "null pointer argument");
+  hipLaunchKernelGGL(pack_kernel, dim3(grid_for_elems(total, 256)), dim3(256), 0,
+                     as_stream(stream), codes, n, d, bit_width, packed);
+  TQ_LAUNCH_CHECK("pack_kernel");
+  return TQ_OK;
+}
+
+int tq_unpack_codes(const uint8_t* packed, int64_t n, int32_t d, int32_t bit_width, uint8_t* codes,
+                    void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 8, "bit_width must be 1-8, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && n >= 0, "bad shape");
+  const int64_t total = n * (int64_t)d;
+  if (total == 0) return TQ_OK;
+  TQ_REQUIRE(codes && packed, "null pointer argument");
+  hipLaunchKernelGGL(unpack_kernel, dim3(grid_for_elems(total, 256)), dim3(256), 0,
+                     as_stream(stream), packed, n, d, bit_width, codes);
+  TQ_LAUNCH_CHECK("unpack_kernel");
+  return TQ_OK;
+}
+
+int tq_dequantize_mse(const uint8_t* packed, const float* norms, int64_t n, int32_t d,
+                      int32_t bit_width, const float* centroids, const float* rotation,
+                      tq_dtype out_dtype, void* out, void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && d <= kMaxD, "dim must be in [1, %d], got %d", kMaxD, d);
+  TQ_REQUIRE(valid_dtype(out_dtype), "unknown dtype");
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(packed && norms && centroids && rotation && out, "null pointer argument");
+  DequantArgs a{packed, nullptr, nullptr, norms, n, d, bit_width, centroids, rotation, nullptr,
+                out_dtype, out};
+  hipLaunchKernelGGL(dequant_kernel<false>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
+                     as_stream(stream), a);
+  TQ_LAUNCH_CHECK("dequant_kernel<mse>");
+  return TQ_OK;
+}
+
+int tq_dequantize_prod(const uint8_t* mse_packed, const uint8_t* signs, const float* res_norms,
+                       const float* norms, int64_t n, int32_t d, int32_t bit_width,
+                       const float* centroids, const float* rotation, const float* qjl,
+                       tq_dtype out_dtype, void* out, void* stream) {
+  TQ_REQUIRE(bit_width >= 2 && bit_width <= 5, "Prod mode requires bits in [2, 5], got %d",
+             bit_width);
+  TQ_REQUIRE(d >= 1 && d <= kMaxD, "dim must be in [1, %d], got %d", kMaxD, d);
+  TQ_REQUIRE(out_dtype == TQ_F32, "dequantize_prod computes in fp32 only");
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(mse_packed && signs && res_norms && norms && centroids && rotation && qjl && out,
+             "null pointer argument");
+  DequantArgs a{mse_packed, signs, res_norms, norms, n, d, bit_width - 1, centroids, rotation, qjl,
+                out_dtype, out};
+  hipLaunchKernelGGL(dequant_kernel<true>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
+                     as_stream(stream), a);
+  TQ_LAUNCH_CHECK("dequant_kernel<prod>");
+  return TQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,912 @@
+// tq_scan.hip -- scoring over packed codes on gfx950.
+//
+// Kernels
+//   lut_kernel      q_rot = R q (sequential fp32 mul/add per output, like
+//                   csrc/core/turboquant_core.cpp:429-437) and the per-query table
+//                   LUT[j][l] = q_rot[j] * c[l] (core.cpp:440-446; triton_kernels.py:437).
+//   scan_kernel     ADC scan.  One lane = one packed row; the row's bit planes are
+//                   loaded with 16-byte loads, transposed to per-octet words with
+//                   v_perm_b32, and every dim's code becomes an LDS byte address
+//                   (code*8) with one v_and + one v_dot4_u32_u8.  The table for dim
+//                   j sits in LDS with an 8-byte stride per code (two dims share a
+//                   128-byte block), so a wave's 64 lookups of one dim touch 16
+//                   distinct banks or broadcast: conflict-free.  Sums run over j in
+//                   increasing order and are scaled by the row norm last, which is
+//                   the reference's own order (core.cpp:455-483).
+//                   Modes: TOPK keeps per-wave candidate lists in LDS (insert when
+//                   score beats the wave's k-th best, strict '>' with lower index
+//                   winning ties, as the core's heap does: core.cpp:487-494) and
+//                   writes each workgroup's sorted top-k; ALL writes every score
+//                   (attention_scores_packed, attn_scores.cu:31-104 semantics).
+//   merge_kernel    per query: prune by the largest per-block k-th score, rank-sort
+//                   the survivors, write top-k (ids int64, padding (-inf, -1)).
+//   softmax_stats   per query: max and sum of exp over its valid scores.
+//   values_kernel   o_part[q][j] = sum_t w[q][t] * vn[t] * c[code_tj] over one
+//                   split of the tokens; 16 fp32 accumulators per thread (4 queries
+//                   x 4 dims), V rows staged in LDS.
+//   combine_kernel  sum of the split partials, then o = o_rot @ M (M = R).
+
+#include "tq_common.h"
+
+#include <climits>
+
+namespace tq {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxK = 32;
+constexpr int kCandCap = 64 + kMaxK;  // per (wave, query) candidate slots
+constexpr int kValTokens = 256;       // tokens staged per values chunk
+constexpr int kSplitTokens = 1024;    // tokens per values split (decode / values op)
+
+// ------------------------------------------------------------------ LUT
+// lut[qg][j][l] for j < dpad (zeros for j >= d).
+__global__ void lut_kernel(const void* __restrict__ q, int q_dt, int d, int dpad,
+                           const float* __restrict__ rot, const float* __restrict__ cen, int nlev,
+                           float* __restrict__ lut) {
+  __shared__ float qs[256];
+  const int qg = blockIdx.x;
+  for (int k = threadIdx.x; k < d; k += blockDim.x) qs[k] = load_as_f32(q, (int64_t)qg * d + k, q_dt);
+  __syncthreads();
+  float* out = lut + (size_t)qg * dpad * nlev;
+  for (int j = threadIdx.x; j < dpad; j += blockDim.x) {
+    float v = 0.f;
+    if (j < d) {
+      const float* r = rot + (size_t)j * d;
+      for (int k = 0; k < d; ++k) v = __fadd_rn(v, __fmul_rn(qs[k], r[k]));
+    }
+    for (int l = 0; l < nlev; ++l) out[(size_t)j * nlev + l] = (j < d) ? __fmul_rn(v, cen[l]) : 0.f;
+  }
+}
+
+// ------------------------------------------------------------------ scan
+struct ScanArgs {
+  const uint8_t* packed;    // rows of stream s start at packed + s * stream_rows * P
+  const float* norms;       // stream s starts at norms + s * stream_rows
+  int64_t stream_rows;      // row stride between streams
+  int64_t nrows;            // rows per stream when seq_lens == nullptr
+  const int32_t* seq_lens;  // per batch row counts (decode); stream s -> batch s / spb
+  int spb;                  // streams per batch
+  int bpp;                  // bytes per plane (runtime; used by the generic loader)
+  const float* lut;         // [nq_total][dpad][nlev]
+  int dpad;
+  int qps;                  // queries per stream
+  float post_scale;         // multiplies norm * sum (decode: softmax scale)
+  int k;
+  float* part_s;            // TOPK: [nq_total][gridDim.x][k]
+  int32_t* part_i;
+  float* scores;            // ALL:  [nq_total][stream_rows]
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <int BITS, int BPP>
+struct RowLoader {
+  static constexpr int P = BITS * BPP;
+  static constexpr int NW = (P + 3) / 4;  // 32-bit words per row (fast path: P % 4 == 0)
+  // Plane p, word w of the row: bytes [p*BPP + 4w, +4) (dims 32w..32w+31 of plane p).
+  __device__ static __forceinline__ void load(const uint8_t* __restrict__ row, uint32_t (&wd)[NW]) {
+    if constexpr (P % 16 == 0) {
+      const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
+#pragma unroll
+      for (int i = 0; i < P / 16; ++i) {
+        const u32x4 v = __builtin_nontemporal_load(r4 + i);
+        wd[4 * i + 0] = v.x; wd[4 * i + 1] = v.y; wd[4 * i + 2] = v.z; wd[4 * i + 3] = v.w;
+      }
+    } else if constexpr (P % 8 == 0) {
+      const u32x2* r2 = reinterpret_cast<const u32x2*>(row);
+#pragma unroll
+      for (int i = 0; i < P / 8; ++i) {
+        const u32x2 v = __builtin_nontemporal_load(r2 + i);
+        wd[2 * i + 0] = v.x; wd[2 * i + 1] = v.y;
+      }
+    } else {
+      const uint32_t* r1 = reinterpret_cast<const uint32_t*>(row);
+#pragma unroll
+      for (int i = 0; i < NW; ++i) wd[i] = __builtin_nontemporal_load(r1 + i);
+    }
+  }
+};
+
+// Generic loader for any bytes-per-plane (<= 32): assembles the plane words of a
+// BPP_T=32 layout from byte loads; missing bytes are zero (pad dims decode to code 0,
+// whose table entries are zero).
+template <int BITS>
+__device__ __forceinline__ void load_generic(const uint8_t* __restrict__ row, int bpp,
+                                             uint32_t (&wd)[BITS * 8]) {
+#pragma unroll
+  for (int p = 0; p < BITS; ++p) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int kb = 4 * w + m;
+        if (kb < bpp) v |= (uint32_t)row[p * bpp + kb] << (8 * m);
+      }
+      wd[p * 8 + w] = v;
+    }
+  }
+}
+
+// Byte address (code * 8) of every dim of one 32-dim word group, for QB tables.
+// A[p] = word w of plane p.  Calls f(dim_in_group, addr8) for dims 0..31 in order.
+template <int BITS, typename F>
+__device__ __forceinline__ void decode_group(const uint32_t (&A)[4], F&& f) {
+  const uint32_t a0 = A[0];
+  const uint32_t a1 = BITS > 1 ? A[1] : 0u;
+  const uint32_t a2 = BITS > 2 ? A[2] : 0u;
+  const uint32_t a3 = BITS > 3 ? A[3] : 0u;
+  const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u);
+  const uint32_t hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+  const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+  uint32_t X[4];
+  X[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+  X[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+  X[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+  X[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+  // X[m] byte p = plane p's byte m (dims 8m..8m+7, dim 8m+i at bit 7-i).
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t xh = X[m];
+    const uint32_t xl = X[m] >> 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // shift s of dim i's bit within each byte after choosing xh (i>=4) or xl (i<4)
+      const int s = (i >= 4) ? (7 - i) : (3 - i);
+      const uint32_t src = (i >= 4) ? xh : xl;
+      const uint32_t z = src & (0x01010101u << s);
+      const uint32_t w = (s == 0) ? 0x40201008u : (s == 1) ? 0x20100804u
+                       : (s == 2) ? 0x10080402u : 0x08040201u;
+      f(8 * m + i, __builtin_amdgcn_udot4(z, w, 0u, false));
+    }
+  }
+}
+
+__device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
+  return sa > sb || (sa == sb && ia < ib);
+}
+
+// Reduce a wave's candidate list (cs/ci, `count` entries, count <= 128) to its best
+// min(count, k) entries in sorted order.  Wave-uniform arguments.
+__device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int k, float& th,
+                                             int& thi) {
+  const int lane = threadIdx.x & 63;
+  const bool v0 = lane < count, v1 = lane + 64 < count;
+  float s0 = 0.f, s1 = 0.f;
+  int i0 = 0, i1 = 0;
+  if (v0) { s0 = cs[lane]; i0 = ci[lane]; }
+  if (v1) { s1 = cs[lane + 64]; i1 = ci[lane + 64]; }
+  int r0 = 0, r1 = 0;
+  for (int e = 0; e < count; ++e) {
+    const float se = cs[e];
+    const int ie = ci[e];
+    r0 += better(se, ie, s0, i0);
+    r1 += better(se, ie, s1, i1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (v0 && r0 < k) { cs[r0] = s0; ci[r0] = i0; }
+  if (v1 && r1 < k) { cs[r1] = s1; ci[r1] = i1; }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  count = count < k ? count : k;
+  if (count == k) {
+    th = cs[k - 1];
+    thi = ci[k - 1];
+  }
+}
+
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
+__global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
+  constexpr int NLEV = 1 << BITS;
+  constexpr int BPPT = GENERIC ? 32 : BPP;          // layout the decoder sees
+  constexpr int DP = 8 * BPPT;                      // dims covered by the decoder
+  constexpr int QSTRIDE = DP * NLEV * 4;            // bytes per query table
+  constexpr int NW = GENERIC ? BITS * 8 : RowLoader<BITS, BPP>::NW;
+  constexpr int WPP = BPPT / 4;                     // words per plane
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* lut_s = smem;
+  float* cand_s = reinterpret_cast<float*>(smem + QB * QSTRIDE);
+  int* cand_i = reinterpret_cast<int*>(cand_s + kWaves * QB * kCandCap);
+  int* cnt_s = cand_i + kWaves * QB * kCandCap;
+
+  const int s = blockIdx.z;
+  const int qb = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  int64_t nrows = a.nrows;
+  if (a.seq_lens) {
+    const int64_t sl = a.seq_lens[s / a.spb];
+    nrows = sl < a.stream_rows ? sl : a.stream_rows;
+  }
+  const int q0 = s * a.qps + qb * QB;            // first global query of this block
+  const int nq = min(QB, a.qps - qb * QB);       // valid queries in this block
+  const int P = BITS * a.bpp;
+
+  // Stage the tables: lut_s[qi][(j>>1)*NLEV*8 + l*8 + (j&1)*4].
+  for (int idx = threadIdx.x; idx < QB * DP * NLEV; idx += kThreads) {
+    const int qi = idx / (DP * NLEV);
+    const int rem = idx - qi * DP * NLEV;
+    const int j = rem / NLEV, l = rem - j * NLEV;
+    float v = 0.f;
+    if (qi < nq && j < a.dpad) v = a.lut[((size_t)(q0 + qi) * a.dpad + j) * NLEV + l];
+    *reinterpret_cast<float*>(lut_s + qi * QSTRIDE + (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4) = v;
+  }
+  __syncthreads();
+
+  // Contiguous row range of this block, 64-row steps interleaved over the waves.
+  const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
+  const int64_t rbeg = (int64_t)blockIdx.x * per_block;
+  const int64_t rend = min(nrows, rbeg + per_block);
+  const uint8_t* base = a.packed + (size_t)s * a.stream_rows * P;
+  const float* nbase = a.norms + (size_t)s * a.stream_rows;
+
+  float th[QB];
+  int thi[QB];
+  int cnt[QB];
+#pragma unroll
+  for (int qi = 0; qi < QB; ++qi) { th[qi] = -INFINITY; thi[qi] = INT_MAX; cnt[qi] = 0; }
+  float* my_cs = cand_s + wave * QB * kCandCap;
+  int* my_ci = cand_i + wave * QB * kCandCap;
+
+  uint32_t cur[NW];
+  int64_t row = rbeg + wave * 64 + lane;
+  auto load_row = [&](int64_t r, uint32_t (&w)[NW]) {
+    if (r < rend) {
+      if constexpr (GENERIC) load_generic<BITS>(base + r * P, a.bpp, w);
+      else RowLoader<BITS, BPP>::load(base + r * P, w);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = 0u;
+    }
+  };
+  load_row(row, cur);
+  for (int64_t step0 = rbeg + wave * 64; step0 < rend; step0 += kWaves * 64) {
+    const int64_t nxt_row = row + kWaves * 64;
+    uint32_t nxt[NW];
+    load_row(nxt_row, nxt);
+    const float nrm = row < rend ? __builtin_nontemporal_load(nbase + row) : 0.f;
+
+    float acc[QB];
+#pragma unroll
+    for (int qi = 0; qi < QB; ++qi) acc[qi] = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPP; ++w) {
+      uint32_t A[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) A[p] = (p < BITS) ? cur[p * WPP + w] : 0u;
+      decode_group<BITS>(A, [&](int di, uint32_t addr8) {
+        const int j = 32 * w + di;
+        const int off = (j >> 1) * NLEV * 8 + (j & 1) * 4;
+#pragma unroll
+        for (int qi = 0; qi < QB; ++qi)
+          acc[qi] += *reinterpret_cast<const float*>(lut_s + qi * QSTRIDE + off + addr8);
+      });
+    }
+
+    if constexpr (TOPK) {
+      const bool valid = row < rend;
+#pragma unroll
+      for (int qi = 0; qi < QB; ++qi) {
+        if (qi >= nq) break;
+        const float sc = acc[qi] * nrm * a.post_scale;
+        const int id = (int)row;
+        bool pred = valid && better(sc, id, th[qi], thi[qi]);
+        uint64_t mask = __ballot(pred);
+        int nnew = __popcll(mask);
+        if (nnew == 0) continue;
+        float* cs = my_cs + qi * kCandCap;
+        int* ci = my_ci + qi * kCandCap;
+        if (cnt[qi] + nnew > kCandCap) {
+          wave_compact(cs, ci, cnt[qi], a.k, th[qi], thi[qi]);
+          pred = valid && better(sc, id, th[qi], thi[qi]);
+          mask = __ballot(pred);
+          nnew = __popcll(mask);
+        }
+        if (pred) {
+          const int pos = cnt[qi] + (int)__builtin_amdgcn_mbcnt_hi(
+                                        (uint32_t)(mask >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+          cs[pos] = sc;
+          ci[pos] = id;
+        }
+        cnt[qi] += nnew;
+      }
+    } else {
+      if (row < rend) {
+#pragma unroll
+        for (int qi = 0; qi < QB; ++qi)
+          if (qi < nq) a.scores[(size_t)(q0 + qi) * a.stream_rows + row] = acc[qi] * nrm * a.post_scale;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NW; ++i) cur[i] = nxt[i];
+    row = nxt_row;
+  }
+
+  if constexpr (TOPK) {
+#pragma unroll
+    for (int qi = 0; qi < QB; ++qi) {
+      if (qi >= nq) break;
+      if (cnt[qi] > a.k) wave_compact(my_cs + qi * kCandCap, my_ci + qi * kCandCap, cnt[qi], a.k,
+                                      th[qi], thi[qi]);
+      if (lane == 0) cnt_s[wave * QB + qi] = cnt[qi];
+    }
+    __syncthreads();
+    // Merge the 4 wave lists of query qi (<= 4k <= 128 entries): wave qi % 4.
+    for (int qi = wave; qi < nq; qi += kWaves) {
+      int total = 0;
+      int off[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) { off[w] = total; total += cnt_s[w * QB + qi]; }
+      // entry e of the union -> (wave w, slot e - off[w])
+      auto fetch = [&](int e, float& sc, int& id) {
+        int w = 0;
+#pragma unroll
+        for (int t = 1; t < kWaves; ++t) w += (e >= off[t]);
+        const int slot = e - off[w];
+        sc = cand_s[(w * QB + qi) * kCandCap + slot];
+        id = cand_i[(w * QB + qi) * kCandCap + slot];
+      };
+      float* ps = a.part_s + ((size_t)(q0 + qi) * gridDim.x + blockIdx.x) * a.k;
+      int32_t* pi = a.part_i + ((size_t)(q0 + qi) * gridDim.x + blockIdx.x) * a.k;
+      for (int e = lane; e < 2 * 64; e += 64) {
+        if (e < total) {
+          float se; int ie;
+          fetch(e, se, ie);
+          int rank = 0;
+          for (int f = 0; f < total; ++f) {
+            float sf; int jf;
+            fetch(f, sf, jf);
+            rank += better(sf, jf, se, ie);
+          }
+          if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
+        }
+      }
+      for (int e = total + lane; e < a.k; e += 64) { ps[e] = -INFINITY; pi[e] = -1; }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ merge
+constexpr int kMergeCap = 2048;
+
+__global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
+                                                         const int32_t* __restrict__ part_i,
+                                                         int nblocks, int k, float* __restrict__ out_s,
+                                                         int64_t* __restrict__ out_i) {
+  __shared__ float red[kThreads];
+  __shared__ float ss[kMergeCap];
+  __shared__ int si[kMergeCap];
+  __shared__ int nsurv;
+  const int q = blockIdx.x;
+  const float* ps = part_s + (size_t)q * nblocks * k;
+  const int32_t* pi = part_i + (size_t)q * nblocks * k;
+  // tau = max over blocks of the block's k-th best (its last valid entry when full).
+  float t = -INFINITY;
+  for (int b = threadIdx.x; b < nblocks; b += kThreads) {
+    if (pi[(size_t)b * k + k - 1] >= 0) t = fmaxf(t, ps[(size_t)b * k + k - 1]);
+  }
+  red[threadIdx.x] = t;
+  if (threadIdx.x == 0) nsurv = 0;
+  __syncthreads();
+  for (int st = kThreads / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
+    __syncthreads();
+  }
+  const float tau = red[0];
+  const int total = nblocks * k;
+  for (int e = threadIdx.x; e < total; e += kThreads) {
+    const int id = pi[e];
+    const float sc = ps[e];
+    if (id >= 0 && sc >= tau) {
+      const int pos = atomicAdd(&nsurv, 1);
+      if (pos < kMergeCap) { ss[pos] = sc; si[pos] = id; }
+    }
+  }
+  __syncthreads();
+  const int m = nsurv;
+  float* os = out_s + (size_t)q * k;
+  int64_t* oi = out_i + (size_t)q * k;
+  if (m <= kMergeCap) {
+    for (int e = threadIdx.x; e < m; e += kThreads) {
+      const float se = ss[e];
+      const int ie = si[e];
+      int rank = 0;
+      for (int f = 0; f < m; ++f) rank += better(ss[f], si[f], se, ie);
+      if (rank < k) { os[rank] = se; oi[rank] = ie; }
+    }
+    for (int e = m + threadIdx.x; e < k; e += kThreads) { os[e] = -INFINITY; oi[e] = -1; }
+  } else {
+    // Many exact ties at tau: k rounds of block arg-best over every candidate.
+    __shared__ float bs[kThreads];
+    __shared__ int bi[kThreads];
+    float last_s = INFINITY;
+    int last_i = -1;
+    for (int r = 0; r < k; ++r) {
+      float cs = -INFINITY;
+      int ci = INT_MAX;
+      bool have = false;
+      for (int e = threadIdx.x; e < total; e += kThreads) {
+        const int id = pi[e];
+        const float sc = ps[e];
+        if (id < 0 || !better(last_s, last_i, sc, id)) continue;  // already emitted
+        if (!have || better(sc, id, cs, ci)) { cs = sc; ci = id; have = true; }
+      }
+      bs[threadIdx.x] = cs;
+      bi[threadIdx.x] = have ? ci : INT_MAX;
+      __syncthreads();
+      for (int st = kThreads / 2; st > 0; st >>= 1) {
+        if (threadIdx.x < st) {
+          const bool ob = bi[threadIdx.x + st] != INT_MAX;
+          const bool mb = bi[threadIdx.x] != INT_MAX;
+          if (ob && (!mb || better(bs[threadIdx.x + st], bi[threadIdx.x + st], bs[threadIdx.x],
+                                   bi[threadIdx.x]))) {
+            bs[threadIdx.x] = bs[threadIdx.x + st];
+            bi[threadIdx.x] = bi[threadIdx.x + st];
+          }
+        }
+        __syncthreads();
+      }
+      last_s = bs[0];
+      last_i = bi[0];
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        os[r] = last_i == INT_MAX ? -INFINITY : last_s;
+        oi[r] = last_i == INT_MAX ? -1 : last_i;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ softmax stats
+// stats[q] = (max_t s, sum_t exp(s - max)) over the valid tokens of query q's stream.
+__global__ __launch_bounds__(kThreads) void softmax_stats_kernel(const float* __restrict__ scores,
+                                                                 int64_t t_max,
+                                                                 const int32_t* __restrict__ seq_lens,
+                                                                 int q_per_batch,
+                                                                 float2* __restrict__ stats) {
+  __shared__ float red[kThreads];
+  const int q = blockIdx.x;
+  const int64_t n = min<int64_t>(seq_lens[q / q_per_batch], t_max);
+  const float* sp = scores + (size_t)q * t_max;
+  float m = -INFINITY;
+  for (int64_t t = threadIdx.x; t < n; t += kThreads) m = fmaxf(m, sp[t]);
+  red[threadIdx.x] = m;
+  __syncthreads();
+  for (int st = kThreads / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
+    __syncthreads();
+  }
+  m = red[0];
+  __syncthreads();
+  float l = 0.f;
+  for (int64_t t = threadIdx.x; t < n; t += kThreads) l += __expf(sp[t] - m);
+  red[threadIdx.x] = l;
+  __syncthreads();
+  for (int st = kThreads / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) stats[q] = make_float2(m, red[0]);
+}
+
+// ------------------------------------------------------------------ values
+struct ValuesArgs {
+  const uint8_t* packed;    // stream s rows at packed + s * stream_rows * P
+  const float* vnorms;      // stream s at vnorms + s * stream_rows
+  int64_t stream_rows;
+  int64_t nrows;            // when seq_lens == nullptr
+  const int32_t* seq_lens;
+  int spb;
+  int d;
+  int bits;
+  const float* cen;
+  int qps;                  // queries per stream
+  // weights: explicit [nq_total][w_stride] (op), or exp(s - m) / l from scores + stats
+  const float* w;
+  int64_t w_stride;
+  const float* scores;      // [nq_total][stream_rows]
+  const float2* stats;
+  float* part;              // [nq_total][nsplit][d]
+  int nsplit;
+};
+
+template <bool kDecode>
+__global__ __launch_bounds__(kThreads) void values_kernel(ValuesArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t rows_s[kValTokens * 4 * 32];
+  __shared__ __attribute__((aligned(16))) float w_s[kValTokens][4];
+  __shared__ float cen_s[16];
+  __shared__ float red_s[kThreads / 4 * 16];
+  const int sp = blockIdx.x, qb = blockIdx.y, s = blockIdx.z;
+  const int d = a.d, bits = a.bits;
+  const int bpp = (d + 7) >> 3;
+  const int P = bits * bpp;
+  int64_t nrows = a.nrows;
+  if (a.seq_lens) {
+    const int64_t sl = a.seq_lens[s / a.spb];
+    nrows = sl < a.stream_rows ? sl : a.stream_rows;
+  }
+  const int q0 = s * a.qps + qb * 4;
+  const int nq = min(4, a.qps - qb * 4);
+  const int64_t t0 = (int64_t)sp * kSplitTokens;
+  const int64_t t1 = min<int64_t>(t0 + kSplitTokens, nrows);
+  const int ng = (d + 3) >> 2;          // dim groups of 4
+  const int nsl = kThreads / ng;        // token slices
+  const int tid = threadIdx.x;
+  const int g = tid % ng, sl = tid / ng;
+  const bool active = sl < nsl;
+  if (tid < (1 << bits)) cen_s[tid] = a.cen[tid];
+  float2 st[4];
+  if (kDecode) {
+#pragma unroll
+    for (int qi = 0; qi < 4; ++qi) st[qi] = qi < nq ? a.stats[q0 + qi] : make_float2(0.f, 1.f);
+  }
+  float acc[4][4];
+#pragma unroll
+  for (int qi = 0; qi < 4; ++qi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[qi][i] = 0.f;
+
+  const uint8_t* base = a.packed + (size_t)s * a.stream_rows * P;
+  const float* vn = a.vnorms + (size_t)s * a.stream_rows;
+  for (int64_t c0 = t0; c0 < t1; c0 += kValTokens) {
+    const int nt = (int)min<int64_t>(kValTokens, t1 - c0);
+    __syncthreads();
+    for (int idx = tid; idx < nt * P; idx += kThreads) rows_s[idx] = base[(size_t)c0 * P + idx];
+    for (int idx = tid; idx < nt * 4; idx += kThreads) {
+      const int t = idx >> 2, qi = idx & 3;
+      float w = 0.f;
+      if (qi < nq) {
+        const int64_t tt = c0 + t;
+        if (kDecode) {
+          const float sc = a.scores[(size_t)(q0 + qi) * a.stream_rows + tt];
+          w = __expf(sc - st[qi].x) / st[qi].y;
+        } else {
+          w = a.w[(size_t)(q0 + qi) * a.w_stride + tt];
+        }
+        w *= vn[tt];
+      }
+      w_s[t][qi] = w;
+    }
+    __syncthreads();
+    if (active) {
+      const int kb = g >> 1;
+      const int sh = (g & 1) ? 0 : 4;
+      for (int t = sl; t < nt; t += nsl) {
+        const uint8_t* r = rows_s + t * P;
+        uint32_t nib[4];
+        for (int p = 0; p < 4; ++p) nib[p] = p < bits ? (r[p * bpp + kb] >> sh) & 0xFu : 0u;
+        const float4 w4 = *reinterpret_cast<const float4*>(&w_s[t][0]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t code = ((nib[0] >> (3 - i)) & 1u) | (((nib[1] >> (3 - i)) & 1u) << 1) |
+                                (((nib[2] >> (3 - i)) & 1u) << 2) | (((nib[3] >> (3 - i)) & 1u) << 3);
+          const float v = cen_s[code];
+          acc[0][i] = fmaf(w4.x, v, acc[0][i]);
+          acc[1][i] = fmaf(w4.y, v, acc[1][i]);
+          acc[2][i] = fmaf(w4.z, v, acc[2][i]);
+          acc[3][i] = fmaf(w4.w, v, acc[3][i]);
+        }
+      }
+    }
+  }
+  // reduce over slices: red_s[g][qi*4+i] accumulated slice by slice
+  __syncthreads();
+  for (int slice = 0; slice < nsl; ++slice) {
+    if (active && sl == slice) {
+#pragma unroll
+      for (int qi = 0; qi < 4; ++qi)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float& dst = red_s[g * 16 + qi * 4 + i];
+          dst = (slice == 0) ? acc[qi][i] : dst + acc[qi][i];
+        }
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < nq * d; idx += kThreads) {
+    const int qi = idx / d, j = idx - qi * d;
+    const float v = (t0 < t1) ? red_s[(j >> 2) * 16 + qi * 4 + (j & 3)] : 0.f;
+    a.part[((size_t)(q0 + qi) * a.nsplit + sp) * d + j] = v;
+  }
+}
+
+// out[q][k] = sum_j (sum_sp part[q][sp][j]) * M[j][k], cast to out_dt.
+__global__ void combine_kernel(const float* __restrict__ part, int nsplit, int d,
+                               const float* __restrict__ M, const int32_t* __restrict__ seq_lens,
+                               int q_per_batch, int out_dt, void* __restrict__ out) {
+  __shared__ float o_s[256];
+  const int q = blockIdx.x;
+  int ns = nsplit;
+  if (seq_lens) {
+    const int64_t n = seq_lens[q / q_per_batch];
+    const int64_t need = (n + kSplitTokens - 1) / kSplitTokens;
+    ns = (int)min<int64_t>(need, nsplit);
+  }
+  for (int j = threadIdx.x; j < d; j += blockDim.x) {
+    float v = 0.f;
+    for (int sp = 0; sp < ns; ++sp) v += part[((size_t)q * nsplit + sp) * d + j];
+    o_s[j] = v;
+  }
+  __syncthreads();
+  for (int kk = threadIdx.x; kk < d; kk += blockDim.x) {
+    float v = 0.f;
+    for (int j = 0; j < d; ++j) v = fmaf(o_s[j], M[(size_t)j * d + kk], v);
+    store_from_f32(out, (int64_t)q * d + kk, v, out_dt);
+  }
+}
+
+// ------------------------------------------------------------------ host helpers
+int scan_blocks(int64_t nrows) {
+  const int64_t want = (nrows + 64 * 8 * kWaves - 1) / (64 * 8 * kWaves);  // >= 8 steps per wave
+  const int64_t cap = (int64_t)device_cu_count() * 4;
+  int64_t b = want < cap ? want : cap;
+  return (int)(b < 1 ? 1 : b);
+}
+
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
+int launch_scan_t(const ScanArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int NLEV = 1 << BITS;
+  constexpr int BPPT = GENERIC ? 32 : BPP;
+  constexpr size_t lut_bytes = (size_t)QB * 8 * BPPT * NLEV * 4;
+  constexpr size_t cand_bytes = TOPK ? (size_t)kWaves * QB * kCandCap * 8 + kWaves * QB * 4 : 0;
+  constexpr size_t smem = lut_bytes + cand_bytes;
+  auto kern = scan_kernel<BITS, BPP, QB, TOPK, GENERIC>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    TQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, a);
+  TQ_LAUNCH_CHECK("scan_kernel");
+  return TQ_OK;
+}
+
+template <int BITS, bool TOPK>
+int launch_scan_bits(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
+  // The fast loaders issue 8/16-byte loads: they need a 16-byte aligned base
+  // (row strides of the fast layouts keep that alignment).
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
+  if (aligned && a.bpp == 16) {
+    return qb == 4 ? launch_scan_t<BITS, 16, 4, TOPK, false>(a, grid, st)
+                   : launch_scan_t<BITS, 16, 1, TOPK, false>(a, grid, st);
+  }
+  if (aligned && a.bpp == 8) {
+    return qb == 4 ? launch_scan_t<BITS, 8, 4, TOPK, false>(a, grid, st)
+                   : launch_scan_t<BITS, 8, 1, TOPK, false>(a, grid, st);
+  }
+  return qb == 4 ? launch_scan_t<BITS, 32, 4, TOPK, true>(a, grid, st)
+                 : launch_scan_t<BITS, 32, 1, TOPK, true>(a, grid, st);
+}
+
+int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st) {
+  const int qb = a.qps >= 2 ? 4 : 1;
+  const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
+  dim3 grid(topk ? (unsigned)scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
+            (unsigned)((a.qps + qb - 1) / qb), (unsigned)nstreams);
+  switch (bits) {
+    case 1: return topk ? launch_scan_bits<1, true>(a, qb, grid, st) : launch_scan_bits<1, false>(a, qb, grid, st);
+    case 2: return topk ? launch_scan_bits<2, true>(a, qb, grid, st) : launch_scan_bits<2, false>(a, qb, grid, st);
+    case 3: return topk ? launch_scan_bits<3, true>(a, qb, grid, st) : launch_scan_bits<3, false>(a, qb, grid, st);
+    case 4: return topk ? launch_scan_bits<4, true>(a, qb, grid, st) : launch_scan_bits<4, false>(a, qb, grid, st);
+  }
+  return fail(TQ_EINVAL, "bit_width must be 1-4, got %d", bits);
+}
+
+int launch_lut(const void* q, int q_dt, int64_t nq, int d, int dpad, const float* rot,
+               const float* cen, int nlev, float* lut, hipStream_t st) {
+  hipLaunchKernelGGL(lut_kernel, dim3((unsigned)nq), dim3(256), 0, st, q, q_dt, d, dpad, rot, cen,
+                     nlev, lut);
+  TQ_LAUNCH_CHECK("lut_kernel");
+  return TQ_OK;
+}
+
+inline int dpad_for(int d) {
+  const int bpp = (d + 7) / 8;
+  return (bpp == 8 || bpp == 16) ? 8 * bpp : 256;
+}
+
+size_t lut_bytes(int64_t nq, int d, int bits) {
+  return align_up((size_t)nq * dpad_for(d) * (1u << bits) * 4, 256);
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N, int32_t k) {
+  if (nq <= 0 || d <= 0 || bit_width < 1 || bit_width > 4) return 0;
+  size_t bytes = lut_bytes(nq, d, bit_width);
+  if (k > 0) {
+    const size_t nb = (size_t)scan_blocks(N);
+    bytes += align_up((size_t)nq * nb * k * 4, 256) * 2;
+  }
+  return bytes;
+}
+
+int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                    const uint8_t* packed, const float* norms, int64_t N, const float* centroids,
+                    const float* rotation, int32_t bit_width, int32_t k, float* out_scores,
+                    int64_t* out_ids, void* workspace, size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
+  TQ_REQUIRE(k >= 1 && k <= kMaxK, "k must be in [1, %d], got %d", kMaxK, k);
+  TQ_REQUIRE(nq >= 0 && N >= 0, "bad sizes");
+  TQ_REQUIRE(N <= INT_MAX, "N must fit in int32 ids");
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  if (nq == 0) return TQ_OK;
+  TQ_REQUIRE(queries && out_scores && out_ids && centroids && rotation, "null pointer argument");
+  TQ_REQUIRE(N == 0 || (packed && norms), "null pointer argument");
+  const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, N, k);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t st = as_stream(stream);
+  const int dpad = dpad_for(d);
+  char* ws = static_cast<char*>(workspace);
+  float* lut = reinterpret_cast<float*>(ws);
+  ws += lut_bytes(nq, d, bit_width);
+  const int nb = scan_blocks(N);
+  float* ps = reinterpret_cast<float*>(ws);
+  ws += align_up((size_t)nq * nb * k * 4, 256);
+  int32_t* pi = reinterpret_cast<int32_t*>(ws);
+  int rc = launch_lut(queries, q_dtype, nq, d, dpad, rotation, centroids, 1 << bit_width, lut, st);
+  if (rc) return rc;
+  ScanArgs a{};
+  a.packed = packed; a.norms = norms; a.stream_rows = N; a.nrows = N; a.seq_lens = nullptr; a.spb = 1;
+  a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad; a.qps = (int)nq; a.post_scale = 1.f; a.k = k;
+  a.part_s = ps; a.part_i = pi; a.scores = nullptr;
+  TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
+  rc = launch_scan(a, bit_width, true, 1, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
+                     out_scores, out_ids);
+  TQ_LAUNCH_CHECK("merge_kernel");
+  return TQ_OK;
+}
+
+int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                               const uint8_t* packed_keys, const float* key_norms, int64_t T,
+                               const float* centroids, const float* rotation, int32_t bit_width,
+                               float* scores, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
+  TQ_REQUIRE(nq >= 0 && T >= 0, "bad sizes");
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  if (nq == 0 || T == 0) return TQ_OK;
+  TQ_REQUIRE(query && packed_keys && key_norms && centroids && rotation && scores,
+             "null pointer argument");
+  const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, T, 0);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t st = as_stream(stream);
+  const int dpad = dpad_for(d);
+  float* lut = static_cast<float*>(workspace);
+  int rc = launch_lut(query, q_dtype, nq, d, dpad, rotation, centroids, 1 << bit_width, lut, st);
+  if (rc) return rc;
+  ScanArgs a{};
+  a.packed = packed_keys; a.norms = key_norms; a.stream_rows = T; a.nrows = T; a.seq_lens = nullptr;
+  a.spb = 1; a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad; a.qps = (int)nq; a.post_scale = 1.f;
+  a.k = 0; a.scores = scores;
+  TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
+  return launch_scan(a, bit_width, false, 1, st);
+}
+
+size_t tq_values_workspace_bytes(int64_t nq, int32_t d, int64_t T) {
+  if (nq <= 0 || d <= 0) return 0;
+  const int64_t ns = (T + kSplitTokens - 1) / kSplitTokens;
+  return align_up((size_t)nq * (ns > 0 ? ns : 1) * d * 4, 256);
+}
+
+int tq_attention_values_packed(const float* attn_weights, int64_t nq, int64_t T,
+                               const uint8_t* packed_values, const float* value_norms,
+                               const float* centroids, const float* rotation_T, int32_t d,
+                               int32_t bit_width, float* out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
+  TQ_REQUIRE(nq >= 0 && T >= 0, "bad sizes");
+  if (nq == 0) return TQ_OK;
+  TQ_REQUIRE(attn_weights || T == 0, "null pointer argument");
+  TQ_REQUIRE(out && centroids && rotation_T, "null pointer argument");
+  TQ_REQUIRE(T == 0 || (packed_values && value_norms), "null pointer argument");
+  const size_t need = tq_values_workspace_bytes(nq, d, T);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t st = as_stream(stream);
+  float* part = static_cast<float*>(workspace);
+  const int ns = (int)((T + kSplitTokens - 1) / kSplitTokens);
+  TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
+  if (ns > 0) {
+    ValuesArgs a{};
+    a.packed = packed_values; a.vnorms = value_norms; a.stream_rows = T; a.nrows = T;
+    a.seq_lens = nullptr; a.spb = 1; a.d = d; a.bits = bit_width; a.cen = centroids;
+    a.qps = (int)nq; a.w = attn_weights; a.w_stride = T; a.scores = nullptr; a.stats = nullptr;
+    a.part = part; a.nsplit = ns;
+    hipLaunchKernelGGL(values_kernel<false>, dim3((unsigned)ns, (unsigned)((nq + 3) / 4), 1),
+                       dim3(kThreads), 0, st, a);
+    TQ_LAUNCH_CHECK("values_kernel");
+  }
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)nq), dim3(256), 0, st, part, ns, d, rotation_T,
+                     nullptr, 1, (int)TQ_F32, out);
+  TQ_LAUNCH_CHECK("combine_kernel");
+  return TQ_OK;
+}
+
+size_t tq_decode_workspace_bytes(int32_t B, int32_t hq, int32_t d, int64_t t_max) {
+  if (B <= 0 || hq <= 0 || d <= 0) return 0;
+  const size_t nq = (size_t)B * hq;
+  const int64_t ns = (t_max + kSplitTokens - 1) / kSplitTokens;
+  size_t bytes = lut_bytes((int64_t)nq, d, 4);
+  bytes += align_up(nq * (size_t)(t_max > 0 ? t_max : 1) * 4, 256);   // scores
+  bytes += align_up(nq * sizeof(float2), 256);                        // stats
+  bytes += align_up(nq * (size_t)(ns > 0 ? ns : 1) * d * 4, 256);     // partials
+  return bytes;
+}
+
+int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                               int32_t d, const uint8_t* kpacked, const float* knorms,
+                               const uint8_t* vpacked, const float* vnorms, int64_t t_max,
+                               const int32_t* seq_lens, const float* kcentroids,
+                               const float* vcentroids, const float* krotation,
+                               const float* vrotation, int32_t kbits, int32_t vbits, float scale,
+                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(kbits >= 1 && kbits <= 4 && vbits >= 1 && vbits <= 4, "bits must be 1-4");
+  TQ_REQUIRE(d >= 1 && d <= 256, "head_dim must be in [1, 256], got %d", d);
+  TQ_REQUIRE(B >= 0 && hq >= 1 && hkv >= 1 && hq % hkv == 0,
+             "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
+  TQ_REQUIRE(t_max >= 0, "bad t_max");
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  if (B == 0) return TQ_OK;
+  TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
+             "null pointer argument");
+  TQ_REQUIRE(t_max == 0 || (kpacked && knorms && vpacked && vnorms), "null pointer argument");
+  const size_t need = tq_decode_workspace_bytes(B, hq, d, t_max);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
+  hipStream_t st = as_stream(stream);
+  const int64_t nq = (int64_t)B * hq;
+  const int G = hq / hkv;
+  const int dpad = dpad_for(d);
+  const int ns = (int)((t_max + kSplitTokens - 1) / kSplitTokens);
+  char* ws = static_cast<char*>(workspace);
+  float* lut = reinterpret_cast<float*>(ws);
+  ws += lut_bytes(nq, d, 4);
+  float* scores = reinterpret_cast<float*>(ws);
+  ws += align_up((size_t)nq * (size_t)(t_max > 0 ? t_max : 1) * 4, 256);
+  float2* stats = reinterpret_cast<float2*>(ws);
+  ws += align_up((size_t)nq * sizeof(float2), 256);
+  float* part = reinterpret_cast<float*>(ws);
+  if (t_max > 0) {
+    int rc = launch_lut(q, q_dtype, nq, d, dpad, krotation, kcentroids, 1 << kbits, lut, st);
+    if (rc) return rc;
+    ScanArgs a{};
+    a.packed = kpacked; a.norms = knorms; a.stream_rows = t_max; a.nrows = t_max;
+    a.seq_lens = seq_lens; a.spb = hkv; a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad;
+    a.qps = G; a.post_scale = scale; a.k = 0; a.scores = scores;
+    rc = launch_scan(a, kbits, false, B * hkv, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(softmax_stats_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, scores,
+                       t_max, seq_lens, hq, stats);
+    TQ_LAUNCH_CHECK("softmax_stats_kernel");
+    ValuesArgs v{};
+    v.packed = vpacked; v.vnorms = vnorms; v.stream_rows = t_max; v.nrows = t_max;
+    v.seq_lens = seq_lens; v.spb = hkv; v.d = d; v.bits = vbits; v.cen = vcentroids; v.qps = G;
+    v.w = nullptr; v.w_stride = 0; v.scores = scores; v.stats = stats; v.part = part; v.nsplit = ns;
+    hipLaunchKernelGGL(values_kernel<true>,
+                       dim3((unsigned)ns, (unsigned)((G + 3) / 4), (unsigned)(B * hkv)),
+                       dim3(kThreads), 0, st, v);
+    TQ_LAUNCH_CHECK("values_kernel");
+  }
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)nq), dim3(256), 0, st, part, ns, d, vrotation,
+                     seq_lens, hq, (int)q_dtype, out);
+  TQ_LAUNCH_CHECK("combine_kernel");
+  return TQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+"""Direct wrappers of torch.ops.turboquant (mirrors turboquant_kv/ops.py:49-246).
+
+Unlike the reference's dispatch chain (Triton -> torch.ops -> Python, with every
+error swallowed, ops.py:51-56,159-179), each function here calls exactly one op
+and lets errors propagate.
+"""
+
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from turboquant_kv._lib import ops as _ops, require_device as _require_device
+
+
+def pack_codes(codes: torch.Tensor, bit_width: int) -> torch.Tensor:
+    _require_device(codes, "codes")
+    return _ops().pack_codes(codes, bit_width)
+
+
+def unpack_codes(packed: torch.Tensor, bit_width: int, dim: int) -> torch.Tensor:
+    _require_device(packed, "packed")
+    return _ops().unpack_codes(packed, bit_width, dim)
+
+
+def rotate_and_quantize(vectors: torch.Tensor, rotation: torch.Tensor, boundaries: torch.Tensor,
+                        bit_width: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(packed, norms fp32) of fp32-upcast vectors (ops.py:74-104)."""
+    _require_device(vectors, "vectors")
+    return _ops().rotate_and_quantize(vectors, rotation, boundaries, bit_width)
+
+
+def attention_scores_packed(query, packed_keys, key_norms, centroids, rotation, bit_width):
+    """scores[b, h, t] = n_t * (R q_bh) . c[code_t], no 1/sqrt(d) (ops.py:131-194)."""
+    _require_device(query, "query")
+    return _ops().attention_scores_packed(query, packed_keys, key_norms, centroids, rotation,
+                                          bit_width)
+
+
+def attention_values_packed(attn_weights, packed_values, value_norms, centroids, rotation_T,
+                            bit_width):
+    """out[b, h] = (sum_t w n_t c[code_t]) @ rotation_T; pass R itself to invert the
+    rotation (ops.py:202-246)."""
+    _require_device(attn_weights, "attn_weights")
+    return _ops().attention_values_packed(attn_weights, packed_values, value_norms, centroids,
+                                          rotation_T, bit_width)
+
+
+def ip_scan_topk(queries, packed, norms, centroids, rotation, bit_width, k):
+    """Top-k inner-product search over packed codes: (scores f32 [Q,k], ids i64 [Q,k])."""
+    _require_device(queries, "queries")
+    return _ops().ip_scan_topk(queries, packed, norms, centroids, rotation, bit_width, k)
+
+
+def decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcentroids,
+                            vcentroids, krotation, vrotation, kbits, vbits, scale):
+    """Fused GQA decode attention over packed K/V -> [B, Hq, d] in q.dtype."""
+    _require_device(q, "q")
+    return _ops().decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens,
+                                          kcentroids, vcentroids, krotation, vrotation, kbits,
+                                          vbits, float(scale))

@@ -1,0 +1,215 @@
+"""TurboQuantIndex: brute-force inner-product search over packed codes on the GPU.
+
+API of turboquant_kv/search.py:37-317.  The database lives on the device in a
+buffer that grows geometrically (the reference re-concatenates on every add,
+search.py:145-176).  MSE-mode search runs the fused ADC scan + top-k kernel: the
+query is rotated, a per-dimension query x centroid table is built, every packed
+row is scored from that table and the top k are kept with equal scores ordered by
+lower index (the order of the reference's C++ heap, turboquant_core.cpp:487-494).
+Queries are upcast to fp32 before rotation, as the reference's op and C++ paths do
+(ops.py:188; bindings.cpp:105); the reference's Python fallback computes in the query
+dtype (search.py:209-221).  Prod mode scores against dequantized vectors, as the
+reference does (search.py:229-252).
+
+save/load use the reference's Python file format (search.py:29-34, 254-317).
+"""
+
+from __future__ import annotations
+
+import struct
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+
+from turboquant_kv import ops
+from turboquant_kv._lib import ops as _ops
+from turboquant_kv.codebook import lloyd_max_codebook, make_qjl_matrix, make_rotation_matrix
+
+HEADER_FORMAT = "<BII"  # bit_width u8, dim u32, n_vectors u32
+HEADER_SIZE = struct.calcsize(HEADER_FORMAT)
+MODE_MSE = 0
+MODE_PROD = 1
+_SCAN_MAX_K = 32  # the fused top-k kernel's per-call limit
+
+
+class TurboQuantIndex:
+    def __init__(self, dim: int, bit_width: int = 3, mode: str = "mse", rotation: str = "dense_qr",
+                 seed: int = 42, device="cuda"):
+        if mode not in ("mse", "prod"):
+            raise ValueError(f"Unknown mode: {mode}")
+        self.dim = dim
+        self.bit_width = bit_width
+        self.mode = mode
+        self.rotation_method = rotation
+        self.seed = seed
+        self.device = torch.device(device)
+        self._use_cpp = False  # attribute of the reference API; the C++ core is not used
+        self._rotation = make_rotation_matrix(dim, seed=seed, method=rotation)
+        self._rot_dev = self._rotation.to(self.device)
+        if mode == "mse":
+            self._codebook = lloyd_max_codebook(bit_width, dim)
+            self._code_bits = bit_width
+        else:
+            self._codebook = lloyd_max_codebook(bit_width - 1, dim)
+            self._code_bits = bit_width - 1
+            self._S_matrix = make_qjl_matrix(dim, dim, seed)
+            self._S_dev = self._S_matrix.to(self.device)
+        self._bnd = self._codebook[0].to(self.device)
+        self._cen = self._codebook[1].to(self.device)
+        self.n_vectors = 0
+        self._cap = 0
+        self._packed_buf: Optional[torch.Tensor] = None
+        self._norm_buf: Optional[torch.Tensor] = None
+        self._sign_buf: Optional[torch.Tensor] = None
+        self._res_buf: Optional[torch.Tensor] = None
+
+    # ------------------------------------------------------------------ storage views
+    @property
+    def _packed_codes(self) -> Optional[torch.Tensor]:
+        return None if self._packed_buf is None else self._packed_buf[: self.n_vectors]
+
+    @property
+    def _norms(self) -> Optional[torch.Tensor]:
+        return None if self._norm_buf is None else self._norm_buf[: self.n_vectors]
+
+    @property
+    def _qjl_signs(self) -> Optional[torch.Tensor]:
+        return None if self._sign_buf is None else self._sign_buf[: self.n_vectors]
+
+    @property
+    def _residual_norms(self) -> Optional[torch.Tensor]:
+        return None if self._res_buf is None else self._res_buf[: self.n_vectors]
+
+    def _reserve(self, n_total: int) -> None:
+        if n_total <= self._cap:
+            return
+        cap = max(n_total, 2 * self._cap, 1024)
+        bpp = (self.dim + 7) // 8
+        dev = self.device
+
+        def grow(old, shape, dtype):
+            new = torch.empty(shape, dtype=dtype, device=dev)
+            if old is not None and self.n_vectors:
+                new[: self.n_vectors] = old[: self.n_vectors]
+            return new
+
+        self._packed_buf = grow(self._packed_buf, (cap, self._code_bits * bpp), torch.uint8)
+        self._norm_buf = grow(self._norm_buf, (cap,), torch.float32)
+        if self.mode == "prod":
+            self._sign_buf = grow(self._sign_buf, (cap, bpp), torch.uint8)
+            self._res_buf = grow(self._res_buf, (cap,), torch.float32)
+        self._cap = cap
+
+    @classmethod
+    def from_vectors(cls, vectors: torch.Tensor, bit_width: int = 3, mode: str = "mse",
+                     rotation: str = "dense_qr", seed: int = 42, device=None) -> "TurboQuantIndex":
+        if device is None:
+            device = vectors.device if vectors.is_cuda else "cuda"
+        idx = cls(dim=vectors.shape[-1], bit_width=bit_width, mode=mode, rotation=rotation,
+                  seed=seed, device=device)
+        idx.add(vectors)
+        return idx
+
+    def add(self, vectors: torch.Tensor) -> None:
+        """Quantize (N, dim) or (dim,) vectors on the device and append them."""
+        if vectors.dim() == 1:
+            vectors = vectors.unsqueeze(0)
+        if vectors.shape[-1] != self.dim:
+            raise ValueError(f"expected dim {self.dim}, got {vectors.shape[-1]}")
+        x = vectors.to(self.device)
+        if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            x = x.float()
+        n = x.shape[0]
+        if n == 0:
+            return
+        self._reserve(self.n_vectors + n)
+        sl = slice(self.n_vectors, self.n_vectors + n)
+        if self.mode == "mse":
+            p, nm = _ops().quantize_mse_packed(x, self._rot_dev, self._bnd, self.bit_width)
+            self._packed_buf[sl] = p
+            self._norm_buf[sl] = nm.float()
+        else:
+            mp, sg, rn, nm = _ops().quantize_prod_packed(x, self._rot_dev, self._bnd, self._cen,
+                                                         self._S_dev, self.bit_width)
+            self._packed_buf[sl] = mp
+            self._sign_buf[sl] = sg
+            self._res_buf[sl] = rn.float()
+            self._norm_buf[sl] = nm.float()
+        self.n_vectors += n
+
+    def search(self, queries: torch.Tensor, k: int = 10) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Top-k inner products: (scores (Q, k'), indices (Q, k')) with k' = min(k, n_vectors)."""
+        if queries.dim() == 1:
+            queries = queries.unsqueeze(0)
+        assert self.n_vectors > 0, "Index is empty"
+        q = queries.to(self.device)
+        k = min(k, self.n_vectors)
+        if self.mode == "mse":
+            if k <= _SCAN_MAX_K:
+                return ops.ip_scan_topk(q, self._packed_codes, self._norms, self._cen,
+                                        self._rot_dev, self.bit_width, k)
+            s = ops.attention_scores_packed(q.float().unsqueeze(0), self._packed_codes,
+                                            self._norms, self._cen, self._rot_dev,
+                                            self.bit_width)[0]
+            top = torch.topk(s, k, dim=-1)
+            return top.values, top.indices
+        recon = _ops().dequantize_prod_packed(self._packed_codes, self._qjl_signs,
+                                              self._residual_norms, self._norms, self._cen,
+                                              self._rot_dev, self._S_dev, self.bit_width, self.dim)
+        scores = q.float() @ recon.t()
+        top = torch.topk(scores, k, dim=-1)
+        return top.values, top.indices
+
+    # ------------------------------------------------------------------ persistence
+    def save(self, path: str) -> None:
+        """header <BII (bit_width, dim, n) + mode byte + packed + norms f32
+        [+ signs + residual norms f32] (search.py:254-275)."""
+        mode_byte = MODE_MSE if self.mode == "mse" else MODE_PROD
+        with open(path, "wb") as f:
+            f.write(struct.pack(HEADER_FORMAT, self.bit_width, self.dim, self.n_vectors))
+            f.write(struct.pack("<B", mode_byte))
+            if self.n_vectors:
+                f.write(self._packed_codes.cpu().numpy().tobytes())
+                f.write(self._norms.cpu().numpy().astype(np.float32).tobytes())
+                if self.mode == "prod":
+                    f.write(self._qjl_signs.cpu().numpy().tobytes())
+                    f.write(self._residual_norms.cpu().numpy().astype(np.float32).tobytes())
+
+    @classmethod
+    def load(cls, path: str, rotation: str = "dense_qr", seed: int = 42,
+             device="cuda") -> "TurboQuantIndex":
+        with open(path, "rb") as f:
+            head = f.read(HEADER_SIZE)
+            if len(head) != HEADER_SIZE:
+                raise ValueError(f"{path}: truncated header")
+            bit_width, dim, n = struct.unpack(HEADER_FORMAT, head)
+            mb = f.read(1)
+            if len(mb) != 1:
+                raise ValueError(f"{path}: truncated header")
+            mode = "mse" if mb[0] == MODE_MSE else "prod"
+            bpp = (dim + 7) // 8
+            code_bits = bit_width if mode == "mse" else bit_width - 1
+
+            def take(nbytes):
+                buf = f.read(nbytes)
+                if len(buf) != nbytes:
+                    raise ValueError(f"{path}: truncated body")
+                return buf
+
+            packed = np.frombuffer(take(code_bits * bpp * n), dtype=np.uint8).reshape(n, -1)
+            norms = np.frombuffer(take(4 * n), dtype=np.float32)
+            if mode == "prod":
+                signs = np.frombuffer(take(bpp * n), dtype=np.uint8).reshape(n, -1)
+                res = np.frombuffer(take(4 * n), dtype=np.float32)
+        idx = cls(dim=dim, bit_width=bit_width, mode=mode, rotation=rotation, seed=seed,
+                  device=device)
+        if n:
+            idx._reserve(n)
+            idx._packed_buf[:n] = torch.from_numpy(packed.copy()).to(idx.device)
+            idx._norm_buf[:n] = torch.from_numpy(norms.copy()).to(idx.device)
+            if mode == "prod":
+                idx._sign_buf[:n] = torch.from_numpy(signs.copy()).to(idx.device)
+                idx._res_buf[:n] = torch.from_numpy(res.copy()).to(idx.device)
+        idx.n_vectors = n
+        return idx
