@@ -24,13 +24,21 @@ DEV = "cuda"
 L = capi.lib
 
 
+_ALIVE = []
+
+
 def T(a, dtype=None):
+    """Device copy of a numpy array, kept alive until the next wrapper call: a pointer
+    handed to the C ABI must outlive the asynchronous kernel that reads it."""
     t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    return t if dtype is None else t.to(dtype)
+    t = t if dtype is None else t.to(dtype)
+    _ALIVE.append(t)
+    return t
 
 
 def sync():
     torch.cuda.synchronize()
+    _ALIVE.clear()
 
 
 # ------------------------------------------------------------------ wrappers

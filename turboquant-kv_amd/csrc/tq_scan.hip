@@ -45,6 +45,9 @@ constexpr int kSplitTokens = 1024;    // tokens per values split (decode / value
 __global__ void lut_kernel(const void* __restrict__ q, int q_dt, int d, int dpad,
                            const float* __restrict__ rot, const float* __restrict__ cen, int nlev,
                            float* __restrict__ lut) {
+  // Separate multiply and add roundings, exactly as the reference's C++ core; HIP
+  // would otherwise contract them into FMAs.
+#pragma clang fp contract(off)
   __shared__ float qs[256];
   const int qg = blockIdx.x;
   for (int k = threadIdx.x; k < d; k += blockDim.x) qs[k] = load_as_f32(q, (int64_t)qg * d + k, q_dt);
@@ -54,9 +57,9 @@ __global__ void lut_kernel(const void* __restrict__ q, int q_dt, int d, int dpad
     float v = 0.f;
     if (j < d) {
       const float* r = rot + (size_t)j * d;
-      for (int k = 0; k < d; ++k) v = __fadd_rn(v, __fmul_rn(qs[k], r[k]));
+      for (int k = 0; k < d; ++k) v = v + qs[k] * r[k];
     }
-    for (int l = 0; l < nlev; ++l) out[(size_t)j * nlev + l] = (j < d) ? __fmul_rn(v, cen[l]) : 0.f;
+    for (int l = 0; l < nlev; ++l) out[(size_t)j * nlev + l] = (j < d) ? v * cen[l] : 0.f;
   }
 }
 
