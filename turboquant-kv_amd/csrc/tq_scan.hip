@@ -57,7 +57,17 @@ __global__ void lut_kernel(const void* __restrict__ q, int q_dt, int d, int dpad
     float v = 0.f;
     if (j < d) {
       const float* r = rot + (size_t)j * d;
-      for (int k = 0; k < d; ++k) v = v + qs[k] * r[k];
+      if ((d & 3) == 0) {
+        for (int k = 0; k < d; k += 4) {
+          const float4 r4 = *reinterpret_cast<const float4*>(r + k);
+          v = v + qs[k] * r4.x;
+          v = v + qs[k + 1] * r4.y;
+          v = v + qs[k + 2] * r4.z;
+          v = v + qs[k + 3] * r4.w;
+        }
+      } else {
+        for (int k = 0; k < d; ++k) v = v + qs[k] * r[k];
+      }
     }
     for (int l = 0; l < nlev; ++l) out[(size_t)j * nlev + l] = (j < d) ? v * cen[l] : 0.f;
   }
@@ -95,20 +105,20 @@ struct RowLoader {
       const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
 #pragma unroll
       for (int i = 0; i < P / 16; ++i) {
-        const u32x4 v = __builtin_nontemporal_load(r4 + i);
+        const u32x4 v = r4[i];
         wd[4 * i + 0] = v.x; wd[4 * i + 1] = v.y; wd[4 * i + 2] = v.z; wd[4 * i + 3] = v.w;
       }
     } else if constexpr (P % 8 == 0) {
       const u32x2* r2 = reinterpret_cast<const u32x2*>(row);
 #pragma unroll
       for (int i = 0; i < P / 8; ++i) {
-        const u32x2 v = __builtin_nontemporal_load(r2 + i);
+        const u32x2 v = r2[i];
         wd[2 * i + 0] = v.x; wd[2 * i + 1] = v.y;
       }
     } else {
       const uint32_t* r1 = reinterpret_cast<const uint32_t*>(row);
 #pragma unroll
-      for (int i = 0; i < NW; ++i) wd[i] = __builtin_nontemporal_load(r1 + i);
+      for (int i = 0; i < NW; ++i) wd[i] = r1[i];
     }
   }
 };
@@ -134,10 +144,11 @@ __device__ __forceinline__ void load_generic(const uint8_t* __restrict__ row, in
   }
 }
 
-// Byte address (code * 8) of every dim of one 32-dim word group, for QB tables.
+// Byte address (code * SC) of every dim of one 32-dim word group.
 // A[p] = word w of plane p.  Calls f(dim_in_group, addr8) for dims 0..31 in order.
-template <int BITS, typename F>
-__device__ __forceinline__ void decode_group(const uint32_t (&A)[4], F&& f) {
+template <int BITS, int SC, typename F, typename G>
+__device__ __forceinline__ void decode_group(const uint32_t (&A)[4], F&& f, G&& after_octet) {
+  static_assert(SC == 8 || SC == 16, "code stride");
   const uint32_t a0 = A[0];
   const uint32_t a1 = BITS > 1 ? A[1] : 0u;
   const uint32_t a2 = BITS > 2 ? A[2] : 0u;
@@ -162,10 +173,14 @@ __device__ __forceinline__ void decode_group(const uint32_t (&A)[4], F&& f) {
       const int s = (i >= 4) ? (7 - i) : (3 - i);
       const uint32_t src = (i >= 4) ? xh : xl;
       const uint32_t z = src & (0x01010101u << s);
-      const uint32_t w = (s == 0) ? 0x40201008u : (s == 1) ? 0x20100804u
-                       : (s == 2) ? 0x10080402u : 0x08040201u;
+      // byte p of the weight = SC * 2^p / 2^s, so the dot product is code * SC
+      const uint32_t w = SC == 8 ? ((s == 0) ? 0x40201008u : (s == 1) ? 0x20100804u
+                                  : (s == 2) ? 0x10080402u : 0x08040201u)
+                                 : ((s == 0) ? 0x80402010u : (s == 1) ? 0x40201008u
+                                  : (s == 2) ? 0x20100804u : 0x10080402u);
       f(8 * m + i, __builtin_amdgcn_udot4(z, w, 0u, false));
     }
+    after_octet();
   }
 }
 
@@ -211,11 +226,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   constexpr int QSTRIDE = DP * NLEV * 4;            // bytes per query table
   constexpr int NW = GENERIC ? BITS * 8 : RowLoader<BITS, BPP>::NW;
   constexpr int WPP = BPPT / 4;                     // words per plane
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  char* lut_s = smem;
-  float* cand_s = reinterpret_cast<float*>(smem + QB * QSTRIDE);
-  int* cand_i = reinterpret_cast<int*>(cand_s + kWaves * QB * kCandCap);
-  int* cnt_s = cand_i + kWaves * QB * kCandCap;
+  // Static LDS: the table's base address is a link-time constant, so every lookup is a
+  // ds_read with an immediate offset and no address add.
+  __shared__ __attribute__((aligned(16))) char lut_s[QB * QSTRIDE];
+  __shared__ float cand_s[TOPK ? kWaves * QB * kCandCap : 1];
+  __shared__ int cand_i[TOPK ? kWaves * QB * kCandCap : 1];
+  __shared__ int cnt_s[TOPK ? kWaves * QB : 1];
 
   const int s = blockIdx.z;
   const int qb = blockIdx.y;
@@ -229,14 +245,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   const int nq = min(QB, a.qps - qb * QB);       // valid queries in this block
   const int P = BITS * a.bpp;
 
-  // Stage the tables: lut_s[qi][(j>>1)*NLEV*8 + l*8 + (j&1)*4].
+  // Stage the tables.  QB == 1: entry (j, l) at (j>>1)*NLEV*8 + l*8 + (j&1)*4 (two dims
+  // interleaved, 8-byte code stride).  QB > 1: the QB queries' entries of (j, l) are
+  // contiguous at (j*NLEV + l)*QB*4, so one 8/16-byte read serves every query.
   for (int idx = threadIdx.x; idx < QB * DP * NLEV; idx += kThreads) {
     const int qi = idx / (DP * NLEV);
     const int rem = idx - qi * DP * NLEV;
     const int j = rem / NLEV, l = rem - j * NLEV;
     float v = 0.f;
     if (qi < nq && j < a.dpad) v = a.lut[((size_t)(q0 + qi) * a.dpad + j) * NLEV + l];
-    *reinterpret_cast<float*>(lut_s + qi * QSTRIDE + (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4) = v;
+    const int off = QB == 1 ? (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4
+                            : (j * NLEV + l) * QB * 4 + qi * 4;
+    *reinterpret_cast<float*>(lut_s + off) = v;
   }
   __syncthreads();
 
@@ -257,21 +277,21 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
 
   uint32_t cur[NW];
   int64_t row = rbeg + wave * 64 + lane;
+  // Loads are unconditional (rows past the end re-read the last row and are masked
+  // when scored): a branch around them would make the compiler wait for every
+  // outstanding load, including the next row's prefetch, before each row.
+  const int64_t rlast = rend - 1;
   auto load_row = [&](int64_t r, uint32_t (&w)[NW]) {
-    if (r < rend) {
-      if constexpr (GENERIC) load_generic<BITS>(base + r * P, a.bpp, w);
-      else RowLoader<BITS, BPP>::load(base + r * P, w);
-    } else {
-#pragma unroll
-      for (int i = 0; i < NW; ++i) w[i] = 0u;
-    }
+    const int64_t rl = r < rend ? r : rlast;
+    if constexpr (GENERIC) load_generic<BITS>(base + rl * P, a.bpp, w);
+    else RowLoader<BITS, BPP>::load(base + rl * P, w);
   };
-  load_row(row, cur);
+  if (rbeg < rend) load_row(row, cur);
   for (int64_t step0 = rbeg + wave * 64; step0 < rend; step0 += kWaves * 64) {
     const int64_t nxt_row = row + kWaves * 64;
     uint32_t nxt[NW];
     load_row(nxt_row, nxt);
-    const float nrm = row < rend ? __builtin_nontemporal_load(nbase + row) : 0.f;
+    const float nrm = __builtin_nontemporal_load(nbase + (row < rend ? row : rlast));
 
     float acc[QB];
 #pragma unroll
@@ -281,12 +301,28 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
       uint32_t A[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) A[p] = (p < BITS) ? cur[p * WPP + w] : 0u;
-      decode_group<BITS>(A, [&](int di, uint32_t addr8) {
+      constexpr int SC = QB == 4 ? 16 : 8;
+      decode_group<BITS, SC>(A, [&](int di, uint32_t addr) {
         const int j = 32 * w + di;
-        const int off = (j >> 1) * NLEV * 8 + (j & 1) * 4;
-#pragma unroll
-        for (int qi = 0; qi < QB; ++qi)
-          acc[qi] += *reinterpret_cast<const float*>(lut_s + qi * QSTRIDE + off + addr8);
+        if constexpr (QB == 1) {
+          acc[0] += *reinterpret_cast<const float*>(lut_s + (j >> 1) * NLEV * 8 + (j & 1) * 4 + addr);
+        } else if constexpr (QB == 2) {
+          const float2 v = *reinterpret_cast<const float2*>(lut_s + j * NLEV * 8 + addr);
+          acc[0] += v.x;
+          acc[1] += v.y;
+        } else {
+          const float4 v = *reinterpret_cast<const float4*>(lut_s + j * NLEV * 16 + addr);
+          acc[0] += v.x;
+          acc[1] += v.y;
+          acc[2] += v.z;
+          acc[3] += v.w;
+        }
+      }, [&]() {
+        // Multi-query tables return 8-16 bytes per lookup; without this the compiler
+        // issues every lookup of the row before the adds and spills.  Pinning the
+        // accumulators here makes each octet's adds complete in order.
+        if constexpr (QB == 2) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+        if constexpr (QB == 4) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
       });
     }
 
@@ -376,36 +412,100 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
 
 // ------------------------------------------------------------------ merge
 constexpr int kMergeCap = 2048;
+constexpr int kMaxBlocksPerLane = 8;  // merge handles up to 64 * 4 * 8 = 2048 block lists
 
+// Wave-wide arg-best over per-lane candidates (score desc, id asc); returns the
+// winner's (score, id) in every lane.  Lanes with id == INT_MAX hold nothing.
+__device__ __forceinline__ void wave_best(float& s, int& id) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float so = __shfl_xor(s, off, 64);
+    const int io = __shfl_xor(id, off, 64);
+    if (io != INT_MAX && (id == INT_MAX || better(so, io, s, id))) { s = so; id = io; }
+  }
+}
+
+// Per query: the k-th best of the per-block maxima is a lower bound of the k-th best
+// score overall (those k maxima are k distinct rows), so only candidates at or above
+// it can be in the answer.  The survivors are rank-sorted.
 __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
                                                          const int32_t* __restrict__ part_i,
                                                          int nblocks, int k, float* __restrict__ out_s,
                                                          int64_t* __restrict__ out_i) {
-  __shared__ float red[kThreads];
+  __shared__ float wbest_s[kWaves * kMaxK];
+  __shared__ int wbest_i[kWaves * kMaxK];
   __shared__ float ss[kMergeCap];
   __shared__ int si[kMergeCap];
   __shared__ int nsurv;
+  __shared__ float tau_s;
   const int q = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* ps = part_s + (size_t)q * nblocks * k;
   const int32_t* pi = part_i + (size_t)q * nblocks * k;
-  // tau = max over blocks of the block's k-th best (its last valid entry when full).
-  float t = -INFINITY;
-  for (int b = threadIdx.x; b < nblocks; b += kThreads) {
-    if (pi[(size_t)b * k + k - 1] >= 0) t = fmaxf(t, ps[(size_t)b * k + k - 1]);
+  // 1. each wave: its k best block maxima (block b's list is sorted, entry 0 = its max)
+  float ms[kMaxBlocksPerLane];
+  int mi[kMaxBlocksPerLane];
+#pragma unroll
+  for (int r = 0; r < kMaxBlocksPerLane; ++r) {
+    const int b = threadIdx.x + r * kThreads;
+    const bool ok = b < nblocks && pi[(size_t)b * k] >= 0;
+    ms[r] = ok ? ps[(size_t)b * k] : -INFINITY;
+    mi[r] = ok ? pi[(size_t)b * k] : INT_MAX;
   }
-  red[threadIdx.x] = t;
+  for (int r = 0; r < k; ++r) {
+    float bs = -INFINITY;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int t = 0; t < kMaxBlocksPerLane; ++t)
+      if (mi[t] != INT_MAX && (bi == INT_MAX || better(ms[t], mi[t], bs, bi))) { bs = ms[t]; bi = mi[t]; }
+    wave_best(bs, bi);
+#pragma unroll
+    for (int t = 0; t < kMaxBlocksPerLane; ++t)
+      if (mi[t] == bi) mi[t] = INT_MAX;  // ids are unique: consume the winner
+    if (lane == 0) { wbest_s[wave * kMaxK + r] = bs; wbest_i[wave * kMaxK + r] = bi; }
+  }
   if (threadIdx.x == 0) nsurv = 0;
   __syncthreads();
-  for (int st = kThreads / 2; st > 0; st >>= 1) {
-    if (threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
-    __syncthreads();
+  // 2. wave 0: k-th best of the 4k wave winners -> tau
+  if (wave == 0) {
+    float cs[kWaves];
+    int ci[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const bool ok = lane < k;
+      cs[w] = ok ? wbest_s[w * kMaxK + lane] : -INFINITY;
+      ci[w] = ok ? wbest_i[w * kMaxK + lane] : INT_MAX;
+    }
+    float last = -INFINITY;
+    int last_i = INT_MAX;
+    for (int r = 0; r < k; ++r) {
+      float bs = -INFINITY;
+      int bi = INT_MAX;
+#pragma unroll
+      for (int t = 0; t < kWaves; ++t)
+        if (ci[t] != INT_MAX && (bi == INT_MAX || better(cs[t], ci[t], bs, bi))) { bs = cs[t]; bi = ci[t]; }
+      wave_best(bs, bi);
+#pragma unroll
+      for (int t = 0; t < kWaves; ++t)
+        if (ci[t] == bi) ci[t] = INT_MAX;
+      last = bs;
+      last_i = bi;
+    }
+    if (lane == 0) tau_s = (last_i == INT_MAX) ? -INFINITY : last;
   }
-  const float tau = red[0];
+  __syncthreads();
+  const float tau = tau_s;
+  // 3. survivors: only lists whose maximum reaches tau can hold any, and each list
+  // is sorted, so a list is read only until its first entry below tau.
   const int total = nblocks * k;
-  for (int e = threadIdx.x; e < total; e += kThreads) {
-    const int id = pi[e];
-    const float sc = ps[e];
-    if (id >= 0 && sc >= tau) {
+#pragma unroll
+  for (int r = 0; r < kMaxBlocksPerLane; ++r) {
+    const int b = threadIdx.x + r * kThreads;
+    if (b >= nblocks || !(ms[r] >= tau) || pi[(size_t)b * k] < 0) continue;
+    for (int e = 0; e < k; ++e) {
+      const int id = pi[(size_t)b * k + e];
+      const float sc = ps[(size_t)b * k + e];
+      if (id < 0 || !(sc >= tau)) break;
       const int pos = atomicAdd(&nsurv, 1);
       if (pos < kMergeCap) { ss[pos] = sc; si[pos] = id; }
     }
@@ -423,44 +523,35 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
       if (rank < k) { os[rank] = se; oi[rank] = ie; }
     }
     for (int e = m + threadIdx.x; e < k; e += kThreads) { os[e] = -INFINITY; oi[e] = -1; }
-  } else {
-    // Many exact ties at tau: k rounds of block arg-best over every candidate.
-    __shared__ float bs[kThreads];
-    __shared__ int bi[kThreads];
-    float last_s = INFINITY;
-    int last_i = -1;
-    for (int r = 0; r < k; ++r) {
-      float cs = -INFINITY;
-      int ci = INT_MAX;
-      bool have = false;
-      for (int e = threadIdx.x; e < total; e += kThreads) {
-        const int id = pi[e];
-        const float sc = ps[e];
-        if (id < 0 || !better(last_s, last_i, sc, id)) continue;  // already emitted
-        if (!have || better(sc, id, cs, ci)) { cs = sc; ci = id; have = true; }
-      }
-      bs[threadIdx.x] = cs;
-      bi[threadIdx.x] = have ? ci : INT_MAX;
-      __syncthreads();
-      for (int st = kThreads / 2; st > 0; st >>= 1) {
-        if (threadIdx.x < st) {
-          const bool ob = bi[threadIdx.x + st] != INT_MAX;
-          const bool mb = bi[threadIdx.x] != INT_MAX;
-          if (ob && (!mb || better(bs[threadIdx.x + st], bi[threadIdx.x + st], bs[threadIdx.x],
-                                   bi[threadIdx.x]))) {
-            bs[threadIdx.x] = bs[threadIdx.x + st];
-            bi[threadIdx.x] = bi[threadIdx.x + st];
-          }
-        }
-        __syncthreads();
-      }
-      last_s = bs[0];
-      last_i = bi[0];
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        os[r] = last_i == INT_MAX ? -INFINITY : last_s;
-        oi[r] = last_i == INT_MAX ? -1 : last_i;
-      }
+    return;
+  }
+  // 4. more than kMergeCap rows tie at tau: k rounds of block arg-best over everything
+  __shared__ float bs_s[kWaves];
+  __shared__ int bi_s[kWaves];
+  float last_s = INFINITY;
+  int last_i = -1;
+  for (int r = 0; r < k; ++r) {
+    float cs = -INFINITY;
+    int ci = INT_MAX;
+    for (int e = threadIdx.x; e < total; e += kThreads) {
+      const int id = pi[e];
+      const float sc = ps[e];
+      if (id < 0 || !better(last_s, last_i, sc, id)) continue;  // emitted already
+      if (ci == INT_MAX || better(sc, id, cs, ci)) { cs = sc; ci = id; }
+    }
+    wave_best(cs, ci);
+    if (lane == 0) { bs_s[wave] = cs; bi_s[wave] = ci; }
+    __syncthreads();
+    cs = bs_s[0];
+    ci = bi_s[0];
+    for (int w = 1; w < kWaves; ++w)
+      if (bi_s[w] != INT_MAX && (ci == INT_MAX || better(bs_s[w], bi_s[w], cs, ci))) { cs = bs_s[w]; ci = bi_s[w]; }
+    __syncthreads();
+    last_s = cs;
+    last_i = ci;
+    if (threadIdx.x == 0) {
+      os[r] = ci == INT_MAX ? -INFINITY : cs;
+      oi[r] = ci == INT_MAX ? -1 : ci;
     }
   }
 }
@@ -646,28 +737,25 @@ __global__ void combine_kernel(const float* __restrict__ part, int nsplit, int d
 // ------------------------------------------------------------------ host helpers
 int scan_blocks(int64_t nrows) {
   const int64_t want = (nrows + 64 * 8 * kWaves - 1) / (64 * 8 * kWaves);  // >= 8 steps per wave
-  const int64_t cap = (int64_t)device_cu_count() * 4;
+  int64_t cap = (int64_t)device_cu_count() * 4;
+  if (cap > (int64_t)kThreads * kMaxBlocksPerLane) cap = (int64_t)kThreads * kMaxBlocksPerLane;
   int64_t b = want < cap ? want : cap;
   return (int)(b < 1 ? 1 : b);
 }
 
 template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
 int launch_scan_t(const ScanArgs& a, dim3 grid, hipStream_t st) {
-  constexpr int NLEV = 1 << BITS;
-  constexpr int BPPT = GENERIC ? 32 : BPP;
-  constexpr size_t lut_bytes = (size_t)QB * 8 * BPPT * NLEV * 4;
-  constexpr size_t cand_bytes = TOPK ? (size_t)kWaves * QB * kCandCap * 8 + kWaves * QB * 4 : 0;
-  constexpr size_t smem = lut_bytes + cand_bytes;
-  auto kern = scan_kernel<BITS, BPP, QB, TOPK, GENERIC>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    TQ_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-    attr_set = true;
-  }
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, a);
+  static_assert(QB * 8 * (GENERIC ? 32 : BPP) * (1 << BITS) * 4 <= 48 * 1024, "table too large");
+  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC>), grid, dim3(kThreads), 0, st, a);
   TQ_LAUNCH_CHECK("scan_kernel");
   return TQ_OK;
+}
+
+// Queries per block: 4 for the 64/128-dim layouts, 2 for the generic (256-dim) one.
+inline int queries_per_block(const ScanArgs& a) {
+  const bool fast = a.bpp == 8 || a.bpp == 16;
+  if (a.qps < 2) return 1;
+  return fast ? 4 : 2;
 }
 
 template <int BITS, bool TOPK>
@@ -683,12 +771,14 @@ int launch_scan_bits(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
     return qb == 4 ? launch_scan_t<BITS, 8, 4, TOPK, false>(a, grid, st)
                    : launch_scan_t<BITS, 8, 1, TOPK, false>(a, grid, st);
   }
-  return qb == 4 ? launch_scan_t<BITS, 32, 4, TOPK, true>(a, grid, st)
+  return qb >= 2 ? launch_scan_t<BITS, 32, 2, TOPK, true>(a, grid, st)
                  : launch_scan_t<BITS, 32, 1, TOPK, true>(a, grid, st);
 }
 
 int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st) {
-  const int qb = a.qps >= 2 ? 4 : 1;
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
+  int qb = queries_per_block(a);
+  if (!aligned && qb > 2) qb = 2;
   const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
   dim3 grid(topk ? (unsigned)scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
             (unsigned)((a.qps + qb - 1) / qb), (unsigned)nstreams);
