@@ -160,7 +160,9 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
  *   q [B, hq, d] of q_dtype; kpacked [B, hkv, t_max, kb*ceil(d/8)], knorms
  *   [B, hkv, t_max] fp32; vpacked/vnorms likewise with vb; seq_lens [B] int32 on
  *   the device (tokens 0..seq_lens[b]-1 are attended); out [B, hq, d] of q_dtype.
- *   d in {64, 128}; kb, vb in 2..4.  Needs tq_decode_workspace_bytes(...).
+ *   lse: optional fp32 [B, hq] (NULL to skip) receiving max_t s_t + log(sum_t exp(s_t - max)),
+ *   -inf for an empty sequence, so callers can merge further tokens by log-sum-exp.
+ *   d <= 256; kb, vb in 1..4.  Needs tq_decode_workspace_bytes(...).
  */
 size_t tq_decode_workspace_bytes(int32_t B, int32_t hq, int32_t d, int64_t t_max);
 int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
@@ -169,7 +171,8 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                                int64_t t_max, const int32_t* seq_lens, const float* kcentroids,
                                const float* vcentroids, const float* krotation,
                                const float* vrotation, int32_t kbits, int32_t vbits, float scale,
-                               void* out, void* workspace, size_t workspace_bytes, void* stream);
+                               void* out, float* lse, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 #ifdef __cplusplus
 }

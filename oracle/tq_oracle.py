@@ -304,7 +304,7 @@ def values_f64(w, packed, norms, cen, M, bits):
 
 
 def decode_attention_f64(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, Rk, Rv, kbits,
-                         vbits, scale):
+                         vbits, scale, return_lse=False):
     """float64 GQA decode attention over packed K/V (cache.py:282-339 + softmax,
     vllm_plugin/__init__.py:400), q head h reading kv head h // (Hq / Hkv).
     q [B, Hq, d]; kpacked [B, Hkv, T, Pk]; knorms [B, Hkv, T]; -> [B, Hq, d]."""
@@ -313,6 +313,7 @@ def decode_attention_f64(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, 
     Hkv = kpacked.shape[1]
     G = Hq // Hkv
     out = np.zeros((B, Hq, d))
+    lse = np.full((B, Hq), -np.inf)
     for b in range(B):
         T = int(seq_lens[b])
         if T == 0:
@@ -325,6 +326,7 @@ def decode_attention_f64(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, 
             for h in range(g * G, (g + 1) * G):
                 s = (K @ q[b, h]) * scale
                 p = np.exp(s - s.max())
+                lse[b, h] = s.max() + np.log(p.sum())
                 p /= p.sum()
                 out[b, h] = p @ V
-    return out
+    return (out, lse) if return_lse else out

@@ -117,6 +117,7 @@ def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
     B, Hq, d = q_t.shape
     Hkv, Tm = kp.shape[1], kp.shape[2]
     out = torch.empty_like(q_t)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
     ws = torch.empty(max(L().tq_decode_workspace_bytes(B, Hq, d, Tm), 1), dtype=torch.uint8, device=DEV)
     dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
     sl = T(np.asarray(seq_lens, np.int32))
@@ -124,9 +125,9 @@ def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
         capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(T(kp)),
         capi.p(T(kn)), capi.p(T(vp)), capi.p(T(vn)), capi.i64(Tm), capi.p(sl), capi.p(T(kc)),
         capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(kb), capi.i32(vb), ctypes.c_float(scale),
-        capi.p(out), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+        capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
     sync()
-    return out.float().cpu().numpy()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
 
 
 CASES = {"d128": (128, (2, 3, 4)), "d200": (200, (3, 4)), "d64": (64, (2, 3, 4))}
@@ -343,12 +344,15 @@ def test_decode_attention_vs_f64(d, kb, vb):
     kn, vn = kn.reshape(B, Hkv, Tm), vn.reshape(B, Hkv, Tm)
     q = rs.randn(B, Hq, d).astype(np.float32)
     scale = 1.0 / math.sqrt(d)
-    want = O.decode_attention_f64(q, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
-    got = k_decode(T(q), kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
-    assert np.all(got[1] == 0)  # empty sequence -> zeros
+    want, want_lse = O.decode_attention_f64(q, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale,
+                                            return_lse=True)
+    got, lse = k_decode(T(q), kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
+    assert np.all(got[1] == 0) and np.isneginf(lse[1]).all()  # empty sequence
     assert np.max(np.abs(got - want)) <= 1e-3 * np.max(np.abs(want))
+    ok = np.isfinite(want_lse)
+    assert np.max(np.abs(lse[ok] - want_lse[ok])) <= 1e-4 * np.max(np.abs(want_lse[ok]))
     qb = torch.from_numpy(q).to(DEV).to(torch.bfloat16)
     want_b = O.decode_attention_f64(qb.float().cpu().numpy(), kp, kn, vp, vn, seq, ck, cv, Rk, Rv,
                                     kb, vb, scale)
-    got_b = k_decode(qb, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
+    got_b, _ = k_decode(qb, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
     assert np.max(np.abs(got_b - want_b)) <= 1e-2 * np.max(np.abs(want_b))

@@ -51,7 +51,7 @@ def test_capi_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(lib, s), s
     lib.tq_abi_version.restype = ctypes.c_int
-    assert lib.tq_abi_version() == 1
+    assert lib.tq_abi_version() == 2
 
 
 @pytest.mark.skipif(not _built(), reason="native library not built")
@@ -67,7 +67,7 @@ def test_capi_rejects_bad_arguments_without_launching():
     assert rc == 1 and b"k must be" in lib.tq_last_error()
     rc = lib.tq_decode_attention_packed(z, 0, capi.i32(1), capi.i32(6), capi.i32(4), capi.i32(64),
                                         z, z, z, z, capi.i64(8), z, z, z, z, z, capi.i32(4),
-                                        capi.i32(2), ctypes.c_float(1.0), z, z, ctypes.c_size_t(0), z)
+                                        capi.i32(2), ctypes.c_float(1.0), z, z, z, ctypes.c_size_t(0), z)
     assert rc == 1 and b"multiple" in lib.tq_last_error()
     # empty inputs are valid no-ops
     assert lib.tq_rotate_and_quantize(z, 0, 0, capi.i64(0), capi.i32(64), z, z, capi.i32(4), z, z, z) == 0

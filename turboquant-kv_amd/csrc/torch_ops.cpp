@@ -337,12 +337,13 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk(const at::Tensor& queries, const
   return {os, oi};
 }
 
-at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacked,
+std::tuple<at::Tensor, at::Tensor> decode_attention_packed_lse(
+    const at::Tensor& q, const at::Tensor& kpacked,
                                    const at::Tensor& knorms, const at::Tensor& vpacked,
                                    const at::Tensor& vnorms, const at::Tensor& seq_lens,
                                    const at::Tensor& kcentroids, const at::Tensor& vcentroids,
-                                   const at::Tensor& krotation, const at::Tensor& vrotation,
-                                   int64_t kbits, int64_t vbits, double scale) {
+    const at::Tensor& krotation, const at::Tensor& vrotation,
+    int64_t kbits, int64_t vbits, double scale) {
   require_gpu(q, "q");
   TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
   TORCH_CHECK(kpacked.dim() == 4 && vpacked.dim() == 4, "packed K/V must be [B, Hkv, T, P]");
@@ -376,15 +377,28 @@ at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacke
   auto Rv = f32c(vrotation, dev);
   TORCH_CHECK(kc.numel() == (1 << kbits) && vc.numel() == (1 << vbits), "centroid lengths");
   auto out = at::empty({B, Hq, d}, qq.options());
-  if (B == 0) return out;
+  auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
+  if (B == 0) return {out, lse};
   auto ws = workspace(tq_decode_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)d, Tm), dev);
   check_rc(tq_decode_attention_packed(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
       kpacked.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vpacked.data_ptr<uint8_t>(),
       vnorms.data_ptr<float>(), Tm, sl.data_ptr<int32_t>(), kc.data_ptr<float>(),
       vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), (int32_t)kbits,
-      (int32_t)vbits, (float)scale, out.data_ptr(), ws.data_ptr(), ws.numel(), cur_stream(qq)));
-  return out;
+      (int32_t)vbits, (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(),
+      ws.numel(), cur_stream(qq)));
+  return {out, lse};
+}
+
+at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacked,
+                                   const at::Tensor& knorms, const at::Tensor& vpacked,
+                                   const at::Tensor& vnorms, const at::Tensor& seq_lens,
+                                   const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+                                   const at::Tensor& krotation, const at::Tensor& vrotation,
+                                   int64_t kbits, int64_t vbits, double scale) {
+  return std::get<0>(decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens,
+                                                 kcentroids, vcentroids, krotation, vrotation,
+                                                 kbits, vbits, scale));
 }
 
 }  // namespace
@@ -413,6 +427,10 @@ TORCH_LIBRARY(turboquant, m) {
   m.def("decode_attention_packed(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale) -> Tensor");
+  m.def("decode_attention_packed_lse(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
+        " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
+        " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale)"
+        " -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
@@ -427,4 +445,5 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("dequantize_prod_packed", &dequantize_prod_packed);
   m.impl("ip_scan_topk", &ip_scan_topk);
   m.impl("decode_attention_packed", &decode_attention_packed);
+  m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);
 }

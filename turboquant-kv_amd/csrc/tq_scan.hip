@@ -709,12 +709,18 @@ __global__ __launch_bounds__(kThreads) void values_kernel(ValuesArgs a) {
   }
 }
 
-// out[q][k] = sum_j (sum_sp part[q][sp][j]) * M[j][k], cast to out_dt.
+// out[q][k] = sum_j (sum_sp part[q][sp][j]) * M[j][k], cast to out_dt; optionally the
+// log-sum-exp of the query's scores from its softmax stats.
 __global__ void combine_kernel(const float* __restrict__ part, int nsplit, int d,
                                const float* __restrict__ M, const int32_t* __restrict__ seq_lens,
-                               int q_per_batch, int out_dt, void* __restrict__ out) {
+                               int q_per_batch, int out_dt, void* __restrict__ out,
+                               const float2* __restrict__ stats, float* __restrict__ lse) {
   __shared__ float o_s[256];
   const int q = blockIdx.x;
+  if (lse && threadIdx.x == 0) {
+    const bool empty = seq_lens && seq_lens[q / q_per_batch] <= 0;
+    lse[q] = (empty || !stats) ? -INFINITY : stats[q].x + logf(stats[q].y);
+  }
   int ns = nsplit;
   if (seq_lens) {
     const int64_t n = seq_lens[q / q_per_batch];
@@ -926,7 +932,7 @@ int tq_attention_values_packed(const float* attn_weights, int64_t nq, int64_t T,
     TQ_LAUNCH_CHECK("values_kernel");
   }
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)nq), dim3(256), 0, st, part, ns, d, rotation_T,
-                     nullptr, 1, (int)TQ_F32, out);
+                     nullptr, 1, (int)TQ_F32, out, nullptr, nullptr);
   TQ_LAUNCH_CHECK("combine_kernel");
   return TQ_OK;
 }
@@ -948,7 +954,8 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                                const int32_t* seq_lens, const float* kcentroids,
                                const float* vcentroids, const float* krotation,
                                const float* vrotation, int32_t kbits, int32_t vbits, float scale,
-                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
+                               void* out, float* lse, void* workspace, size_t workspace_bytes,
+                               void* stream) {
   TQ_REQUIRE(kbits >= 1 && kbits <= 4 && vbits >= 1 && vbits <= 4, "bits must be 1-4");
   TQ_REQUIRE(d >= 1 && d <= 256, "head_dim must be in [1, 256], got %d", d);
   TQ_REQUIRE(B >= 0 && hq >= 1 && hkv >= 1 && hq % hkv == 0,
@@ -997,7 +1004,7 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
     TQ_LAUNCH_CHECK("values_kernel");
   }
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)nq), dim3(256), 0, st, part, ns, d, vrotation,
-                     seq_lens, hq, (int)q_dtype, out);
+                     seq_lens, hq, (int)q_dtype, out, t_max > 0 ? stats : nullptr, lse);
   TQ_LAUNCH_CHECK("combine_kernel");
   return TQ_OK;
 }

@@ -60,3 +60,13 @@ def decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcent
     return _ops().decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens,
                                           kcentroids, vcentroids, krotation, vrotation, kbits,
                                           vbits, float(scale))
+
+
+def decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcentroids,
+                                vcentroids, krotation, vrotation, kbits, vbits, scale):
+    """decode_attention_packed plus the per-head log-sum-exp of the scores ([B, Hq] fp32),
+    for merging more tokens afterwards."""
+    _require_device(q, "q")
+    return _ops().decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens,
+                                              kcentroids, vcentroids, krotation, vrotation, kbits,
+                                              vbits, float(scale))
