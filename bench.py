@@ -34,6 +34,10 @@ sys.path.insert(0, os.path.join(ROOT, "turboquant-kv_amd"))
 HBM_PEAK_GBS = 8000.0
 METRIC = "packed-KV decode-attn GB/s (% HBM peak); 10M×d128 4-bit IP scan queries/s"
 PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms
+# HBM bytes per launch of scan_kernel<4,16,1,true,false> on the headline workload, from
+# rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a copy kernel's readings (FETCH x2.0,
+# WRITE x1.0); commands and raw counts in profiles/scan_kernel_b4_q1_N10M_d128.md.
+SCAN_TRAFFIC_BYTES = 680.3e6
 
 
 def log(msg):
@@ -203,35 +207,35 @@ def bench_quantize(args, extra):
         log(f"quantize {name}: {ms:.2f} ms, {n / ms * 1e3 / 1e6:.2f} M vec/s")
 
 
-def cpu_baseline(db, budget_s=15.0):
-    """The reference's C++ search_packed on a bounded sample of the same database."""
+def cpu_baseline(db, budget_s=12.0):
+    """The reference's C++ search_packed over the same 10M-row database, one query per
+    OpenMP thread, enough rounds of queries for about `budget_s` seconds."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import cpu_libs
 
     packed, norms, R, cen = db
-    kind = "reference" if cpu_libs.have_ref() else "port"
     if not (cpu_libs.have_ref() or cpu_libs.have_port()):
         return None
+    kind = "reference" if cpu_libs.have_ref() else "port"
     cores = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
-    n_s = 1_000_000
-    p = packed[:n_s].cpu().numpy()
-    nm = norms[:n_s].cpu().numpy()
+    p = packed.cpu().numpy()
+    nm = norms.cpu().numpy()
     Rn, cn = R.cpu().numpy(), cen.cpu().numpy()
-    qn = queries(cores, 128, seed=3).float().cpu().numpy()
+    qn = queries(cores * 64, 128, seed=3).float().cpu().numpy()
     t0 = time.perf_counter()
-    cpu_libs.search_packed(qn[:1], p, nm, Rn, cn, 4, 10, kind)
+    cpu_libs.search_packed(qn[:cores], p, nm, Rn, cn, 4, 10, kind)  # one query per thread
     t1 = time.perf_counter() - t0
-    nq = max(1, min(len(qn), int(budget_s / max(t1, 1e-3))))
+    rounds = max(1, min(64, int(budget_s / max(t1, 1e-3))))
+    nq = cores * rounds
     t0 = time.perf_counter()
     cpu_libs.search_packed(qn[:nq], p, nm, Rn, cn, 4, 10, kind)
     dt = time.perf_counter() - t0
-    qps_10m = nq / dt * (n_s / 10_000_000)
-    return {"value": qps_10m, "unit": "queries/s", "cores": min(cores, nq), "kind": kind,
-            "sample": f"{nq} queries x first {n_s} rows of the same 4-bit database, "
-                      f"{dt:.2f} s, one query per OpenMP thread; scaled by {n_s}/1e7 to N=10M"}
+    return {"value": nq / dt, "unit": "queries/s", "cores": cores, "kind": kind,
+            "sample": f"{nq} queries over all {p.shape[0]} rows of the same 4-bit database "
+                      f"({dt:.1f} s, one query per OpenMP thread, k=10)"}
 
 
 def main():
@@ -288,8 +292,8 @@ def main():
         "config": {"workload": "ip_scan_topk N=10,000,000 d=128 b=4 Q=1 (fp16 query) k=10",
                    "N": 10_000_000, "d": 128, "bits": 4, "queries_per_step": 1, "k": 10},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "ip_scan_topk op (lut_kernel + scan_kernel + merge_kernel)",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": SCAN_TRAFFIC_BYTES,
+                     "kernel": "ip_scan_topk op (scan_kernel + merge_kernel)",
                      "bytes_per_launch": bytes_alg},
         "cpu_baseline": cpu,
         "decode_attn_GBps": {str(T): v[1] / v[0] / 1e6 for T, v in dec.items()},

@@ -356,3 +356,21 @@ def test_decode_attention_vs_f64(d, kb, vb):
                                     kb, vb, scale)
     got_b, _ = k_decode(qb, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, scale)
     assert np.max(np.abs(got_b - want_b)) <= 1e-2 * np.max(np.abs(want_b))
+
+
+def test_scan_many_exact_ties_take_fallback():
+    # 3000 identical rows tie exactly; more survivors than the merge's sort buffer, so
+    # the exact k-round fallback must return the lowest ids among the tied rows.
+    rs = np.random.RandomState(12)
+    d, b = 128, 4
+    R, cen, p, nm = _db(rs, 20000, d, b)
+    best = int(np.argmax(O.lut_scores_f32(rs.randn(1, d).astype(np.float32), p, nm, cen, R, b)))
+    q = rs.randn(2, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q[:1], p, nm, cen, R, b)))
+    idx = rs.choice(20000, 3000, replace=False)
+    p[idx] = p[top]
+    nm[idx] = nm[top]
+    s, i = k_scan(q, p, nm, cen, R, b, 16)
+    so, io = O.search_topk(q, p, nm, cen, R, b, 16)
+    assert np.array_equal(i, io)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))

@@ -1,25 +1,28 @@
 // tq_scan.hip -- scoring over packed codes on gfx950.
 //
 // Kernels
-//   lut_kernel      q_rot = R q (sequential fp32 mul/add per output, like
-//                   csrc/core/turboquant_core.cpp:429-437) and the per-query table
-//                   LUT[j][l] = q_rot[j] * c[l] (core.cpp:440-446; triton_kernels.py:437).
-//   scan_kernel     ADC scan.  One lane = one packed row; the row's bit planes are
-//                   loaded with 16-byte loads, transposed to per-octet words with
-//                   v_perm_b32, and every dim's code becomes an LDS byte address
-//                   (code*8) with one v_and + one v_dot4_u32_u8.  The table for dim
-//                   j sits in LDS with an 8-byte stride per code (two dims share a
-//                   128-byte block), so a wave's 64 lookups of one dim touch 16
-//                   distinct banks or broadcast: conflict-free.  Sums run over j in
-//                   increasing order and are scaled by the row norm last, which is
-//                   the reference's own order (core.cpp:455-483).
+//   scan_kernel     ADC scan.  Each block first builds its queries' tables in LDS:
+//                   q_rot = R q (sequential fp32 mul/add per output, like
+//                   csrc/core/turboquant_core.cpp:429-437) and LUT[j][l] = q_rot[j] * c[l]
+//                   (core.cpp:440-446; triton_kernels.py:437).  Then one lane = one
+//                   packed row: the row's bit planes are loaded with 16-byte loads,
+//                   transposed to per-octet words with v_perm_b32, and every dim's
+//                   code becomes an LDS byte address (code*8) with one v_and + one
+//                   v_dot4_u32_u8.  The table for dim j sits in LDS with an 8-byte
+//                   stride per code (two dims share a 128-byte block), so a wave's 64
+//                   lookups of one dim touch 16 distinct banks or broadcast:
+//                   conflict-free.  Sums run over j in increasing order and are scaled
+//                   by the row norm last, the reference's own order (core.cpp:455-483).
 //                   Modes: TOPK keeps per-wave candidate lists in LDS (insert when
 //                   score beats the wave's k-th best, strict '>' with lower index
 //                   winning ties, as the core's heap does: core.cpp:487-494) and
 //                   writes each workgroup's sorted top-k; ALL writes every score
 //                   (attention_scores_packed, attn_scores.cu:31-104 semantics).
-//   merge_kernel    per query: prune by the largest per-block k-th score, rank-sort
-//                   the survivors, write top-k (ids int64, padding (-inf, -1)).
+//   merge_kernel    per query: prunes the block lists with the k-th best of the
+//                   per-block maxima, rank-sorts the survivors and writes top-k
+//                   (int64 ids, (-inf, -1) pads).  A launch of its own: merging in the
+//                   scan's last block would need an agent-scope release per block,
+//                   i.e. an L2 write-back on every one of the 8 XCDs' caches.
 //   softmax_stats   per query: max and sum of exp over its valid scores.
 //   values_kernel   o_part[q][j] = sum_t w[q][t] * vn[t] * c[code_tj] over one
 //                   split of the tokens; 16 fp32 accumulators per thread (4 queries
@@ -40,39 +43,6 @@ constexpr int kCandCap = 64 + kMaxK;  // per (wave, query) candidate slots
 constexpr int kValTokens = 256;       // tokens staged per values chunk
 constexpr int kSplitTokens = 1024;    // tokens per values split (decode / values op)
 
-// ------------------------------------------------------------------ LUT
-// lut[qg][j][l] for j < dpad (zeros for j >= d).
-__global__ void lut_kernel(const void* __restrict__ q, int q_dt, int d, int dpad,
-                           const float* __restrict__ rot, const float* __restrict__ cen, int nlev,
-                           float* __restrict__ lut) {
-  // Separate multiply and add roundings, exactly as the reference's C++ core; HIP
-  // would otherwise contract them into FMAs.
-#pragma clang fp contract(off)
-  __shared__ float qs[256];
-  const int qg = blockIdx.x;
-  for (int k = threadIdx.x; k < d; k += blockDim.x) qs[k] = load_as_f32(q, (int64_t)qg * d + k, q_dt);
-  __syncthreads();
-  float* out = lut + (size_t)qg * dpad * nlev;
-  for (int j = threadIdx.x; j < dpad; j += blockDim.x) {
-    float v = 0.f;
-    if (j < d) {
-      const float* r = rot + (size_t)j * d;
-      if ((d & 3) == 0) {
-        for (int k = 0; k < d; k += 4) {
-          const float4 r4 = *reinterpret_cast<const float4*>(r + k);
-          v = v + qs[k] * r4.x;
-          v = v + qs[k + 1] * r4.y;
-          v = v + qs[k + 2] * r4.z;
-          v = v + qs[k + 3] * r4.w;
-        }
-      } else {
-        for (int k = 0; k < d; ++k) v = v + qs[k] * r[k];
-      }
-    }
-    for (int l = 0; l < nlev; ++l) out[(size_t)j * nlev + l] = (j < d) ? v * cen[l] : 0.f;
-  }
-}
-
 // ------------------------------------------------------------------ scan
 struct ScanArgs {
   const uint8_t* packed;    // rows of stream s start at packed + s * stream_rows * P
@@ -82,14 +52,19 @@ struct ScanArgs {
   const int32_t* seq_lens;  // per batch row counts (decode); stream s -> batch s / spb
   int spb;                  // streams per batch
   int bpp;                  // bytes per plane (runtime; used by the generic loader)
-  const float* lut;         // [nq_total][dpad][nlev]
-  int dpad;
+  const void* q;            // [nq_total][d] queries (q_dt); the table is built per block
+  int q_dt;
+  int d;
+  const float* rot;         // [d][d]
+  const float* cen;         // [2^bits]
   int qps;                  // queries per stream
   float post_scale;         // multiplies norm * sum (decode: softmax scale)
   int k;
   float* part_s;            // TOPK: [nq_total][gridDim.x][k]
   int32_t* part_i;
   float* scores;            // ALL:  [nq_total][stream_rows]
+  float* out_s;             // [nq_total][k] (TOPK: written by merge_kernel)
+  int64_t* out_i;
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -218,6 +193,49 @@ __device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int
   }
 }
 
+// The block's query tables in LDS.  q_rot[j] = sum_k q[k] * R[j][k] with k ascending and
+// separate multiply and add roundings, table entry = q_rot[j] * c[l] -- the arithmetic
+// of csrc/core/turboquant_core.cpp:429-446, so scores match the reference bit for bit.
+// Layout: QB == 1: entry (j, l) at (j>>1)*NLEV*8 + l*8 + (j&1)*4 (two dims interleaved,
+// 8-byte code stride); QB > 1: the QB queries' entries of (j, l) contiguous at
+// (j*NLEV + l)*QB*4, so one 8/16-byte read serves every query.  Dims d..DP-1 are zero.
+template <int NLEV, int DP, int QB>
+__device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, char* lut_s) {
+#pragma clang fp contract(off)
+  __shared__ float qs[QB][256];
+  const int d = a.d;
+  for (int idx = threadIdx.x; idx < QB * d; idx += kThreads) {
+    const int qi = idx / d, k = idx - qi * d;
+    qs[qi][k] = qi < nq ? load_as_f32(a.q, (int64_t)(q0 + qi) * d + k, a.q_dt) : 0.f;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < QB * DP; idx += kThreads) {
+    const int qi = idx / DP, j = idx - qi * DP;
+    float v = 0.f;
+    if (qi < nq && j < d) {
+      const float* r = a.rot + (size_t)j * d;
+      if ((d & 3) == 0) {
+        for (int k = 0; k < d; k += 4) {
+          const float4 r4 = *reinterpret_cast<const float4*>(r + k);
+          v = v + qs[qi][k] * r4.x;
+          v = v + qs[qi][k + 1] * r4.y;
+          v = v + qs[qi][k + 2] * r4.z;
+          v = v + qs[qi][k + 3] * r4.w;
+        }
+      } else {
+        for (int k = 0; k < d; ++k) v = v + qs[qi][k] * r[k];
+      }
+    }
+    for (int l = 0; l < NLEV; ++l) {
+      const float e = (qi < nq && j < d) ? v * a.cen[l] : 0.f;
+      const int off = QB == 1 ? (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4
+                              : (j * NLEV + l) * QB * 4 + qi * 4;
+      *reinterpret_cast<float*>(lut_s + off) = e;
+    }
+  }
+  __syncthreads();
+}
+
 template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
 __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   constexpr int NLEV = 1 << BITS;
@@ -245,20 +263,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   const int nq = min(QB, a.qps - qb * QB);       // valid queries in this block
   const int P = BITS * a.bpp;
 
-  // Stage the tables.  QB == 1: entry (j, l) at (j>>1)*NLEV*8 + l*8 + (j&1)*4 (two dims
-  // interleaved, 8-byte code stride).  QB > 1: the QB queries' entries of (j, l) are
-  // contiguous at (j*NLEV + l)*QB*4, so one 8/16-byte read serves every query.
-  for (int idx = threadIdx.x; idx < QB * DP * NLEV; idx += kThreads) {
-    const int qi = idx / (DP * NLEV);
-    const int rem = idx - qi * DP * NLEV;
-    const int j = rem / NLEV, l = rem - j * NLEV;
-    float v = 0.f;
-    if (qi < nq && j < a.dpad) v = a.lut[((size_t)(q0 + qi) * a.dpad + j) * NLEV + l];
-    const int off = QB == 1 ? (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4
-                            : (j * NLEV + l) * QB * 4 + qi * 4;
-    *reinterpret_cast<float*>(lut_s + off) = v;
-  }
-  __syncthreads();
+  build_tables<NLEV, DP, QB>(a, q0, nq, lut_s);
 
   // Contiguous row range of this block, 64-row steps interleaved over the waves.
   const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
@@ -275,7 +280,6 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   float* my_cs = cand_s + wave * QB * kCandCap;
   int* my_ci = cand_i + wave * QB * kCandCap;
 
-  uint32_t cur[NW];
   int64_t row = rbeg + wave * 64 + lane;
   // Loads are unconditional (rows past the end re-read the last row and are masked
   // when scored): a branch around them would make the compiler wait for every
@@ -286,11 +290,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
     if constexpr (GENERIC) load_generic<BITS>(base + rl * P, a.bpp, w);
     else RowLoader<BITS, BPP>::load(base + rl * P, w);
   };
-  if (rbeg < rend) load_row(row, cur);
-  for (int64_t step0 = rbeg + wave * 64; step0 < rend; step0 += kWaves * 64) {
-    const int64_t nxt_row = row + kWaves * 64;
-    uint32_t nxt[NW];
-    load_row(nxt_row, nxt);
+  // One 64-row step of this wave: score row `row` from its plane words `cur`.
+  auto step = [&](const uint32_t (&cur)[NW], const int64_t row) {
     const float nrm = __builtin_nontemporal_load(nbase + (row < rend ? row : rlast));
 
     float acc[QB];
@@ -361,9 +362,19 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
           if (qi < nq) a.scores[(size_t)(q0 + qi) * a.stream_rows + row] = acc[qi] * nrm * a.post_scale;
       }
     }
+  };
+  // The next row's loads are issued before the current row is scored.
+  constexpr int64_t kStride = kWaves * 64;
+  uint32_t cur[NW];
+  int64_t step0 = rbeg + wave * 64;
+  if (step0 < rend) load_row(row, cur);
+  for (; step0 < rend; step0 += kStride) {
+    uint32_t nxt[NW];
+    load_row(row + kStride, nxt);
+    step(cur, row);
 #pragma unroll
     for (int i = 0; i < NW; ++i) cur[i] = nxt[i];
-    row = nxt_row;
+    row += kStride;
   }
 
   if constexpr (TOPK) {
@@ -411,46 +422,65 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
 }
 
 // ------------------------------------------------------------------ merge
-constexpr int kMergeCap = 2048;
+constexpr int kMergeCap = 512;       // survivors kept for the rank sort (more: exact fallback)
 constexpr int kMaxBlocksPerLane = 8;  // merge handles up to 64 * 4 * 8 = 2048 block lists
 
 // Wave-wide arg-best over per-lane candidates (score desc, id asc); returns the
-// winner's (score, id) in every lane.  Lanes with id == INT_MAX hold nothing.
+// winner's (score, id) in every lane.  Lanes with id == INT_MAX hold nothing.  Uses DPP
+// row operations (quad swaps, row mirrors, row broadcasts), a few cycles each, rather than
+// LDS-routed shuffles: this runs in single-block kernels where latency is the cost.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void best_step(float& s, int& id) {
+  const int so_bits = __builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), CTRL, ROWS, 0xF, false);
+  const int io = __builtin_amdgcn_update_dpp(id, id, CTRL, ROWS, 0xF, false);
+  const float so = __int_as_float(so_bits);
+  if (io != INT_MAX && (id == INT_MAX || better(so, io, s, id))) { s = so; id = io; }
+}
+
 __device__ __forceinline__ void wave_best(float& s, int& id) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float so = __shfl_xor(s, off, 64);
-    const int io = __shfl_xor(id, off, 64);
-    if (io != INT_MAX && (id == INT_MAX || better(so, io, s, id))) { s = so; id = io; }
-  }
+  best_step<0xB1, 0xF>(s, id);   // quad_perm [1,0,3,2]
+  best_step<0x4E, 0xF>(s, id);   // quad_perm [2,3,0,1]
+  best_step<0x141, 0xF>(s, id);  // row_half_mirror: 8-lane groups
+  best_step<0x140, 0xF>(s, id);  // row_mirror: 16-lane rows
+  best_step<0x142, 0xA>(s, id);  // row_bcast15 into rows 1 and 3
+  best_step<0x143, 0xC>(s, id);  // row_bcast31 into rows 2 and 3
+  s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 63));
+  id = __builtin_amdgcn_readlane(id, 63);
 }
 
 // Per query: the k-th best of the per-block maxima is a lower bound of the k-th best
 // score overall (those k maxima are k distinct rows), so only candidates at or above
 // it can be in the answer.  The survivors are rank-sorted.
-__global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
-                                                         const int32_t* __restrict__ part_i,
-                                                         int nblocks, int k, float* __restrict__ out_s,
-                                                         int64_t* __restrict__ out_i) {
+// Runs on all kThreads threads of a block (it synchronizes), for query q.
+__device__ void merge_query(const float* __restrict__ part_s, const int32_t* __restrict__ part_i,
+                            int nblocks, int k, int q, float* __restrict__ out_s,
+                            int64_t* __restrict__ out_i) {
   __shared__ float wbest_s[kWaves * kMaxK];
   __shared__ int wbest_i[kWaves * kMaxK];
   __shared__ float ss[kMergeCap];
   __shared__ int si[kMergeCap];
   __shared__ int nsurv;
+  __shared__ int nlists;
+  __shared__ int lists[kMergeCap];
   __shared__ float tau_s;
-  const int q = blockIdx.x;
+  __syncthreads();  // the shared buffers may still be read by a previous call
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* ps = part_s + (size_t)q * nblocks * k;
   const int32_t* pi = part_i + (size_t)q * nblocks * k;
   // 1. each wave: its k best block maxima (block b's list is sorted, entry 0 = its max)
   float ms[kMaxBlocksPerLane];
   int mi[kMaxBlocksPerLane];
+  // Every load is issued unconditionally (clamped index) so all of them are in flight
+  // together: these lists were just written on other XCDs and each load is a far miss.
 #pragma unroll
   for (int r = 0; r < kMaxBlocksPerLane; ++r) {
     const int b = threadIdx.x + r * kThreads;
-    const bool ok = b < nblocks && pi[(size_t)b * k] >= 0;
-    ms[r] = ok ? ps[(size_t)b * k] : -INFINITY;
-    mi[r] = ok ? pi[(size_t)b * k] : INT_MAX;
+    const size_t bc = (size_t)(b < nblocks ? b : nblocks - 1) * k;
+    const int id = pi[bc];
+    const float sc = ps[bc];
+    const bool ok = b < nblocks && id >= 0;
+    ms[r] = ok ? sc : -INFINITY;
+    mi[r] = ok ? id : INT_MAX;
   }
   for (int r = 0; r < k; ++r) {
     float bs = -INFINITY;
@@ -464,7 +494,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
       if (mi[t] == bi) mi[t] = INT_MAX;  // ids are unique: consume the winner
     if (lane == 0) { wbest_s[wave * kMaxK + r] = bs; wbest_i[wave * kMaxK + r] = bi; }
   }
-  if (threadIdx.x == 0) nsurv = 0;
+  if (threadIdx.x == 0) { nsurv = 0; nlists = 0; }
   __syncthreads();
   // 2. wave 0: k-th best of the 4k wave winners -> tau
   if (wave == 0) {
@@ -495,17 +525,25 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
   }
   __syncthreads();
   const float tau = tau_s;
-  // 3. survivors: only lists whose maximum reaches tau can hold any, and each list
-  // is sorted, so a list is read only until its first entry below tau.
+  // 3. survivors: only lists whose maximum reaches tau can hold any.  Collect those
+  // lists, then read all their entries at once.
   const int total = nblocks * k;
 #pragma unroll
   for (int r = 0; r < kMaxBlocksPerLane; ++r) {
     const int b = threadIdx.x + r * kThreads;
-    if (b >= nblocks || !(ms[r] >= tau) || pi[(size_t)b * k] < 0) continue;
-    for (int e = 0; e < k; ++e) {
-      const int id = pi[(size_t)b * k + e];
-      const float sc = ps[(size_t)b * k + e];
-      if (id < 0 || !(sc >= tau)) break;
+    if (b < nblocks && ms[r] >= tau) {
+      const int pos = atomicAdd(&nlists, 1);
+      if (pos < kMergeCap) lists[pos] = b;
+    }
+  }
+  __syncthreads();
+  const int nl = min(nlists, kMergeCap);
+  for (int e = threadIdx.x; e < nl * k; e += kThreads) {
+    const int li = e / k;
+    const size_t at = (size_t)lists[li] * k + (e - li * k);
+    const int id = pi[at];
+    const float sc = ps[at];
+    if (id >= 0 && sc >= tau) {
       const int pos = atomicAdd(&nsurv, 1);
       if (pos < kMergeCap) { ss[pos] = sc; si[pos] = id; }
     }
@@ -523,7 +561,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
       if (rank < k) { os[rank] = se; oi[rank] = ie; }
     }
     for (int e = m + threadIdx.x; e < k; e += kThreads) { os[e] = -INFINITY; oi[e] = -1; }
-    return;
+    return;  // uniform: every thread of the block takes the same branch
   }
   // 4. more than kMergeCap rows tie at tau: k rounds of block arg-best over everything
   __shared__ float bs_s[kWaves];
@@ -554,6 +592,14 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
       oi[r] = ci == INT_MAX ? -1 : ci;
     }
   }
+}
+
+__global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
+                                                         const int32_t* __restrict__ part_i,
+                                                         int nblocks, int k,
+                                                         float* __restrict__ out_s,
+                                                         int64_t* __restrict__ out_i) {
+  merge_query(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
 }
 
 // ------------------------------------------------------------------ softmax stats
@@ -741,6 +787,7 @@ __global__ void combine_kernel(const float* __restrict__ part, int nsplit, int d
 }
 
 // ------------------------------------------------------------------ host helpers
+
 int scan_blocks(int64_t nrows) {
   const int64_t want = (nrows + 64 * 8 * kWaves - 1) / (64 * 8 * kWaves);  // >= 8 steps per wave
   int64_t cap = (int64_t)device_cu_count() * 4;
@@ -797,23 +844,6 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   return fail(TQ_EINVAL, "bit_width must be 1-4, got %d", bits);
 }
 
-int launch_lut(const void* q, int q_dt, int64_t nq, int d, int dpad, const float* rot,
-               const float* cen, int nlev, float* lut, hipStream_t st) {
-  hipLaunchKernelGGL(lut_kernel, dim3((unsigned)nq), dim3(256), 0, st, q, q_dt, d, dpad, rot, cen,
-                     nlev, lut);
-  TQ_LAUNCH_CHECK("lut_kernel");
-  return TQ_OK;
-}
-
-inline int dpad_for(int d) {
-  const int bpp = (d + 7) / 8;
-  return (bpp == 8 || bpp == 16) ? 8 * bpp : 256;
-}
-
-size_t lut_bytes(int64_t nq, int d, int bits) {
-  return align_up((size_t)nq * dpad_for(d) * (1u << bits) * 4, 256);
-}
-
 }  // namespace
 }  // namespace tq
 
@@ -823,7 +853,7 @@ extern "C" {
 
 size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N, int32_t k) {
   if (nq <= 0 || d <= 0 || bit_width < 1 || bit_width > 4) return 0;
-  size_t bytes = lut_bytes(nq, d, bit_width);
+  size_t bytes = 256;
   if (k > 0) {
     const size_t nb = (size_t)scan_blocks(N);
     bytes += align_up((size_t)nq * nb * k * 4, 256) * 2;
@@ -847,23 +877,20 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
   const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, N, k);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t st = as_stream(stream);
-  const int dpad = dpad_for(d);
-  char* ws = static_cast<char*>(workspace);
-  float* lut = reinterpret_cast<float*>(ws);
-  ws += lut_bytes(nq, d, bit_width);
+  char* ws = static_cast<char*>(workspace) + 256;
   const int nb = scan_blocks(N);
   float* ps = reinterpret_cast<float*>(ws);
   ws += align_up((size_t)nq * nb * k * 4, 256);
   int32_t* pi = reinterpret_cast<int32_t*>(ws);
-  int rc = launch_lut(queries, q_dtype, nq, d, dpad, rotation, centroids, 1 << bit_width, lut, st);
-  if (rc) return rc;
   ScanArgs a{};
   a.packed = packed; a.norms = norms; a.stream_rows = N; a.nrows = N; a.seq_lens = nullptr; a.spb = 1;
-  a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad; a.qps = (int)nq; a.post_scale = 1.f; a.k = k;
+  a.bpp = (d + 7) / 8; a.q = queries; a.q_dt = q_dtype; a.d = d; a.rot = rotation; a.cen = centroids;
+  a.qps = (int)nq; a.post_scale = 1.f; a.k = k;
   a.part_s = ps; a.part_i = pi; a.scores = nullptr;
+  a.out_s = out_scores; a.out_i = out_ids;
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  rc = launch_scan(a, bit_width, true, 1, st);
-  if (rc) return rc;
+  const int rc = launch_scan(a, bit_width, true, 1, st);
+  if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
                      out_scores, out_ids);
   TQ_LAUNCH_CHECK("merge_kernel");
@@ -885,13 +912,10 @@ int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, 
   const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, T, 0);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t st = as_stream(stream);
-  const int dpad = dpad_for(d);
-  float* lut = static_cast<float*>(workspace);
-  int rc = launch_lut(query, q_dtype, nq, d, dpad, rotation, centroids, 1 << bit_width, lut, st);
-  if (rc) return rc;
   ScanArgs a{};
   a.packed = packed_keys; a.norms = key_norms; a.stream_rows = T; a.nrows = T; a.seq_lens = nullptr;
-  a.spb = 1; a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad; a.qps = (int)nq; a.post_scale = 1.f;
+  a.spb = 1; a.bpp = (d + 7) / 8; a.q = query; a.q_dt = q_dtype; a.d = d; a.rot = rotation;
+  a.cen = centroids; a.qps = (int)nq; a.post_scale = 1.f;
   a.k = 0; a.scores = scores;
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
   return launch_scan(a, bit_width, false, 1, st);
@@ -941,7 +965,7 @@ size_t tq_decode_workspace_bytes(int32_t B, int32_t hq, int32_t d, int64_t t_max
   if (B <= 0 || hq <= 0 || d <= 0) return 0;
   const size_t nq = (size_t)B * hq;
   const int64_t ns = (t_max + kSplitTokens - 1) / kSplitTokens;
-  size_t bytes = lut_bytes((int64_t)nq, d, 4);
+  size_t bytes = 256;
   bytes += align_up(nq * (size_t)(t_max > 0 ? t_max : 1) * 4, 256);   // scores
   bytes += align_up(nq * sizeof(float2), 256);                        // stats
   bytes += align_up(nq * (size_t)(ns > 0 ? ns : 1) * d * 4, 256);     // partials
@@ -972,24 +996,20 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
   hipStream_t st = as_stream(stream);
   const int64_t nq = (int64_t)B * hq;
   const int G = hq / hkv;
-  const int dpad = dpad_for(d);
   const int ns = (int)((t_max + kSplitTokens - 1) / kSplitTokens);
-  char* ws = static_cast<char*>(workspace);
-  float* lut = reinterpret_cast<float*>(ws);
-  ws += lut_bytes(nq, d, 4);
+  char* ws = static_cast<char*>(workspace) + 256;
   float* scores = reinterpret_cast<float*>(ws);
   ws += align_up((size_t)nq * (size_t)(t_max > 0 ? t_max : 1) * 4, 256);
   float2* stats = reinterpret_cast<float2*>(ws);
   ws += align_up((size_t)nq * sizeof(float2), 256);
   float* part = reinterpret_cast<float*>(ws);
   if (t_max > 0) {
-    int rc = launch_lut(q, q_dtype, nq, d, dpad, krotation, kcentroids, 1 << kbits, lut, st);
-    if (rc) return rc;
     ScanArgs a{};
     a.packed = kpacked; a.norms = knorms; a.stream_rows = t_max; a.nrows = t_max;
-    a.seq_lens = seq_lens; a.spb = hkv; a.bpp = (d + 7) / 8; a.lut = lut; a.dpad = dpad;
+    a.seq_lens = seq_lens; a.spb = hkv; a.bpp = (d + 7) / 8; a.q = q; a.q_dt = q_dtype; a.d = d;
+    a.rot = krotation; a.cen = kcentroids;
     a.qps = G; a.post_scale = scale; a.k = 0; a.scores = scores;
-    rc = launch_scan(a, kbits, false, B * hkv, st);
+    int rc = launch_scan(a, kbits, false, B * hkv, st);
     if (rc) return rc;
     hipLaunchKernelGGL(softmax_stats_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, scores,
                        t_max, seq_lens, hq, stats);
