@@ -358,6 +358,42 @@ def test_decode_attention_vs_f64(d, kb, vb):
     assert np.max(np.abs(got_b - want_b)) <= 1e-2 * np.max(np.abs(want_b))
 
 
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 1), (2, 2), (1, 1), (4, 1)])
+@pytest.mark.parametrize("G", [1, 3, 4])
+def test_fused_decode_ragged_vs_f64(kb, vb, G):
+    # head_dim 64, fp16/bf16 queries: the single-kernel MFMA path.  Ragged lengths cover
+    # empty, sub-tile, tile-boundary and multi-split sequences and a capacity that is not
+    # a multiple of 4; the second query set is scaled up so the softmax is peaky and the
+    # running maximum moves.
+    rs = np.random.RandomState(100 * kb + 10 * vb + G)
+    d, Hkv, Tm = 64, 2, 5003
+    seq = [0, 1, 3, 63, 64, 65, 257, 5003]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(kb, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    K = rs.randn(B * Hkv * Tm, d).astype(np.float32) * rs.uniform(0.2, 3.0, (B * Hkv * Tm, 1)).astype(np.float32)
+    V = rs.randn(B * Hkv * Tm, d).astype(np.float32) * rs.uniform(0.2, 3.0, (B * Hkv * Tm, 1)).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, kb, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kp, vp = kp.reshape(B, Hkv, Tm, -1), vp.reshape(B, Hkv, Tm, -1)
+    kn, vn = kn.reshape(B, Hkv, Tm), vn.reshape(B, Hkv, Tm)
+    for qscale in (1.0, 6.0):
+        q = (rs.randn(B, Hq, d) * qscale).astype(np.float32)
+        for dt, tol in ((torch.bfloat16, 1e-2), (torch.float16, 3e-3)):
+            qt = torch.from_numpy(q).to(DEV).to(dt)
+            qf = qt.float().cpu().numpy()
+            want, want_lse = O.decode_attention_f64(qf, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb,
+                                                    0.125, return_lse=True)
+            got, lse = k_decode(qt, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, kb, vb, 0.125)
+            assert np.all(got[0] == 0) and np.isneginf(lse[0]).all()
+            for bi in range(1, B):
+                err = np.max(np.abs(got[bi] - want[bi])) / np.max(np.abs(want[bi]))
+                assert err <= tol, (qscale, dt, seq[bi], err)
+            ok = np.isfinite(want_lse)
+            assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= 1e-4
+
+
 def test_scan_many_exact_ties_take_fallback():
     # 3000 identical rows tie exactly; more survivors than the merge's sort buffer, so
     # the exact k-round fallback must return the lowest ids among the tied rows.

@@ -8,7 +8,7 @@ Outputs (git-ignored, shipped with the tree):
     turboquant_kv/_lib/libturboquant_torch.so  TORCH_LIBRARY(turboquant) -> C ABI
 
 Every HIP source is compiled with hipcc for gfx950 only, with packed-fp32 code
-generation disabled.  The two .hip files compile in parallel.
+generation disabled.  The .hip files compile in parallel.
 """
 
 from __future__ import annotations
@@ -27,7 +27,7 @@ OBJDIR = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(LIBDIR, "libturboquant_hip.so")
 TORCH_LIB = os.path.join(LIBDIR, "libturboquant_torch.so")
 
-HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip"]
+HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = [

@@ -30,6 +30,7 @@
 //   combine_kernel  sum of the split partials, then o = o_rot @ M (M = R).
 
 #include "tq_common.h"
+#include "tq_decode.h"
 
 #include <climits>
 
@@ -969,7 +970,8 @@ size_t tq_decode_workspace_bytes(int32_t B, int32_t hq, int32_t d, int64_t t_max
   bytes += align_up(nq * (size_t)(t_max > 0 ? t_max : 1) * 4, 256);   // scores
   bytes += align_up(nq * sizeof(float2), 256);                        // stats
   bytes += align_up(nq * (size_t)(ns > 0 ? ns : 1) * d * 4, 256);     // partials
-  return bytes;
+  const size_t fused = fused_decode_workspace_bytes(B, hq, d, t_max);
+  return bytes > fused ? bytes : fused;
 }
 
 int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
@@ -994,6 +996,10 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
   hipStream_t st = as_stream(stream);
+  const FusedDecodeCall fc{q, (int)q_dtype, B, hq, hkv, d, kpacked, knorms, vpacked, vnorms,
+                           t_max, seq_lens, kcentroids, vcentroids, krotation, vrotation,
+                           kbits, vbits, scale, out, lse};
+  if (fused_decode_covers(fc)) return launch_fused_decode(fc, workspace, workspace_bytes, st);
   const int64_t nq = (int64_t)B * hq;
   const int G = hq / hkv;
   const int ns = (int)((t_max + kSplitTokens - 1) / kSplitTokens);
