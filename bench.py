@@ -157,9 +157,16 @@ def bench_decode(args, extra):
                 V[:, h, :, ch[h]] *= 20
             kp, kn = ops.quantize_mse_packed(K.reshape(-1, d), Rk, bk, kb)
             vp, vn = ops.quantize_mse_packed(V.reshape(-1, d), Rv, bv, vb)
-            caches.append((kp.view(B, Hkv, T, -1), kn.float().view(B, Hkv, T),
-                           vp.view(B, Hkv, T, -1), vn.float().view(B, Hkv, T)))
             del K, V
+            # the decode layout QuantizedKVCache keeps (same bytes per token)
+            kdl = torch.zeros(B * Hkv, T, d // 2, dtype=torch.uint8, device="cuda")
+            vdl = torch.zeros(B * Hkv, T // 4, d, dtype=torch.uint8, device="cuda")
+            ops.pack_decode_layout(kp.view(B * Hkv, T, -1), kdl, d, kb, 0, 0)
+            ops.pack_decode_layout(vp.view(B * Hkv, T, -1), vdl, d, vb, 1, 0)
+            caches.append((kp.view(B, Hkv, T, -1), kn.float().view(B, Hkv, T),
+                           vp.view(B, Hkv, T, -1), vn.float().view(B, Hkv, T),
+                           kdl.view(B, Hkv, T, -1), vdl.view(B, Hkv, T // 4, -1)))
+            del kp, vp
         q = torch.randn(B, Hq, d, generator=g, device="cuda").to(torch.bfloat16)
         sl = torch.full((B,), T, dtype=torch.int32, device="cuda")
         it = [0]
@@ -167,16 +174,26 @@ def bench_decode(args, extra):
         def fn():
             c = caches[it[0] % len(caches)]
             it[0] += 1
+            return ops.decode_attention_dl(q, c[4], c[1], c[5], c[3], sl, ck, cv, Rk, Rv, 1.0 / 8.0)
+
+        def fn_bitplane():
+            c = caches[it[0] % len(caches)]
+            it[0] += 1
             return ops.decode_attention_packed(q, c[0], c[1], c[2], c[3], sl, ck, cv, Rk, Rv, kb,
                                                vb, 1.0 / 8.0)
 
         ms = time_op(fn, 20, 3)
+        ms_bp = time_op(fn_bitplane, 20, 3)
         bytes_alg = per + 2 * B * Hq * d * 2
         out[T] = (ms, bytes_alg)
         extra[f"decode_attn_T{T}"] = {"us_per_step": ms * 1e3, "GBps": bytes_alg / ms / 1e6,
                                       "hbm_frac": bytes_alg / ms / 1e6 / HBM_PEAK_GBS,
-                                      "tokens_per_s": B / ms * 1e3, "cache_copies": ncopies}
-        log(f"decode T={T}: {ms * 1e3:.1f} us, {bytes_alg / ms / 1e6:.0f} GB/s")
+                                      "tokens_per_s": B / ms * 1e3, "cache_copies": ncopies,
+                                      "layout": "decode layout (QuantizedKVCache storage)",
+                                      "bitplane_rows_us": ms_bp * 1e3,
+                                      "bitplane_rows_GBps": bytes_alg / ms_bp / 1e6}
+        log(f"decode T={T}: {ms * 1e3:.1f} us, {bytes_alg / ms / 1e6:.0f} GB/s "
+            f"(bit-plane rows: {ms_bp * 1e3:.1f} us)")
         del caches
     return out
 

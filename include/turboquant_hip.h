@@ -174,6 +174,42 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                                void* out, float* lse, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/*
+ * Decode layout: the codes of a 4-bit key / 2-bit value packed KV cache arranged for
+ * the decode kernel, same bytes per token as the bit-plane rows.  The reference stores
+ * its cache privately (cache.py:81-130), so this arrangement is internal to
+ * QuantizedKVCache; these entry points convert it from and to the reference rows.
+ *   keys    [streams][t_cap][d/2]:     byte p = (code[2p] << 4) | code[2p+1]
+ *   values  [streams][t_cap/4][d]:     byte j of block k = sum_t code[4k+t][j] << 2t
+ * tq_pack_decode_layout writes tokens [pos, pos+n) of every stream from bit-plane rows
+ * packed [streams][n][bits*ceil(d/8)] (values: bits of the block's other tokens are
+ * kept); tq_unpack_decode_layout returns tokens [t0, t0+n) as bit-plane rows.
+ * values = 0 for keys (bit_width 4), 1 for values (bit_width 2).
+ */
+int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,
+                          int32_t bit_width, int32_t values, uint8_t* cache, int64_t t_cap,
+                          int64_t pos, void* stream);
+int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_cap, int64_t t0,
+                            int64_t n, int32_t d, int32_t bit_width, int32_t values,
+                            uint8_t* packed, void* stream);
+
+/*
+ * tq_decode_attention_packed over a decode-layout cache (same semantics and output):
+ * head_dim 64, 4-bit keys, 2-bit values, 1-4 query heads per KV head, t_cap a multiple
+ * of 4.  kpairs [B, hkv, t_cap, 32], vblocks [B, hkv, t_cap/4, 64], norms as above.
+ * fp32 queries get fp32-accurate outputs; fp16/bf16 queries use fp16 value products
+ * (relative error about 5e-4, below the output type's own rounding tolerance).
+ */
+size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t t_cap);
+int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                           int32_t d, const uint8_t* kpairs, const float* knorms,
+                           const uint8_t* vblocks, const float* vnorms, int64_t t_cap,
+                           const int32_t* seq_lens, const float* kcentroids,
+                           const float* vcentroids, const float* krotation,
+                           const float* vrotation, int32_t kbits, int32_t vbits, float scale,
+                           void* out, float* lse, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,8 +21,10 @@ def lib():
         _lib = ctypes.CDLL(LIB)
         _lib.tq_last_error.restype = ctypes.c_char_p
         for name in ("tq_scan_workspace_bytes", "tq_values_workspace_bytes",
-                     "tq_decode_workspace_bytes"):
+                     "tq_decode_workspace_bytes", "tq_decode_dl_workspace_bytes"):
             getattr(_lib, name).restype = ctypes.c_size_t
+        _lib.tq_decode_dl_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32,
+                                                      ctypes.c_int32, ctypes.c_int64]
         _lib.tq_scan_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                                  ctypes.c_int64, ctypes.c_int32]
         _lib.tq_values_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int64]

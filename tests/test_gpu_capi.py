@@ -130,6 +130,48 @@ def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
 
+def k_pack_dl(packed, t_cap, pos, values, cache=None):
+    """Bit-plane rows [S, n, P] -> decode-layout cache (created zeroed when None)."""
+    S, n, _ = packed.shape
+    d = 64
+    if cache is None:
+        shape = (S, t_cap // 4, d) if values else (S, t_cap, d // 2)
+        cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_pack_decode_layout(capi.p(T(packed)), capi.i64(S), capi.i64(n), capi.i32(d),
+                                         capi.i32(2 if values else 4), capi.i32(values), capi.p(cache),
+                                         capi.i64(t_cap), capi.i64(pos), capi.stream()))
+    sync()
+    return cache
+
+
+def k_unpack_dl(cache, t_cap, t0, n, values):
+    S = cache.shape[0]
+    bits = 2 if values else 4
+    out = torch.empty(S, n, bits * 8, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_unpack_decode_layout(capi.p(cache), capi.i64(S), capi.i64(t_cap), capi.i64(t0),
+                                           capi.i64(n), capi.i32(64), capi.i32(bits), capi.i32(values),
+                                           capi.p(out), capi.stream()))
+    sync()
+    return out.cpu().numpy()
+
+
+def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale):
+    B, Hq, d = q_t.shape
+    Hkv, Tc = kn.shape[1], kn.shape[2]
+    out = torch.empty_like(q_t)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
+    ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
+    sl = T(np.asarray(seq_lens, np.int32))
+    capi.check(L().tq_decode_attention_dl(
+        capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache),
+        capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)), capi.i64(Tc), capi.p(sl), capi.p(T(kc)),
+        capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(2), ctypes.c_float(scale),
+        capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
 CASES = {"d128": (128, (2, 3, 4)), "d200": (200, (3, 4)), "d64": (64, (2, 3, 4))}
 
 
@@ -392,6 +434,65 @@ def test_fused_decode_ragged_vs_f64(kb, vb, G):
                 assert err <= tol, (qscale, dt, seq[bi], err)
             ok = np.isfinite(want_lse)
             assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= 1e-4
+
+
+def test_decode_layout_pack_roundtrip():
+    # Appends in uneven pieces (partial value blocks are merged with their earlier tokens);
+    # the layout bytes are checked against an independent numpy packing of the codes and
+    # the unpacked rows must equal the bit-plane input.
+    rs = np.random.RandomState(21)
+    S, t_cap, d = 3, 40, 64
+    kcodes = rs.randint(0, 16, (S, t_cap, d))
+    vcodes = rs.randint(0, 4, (S, t_cap, d))
+    kp = np.stack([O.pack_codes(kcodes[s], 4) for s in range(S)])
+    vp = np.stack([O.pack_codes(vcodes[s], 2) for s in range(S)])
+    kc = vc = None
+    for pos, n in ((0, 5), (5, 1), (6, 7), (13, 3), (16, 24)):
+        kc = k_pack_dl(np.ascontiguousarray(kp[:, pos:pos + n]), t_cap, pos, 0, kc)
+        vc = k_pack_dl(np.ascontiguousarray(vp[:, pos:pos + n]), t_cap, pos, 1, vc)
+    want_k = (kcodes[:, :, 0::2] << 4) | kcodes[:, :, 1::2]
+    assert np.array_equal(kc.cpu().numpy(), want_k.astype(np.uint8))
+    vb = vcodes.reshape(S, t_cap // 4, 4, d)
+    want_v = vb[:, :, 0] | (vb[:, :, 1] << 2) | (vb[:, :, 2] << 4) | (vb[:, :, 3] << 6)
+    assert np.array_equal(vc.cpu().numpy(), want_v.astype(np.uint8))
+    assert np.array_equal(k_unpack_dl(kc, t_cap, 0, t_cap, 0), kp)
+    assert np.array_equal(k_unpack_dl(vc, t_cap, 7, 30, 1), vp[:, 7:37])
+
+
+@pytest.mark.parametrize("G", [1, 2, 4])
+def test_decode_layout_attention_vs_f64(G):
+    # Same cases as the bit-plane kernel, through the decode layout; fp32 queries take
+    # the exact value product.
+    rs = np.random.RandomState(300 + G)
+    d, Hkv, Tc = 64, 2, 5004
+    seq = [0, 1, 3, 63, 64, 65, 257, 513, 5004]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(2, d)
+    n = B * Hkv * Tc
+    K = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    V = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, 2, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, Tc, -1), Tc, 0, 0)
+    vc = k_pack_dl(vp.reshape(B * Hkv, Tc, -1), Tc, 0, 1)
+    kp, vp = kp.reshape(B, Hkv, Tc, -1), vp.reshape(B, Hkv, Tc, -1)
+    kn, vn = kn.reshape(B, Hkv, Tc), vn.reshape(B, Hkv, Tc)
+    for qscale in (1.0, 6.0):
+        q = (rs.randn(B, Hq, d) * qscale).astype(np.float32)
+        for dt, tol in ((torch.float32, 1e-3), (torch.bfloat16, 1e-2), (torch.float16, 3e-3)):
+            qt = torch.from_numpy(q).to(DEV).to(dt)
+            qf = qt.float().cpu().numpy()
+            want, want_lse = O.decode_attention_f64(qf, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, 4, 2,
+                                                    0.125, return_lse=True)
+            got, lse = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125)
+            assert np.all(got[0] == 0) and np.isneginf(lse[0]).all()
+            for bi in range(1, B):
+                err = np.max(np.abs(got[bi] - want[bi])) / np.max(np.abs(want[bi]))
+                assert err <= (1e-4 if dt == torch.float32 else tol), (qscale, dt, seq[bi], err)
+            ok = np.isfinite(want_lse)
+            assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= 1e-5
 
 
 def test_scan_many_exact_ties_take_fallback():

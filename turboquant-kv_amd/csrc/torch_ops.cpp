@@ -401,6 +401,96 @@ at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacke
                                                  kbits, vbits, scale));
 }
 
+// ------------------------------------------------------------ decode layout
+
+void pack_decode_layout(const at::Tensor& packed, at::Tensor& cache, int64_t dim,
+                        int64_t bit_width, int64_t values, int64_t pos) {
+  require_gpu(cache, "cache");
+  c10::DeviceGuard g(cache.device());
+  const auto dev = cache.device();
+  TORCH_CHECK(cache.scalar_type() == at::kByte && cache.is_contiguous() && cache.dim() == 3,
+              "cache must be contiguous uint8 [streams, rows, width]");
+  auto pk = packed.to(dev, at::kByte).contiguous();
+  TORCH_CHECK(pk.dim() == 3 && pk.size(0) == cache.size(0), "packed must be [streams, n, P]");
+  TORCH_CHECK(pk.size(2) == packed_width(bit_width, dim), "packed width mismatch");
+  const int64_t t_cap = values ? cache.size(1) * 4 : cache.size(1);
+  TORCH_CHECK(cache.size(2) == (values ? dim : dim / 2), "cache width mismatch");
+  check_rc(tq_pack_decode_layout(pk.data_ptr<uint8_t>(), pk.size(0), pk.size(1), (int32_t)dim,
+                                 (int32_t)bit_width, (int32_t)values, cache.data_ptr<uint8_t>(),
+                                 t_cap, pos, cur_stream(cache)));
+}
+
+at::Tensor unpack_decode_layout(const at::Tensor& cache, int64_t dim, int64_t bit_width,
+                                int64_t values, int64_t t0, int64_t n) {
+  require_gpu(cache, "cache");
+  c10::DeviceGuard g(cache.device());
+  TORCH_CHECK(cache.scalar_type() == at::kByte && cache.is_contiguous() && cache.dim() == 3,
+              "cache must be contiguous uint8 [streams, rows, width]");
+  const int64_t t_cap = values ? cache.size(1) * 4 : cache.size(1);
+  auto out = at::empty({cache.size(0), n, packed_width(bit_width, dim)}, cache.options());
+  check_rc(tq_unpack_decode_layout(cache.data_ptr<uint8_t>(), cache.size(0), t_cap, t0, n,
+                                   (int32_t)dim, (int32_t)bit_width, (int32_t)values,
+                                   out.data_ptr<uint8_t>(), cur_stream(cache)));
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
+    const at::Tensor& q, const at::Tensor& kpairs, const at::Tensor& knorms,
+    const at::Tensor& vblocks, const at::Tensor& vnorms, const at::Tensor& seq_lens,
+    const at::Tensor& kcentroids, const at::Tensor& vcentroids, const at::Tensor& krotation,
+    const at::Tensor& vrotation, double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
+  TORCH_CHECK(kpairs.dim() == 4 && vblocks.dim() == 4,
+              "kpairs must be [B, Hkv, T, d/2] and vblocks [B, Hkv, T/4, d]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  const int64_t B = qq.size(0), Hq = qq.size(1), d = qq.size(2);
+  const int64_t Hkv = kpairs.size(1), Tc = kpairs.size(2);
+  TORCH_CHECK(kpairs.scalar_type() == at::kByte && vblocks.scalar_type() == at::kByte,
+              "kpairs/vblocks must be uint8");
+  TORCH_CHECK(kpairs.is_contiguous() && vblocks.is_contiguous() && knorms.is_contiguous() &&
+                  vnorms.is_contiguous(),
+              "K/V and norms must be contiguous");
+  TORCH_CHECK(kpairs.device() == dev && vblocks.device() == dev && knorms.device() == dev &&
+                  vnorms.device() == dev,
+              "K/V must be on the query's device");
+  TORCH_CHECK(kpairs.size(0) == B && kpairs.size(3) == d / 2 && vblocks.size(0) == B &&
+                  vblocks.size(1) == Hkv && vblocks.size(2) * 4 == Tc && vblocks.size(3) == d,
+              "decode-layout K/V shape mismatch");
+  TORCH_CHECK(knorms.scalar_type() == at::kFloat && vnorms.scalar_type() == at::kFloat &&
+                  knorms.numel() == B * Hkv * Tc && vnorms.numel() == B * Hkv * Tc,
+              "norms must be float32 [B, Hkv, T]");
+  auto sl = seq_lens.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  auto kc = f32c(kcentroids, dev);
+  auto vc = f32c(vcentroids, dev);
+  auto Rk = f32c(krotation, dev);
+  auto Rv = f32c(vrotation, dev);
+  auto out = at::empty({B, Hq, d}, qq.options());
+  auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
+  if (B == 0) return {out, lse};
+  auto ws = workspace(tq_decode_dl_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)Hkv, Tc), dev);
+  check_rc(tq_decode_attention_dl(
+      qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
+      kpairs.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vblocks.data_ptr<uint8_t>(),
+      vnorms.data_ptr<float>(), Tc, sl.data_ptr<int32_t>(), kc.data_ptr<float>(),
+      vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), 4, 2, (float)scale,
+      out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(), ws.numel(), cur_stream(qq)));
+  return {out, lse};
+}
+
+at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
+                               const at::Tensor& knorms, const at::Tensor& vblocks,
+                               const at::Tensor& vnorms, const at::Tensor& seq_lens,
+                               const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+                               const at::Tensor& krotation, const at::Tensor& vrotation,
+                               double scale) {
+  return std::get<0>(decode_attention_dl_lse(q, kpairs, knorms, vblocks, vnorms, seq_lens,
+                                             kcentroids, vcentroids, krotation, vrotation, scale));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(turboquant, m) {
@@ -431,6 +521,16 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale)"
         " -> (Tensor, Tensor)");
+  m.def("pack_decode_layout(Tensor packed, Tensor(a!) cache, int dim, int bit_width, int values,"
+        " int pos) -> ()");
+  m.def("unpack_decode_layout(Tensor cache, int dim, int bit_width, int values, int t0, int n)"
+        " -> Tensor");
+  m.def("decode_attention_dl(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
+        " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
+        " Tensor krotation, Tensor vrotation, float scale) -> Tensor");
+  m.def("decode_attention_dl_lse(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
+        " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
+        " Tensor krotation, Tensor vrotation, float scale) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
@@ -446,4 +546,8 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("ip_scan_topk", &ip_scan_topk);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);
+  m.impl("pack_decode_layout", &pack_decode_layout);
+  m.impl("unpack_decode_layout", &unpack_decode_layout);
+  m.impl("decode_attention_dl", &decode_attention_dl);
+  m.impl("decode_attention_dl_lse", &decode_attention_dl_lse);
 }

@@ -253,13 +253,16 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
 
     // ---- online softmax (register r = token t0 + 4 * quad + r)
     const v4f skk = (sk[0] + sk[1]) + (sk[2] + sk[3]);
-    float s[4];
+    float s[4], vn[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = skk[r] * cur.kn[r];
+    for (int r = 0; r < 4; ++r) {
+      s[r] = skk[r] * cur.kn[r];
+      vn[r] = cur.vn[r];
+    }
     if (t0 + 64 > te) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (t0 + 4 * quad + r >= te) s[r] = -INFINITY;
+        if (t0 + 4 * quad + r >= te) { s[r] = -INFINITY; vn[r] = 0.f; }
     }
     const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     if (__any(lm > M)) {
@@ -388,6 +391,453 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
   if (lse && j == 0) lse[row] = any ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
 }
 
+// ------------------------------------------------------------------ decode layout
+// The decode layout holds the same codes as the bit-plane rows, arranged for the
+// decode kernel (4-bit keys, 2-bit values):
+//   keys    per token d/2 bytes; byte p = (code[2p] << 4) | code[2p+1]
+//   values  per block of 4 consecutive tokens d bytes; byte j = sum_t code[t][j] << 2t
+// Every byte is then one table index: a single v_perm builds its LDS address.
+constexpr int kDlThreads = 512;
+constexpr int kDlWaves = kDlThreads / 64;
+constexpr int kDlEntry = 256;                  // bytes per table index (all copies)
+constexpr int kDlTab = 256 * kDlEntry;         // 64 KB per table
+constexpr int kDlMinSplit = kDlWaves * 64;     // one tile per wave
+
+struct DlArgs {
+  const void* q;
+  int q_dt;
+  int hq, hkv, G;
+  const uint8_t* kpairs;   // [B*hkv][t_cap][32]
+  const float* knorms;     // [B*hkv][t_cap]
+  const uint8_t* vblocks;  // [B*hkv][t_cap/4][64]
+  const float* vnorms;
+  int64_t t_cap;
+  const int32_t* seq_lens;
+  const float* kcen;  // 16
+  const float* vcen;  // 4
+  const float* krot;
+  float qscale;  // softmax scale * log2(e)
+  int64_t split_tokens;
+  int nsplit;
+  float* part;
+  float2* stats;
+  // one split per stream: the kernel writes the output itself
+  const float* vrot;
+  void* out;
+  float* lse;
+};
+
+__device__ __forceinline__ uint32_t byte_addr(uint32_t base_copy, uint32_t w, int byte) {
+  // (byte `byte` of w) * 256 + base_copy: base_copy holds the copy offset in byte 0
+  // and a multiple of 64 KB in byte 2
+  return __builtin_amdgcn_perm(base_copy, w, 0x0c060004u | ((uint32_t)byte << 8));
+}
+
+__device__ __forceinline__ v4h as_v4h(uint32_t lo, uint32_t hi) {
+  u32x2 t = {lo, hi};
+  return __builtin_bit_cast(v4h, t);
+}
+
+// Scale that brings max |x| into [0.5, 1): 2^-e with x = m * 2^e.
+__device__ __forceinline__ float pow2_scale(float amax) {
+  int e = 0;
+  if (amax > 0.f && amax < INFINITY) frexpf(amax, &e);
+  return ldexpf(1.f, -e);
+}
+
+// EXACT_V: the weights and V centroids enter as fp16 hi + lo parts (three products,
+// about 1e-6 relative), for fp32 outputs; otherwise one fp16 product (about 5e-4).
+template <bool EXACT_V>
+__global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
+  // K table: index = pair byte; 32 copies of (c[high nibble], c[low nibble]) fp32.
+  // V table: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
+  // copies of 4 hi + 4 lo halves.  After the tile loop the bytes hold the reduction.
+  __shared__ __attribute__((aligned(16))) char tabs[2 * kDlTab];
+  __shared__ __attribute__((aligned(16))) float qr_s[4][kDim];
+  __shared__ float qs_s[4][kDim];
+  __shared__ float cen_s[20];
+  __shared__ float sc_s[1];  // value centroid scale
+  __shared__ float red_m[kDlWaves][4];
+  __shared__ float red_l[kDlWaves][4];
+  char* const ktab = tabs;
+  char* const vtab = tabs + kDlTab;
+
+  const int split = blockIdx.x;
+  const int bg = blockIdx.y;
+  const int b = bg / a.hkv;
+  const int g = bg - b * a.hkv;
+  const int64_t T = min((int64_t)max(a.seq_lens[b], 0), a.t_cap);
+  const int64_t t_begin = (int64_t)split * a.split_tokens;
+  const int64_t t_end = min(T, t_begin + a.split_tokens);
+  const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.G;
+  const int tid = threadIdx.x;
+  if (t_begin >= t_end) {  // uniform
+    if (a.out != nullptr && T == 0 && tid < a.G * kDim) {  // empty sequence: zeros, lse -inf
+      store_from_f32(a.out, qh0 * kDim + tid, 0.f, a.q_dt);
+      if (a.lse && (tid & 63) == 0) a.lse[qh0 + (tid >> 6)] = -INFINITY;
+    }
+    return;
+  }
+
+  // ---- prologue
+  if (tid < 16) cen_s[tid] = a.kcen[tid];
+  else if (tid < 20) cen_s[tid] = a.vcen[tid - 16];
+  if (tid < 4 * kDim) {
+    const int h = tid >> 6, k = tid & 63;
+    qs_s[h][k] = h < a.G ? load_as_f32(a.q, (qh0 + h) * kDim + k, a.q_dt) : 0.f;
+  }
+  __syncthreads();
+  if (tid < 4 * kDim) {
+    const int h = tid >> 6, j = tid & 63;
+    const float4* r4 = reinterpret_cast<const float4*>(a.krot + j * kDim);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kDim / 4; ++k) {
+      const float4 r = r4[k];
+      v = fmaf(r.x, qs_s[h][4 * k], v);
+      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
+      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
+      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
+    }
+    qr_s[h][j] = v * a.qscale;
+  } else if (tid < 4 * kDim + 64) {  // wave 4: value centroid scale
+    const int l = tid & 63;
+    const float vm = wave_max(l < 4 ? fabsf(cen_s[16 + l]) : 0.f);
+    if (l == 0) sc_s[0] = pow2_scale(vm);
+  }
+  __syncthreads();
+  const float vsc = sc_s[0];
+  for (int e = tid; e < 256 * 32; e += kDlThreads) {
+    const int i = e >> 5, c = e & 31;
+    *reinterpret_cast<float2*>(ktab + i * kDlEntry + c * 8) = make_float2(cen_s[i >> 4], cen_s[i & 15]);
+    if constexpr (!EXACT_V) {
+      v4h vv;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) vv[t] = (_Float16)(cen_s[16 + ((i >> (2 * t)) & 3)] * vsc);
+      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 8) = vv;
+    } else if (c < 16) {
+      v4h vh, vl;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float x = cen_s[16 + ((i >> (2 * t)) & 3)] * vsc;
+        vh[t] = (_Float16)x;
+        vl[t] = (_Float16)(x - (float)vh[t]);
+      }
+      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 16) = vh;
+      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 16 + 8) = vl;
+    }
+  }
+  __syncthreads();
+
+  const int wave = tid >> 6, lane = tid & 63;
+  const int quad = lane >> 2, hn = lane & 3;
+  float qv[kDim];  // (R_k q) * scale * log2(e) of head hn
+#pragma unroll
+  for (int j = 0; j < kDim; j += 4) {
+    const float4 t4 = *reinterpret_cast<const float4*>(&qr_s[hn][j]);
+    qv[j] = t4.x; qv[j + 1] = t4.y; qv[j + 2] = t4.z; qv[j + 3] = t4.w;
+  }
+  // byte 0: copy offset; byte 2 of vcopy: the V table's 64 KB base
+  const uint32_t kcopy = (uint32_t)(lane & 31) * 8;
+  const uint32_t vcopy =
+      (uint32_t)kDlTab | (EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8);
+
+  const size_t sbase = (size_t)bg * (size_t)a.t_cap;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
+  const __amdgpu_buffer_rsrc_t vrs =
+      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 3) >> 2) * 64);
+  // Norms are read four tokens at a time: the range covers whole quads (inside the
+  // allocation, t_cap % 4 == 0); entries past t_end are masked.
+  const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
+  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
+  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
+  const int te = (int)t_end;
+
+  struct Tile {
+    uint32_t k[8];   // this lane's token: 32 pair bytes
+    uint32_t v[4];   // this quad's block: value bytes of dims 16*hn .. 16*hn+15
+    float kn[4], vn[4];
+  };
+  auto load_tile = [&](int t0, Tile& x) {
+    const uint32_t ko = (uint32_t)(t0 + lane) * 32;
+    const u32x4 k0 = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
+    const u32x4 k1 = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 16, 0);
+    x.k[0] = k0.x; x.k[1] = k0.y; x.k[2] = k0.z; x.k[3] = k0.w;
+    x.k[4] = k1.x; x.k[5] = k1.y; x.k[6] = k1.z; x.k[7] = k1.w;
+    const uint32_t vo = (uint32_t)((t0 >> 2) + quad) * 64 + 16 * hn;
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
+    x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+    // norms of the quad's four tokens: 16-byte aligned (t_cap % 4 == 0, aligned base)
+    const uint32_t no = (uint32_t)(t0 + 4 * quad) * 4;
+    const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
+    const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
+    // (__builtin_bit_cast of a vector element would read element 0: convert by value)
+    x.kn[0] = __uint_as_float(kn4.x); x.kn[1] = __uint_as_float(kn4.y);
+    x.kn[2] = __uint_as_float(kn4.z); x.kn[3] = __uint_as_float(kn4.w);
+    x.vn[0] = __uint_as_float(vn4.x); x.vn[1] = __uint_as_float(vn4.y);
+    x.vn[2] = __uint_as_float(vn4.z); x.vn[3] = __uint_as_float(vn4.w);
+  };
+
+  float M = -INFINITY, l = 0.f;
+  v4f acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  // One 64-token tile of this wave: x holds its data, loaded one tile ahead.
+  auto process = [&](const Tile& cur, int t0) {
+    // ---- q.K: A = c[code] of this lane's token (fp32), B = query of head hn
+    v4f sk[8];  // eight chains: no MFMA waits on the one issued just before it
+#pragma unroll
+    for (int x = 0; x < 8; ++x) sk[x] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 32; ++p) {
+      const float2 cc = *reinterpret_cast<const float2*>(tabs + byte_addr(kcopy, cur.k[p >> 2], p & 3));
+      sk[p & 3] = __builtin_amdgcn_mfma_f32_4x4x1f32(cc.x, qv[2 * p], sk[p & 3], 0, 0, 0);
+      sk[4 + (p & 3)] = __builtin_amdgcn_mfma_f32_4x4x1f32(cc.y, qv[2 * p + 1], sk[4 + (p & 3)], 0, 0, 0);
+    }
+    const v4f skk = ((sk[0] + sk[1]) + (sk[2] + sk[3])) + ((sk[4] + sk[5]) + (sk[6] + sk[7]));
+
+    // ---- online softmax (register r = token t0 + 4 * quad + r, head hn)
+    // Tokens at or past te are masked with selects at their use (branch-free: a masked
+    // copy of the norms merged from a branch was miscompiled -- registers of the live
+    // norms reused before their last read).
+    const int nvalid = te - (t0 + 4 * quad);
+    float s[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = r < nvalid ? skk[r] * cur.kn[r] : -INFINITY;
+    const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    if (__any(lm > M)) {
+      float m2 = lm;
+      m2 = fmaxf(m2, __shfl_xor(m2, 4));
+      m2 = fmaxf(m2, __shfl_xor(m2, 8));
+      m2 = fmaxf(m2, __shfl_xor(m2, 16));
+      m2 = fmaxf(m2, __shfl_xor(m2, 32));
+      const float mn = fmaxf(M, m2);
+      const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
+      l *= f;
+      const v4f fv = {__shfl(f, 0), __shfl(f, 1), __shfl(f, 2), __shfl(f, 3)};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] *= fv;
+      M = mn;
+    }
+    v4h wh, wl;
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p = __builtin_amdgcn_exp2f(s[r] - M);
+      psum += p;
+      const float w = r < nvalid ? p * cur.vn[r] : 0.f;
+      wh[r] = (_Float16)w;
+      if constexpr (EXACT_V) wl[r] = (_Float16)(w - (float)wh[r]);
+    }
+    l += psum;
+    // The weights are written by VALU conversions and read by the MFMAs below as the A
+    // operand.  Pinning them here (the empty asm materializes them) and the schedule
+    // barriers keep the table lookups (at least 16 instructions) between the two: issued
+    // right after a v_cvt_pk_f16_f32, an MFMA has read stale operand registers on gfx950.
+    {
+      u32x2 w2 = __builtin_bit_cast(u32x2, wh);
+      uint32_t w2x = w2.x, w2y = w2.y;
+      asm volatile("" : "+v"(w2x), "+v"(w2y));
+      wh = as_v4h(w2x, w2y);
+      if constexpr (EXACT_V) {
+        u32x2 l2 = __builtin_bit_cast(u32x2, wl);
+        uint32_t l2x = l2.x, l2y = l2.y;
+        asm volatile("" : "+v"(l2x), "+v"(l2y));
+        wl = as_v4h(l2x, l2y);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- p.V: acc[i] (lane (quad, hn), register m) = head m, dim 16*hn + i
+    if constexpr (!EXACT_V) {
+      v4h bv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        bv[i] = *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[i >> 2], i & 3));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bv[i], acc[i], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i0 = 0; i0 < 16; i0 += 4) {
+        v4h bh[4], bl[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u32x4 e = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[(i0 + u) >> 2], (i0 + u) & 3));
+          bh[u] = as_v4h(e.x, e.y);
+          bl[u] = as_v4h(e.z, e.w);
+        }
+        if (i0 == 0) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bh[u], acc[i0 + u], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wl, bh[u], acc[i0 + u], 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bl[u], acc[i0 + u], 0, 0, 0);
+      }
+    }
+
+  };
+
+  // Two tile buffers used in turn, so no copy waits for the prefetch to land.
+  constexpr int kStep = kDlWaves * 64;
+  int t0 = (int)t_begin + wave * 64;
+  Tile ta, tb;
+  if (t0 < te) load_tile(t0, ta);
+  while (t0 < te) {
+    load_tile(t0 + kStep, tb);
+    process(ta, t0);
+    t0 += kStep;
+    if (t0 >= te) break;
+    load_tile(t0 + kStep, ta);
+    process(tb, t0);
+    t0 += kStep;
+  }
+
+  // ---- reduction: lanes of a head; quads of a row (DPP); rows and waves (LDS)
+  l += __shfl_xor(l, 4);
+  l += __shfl_xor(l, 8);
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (lane < 4) {
+    red_m[wave][lane] = M;
+    red_l[wave][lane] = l;
+  }
+  __syncthreads();  // also: every wave is done with the tables
+  float mx[4], fw[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    float v = red_m[0][m];
+#pragma unroll
+    for (int w = 1; w < kDlWaves; ++w) v = fmaxf(v, red_m[w][m]);
+    mx[m] = v;
+    const float mw = red_m[wave][m];
+    fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]);
+  }
+  float* red = reinterpret_cast<float*>(tabs);  // [wave*4 + row][i][hn][m]
+  const v4f fwv = {fw[0], fw[1], fw[2], fw[3]};
+  const int row = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v4f x = acc[i] * fwv;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {  // sum of the row's four quads (same hn)
+      float y = x[m];
+      y += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x124, 0xF, 0xF, false));
+      y += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x128, 0xF, 0xF, false));
+      x[m] = y;
+    }
+    if ((lane & 15) < 4)
+      *reinterpret_cast<v4f*>(red + (((wave * 4 + row) * 16 + i) * 16 + hn * 4)) = x;
+  }
+  __syncthreads();
+  if (tid < 4 * kDim) {
+    const int m = tid >> 6, dim = tid & 63;
+    const int j = dim >> 4, i = dim & 15;
+    float sum = 0.f;
+    for (int wr = 0; wr < kDlWaves * 4; ++wr) sum += red[(wr * 16 + i) * 16 + j * 4 + m];
+    float L = 0.f;
+    for (int w = 0; w < kDlWaves; ++w)
+      if (red_m[w][m] != -INFINITY) L += red_l[w][m] * __builtin_amdgcn_exp2f(red_m[w][m] - mx[m]);
+    if (a.out == nullptr) {  // several splits: partials for the combine kernel
+      if (m < a.G) {
+        a.part[((qh0 + m) * a.nsplit + split) * kDim + dim] = sum / vsc;
+        if (dim == 0) a.stats[(qh0 + m) * a.nsplit + split] = make_float2(mx[m], L);
+      }
+    } else {  // the whole sequence: out = (o / L) @ R_v here
+      qs_s[m][dim] = L > 0.f ? sum / (vsc * L) : 0.f;
+    }
+    if (a.out != nullptr && m < a.G && dim == 0 && a.lse)
+      a.lse[qh0 + m] = L > 0.f ? (mx[m] + log2f(L)) * 0.69314718055994531f : -INFINITY;
+  }
+  if (a.out != nullptr) {
+    __syncthreads();
+    if (tid < 4 * kDim) {
+      const int m = tid >> 6, dim = tid & 63;
+      if (m < a.G) {
+        float r = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], a.vrot[k * kDim + dim], r);
+        store_from_f32(a.out, (qh0 + m) * kDim + dim, r, a.q_dt);
+      }
+    }
+  }
+}
+
+// Bit-plane rows -> decode layout.  keys: one thread per output byte.  values: one
+// thread per (block, dim) byte of the blocks that tokens [pos, pos + n) touch; bits of
+// tokens outside that range are kept.
+__global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_streams, int64_t n,
+                               int d, int bits, int values, uint8_t* __restrict__ cache,
+                               int64_t t_cap, int64_t pos) {
+  const int bpp = (d + 7) / 8;
+  const int P = bits * bpp;
+  auto code = [&](int64_t s, int64_t t, int j) -> uint32_t {  // t relative to pos
+    const uint8_t* row = packed + (s * n + t) * P;
+    uint32_t c = 0;
+    for (int p = 0; p < bits; ++p) c |= ((row[p * bpp + (j >> 3)] >> (7 - (j & 7))) & 1u) << p;
+    return c;
+  };
+  if (!values) {
+    const int half = d / 2;
+    const int64_t total = n_streams * n * half;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+      const int pidx = (int)(e % half);
+      const int64_t r = e / half, s = r / n, t = r - s * n;
+      cache[(s * t_cap + pos + t) * half + pidx] =
+          (uint8_t)((code(s, t, 2 * pidx) << 4) | code(s, t, 2 * pidx + 1));
+    }
+  } else {
+    const int64_t b0 = pos >> 2, b1 = (pos + n + 3) >> 2;
+    const int64_t nb = b1 - b0;
+    const int64_t total = n_streams * nb * d;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+      const int j = (int)(e % d);
+      const int64_t r = e / d, s = r / nb, blk = b0 + (r - s * nb);
+      uint8_t* dst = cache + (s * (t_cap >> 2) + blk) * d + j;
+      uint32_t v = *dst;
+      for (int tt = 0; tt < 4; ++tt) {
+        const int64_t t = blk * 4 + tt - pos;
+        if (t < 0 || t >= n) continue;
+        v = (v & ~(3u << (2 * tt))) | (code(s, t, j) << (2 * tt));
+      }
+      *dst = (uint8_t)v;
+    }
+  }
+}
+
+// Decode layout -> bit-plane rows of tokens [t0, t0 + n): one thread per output byte.
+__global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_streams,
+                                 int64_t t_cap, int64_t t0, int64_t n, int d, int bits, int values,
+                                 uint8_t* __restrict__ packed) {
+  const int bpp = (d + 7) / 8;
+  const int P = bits * bpp;
+  const int64_t total = n_streams * n * P;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int byte = (int)(e % P);
+    const int64_t r = e / P, s = r / n, t = t0 + (r - s * n);
+    const int p = byte / bpp, o = byte - p * bpp;
+    uint32_t out = 0;
+    for (int k = 0; k < 8; ++k) {
+      const int j = 8 * o + k;
+      if (j >= d) break;
+      uint32_t c;
+      if (!values) {
+        const uint8_t pb = cache[(s * t_cap + t) * (d / 2) + (j >> 1)];
+        c = (j & 1) ? (pb & 15u) : (pb >> 4);
+      } else {
+        c = (cache[(s * (t_cap >> 2) + (t >> 2)) * d + j] >> (2 * (t & 3))) & 3u;
+      }
+      out |= ((c >> p) & 1u) << (7 - k);
+    }
+    packed[e] = (uint8_t)out;
+  }
+}
+
 struct SplitPlan {
   int64_t split_tokens;
   int nsplit;
@@ -477,3 +927,128 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
 }
 
 }  // namespace tq
+
+// ------------------------------------------------------------------ decode-layout C ABI
+namespace tq {
+namespace {
+
+SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
+  // one 512-thread workgroup per CU (128 KB of tables)
+  const int64_t streams = (int64_t)B * hkv;
+  const int64_t want = std::max<int64_t>(1, ((int64_t)device_cu_count() + streams - 1) / streams);
+  int64_t split = (t_cap + want - 1) / want;
+  split = std::max<int64_t>(kDlMinSplit, (split + kDlMinSplit - 1) / kDlMinSplit * kDlMinSplit);
+  return {split, (int)((t_cap + split - 1) / split)};
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t t_cap) {
+  if (B <= 0 || hq <= 0 || hkv <= 0 || t_cap <= 0) return 256;
+  const SplitPlan p = plan_dl_splits(B, hkv, t_cap);
+  const size_t rows = (size_t)B * hq;
+  return 256 + align_up(rows * p.nsplit * kDim * 4, 256) + align_up(rows * p.nsplit * 8, 256);
+}
+
+int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                           int32_t d, const uint8_t* kpairs, const float* knorms,
+                           const uint8_t* vblocks, const float* vnorms, int64_t t_cap,
+                           const int32_t* seq_lens, const float* kcentroids,
+                           const float* vcentroids, const float* krotation,
+                           const float* vrotation, int32_t kbits, int32_t vbits, float scale,
+                           void* out, float* lse, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  if (d != kDim || kbits != 4 || vbits != 2)
+    return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-bit "
+                                 "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
+  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
+             "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
+  TQ_REQUIRE(t_cap >= 0 && t_cap % 4 == 0, "capacity must be a multiple of 4, got %lld",
+             (long long)t_cap);
+  TQ_REQUIRE(t_cap * 32 < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
+  TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
+  if (B == 0) return TQ_OK;
+  TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
+             "null pointer argument");
+  TQ_REQUIRE(t_cap == 0 || (kpairs && knorms && vblocks && vnorms), "null pointer argument");
+  TQ_REQUIRE((reinterpret_cast<uintptr_t>(krotation) & 15u) == 0, "rotation must be 16-byte aligned");
+  TQ_REQUIRE(t_cap == 0 || ((reinterpret_cast<uintptr_t>(kpairs) | reinterpret_cast<uintptr_t>(vblocks) |
+                             reinterpret_cast<uintptr_t>(knorms) | reinterpret_cast<uintptr_t>(vnorms)) &
+                            15u) == 0,
+             "decode-layout K/V and norms must be 16-byte aligned");
+  const size_t need = tq_decode_dl_workspace_bytes(B, hq, hkv, t_cap);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t st = as_stream(stream);
+  const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
+  const size_t rows = (size_t)B * hq;
+  char* ws = static_cast<char*>(workspace) + 256;
+  float* part = reinterpret_cast<float*>(ws);
+  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
+  if (t_cap > 0) {
+    DlArgs a{};
+    a.q = q; a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv; a.G = hq / hkv;
+    a.kpairs = kpairs; a.knorms = knorms; a.vblocks = vblocks; a.vnorms = vnorms;
+    a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
+    a.krot = krotation; a.qscale = scale * 1.4426950408889634f;
+    a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
+    const bool single = p.nsplit == 1;
+    a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
+    const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
+    if (q_dtype == TQ_F32)
+      hipLaunchKernelGGL(dl_decode_kernel<true>, grid, dim3(kDlThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL(dl_decode_kernel<false>, grid, dim3(kDlThreads), 0, st, a);
+    TQ_LAUNCH_CHECK("dl_decode_kernel");
+    if (single) return TQ_OK;
+  }
+  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
+                     p.nsplit, p.split_tokens, seq_lens, t_cap, hq, vrotation, (int)q_dtype, out,
+                     lse);
+  TQ_LAUNCH_CHECK("fused_combine_kernel");
+  return TQ_OK;
+}
+
+int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,
+                          int32_t bit_width, int32_t values, uint8_t* cache, int64_t t_cap,
+                          int64_t pos, void* stream) {
+  TQ_REQUIRE(values == 0 || values == 1, "values must be 0 (keys) or 1 (values)");
+  TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
+  TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
+  TQ_REQUIRE(n_streams >= 0 && n >= 0 && pos >= 0 && pos + n <= t_cap, "bad token range");
+  TQ_REQUIRE(!values || t_cap % 4 == 0, "value capacity must be a multiple of 4");
+  if (n_streams == 0 || n == 0) return TQ_OK;
+  TQ_REQUIRE(packed && cache, "null pointer argument");
+  const int64_t per = values ? (((pos + n + 3) >> 2) - (pos >> 2)) * d : n * (d / 2);
+  const int64_t total = n_streams * per;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
+                     n_streams, n, d, bit_width, values, cache, t_cap, pos);
+  TQ_LAUNCH_CHECK("dl_pack_kernel");
+  return TQ_OK;
+}
+
+int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_cap, int64_t t0,
+                            int64_t n, int32_t d, int32_t bit_width, int32_t values,
+                            uint8_t* packed, void* stream) {
+  TQ_REQUIRE(values == 0 || values == 1, "values must be 0 (keys) or 1 (values)");
+  TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
+  TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
+  TQ_REQUIRE(n_streams >= 0 && n >= 0 && t0 >= 0 && t0 + n <= t_cap, "bad token range");
+  TQ_REQUIRE(!values || t_cap % 4 == 0, "value capacity must be a multiple of 4");
+  if (n_streams == 0 || n == 0) return TQ_OK;
+  TQ_REQUIRE(packed && cache, "null pointer argument");
+  const int64_t total = n_streams * n * bit_width * ((d + 7) / 8);
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(dl_unpack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     cache, n_streams, t_cap, t0, n, d, bit_width, values, packed);
+  TQ_LAUNCH_CHECK("dl_unpack_kernel");
+  return TQ_OK;
+}
+
+}  // extern "C"
