@@ -10,6 +10,12 @@ Scores and values read the packed codes directly (attention_scores_packed /
 attention_values_packed kernels); `decode_attention` runs the fused GQA decode
 kernel.  Query heads may be a multiple of the KV heads (head h reads KV head
 h // (Hq / H), as HF's repeat_kv does); the reference only handles equal counts.
+
+For 4-bit keys and 2-bit values at head_dim 64 (MSE mode) the codes are kept in the
+decode layout (same bytes per token, arranged for the decode kernel: key bytes hold two
+4-bit codes, value bytes hold one dim of four consecutive tokens); the reference keeps
+its packed storage private (cache.py:81-130), so only `_key_packed` / `_val_packed`,
+which return the bit-plane rows, see the difference.
 """
 
 from __future__ import annotations
@@ -75,23 +81,30 @@ class QuantizedKVCache:
         self._vbnd, self._vcen = vcb[0].to(dev), vcb[1].to(dev)
 
         bpp = (head_dim + 7) // 8
-        B, H, T = batch_size, num_heads, max_seq_len
+        self._dl = (not self._is_prod and kb == 4 and vb == 2 and head_dim == 64)
+        # decode-layout value blocks hold 4 tokens: capacity rounded up to a multiple of 4
+        self._t_cap = (max_seq_len + 3) // 4 * 4 if self._dl else max_seq_len
+        B, H, T = batch_size, num_heads, self._t_cap
         u8 = dict(dtype=torch.uint8, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         self._protected = config.protected_layers > 0
-        self._key_packed, self._key_norms, self._val_packed, self._val_norms = [], [], [], []
+        self._kstore, self._key_norms, self._vstore, self._val_norms = [], [], [], []
         self._key_qjl_signs, self._key_res_norms, self._val_qjl_signs, self._val_res_norms = [], [], [], []
         self._key_fp, self._val_fp = [], []
         for layer in range(num_layers):
             if self._protected and layer < config.protected_layers:
                 self._key_fp.append(torch.zeros(B, H, T, head_dim, dtype=torch.float16, device=dev))
                 self._val_fp.append(torch.zeros(B, H, T, head_dim, dtype=torch.float16, device=dev))
-                for lst in (self._key_packed, self._key_norms, self._val_packed, self._val_norms):
+                for lst in (self._kstore, self._key_norms, self._vstore, self._val_norms):
                     lst.append(None)
                 continue
-            self._key_packed.append(torch.zeros(B, H, T, kb * bpp, **u8))
+            if self._dl:
+                self._kstore.append(torch.zeros(B, H, T, head_dim // 2, **u8))
+                self._vstore.append(torch.zeros(B, H, T // 4, head_dim, **u8))
+            else:
+                self._kstore.append(torch.zeros(B, H, T, kb * bpp, **u8))
+                self._vstore.append(torch.zeros(B, H, T, vb * bpp, **u8))
             self._key_norms.append(torch.zeros(B, H, T, **f32))
-            self._val_packed.append(torch.zeros(B, H, T, vb * bpp, **u8))
             self._val_norms.append(torch.zeros(B, H, T, **f32))
             if self._is_prod:
                 self._key_qjl_signs.append(torch.zeros(B, H, T, bpp, **u8))
@@ -102,6 +115,28 @@ class QuantizedKVCache:
     # ------------------------------------------------------------------ helpers
     def _is_protected_layer(self, layer_id: int) -> bool:
         return self._protected and layer_id < self.config.protected_layers
+
+    def _rows(self, layer_id: int, values: bool, T: int) -> torch.Tensor:
+        """Bit-plane packed rows [B, H, T, P] of tokens 0..T-1 (reference.py:191-224)."""
+        st = (self._vstore if values else self._kstore)[layer_id]
+        if not self._dl:
+            return st[:, :, :T]
+        B, H = self.batch_size, self.num_heads
+        bits = self._vbits_stored if values else self._kbits_stored
+        r = ops.unpack_decode_layout(st.view(B * H, st.shape[2], st.shape[3]), self.head_dim, bits,
+                                     values, 0, T)
+        return r.view(B, H, T, -1)
+
+    @property
+    def _key_packed(self):
+        """Per layer: packed key rows [B, H, max_seq_len, P] (None for protected layers)."""
+        return [None if st is None else self._rows(l, False, self.max_seq_len)
+                for l, st in enumerate(self._kstore)]
+
+    @property
+    def _val_packed(self):
+        return [None if st is None else self._rows(l, True, self.max_seq_len)
+                for l, st in enumerate(self._vstore)]
 
     def _as_bhsd(self, t: torch.Tensor) -> torch.Tensor:
         if t.dim() == 3:
@@ -133,19 +168,31 @@ class QuantizedKVCache:
             return
         T = self._ops_quantize(key, self._key_rotation, self._kbnd, self._kcen,
                                getattr(self, "_key_S", None), self.config.key_bits)
-        self._key_packed[layer_id][:, :, sl] = T[0].view(B, H, s, -1)
+        self._store(layer_id, False, T[0].view(B * H, s, -1), pos)
         self._key_norms[layer_id][:, :, sl] = T[-1].float().view(B, H, s)
         if self._is_prod:
             self._key_qjl_signs[layer_id][:, :, sl] = T[1].view(B, H, s, -1)
             self._key_res_norms[layer_id][:, :, sl] = T[2].float().view(B, H, s)
         V = self._ops_quantize(value, self._val_rotation, self._vbnd, self._vcen,
                                getattr(self, "_val_S", None), self.config.value_bits)
-        self._val_packed[layer_id][:, :, sl] = V[0].view(B, H, s, -1)
+        self._store(layer_id, True, V[0].view(B * H, s, -1), pos)
         self._val_norms[layer_id][:, :, sl] = V[-1].float().view(B, H, s)
         if self._is_prod:
             self._val_qjl_signs[layer_id][:, :, sl] = V[1].view(B, H, s, -1)
             self._val_res_norms[layer_id][:, :, sl] = V[2].float().view(B, H, s)
         self.seq_lens[layer_id] += s
+
+    def _store(self, layer_id: int, values: bool, rows: torch.Tensor, pos: int) -> None:
+        """Write bit-plane rows [B*H, s, P] at tokens pos..pos+s of every (batch, head)."""
+        st = (self._vstore if values else self._kstore)[layer_id]
+        B, H = self.batch_size, self.num_heads
+        s = rows.shape[1]
+        if self._dl:
+            bits = self._vbits_stored if values else self._kbits_stored
+            ops.pack_decode_layout(rows, st.view(B * H, st.shape[2], st.shape[3]), self.head_dim,
+                                   bits, values, pos)
+        else:
+            st[:, :, pos:pos + s] = rows.view(B, H, s, -1)
 
     def _ops_quantize(self, x, R, bnd, cen, S, bits):
         flat = x.reshape(-1, self.head_dim)
@@ -154,13 +201,13 @@ class QuantizedKVCache:
         return _ops().quantize_mse_packed(flat, R, bnd, bits)
 
     # ------------------------------------------------------------------ dequantize
-    def _dequant(self, layer_id, packed, norms, signs, res, R, cen, S, bits):
+    def _dequant(self, layer_id, values, norms, signs, res, R, cen, S, bits):
         T = int(self.seq_lens[layer_id].item())
         B, H, d = self.batch_size, self.num_heads, self.head_dim
         if T == 0:
             out = torch.zeros(B, H, 0, d, dtype=torch.float32, device=self.device)
         else:
-            p = packed[layer_id][:, :, :T].reshape(B * H * T, -1)
+            p = self._rows(layer_id, values, T).reshape(B * H * T, -1)
             n = norms[layer_id][:, :, :T].reshape(-1)
             if self._is_prod:
                 out = _ops().dequantize_prod_packed(
@@ -177,7 +224,7 @@ class QuantizedKVCache:
             T = int(self.seq_lens[layer_id].item())
             k = self._key_fp[layer_id][:, :, :T].float()
             return k[0] if self.batch_size == 1 else k
-        return self._dequant(layer_id, self._key_packed, self._key_norms, self._key_qjl_signs,
+        return self._dequant(layer_id, False, self._key_norms, self._key_qjl_signs,
                              self._key_res_norms, self._key_rotation, self._kcen,
                              getattr(self, "_key_S", None), self.config.key_bits)
 
@@ -186,7 +233,7 @@ class QuantizedKVCache:
             T = int(self.seq_lens[layer_id].item())
             v = self._val_fp[layer_id][:, :, :T].float()
             return v[0] if self.batch_size == 1 else v
-        return self._dequant(layer_id, self._val_packed, self._val_norms, self._val_qjl_signs,
+        return self._dequant(layer_id, True, self._val_norms, self._val_qjl_signs,
                              self._val_res_norms, self._val_rotation, self._vcen,
                              getattr(self, "_val_S", None), self.config.value_bits)
 
@@ -219,13 +266,14 @@ class QuantizedKVCache:
         else:
             logits = torch.empty(Bq, Hq, sq, T, dtype=torch.float32, device=self.device)
             if T > 0:
+                rows = self._rows(layer_id, False, T)
                 qf = q4.float()
                 for kvb in range(self.batch_size):
                     qbs = slice(None) if self.batch_size == 1 else slice(kvb, kvb + 1)
                     for g in range(self.num_heads):
                         qs = qf[qbs, g * G:(g + 1) * G]            # (b', G, sq, d)
                         s = ops.attention_scores_packed(
-                            qs.reshape(1, -1, d), self._key_packed[layer_id][kvb, g, :T],
+                            qs.reshape(1, -1, d), rows[kvb, g],
                             self._key_norms[layer_id][kvb, g, :T], self._kcen, self._key_rotation,
                             self.config.key_bits)
                         logits[qbs, g * G:(g + 1) * G] = s.view(qs.shape[0], G, sq, T)
@@ -247,13 +295,14 @@ class QuantizedKVCache:
             out = torch.matmul(w4.float(), vals.expand(Bq, -1, -1, -1))
         else:
             out = torch.empty(Bq, Hq, sq, d, dtype=torch.float32, device=self.device)
+            rows = self._rows(layer_id, True, T) if T > 0 else None
             wf = w4.float()
             for kvb in range(self.batch_size):
                 qbs = slice(None) if self.batch_size == 1 else slice(kvb, kvb + 1)
                 for g in range(self.num_heads):
                     ws = wf[qbs, g * G:(g + 1) * G]
                     o = ops.attention_values_packed(
-                        ws.reshape(1, -1, T), self._val_packed[layer_id][kvb, g, :T],
+                        ws.reshape(1, -1, T), rows[kvb, g],
                         self._val_norms[layer_id][kvb, g, :T], self._vcen, self._val_rotation,
                         self.config.value_bits)
                     out[qbs, g * G:(g + 1) * G] = o.view(ws.shape[0], G, sq, d)
@@ -278,10 +327,18 @@ class QuantizedKVCache:
         if seq_lens is None:
             seq_lens = torch.full((B,), int(self.seq_lens[layer_id].item()), dtype=torch.int32,
                                   device=self.device)
+        G = q.shape[1] // self.num_heads
+        if self._dl and G <= 4 and q.shape[1] % self.num_heads == 0:
+            return ops.decode_attention_dl(
+                q, self._kstore[layer_id], self._key_norms[layer_id], self._vstore[layer_id],
+                self._val_norms[layer_id], seq_lens, self._kcen, self._vcen, self._key_rotation,
+                self._val_rotation, scale)
+        Tc = self._t_cap
         return ops.decode_attention_packed(
-            q, self._key_packed[layer_id], self._key_norms[layer_id], self._val_packed[layer_id],
-            self._val_norms[layer_id], seq_lens, self._kcen, self._vcen, self._key_rotation,
-            self._val_rotation, self.config.key_bits, self.config.value_bits, scale)
+            q, self._rows(layer_id, False, Tc), self._key_norms[layer_id],
+            self._rows(layer_id, True, Tc), self._val_norms[layer_id], seq_lens, self._kcen,
+            self._vcen, self._key_rotation, self._val_rotation, self.config.key_bits,
+            self.config.value_bits, scale)
 
     # ------------------------------------------------------------------ accounting
     def memory_bytes(self) -> int:

@@ -70,3 +70,33 @@ def decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens, k
     return _ops().decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens,
                                               kcentroids, vcentroids, krotation, vrotation, kbits,
                                               vbits, float(scale))
+
+
+def pack_decode_layout(packed: torch.Tensor, cache: torch.Tensor, dim: int, bit_width: int,
+                       values: bool, pos: int) -> None:
+    """Write bit-plane rows [streams, n, P] into a decode-layout cache at tokens pos..pos+n
+    (keys: [streams, t_cap, dim/2] pair bytes, 4-bit; values: [streams, t_cap/4, dim] block
+    bytes, 2-bit)."""
+    _require_device(cache, "cache")
+    _ops().pack_decode_layout(packed, cache, dim, bit_width, int(values), pos)
+
+
+def unpack_decode_layout(cache: torch.Tensor, dim: int, bit_width: int, values: bool, t0: int,
+                         n: int) -> torch.Tensor:
+    """Tokens t0..t0+n of a decode-layout cache as bit-plane rows [streams, n, P]."""
+    _require_device(cache, "cache")
+    return _ops().unpack_decode_layout(cache, dim, bit_width, int(values), t0, n)
+
+
+def decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids, vcentroids,
+                        krotation, vrotation, scale, return_lse: bool = False):
+    """decode_attention_packed over a decode-layout cache (4-bit keys, 2-bit values,
+    head_dim 64, 1-4 query heads per KV head): [B, Hq, d] in q.dtype (and the [B, Hq]
+    log-sum-exp with return_lse)."""
+    _require_device(q, "q")
+    if return_lse:
+        return _ops().decode_attention_dl_lse(q, kpairs, knorms, vblocks, vnorms, seq_lens,
+                                              kcentroids, vcentroids, krotation, vrotation,
+                                              float(scale))
+    return _ops().decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids,
+                                      vcentroids, krotation, vrotation, float(scale))
