@@ -150,6 +150,25 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
                     size_t workspace_bytes, void* stream);
 
 /*
+ * The same scan (and tq_attention_scores_packed) over 4-bit rows in the pair layout:
+ * row i is d/2 bytes, byte p = code[i][2p] << 4 | code[i][2p+1] -- the bytes of the
+ * bit-plane row rearranged, written by tq_pack_decode_layout (values = 0, one stream,
+ * t_cap = N).  Identical scores and ids; each code is one masked nibble, so a lookup
+ * costs one address instruction instead of two.  d must be 64 or 128 and `pairs`
+ * 16-byte aligned.  Workspace: tq_scan_workspace_bytes(nq, d, 4, N, k) / (nq, d, 4, 0, 0).
+ * TurboQuantIndex keeps 4-bit MSE databases of those dims in this layout.
+ */
+int tq_ip_scan_topk_pairs(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                          const uint8_t* pairs, const float* norms, int64_t N,
+                          const float* centroids, const float* rotation, int32_t k,
+                          float* out_scores, int64_t* out_ids, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                              const uint8_t* pairs, const float* key_norms, int64_t T,
+                              const float* centroids, const float* rotation, float* scores,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Fused GQA decode attention over a packed KV cache (new op: the semantics of
  * QuantizedKVCache.attention_scores -> softmax -> attention_values,
  * turboquant_kv/cache.py:282-339 with turboquant_kv/vllm_plugin/__init__.py:400,

@@ -130,6 +130,46 @@ def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
 
+def k_pack_pairs(packed, d):
+    """Bit-plane 4-bit rows [N, d/2] -> pair-layout rows (tq_pack_decode_layout, one stream)."""
+    N = packed.shape[0]
+    out = torch.zeros(max(N, 1), d // 2, dtype=torch.uint8, device=DEV)
+    if N:
+        capi.check(L().tq_pack_decode_layout(capi.p(T(packed)), capi.i64(1), capi.i64(N), capi.i32(d),
+                                             capi.i32(4), capi.i32(0), capi.p(out), capi.i64(N),
+                                             capi.i64(0), capi.stream()))
+        sync()
+    return out[:N]
+
+
+def k_scan_pairs(q, pairs, norms, cen, R, k, q_dt=capi.TQ_F32):
+    Q, d = q.shape
+    N = pairs.shape[0]
+    os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
+    oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, 4, N, k), 1), dtype=torch.uint8, device=DEV)
+    nt = T(norms) if N else torch.empty(0, dtype=torch.float32, device=DEV)
+    capi.check(L().tq_ip_scan_topk_pairs(capi.p(T(q)), q_dt, capi.i64(Q), capi.i32(d), capi.p(pairs),
+                                         capi.p(nt), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
+                                         capi.i32(k), capi.p(os_), capi.p(oi), capi.p(ws),
+                                         ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return os_.cpu().numpy(), oi.cpu().numpy()
+
+
+def k_scores_pairs(q, pairs, norms, cen, R):
+    Q, d = q.shape
+    N = pairs.shape[0]
+    out = torch.empty(Q, N, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, 4, N, 0), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_attention_scores_pairs(capi.p(T(q)), capi.TQ_F32, capi.i64(Q), capi.i32(d),
+                                             capi.p(pairs), capi.p(T(norms)), capi.i64(N),
+                                             capi.p(T(cen)), capi.p(T(R)), capi.p(out), capi.p(ws),
+                                             ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.cpu().numpy()
+
+
 def k_pack_dl(packed, t_cap, pos, values, cache=None):
     """Bit-plane rows [S, n, P] -> decode-layout cache (created zeroed when None)."""
     S, n, _ = packed.shape
@@ -366,6 +406,72 @@ def test_scan_ties_padding_and_fp16_queries():
     s, i = k_scan(q16, p, nm, cen, R, b, 10, capi.TQ_F16)
     so, io = O.search_topk(q16.astype(np.float32), p, nm, cen, R, b, 10)
     assert np.array_equal(i, io)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_pairs_layout_scan_bit_exact(d):
+    rs = np.random.RandomState(5 * d)
+    N = 20000 + 37  # ragged: not a multiple of the 64-row step
+    R, cen, p, nm = _db(rs, N, d, 4)
+    pairs = k_pack_pairs(p, d)
+    codes = O.unpack_codes(p, 4, d).astype(np.uint8)
+    assert np.array_equal(pairs.cpu().numpy(), (codes[:, 0::2] << 4) | codes[:, 1::2])
+    for Q, k in ((1, 10), (4, 1), (7, 32)):
+        q = rs.randn(Q, d).astype(np.float32)
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = O.search_topk(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), (d, Q, k)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    q = rs.randn(3, d).astype(np.float32)
+    got = k_scores_pairs(q, pairs[:1500], nm[:1500], cen, R)
+    want = O.lut_scores_f32(q, p[:1500], nm[:1500], cen, R, 4)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    q16 = q.astype(np.float16)
+    s, i = k_scan_pairs(q16, pairs, nm, cen, R, 10, capi.TQ_F16)
+    so, io = O.search_topk(q16.astype(np.float32), p, nm, cen, R, 4, 10)
+    assert np.array_equal(i, io)
+
+
+@pytest.mark.parametrize("N", [600_000, 2_200_000])
+def test_scan_many_blocks_merge(N):
+    # Enough rows for hundreds of block lists (up to the full 1024-block grid), so the
+    # merge's group maxima span several blocks per thread.
+    rs = np.random.RandomState(N % 1000)
+    d = 64
+    R, cen, p, nm = _db(rs, N, d, 4)
+    q = rs.randn(3, d).astype(np.float32)
+    pairs = k_pack_pairs(p, d)
+    s32, i32 = O.search_topk(q, p, nm, cen, R, 4, 32)  # top-k for smaller k is its prefix
+    for k in (1, 10, 32):
+        so, io = s32[:, :k], i32[:, :k]
+        s, i = k_scan(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        assert np.array_equal(i, io), k
+
+
+def test_pairs_scan_ties_padding_and_golden(golden):
+    rs = np.random.RandomState(13)
+    d = 128
+    R, cen, p, nm = _db(rs, 40, d, 4)
+    p = np.concatenate([p, p[:7], p[:7]])  # duplicated rows tie exactly
+    nm = np.concatenate([nm, nm[:7], nm[:7]])
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(3, d).astype(np.float32)
+    s, i = k_scan_pairs(q, pairs, nm, cen, R, 30)
+    so, io = O.search_topk(q, p, nm, cen, R, 4, 30)
+    assert np.array_equal(i, io)
+    s, i = k_scan_pairs(q, pairs[:5], nm[:5], cen, R, 8)  # k > N pads (-inf, -1)
+    assert (i[:, 5:] == -1).all() and np.isneginf(s[:, 5:]).all()
+    s, i = k_scan_pairs(q, pairs[:0], nm[:0], cen, R, 4)  # empty database
+    assert (i == -1).all() and np.isneginf(s).all()
+    ix, m, rot = golden("index"), golden("quant_mse"), golden("rotation")
+    _, cen4 = O.lloyd_max_codebook(4, 128)
+    s, i = k_scan_pairs(ix["queries"], k_pack_pairs(ix["b4_packed"], 128), m["d128_b4_norms"], cen4,
+                        rot["R_d128_s42"], 10)
+    assert np.array_equal(i, ix["b4_ids"])
+    assert np.allclose(s, ix["b4_scores"], rtol=1e-5, atol=1e-6)
 
 
 # ------------------------------------------------------------------ decode attention

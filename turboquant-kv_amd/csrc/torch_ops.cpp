@@ -337,6 +337,68 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk(const at::Tensor& queries, const
   return {os, oi};
 }
 
+// Same scan over 4-bit pair-layout rows [N, d/2] (d = 64 or 128).
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_pairs(const at::Tensor& queries,
+                                                      const at::Tensor& pairs,
+                                                      const at::Tensor& norms,
+                                                      const at::Tensor& centroids,
+                                                      const at::Tensor& rotation, int64_t k) {
+  require_gpu(queries, "queries");
+  TORCH_CHECK(queries.dim() == 2, "queries must be [Q, d]");
+  TORCH_CHECK(pairs.dim() == 2 && pairs.scalar_type() == at::kByte, "pairs must be uint8 [N, d/2]");
+  c10::DeviceGuard g(queries.device());
+  const auto dev = queries.device();
+  auto q = floatc(queries, dev);
+  auto p = pairs.to(dev).contiguous();
+  auto nm = f32c(norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t Q = q.size(0), d = q.size(1), N = p.size(0);
+  TORCH_CHECK(p.size(1) * 2 == d, "pairs must hold d/2 bytes per row");
+  TORCH_CHECK(nm.numel() == N, "norms must have N entries");
+  TORCH_CHECK(cen.numel() == 16, "pair layout holds 4-bit codes: 16 centroids");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
+  auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
+  if (Q == 0) return {os, oi};
+  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, 4, N, (int32_t)k), dev);
+  check_rc(tq_ip_scan_topk_pairs(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
+                                 p.data_ptr<uint8_t>(), nm.data_ptr<float>(), N,
+                                 cen.data_ptr<float>(), R.data_ptr<float>(), (int32_t)k,
+                                 os.data_ptr<float>(), oi.data_ptr<int64_t>(), ws.data_ptr(),
+                                 ws.numel(), cur_stream(q)));
+  return {os, oi};
+}
+
+at::Tensor attention_scores_pairs(const at::Tensor& query, const at::Tensor& pairs,
+                                  const at::Tensor& key_norms, const at::Tensor& centroids,
+                                  const at::Tensor& rotation) {
+  require_gpu(query, "query");
+  TORCH_CHECK(query.dim() == 3, "query must be [batch, heads, head_dim]");
+  TORCH_CHECK(pairs.dim() == 2 && pairs.scalar_type() == at::kByte, "pairs must be uint8 [T, d/2]");
+  c10::DeviceGuard g(query.device());
+  const auto dev = query.device();
+  auto q = f32c(query, dev);
+  auto pk = pairs.to(dev).contiguous();
+  auto kn = f32c(key_norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t B = q.size(0), H = q.size(1), d = q.size(2), T = pk.size(0);
+  TORCH_CHECK(pk.size(1) * 2 == d, "pairs must hold d/2 bytes per row");
+  TORCH_CHECK(kn.numel() == T, "key_norms must have seq_len entries");
+  TORCH_CHECK(cen.numel() == 16, "pair layout holds 4-bit codes: 16 centroids");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto scores = at::empty({B, H, T}, q.options());
+  if (B * H == 0 || T == 0) return scores;
+  auto ws = workspace(tq_scan_workspace_bytes(B * H, (int32_t)d, 4, T, 0), dev);
+  check_rc(tq_attention_scores_pairs(q.data_ptr(), TQ_F32, B * H, (int32_t)d,
+                                     pk.data_ptr<uint8_t>(), kn.data_ptr<float>(), T,
+                                     cen.data_ptr<float>(), R.data_ptr<float>(),
+                                     scores.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                                     cur_stream(q)));
+  return scores;
+}
+
 std::tuple<at::Tensor, at::Tensor> decode_attention_packed_lse(
     const at::Tensor& q, const at::Tensor& kpacked,
                                    const at::Tensor& knorms, const at::Tensor& vpacked,
@@ -514,6 +576,10 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor centroids, Tensor rotation, Tensor qjl, int bit_width, int dim) -> Tensor");
   m.def("ip_scan_topk(Tensor queries, Tensor packed, Tensor norms, Tensor centroids,"
         " Tensor rotation, int bit_width, int k) -> (Tensor, Tensor)");
+  m.def("ip_scan_topk_pairs(Tensor queries, Tensor pairs, Tensor norms, Tensor centroids,"
+        " Tensor rotation, int k) -> (Tensor, Tensor)");
+  m.def("attention_scores_pairs(Tensor query, Tensor pairs, Tensor key_norms, Tensor centroids,"
+        " Tensor rotation) -> Tensor");
   m.def("decode_attention_packed(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale) -> Tensor");
@@ -544,6 +610,8 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("dequantize_mse_packed", &dequantize_mse_packed);
   m.impl("dequantize_prod_packed", &dequantize_prod_packed);
   m.impl("ip_scan_topk", &ip_scan_topk);
+  m.impl("ip_scan_topk_pairs", &ip_scan_topk_pairs);
+  m.impl("attention_scores_pairs", &attention_scores_pairs);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);
   m.impl("pack_decode_layout", &pack_decode_layout);

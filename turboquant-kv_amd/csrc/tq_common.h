@@ -48,6 +48,16 @@ int device_cu_count();
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// ---------------------------------------------------------------- buffer loads
+// Raw buffer resource over [p, p + bytes): loads through it take 32-bit byte offsets and
+// return zeros for any access that reaches past `bytes` (the hardware range check), so
+// tails need no clamp.  Cache-policy argument of the raw loads: 0 = default, kNT =
+// non-temporal (only for accesses that cover whole cache lines per instruction).
+constexpr int kNT = 2;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+
 // ---------------------------------------------------------------- dtype helpers
 // Round an fp32 value to the nearest bf16 / fp16 value (ties to even) and return it
 // widened back to fp32.  This is how the reference's torch ops round every

@@ -73,7 +73,7 @@ struct DecodeArgs {
 // Raw buffer resource over `bytes` bytes at `p` (gfx9 dword 3); loads past the end
 // return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+  return buf_rsrc(p, bytes);
 }
 
 // NB bytes of a packed row (8, 16, 24 or 32) at byte offset `off` as 32-bit words.

@@ -237,8 +237,26 @@ __device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, 
   __syncthreads();
 }
 
-template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
+// Calls f(dim, addr) for the 8 dims of one 32-bit word of pair-layout bytes (byte p =
+// code[2p] << 4 | code[2p+1]), in dim order; addr = code * SC.  Two shift-and-mask pairs
+// per word put every code of one nibble position at the SC scale, then one v_perm per dim
+// moves its byte into an otherwise zero register.  (A 16-byte code stride would save one
+// shift but puts codes l and l+8 in one LDS bank: 2-way conflicts on every lookup.)
+template <int SC, typename F>
+__device__ __forceinline__ void decode_pairs(uint32_t w, int j0, F&& f) {
+  static_assert(SC == 8 || SC == 16, "code stride");
+  const uint32_t wh = SC == 8 ? (w >> 1) & 0x78787878u : w & 0xF0F0F0F0u;
+  const uint32_t wl = SC == 8 ? (w << 3) & 0x78787878u : (w << 4) & 0xF0F0F0F0u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f(j0 + 2 * k, __builtin_amdgcn_perm(0u, wh, 0x0c0c0c00u | k));
+    f(j0 + 2 * k + 1, __builtin_amdgcn_perm(0u, wl, 0x0c0c0c00u | k));
+  }
+}
+
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS>
 __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
+  static_assert(!PAIRS || (BITS == 4 && !GENERIC), "pair layout: 4-bit fast rows only");
   constexpr int NLEV = 1 << BITS;
   constexpr int BPPT = GENERIC ? 32 : BPP;          // layout the decoder sees
   constexpr int DP = 8 * BPPT;                      // dims covered by the decoder
@@ -286,18 +304,74 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   // when scored): a branch around them would make the compiler wait for every
   // outstanding load, including the next row's prefetch, before each row.
   const int64_t rlast = rend - 1;
-  auto load_row = [&](int64_t r, uint32_t (&w)[NW]) {
-    const int64_t rl = r < rend ? r : rlast;
-    if constexpr (GENERIC) load_generic<BITS>(base + rl * P, a.bpp, w);
-    else RowLoader<BITS, BPP>::load(base + rl * P, w);
+  // A row's words and its norm, loaded together: a norm load issued inside the step
+  // would make the step wait (loads complete in issue order) for every row prefetched
+  // before it.
+  struct RowBuf {
+    uint32_t w[NW];
+    float n;
   };
-  // One 64-row step of this wave: score row `row` from its plane words `cur`.
-  auto step = [&](const uint32_t (&cur)[NW], const int64_t row) {
-    const float nrm = __builtin_nontemporal_load(nbase + (row < rend ? row : rlast));
+  // Fast layouts load through per-block buffer resources: 32-bit offsets from the
+  // block's first row, and rows at or past rend read as zeros (no clamp).
+  const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
+  const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * P, nbr * (uint32_t)P);
+  const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
+  auto load_row = [&](int64_t r, RowBuf& b) {
+    if constexpr (GENERIC) {
+      const int64_t rl = r < rend ? r : rlast;
+      load_generic<BITS>(base + rl * P, a.bpp, b.w);
+      b.n = __builtin_nontemporal_load(nbase + rl);
+    } else {
+      constexpr int PB = BITS * BPP;
+      const uint32_t rr = (uint32_t)(r - rbeg);
+      const int off = (int)(rr * (uint32_t)PB);
+      if constexpr (PB % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < PB / 16; ++i) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows_rs, off, 16 * i, 0);
+          b.w[4 * i + 0] = v.x; b.w[4 * i + 1] = v.y; b.w[4 * i + 2] = v.z; b.w[4 * i + 3] = v.w;
+        }
+      } else {
+        static_assert(PB % 8 == 0, "fast rows are a whole number of 8-byte units");
+#pragma unroll
+        for (int i = 0; i < PB / 8; ++i) {
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rows_rs, off, 8 * i, 0);
+          b.w[2 * i + 0] = v.x; b.w[2 * i + 1] = v.y;
+        }
+      }
+      b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
+    }
+  };
+  // One 64-row step of this wave: score row `row` from its plane words `rb.w`.
+  auto step = [&](const RowBuf& rb, const int64_t row) {
+    const uint32_t (&cur)[NW] = rb.w;
+    const float nrm = rb.n;
 
     float acc[QB];
 #pragma unroll
     for (int qi = 0; qi < QB; ++qi) acc[qi] = 0.f;
+    if constexpr (PAIRS) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        decode_pairs<QB == 4 ? 16 : 8>(cur[w], 8 * w, [&](int j, uint32_t addr) {
+          if constexpr (QB == 1) {
+            acc[0] += *reinterpret_cast<const float*>(lut_s + (j >> 1) * NLEV * 8 + (j & 1) * 4 + addr);
+          } else if constexpr (QB == 2) {
+            const float2 v = *reinterpret_cast<const float2*>(lut_s + j * NLEV * 8 + addr);
+            acc[0] += v.x;
+            acc[1] += v.y;
+          } else {
+            const float4 v = *reinterpret_cast<const float4*>(lut_s + j * NLEV * 16 + addr);
+            acc[0] += v.x;
+            acc[1] += v.y;
+            acc[2] += v.z;
+            acc[3] += v.w;
+          }
+        });
+        if constexpr (QB == 2) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+        if constexpr (QB == 4) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+      }
+    } else {
 #pragma unroll
     for (int w = 0; w < WPP; ++w) {
       uint32_t A[4];
@@ -327,12 +401,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         if constexpr (QB == 4) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
       });
     }
+    }
 
     if constexpr (TOPK) {
       const bool valid = row < rend;
 #pragma unroll
       for (int qi = 0; qi < QB; ++qi) {
-        if (qi >= nq) break;
+        if (QB > 1 && qi >= nq) break;  // a one-query block always has its query
         const float sc = acc[qi] * nrm * a.post_scale;
         const int id = (int)row;
         bool pred = valid && better(sc, id, th[qi], thi[qi]);
@@ -364,17 +439,27 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
       }
     }
   };
-  // The next row's loads are issued before the current row is scored.
+  // Pair-layout rows are loaded two steps ahead, others one, into rotating register
+  // buffers: a row loaded from HBM under full load takes longer than one step to
+  // arrive.  (A copy between buffers would wait for the loads in flight.)
+  // The next step's rows are loaded before the current step is scored, into the other
+  // of two register buffers (a copy between them would wait for the loads in flight;
+  // a third buffer measured slower).  The step count is made wave-uniform explicitly:
+  // a loop on the per-lane row index compiles to an exec-masked loop whose merged
+  // states make the load waits conservative.
   constexpr int64_t kStride = kWaves * 64;
-  uint32_t cur[NW];
-  int64_t step0 = rbeg + wave * 64;
-  if (step0 < rend) load_row(row, cur);
-  for (; step0 < rend; step0 += kStride) {
-    uint32_t nxt[NW];
-    load_row(row + kStride, nxt);
-    step(cur, row);
-#pragma unroll
-    for (int i = 0; i < NW; ++i) cur[i] = nxt[i];
+  const int64_t first = rbeg + wave * 64;
+  const int nsteps = __builtin_amdgcn_readfirstlane(
+      first < rend ? (int)((rend - first + kStride - 1) / kStride) : 0);
+  RowBuf ta, tb;
+  if (nsteps > 0) load_row(row, ta);
+  for (int it = 0; it < nsteps; it += 2) {
+    load_row(row + kStride, tb);
+    step(ta, row);
+    row += kStride;
+    if (it + 1 >= nsteps) break;
+    load_row(row + kStride, ta);
+    step(tb, row);
     row += kStride;
   }
 
@@ -449,15 +534,18 @@ __device__ __forceinline__ void wave_best(float& s, int& id) {
   id = __builtin_amdgcn_readlane(id, 63);
 }
 
-// Per query: the k-th best of the per-block maxima is a lower bound of the k-th best
-// score overall (those k maxima are k distinct rows), so only candidates at or above
-// it can be in the answer.  The survivors are rank-sorted.
+// Per query.  tau = the k-th best of 64 group maxima (group = the block lists of 4
+// adjacent threads) is a lower bound of the k-th best score overall: those k maxima are
+// k distinct rows.  Only list entries at or above tau can be in the answer; they are
+// rank-sorted.  Every step is a fixed number of passes (no per-k rounds of wave
+// reductions, whose DPP chains cost about a microsecond each).
 // Runs on all kThreads threads of a block (it synchronizes), for query q.
 __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __restrict__ part_i,
                             int nblocks, int k, int q, float* __restrict__ out_s,
                             int64_t* __restrict__ out_i) {
-  __shared__ float wbest_s[kWaves * kMaxK];
-  __shared__ int wbest_i[kWaves * kMaxK];
+  static_assert(kThreads == 256, "64 groups of 4 threads");
+  __shared__ __attribute__((aligned(16))) float gs[64];
+  __shared__ __attribute__((aligned(16))) int gi[64];
   __shared__ float ss[kMergeCap];
   __shared__ int si[kMergeCap];
   __shared__ int nsurv;
@@ -468,7 +556,7 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const float* ps = part_s + (size_t)q * nblocks * k;
   const int32_t* pi = part_i + (size_t)q * nblocks * k;
-  // 1. each wave: its k best block maxima (block b's list is sorted, entry 0 = its max)
+  // 1. block maxima (block b's list is sorted, entry 0 = its max), then each group's best
   float ms[kMaxBlocksPerLane];
   int mi[kMaxBlocksPerLane];
   // Every load is issued unconditionally (clamped index) so all of them are in flight
@@ -483,46 +571,32 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
     ms[r] = ok ? sc : -INFINITY;
     mi[r] = ok ? id : INT_MAX;
   }
-  for (int r = 0; r < k; ++r) {
-    float bs = -INFINITY;
-    int bi = INT_MAX;
+  float bs = -INFINITY;
+  int bi = INT_MAX;
 #pragma unroll
-    for (int t = 0; t < kMaxBlocksPerLane; ++t)
-      if (mi[t] != INT_MAX && (bi == INT_MAX || better(ms[t], mi[t], bs, bi))) { bs = ms[t]; bi = mi[t]; }
-    wave_best(bs, bi);
-#pragma unroll
-    for (int t = 0; t < kMaxBlocksPerLane; ++t)
-      if (mi[t] == bi) mi[t] = INT_MAX;  // ids are unique: consume the winner
-    if (lane == 0) { wbest_s[wave * kMaxK + r] = bs; wbest_i[wave * kMaxK + r] = bi; }
-  }
-  if (threadIdx.x == 0) { nsurv = 0; nlists = 0; }
+  for (int t = 0; t < kMaxBlocksPerLane; ++t)
+    if (mi[t] != INT_MAX && (bi == INT_MAX || better(ms[t], mi[t], bs, bi))) { bs = ms[t]; bi = mi[t]; }
+  best_step<0xB1, 0xF>(bs, bi);  // quad_perm [1,0,3,2]
+  best_step<0x4E, 0xF>(bs, bi);  // quad_perm [2,3,0,1]
+  if ((lane & 3) == 0) { gs[threadIdx.x >> 2] = bs; gi[threadIdx.x >> 2] = bi; }
+  if (threadIdx.x == 0) { nsurv = 0; nlists = 0; tau_s = -INFINITY; }
   __syncthreads();
-  // 2. wave 0: k-th best of the 4k wave winners -> tau
+  // 2. wave 0: rank of each group maximum among the 64 (a strict order: score, then id);
+  // the one ranked k-1 is tau.  With fewer than k non-empty groups tau stays -inf.
   if (wave == 0) {
-    float cs[kWaves];
-    int ci[kWaves];
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const bool ok = lane < k;
-      cs[w] = ok ? wbest_s[w * kMaxK + lane] : -INFINITY;
-      ci[w] = ok ? wbest_i[w * kMaxK + lane] : INT_MAX;
+    const float s0 = gs[lane];
+    const int i0 = gi[lane];
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < 64; j += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(gs + j);
+      const int4 i4 = *reinterpret_cast<const int4*>(gi + j);
+      rank += (i4.x != INT_MAX) & better(s4.x, i4.x, s0, i0);
+      rank += (i4.y != INT_MAX) & better(s4.y, i4.y, s0, i0);
+      rank += (i4.z != INT_MAX) & better(s4.z, i4.z, s0, i0);
+      rank += (i4.w != INT_MAX) & better(s4.w, i4.w, s0, i0);
     }
-    float last = -INFINITY;
-    int last_i = INT_MAX;
-    for (int r = 0; r < k; ++r) {
-      float bs = -INFINITY;
-      int bi = INT_MAX;
-#pragma unroll
-      for (int t = 0; t < kWaves; ++t)
-        if (ci[t] != INT_MAX && (bi == INT_MAX || better(cs[t], ci[t], bs, bi))) { bs = cs[t]; bi = ci[t]; }
-      wave_best(bs, bi);
-#pragma unroll
-      for (int t = 0; t < kWaves; ++t)
-        if (ci[t] == bi) ci[t] = INT_MAX;
-      last = bs;
-      last_i = bi;
-    }
-    if (lane == 0) tau_s = (last_i == INT_MAX) ? -INFINITY : last;
+    if (i0 != INT_MAX && rank == k - 1) tau_s = s0;
   }
   __syncthreads();
   const float tau = tau_s;
@@ -532,13 +606,14 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
 #pragma unroll
   for (int r = 0; r < kMaxBlocksPerLane; ++r) {
     const int b = threadIdx.x + r * kThreads;
-    if (b < nblocks && ms[r] >= tau) {
+    if (b < nblocks && mi[r] != INT_MAX && ms[r] >= tau) {
       const int pos = atomicAdd(&nlists, 1);
       if (pos < kMergeCap) lists[pos] = b;
     }
   }
   __syncthreads();
-  const int nl = min(nlists, kMergeCap);
+  const int nl_all = nlists;
+  const int nl = min(nl_all, kMergeCap);
   for (int e = threadIdx.x; e < nl * k; e += kThreads) {
     const int li = e / k;
     const size_t at = (size_t)lists[li] * k + (e - li * k);
@@ -553,7 +628,8 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
   const int m = nsurv;
   float* os = out_s + (size_t)q * k;
   int64_t* oi = out_i + (size_t)q * k;
-  if (m <= kMergeCap) {
+  // More than kMergeCap lists (or survivors) means many rows tie at tau: exact fallback.
+  if (m <= kMergeCap && nl_all <= kMergeCap) {
     for (int e = threadIdx.x; e < m; e += kThreads) {
       const float se = ss[e];
       const int ie = si[e];
@@ -797,10 +873,10 @@ int scan_blocks(int64_t nrows) {
   return (int)(b < 1 ? 1 : b);
 }
 
-template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC>
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS = false>
 int launch_scan_t(const ScanArgs& a, dim3 grid, hipStream_t st) {
   static_assert(QB * 8 * (GENERIC ? 32 : BPP) * (1 << BITS) * 4 <= 48 * 1024, "table too large");
-  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC>), grid, dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC, PAIRS>), grid, dim3(kThreads), 0, st, a);
   TQ_LAUNCH_CHECK("scan_kernel");
   return TQ_OK;
 }
@@ -829,13 +905,34 @@ int launch_scan_bits(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
                  : launch_scan_t<BITS, 32, 1, TOPK, true>(a, grid, st);
 }
 
-int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st) {
+// Pair-layout rows: 4-bit codes, 64 or 128 dims, 16-byte aligned base (checked by callers).
+template <bool TOPK>
+int launch_scan_pairs(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
+  if (a.bpp == 16) {
+    return qb == 4 ? launch_scan_t<4, 16, 4, TOPK, false, true>(a, grid, st)
+                   : launch_scan_t<4, 16, 1, TOPK, false, true>(a, grid, st);
+  }
+  return qb == 4 ? launch_scan_t<4, 8, 4, TOPK, false, true>(a, grid, st)
+                 : launch_scan_t<4, 8, 1, TOPK, false, true>(a, grid, st);
+}
+
+int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st,
+                bool pairs = false) {
   const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
   int qb = queries_per_block(a);
   if (!aligned && qb > 2) qb = 2;
   const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
   dim3 grid(topk ? (unsigned)scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
             (unsigned)((a.qps + qb - 1) / qb), (unsigned)nstreams);
+  // The fast loaders address a block's rows with 32-bit buffer offsets.
+  const int64_t per_block = ((rows_hint + grid.x - 1) / grid.x + 63) / 64 * 64;
+  if (per_block * (int64_t)(bits * a.bpp) >= ((int64_t)1 << 32))
+    return fail(TQ_EINVAL, "too many rows per scan block");
+  if (pairs) {
+    if (bits != 4 || !aligned || (a.bpp != 8 && a.bpp != 16))
+      return fail(TQ_EINVAL, "pair-layout scan needs 4-bit codes, dim 64 or 128 and a 16-byte aligned base");
+    return topk ? launch_scan_pairs<true>(a, qb, grid, st) : launch_scan_pairs<false>(a, qb, grid, st);
+  }
   switch (bits) {
     case 1: return topk ? launch_scan_bits<1, true>(a, qb, grid, st) : launch_scan_bits<1, false>(a, qb, grid, st);
     case 2: return topk ? launch_scan_bits<2, true>(a, qb, grid, st) : launch_scan_bits<2, false>(a, qb, grid, st);
@@ -862,10 +959,15 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
   return bytes;
 }
 
-int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
-                    const uint8_t* packed, const float* norms, int64_t N, const float* centroids,
-                    const float* rotation, int32_t bit_width, int32_t k, float* out_scores,
-                    int64_t* out_ids, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                 const uint8_t* packed, const float* norms, int64_t N, const float* centroids,
+                 const float* rotation, int32_t bit_width, int32_t k, float* out_scores,
+                 int64_t* out_ids, void* workspace, size_t workspace_bytes, void* stream,
+                 bool pairs) {
   TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
   TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
   TQ_REQUIRE(k >= 1 && k <= kMaxK, "k must be in [1, %d], got %d", kMaxK, k);
@@ -890,7 +992,7 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
   a.part_s = ps; a.part_i = pi; a.scores = nullptr;
   a.out_s = out_scores; a.out_i = out_ids;
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  const int rc = launch_scan(a, bit_width, true, 1, st);
+  const int rc = launch_scan(a, bit_width, true, 1, st, pairs);
   if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
                      out_scores, out_ids);
@@ -898,11 +1000,11 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
   return TQ_OK;
 }
 
-int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
-                               const uint8_t* packed_keys, const float* key_norms, int64_t T,
-                               const float* centroids, const float* rotation, int32_t bit_width,
-                               float* scores, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+int attention_scores(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                     const uint8_t* packed_keys, const float* key_norms, int64_t T,
+                     const float* centroids, const float* rotation, int32_t bit_width,
+                     float* scores, void* workspace, size_t workspace_bytes, void* stream,
+                     bool pairs) {
   TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
   TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
   TQ_REQUIRE(nq >= 0 && T >= 0, "bad sizes");
@@ -919,7 +1021,51 @@ int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, 
   a.cen = centroids; a.qps = (int)nq; a.post_scale = 1.f;
   a.k = 0; a.scores = scores;
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  return launch_scan(a, bit_width, false, 1, st);
+  return launch_scan(a, bit_width, false, 1, st, pairs);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                    const uint8_t* packed, const float* norms, int64_t N, const float* centroids,
+                    const float* rotation, int32_t bit_width, int32_t k, float* out_scores,
+                    int64_t* out_ids, void* workspace, size_t workspace_bytes, void* stream) {
+  return ip_scan_topk(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, bit_width,
+                      k, out_scores, out_ids, workspace, workspace_bytes, stream, false);
+}
+
+int tq_ip_scan_topk_pairs(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                          const uint8_t* pairs, const float* norms, int64_t N,
+                          const float* centroids, const float* rotation, int32_t k,
+                          float* out_scores, int64_t* out_ids, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(d == 64 || d == 128, "pair-layout scan needs dim 64 or 128, got %d", d);
+  TQ_REQUIRE(N == 0 || (reinterpret_cast<uintptr_t>(pairs) & 15u) == 0,
+             "pair-layout rows must be 16-byte aligned");
+  return ip_scan_topk(queries, q_dtype, nq, d, pairs, norms, N, centroids, rotation, 4, k,
+                      out_scores, out_ids, workspace, workspace_bytes, stream, true);
+}
+
+int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                               const uint8_t* packed_keys, const float* key_norms, int64_t T,
+                               const float* centroids, const float* rotation, int32_t bit_width,
+                               float* scores, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return attention_scores(query, q_dtype, nq, d, packed_keys, key_norms, T, centroids, rotation,
+                          bit_width, scores, workspace, workspace_bytes, stream, false);
+}
+
+int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                              const uint8_t* pairs, const float* key_norms, int64_t T,
+                              const float* centroids, const float* rotation, float* scores,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(d == 64 || d == 128, "pair-layout scan needs dim 64 or 128, got %d", d);
+  TQ_REQUIRE(T == 0 || (reinterpret_cast<uintptr_t>(pairs) & 15u) == 0,
+             "pair-layout rows must be 16-byte aligned");
+  return attention_scores(query, q_dtype, nq, d, pairs, key_norms, T, centroids, rotation, 4,
+                          scores, workspace, workspace_bytes, stream, true);
 }
 
 size_t tq_values_workspace_bytes(int64_t nq, int32_t d, int64_t T) {

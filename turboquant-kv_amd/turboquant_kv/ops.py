@@ -53,6 +53,19 @@ def ip_scan_topk(queries, packed, norms, centroids, rotation, bit_width, k):
     return _ops().ip_scan_topk(queries, packed, norms, centroids, rotation, bit_width, k)
 
 
+def ip_scan_topk_pairs(queries, pairs, norms, centroids, rotation, k):
+    """ip_scan_topk over 4-bit pair-layout rows [N, d/2] (byte p = code[2p] << 4 |
+    code[2p+1]; d = 64 or 128): the same scores and ids."""
+    _require_device(queries, "queries")
+    return _ops().ip_scan_topk_pairs(queries, pairs, norms, centroids, rotation, k)
+
+
+def attention_scores_pairs(query, pairs, key_norms, centroids, rotation):
+    """attention_scores_packed over 4-bit pair-layout rows [T, d/2] (d = 64 or 128)."""
+    _require_device(query, "query")
+    return _ops().attention_scores_pairs(query, pairs, key_norms, centroids, rotation)
+
+
 def decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcentroids,
                             vcentroids, krotation, vrotation, kbits, vbits, scale):
     """Fused GQA decode attention over packed K/V -> [B, Hq, d] in q.dtype."""

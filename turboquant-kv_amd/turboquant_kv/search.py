@@ -11,7 +11,13 @@ Queries are upcast to fp32 before rotation, as the reference's op and C++ paths 
 dtype (search.py:209-221).  Prod mode scores against dequantized vectors, as the
 reference does (search.py:229-252).
 
-save/load use the reference's Python file format (search.py:29-34, 254-317).
+4-bit MSE databases of dim 64 or 128 are kept in the pair layout (row byte p =
+code[2p] << 4 | code[2p+1]): the same bytes per row as the bit-plane format, arranged so
+that every code is one masked nibble, which the scan turns into a table address with a
+single instruction.  Scores and ids are identical to the bit-plane scan.
+
+save/load use the reference's Python file format (search.py:29-34, 254-317); the pair
+layout is converted back to bit planes on save and from them on load.
 """
 
 from __future__ import annotations
@@ -55,6 +61,8 @@ class TurboQuantIndex:
             self._code_bits = bit_width - 1
             self._S_matrix = make_qjl_matrix(dim, dim, seed)
             self._S_dev = self._S_matrix.to(self.device)
+        # 4-bit MSE rows of 64/128 dims live in the pair layout (same row width).
+        self._pairs = mode == "mse" and bit_width == 4 and dim in (64, 128)
         self._bnd = self._codebook[0].to(self.device)
         self._cen = self._codebook[1].to(self.device)
         self.n_vectors = 0
@@ -68,6 +76,21 @@ class TurboQuantIndex:
     @property
     def _packed_codes(self) -> Optional[torch.Tensor]:
         return None if self._packed_buf is None else self._packed_buf[: self.n_vectors]
+
+    def _bitplane_codes(self) -> Optional[torch.Tensor]:
+        """The database rows in the reference's bit-plane format [n, b*ceil(d/8)]."""
+        if self._packed_buf is None or not self._pairs:
+            return self._packed_codes
+        return ops.unpack_decode_layout(self._packed_buf.unsqueeze(0), self.dim, 4, False, 0,
+                                        self.n_vectors)[0]
+
+    def _store_codes(self, packed: torch.Tensor, pos: int) -> None:
+        """Write bit-plane rows at rows pos.. of the database buffer."""
+        if self._pairs:
+            ops.pack_decode_layout(packed.unsqueeze(0), self._packed_buf.unsqueeze(0), self.dim,
+                                   4, False, pos)
+        else:
+            self._packed_buf[pos: pos + packed.shape[0]] = packed
 
     @property
     def _norms(self) -> Optional[torch.Tensor]:
@@ -127,7 +150,7 @@ class TurboQuantIndex:
         sl = slice(self.n_vectors, self.n_vectors + n)
         if self.mode == "mse":
             p, nm = _ops().quantize_mse_packed(x, self._rot_dev, self._bnd, self.bit_width)
-            self._packed_buf[sl] = p
+            self._store_codes(p, self.n_vectors)
             self._norm_buf[sl] = nm.float()
         else:
             mp, sg, rn, nm = _ops().quantize_prod_packed(x, self._rot_dev, self._bnd, self._cen,
@@ -147,11 +170,18 @@ class TurboQuantIndex:
         k = min(k, self.n_vectors)
         if self.mode == "mse":
             if k <= _SCAN_MAX_K:
+                if self._pairs:
+                    return ops.ip_scan_topk_pairs(q, self._packed_codes, self._norms, self._cen,
+                                                  self._rot_dev, k)
                 return ops.ip_scan_topk(q, self._packed_codes, self._norms, self._cen,
                                         self._rot_dev, self.bit_width, k)
-            s = ops.attention_scores_packed(q.float().unsqueeze(0), self._packed_codes,
-                                            self._norms, self._cen, self._rot_dev,
-                                            self.bit_width)[0]
+            if self._pairs:
+                s = ops.attention_scores_pairs(q.float().unsqueeze(0), self._packed_codes,
+                                               self._norms, self._cen, self._rot_dev)[0]
+            else:
+                s = ops.attention_scores_packed(q.float().unsqueeze(0), self._packed_codes,
+                                                self._norms, self._cen, self._rot_dev,
+                                                self.bit_width)[0]
             top = torch.topk(s, k, dim=-1)
             return top.values, top.indices
         recon = _ops().dequantize_prod_packed(self._packed_codes, self._qjl_signs,
@@ -170,7 +200,7 @@ class TurboQuantIndex:
             f.write(struct.pack(HEADER_FORMAT, self.bit_width, self.dim, self.n_vectors))
             f.write(struct.pack("<B", mode_byte))
             if self.n_vectors:
-                f.write(self._packed_codes.cpu().numpy().tobytes())
+                f.write(self._bitplane_codes().cpu().numpy().tobytes())
                 f.write(self._norms.cpu().numpy().astype(np.float32).tobytes())
                 if self.mode == "prod":
                     f.write(self._qjl_signs.cpu().numpy().tobytes())
@@ -206,7 +236,7 @@ class TurboQuantIndex:
                   device=device)
         if n:
             idx._reserve(n)
-            idx._packed_buf[:n] = torch.from_numpy(packed.copy()).to(idx.device)
+            idx._store_codes(torch.from_numpy(packed.copy()).to(idx.device), 0)
             idx._norm_buf[:n] = torch.from_numpy(norms.copy()).to(idx.device)
             if mode == "prod":
                 idx._sign_buf[:n] = torch.from_numpy(signs.copy()).to(idx.device)
