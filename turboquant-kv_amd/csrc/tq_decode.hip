@@ -401,6 +401,12 @@ constexpr int kDlThreads = 512;
 constexpr int kDlWaves = kDlThreads / 64;
 constexpr int kDlEntry = 256;                  // bytes per table index (all copies)
 constexpr int kDlTab = 256 * kDlEntry;         // 64 KB per table
+// K table: hi parts of entry i at kDlTab + i * 256 + 128 (upper half of the slot), lo
+// parts kDlKLo bytes further (lower half of slot i + 5).  The distance is neither a
+// ds_read2 offset (<= 1020) nor a multiple of 256 (ds_read2st64), so the two reads of an
+// entry stay separate ds_read_b32 and each MFMA operand pair is loaded in place.
+constexpr int kDlKLo = 1152;
+constexpr int kDlTabs = 2 * kDlTab + 5 * kDlEntry;
 constexpr int kDlMinSplit = kDlWaves * 64;     // one tile per wave
 
 struct DlArgs {
@@ -449,18 +455,20 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // about 1e-6 relative), for fp32 outputs; otherwise one fp16 product (about 5e-4).
 template <bool EXACT_V>
 __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
-  // K table: index = pair byte; 32 copies of (c[high nibble], c[low nibble]) fp32.
-  // V table: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
-  // copies of 4 hi + 4 lo halves.  After the tile loop the bytes hold the reduction.
-  __shared__ __attribute__((aligned(16))) char tabs[2 * kDlTab];
-  __shared__ __attribute__((aligned(16))) float qr_s[4][kDim];
+  // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
+  // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
+  // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
+  // at kDlKLo).  After the tile loop the bytes hold the reduction.
+  __shared__ __attribute__((aligned(16))) char tabs[kDlTabs];
+  __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4][2][kDim];  // q * qs2: hi, lo
   __shared__ float qs_s[4][kDim];
   __shared__ float cen_s[20];
-  __shared__ float sc_s[1];  // value centroid scale
+  __shared__ float sc_s[2];  // value and key centroid scales
+  __shared__ float qs2_s[4];  // per-head query scales
   __shared__ float red_m[kDlWaves][4];
   __shared__ float red_l[kDlWaves][4];
-  char* const ktab = tabs;
-  char* const vtab = tabs + kDlTab;
+  char* const ktab = tabs + kDlTab;
+  char* const vtab = tabs;
 
   const int split = blockIdx.x;
   const int bg = blockIdx.y;
@@ -487,7 +495,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
     qs_s[h][k] = h < a.G ? load_as_f32(a.q, (qh0 + h) * kDim + k, a.q_dt) : 0.f;
   }
   __syncthreads();
-  if (tid < 4 * kDim) {
+  if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane
     const int h = tid >> 6, j = tid & 63;
     const float4* r4 = reinterpret_cast<const float4*>(a.krot + j * kDim);
     float v = 0.f;
@@ -499,17 +507,37 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
       v = fmaf(r.z, qs_s[h][4 * k + 2], v);
       v = fmaf(r.w, qs_s[h][4 * k + 3], v);
     }
-    qr_s[h][j] = v * a.qscale;
+    v *= a.qscale;
+    // fp16 hi + lo parts of the rotated query, scaled by a power of two that brings the
+    // head's largest element into [0.5, 1) (lo parts stay normal numbers)
+    const float s2 = pow2_scale(wave_max(fabsf(v)));
+    const float x = v * s2;
+    const _Float16 xh = (_Float16)x;
+    qhl_s[h][0][j] = xh;
+    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
+    if (j == 0) qs2_s[h] = s2;
   } else if (tid < 4 * kDim + 64) {  // wave 4: value centroid scale
     const int l = tid & 63;
     const float vm = wave_max(l < 4 ? fabsf(cen_s[16 + l]) : 0.f);
     if (l == 0) sc_s[0] = pow2_scale(vm);
+  } else if (tid < 4 * kDim + 128) {  // wave 5: key centroid scale
+    const int l = tid & 63;
+    const float km = wave_max(l < 16 ? fabsf(cen_s[l]) : 0.f);
+    if (l == 0) sc_s[1] = pow2_scale(km);
   }
   __syncthreads();
   const float vsc = sc_s[0];
+  const float ksc = sc_s[1];
   for (int e = tid; e < 256 * 32; e += kDlThreads) {
     const int i = e >> 5, c = e & 31;
-    *reinterpret_cast<float2*>(ktab + i * kDlEntry + c * 8) = make_float2(cen_s[i >> 4], cen_s[i & 15]);
+    {
+      const float x0 = cen_s[i >> 4] * ksc, x1 = cen_s[i & 15] * ksc;
+      const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+      typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<h2_t*>(ktab + i * kDlEntry + 128 + c * 4) = (h2_t){h0, h1};
+      *reinterpret_cast<h2_t*>(ktab + i * kDlEntry + 128 + kDlKLo + c * 4) =
+          (h2_t){(_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1)};
+    }
     if constexpr (!EXACT_V) {
       v4h vv;
 #pragma unroll
@@ -531,16 +559,18 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
 
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 2, hn = lane & 3;
-  float qv[kDim];  // (R_k q) * scale * log2(e) of head hn
+  // (R_k q) * scale * log2(e) * qs2 of head hn, four dims per operand: hi and lo halves
+  v4h qh4[kDim / 4], ql4[kDim / 4];
 #pragma unroll
-  for (int j = 0; j < kDim; j += 4) {
-    const float4 t4 = *reinterpret_cast<const float4*>(&qr_s[hn][j]);
-    qv[j] = t4.x; qv[j + 1] = t4.y; qv[j + 2] = t4.z; qv[j + 3] = t4.w;
+  for (int g = 0; g < kDim / 4; ++g) {
+    qh4[g] = *reinterpret_cast<const v4h*>(&qhl_s[hn][0][4 * g]);
+    ql4[g] = *reinterpret_cast<const v4h*>(&qhl_s[hn][1][4 * g]);
   }
-  // byte 0: copy offset; byte 2 of vcopy: the V table's 64 KB base
-  const uint32_t kcopy = (uint32_t)(lane & 31) * 8;
+  const float kinv = 1.f / (ksc * qs2_s[hn]);  // a power of two: exact
+  // byte 0: copy offset; byte 2 of kcopy: the K table's 64 KB base
+  const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
   const uint32_t vcopy =
-      (uint32_t)kDlTab | (EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8);
+      EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
 
   const size_t sbase = (size_t)bg * (size_t)a.t_cap;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
@@ -585,17 +615,27 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
 
   // One 64-token tile of this wave: x holds its data, loaded one tile ahead.
   auto process = [&](const Tile& cur, int t0) {
-    // ---- q.K: A = c[code] of this lane's token (fp32), B = query of head hn
-    v4f sk[8];  // eight chains: no MFMA waits on the one issued just before it
+    // ---- q.K: A = c[code] of this lane's token, B = query of head hn, four dims per
+    // MFMA, fp16 hi/lo parts: c.q = ch.qh + ch.ql + cl.qh (the cl.ql term is 2^-22
+    // relative), accumulated in fp32
+    v4f sk[6];  // six chains: no MFMA waits on the one issued just before it
 #pragma unroll
-    for (int x = 0; x < 8; ++x) sk[x] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int x = 0; x < 6; ++x) sk[x] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int p = 0; p < 32; ++p) {
-      const float2 cc = *reinterpret_cast<const float2*>(tabs + byte_addr(kcopy, cur.k[p >> 2], p & 3));
-      sk[p & 3] = __builtin_amdgcn_mfma_f32_4x4x1f32(cc.x, qv[2 * p], sk[p & 3], 0, 0, 0);
-      sk[4 + (p & 3)] = __builtin_amdgcn_mfma_f32_4x4x1f32(cc.y, qv[2 * p + 1], sk[4 + (p & 3)], 0, 0, 0);
+    for (int g = 0; g < kDim / 4; ++g) {  // dims 4g .. 4g+3 = pair bytes 2g, 2g+1
+      const uint32_t w = cur.k[g >> 1];
+      const uint32_t a0 = byte_addr(kcopy, w, 2 * (g & 1));
+      const uint32_t a1 = byte_addr(kcopy, w, 2 * (g & 1) + 1);
+      const v4h ah = as_v4h(*reinterpret_cast<const uint32_t*>(tabs + a0),
+                            *reinterpret_cast<const uint32_t*>(tabs + a1));
+      const v4h al = as_v4h(*reinterpret_cast<const uint32_t*>(tabs + a0 + kDlKLo),
+                            *reinterpret_cast<const uint32_t*>(tabs + a1 + kDlKLo));
+      const int c = 3 * (g & 1);
+      sk[c] = __builtin_amdgcn_mfma_f32_4x4x4f16(ah, qh4[g], sk[c], 0, 0, 0);
+      sk[c + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ah, ql4[g], sk[c + 1], 0, 0, 0);
+      sk[c + 2] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, qh4[g], sk[c + 2], 0, 0, 0);
     }
-    const v4f skk = ((sk[0] + sk[1]) + (sk[2] + sk[3])) + ((sk[4] + sk[5]) + (sk[6] + sk[7]));
+    const v4f skk = ((sk[0] + sk[3]) + (sk[1] + sk[4]) + (sk[2] + sk[5])) * kinv;
 
     // ---- online softmax (register r = token t0 + 4 * quad + r, head hn)
     // Tokens at or past te are masked with selects at their use (branch-free: a masked
