@@ -114,17 +114,19 @@ def bench_scan(args, extra):
     ops.pack_decode_layout(packed.unsqueeze(0), pairs, d, 4, 0, 0)
     pairs = pairs[0]
     q1 = queries(1, d)
-    fn = lambda: ops.ip_scan_topk_pairs(q1, pairs, norms, cen, R, k)
-    ms = time_op(fn, args.steps, args.warmup)
     bytes_alg = N * (4 * 16 + 4) + 1 * d * 2 + k * 12
-    res["headline"] = (ms, bytes_alg)
-    log(f"scan b=4 Q=1 (pair layout): {ms * 1e3:.1f} us/query, {bytes_alg / ms / 1e6:.0f} GB/s")
-    t = time_op(lambda: ops.ip_scan_topk(q1, packed, norms, cen, R, 4, k), 20, 3)
+    # The bit-plane comparison runs first: the GPU's clocks take a few milliseconds of
+    # sustained load to settle, and the headline is timed after that.
+    t = time_op(lambda: ops.ip_scan_topk(q1, packed, norms, cen, R, 4, k), 40, 3)
     extra["scan_b4_Q1_bitplane"] = {"us_per_query": t * 1e3, "queries_per_s": 1e3 / t,
                                     "GBps": bytes_alg / t / 1e6,
                                     "hbm_frac": bytes_alg / t / 1e6 / HBM_PEAK_GBS,
                                     "note": "same scan over the reference's bit-plane rows"}
     log(f"scan b=4 Q=1 (bit-plane rows): {t * 1e3:.1f} us/query, {bytes_alg / t / 1e6:.0f} GB/s")
+    fn = lambda: ops.ip_scan_topk_pairs(q1, pairs, norms, cen, R, k)
+    ms = time_op(fn, args.steps, args.warmup)
+    res["headline"] = (ms, bytes_alg)
+    log(f"scan b=4 Q=1 (pair layout): {ms * 1e3:.1f} us/query, {bytes_alg / ms / 1e6:.0f} GB/s")
     if not args.quick:
         for Q, steps in ((64, 3), (1024, 1)):
             qq = queries(Q, d, seed=2)
@@ -173,12 +175,12 @@ def bench_decode(args, extra):
             del K, V
             # the decode layout QuantizedKVCache keeps (same bytes per token)
             kdl = torch.zeros(B * Hkv, T, d // 2, dtype=torch.uint8, device="cuda")
-            vdl = torch.zeros(B * Hkv, T // 4, d, dtype=torch.uint8, device="cuda")
+            vdl = torch.zeros(B * Hkv, T // 16, 4 * d, dtype=torch.uint8, device="cuda")
             ops.pack_decode_layout(kp.view(B * Hkv, T, -1), kdl, d, kb, 0, 0)
             ops.pack_decode_layout(vp.view(B * Hkv, T, -1), vdl, d, vb, 1, 0)
             caches.append((kp.view(B, Hkv, T, -1), kn.float().view(B, Hkv, T),
                            vp.view(B, Hkv, T, -1), vn.float().view(B, Hkv, T),
-                           kdl.view(B, Hkv, T, -1), vdl.view(B, Hkv, T // 4, -1)))
+                           kdl.view(B, Hkv, T, -1), vdl.view(B, Hkv, T // 16, -1)))
             del kp, vp
         q = torch.randn(B, Hq, d, generator=g, device="cuda").to(torch.bfloat16)
         sl = torch.full((B,), T, dtype=torch.int32, device="cuda")

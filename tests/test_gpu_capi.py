@@ -175,7 +175,7 @@ def k_pack_dl(packed, t_cap, pos, values, cache=None):
     S, n, _ = packed.shape
     d = 64
     if cache is None:
-        shape = (S, t_cap // 4, d) if values else (S, t_cap, d // 2)
+        shape = (S, t_cap // 16, 4 * d) if values else (S, t_cap, d // 2)
         cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
     capi.check(L().tq_pack_decode_layout(capi.p(T(packed)), capi.i64(S), capi.i64(n), capi.i32(d),
                                          capi.i32(2 if values else 4), capi.i32(values), capi.p(cache),
@@ -547,19 +547,22 @@ def test_decode_layout_pack_roundtrip():
     # the layout bytes are checked against an independent numpy packing of the codes and
     # the unpacked rows must equal the bit-plane input.
     rs = np.random.RandomState(21)
-    S, t_cap, d = 3, 40, 64
+    S, t_cap, d = 3, 48, 64
     kcodes = rs.randint(0, 16, (S, t_cap, d))
     vcodes = rs.randint(0, 4, (S, t_cap, d))
     kp = np.stack([O.pack_codes(kcodes[s], 4) for s in range(S)])
     vp = np.stack([O.pack_codes(vcodes[s], 2) for s in range(S)])
     kc = vc = None
-    for pos, n in ((0, 5), (5, 1), (6, 7), (13, 3), (16, 24)):
+    for pos, n in ((0, 5), (5, 1), (6, 7), (13, 3), (16, 21), (37, 11)):
         kc = k_pack_dl(np.ascontiguousarray(kp[:, pos:pos + n]), t_cap, pos, 0, kc)
         vc = k_pack_dl(np.ascontiguousarray(vp[:, pos:pos + n]), t_cap, pos, 1, vc)
     want_k = (kcodes[:, :, 0::2] << 4) | kcodes[:, :, 1::2]
     assert np.array_equal(kc.cpu().numpy(), want_k.astype(np.uint8))
-    vb = vcodes.reshape(S, t_cap // 4, 4, d)
-    want_v = vb[:, :, 0] | (vb[:, :, 1] << 2) | (vb[:, :, 2] << 4) | (vb[:, :, 3] << 6)
+    # values: chunks of 16 tokens; byte c*16 + tg*4 + dg holds dim 16*dg + c of tokens
+    # 16*chunk + 4*tg + t at bits 2t
+    vb = vcodes.reshape(S, t_cap // 16, 4, 4, 4, 16)  # [S, chunk, tg, t, dg, c]
+    packed_v = vb[:, :, :, 0] | (vb[:, :, :, 1] << 2) | (vb[:, :, :, 2] << 4) | (vb[:, :, :, 3] << 6)
+    want_v = packed_v.transpose(0, 1, 4, 2, 3).reshape(S, t_cap // 16, 256)  # [S, chunk, c, tg, dg]
     assert np.array_equal(vc.cpu().numpy(), want_v.astype(np.uint8))
     assert np.array_equal(k_unpack_dl(kc, t_cap, 0, t_cap, 0), kp)
     assert np.array_equal(k_unpack_dl(vc, t_cap, 7, 30, 1), vp[:, 7:37])
@@ -570,7 +573,7 @@ def test_decode_layout_attention_vs_f64(G):
     # Same cases as the bit-plane kernel, through the decode layout; fp32 queries take
     # the exact value product.
     rs = np.random.RandomState(300 + G)
-    d, Hkv, Tc = 64, 2, 5004
+    d, Hkv, Tc = 64, 2, 5008
     seq = [0, 1, 3, 63, 64, 65, 257, 513, 5004]
     B, Hq = len(seq), Hkv * G
     Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)

@@ -397,7 +397,7 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
 //   keys    per token d/2 bytes; byte p = (code[2p] << 4) | code[2p+1]
 //   values  per block of 4 consecutive tokens d bytes; byte j = sum_t code[t][j] << 2t
 // Every byte is then one table index: a single v_perm builds its LDS address.
-constexpr int kDlThreads = 512;
+constexpr int kDlThreads = 512;  // 8 waves (12 measured slower)
 constexpr int kDlWaves = kDlThreads / 64;
 constexpr int kDlEntry = 256;                  // bytes per table index (all copies)
 constexpr int kDlTab = 256 * kDlEntry;         // 64 KB per table
@@ -444,6 +444,16 @@ __device__ __forceinline__ v4h as_v4h(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(v4h, t);
 }
 
+// DPP row_shl:N on both words of a v4h: lane i of each 16-lane row takes lane i + N's
+// value (zero where i + N leaves the row).
+template <int N>
+__device__ __forceinline__ v4h row_shl_h(v4h x) {
+  const u32x2 w = __builtin_bit_cast(u32x2, x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w.x, 0x100 + N, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w.y, 0x100 + N, 0xF, 0xF, true);
+  return as_v4h(lo, hi);
+}
+
 // Scale that brings max |x| into [0.5, 1): 2^-e with x = m * 2^e.
 __device__ __forceinline__ float pow2_scale(float amax) {
   int e = 0;
@@ -454,7 +464,7 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // EXACT_V: the weights and V centroids enter as fp16 hi + lo parts (three products,
 // about 1e-6 relative), for fp32 outputs; otherwise one fp16 product (about 5e-4).
 template <bool EXACT_V>
-__global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
+__global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
   // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
   // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
@@ -575,7 +585,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
   const size_t sbase = (size_t)bg * (size_t)a.t_cap;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 3) >> 2) * 64);
+      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 15) >> 4) * 256);
   // Norms are read four tokens at a time: the range covers whole quads (inside the
   // allocation, t_cap % 4 == 0); entries past t_end are masked.
   const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
@@ -585,7 +595,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
 
   struct Tile {
     uint32_t k[8];   // this lane's token: 32 pair bytes
-    uint32_t v[4];   // this quad's block: value bytes of dims 16*hn .. 16*hn+15
+    uint32_t v[4];   // value chunk lane/16, column lane%16: word tg = 4 dim-group bytes
     float kn[4], vn[4];
   };
   auto load_tile = [&](int t0, Tile& x) {
@@ -594,7 +604,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
     const u32x4 k1 = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 16, 0);
     x.k[0] = k0.x; x.k[1] = k0.y; x.k[2] = k0.z; x.k[3] = k0.w;
     x.k[4] = k1.x; x.k[5] = k1.y; x.k[6] = k1.z; x.k[7] = k1.w;
-    const uint32_t vo = (uint32_t)((t0 >> 2) + quad) * 64 + 16 * hn;
+    const uint32_t vo = (uint32_t)((t0 >> 4) + (lane >> 4)) * 256 + (uint32_t)(lane & 15) * 16;
     const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
     x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
     // norms of the quad's four tokens: 16-byte aligned (t_cap % 4 == 0, aligned base)
@@ -609,9 +619,9 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
   };
 
   float M = -INFINITY, l = 0.f;
-  v4f acc[16];
+  v4f acc[4];  // dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 16 dg + lane
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   // One 64-token tile of this wave: x holds its data, loaded one tile ahead.
   auto process = [&](const Tile& cur, int t0) {
@@ -657,7 +667,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
       l *= f;
       const v4f fv = {__shfl(f, 0), __shfl(f, 1), __shfl(f, 2), __shfl(f, 3)};
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] *= fv;
+      for (int i = 0; i < 4; ++i) acc[i] *= fv;
       M = mn;
     }
     v4h wh, wl;
@@ -689,32 +699,47 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- p.V: acc[i] (lane (quad, hn), register m) = head m, dim 16*hn + i
+    // ---- p.V: one 16x16x16 MFMA per (token group tg, dim group dg): A rows = heads
+    // (rows 4-15 unused), k = tokens 16q + 4tg + t of lane group q = lane / 16, B cols =
+    // dims 16 dg + lane % 16.  A_tg is the weights of lane 16q + 4tg + h moved to lane
+    // 16q + h: a row shift left by 4tg.
+    v4h aw[4], awl[4];
+    aw[0] = wh;
+    aw[1] = row_shl_h<4>(wh);
+    aw[2] = row_shl_h<8>(wh);
+    aw[3] = row_shl_h<12>(wh);
+    if constexpr (EXACT_V) {
+      awl[0] = wl;
+      awl[1] = row_shl_h<4>(wl);
+      awl[2] = row_shl_h<8>(wl);
+      awl[3] = row_shl_h<12>(wl);
+    }
     if constexpr (!EXACT_V) {
       v4h bv[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
+      for (int i = 0; i < 16; ++i)  // i = 4 tg + dg
         bv[i] = *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[i >> 2], i & 3));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bv[i], acc[i], 0, 0, 0);
+      for (int i = 0; i < 16; ++i)
+        acc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[i >> 2], bv[i], acc[i & 3], 0, 0, 0);
     } else {
 #pragma unroll
-      for (int i0 = 0; i0 < 16; i0 += 4) {
+      for (int tg = 0; tg < 4; ++tg) {
         v4h bh[4], bl[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const u32x4 e = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[(i0 + u) >> 2], (i0 + u) & 3));
-          bh[u] = as_v4h(e.x, e.y);
-          bl[u] = as_v4h(e.z, e.w);
+        for (int dg = 0; dg < 4; ++dg) {
+          const u32x4 e = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[tg], dg));
+          bh[dg] = as_v4h(e.x, e.y);
+          bl[dg] = as_v4h(e.z, e.w);
         }
-        if (i0 == 0) __builtin_amdgcn_sched_barrier(0);
+        if (tg == 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bh[u], acc[i0 + u], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[tg], bh[dg], acc[dg], 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wl, bh[u], acc[i0 + u], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(awl[tg], bh[dg], acc[dg], 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[i0 + u] = __builtin_amdgcn_mfma_f32_4x4x4f16(wh, bl[u], acc[i0 + u], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[tg], bl[dg], acc[dg], 0, 0, 0);
       }
     }
 
@@ -735,7 +760,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
     t0 += kStep;
   }
 
-  // ---- reduction: lanes of a head; quads of a row (DPP); rows and waves (LDS)
+  // ---- reduction: l over the lanes of a head; outputs over the waves (LDS)
   l += __shfl_xor(l, 4);
   l += __shfl_xor(l, 8);
   l += __shfl_xor(l, 16);
@@ -755,28 +780,18 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
     const float mw = red_m[wave][m];
     fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]);
   }
-  float* red = reinterpret_cast<float*>(tabs);  // [wave*4 + row][i][hn][m]
-  const v4f fwv = {fw[0], fw[1], fw[2], fw[3]};
-  const int row = lane >> 4;
+  float* red = reinterpret_cast<float*>(tabs);  // [wave][head m][dim]
+  if (lane < 16) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    v4f x = acc[i] * fwv;
+    for (int dg = 0; dg < 4; ++dg)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {  // sum of the row's four quads (same hn)
-      float y = x[m];
-      y += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x124, 0xF, 0xF, false));
-      y += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x128, 0xF, 0xF, false));
-      x[m] = y;
-    }
-    if ((lane & 15) < 4)
-      *reinterpret_cast<v4f*>(red + (((wave * 4 + row) * 16 + i) * 16 + hn * 4)) = x;
+      for (int m = 0; m < 4; ++m) red[(wave * 4 + m) * kDim + 16 * dg + lane] = acc[dg][m] * fw[m];
   }
   __syncthreads();
   if (tid < 4 * kDim) {
     const int m = tid >> 6, dim = tid & 63;
-    const int j = dim >> 4, i = dim & 15;
     float sum = 0.f;
-    for (int wr = 0; wr < kDlWaves * 4; ++wr) sum += red[(wr * 16 + i) * 16 + j * 4 + m];
+    for (int w = 0; w < kDlWaves; ++w) sum += red[(w * 4 + m) * kDim + dim];
     float L = 0.f;
     for (int w = 0; w < kDlWaves; ++w)
       if (red_m[w][m] != -INFINITY) L += red_l[w][m] * __builtin_amdgcn_exp2f(red_m[w][m] - mx[m]);
@@ -806,7 +821,7 @@ __global__ __launch_bounds__(kDlThreads, 2) void dl_decode_kernel(DlArgs a) {
 }
 
 // Bit-plane rows -> decode layout.  keys: one thread per output byte.  values: one
-// thread per (block, dim) byte of the blocks that tokens [pos, pos + n) touch; bits of
+// thread per byte of the 16-token chunks that tokens [pos, pos + n) touch; bits of
 // tokens outside that range are kept.
 __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_streams, int64_t n,
                                int d, int bits, int values, uint8_t* __restrict__ cache,
@@ -830,17 +845,24 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
           (uint8_t)((code(s, t, 2 * pidx) << 4) | code(s, t, 2 * pidx + 1));
     }
   } else {
-    const int64_t b0 = pos >> 2, b1 = (pos + n + 3) >> 2;
-    const int64_t nb = b1 - b0;
-    const int64_t total = n_streams * nb * d;
+    // chunks of 16 tokens, d/4 bytes per token column: byte c * (d/4) + tg * (d/16) + dg
+    // of chunk Q holds dim 16 * dg + c of tokens 16Q + 4tg + t, 2 bits each (t = 0..3)
+    const int csz = d * 4;  // bytes per chunk
+    const int ndg = d / 16;
+    const int64_t c0 = pos >> 4, c1 = (pos + n + 15) >> 4;
+    const int64_t nch = c1 - c0;
+    const int64_t total = n_streams * nch * csz;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-      const int j = (int)(e % d);
-      const int64_t r = e / d, s = r / nb, blk = b0 + (r - s * nb);
-      uint8_t* dst = cache + (s * (t_cap >> 2) + blk) * d + j;
+      const int byte = (int)(e % csz);
+      const int64_t r = e / csz, s = r / nch, ch = c0 + (r - s * nch);
+      const int c = byte / (4 * ndg), rem = byte - c * 4 * ndg;
+      const int tg = rem / ndg, dg = rem - tg * ndg;
+      const int j = 16 * dg + c;
+      uint8_t* dst = cache + (s * (t_cap >> 4) + ch) * csz + byte;
       uint32_t v = *dst;
       for (int tt = 0; tt < 4; ++tt) {
-        const int64_t t = blk * 4 + tt - pos;
+        const int64_t t = ch * 16 + tg * 4 + tt - pos;
         if (t < 0 || t >= n) continue;
         v = (v & ~(3u << (2 * tt))) | (code(s, t, j) << (2 * tt));
       }
@@ -870,7 +892,10 @@ __global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_st
         const uint8_t pb = cache[(s * t_cap + t) * (d / 2) + (j >> 1)];
         c = (j & 1) ? (pb & 15u) : (pb >> 4);
       } else {
-        c = (cache[(s * (t_cap >> 2) + (t >> 2)) * d + j] >> (2 * (t & 3))) & 3u;
+        const int ndg = d / 16;
+        const int64_t at = (s * (t_cap >> 4) + (t >> 4)) * (d * 4) + (j & 15) * 4 * ndg +
+                           ((t >> 2) & 3) * ndg + (j >> 4);
+        c = (cache[at] >> (2 * (t & 3))) & 3u;
       }
       out |= ((c >> p) & 1u) << (7 - k);
     }
@@ -973,7 +998,7 @@ namespace tq {
 namespace {
 
 SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
-  // one 512-thread workgroup per CU (128 KB of tables)
+  // one 512-thread workgroup per CU (132 KB of tables)
   const int64_t streams = (int64_t)B * hkv;
   const int64_t want = std::max<int64_t>(1, ((int64_t)device_cu_count() + streams - 1) / streams);
   int64_t split = (t_cap + want - 1) / want;
@@ -1009,7 +1034,7 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                                  "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
   TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
              "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
-  TQ_REQUIRE(t_cap >= 0 && t_cap % 4 == 0, "capacity must be a multiple of 4, got %lld",
+  TQ_REQUIRE(t_cap >= 0 && t_cap % 16 == 0, "capacity must be a multiple of 16, got %lld",
              (long long)t_cap);
   TQ_REQUIRE(t_cap * 32 < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
   TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
@@ -1061,10 +1086,11 @@ int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, i
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
   TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && pos >= 0 && pos + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || t_cap % 4 == 0, "value capacity must be a multiple of 4");
+  TQ_REQUIRE(!values || (t_cap % 16 == 0 && d % 16 == 0),
+             "value capacity and dim must be multiples of 16");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
-  const int64_t per = values ? (((pos + n + 3) >> 2) - (pos >> 2)) * d : n * (d / 2);
+  const int64_t per = values ? (((pos + n + 15) >> 4) - (pos >> 4)) * 4 * d : n * (d / 2);
   const int64_t total = n_streams * per;
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
   hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
@@ -1080,7 +1106,8 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
   TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && t0 >= 0 && t0 + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || t_cap % 4 == 0, "value capacity must be a multiple of 4");
+  TQ_REQUIRE(!values || (t_cap % 16 == 0 && d % 16 == 0),
+             "value capacity and dim must be multiples of 16");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
   const int64_t total = n_streams * n * bit_width * ((d + 7) / 8);
