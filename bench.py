@@ -175,12 +175,12 @@ def bench_decode(args, extra):
             del K, V
             # the decode layout QuantizedKVCache keeps (same bytes per token)
             kdl = torch.zeros(B * Hkv, T, d // 2, dtype=torch.uint8, device="cuda")
-            vdl = torch.zeros(B * Hkv, T // 16, 4 * d, dtype=torch.uint8, device="cuda")
+            vdl = torch.zeros(B * Hkv, T // 64, 16 * d, dtype=torch.uint8, device="cuda")
             ops.pack_decode_layout(kp.view(B * Hkv, T, -1), kdl, d, kb, 0, 0)
             ops.pack_decode_layout(vp.view(B * Hkv, T, -1), vdl, d, vb, 1, 0)
             caches.append((kp.view(B, Hkv, T, -1), kn.float().view(B, Hkv, T),
                            vp.view(B, Hkv, T, -1), vn.float().view(B, Hkv, T),
-                           kdl.view(B, Hkv, T, -1), vdl.view(B, Hkv, T // 16, -1)))
+                           kdl.view(B, Hkv, T, -1), vdl.view(B, Hkv, T // 64, -1)))
             del kp, vp
         q = torch.randn(B, Hq, d, generator=g, device="cuda").to(torch.bfloat16)
         sl = torch.full((B,), T, dtype=torch.int32, device="cuda")

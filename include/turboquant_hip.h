@@ -199,10 +199,10 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
  * its cache privately (cache.py:81-130), so this arrangement is internal to
  * QuantizedKVCache; these entry points convert it from and to the reference rows.
  *   keys    [streams][t_cap][d/2]:   byte p = (code[2p] << 4) | code[2p+1]
- *   values  [streams][t_cap/16][4d]: chunk Q holds tokens 16Q..16Q+15; its byte
- *           c*(d/4) + tg*(d/16) + dg = sum_t code[16Q + 4tg + t][16dg + c] << 2t
- *           (c < 16, tg < 4, dg < d/16, t < 4): lane c of a 16-lane group reads the 16
- *           bytes its 16x16x16 MFMAs need as one load (t_cap and d multiples of 16)
+ *   values  [streams][t_cap/64][1024] (d = 64): tile T holds tokens 64T..64T+63; its
+ *           byte 16*(16*sl + c) + 4*m + dg = sum_t code[64T + 4*(4m + sl) + t][16dg + c]
+ *           << 2t (sl, m, dg, t < 4; c < 16): lane 16*sl + c reads the 16 bytes its
+ *           16x16x32 MFMAs need as one load (t_cap a multiple of 64)
  * tq_pack_decode_layout writes tokens [pos, pos+n) of every stream from bit-plane rows
  * packed [streams][n][bits*ceil(d/8)] (values: bits of the chunk's other tokens are
  * kept); tq_unpack_decode_layout returns tokens [t0, t0+n) as bit-plane rows.
@@ -218,7 +218,7 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
 /*
  * tq_decode_attention_packed over a decode-layout cache (same semantics and output):
  * head_dim 64, 4-bit keys, 2-bit values, 1-4 query heads per KV head, t_cap a multiple
- * of 16.  kpairs [B, hkv, t_cap, 32], vblocks [B, hkv, t_cap/16, 256], norms as above.
+ * of 64.  kpairs [B, hkv, t_cap, 32], vblocks [B, hkv, t_cap/64, 1024], norms as above.
  * Scores are accurate to about 1e-6 relative (fp16 hi/lo products, fp32 accumulation);
  * fp32 queries get fp32-accurate outputs; fp16/bf16 queries use fp16 value products
  * (relative error about 5e-4, below the output type's own rounding tolerance).

@@ -475,8 +475,8 @@ void pack_decode_layout(const at::Tensor& packed, at::Tensor& cache, int64_t dim
   auto pk = packed.to(dev, at::kByte).contiguous();
   TORCH_CHECK(pk.dim() == 3 && pk.size(0) == cache.size(0), "packed must be [streams, n, P]");
   TORCH_CHECK(pk.size(2) == packed_width(bit_width, dim), "packed width mismatch");
-  const int64_t t_cap = values ? cache.size(1) * 16 : cache.size(1);
-  TORCH_CHECK(cache.size(2) == (values ? 4 * dim : dim / 2), "cache width mismatch");
+  const int64_t t_cap = values ? cache.size(1) * 64 : cache.size(1);
+  TORCH_CHECK(cache.size(2) == (values ? 16 * dim : dim / 2), "cache width mismatch");
   check_rc(tq_pack_decode_layout(pk.data_ptr<uint8_t>(), pk.size(0), pk.size(1), (int32_t)dim,
                                  (int32_t)bit_width, (int32_t)values, cache.data_ptr<uint8_t>(),
                                  t_cap, pos, cur_stream(cache)));
@@ -488,7 +488,7 @@ at::Tensor unpack_decode_layout(const at::Tensor& cache, int64_t dim, int64_t bi
   c10::DeviceGuard g(cache.device());
   TORCH_CHECK(cache.scalar_type() == at::kByte && cache.is_contiguous() && cache.dim() == 3,
               "cache must be contiguous uint8 [streams, rows, width]");
-  const int64_t t_cap = values ? cache.size(1) * 16 : cache.size(1);
+  const int64_t t_cap = values ? cache.size(1) * 64 : cache.size(1);
   auto out = at::empty({cache.size(0), n, packed_width(bit_width, dim)}, cache.options());
   check_rc(tq_unpack_decode_layout(cache.data_ptr<uint8_t>(), cache.size(0), t_cap, t0, n,
                                    (int32_t)dim, (int32_t)bit_width, (int32_t)values,
@@ -504,7 +504,7 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   require_gpu(q, "q");
   TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
   TORCH_CHECK(kpairs.dim() == 4 && vblocks.dim() == 4,
-              "kpairs must be [B, Hkv, T, d/2] and vblocks [B, Hkv, T/16, 4d]");
+              "kpairs must be [B, Hkv, T, d/2] and vblocks [B, Hkv, T/64, 16d]");
   c10::DeviceGuard g(q.device());
   const auto dev = q.device();
   auto qq = floatc(q, dev);
@@ -519,7 +519,7 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
                   vnorms.device() == dev,
               "K/V must be on the query's device");
   TORCH_CHECK(kpairs.size(0) == B && kpairs.size(3) == d / 2 && vblocks.size(0) == B &&
-                  vblocks.size(1) == Hkv && vblocks.size(2) * 16 == Tc && vblocks.size(3) == 4 * d,
+                  vblocks.size(1) == Hkv && vblocks.size(2) * 64 == Tc && vblocks.size(3) == 16 * d,
               "decode-layout K/V shape mismatch");
   TORCH_CHECK(knorms.scalar_type() == at::kFloat && vnorms.scalar_type() == at::kFloat &&
                   knorms.numel() == B * Hkv * Tc && vnorms.numel() == B * Hkv * Tc,

@@ -444,6 +444,29 @@ __device__ __forceinline__ v4h as_v4h(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(v4h, t);
 }
 
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v8h as_v8h(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 t = {a, b, c, d};
+  return __builtin_bit_cast(v8h, t);
+}
+
+__device__ __forceinline__ v8h cat_h(v4h lo, v4h hi) {
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return as_v8h(a.x, a.y, b.x, b.y);
+}
+
+// DPP row shifts of a float within each 16-lane row: row_shl:N -- lane i takes lane
+// i + N; row_shr:N -- lane i takes lane i - N (zero where the source leaves the row).
+template <int N>
+__device__ __forceinline__ float row_shl_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
+}
+template <int N>
+__device__ __forceinline__ float row_shr_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xF, 0xF, true));
+}
+
 // DPP row_shl:N on both words of a v4h: lane i of each 16-lane row takes lane i + N's
 // value (zero where i + N leaves the row).
 template <int N>
@@ -463,7 +486,11 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 
 // EXACT_V: the weights and V centroids enter as fp16 hi + lo parts (three products,
 // about 1e-6 relative), for fp32 outputs; otherwise one fp16 product (about 5e-4).
-template <bool EXACT_V>
+// PREC_K: q.K from fp16 hi + lo parts of query and centroids (three products, about 1e-6
+// relative), for fp32 and fp16 outputs; otherwise (bf16 outputs) one fp16 product per
+// term, about 2^-11 relative per operand -- finer than the bf16 arithmetic the reference
+// scores bf16 inputs in.
+template <bool EXACT_V, bool PREC_K>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
   // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
@@ -568,15 +595,35 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   __syncthreads();
 
   const int wave = tid >> 6, lane = tid & 63;
-  const int quad = lane >> 2, hn = lane & 3;
-  // (R_k q) * scale * log2(e) * qs2 of head hn, four dims per operand: hi and lo halves
-  v4h qh4[kDim / 4], ql4[kDim / 4];
+  // q.K runs on 16x16x32 MFMAs: rows = 16 tokens, k = 32 dims, cols = (part, head): col
+  // h holds the hi halves of head h's (R_k q) * scale * log2(e) * qs2, col 4 + h the lo
+  // halves, cols 8-15 zero.  Lane slice sl = lane / 16, chunk c: k = 8 sl + i is dim
+  // 16 sl + 8 c + i (the dims of key bytes 8 sl + 4 c .. + 3).  bq[c]: hi and lo columns
+  // (multiplies the centroid hi parts); bqh[c]: hi columns only (centroid lo parts).
+  // Without PREC_K each token group g has its own columns instead: col 4g + h = head h
+  // (hi halves), so one accumulator collects all four groups already in the score layout
+  // below.  bcol[c][g]: the lane's hi halves if col / 4 == g, else zero.
+  const int sl = lane >> 4, col = lane & 15;
+  v8h bq[2], bqh[2], bcol[2][4];
 #pragma unroll
-  for (int g = 0; g < kDim / 4; ++g) {
-    qh4[g] = *reinterpret_cast<const v4h*>(&qhl_s[hn][0][4 * g]);
-    ql4[g] = *reinterpret_cast<const v4h*>(&qhl_s[hn][1][4 * g]);
+  for (int c = 0; c < 2; ++c) {
+    const int d0 = 16 * sl + 8 * c;
+    const v8h z = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (PREC_K) {
+      const v8h hi = col < 4 ? *reinterpret_cast<const v8h*>(&qhl_s[col][0][d0]) : z;
+      const v8h lo = (col >= 4 && col < 8) ? *reinterpret_cast<const v8h*>(&qhl_s[col - 4][1][d0]) : z;
+      bq[c] = col < 4 ? hi : lo;
+      bqh[c] = hi;
+    } else {
+      const v8h hi = *reinterpret_cast<const v8h*>(&qhl_s[col & 3][0][d0]);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) bcol[c][g] = (col >> 2) == g ? hi : z;
+    }
   }
-  const float kinv = 1.f / (ksc * qs2_s[hn]);  // a power of two: exact
+  // Score layout after q.K: lane 16 sl + 4 g + h holds tokens 16 g + 4 sl + r (register r)
+  // of head h; g = token group of the 16x16x32 MFMA whose rows hold them.
+  const int hh = lane & 3, gq = (lane >> 2) & 3;
+  const float kinv = 1.f / (ksc * qs2_s[hh]);  // a power of two: exact
   // byte 0: copy offset; byte 2 of kcopy: the K table's 64 KB base
   const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
   const uint32_t vcopy =
@@ -585,7 +632,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const size_t sbase = (size_t)bg * (size_t)a.t_cap;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 15) >> 4) * 256);
+      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 63) >> 6) * 1024);
   // Norms are read four tokens at a time: the range covers whole quads (inside the
   // allocation, t_cap % 4 == 0); entries past t_end are masked.
   const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
@@ -594,21 +641,18 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const int te = (int)t_end;
 
   struct Tile {
-    uint32_t k[8];   // this lane's token: 32 pair bytes
-    uint32_t v[4];   // value chunk lane/16, column lane%16: word tg = 4 dim-group bytes
-    float kn[4], vn[4];
+    u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
+    uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
+    float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
   };
   auto load_tile = [&](int t0, Tile& x) {
-    const uint32_t ko = (uint32_t)(t0 + lane) * 32;
-    const u32x4 k0 = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 0, 0);
-    const u32x4 k1 = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)ko, 16, 0);
-    x.k[0] = k0.x; x.k[1] = k0.y; x.k[2] = k0.z; x.k[3] = k0.w;
-    x.k[4] = k1.x; x.k[5] = k1.y; x.k[6] = k1.z; x.k[7] = k1.w;
-    const uint32_t vo = (uint32_t)((t0 >> 4) + (lane >> 4)) * 256 + (uint32_t)(lane & 15) * 16;
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)vo, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((uint32_t)(t0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)(t0 >> 6) * 1024 + lane * 16), 0, 0);
     x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
-    // norms of the quad's four tokens: 16-byte aligned (t_cap % 4 == 0, aligned base)
-    const uint32_t no = (uint32_t)(t0 + 4 * quad) * 4;
+    // norms of the lane's four tokens: 16-byte aligned (t_cap % 64 == 0, aligned base)
+    const uint32_t no = (uint32_t)(t0 + 16 * gq + 4 * sl) * 4;
     const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
     const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
     // (__builtin_bit_cast of a vector element would read element 0: convert by value)
@@ -625,33 +669,71 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 
   // One 64-token tile of this wave: x holds its data, loaded one tile ahead.
   auto process = [&](const Tile& cur, int t0) {
-    // ---- q.K: A = c[code] of this lane's token, B = query of head hn, four dims per
-    // MFMA, fp16 hi/lo parts: c.q = ch.qh + ch.ql + cl.qh (the cl.ql term is 2^-22
-    // relative), accumulated in fp32
-    v4f sk[6];  // six chains: no MFMA waits on the one issued just before it
+    // ---- q.K: per token group g, four 16x16x32 MFMAs: chunks c = 0, 1 of the lane's 8
+    // key bytes, centroid hi parts against the (hi | lo) query columns and centroid lo
+    // parts against the hi columns: c.q = ch.qh + ch.ql + cl.qh (the cl.ql term is 2^-22
+    // relative), accumulated in fp32.  dk[g] (lane 16 sl + n, register r) = token 16 g +
+    // 4 sl + r, column n.
+    v4f skk;
+    if constexpr (!PREC_K) {
+      // one product per term; chunk c accumulates in its own chain
+      v4f d2[2] = {(v4f){0.f, 0.f, 0.f, 0.f}, (v4f){0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int x = 0; x < 6; ++x) sk[x] = (v4f){0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < 4; ++g) {
 #pragma unroll
-    for (int g = 0; g < kDim / 4; ++g) {  // dims 4g .. 4g+3 = pair bytes 2g, 2g+1
-      const uint32_t w = cur.k[g >> 1];
-      const uint32_t a0 = byte_addr(kcopy, w, 2 * (g & 1));
-      const uint32_t a1 = byte_addr(kcopy, w, 2 * (g & 1) + 1);
-      const v4h ah = as_v4h(*reinterpret_cast<const uint32_t*>(tabs + a0),
-                            *reinterpret_cast<const uint32_t*>(tabs + a1));
-      const v4h al = as_v4h(*reinterpret_cast<const uint32_t*>(tabs + a0 + kDlKLo),
-                            *reinterpret_cast<const uint32_t*>(tabs + a1 + kDlKLo));
-      const int c = 3 * (g & 1);
-      sk[c] = __builtin_amdgcn_mfma_f32_4x4x4f16(ah, qh4[g], sk[c], 0, 0, 0);
-      sk[c + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(ah, ql4[g], sk[c + 1], 0, 0, 0);
-      sk[c + 2] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, qh4[g], sk[c + 2], 0, 0, 0);
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t w = c ? cur.k[g].y : cur.k[g].x;
+          uint32_t ad[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ad[j] = byte_addr(kcopy, w, j);
+          const v8h ah = as_v8h(*reinterpret_cast<const uint32_t*>(tabs + ad[0]),
+                                *reinterpret_cast<const uint32_t*>(tabs + ad[1]),
+                                *reinterpret_cast<const uint32_t*>(tabs + ad[2]),
+                                *reinterpret_cast<const uint32_t*>(tabs + ad[3]));
+          d2[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bcol[c][g], d2[c], 0, 0, 0);
+        }
+      }
+      skk = (d2[0] + d2[1]) * kinv;
+    } else {
+    v4f dk[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      dk[g] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint32_t w = c ? cur.k[g].y : cur.k[g].x;
+        uint32_t ad[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ad[j] = byte_addr(kcopy, w, j);
+        const v8h ah = as_v8h(*reinterpret_cast<const uint32_t*>(tabs + ad[0]),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[1]),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[2]),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[3]));
+        const v8h al = as_v8h(*reinterpret_cast<const uint32_t*>(tabs + ad[0] + kDlKLo),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[1] + kDlKLo),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[2] + kDlKLo),
+                              *reinterpret_cast<const uint32_t*>(tabs + ad[3] + kDlKLo));
+        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[c], dk[g], 0, 0, 0);
+        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[c], dk[g], 0, 0, 0);
+      }
     }
-    const v4f skk = ((sk[0] + sk[3]) + (sk[1] + sk[4]) + (sk[2] + sk[5])) * kinv;
+    // Lane 16 sl + 4 g + h takes group g's column h (lane 16 sl + h) plus column 4 + h
+    // (lane 16 sl + 4 + h): row shifts within each 16-lane row, then a select by g.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x0 = dk[0][r] + row_shl_f<4>(dk[0][r]);
+      const float x1 = row_shr_f<4>(dk[1][r]) + dk[1][r];
+      const float x2 = row_shr_f<8>(dk[2][r]) + row_shr_f<4>(dk[2][r]);
+      const float x3 = row_shr_f<12>(dk[3][r]) + row_shr_f<8>(dk[3][r]);
+      skk[r] = (gq == 0 ? x0 : gq == 1 ? x1 : gq == 2 ? x2 : x3) * kinv;
+    }
+    }
 
-    // ---- online softmax (register r = token t0 + 4 * quad + r, head hn)
+    // ---- online softmax (register r = token t0 + 16 gq + 4 sl + r, head hh)
     // Tokens at or past te are masked with selects at their use (branch-free: a masked
     // copy of the norms merged from a branch was miscompiled -- registers of the live
     // norms reused before their last read).
-    const int nvalid = te - (t0 + 4 * quad);
+    const int nvalid = te - (t0 + 16 * gq + 4 * sl);
     float s[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[r] = r < nvalid ? skk[r] * cur.kn[r] : -INFINITY;
@@ -699,65 +781,71 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- p.V: one 16x16x16 MFMA per (token group tg, dim group dg): A rows = heads
-    // (rows 4-15 unused), k = tokens 16q + 4tg + t of lane group q = lane / 16, B cols =
-    // dims 16 dg + lane % 16.  A_tg is the weights of lane 16q + 4tg + h moved to lane
-    // 16q + h: a row shift left by 4tg.
-    v4h aw[4], awl[4];
-    aw[0] = wh;
-    aw[1] = row_shl_h<4>(wh);
-    aw[2] = row_shl_h<8>(wh);
-    aw[3] = row_shl_h<12>(wh);
+    // ---- p.V: one 16x16x32 MFMA per (token half G, dim group dg): A rows = heads (rows
+    // 4-15 unused), k = 8 sl + j: tokens of block 8G + sl (j < 4) and 8G + 4 + sl (j >= 4),
+    // B cols = dims 16 dg + col.  Lane 16 sl + h takes the weights of lanes 16 sl + 8G + h
+    // and 16 sl + 8G + 4 + h: row shifts left by 8G and 8G + 4.
+    v8h aw[2], awl[2];
+    aw[0] = cat_h(wh, row_shl_h<4>(wh));
+    aw[1] = cat_h(row_shl_h<8>(wh), row_shl_h<12>(wh));
     if constexpr (EXACT_V) {
-      awl[0] = wl;
-      awl[1] = row_shl_h<4>(wl);
-      awl[2] = row_shl_h<8>(wl);
-      awl[3] = row_shl_h<12>(wl);
+      awl[0] = cat_h(wl, row_shl_h<4>(wl));
+      awl[1] = cat_h(row_shl_h<8>(wl), row_shl_h<12>(wl));
     }
     if constexpr (!EXACT_V) {
-      v4h bv[16];
+      v8h bv[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)  // i = 4 tg + dg
-        bv[i] = *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[i >> 2], i & 3));
+      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
+        const int G = i >> 2, dg = i & 3;
+        bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg)),
+                      *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg)));
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        acc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[i >> 2], bv[i], acc[i & 3], 0, 0, 0);
+      for (int i = 0; i < 8; ++i)
+        acc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[i >> 2], bv[i], acc[i & 3], 0, 0, 0);
     } else {
 #pragma unroll
-      for (int tg = 0; tg < 4; ++tg) {
-        v4h bh[4], bl[4];
+      for (int G = 0; G < 2; ++G) {
+        v8h bh[4], bl[4];
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
-          const u32x4 e = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[tg], dg));
-          bh[dg] = as_v4h(e.x, e.y);
-          bl[dg] = as_v4h(e.z, e.w);
+          const u32x4 e0 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg));
+          const u32x4 e1 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg));
+          bh[dg] = as_v8h(e0.x, e0.y, e1.x, e1.y);
+          bl[dg] = as_v8h(e0.z, e0.w, e1.z, e1.w);
         }
-        if (tg == 0) __builtin_amdgcn_sched_barrier(0);
+        if (G == 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[tg], bh[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bh[dg], acc[dg], 0, 0, 0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(awl[tg], bh[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(awl[G], bh[dg], acc[dg], 0, 0, 0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x16f16(aw[tg], bl[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bl[dg], acc[dg], 0, 0, 0);
       }
     }
 
   };
 
-  // Two tile buffers used in turn, so no copy waits for the prefetch to land.
+  // Tiles are loaded two ahead into three buffers used in turn: one tile of lookahead
+  // does not cover the HBM latency under full load.  Loads past te read zeros (buffer
+  // range check); the tile count is made wave-uniform explicitly.
   constexpr int kStep = kDlWaves * 64;
-  int t0 = (int)t_begin + wave * 64;
-  Tile ta, tb;
-  if (t0 < te) load_tile(t0, ta);
-  while (t0 < te) {
-    load_tile(t0 + kStep, tb);
-    process(ta, t0);
-    t0 += kStep;
-    if (t0 >= te) break;
-    load_tile(t0 + kStep, ta);
-    process(tb, t0);
-    t0 += kStep;
+  const int tf = (int)t_begin + wave * 64;
+  const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
+  Tile ta, tb, tc;
+  load_tile(tf, ta);
+  load_tile(tf + kStep, tb);
+  for (int it = 0; it < ntiles; it += 3) {
+    const int t = tf + it * kStep;
+    load_tile(t + 2 * kStep, tc);
+    process(ta, t);
+    if (it + 1 >= ntiles) break;
+    load_tile(t + 3 * kStep, ta);
+    process(tb, t + kStep);
+    if (it + 2 >= ntiles) break;
+    load_tile(t + 4 * kStep, tb);
+    process(tc, t + 2 * kStep);
   }
 
   // ---- reduction: l over the lanes of a head; outputs over the waves (LDS)
@@ -821,7 +909,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 }
 
 // Bit-plane rows -> decode layout.  keys: one thread per output byte.  values: one
-// thread per byte of the 16-token chunks that tokens [pos, pos + n) touch; bits of
+// thread per byte of the 64-token tiles that tokens [pos, pos + n) touch; bits of
 // tokens outside that range are kept.
 __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_streams, int64_t n,
                                int d, int bits, int values, uint8_t* __restrict__ cache,
@@ -845,24 +933,22 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
           (uint8_t)((code(s, t, 2 * pidx) << 4) | code(s, t, 2 * pidx + 1));
     }
   } else {
-    // chunks of 16 tokens, d/4 bytes per token column: byte c * (d/4) + tg * (d/16) + dg
-    // of chunk Q holds dim 16 * dg + c of tokens 16Q + 4tg + t, 2 bits each (t = 0..3)
-    const int csz = d * 4;  // bytes per chunk
-    const int ndg = d / 16;
-    const int64_t c0 = pos >> 4, c1 = (pos + n + 15) >> 4;
-    const int64_t nch = c1 - c0;
-    const int64_t total = n_streams * nch * csz;
+    // value tiles of 64 tokens (d = 64): byte 16 L + 4 m + dg of tile T, L = 16 sl + c,
+    // holds dim 16 dg + c of tokens 64 T + 4 (4 m + sl) + t, 2 bits each (t = 0..3)
+    const int64_t c0 = pos >> 6, c1 = (pos + n + 63) >> 6;
+    const int64_t nt = c1 - c0;
+    const int64_t total = n_streams * nt * 1024;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-      const int byte = (int)(e % csz);
-      const int64_t r = e / csz, s = r / nch, ch = c0 + (r - s * nch);
-      const int c = byte / (4 * ndg), rem = byte - c * 4 * ndg;
-      const int tg = rem / ndg, dg = rem - tg * ndg;
+      const int byte = (int)(e & 1023);
+      const int64_t r = e >> 10, s = r / nt, tile = c0 + (r - s * nt);
+      const int L = byte >> 4, m = (byte >> 2) & 3, dg = byte & 3;
+      const int sl = L >> 4, c = L & 15;
       const int j = 16 * dg + c;
-      uint8_t* dst = cache + (s * (t_cap >> 4) + ch) * csz + byte;
+      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * 1024 + byte;
       uint32_t v = *dst;
       for (int tt = 0; tt < 4; ++tt) {
-        const int64_t t = ch * 16 + tg * 4 + tt - pos;
+        const int64_t t = tile * 64 + 4 * (4 * m + sl) + tt - pos;
         if (t < 0 || t >= n) continue;
         v = (v & ~(3u << (2 * tt))) | (code(s, t, j) << (2 * tt));
       }
@@ -892,9 +978,9 @@ __global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_st
         const uint8_t pb = cache[(s * t_cap + t) * (d / 2) + (j >> 1)];
         c = (j & 1) ? (pb & 15u) : (pb >> 4);
       } else {
-        const int ndg = d / 16;
-        const int64_t at = (s * (t_cap >> 4) + (t >> 4)) * (d * 4) + (j & 15) * 4 * ndg +
-                           ((t >> 2) & 3) * ndg + (j >> 4);
+        const int blk = (int)((t >> 2) & 15);  // block within the 64-token tile = 4 m + sl
+        const int64_t at = (s * (t_cap >> 6) + (t >> 6)) * 1024 + ((blk & 3) * 16 + (j & 15)) * 16 +
+                           (blk >> 2) * 4 + (j >> 4);
         c = (cache[at] >> (2 * (t & 3))) & 3u;
       }
       out |= ((c >> p) & 1u) << (7 - k);
@@ -1034,7 +1120,7 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                                  "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
   TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
              "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
-  TQ_REQUIRE(t_cap >= 0 && t_cap % 16 == 0, "capacity must be a multiple of 16, got %lld",
+  TQ_REQUIRE(t_cap >= 0 && t_cap % 64 == 0, "capacity must be a multiple of 64, got %lld",
              (long long)t_cap);
   TQ_REQUIRE(t_cap * 32 < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
   TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
@@ -1066,9 +1152,11 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
     a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
     const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
     if (q_dtype == TQ_F32)
-      hipLaunchKernelGGL(dl_decode_kernel<true>, grid, dim3(kDlThreads), 0, st, a);
+      hipLaunchKernelGGL((dl_decode_kernel<true, true>), grid, dim3(kDlThreads), 0, st, a);
+    else if (q_dtype == TQ_F16)
+      hipLaunchKernelGGL((dl_decode_kernel<false, true>), grid, dim3(kDlThreads), 0, st, a);
     else
-      hipLaunchKernelGGL(dl_decode_kernel<false>, grid, dim3(kDlThreads), 0, st, a);
+      hipLaunchKernelGGL((dl_decode_kernel<false, false>), grid, dim3(kDlThreads), 0, st, a);
     TQ_LAUNCH_CHECK("dl_decode_kernel");
     if (single) return TQ_OK;
   }
@@ -1086,11 +1174,11 @@ int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, i
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
   TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && pos >= 0 && pos + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || (t_cap % 16 == 0 && d % 16 == 0),
-             "value capacity and dim must be multiples of 16");
+  TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
+             "value tiles need dim 64 and a capacity that is a multiple of 64");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
-  const int64_t per = values ? (((pos + n + 15) >> 4) - (pos >> 4)) * 4 * d : n * (d / 2);
+  const int64_t per = values ? (((pos + n + 63) >> 6) - (pos >> 6)) * 1024 : n * (d / 2);
   const int64_t total = n_streams * per;
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
   hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
@@ -1106,8 +1194,8 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
   TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && t0 >= 0 && t0 + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || (t_cap % 16 == 0 && d % 16 == 0),
-             "value capacity and dim must be multiples of 16");
+  TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
+             "value tiles need dim 64 and a capacity that is a multiple of 64");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
   const int64_t total = n_streams * n * bit_width * ((d + 7) / 8);

@@ -82,8 +82,8 @@ class QuantizedKVCache:
 
         bpp = (head_dim + 7) // 8
         self._dl = (not self._is_prod and kb == 4 and vb == 2 and head_dim == 64)
-        # decode-layout value chunks hold 16 tokens: capacity rounded up to a multiple of 16
-        self._t_cap = (max_seq_len + 15) // 16 * 16 if self._dl else max_seq_len
+        # decode-layout value tiles hold 64 tokens: capacity rounded up to a multiple of 64
+        self._t_cap = (max_seq_len + 63) // 64 * 64 if self._dl else max_seq_len
         B, H, T = batch_size, num_heads, self._t_cap
         u8 = dict(dtype=torch.uint8, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
@@ -100,7 +100,7 @@ class QuantizedKVCache:
                 continue
             if self._dl:
                 self._kstore.append(torch.zeros(B, H, T, head_dim // 2, **u8))
-                self._vstore.append(torch.zeros(B, H, T // 16, 4 * head_dim, **u8))
+                self._vstore.append(torch.zeros(B, H, T // 64, 16 * head_dim, **u8))
             else:
                 self._kstore.append(torch.zeros(B, H, T, kb * bpp, **u8))
                 self._vstore.append(torch.zeros(B, H, T, vb * bpp, **u8))

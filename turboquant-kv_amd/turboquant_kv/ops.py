@@ -88,8 +88,8 @@ def decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens, k
 def pack_decode_layout(packed: torch.Tensor, cache: torch.Tensor, dim: int, bit_width: int,
                        values: bool, pos: int) -> None:
     """Write bit-plane rows [streams, n, P] into a decode-layout cache at tokens pos..pos+n
-    (keys: [streams, t_cap, dim/2] pair bytes, 4-bit; values: [streams, t_cap/16, 4*dim]
-    chunk bytes, 2-bit)."""
+    (keys: [streams, t_cap, dim/2] pair bytes, 4-bit; values: [streams, t_cap/64, 16*dim]
+    tile bytes, 2-bit; dim 64)."""
     _require_device(cache, "cache")
     _ops().pack_decode_layout(packed, cache, dim, bit_width, int(values), pos)
 
