@@ -456,6 +456,11 @@ __device__ __forceinline__ v8h cat_h(v4h lo, v4h hi) {
   return as_v8h(a.x, a.y, b.x, b.y);
 }
 
+__device__ __forceinline__ uint32_t pack_h2(_Float16 lo, _Float16 hi) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, (h2_t){lo, hi});
+}
+
 // DPP row shifts of a float within each 16-lane row: row_shl:N -- lane i takes lane
 // i + N; row_shr:N -- lane i takes lane i - N (zero where the source leaves the row).
 template <int N>
@@ -524,6 +529,48 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     return;
   }
 
+  const int wave = tid >> 6, lane = tid & 63;
+  // Lane roles (see the score layout and the tile loads below).
+  const int sl = lane >> 4, col = lane & 15;
+  const int hh = lane & 3, gq = (lane >> 2) & 3;
+  const size_t sbase = (size_t)bg * (size_t)a.t_cap;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
+  const __amdgpu_buffer_rsrc_t vrs =
+      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 63) >> 6) * 1024);
+  // Norms are read four tokens at a time: the range covers whole quads (inside the
+  // allocation, t_cap % 4 == 0); entries past t_end are masked.
+  const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
+  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
+  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
+  const int te = (int)t_end;
+
+  struct Tile {
+    u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
+    uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
+    float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
+  };
+  auto load_tile = [&](int t0, Tile& x) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((uint32_t)(t0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)(t0 >> 6) * 1024 + lane * 16), 0, 0);
+    x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+    // norms of the lane's four tokens: 16-byte aligned (t_cap % 64 == 0, aligned base)
+    const uint32_t no = (uint32_t)(t0 + 16 * gq + 4 * sl) * 4;
+    const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
+    const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
+    // (__builtin_bit_cast of a vector element would read element 0: convert by value)
+    x.kn[0] = __uint_as_float(kn4.x); x.kn[1] = __uint_as_float(kn4.y);
+    x.kn[2] = __uint_as_float(kn4.z); x.kn[3] = __uint_as_float(kn4.w);
+    x.vn[0] = __uint_as_float(vn4.x); x.vn[1] = __uint_as_float(vn4.y);
+    x.vn[2] = __uint_as_float(vn4.z); x.vn[3] = __uint_as_float(vn4.w);
+  };
+
+  constexpr int kStep = kDlWaves * 64;
+  const int tf = (int)t_begin + wave * 64;
+  const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
+  Tile ta, tb, tc;
+
   // ---- prologue
   if (tid < 16) cen_s[tid] = a.kcen[tid];
   else if (tid < 20) cen_s[tid] = a.vcen[tid - 16];
@@ -563,38 +610,42 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if (l == 0) sc_s[1] = pow2_scale(km);
   }
   __syncthreads();
+  // The first two tiles are requested here, after the prologue's own global reads (loads
+  // complete in issue order) and before the tables are built: their HBM latency runs
+  // under the table fill.
+  load_tile(tf, ta);
+  load_tile(tf + kStep, tb);
   const float vsc = sc_s[0];
   const float ksc = sc_s[1];
-  for (int e = tid; e < 256 * 32; e += kDlThreads) {
-    const int i = e >> 5, c = e & 31;
-    {
-      const float x0 = cen_s[i >> 4] * ksc, x1 = cen_s[i & 15] * ksc;
-      const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-      typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<h2_t*>(ktab + i * kDlEntry + 128 + c * 4) = (h2_t){h0, h1};
-      *reinterpret_cast<h2_t*>(ktab + i * kDlEntry + 128 + kDlKLo + c * 4) =
-          (h2_t){(_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1)};
+  // Tables: each thread writes 16-byte runs of identical copies.  K: entry i, copies 4q ..
+  // 4q + 3 of the hi parts (and of the lo parts with PREC_K).  V: entry i, copies 2q,
+  // 2q + 1 (or, EXACT_V, copy q: hi and lo halves).
+  for (int e = tid; e < 256 * 8; e += kDlThreads) {
+    const int i = e >> 3, q = e & 7;
+    const float x0 = cen_s[i >> 4] * ksc, x1 = cen_s[i & 15] * ksc;
+    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+    const uint32_t wh = pack_h2(h0, h1);
+    *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + q * 16) = (u32x4){wh, wh, wh, wh};
+    if constexpr (PREC_K) {
+      const uint32_t wl = pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
+      *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + kDlKLo + q * 16) = (u32x4){wl, wl, wl, wl};
     }
-    if constexpr (!EXACT_V) {
-      v4h vv;
+  }
+  for (int e = tid; e < 256 * 16; e += kDlThreads) {
+    const int i = e >> 4, q = e & 15;
+    v4h vh, vl;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) vv[t] = (_Float16)(cen_s[16 + ((i >> (2 * t)) & 3)] * vsc);
-      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 8) = vv;
-    } else if (c < 16) {
-      v4h vh, vl;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float x = cen_s[16 + ((i >> (2 * t)) & 3)] * vsc;
-        vh[t] = (_Float16)x;
-        vl[t] = (_Float16)(x - (float)vh[t]);
-      }
-      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 16) = vh;
-      *reinterpret_cast<v4h*>(vtab + i * kDlEntry + c * 16 + 8) = vl;
+    for (int t = 0; t < 4; ++t) {
+      const float x = cen_s[16 + ((i >> (2 * t)) & 3)] * vsc;
+      vh[t] = (_Float16)x;
+      vl[t] = (_Float16)(x - (float)vh[t]);
     }
+    const u32x2 h = __builtin_bit_cast(u32x2, vh), lo = __builtin_bit_cast(u32x2, vl);
+    *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) =
+        EXACT_V ? (u32x4){h.x, h.y, lo.x, lo.y} : (u32x4){h.x, h.y, h.x, h.y};
   }
   __syncthreads();
 
-  const int wave = tid >> 6, lane = tid & 63;
   // q.K runs on 16x16x32 MFMAs: rows = 16 tokens, k = 32 dims, cols = (part, head): col
   // h holds the hi halves of head h's (R_k q) * scale * log2(e) * qs2, col 4 + h the lo
   // halves, cols 8-15 zero.  Lane slice sl = lane / 16, chunk c: k = 8 sl + i is dim
@@ -603,7 +654,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // Without PREC_K each token group g has its own columns instead: col 4g + h = head h
   // (hi halves), so one accumulator collects all four groups already in the score layout
   // below.  bcol[c][g]: the lane's hi halves if col / 4 == g, else zero.
-  const int sl = lane >> 4, col = lane & 15;
   v8h bq[2], bqh[2], bcol[2][4];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -622,45 +672,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   }
   // Score layout after q.K: lane 16 sl + 4 g + h holds tokens 16 g + 4 sl + r (register r)
   // of head h; g = token group of the 16x16x32 MFMA whose rows hold them.
-  const int hh = lane & 3, gq = (lane >> 2) & 3;
   const float kinv = 1.f / (ksc * qs2_s[hh]);  // a power of two: exact
   // byte 0: copy offset; byte 2 of kcopy: the K table's 64 KB base
   const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
   const uint32_t vcopy =
       EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
-
-  const size_t sbase = (size_t)bg * (size_t)a.t_cap;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
-  const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 63) >> 6) * 1024);
-  // Norms are read four tokens at a time: the range covers whole quads (inside the
-  // allocation, t_cap % 4 == 0); entries past t_end are masked.
-  const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
-  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
-  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
-  const int te = (int)t_end;
-
-  struct Tile {
-    u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
-    uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
-    float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
-  };
-  auto load_tile = [&](int t0, Tile& x) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((uint32_t)(t0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)(t0 >> 6) * 1024 + lane * 16), 0, 0);
-    x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
-    // norms of the lane's four tokens: 16-byte aligned (t_cap % 64 == 0, aligned base)
-    const uint32_t no = (uint32_t)(t0 + 16 * gq + 4 * sl) * 4;
-    const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
-    const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
-    // (__builtin_bit_cast of a vector element would read element 0: convert by value)
-    x.kn[0] = __uint_as_float(kn4.x); x.kn[1] = __uint_as_float(kn4.y);
-    x.kn[2] = __uint_as_float(kn4.z); x.kn[3] = __uint_as_float(kn4.w);
-    x.vn[0] = __uint_as_float(vn4.x); x.vn[1] = __uint_as_float(vn4.y);
-    x.vn[2] = __uint_as_float(vn4.z); x.vn[3] = __uint_as_float(vn4.w);
-  };
 
   float M = -INFINITY, l = 0.f;
   v4f acc[4];  // dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 16 dg + lane
@@ -729,6 +745,18 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     }
     }
 
+    // The value-centroid lookups depend only on the tile's bytes: issued here, their LDS
+    // latency runs under the softmax arithmetic.  (p.V below describes the operands.)
+    v8h bv[8];
+    if constexpr (!EXACT_V) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
+        const int G = i >> 2, dg = i & 3;
+        bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg)),
+                      *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg)));
+      }
+    }
+
     // ---- online softmax (register r = token t0 + 16 gq + 4 sl + r, head hh)
     // Tokens at or past te are masked with selects at their use (branch-free: a masked
     // copy of the norms merged from a branch was miscompiled -- registers of the live
@@ -793,14 +821,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       awl[1] = cat_h(row_shl_h<8>(wl), row_shl_h<12>(wl));
     }
     if constexpr (!EXACT_V) {
-      v8h bv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
-        const int G = i >> 2, dg = i & 3;
-        bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg)),
-                      *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg)));
-      }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         acc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[i >> 2], bv[i], acc[i & 3], 0, 0, 0);
@@ -830,12 +850,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // Tiles are loaded two ahead into three buffers used in turn: one tile of lookahead
   // does not cover the HBM latency under full load.  Loads past te read zeros (buffer
   // range check); the tile count is made wave-uniform explicitly.
-  constexpr int kStep = kDlWaves * 64;
-  const int tf = (int)t_begin + wave * 64;
-  const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
-  Tile ta, tb, tc;
-  load_tile(tf, ta);
-  load_tile(tf + kStep, tb);
   for (int it = 0; it < ntiles; it += 3) {
     const int t = tf + it * kStep;
     load_tile(t + 2 * kStep, tc);
