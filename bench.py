@@ -37,9 +37,9 @@ sys.path.insert(0, os.path.join(ROOT, "turboquant-kv_amd"))
 HBM_PEAK_GBS = 8000.0
 METRIC = "packed-KV decode-attn GB/s (% HBM peak); 10M×d128 4-bit IP scan queries/s"
 PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms
-# HBM bytes per launch of scan_kernel<4,16,1,true,false> on the headline workload, from
+# HBM bytes per launch of pair_scan_kernel<128,true> on the headline workload, from
 # rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a copy kernel's readings (FETCH x2.0,
-# WRITE x1.0); commands and raw counts in profiles/scan_kernel_b4_q1_N10M_d128.md.
+# WRITE x1.0); commands and raw counts in profiles/pair_scan_kernel_b4_q1_N10M_d128.md.
 SCAN_TRAFFIC_BYTES = 680.8e6
 
 
@@ -325,7 +325,7 @@ def main():
                    "N": 10_000_000, "d": 128, "bits": 4, "queries_per_step": 1, "k": 10},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": SCAN_TRAFFIC_BYTES,
-                     "kernel": "ip_scan_topk_pairs op (scan_kernel + merge_kernel)",
+                     "kernel": "ip_scan_topk_pairs op (pair_scan_kernel<128,true> + merge_kernel)",
                      "bytes_per_launch": bytes_alg},
         "cpu_baseline": cpu,
         "decode_attn_GBps": {str(T): v[1] / v[0] / 1e6 for T, v in dec.items()},

@@ -474,6 +474,56 @@ def test_pairs_scan_ties_padding_and_golden(golden):
     assert np.allclose(s, ix["b4_scores"], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_pairs_scan_one_query(d):
+    # One query per call runs the pair-byte kernel (both centroids of a byte from one
+    # table read, products formed in registers, a block-wide bound after each wave's
+    # first 64 rows).  Scores stay bit-exact.
+    rs = np.random.RandomState(70 + d)
+    N = 300_000 + 29
+    R, cen, p, nm = _db(rs, N, d, 4)
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(1, d).astype(np.float32)
+    s32, i32 = O.search_topk(q, p, nm, cen, R, 4, 32)
+    for k in (1, 10, 32):  # k = 32: the block list merge ranks more than 128 entries
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        assert np.array_equal(i, i32[:, :k]), k
+        assert np.array_equal(s.view(np.uint32), s32[:, :k].view(np.uint32)), k
+    # small and ragged databases: waves without rows, a partial last step, k > N
+    for n in (1, 5, 63, 64, 65, 700, 769, 5000):
+        s, i = k_scan_pairs(q, pairs[:n], nm[:n], cen, R, 10)
+        so, io = O.search_topk(q, p[:n], nm[:n], cen, R, 4, 10)
+        assert np.array_equal(i, io), n
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), n
+    q16 = q.astype(np.float16)
+    s, i = k_scan_pairs(q16, pairs, nm, cen, R, 10, capi.TQ_F16)
+    so, io = O.search_topk(q16.astype(np.float32), p, nm, cen, R, 4, 10)
+    assert np.array_equal(i, io)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    got = k_scores_pairs(q, pairs[:20000], nm[:20000], cen, R)  # every score, one query
+    want = O.lut_scores_f32(q, p[:20000], nm[:20000], cen, R, 4)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_pairs_scan_one_query_ties():
+    # 3000 copies of the best row tie exactly: the block bound and the wave lists must
+    # keep the lowest ids among them (and the merge takes its exact fallback).
+    rs = np.random.RandomState(17)
+    d = 128
+    R, cen, p, nm = _db(rs, 30000, d, 4)
+    q = rs.randn(1, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q, p, nm, cen, R, 4)))
+    idx = rs.choice(30000, 3000, replace=False)
+    p[idx] = p[top]
+    nm[idx] = nm[top]
+    pairs = k_pack_pairs(p, d)
+    for k in (4, 16, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = O.search_topk(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
 # ------------------------------------------------------------------ decode attention
 @pytest.mark.parametrize("d,kb,vb", [(64, 4, 2), (128, 3, 4), (64, 2, 3)])
 def test_decode_attention_vs_f64(d, kb, vb):

@@ -33,6 +33,7 @@
 #include "tq_decode.h"
 
 #include <climits>
+#include <utility>
 
 namespace tq {
 namespace {
@@ -507,6 +508,380 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ pair-layout scan, one query
+// The same scores as scan_kernel<4, *, 1, *, false, true>, with half the LDS reads.  A
+// 256-entry table indexed by a whole pair byte returns both centroids of the byte's two
+// dims in one 8-byte read (32 copies, one per lane of a half-wave: conflict-free); the
+// products q_rot[j] * c[code] are formed in registers with q_rot[j] broadcast from the
+// lane that holds it (DPP row_newbcast, folded into v_mul_f32).  Each product is rounded
+// to fp32 on its own and added in dim order: the reference's arithmetic, as with the
+// per-dim table (csrc/core/turboquant_core.cpp:440-446, 455-483).  A lookup of a wave64
+// 4-byte read costs about as much LDS time as an 8-byte one, so the per-dim table's 128
+// reads per row bounded the scan near the HBM time; here it is 64.
+constexpr int kPsThreads = 768;                 // two blocks per CU (the table is 64 KB)
+constexpr int kPsWaves = kPsThreads / 64;
+constexpr int kPsBlocksPerScan = 3;             // kThreads-sized scan blocks per pair block
+constexpr int kCtabBytes = 256 * 256;           // byte value x 32 copies x (c_hi, c_lo)
+
+// q_rot[j] (row j of this block's broadcast set) from lane (j & 15) of each 16-lane row.
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + N, 0xF, 0xF, false));
+}
+
+// acc += q_rot[2P] * c[hi(P)], then acc += q_rot[2P+1] * c[lo(P)] for pair byte P.
+template <int P, int NQ>
+__device__ __forceinline__ void pair_byte(float& acc, const uint32_t* wds, uint32_t copy8,
+                                          const char* ctab, const float (&qv)[NQ]) {
+#pragma clang fp contract(off)
+  // address = byte << 8 | copy offset: v_perm picks the byte into bits 8-15
+  const uint32_t addr = __builtin_amdgcn_perm(wds[P >> 2], copy8, 0x0c0c0000u | ((4u + (P & 3)) << 8));
+  const float2 cc = *reinterpret_cast<const float2*>(ctab + addr);
+  const float p0 = row_bcast<(2 * P) & 15>(qv[(2 * P) >> 4]) * cc.x;
+  acc = acc + p0;
+  const float p1 = row_bcast<(2 * P + 1) & 15>(qv[(2 * P) >> 4]) * cc.y;
+  acc = acc + p1;
+}
+
+// Bytes [G0, G0 + kPairGroup) of a row; a schedule barrier after each group keeps the
+// compiler from issuing every table read of the row ahead of the adds (each holds two
+// registers until its adds).
+constexpr int kPairGroup = 16;
+template <int G0, int NQ, int... Ps>
+__device__ __forceinline__ void pair_group(float& acc, const uint32_t* wds, uint32_t copy8,
+                                           const char* ctab, const float (&qv)[NQ],
+                                           std::integer_sequence<int, Ps...>) {
+  (pair_byte<G0 + Ps, NQ>(acc, wds, copy8, ctab, qv), ...);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NQ, int... Gs>
+__device__ __forceinline__ float pair_row(const uint32_t* wds, uint32_t copy8, const char* ctab,
+                                          const float (&qv)[NQ], std::integer_sequence<int, Gs...>) {
+  float acc = 0.f;
+  (pair_group<Gs * kPairGroup, NQ>(acc, wds, copy8, ctab, qv,
+                                   std::make_integer_sequence<int, kPairGroup>{}), ...);
+  return acc;
+}
+
+// Bitonic sort of one (score, id) per lane over the 64 lanes, best first (score desc, id
+// asc).  Pads are (-inf, INT_MAX): every entry is better than a pad.
+__device__ __forceinline__ void wave_sort64(float& s, int& id) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const float ps = __shfl_xor(s, stride);
+      const int pid = __shfl_xor(id, stride);
+      // within a best-first run the lower lane keeps the better entry; runs alternate
+      const bool keep_better = ((lane & stride) == 0) == ((lane & size) == 0 || size == 64);
+      if (keep_better == better(ps, pid, s, id)) { s = ps; id = pid; }
+    }
+  }
+}
+
+// Bitonic sort of 128 entries, element e = lane + 64 r in register r, best first.
+__device__ __forceinline__ void wave_sort128(float (&s)[2], int (&id)[2]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 128; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride == 64) {  // partner in this lane's other register; one best-first run
+        if (better(s[1], id[1], s[0], id[0])) {
+          const float ts = s[0]; s[0] = s[1]; s[1] = ts;
+          const int ti = id[0]; id[0] = id[1]; id[1] = ti;
+        }
+        continue;
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = lane + 64 * r;
+        const float ps = __shfl_xor(s[r], stride);
+        const int pid = __shfl_xor(id[r], stride);
+        const bool keep_better = ((e & stride) == 0) == ((e & size) == 0 || size == 128);
+        if (keep_better == better(ps, pid, s[r], id[r])) { s[r] = ps; id[r] = pid; }
+      }
+    }
+  }
+}
+
+// Reduce a wave's candidate list (count <= 128 entries) to its best min(count, k) in
+// sorted order; th/thi become the k-th best once there are k.  Wave-uniform arguments.
+__device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count, int k, float& th,
+                                                  int& thi) {
+  const int lane = threadIdx.x & 63;
+  float s[2];
+  int id[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int e = lane + 64 * r;
+    s[r] = e < count ? cs[e] : -INFINITY;
+    id[r] = e < count ? ci[e] : INT_MAX;
+  }
+  if (count <= 64) wave_sort64(s[0], id[0]);  // uniform
+  else wave_sort128(s, id);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (lane < k && lane < count) { cs[lane] = s[0]; ci[lane] = id[0]; }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  count = count < k ? count : k;
+  if (count == k) {
+    th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s[0]), k - 1));
+    thi = __builtin_amdgcn_readlane(id[0], k - 1);
+  }
+}
+
+template <int D, bool TOPK>
+__global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
+#pragma clang fp contract(off)
+  static_assert(D == 64 || D == 128, "pair scan dims");
+  constexpr int RB = D / 2;   // bytes per row
+  constexpr int NW = RB / 4;  // 32-bit words per row
+  constexpr int NQ = D / 16;  // q_rot registers
+  static_assert(RB % kPairGroup == 0, "whole byte groups per row");
+  __shared__ __attribute__((aligned(16))) char ctab[kCtabBytes];
+  __shared__ float qs_s[D];
+  __shared__ float qr_s[D];
+  __shared__ float cen_s[16];
+  __shared__ float cand_s[TOPK ? kPsWaves * kCandCap : 1];
+  __shared__ int cand_i[TOPK ? kPsWaves * kCandCap : 1];
+  __shared__ int cnt_s[TOPK ? kPsWaves : 1];
+  __shared__ float bnd_s;
+  __shared__ int bnd_i;
+
+  const int s = blockIdx.z;
+  const int q0 = s * a.qps + blockIdx.y;  // this block's query
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+
+  // ---- query rotation (build_tables' arithmetic) and the centroid-pair table
+  if (tid < D) qs_s[tid] = load_as_f32(a.q, (int64_t)q0 * D + tid, a.q_dt);
+  else if (tid < D + 16) cen_s[tid - D] = a.cen[tid - D];
+  __syncthreads();
+  if (tid < D) {
+    const float* r = a.rot + (size_t)tid * D;
+    float v = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < D; k += 4) {
+      const float4 r4 = *reinterpret_cast<const float4*>(r + k);
+      v = v + qs_s[k] * r4.x;
+      v = v + qs_s[k + 1] * r4.y;
+      v = v + qs_s[k + 2] * r4.z;
+      v = v + qs_s[k + 3] * r4.w;
+    }
+    qr_s[tid] = v;
+  }
+  for (int e = tid; e < 256 * 16; e += kPsThreads) {  // entry b, copies 2c and 2c + 1
+    const int b = e >> 4, c = e & 15;
+    const float hi = cen_s[b >> 4], lo = cen_s[b & 15];
+    *reinterpret_cast<float4*>(ctab + b * 256 + c * 16) = make_float4(hi, lo, hi, lo);
+  }
+  __syncthreads();
+  float qv[NQ];
+#pragma unroll
+  for (int m = 0; m < NQ; ++m) qv[m] = qr_s[16 * m + (lane & 15)];
+  const uint32_t copy8 = (uint32_t)(lane & 31) * 8;
+
+  int64_t nrows = a.nrows;
+  if (a.seq_lens) {
+    const int64_t sl = a.seq_lens[s / a.spb];
+    nrows = sl < a.stream_rows ? sl : a.stream_rows;
+  }
+  const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
+  const int64_t rbeg = (int64_t)blockIdx.x * per_block;
+  const int64_t rend = min(nrows, rbeg + per_block);
+  const uint8_t* base = a.packed + (size_t)s * a.stream_rows * RB;
+  const float* nbase = a.norms + (size_t)s * a.stream_rows;
+
+  float th = -INFINITY;
+  int thi = INT_MAX;
+  int cnt = 0;
+  float* cs = cand_s + wave * kCandCap;
+  int* ci = cand_i + wave * kCandCap;
+
+  struct RowBuf {
+    uint32_t w[NW];
+    float n;
+  };
+  const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
+  const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * RB, nbr * (uint32_t)RB);
+  const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
+  auto load_row = [&](int64_t r, RowBuf& b) {
+    const uint32_t rr = (uint32_t)(r - rbeg);
+    const int off = (int)(rr * (uint32_t)RB);
+#pragma unroll
+    for (int i = 0; i < RB / 16; ++i) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows_rs, off, 16 * i, 0);
+      b.w[4 * i + 0] = v.x; b.w[4 * i + 1] = v.y; b.w[4 * i + 2] = v.z; b.w[4 * i + 3] = v.w;
+    }
+    b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
+  };
+
+  auto score = [&](const RowBuf& rb) {
+    // The broadcasts of qv are loop-invariant: hoisted, each would hold a register of its
+    // own (128 for d = 128).  Redefining qv here keeps them inside the multiplies.
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) asm volatile("" : "+v"(qv[m]));
+    const float acc = pair_row<NQ>(rb.w, copy8, ctab, qv, std::make_integer_sequence<int, RB / kPairGroup>{});
+    float sc = acc * rb.n * a.post_scale;
+    // materialized here: sunk into a branch that uses it, the products would be split
+    // from their broadcasts (a DPP move cannot move into divergent code)
+    asm volatile("" : "+v"(sc));
+    return sc;
+  };
+  // Steps after the first: list the rows that beat the bound (th, thi).
+  auto step = [&](const RowBuf& rb, const int64_t row) {
+    const float sc = score(rb);
+    const bool valid = row < rend;
+    if constexpr (TOPK) {
+      const int id = (int)row;
+      bool pred = valid && better(sc, id, th, thi);
+      uint64_t mask = __ballot(pred);
+      int nnew = __popcll(mask);
+      if (nnew == 0) return;
+      if (cnt + nnew > kCandCap) {
+        const float bs = th;
+        const int bi = thi;
+        wave_compact_sort(cs, ci, cnt, a.k, th, thi);
+        if (better(bs, bi, th, thi)) { th = bs; thi = bi; }  // keep the block bound
+        pred = valid && better(sc, id, th, thi);
+        mask = __ballot(pred);
+        nnew = __popcll(mask);
+      }
+      if (pred) {
+        const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        cs[pos] = sc;
+        ci[pos] = id;
+      }
+      cnt += nnew;
+    } else {
+      if (valid) a.scores[(size_t)q0 * a.stream_rows + row] = sc;
+    }
+  };
+
+  constexpr int64_t kStride = kPsWaves * 64;
+  const int64_t first = rbeg + wave * 64;
+  int64_t row = first + lane;
+  const int nsteps = __builtin_amdgcn_readfirstlane(
+      first < rend ? (int)((rend - first + kStride - 1) / kStride) : 0);
+  RowBuf ta, tb;
+  if (nsteps > 0) load_row(row, ta);
+  if (nsteps > 1) load_row(row + kStride, tb);
+  // ---- step 0 of every wave (waves without rows take part with nothing valid)
+  {
+    const float sc = nsteps > 0 ? score(ta) : 0.f;
+    const bool valid = nsteps > 0 && row < rend;
+    if constexpr (TOPK) {
+      // Keep the best k of the wave's first 64 rows (a sort across the lanes).  NaN
+      // scores are never listed: no comparison with a bound holds for them.
+      const bool real = valid && !__builtin_isnan(sc);
+      float ss = real ? sc : -INFINITY;
+      int ii = real ? (int)row : INT_MAX;
+      wave_sort64(ss, ii);
+      const int nreal = __popcll(__ballot(real));
+      if (lane < a.k && lane < nreal) { cs[lane] = ss; ci[lane] = ii; }
+      cnt = nreal < a.k ? nreal : a.k;
+      if (cnt == a.k) {
+        th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), a.k - 1));
+        thi = __builtin_amdgcn_readlane(ii, a.k - 1);
+      }
+      if (lane == 0) cnt_s[wave] = cnt;
+      __syncthreads();
+      // Block bound: the k-th best of the waves' first-step lists (up to 10 entries from
+      // each, sorted) bounds the block's answer from below, so every wave lists only rows
+      // that beat it: about 20 more per wave instead of a refill of its list.
+      constexpr int kTake = 128 / kPsWaves;
+      if (wave == 0) {
+        float sv[2];
+        int iv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int e = lane + 64 * r;
+          const int w = e / kTake, j = e - w * kTake;
+          const bool ok = w < kPsWaves && j < cnt_s[w < kPsWaves ? w : 0];
+          sv[r] = ok ? cand_s[w * kCandCap + j] : -INFINITY;
+          iv[r] = ok ? cand_i[w * kCandCap + j] : INT_MAX;
+        }
+        wave_sort128(sv, iv);
+        const float bs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0]), a.k - 1));
+        const int bi = __builtin_amdgcn_readlane(iv[0], a.k - 1);
+        if (lane == 0) { bnd_s = bs; bnd_i = bi; }  // (-inf, INT_MAX): fewer than k rows
+      }
+      __syncthreads();
+      const float bs = bnd_s;
+      const int bi = bnd_i;
+      if (bi != INT_MAX && better(bs, bi, th, thi)) { th = bs; thi = bi; }
+    } else {
+      if (valid) a.scores[(size_t)q0 * a.stream_rows + row] = sc;
+    }
+  }
+  row += kStride;
+  // tb holds step 1's rows
+  for (int it = 1; it < nsteps; it += 2) {
+    load_row(row + kStride, ta);
+    step(tb, row);
+    row += kStride;
+    if (it + 1 >= nsteps) break;
+    load_row(row + kStride, tb);
+    step(ta, row);
+    row += kStride;
+  }
+
+  if constexpr (TOPK) {
+    if (cnt > a.k) wave_compact_sort(cs, ci, cnt, a.k, th, thi);
+    if (lane == 0) cnt_s[wave] = cnt;
+    __syncthreads();
+    // wave 0: the block's best k of the wave lists (<= k entries each)
+    if (wave == 0) {
+      int total = 0;
+      int off[kPsWaves];
+#pragma unroll
+      for (int w = 0; w < kPsWaves; ++w) { off[w] = total; total += cnt_s[w]; }
+      auto fetch = [&](int e, float& sc, int& id) {
+        int w = 0;
+#pragma unroll
+        for (int t = 1; t < kPsWaves; ++t) w += (e >= off[t]);
+        const int slot = e - off[w];
+        sc = cand_s[w * kCandCap + slot];
+        id = cand_i[w * kCandCap + slot];
+      };
+      float* ps = a.part_s + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
+      int32_t* pi = a.part_i + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
+      if (total <= 128) {
+        float sv[2];
+        int iv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int e = lane + 64 * r;
+          if (e < total) fetch(e, sv[r], iv[r]);
+          else { sv[r] = -INFINITY; iv[r] = INT_MAX; }
+        }
+        wave_sort128(sv, iv);
+        if (lane < a.k) {
+          ps[lane] = lane < total ? sv[0] : -INFINITY;
+          pi[lane] = lane < total ? iv[0] : -1;
+        }
+      } else {  // k > 10: rank every entry of the union
+        for (int e = lane; e < total; e += 64) {
+          float se; int ie;
+          fetch(e, se, ie);
+          int rank = 0;
+          for (int f = 0; f < total; ++f) {
+            float sf; int jf;
+            fetch(f, sf, jf);
+            rank += better(sf, jf, se, ie);
+          }
+          if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ merge
 constexpr int kMergeCap = 512;       // survivors kept for the rank sort (more: exact fallback)
 constexpr int kMaxBlocksPerLane = 8;  // merge handles up to 64 * 4 * 8 = 2048 block lists
@@ -918,14 +1293,32 @@ int launch_scan_pairs(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
                  : launch_scan_t<4, 8, 1, TOPK, false, true>(a, grid, st);
 }
 
+// Row blocks of a pair-layout one-query scan: pair_scan_kernel's blocks are three
+// scan_kernel blocks in size (the same waves in all).
+int pair_scan_blocks(int64_t nrows) {
+  const int b = (scan_blocks(nrows) + kPsBlocksPerScan - 1) / kPsBlocksPerScan;
+  return b < 1 ? 1 : b;
+}
+
+template <bool TOPK>
+int launch_pair_scan(const ScanArgs& a, dim3 grid, hipStream_t st) {
+  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK>), grid, dim3(kPsThreads), 0, st, a);
+  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK>), grid, dim3(kPsThreads), 0, st, a);
+  TQ_LAUNCH_CHECK("pair_scan_kernel");
+  return TQ_OK;
+}
+
+// *nblocks_out: the grid's row blocks (TOPK: the lists merge_kernel reads per query).
 int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st,
-                bool pairs = false) {
+                bool pairs = false, int* nblocks_out = nullptr) {
   const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
   int qb = queries_per_block(a);
   if (!aligned && qb > 2) qb = 2;
   const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
-  dim3 grid(topk ? (unsigned)scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
+  const bool pair1 = pairs && qb == 1;
+  dim3 grid(pair1 ? (unsigned)pair_scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
             (unsigned)((a.qps + qb - 1) / qb), (unsigned)nstreams);
+  if (nblocks_out) *nblocks_out = (int)grid.x;
   // The fast loaders address a block's rows with 32-bit buffer offsets.
   const int64_t per_block = ((rows_hint + grid.x - 1) / grid.x + 63) / 64 * 64;
   if (per_block * (int64_t)(bits * a.bpp) >= ((int64_t)1 << 32))
@@ -933,6 +1326,7 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   if (pairs) {
     if (bits != 4 || !aligned || (a.bpp != 8 && a.bpp != 16))
       return fail(TQ_EINVAL, "pair-layout scan needs 4-bit codes, dim 64 or 128 and a 16-byte aligned base");
+    if (pair1) return topk ? launch_pair_scan<true>(a, grid, st) : launch_pair_scan<false>(a, grid, st);
     return topk ? launch_scan_pairs<true>(a, qb, grid, st) : launch_scan_pairs<false>(a, qb, grid, st);
   }
   switch (bits) {
@@ -983,9 +1377,10 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace) + 256;
-  const int nb = scan_blocks(N);
+  // The lists are laid out for scan_blocks(N) blocks; a launch uses at most that many.
+  const int nb_max = scan_blocks(N);
   float* ps = reinterpret_cast<float*>(ws);
-  ws += align_up((size_t)nq * nb * k * 4, 256);
+  ws += align_up((size_t)nq * nb_max * k * 4, 256);
   int32_t* pi = reinterpret_cast<int32_t*>(ws);
   ScanArgs a{};
   a.packed = packed; a.norms = norms; a.stream_rows = N; a.nrows = N; a.seq_lens = nullptr; a.spb = 1;
@@ -994,7 +1389,8 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.part_s = ps; a.part_i = pi; a.scores = nullptr;
   a.out_s = out_scores; a.out_i = out_ids;
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  const int rc = launch_scan(a, bit_width, true, 1, st, pairs);
+  int nb = 0;
+  const int rc = launch_scan(a, bit_width, true, 1, st, pairs, &nb);
   if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
                      out_scores, out_ids);
