@@ -161,8 +161,10 @@ __device__ __forceinline__ void decode_group(const uint32_t (&A)[4], F&& f, G&& 
   }
 }
 
+// Written with bitwise operators: short-circuit forms compile to exec-mask branches,
+// which cost about a hundred cycles per comparison in the single-block merges.
 __device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
-  return sa > sb || (sa == sb && ia < ib);
+  return (sa > sb) | ((sa == sb) & (ia < ib));
 }
 
 // Reduce a wave's candidate list (cs/ci, `count` entries, count <= 128) to its best
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         if (QB > 1 && qi >= nq) break;  // a one-query block always has its query
         const float sc = acc[qi] * nrm * a.post_scale;
         const int id = (int)row;
-        bool pred = valid && better(sc, id, th[qi], thi[qi]);
+        bool pred = valid & better(sc, id, th[qi], thi[qi]);
         uint64_t mask = __ballot(pred);
         int nnew = __popcll(mask);
         if (nnew == 0) continue;
@@ -419,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         int* ci = my_ci + qi * kCandCap;
         if (cnt[qi] + nnew > kCandCap) {
           wave_compact(cs, ci, cnt[qi], a.k, th[qi], thi[qi]);
-          pred = valid && better(sc, id, th[qi], thi[qi]);
+          pred = valid & better(sc, id, th[qi], thi[qi]);
           mask = __ballot(pred);
           nnew = __popcll(mask);
         }
@@ -738,7 +740,7 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
     const bool valid = row < rend;
     if constexpr (TOPK) {
       const int id = (int)row;
-      bool pred = valid && better(sc, id, th, thi);
+      bool pred = valid & better(sc, id, th, thi);
       uint64_t mask = __ballot(pred);
       int nnew = __popcll(mask);
       if (nnew == 0) return;
@@ -747,7 +749,7 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
         const int bi = thi;
         wave_compact_sort(cs, ci, cnt, a.k, th, thi);
         if (better(bs, bi, th, thi)) { th = bs; thi = bi; }  // keep the block bound
-        pred = valid && better(sc, id, th, thi);
+        pred = valid & better(sc, id, th, thi);
         mask = __ballot(pred);
         nnew = __popcll(mask);
       }
@@ -895,7 +897,9 @@ __device__ __forceinline__ void best_step(float& s, int& id) {
   const int so_bits = __builtin_amdgcn_update_dpp(__float_as_int(s), __float_as_int(s), CTRL, ROWS, 0xF, false);
   const int io = __builtin_amdgcn_update_dpp(id, id, CTRL, ROWS, 0xF, false);
   const float so = __int_as_float(so_bits);
-  if (io != INT_MAX && (id == INT_MAX || better(so, io, s, id))) { s = so; id = io; }
+  const bool take = (io != INT_MAX) & ((id == INT_MAX) | better(so, io, s, id));
+  s = take ? so : s;
+  id = take ? io : id;
 }
 
 __device__ __forceinline__ void wave_best(float& s, int& id) {
@@ -949,8 +953,11 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
   float bs = -INFINITY;
   int bi = INT_MAX;
 #pragma unroll
-  for (int t = 0; t < kMaxBlocksPerLane; ++t)
-    if (mi[t] != INT_MAX && (bi == INT_MAX || better(ms[t], mi[t], bs, bi))) { bs = ms[t]; bi = mi[t]; }
+  for (int t = 0; t < kMaxBlocksPerLane; ++t) {
+    const bool take = (mi[t] != INT_MAX) & ((bi == INT_MAX) | better(ms[t], mi[t], bs, bi));
+    bs = take ? ms[t] : bs;
+    bi = take ? mi[t] : bi;
+  }
   best_step<0xB1, 0xF>(bs, bi);  // quad_perm [1,0,3,2]
   best_step<0x4E, 0xF>(bs, bi);  // quad_perm [2,3,0,1]
   if ((lane & 3) == 0) { gs[threadIdx.x >> 2] = bs; gi[threadIdx.x >> 2] = bi; }
@@ -1035,7 +1042,7 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
     cs = bs_s[0];
     ci = bi_s[0];
     for (int w = 1; w < kWaves; ++w)
-      if (bi_s[w] != INT_MAX && (ci == INT_MAX || better(bs_s[w], bi_s[w], cs, ci))) { cs = bs_s[w]; ci = bi_s[w]; }
+      if ((bi_s[w] != INT_MAX) & ((ci == INT_MAX) | better(bs_s[w], bi_s[w], cs, ci))) { cs = bs_s[w]; ci = bi_s[w]; }
     __syncthreads();
     last_s = cs;
     last_i = ci;
@@ -1046,12 +1053,101 @@ __device__ void merge_query(const float* __restrict__ part_s, const int32_t* __r
   }
 }
 
+// merge_query for at most kThreads * kMergeRegs list entries: every entry is loaded
+// once, in one round of coalesced loads, and stays in registers -- tau (as in
+// merge_query, from 64 group maxima, a group being the entries of 4 adjacent threads) and
+// the survivors come from there without a second round trip to memory.
+constexpr int kMergeRegs = 24;
+__device__ void merge_query_regs(const float* __restrict__ part_s, const int32_t* __restrict__ part_i,
+                                 int nblocks, int k, int q, float* __restrict__ out_s,
+                                 int64_t* __restrict__ out_i) {
+  __shared__ __attribute__((aligned(16))) float gs[64];
+  __shared__ __attribute__((aligned(16))) int gi[64];
+  __shared__ float ss[kMergeCap];
+  __shared__ int si[kMergeCap];
+  __shared__ int nsurv;
+  __shared__ float tau_s;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int total = nblocks * k;
+  const float* ps = part_s + (size_t)q * total;
+  const int32_t* pi = part_i + (size_t)q * total;
+  float es[kMergeRegs];
+  int ei[kMergeRegs];
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) {
+    const int e = threadIdx.x + r * kThreads;
+    const int ec = e < total ? e : total - 1;
+    const float sc = ps[ec];
+    const int id = pi[ec];
+    const bool ok = (e < total) & (id >= 0);
+    es[r] = ok ? sc : -INFINITY;
+    ei[r] = ok ? id : INT_MAX;
+  }
+  float bs = -INFINITY;
+  int bi = INT_MAX;
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) {
+    const bool take = (ei[r] != INT_MAX) & ((bi == INT_MAX) | better(es[r], ei[r], bs, bi));
+    bs = take ? es[r] : bs;
+    bi = take ? ei[r] : bi;
+  }
+  best_step<0xB1, 0xF>(bs, bi);  // quad_perm [1,0,3,2]
+  best_step<0x4E, 0xF>(bs, bi);  // quad_perm [2,3,0,1]
+  if ((lane & 3) == 0) { gs[threadIdx.x >> 2] = bs; gi[threadIdx.x >> 2] = bi; }
+  if (threadIdx.x == 0) { nsurv = 0; tau_s = -INFINITY; }
+  __syncthreads();
+  if (wave == 0) {
+    const float s0 = gs[lane];
+    const int i0 = gi[lane];
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < 64; j += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(gs + j);
+      const int4 i4 = *reinterpret_cast<const int4*>(gi + j);
+      rank += (i4.x != INT_MAX) & better(s4.x, i4.x, s0, i0);
+      rank += (i4.y != INT_MAX) & better(s4.y, i4.y, s0, i0);
+      rank += (i4.z != INT_MAX) & better(s4.z, i4.z, s0, i0);
+      rank += (i4.w != INT_MAX) & better(s4.w, i4.w, s0, i0);
+    }
+    if ((i0 != INT_MAX) & (rank == k - 1)) tau_s = s0;
+  }
+  __syncthreads();
+  const float tau = tau_s;
+#pragma unroll
+  for (int r = 0; r < kMergeRegs; ++r) {
+    if (ei[r] != INT_MAX && es[r] >= tau) {
+      const int pos = atomicAdd(&nsurv, 1);
+      if (pos < kMergeCap) { ss[pos] = es[r]; si[pos] = ei[r]; }
+    }
+  }
+  __syncthreads();
+  const int m = nsurv;
+  float* os = out_s + (size_t)q * k;
+  int64_t* oi = out_i + (size_t)q * k;
+  if (m <= kMergeCap) {
+    for (int e = threadIdx.x; e < m; e += kThreads) {
+      const float se = ss[e];
+      const int ie = si[e];
+      int rank = 0;
+      for (int f = 0; f < m; ++f) rank += better(ss[f], si[f], se, ie);
+      if (rank < k) { os[rank] = se; oi[rank] = ie; }
+    }
+    for (int e = m + threadIdx.x; e < k; e += kThreads) { os[e] = -INFINITY; oi[e] = -1; }
+    return;  // uniform
+  }
+  // more than kMergeCap rows tie at tau: the general path (its exact fallback)
+  merge_query(part_s, part_i, nblocks, k, q, out_s, out_i);
+}
+
 __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
                                                          const int32_t* __restrict__ part_i,
                                                          int nblocks, int k,
                                                          float* __restrict__ out_s,
                                                          int64_t* __restrict__ out_i) {
-  merge_query(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
+  if (nblocks * k <= kThreads * kMergeRegs)  // uniform
+    merge_query_regs(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
+  else
+    merge_query(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
 }
 
 // ------------------------------------------------------------------ softmax stats
