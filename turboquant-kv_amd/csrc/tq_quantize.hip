@@ -273,6 +273,206 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(QuantArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- MFMA quantize (fp32, d 64/128)
+// The same arithmetic as quantize_kernel for fp32 inputs, with every d x d contraction on
+// v_mfma_f32_16x16x4f32 (exact fp32 products, fp32 sums; the summation order differs
+// from the reference's like any GEMM's, which the decision band of the codes allows).
+// A workgroup of d / 16 waves stays on its CU and takes 64-row tiles in turn.
+//  * GEMMs: wave w computes output columns [16 w, 16 w + 16) of all 64 rows, so the matrix
+//    operand of each of its contractions -- rows 16 w.. of R (u R^T), columns 16 w.. of R
+//    (c[codes] R), rows 16 w.. of S (r S^T) -- is fixed: it is held in registers for the
+//    whole kernel and only the tile operand comes from LDS, one read per four MFMAs.  A
+//    k-step takes the four k = s, s+16, s+32, s+48 of a 64-wide block: with the tiles at a
+//    row stride of d + 1 (= 1 mod 64 words) those reads hit 64 distinct banks.
+//  * Row work (norms, normalization, bit-plane packing): thread t owns 16 consecutive dims
+//    of row t / (d/16), from registers; a row's partial sums meet over d/16 adjacent lanes.
+//    x / n is formed as q0 = x y, q = q0 + (x - q0 n) y with y the reciprocal of n refined
+//    by one Newton step: the correctly rounded quotient (checked against IEEE division on
+//    8e7 random pairs) at 3 operations per element instead of a full division each.
+// The next tile's rows are loaded into registers while the current one is processed.
+constexpr int kQmRows = 64;
+template <int D> constexpr int qm_threads() { return 64 * (D / 16); }
+
+// 1/b correctly rounded (b normal): hardware reciprocal plus one Newton step
+__device__ __forceinline__ float qm_recip(float b) {
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  return fmaf(fmaf(-b, y0, 1.f), y0, y0);
+}
+// a / b from y = qm_recip(b)
+__device__ __forceinline__ float qm_div(float a, float b, float y) {
+  const float q0 = a * y;
+  return fmaf(fmaf(-q0, b, a), y, q0);
+}
+// Plane p of 16 codes (bytes of w[0..3], dim order) as two bit-plane bytes, dim 8i+j at
+// bit 7-j: four codes' bits gather into a nibble with one multiply.
+__device__ __forceinline__ uint32_t qm_plane16(const uint32_t (&w)[4], int p) {
+  uint32_t nib[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) nib[i] = ((((w[i] >> p) & 0x01010101u) * 0x08040201u) >> 24) & 0xFu;
+  return (nib[0] << 4 | nib[1]) | (nib[2] << 4 | nib[3]) << 8;
+}
+
+template <bool kProd, int D, int NB>
+__global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArgs a) {
+#pragma clang fp contract(off)
+  constexpr int kQmThreads = qm_threads<D>();
+  constexpr int TPR = kQmThreads / kQmRows;      // threads per row (16 dims each)
+  constexpr int LD = D + 1;                      // LDS row stride in floats
+  constexpr int KS = D / 4;                      // k-steps per contraction
+  constexpr int RB = kQmRows / 16;               // 16-row blocks per tile
+  constexpr int BPP = D / 8;
+  static_assert(TPR * 16 == D, "16 dims per thread");
+  typedef float v4f_t __attribute__((ext_vector_type(4)));
+  __shared__ float ta[kQmRows * LD];             // u -> residual
+  __shared__ float tb[kProd ? kQmRows * LD : 1]; // u / ||u|| -> centroid values
+  __shared__ __attribute__((aligned(16))) uint8_t cs[kQmRows * D];  // codes, then signs
+  __shared__ float cen_s[16];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int col = wave * 16 + c16;         // this lane's GEMM output column
+  const int trow = tid / TPR, part = tid % TPR;  // row work: row, dims 16 part..
+  auto kof = [&](int t) { return 64 * (t >> 4) + (t & 15) + 16 * g; };
+  float bnd_r[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) bnd_r[i] = a.bnd[i];
+  if (kProd && tid < 16) cen_s[tid] = tid <= NB ? a.cen[tid] : 0.f;
+  // matrix operands: bR[t] = R[col][k_t] (u R^T), bC[t] = R[k_t][col] (c R), bS[t] = S[col][k_t]
+  float bR[KS], bC[kProd ? KS : 1], bS[kProd ? KS : 1];
+#pragma unroll
+  for (int t = 0; t < KS; ++t) {
+    bR[t] = a.rot[col * D + kof(t)];
+    if constexpr (kProd) {
+      bC[t] = a.rot[kof(t) * D + col];
+      bS[t] = a.qjl[col * D + kof(t)];
+    }
+  }
+  const float eps = 1e-10f;
+  const int64_t ntiles = (a.n + kQmRows - 1) / kQmRows;
+  const float* xin = static_cast<const float*>(a.x);
+
+  float4 xr[4];  // this thread's 16 dims of its row of the next tile
+  auto load_tile = [&](int64_t tile) {
+    const int64_t row = tile * kQmRows + trow;
+    const float4* src = reinterpret_cast<const float4*>(xin + row * D + 16 * part);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[i] = row < a.n ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  // sum over the row's TPR adjacent lanes (every lane of the row gets it)
+  auto row_sum = [&](float v) {
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+  };
+  auto row_norm = [&](const float (&v)[16]) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = fmaf(v[i], v[i], s);
+    return sqrtf(row_sum(s));
+  };
+  // acc[rb] = rows 16 rb.. of T (LDS tile, the k index along a row) times the register
+  // operand b: D[row][col] = sum_k T[row][k] b(k).
+  auto gemm = [&](const float* T, const float (&bm)[KS], v4f_t (&acc)[RB]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = (v4f_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const int k = kof(t);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(T[(16 * rb + c16) * LD + k], bm[t], acc[rb], 0, 0, 0);
+      if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bounds the tile reads in flight
+    }
+  };
+  // Bit planes of this thread's 16 codes in cs, stored for row r0 + trow.
+  auto pack_cs = [&](int rows, int64_t r0, int bits, uint8_t* __restrict__ out) {
+    const uint4 c = *reinterpret_cast<const uint4*>(&cs[trow * D + 16 * part]);
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    if (trow < rows) {
+      uint8_t* dst = out + (r0 + trow) * (int64_t)(bits * BPP) + 2 * part;
+      for (int p = 0; p < bits; ++p)
+        *reinterpret_cast<uint16_t*>(dst + p * BPP) = (uint16_t)qm_plane16(w, p);
+    }
+  };
+
+  if (blockIdx.x < ntiles) load_tile(blockIdx.x);
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r0 = tile * kQmRows;
+    const int rows = (int)min<int64_t>(kQmRows, a.n - r0);
+    float u[16];
+    {
+      float x[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { x[4 * i] = xr[i].x; x[4 * i + 1] = xr[i].y; x[4 * i + 2] = xr[i].z; x[4 * i + 3] = xr[i].w; }
+      if (tile + gridDim.x < ntiles) load_tile(tile + gridDim.x);
+      const float n = row_norm(x);
+      if (part == 0 && trow < rows) a.norms[r0 + trow] = n;
+      const float den = fmaxf(n, eps), y = qm_recip(den);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) u[i] = qm_div(x[i], den, y);  // u = x / max(n, eps)
+    }
+    __syncthreads();  // the previous tile is fully consumed
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ta[trow * LD + 16 * part + i] = u[i];
+    if constexpr (kProd) {
+      // quantize_mse normalizes its (already unit) input again
+      const float den = fmaxf(row_norm(u), eps), y = qm_recip(den);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tb[trow * LD + 16 * part + i] = qm_div(u[i], den, y);
+    }
+    __syncthreads();
+    // ---- y = u R^T, codes = #{bnd < y}
+    v4f_t acc[RB];
+    gemm(kProd ? tb : ta, bR, acc);
+    if (kProd) __syncthreads();  // every wave is done reading tb before it takes c[codes]
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rb + 4 * g + r;
+        const float yv = acc[rb][r];
+        int code = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) code += (bnd_r[i] < yv) ? 1 : 0;
+        cs[row * D + col] = (uint8_t)code;
+        if (kProd) tb[row * LD + col] = cen_s[code];
+      }
+    }
+    __syncthreads();
+    pack_cs(rows, r0, a.bits, a.packed);
+    if constexpr (kProd) {
+      // ---- residual = u - c[codes] R (ta, u, is no operand of this product: each lane
+      // rewrites its own elements)
+      gemm(tb, bC, acc);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * rb + 4 * g + r;
+          ta[row * LD + col] = ta[row * LD + col] - acc[rb][r];
+        }
+      }
+      __syncthreads();  // residual complete; the code pack is done with cs
+      {
+        float rv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rv[i] = ta[trow * LD + 16 * part + i];
+        const float gam = row_norm(rv);
+        if (part == 0 && trow < rows) a.res_norms[r0 + trow] = gam;
+      }
+      // ---- signs of residual S^T
+      gemm(ta, bS, acc);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cs[(16 * rb + 4 * g + r) * D + col] = acc[rb][r] >= 0.f ? 1 : 0;
+      }
+      __syncthreads();
+      pack_cs(rows, r0, 1, a.signs);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- pack / unpack
 __global__ void pack_kernel(const uint8_t* __restrict__ codes, int64_t n, int d, int bits,
                             uint8_t* __restrict__ packed) {
@@ -393,6 +593,37 @@ int grid_for_tiles(int64_t n) {
   return (int)(tiles < cap ? tiles : cap);
 }
 
+// The MFMA quantize kernel covers fp32 inputs kept in fp32, d = 64 or 128, 16-byte
+// aligned rows; its workgroups stay on their CUs (at most one per tile).
+bool use_mfma_quantize(const void* x, tq_dtype in_dt, tq_dtype rdt, int d) {
+  return in_dt == TQ_F32 && rdt == TQ_F32 && (d == 64 || d == 128) &&
+         (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+template <bool kProd>
+void launch_quantize_mfma(const QuantArgs& a, hipStream_t st) {
+  const int64_t tiles = (a.n + kQmRows - 1) / kQmRows;
+  // workgroups per CU that the registers (matrix operands held per wave) allow
+  const int per_cu = a.d == 128 ? (kProd ? 1 : 2) : (kProd ? 2 : 4);
+  const int64_t cap = (int64_t)device_cu_count() * per_cu;
+  const dim3 grid((unsigned)(tiles < cap ? tiles : cap));
+  if (a.d == 128) {
+    switch (a.bits) {
+      case 1: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 1>), grid, dim3(qm_threads<128>()), 0, st, a); break;
+      case 2: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 3>), grid, dim3(qm_threads<128>()), 0, st, a); break;
+      case 3: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 7>), grid, dim3(qm_threads<128>()), 0, st, a); break;
+      default: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 15>), grid, dim3(qm_threads<128>()), 0, st, a); break;
+    }
+  } else {
+    switch (a.bits) {
+      case 1: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 64, 1>), grid, dim3(qm_threads<64>()), 0, st, a); break;
+      case 2: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 64, 3>), grid, dim3(qm_threads<64>()), 0, st, a); break;
+      case 3: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 64, 7>), grid, dim3(qm_threads<64>()), 0, st, a); break;
+      default: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 64, 15>), grid, dim3(qm_threads<64>()), 0, st, a); break;
+    }
+  }
+}
+
 int grid_for_elems(int64_t total, int threads) {
   const int64_t blocks = (total + threads - 1) / threads;
   const int64_t cap = (int64_t)device_cu_count() * 16;
@@ -421,6 +652,11 @@ int tq_rotate_and_quantize(const void* vectors, tq_dtype in_dtype, tq_dtype roun
   TQ_REQUIRE(vectors && rotation && boundaries && packed && norms, "null pointer argument");
   QuantArgs a{vectors, in_dtype, round_dtype, n, d, rotation, boundaries, nullptr, nullptr,
               bit_width, packed, nullptr, nullptr, norms};
+  if (use_mfma_quantize(vectors, in_dtype, round_dtype, d)) {
+    launch_quantize_mfma<false>(a, as_stream(stream));
+    TQ_LAUNCH_CHECK("quantize_mfma_kernel<mse>");
+    return TQ_OK;
+  }
   hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
                      as_stream(stream), a);
   TQ_LAUNCH_CHECK("quantize_kernel<mse>");
@@ -443,6 +679,11 @@ int tq_quantize_prod(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtyp
              "null pointer argument");
   QuantArgs a{vectors, in_dtype, round_dtype, n, d, rotation, boundaries, centroids, qjl,
               bit_width - 1, mse_packed, signs, res_norms, norms};
+  if (use_mfma_quantize(vectors, in_dtype, round_dtype, d)) {
+    launch_quantize_mfma<true>(a, as_stream(stream));
+    TQ_LAUNCH_CHECK("quantize_mfma_kernel<prod>");
+    return TQ_OK;
+  }
   hipLaunchKernelGGL(quantize_kernel<true>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
                      as_stream(stream), a);
   TQ_LAUNCH_CHECK("quantize_kernel<prod>");
