@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "turboquant-kv_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (vector or MFMA)
 METRIC = "packed-KV decode-attn GB/s (% HBM peak); 10M×d128 4-bit IP scan queries/s"
 PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms
 # HBM bytes per launch of pair_scan_kernel<128,true> on the headline workload, from
@@ -230,13 +231,19 @@ def bench_quantize(args, extra):
         R = make_rotation_matrix(d, 42).cuda()
         S = make_qjl_matrix(d, d, 42).cuda()
         bnd, cen = [t.cuda() for t in lloyd_max_codebook(3, d)]
-        ms = time_op(lambda: ops.quantize_prod_packed(x, R, bnd, cen, S, 4), 5, 1)
+        ms = time_op(lambda: ops.quantize_prod_packed(x, R, bnd, cen, S, 4), 20, 5)
         bpp = (d + 7) // 8
         byts = n * (d * 4 + 3 * bpp + bpp + 8)
-        flops = n * 6.0 * d * d
-        extra[f"quantize_{name}"] = {"ms": ms, "vectors_per_s": n / ms * 1e3, "GBps": byts / ms / 1e6,
-                                     "TFLOPs": flops / ms / 1e9}
-        log(f"quantize {name}: {ms:.2f} ms, {n / ms * 1e3 / 1e6:.2f} M vec/s")
+        flops = n * 6.0 * d * d  # three d x d contractions per vector
+        tf = flops / ms / 1e9
+        mfma = d in (64, 128)  # fp32 MFMA kernel; other dims run the fp32 VALU kernel
+        extra[f"quantize_{name}"] = {
+            "ms": ms, "vectors_per_s": n / ms * 1e3, "GBps": byts / ms / 1e6, "TFLOPs": tf,
+            "roofline": {"bound": "mfma" if mfma else "valu", "achieved": tf,
+                         "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tf / FP32_PEAK_TFLOPS},
+            "kernel": "quantize_mfma_kernel<true,128,7>" if mfma else "quantize_kernel<true>"}
+        log(f"quantize {name}: {ms:.2f} ms, {n / ms * 1e3 / 1e6:.2f} M vec/s, {tf:.1f} TFLOP/s "
+            f"({tf / FP32_PEAK_TFLOPS:.0%} of fp32 peak)")
 
 
 def cpu_baseline(db, budget_s=12.0):
@@ -277,6 +284,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline + T=32K decode only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quantize-only", action="store_true",
+                    help="only the quantize_prod cases (configs 3a/3b), e.g. for a profiler run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (counter calibration)")
     args = ap.parse_args()
@@ -298,6 +307,11 @@ def main():
 
     _lib.load()
     torch.cuda.init()
+    if args.quantize_only:
+        extra = {}
+        bench_quantize(args, extra)
+        print(json.dumps(extra))
+        return
     extra = {}
     t0 = time.perf_counter()
     scan = bench_scan(args, extra)
