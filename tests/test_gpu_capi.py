@@ -285,6 +285,41 @@ def test_quantize_prod_vs_reference(golden):
         assert np.allclose(rn[ok], pr[f"{name}_res_norms"][ok], rtol=2e-5, atol=1e-7)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_quantize_mfma_ragged_vs_oracle(d):
+    # fp32 inputs of d 64/128 run the MFMA kernel (64-row tiles): ragged row counts,
+    # every bit width of both modes, against the oracle's float64 decision margins.
+    rs = np.random.RandomState(900 + d)
+    R = O.dense_qr_rotation(d, 42)
+    S = O.qjl_matrix(d, d, 42)
+    for n in (1, 63, 65, 1000, 4099):
+        x = (rs.randn(n, d) * np.exp(rs.randn(1, d))).astype(np.float32)
+        x[n // 2] = 0.0  # a zero row
+        for b in (1, 2, 3, 4):
+            bnd, _ = O.lloyd_max_codebook(b, d)
+            packed, norms = k_quantize(T(x), R, bnd, b)
+            _, n_o, c_o = O.quantize_mse(x, b, R, bnd)
+            amb = O.code_margin(x, R, bnd)
+            codes = O.unpack_codes(packed, b, d)
+            assert not ((codes != c_o) & ~amb).any(), (d, n, b)
+            assert np.array_equal(O.pack_codes(codes, b), packed)
+            assert np.allclose(norms, n_o, rtol=5e-7, atol=0), (d, n, b)
+        for b in (2, 3, 4):
+            bnd, cen = O.lloyd_max_codebook(b - 1, d)
+            mp, sg, rn, nm = k_prod(x, R, bnd, cen, S, b)
+            mp_o, sg_o, rn_o, nm_o, c_o, proj64 = O.quantize_prod(x, b, R, bnd, cen, S)
+            u = x / np.maximum(np.linalg.norm(x.astype(np.float64), axis=1), 1e-10)[:, None]
+            amb = O.code_margin(u.astype(np.float32), R, bnd)
+            codes = O.unpack_codes(mp, b - 1, d)
+            assert not ((codes != c_o) & ~amb).any(), (d, n, b)
+            same = ~(codes != c_o).any(axis=1)
+            sign_band = np.abs(proj64) <= 2.0 ** -16 * np.max(np.abs(proj64), axis=1, keepdims=True)
+            s_k, s_o = O.unpack_codes(sg, 1, d), O.unpack_codes(sg_o, 1, d)
+            assert not ((s_k != s_o) & ~sign_band & same[:, None]).any(), (d, n, b)
+            assert np.allclose(nm, nm_o, rtol=5e-7), (d, n, b)
+            assert np.allclose(rn[same], rn_o[same], rtol=2e-5, atol=1e-7), (d, n, b)
+
+
 # ------------------------------------------------------------------ pack / unpack
 @pytest.mark.parametrize("bits", [1, 2, 3, 4, 8])
 @pytest.mark.parametrize("d", [1, 7, 64, 100, 128, 200, 256])
