@@ -13,7 +13,8 @@ the reference's bit-plane rows is reported beside it under "extra".
 Also measured in the same run and reported under "extra": the Q = 64 / 1024 batches
 and the 3- and 2-bit databases of the same config; fused GQA decode attention over a
 packed KV cache (configs[3]: B=32, Hq=32, Hkv=8, d=64, K4/V2, T = 4K/16K/32K);
-quantize throughput (configs[2]: prod 3+1 bit, N=1M d=128 and N=390k d=200).
+quantize throughput (configs[2]: prod 3+1 bit, N=1M d=128 and N=390k d=200); prod-mode
+index search over 10M x 128 rows of 3-bit codes + QJL signs.
 
 roofline: the scan op's algorithmic bytes (N*(b*16 + 4) + Q*d*2 + Q*k*12) over its
 average duration from HIP events on the launch stream; peak = 8 TB/s.
@@ -246,6 +247,60 @@ def bench_quantize(args, extra):
             f"({tf / FP32_PEAK_TFLOPS:.0%} of fp32 peak)")
 
 
+def bench_prod_scan(args, extra):
+    """Prod-mode index search (TurboQuantIndex mode="prod", bit_width 4 = 3-bit MSE codes +
+    1-bit QJL signs) over the headline's 10M x 128 shape: ip_scan_topk_prod scores the
+    packed rows (72 B each); the reference's algorithm (search.py:229-252: dequantize_prod
+    of every row, then q @ recon^T and topk) is timed beside it."""
+    import torch
+    from turboquant_kv import _lib
+    from turboquant_kv.codebook import lloyd_max_codebook, make_qjl_matrix, make_rotation_matrix
+
+    ops = _lib.ops()
+    N, d, k, b = 10_000_000, 128, 10, 4
+    g = torch.Generator(device="cuda").manual_seed(5)
+    R = make_rotation_matrix(d, 42).cuda()
+    S = make_qjl_matrix(d, d, 42).cuda()
+    bnd, cen = [t.cuda() for t in lloyd_max_codebook(b - 1, d)]
+    bpp = d // 8
+    mp = torch.empty(N, (b - 1) * bpp, dtype=torch.uint8, device="cuda")
+    sg = torch.empty(N, bpp, dtype=torch.uint8, device="cuda")
+    rn = torch.empty(N, dtype=torch.float32, device="cuda")
+    nm = torch.empty(N, dtype=torch.float32, device="cuda")
+    chunk = 2_000_000
+    for c in range(0, N, chunk):
+        m = min(chunk, N - c)
+        x = torch.randn(m, d, generator=g, device="cuda")
+        x = x / x.norm(dim=1, keepdim=True)
+        a, s_, r_, n_ = ops.quantize_prod_packed(x, R, bnd, cen, S, b)
+        mp[c:c + m], sg[c:c + m], rn[c:c + m], nm[c:c + m] = a, s_, r_, n_
+        del x, a, s_, r_, n_
+    q1 = queries(1, d, seed=4)
+    bytes_alg = N * ((b - 1) * bpp + bpp + 8) + d * 2 + k * 12
+    ms = time_op(lambda: ops.ip_scan_topk_prod(q1, mp, sg, rn, nm, cen, R, S, b, k), 30, 3)
+    gbs = bytes_alg / ms / 1e6
+    extra["scan_prod_b4_Q1"] = {
+        "us_per_query": ms * 1e3, "queries_per_s": 1e3 / ms, "GBps": gbs,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": bytes_alg},
+        "kernel": "scan_kernel<3,16,1,true,false,false,true> + merge_kernel",
+        "workload": "ip_scan_topk_prod N=10,000,000 d=128 bits=4 (3+1) Q=1 fp16 query k=10"}
+    log(f"prod scan b=4 Q=1: {ms * 1e3:.1f} us/query, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.0%})")
+    if not args.quick:
+        qf = q1.float()
+
+        def reference_algorithm():
+            recon = ops.dequantize_prod_packed(mp, sg, rn, nm, cen, R, S, b, d)
+            return torch.topk(qf @ recon.t(), k, dim=-1)
+
+        t = time_op(reference_algorithm, 3, 1)
+        extra["scan_prod_b4_Q1_dequantize_matmul"] = {
+            "ms_per_query": t, "queries_per_s": 1e3 / t,
+            "note": "the reference's prod search algorithm on this GPU (dequantize_prod kernel "
+                    "+ torch matmul + topk), for comparison"}
+        log(f"prod search by dequantize + matmul: {t:.2f} ms/query")
+
+
 def cpu_baseline(db, budget_s=12.0):
     """The reference's C++ search_packed over the same 10M-row database, one query per
     OpenMP thread, enough rounds of queries for about `budget_s` seconds."""
@@ -286,6 +341,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quantize-only", action="store_true",
                     help="only the quantize_prod cases (configs 3a/3b), e.g. for a profiler run")
+    ap.add_argument("--prod-only", action="store_true",
+                    help="only the prod-mode scan (10M x 128, 3+1 bit), e.g. for a profiler run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (counter calibration)")
     args = ap.parse_args()
@@ -312,12 +369,19 @@ def main():
         bench_quantize(args, extra)
         print(json.dumps(extra))
         return
+    if args.prod_only:
+        extra = {}
+        args.quick = True
+        bench_prod_scan(args, extra)
+        print(json.dumps(extra))
+        return
     extra = {}
     t0 = time.perf_counter()
     scan = bench_scan(args, extra)
     dec = bench_decode(args, extra)
     if not args.quick:
         bench_quantize(args, extra)
+        bench_prod_scan(args, extra)
     cpu = None if args.no_cpu else cpu_baseline(scan["db4"])
     ms, bytes_alg = scan["headline"]
     achieved = bytes_alg / ms / 1e6

@@ -169,6 +169,34 @@ int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, i
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Prod-mode scoring without reconstruction.  Replaces TurboQuantIndex._search_prod
+ * (turboquant_kv/search.py:229-252: dequantize_prod of every row, then queries @ recon^T
+ * and topk) and, for prod-mode caches, the dequantize-then-matmul of
+ * QuantizedKVCache.attention_scores (cache.py:282-310, without its 1/sqrt(d)):
+ *   score[q, i] = norms[i] * ( sum_j (R q)_j c[code_ij]
+ *                              + sqrt(pi/2)/d * res_norms[i] * sum_j (S q)_j (2 sign_ij - 1) )
+ * which is <q, dequantize_prod(row i)> (reference.py:472-533) rearranged.  Rows are
+ * what tq_quantize_prod writes: mse_packed [N, (b-1)*ceil(d/8)], signs [N, ceil(d/8)],
+ * res_norms [N], norms [N]; centroids [2^(b-1)] (the (b-1)-bit codebook), rotation R
+ * and qjl S [d, d] fp32.  2 <= bit_width <= 4 (the prod bit budget b).  fp32 sums in
+ * another order than the reference's GEMM: scores agree to fp32 rounding, not bit for
+ * bit.  Top-k: same output and tie rule as tq_ip_scan_topk.  Workspace:
+ * tq_scan_workspace_bytes(nq, d, b, N, k) / (nq, d, b, 0, 0).
+ */
+int tq_ip_scan_topk_prod(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                         const uint8_t* mse_packed, const uint8_t* signs, const float* res_norms,
+                         const float* norms, int64_t N, const float* centroids,
+                         const float* rotation, const float* qjl, int32_t bit_width, int32_t k,
+                         float* out_scores, int64_t* out_ids, void* workspace,
+                         size_t workspace_bytes, void* stream);
+int tq_attention_scores_prod(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                             const uint8_t* mse_packed, const uint8_t* signs,
+                             const float* res_norms, const float* key_norms, int64_t T,
+                             const float* centroids, const float* rotation, const float* qjl,
+                             int32_t bit_width, float* scores, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
  * Fused GQA decode attention over a packed KV cache (new op: the semantics of
  * QuantizedKVCache.attention_scores -> softmax -> attention_values,
  * turboquant_kv/cache.py:282-339 with turboquant_kv/vllm_plugin/__init__.py:400,

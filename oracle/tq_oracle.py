@@ -20,6 +20,8 @@ Floating-point behaviour is stated per function:
 * scores / search: the LUT form of csrc/core/turboquant_core.cpp:407-514 in exact
   float32 (sequential j, one rounding per add), so scores are bit-reproducible;
   float64 closed forms are given for tolerance checks.
+* prod scores / search: float64 closed form of search.py:229-252 (q @ dequantize_prod^T);
+  pinned by the reference's dequantize_prod output in quant_prod.npz.
 * decode attention: float64 closed form of cache.py:282-339 + softmax, with GQA.
 """
 
@@ -279,6 +281,14 @@ def topk_desc(scores, k):
         out_s[q, :len(order)] = scores[q, order]
         out_i[q, :len(order)] = order
     return out_s, out_i
+
+
+def prod_scores_f64(q, mse_packed, signs_packed, gamma, norms, bits, dim, R, cen, S):
+    """Prod-mode index scores in float64: queries @ dequantize_prod(rows)^T, the
+    computation of TurboQuantIndex._search_prod (search.py:229-252) without its fp32
+    roundings.  Returns float64 [Q, N]."""
+    rec = dequantize_prod(mse_packed, signs_packed, gamma, norms, bits, dim, R, cen, S)
+    return np.asarray(q, np.float64) @ rec.T
 
 
 def search_topk(q, packed, norms, cen, R, bits, k):

@@ -122,6 +122,52 @@ def test_index_top1_matches_brute_force():
     assert (top.squeeze(-1) == exact).float().mean().item() >= 0.5
 
 
+def test_prod_index_search_scores_without_reconstruction():
+    # TurboQuantIndex prod search scores the packed rows; the reference dequantizes every
+    # row and multiplies (search.py:229-252).  Both against the float64 composition.
+    from turboquant_kv import TurboQuantIndex
+    rs = np.random.RandomState(4)
+    for d, b in ((128, 4), (200, 3), (64, 2)):
+        db = rs.randn(3000, d).astype(np.float32)
+        idx = TurboQuantIndex.from_vectors(T(db), bit_width=b, mode="prod")
+        q = rs.randn(6, d).astype(np.float32)
+        rows = [t.cpu().numpy() for t in (idx._packed_codes, idx._qjl_signs,
+                                          idx._residual_norms, idx._norms)]
+        R, S = idx._rot_dev.cpu().numpy(), idx._S_dev.cpu().numpy()
+        ref = O.prod_scores_f64(q, *rows, b, d, R, idx._cen.cpu().numpy(), S)
+        tol = 1e-4 * np.linalg.norm(q, axis=1)[:, None] * rows[3][None, :] * (1 + 2 * rows[2][None, :])
+        recon = torch.ops.turboquant.dequantize_prod_packed(
+            idx._packed_codes, idx._qjl_signs, idx._residual_norms, idx._norms, idx._cen,
+            idx._rot_dev, idx._S_dev, b, d)
+        composed = (T(q) @ recon.t()).cpu().numpy()
+        assert np.all(np.abs(composed - ref) <= tol)
+        for k in (10, 50):  # scan + merge; all scores + torch.topk
+            s, i = idx.search(T(q), k=k)
+            s, i = s.cpu().numpy(), i.cpu().numpy()
+            assert np.all(np.abs(s - np.take_along_axis(ref, i, 1)) <= np.take_along_axis(tol, i, 1))
+            _, io = O.topk_desc(ref, k)
+            diff = i != io
+            a, o = np.take_along_axis(ref, i, 1), np.take_along_axis(ref, io, 1)
+            ta, to = np.take_along_axis(tol, i, 1), np.take_along_axis(tol, io, 1)
+            assert np.all(~diff | (np.abs(a - o) <= ta + to)), (d, b, k)
+
+
+def test_prod_cache_scores_without_reconstruction():
+    from turboquant_kv import QuantizedKVCache, TurboQuantConfig
+    torch.manual_seed(3)
+    B, Hq, H, d = 2, 4, 2, 128
+    kv = QuantizedKVCache(TurboQuantConfig(key_bits=4, value_bits=3, mode="prod"), 1, 300, H, d,
+                          device=DEV, batch_size=B)
+    kv.append(0, torch.randn(B, H, 130, d, device=DEV), torch.randn(B, H, 130, d, device=DEV))
+    kv.append(0, torch.randn(B, H, 7, d, device=DEV), torch.randn(B, H, 7, d, device=DEV))
+    q = torch.randn(B, Hq, 3, d, device=DEV)
+    logits = kv.attention_scores(0, q)
+    keys = kv._dequantize_keys(0).repeat_interleave(Hq // H, dim=1)   # (B, Hq, T, d)
+    ref = torch.matmul(q.double(), keys.double().transpose(-2, -1)) / math.sqrt(d)
+    scale = q.double().norm(dim=-1, keepdim=True) * keys.double().norm(dim=-1)[:, :, None, :]
+    assert ((logits.double() - ref).abs() <= 1e-4 * scale / math.sqrt(d) + 1e-6).all()
+
+
 def test_cache_vs_reference(golden):
     from turboquant_kv import QuantizedKVCache, TurboQuantConfig
     c = golden("cache")

@@ -709,3 +709,147 @@ def test_scan_many_exact_ties_take_fallback():
     so, io = O.search_topk(q, p, nm, cen, R, b, 16)
     assert np.array_equal(i, io)
     assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+# ------------------------------------------------------------------ prod-mode scoring
+def k_scan_prod(q, mp, sg, rn, nm, cen, R, S, bits, k, sg_offset_rows=0):
+    """tq_ip_scan_topk_prod; sg_offset_rows > 0 passes the sign rows at that row offset
+    of a larger buffer (a base that is not 16-byte aligned when bpp % 16 != 0)."""
+    Q, d = q.shape
+    N = mp.shape[0]
+    os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
+    oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, bits, N, k), 1), dtype=torch.uint8, device=DEV)
+    sgt = T(np.concatenate([np.zeros((sg_offset_rows, sg.shape[1]), np.uint8), sg]))[sg_offset_rows:]
+    capi.check(L().tq_ip_scan_topk_prod(capi.p(T(q)), capi.TQ_F32, capi.i64(Q), capi.i32(d),
+                                        capi.p(T(mp)), capi.p(sgt), capi.p(T(rn)), capi.p(T(nm)),
+                                        capi.i64(N), capi.p(T(cen)), capi.p(T(R)), capi.p(T(S)),
+                                        capi.i32(bits), capi.i32(k), capi.p(os_), capi.p(oi),
+                                        capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return os_.cpu().numpy(), oi.cpu().numpy()
+
+
+def k_scores_prod(q, mp, sg, rn, nm, cen, R, S, bits):
+    Q, d = q.shape
+    N = mp.shape[0]
+    out = torch.empty(Q, N, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, bits, N, 0), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_attention_scores_prod(capi.p(T(q)), capi.TQ_F32, capi.i64(Q), capi.i32(d),
+                                            capi.p(T(mp)), capi.p(T(sg)), capi.p(T(rn)),
+                                            capi.p(T(nm)), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
+                                            capi.p(T(S)), capi.i32(bits), capi.p(out), capi.p(ws),
+                                            ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.cpu().numpy()
+
+
+def _prod_db(rs, n, d, b, seed=42):
+    R, S = O.dense_qr_rotation(d, seed), O.qjl_matrix(d, d, seed + 12345)
+    bnd, cen = O.lloyd_max_codebook(b - 1, d)
+    x = (rs.randn(n, d) * rs.uniform(0.5, 2.0, (n, 1))).astype(np.float32)
+    mp, sg, g, nm, _, _ = O.quantize_prod(x, b, R, bnd, cen, S)
+    return R, S, cen, mp, sg, g, nm
+
+
+def _prod_tol(q, nm, g):
+    """fp32 against float64: every term of both sums is at most |q| * n * (1 + 2 gamma) in
+    magnitude summed over dims; 1e-4 of that is far above the d * 2^-24 rounding bound."""
+    return 1e-4 * np.linalg.norm(q, axis=1)[:, None] * nm[None, :] * (1.0 + 2.0 * g[None, :])
+
+
+def _check_prod_topk(s, i, ref, tol, k):
+    """Scores within tol of the float64 reference; ids equal the float64 top-k except
+    where a swapped pair's float64 scores lie within the tolerance of each other."""
+    so, io = O.topk_desc(ref, k)
+    for qi in range(ref.shape[0]):
+        n_valid = min(k, ref.shape[1])
+        assert np.all(i[qi, n_valid:] == -1) and np.all(np.isneginf(s[qi, n_valid:]))
+        ids = i[qi, :n_valid]
+        assert len(set(ids.tolist())) == n_valid
+        assert np.all(np.diff(s[qi, :n_valid]) <= 0)
+        assert np.all(np.abs(s[qi, :n_valid] - ref[qi, ids]) <= tol[qi, ids])
+        for r in range(n_valid):
+            if ids[r] != io[qi, r]:
+                a, bb = ids[r], io[qi, r]
+                assert abs(ref[qi, a] - ref[qi, bb]) <= tol[qi, a] + tol[qi, bb], (qi, r)
+
+
+@pytest.mark.parametrize("d", [64, 96, 128, 200])
+@pytest.mark.parametrize("b", [2, 3, 4])
+def test_prod_scan_topk_vs_f64(d, b):
+    rs = np.random.RandomState(5 * d + b)
+    R, S, cen, mp, sg, g, nm = _prod_db(rs, 12000, d, b)
+    for Q, k in ((1, 10), (4, 1), (7, 32)):
+        q = rs.randn(Q, d).astype(np.float32)
+        s, i = k_scan_prod(q, mp, sg, g, nm, cen, R, S, b, k)
+        ref = O.prod_scores_f64(q, mp, sg, g, nm, b, d, R, cen, S)
+        _check_prod_topk(s, i, ref, _prod_tol(q, nm, g), k)
+
+
+@pytest.mark.parametrize("d,b", [(64, 2), (96, 3), (128, 4), (200, 4)])
+def test_prod_attention_scores_vs_f64(d, b):
+    rs = np.random.RandomState(17 * d + b)
+    R, S, cen, mp, sg, g, nm = _prod_db(rs, 3000, d, b, seed=43)
+    for Q in (1, 3, 8):
+        q = rs.randn(Q, d).astype(np.float32)
+        got = k_scores_prod(q, mp, sg, g, nm, cen, R, S, b)
+        ref = O.prod_scores_f64(q, mp, sg, g, nm, b, d, R, cen, S)
+        assert np.all(np.abs(got - ref) <= _prod_tol(q, nm, g)), (d, b, Q)
+
+
+def test_prod_scan_reference_rows(golden):
+    # The reference's own quantize_prod outputs (fixture) as the database (the d128 set
+    # holds a zero vector at row 0).
+    pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
+    rs = np.random.RandomState(23)
+    for name, d in (("d128", 128), ("d200", 200)):
+        R, S = rot[f"R_d{d}_s42"], qj[f"S_d{d}_s42"]
+        _, cen = O.lloyd_max_codebook(3, d)
+        rows = [pr[f"{name}_{k}"] for k in ("mse_packed", "signs", "res_norms", "norms")]
+        q = rs.randn(5, d).astype(np.float32)
+        ref = O.prod_scores_f64(q, *rows, 4, d, R, cen, S)
+        tol = _prod_tol(q, rows[3], rows[2])
+        s, i = k_scan_prod(q, *rows, cen, R, S, 4, 10)
+        _check_prod_topk(s, i, ref, tol, 10)
+        got = k_scores_prod(q, *rows, cen, R, S, 4)
+        assert np.all(np.abs(got - ref) <= tol)
+        # zero rows score exactly 0
+        zero = rows[3] == 0
+        assert zero.sum() == (1 if d == 128 else 0) and np.all(got[:, zero] == 0)
+
+
+def test_prod_scan_ties_padding_and_unaligned_signs():
+    rs = np.random.RandomState(31)
+    d, b = 64, 4
+    R, S, cen, mp, sg, g, nm = _prod_db(rs, 5000, d, b)
+    q = rs.randn(3, d).astype(np.float32)
+    ref = O.prod_scores_f64(q, mp, sg, g, nm, b, d, R, cen, S)
+    top = int(np.argmax(ref[0]))
+    # 40 exact copies of the best row tie exactly: the lowest ids come first
+    idx = np.sort(rs.choice(5000, 40, replace=False))
+    for a in (mp, sg, g, nm):
+        a[idx] = a[top]
+    ref = O.prod_scores_f64(q, mp, sg, g, nm, b, d, R, cen, S)
+    s, i = k_scan_prod(q, mp, sg, g, nm, cen, R, S, b, 16)
+    tied = np.unique(np.concatenate([idx, [top]]))[:16]
+    assert np.array_equal(i[0], tied)
+    assert np.all(s[0] == s[0, 0])
+    _check_prod_topk(s, i, ref, _prod_tol(q, nm, g), 16)
+    # sign rows at an 8-byte offset (not 16-byte aligned): the generic loader, same results
+    s2, i2 = k_scan_prod(q, mp, sg, g, nm, cen, R, S, b, 16, sg_offset_rows=1)
+    assert np.array_equal(i2, i) and np.array_equal(s2.view(np.uint32), s.view(np.uint32))
+    # k above N pads with (-inf, -1)
+    s3, i3 = k_scan_prod(q, mp[:7], sg[:7], g[:7], nm[:7], cen, R, S, b, 12)
+    _check_prod_topk(s3, i3, ref[:, :7], _prod_tol(q, nm[:7], g[:7]), 12)
+    # empty key set: nothing to write
+    assert k_scores_prod(q, mp[:0], sg[:0], g[:0], nm[:0], cen, R, S, b).shape == (3, 0)
+
+
+def test_prod_scan_rejects_bad_bits():
+    q = np.zeros((1, 64), np.float32)
+    for bits in (1, 5):
+        with pytest.raises(RuntimeError, match="bit_width"):
+            k_scan_prod(q, np.zeros((4, 8 * max(bits - 1, 1)), np.uint8), np.zeros((4, 8), np.uint8),
+                        np.ones(4, np.float32), np.ones(4, np.float32), np.zeros(2, np.float32),
+                        np.eye(64, dtype=np.float32), np.eye(64, dtype=np.float32), bits, 4)

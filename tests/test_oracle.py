@@ -195,6 +195,58 @@ def test_dequantize_matches_reference(golden):
         assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
 
 
+def test_prod_scores_match_reference_reconstruction(golden):
+    # prod_scores_f64 against queries @ (the reference's own dequantize_prod output)^T
+    pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
+    rs = np.random.RandomState(5)
+    for name, d in (("d128", 128), ("d200", 200)):
+        R, S = rot[f"R_d{d}_s42"], qj[f"S_d{d}_s42"]
+        _, cen = O.lloyd_max_codebook(3, d)
+        q = rs.randn(6, d).astype(np.float32)
+        got = O.prod_scores_f64(q, pr[f"{name}_mse_packed"][:64], pr[f"{name}_signs"][:64],
+                                pr[f"{name}_res_norms"][:64], pr[f"{name}_norms"][:64], 4, d,
+                                R, cen, S)
+        ref = q.astype(np.float64) @ pr[f"{name}_deq64"].astype(np.float64).T
+        # row 0 of the fixture is the zero vector (norm 0): its scores are exactly 0
+        scale = np.linalg.norm(q, axis=1)[:, None] * pr[f"{name}_norms"][None, :64]
+        assert np.all(np.abs(got - ref) <= 1e-5 * scale)
+
+
+def _prod_fused_f64(q, mp, sg, g, n, bits, d, R, cen, S):
+    """The scan kernels' rearrangement: n * (<R q, c[codes]> + sqrt(pi/2)/d * g * <S q, +-1>)."""
+    codes = O.unpack_codes(mp, bits - 1, d)
+    sgn = 2.0 * O.unpack_codes(sg, 1, d).astype(np.float64) - 1.0
+    q64 = np.asarray(q, np.float64)
+    qr, qs = q64 @ np.asarray(R, np.float64).T, q64 @ np.asarray(S, np.float64).T
+    mse = qr @ np.asarray(cen, np.float64)[codes].T
+    corr = math.sqrt(math.pi / 2) / d * g[None, :].astype(np.float64) * (qs @ sgn.T)
+    return (mse + corr) * n[None, :].astype(np.float64)
+
+
+def test_prod_scores_rearrangement_and_special_cases(golden):
+    pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
+    d, R, S = 128, rot["R_d128_s42"], qj["S_d128_s42"]
+    _, cen = O.lloyd_max_codebook(3, d)
+    mp, sg = pr["d128_mse_packed"], pr["d128_signs"]
+    g, n = pr["d128_res_norms"], pr["d128_norms"]
+    q = np.random.RandomState(9).randn(4, d).astype(np.float32)
+    ref = O.prod_scores_f64(q, mp, sg, g, n, 4, d, R, cen, S)
+    scale = np.max(np.abs(ref))
+    # the scan kernels' form of the same score
+    assert np.max(np.abs(_prod_fused_f64(q, mp, sg, g, n, 4, d, R, cen, S) - ref)) <= 1e-12 * scale
+    # gamma = 0 leaves the (bits-1)-bit MSE score
+    z = np.zeros_like(g)
+    assert np.allclose(O.prod_scores_f64(q, mp, sg, z, n, 4, d, R, cen, S),
+                       O.scores_f64(q, mp, n, cen, R, 3), rtol=0, atol=1e-12 * scale)
+    # flipping every sign negates the residual term
+    mse = O.scores_f64(q, mp, n, cen, R, 3)
+    flip = O.prod_scores_f64(q, mp, (~sg).astype(np.uint8), g, n, 4, d, R, cen, S)
+    assert np.allclose(flip - mse, -(ref - mse), rtol=0, atol=1e-10 * scale)
+    # a transposed S in the rearrangement is caught
+    bad = _prod_fused_f64(q, mp, sg, g, n, 4, d, R, cen, S.T.copy())
+    assert np.max(np.abs(bad - ref)) > 1e-3 * scale
+
+
 def test_mse_distortion_bound():
     # mean over vectors of mean_j (x - x_hat)^2 < 2 * sqrt(3 pi)/2 * 4^-b
     # (reference tests/test_reference.py:74-100)

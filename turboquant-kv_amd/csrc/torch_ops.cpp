@@ -370,6 +370,98 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk_pairs(const at::Tensor& queries,
   return {os, oi};
 }
 
+// Prod rows (quantize_prod_packed's outputs): checks shared by the two prod scoring ops.
+struct ProdRowsT {
+  at::Tensor mp, sg, rn, nm, cen, R, S;
+};
+ProdRowsT prod_rows(const at::Tensor& mse_packed, const at::Tensor& signs,
+                    const at::Tensor& res_norms, const at::Tensor& norms,
+                    const at::Tensor& centroids, const at::Tensor& rotation, const at::Tensor& qjl,
+                    int64_t bit_width, int64_t d, c10::Device dev) {
+  TORCH_CHECK(bit_width >= 2 && bit_width <= 4, "prod scoring supports bit_width 2-4");
+  TORCH_CHECK(mse_packed.dim() == 2 && mse_packed.scalar_type() == at::kByte,
+              "mse_packed must be uint8 [N, P]");
+  ProdRowsT r;
+  r.mp = mse_packed.to(dev).contiguous();
+  const int64_t n = r.mp.size(0);
+  TORCH_CHECK(r.mp.size(1) == packed_width(bit_width - 1, d), "packed dim mismatch");
+  r.sg = signs.to(dev).contiguous();
+  TORCH_CHECK(r.sg.scalar_type() == at::kByte && r.sg.dim() == 2 && r.sg.size(0) == n &&
+                  r.sg.size(1) == (d + 7) / 8,
+              "signs must be uint8 [N, ceil(d/8)]");
+  r.rn = f32c(res_norms, dev);
+  r.nm = f32c(norms, dev);
+  r.cen = f32c(centroids, dev);
+  r.R = f32c(rotation, dev);
+  r.S = f32c(qjl, dev);
+  TORCH_CHECK(r.rn.numel() == n && r.nm.numel() == n, "norms must have N entries");
+  TORCH_CHECK(r.cen.numel() == (1 << (bit_width - 1)), "centroids length must be 2^(bits-1)");
+  TORCH_CHECK(r.R.dim() == 2 && r.R.size(0) == d && r.R.size(1) == d, "rotation must be [d, d]");
+  TORCH_CHECK(r.S.dim() == 2 && r.S.size(0) == d && r.S.size(1) == d, "S_matrix must be [d, d]");
+  return r;
+}
+
+// <q, dequantize_prod(row)> for every row, top-k (search.py:229-252 without the
+// reconstruction).
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod(const at::Tensor& queries,
+                                                     const at::Tensor& mse_packed,
+                                                     const at::Tensor& signs,
+                                                     const at::Tensor& res_norms,
+                                                     const at::Tensor& norms,
+                                                     const at::Tensor& centroids,
+                                                     const at::Tensor& rotation,
+                                                     const at::Tensor& qjl, int64_t bit_width,
+                                                     int64_t k) {
+  require_gpu(queries, "queries");
+  TORCH_CHECK(queries.dim() == 2, "queries must be [Q, d]");
+  c10::DeviceGuard g(queries.device());
+  const auto dev = queries.device();
+  auto q = floatc(queries, dev);
+  const int64_t Q = q.size(0), d = q.size(1);
+  auto r = prod_rows(mse_packed, signs, res_norms, norms, centroids, rotation, qjl, bit_width, d, dev);
+  const int64_t N = r.mp.size(0);
+  auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
+  auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
+  if (Q == 0) return {os, oi};
+  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
+  check_rc(tq_ip_scan_topk_prod(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
+                                r.mp.data_ptr<uint8_t>(), r.sg.data_ptr<uint8_t>(),
+                                r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), N,
+                                r.cen.data_ptr<float>(), r.R.data_ptr<float>(),
+                                r.S.data_ptr<float>(), (int32_t)bit_width, (int32_t)k,
+                                os.data_ptr<float>(), oi.data_ptr<int64_t>(), ws.data_ptr(),
+                                ws.numel(), cur_stream(q)));
+  return {os, oi};
+}
+
+// attention_scores_packed for prod-mode keys: query [B, H, d] -> [B, H, T] fp32.
+at::Tensor attention_scores_prod(const at::Tensor& query, const at::Tensor& mse_packed,
+                                 const at::Tensor& signs, const at::Tensor& res_norms,
+                                 const at::Tensor& key_norms, const at::Tensor& centroids,
+                                 const at::Tensor& rotation, const at::Tensor& qjl,
+                                 int64_t bit_width) {
+  require_gpu(query, "query");
+  TORCH_CHECK(query.dim() == 3, "query must be [batch, heads, head_dim]");
+  c10::DeviceGuard g(query.device());
+  const auto dev = query.device();
+  auto q = f32c(query, dev);
+  const int64_t B = q.size(0), H = q.size(1), d = q.size(2);
+  auto r = prod_rows(mse_packed, signs, res_norms, key_norms, centroids, rotation, qjl, bit_width,
+                     d, dev);
+  const int64_t T = r.mp.size(0);
+  auto scores = at::empty({B, H, T}, q.options());
+  if (B * H == 0 || T == 0) return scores;
+  auto ws = workspace(tq_scan_workspace_bytes(B * H, (int32_t)d, (int32_t)bit_width, T, 0), dev);
+  check_rc(tq_attention_scores_prod(q.data_ptr(), TQ_F32, B * H, (int32_t)d,
+                                    r.mp.data_ptr<uint8_t>(), r.sg.data_ptr<uint8_t>(),
+                                    r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), T,
+                                    r.cen.data_ptr<float>(), r.R.data_ptr<float>(),
+                                    r.S.data_ptr<float>(), (int32_t)bit_width,
+                                    scores.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                                    cur_stream(q)));
+  return scores;
+}
+
 at::Tensor attention_scores_pairs(const at::Tensor& query, const at::Tensor& pairs,
                                   const at::Tensor& key_norms, const at::Tensor& centroids,
                                   const at::Tensor& rotation) {
@@ -580,6 +672,11 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor rotation, int k) -> (Tensor, Tensor)");
   m.def("attention_scores_pairs(Tensor query, Tensor pairs, Tensor key_norms, Tensor centroids,"
         " Tensor rotation) -> Tensor");
+  m.def("ip_scan_topk_prod(Tensor queries, Tensor mse_packed, Tensor signs, Tensor res_norms,"
+        " Tensor norms, Tensor centroids, Tensor rotation, Tensor qjl, int bit_width, int k)"
+        " -> (Tensor, Tensor)");
+  m.def("attention_scores_prod(Tensor query, Tensor mse_packed, Tensor signs, Tensor res_norms,"
+        " Tensor key_norms, Tensor centroids, Tensor rotation, Tensor qjl, int bit_width) -> Tensor");
   m.def("decode_attention_packed(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale) -> Tensor");
@@ -612,6 +709,8 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("ip_scan_topk", &ip_scan_topk);
   m.impl("ip_scan_topk_pairs", &ip_scan_topk_pairs);
   m.impl("attention_scores_pairs", &attention_scores_pairs);
+  m.impl("ip_scan_topk_prod", &ip_scan_topk_prod);
+  m.impl("attention_scores_prod", &attention_scores_prod);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);
   m.impl("pack_decode_layout", &pack_decode_layout);

@@ -59,6 +59,13 @@ struct ScanArgs {
   int d;
   const float* rot;         // [d][d]
   const float* cen;         // [2^bits]
+  // Prod mode (signs != nullptr): rows also carry a QJL sign row (bpp bytes, the 1-bit
+  // bit-plane layout) and a residual norm gamma, and score
+  // n * (sum_j q_rot[j] c[code_j] + gamma * qjl_scale * sum_j (S q)_j (+-1)_j).
+  const uint8_t* signs;     // stream s starts at signs + s * stream_rows * bpp
+  const float* gammas;      // stream s starts at gammas + s * stream_rows
+  const float* qjl;         // [d][d] S
+  float qjl_scale;          // sqrt(pi/2) / d
   int qps;                  // queries per stream
   float post_scale;         // multiplies norm * sum (decode: softmax scale)
   int k;
@@ -240,6 +247,44 @@ __device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, 
   __syncthreads();
 }
 
+// Prod mode: the QJL term of every query as a table over groups of 4 sign bits.
+// qs = S q (qs[j] = sum_k S[j][k] q[k]); entry (g, v) = qjl_scale * sum_{i<4, 4g+i<d}
+// (bit 3-i of v ? +qs[4g+i] : -qs[4g+i]) -- v is the nibble holding the signs of dims
+// 4g..4g+3, MSB first as in the packed sign row, so sum_g T[g][nibble_g] =
+// qjl_scale * <S q, +-1> = qjl_scale * <q, (+-1) S> (the residual term of
+// reference.py:522-529 dotted with q).  Groups past d are zero, as are pad dims.
+// Layout as the pair-layout tables (16 entries per group): QB == 1: entry (g, v) at
+// (g>>1)*128 + v*8 + (g&1)*4; QB > 1: the QB queries' entries contiguous at
+// (g*16 + v)*QB*4.
+template <int DP, int QB>
+__device__ __forceinline__ void build_sign_tables(const ScanArgs& a, int q0, int nq, char* sgn_s) {
+  __shared__ float qss[QB][DP];
+  const int d = a.d;
+  for (int idx = threadIdx.x; idx < QB * DP; idx += kThreads) {
+    const int qi = idx / DP, j = idx - qi * DP;
+    float v = 0.f;
+    if (qi < nq && j < d) {
+      const float* srow = a.qjl + (size_t)j * d;
+      for (int k = 0; k < d; ++k) v = fmaf(load_as_f32(a.q, (int64_t)(q0 + qi) * d + k, a.q_dt), srow[k], v);
+    }
+    qss[qi][j] = v;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < QB * DP * 4; idx += kThreads) {
+    const int qi = idx / (DP * 4), e = idx - qi * (DP * 4);
+    const int g = e >> 4, v = e & 15;
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = qss[qi][4 * g + i];
+      t += ((v >> (3 - i)) & 1) ? x : -x;
+    }
+    const int off = QB == 1 ? (g >> 1) * 128 + v * 8 + (g & 1) * 4 : (g * 16 + v) * QB * 4 + qi * 4;
+    *reinterpret_cast<float*>(sgn_s + off) = t * a.qjl_scale;
+  }
+  __syncthreads();
+}
+
 // Calls f(dim, addr) for the 8 dims of one 32-bit word of pair-layout bytes (byte p =
 // code[2p] << 4 | code[2p+1]), in dim order; addr = code * SC.  Two shift-and-mask pairs
 // per word put every code of one nibble position at the SC scale, then one v_perm per dim
@@ -257,9 +302,10 @@ __device__ __forceinline__ void decode_pairs(uint32_t w, int j0, F&& f) {
   }
 }
 
-template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS>
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS, bool PROD>
 __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   static_assert(!PAIRS || (BITS == 4 && !GENERIC), "pair layout: 4-bit fast rows only");
+  static_assert(!PROD || (!PAIRS && BITS <= 3), "prod rows: bit-plane MSE codes of 1-3 bits");
   constexpr int NLEV = 1 << BITS;
   constexpr int BPPT = GENERIC ? 32 : BPP;          // layout the decoder sees
   constexpr int DP = 8 * BPPT;                      // dims covered by the decoder
@@ -269,6 +315,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   // Static LDS: the table's base address is a link-time constant, so every lookup is a
   // ds_read with an immediate offset and no address add.
   __shared__ __attribute__((aligned(16))) char lut_s[QB * QSTRIDE];
+  constexpr int SW = GENERIC ? 8 : BPP / 4;         // sign-row words (prod mode)
+  __shared__ __attribute__((aligned(16))) char sgn_s[PROD ? QB * DP * 16 : 16];
   __shared__ float cand_s[TOPK ? kWaves * QB * kCandCap : 1];
   __shared__ int cand_i[TOPK ? kWaves * QB * kCandCap : 1];
   __shared__ int cnt_s[TOPK ? kWaves * QB : 1];
@@ -286,6 +334,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   const int P = BITS * a.bpp;
 
   build_tables<NLEV, DP, QB>(a, q0, nq, lut_s);
+  if constexpr (PROD) build_sign_tables<DP, QB>(a, q0, nq, sgn_s);
 
   // Contiguous row range of this block, 64-row steps interleaved over the waves.
   const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
@@ -313,17 +362,31 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   struct RowBuf {
     uint32_t w[NW];
     float n;
+    uint32_t sw[PROD ? SW : 1];  // prod: sign row
+    float g;                     // prod: residual norm
   };
   // Fast layouts load through per-block buffer resources: 32-bit offsets from the
   // block's first row, and rows at or past rend read as zeros (no clamp).
   const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
   const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * P, nbr * (uint32_t)P);
   const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
+  const uint8_t* sbase = PROD ? a.signs + (size_t)s * a.stream_rows * a.bpp : nullptr;
+  const float* gbase = PROD ? a.gammas + (size_t)s * a.stream_rows : nullptr;
+  const __amdgpu_buffer_rsrc_t sgn_rs =
+      buf_rsrc(PROD ? sbase + rbeg * BPP : a.packed, PROD ? nbr * (uint32_t)BPP : 0u);
+  const __amdgpu_buffer_rsrc_t gam_rs = buf_rsrc(PROD ? gbase + rbeg : a.norms, PROD ? nbr * 4u : 0u);
   auto load_row = [&](int64_t r, RowBuf& b) {
     if constexpr (GENERIC) {
       const int64_t rl = r < rend ? r : rlast;
       load_generic<BITS>(base + rl * P, a.bpp, b.w);
       b.n = __builtin_nontemporal_load(nbase + rl);
+      if constexpr (PROD) {
+        uint32_t sw[8];
+        load_generic<1>(sbase + rl * a.bpp, a.bpp, sw);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b.sw[i] = sw[i];
+        b.g = __builtin_nontemporal_load(gbase + rl);
+      }
     } else {
       constexpr int PB = BITS * BPP;
       const uint32_t rr = (uint32_t)(r - rbeg);
@@ -343,6 +406,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         }
       }
       b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
+      if constexpr (PROD) {
+        const int soff = (int)(rr * (uint32_t)BPP);
+        if constexpr (BPP == 16) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(sgn_rs, soff, 0, 0);
+          b.sw[0] = v.x; b.sw[1] = v.y; b.sw[2] = v.z; b.sw[3] = v.w;
+        } else {
+          static_assert(BPP == 8, "fast prod rows: 64 or 128 dims");
+          const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(sgn_rs, soff, 0, 0);
+          b.sw[0] = v.x; b.sw[1] = v.y;
+        }
+        b.g = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gam_rs, (int)(rr * 4u), 0, kNT));
+      }
     }
   };
   // One 64-row step of this wave: score row `row` from its plane words `rb.w`.
@@ -404,6 +479,35 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
         if constexpr (QB == 4) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
       });
     }
+    }
+    if constexpr (PROD) {
+      // QJL term: one lookup per 4 sign bits (decode_pairs reads a sign byte's two
+      // nibbles as groups 2p and 2p+1), added to the MSE sum scaled by gamma.
+      float sacc[QB];
+#pragma unroll
+      for (int qi = 0; qi < QB; ++qi) sacc[qi] = 0.f;
+#pragma unroll
+      for (int w = 0; w < SW; ++w) {
+        decode_pairs<QB == 4 ? 16 : 8>(rb.sw[w], 8 * w, [&](int g, uint32_t addr) {
+          if constexpr (QB == 1) {
+            sacc[0] += *reinterpret_cast<const float*>(sgn_s + (g >> 1) * 128 + (g & 1) * 4 + addr);
+          } else if constexpr (QB == 2) {
+            const float2 v = *reinterpret_cast<const float2*>(sgn_s + g * 128 + addr);
+            sacc[0] += v.x;
+            sacc[1] += v.y;
+          } else {
+            const float4 v = *reinterpret_cast<const float4*>(sgn_s + g * 256 + addr);
+            sacc[0] += v.x;
+            sacc[1] += v.y;
+            sacc[2] += v.z;
+            sacc[3] += v.w;
+          }
+        });
+        if constexpr (QB == 2) asm volatile("" : "+v"(sacc[0]), "+v"(sacc[1]));
+        if constexpr (QB == 4) asm volatile("" : "+v"(sacc[0]), "+v"(sacc[1]), "+v"(sacc[2]), "+v"(sacc[3]));
+      }
+#pragma unroll
+      for (int qi = 0; qi < QB; ++qi) acc[qi] = fmaf(rb.g, sacc[qi], acc[qi]);
     }
 
     if constexpr (TOPK) {
@@ -1346,10 +1450,12 @@ int scan_blocks(int64_t nrows) {
   return (int)(b < 1 ? 1 : b);
 }
 
-template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS = false>
+template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS = false, bool PROD = false>
 int launch_scan_t(const ScanArgs& a, dim3 grid, hipStream_t st) {
-  static_assert(QB * 8 * (GENERIC ? 32 : BPP) * (1 << BITS) * 4 <= 48 * 1024, "table too large");
-  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC, PAIRS>), grid, dim3(kThreads), 0, st, a);
+  static_assert(QB * 8 * (GENERIC ? 32 : BPP) * ((1 << BITS) * 4 + (PROD ? 16 : 0)) <= 48 * 1024,
+                "table too large");
+  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC, PAIRS, PROD>), grid, dim3(kThreads), 0,
+                     st, a);
   TQ_LAUNCH_CHECK("scan_kernel");
   return TQ_OK;
 }
@@ -1361,21 +1467,25 @@ inline int queries_per_block(const ScanArgs& a) {
   return fast ? 4 : 2;
 }
 
-template <int BITS, bool TOPK>
+// The fast loaders issue 8/16-byte loads: they need 16-byte aligned bases (row strides
+// of the fast layouts keep that alignment).
+inline bool fast_aligned(const ScanArgs& a) {
+  return ((reinterpret_cast<uintptr_t>(a.packed) | reinterpret_cast<uintptr_t>(a.signs)) & 15u) == 0;
+}
+
+template <int BITS, bool TOPK, bool PROD = false>
 int launch_scan_bits(const ScanArgs& a, int qb, dim3 grid, hipStream_t st) {
-  // The fast loaders issue 8/16-byte loads: they need a 16-byte aligned base
-  // (row strides of the fast layouts keep that alignment).
-  const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
+  const bool aligned = fast_aligned(a);
   if (aligned && a.bpp == 16) {
-    return qb == 4 ? launch_scan_t<BITS, 16, 4, TOPK, false>(a, grid, st)
-                   : launch_scan_t<BITS, 16, 1, TOPK, false>(a, grid, st);
+    return qb == 4 ? launch_scan_t<BITS, 16, 4, TOPK, false, false, PROD>(a, grid, st)
+                   : launch_scan_t<BITS, 16, 1, TOPK, false, false, PROD>(a, grid, st);
   }
   if (aligned && a.bpp == 8) {
-    return qb == 4 ? launch_scan_t<BITS, 8, 4, TOPK, false>(a, grid, st)
-                   : launch_scan_t<BITS, 8, 1, TOPK, false>(a, grid, st);
+    return qb == 4 ? launch_scan_t<BITS, 8, 4, TOPK, false, false, PROD>(a, grid, st)
+                   : launch_scan_t<BITS, 8, 1, TOPK, false, false, PROD>(a, grid, st);
   }
-  return qb >= 2 ? launch_scan_t<BITS, 32, 2, TOPK, true>(a, grid, st)
-                 : launch_scan_t<BITS, 32, 1, TOPK, true>(a, grid, st);
+  return qb >= 2 ? launch_scan_t<BITS, 32, 2, TOPK, true, false, PROD>(a, grid, st)
+                 : launch_scan_t<BITS, 32, 1, TOPK, true, false, PROD>(a, grid, st);
 }
 
 // Pair-layout rows: 4-bit codes, 64 or 128 dims, 16-byte aligned base (checked by callers).
@@ -1407,7 +1517,7 @@ int launch_pair_scan(const ScanArgs& a, dim3 grid, hipStream_t st) {
 // *nblocks_out: the grid's row blocks (TOPK: the lists merge_kernel reads per query).
 int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_t st,
                 bool pairs = false, int* nblocks_out = nullptr) {
-  const bool aligned = (reinterpret_cast<uintptr_t>(a.packed) & 15u) == 0;
+  const bool aligned = fast_aligned(a);
   int qb = queries_per_block(a);
   if (!aligned && qb > 2) qb = 2;
   const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
@@ -1424,6 +1534,15 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
       return fail(TQ_EINVAL, "pair-layout scan needs 4-bit codes, dim 64 or 128 and a 16-byte aligned base");
     if (pair1) return topk ? launch_pair_scan<true>(a, grid, st) : launch_pair_scan<false>(a, grid, st);
     return topk ? launch_scan_pairs<true>(a, qb, grid, st) : launch_scan_pairs<false>(a, qb, grid, st);
+  }
+  if (a.signs) {
+    // Prod rows: `bits` is the MSE code width (the prod bit budget minus the sign bit).
+    switch (bits) {
+      case 1: return topk ? launch_scan_bits<1, true, true>(a, qb, grid, st) : launch_scan_bits<1, false, true>(a, qb, grid, st);
+      case 2: return topk ? launch_scan_bits<2, true, true>(a, qb, grid, st) : launch_scan_bits<2, false, true>(a, qb, grid, st);
+      case 3: return topk ? launch_scan_bits<3, true, true>(a, qb, grid, st) : launch_scan_bits<3, false, true>(a, qb, grid, st);
+    }
+    return fail(TQ_EINVAL, "prod bit_width must be 2-4, got %d", bits + 1);
   }
   switch (bits) {
     case 1: return topk ? launch_scan_bits<1, true>(a, qb, grid, st) : launch_scan_bits<1, false>(a, qb, grid, st);
@@ -1455,12 +1574,27 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
 
 namespace {
 
+// The QJL half of prod rows (reference.py:392-469 outputs beside the MSE codes).
+struct ProdRows {
+  const uint8_t* signs;   // [rows][ceil(d/8)] sign bits, 1-bit bit-plane layout
+  const float* gammas;    // [rows] residual norms
+  const float* qjl;       // [d][d] S
+};
+
+void set_prod(ScanArgs& a, const ProdRows& p) {
+  a.signs = p.signs; a.gammas = p.gammas; a.qjl = p.qjl;
+  a.qjl_scale = (float)(1.2533141373155002512 / a.d);  // sqrt(pi/2) / d, as reference.py:527
+}
+
 int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
                  const uint8_t* packed, const float* norms, int64_t N, const float* centroids,
                  const float* rotation, int32_t bit_width, int32_t k, float* out_scores,
                  int64_t* out_ids, void* workspace, size_t workspace_bytes, void* stream,
-                 bool pairs) {
+                 bool pairs, const ProdRows* prod = nullptr) {
   TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(!prod || bit_width >= 2, "prod bit_width must be 2-4, got %d", bit_width);
+  TQ_REQUIRE(!prod || N == 0 || (prod->signs && prod->gammas), "null pointer argument");
+  TQ_REQUIRE(!prod || prod->qjl, "null pointer argument");
   TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
   TQ_REQUIRE(k >= 1 && k <= kMaxK, "k must be in [1, %d], got %d", kMaxK, k);
   TQ_REQUIRE(nq >= 0 && N >= 0, "bad sizes");
@@ -1484,9 +1618,10 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.qps = (int)nq; a.post_scale = 1.f; a.k = k;
   a.part_s = ps; a.part_i = pi; a.scores = nullptr;
   a.out_s = out_scores; a.out_i = out_ids;
+  if (prod) set_prod(a, *prod);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
   int nb = 0;
-  const int rc = launch_scan(a, bit_width, true, 1, st, pairs, &nb);
+  const int rc = launch_scan(a, prod ? bit_width - 1 : bit_width, true, 1, st, pairs, &nb);
   if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
                      out_scores, out_ids);
@@ -1498,8 +1633,11 @@ int attention_scores(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
                      const uint8_t* packed_keys, const float* key_norms, int64_t T,
                      const float* centroids, const float* rotation, int32_t bit_width,
                      float* scores, void* workspace, size_t workspace_bytes, void* stream,
-                     bool pairs) {
+                     bool pairs, const ProdRows* prod = nullptr) {
   TQ_REQUIRE(bit_width >= 1 && bit_width <= 4, "bit_width must be 1-4, got %d", bit_width);
+  TQ_REQUIRE(!prod || bit_width >= 2, "prod bit_width must be 2-4, got %d", bit_width);
+  TQ_REQUIRE(!prod || T == 0 || (prod->signs && prod->gammas), "null pointer argument");
+  TQ_REQUIRE(!prod || prod->qjl, "null pointer argument");
   TQ_REQUIRE(d >= 1 && d <= 256, "dim must be in [1, 256], got %d", d);
   TQ_REQUIRE(nq >= 0 && T >= 0, "bad sizes");
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
@@ -1514,8 +1652,9 @@ int attention_scores(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.spb = 1; a.bpp = (d + 7) / 8; a.q = query; a.q_dt = q_dtype; a.d = d; a.rot = rotation;
   a.cen = centroids; a.qps = (int)nq; a.post_scale = 1.f;
   a.k = 0; a.scores = scores;
+  if (prod) set_prod(a, *prod);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  return launch_scan(a, bit_width, false, 1, st, pairs);
+  return launch_scan(a, prod ? bit_width - 1 : bit_width, false, 1, st, pairs);
 }
 
 }  // namespace
@@ -1549,6 +1688,29 @@ int tq_attention_scores_packed(const void* query, tq_dtype q_dtype, int64_t nq, 
                                void* stream) {
   return attention_scores(query, q_dtype, nq, d, packed_keys, key_norms, T, centroids, rotation,
                           bit_width, scores, workspace, workspace_bytes, stream, false);
+}
+
+int tq_ip_scan_topk_prod(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                         const uint8_t* mse_packed, const uint8_t* signs, const float* res_norms,
+                         const float* norms, int64_t N, const float* centroids,
+                         const float* rotation, const float* qjl, int32_t bit_width, int32_t k,
+                         float* out_scores, int64_t* out_ids, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  const ProdRows p{signs, res_norms, qjl};
+  return ip_scan_topk(queries, q_dtype, nq, d, mse_packed, norms, N, centroids, rotation,
+                      bit_width, k, out_scores, out_ids, workspace, workspace_bytes, stream,
+                      false, &p);
+}
+
+int tq_attention_scores_prod(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                             const uint8_t* mse_packed, const uint8_t* signs,
+                             const float* res_norms, const float* key_norms, int64_t T,
+                             const float* centroids, const float* rotation, const float* qjl,
+                             int32_t bit_width, float* scores, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  const ProdRows p{signs, res_norms, qjl};
+  return attention_scores(query, q_dtype, nq, d, mse_packed, key_norms, T, centroids, rotation,
+                          bit_width, scores, workspace, workspace_bytes, stream, false, &p);
 }
 
 int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,

@@ -258,7 +258,7 @@ class QuantizedKVCache:
         G = self._query_groups(q4)
         T = int(self.seq_lens[layer_id].item())
         scale = 1.0 / math.sqrt(self.head_dim)
-        if self._is_protected_layer(layer_id) or self._is_prod:
+        if self._is_protected_layer(layer_id) or (self._is_prod and self.config.key_bits > 4):
             keys = self._dequantize_keys(layer_id)
             keys = keys.unsqueeze(0) if keys.dim() == 3 else keys
             keys = keys.repeat_interleave(G, dim=1) if G > 1 else keys
@@ -272,10 +272,19 @@ class QuantizedKVCache:
                     qbs = slice(None) if self.batch_size == 1 else slice(kvb, kvb + 1)
                     for g in range(self.num_heads):
                         qs = qf[qbs, g * G:(g + 1) * G]            # (b', G, sq, d)
-                        s = ops.attention_scores_packed(
-                            qs.reshape(1, -1, d), rows[kvb, g],
-                            self._key_norms[layer_id][kvb, g, :T], self._kcen, self._key_rotation,
-                            self.config.key_bits)
+                        if self._is_prod:
+                            # <q, dequantize_prod(k_t)> scored from the packed rows.
+                            s = ops.attention_scores_prod(
+                                qs.reshape(1, -1, d), rows[kvb, g],
+                                self._key_qjl_signs[layer_id][kvb, g, :T],
+                                self._key_res_norms[layer_id][kvb, g, :T],
+                                self._key_norms[layer_id][kvb, g, :T], self._kcen,
+                                self._key_rotation, self._key_S, self.config.key_bits)
+                        else:
+                            s = ops.attention_scores_packed(
+                                qs.reshape(1, -1, d), rows[kvb, g],
+                                self._key_norms[layer_id][kvb, g, :T], self._kcen,
+                                self._key_rotation, self.config.key_bits)
                         logits[qbs, g * G:(g + 1) * G] = s.view(qs.shape[0], G, sq, T)
                 logits = logits * scale
         return logits if has_batch else logits.squeeze(0)

@@ -66,6 +66,24 @@ def attention_scores_pairs(query, pairs, key_norms, centroids, rotation):
     return _ops().attention_scores_pairs(query, pairs, key_norms, centroids, rotation)
 
 
+def ip_scan_topk_prod(queries, mse_packed, signs, res_norms, norms, centroids, rotation, qjl,
+                      bit_width, k):
+    """Top-k of <q, dequantize_prod(row)> (search.py:229-252) scored from the packed rows:
+    n * (sum_j (R q)_j c[code_j] + sqrt(pi/2)/d * gamma * sum_j (S q)_j (+-1)_j).
+    bit_width is the prod bit budget (2-4); centroids are the (bit_width-1)-bit codebook."""
+    _require_device(queries, "queries")
+    return _ops().ip_scan_topk_prod(queries, mse_packed, signs, res_norms, norms, centroids,
+                                    rotation, qjl, bit_width, k)
+
+
+def attention_scores_prod(query, mse_packed, signs, res_norms, key_norms, centroids, rotation,
+                          qjl, bit_width):
+    """<q, dequantize_prod(key_t)> for query [B, H, d] -> [B, H, T] fp32 (no 1/sqrt(d))."""
+    _require_device(query, "query")
+    return _ops().attention_scores_prod(query, mse_packed, signs, res_norms, key_norms, centroids,
+                                        rotation, qjl, bit_width)
+
+
 def decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcentroids,
                             vcentroids, krotation, vrotation, kbits, vbits, scale):
     """Fused GQA decode attention over packed K/V -> [B, Hq, d] in q.dtype."""

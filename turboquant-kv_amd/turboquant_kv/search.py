@@ -184,6 +184,19 @@ class TurboQuantIndex:
                                                 self.bit_width)[0]
             top = torch.topk(s, k, dim=-1)
             return top.values, top.indices
+        if self.bit_width <= 4:
+            # Scored from the packed rows: <q, dequantize_prod(row)> rearranged as
+            # n * (<R q, c[codes]> + sqrt(pi/2)/d * gamma * <S q, +-1>).
+            if k <= _SCAN_MAX_K:
+                return ops.ip_scan_topk_prod(q, self._packed_codes, self._qjl_signs,
+                                             self._residual_norms, self._norms, self._cen,
+                                             self._rot_dev, self._S_dev, self.bit_width, k)
+            s = ops.attention_scores_prod(q.float().unsqueeze(0), self._packed_codes,
+                                          self._qjl_signs, self._residual_norms, self._norms,
+                                          self._cen, self._rot_dev, self._S_dev,
+                                          self.bit_width)[0]
+            top = torch.topk(s, k, dim=-1)
+            return top.values, top.indices
         recon = _ops().dequantize_prod_packed(self._packed_codes, self._qjl_signs,
                                               self._residual_norms, self._norms, self._cen,
                                               self._rot_dev, self._S_dev, self.bit_width, self.dim)
