@@ -210,10 +210,22 @@ __device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int
 // Layout: QB == 1: entry (j, l) at (j>>1)*NLEV*8 + l*8 + (j&1)*4 (two dims interleaved,
 // 8-byte code stride); QB > 1: the QB queries' entries of (j, l) contiguous at
 // (j*NLEV + l)*QB*4, so one 8/16-byte read serves every query.  Dims d..DP-1 are zero.
-template <int NLEV, int DP, int QB>
-__device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, char* lut_s) {
+//
+// PROD adds the QJL term of every query as a table over groups of 4 sign bits:
+// qs = S q (qs[j] = sum_k S[j][k] q[k], computed in the same pass over k as q_rot);
+// entry (g, v) = qjl_scale * sum_{i<4, 4g+i<d} (bit 3-i of v ? +qs[4g+i] : -qs[4g+i]),
+// v being the nibble that holds the signs of dims 4g..4g+3 (MSB first, as in the packed
+// sign row).  So sum_g T[g][nibble_g] = qjl_scale * <S q, +-1> = qjl_scale * <q, (+-1) S>,
+// the residual term of reference.py:522-529 dotted with q.  Groups past d are zero, as
+// are pad dims.  Layout as the pair-layout tables (16 entries per group): QB == 1: entry
+// (g, v) at (g>>1)*128 + v*8 + (g&1)*4; QB > 1: the QB queries' entries contiguous at
+// (g*16 + v)*QB*4.
+template <int NLEV, int DP, int QB, bool PROD = false>
+__device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, char* lut_s,
+                                             char* sgn_s = nullptr) {
 #pragma clang fp contract(off)
   __shared__ float qs[QB][256];
+  __shared__ float qss[PROD ? QB : 1][PROD ? DP : 1];
   const int d = a.d;
   for (int idx = threadIdx.x; idx < QB * d; idx += kThreads) {
     const int qi = idx / d, k = idx - qi * d;
@@ -222,9 +234,10 @@ __device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, 
   __syncthreads();
   for (int idx = threadIdx.x; idx < QB * DP; idx += kThreads) {
     const int qi = idx / DP, j = idx - qi * DP;
-    float v = 0.f;
+    float v = 0.f, w = 0.f;
     if (qi < nq && j < d) {
       const float* r = a.rot + (size_t)j * d;
+      const float* sr = PROD ? a.qjl + (size_t)j * d : nullptr;
       if ((d & 3) == 0) {
         for (int k = 0; k < d; k += 4) {
           const float4 r4 = *reinterpret_cast<const float4*>(r + k);
@@ -232,11 +245,22 @@ __device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, 
           v = v + qs[qi][k + 1] * r4.y;
           v = v + qs[qi][k + 2] * r4.z;
           v = v + qs[qi][k + 3] * r4.w;
+          if constexpr (PROD) {
+            const float4 s4 = *reinterpret_cast<const float4*>(sr + k);
+            w = fmaf(qs[qi][k], s4.x, w);
+            w = fmaf(qs[qi][k + 1], s4.y, w);
+            w = fmaf(qs[qi][k + 2], s4.z, w);
+            w = fmaf(qs[qi][k + 3], s4.w, w);
+          }
         }
       } else {
-        for (int k = 0; k < d; ++k) v = v + qs[qi][k] * r[k];
+        for (int k = 0; k < d; ++k) {
+          v = v + qs[qi][k] * r[k];
+          if constexpr (PROD) w = fmaf(qs[qi][k], sr[k], w);
+        }
       }
     }
+    if constexpr (PROD) qss[qi][j] = w;
     for (int l = 0; l < NLEV; ++l) {
       const float e = (qi < nq && j < d) ? v * a.cen[l] : 0.f;
       const int off = QB == 1 ? (j >> 1) * NLEV * 8 + l * 8 + (j & 1) * 4
@@ -245,44 +269,21 @@ __device__ __forceinline__ void build_tables(const ScanArgs& a, int q0, int nq, 
     }
   }
   __syncthreads();
-}
-
-// Prod mode: the QJL term of every query as a table over groups of 4 sign bits.
-// qs = S q (qs[j] = sum_k S[j][k] q[k]); entry (g, v) = qjl_scale * sum_{i<4, 4g+i<d}
-// (bit 3-i of v ? +qs[4g+i] : -qs[4g+i]) -- v is the nibble holding the signs of dims
-// 4g..4g+3, MSB first as in the packed sign row, so sum_g T[g][nibble_g] =
-// qjl_scale * <S q, +-1> = qjl_scale * <q, (+-1) S> (the residual term of
-// reference.py:522-529 dotted with q).  Groups past d are zero, as are pad dims.
-// Layout as the pair-layout tables (16 entries per group): QB == 1: entry (g, v) at
-// (g>>1)*128 + v*8 + (g&1)*4; QB > 1: the QB queries' entries contiguous at
-// (g*16 + v)*QB*4.
-template <int DP, int QB>
-__device__ __forceinline__ void build_sign_tables(const ScanArgs& a, int q0, int nq, char* sgn_s) {
-  __shared__ float qss[QB][DP];
-  const int d = a.d;
-  for (int idx = threadIdx.x; idx < QB * DP; idx += kThreads) {
-    const int qi = idx / DP, j = idx - qi * DP;
-    float v = 0.f;
-    if (qi < nq && j < d) {
-      const float* srow = a.qjl + (size_t)j * d;
-      for (int k = 0; k < d; ++k) v = fmaf(load_as_f32(a.q, (int64_t)(q0 + qi) * d + k, a.q_dt), srow[k], v);
-    }
-    qss[qi][j] = v;
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < QB * DP * 4; idx += kThreads) {
-    const int qi = idx / (DP * 4), e = idx - qi * (DP * 4);
-    const int g = e >> 4, v = e & 15;
-    float t = 0.f;
+  if constexpr (PROD) {
+    for (int idx = threadIdx.x; idx < QB * DP * 4; idx += kThreads) {
+      const int qi = idx / (DP * 4), e = idx - qi * (DP * 4);
+      const int g = e >> 4, v = e & 15;
+      float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = qss[qi][4 * g + i];
-      t += ((v >> (3 - i)) & 1) ? x : -x;
+      for (int i = 0; i < 4; ++i) {
+        const float x = qss[qi][4 * g + i];
+        t += ((v >> (3 - i)) & 1) ? x : -x;
+      }
+      const int off = QB == 1 ? (g >> 1) * 128 + v * 8 + (g & 1) * 4 : (g * 16 + v) * QB * 4 + qi * 4;
+      *reinterpret_cast<float*>(sgn_s + off) = t * a.qjl_scale;
     }
-    const int off = QB == 1 ? (g >> 1) * 128 + v * 8 + (g & 1) * 4 : (g * 16 + v) * QB * 4 + qi * 4;
-    *reinterpret_cast<float*>(sgn_s + off) = t * a.qjl_scale;
+    __syncthreads();
   }
-  __syncthreads();
 }
 
 // Calls f(dim, addr) for the 8 dims of one 32-bit word of pair-layout bytes (byte p =
@@ -302,8 +303,11 @@ __device__ __forceinline__ void decode_pairs(uint32_t w, int j0, F&& f) {
   }
 }
 
+// One-query top-k prod scans over the fast layouts are held to 80 VGPRs: six 4-wave
+// blocks per CU (scan_blocks' grid) are then all resident.
 template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS, bool PROD>
-__global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
+    (PROD && TOPK && !GENERIC && QB == 1) ? 6 : 0))) void scan_kernel(ScanArgs a) {
   static_assert(!PAIRS || (BITS == 4 && !GENERIC), "pair layout: 4-bit fast rows only");
   static_assert(!PROD || (!PAIRS && BITS <= 3), "prod rows: bit-plane MSE codes of 1-3 bits");
   constexpr int NLEV = 1 << BITS;
@@ -333,8 +337,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanArgs a) {
   const int nq = min(QB, a.qps - qb * QB);       // valid queries in this block
   const int P = BITS * a.bpp;
 
-  build_tables<NLEV, DP, QB>(a, q0, nq, lut_s);
-  if constexpr (PROD) build_sign_tables<DP, QB>(a, q0, nq, sgn_s);
+  build_tables<NLEV, DP, QB, PROD>(a, q0, nq, lut_s, sgn_s);
 
   // Contiguous row range of this block, 64-row steps interleaved over the waves.
   const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
