@@ -211,6 +211,28 @@ def bench_decode(args, extra):
                                       "bitplane_rows_GBps": bytes_alg / ms_bp / 1e6}
         log(f"decode T={T}: {ms * 1e3:.1f} us, {bytes_alg / ms / 1e6:.0f} GB/s "
             f"(bit-plane rows: {ms_bp * 1e3:.1f} us)")
+        if T == 32768:
+            # vLLM paging: the same rows in block pools of 16 tokens, blocks shuffled
+            bs = 16
+            nbs = T // bs
+            perm = torch.randperm(B * nbs, generator=g, device="cuda")
+            tab = perm.view(B, nbs).to(torch.int32)
+            c = caches[0]
+
+            def to_pool(x):  # [B, Hkv, T, ...] -> [B * nbs, Hkv, bs, ...] at the table's blocks
+                y = x.reshape(B, Hkv, nbs, bs, *x.shape[3:]).transpose(1, 2)
+                pool = torch.empty((B * nbs, Hkv, bs) + tuple(x.shape[3:]), dtype=x.dtype, device="cuda")
+                pool[perm] = y.reshape(B * nbs, Hkv, bs, *x.shape[3:])
+                return pool
+
+            pk, pkn, pv, pvn = (to_pool(t) for t in c[:4])
+            ms_pg = time_op(lambda: ops.decode_attention_paged(q, pk, pkn, pv, pvn, tab, sl, ck, cv,
+                                                               Rk, Rv, kb, vb, 1.0 / 8.0), 20, 3)
+            extra[f"decode_attn_T{T}"].update({"paged_bs16_us": ms_pg * 1e3,
+                                               "paged_bs16_GBps": bytes_alg / ms_pg / 1e6})
+            log(f"decode T={T} paged (block 16, shuffled): {ms_pg * 1e3:.1f} us, "
+                f"{bytes_alg / ms_pg / 1e6:.0f} GB/s")
+            del pk, pkn, pv, pvn
         del caches
     return out
 

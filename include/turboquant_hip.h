@@ -261,6 +261,56 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                            void* out, float* lse, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/*
+ * Paged KV storage (vLLM block tables).  The reference's vLLM backend keeps one
+ * contiguous QuantizedKVCache per model with no block tables
+ * (turboquant_kv/vllm_plugin/__init__.py:114-304, 350-412); these entry points give its
+ * TurboQuantAttentionImpl what vLLM's cache engine hands an attention backend.
+ * A layer's pools hold packed rows and fp32 norms block by block:
+ *   pool [num_blocks][hkv][block_size][P] u8, norm_pool [num_blocks][hkv][block_size];
+ * token t of sequence s sits in block block_tables[s * bt_stride + t / block_size] at slot
+ * t % block_size, and a new token's flat slot is block * block_size + slot (vLLM's
+ * slot_mapping).
+ *
+ * tq_paged_store: rows [n_tokens][hkv][row_bytes] (+ norms [n_tokens][hkv], or both NULL)
+ * to the slots slot_mapping[n_tokens] (int64); slots < 0 or >= num_blocks * block_size
+ * are skipped (vLLM pads with -1).  Replaces the append of vllm_plugin:395 for a batch
+ * of sequences.
+ */
+int tq_paged_store(const uint8_t* rows, const float* norms, int64_t n_tokens, int32_t hkv,
+                   int32_t row_bytes, const int64_t* slot_mapping, uint8_t* pool, float* norm_pool,
+                   int64_t num_blocks, int32_t block_size, void* stream);
+/*
+ * tq_paged_gather: the first min(seq_lens[b], t_max) tokens of batch rows b < B into
+ * contiguous out_rows [B][hkv][t_max][row_bytes] (+ out_norms [B][hkv][t_max]); later
+ * tokens, and tokens whose block id is outside [0, num_blocks), come out as zero rows.
+ * t_max <= bt_stride * block_size.
+ */
+int tq_paged_gather(const uint8_t* pool, const float* norm_pool, int64_t num_blocks, int32_t hkv,
+                    int32_t block_size, int32_t row_bytes, const int32_t* block_tables,
+                    int32_t bt_stride, const int32_t* seq_lens, int32_t B, int64_t t_max,
+                    uint8_t* out_rows, float* out_norms, void* stream);
+/*
+ * tq_decode_attention_packed over paged pools (same semantics and outputs): batch row b
+ * attends to its first seq_lens[b] tokens, found through block_tables [B][bt_stride]
+ * (bt_stride = max_blocks_per_seq).  Head_dim 64, K 1-4 / V 1-2 bits, at most 4 query
+ * heads per KV head, fp16/bf16 queries and a power-of-two block_size >= 4 run the fused
+ * decode kernel reading the pools directly; other shapes gather the rows into the
+ * workspace first.  Pools 16-byte aligned; num_blocks * hkv * block_size * P < 2^31.
+ */
+size_t tq_decode_paged_workspace_bytes(tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                                       int32_t d, int32_t kbits, int32_t vbits,
+                                       int32_t max_blocks_per_seq, int32_t block_size);
+int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                              int32_t d, const uint8_t* kpool, const float* knorm_pool,
+                              const uint8_t* vpool, const float* vnorm_pool, int64_t num_blocks,
+                              int32_t block_size, const int32_t* block_tables,
+                              int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                              const float* kcentroids, const float* vcentroids,
+                              const float* krotation, const float* vrotation, int32_t kbits,
+                              int32_t vbits, float scale, void* out, float* lse, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -340,3 +340,58 @@ def decode_attention_f64(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, 
                 p /= p.sum()
                 out[b, h] = p @ V
     return (out, lse) if return_lse else out
+
+
+# ----------------------------------------------------------------- paged KV (vLLM block tables)
+
+
+def paged_rows(pool, block_table, T):
+    """Rows of tokens 0..T-1 of one sequence from a block pool [num_blocks, H, bs, ...]:
+    token t sits in block block_table[t // bs] at slot t % bs (vLLM's paging).
+    Returns [H, T, ...]."""
+    pool = np.asarray(pool)
+    bs = pool.shape[2]
+    t = np.arange(T)
+    blk = np.asarray(block_table, np.int64)[t // bs]
+    return np.stack([pool[blk[i], :, t[i] % bs] for i in range(T)], axis=1) if T else \
+        np.zeros((pool.shape[1], 0) + pool.shape[3:], pool.dtype)
+
+
+def paged_attention_f64(q, kpool, knorm_pool, vpool, vnorm_pool, block_table, T, kc, vc, Rk, Rv,
+                        kbits, vbits, scale, kprod=None, vprod=None):
+    """float64 attention of one sequence's n new tokens q [n, Hq, d] -- positions
+    T-n .. T-1 -- over its first T cached tokens, causally (token i sees positions
+    <= T-n+i), with GQA (q head h reads kv head h // (Hq/Hkv)).  K/V are the
+    dequantized pool rows (reference.py:320-367; with kprod/vprod = (sign_pool,
+    res_pool, S) the prod reconstruction of reference.py:472-533 at bits-1 codes).
+    The reference's vLLM step (vllm_plugin/__init__.py:380-412) is this with n = 1 and
+    one sequence.  Returns [n, Hq, d]."""
+    q = np.asarray(q, np.float64)
+    n, Hq, d = q.shape
+    Hkv = kpool.shape[1]
+    G = Hq // Hkv
+
+    def deq(pool, npool, cen, R, bits, prod):
+        rows, nrm = paged_rows(pool, block_table, T), paged_rows(npool, block_table, T)
+        out = []
+        for g in range(Hkv):
+            if prod is None:
+                codes = unpack_codes(rows[g], bits, d)
+                x = (np.asarray(cen, np.float64)[codes] @ np.asarray(R, np.float64)) * nrm[g].astype(np.float64)[:, None]
+            else:
+                sg, rs = paged_rows(prod[0], block_table, T)[g], paged_rows(prod[1], block_table, T)[g]
+                x = dequantize_prod(rows[g], sg, rs, nrm[g], bits, d, R, cen, prod[2])
+            out.append(x)
+        return out
+
+    K = deq(kpool, knorm_pool, kc, Rk, kbits, kprod)
+    V = deq(vpool, vnorm_pool, vc, Rv, vbits, vprod)
+    out = np.zeros((n, Hq, d))
+    for i in range(n):
+        vis = T - n + i + 1
+        for h in range(Hq):
+            g = h // G
+            s = (K[g][:vis] @ q[i, h]) * scale
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ V[g][:vis]
+    return out

@@ -1,0 +1,270 @@
+"""GPU tests of the paged (vLLM block-table) KV path: slot-mapped stores and gathers
+bit-exact against numpy, paged decode against the contiguous decode kernels and the
+float64 oracle, and the vLLM attention step (mixed prefill + decode batches, causal
+prefill, GQA, prod mode, protected layers) against the float64 paged oracle."""
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import capi
+import tq_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+L = capi.lib
+_ALIVE = []
+
+
+def T(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    t = t if dtype is None else t.to(dtype)
+    _ALIVE.append(t)
+    return t
+
+
+def sync():
+    torch.cuda.synchronize()
+    _ALIVE.clear()
+
+
+def _tables(rs, lens, bs, nblocks, width):
+    """Block tables of distinct random blocks; entries past a sequence's blocks are -1."""
+    perm = rs.permutation(nblocks)
+    tab = np.full((len(lens), width), -1, np.int32)
+    used = 0
+    for i, n in enumerate(lens):
+        k = (n + bs - 1) // bs
+        tab[i, :k] = perm[used:used + k]
+        used += k
+    return tab
+
+
+def _np_store(rows, norms, slots, pool, npool):
+    bs = pool.shape[2]
+    for t, s in enumerate(slots):
+        if 0 <= s < pool.shape[0] * bs:
+            pool[s // bs, :, s % bs] = rows[t]
+            npool[s // bs, :, s % bs] = norms[t]
+
+
+@pytest.mark.parametrize("P", [32, 25])
+def test_paged_store_and_gather_bit_exact(P):
+    rs = np.random.RandomState(P)
+    nb, H, bs = 12, 3, 16
+    pool = np.zeros((nb, H, bs, P), np.uint8)
+    npool = np.zeros((nb, H, bs), np.float32)
+    pt, nt = T(pool), T(npool)
+    lens = [37, 5, 0]
+    tab = _tables(rs, lens, bs, nb, 4)
+    # every token of the three sequences, in shuffled order, plus two padding slots
+    slots = [tab[i, t // bs] * bs + t % bs for i, n in enumerate(lens) for t in range(n)]
+    slots = np.array(slots + [-1, nb * bs + 3], np.int64)[rs.permutation(len(slots) + 2)]
+    rows = rs.randint(0, 256, (len(slots), H, P)).astype(np.uint8)
+    norms = rs.rand(len(slots), H).astype(np.float32)
+    capi.check(L().tq_paged_store(capi.p(T(rows)), capi.p(T(norms)), capi.i64(len(slots)), capi.i32(H),
+                                  capi.i32(P), capi.p(T(slots)), capi.p(pt), capi.p(nt), capi.i64(nb),
+                                  capi.i32(bs), capi.stream()))
+    sync()
+    _np_store(rows, norms, slots, pool, npool)
+    assert np.array_equal(pt.cpu().numpy(), pool) and np.array_equal(nt.cpu().numpy(), npool)
+    tmax = 48
+    out = torch.empty(3, H, tmax, P, dtype=torch.uint8, device=DEV)
+    onr = torch.empty(3, H, tmax, dtype=torch.float32, device=DEV)
+    tab[0, 3] = 99  # past sequence 0's tokens anyway; must not be read
+    capi.check(L().tq_paged_gather(capi.p(pt), capi.p(nt), capi.i64(nb), capi.i32(H), capi.i32(bs),
+                                   capi.i32(P), capi.p(T(tab)), capi.i32(tab.shape[1]),
+                                   capi.p(T(np.array(lens, np.int32))), capi.i32(3), capi.i64(tmax),
+                                   capi.p(out), capi.p(onr), capi.stream()))
+    sync()
+    o, on = out.cpu().numpy(), onr.cpu().numpy()
+    for i, n in enumerate(lens):
+        assert np.array_equal(o[i, :, :n], O.paged_rows(pool, tab[i], n))
+        assert np.array_equal(on[i, :, :n], O.paged_rows(npool, tab[i], n))
+        assert not o[i, :, n:].any() and not on[i, :, n:].any()
+
+
+def k_decode_paged(q_t, kpool, knp, vpool, vnp, tab, lens, kc, vc, Rk, Rv, kb, vb, scale):
+    B, Hq, d = q_t.shape
+    nb, Hkv, bs = kpool.shape[:3]
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
+    out = torch.empty_like(q_t)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
+    wsb = L().tq_decode_paged_workspace_bytes(dt, B, Hq, Hkv, d, kb, vb, tab.shape[1], bs)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_decode_attention_paged(
+        capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(T(kpool)),
+        capi.p(T(knp)), capi.p(T(vpool)), capi.p(T(vnp)), capi.i64(nb), capi.i32(bs), capi.p(T(tab)),
+        capi.i32(tab.shape[1]), capi.p(T(np.asarray(lens, np.int32))), capi.p(T(kc)), capi.p(T(vc)),
+        capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(kb), capi.i32(vb), ctypes.c_float(scale), capi.p(out),
+        capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
+def k_decode(q_t, kp, kn, vp, vn, seq_lens, kc, vc, Rk, Rv, kb, vb, scale):
+    B, Hq, d = q_t.shape
+    Hkv, Tm = kp.shape[1], kp.shape[2]
+    out = torch.empty_like(q_t)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_decode_workspace_bytes(B, Hq, d, Tm), 1), dtype=torch.uint8, device=DEV)
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
+    capi.check(L().tq_decode_attention_packed(
+        capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(T(kp)),
+        capi.p(T(kn)), capi.p(T(vp)), capi.p(T(vn)), capi.i64(Tm), capi.p(T(np.asarray(seq_lens, np.int32))),
+        capi.p(T(kc)), capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(kb), capi.i32(vb),
+        ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
+        capi.stream()))
+    sync()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
+@pytest.mark.parametrize("d,kb,vb,G,bs,qdt", [(64, 4, 2, 4, 16, torch.bfloat16),
+                                              (64, 3, 1, 2, 64, torch.float16),
+                                              (64, 4, 2, 1, 8, torch.bfloat16),
+                                              (128, 4, 2, 2, 16, torch.bfloat16),   # gathered path
+                                              (64, 4, 2, 4, 16, torch.float32)])    # gathered path
+def test_decode_paged_vs_contiguous_and_f64(d, kb, vb, G, bs, qdt):
+    rs = np.random.RandomState(d + kb * 10 + bs)
+    Hkv, B = 2, 4
+    Hq = G * Hkv
+    lens = [0, 3, 700, 1500]
+    width = (max(lens) + bs - 1) // bs + 1
+    nb = sum((n + bs - 1) // bs for n in lens) + 5
+    tab = _tables(rs, lens, bs, nb, width)
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    _, ck = O.lloyd_max_codebook(kb, d)
+    _, cv = O.lloyd_max_codebook(vb, d)
+    bpp = d // 8
+    kpool = rs.randint(0, 256, (nb, Hkv, bs, kb * bpp)).astype(np.uint8)
+    vpool = rs.randint(0, 256, (nb, Hkv, bs, vb * bpp)).astype(np.uint8)
+    knp = rs.uniform(0.5, 2.0, (nb, Hkv, bs)).astype(np.float32)
+    vnp = rs.uniform(0.5, 2.0, (nb, Hkv, bs)).astype(np.float32)
+    q = torch.from_numpy(rs.randn(B, Hq, d).astype(np.float32)).to(DEV).to(qdt)
+    scale = 1.0 / math.sqrt(d)
+    got, lse = k_decode_paged(q, kpool, knp, vpool, vnp, tab, lens, ck, cv, Rk, Rv, kb, vb, scale)
+    # the same tokens laid out contiguously, through the contiguous decode entry point
+    Tm = width * bs
+    kc_, kn_, vc_, vn_ = (np.zeros((B, Hkv, Tm) + p.shape[3:], p.dtype) for p in (kpool, knp, vpool, vnp))
+    for b, n in enumerate(lens):
+        for arr, pool in ((kc_, kpool), (kn_, knp), (vc_, vpool), (vn_, vnp)):
+            arr[b, :, :n] = O.paged_rows(pool, tab[b], n)
+    ref, ref_lse = k_decode(q, kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv, kb, vb, scale)
+    if d == 64 and qdt != torch.float32:   # same fused kernel and split plan: identical sums
+        assert np.array_equal(got, ref) and np.array_equal(lse, ref_lse)
+    else:
+        assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    want = O.decode_attention_f64(q.float().cpu().numpy(), kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv,
+                                  kb, vb, scale)
+    assert np.all(got[0] == 0)
+    tol = 1e-2 if qdt != torch.float32 else 1e-3
+    assert np.max(np.abs(got - want)) <= tol * np.max(np.abs(want))
+
+
+def _step_meta(blocks, before, n_new, bs):
+    """One vLLM-ordered batch: sequences with n_new > 1 are prefills (listed first), the
+    rest decode one token.  blocks[i] = sequence i's physical blocks for all its tokens."""
+    from turboquant_kv.vllm_plugin import TurboQuantAttentionMetadata
+    order = sorted(range(len(n_new)), key=lambda i: n_new[i] == 1)
+    width = max(len(b) for b in blocks)
+    tab = np.full((len(order), width), -1, np.int32)
+    slots, qsl, lens = [], [0], []
+    for j, i in enumerate(order):
+        tab[j, :len(blocks[i])] = blocks[i]
+        lens.append(before[i] + n_new[i])
+        slots += [blocks[i][t // bs] * bs + t % bs for t in range(before[i], lens[-1])]
+        qsl.append(qsl[-1] + n_new[i])
+    md = TurboQuantAttentionMetadata(
+        slot_mapping=torch.tensor(slots, dtype=torch.long, device=DEV),
+        seq_lens=torch.tensor(lens, dtype=torch.int32, device=DEV),
+        block_tables=torch.from_numpy(tab).to(DEV),
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32),
+        num_prefills=sum(1 for i in order if n_new[i] > 1))
+    return md, order, lens, tab
+
+
+@pytest.mark.parametrize("mode,kb,vb,d,G", [("mse", 4, 2, 64, 4), ("mse", 3, 2, 128, 2),
+                                            ("prod", 4, 3, 64, 2)])
+def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G):
+    # Two steps through the vLLM entry: a batch of prompts (prefill), then a mixed batch
+    # -- a chunked prefill continuing one sequence and single-token decodes of the
+    # others -- each checked against the float64 paged oracle (causal, GQA).
+    from turboquant_kv.vllm_plugin import (TurboQuantKVCacheConfig, TurboQuantPagedKVCache,
+                                           paged_attention_step)
+    rs = np.random.RandomState(kb * 7 + d)
+    Hkv, bs, nb = 2, 16, 64
+    Hq = G * Hkv
+    cfg = TurboQuantKVCacheConfig(key_bits=kb, value_bits=vb, mode=mode, block_size=bs,
+                                  num_gpu_blocks=nb)
+    kv = TurboQuantPagedKVCache(cfg, num_layers=1, num_heads=Hkv, head_dim=d, device=DEV)
+    pools = kv.pools()
+    scale = 1.0 / math.sqrt(d)
+    steps = [[40, 17, 70, 5], [30, 1, 1, 1]]   # new tokens per sequence in each step
+    final = [sum(s[i] for s in steps) for i in range(4)]
+    perm = [int(b) for b in rs.permutation(nb)]
+    blocks, used = [], 0
+    for n in final:
+        k = (n + bs - 1) // bs
+        blocks.append(perm[used:used + k])
+        used += k
+    before = [0, 0, 0, 0]
+    for step, n_new in enumerate(steps):
+        md, order, lens, tab = _step_meta(blocks, before, n_new, bs)
+        n_tok = sum(n_new)
+        q = torch.randn(n_tok, Hq, d, device=DEV, dtype=torch.bfloat16)
+        k = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)
+        v = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)
+        out = paged_attention_step(q, k, v, kv, md, scale)
+        assert out.shape == q.shape and out.dtype == q.dtype
+        P = {key: t.cpu().numpy() for key, t in pools.layers[0].items()}
+        kc, vc = pools.kcen.cpu().numpy(), pools.vcen.cpu().numpy()
+        Rk, Rv = pools.R_k.cpu().numpy(), pools.R_v.cpu().numpy()
+        kprod = vprod = None
+        if mode == "prod":
+            kprod = (P["ks"], P["kr"], pools.S_k.cpu().numpy())
+            vprod = (P["vs"], P["vr"], pools.S_v.cpu().numpy())
+        qsl = md.query_start_loc.tolist()
+        for j in range(len(order)):
+            a, b = qsl[j], qsl[j + 1]
+            want = O.paged_attention_f64(q[a:b].float().cpu().numpy(), P["k"], P["kn"], P["v"],
+                                         P["vn"], tab[j], lens[j], kc, vc, Rk, Rv,
+                                         pools.kbits if mode == "mse" else kb,
+                                         pools.vbits if mode == "mse" else vb, scale, kprod, vprod)
+            got = out[a:b].float().cpu().numpy()
+            assert np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want)), (step, j)
+        before = [before[i] + n_new[i] for i in range(4)]
+
+
+def test_vllm_paged_protected_layer_and_padding():
+    from turboquant_kv.vllm_plugin import (TurboQuantAttentionMetadata, TurboQuantKVCacheConfig,
+                                           TurboQuantPagedKVCache, paged_attention_step)
+    rs = np.random.RandomState(3)
+    Hkv, Hq, d, bs, nb = 2, 4, 64, 16, 16
+    cfg = TurboQuantKVCacheConfig(key_bits=4, value_bits=2, block_size=bs, num_gpu_blocks=nb,
+                                  protected_layers=1)
+    kv = TurboQuantPagedKVCache(cfg, num_layers=2, num_heads=Hkv, head_dim=d, device=DEV)
+    tab = np.array([[5, 2, 9]], np.int32)
+    n = 35
+    slots = [tab[0, t // bs] * bs + t % bs for t in range(n)] + [-1, -1]   # two padding tokens
+    q = torch.randn(n + 2, Hq, d, device=DEV)
+    k = torch.randn(n + 2, Hkv, d, device=DEV)
+    v = torch.randn(n + 2, Hkv, d, device=DEV)
+    md = TurboQuantAttentionMetadata(torch.tensor(slots, device=DEV), torch.tensor([n], dtype=torch.int32),
+                                     torch.from_numpy(tab).to(DEV), torch.tensor([0, n]), 1, layer_id=0)
+    out = paged_attention_step(q, k, v, kv, md, 0.125)
+    # protected layer: fp16 K/V, causal softmax attention in float64
+    qf = q[:n].double().transpose(0, 1).contiguous()                          # [Hq, n, d]
+    kf = k[:n].half().double().repeat_interleave(2, dim=1).transpose(0, 1).contiguous()
+    vf = v[:n].half().double().repeat_interleave(2, dim=1).transpose(0, 1).contiguous()
+    s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * 0.125
+    s = s.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool, device=DEV), 1), float("-inf"))
+    want = torch.matmul(torch.softmax(s, -1), vf).transpose(0, 1)
+    assert (out[:n].double() - want).abs().max().item() <= 1e-4 * want.abs().max().item()
+    # padding slots wrote nothing: only the sequence's three blocks hold data
+    fp = kv.pools().layers[0]["k_fp"]
+    used = torch.zeros(nb, dtype=torch.bool)
+    used[[5, 2, 9]] = True
+    assert fp[~used.to(DEV)].abs().sum().item() == 0

@@ -324,3 +324,62 @@ def test_cache_fixture_matches_oracle(golden):
                                  c["val_packed"][None], c["val_norms"][None], [128], ck, cv, R, Rv,
                                  4, 2, 1 / 8)
     assert np.max(np.abs(out[0] - c["output"][:, 0])) <= 1e-5 * np.max(np.abs(c["output"]))
+
+
+# ------------------------------------------------------------------ paged KV
+def _to_pool(rows, bs, table, nblocks):
+    """[H, T, ...] rows -> a pool [nblocks, H, bs, ...] holding token t in block
+    table[t // bs] at slot t % bs (a plain loop, independent of paged_rows)."""
+    H, T = rows.shape[:2]
+    pool = np.zeros((nblocks, H, bs) + rows.shape[2:], rows.dtype)
+    for t in range(T):
+        pool[table[t // bs], :, t % bs] = rows[:, t]
+    return pool
+
+
+def test_paged_oracle_matches_reference_cache_output(golden):
+    # The reference's own QuantizedKVCache output (128 tokens, 4 heads) from rows placed
+    # in scattered blocks of 16: one new token at position 127 sees every token.
+    c, rot = golden("cache"), golden("rotation")
+    R, Rv = rot["R_d64_s42"], rot["R_d64_s43"]
+    _, ck = O.lloyd_max_codebook(4, 64)
+    _, cv = O.lloyd_max_codebook(2, 64)
+    table = np.random.RandomState(0).permutation(20)[:8]
+    pools = [_to_pool(c[k], 16, table, 20) for k in ("key_packed", "key_norms", "val_packed", "val_norms")]
+    out = O.paged_attention_f64(c["query"][:, 0][None], *pools, table, 128, ck, cv, R, Rv, 4, 2, 1 / 8)
+    assert np.max(np.abs(out[0] - c["output"][:, 0])) <= 1e-5 * np.max(np.abs(c["output"]))
+
+
+def test_paged_oracle_causal_rows_and_block_invariance(golden):
+    c, rot = golden("cache"), golden("rotation")
+    R, Rv = rot["R_d64_s42"], rot["R_d64_s43"]
+    _, ck = O.lloyd_max_codebook(4, 64)
+    _, cv = O.lloyd_max_codebook(2, 64)
+    rs = np.random.RandomState(1)
+    q = rs.randn(6, 8, 64)                       # 6 new tokens, 8 query heads on 4 kv heads (GQA)
+    T = 100
+    keys = ("key_packed", "key_norms", "val_packed", "val_norms")
+    t1 = rs.permutation(16)[:7]
+    t2 = rs.permutation(16)[:7]
+    p1 = [_to_pool(c[k][:, :T], 16, t1, 16) for k in keys]
+    p2 = [_to_pool(c[k][:, :T], 16, t2, 16) for k in keys]
+    a = O.paged_attention_f64(q, *p1, t1, T, ck, cv, R, Rv, 4, 2, 0.125)
+    b = O.paged_attention_f64(q, *p2, t2, T, ck, cv, R, Rv, 4, 2, 0.125)
+    assert np.allclose(a, b, rtol=0, atol=1e-12)            # physical placement is invisible
+    # row i = one-token decode over the first T-6+i+1 tokens, kv head h // 2
+    for i in range(6):
+        vis = T - 6 + i + 1
+        qq = q[i][None]
+        dec = O.decode_attention_f64(qq, c["key_packed"][None, :, :vis],
+                                     c["key_norms"][None, :, :vis], c["val_packed"][None, :, :vis],
+                                     c["val_norms"][None, :, :vis], [vis], ck, cv, R, Rv, 4, 2, 0.125)
+        assert np.allclose(a[i], dec[0], rtol=0, atol=1e-10), i
+    # a planted mistake -- tokens addressed as (slot, block) instead of (block, slot) --
+    # reorders the context, which the causal rows see
+    def swapped(x):
+        return np.swapaxes(x.reshape(4, 6, 16, *x.shape[2:]), 1, 2).reshape(x.shape)
+    right = O.paged_attention_f64(q, *[_to_pool(c[k][:, :96], 16, t1, 16) for k in keys],
+                                  t1, 96, ck, cv, R, Rv, 4, 2, 0.125)
+    wrong = O.paged_attention_f64(q, *[_to_pool(swapped(c[k][:, :96]), 16, t1, 16) for k in keys],
+                                  t1, 96, ck, cv, R, Rv, 4, 2, 0.125)
+    assert np.max(np.abs(wrong - right)) > 1e-3

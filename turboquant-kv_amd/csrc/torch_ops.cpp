@@ -555,6 +555,127 @@ at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacke
                                                  kbits, vbits, scale));
 }
 
+// ------------------------------------------------------------ paged pools (vLLM block tables)
+
+// rows [n, hkv, P] u8 (+ norms [n, hkv] f32) to the slots slot_mapping [n] of
+// pool [num_blocks, hkv, block_size, P] (+ norm_pool [num_blocks, hkv, block_size]).
+void paged_store(const at::Tensor& rows, const c10::optional<at::Tensor>& norms,
+                 const at::Tensor& slot_mapping, at::Tensor& pool,
+                 const c10::optional<at::Tensor>& norm_pool) {
+  require_gpu(pool, "pool");
+  TORCH_CHECK(pool.dim() == 4 && pool.scalar_type() == at::kByte && pool.is_contiguous(),
+              "pool must be contiguous uint8 [num_blocks, hkv, block_size, P]");
+  TORCH_CHECK(rows.dim() == 3 && rows.scalar_type() == at::kByte, "rows must be uint8 [n, hkv, P]");
+  TORCH_CHECK(norms.has_value() == norm_pool.has_value(), "norms and norm_pool go together");
+  c10::DeviceGuard g(pool.device());
+  const auto dev = pool.device();
+  const int64_t n = rows.size(0), hkv = pool.size(1), bs = pool.size(2), P = pool.size(3);
+  TORCH_CHECK(rows.size(1) == hkv && rows.size(2) == P, "rows must be [n, hkv, P] of the pool's hkv, P");
+  auto r = rows.to(dev).contiguous();
+  auto sm = slot_mapping.to(dev, at::kLong).contiguous();
+  TORCH_CHECK(sm.numel() == n, "slot_mapping must have one entry per token");
+  at::Tensor nm, np;
+  if (norms.has_value()) {
+    nm = f32c(*norms, dev);
+    np = *norm_pool;
+    TORCH_CHECK(nm.numel() == n * hkv, "norms must be [n, hkv]");
+    TORCH_CHECK(np.device() == dev && np.scalar_type() == at::kFloat && np.is_contiguous() &&
+                    np.numel() == pool.size(0) * hkv * bs,
+                "norm_pool must be contiguous float32 [num_blocks, hkv, block_size]");
+  }
+  check_rc(tq_paged_store(r.data_ptr<uint8_t>(), nm.defined() ? nm.data_ptr<float>() : nullptr, n,
+                          (int32_t)hkv, (int32_t)P, sm.data_ptr<int64_t>(), pool.data_ptr<uint8_t>(),
+                          np.defined() ? np.data_ptr<float>() : nullptr, pool.size(0), (int32_t)bs,
+                          cur_stream(pool)));
+}
+
+// The first seq_lens[b] tokens of each batch row as contiguous [B, hkv, t_max, P] rows
+// (+ [B, hkv, t_max] norms; empty without norm_pool).
+std::tuple<at::Tensor, at::Tensor> paged_gather(const at::Tensor& pool,
+                                                const c10::optional<at::Tensor>& norm_pool,
+                                                const at::Tensor& block_tables,
+                                                const at::Tensor& seq_lens, int64_t t_max) {
+  require_gpu(pool, "pool");
+  TORCH_CHECK(pool.dim() == 4 && pool.scalar_type() == at::kByte && pool.is_contiguous(),
+              "pool must be contiguous uint8 [num_blocks, hkv, block_size, P]");
+  c10::DeviceGuard g(pool.device());
+  const auto dev = pool.device();
+  const int64_t hkv = pool.size(1), bs = pool.size(2), P = pool.size(3);
+  auto bt = block_tables.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(bt.dim() == 2, "block_tables must be [B, max_blocks]");
+  auto sl = seq_lens.to(dev, at::kInt).contiguous();
+  const int64_t B = bt.size(0);
+  TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  auto rows = at::empty({B, hkv, t_max, P}, pool.options());
+  at::Tensor np, on;
+  if (norm_pool.has_value()) {
+    np = *norm_pool;
+    TORCH_CHECK(np.device() == dev && np.scalar_type() == at::kFloat && np.is_contiguous() &&
+                    np.numel() == pool.size(0) * hkv * bs,
+                "norm_pool must be contiguous float32 [num_blocks, hkv, block_size]");
+    on = at::empty({B, hkv, t_max}, pool.options().dtype(at::kFloat));
+  } else {
+    on = at::empty({0}, pool.options().dtype(at::kFloat));
+  }
+  check_rc(tq_paged_gather(pool.data_ptr<uint8_t>(), np.defined() ? np.data_ptr<float>() : nullptr,
+                           pool.size(0), (int32_t)hkv, (int32_t)bs, (int32_t)P, bt.data_ptr<int32_t>(),
+                           (int32_t)bt.size(1), sl.data_ptr<int32_t>(), (int32_t)B, t_max,
+                           rows.data_ptr<uint8_t>(), np.defined() ? on.data_ptr<float>() : nullptr,
+                           cur_stream(pool)));
+  return {rows, on};
+}
+
+std::tuple<at::Tensor, at::Tensor> decode_attention_paged(
+    const at::Tensor& q, const at::Tensor& kpool, const at::Tensor& knorm_pool,
+    const at::Tensor& vpool, const at::Tensor& vnorm_pool, const at::Tensor& block_tables,
+    const at::Tensor& seq_lens, const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+    const at::Tensor& krotation, const at::Tensor& vrotation, int64_t kbits, int64_t vbits,
+    double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
+  TORCH_CHECK(kpool.dim() == 4 && vpool.dim() == 4, "pools must be [num_blocks, hkv, block_size, P]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  const int64_t B = qq.size(0), Hq = qq.size(1), d = qq.size(2);
+  const int64_t nb = kpool.size(0), Hkv = kpool.size(1), bs = kpool.size(2);
+  for (const at::Tensor* t : {&kpool, &vpool, &knorm_pool, &vnorm_pool})
+    TORCH_CHECK(t->device() == dev && t->is_contiguous(), "pools must be contiguous on the query's device");
+  TORCH_CHECK(kpool.scalar_type() == at::kByte && vpool.scalar_type() == at::kByte, "pools must be uint8");
+  TORCH_CHECK(vpool.size(0) == nb && vpool.size(1) == Hkv && vpool.size(2) == bs, "K/V pool shapes differ");
+  TORCH_CHECK(kpool.size(3) == packed_width(kbits, d) && vpool.size(3) == packed_width(vbits, d),
+              "pool row widths must be bits * ceil(d/8)");
+  TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
+                  knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
+              "norm pools must be float32 [num_blocks, hkv, block_size]");
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "num_heads must be a multiple of num_kv_heads");
+  auto bt = block_tables.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(bt.dim() == 2 && bt.size(0) == B, "block_tables must be [B, max_blocks]");
+  auto sl = seq_lens.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  auto kc = f32c(kcentroids, dev);
+  auto vc = f32c(vcentroids, dev);
+  auto Rk = f32c(krotation, dev);
+  auto Rv = f32c(vrotation, dev);
+  TORCH_CHECK(kc.numel() == (1 << kbits) && vc.numel() == (1 << vbits), "centroid lengths");
+  auto out = at::empty({B, Hq, d}, qq.options());
+  auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
+  if (B == 0) return {out, lse};
+  const tq_dtype qdt = to_tq(qq.scalar_type());
+  auto ws = workspace(tq_decode_paged_workspace_bytes(qdt, (int32_t)B, (int32_t)Hq, (int32_t)Hkv,
+                                                      (int32_t)d, (int32_t)kbits, (int32_t)vbits,
+                                                      (int32_t)bt.size(1), (int32_t)bs),
+                      dev);
+  check_rc(tq_decode_attention_paged(
+      qq.data_ptr(), qdt, (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
+      kpool.data_ptr<uint8_t>(), knorm_pool.data_ptr<float>(), vpool.data_ptr<uint8_t>(),
+      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, bt.data_ptr<int32_t>(), (int32_t)bt.size(1),
+      sl.data_ptr<int32_t>(), kc.data_ptr<float>(), vc.data_ptr<float>(), Rk.data_ptr<float>(),
+      Rv.data_ptr<float>(), (int32_t)kbits, (int32_t)vbits, (float)scale, out.data_ptr(),
+      lse.data_ptr<float>(), ws.data_ptr(), ws.numel(), cur_stream(qq)));
+  return {out, lse};
+}
+
 // ------------------------------------------------------------ decode layout
 
 void pack_decode_layout(const at::Tensor& packed, at::Tensor& cache, int64_t dim,
@@ -672,6 +793,14 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor rotation, int k) -> (Tensor, Tensor)");
   m.def("attention_scores_pairs(Tensor query, Tensor pairs, Tensor key_norms, Tensor centroids,"
         " Tensor rotation) -> Tensor");
+  m.def("paged_store(Tensor rows, Tensor? norms, Tensor slot_mapping, Tensor(a!) pool,"
+        " Tensor(b!)? norm_pool) -> ()");
+  m.def("paged_gather(Tensor pool, Tensor? norm_pool, Tensor block_tables, Tensor seq_lens,"
+        " int t_max) -> (Tensor, Tensor)");
+  m.def("decode_attention_paged(Tensor q, Tensor kpool, Tensor knorm_pool, Tensor vpool,"
+        " Tensor vnorm_pool, Tensor block_tables, Tensor seq_lens, Tensor kcentroids,"
+        " Tensor vcentroids, Tensor krotation, Tensor vrotation, int kbits, int vbits,"
+        " float scale) -> (Tensor, Tensor)");
   m.def("ip_scan_topk_prod(Tensor queries, Tensor mse_packed, Tensor signs, Tensor res_norms,"
         " Tensor norms, Tensor centroids, Tensor rotation, Tensor qjl, int bit_width, int k)"
         " -> (Tensor, Tensor)");
@@ -710,6 +839,9 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("ip_scan_topk_pairs", &ip_scan_topk_pairs);
   m.impl("attention_scores_pairs", &attention_scores_pairs);
   m.impl("ip_scan_topk_prod", &ip_scan_topk_prod);
+  m.impl("paged_store", &paged_store);
+  m.impl("paged_gather", &paged_gather);
+  m.impl("decode_attention_paged", &decode_attention_paged);
   m.impl("attention_scores_prod", &attention_scores_prod);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);

@@ -68,6 +68,13 @@ struct DecodeArgs {
   int nsplit;
   float* part;           // [B*hq][nsplit][64]: sum_t 2^(s_t - max) |v_t| c[code_t]
   float2* stats;         // [B*hq][nsplit]: (max, sum_t 2^(s_t - max)), log2 domain
+  // Paged caches (PAGED kernels): K/V rows and norms live in block pools
+  // [num_blocks][hkv][block_size][row] and token t of batch row b sits in block
+  // block_tables[b * bt_stride + t / block_size], slot t % block_size.
+  const int32_t* block_tables;
+  int bt_stride;
+  int bs_log2;           // log2(block_size), block_size >= 4
+  uint32_t pool_rows;    // num_blocks * hkv * block_size
 };
 
 // Raw buffer resource over `bytes` bytes at `p` (gfx9 dword 3); loads past the end
@@ -108,7 +115,7 @@ __device__ __forceinline__ uint32_t quad_transpose(uint32_t x, uint32_t sel1, ui
   return perm(yp, y, sel2);
 }
 
-template <int KB, int VB>
+template <int KB, int VB, bool PAGED = false>
 __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs a) {
   constexpr int PK = KB * 8, PV = VB * 8;  // packed row bytes (d = 64)
   // Tables first; after the tile loop the same bytes hold the cross-quad reduction.
@@ -180,13 +187,22 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
   const uint32_t copy = (uint32_t)(lane & 15) * 8;
   const uint32_t sel1 = hn < 2 ? 0x05040100u : 0x03020706u;
   const uint32_t sel2 = (hn & 1) ? 0x03070105u : 0x06020400u;
-  // Per-stream buffers cover exactly the split's valid tokens: rows and norms past
-  // t_end read as zero (and are masked), so no load needs a clamp or a branch.
-  const size_t sbase = (size_t)bg * (size_t)a.t_max;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpacked + sbase * PK, (uint32_t)t_end * PK);
-  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.vpacked + sbase * PV, (uint32_t)t_end * PV);
-  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, (uint32_t)t_end * 4);
-  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, (uint32_t)t_end * 4);
+  // Contiguous caches: per-stream buffers cover exactly the split's valid tokens, so
+  // rows and norms past t_end read as zero (and are masked) -- no load needs a clamp or
+  // a branch.  Paged caches: the buffers cover the whole pools; a token's row index
+  // comes from the block table, whose buffer covers the blocks holding tokens below
+  // t_end (entries past it read as block 0: rows that are loaded and masked).  Block
+  // ids outside the pool address rows outside the buffer, which read as zero.
+  const size_t sbase = PAGED ? 0 : (size_t)bg * (size_t)a.t_max;
+  const uint32_t nrec = PAGED ? a.pool_rows : (uint32_t)t_end;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpacked + sbase * PK, nrec * PK);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.vpacked + sbase * PV, nrec * PV);
+  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nrec * 4);
+  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nrec * 4);
+  const int bsl = PAGED ? a.bs_log2 : 0;
+  const __amdgpu_buffer_rsrc_t btrs =
+      make_rsrc(PAGED ? a.block_tables + (size_t)b * a.bt_stride : a.seq_lens,
+                PAGED ? (uint32_t)(((t_end + (1 << bsl) - 1) >> bsl) * 4) : 0u);
   const int te = (int)t_end;
 
   struct Tile {
@@ -194,11 +210,24 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
     uint32_t v[PV / 4];
     float kn[4], vn[4];
   };
-  auto load_tile = [&](int t0, Tile& x) {
-    const uint32_t tr = (uint32_t)(t0 + lane);
+  // Paged: block id of token t0 + lane, loaded a tile ahead of its rows.
+  auto load_block = [&](int t0) -> uint32_t {
+    if constexpr (!PAGED) return 0u;
+    return __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)(t0 + lane) >> bsl) * 4), 0, 0);
+  };
+  auto load_tile = [&](int t0, Tile& x, uint32_t blk) {
+    uint32_t tr, nr;
+    if constexpr (PAGED) {
+      // the lane quad's four tokens share a block (block_size >= 4, t0 % 4 == 0)
+      tr = ((blk * (uint32_t)a.hkv + (uint32_t)g) << bsl) | ((uint32_t)(t0 + lane) & ((1u << bsl) - 1));
+      nr = tr - (uint32_t)hn;
+    } else {
+      tr = (uint32_t)(t0 + lane);
+      nr = (uint32_t)(t0 + 4 * quad);
+    }
     load_row<PK>(krs, tr * PK, x.k);
     load_row<PV>(vrs, tr * PV, x.v);
-    const uint32_t no = (uint32_t)(t0 + 4 * quad) * 4;
+    const uint32_t no = nr * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       x.kn[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(knrs, (int)no, 4 * r, 0));
@@ -214,10 +243,15 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
 
   int t0 = (int)t_begin + wave * 64;
   Tile cur, nxt;
-  if (t0 < te) load_tile(t0, cur);
+  uint32_t blk_nxt = 0;
+  if (t0 < te) {
+    load_tile(t0, cur, load_block(t0));
+    blk_nxt = load_block(t0 + kDecWaves * 64);
+  }
   while (t0 < te) {
     const int tn = t0 + kDecWaves * 64;
-    load_tile(tn, nxt);
+    load_tile(tn, nxt, blk_nxt);
+    blk_nxt = load_block(tn + kDecWaves * 64);
 
     // ---- q.K: octet words [plane3 | plane2 | plane1 | plane0] bytes
     uint32_t W[8];
@@ -1045,10 +1079,10 @@ bool fused_enabled() {
   return on;
 }
 
-template <int KB>
+template <int KB, bool PAGED = false>
 int launch_kb(int vb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
-  if (vb == 1) hipLaunchKernelGGL((fused_decode_kernel<KB, 1>), grid, dim3(kDecThreads), 0, st, a);
-  else hipLaunchKernelGGL((fused_decode_kernel<KB, 2>), grid, dim3(kDecThreads), 0, st, a);
+  if (vb == 1) hipLaunchKernelGGL((fused_decode_kernel<KB, 1, PAGED>), grid, dim3(kDecThreads), 0, st, a);
+  else hipLaunchKernelGGL((fused_decode_kernel<KB, 2, PAGED>), grid, dim3(kDecThreads), 0, st, a);
   TQ_LAUNCH_CHECK("fused_decode_kernel");
   return TQ_OK;
 }
@@ -1080,7 +1114,7 @@ size_t fused_decode_workspace_bytes(int B, int hq, int d, int64_t t_max) {
 }
 
 int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t workspace_bytes,
-                        hipStream_t st) {
+                        hipStream_t st, const PagedPools* pg) {
   const SplitPlan p = plan_splits(c.B, c.hkv, c.t_max);
   const size_t rows = (size_t)c.B * c.hq;
   const size_t part_bytes = align_up(rows * p.nsplit * kDim * 4, 256);
@@ -1097,11 +1131,22 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
   a.stats = reinterpret_cast<float2*>(ws + part_bytes);
   const dim3 grid((unsigned)p.nsplit, (unsigned)(c.B * c.hkv));
   int rc = TQ_OK;
-  switch (c.kbits) {
-    case 1: rc = launch_kb<1>(c.vbits, grid, a, st); break;
-    case 2: rc = launch_kb<2>(c.vbits, grid, a, st); break;
-    case 3: rc = launch_kb<3>(c.vbits, grid, a, st); break;
-    default: rc = launch_kb<4>(c.vbits, grid, a, st); break;
+  if (pg) {
+    a.block_tables = pg->block_tables; a.bt_stride = pg->bt_stride; a.bs_log2 = pg->bs_log2;
+    a.pool_rows = pg->pool_rows;
+    switch (c.kbits) {
+      case 1: rc = launch_kb<1, true>(c.vbits, grid, a, st); break;
+      case 2: rc = launch_kb<2, true>(c.vbits, grid, a, st); break;
+      case 3: rc = launch_kb<3, true>(c.vbits, grid, a, st); break;
+      default: rc = launch_kb<4, true>(c.vbits, grid, a, st); break;
+    }
+  } else {
+    switch (c.kbits) {
+      case 1: rc = launch_kb<1>(c.vbits, grid, a, st); break;
+      case 2: rc = launch_kb<2>(c.vbits, grid, a, st); break;
+      case 3: rc = launch_kb<3>(c.vbits, grid, a, st); break;
+      default: rc = launch_kb<4>(c.vbits, grid, a, st); break;
+    }
   }
   if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, a.part,

@@ -131,3 +131,30 @@ def decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids
                                               float(scale))
     return _ops().decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids,
                                       vcentroids, krotation, vrotation, float(scale))
+
+
+def paged_store(rows, norms, slot_mapping, pool, norm_pool):
+    """Scatter rows [n, hkv, P] (+ norms [n, hkv]) to the flat slots slot_mapping [n] of a
+    block pool [num_blocks, hkv, block_size, P] (+ [num_blocks, hkv, block_size]); slots
+    outside the pool (vLLM's -1 padding) are skipped."""
+    _require_device(pool, "pool")
+    _ops().paged_store(rows, norms, slot_mapping, pool, norm_pool)
+
+
+def paged_gather(pool, norm_pool, block_tables, seq_lens, t_max):
+    """Rows [B, hkv, t_max, P] and norms [B, hkv, t_max] of each sequence's first
+    seq_lens[b] tokens, read through block_tables [B, max_blocks] (zeros past the end)."""
+    _require_device(pool, "pool")
+    return _ops().paged_gather(pool, norm_pool, block_tables, seq_lens, t_max)
+
+
+def decode_attention_paged(q, kpool, knorm_pool, vpool, vnorm_pool, block_tables, seq_lens,
+                           kcentroids, vcentroids, krotation, vrotation, kbits, vbits, scale,
+                           return_lse=False):
+    """decode_attention_packed over paged block pools: batch row b attends to its first
+    seq_lens[b] tokens, found through block_tables [B, max_blocks]."""
+    _require_device(q, "q")
+    out, lse = _ops().decode_attention_paged(q, kpool, knorm_pool, vpool, vnorm_pool, block_tables,
+                                             seq_lens, kcentroids, vcentroids, krotation, vrotation,
+                                             kbits, vbits, scale)
+    return (out, lse) if return_lse else out

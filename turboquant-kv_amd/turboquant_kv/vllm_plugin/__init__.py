@@ -10,6 +10,12 @@ Differences from the reference, all on the compute side: the cache lives in pack
 device storage and is read by the HIP kernels (no per-step dequantization); query heads
 may be a multiple of the KV heads (grouped-query attention, which the reference cannot
 express, cache.py:294-307); a single-token step runs the fused decode kernel.
+
+Paged operation (what vLLM's cache engine and scheduler provide, which the reference's
+backend ignores): TurboQuantPagedKVCache.pools() holds K/V in block pools
+(vllm_plugin/paged.py), and TurboQuantAttentionImpl.forward with metadata that carries
+`block_tables` and `slot_mapping` stores the new tokens at their slots, runs causal
+prefill per prefill sequence and one paged decode launch for the decode sequences.
 """
 
 from __future__ import annotations
@@ -22,6 +28,7 @@ import torch
 
 from turboquant_kv.cache import QuantizedKVCache
 from turboquant_kv.config import TurboQuantConfig
+from turboquant_kv.vllm_plugin.paged import PagedKVPools, TurboQuantAttentionMetadata
 
 _VLLM_AVAILABLE = False
 try:  # pragma: no cover - vLLM is not installed in this image
@@ -78,10 +85,10 @@ class TurboQuantPagedKVCache:
         self.block_size = config.block_size
         self._total_blocks = config.num_gpu_blocks
         self._max_tokens = self._total_blocks * self.block_size
+        # The single-sequence cache of the reference's API (append / attention_scores /
+        # attention_values) and the paged pools are each built on first use.
         self._cache: Optional[QuantizedKVCache] = None
-        if self._max_tokens > 0:
-            self._cache = QuantizedKVCache(self.tq_config, num_layers, self._max_tokens, num_heads,
-                                           head_dim, device=device)
+        self._pools: Optional[PagedKVPools] = None
         self._block_offsets: Dict[int, List[int]] = {}
 
     def allocate(self, num_layers: int, num_heads: int, head_dim: int, num_gpu_blocks: int,
@@ -94,11 +101,24 @@ class TurboQuantPagedKVCache:
         self.dtype, self.device = dtype, torch.device(device)
         self._cache = QuantizedKVCache(self.tq_config, num_layers, self._max_tokens, num_heads,
                                        head_dim, device=device)
+        self._pools = None
 
     def _require(self) -> QuantizedKVCache:
         if self._cache is None:
-            raise RuntimeError("TurboQuantPagedKVCache has not been allocated. Call allocate() first.")
+            if self._max_tokens <= 0:
+                raise RuntimeError("TurboQuantPagedKVCache has not been allocated. Call allocate() first.")
+            self._cache = QuantizedKVCache(self.tq_config, self.num_layers, self._max_tokens,
+                                           self.num_heads, self.head_dim, device=self.device)
         return self._cache
+
+    def pools(self) -> PagedKVPools:
+        """The block pools: num_gpu_blocks blocks of block_size tokens per layer."""
+        if self._pools is None:
+            if self._total_blocks <= 0:
+                raise RuntimeError("TurboQuantPagedKVCache has no blocks. Call allocate() first.")
+            self._pools = PagedKVPools(self.tq_config, self.num_layers, self._total_blocks,
+                                       self.block_size, self.num_heads, self.head_dim, self.device)
+        return self._pools
 
     def append(self, layer_id: int, key: torch.Tensor, value: torch.Tensor) -> None:
         self._require().append(layer_id, key, value)
@@ -114,20 +134,19 @@ class TurboQuantPagedKVCache:
         return self._cache._dequantize_values(layer_id)
 
     def attention_scores(self, layer_id: int, query: torch.Tensor) -> torch.Tensor:
-        if self._cache is None:
-            raise RuntimeError("Cache not allocated.")
-        return self._cache.attention_scores(layer_id, query)
+        return self._require().attention_scores(layer_id, query)
 
     def attention_values(self, layer_id: int, attn_weights: torch.Tensor) -> torch.Tensor:
-        if self._cache is None:
-            raise RuntimeError("Cache not allocated.")
-        return self._cache.attention_values(layer_id, attn_weights)
+        return self._require().attention_values(layer_id, attn_weights)
 
     def get_seq_length(self, layer_id: int) -> int:
         return 0 if self._cache is None else int(self._cache.seq_lens[layer_id].item())
 
     def memory_bytes(self) -> int:
-        return 0 if self._cache is None else self._cache.memory_bytes()
+        """Packed bytes of the single-sequence cache (the reference's count); with pools
+        allocated, their bytes are added."""
+        n = 0 if self._cache is None else self._cache.memory_bytes()
+        return n + (0 if self._pools is None else self._pools.memory_bytes())
 
     @property
     def compression_ratio(self) -> float:
@@ -178,6 +197,8 @@ class TurboQuantAttentionImpl(AttentionImpl):
     def forward(self, query, key, value, kv_cache: TurboQuantPagedKVCache, attn_metadata,
                 k_scale: float = 1.0, v_scale: float = 1.0, attn_type: Any = None,
                 output: Optional[torch.Tensor] = None, **kwargs: Any) -> torch.Tensor:  # pragma: no cover
+        if getattr(attn_metadata, "block_tables", None) is not None:
+            return kv_cache.pools().forward(query, key, value, attn_metadata, self.scale, output)
         layer_id: int = getattr(attn_metadata, "layer_id", 0)
         return attention_step(query, key, value, kv_cache, layer_id, self.scale, output)
 
@@ -225,5 +246,13 @@ def register() -> None:
     _REGISTERED = True
 
 
+def paged_attention_step(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                         kv_cache: TurboQuantPagedKVCache, metadata: TurboQuantAttentionMetadata,
+                         scale: float, output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """TurboQuantAttentionImpl.forward on paged metadata, callable without vLLM."""
+    return kv_cache.pools().forward(query, key, value, metadata, scale, output)
+
+
 __all__ = ["TurboQuantKVCacheConfig", "TurboQuantPagedKVCache", "TurboQuantAttentionBackend",
-           "TurboQuantAttentionImpl", "attention_step", "register"]
+           "TurboQuantAttentionImpl", "TurboQuantAttentionMetadata", "PagedKVPools",
+           "attention_step", "paged_attention_step", "register"]
