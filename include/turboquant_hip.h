@@ -311,6 +311,20 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
                               int32_t vbits, float scale, void* out, float* lse, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/*
+ * Host-side tables of the reference's standalone C++ core, for TQIX v1 index files
+ * (turboquant_core.cpp:559-618), which record only (dim, bit_width, seed): the reader
+ * rebuilds the rotation and codebook the writer used.  No device work; outputs are host
+ * memory.  Same matrices and codebooks as the core's, bit for bit.
+ *   tq_core_rotation  replaces turboquant::make_rotation_matrix (turboquant_core.cpp:137-213):
+ *                     out [dim][dim] fp32 row-major (orthonormal columns; scores use
+ *                     q_rot[j] = sum_k q[k] * out[j][k], as search_packed does).
+ *   tq_core_codebook  replaces turboquant::Codebook(bits, dim) (turboquant_core.cpp:71-132):
+ *                     scaled boundaries [2^bits - 1] and centroids [2^bits] fp32.
+ */
+int tq_core_rotation(int32_t dim, int32_t seed, float* out);
+int tq_core_codebook(int32_t bits, int32_t dim, float* boundaries, float* centroids);
+
 #ifdef __cplusplus
 }
 #endif

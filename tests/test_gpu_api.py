@@ -168,6 +168,41 @@ def test_prod_cache_scores_without_reconstruction():
     assert ((logits.double() - ref).abs() <= 1e-4 * scale / math.sqrt(d) + 1e-6).all()
 
 
+def test_tqix_index_from_reference_core_file(golden, tmp_path):
+    # A TQIX file written by the reference's C++ core (TurboQuantIndex::save after add):
+    # loaded here, the GPU scan returns the core's own search results bit for bit, and
+    # save_tqix writes the same bytes back.
+    from turboquant_kv import TurboQuantIndex
+    z = golden("tqix")
+    src = os.path.join(os.path.dirname(__file__), "golden", "core_d64_b3_s7.tqix")
+    idx = TurboQuantIndex.load_tqix(src)
+    assert (idx.dim, idx.bit_width, idx.seed, idx.n_vectors, idx.rotation_method) == (64, 3, 7, 300, "core")
+    s, i = idx.search(T(z["queries"]), k=10)
+    assert np.array_equal(i.cpu().numpy(), z["ids"])
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), z["scores"].view(np.uint32))
+    out = tmp_path / "rt.tqix"
+    idx.save_tqix(str(out))
+    assert out.read_bytes() == open(src, "rb").read()
+    # an index built here with the core's tables: codes equal the core's outside the
+    # fp32 ambiguity band (its quantize multiplies by 1/norm), and TQIX round-trips
+    own = TurboQuantIndex(64, bit_width=3, rotation="core", seed=7)
+    own.add(T(z["vectors"]))
+    got = O.unpack_codes(own._packed_codes.cpu().numpy(), 3, 64)
+    want = O.unpack_codes(open_tqix_codes(src), 3, 64)
+    amb = O.code_margin(z["vectors"], z["R_d64_s7"], z["bnd_b3_d64"])
+    assert not ((got != want) & ~amb).any()
+    own.save_tqix(str(tmp_path / "own.tqix"))
+    back = TurboQuantIndex.load_tqix(str(tmp_path / "own.tqix"))
+    assert torch.equal(back._packed_codes, own._packed_codes) and torch.equal(back._norms, own._norms)
+    with pytest.raises(ValueError, match="core"):
+        TurboQuantIndex(64, bit_width=3).save_tqix(str(tmp_path / "x.tqix"))
+
+
+def open_tqix_codes(path):
+    from turboquant_kv.formats import read_tqix
+    return read_tqix(path).packed
+
+
 def test_cache_vs_reference(golden):
     from turboquant_kv import QuantizedKVCache, TurboQuantConfig
     c = golden("cache")

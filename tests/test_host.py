@@ -80,7 +80,9 @@ def test_torch_ops_schemas_registered():
     for name in ("rotate_and_quantize", "attention_scores_packed", "attention_values_packed",
                  "pack_codes", "unpack_codes", "quantize_mse_packed", "quantize_prod_packed",
                  "dequantize_mse_packed", "dequantize_prod_packed", "ip_scan_topk",
-                 "decode_attention_packed"):
+                 "decode_attention_packed", "ip_scan_topk_prod", "attention_scores_prod",
+                 "paged_store", "paged_gather", "decode_attention_paged", "core_rotation",
+                 "core_codebook"):
         assert hasattr(t, name), name
 
 
@@ -99,3 +101,67 @@ def test_index_file_format_header():
     from turboquant_kv.search import HEADER_FORMAT, HEADER_SIZE
     assert HEADER_FORMAT == "<BII" and HEADER_SIZE == 9
     assert struct.pack(HEADER_FORMAT, 4, 128, 3) == b"\x04\x80\x00\x00\x00\x03\x00\x00\x00"
+
+
+# ------------------------------------------------------------------ TQIX (the C++ core's files)
+@pytest.mark.skipif(not _built(), reason="native library not built")
+def test_core_tables_bit_exact_with_reference_core(golden):
+    # tq_core_rotation / tq_core_codebook (host code) against the matrices and codebooks
+    # the reference's compiled core produced (tests/golden/make_tqix_golden.py)
+    z = golden("tqix")
+    lib = capi.lib()
+    for key in [k for k in z.files if k.startswith("R_d")]:
+        d, seed = (int(v) for v in key[3:].split("_s"))
+        R = np.zeros((d, d), np.float32)
+        assert lib.tq_core_rotation(capi.i32(d), capi.i32(seed), R.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert np.array_equal(R.view(np.uint32), z[key].view(np.uint32)), key
+        assert np.allclose(R.T.astype(np.float64) @ R, np.eye(d), atol=1e-5)
+    for b in (1, 2, 3, 4):
+        for d in (64, 128, 200):
+            bnd = np.zeros((1 << b) - 1, np.float32)
+            cen = np.zeros(1 << b, np.float32)
+            assert lib.tq_core_codebook(capi.i32(b), capi.i32(d), bnd.ctypes.data_as(ctypes.c_void_p),
+                                        cen.ctypes.data_as(ctypes.c_void_p)) == 0
+            assert np.array_equal(bnd.view(np.uint32), z[f"bnd_b{b}_d{d}"].view(np.uint32)), (b, d)
+            assert np.array_equal(cen.view(np.uint32), z[f"cen_b{b}_d{d}"].view(np.uint32)), (b, d)
+    # the same tables through the Python API
+    from turboquant_kv.codebook import core_codebook, make_rotation_matrix
+    assert np.array_equal(make_rotation_matrix(64, 7, "core").numpy(), z["R_d64_s7"])
+    assert np.array_equal(core_codebook(3, 64)[1].numpy(), z["cen_b3_d64"])
+
+
+def test_tqix_read_write_byte_exact_and_errors(tmp_path):
+    from turboquant_kv.formats import TQIX_MAGIC, read_tqix, write_tqix
+    src = os.path.join(os.path.dirname(__file__), "golden", "core_d64_b3_s7.tqix")
+    raw = open(src, "rb").read()
+    assert struct.unpack("<6I", raw[:24]) == (TQIX_MAGIC, 1, 64, 3, 7, 300) and raw[:4] == b"XIQT"
+    f = read_tqix(src)
+    assert (f.dim, f.bit_width, f.seed, f.n_vectors) == (64, 3, 7, 300)
+    assert f.packed.shape == (300, 24) and f.norms.dtype == np.float32
+    assert f.norms[5] == 0.0  # the fixture's zero vector
+    out = tmp_path / "copy.tqix"
+    write_tqix(str(out), f.dim, f.bit_width, f.seed, f.packed, f.norms)
+    assert out.read_bytes() == raw
+    empty = tmp_path / "empty.tqix"
+    write_tqix(str(empty), 128, 4, -1, np.zeros((0, 64), np.uint8), np.zeros(0, np.float32))
+    e = read_tqix(str(empty))
+    assert (e.dim, e.bit_width, e.seed, e.n_vectors) == (128, 4, -1, 0)
+    for name, data, msg in (("magic", b"QTIX" + raw[4:], "bad magic"),
+                            ("version", raw[:4] + struct.pack("<I", 2) + raw[8:], "version"),
+                            ("short", raw[:-1], "truncated"), ("head", raw[:10], "truncated")):
+        p = tmp_path / f"{name}.tqix"
+        p.write_bytes(data)
+        with pytest.raises(ValueError, match=msg):
+            read_tqix(str(p))
+
+
+def test_oracle_reproduces_reference_core_search_on_tqix_file(golden):
+    # the fixture's search results are the core's arithmetic: the oracle's LUT form
+    # (csrc/core/turboquant_core.cpp:407-514) over the file with the core's tables
+    import tq_oracle as O
+    from turboquant_kv.formats import read_tqix
+    z = golden("tqix")
+    f = read_tqix(os.path.join(os.path.dirname(__file__), "golden", "core_d64_b3_s7.tqix"))
+    s, i = O.search_topk(z["queries"], f.packed, f.norms, z["cen_b3_d64"], z["R_d64_s7"], 3, 10)
+    assert np.array_equal(i, z["ids"])
+    assert np.array_equal(s.view(np.uint32), z["scores"].view(np.uint32))

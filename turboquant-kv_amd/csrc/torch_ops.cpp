@@ -555,6 +555,23 @@ at::Tensor decode_attention_packed(const at::Tensor& q, const at::Tensor& kpacke
                                                  kbits, vbits, scale));
 }
 
+// ------------------------------------------------------------ the C++ core's tables (TQIX files)
+
+at::Tensor core_rotation(int64_t dim, int64_t seed) {
+  auto R = at::empty({dim, dim}, at::TensorOptions().dtype(at::kFloat));
+  check_rc(tq_core_rotation((int32_t)dim, (int32_t)seed, R.data_ptr<float>()));
+  return R;
+}
+
+std::tuple<at::Tensor, at::Tensor> core_codebook(int64_t bits, int64_t dim) {
+  TORCH_CHECK(bits >= 1 && bits <= 8, "bits must be in [1, 8]");
+  auto o = at::TensorOptions().dtype(at::kFloat);
+  auto bnd = at::empty({(1 << bits) - 1}, o);
+  auto cen = at::empty({1 << bits}, o);
+  check_rc(tq_core_codebook((int32_t)bits, (int32_t)dim, bnd.data_ptr<float>(), cen.data_ptr<float>()));
+  return {bnd, cen};
+}
+
 // ------------------------------------------------------------ paged pools (vLLM block tables)
 
 // rows [n, hkv, P] u8 (+ norms [n, hkv] f32) to the slots slot_mapping [n] of
@@ -793,6 +810,9 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor rotation, int k) -> (Tensor, Tensor)");
   m.def("attention_scores_pairs(Tensor query, Tensor pairs, Tensor key_norms, Tensor centroids,"
         " Tensor rotation) -> Tensor");
+  // host-side tables (no tensor arguments: registered with catch-all kernels)
+  m.def("core_rotation(int dim, int seed) -> Tensor", &core_rotation);
+  m.def("core_codebook(int bits, int dim) -> (Tensor, Tensor)", &core_codebook);
   m.def("paged_store(Tensor rows, Tensor? norms, Tensor slot_mapping, Tensor(a!) pool,"
         " Tensor(b!)? norm_pool) -> ()");
   m.def("paged_gather(Tensor pool, Tensor? norm_pool, Tensor block_tables, Tensor seq_lens,"

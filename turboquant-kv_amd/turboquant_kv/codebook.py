@@ -54,12 +54,33 @@ def lloyd_max_codebook(bits: int, dim: int) -> Tuple[torch.Tensor, torch.Tensor]
 
 
 def make_rotation_matrix(dim: int, seed: int = 42, method: str = "dense_qr") -> torch.Tensor:
-    """Orthogonal (dim, dim) float32 matrix (reference.py:81-97)."""
+    """Orthogonal (dim, dim) float32 matrix (reference.py:81-97).  method "core" gives the
+    reference C++ core's matrix for the same seed (turboquant_core.cpp:137-213), the one
+    its TQIX index files are written with."""
     if method == "dense_qr":
         return _dense_qr(dim, seed)
     if method == "rht":
         return make_rht_rotation(dim, seed)
+    if method == "core":
+        return core_rotation(dim, seed)
     raise ValueError(f"Unknown rotation method: {method}")
+
+
+def core_rotation(dim: int, seed: int) -> torch.Tensor:
+    """The reference C++ core's rotation (std::mt19937 Gaussian draw, two-pass modified
+    Gram-Schmidt, non-negative diagonal; turboquant_core.cpp:137-213), built by the native
+    library's tq_core_rotation."""
+    from turboquant_kv._lib import ops
+    return ops().core_rotation(dim, seed)
+
+
+@lru_cache(maxsize=16)
+def core_codebook(bits: int, dim: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The reference C++ core's Lloyd-Max codebook (turboquant_core.cpp:71-132), scaled
+    (boundaries[2^b - 1], centroids[2^b]) float32, built by tq_core_codebook.  Shared
+    tensors: do not modify them in place."""
+    from turboquant_kv._lib import ops
+    return tuple(ops().core_codebook(bits, dim))
 
 
 def _dense_qr(dim: int, seed: int) -> torch.Tensor:

@@ -17,7 +17,10 @@ that every code is one masked nibble, which the scan turns into a table address 
 single instruction.  Scores and ids are identical to the bit-plane scan.
 
 save/load use the reference's Python file format (search.py:29-34, 254-317); the pair
-layout is converted back to bit planes on save and from them on load.
+layout is converted back to bit planes on save and from them on load.  save_tqix /
+load_tqix read and write the C++ core's TQIX v1 files (turboquant_core.cpp:559-618):
+rotation="core" builds the core's rotation and codebook for the seed, so an index loaded
+from a file the core wrote returns the core's own search results.
 """
 
 from __future__ import annotations
@@ -30,7 +33,9 @@ import torch
 
 from turboquant_kv import ops
 from turboquant_kv._lib import ops as _ops
-from turboquant_kv.codebook import lloyd_max_codebook, make_qjl_matrix, make_rotation_matrix
+from turboquant_kv.codebook import (core_codebook, lloyd_max_codebook, make_qjl_matrix,
+                                    make_rotation_matrix)
+from turboquant_kv.formats import read_tqix, write_tqix
 
 HEADER_FORMAT = "<BII"  # bit_width u8, dim u32, n_vectors u32
 HEADER_SIZE = struct.calcsize(HEADER_FORMAT)
@@ -51,10 +56,13 @@ class TurboQuantIndex:
         self.seed = seed
         self.device = torch.device(device)
         self._use_cpp = False  # attribute of the reference API; the C++ core is not used
+        if rotation == "core" and mode != "mse":
+            raise ValueError('rotation="core" (the C++ core\'s tables) has no prod mode')
         self._rotation = make_rotation_matrix(dim, seed=seed, method=rotation)
         self._rot_dev = self._rotation.to(self.device)
         if mode == "mse":
-            self._codebook = lloyd_max_codebook(bit_width, dim)
+            self._codebook = (core_codebook(bit_width, dim) if rotation == "core"
+                              else lloyd_max_codebook(bit_width, dim))
             self._code_bits = bit_width
         else:
             self._codebook = lloyd_max_codebook(bit_width - 1, dim)
@@ -218,6 +226,33 @@ class TurboQuantIndex:
                 if self.mode == "prod":
                     f.write(self._qjl_signs.cpu().numpy().tobytes())
                     f.write(self._residual_norms.cpu().numpy().astype(np.float32).tobytes())
+
+    def save_tqix(self, path: str) -> None:
+        """Write the index as a TQIX v1 file (turboquant_core.cpp:559-578).  The file keeps
+        only (dim, bit_width, seed): a reader rebuilds the C++ core's rotation and codebook,
+        so only indexes built with rotation="core" (MSE mode) can be written."""
+        if self.mode != "mse" or self.rotation_method != "core":
+            raise ValueError('TQIX files hold MSE indexes built with rotation="core"')
+        n = self.n_vectors
+        packed = (self._bitplane_codes().cpu().numpy() if n else
+                  np.zeros((0, self._code_bits * ((self.dim + 7) // 8)), np.uint8))
+        norms = self._norms.cpu().numpy() if n else np.zeros(0, np.float32)
+        write_tqix(path, self.dim, self.bit_width, self.seed, packed, norms)
+
+    @classmethod
+    def load_tqix(cls, path: str, device="cuda") -> "TurboQuantIndex":
+        """An index from a TQIX v1 file written by the C++ core (or save_tqix), with the
+        core's rotation and codebook for its seed (turboquant_core.cpp:580-618)."""
+        f = read_tqix(path)
+        idx = cls(dim=f.dim, bit_width=f.bit_width, mode="mse", rotation="core", seed=f.seed,
+                  device=device)
+        n = f.n_vectors
+        if n:
+            idx._reserve(n)
+            idx._store_codes(torch.from_numpy(f.packed).to(idx.device), 0)
+            idx._norm_buf[:n] = torch.from_numpy(f.norms).to(idx.device)
+        idx.n_vectors = n
+        return idx
 
     @classmethod
     def load(cls, path: str, rotation: str = "dense_qr", seed: int = 42,
