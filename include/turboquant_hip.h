@@ -325,6 +325,23 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
 int tq_core_rotation(int32_t dim, int32_t seed, float* out);
 int tq_core_codebook(int32_t bits, int32_t dim, float* boundaries, float* centroids);
 
+/*
+ * Huffman streams of code indices (host memory; the byte format of HuffmanCoder.encode /
+ * decode, turboquant_kv/entropy.py:162-231): uint32 LE symbol count, uint32 LE bit count,
+ * then the code words most significant bit first, zero-padded to a byte.  The caller
+ * supplies the code table (code_words[s] holds code_lens[s] bits, right-aligned).
+ * tq_huffman_encode writes 8 + ceil(bits/8) bytes (*out_bytes; TQ_EINVAL when
+ * out_capacity is smaller).  tq_huffman_decode matches prefixes against the table
+ * (code c -> symbols[c]; a later duplicate entry wins), decodes at most n_symbols (< 0:
+ * the header's count) and sets *n_out to the number decoded.
+ */
+int tq_huffman_encode(const uint8_t* codes, int64_t n, const uint64_t* code_words,
+                      const uint8_t* code_lens, int32_t n_levels, uint8_t* out, size_t out_capacity,
+                      size_t* out_bytes);
+int tq_huffman_decode(const uint8_t* data, size_t data_bytes, int64_t n_symbols,
+                      const uint64_t* code_words, const uint8_t* code_lens, const int32_t* symbols,
+                      int32_t n_codes, uint8_t* out, int64_t* n_out);
+
 #ifdef __cplusplus
 }
 #endif

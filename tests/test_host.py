@@ -165,3 +165,56 @@ def test_oracle_reproduces_reference_core_search_on_tqix_file(golden):
     s, i = O.search_topk(z["queries"], f.packed, f.norms, z["cen_b3_d64"], z["R_d64_s7"], 3, 10)
     assert np.array_equal(i, z["ids"])
     assert np.array_equal(s.view(np.uint32), z["scores"].view(np.uint32))
+
+
+# ------------------------------------------------------------------ Huffman code storage
+@pytest.mark.skipif(not _built(), reason="native library not built")
+def test_huffman_code_words_and_streams_match_reference(golden):
+    # code words and byte streams written by the reference's entropy module
+    # (tests/golden/make_entropy_golden.py)
+    from turboquant_kv.entropy import EntropyPackedStorage, HuffmanCoder, compute_codeword_probabilities
+    z = golden("entropy")
+    for bits in (1, 2, 3, 4, 5):
+        for dim in (64, 128):
+            assert np.allclose(compute_codeword_probabilities(bits, dim), z[f"probs_b{bits}_d{dim}"],
+                               rtol=1e-12, atol=0)
+            c = HuffmanCoder(bits, dim)
+            words = [c.codebook[s] for s in range(1 << bits)]
+            assert [len(w) for w in words] == z[f"lens_b{bits}_d{dim}"].tolist(), (bits, dim)
+            assert [int(w, 2) for w in words] == z[f"words_b{bits}_d{dim}"].tolist(), (bits, dim)
+            # Kraft equality: a complete prefix code
+            assert abs(sum(2.0 ** -len(w) for w in words) - 1.0) < 1e-12
+            assert c.entropy() <= c.avg_code_length() < c.entropy() + 1
+    i = 0
+    while f"case{i}_meta" in z.files:
+        bits, dim = z[f"case{i}_meta"].tolist()
+        codes = torch.from_numpy(z[f"case{i}_codes"])
+        st = EntropyPackedStorage.from_codes(codes, bits, dim)
+        assert st._data == z[f"case{i}_bytes"].tobytes(), i
+        assert torch.equal(st.to_codes(), torch.from_numpy(z[f"case{i}_decoded"]))
+        assert abs(st.savings_pct - float(z[f"case{i}_savings"])) < 1e-12
+        i += 1
+    assert i == 5
+    assert HuffmanCoder(4, 64).encode(torch.zeros(0, dtype=torch.uint8)) == z["empty_bytes"].tobytes()
+
+
+@pytest.mark.skipif(not _built(), reason="native library not built")
+def test_huffman_round_trip_limits_and_short_streams():
+    from turboquant_kv.entropy import EntropyPackedStorage, HuffmanCoder
+    rs = np.random.RandomState(9)
+    c = HuffmanCoder(4, 128)
+    probs = c.probs
+    codes = torch.from_numpy(rs.choice(16, 200000, p=probs).astype(np.uint8))
+    data = c.encode(codes)
+    n, nbits = struct.unpack("<II", data[:8])
+    assert n == 200000
+    assert nbits == int(sum(np.bincount(codes.numpy(), minlength=16)[s] * len(c.codebook[s]) for s in range(16)))
+    assert len(data) == 8 + (nbits + 7) // 8
+    assert torch.equal(c.decode(data), codes)
+    assert torch.equal(c.decode(data, 1000), codes[:1000])
+    # a stream cut short decodes the symbols it still holds
+    cut = c.decode(data[:8 + 100])
+    assert 0 < cut.numel() < 200000 and torch.equal(cut, codes[:cut.numel()])
+    st = EntropyPackedStorage.from_codes(codes.view(-1, 100), 4, 128)
+    assert st.to_codes().shape == (2000, 100)
+    assert 0 < st.savings_pct < 10  # ~3.8 bits/code against 4

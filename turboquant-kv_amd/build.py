@@ -27,7 +27,8 @@ OBJDIR = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(LIBDIR, "libturboquant_hip.so")
 TORCH_LIB = os.path.join(LIBDIR, "libturboquant_torch.so")
 
-HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip", "tq_paged.hip", "tq_core_tables.hip"]
+HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip", "tq_paged.hip", "tq_core_tables.hip",
+               "tq_entropy.hip"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = [

@@ -572,6 +572,53 @@ std::tuple<at::Tensor, at::Tensor> core_codebook(int64_t bits, int64_t dim) {
   return {bnd, cen};
 }
 
+// ------------------------------------------------------------ Huffman streams (host tensors)
+
+at::Tensor huffman_encode(const at::Tensor& codes, const at::Tensor& code_words,
+                          const at::Tensor& code_lens) {
+  TORCH_CHECK(!codes.is_cuda() && !code_words.is_cuda() && !code_lens.is_cuda(),
+              "huffman_encode works on host tensors");
+  auto c = codes.to(at::kByte).contiguous().reshape({-1});
+  auto w = code_words.to(at::kLong).contiguous();
+  auto l = code_lens.to(at::kByte).contiguous();
+  TORCH_CHECK(w.numel() == l.numel(), "one code word and length per symbol");
+  uint64_t nbits = 0;
+  const uint8_t* cp = c.data_ptr<uint8_t>();
+  const uint8_t* lp = l.data_ptr<uint8_t>();
+  for (int64_t i = 0; i < c.numel(); ++i) {
+    TORCH_CHECK(cp[i] < l.numel(), "symbol out of range");
+    nbits += lp[cp[i]];
+  }
+  auto out = at::empty({(int64_t)(8 + (nbits + 7) / 8)}, at::TensorOptions().dtype(at::kByte));
+  size_t nb = 0;
+  check_rc(tq_huffman_encode(cp, c.numel(), reinterpret_cast<const uint64_t*>(w.data_ptr<int64_t>()),
+                             lp, (int32_t)l.numel(), out.data_ptr<uint8_t>(), out.numel(), &nb));
+  return out;
+}
+
+at::Tensor huffman_decode(const at::Tensor& data, int64_t n_symbols, const at::Tensor& code_words,
+                          const at::Tensor& code_lens, const at::Tensor& symbols) {
+  TORCH_CHECK(!data.is_cuda(), "huffman_decode works on host tensors");
+  auto d = data.to(at::kByte).contiguous();
+  auto w = code_words.to(at::kLong).contiguous();
+  auto l = code_lens.to(at::kByte).contiguous();
+  auto sy = symbols.to(at::kInt).contiguous();
+  TORCH_CHECK(w.numel() == l.numel() && w.numel() == sy.numel(), "code table sizes differ");
+  TORCH_CHECK(d.numel() >= 8, "stream shorter than its header");
+  int64_t n = n_symbols;
+  if (n < 0) {
+    const uint8_t* p = d.data_ptr<uint8_t>();
+    n = (int64_t)((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
+  }
+  auto out = at::empty({n}, at::TensorOptions().dtype(at::kByte));
+  int64_t got = 0;
+  check_rc(tq_huffman_decode(d.data_ptr<uint8_t>(), d.numel(), n,
+                             reinterpret_cast<const uint64_t*>(w.data_ptr<int64_t>()),
+                             l.data_ptr<uint8_t>(), sy.data_ptr<int32_t>(), (int32_t)sy.numel(),
+                             out.data_ptr<uint8_t>(), &got));
+  return out.narrow(0, 0, got).clone();
+}
+
 // ------------------------------------------------------------ paged pools (vLLM block tables)
 
 // rows [n, hkv, P] u8 (+ norms [n, hkv] f32) to the slots slot_mapping [n] of
@@ -813,6 +860,9 @@ TORCH_LIBRARY(turboquant, m) {
   // host-side tables (no tensor arguments: registered with catch-all kernels)
   m.def("core_rotation(int dim, int seed) -> Tensor", &core_rotation);
   m.def("core_codebook(int bits, int dim) -> (Tensor, Tensor)", &core_codebook);
+  m.def("huffman_encode(Tensor codes, Tensor code_words, Tensor code_lens) -> Tensor", &huffman_encode);
+  m.def("huffman_decode(Tensor data, int n_symbols, Tensor code_words, Tensor code_lens,"
+        " Tensor symbols) -> Tensor", &huffman_decode);
   m.def("paged_store(Tensor rows, Tensor? norms, Tensor slot_mapping, Tensor(a!) pool,"
         " Tensor(b!)? norm_pool) -> ()");
   m.def("paged_gather(Tensor pool, Tensor? norm_pool, Tensor block_tables, Tensor seq_lens,"

@@ -3,14 +3,15 @@
 Drop-in for the reference package's quantize-and-score path (turboquant_kv/__init__.py:7-61):
 the quantize/dequantize functions, QuantizedKVCache, TurboQuantIndex, the HF
 TurboQuantCache and the vLLM backend, computed by hand-written HIP kernels behind
-torch.ops.turboquant.  The multi-GPU wrapper and the on-disk entropy coder are not
-part of this package.
+torch.ops.turboquant; the Huffman storage of code indices (entropy.py) and the C++
+core's TQIX index files (formats.py).  The multi-GPU wrapper is not part of this package.
 """
 
 from turboquant_kv.config import TurboQuantConfig
 from turboquant_kv.cache import QuantizedKVCache
 from turboquant_kv.search import TurboQuantIndex
 from turboquant_kv.quantizers import TurboQuantMSE, TurboQuantProd
+from turboquant_kv.entropy import HuffmanCoder, EntropyPackedStorage
 from turboquant_kv.reference import (
     quantize_mse,
     dequantize_mse,
@@ -42,6 +43,8 @@ __all__ = [
     "TurboQuantIndex",
     "TurboQuantMSE",
     "TurboQuantProd",
+    "HuffmanCoder",
+    "EntropyPackedStorage",
     "quantize_mse",
     "dequantize_mse",
     "quantize_prod",
