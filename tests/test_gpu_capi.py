@@ -285,10 +285,12 @@ def test_quantize_prod_vs_reference(golden):
         assert np.allclose(rn[ok], pr[f"{name}_res_norms"][ok], rtol=2e-5, atol=1e-7)
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 132, 160, 200, 256])
 def test_quantize_mfma_ragged_vs_oracle(d):
-    # fp32 inputs of d 64/128 run the MFMA kernel (64-row tiles): ragged row counts,
-    # every bit width of both modes, against the oracle's float64 decision margins.
+    # fp32 inputs run the MFMA kernel (64-row tiles; d 64/128 with register-resident
+    # operands, d of 132-256 padded to 192/208/256 with operands reloaded per contraction):
+    # ragged row counts, every bit width of both modes, against the oracle's float64
+    # decision margins.
     rs = np.random.RandomState(900 + d)
     R = O.dense_qr_rotation(d, 42)
     S = O.qjl_matrix(d, d, 42)

@@ -404,6 +404,10 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
   const int64_t row = blockIdx.x;
   const int b = (int)(row / hq);
   const int j = threadIdx.x;
+  // column j of R_v, requested first: its loads overlap the split merge below
+  float rcol[kDim];
+#pragma unroll
+  for (int k = 0; k < kDim; ++k) rcol[k] = vrot[k * kDim + j];
   const int64_t T = min((int64_t)max(seq_lens[b], 0), t_max);
   const int ns = (int)((T + split_tokens - 1) / split_tokens);
   float M = -INFINITY;
@@ -419,8 +423,8 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
   o_s[j] = any ? o / L : 0.f;
   __syncthreads();
   float r = 0.f;
-#pragma unroll 8
-  for (int k = 0; k < kDim; ++k) r = fmaf(o_s[k], vrot[k * kDim + j], r);
+#pragma unroll
+  for (int k = 0; k < kDim; ++k) r = fmaf(o_s[k], rcol[k], r);
   store_from_f32(out, row * kDim + j, r, out_dt);
   if (lse && j == 0) lse[row] = any ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
 }

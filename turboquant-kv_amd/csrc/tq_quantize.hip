@@ -290,6 +290,13 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(QuantArgs a) {
 //    by one Newton step: the correctly rounded quotient (checked against IEEE division on
 //    8e7 random pairs) at 3 operations per element instead of a full division each.
 // The next tile's rows are loaded into registers while the current one is processed.
+//
+// Wider rows (RELOAD: d up to 256, padded to D = a multiple of 16) do not fit three
+// register-resident operands: each wave reloads the operand of every contraction from
+// global memory (L2: R and S stay cached) just before it, one matrix at a time.  A
+// 64-row tile is tens of microseconds of MFMA work per CU, against a few kilobytes of
+// operand per wave.  Dims d..D-1 are zero in the tile and in the operands, so the
+// padded columns add nothing to any sum; their codes and signs are not stored.
 constexpr int kQmRows = 64;
 template <int D> constexpr int qm_threads() { return 64 * (D / 16); }
 
@@ -312,7 +319,7 @@ __device__ __forceinline__ uint32_t qm_plane16(const uint32_t (&w)[4], int p) {
   return (nib[0] << 4 | nib[1]) | (nib[2] << 4 | nib[3]) << 8;
 }
 
-template <bool kProd, int D, int NB>
+template <bool kProd, int D, int NB, bool RELOAD = false>
 __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArgs a) {
 #pragma clang fp contract(off)
   constexpr int kQmThreads = qm_threads<D>();
@@ -320,8 +327,9 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
   constexpr int LD = D + 1;                      // LDS row stride in floats
   constexpr int KS = D / 4;                      // k-steps per contraction
   constexpr int RB = kQmRows / 16;               // 16-row blocks per tile
-  constexpr int BPP = D / 8;
+  constexpr int BPP = D / 8;  // RELOAD: the row's bytes per plane are (d + 7) / 8
   static_assert(TPR * 16 == D, "16 dims per thread");
+  const int d = RELOAD ? a.d : D;  // real dim (RELOAD: d % 4 == 0, d <= D)
   typedef float v4f_t __attribute__((ext_vector_type(4)));
   __shared__ float ta[kQmRows * LD];             // u -> residual
   __shared__ float tb[kProd ? kQmRows * LD : 1]; // u / ||u|| -> centroid values
@@ -332,20 +340,49 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
   const int g = lane >> 4, c16 = lane & 15;
   const int col = wave * 16 + c16;         // this lane's GEMM output column
   const int trow = tid / TPR, part = tid % TPR;  // row work: row, dims 16 part..
-  auto kof = [&](int t) { return 64 * (t >> 4) + (t & 15) + 16 * g; };
+  // k index of lane group g at k-step t: the four k = s, s+16, s+32, s+48 of a 64-wide
+  // block (conflict-free tile reads); a last 16-wide block (D % 64 == 16) takes four
+  // consecutive k per step
+  constexpr int KF = (D / 64) * 16;  // k-steps in whole 64-wide blocks
+  static_assert(D % 64 == 0 || D % 64 == 16, "D: whole 64-wide blocks plus at most 16");
+  auto kof = [&](int t) {
+    return t < KF ? 64 * (t >> 4) + (t & 15) + 16 * g : 64 * (D / 64) + 4 * (t - KF) + g;
+  };
   float bnd_r[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) bnd_r[i] = a.bnd[i];
   if (kProd && tid < 16) cen_s[tid] = tid <= NB ? a.cen[tid] : 0.f;
   // matrix operands: bR[t] = R[col][k_t] (u R^T), bC[t] = R[k_t][col] (c R), bS[t] = S[col][k_t]
-  float bR[KS], bC[kProd ? KS : 1], bS[kProd ? KS : 1];
+  // (RELOAD: one array, refilled before each contraction; zero outside d x d)
+  constexpr bool kHold = !RELOAD;
+  float bR[KS], bC[kProd && kHold ? KS : 1], bS[kProd && kHold ? KS : 1];
+  auto load_op = [&](float (&bm)[KS], const float* __restrict__ M, bool transposed) {
+    if constexpr (RELOAD) {
+      // Indices clamped into the d x d matrix (every load stays inside it), the padded
+      // entries then zeroed.  The clamped column and d pass through an empty asm so the
+      // 3 x KS address computations are redone per call, not hoisted out of the tile loop
+      // (held across it they would need hundreds of registers).
+      int cc = col < d ? col : d - 1, dd = d;
+      asm volatile("" : "+v"(cc), "+v"(dd));
 #pragma unroll
-  for (int t = 0; t < KS; ++t) {
-    bR[t] = a.rot[col * D + kof(t)];
-    if constexpr (kProd) {
-      bC[t] = a.rot[kof(t) * D + col];
-      bS[t] = a.qjl[col * D + kof(t)];
+      for (int t = 0; t < KS; ++t) {
+        const int k = kof(t);
+        const int kc = k < dd ? k : dd - 1;
+        const float v = transposed ? M[kc * dd + cc] : M[cc * dd + kc];
+        bm[t] = (col < d && k < d) ? v : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        const int k = kof(t);
+        bm[t] = transposed ? M[k * D + col] : M[col * D + k];
+      }
     }
+  };
+  load_op(bR, a.rot, false);
+  if constexpr (kProd && kHold) {
+    load_op(bC, a.rot, true);
+    load_op(bS, a.qjl, false);
   }
   const float eps = 1e-10f;
   const int64_t ntiles = (a.n + kQmRows - 1) / kQmRows;
@@ -354,15 +391,31 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
   float4 xr[4];  // this thread's 16 dims of its row of the next tile
   auto load_tile = [&](int64_t tile) {
     const int64_t row = tile * kQmRows + trow;
-    const float4* src = reinterpret_cast<const float4*>(xin + row * D + 16 * part);
+    const float4* src = reinterpret_cast<const float4*>(xin + row * d + 16 * part);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xr[i] = row < a.n ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 4; ++i)
+      xr[i] = (row < a.n && (!RELOAD || 16 * part + 4 * i < d)) ? src[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   };
-  // sum over the row's TPR adjacent lanes (every lane of the row gets it)
+  // sum over the row's TPR threads (every thread of the row gets it).  A power-of-two
+  // TPR keeps a row inside a wave (butterfly over adjacent lanes); otherwise (d padded to
+  // 192 or 208: 12 or 13 threads, rows straddling waves) the partials meet in LDS.  Called
+  // by every thread of the workgroup at the same point.
+  constexpr bool kPow2Row = (TPR & (TPR - 1)) == 0;
+  __shared__ float rsum_s[kPow2Row ? 1 : kQmRows * TPR];
   auto row_sum = [&](float v) {
+    if constexpr (kPow2Row) {
 #pragma unroll
-    for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
+      for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o, 64);
+      return v;
+    } else {
+      rsum_s[trow * TPR + part] = v;
+      __syncthreads();
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < TPR; ++i) t += rsum_s[trow * TPR + i];
+      __syncthreads();
+      return t;
+    }
   };
   auto row_norm = [&](const float (&v)[16]) {
     float s = 0.f;
@@ -389,14 +442,27 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
     const uint4 c = *reinterpret_cast<const uint4*>(&cs[trow * D + 16 * part]);
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
     if (trow < rows) {
-      uint8_t* dst = out + (r0 + trow) * (int64_t)(bits * BPP) + 2 * part;
-      for (int p = 0; p < bits; ++p)
-        *reinterpret_cast<uint16_t*>(dst + p * BPP) = (uint16_t)qm_plane16(w, p);
+      if constexpr (RELOAD) {  // odd plane widths: byte stores, dims below d only
+        const int bpp = (d + 7) >> 3;
+        uint8_t* dst = out + (r0 + trow) * (int64_t)(bits * bpp) + 2 * part;
+        for (int p = 0; p < bits; ++p) {
+          const uint32_t v = qm_plane16(w, p);
+          if (2 * part < bpp) dst[p * bpp] = (uint8_t)v;
+          if (2 * part + 1 < bpp) dst[p * bpp + 1] = (uint8_t)(v >> 8);
+        }
+      } else {
+        uint8_t* dst = out + (r0 + trow) * (int64_t)(bits * BPP) + 2 * part;
+        for (int p = 0; p < bits; ++p)
+          *reinterpret_cast<uint16_t*>(dst + p * BPP) = (uint16_t)qm_plane16(w, p);
+      }
     }
   };
 
-  if (blockIdx.x < ntiles) load_tile(blockIdx.x);
+  // RELOAD: a tile's rows are loaded when it starts (a prefetched tile would stay live
+  // through the three contractions; a tile is long enough to absorb one load latency)
+  if (!RELOAD && blockIdx.x < ntiles) load_tile(blockIdx.x);
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    if constexpr (RELOAD) load_tile(tile);
     const int64_t r0 = tile * kQmRows;
     const int rows = (int)min<int64_t>(kQmRows, a.n - r0);
     float u[16];
@@ -404,7 +470,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       float x[16];
 #pragma unroll
       for (int i = 0; i < 4; ++i) { x[4 * i] = xr[i].x; x[4 * i + 1] = xr[i].y; x[4 * i + 2] = xr[i].z; x[4 * i + 3] = xr[i].w; }
-      if (tile + gridDim.x < ntiles) load_tile(tile + gridDim.x);
+      if (!RELOAD && tile + gridDim.x < ntiles) load_tile(tile + gridDim.x);
       const float n = row_norm(x);
       if (part == 0 && trow < rows) a.norms[r0 + trow] = n;
       const float den = fmaxf(n, eps), y = qm_recip(den);
@@ -423,6 +489,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
     __syncthreads();
     // ---- y = u R^T, codes = #{bnd < y}
     v4f_t acc[RB];
+    if constexpr (RELOAD && kProd) load_op(bR, a.rot, false);  // replaced by S last tile
     gemm(kProd ? tb : ta, bR, acc);
     if (kProd) __syncthreads();  // every wave is done reading tb before it takes c[codes]
 #pragma unroll
@@ -434,7 +501,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
         int code = 0;
 #pragma unroll
         for (int i = 0; i < NB; ++i) code += (bnd_r[i] < yv) ? 1 : 0;
-        cs[row * D + col] = (uint8_t)code;
+        cs[row * D + col] = (uint8_t)((RELOAD && col >= d) ? 0 : code);  // pad bits stay 0
         if (kProd) tb[row * LD + col] = cen_s[code];
       }
     }
@@ -443,7 +510,12 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
     if constexpr (kProd) {
       // ---- residual = u - c[codes] R (ta, u, is no operand of this product: each lane
       // rewrites its own elements)
-      gemm(tb, bC, acc);
+      if constexpr (RELOAD) {
+        load_op(bR, a.rot, true);
+        gemm(tb, bR, acc);
+      } else {
+        gemm(tb, bC, acc);
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -461,11 +533,17 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
         if (part == 0 && trow < rows) a.res_norms[r0 + trow] = gam;
       }
       // ---- signs of residual S^T
-      gemm(ta, bS, acc);
+      if constexpr (RELOAD) {
+        load_op(bR, a.qjl, false);
+        gemm(ta, bR, acc);
+      } else {
+        gemm(ta, bS, acc);
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cs[(16 * rb + 4 * g + r) * D + col] = acc[rb][r] >= 0.f ? 1 : 0;
+        for (int r = 0; r < 4; ++r)
+          cs[(16 * rb + 4 * g + r) * D + col] = (acc[rb][r] >= 0.f && (!RELOAD || col < d)) ? 1 : 0;
       }
       __syncthreads();
       pack_cs(rows, r0, 1, a.signs);
@@ -595,19 +673,43 @@ int grid_for_tiles(int64_t n) {
 
 // The MFMA quantize kernel covers fp32 inputs kept in fp32, d = 64 or 128, 16-byte
 // aligned rows; its workgroups stay on their CUs (at most one per tile).
+// Padded width of the operand-reloading MFMA kernel for d, 0 if none applies.
+int qm_reload_dim(int d) {
+  if (d % 4 != 0 || d <= 128 || d > 256) return 0;
+  return d <= 192 ? 192 : d <= 208 ? 208 : 256;
+}
+
 bool use_mfma_quantize(const void* x, tq_dtype in_dt, tq_dtype rdt, int d) {
-  return in_dt == TQ_F32 && rdt == TQ_F32 && (d == 64 || d == 128) &&
+  return in_dt == TQ_F32 && rdt == TQ_F32 && (d == 64 || d == 128 || qm_reload_dim(d) > 0) &&
          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+template <bool kProd, int D>
+void launch_qm_reload(const QuantArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.bits) {
+    case 1: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, D, 1, true>), grid, dim3(qm_threads<D>()), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, D, 3, true>), grid, dim3(qm_threads<D>()), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, D, 7, true>), grid, dim3(qm_threads<D>()), 0, st, a); break;
+    default: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, D, 15, true>), grid, dim3(qm_threads<D>()), 0, st, a); break;
+  }
 }
 
 template <bool kProd>
 void launch_quantize_mfma(const QuantArgs& a, hipStream_t st) {
   const int64_t tiles = (a.n + kQmRows - 1) / kQmRows;
-  // workgroups per CU that the registers (matrix operands held per wave) allow
-  const int per_cu = a.d == 128 ? (kProd ? 1 : 2) : (kProd ? 2 : 4);
+  // workgroups per CU that the registers (matrix operands held per wave) allow; the
+  // reloading kernel's 12-16 waves and its tiles' LDS take one CU each
+  const int rd = qm_reload_dim(a.d);
+  const int per_cu = rd ? 1 : a.d == 128 ? (kProd ? 1 : 2) : (kProd ? 2 : 4);
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
   const dim3 grid((unsigned)(tiles < cap ? tiles : cap));
-  if (a.d == 128) {
+  if (rd == 192) {
+    launch_qm_reload<kProd, 192>(a, grid, st);
+  } else if (rd == 208) {
+    launch_qm_reload<kProd, 208>(a, grid, st);
+  } else if (rd == 256) {
+    launch_qm_reload<kProd, 256>(a, grid, st);
+  } else if (a.d == 128) {
     switch (a.bits) {
       case 1: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 1>), grid, dim3(qm_threads<128>()), 0, st, a); break;
       case 2: hipLaunchKernelGGL((quantize_mfma_kernel<kProd, 128, 3>), grid, dim3(qm_threads<128>()), 0, st, a); break;
