@@ -312,6 +312,37 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
                               size_t workspace_bytes, void* stream);
 
 /*
+ * Paged pools in the decode layout (4-bit keys, 2-bit values, head_dim 64): the same
+ * kernel as tq_decode_attention_dl with one block lookup per 64-token tile, for vLLM
+ * block sizes that are powers of two >= 64 (so a tile never straddles blocks).  Replaces,
+ * like tq_decode_attention_paged, the reference backend's forward
+ * (turboquant_kv/vllm_plugin/__init__.py:209-304) at those block sizes.
+ *   kpairs_pool [num_blocks][hkv][block_size][32]   key pair bytes (tq_pack_decode_layout,
+ *                                                   values = 0) stored with tq_paged_store
+ *   vtile_pool  [num_blocks][hkv][block_size/64][1024] value tiles (byte layout above)
+ *   knorm_pool, vnorm_pool [num_blocks][hkv][block_size]
+ * tq_paged_store_value_tiles writes new tokens' 2-bit value rows [n_tokens][hkv][16]
+ * (bit planes) and norms [n_tokens][hkv] into their slots (slot_mapping as in
+ * tq_paged_store; negative or out-of-pool slots skipped), leaving the other tokens of
+ * each tile as they are.  Workspace: tq_decode_dl_workspace_bytes(B, hq, hkv,
+ * max_blocks_per_seq * block_size).  Pools 16-byte aligned; num_blocks * hkv * block_size
+ * * 32 < 2^31.  Outputs as tq_decode_attention_dl's.
+ */
+int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
+                               int32_t hkv, const int64_t* slot_mapping, uint8_t* vtile_pool,
+                               float* vnorm_pool, int64_t num_blocks, int32_t block_size,
+                               void* stream);
+int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                                 int32_t d, const uint8_t* kpairs_pool, const float* knorm_pool,
+                                 const uint8_t* vtile_pool, const float* vnorm_pool,
+                                 int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
+                                 int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                 const float* kcentroids, const float* vcentroids,
+                                 const float* krotation, const float* vrotation, float scale,
+                                 void* out, float* lse, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/*
  * Host-side tables of the reference's standalone C++ core, for TQIX v1 index files
  * (turboquant_core.cpp:559-618), which record only (dim, bit_width, seed): the reader
  * rebuilds the rotation and codebook the writer used.  No device work; outputs are host

@@ -268,3 +268,169 @@ def test_vllm_paged_protected_layer_and_padding():
     used = torch.zeros(nb, dtype=torch.bool)
     used[[5, 2, 9]] = True
     assert fp[~used.to(DEV)].abs().sum().item() == 0
+
+
+# ------------------------------------------------------------------ decode-layout pools
+def _dl_pools(rs, lens, bs, nb, width, Hkv):
+    """Random 4-bit key / 2-bit value bit-plane rows of every token, stored into
+    decode-layout block pools through the C ABI (values in two shuffled calls, so tiles are
+    filled piecewise).  Returns the pools and each sequence's contiguous rows and norms."""
+    from turboquant_kv import ops
+    tab = _tables(rs, lens, bs, nb, width)
+    slots = np.array([tab[i, t // bs] * bs + t % bs for i, n in enumerate(lens) for t in range(n)],
+                     np.int64)
+    n = len(slots)
+    krows = rs.randint(0, 256, (n, Hkv, 32)).astype(np.uint8)
+    vrows = rs.randint(0, 256, (n, Hkv, 16)).astype(np.uint8)
+    kn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
+    vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
+    kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
+    knp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
+    vt = torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV)
+    vnp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
+    pairs = torch.empty(n * Hkv, 1, 32, dtype=torch.uint8, device=DEV)
+    ops.pack_decode_layout(T(krows).view(n * Hkv, 1, 32), pairs, 64, 4, False, 0)
+    capi.check(L().tq_paged_store(capi.p(pairs), capi.p(T(kn)), capi.i64(n), capi.i32(Hkv), capi.i32(32),
+                                  capi.p(T(slots)), capi.p(kp), capi.p(knp), capi.i64(nb), capi.i32(bs),
+                                  capi.stream()))
+    order = rs.permutation(n)
+    for part in (order[: n // 2], order[n // 2:]):
+        sp = np.concatenate([slots[part], [-1]]).astype(np.int64)       # plus one padding slot
+        rp = np.concatenate([vrows[part], vrows[:1]])
+        npart = np.concatenate([vn[part], vn[:1]])
+        capi.check(L().tq_paged_store_value_tiles(capi.p(T(rp)), capi.p(T(npart)), capi.i64(len(sp)),
+                                                  capi.i32(Hkv), capi.p(T(sp)), capi.p(vt), capi.p(vnp),
+                                                  capi.i64(nb), capi.i32(bs), capi.stream()))
+    sync()
+    seqs, o = [], 0
+    for L_ in lens:
+        seqs.append((krows[o:o + L_].transpose(1, 0, 2), kn[o:o + L_].T, vrows[o:o + L_].transpose(1, 0, 2),
+                     vn[o:o + L_].T))
+        o += L_
+    return tab, kp, knp, vt, vnp, seqs
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_paged_dl_store_round_trip(bs):
+    from turboquant_kv import ops
+    rs = np.random.RandomState(bs)
+    Hkv, lens = 2, [130, 64, 1, 0]
+    width = (max(lens) + bs - 1) // bs + 1
+    nb = sum((n + bs - 1) // bs for n in lens) + 3
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        one = lambda v: torch.tensor([v], dtype=torch.int32, device=DEV)
+        bt = T(tab[b:b + 1])
+        pr, pn = ops.paged_gather(kp, knp, bt, one(n), n)
+        nt = (n + 63) // 64
+        tiles, _ = ops.paged_gather(vt, None, bt, one(nt), nt)
+        _, vnn = ops.paged_gather(kp, vnp, bt, one(n), n)
+        kr, knr, vr, vnr = seqs[b]
+        assert np.array_equal(ops.unpack_decode_layout(pr[0], 64, 4, False, 0, n).cpu().numpy(), kr)
+        assert np.array_equal(ops.unpack_decode_layout(tiles[0], 64, 2, True, 0, n).cpu().numpy(), vr)
+        assert np.array_equal(pn[0].cpu().numpy(), knr) and np.array_equal(vnn[0].cpu().numpy(), vnr)
+
+
+@pytest.mark.parametrize("bs,G,qdt", [(64, 4, torch.bfloat16), (128, 2, torch.float16),
+                                      (64, 1, torch.float32)])
+def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
+    from turboquant_kv import ops
+    rs = np.random.RandomState(bs + G)
+    Hkv = 2
+    Hq = G * Hkv
+    lens = [0, 3, 700, 1500, 64]
+    B = len(lens)
+    width = (max(lens) + bs - 1) // bs + 1
+    nb = sum((n + bs - 1) // bs for n in lens) + 4
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    tab[0, 0] = 7   # a block id past sequence 0's (empty) context: never read
+    Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
+    _, ck = O.lloyd_max_codebook(4, 64)
+    _, cv = O.lloyd_max_codebook(2, 64)
+    q = torch.from_numpy(rs.randn(B, Hq, 64).astype(np.float32)).to(DEV).to(qdt)
+    scale = 0.125
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[qdt]
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
+    Tc = width * bs
+    ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_decode_attention_paged_dl(
+        capi.p(q), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp), capi.p(knp),
+        capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(tab)), capi.i32(width),
+        capi.p(T(np.asarray(lens, np.int32))), capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)),
+        ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
+        capi.stream()))
+    sync()
+    got, got_lse = out.float().cpu().numpy(), lse.cpu().numpy()
+    # the same tokens in contiguous decode-layout caches of the same capacity
+    kc_ = np.zeros((B, Hkv, Tc, 32), np.uint8)
+    vc_ = np.zeros((B, Hkv, Tc, 16), np.uint8)
+    kn_, vn_ = np.zeros((B, Hkv, Tc), np.float32), np.zeros((B, Hkv, Tc), np.float32)
+    for b, n in enumerate(lens):
+        kc_[b, :, :n], kn_[b, :, :n], vc_[b, :, :n], vn_[b, :, :n] = seqs[b]
+    kpairs = torch.empty(B * Hkv, Tc, 32, dtype=torch.uint8, device=DEV)
+    vblocks = torch.zeros(B * Hkv, Tc // 64, 1024, dtype=torch.uint8, device=DEV)
+    ops.pack_decode_layout(T(kc_).view(B * Hkv, Tc, 32), kpairs, 64, 4, False, 0)
+    ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 16), vblocks, 64, 2, True, 0)
+    ref, ref_lse = ops.decode_attention_dl(q, kpairs.view(B, Hkv, Tc, 32), T(kn_),
+                                           vblocks.view(B, Hkv, Tc // 64, 1024), T(vn_),
+                                           T(np.asarray(lens, np.int32)), T(ck), T(cv), T(Rk), T(Rv),
+                                           scale, return_lse=True)
+    # same kernel, same split plan: identical sums
+    assert np.array_equal(got, ref.float().cpu().numpy())
+    assert np.array_equal(got_lse, ref_lse.cpu().numpy())
+    want = O.decode_attention_f64(q.float().cpu().numpy(), kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv,
+                                  4, 2, scale)
+    assert np.all(got[0] == 0) and np.all(np.isneginf(got_lse[0]))
+    tol = 1e-2 if qdt != torch.float32 else 1e-4
+    assert np.max(np.abs(got - want)) <= tol * np.max(np.abs(want))
+
+
+def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64():
+    # The vLLM step (chunked prefill + decodes) on decode-layout pools: the stored codes
+    # equal the bit-plane pools' and outputs match the float64 paged oracle.
+    from turboquant_kv.vllm_plugin import PagedKVPools
+    from turboquant_kv.config import TurboQuantConfig
+    rs = np.random.RandomState(11)
+    Hkv, Hq, d, bs, nb = 2, 8, 64, 64, 24
+    cfg = TurboQuantConfig(key_bits=4, value_bits=2)
+    bp = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV)
+    dl = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV, layout="decode")
+    steps = [[100, 17, 200, 5], [70, 1, 1, 1]]
+    final = [sum(s[i] for s in steps) for i in range(4)]
+    perm = [int(b) for b in rs.permutation(nb)]
+    blocks, used = [], 0
+    for n in final:
+        k = (n + bs - 1) // bs
+        blocks.append(perm[used:used + k])
+        used += k
+    before = [0, 0, 0, 0]
+    scale = 0.125
+    for step, n_new in enumerate(steps):
+        md, order, lens, tab = _step_meta(blocks, before, n_new, bs)
+        n_tok = sum(n_new)
+        q = torch.randn(n_tok, Hq, d, device=DEV, dtype=torch.bfloat16)
+        k = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)
+        v = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)
+        out_bp = bp.forward(q, k, v, md, scale)
+        out_dl = dl.forward(q, k, v, md, scale)
+        P = {key: t.cpu().numpy() for key, t in bp.layers[0].items()}
+        kc, vc = bp.kcen.cpu().numpy(), bp.vcen.cpu().numpy()
+        Rk, Rv = bp.R_k.cpu().numpy(), bp.R_v.cpu().numpy()
+        qsl = md.query_start_loc.tolist()
+        for j in range(len(order)):
+            bt = md.block_tables[j]
+            for kind in ("k", "v"):
+                r_bp, n_bp = bp._gather(bp.layers[0], kind, bt, lens[j])
+                r_dl, n_dl = dl._gather(dl.layers[0], kind, bt, lens[j])
+                assert torch.equal(r_bp, r_dl) and torch.equal(n_bp, n_dl), (step, j, kind)
+            a, b = qsl[j], qsl[j + 1]
+            want = O.paged_attention_f64(q[a:b].float().cpu().numpy(), P["k"], P["kn"], P["v"], P["vn"],
+                                         tab[j], lens[j], kc, vc, Rk, Rv, 4, 2, scale)
+            got = out_dl[a:b].float().cpu().numpy()
+            assert np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want)), (step, j)
+            ref = out_bp[a:b].float().cpu().numpy()
+            assert np.max(np.abs(got - ref)) <= 2e-2 * np.max(np.abs(want)), (step, j)
+        before = [before[i] + n_new[i] for i in range(4)]

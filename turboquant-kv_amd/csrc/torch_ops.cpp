@@ -820,6 +820,86 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   return {out, lse};
 }
 
+// 2-bit value rows [n, hkv, 16] + norms [n, hkv] into the value tiles
+// vtile_pool [num_blocks, hkv, block_size/64, 1024] (+ vnorm_pool [num_blocks, hkv, block_size]).
+void paged_store_value_tiles(const at::Tensor& rows, const at::Tensor& norms,
+                             const at::Tensor& slot_mapping, at::Tensor& vtile_pool,
+                             at::Tensor& vnorm_pool) {
+  require_gpu(vtile_pool, "vtile_pool");
+  TORCH_CHECK(vtile_pool.dim() == 4 && vtile_pool.scalar_type() == at::kByte &&
+                  vtile_pool.is_contiguous() && vtile_pool.size(3) == 1024,
+              "vtile_pool must be contiguous uint8 [num_blocks, hkv, block_size/64, 1024]");
+  c10::DeviceGuard g(vtile_pool.device());
+  const auto dev = vtile_pool.device();
+  const int64_t nb = vtile_pool.size(0), hkv = vtile_pool.size(1), bs = vtile_pool.size(2) * 64;
+  TORCH_CHECK(rows.dim() == 3 && rows.scalar_type() == at::kByte && rows.size(1) == hkv &&
+                  rows.size(2) == 16,
+              "rows must be uint8 [n, hkv, 16] (2-bit codes of d = 64)");
+  const int64_t n = rows.size(0);
+  auto r = rows.to(dev).contiguous();
+  auto nm = f32c(norms, dev);
+  TORCH_CHECK(nm.numel() == n * hkv, "norms must be [n, hkv]");
+  auto sm = slot_mapping.to(dev, at::kLong).contiguous();
+  TORCH_CHECK(sm.numel() == n, "slot_mapping must have one entry per token");
+  TORCH_CHECK(vnorm_pool.device() == dev && vnorm_pool.scalar_type() == at::kFloat &&
+                  vnorm_pool.is_contiguous() && vnorm_pool.numel() == nb * hkv * bs,
+              "vnorm_pool must be contiguous float32 [num_blocks, hkv, block_size]");
+  check_rc(tq_paged_store_value_tiles(r.data_ptr<uint8_t>(), nm.data_ptr<float>(), n, (int32_t)hkv,
+                                      sm.data_ptr<int64_t>(), vtile_pool.data_ptr<uint8_t>(),
+                                      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs,
+                                      cur_stream(vtile_pool)));
+}
+
+std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
+    const at::Tensor& q, const at::Tensor& kpairs_pool, const at::Tensor& knorm_pool,
+    const at::Tensor& vtile_pool, const at::Tensor& vnorm_pool, const at::Tensor& block_tables,
+    const at::Tensor& seq_lens, const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+    const at::Tensor& krotation, const at::Tensor& vrotation, double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
+  TORCH_CHECK(kpairs_pool.dim() == 4 && vtile_pool.dim() == 4,
+              "kpairs_pool must be [num_blocks, hkv, block_size, d/2] and vtile_pool "
+              "[num_blocks, hkv, block_size/64, 16d]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  const int64_t B = qq.size(0), Hq = qq.size(1), d = qq.size(2);
+  const int64_t nb = kpairs_pool.size(0), Hkv = kpairs_pool.size(1), bs = kpairs_pool.size(2);
+  for (const at::Tensor* t : {&kpairs_pool, &vtile_pool, &knorm_pool, &vnorm_pool})
+    TORCH_CHECK(t->device() == dev && t->is_contiguous(), "pools must be contiguous on the query's device");
+  TORCH_CHECK(kpairs_pool.scalar_type() == at::kByte && vtile_pool.scalar_type() == at::kByte,
+              "pools must be uint8");
+  TORCH_CHECK(kpairs_pool.size(3) == d / 2 && vtile_pool.size(0) == nb && vtile_pool.size(1) == Hkv &&
+                  vtile_pool.size(2) * 64 == bs && vtile_pool.size(3) == 16 * d,
+              "decode-layout pool shapes mismatch");
+  TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
+                  knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
+              "norm pools must be float32 [num_blocks, hkv, block_size]");
+  auto bt = block_tables.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(bt.dim() == 2 && bt.size(0) == B, "block_tables must be [B, max_blocks]");
+  auto sl = seq_lens.to(dev, at::kInt).contiguous();
+  TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  auto kc = f32c(kcentroids, dev);
+  auto vc = f32c(vcentroids, dev);
+  auto Rk = f32c(krotation, dev);
+  auto Rv = f32c(vrotation, dev);
+  TORCH_CHECK(kc.numel() == 16 && vc.numel() == 4, "decode layout: 4-bit keys, 2-bit values");
+  auto out = at::empty({B, Hq, d}, qq.options());
+  auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
+  if (B == 0) return {out, lse};
+  auto ws = workspace(tq_decode_dl_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)Hkv,
+                                                   bt.size(1) * bs),
+                      dev);
+  check_rc(tq_decode_attention_paged_dl(
+      qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
+      kpairs_pool.data_ptr<uint8_t>(), knorm_pool.data_ptr<float>(), vtile_pool.data_ptr<uint8_t>(),
+      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, bt.data_ptr<int32_t>(), (int32_t)bt.size(1),
+      sl.data_ptr<int32_t>(), kc.data_ptr<float>(), vc.data_ptr<float>(), Rk.data_ptr<float>(),
+      Rv.data_ptr<float>(), (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(),
+      ws.numel(), cur_stream(qq)));
+  return {out, lse};
+}
+
 at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
                                const at::Tensor& knorms, const at::Tensor& vblocks,
                                const at::Tensor& vnorms, const at::Tensor& seq_lens,
@@ -893,6 +973,12 @@ TORCH_LIBRARY(turboquant, m) {
   m.def("decode_attention_dl_lse(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, float scale) -> (Tensor, Tensor)");
+  m.def("paged_store_value_tiles(Tensor rows, Tensor norms, Tensor slot_mapping,"
+        " Tensor(a!) vtile_pool, Tensor(b!) vnorm_pool) -> ()");
+  m.def("decode_attention_paged_dl(Tensor q, Tensor kpairs_pool, Tensor knorm_pool,"
+        " Tensor vtile_pool, Tensor vnorm_pool, Tensor block_tables, Tensor seq_lens,"
+        " Tensor kcentroids, Tensor vcentroids, Tensor krotation, Tensor vrotation,"
+        " float scale) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
@@ -912,6 +998,8 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("paged_store", &paged_store);
   m.impl("paged_gather", &paged_gather);
   m.impl("decode_attention_paged", &decode_attention_paged);
+  m.impl("paged_store_value_tiles", &paged_store_value_tiles);
+  m.impl("decode_attention_paged_dl", &decode_attention_paged_dl);
   m.impl("attention_scores_prod", &attention_scores_prod);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);

@@ -469,6 +469,14 @@ struct DlArgs {
   const float* vrot;
   void* out;
   float* lse;
+  // Paged pools (PAGED kernels): block b of a sequence holds its tokens [b*bs, (b+1)*bs);
+  // kpairs [num_blocks][hkv][bs][32], knorms/vnorms [num_blocks][hkv][bs], vblocks
+  // [num_blocks][hkv][bs/64][1024]; bs a power of two >= 64, so a 64-token tile lies in
+  // one block.
+  const int32_t* block_tables;
+  int bt_stride;
+  int bs_log2;
+  uint32_t pool_rows;  // num_blocks * hkv * bs
 };
 
 __device__ __forceinline__ uint32_t byte_addr(uint32_t base_copy, uint32_t w, int byte) {
@@ -533,7 +541,7 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // relative), for fp32 and fp16 outputs; otherwise (bf16 outputs) one fp16 product per
 // term, about 2^-11 relative per operand -- finer than the bf16 arithmetic the reference
 // scores bf16 inputs in.
-template <bool EXACT_V, bool PREC_K>
+template <bool EXACT_V, bool PREC_K, bool PAGED = false>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
   // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
@@ -571,15 +579,25 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // Lane roles (see the score layout and the tile loads below).
   const int sl = lane >> 4, col = lane & 15;
   const int hh = lane & 3, gq = (lane >> 2) & 3;
-  const size_t sbase = (size_t)bg * (size_t)a.t_cap;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, (uint32_t)t_end * 32);
+  // Contiguous: the buffers cover the stream's tokens below t_end.  Paged: they cover the
+  // whole pools, and a tile's block id comes through a buffer over the sequence's block
+  // table (entries past the blocks holding tokens below t_end read as block 0: loaded and
+  // masked; ids outside the pool address bytes outside the buffers, which read as zero).
+  const size_t sbase = PAGED ? 0 : (size_t)bg * (size_t)a.t_cap;
+  const uint32_t nrows = PAGED ? a.pool_rows : (uint32_t)t_end;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, nrows * 32);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * 16, (uint32_t)((t_end + 63) >> 6) * 1024);
+      make_rsrc(a.vblocks + sbase * 16, PAGED ? nrows * 16 : (uint32_t)((t_end + 63) >> 6) * 1024);
   // Norms are read four tokens at a time: the range covers whole quads (inside the
   // allocation, t_cap % 4 == 0); entries past t_end are masked.
-  const uint32_t nbytes = (uint32_t)((t_end + 3) >> 2) * 16;
+  const uint32_t nbytes = PAGED ? nrows * 4 : (uint32_t)((t_end + 3) >> 2) * 16;
   const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
   const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
+  const int bsl = PAGED ? a.bs_log2 : 0;
+  const int kvh = g;  // the kv head (the tile loads below name their token groups g)
+  const __amdgpu_buffer_rsrc_t btrs =
+      make_rsrc(PAGED ? a.block_tables + (size_t)b * a.bt_stride : a.seq_lens,
+                PAGED ? (uint32_t)(((t_end + (1 << bsl) - 1) >> bsl) * 4) : 0u);
   const int te = (int)t_end;
 
   struct Tile {
@@ -587,14 +605,28 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
     float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
   };
-  auto load_tile = [&](int t0, Tile& x) {
+  // Paged: block id of the tile at t0 (one per tile, the same in every lane), requested
+  // a tile ahead of the tile's own loads.
+  auto load_block = [&](int t0) -> uint32_t {
+    if constexpr (!PAGED) return 0u;
+    return __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)t0 >> bsl) * 4), 0, 0);
+  };
+  auto load_tile = [&](int t0, Tile& x, uint32_t blk) {
+    // r0: pool row of the tile's first token; vt: its value tile
+    uint32_t r0 = (uint32_t)t0, vt = (uint32_t)t0 >> 6;
+    if constexpr (PAGED) {
+      const uint32_t sb = blk * (uint32_t)a.hkv + (uint32_t)kvh;
+      const uint32_t in = (uint32_t)t0 & ((1u << bsl) - 1);
+      r0 = (sb << bsl) | in;
+      vt = (sb << (bsl - 6)) | (in >> 6);
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((uint32_t)(t0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)((uint32_t)(t0 >> 6) * 1024 + lane * 16), 0, 0);
+      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((r0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * 1024 + lane * 16), 0, 0);
     x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
     // norms of the lane's four tokens: 16-byte aligned (t_cap % 64 == 0, aligned base)
-    const uint32_t no = (uint32_t)(t0 + 16 * gq + 4 * sl) * 4;
+    const uint32_t no = (r0 + 16 * gq + 4 * sl) * 4;
     const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
     const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
     // (__builtin_bit_cast of a vector element would read element 0: convert by value)
@@ -632,8 +664,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 #pragma unroll
     for (int k = 0; k < kDim / 4; ++k) rrow[k] = r4[k];
   }
-  load_tile(tf, ta);
-  load_tile(tf + kStep, tb);
+  uint32_t bnx = 0;  // paged: block id of the next tile to load
+  load_tile(tf, ta, load_block(tf));
+  load_tile(tf + kStep, tb, load_block(tf + kStep));
+  bnx = load_block(tf + 2 * kStep);
   if (tid < 20) cen_s[tid] = cenv;
   if (tid < 4 * kDim) {
     const uint32_t bits = a.q_dt == TQ_F32 ? qraw : (qraw >> (8 * (qbyte & 2))) & 0xFFFFu;
@@ -910,13 +944,16 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // range check); the tile count is made wave-uniform explicitly.
   for (int it = 0; it < ntiles; it += 3) {
     const int t = tf + it * kStep;
-    load_tile(t + 2 * kStep, tc);
+    uint32_t b1 = load_block(t + 3 * kStep);
+    load_tile(t + 2 * kStep, tc, bnx);
     process(ta, t);
     if (it + 1 >= ntiles) break;
-    load_tile(t + 3 * kStep, ta);
+    uint32_t b2 = load_block(t + 4 * kStep);
+    load_tile(t + 3 * kStep, ta, b1);
     process(tb, t + kStep);
     if (it + 2 >= ntiles) break;
-    load_tile(t + 4 * kStep, tb);
+    bnx = load_block(t + 5 * kStep);
+    load_tile(t + 4 * kStep, tb, b2);
     process(tc, t + 2 * kStep);
   }
 
@@ -1162,6 +1199,46 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
 
 }  // namespace tq
 
+// ------------------------------------------------------------------ paged value tiles
+namespace tq {
+namespace {
+
+// New tokens' 2-bit value codes (bit-plane rows [n][hkv][16], d = 64) into the 64-token
+// value tiles of a paged pool, one thread per (token, head, dim).  Token t of tile T sits
+// at byte 16 (16 sl + c) + 4 m + dg, bits 2 (t % 4), with 4 m + sl = (t % 64) / 4, dim =
+// 16 dg + c (the decode layout).  Tokens of one tile share bytes, so each field is cleared
+// and set with 32-bit atomics (disjoint bits: concurrent tokens do not interfere); slots
+// outside the pool are skipped.
+__global__ __launch_bounds__(256) void paged_vtile_store_kernel(
+    const uint8_t* __restrict__ rows, const float* __restrict__ norms, int64_t n, int hkv,
+    const int64_t* __restrict__ slot_mapping, uint32_t* __restrict__ vpool,
+    float* __restrict__ vnorm_pool, int64_t num_slots, int bs_log2) {
+  const int64_t total = n * hkv * kDim;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int j = (int)(e & (kDim - 1));
+    const int64_t th = e >> 6;  // (token, head)
+    const int64_t tok = th / hkv;
+    const int h = (int)(th - tok * hkv);
+    const int64_t slot = slot_mapping[tok];
+    if (slot < 0 || slot >= num_slots) continue;
+    const int64_t blk = slot >> bs_log2;
+    const int off = (int)(slot & ((1 << bs_log2) - 1));
+    const uint8_t* row = rows + th * 16;  // plane 0: bytes 0-7, plane 1: bytes 8-15
+    const uint32_t code = ((row[j >> 3] >> (7 - (j & 7))) & 1u) | (((row[8 + (j >> 3)] >> (7 - (j & 7))) & 1u) << 1);
+    const int tt = off & 63, q4 = tt >> 2;
+    const int byte = 16 * (16 * (q4 & 3) + (j & 15)) + 4 * (q4 >> 2) + (j >> 4);
+    const int shift = 8 * (byte & 3) + 2 * (tt & 3);
+    const int64_t tile = ((blk * hkv + h) << (bs_log2 - 6)) + (off >> 6);
+    uint32_t* w = vpool + tile * 256 + (byte >> 2);
+    atomicAnd(w, ~(3u << shift));
+    atomicOr(w, code << shift);
+    if (j == 0) vnorm_pool[((blk * hkv + h) << bs_log2) + off] = norms[th];
+  }
+}
+
+}  // namespace
+}  // namespace tq
+
 // ------------------------------------------------------------------ decode-layout C ABI
 namespace tq {
 namespace {
@@ -1240,6 +1317,95 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
       hipLaunchKernelGGL((dl_decode_kernel<false, true>), grid, dim3(kDlThreads), 0, st, a);
     else
       hipLaunchKernelGGL((dl_decode_kernel<false, false>), grid, dim3(kDlThreads), 0, st, a);
+    TQ_LAUNCH_CHECK("dl_decode_kernel");
+    if (single) return TQ_OK;
+  }
+  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
+                     p.nsplit, p.split_tokens, seq_lens, t_cap, hq, vrotation, (int)q_dtype, out,
+                     lse);
+  TQ_LAUNCH_CHECK("fused_combine_kernel");
+  return TQ_OK;
+}
+
+int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
+                               int32_t hkv, const int64_t* slot_mapping, uint8_t* vpool,
+                               float* vnorm_pool, int64_t num_blocks, int32_t block_size,
+                               void* stream) {
+  TQ_REQUIRE(n_tokens >= 0 && hkv >= 1 && num_blocks >= 0, "bad sizes");
+  int bsl = 0;
+  while ((1 << bsl) < block_size) ++bsl;
+  TQ_REQUIRE(block_size >= 64 && (1 << bsl) == block_size,
+             "value tiles need a power-of-two block_size >= 64, got %d", block_size);
+  if (n_tokens == 0) return TQ_OK;
+  TQ_REQUIRE(rows && norms && slot_mapping && vpool && vnorm_pool, "null pointer argument");
+  TQ_REQUIRE((reinterpret_cast<uintptr_t>(vpool) & 3u) == 0, "value pool must be 4-byte aligned");
+  const int64_t total = n_tokens * hkv * kDim;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(paged_vtile_store_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     rows, norms, n_tokens, (int)hkv, slot_mapping, reinterpret_cast<uint32_t*>(vpool),
+                     vnorm_pool, num_blocks << bsl, bsl);
+  TQ_LAUNCH_CHECK("paged_vtile_store_kernel");
+  return TQ_OK;
+}
+
+int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                                 int32_t d, const uint8_t* kpairs_pool, const float* knorm_pool,
+                                 const uint8_t* vtile_pool, const float* vnorm_pool,
+                                 int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
+                                 int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                 const float* kcentroids, const float* vcentroids,
+                                 const float* krotation, const float* vrotation, float scale,
+                                 void* out, float* lse, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  TQ_REQUIRE(d == kDim, "decode layout covers head_dim 64, got %d", d);
+  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
+             "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
+  int bsl = 0;
+  while ((1 << bsl) < block_size) ++bsl;
+  TQ_REQUIRE(block_size >= 64 && (1 << bsl) == block_size,
+             "decode-layout pools need a power-of-two block_size >= 64, got %d", block_size);
+  TQ_REQUIRE(num_blocks >= 0 && max_blocks_per_seq >= 0, "bad sizes");
+  const int64_t t_cap = (int64_t)max_blocks_per_seq * block_size;
+  const int64_t pool_rows = num_blocks * hkv * block_size;
+  TQ_REQUIRE(pool_rows * 32 < (int64_t)INT_MAX, "pools too large for 32-bit offsets");
+  TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
+  if (B == 0) return TQ_OK;
+  TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
+             "null pointer argument");
+  TQ_REQUIRE(t_cap == 0 || (kpairs_pool && knorm_pool && vtile_pool && vnorm_pool && block_tables),
+             "null pointer argument");
+  TQ_REQUIRE((reinterpret_cast<uintptr_t>(krotation) & 15u) == 0, "rotation must be 16-byte aligned");
+  TQ_REQUIRE(t_cap == 0 || ((reinterpret_cast<uintptr_t>(kpairs_pool) | reinterpret_cast<uintptr_t>(vtile_pool) |
+                             reinterpret_cast<uintptr_t>(knorm_pool) | reinterpret_cast<uintptr_t>(vnorm_pool)) &
+                            15u) == 0,
+             "decode-layout pools must be 16-byte aligned");
+  const size_t need = tq_decode_dl_workspace_bytes(B, hq, hkv, t_cap);
+  TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
+  hipStream_t st = as_stream(stream);
+  const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
+  const size_t rows = (size_t)B * hq;
+  char* ws = static_cast<char*>(workspace) + 256;
+  float* part = reinterpret_cast<float*>(ws);
+  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
+  if (t_cap > 0) {
+    DlArgs a{};
+    a.q = q; a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv; a.G = hq / hkv;
+    a.kpairs = kpairs_pool; a.knorms = knorm_pool; a.vblocks = vtile_pool; a.vnorms = vnorm_pool;
+    a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
+    a.krot = krotation; a.qscale = scale * 1.4426950408889634f;
+    a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
+    a.block_tables = block_tables; a.bt_stride = max_blocks_per_seq; a.bs_log2 = bsl;
+    a.pool_rows = (uint32_t)pool_rows;
+    const bool single = p.nsplit == 1;
+    a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
+    const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
+    if (q_dtype == TQ_F32)
+      hipLaunchKernelGGL((dl_decode_kernel<true, true, true>), grid, dim3(kDlThreads), 0, st, a);
+    else if (q_dtype == TQ_F16)
+      hipLaunchKernelGGL((dl_decode_kernel<false, true, true>), grid, dim3(kDlThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((dl_decode_kernel<false, false, true>), grid, dim3(kDlThreads), 0, st, a);
     TQ_LAUNCH_CHECK("dl_decode_kernel");
     if (single) return TQ_OK;
   }

@@ -62,6 +62,10 @@ class TurboQuantKVCacheConfig:
     num_cpu_blocks: int = 0
     protected_layers: int = 0
     seed: int = 42
+    # block pool layout: "bitplane", "decode" (the MFMA decode kernel's layout: mse, 4-bit
+    # keys, 2-bit values, head_dim 64, power-of-two block_size >= 64) or "auto" (decode
+    # where it applies)
+    pool_layout: str = "auto"
 
     def to_turboquant_config(self) -> TurboQuantConfig:
         return TurboQuantConfig(key_bits=self.key_bits, value_bits=self.value_bits, mode=self.mode,
@@ -116,8 +120,13 @@ class TurboQuantPagedKVCache:
         if self._pools is None:
             if self._total_blocks <= 0:
                 raise RuntimeError("TurboQuantPagedKVCache has no blocks. Call allocate() first.")
+            layout = self.config.pool_layout
+            if layout == "auto":
+                layout = ("decode" if PagedKVPools.decode_layout_supported(
+                    self.tq_config, self.head_dim, self.block_size) else "bitplane")
             self._pools = PagedKVPools(self.tq_config, self.num_layers, self._total_blocks,
-                                       self.block_size, self.num_heads, self.head_dim, self.device)
+                                       self.block_size, self.num_heads, self.head_dim, self.device,
+                                       layout=layout)
         return self._pools
 
     def append(self, layer_id: int, key: torch.Tensor, value: torch.Tensor) -> None:

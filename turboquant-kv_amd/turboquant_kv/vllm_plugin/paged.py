@@ -17,6 +17,13 @@ its n new tokens sees the first T - n + i + 1 tokens of its context.
 Keys use `seed`, values `seed + 1`, prod mode the (bits-1)-bit codebook and the QJL
 matrices of seed + 12345 / seed + 1 + 12345 -- the QuantizedKVCache conventions
 (cache.py:56-76).  Protected layers keep fp16 rows in pools of the same block layout.
+
+layout="decode" (mse mode, 4-bit keys, 2-bit values, head_dim 64, block_size a power of
+two >= 64) keeps the quantized layers in the decode layout instead: key pair bytes
+[num_blocks, H, block_size, 32] and 64-token value tiles [num_blocks, H, block_size/64,
+1024], read by the MFMA decode kernel through the block tables
+(`decode_attention_paged_dl`); a prefill sequence runs as that decode with one row per new
+token whose context ends at its own position (the causal mask).
 """
 
 from __future__ import annotations
@@ -58,9 +65,15 @@ class PagedKVPools:
     """A model's paged packed KV storage: per layer, K/V block pools and norms."""
 
     def __init__(self, config: TurboQuantConfig, num_layers: int, num_blocks: int, block_size: int,
-                 num_kv_heads: int, head_dim: int, device="cuda"):
+                 num_kv_heads: int, head_dim: int, device="cuda", layout: str = "bitplane"):
         if config.mode not in ("mse", "prod"):
             raise ValueError(f"Unknown mode: {config.mode}")
+        if layout not in ("bitplane", "decode"):
+            raise ValueError(f"Unknown layout: {layout}")
+        if layout == "decode" and not self.decode_layout_supported(config, head_dim, block_size):
+            raise ValueError("layout='decode' needs mse mode, 4-bit keys, 2-bit values, "
+                             "head_dim 64 and a power-of-two block_size >= 64")
+        self.layout = layout
         self.config = config
         self.num_layers = num_layers
         self.num_blocks = num_blocks
@@ -90,12 +103,23 @@ class PagedKVPools:
                 self.layers.append({"k_fp": torch.zeros(nb, H, bs, head_dim, dtype=torch.float16, device=dev),
                                     "v_fp": torch.zeros(nb, H, bs, head_dim, dtype=torch.float16, device=dev)})
                 continue
+            if layout == "decode":
+                self.layers.append({"kp": torch.zeros(nb, H, bs, head_dim // 2, **u8),
+                                    "kn": torch.zeros(nb, H, bs, **f32),
+                                    "vt": torch.zeros(nb, H, bs // 64, 16 * head_dim, **u8),
+                                    "vn": torch.zeros(nb, H, bs, **f32)})
+                continue
             st = {"k": torch.zeros(nb, H, bs, kb * bpp, **u8), "kn": torch.zeros(nb, H, bs, **f32),
                   "v": torch.zeros(nb, H, bs, vb * bpp, **u8), "vn": torch.zeros(nb, H, bs, **f32)}
             if self.prod:
                 st.update(ks=torch.zeros(nb, H, bs, bpp, **u8), kr=torch.zeros(nb, H, bs, **f32),
                           vs=torch.zeros(nb, H, bs, bpp, **u8), vr=torch.zeros(nb, H, bs, **f32))
             self.layers.append(st)
+
+    @staticmethod
+    def decode_layout_supported(config: TurboQuantConfig, head_dim: int, block_size: int) -> bool:
+        return (config.mode == "mse" and config.key_bits == 4 and config.value_bits == 2
+                and head_dim == 64 and block_size >= 64 and block_size & (block_size - 1) == 0)
 
     # ------------------------------------------------------------------ writes
     def _quantize(self, x: torch.Tensor, R, bnd, cen, S, bits_total):
@@ -121,6 +145,13 @@ class PagedKVPools:
                             getattr(self, "S_k", None), self.config.key_bits)
         vq = self._quantize(value.to(self.device), self.R_v, self.vbnd, self.vcen,
                             getattr(self, "S_v", None), self.config.value_bits)
+        if "kp" in st:
+            pairs = torch.empty(n * H, 1, self.head_dim // 2, dtype=torch.uint8, device=self.device)
+            ops.pack_decode_layout(kq[0].view(n * H, 1, -1), pairs, self.head_dim, 4, False, 0)
+            ops.paged_store(pairs.view(n, H, -1), kq[-1].float().view(n, H), sm, st["kp"], st["kn"])
+            ops.paged_store_value_tiles(vq[0].view(n, H, -1), vq[-1].float().view(n, H), sm,
+                                        st["vt"], st["vn"])
+            return
         ops.paged_store(kq[0].view(n, H, -1), kq[-1].float().view(n, H), sm, st["k"], st["kn"])
         ops.paged_store(vq[0].view(n, H, -1), vq[-1].float().view(n, H), sm, st["v"], st["vn"])
         if self.prod:
@@ -145,6 +176,17 @@ class PagedKVPools:
 
     def _gather(self, st: dict, key: str, block_table: torch.Tensor, T: int):
         """Rows and norms of tokens 0..T-1 of one sequence: ([H, T, P], [H, T])."""
+        if "kp" in st:  # decode layout: back to bit-plane rows
+            d = self.head_dim
+            one = lambda v: torch.tensor([v], dtype=torch.int32, device=self.device)
+            if key == "k":
+                pairs, norms = ops.paged_gather(st["kp"], st["kn"], block_table.view(1, -1), one(T), T)
+                return ops.unpack_decode_layout(pairs[0], d, 4, False, 0, T), norms[0]
+            # value tiles: block_size/64 tiles per block, gathered as rows of 1024 bytes
+            nt = (T + 63) // 64
+            tiles, _ = ops.paged_gather(st["vt"], None, block_table.view(1, -1), one(nt), nt)
+            _, norms = ops.paged_gather(st["kp"], st["vn"], block_table.view(1, -1), one(T), T)
+            return ops.unpack_decode_layout(tiles[0], d, 2, True, 0, T), norms[0]
         norm_key = {"k": "kn", "v": "vn", "ks": "kr", "vs": "vr"}[key]
         rows, norms = ops.paged_gather(st[key], st[norm_key], block_table.view(1, -1),
                                        torch.tensor([T], dtype=torch.int32, device=self.device), T)
@@ -182,6 +224,11 @@ class PagedKVPools:
         H = self.num_kv_heads
         G = Hq // H
         st = self.layers[layer]
+        if "kp" in st:
+            # one decode row per new token, its context ending at its own position
+            bt = block_table.to(self.device, torch.int32).view(1, -1).expand(n, -1).contiguous()
+            lens = torch.arange(T - n + 1, T + 1, dtype=torch.int32, device=self.device)
+            return self._decode_dl(st, q.to(self.device).float(), bt, lens, scale)
         qf = q.to(self.device).float()
         pos = torch.arange(T - n, T, device=self.device)
         mask = torch.arange(T, device=self.device)[None, :] > pos[:, None]       # [n, T]
@@ -220,6 +267,8 @@ class PagedKVPools:
         """One new token per sequence: q [B, Hq, d] over each sequence's first seq_lens[b]
         tokens -> [B, Hq, d] in q's dtype."""
         st = self.layers[layer]
+        if "kp" in st:
+            return self._decode_dl(st, q.to(self.device), block_tables, seq_lens, scale)
         if "k_fp" not in st and not self.prod:
             out, _ = _ops().decode_attention_paged(
                 q.to(self.device), st["k"], st["kn"], st["v"], st["vn"], block_tables, seq_lens,
@@ -229,6 +278,11 @@ class PagedKVPools:
         lens = seq_lens.tolist()
         return torch.cat([self.prefill(layer, q[b:b + 1], block_tables[b], int(lens[b]), scale)
                           for b in range(q.shape[0])]).to(q.dtype)
+
+    def _decode_dl(self, st: dict, q, block_tables, seq_lens, scale) -> torch.Tensor:
+        return ops.decode_attention_paged_dl(q, st["kp"], st["kn"], st["vt"], st["vn"], block_tables,
+                                             seq_lens, self.kcen, self.vcen, self.R_k, self.R_v,
+                                             float(scale))
 
     def forward(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                 md: TurboQuantAttentionMetadata, scale: float,
