@@ -232,7 +232,23 @@ def bench_decode(args, extra):
                                                "paged_bs16_GBps": bytes_alg / ms_pg / 1e6})
             log(f"decode T={T} paged (block 16, shuffled): {ms_pg * 1e3:.1f} us, "
                 f"{bytes_alg / ms_pg / 1e6:.0f} GB/s")
-            del pk, pkn, pv, pvn
+            # the decode layout in block pools of 64 tokens (one value tile per block),
+            # blocks shuffled, read by the MFMA decode kernel through the table
+            bs = 64
+            nbs = T // bs
+            perm = torch.randperm(B * nbs, generator=g, device="cuda")
+            tab = perm.view(B, nbs).to(torch.int32)
+            pkn, pvn = to_pool(c[1]), to_pool(c[3])
+            pkp = to_pool(c[4])
+            pvt = torch.empty(B * nbs, Hkv, 1, 16 * d, dtype=torch.uint8, device="cuda")
+            pvt[perm] = c[5].transpose(1, 2).reshape(B * nbs, Hkv, 1, 16 * d)
+            ms_pdl = time_op(lambda: ops.decode_attention_paged_dl(q, pkp, pkn, pvt, pvn, tab, sl, ck,
+                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3)
+            extra[f"decode_attn_T{T}"].update({"paged_dl_bs64_us": ms_pdl * 1e3,
+                                               "paged_dl_bs64_GBps": bytes_alg / ms_pdl / 1e6})
+            log(f"decode T={T} paged decode layout (block 64, shuffled): {ms_pdl * 1e3:.1f} us, "
+                f"{bytes_alg / ms_pdl / 1e6:.0f} GB/s")
+            del pkp, pkn, pvt, pvn
         del caches
     return out
 
