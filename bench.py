@@ -232,6 +232,20 @@ def bench_decode(args, extra):
                                                "paged_bs16_GBps": bytes_alg / ms_pg / 1e6})
             log(f"decode T={T} paged (block 16, shuffled): {ms_pg * 1e3:.1f} us, "
                 f"{bytes_alg / ms_pg / 1e6:.0f} GB/s")
+            del pk, pv
+            # the decode layout in the same block-16 pools (16-token value sub-blocks)
+            pkp = to_pool(c[4])
+            sub = c[5].reshape(B, Hkv, T // 64, 64, 4, 4).permute(0, 1, 2, 4, 3, 5)
+            sub = sub.reshape(B, Hkv, nbs, 1, 4 * d).transpose(1, 2)
+            pvs = torch.empty(B * nbs, Hkv, 1, 4 * d, dtype=torch.uint8, device="cuda")
+            pvs[perm] = sub.reshape(B * nbs, Hkv, 1, 4 * d)
+            ms_p16 = time_op(lambda: ops.decode_attention_paged_dl(q, pkp, pkn, pvs, pvn, tab, sl, ck,
+                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3)
+            extra[f"decode_attn_T{T}"].update({"paged_dl_bs16_us": ms_p16 * 1e3,
+                                               "paged_dl_bs16_GBps": bytes_alg / ms_p16 / 1e6})
+            log(f"decode T={T} paged decode layout (block 16, shuffled): {ms_p16 * 1e3:.1f} us, "
+                f"{bytes_alg / ms_p16 / 1e6:.0f} GB/s")
+            del pkp, pkn, pvs, pvn, sub
             # the decode layout in block pools of 64 tokens (one value tile per block),
             # blocks shuffled, read by the MFMA decode kernel through the table
             bs = 64

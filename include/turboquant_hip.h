@@ -313,13 +313,17 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
 
 /*
  * Paged pools in the decode layout (4-bit keys, 2-bit values, head_dim 64): the same
- * kernel as tq_decode_attention_dl with one block lookup per 64-token tile, for vLLM
- * block sizes that are powers of two >= 64 (so a tile never straddles blocks).  Replaces,
- * like tq_decode_attention_paged, the reference backend's forward
- * (turboquant_kv/vllm_plugin/__init__.py:209-304) at those block sizes.
+ * kernel as tq_decode_attention_dl with block lookups per 64-token tile (one for block
+ * sizes >= 64, one per 16-token group below), for power-of-two block sizes >= 16.
+ * Replaces, like tq_decode_attention_paged, the reference backend's forward
+ * (turboquant_kv/vllm_plugin/__init__.py:209-304).
  *   kpairs_pool [num_blocks][hkv][block_size][32]   key pair bytes (tq_pack_decode_layout,
  *                                                   values = 0) stored with tq_paged_store
- *   vtile_pool  [num_blocks][hkv][block_size/64][1024] value tiles (byte layout above)
+ *   vtile_pool  block_size >= 64: [num_blocks][hkv][block_size/64][1024] value tiles
+ *               (byte layout above); block_size 16, 32: [num_blocks][hkv][block_size/16]
+ *               [256] sub-blocks, token t of one at byte 4*(16*sl + c) + dg, bits 2*(t%4),
+ *               sl = t/4, dim 16*dg + c (bytes 16L + 4m + dg of a 64-token tile row are
+ *               byte 4L + dg of its sub-block m)
  *   knorm_pool, vnorm_pool [num_blocks][hkv][block_size]
  * tq_paged_store_value_tiles writes new tokens' 2-bit value rows [n_tokens][hkv][16]
  * (bit planes) and norms [n_tokens][hkv] into their slots (slot_mapping as in

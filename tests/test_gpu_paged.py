@@ -186,9 +186,32 @@ def _step_meta(blocks, before, n_new, bs):
     return md, order, lens, tab
 
 
-@pytest.mark.parametrize("mode,kb,vb,d,G", [("mse", 4, 2, 64, 4), ("mse", 3, 2, 128, 2),
-                                            ("prod", 4, 3, 64, 2)])
-def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G):
+def _bitplane_pools(pools, tab, lens):
+    """The layer-0 pools as numpy arrays; decode-layout pools are converted to bit-plane
+    rows (through the pools' own gather + unpack) at the sequences' blocks."""
+    st = pools.layers[0]
+    P = {key: t.cpu().numpy() for key, t in st.items()}
+    if "kp" not in st:
+        return P
+    nb, H, bs = st["kn"].shape
+    out = {"k": np.zeros((nb, H, bs, 32), np.uint8), "v": np.zeros((nb, H, bs, 16), np.uint8),
+           "kn": np.zeros((nb, H, bs), np.float32), "vn": np.zeros((nb, H, bs), np.float32)}
+    for j, n in enumerate(lens):
+        bt = torch.from_numpy(tab[j]).to(DEV)
+        for kind in ("k", "v"):
+            rows, norms = pools._gather(st, kind, bt, n)
+            rows, norms = rows.cpu().numpy(), norms.cpu().numpy()
+            for t in range(n):
+                out[kind][tab[j, t // bs], :, t % bs] = rows[:, t]
+                out[kind + "n"][tab[j, t // bs], :, t % bs] = norms[:, t]
+    return out
+
+
+@pytest.mark.parametrize("mode,kb,vb,d,G,layout", [("mse", 4, 2, 64, 4, "bitplane"),
+                                                   ("mse", 4, 2, 64, 4, "auto"),
+                                                   ("mse", 3, 2, 128, 2, "auto"),
+                                                   ("prod", 4, 3, 64, 2, "auto")])
+def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G, layout):
     # Two steps through the vLLM entry: a batch of prompts (prefill), then a mixed batch
     # -- a chunked prefill continuing one sequence and single-token decodes of the
     # others -- each checked against the float64 paged oracle (causal, GQA).
@@ -198,9 +221,11 @@ def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G):
     Hkv, bs, nb = 2, 16, 64
     Hq = G * Hkv
     cfg = TurboQuantKVCacheConfig(key_bits=kb, value_bits=vb, mode=mode, block_size=bs,
-                                  num_gpu_blocks=nb)
+                                  num_gpu_blocks=nb, pool_layout=layout)
     kv = TurboQuantPagedKVCache(cfg, num_layers=1, num_heads=Hkv, head_dim=d, device=DEV)
     pools = kv.pools()
+    assert pools.layout == ("decode" if (mode, kb, vb, d, layout) == ("mse", 4, 2, 64, "auto")
+                            else "bitplane")
     scale = 1.0 / math.sqrt(d)
     steps = [[40, 17, 70, 5], [30, 1, 1, 1]]   # new tokens per sequence in each step
     final = [sum(s[i] for s in steps) for i in range(4)]
@@ -219,7 +244,7 @@ def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G):
         v = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)
         out = paged_attention_step(q, k, v, kv, md, scale)
         assert out.shape == q.shape and out.dtype == q.dtype
-        P = {key: t.cpu().numpy() for key, t in pools.layers[0].items()}
+        P = _bitplane_pools(pools, tab, lens)
         kc, vc = pools.kcen.cpu().numpy(), pools.vcen.cpu().numpy()
         Rk, Rv = pools.R_k.cpu().numpy(), pools.R_v.cpu().numpy()
         kprod = vprod = None
@@ -286,7 +311,8 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv):
     vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
     knp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
-    vt = torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV)
+    vt = (torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV) if bs >= 64 else
+          torch.zeros(nb, Hkv, bs // 16, 256, dtype=torch.uint8, device=DEV))
     vnp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
     pairs = torch.empty(n * Hkv, 1, 32, dtype=torch.uint8, device=DEV)
     ops.pack_decode_layout(T(krows).view(n * Hkv, 1, 32), pairs, 64, 4, False, 0)
@@ -310,9 +336,10 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv):
     return tab, kp, knp, vt, vnp, seqs
 
 
-@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
 def test_paged_dl_store_round_trip(bs):
     from turboquant_kv import ops
+    from turboquant_kv.vllm_plugin.paged import gather_value_tiles
     rs = np.random.RandomState(bs)
     Hkv, lens = 2, [130, 64, 1, 0]
     width = (max(lens) + bs - 1) // bs + 1
@@ -324,17 +351,17 @@ def test_paged_dl_store_round_trip(bs):
         one = lambda v: torch.tensor([v], dtype=torch.int32, device=DEV)
         bt = T(tab[b:b + 1])
         pr, pn = ops.paged_gather(kp, knp, bt, one(n), n)
-        nt = (n + 63) // 64
-        tiles, _ = ops.paged_gather(vt, None, bt, one(nt), nt)
+        tiles = gather_value_tiles(vt, bt, n)
         _, vnn = ops.paged_gather(kp, vnp, bt, one(n), n)
         kr, knr, vr, vnr = seqs[b]
         assert np.array_equal(ops.unpack_decode_layout(pr[0], 64, 4, False, 0, n).cpu().numpy(), kr)
-        assert np.array_equal(ops.unpack_decode_layout(tiles[0], 64, 2, True, 0, n).cpu().numpy(), vr)
+        assert np.array_equal(ops.unpack_decode_layout(tiles, 64, 2, True, 0, n).cpu().numpy(), vr)
         assert np.array_equal(pn[0].cpu().numpy(), knr) and np.array_equal(vnn[0].cpu().numpy(), vnr)
 
 
 @pytest.mark.parametrize("bs,G,qdt", [(64, 4, torch.bfloat16), (128, 2, torch.float16),
-                                      (64, 1, torch.float32)])
+                                      (64, 1, torch.float32), (16, 4, torch.bfloat16),
+                                      (32, 2, torch.float16), (16, 1, torch.float32)])
 def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     from turboquant_kv import ops
     rs = np.random.RandomState(bs + G)
@@ -343,6 +370,7 @@ def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     lens = [0, 3, 700, 1500, 64]
     B = len(lens)
     width = (max(lens) + bs - 1) // bs + 1
+    width = -(-width * bs // 64) * 64 // bs   # the contiguous reference needs t_cap % 64 == 0
     nb = sum((n + bs - 1) // bs for n in lens) + 4
     tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
     tab[0, 0] = 7   # a block id past sequence 0's (empty) context: never read
@@ -388,13 +416,14 @@ def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     assert np.max(np.abs(got - want)) <= tol * np.max(np.abs(want))
 
 
-def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64():
+@pytest.mark.parametrize("bs", [64, 16])
+def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
     # The vLLM step (chunked prefill + decodes) on decode-layout pools: the stored codes
     # equal the bit-plane pools' and outputs match the float64 paged oracle.
     from turboquant_kv.vllm_plugin import PagedKVPools
     from turboquant_kv.config import TurboQuantConfig
     rs = np.random.RandomState(11)
-    Hkv, Hq, d, bs, nb = 2, 8, 64, 64, 24
+    Hkv, Hq, d, nb = 2, 8, 64, 24 * 64 // bs
     cfg = TurboQuantConfig(key_bits=4, value_bits=2)
     bp = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV)
     dl = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV, layout="decode")

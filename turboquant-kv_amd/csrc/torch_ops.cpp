@@ -827,11 +827,14 @@ void paged_store_value_tiles(const at::Tensor& rows, const at::Tensor& norms,
                              at::Tensor& vnorm_pool) {
   require_gpu(vtile_pool, "vtile_pool");
   TORCH_CHECK(vtile_pool.dim() == 4 && vtile_pool.scalar_type() == at::kByte &&
-                  vtile_pool.is_contiguous() && vtile_pool.size(3) == 1024,
-              "vtile_pool must be contiguous uint8 [num_blocks, hkv, block_size/64, 1024]");
+                  vtile_pool.is_contiguous() && (vtile_pool.size(3) == 1024 || vtile_pool.size(3) == 256),
+              "vtile_pool must be contiguous uint8 [num_blocks, hkv, block_size/64, 1024] "
+              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 256] (block_size 16, 32)");
   c10::DeviceGuard g(vtile_pool.device());
   const auto dev = vtile_pool.device();
-  const int64_t nb = vtile_pool.size(0), hkv = vtile_pool.size(1), bs = vtile_pool.size(2) * 64;
+  const int64_t nb = vtile_pool.size(0), hkv = vtile_pool.size(1);
+  const int64_t bs = vtile_pool.size(2) * (vtile_pool.size(3) == 1024 ? 64 : 16);
+  TORCH_CHECK((vtile_pool.size(3) == 1024) == (bs >= 64), "value tile shape does not match block_size");
   TORCH_CHECK(rows.dim() == 3 && rows.scalar_type() == at::kByte && rows.size(1) == hkv &&
                   rows.size(2) == 16,
               "rows must be uint8 [n, hkv, 16] (2-bit codes of d = 64)");
@@ -869,9 +872,11 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
     TORCH_CHECK(t->device() == dev && t->is_contiguous(), "pools must be contiguous on the query's device");
   TORCH_CHECK(kpairs_pool.scalar_type() == at::kByte && vtile_pool.scalar_type() == at::kByte,
               "pools must be uint8");
+  const int64_t tile_tokens = bs >= 64 ? 64 : 16;
   TORCH_CHECK(kpairs_pool.size(3) == d / 2 && vtile_pool.size(0) == nb && vtile_pool.size(1) == Hkv &&
-                  vtile_pool.size(2) * 64 == bs && vtile_pool.size(3) == 16 * d,
-              "decode-layout pool shapes mismatch");
+                  vtile_pool.size(2) * tile_tokens == bs && vtile_pool.size(3) == tile_tokens * d / 4,
+              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, 16d] "
+              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 4d] (block_size 16, 32)");
   TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
                   knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
               "norm pools must be float32 [num_blocks, hkv, block_size]");

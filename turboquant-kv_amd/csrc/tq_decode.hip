@@ -33,6 +33,7 @@
 #include "tq_decode.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <climits>
 #include <cstdlib>
 
@@ -471,8 +472,8 @@ struct DlArgs {
   float* lse;
   // Paged pools (PAGED kernels): block b of a sequence holds its tokens [b*bs, (b+1)*bs);
   // kpairs [num_blocks][hkv][bs][32], knorms/vnorms [num_blocks][hkv][bs], vblocks
-  // [num_blocks][hkv][bs/64][1024]; bs a power of two >= 64, so a 64-token tile lies in
-  // one block.
+  // [num_blocks][hkv][bs/64][1024] for bs a power of two >= 64 (a 64-token tile lies in
+  // one block), [num_blocks][hkv][bs/16][256] for bs 16 or 32.
   const int32_t* block_tables;
   int bt_stride;
   int bs_log2;
@@ -541,8 +542,12 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // relative), for fp32 and fp16 outputs; otherwise (bf16 outputs) one fp16 product per
 // term, about 2^-11 relative per operand -- finer than the bf16 arithmetic the reference
 // scores bf16 inputs in.
-template <bool EXACT_V, bool PREC_K, bool PAGED = false>
+// PG: 0 contiguous caches; 1 paged pools of block_size >= 64 (64-token value tiles);
+// 2 paged pools of block_size 16 or 32 (16-token value sub-blocks of 256 B: lane
+// 16 sl + c's word holds what word m of its 64-token tile row holds for sub-block m).
+template <bool EXACT_V, bool PREC_K, int PG = 0>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
+  constexpr bool PAGED = PG != 0, SUB16 = PG == 2;
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
   // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
   // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
@@ -605,28 +610,58 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
     float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
   };
-  // Paged: block id of the tile at t0 (one per tile, the same in every lane), requested
-  // a tile ahead of the tile's own loads.
-  auto load_block = [&](int t0) -> uint32_t {
-    if constexpr (!PAGED) return 0u;
-    return __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)t0 >> bsl) * 4), 0, 0);
+  // Paged: block id of the tile at t0 (one per tile, the same in every lane; SUB16: one
+  // per 16-token group of the tile), requested a tile ahead of the tile's own loads.
+  using Blk = typename std::conditional<SUB16, u32x4, uint32_t>::type;
+  auto load_block = [&](int t0) -> Blk {
+    if constexpr (!PAGED) {
+      return Blk{};
+    } else if constexpr (!SUB16) {
+      return __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)t0 >> bsl) * 4), 0, 0);
+    } else {
+      Blk r;
+      r.x = __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)t0 >> bsl) * 4), 0, 0);
+      r.y = __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)(t0 + 16) >> bsl) * 4), 0, 0);
+      r.z = __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)(t0 + 32) >> bsl) * 4), 0, 0);
+      r.w = __builtin_amdgcn_raw_buffer_load_b32(btrs, (int)(((uint32_t)(t0 + 48) >> bsl) * 4), 0, 0);
+      return r;
+    }
   };
-  auto load_tile = [&](int t0, Tile& x, uint32_t blk) {
-    // r0: pool row of the tile's first token; vt: its value tile
-    uint32_t r0 = (uint32_t)t0, vt = (uint32_t)t0 >> 6;
-    if constexpr (PAGED) {
+  auto load_tile = [&](int t0, Tile& x, Blk blk) {
+    // rg[g]: pool row of the first token of the tile's 16-token group g; vt: value tile
+    uint32_t rg[4], vt = (uint32_t)t0 >> 6;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) rg[g] = (uint32_t)t0 + 16 * g;
+    if constexpr (PG == 1) {
       const uint32_t sb = blk * (uint32_t)a.hkv + (uint32_t)kvh;
       const uint32_t in = (uint32_t)t0 & ((1u << bsl) - 1);
-      r0 = (sb << bsl) | in;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) rg[g] = ((sb << bsl) | in) + 16 * g;
       vt = (sb << (bsl - 6)) | (in >> 6);
+    } else if constexpr (SUB16) {
+      const uint32_t bl[4] = {blk.x, blk.y, blk.z, blk.w};
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        rg[g] = ((bl[g] * (uint32_t)a.hkv + (uint32_t)kvh) << bsl) |
+                (((uint32_t)t0 + 16 * g) & ((1u << bsl) - 1));
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((r0 + 16 * g + col) * 32 + 8 * sl), 0, 0);
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * 1024 + lane * 16), 0, 0);
-    x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
-    // norms of the lane's four tokens: 16-byte aligned (t_cap % 64 == 0, aligned base)
-    const uint32_t no = (r0 + 16 * gq + 4 * sl) * 4;
+      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 + 8 * sl), 0, 0);
+    if constexpr (SUB16) {
+      // value sub-block of group m = its first pool row / 16 (rows of a group are 16-aligned)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)((rg[m] >> 4) * 256 + lane * 4), 0, 0);
+    } else {
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * 1024 + lane * 16), 0, 0);
+      x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+    }
+    // norms of the lane's four tokens (group gq): 16-byte aligned (t_cap % 64 == 0,
+    // aligned base)
+    uint32_t rq = rg[0] + 16 * gq;
+    if constexpr (SUB16) rq = gq == 0 ? rg[0] : gq == 1 ? rg[1] : gq == 2 ? rg[2] : rg[3];
+    const uint32_t no = (rq + 4 * sl) * 4;
     const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
     const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
     // (__builtin_bit_cast of a vector element would read element 0: convert by value)
@@ -664,7 +699,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 #pragma unroll
     for (int k = 0; k < kDim / 4; ++k) rrow[k] = r4[k];
   }
-  uint32_t bnx = 0;  // paged: block id of the next tile to load
+  Blk bnx{};  // paged: block id(s) of the next tile to load
   load_tile(tf, ta, load_block(tf));
   load_tile(tf + kStep, tb, load_block(tf + kStep));
   bnx = load_block(tf + 2 * kStep);
@@ -944,11 +979,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // range check); the tile count is made wave-uniform explicitly.
   for (int it = 0; it < ntiles; it += 3) {
     const int t = tf + it * kStep;
-    uint32_t b1 = load_block(t + 3 * kStep);
+    const Blk b1 = load_block(t + 3 * kStep);
     load_tile(t + 2 * kStep, tc, bnx);
     process(ta, t);
     if (it + 1 >= ntiles) break;
-    uint32_t b2 = load_block(t + 4 * kStep);
+    const Blk b2 = load_block(t + 4 * kStep);
     load_tile(t + 3 * kStep, ta, b1);
     process(tb, t + kStep);
     if (it + 2 >= ntiles) break;
@@ -1203,10 +1238,11 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
 namespace tq {
 namespace {
 
-// New tokens' 2-bit value codes (bit-plane rows [n][hkv][16], d = 64) into the 64-token
-// value tiles of a paged pool, one thread per (token, head, dim).  Token t of tile T sits
-// at byte 16 (16 sl + c) + 4 m + dg, bits 2 (t % 4), with 4 m + sl = (t % 64) / 4, dim =
-// 16 dg + c (the decode layout).  Tokens of one tile share bytes, so each field is cleared
+// New tokens' 2-bit value codes (bit-plane rows [n][hkv][16], d = 64) into the value
+// tiles of a paged pool, one thread per (token, head, dim).  Token t of a 64-token tile
+// sits at byte 16 (16 sl + c) + 4 m + dg, bits 2 (t % 4), with 4 m + sl = (t % 64) / 4,
+// dim = 16 dg + c (the decode layout); below block_size 64, token t of a 16-token
+// sub-block sits at byte 4 (16 sl + c) + dg, sl = (t % 16) / 4.  Tokens of one tile share bytes, so each field is cleared
 // and set with 32-bit atomics (disjoint bits: concurrent tokens do not interfere); slots
 // outside the pool are skipped.
 __global__ __launch_bounds__(256) void paged_vtile_store_kernel(
@@ -1226,10 +1262,18 @@ __global__ __launch_bounds__(256) void paged_vtile_store_kernel(
     const uint8_t* row = rows + th * 16;  // plane 0: bytes 0-7, plane 1: bytes 8-15
     const uint32_t code = ((row[j >> 3] >> (7 - (j & 7))) & 1u) | (((row[8 + (j >> 3)] >> (7 - (j & 7))) & 1u) << 1);
     const int tt = off & 63, q4 = tt >> 2;
-    const int byte = 16 * (16 * (q4 & 3) + (j & 15)) + 4 * (q4 >> 2) + (j >> 4);
-    const int shift = 8 * (byte & 3) + 2 * (tt & 3);
-    const int64_t tile = ((blk * hkv + h) << (bs_log2 - 6)) + (off >> 6);
-    uint32_t* w = vpool + tile * 256 + (byte >> 2);
+    uint32_t* w;
+    int shift;
+    if (bs_log2 >= 6) {  // 64-token tiles of 1024 B
+      const int byte = 16 * (16 * (q4 & 3) + (j & 15)) + 4 * (q4 >> 2) + (j >> 4);
+      shift = 8 * (byte & 3) + 2 * (tt & 3);
+      const int64_t tile = ((blk * hkv + h) << (bs_log2 - 6)) + (off >> 6);
+      w = vpool + tile * 256 + (byte >> 2);
+    } else {  // 16-token sub-blocks of 256 B: byte 4 (16 sl + c) + dg
+      shift = 8 * (j >> 4) + 2 * (tt & 3);
+      const int64_t sub = (((blk * hkv + h) << bs_log2) + off) >> 4;
+      w = vpool + sub * 64 + 16 * (q4 & 3) + (j & 15);
+    }
     atomicAnd(w, ~(3u << shift));
     atomicOr(w, code << shift);
     if (j == 0) vnorm_pool[((blk * hkv + h) << bs_log2) + off] = norms[th];
@@ -1334,8 +1378,8 @@ int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t 
   TQ_REQUIRE(n_tokens >= 0 && hkv >= 1 && num_blocks >= 0, "bad sizes");
   int bsl = 0;
   while ((1 << bsl) < block_size) ++bsl;
-  TQ_REQUIRE(block_size >= 64 && (1 << bsl) == block_size,
-             "value tiles need a power-of-two block_size >= 64, got %d", block_size);
+  TQ_REQUIRE(block_size >= 16 && (1 << bsl) == block_size,
+             "value tiles need a power-of-two block_size >= 16, got %d", block_size);
   if (n_tokens == 0) return TQ_OK;
   TQ_REQUIRE(rows && norms && slot_mapping && vpool && vnorm_pool, "null pointer argument");
   TQ_REQUIRE((reinterpret_cast<uintptr_t>(vpool) & 3u) == 0, "value pool must be 4-byte aligned");
@@ -1363,8 +1407,8 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
              "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
   int bsl = 0;
   while ((1 << bsl) < block_size) ++bsl;
-  TQ_REQUIRE(block_size >= 64 && (1 << bsl) == block_size,
-             "decode-layout pools need a power-of-two block_size >= 64, got %d", block_size);
+  TQ_REQUIRE(block_size >= 16 && (1 << bsl) == block_size,
+             "decode-layout pools need a power-of-two block_size >= 16, got %d", block_size);
   TQ_REQUIRE(num_blocks >= 0 && max_blocks_per_seq >= 0, "bad sizes");
   const int64_t t_cap = (int64_t)max_blocks_per_seq * block_size;
   const int64_t pool_rows = num_blocks * hkv * block_size;
@@ -1400,12 +1444,21 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
     const bool single = p.nsplit == 1;
     a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
     const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
-    if (q_dtype == TQ_F32)
-      hipLaunchKernelGGL((dl_decode_kernel<true, true, true>), grid, dim3(kDlThreads), 0, st, a);
-    else if (q_dtype == TQ_F16)
-      hipLaunchKernelGGL((dl_decode_kernel<false, true, true>), grid, dim3(kDlThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((dl_decode_kernel<false, false, true>), grid, dim3(kDlThreads), 0, st, a);
+    if (bsl >= 6) {
+      if (q_dtype == TQ_F32)
+        hipLaunchKernelGGL((dl_decode_kernel<true, true, 1>), grid, dim3(kDlThreads), 0, st, a);
+      else if (q_dtype == TQ_F16)
+        hipLaunchKernelGGL((dl_decode_kernel<false, true, 1>), grid, dim3(kDlThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((dl_decode_kernel<false, false, 1>), grid, dim3(kDlThreads), 0, st, a);
+    } else {
+      if (q_dtype == TQ_F32)
+        hipLaunchKernelGGL((dl_decode_kernel<true, true, 2>), grid, dim3(kDlThreads), 0, st, a);
+      else if (q_dtype == TQ_F16)
+        hipLaunchKernelGGL((dl_decode_kernel<false, true, 2>), grid, dim3(kDlThreads), 0, st, a);
+      else
+        hipLaunchKernelGGL((dl_decode_kernel<false, false, 2>), grid, dim3(kDlThreads), 0, st, a);
+    }
     TQ_LAUNCH_CHECK("dl_decode_kernel");
     if (single) return TQ_OK;
   }

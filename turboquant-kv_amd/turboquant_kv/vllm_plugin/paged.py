@@ -19,9 +19,10 @@ matrices of seed + 12345 / seed + 1 + 12345 -- the QuantizedKVCache conventions
 (cache.py:56-76).  Protected layers keep fp16 rows in pools of the same block layout.
 
 layout="decode" (mse mode, 4-bit keys, 2-bit values, head_dim 64, block_size a power of
-two >= 64) keeps the quantized layers in the decode layout instead: key pair bytes
-[num_blocks, H, block_size, 32] and 64-token value tiles [num_blocks, H, block_size/64,
-1024], read by the MFMA decode kernel through the block tables
+two >= 16) keeps the quantized layers in the decode layout instead: key pair bytes
+[num_blocks, H, block_size, 32] and value tiles -- [num_blocks, H, block_size/64, 1024]
+(64-token tiles) for block sizes >= 64, [num_blocks, H, block_size/16, 256] (16-token
+sub-blocks) below -- read by the MFMA decode kernel through the block tables
 (`decode_attention_paged_dl`); a prefill sequence runs as that decode with one row per new
 token whose context ends at its own position (the causal mask).
 """
@@ -61,6 +62,23 @@ class TurboQuantAttentionMetadata:
     layer_id: int = 0
 
 
+def gather_value_tiles(vt_pool: torch.Tensor, block_table: torch.Tensor, T: int) -> torch.Tensor:
+    """Value tiles of tokens 0..T-1 of one sequence from a decode-layout pool, in the
+    contiguous decode layout [H, ceil(T/64), 1024] (unpack_decode_layout's input)."""
+    nb, H, per_block, width = vt_pool.shape
+    dev = vt_pool.device
+    n = (T + 63) // 64 if width == 1024 else (T + 15) // 16
+    tiles, _ = ops.paged_gather(vt_pool, None, block_table.view(1, -1),
+                                torch.tensor([n], dtype=torch.int32, device=dev), n)
+    if width == 1024:
+        return tiles[0]
+    # 16-token sub-blocks: sub-block m of a tile holds word m of each lane's 16 bytes
+    nt = (T + 63) // 64
+    sub = torch.zeros(H, nt * 4, 256, dtype=torch.uint8, device=dev)
+    sub[:, :n] = tiles[0]
+    return sub.view(H, nt, 4, 64, 4).permute(0, 1, 3, 2, 4).reshape(H, nt, 1024)
+
+
 class PagedKVPools:
     """A model's paged packed KV storage: per layer, K/V block pools and norms."""
 
@@ -72,7 +90,7 @@ class PagedKVPools:
             raise ValueError(f"Unknown layout: {layout}")
         if layout == "decode" and not self.decode_layout_supported(config, head_dim, block_size):
             raise ValueError("layout='decode' needs mse mode, 4-bit keys, 2-bit values, "
-                             "head_dim 64 and a power-of-two block_size >= 64")
+                             "head_dim 64 and a power-of-two block_size >= 16")
         self.layout = layout
         self.config = config
         self.num_layers = num_layers
@@ -106,7 +124,8 @@ class PagedKVPools:
             if layout == "decode":
                 self.layers.append({"kp": torch.zeros(nb, H, bs, head_dim // 2, **u8),
                                     "kn": torch.zeros(nb, H, bs, **f32),
-                                    "vt": torch.zeros(nb, H, bs // 64, 16 * head_dim, **u8),
+                                    "vt": (torch.zeros(nb, H, bs // 64, 1024, **u8) if bs >= 64
+                                           else torch.zeros(nb, H, bs // 16, 256, **u8)),
                                     "vn": torch.zeros(nb, H, bs, **f32)})
                 continue
             st = {"k": torch.zeros(nb, H, bs, kb * bpp, **u8), "kn": torch.zeros(nb, H, bs, **f32),
@@ -119,7 +138,7 @@ class PagedKVPools:
     @staticmethod
     def decode_layout_supported(config: TurboQuantConfig, head_dim: int, block_size: int) -> bool:
         return (config.mode == "mse" and config.key_bits == 4 and config.value_bits == 2
-                and head_dim == 64 and block_size >= 64 and block_size & (block_size - 1) == 0)
+                and head_dim == 64 and block_size >= 16 and block_size & (block_size - 1) == 0)
 
     # ------------------------------------------------------------------ writes
     def _quantize(self, x: torch.Tensor, R, bnd, cen, S, bits_total):
@@ -182,11 +201,9 @@ class PagedKVPools:
             if key == "k":
                 pairs, norms = ops.paged_gather(st["kp"], st["kn"], block_table.view(1, -1), one(T), T)
                 return ops.unpack_decode_layout(pairs[0], d, 4, False, 0, T), norms[0]
-            # value tiles: block_size/64 tiles per block, gathered as rows of 1024 bytes
-            nt = (T + 63) // 64
-            tiles, _ = ops.paged_gather(st["vt"], None, block_table.view(1, -1), one(nt), nt)
+            tiles = gather_value_tiles(st["vt"], block_table, T)
             _, norms = ops.paged_gather(st["kp"], st["vn"], block_table.view(1, -1), one(T), T)
-            return ops.unpack_decode_layout(tiles[0], d, 2, True, 0, T), norms[0]
+            return ops.unpack_decode_layout(tiles, d, 2, True, 0, T), norms[0]
         norm_key = {"k": "kn", "v": "vn", "ks": "kr", "vs": "vr"}[key]
         rows, norms = ops.paged_gather(st[key], st[norm_key], block_table.view(1, -1),
                                        torch.tensor([T], dtype=torch.int32, device=self.device), T)
