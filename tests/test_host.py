@@ -218,3 +218,22 @@ def test_huffman_round_trip_limits_and_short_streams():
     st = EntropyPackedStorage.from_codes(codes.view(-1, 100), 4, 128)
     assert st.to_codes().shape == (2000, 100)
     assert 0 < st.savings_pct < 10  # ~3.8 bits/code against 4
+
+
+def test_paged_pool_layout_selection():
+    # Decode-layout pools take mse K4/V2 at head_dim 64 and power-of-two block sizes >= 16;
+    # anything else is refused up front (before any allocation), and the vLLM cache config's
+    # "auto" resolves to the decode layout exactly where it applies.
+    from turboquant_kv.config import TurboQuantConfig
+    from turboquant_kv.vllm_plugin.paged import PagedKVPools
+    ok = PagedKVPools.decode_layout_supported
+    mse = TurboQuantConfig(key_bits=4, value_bits=2)
+    assert ok(mse, 64, 16) and ok(mse, 64, 32) and ok(mse, 64, 64) and ok(mse, 64, 256)
+    assert not ok(mse, 64, 8) and not ok(mse, 64, 48) and not ok(mse, 128, 16)
+    assert not ok(TurboQuantConfig(key_bits=3, value_bits=2), 64, 16)
+    assert not ok(TurboQuantConfig(key_bits=4, value_bits=2, mode="prod"), 64, 16)
+    for cfg, d, bs in ((TurboQuantConfig(mode="prod"), 64, 16), (mse, 64, 24), (mse, 128, 64)):
+        with pytest.raises(ValueError, match="layout='decode'"):
+            PagedKVPools(cfg, 1, 4, bs, 2, d, device="cpu", layout="decode")
+    with pytest.raises(ValueError, match="Unknown layout"):
+        PagedKVPools(mse, 1, 4, 16, 2, 64, device="cpu", layout="tiles")
