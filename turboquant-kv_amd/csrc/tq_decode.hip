@@ -563,8 +563,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   char* const ktab = tabs + kDlTab;
   char* const vtab = tabs;
 
-  const int split = blockIdx.x;
-  const int bg = blockIdx.y;
+  int split = blockIdx.x, bg = blockIdx.y;
+  if constexpr (PAGED) {
+    // XCD-aware order: workgroups go to the 8 XCDs round-robin in linear order, so linear
+    // id L runs on XCD L % 8.  Work item W = (L % 8) * (N / 8) + L / 8 puts consecutive
+    // (sequence, kv head) streams on one XCD, where the norm lines that adjacent heads of
+    // a block share are fetched into that XCD's L2 once.
+    const uint32_t N = gridDim.x * gridDim.y;
+    if ((N & 7u) == 0) {
+      const uint32_t L = blockIdx.x + blockIdx.y * gridDim.x;
+      const uint32_t W = (L & 7u) * (N >> 3) + (L >> 3);
+      split = (int)(W % gridDim.x);
+      bg = (int)(W / gridDim.x);
+    }
+  }
   const int b = bg / a.hkv;
   const int g = bg - b * a.hkv;
   const int64_t T = min((int64_t)max(a.seq_lens[b], 0), a.t_cap);
