@@ -463,3 +463,24 @@ def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
             ref = out_bp[a:b].float().cpu().numpy()
             assert np.max(np.abs(got - ref)) <= 2e-2 * np.max(np.abs(want)), (step, j)
         before = [before[i] + n_new[i] for i in range(4)]
+
+
+def test_decode_layout_prefill_in_chunks_equals_one_launch():
+    # A prefill whose (token, kv head) streams exceed one launch's limit runs in chunks;
+    # the chunked result equals the single launch's bit for bit.
+    from turboquant_kv.vllm_plugin import PagedKVPools
+    from turboquant_kv.config import TurboQuantConfig
+    Hkv, Hq, d, bs, nb = 2, 8, 64, 16, 16
+    pools = PagedKVPools(TurboQuantConfig(), 1, nb, bs, Hkv, d, DEV, layout="decode")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    n = 100
+    table = torch.randperm(nb, generator=g, device=DEV)[:8].to(torch.int32)
+    slots = (table.long()[torch.arange(n, device=DEV) // bs] * bs + torch.arange(n, device=DEV) % bs)
+    k = torch.randn(n, Hkv, d, generator=g, device=DEV)
+    v = torch.randn(n, Hkv, d, generator=g, device=DEV)
+    pools.write(0, k, v, slots)
+    q = torch.randn(n, Hq, d, generator=g, device=DEV)
+    whole = pools.prefill(0, q, table, n, 0.125)
+    pools.dl_max_streams = 64          # 32 rows per launch: four launches
+    chunked = pools.prefill(0, q, table, n, 0.125)
+    assert torch.equal(whole, chunked)
