@@ -302,6 +302,56 @@ def bench_quantize(args, extra):
             f"({tf / FP32_PEAK_TFLOPS:.0%} of fp32 peak)")
 
 
+def bench_formats(args, extra):
+    """On-disk formats (host byte work): Huffman streams of 10M 4-bit code indices
+    (HuffmanCoder encode / decode, native bit packing) and a TQIX v1 file of a 1M x 128
+    4-bit index written and read back through TurboQuantIndex."""
+    import os
+    import tempfile
+    import time
+
+    import torch
+    from turboquant_kv import EntropyPackedStorage, TurboQuantIndex
+
+    g = torch.Generator().manual_seed(0)
+    n = 10_000_000
+    # codes distributed as the Lloyd-Max cells of N(0, 1) (what a quantizer emits)
+    x = torch.randn(n, generator=g)
+    edges = torch.tensor([-2.401, -1.844, -1.437, -1.099, -0.7996, -0.5224, -0.2582, 0.0,
+                          0.2582, 0.5224, 0.7996, 1.099, 1.437, 1.844, 2.401])
+    codes = torch.bucketize(x, edges).to(torch.uint8).view(-1, 128)
+    t0 = time.perf_counter()
+    st = EntropyPackedStorage.from_codes(codes, 4, 128)
+    t1 = time.perf_counter()
+    back = st.to_codes()
+    t2 = time.perf_counter()
+    assert torch.equal(back, codes)
+    extra["huffman_4bit_10M"] = {"encode_Msym_per_s": n / (t1 - t0) / 1e6,
+                                 "decode_Msym_per_s": n / (t2 - t1) / 1e6,
+                                 "savings_pct": st.savings_pct, "threads": 1}
+    log(f"huffman 10M 4-bit codes: encode {n / (t1 - t0) / 1e6:.0f} M sym/s, decode "
+        f"{n / (t2 - t1) / 1e6:.0f} M sym/s, {st.savings_pct:.1f} % smaller")
+    N, d = 1_000_000, 128
+    idx = TurboQuantIndex(dim=d, bit_width=4, rotation="core", seed=7)
+    idx.add(torch.randn(N, d, generator=g).cuda())
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "bench.tqix")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        idx.save_tqix(path)
+        t1 = time.perf_counter()
+        idx2 = TurboQuantIndex.load_tqix(path)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        size = os.path.getsize(path)
+    assert idx2._norms.numel() == N
+    extra["tqix_1M_d128_b4"] = {"bytes": size, "write_GBps": size / (t1 - t0) / 1e9,
+                                "read_GBps": size / (t2 - t1) / 1e9,
+                                "note": "host file I/O + device transfer, tmpfs or disk of the box"}
+    log(f"TQIX 1M x 128 4-bit ({size / 1e6:.0f} MB): write {size / (t1 - t0) / 1e9:.2f} GB/s, "
+        f"read {size / (t2 - t1) / 1e9:.2f} GB/s")
+
+
 def bench_prod_scan(args, extra):
     """Prod-mode index search (TurboQuantIndex mode="prod", bit_width 4 = 3-bit MSE codes +
     1-bit QJL signs) over the headline's 10M x 128 shape: ip_scan_topk_prod scores the
@@ -437,6 +487,7 @@ def main():
     if not args.quick:
         bench_quantize(args, extra)
         bench_prod_scan(args, extra)
+        bench_formats(args, extra)
     cpu = None if args.no_cpu else cpu_baseline(scan["db4"])
     ms, bytes_alg = scan["headline"]
     achieved = bytes_alg / ms / 1e6
