@@ -87,7 +87,37 @@ int tq_huffman_decode(const uint8_t* data, size_t data_bytes, int64_t n_symbols,
     if (code_lens[c] > maxlen) maxlen = code_lens[c];
   }
   const uint8_t* body = data + 8;
+  const size_t body_bytes = data_bytes - 8;
   int64_t done = 0;
+  if (maxlen <= 20) {
+    // Window table: entry w of the 2^maxlen windows holds the shortest code word that
+    // prefixes w ((length << 16) | symbol; 0: none) -- the word the bit-by-bit walk below
+    // would match first.  A word longer than the bits left, or no word at all, ends the
+    // stream as the walk does.
+    std::vector<uint32_t> peek((size_t)1 << maxlen, 0u);
+    for (const auto& kv : table) {
+      const int l = (int)(kv.first >> 56);
+      const uint64_t word = kv.first & ((1ull << 56) - 1);
+      if (word >> l) continue;  // wider than its length: never matched
+      const uint32_t e = ((uint32_t)l << 16) | (uint32_t)(kv.second & 0xFFFF);
+      const size_t base = (size_t)word << (maxlen - l), span = (size_t)1 << (maxlen - l);
+      for (size_t i = base; i < base + span; ++i)
+        if (peek[i] == 0 || (int)(peek[i] >> 16) > l) peek[i] = e;
+    }
+    const uint32_t wmask = (1u << maxlen) - 1;
+    uint64_t p = 0;
+    while (done < n_symbols && p < nbits) {
+      const size_t at = (size_t)(p >> 3);
+      uint64_t v = 0;  // 32 bits from byte `at`, zeros past the body
+      for (int i = 0; i < 4; ++i) v = (v << 8) | (at + i < body_bytes ? body[at + i] : 0u);
+      const uint32_t e = peek[(uint32_t)(v >> (32 - (int)(p & 7) - maxlen)) & wmask];
+      if (e == 0 || p + (e >> 16) > nbits) break;
+      out[done++] = (uint8_t)(e & 0xFFFF);
+      p += e >> 16;
+    }
+    *n_out = done;
+    return TQ_OK;
+  }
   uint64_t cur = 0;
   int len = 0;
   for (uint64_t p = 0; p < nbits && done < n_symbols; ++p) {
