@@ -237,3 +237,27 @@ def test_paged_pool_layout_selection():
             PagedKVPools(cfg, 1, 4, bs, 2, d, device="cpu", layout="decode")
     with pytest.raises(ValueError, match="Unknown layout"):
         PagedKVPools(mse, 1, 4, 16, 2, 64, device="cpu", layout="tiles")
+
+
+def test_huffman_window_table_decoder_equals_bit_walk():
+    # Streams decoded through the window table (longest word <= 20 bits) and through the
+    # per-bit walk (forced by one extra 24-bit word that never occurs) give the same
+    # symbols, for a table with a prefix relation ("0" and "000") and a duplicate word
+    # (the later entry wins), and for truncated streams.
+    from turboquant_kv._lib import ops
+    words = torch.tensor([0b0, 0b10, 0b110, 0b111, 0b000, 0b10], dtype=torch.int64)
+    lens = torch.tensor([1, 2, 3, 3, 3, 2], dtype=torch.uint8)
+    syms = torch.tensor([0, 1, 2, 3, 4, 5], dtype=torch.int32)
+    long_w = torch.cat([words, torch.tensor([0xABCDEF], dtype=torch.int64)])
+    long_l = torch.cat([lens, torch.tensor([24], dtype=torch.uint8)])
+    long_s = torch.cat([syms, torch.tensor([6], dtype=torch.int32)])
+    rs = np.random.RandomState(4)
+    for nbytes in (0, 1, 2, 7, 64, 1000):
+        body = rs.randint(0, 256, nbytes).astype(np.uint8)
+        for nbits in (nbytes * 8, max(nbytes * 8 - 5, 0)):
+            hdr = np.array([1 << 20, nbits], np.uint32).view(np.uint8)
+            data = torch.from_numpy(np.concatenate([hdr, body]))
+            a = ops().huffman_decode(data, -1, words, lens, syms)
+            b = ops().huffman_decode(data, -1, long_w, long_l, long_s)
+            assert torch.equal(a, b), (nbytes, nbits)
+            assert not (a == 1).any() and not (a == 4).any()   # replaced / shadowed words
