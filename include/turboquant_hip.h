@@ -222,19 +222,26 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                                void* stream);
 
 /*
- * Decode layout: the codes of a 4-bit key / 2-bit value packed KV cache arranged for
- * the decode kernel, same bytes per token as the bit-plane rows.  The reference stores
- * its cache privately (cache.py:81-130), so this arrangement is internal to
- * QuantizedKVCache; these entry points convert it from and to the reference rows.
+ * Decode layout: the codes of a packed KV cache with 4-bit keys and 2-, 3- or 4-bit
+ * values arranged for the decode kernel, same bytes per token as the bit-plane rows.
+ * The reference stores its cache privately (cache.py:81-130), so this arrangement is
+ * internal to QuantizedKVCache; these entry points convert it from and to the reference
+ * rows.
  *   keys    [streams][t_cap][d/2]:   byte p = (code[2p] << 4) | code[2p+1]
- *   values  [streams][t_cap/64][1024] (d = 64): tile T holds tokens 64T..64T+63; its
- *           byte 16*(16*sl + c) + 4*m + dg = sum_t code[64T + 4*(4m + sl) + t][16dg + c]
- *           << 2t (sl, m, dg, t < 4; c < 16): lane 16*sl + c reads the 16 bytes its
- *           16x16x32 MFMAs need as one load (t_cap a multiple of 64)
+ *   values  [streams][t_cap/64][512*vb] (d = 64): tile T holds tokens 64T..64T+63.  Lane
+ *           L = 16*sl + c of a wave owns words 0-3 at tile byte 16*L and words 4.. at
+ *           1024 + (8*vb - 16)*L; token t of block 4m + sl (t, m, sl < 4), dim 16dg + c:
+ *     vb 2  word m, byte dg, bits 2t
+ *     vb 4  word 4*(m/2) + dg, byte 2*(m%2) + t/2, bits 4*(t%2)
+ *     vb 3  dg < 3: word 3*(m/2) + dg, the same byte, bits 3*(t%2); dg 3: the byte's
+ *           6-bit pair index (code[t even] | code[t odd] << 3) split two bits at a time
+ *           into bits 6-7 of that byte of words 3*(m/2) + 0, 1, 2
+ *           so each byte is one table index and a lane reads its operand bytes of a tile
+ *           with one or two loads (t_cap a multiple of 64)
  * tq_pack_decode_layout writes tokens [pos, pos+n) of every stream from bit-plane rows
  * packed [streams][n][bits*ceil(d/8)] (values: bits of the chunk's other tokens are
  * kept); tq_unpack_decode_layout returns tokens [t0, t0+n) as bit-plane rows.
- * values = 0 for keys (bit_width 4), 1 for values (bit_width 2).
+ * values = 0 for keys (bit_width 4), 1 for values (bit_width 2-4).
  */
 int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,
                           int32_t bit_width, int32_t values, uint8_t* cache, int64_t t_cap,
@@ -245,13 +252,15 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
 
 /*
  * tq_decode_attention_packed over a decode-layout cache (same semantics and output):
- * head_dim 64, 4-bit keys, 2-bit values, 1-4 query heads per KV head, t_cap a multiple
- * of 64.  kpairs [B, hkv, t_cap, 32], vblocks [B, hkv, t_cap/64, 1024], norms as above.
+ * head_dim 64, 4-bit keys, 2-4 bit values (vbits), any number of query heads per KV head
+ * (launched four at a time), t_cap a multiple of 64.  kpairs [B, hkv, t_cap, 32],
+ * vblocks [B, hkv, t_cap/64, 512*vbits], norms as above.
  * Scores are accurate to about 1e-6 relative (fp16 hi/lo products, fp32 accumulation);
  * fp32 queries get fp32-accurate outputs; fp16/bf16 queries use fp16 value products
  * (relative error about 5e-4, below the output type's own rounding tolerance).
  */
 size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t t_cap);
+/* kbits must be 4 and vbits 2, 3 or 4 (TQ_EUNSUPPORTED otherwise). */
 int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
                            int32_t d, const uint8_t* kpairs, const float* knorms,
                            const uint8_t* vblocks, const float* vnorms, int64_t t_cap,
@@ -312,8 +321,9 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
                               size_t workspace_bytes, void* stream);
 
 /*
- * Paged pools in the decode layout (4-bit keys, 2-bit values, head_dim 64): the same
- * kernel as tq_decode_attention_dl with block lookups per 64-token tile (one for block
+ * Paged pools in the decode layout (4-bit keys, 2-bit values, head_dim 64, any number of
+ * query heads per KV head): the same kernel as tq_decode_attention_dl with block lookups
+ * per 64-token tile (one for block
  * sizes >= 64, one per 16-token group below), for power-of-two block sizes >= 16.
  * Replaces, like tq_decode_attention_paged, the reference backend's forward
  * (turboquant_kv/vllm_plugin/__init__.py:209-304).

@@ -170,23 +170,24 @@ def k_scores_pairs(q, pairs, norms, cen, R):
     return out.cpu().numpy()
 
 
-def k_pack_dl(packed, t_cap, pos, values, cache=None):
+def k_pack_dl(packed, t_cap, pos, values, cache=None, vbits=2):
     """Bit-plane rows [S, n, P] -> decode-layout cache (created zeroed when None)."""
     S, n, _ = packed.shape
     d = 64
+    bits = vbits if values else 4
     if cache is None:
-        shape = (S, t_cap // 64, 16 * d) if values else (S, t_cap, d // 2)
+        shape = (S, t_cap // 64, 8 * vbits * d) if values else (S, t_cap, d // 2)
         cache = torch.zeros(shape, dtype=torch.uint8, device=DEV)
     capi.check(L().tq_pack_decode_layout(capi.p(T(packed)), capi.i64(S), capi.i64(n), capi.i32(d),
-                                         capi.i32(2 if values else 4), capi.i32(values), capi.p(cache),
+                                         capi.i32(bits), capi.i32(values), capi.p(cache),
                                          capi.i64(t_cap), capi.i64(pos), capi.stream()))
     sync()
     return cache
 
 
-def k_unpack_dl(cache, t_cap, t0, n, values):
+def k_unpack_dl(cache, t_cap, t0, n, values, vbits=2):
     S = cache.shape[0]
-    bits = 2 if values else 4
+    bits = vbits if values else 4
     out = torch.empty(S, n, bits * 8, dtype=torch.uint8, device=DEV)
     capi.check(L().tq_unpack_decode_layout(capi.p(cache), capi.i64(S), capi.i64(t_cap), capi.i64(t0),
                                            capi.i64(n), capi.i32(64), capi.i32(bits), capi.i32(values),
@@ -195,7 +196,7 @@ def k_unpack_dl(cache, t_cap, t0, n, values):
     return out.cpu().numpy()
 
 
-def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale):
+def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale, vbits=2):
     B, Hq, d = q_t.shape
     Hkv, Tc = kn.shape[1], kn.shape[2]
     out = torch.empty_like(q_t)
@@ -206,7 +207,7 @@ def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale):
     capi.check(L().tq_decode_attention_dl(
         capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache),
         capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)), capi.i64(Tc), capi.p(sl), capi.p(T(kc)),
-        capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(2), ctypes.c_float(scale),
+        capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(vbits), ctypes.c_float(scale),
         capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
     sync()
     return out.float().cpu().numpy(), lse.cpu().numpy()
@@ -693,6 +694,135 @@ def test_decode_layout_attention_vs_f64(G):
             # than bf16 arithmetic); fp32 / fp16 queries use hi + lo parts
             lse_tol = 2e-3 if dt == torch.bfloat16 else 1e-5
             assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= lse_tol
+
+
+def dl_value_tiles_np(codes, vb):
+    """Independent numpy packing of 3/4-bit value codes [S, t_cap, 64] into decode-layout
+    tiles [S, t_cap/64, 512*vb]: lane L = 16 sl + c owns words 0-3 at byte 16 L and the
+    rest at 1024 + (8 vb - 16) L; byte k = 2 (m % 2) + t // 2 of word w holds the pair
+    (tokens t = 2p, 2p + 1 of block 4m + sl, dim j): vb 4: w = 4 (m // 2) + j // 16, codes
+    at bits 0-3 / 4-7; vb 3: dims j < 48 at w = 3 (m // 2) + j // 16, bits 0-2 / 3-5, and
+    dims 48-63's 6-bit pair index spread two bits at a time over bits 6-7 of words
+    3 (m // 2) + 0, 1, 2."""
+    S, tc, d = codes.shape
+    nt = tc // 64
+    x = codes.reshape(S, nt, 4, 4, 4, d).astype(np.uint32)  # [S, tile, m, sl, t, j]
+    out = np.zeros((S, nt, 512 * vb), np.uint32)
+
+    def off(L, w, k):
+        return 16 * L + 4 * w + k if w < 4 else 1024 + (8 * vb - 16) * L + 4 * (w - 4) + k
+
+    for sl in range(4):
+        for c in range(16):
+            L = 16 * sl + c
+            for m in range(4):
+                G, mm = divmod(m, 2)
+                for pp in range(2):
+                    k = 2 * mm + pp
+                    e0, e1 = x[:, :, m, sl, 2 * pp], x[:, :, m, sl, 2 * pp + 1]  # [S, nt, j]
+                    if vb == 4:
+                        for dg in range(4):
+                            j = 16 * dg + c
+                            out[:, :, off(L, 4 * G + dg, k)] = e0[..., j] | (e1[..., j] << 4)
+                    else:
+                        i3 = e0[..., 48 + c] | (e1[..., 48 + c] << 3)
+                        for i in range(3):
+                            j = 16 * i + c
+                            out[:, :, off(L, 3 * G + i, k)] = (e0[..., j] | (e1[..., j] << 3) |
+                                                               (((i3 >> (2 * i)) & 3) << 6))
+    return out.astype(np.uint8)
+
+
+@pytest.mark.parametrize("vb", [3, 4])
+def test_decode_layout_value_tiles_pack_roundtrip(vb):
+    # Appends in uneven pieces that straddle pairs, blocks and tiles; the tile bytes must
+    # equal the independent numpy packing and unpack to the bit-plane input.
+    rs = np.random.RandomState(40 + vb)
+    S, t_cap, d = 3, 192, 64
+    codes = rs.randint(0, 1 << vb, (S, t_cap, d))
+    vp = np.stack([O.pack_codes(codes[s], vb) for s in range(S)])
+    vc = None
+    for pos, n in ((0, 1), (1, 2), (3, 6), (9, 30), (39, 25), (64, 65), (129, 63)):
+        vc = k_pack_dl(np.ascontiguousarray(vp[:, pos:pos + n]), t_cap, pos, 1, vc, vbits=vb)
+    assert np.array_equal(vc.cpu().numpy(), dl_value_tiles_np(codes, vb))
+    assert np.array_equal(k_unpack_dl(vc, t_cap, 0, t_cap, 1, vbits=vb), vp)
+    assert np.array_equal(k_unpack_dl(vc, t_cap, 5, 70, 1, vbits=vb), vp[:, 5:75])
+    # a planted transposition in the numpy packing (dims 48-63 swapped with 32-47) must
+    # not pass: the dim group 3 bits are where the 3-bit layout differs
+    if vb == 3:
+        bad = codes.copy()
+        bad[:, :, 32:48], bad[:, :, 48:64] = codes[:, :, 48:64], codes[:, :, 32:48]
+        assert not np.array_equal(vc.cpu().numpy(), dl_value_tiles_np(bad, vb))
+
+
+@pytest.mark.parametrize("vb,G", [(3, 1), (3, 4), (4, 4), (3, 8), (2, 7), (2, 8), (4, 5)])
+def test_decode_layout_vbits_and_groups_vs_f64(vb, G):
+    # 3- and 4-bit value tiles and more than four query heads per KV head (launched four
+    # heads at a time); ragged lengths, fp32 / bf16 / fp16 queries.
+    rs = np.random.RandomState(500 + 10 * vb + G)
+    d, Hkv, Tc = 64, 2, 2112
+    seq = [0, 1, 63, 64, 65, 513, 2100]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    n = B * Hkv * Tc
+    K = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    V = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, Tc, -1), Tc, 0, 0)
+    vc = k_pack_dl(vp.reshape(B * Hkv, Tc, -1), Tc, 0, 1, vbits=vb)
+    kp, vp = kp.reshape(B, Hkv, Tc, -1), vp.reshape(B, Hkv, Tc, -1)
+    kn, vn = kn.reshape(B, Hkv, Tc), vn.reshape(B, Hkv, Tc)
+    q = (rs.randn(B, Hq, d) * 3.0).astype(np.float32)
+    for dt, tol in ((torch.float32, 1e-4), (torch.bfloat16, 1e-2), (torch.float16, 3e-3)):
+        qt = torch.from_numpy(q).to(DEV).to(dt)
+        qf = qt.float().cpu().numpy()
+        want, want_lse = O.decode_attention_f64(qf, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, 4, vb,
+                                                0.125, return_lse=True)
+        got, lse = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+        assert np.all(got[0] == 0) and np.isneginf(lse[0]).all()
+        for bi in range(1, B):
+            err = np.max(np.abs(got[bi] - want[bi])) / np.max(np.abs(want[bi]))
+            assert err <= tol, (dt, seq[bi], err)
+        ok = np.isfinite(want_lse)
+        lse_tol = 2e-3 if dt == torch.bfloat16 else 1e-5
+        assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= lse_tol
+
+
+@pytest.mark.parametrize("vb,T", [(2, 2048), (3, 1024)])
+def test_decode_layout_config_shape_vs_f64(vb, T):
+    # The benchmarked launch: B = 32, Hq = 32, Hkv = 8 (256 streams, one split per stream,
+    # so the kernel applies R_v and writes the output itself), bf16 K/V with four outlier
+    # channels per KV head scaled x20, bf16 queries, scale 1/8.
+    rs = np.random.RandomState(7 + vb)
+    B, Hq, Hkv, d = 32, 32, 8, 64
+    assert L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, T) >= 256
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    K = rs.randn(B, Hkv, T, d).astype(np.float32)
+    V = rs.randn(B, Hkv, T, d).astype(np.float32)
+    for h in range(Hkv):
+        ch = rs.choice(d, 4, replace=False)
+        K[:, h, :, ch] *= 20.0
+        V[:, h, :, ch] *= 20.0
+    K = torch.from_numpy(K).to(torch.bfloat16).float().numpy().reshape(-1, d)
+    V = torch.from_numpy(V).to(torch.bfloat16).float().numpy().reshape(-1, d)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, T, -1), T, 0, 0)
+    vc = k_pack_dl(vp.reshape(B * Hkv, T, -1), T, 0, 1, vbits=vb)
+    kp, vp = kp.reshape(B, Hkv, T, -1), vp.reshape(B, Hkv, T, -1)
+    kn, vn = kn.reshape(B, Hkv, T), vn.reshape(B, Hkv, T)
+    qt = torch.from_numpy(rs.randn(B, Hq, d).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    seq = [T] * B
+    want = O.decode_attention_f64(qt.float().cpu().numpy(), kp, kn, vp, vn, seq, ck, cv, Rk, Rv,
+                                  4, vb, 0.125)
+    got, _ = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+    err = np.max(np.abs(got - want), axis=-1) / np.max(np.abs(want), axis=-1)
+    assert err.max() <= 1e-2, err.max()
 
 
 def test_scan_many_exact_ties_take_fallback():

@@ -209,6 +209,8 @@ def _bitplane_pools(pools, tab, lens):
 
 @pytest.mark.parametrize("mode,kb,vb,d,G,layout", [("mse", 4, 2, 64, 4, "bitplane"),
                                                    ("mse", 4, 2, 64, 4, "auto"),
+                                                   ("mse", 4, 2, 64, 8, "auto"),
+                                                   ("mse", 4, 2, 64, 7, "auto"),
                                                    ("mse", 3, 2, 128, 2, "auto"),
                                                    ("prod", 4, 3, 64, 2, "auto")])
 def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G, layout):
@@ -361,7 +363,8 @@ def test_paged_dl_store_round_trip(bs):
 
 @pytest.mark.parametrize("bs,G,qdt", [(64, 4, torch.bfloat16), (128, 2, torch.float16),
                                       (64, 1, torch.float32), (16, 4, torch.bfloat16),
-                                      (32, 2, torch.float16), (16, 1, torch.float32)])
+                                      (32, 2, torch.float16), (16, 1, torch.float32),
+                                      (16, 8, torch.bfloat16), (64, 6, torch.float32)])
 def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     from turboquant_kv import ops
     rs = np.random.RandomState(bs + G)
@@ -483,4 +486,34 @@ def test_decode_layout_prefill_in_chunks_equals_one_launch():
     whole = pools.prefill(0, q, table, n, 0.125)
     pools.dl_max_streams = 64          # 32 rows per launch: four launches
     chunked = pools.prefill(0, q, table, n, 0.125)
+    # at T = 100 both split plans have one split per stream: identical sums
     assert torch.equal(whole, chunked)
+
+
+def test_decode_layout_prefill_chunks_with_several_splits_vs_f64():
+    # A longer prefill in launches of 32 rows: each launch's 64 streams are split over
+    # several workgroups (and merged by the combine kernel) while the single launch keeps
+    # one split per stream, so the sums differ in order; both must match the float64
+    # paged oracle.
+    from turboquant_kv.vllm_plugin import PagedKVPools
+    from turboquant_kv.config import TurboQuantConfig
+    Hkv, Hq, d, bs, nb, n = 2, 8, 64, 16, 80, 1200
+    pools = PagedKVPools(TurboQuantConfig(), 1, nb, bs, Hkv, d, DEV, layout="decode")
+    g = torch.Generator(device=DEV).manual_seed(6)
+    table = torch.randperm(nb, generator=g, device=DEV)[:(n + bs - 1) // bs].to(torch.int32)
+    slots = (table.long()[torch.arange(n, device=DEV) // bs] * bs + torch.arange(n, device=DEV) % bs)
+    k = torch.randn(n, Hkv, d, generator=g, device=DEV)
+    v = torch.randn(n, Hkv, d, generator=g, device=DEV)
+    pools.write(0, k, v, slots)
+    q = torch.randn(n, Hq, d, generator=g, device=DEV)
+    whole = pools.prefill(0, q, table, n, 0.125).cpu().numpy()
+    pools.dl_max_streams = 64
+    chunked = pools.prefill(0, q, table, n, 0.125).cpu().numpy()
+    P = _bitplane_pools(pools, table.cpu().numpy()[None], [n])
+    want = O.paged_attention_f64(q.cpu().numpy(), P["k"], P["kn"], P["v"], P["vn"],
+                                 table.cpu().numpy(), n, pools.kcen.cpu().numpy(),
+                                 pools.vcen.cpu().numpy(), pools.R_k.cpu().numpy(),
+                                 pools.R_v.cpu().numpy(), 4, 2, 0.125)
+    for got in (whole, chunked):
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+    assert not np.array_equal(whole, chunked)  # the plans really differ

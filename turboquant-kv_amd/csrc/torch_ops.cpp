@@ -610,6 +610,9 @@ at::Tensor huffman_decode(const at::Tensor& data, int64_t n_symbols, const at::T
     const uint8_t* p = d.data_ptr<uint8_t>();
     n = (int64_t)((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
   }
+  // Every code word is at least one bit long, so the body holds at most 8 symbols per
+  // byte: a corrupt or truncated header cannot make the output larger than that.
+  n = std::min<int64_t>(n, 8 * (d.numel() - 8));
   auto out = at::empty({n}, at::TensorOptions().dtype(at::kByte));
   int64_t got = 0;
   check_rc(tq_huffman_decode(d.data_ptr<uint8_t>(), d.numel(), n,
@@ -753,7 +756,7 @@ void pack_decode_layout(const at::Tensor& packed, at::Tensor& cache, int64_t dim
   TORCH_CHECK(pk.dim() == 3 && pk.size(0) == cache.size(0), "packed must be [streams, n, P]");
   TORCH_CHECK(pk.size(2) == packed_width(bit_width, dim), "packed width mismatch");
   const int64_t t_cap = values ? cache.size(1) * 64 : cache.size(1);
-  TORCH_CHECK(cache.size(2) == (values ? 16 * dim : dim / 2), "cache width mismatch");
+  TORCH_CHECK(cache.size(2) == (values ? 8 * bit_width * dim : dim / 2), "cache width mismatch");
   check_rc(tq_pack_decode_layout(pk.data_ptr<uint8_t>(), pk.size(0), pk.size(1), (int32_t)dim,
                                  (int32_t)bit_width, (int32_t)values, cache.data_ptr<uint8_t>(),
                                  t_cap, pos, cur_stream(cache)));
@@ -781,7 +784,7 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   require_gpu(q, "q");
   TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
   TORCH_CHECK(kpairs.dim() == 4 && vblocks.dim() == 4,
-              "kpairs must be [B, Hkv, T, d/2] and vblocks [B, Hkv, T/64, 16d]");
+              "kpairs must be [B, Hkv, T, d/2] and vblocks [B, Hkv, T/64, 8 * vbits * d]");
   c10::DeviceGuard g(q.device());
   const auto dev = q.device();
   auto qq = floatc(q, dev);
@@ -795,8 +798,11 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   TORCH_CHECK(kpairs.device() == dev && vblocks.device() == dev && knorms.device() == dev &&
                   vnorms.device() == dev,
               "K/V must be on the query's device");
+  // value tiles of 8 * vbits * d bytes per 64 tokens: the width names the value code width
+  const int64_t vbits = d > 0 ? vblocks.size(3) / (8 * d) : 0;
   TORCH_CHECK(kpairs.size(0) == B && kpairs.size(3) == d / 2 && vblocks.size(0) == B &&
-                  vblocks.size(1) == Hkv && vblocks.size(2) * 64 == Tc && vblocks.size(3) == 16 * d,
+                  vblocks.size(1) == Hkv && vblocks.size(2) * 64 == Tc &&
+                  vblocks.size(3) == 8 * vbits * d && vbits >= 2 && vbits <= 4,
               "decode-layout K/V shape mismatch");
   TORCH_CHECK(knorms.scalar_type() == at::kFloat && vnorms.scalar_type() == at::kFloat &&
                   knorms.numel() == B * Hkv * Tc && vnorms.numel() == B * Hkv * Tc,
@@ -807,6 +813,8 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   auto vc = f32c(vcentroids, dev);
   auto Rk = f32c(krotation, dev);
   auto Rv = f32c(vrotation, dev);
+  TORCH_CHECK(kc.numel() == 16 && vc.numel() == (1 << vbits),
+              "decode layout: 16 key centroids and 2^vbits value centroids");
   auto out = at::empty({B, Hq, d}, qq.options());
   auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
   if (B == 0) return {out, lse};
@@ -815,8 +823,9 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
       kpairs.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vblocks.data_ptr<uint8_t>(),
       vnorms.data_ptr<float>(), Tc, sl.data_ptr<int32_t>(), kc.data_ptr<float>(),
-      vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), 4, 2, (float)scale,
-      out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(), ws.numel(), cur_stream(qq)));
+      vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), 4, (int32_t)vbits,
+      (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+      cur_stream(qq)));
   return {out, lse};
 }
 

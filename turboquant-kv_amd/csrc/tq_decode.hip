@@ -432,10 +432,20 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
 
 // ------------------------------------------------------------------ decode layout
 // The decode layout holds the same codes as the bit-plane rows, arranged for the
-// decode kernel (4-bit keys, 2-bit values):
+// decode kernel (4-bit keys; 2-, 3- or 4-bit values; head_dim 64):
 //   keys    per token d/2 bytes; byte p = (code[2p] << 4) | code[2p+1]
-//   values  per block of 4 consecutive tokens d bytes; byte j = sum_t code[t][j] << 2t
-// Every byte is then one table index: a single v_perm builds its LDS address.
+//   values  64-token tiles of 512 * VB bytes.  Lane L = 16 sl + c of a wave reads the
+//           words its p.V operands need: words 0-3 at byte 16 L, words 4.. at byte
+//           1024 + (8 VB - 16) L.  Token tt of the tile is token t = tt % 4 of block
+//           4 m + sl = tt / 4; dim j = 16 dg + c.
+//     VB 2  word m, byte dg: the four tokens' codes at bits 2t (one lookup of four values)
+//     VB 4  word 4 (m / 2) + dg, byte 2 (m % 2) + t / 2: two tokens' codes, token t at
+//           bits 4 (t % 2) (one lookup of a pair)
+//     VB 3  dims of dg 0-2: word 3 (m / 2) + dg, the same byte, token t at bits 3 (t % 2);
+//           dg 3: the 6-bit pair index of that byte position is spread over the top two
+//           bits (6, 7) of the same byte of words 3 (m / 2) + 0, 1, 2 (bits 0-1, 2-3, 4-5)
+// Every byte is then one table index: a single v_perm builds its LDS address (the 3-bit
+// table repeats each pair under the four values of the top two bits).
 constexpr int kDlThreads = 512;  // 8 waves (12 measured slower)
 constexpr int kDlWaves = kDlThreads / 64;
 constexpr int kDlEntry = 256;                  // bytes per table index (all copies)
@@ -459,11 +469,14 @@ struct DlArgs {
   int64_t t_cap;
   const int32_t* seq_lens;
   const float* kcen;  // 16
-  const float* vcen;  // 4
+  const float* vcen;  // 2^VB
   const float* krot;
   float qscale;  // softmax scale * log2(e)
   int64_t split_tokens;
   int nsplit;
+  // Query heads of a KV head handled by this launch: heads hofs .. hofs + G - 1 of the
+  // Gfull heads that share it (more than four take several launches).
+  int Gfull, hofs;
   float* part;
   float2* stats;
   // one split per stream: the kernel writes the output itself
@@ -545,17 +558,22 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // PG: 0 contiguous caches; 1 paged pools of block_size >= 64 (64-token value tiles);
 // 2 paged pools of block_size 16 or 32 (16-token value sub-blocks of 256 B: lane
 // 16 sl + c's word holds what word m of its 64-token tile row holds for sub-block m).
-template <bool EXACT_V, bool PREC_K, int PG = 0>
+// VB: value code width (2, 3 or 4; sub-blocks hold 2-bit values only).
+template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   constexpr bool PAGED = PG != 0, SUB16 = PG == 2;
+  static_assert(VB >= 2 && VB <= 4 && (!SUB16 || VB == 2), "value width");
+  constexpr int VW = VB == 2 ? 4 : 2 * VB;  // value words per lane and tile
+  constexpr uint32_t VTILE = 512u * VB;     // bytes per 64-token value tile
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
-  // copies of 4 hi + 4 lo halves.  K table at 64 KB: index = pair byte; 32 copies of the
+  // copies of 4 hi + 4 lo halves (VB 3, 4: a pair byte's two fp16 centroids, 32 copies
+  // in the first 128 bytes of the entry, the lo halves in the second).  K table at 64 KB: index = pair byte; 32 copies of the
   // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
   // at kDlKLo).  After the tile loop the bytes hold the reduction.
   __shared__ __attribute__((aligned(16))) char tabs[kDlTabs];
   __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4][2][kDim];  // q * qs2: hi, lo
   __shared__ float qs_s[4][kDim];
-  __shared__ float cen_s[20];
+  __shared__ float cen_s[32];  // 16 key centroids, then the value centroids
   __shared__ float sc_s[2];  // value and key centroid scales
   __shared__ float qs2_s[4];  // per-head query scales
   __shared__ float red_m[kDlWaves][4];
@@ -563,26 +581,24 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   char* const ktab = tabs + kDlTab;
   char* const vtab = tabs;
 
-  int split = blockIdx.x, bg = blockIdx.y;
+  // One-dimensional grid: workgroup L = split + nsplit * stream.
+  uint32_t W = blockIdx.x;
   if constexpr (PAGED) {
     // XCD-aware order: workgroups go to the 8 XCDs round-robin in linear order, so linear
     // id L runs on XCD L % 8.  Work item W = (L % 8) * (N / 8) + L / 8 puts consecutive
     // (sequence, kv head) streams on one XCD, where the norm lines that adjacent heads of
     // a block share are fetched into that XCD's L2 once.
-    const uint32_t N = gridDim.x * gridDim.y;
-    if ((N & 7u) == 0) {
-      const uint32_t L = blockIdx.x + blockIdx.y * gridDim.x;
-      const uint32_t W = (L & 7u) * (N >> 3) + (L >> 3);
-      split = (int)(W % gridDim.x);
-      bg = (int)(W / gridDim.x);
-    }
+    const uint32_t N = gridDim.x;
+    if ((N & 7u) == 0) W = (W & 7u) * (N >> 3) + (W >> 3);
   }
+  const int split = (int)(W % (uint32_t)a.nsplit);
+  const int bg = (int)(W / (uint32_t)a.nsplit);
   const int b = bg / a.hkv;
   const int g = bg - b * a.hkv;
   const int64_t T = min((int64_t)max(a.seq_lens[b], 0), a.t_cap);
   const int64_t t_begin = (int64_t)split * a.split_tokens;
   const int64_t t_end = min(T, t_begin + a.split_tokens);
-  const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.G;
+  const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.Gfull + a.hofs;
   const int tid = threadIdx.x;
   if (t_begin >= t_end) {  // uniform
     if (a.out != nullptr && T == 0 && tid < a.G * kDim) {  // empty sequence: zeros, lse -inf
@@ -604,7 +620,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const uint32_t nrows = PAGED ? a.pool_rows : (uint32_t)t_end;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, nrows * 32);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * 16, PAGED ? nrows * 16 : (uint32_t)((t_end + 63) >> 6) * 1024);
+      make_rsrc(a.vblocks + sbase * (8 * VB),
+                PAGED ? nrows * (8 * VB) : (uint32_t)((t_end + 63) >> 6) * VTILE);
   // Norms are read four tokens at a time: the range covers whole quads (inside the
   // allocation, t_cap % 4 == 0); entries past t_end are masked.
   const uint32_t nbytes = PAGED ? nrows * 4 : (uint32_t)((t_end + 3) >> 2) * 16;
@@ -619,7 +636,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 
   struct Tile {
     u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
-    uint32_t v[4];   // value tile column lane: word m = 4 dim-group bytes of block 4m + sl
+    uint32_t v[VW];  // the lane's value tile words (layout above)
     float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
   };
   // Paged: block id of the tile at t0 (one per tile, the same in every lane; SUB16: one
@@ -666,8 +683,15 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       for (int m = 0; m < 4; ++m)
         x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)((rg[m] >> 4) * 256 + lane * 4), 0, 0);
     } else {
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * 1024 + lane * 16), 0, 0);
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + lane * 16), 0, 0);
       x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+      if constexpr (VB == 3) {
+        const u32x2 v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, (int)(vt * VTILE + 1024 + lane * 8), 0, 0);
+        x.v[4] = v1.x; x.v[5] = v1.y;
+      } else if constexpr (VB == 4) {
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + 1024 + lane * 16), 0, 0);
+        x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
+      }
     }
     // norms of the lane's four tokens (group gq): 16-byte aligned (t_cap % 64 == 0,
     // aligned base)
@@ -695,7 +719,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // the epilogue: staged in LDS it took the workgroup to 151 KB, measured 5 % slower.)
   float cenv = 0.f;
   if (tid < 16) cenv = a.kcen[tid];
-  else if (tid < 20) cenv = a.vcen[tid - 16];
+  else if (tid < 16 + (1 << VB)) cenv = a.vcen[tid - 16];
   // the query element as the aligned 32-bit word that holds it (one load whatever the
   // dtype, converted after the barrier: a dtype branch here made the compiler wait for it
   // before issuing the loads below)
@@ -715,7 +739,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   load_tile(tf, ta, load_block(tf));
   load_tile(tf + kStep, tb, load_block(tf + kStep));
   bnx = load_block(tf + 2 * kStep);
-  if (tid < 20) cen_s[tid] = cenv;
+  if (tid < 32) cen_s[tid] = cenv;
   if (tid < 4 * kDim) {
     const uint32_t bits = a.q_dt == TQ_F32 ? qraw : (qraw >> (8 * (qbyte & 2))) & 0xFFFFu;
     const float qv = a.q_dt == TQ_F32 ? __uint_as_float(bits)
@@ -746,7 +770,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if (j == 0) qs2_s[h] = s2;
   } else if (tid < 4 * kDim + 64) {  // wave 4: value centroid scale
     const int l = tid & 63;
-    const float vm = wave_max(l < 4 ? fabsf(cen_s[16 + l]) : 0.f);
+    const float vm = wave_max(l < (1 << VB) ? fabsf(cen_s[16 + l]) : 0.f);
     if (l == 0) sc_s[0] = pow2_scale(vm);
   } else if (tid < 4 * kDim + 128) {  // wave 5: key centroid scale
     const int l = tid & 63;
@@ -770,18 +794,35 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + kDlKLo + q * 16) = (u32x4){wl, wl, wl, wl};
     }
   }
-  for (int e = tid; e < 256 * 16; e += kDlThreads) {
-    const int i = e >> 4, q = e & 15;
-    v4h vh, vl;
+  if constexpr (VB == 2) {
+    for (int e = tid; e < 256 * 16; e += kDlThreads) {
+      const int i = e >> 4, q = e & 15;
+      v4h vh, vl;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float x = cen_s[16 + ((i >> (2 * t)) & 3)] * vsc;
-      vh[t] = (_Float16)x;
-      vl[t] = (_Float16)(x - (float)vh[t]);
+      for (int t = 0; t < 4; ++t) {
+        const float x = cen_s[16 + ((i >> (2 * t)) & 3)] * vsc;
+        vh[t] = (_Float16)x;
+        vl[t] = (_Float16)(x - (float)vh[t]);
+      }
+      const u32x2 h = __builtin_bit_cast(u32x2, vh), lo = __builtin_bit_cast(u32x2, vl);
+      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) =
+          EXACT_V ? (u32x4){h.x, h.y, lo.x, lo.y} : (u32x4){h.x, h.y, h.x, h.y};
     }
-    const u32x2 h = __builtin_bit_cast(u32x2, vh), lo = __builtin_bit_cast(u32x2, vl);
-    *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) =
-        EXACT_V ? (u32x4){h.x, h.y, lo.x, lo.y} : (u32x4){h.x, h.y, h.x, h.y};
+  } else {
+    // pair entries: (c[low code], c[high code]) * vsc as two fp16, copies 4q .. 4q + 3;
+    // lo halves 128 bytes further
+    constexpr int mask = (1 << VB) - 1;
+    for (int e = tid; e < 256 * 8; e += kDlThreads) {
+      const int i = e >> 3, q = e & 7;
+      const float x0 = cen_s[16 + (i & mask)] * vsc, x1 = cen_s[16 + ((i >> VB) & mask)] * vsc;
+      const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+      const uint32_t wh = pack_h2(h0, h1);
+      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) = (u32x4){wh, wh, wh, wh};
+      if constexpr (EXACT_V) {
+        const uint32_t wl = pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
+        *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + 128 + q * 16) = (u32x4){wl, wl, wl, wl};
+      }
+    }
   }
   __syncthreads();
 
@@ -814,8 +855,21 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const float kinv = 1.f / (ksc * qs2_s[hh]);  // a power of two: exact
   // byte 0: copy offset; byte 2 of kcopy: the K table's 64 KB base
   const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
-  const uint32_t vcopy =
-      EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
+  const uint32_t vcopy = VB != 2 ? (uint32_t)(lane & 31) * 4
+                          : EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
+  // VB 3, 4: the word whose four bytes index the pair entries of half G, dim group dg
+  auto vword = [&](const Tile& x, int G, int dg) -> uint32_t {
+    if constexpr (VB == 4) {
+      return x.v[4 * G + dg];
+    } else {
+      if (dg < 3) return x.v[3 * G + dg];
+      const uint32_t x0 = x.v[3 * G], x1 = x.v[3 * G + 1], x2 = x.v[3 * G + 2];
+      return ((x0 >> 6) & 0x03030303u) | ((x1 >> 4) & 0x0C0C0C0Cu) | ((x2 >> 2) & 0x30303030u);
+    }
+  };
+  auto vpair = [&](uint32_t w, int byte) -> uint32_t {
+    return *reinterpret_cast<const uint32_t*>(tabs + byte_addr(vcopy, w, byte));
+  };
 
   float M = -INFINITY, l = 0.f;
   v4f acc[4];  // dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 16 dg + lane
@@ -887,12 +941,18 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     // The value-centroid lookups depend only on the tile's bytes: issued here, their LDS
     // latency runs under the softmax arithmetic.  (p.V below describes the operands.)
     v8h bv[8];
-    if constexpr (!EXACT_V) {
+    if constexpr (!EXACT_V && VB == 2) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
         const int G = i >> 2, dg = i & 3;
         bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg)),
                       *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg)));
+      }
+    } else if constexpr (!EXACT_V) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; bytes: blocks 8G + sl, 8G + 4 + sl
+        const uint32_t w = vword(cur, i >> 2, i & 3);
+        bv[i] = as_v8h(vpair(w, 0), vpair(w, 1), vpair(w, 2), vpair(w, 3));
       }
     }
 
@@ -969,10 +1029,23 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         v8h bh[4], bl[4];
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
-          const u32x4 e0 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg));
-          const u32x4 e1 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg));
-          bh[dg] = as_v8h(e0.x, e0.y, e1.x, e1.y);
-          bl[dg] = as_v8h(e0.z, e0.w, e1.z, e1.w);
+          if constexpr (VB == 2) {
+            const u32x4 e0 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg));
+            const u32x4 e1 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg));
+            bh[dg] = as_v8h(e0.x, e0.y, e1.x, e1.y);
+            bl[dg] = as_v8h(e0.z, e0.w, e1.z, e1.w);
+          } else {
+            const uint32_t w = vword(cur, G, dg);
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const char* e = tabs + byte_addr(vcopy, w, k);
+              hi[k] = *reinterpret_cast<const uint32_t*>(e);
+              lo[k] = *reinterpret_cast<const uint32_t*>(e + 128);
+            }
+            bh[dg] = as_v8h(hi[0], hi[1], hi[2], hi[3]);
+            bl[dg] = as_v8h(lo[0], lo[1], lo[2], lo[3]);
+          }
         }
         if (G == 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1064,6 +1137,41 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   }
 }
 
+// Byte offset, inside a 64-token value tile of width VB 3 or 4, of byte k of lane L's
+// value word w (words 0-3 at 16 L, the rest at 1024 + (8 VB - 16) L).
+__device__ __forceinline__ int vt_byte_off(int VB, int L, int w, int k) {
+  return w < 4 ? 16 * L + 4 * w + k : 1024 + (8 * VB - 16) * L + 4 * (w - 4) + k;
+}
+
+// Bit b of a VB 3 / 4 tile byte (lane L, word w, byte k) holds bit `cbit` of the code of
+// tile token `tt`, dim `j`.
+__device__ __forceinline__ void vt_bit_source(int VB, int L, int w, int k, int b, int& tt, int& j,
+                                              int& cbit) {
+  const int sl = L >> 4, c = L & 15;
+  int G, e;
+  if (VB == 4) {
+    G = w >> 2;
+    j = 16 * (w & 3) + c;
+    e = b >> 2;
+    cbit = b & 3;
+  } else {
+    G = w / 3;
+    const int i = w - 3 * G;
+    if (b < 6) {
+      j = 16 * i + c;
+      e = b / 3;
+      cbit = b - 3 * e;
+    } else {  // bits 2i, 2i + 1 of dim group 3's pair index
+      const int q = 2 * i + (b - 6);
+      j = 48 + c;
+      e = q / 3;
+      cbit = q - 3 * e;
+    }
+  }
+  const int m = 2 * G + (k >> 1);
+  tt = 4 * (4 * m + sl) + 2 * (k & 1) + e;
+}
+
 // Bit-plane rows -> decode layout.  keys: one thread per output byte.  values: one
 // thread per byte of the 64-token tiles that tokens [pos, pos + n) touch; bits of
 // tokens outside that range are kept.
@@ -1088,7 +1196,7 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
       cache[(s * t_cap + pos + t) * half + pidx] =
           (uint8_t)((code(s, t, 2 * pidx) << 4) | code(s, t, 2 * pidx + 1));
     }
-  } else {
+  } else if (bits == 2) {
     // value tiles of 64 tokens (d = 64): byte 16 L + 4 m + dg of tile T, L = 16 sl + c,
     // holds dim 16 dg + c of tokens 64 T + 4 (4 m + sl) + t, 2 bits each (t = 0..3)
     const int64_t c0 = pos >> 6, c1 = (pos + n + 63) >> 6;
@@ -1107,6 +1215,36 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
         const int64_t t = tile * 64 + 4 * (4 * m + sl) + tt - pos;
         if (t < 0 || t >= n) continue;
         v = (v & ~(3u << (2 * tt))) | (code(s, t, j) << (2 * tt));
+      }
+      *dst = (uint8_t)v;
+    }
+  } else {
+    // 3- and 4-bit value tiles of 512 * bits bytes: each byte's bits gathered one by one
+    const int tb = 512 * bits, nb = 8 * bits - 16;
+    const int64_t c0 = pos >> 6, c1 = (pos + n + 63) >> 6;
+    const int64_t nt = c1 - c0;
+    const int64_t total = n_streams * nt * tb;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+      const int off = (int)(e % tb);
+      const int64_t r = e / tb, s = r / nt, tile = c0 + (r - s * nt);
+      int L, w, k;
+      if (off < 1024) {
+        L = off >> 4; w = (off >> 2) & 3; k = off & 3;
+      } else {
+        const int o = off - 1024;
+        L = o / nb;
+        const int rr = o - L * nb;
+        w = 4 + (rr >> 2); k = rr & 3;
+      }
+      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * tb + off;
+      uint32_t v = *dst;
+      for (int b = 0; b < 8; ++b) {
+        int tt, j, cbit;
+        vt_bit_source(bits, L, w, k, b, tt, j, cbit);
+        const int64_t t = tile * 64 + tt - pos;
+        if (t < 0 || t >= n) continue;
+        v = (v & ~(1u << b)) | (((code(s, t, j) >> cbit) & 1u) << b);
       }
       *dst = (uint8_t)v;
     }
@@ -1133,11 +1271,26 @@ __global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_st
       if (!values) {
         const uint8_t pb = cache[(s * t_cap + t) * (d / 2) + (j >> 1)];
         c = (j & 1) ? (pb & 15u) : (pb >> 4);
-      } else {
+      } else if (bits == 2) {
         const int blk = (int)((t >> 2) & 15);  // block within the 64-token tile = 4 m + sl
         const int64_t at = (s * (t_cap >> 6) + (t >> 6)) * 1024 + ((blk & 3) * 16 + (j & 15)) * 16 +
                            (blk >> 2) * 4 + (j >> 4);
         c = (cache[at] >> (2 * (t & 3))) & 3u;
+      } else {
+        const int tt = (int)(t & 63), blk = tt >> 2, m = blk >> 2, sl = blk & 3;
+        const int G = m >> 1, kb = 2 * (m & 1) + ((tt >> 1) & 1), eo = tt & 1;
+        const int L = 16 * sl + (j & 15), dg = j >> 4;
+        const uint8_t* tile = cache + (s * (t_cap >> 6) + (t >> 6)) * (512 * bits);
+        if (bits == 4) {
+          c = (tile[vt_byte_off(4, L, 4 * G + dg, kb)] >> (4 * eo)) & 15u;
+        } else if (dg < 3) {
+          c = (tile[vt_byte_off(3, L, 3 * G + dg, kb)] >> (3 * eo)) & 7u;
+        } else {
+          uint32_t idx = 0;
+          for (int i = 0; i < 3; ++i)
+            idx |= (uint32_t)((tile[vt_byte_off(3, L, 3 * G + i, kb)] >> 6) & 3) << (2 * i);
+          c = (idx >> (3 * eo)) & 7u;
+        }
       }
       out |= ((c >> p) & 1u) << (7 - k);
     }
@@ -1159,14 +1312,6 @@ SplitPlan plan_splits(int B, int hkv, int64_t t_max) {
   return {split, (int)((t_max + split - 1) / split)};
 }
 
-bool fused_enabled() {
-  static const bool on = [] {
-    const char* e = std::getenv("TQ_DECODE_FUSED");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
-
 template <int KB, bool PAGED = false>
 int launch_kb(int vb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
   if (vb == 1) hipLaunchKernelGGL((fused_decode_kernel<KB, 1, PAGED>), grid, dim3(kDecThreads), 0, st, a);
@@ -1178,7 +1323,6 @@ int launch_kb(int vb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
 }  // namespace
 
 bool fused_decode_covers(const FusedDecodeCall& c) {
-  if (!fused_enabled()) return false;
   if (c.d != kDim || c.kbits < 1 || c.kbits > 4 || c.vbits < 1 || c.vbits > 2) return false;
   if (c.hkv < 1 || c.hq % c.hkv != 0 || c.hq / c.hkv > 4) return false;
   if (c.q_dt != TQ_F16 && c.q_dt != TQ_BF16) return false;
@@ -1308,6 +1452,56 @@ SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
   return {split, (int)((t_cap + split - 1) / split)};
 }
 
+template <int PG, int VB>
+void launch_dl_kernel(tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
+  if (q_dtype == TQ_F32)
+    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+  else if (q_dtype == TQ_F16)
+    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+}
+
+// The decode-layout kernel over every (stream, split), in launches of at most four query
+// heads per KV head, then (several splits) the log-sum-exp combine.  `a` carries
+// everything but the split plan, the head range and the outputs.
+int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg,
+           const SplitPlan& p, void* workspace, void* out, float* lse, hipStream_t st) {
+  const size_t rows = (size_t)B * hq;
+  char* ws = static_cast<char*>(workspace) + 256;
+  float* part = reinterpret_cast<float*>(ws);
+  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
+  const bool single = p.nsplit == 1;
+  if (a.t_cap > 0) {
+    a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv;
+    a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
+    a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
+    a.Gfull = hq / hkv;
+    const uint64_t grid = (uint64_t)p.nsplit * (uint64_t)B * (uint64_t)hkv;
+    TQ_REQUIRE(grid <= 0xFFFFFFFFull, "too many (stream, split) workgroups");
+    for (int h0 = 0; h0 < a.Gfull; h0 += 4) {
+      a.hofs = h0;
+      a.G = std::min(4, a.Gfull - h0);
+      if (pg == 0) {
+        if (vbits == 2) launch_dl_kernel<0, 2>(q_dtype, (unsigned)grid, a, st);
+        else if (vbits == 3) launch_dl_kernel<0, 3>(q_dtype, (unsigned)grid, a, st);
+        else launch_dl_kernel<0, 4>(q_dtype, (unsigned)grid, a, st);
+      } else if (pg == 1) {
+        launch_dl_kernel<1, 2>(q_dtype, (unsigned)grid, a, st);
+      } else {
+        launch_dl_kernel<2, 2>(q_dtype, (unsigned)grid, a, st);
+      }
+      TQ_LAUNCH_CHECK("dl_decode_kernel");
+    }
+    if (single) return TQ_OK;
+  }
+  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
+                     p.nsplit, p.split_tokens, a.seq_lens, a.t_cap, hq, a.vrot, (int)q_dtype, out,
+                     lse);
+  TQ_LAUNCH_CHECK("fused_combine_kernel");
+  return TQ_OK;
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -1331,15 +1525,14 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                            void* out, float* lse, void* workspace, size_t workspace_bytes,
                            void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
-  if (d != kDim || kbits != 4 || vbits != 2)
-    return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-bit "
+  if (d != kDim || kbits != 4 || vbits < 2 || vbits > 4)
+    return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-4 bit "
                                  "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
-  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
-             "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
+  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0,
+             "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
   TQ_REQUIRE(t_cap >= 0 && t_cap % 64 == 0, "capacity must be a multiple of 64, got %lld",
              (long long)t_cap);
   TQ_REQUIRE(t_cap * 32 < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
-  TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
   if (B == 0) return TQ_OK;
   TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
              "null pointer argument");
@@ -1351,36 +1544,12 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
              "decode-layout K/V and norms must be 16-byte aligned");
   const size_t need = tq_decode_dl_workspace_bytes(B, hq, hkv, t_cap);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
-  hipStream_t st = as_stream(stream);
   const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
-  const size_t rows = (size_t)B * hq;
-  char* ws = static_cast<char*>(workspace) + 256;
-  float* part = reinterpret_cast<float*>(ws);
-  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
-  if (t_cap > 0) {
-    DlArgs a{};
-    a.q = q; a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv; a.G = hq / hkv;
-    a.kpairs = kpairs; a.knorms = knorms; a.vblocks = vblocks; a.vnorms = vnorms;
-    a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
-    a.krot = krotation; a.qscale = scale * 1.4426950408889634f;
-    a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
-    const bool single = p.nsplit == 1;
-    a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
-    const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
-    if (q_dtype == TQ_F32)
-      hipLaunchKernelGGL((dl_decode_kernel<true, true>), grid, dim3(kDlThreads), 0, st, a);
-    else if (q_dtype == TQ_F16)
-      hipLaunchKernelGGL((dl_decode_kernel<false, true>), grid, dim3(kDlThreads), 0, st, a);
-    else
-      hipLaunchKernelGGL((dl_decode_kernel<false, false>), grid, dim3(kDlThreads), 0, st, a);
-    TQ_LAUNCH_CHECK("dl_decode_kernel");
-    if (single) return TQ_OK;
-  }
-  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
-                     p.nsplit, p.split_tokens, seq_lens, t_cap, hq, vrotation, (int)q_dtype, out,
-                     lse);
-  TQ_LAUNCH_CHECK("fused_combine_kernel");
-  return TQ_OK;
+  DlArgs a{};
+  a.q = q; a.kpairs = kpairs; a.knorms = knorms; a.vblocks = vblocks; a.vnorms = vnorms;
+  a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
+  a.krot = krotation; a.vrot = vrotation; a.qscale = scale * 1.4426950408889634f;
+  return run_dl(a, q_dtype, B, hq, hkv, vbits, 0, p, workspace, out, lse, as_stream(stream));
 }
 
 int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
@@ -1415,8 +1584,8 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
                                  void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
   TQ_REQUIRE(d == kDim, "decode layout covers head_dim 64, got %d", d);
-  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0 && hq / hkv <= 4,
-             "num_heads (%d) must be 1-4 times num_kv_heads (%d)", hq, hkv);
+  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0,
+             "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
   int bsl = 0;
   while ((1 << bsl) < block_size) ++bsl;
   TQ_REQUIRE(block_size >= 16 && (1 << bsl) == block_size,
@@ -1425,7 +1594,6 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
   const int64_t t_cap = (int64_t)max_blocks_per_seq * block_size;
   const int64_t pool_rows = num_blocks * hkv * block_size;
   TQ_REQUIRE(pool_rows * 32 < (int64_t)INT_MAX, "pools too large for 32-bit offsets");
-  TQ_REQUIRE((int64_t)B * hkv <= 65535, "too many (batch, kv head) streams");
   if (B == 0) return TQ_OK;
   TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
              "null pointer argument");
@@ -1438,47 +1606,16 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
              "decode-layout pools must be 16-byte aligned");
   const size_t need = tq_decode_dl_workspace_bytes(B, hq, hkv, t_cap);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
-  hipStream_t st = as_stream(stream);
   const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
-  const size_t rows = (size_t)B * hq;
-  char* ws = static_cast<char*>(workspace) + 256;
-  float* part = reinterpret_cast<float*>(ws);
-  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
-  if (t_cap > 0) {
-    DlArgs a{};
-    a.q = q; a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv; a.G = hq / hkv;
-    a.kpairs = kpairs_pool; a.knorms = knorm_pool; a.vblocks = vtile_pool; a.vnorms = vnorm_pool;
-    a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
-    a.krot = krotation; a.qscale = scale * 1.4426950408889634f;
-    a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
-    a.block_tables = block_tables; a.bt_stride = max_blocks_per_seq; a.bs_log2 = bsl;
-    a.pool_rows = (uint32_t)pool_rows;
-    const bool single = p.nsplit == 1;
-    a.vrot = vrotation; a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
-    const dim3 grid((unsigned)p.nsplit, (unsigned)(B * hkv));
-    if (bsl >= 6) {
-      if (q_dtype == TQ_F32)
-        hipLaunchKernelGGL((dl_decode_kernel<true, true, 1>), grid, dim3(kDlThreads), 0, st, a);
-      else if (q_dtype == TQ_F16)
-        hipLaunchKernelGGL((dl_decode_kernel<false, true, 1>), grid, dim3(kDlThreads), 0, st, a);
-      else
-        hipLaunchKernelGGL((dl_decode_kernel<false, false, 1>), grid, dim3(kDlThreads), 0, st, a);
-    } else {
-      if (q_dtype == TQ_F32)
-        hipLaunchKernelGGL((dl_decode_kernel<true, true, 2>), grid, dim3(kDlThreads), 0, st, a);
-      else if (q_dtype == TQ_F16)
-        hipLaunchKernelGGL((dl_decode_kernel<false, true, 2>), grid, dim3(kDlThreads), 0, st, a);
-      else
-        hipLaunchKernelGGL((dl_decode_kernel<false, false, 2>), grid, dim3(kDlThreads), 0, st, a);
-    }
-    TQ_LAUNCH_CHECK("dl_decode_kernel");
-    if (single) return TQ_OK;
-  }
-  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
-                     p.nsplit, p.split_tokens, seq_lens, t_cap, hq, vrotation, (int)q_dtype, out,
-                     lse);
-  TQ_LAUNCH_CHECK("fused_combine_kernel");
-  return TQ_OK;
+  DlArgs a{};
+  a.q = q; a.kpairs = kpairs_pool; a.knorms = knorm_pool; a.vblocks = vtile_pool;
+  a.vnorms = vnorm_pool; a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids;
+  a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
+  a.qscale = scale * 1.4426950408889634f;
+  a.block_tables = block_tables; a.bt_stride = max_blocks_per_seq; a.bs_log2 = bsl;
+  a.pool_rows = (uint32_t)pool_rows;
+  return run_dl(a, q_dtype, B, hq, hkv, 2, bsl >= 6 ? 1 : 2, p, workspace, out, lse,
+                as_stream(stream));
 }
 
 int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,
@@ -1486,13 +1623,14 @@ int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, i
                           int64_t pos, void* stream) {
   TQ_REQUIRE(values == 0 || values == 1, "values must be 0 (keys) or 1 (values)");
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
-  TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
+  TQ_REQUIRE(values ? (bit_width >= 2 && bit_width <= 4) : bit_width == 4,
+             "decode layout holds 4-bit keys and 2-4 bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && pos >= 0 && pos + n <= t_cap, "bad token range");
   TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
              "value tiles need dim 64 and a capacity that is a multiple of 64");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
-  const int64_t per = values ? (((pos + n + 63) >> 6) - (pos >> 6)) * 1024 : n * (d / 2);
+  const int64_t per = values ? (((pos + n + 63) >> 6) - (pos >> 6)) * 512 * bit_width : n * (d / 2);
   const int64_t total = n_streams * per;
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
   hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
@@ -1506,7 +1644,8 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
                             uint8_t* packed, void* stream) {
   TQ_REQUIRE(values == 0 || values == 1, "values must be 0 (keys) or 1 (values)");
   TQ_REQUIRE(d >= 2 && d <= 256 && d % 2 == 0, "dim must be even and at most 256, got %d", d);
-  TQ_REQUIRE(bit_width == (values ? 2 : 4), "decode layout holds 4-bit keys and 2-bit values");
+  TQ_REQUIRE(values ? (bit_width >= 2 && bit_width <= 4) : bit_width == 4,
+             "decode layout holds 4-bit keys and 2-4 bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && t0 >= 0 && t0 + n <= t_cap, "bad token range");
   TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
              "value tiles need dim 64 and a capacity that is a multiple of 64");

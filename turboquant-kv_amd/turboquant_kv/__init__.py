@@ -11,7 +11,7 @@ from turboquant_kv.config import TurboQuantConfig
 from turboquant_kv.cache import QuantizedKVCache
 from turboquant_kv.search import TurboQuantIndex
 from turboquant_kv.quantizers import TurboQuantMSE, TurboQuantProd
-from turboquant_kv.entropy import HuffmanCoder, EntropyPackedStorage
+from turboquant_kv.entropy import HuffmanCoder, EntropyPackedStorage, compute_codeword_probabilities
 from turboquant_kv.reference import (
     quantize_mse,
     dequantize_mse,
@@ -45,6 +45,7 @@ __all__ = [
     "TurboQuantProd",
     "HuffmanCoder",
     "EntropyPackedStorage",
+    "compute_codeword_probabilities",
     "quantize_mse",
     "dequantize_mse",
     "quantize_prod",

@@ -81,7 +81,8 @@ class QuantizedKVCache:
         self._vbnd, self._vcen = vcb[0].to(dev), vcb[1].to(dev)
 
         bpp = (head_dim + 7) // 8
-        self._dl = (not self._is_prod and kb == 4 and vb == 2 and head_dim == 64)
+        # 4-bit keys and 2-4 bit values of head_dim 64 are kept in the decode layout
+        self._dl = (not self._is_prod and kb == 4 and 2 <= vb <= 4 and head_dim == 64)
         # decode-layout value tiles hold 64 tokens: capacity rounded up to a multiple of 64
         self._t_cap = (max_seq_len + 63) // 64 * 64 if self._dl else max_seq_len
         B, H, T = batch_size, num_heads, self._t_cap
@@ -100,7 +101,7 @@ class QuantizedKVCache:
                 continue
             if self._dl:
                 self._kstore.append(torch.zeros(B, H, T, head_dim // 2, **u8))
-                self._vstore.append(torch.zeros(B, H, T // 64, 16 * head_dim, **u8))
+                self._vstore.append(torch.zeros(B, H, T // 64, 8 * vb * head_dim, **u8))
             else:
                 self._kstore.append(torch.zeros(B, H, T, kb * bpp, **u8))
                 self._vstore.append(torch.zeros(B, H, T, vb * bpp, **u8))
@@ -336,8 +337,7 @@ class QuantizedKVCache:
         if seq_lens is None:
             seq_lens = torch.full((B,), int(self.seq_lens[layer_id].item()), dtype=torch.int32,
                                   device=self.device)
-        G = q.shape[1] // self.num_heads
-        if self._dl and G <= 4 and q.shape[1] % self.num_heads == 0:
+        if self._dl and q.shape[1] % self.num_heads == 0:
             return ops.decode_attention_dl(
                 q, self._kstore[layer_id], self._key_norms[layer_id], self._vstore[layer_id],
                 self._val_norms[layer_id], seq_lens, self._kcen, self._vcen, self._key_rotation,

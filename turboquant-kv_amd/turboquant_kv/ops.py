@@ -106,8 +106,8 @@ def decode_attention_packed_lse(q, kpacked, knorms, vpacked, vnorms, seq_lens, k
 def pack_decode_layout(packed: torch.Tensor, cache: torch.Tensor, dim: int, bit_width: int,
                        values: bool, pos: int) -> None:
     """Write bit-plane rows [streams, n, P] into a decode-layout cache at tokens pos..pos+n
-    (keys: [streams, t_cap, dim/2] pair bytes, 4-bit; values: [streams, t_cap/64, 16*dim]
-    tile bytes, 2-bit; dim 64)."""
+    (keys: [streams, t_cap, dim/2] pair bytes, 4-bit; values: [streams, t_cap/64,
+    8*bit_width*dim] tile bytes, 2-4 bit; dim 64)."""
     _require_device(cache, "cache")
     _ops().pack_decode_layout(packed, cache, dim, bit_width, int(values), pos)
 
@@ -121,9 +121,9 @@ def unpack_decode_layout(cache: torch.Tensor, dim: int, bit_width: int, values: 
 
 def decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids, vcentroids,
                         krotation, vrotation, scale, return_lse: bool = False):
-    """decode_attention_packed over a decode-layout cache (4-bit keys, 2-bit values,
-    head_dim 64, 1-4 query heads per KV head): [B, Hq, d] in q.dtype (and the [B, Hq]
-    log-sum-exp with return_lse)."""
+    """decode_attention_packed over a decode-layout cache (4-bit keys, 2-4 bit values --
+    the width of the value tiles names it --, head_dim 64, any number of query heads per
+    KV head): [B, Hq, d] in q.dtype (and the [B, Hq] log-sum-exp with return_lse)."""
     _require_device(q, "q")
     if return_lse:
         return _ops().decode_attention_dl_lse(q, kpairs, knorms, vblocks, vnorms, seq_lens,
