@@ -406,6 +406,107 @@ def bench_prod_scan(args, extra):
         log(f"prod search by dequantize + matmul: {t:.2f} ms/query")
 
 
+def bench_e2e(args, extra):
+    """greedy decode through TurboQuantCache on a random-init Llama-3.2-1B-shaped
+    model (16 layers, hidden 2048, 32 query / 8 KV heads of 64 dims, FFN 8192, vocab 128,256,
+    tied embeddings, bf16): batch 64, 4096-token random-id prompts, 256 generated tokens,
+    keys 4-bit / values 3-bit, fused attention (the decode kernel over the packed history,
+    the exact new token merged by log-sum-exp).  Reports decode and end-to-end tokens/s,
+    the decode kernel's time per layer at the final length with its HBM fraction, and the
+    cache bytes against a bf16 cache of the same tokens; the same model with transformers'
+    bf16 DynamicCache is timed beside it."""
+    import torch
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+    from turboquant_kv import TurboQuantCache, _lib
+    from turboquant_kv.hf_integration import enable_fused_attention
+
+    ops = _lib.ops()
+    B, T0, n_new = 64, 4096, 256
+    if args.quick:
+        n_new = 64
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=8192, num_hidden_layers=16,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=64,
+                      vocab_size=128256, max_position_embeddings=8192, tie_word_embeddings=True,
+                      rope_theta=500000.0)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(cfg).eval()
+    torch.set_default_dtype(prev)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ids = torch.randint(0, cfg.vocab_size, (B, T0), generator=g, device="cuda")
+
+    def run(cache):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            toks = [nxt]
+            for _ in range(n_new - 1):
+                out = model(input_ids=nxt, past_key_values=cache, use_cache=True)
+                nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+                toks.append(nxt)
+            torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1, torch.cat(toks, 1)
+
+    cache = TurboQuantCache(key_bits=4, value_bits=3, fused_attention=True)
+    enable_fused_attention(model)
+    log("e2e: prefill + decode through TurboQuantCache K4/V3 (fused)")
+    pre, dec, toks = run(cache)
+    T = T0 + n_new - 1
+    mem = cache.memory_bytes()
+    bf16_bytes = cfg.num_hidden_layers * 2 * B * 8 * T * 64 * 2
+    res = {"decode_tokens_per_s": B * (n_new - 1) / dec, "ms_per_decode_step": dec / (n_new - 1) * 1e3,
+           "prefill_s": pre, "end_to_end_tokens_per_s": B * n_new / (pre + dec),
+           "cache_bytes": mem, "cache_bytes_bf16": bf16_bytes, "compression_vs_bf16": bf16_bytes / mem,
+           "batch": B, "prompt": T0, "new_tokens": n_new,
+           "model": "random-init Llama-3.2-1B shape (16 x 2048, 32/8 heads x 64, FFN 8192, "
+                    "vocab 128256, bf16)", "cache": "TurboQuantCache(key_bits=4, value_bits=3, "
+                                                     "fused_attention=True)"}
+    log(f"e2e K4/V3: prefill {pre:.2f} s, decode {dec / (n_new - 1) * 1e3:.2f} ms/step = "
+        f"{B * (n_new - 1) / dec:.0f} tokens/s; cache {mem / 1e9:.2f} GB vs bf16 "
+        f"{bf16_bytes / 1e9:.2f} GB ({bf16_bytes / mem:.2f}x)")
+    # the decode kernel alone on the final caches, one call per layer in turn (16 x 146 MB:
+    # beyond the 256 MB Infinity Cache)
+    layers = cache.layers
+    q = torch.randn(B, 32, 64, generator=g, device="cuda").to(torch.bfloat16)
+    sl = torch.full((B,), T, dtype=torch.int32, device="cuda")
+    it = [0]
+
+    def one():
+        L = layers[it[0] % len(layers)]
+        it[0] += 1
+        return ops.decode_attention_dl_lse(q, L.kp, L.kn, L.vp, L.vn, sl, L.kq.cen, L.vq.cen,
+                                           L.kq.R, L.vq.R, 0.125)
+
+    ms = time_op(one, 32, 4)
+    kb = B * 8 * T * (32 + 24 + 8) + 2 * B * 32 * 64 * 2
+    res["decode_kernel_us_per_layer"] = ms * 1e3
+    res["decode_kernel_GBps"] = kb / ms / 1e6
+    res["decode_kernel_hbm_frac"] = kb / ms / 1e6 / HBM_PEAK_GBS
+    log(f"e2e decode kernel (T={T}, K4/V3): {ms * 1e3:.1f} us per layer, {kb / ms / 1e6:.0f} GB/s")
+    del cache, layers
+    torch.cuda.empty_cache()
+    if not args.quick:
+        model.set_attn_implementation("sdpa")
+        pre_b, dec_b, toks_b = run(DynamicCache())
+        res["bf16_dynamic_cache"] = {"decode_tokens_per_s": B * (n_new - 1) / dec_b,
+                                     "ms_per_decode_step": dec_b / (n_new - 1) * 1e3,
+                                     "prefill_s": pre_b,
+                                     "first_token_agreement": float((toks_b[:, 0] == toks[:, 0]).float().mean())}
+        log(f"e2e bf16 DynamicCache: decode {dec_b / (n_new - 1) * 1e3:.2f} ms/step = "
+            f"{B * (n_new - 1) / dec_b:.0f} tokens/s")
+    extra["e2e_greedy_decode_llama1b_K4V3"] = res
+    del model
+    torch.cuda.empty_cache()
+
+
 def cpu_baseline(db, budget_s=12.0):
     """The reference's C++ search_packed over the same 10M-row database, one query per
     OpenMP thread, enough rounds of queries for about `budget_s` seconds."""
@@ -448,6 +549,8 @@ def main():
                     help="only the quantize_prod cases (configs 3a/3b), e.g. for a profiler run")
     ap.add_argument("--prod-only", action="store_true",
                     help="only the prod-mode scan (10M x 128, 3+1 bit), e.g. for a profiler run")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the end-to-end greedy decode (configs[4])")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (counter calibration)")
     args = ap.parse_args()
@@ -480,6 +583,11 @@ def main():
         bench_prod_scan(args, extra)
         print(json.dumps(extra))
         return
+    if args.e2e_only:
+        extra = {}
+        bench_e2e(args, extra)
+        print(json.dumps(extra))
+        return
     extra = {}
     t0 = time.perf_counter()
     scan = bench_scan(args, extra)
@@ -488,6 +596,7 @@ def main():
         bench_quantize(args, extra)
         bench_prod_scan(args, extra)
         bench_formats(args, extra)
+        bench_e2e(args, extra)
     cpu = None if args.no_cpu else cpu_baseline(scan["db4"])
     ms, bytes_alg = scan["headline"]
     achieved = bytes_alg / ms / 1e6

@@ -39,30 +39,115 @@ def test_hf_update_returns_dequantized_history_plus_exact_new():
     bnd, cen = O.lloyd_max_codebook(4, 64)
     x = k1.reshape(-1, 64).cpu().numpy()
     _, _, codes = O.quantize_mse(x, 4, R, bnd)
-    got = O.unpack_codes(layer.kp[:, :, :5].reshape(-1, 32).cpu().numpy(), 4, 64)
+    rows = layer.rows(False, 5).reshape(-1, 32).cpu().numpy()   # bit-plane rows
+    got = O.unpack_codes(rows, 4, 64)
     assert not ((got != codes) & ~O.code_margin(x, R, bnd)).any()
-    deq = O.dequantize_mse(layer.kp[:, :, :5].reshape(-1, 32).cpu().numpy(),
-                           layer.kn[:, :, :5].reshape(-1).cpu().numpy(), 4, 64, R, cen)
+    deq = O.dequantize_mse(rows, layer.kn[:, :, :5].reshape(-1).cpu().numpy(), 4, 64, R, cen)
     assert np.allclose(K[:, :, :5].reshape(-1, 64).cpu().numpy(), deq, rtol=1e-5, atol=1e-5)
     assert cache.get_seq_length(0) == 6 and cache.memory_bytes() == 2 * 2 * 6 * (32 + 16 + 8)
 
 
-def test_hf_generate_plain_and_fused_agree():
+def _tiny_llama_gqa4(seed=0, dtype=torch.float32):
+    """Two layers, 16 query heads over 4 KV heads of 64 dims (the group size of the
+    end-to-end config)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(hidden_size=1024, intermediate_size=2048, num_hidden_layers=2,
+                      num_attention_heads=16, num_key_value_heads=4, head_dim=64,
+                      vocab_size=1000, max_position_embeddings=1024, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    return LlamaForCausalLM(cfg).to(DEV, dtype).eval()
+
+
+def test_hf_fused_decode_logits_match_reference_semantics():
+    # A K4/V3 TurboQuantCache through a prefill of 512 tokens and three decode steps:
+    # the fused steps (packed history by the decode kernel + exact new token by
+    # log-sum-exp) against the reference's rule run by the general path (dequantized
+    # history + exact new tokens, then SDPA).  fp32 model: the paths differ only in
+    # summation order, so the logits agree tightly.
     from turboquant_kv import TurboQuantCache
     from turboquant_kv.hf_integration import enable_fused_attention
-    model = _tiny_llama()
-    ids = torch.randint(0, 1000, (2, 40), device=DEV, generator=torch.Generator(DEV).manual_seed(1))
+    model = _tiny_llama_gqa4()
+    g = torch.Generator(DEV).manual_seed(1)
+    ids = torch.randint(0, 1000, (4, 512), device=DEV, generator=g)
+    nxt = torch.randint(0, 1000, (4, 3), device=DEV, generator=g)
+
+    def run(fused):
+        cache = TurboQuantCache(key_bits=4, value_bits=3, fused_attention=fused)
+        if fused:
+            enable_fused_attention(model)
+        else:
+            model.set_attn_implementation("sdpa")
+        logits = []
+        with torch.no_grad():
+            model(input_ids=ids, past_key_values=cache, use_cache=True)
+            for i in range(3):
+                out = model(input_ids=nxt[:, i:i + 1], past_key_values=cache, use_cache=True)
+                logits.append(out.logits[:, -1].float())
+        return torch.stack(logits), cache
+
+    ref, c_ref = run(False)
+    got, c_got = run(True)
+    assert c_got.layers[0].dl and c_got.get_seq_length(0) == 515
+    err = ((got - ref).abs().amax(-1) / ref.abs().amax(-1)).max().item()
+    assert err <= 1e-3, err
+    # cache bytes: 4-bit keys + 3-bit values + two fp32 norms per (token, kv head)
+    assert c_got.memory_bytes() == 2 * 4 * 4 * 515 * (32 + 24 + 8)
     with torch.no_grad():
-        plain = model.generate(ids, past_key_values=TurboQuantCache(key_bits=4, value_bits=4),
-                               max_new_tokens=12, do_sample=False)
-        enable_fused_attention(model)
-        fused = model.generate(ids, past_key_values=TurboQuantCache(key_bits=4, value_bits=4,
-                                                                     fused_attention=True),
-                               max_new_tokens=12, do_sample=False)
-    assert plain.shape == fused.shape == (2, 52)
-    # Same prompt handling; decode steps differ only by fp32 summation order.
-    agree = (plain[:, 40:] == fused[:, 40:]).float().mean().item()
-    assert agree >= 0.9, agree
+        out = model.generate(ids[:, :40], past_key_values=TurboQuantCache(4, 3, fused_attention=True),
+                             max_new_tokens=6, do_sample=False)
+    assert out.shape == (4, 46)
+
+
+@pytest.mark.parametrize("vb,G", [(3, 4), (2, 4), (4, 2), (3, 8)])
+def test_hf_fused_decode_step_vs_f64(vb, G):
+    # One decode step of a bf16 layer: the attention function's output against float64
+    # attention over the stored history (dequantized from the cache's own rows) followed
+    # by the exact new token -- the reference's update rule (hf_integration.py:372-390)
+    # and SDPA, with GQA (query head h reads KV head h // G).
+    from turboquant_kv import TurboQuantCache
+    from turboquant_kv.hf_integration import turboquant_attention
+    torch.manual_seed(10 * vb + G)
+    B, Hkv, d, T = 4, 4, 64, 512
+    Hq = G * Hkv
+    cache = TurboQuantCache(key_bits=4, value_bits=vb, fused_attention=True)
+    k0 = (torch.randn(B, Hkv, T, d, device=DEV) * 2).to(torch.bfloat16)
+    v0 = torch.randn(B, Hkv, T, d, device=DEV).to(torch.bfloat16)
+    cache.update(k0, v0, 0)
+    k1 = torch.randn(B, Hkv, 1, d, device=DEV).to(torch.bfloat16)
+    v1 = torch.randn(B, Hkv, 1, d, device=DEV).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 1, d, device=DEV).to(torch.bfloat16)
+    K, V = cache.update(k1, v1, 0)
+
+    class M:
+        layer_idx = 0
+    got, _ = turboquant_attention(M(), q, K, V, None, scaling=1 / 8)
+    got = got.float().cpu().numpy()[:, 0]                       # [B, Hq, d]
+    layer = cache.layers[0]
+    assert layer.dl
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    _, ck = O.lloyd_max_codebook(4, d)
+    _, cv = O.lloyd_max_codebook(vb, d)
+    kr = layer.rows(False, T).cpu().numpy()
+    vr = layer.rows(True, T).cpu().numpy()
+    kn = layer.kn[:, :, :T].cpu().numpy()
+    vn = layer.vn[:, :, :T].cpu().numpy()
+    qf = q.float().cpu().numpy()[:, :, 0].astype(np.float64)
+    k1f = k1.float().cpu().numpy()[:, :, 0].astype(np.float64)
+    v1f = v1.float().cpu().numpy()[:, :, 0].astype(np.float64)
+    want = np.zeros((B, Hq, d))
+    for b in range(B):
+        for g in range(Hkv):
+            Kh = O.dequantize_mse(kr[b, g], kn[b, g], 4, d, Rk, ck).astype(np.float64)
+            Vh = O.dequantize_mse(vr[b, g], vn[b, g], vb, d, Rv, cv).astype(np.float64)
+            Ka = np.concatenate([Kh, k1f[b, g][None]])
+            Va = np.concatenate([Vh, v1f[b, g][None]])
+            for h in range(g * G, (g + 1) * G):
+                s = Ka @ qf[b, h] / 8
+                p = np.exp(s - s.max())
+                want[b, h] = (p / p.sum()) @ Va
+    err = np.max(np.abs(got - want), axis=-1) / np.max(np.abs(want), axis=-1)
+    assert err.max() <= 1e-2, err.max()
 
 
 def test_hf_fused_step_matches_plain_step():

@@ -1,10 +1,14 @@
 """HuggingFace Transformers integration: TurboQuantCache (API of hf_integration.py:272-555).
 
 Targets the layer-based Cache of transformers 5.x: each transformer layer gets a
-`TurboQuantLayer` holding packed device storage [B, H_kv, capacity, P] + fp32 norms that
+`TurboQuantLayer` holding packed device storage + fp32 norms [B, H_kv, capacity] that
 grows geometrically; every `update` quantizes all (batch, head, token) rows of the new
 states in one kernel launch (the reference loops over batch items and heads in Python,
-hf_integration.py:370-415).
+hf_integration.py:370-415).  MSE caches with 4-bit keys, 2-4 bit values and head_dim 64
+(the default K4/V2 and the K4/V3 of the end-to-end config) keep their codes in the decode
+layout -- key pair bytes [B, H_kv, capacity, 32], 64-token value tiles [B, H_kv,
+capacity/64, 512*value_bits] -- that the fused decode kernel streams; other shapes keep
+the reference's bit-plane rows [B, H_kv, capacity, P].
 
 Semantics kept from the reference (hf_integration.py:319-421):
   * protected layers (index < protected_layers) keep exact K/V;
@@ -17,9 +21,11 @@ Fused attention (new): construct the cache with `fused_attention=True` and run t
 with `attn_implementation="turboquant"` (registered here; see `enable_fused_attention`).
 Updates then return only the new tokens, and the attention function attends to the
 packed history with the fused decode kernel, merging the exact new token by log-sum-exp
--- no dequantized copy of the history is materialized.  Steps that carry an attention
-mask, more than one query token or prod-mode storage take the general path (dequantize
-the history, then SDPA), which has the reference's numerics.
+-- no dequantized copy of the history is materialized.  Single-token MSE steps without
+an attention mask run it (decode-layout storage: any number of query heads per KV head;
+bit-plane rows: the shapes tq_decode_attention_packed fuses, else its split kernels);
+prefill chunks, masked steps and prod-mode storage take the general path (dequantize the
+history, then SDPA), which has the reference's numerics.
 """
 
 from __future__ import annotations
@@ -97,6 +103,7 @@ class TurboQuantLayer(_HFLayer):
         self.fused_attention = fused_attention and not protected
         self.seq_len = 0
         self.cap = 0
+        self.dl = False
 
     # ------------------------------------------------------------ storage
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
@@ -111,25 +118,37 @@ class TurboQuantLayer(_HFLayer):
             self.kq = _Quantizer(d, cfg.key_bits, cfg.seed, cfg, self.device)
             self.vq = _Quantizer(d, cfg.value_bits, cfg.seed + 1, cfg, self.device)
             self.keys = self.values = None
+            # decode layout: mse, 4-bit keys, 2-4 bit values, head_dim 64
+            self.dl = (not self.kq.prod and self.kq.code_bits == 4 and
+                       2 <= self.vq.code_bits <= 4 and d == 64)
         self.is_initialized = True
 
     def _grow(self, need: int) -> None:
         if need <= self.cap:
             return
         cap = max(need, 2 * self.cap, 256)
+        if self.dl:
+            cap = (cap + 63) // 64 * 64  # whole 64-token value tiles
         B, H, d = self.batch, self.num_heads, self.head_dim
         bpp = (d + 7) // 8
         dev = self.device
         prod = self.kq.prod
 
-        def grown(old, *tail, dtype):
-            t = torch.zeros(B, H, cap, *tail, dtype=dtype, device=dev)
-            if old is not None and self.seq_len:
-                t[:, :, : self.seq_len] = old[:, :, : self.seq_len]
+        def grown(old, *tail, dtype, per_tile=False):
+            n = cap // 64 if per_tile else cap
+            t = torch.zeros(B, H, n, *tail, dtype=dtype, device=dev)
+            used = (self.seq_len + 63) // 64 if per_tile else self.seq_len
+            if old is not None and used:
+                t[:, :, :used] = old[:, :, :used]
             return t
 
-        self.kp = grown(getattr(self, "kp", None), self.kq.code_bits * bpp, dtype=torch.uint8)
-        self.vp = grown(getattr(self, "vp", None), self.vq.code_bits * bpp, dtype=torch.uint8)
+        if self.dl:
+            self.kp = grown(getattr(self, "kp", None), d // 2, dtype=torch.uint8)
+            self.vp = grown(getattr(self, "vp", None), 8 * self.vq.code_bits * d, dtype=torch.uint8,
+                            per_tile=True)
+        else:
+            self.kp = grown(getattr(self, "kp", None), self.kq.code_bits * bpp, dtype=torch.uint8)
+            self.vp = grown(getattr(self, "vp", None), self.vq.code_bits * bpp, dtype=torch.uint8)
         self.kn = grown(getattr(self, "kn", None), dtype=torch.float32)
         self.vn = grown(getattr(self, "vn", None), dtype=torch.float32)
         if prod:
@@ -143,10 +162,15 @@ class TurboQuantLayer(_HFLayer):
         B, H, s, d = key_states.shape
         self._grow(self.seq_len + s)
         sl = slice(self.seq_len, self.seq_len + s)
-        for q, x, p, n, sg, rs in ((self.kq, key_states, self.kp, self.kn, "ks", "kr"),
-                                   (self.vq, value_states, self.vp, self.vn, "vs", "vr")):
+        for vals, (q, x, p, n, sg, rs) in enumerate(
+                ((self.kq, key_states, self.kp, self.kn, "ks", "kr"),
+                 (self.vq, value_states, self.vp, self.vn, "vs", "vr"))):
             out = q.quantize(x.reshape(-1, d))
-            p[:, :, sl] = out[0].view(B, H, s, -1)
+            if self.dl:
+                _ops().pack_decode_layout(out[0].view(B * H, s, -1), p.view(B * H, p.shape[2], -1),
+                                          d, q.code_bits, vals, self.seq_len)
+            else:
+                p[:, :, sl] = out[0].view(B, H, s, -1)
             n[:, :, sl] = out[-1].float().view(B, H, s)
             if q.prod:
                 getattr(self, sg)[:, :, sl] = out[1].view(B, H, s, -1)
@@ -163,7 +187,7 @@ class TurboQuantLayer(_HFLayer):
         res = []
         for q, p, n, sg, rs in ((self.kq, self.kp, self.kn, "ks", "kr"),
                                 (self.vq, self.vp, self.vn, "vs", "vr")):
-            flat_p = p[:, :, :T].reshape(B * H * T, -1)
+            flat_p = self.rows(p is self.vp, T).reshape(B * H * T, -1)
             flat_n = n[:, :, :T].reshape(-1)
             if q.prod:
                 out = q.dequantize(flat_p, flat_n, getattr(self, sg)[:, :, :T].reshape(B * H * T, -1),
@@ -173,6 +197,19 @@ class TurboQuantLayer(_HFLayer):
                                    dtype=self.dtype)
             res.append(out.view(B, H, T, d).to(self.dtype))
         return res[0], res[1]
+
+    def rows(self, values: bool, T: Optional[int] = None) -> torch.Tensor:
+        """Bit-plane packed rows [B, H, T, P] of tokens 0..T-1 (reference.py:191-224),
+        whatever the storage layout."""
+        T = self.seq_len if T is None else T
+        p = self.vp if values else self.kp
+        if not self.dl:
+            return p[:, :, :T]
+        B, H = self.batch, self.num_heads
+        q = self.vq if values else self.kq
+        r = _ops().unpack_decode_layout(p.view(B * H, p.shape[2], -1), self.head_dim, q.code_bits,
+                                        int(values), 0, T)
+        return r.view(B, H, T, -1)
 
     # ------------------------------------------------------------ Cache layer API
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
@@ -274,9 +311,14 @@ def turboquant_attention(module, query, key, value, attention_mask, scaling=None
     if sq == 1 and attention_mask is None and t_hist > 0 and not layer.kq.prod:
         q = query[:, :, 0, :]
         seq = torch.full((B,), t_hist, dtype=torch.int32, device=query.device)
-        o_h, lse_h = _ops().decode_attention_packed_lse(
-            q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
-            layer.kq.R, layer.vq.R, layer.kq.bits, layer.vq.bits, float(scaling))
+        if layer.dl:
+            o_h, lse_h = _ops().decode_attention_dl_lse(
+                q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
+                layer.kq.R, layer.vq.R, float(scaling))
+        else:
+            o_h, lse_h = _ops().decode_attention_packed_lse(
+                q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
+                layer.kq.R, layer.vq.R, layer.kq.bits, layer.vq.bits, float(scaling))
         G = Hq // k_new.shape[1]
         kn = k_new[:, :, 0, :].float().repeat_interleave(G, dim=1)        # (B, Hq, d)
         vn = value[:, :, 0, :].float().repeat_interleave(G, dim=1)
