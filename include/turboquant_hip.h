@@ -169,6 +169,23 @@ int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, i
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * tq_ip_scan_topk_pairs without a workspace argument.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops that forbid hipMalloc).  The candidate lists live in a static device
+ * array of TQ_NOALLOC_SCRATCH_BYTES per GPU, held from library load until the process
+ * ends; calls that need more (tq_scan_workspace_bytes(nq, d, 4, N, k) above it: about
+ * nq * k <= 340 at N >= 2M) return TQ_EINVAL.  Nothing is allocated and nothing has to
+ * start at zero.  Every call on one GPU shares the array: calls that overlap on that GPU
+ * (other streams or host threads) race.  `stream` must belong to the current device.
+ * Same arguments (without workspace), outputs and tie rule as tq_ip_scan_topk_pairs.
+ */
+#define TQ_NOALLOC_SCRATCH_BYTES (4u << 20)
+int tq_ip_scan_topk_pairs_noalloc(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                  const uint8_t* pairs, const float* norms, int64_t N,
+                                  const float* centroids, const float* rotation, int32_t k,
+                                  float* out_scores, int64_t* out_ids, void* stream);
+
+/*
  * Prod-mode scoring without reconstruction.  Replaces TurboQuantIndex._search_prod
  * (turboquant_kv/search.py:229-252: dequantize_prod of every row, then queries @ recon^T
  * and topk) and, for prod-mode caches, the dequantize-then-matmul of

@@ -33,6 +33,7 @@
 #include "tq_decode.h"
 
 #include <climits>
+#include <mutex>
 #include <utility>
 
 namespace tq {
@@ -1838,6 +1839,74 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                      seq_lens, hq, (int)q_dtype, out, t_max > 0 ? stats : nullptr, lse);
   TQ_LAUNCH_CHECK("combine_kernel");
   return TQ_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ no-allocation scan
+// tq_ip_scan_topk_pairs_noalloc: the pair-layout top-k scan with its per-block candidate
+// lists in a file-scope device array instead of a caller workspace.  Each GPU holds its
+// own copy of `scratch` (TQ_NOALLOC_SCRATCH_BYTES) from the moment the library's code is
+// loaded on it until the process ends.  Host code never passes `scratch` itself to a
+// kernel (its name is a host-side stand-in, not a device address): the device address is
+// looked up once per device with hipGetSymbolAddress and kept in scratch_dev[].
+// Every scan block writes all k slots of its lists before merge_kernel reads them, so
+// nothing in the array has to start at zero; calls that overlap on one GPU race on it.
+static __device__ __align__(256) unsigned char scratch[TQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxScratchDevices];
+
+// Device address of `scratch` on the stream's device, which must be the current one (the
+// symbol lookup answers for the current device).
+int scratch_address(hipStream_t st, void** out) {
+  int cur = 0;
+  TQ_HIP_TRY(hipGetDevice(&cur));
+  hipDevice_t sdev = cur;
+  if (st != nullptr) TQ_HIP_TRY(hipStreamGetDevice(st, &sdev));
+  if ((int)sdev != cur)
+    return fail(TQ_EINVAL, "the stream belongs to device %d, but device %d is current",
+                (int)sdev, cur);
+  if (cur < 0 || cur >= kMaxScratchDevices)
+    return fail(TQ_EUNSUPPORTED, "device ordinal %d above %d", cur, kMaxScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[cur] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TQ_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", cur,
+                  hipGetErrorString(e));
+    scratch_dev[cur] = p;
+  }
+  *out = scratch_dev[cur];
+  return TQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tq_ip_scan_topk_pairs_noalloc(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                  const uint8_t* pairs, const float* norms, int64_t N,
+                                  const float* centroids, const float* rotation, int32_t k,
+                                  float* out_scores, int64_t* out_ids, void* stream) {
+  TQ_REQUIRE(d == 64 || d == 128, "pair-layout scan needs dim 64 or 128, got %d", d);
+  TQ_REQUIRE(k >= 1 && k <= kMaxK, "k must be in [1, %d], got %d", kMaxK, k);
+  TQ_REQUIRE(nq >= 0 && N >= 0, "bad sizes");
+  const size_t need = tq_scan_workspace_bytes(nq, d, 4, N, k);
+  TQ_REQUIRE(need <= (size_t)TQ_NOALLOC_SCRATCH_BYTES,
+             "%lld queries x k=%d over %lld rows need %zu bytes of scratch, above the static "
+             "%u bytes; use tq_ip_scan_topk_pairs with a workspace",
+             (long long)nq, k, (long long)N, need, (unsigned)TQ_NOALLOC_SCRATCH_BYTES);
+  if (nq == 0) return TQ_OK;
+  void* ws = nullptr;
+  const int rc = scratch_address(as_stream(stream), &ws);
+  if (rc != TQ_OK) return rc;
+  return tq_ip_scan_topk_pairs(queries, q_dtype, nq, d, pairs, norms, N, centroids, rotation, k,
+                               out_scores, out_ids, ws, TQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"
