@@ -181,12 +181,15 @@ def code_margin(x, R, bnd, dtype: str = "f32", rel: float | None = None):
     x = np.asarray(x, dtype=np.float32)
     bnd = np.asarray(bnd, np.float32)
     if rel is None:
-        rel = 2.0 ** -18 if dtype == "f32" else 2.0 ** -21
+        rel = 2.0 ** -20 if dtype == "f32" else 2.0 ** -21
     if dtype == "f32":
+        # rel * sum_k |u_k R_jk| covers two fp32 dot products of d terms summed in
+        # different orders (each about sqrt(d) * 2^-25 of that sum, 2^-21.5 at d = 128);
+        # 2^-22 |y| covers the norm and the division landing an ulp or two apart.
         n = np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=-1))
         u = x / np.maximum(n, 1e-10)[:, None]
         y = _rowdot(u, R)
-        band = rel * (np.abs(u) @ np.abs(np.asarray(R, np.float64)).T) + 4e-7 * np.abs(y)
+        band = rel * (np.abs(u) @ np.abs(np.asarray(R, np.float64)).T) + 2.0 ** -22 * np.abs(y)
         d = np.min(np.abs(y[..., None] - bnd.astype(np.float64)), axis=-1)
         return d <= band
     n32 = np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=-1))
@@ -201,6 +204,37 @@ def code_margin(x, R, bnd, dtype: str = "f32", rel: float | None = None):
     band = rel * (np.abs(u).astype(np.float64) @ np.abs(Rr.astype(np.float64)).T)
     amb = round_to((y - band).astype(np.float32), dtype) != round_to((y + band).astype(np.float32), dtype)
     return amb | row_amb[:, None]
+
+
+def boundary_distance(x, R, bnd):
+    """Per coordinate, the float64 distance of y = (x/|x|) R^T from its nearest decision
+    boundary in units of sum_k |u_k R_jk| -- the scale of fp32 dot-product rounding, so
+    a code two fp32 computations disagree on has a small value here."""
+    x = np.asarray(x, dtype=np.float32)
+    n = np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=-1))
+    u = x / np.maximum(n, 1e-10)[:, None]
+    y = _rowdot(u, R)
+    scale = np.abs(u) @ np.abs(np.asarray(R, np.float64)).T
+    d = np.min(np.abs(y[..., None] - np.asarray(bnd, np.float64)), axis=-1)
+    return d / np.maximum(scale, 1e-300)
+
+
+def check_codes(got, want, x, R, bnd, dtype: str = "f32", max_rate: float = 2e-5):
+    """Parity of quantize codes (SURVEY Appendix B.1 policy): codes outside the ambiguity
+    band must be identical; inside it they may differ, but no more often than `max_rate`
+    per coordinate (about 10x the flip rate two fp32 summation orders give near the
+    boundaries, ~1-2e-6).  Returns a summary dict; raises AssertionError otherwise."""
+    amb = code_margin(x, R, bnd, dtype)
+    diff = np.asarray(got) != np.asarray(want)
+    outside = diff & ~amb
+    info = {"coords": int(diff.size), "band": int(amb.sum()), "mismatches": int(diff.sum()),
+            "outside_band": int(outside.sum())}
+    if dtype == "f32" and diff.any():
+        info["max_mismatch_distance"] = float(boundary_distance(x, R, bnd)[diff].max())
+    assert not outside.any(), ("codes differ outside the ambiguity band", info,
+                               np.argwhere(outside)[:5])
+    assert info["mismatches"] <= max(2, max_rate * diff.size), ("too many in-band flips", info)
+    return info
 
 
 def dequantize_mse(packed, norms, bits, dim, R, cen, dtype: str = "f32"):
@@ -340,6 +374,33 @@ def decode_attention_f64(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, 
                 p /= p.sum()
                 out[b, h] = p @ V
     return (out, lse) if return_lse else out
+
+
+def decode_attention_bf16_reference(q, kpacked, knorms, vpacked, vnorms, seq_lens, kc, vc, Rk,
+                                    Rv, kbits, vbits, scale):
+    """The reference's own rounding for a bf16 model's cache, with float64 sums elsewhere:
+    the history is dequantized in the norms' dtype, so every K/V element is rounded to
+    bf16 (reference.py:356-365 computes c[codes] @ R * n in norms.dtype), handed to SDPA
+    in bf16 (hf_integration.py:372-390), and the output is rounded to bf16.  Not the
+    product's parity target: it measures how far the reference's bf16 arithmetic itself
+    sits from decode_attention_f64, the bar the kernels' bf16 paths are held under."""
+    q = round_bf16(np.asarray(q, np.float32)).astype(np.float64)
+    B, Hq, d = q.shape
+    Hkv = kpacked.shape[1]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, d))
+    for b in range(B):
+        T = int(seq_lens[b])
+        if T == 0:
+            continue
+        for g in range(Hkv):
+            K = round_bf16(dequantize_mse(kpacked[b, g, :T], knorms[b, g, :T], kbits, d, Rk, kc)).astype(np.float64)
+            V = round_bf16(dequantize_mse(vpacked[b, g, :T], vnorms[b, g, :T], vbits, d, Rv, vc)).astype(np.float64)
+            for h in range(g * G, (g + 1) * G):
+                s = (K @ q[b, h]) * scale
+                p = np.exp(s - s.max())
+                out[b, h] = round_bf16(((p / p.sum()) @ V).astype(np.float32))
+    return out
 
 
 # ----------------------------------------------------------------- paged KV (vLLM block tables)

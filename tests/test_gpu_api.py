@@ -35,8 +35,8 @@ def test_quantize_mse_api_vs_reference(golden):
         packed, norms = quantize_mse(T(x), b)  # default rotation seed 42, default codebook
         codes = O.unpack_codes(packed.cpu().numpy(), b, 128)
         ref = O.unpack_codes(m[f"d128_b{b}_packed"], b, 128)
-        amb = O.code_margin(x, make_rotation_matrix(128, 42).numpy(), lloyd_max_codebook(b, 128)[0].numpy())
-        assert not ((codes != ref) & ~amb).any()
+        O.check_codes(codes, ref, x, make_rotation_matrix(128, 42).numpy(),
+                      lloyd_max_codebook(b, 128)[0].numpy())
         assert norms.dtype == torch.float32
         rec = dequantize_mse(T(m[f"d128_b{b}_packed"][:64]), T(m[f"d128_b{b}_norms"][:64]), b, 128)
         assert np.allclose(rec.cpu().numpy(), m[f"d128_b{b}_deq64"], rtol=1e-5, atol=2e-6)
@@ -135,7 +135,9 @@ def test_prod_index_search_scores_without_reconstruction():
                                           idx._residual_norms, idx._norms)]
         R, S = idx._rot_dev.cpu().numpy(), idx._S_dev.cpu().numpy()
         ref = O.prod_scores_f64(q, *rows, b, d, R, idx._cen.cpu().numpy(), S)
-        tol = 1e-4 * np.linalg.norm(q, axis=1)[:, None] * rows[3][None, :] * (1 + 2 * rows[2][None, :])
+        # fp32 sums of d terms against float64: d * 2^-24 of the summed magnitude
+        # |q| n (1 + 2 gamma)
+        tol = d * 2.0 ** -24 * np.linalg.norm(q, axis=1)[:, None] * rows[3][None, :] * (1 + 2 * rows[2][None, :])
         recon = torch.ops.turboquant.dequantize_prod_packed(
             idx._packed_codes, idx._qjl_signs, idx._residual_norms, idx._norms, idx._cen,
             idx._rot_dev, idx._S_dev, b, d)
@@ -165,7 +167,8 @@ def test_prod_cache_scores_without_reconstruction():
     keys = kv._dequantize_keys(0).repeat_interleave(Hq // H, dim=1)   # (B, Hq, T, d)
     ref = torch.matmul(q.double(), keys.double().transpose(-2, -1)) / math.sqrt(d)
     scale = q.double().norm(dim=-1, keepdim=True) * keys.double().norm(dim=-1)[:, :, None, :]
-    assert ((logits.double() - ref).abs() <= 1e-4 * scale / math.sqrt(d) + 1e-6).all()
+    # both sides carry fp32 sums of d terms (the prod scan; the dequantize kernel): 2 d 2^-24
+    assert ((logits.double() - ref).abs() <= 2 * d * 2.0 ** -24 * scale / math.sqrt(d) + 1e-7).all()
 
 
 def test_tqix_index_from_reference_core_file(golden, tmp_path):
@@ -189,8 +192,7 @@ def test_tqix_index_from_reference_core_file(golden, tmp_path):
     own.add(T(z["vectors"]))
     got = O.unpack_codes(own._packed_codes.cpu().numpy(), 3, 64)
     want = O.unpack_codes(open_tqix_codes(src), 3, 64)
-    amb = O.code_margin(z["vectors"], z["R_d64_s7"], z["bnd_b3_d64"])
-    assert not ((got != want) & ~amb).any()
+    O.check_codes(got, want, z["vectors"], z["R_d64_s7"], z["bnd_b3_d64"])
     own.save_tqix(str(tmp_path / "own.tqix"))
     back = TurboQuantIndex.load_tqix(str(tmp_path / "own.tqix"))
     assert torch.equal(back._packed_codes, own._packed_codes) and torch.equal(back._norms, own._norms)

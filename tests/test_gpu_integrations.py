@@ -41,7 +41,7 @@ def test_hf_update_returns_dequantized_history_plus_exact_new():
     _, _, codes = O.quantize_mse(x, 4, R, bnd)
     rows = layer.rows(False, 5).reshape(-1, 32).cpu().numpy()   # bit-plane rows
     got = O.unpack_codes(rows, 4, 64)
-    assert not ((got != codes) & ~O.code_margin(x, R, bnd)).any()
+    O.check_codes(got, codes, x, R, bnd)
     deq = O.dequantize_mse(rows, layer.kn[:, :, :5].reshape(-1).cpu().numpy(), 4, 64, R, cen)
     assert np.allclose(K[:, :, :5].reshape(-1, 64).cpu().numpy(), deq, rtol=1e-5, atol=1e-5)
     assert cache.get_seq_length(0) == 6 and cache.memory_bytes() == 2 * 2 * 6 * (32 + 16 + 8)
