@@ -507,6 +507,89 @@ def bench_e2e(args, extra):
     torch.cuda.empty_cache()
 
 
+def bench_cpu_configs(args, extra):
+    """CPU legs of BASELINE.md section 3 beside the GPU numbers of the same work:
+    configs[0] in full -- TurboQuantMSE 4-bit on 65,536 N(0,1) fp32 vectors (torch CPU
+    generator, seed 0), d = 128, R = make_rotation_matrix(128, 42), then 256 queries (the
+    generator's next draws), k = 10 -- quantized by this repo's C/OpenMP restatement of
+    csrc/cpu/quant_cpu.cpp:44-118 and searched by the reference's own core
+    (turboquant_core.cpp:407-514, built into oracle/_ref; the C port where that build is
+    absent); and configs[2]'s TurboQuantProd quantize (3-bit MSE + 1-bit QJL) on a
+    bounded sample of its 1M x 128 heavy-tailed vectors through the numpy restatement of
+    reference.py:392-469 (BLAS matmuls, the library's thread pool)."""
+    import numpy as np
+    import torch
+    from turboquant_kv import _lib
+    from turboquant_kv.codebook import lloyd_max_codebook, make_qjl_matrix, make_rotation_matrix
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cpu_libs
+    import tq_oracle
+
+    ops = _lib.ops()
+    cores = len(os.sched_getaffinity(0))
+    os.environ.setdefault("OMP_NUM_THREADS", str(cores))
+    if not cpu_libs.have_port():
+        log("cpu legs skipped: oracle/libtq_oracle_cpu.so is not built")
+        return
+    kind = "reference" if cpu_libs.have_ref() else "port"
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(65536, 128, generator=gen)
+    qs = torch.randn(256, 128, generator=gen)
+    R = make_rotation_matrix(128, 42)
+    bnd, cen = lloyd_max_codebook(4, 128)
+    xn, Rn, bn, cn, qn = (t.numpy() for t in (x, R, bnd, cen, qs))
+    cpu_libs.rotate_and_quantize(xn[:1024], Rn, bn, 4)  # warm the thread pool
+    t0 = time.perf_counter()
+    packed, norms = cpu_libs.rotate_and_quantize(xn, Rn, bn, 4)
+    tq = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    s_cpu, i_cpu = cpu_libs.search_packed(qn, packed, norms, Rn, cn, 4, 10, kind)
+    ts = time.perf_counter() - t0
+    # the same work on the GPU: quantize, then the 256-query scan over bit-plane rows
+    xg, Rg, bg, cg, qg = (t.cuda() for t in (x, R, bnd, cen, qs))
+    tgq = time_op(lambda: ops.quantize_mse_packed(xg, Rg, bg, 4), 20, 3)
+    pg, ng = ops.quantize_mse_packed(xg, Rg, bg, 4)
+    tgs = time_op(lambda: ops.ip_scan_topk(qg, pg, ng, cg, Rg, 4, 10), 20, 3)
+    _, i_gpu = ops.ip_scan_topk(qg, pg, ng, cg, Rg, 4, 10)
+    same = float((i_gpu.cpu().numpy() == i_cpu).mean())
+    extra["cpu_config0"] = {
+        "quantize_vectors_per_s": 65536 / tq, "search_queries_per_s": 256 / ts, "cores": cores,
+        "quantize": "port (C/OpenMP restatement of quant_cpu.cpp:44-118)",
+        "search": f"{kind} (turboquant_core.cpp search_packed, one query per OpenMP thread)",
+        "sample": "the whole config: 65,536 x 128 fp32 vectors, 256 queries, k = 10",
+        "gpu_quantize_vectors_per_s": 65536 / tgq * 1e3, "gpu_search_queries_per_s": 256 / tgs * 1e3,
+        "gpu_cpu_topk_id_agreement": same}
+    log(f"config 0 CPU ({cores} threads): quantize {65536 / tq / 1e6:.2f} M vec/s, search "
+        f"{256 / ts:.0f} q/s; GPU: {65536 / tgq * 1e3 / 1e6:.0f} M vec/s, {256 / tgs * 1e3:.0f} q/s")
+    # configs[2] prod quantize on a bounded sample (100k of its 1M rows)
+    n = 100_000
+    xc = np.clip(np.floor(np.abs(rs_normal(n, 128) * 40)), 0, 255).astype(np.float32)
+    S = make_qjl_matrix(128, 128, 42).numpy()
+    b3, c3 = (t.numpy() for t in lloyd_max_codebook(3, 128))
+    tq_oracle.quantize_prod(xc[:1000], 4, Rn, b3, c3, S)
+    t0 = time.perf_counter()
+    tq_oracle.quantize_prod(xc, 4, Rn, b3, c3, S)
+    tp = time.perf_counter() - t0
+    threads = cores
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=cores)
+    except ImportError:
+        pass
+    extra["cpu_config2_quantize_prod"] = {
+        "vectors_per_s": n / tp, "seconds": tp, "cores": threads, "kind": "port",
+        "sample": f"{n} of config 2's 1M x 128 heavy-tailed fp32 vectors (floor(|N(0,40)|) "
+                  "clipped to 255), prod 3+1 bit",
+        "note": "numpy restatement of reference.py:392-469 (BLAS matmuls)"}
+    log(f"config 2 prod quantize CPU ({threads} threads): {n / tp / 1e6:.2f} M vec/s")
+
+
+def rs_normal(n, d, seed=0):
+    import numpy as np
+    return np.random.RandomState(seed).randn(n, d)
+
+
 def cpu_baseline(db, budget_s=12.0):
     """The reference's C++ search_packed over the same 10M-row database, one query per
     OpenMP thread, enough rounds of queries for about `budget_s` seconds."""
@@ -598,6 +681,8 @@ def main():
         bench_formats(args, extra)
         bench_e2e(args, extra)
     cpu = None if args.no_cpu else cpu_baseline(scan["db4"])
+    if not args.no_cpu and not args.quick:
+        bench_cpu_configs(args, extra)
     ms, bytes_alg = scan["headline"]
     achieved = bytes_alg / ms / 1e6
     value = 1e3 / ms
