@@ -138,13 +138,25 @@ def bench_scan(args, extra):
     res["db4"] = (packed, norms, R, cen)  # bit-plane rows: the CPU reference's input
     if not args.quick:
         for bits in (3, 2):
+            # TurboQuantIndex keeps 2/3-bit d=128 rows as pair rows (same bytes per row):
+            # one table read of two precomputed products per pair of dims
             p3, n3, R3, c3, _ = make_db(N, d, bits)
-            t = time_op(lambda: ops.ip_scan_topk(q1, p3, n3, c3, R3, bits, k), 20, 3)
+            rows = ops.pack_pair_rows(p3, bits, d)
+            t_bp = time_op(lambda: ops.ip_scan_topk(q1, p3, n3, c3, R3, bits, k), 20, 3)
+            t = time_op(lambda: ops.ip_scan_topk_pair_rows(q1, rows, n3, c3, R3, bits, k), 30, 3)
             ba = N * (bits * 16 + 4)
             extra[f"scan_b{bits}_Q1"] = {"us_per_query": t * 1e3, "queries_per_s": 1e3 / t,
-                                         "GBps": ba / t / 1e6, "hbm_frac": ba / t / 1e6 / HBM_PEAK_GBS}
-            log(f"scan b={bits} Q=1: {t * 1e3:.1f} us, {ba / t / 1e6:.0f} GB/s")
-            del p3, n3
+                                         "GBps": ba / t / 1e6, "hbm_frac": ba / t / 1e6 / HBM_PEAK_GBS,
+                                         "layout": "pair rows (TurboQuantIndex storage)",
+                                         "bitplane_rows_us": t_bp * 1e3}
+            log(f"scan b={bits} Q=1: {t * 1e3:.1f} us, {ba / t / 1e6:.0f} GB/s "
+                f"(bit-plane rows {t_bp * 1e3:.1f} us)")
+            if bits == 3:
+                qq = queries(64, d, seed=2)
+                t64 = time_op(lambda: ops.ip_scan_topk_pair_rows(qq, rows, n3, c3, R3, bits, k), 3, 1)
+                extra["scan_b3_Q64"] = {"ms_per_batch": t64, "queries_per_s": 64 / t64 * 1e3,
+                                        "layout": "pair rows"}
+            del p3, n3, rows
     return res
 
 
@@ -634,6 +646,8 @@ def main():
                     help="only the prod-mode scan (10M x 128, 3+1 bit), e.g. for a profiler run")
     ap.add_argument("--e2e-only", action="store_true",
                     help="only the end-to-end greedy decode (configs[4])")
+    ap.add_argument("--scan-only", action="store_true",
+                    help="only the index scans (configs[1]: 4-, 3- and 2-bit), e.g. for a profiler run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (counter calibration)")
     args = ap.parse_args()
@@ -669,6 +683,11 @@ def main():
     if args.e2e_only:
         extra = {}
         bench_e2e(args, extra)
+        print(json.dumps(extra))
+        return
+    if args.scan_only:
+        extra = {}
+        bench_scan(args, extra)
         print(json.dumps(extra))
         return
     extra = {}

@@ -169,6 +169,38 @@ int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, i
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Pair rows: 2-, 3- or 4-bit codes arranged so one table index covers the codes of a pair
+ * of dims (2p, 2p+1), same bytes per row as the bit-plane rows (d * bits / 8), d = 64 or
+ * 128.  TurboQuantIndex keeps its MSE databases of those dims in this form.
+ *   4 bits: the pair layout above (byte p = code[2p] << 4 | code[2p+1]).
+ *   2 bits: byte b = code[4b] << 6 | code[4b+1] << 4 | code[4b+2] << 2 | code[4b+3]
+ *           (each nibble the index code[2p] << 2 | code[2p+1] of one pair).
+ *   3 bits: per 32 dims (16 pairs) 12 bytes = words X0, X1, X2: the low 6 bits of byte k
+ *           of X_i hold pair 4i + k's index code[2p] << 3 | code[2p+1]; pair 12 + k's
+ *           index bits 2i, 2i+1 sit in bits 6-7 of byte k of X_i.
+ * tq_pack_pair_rows / tq_unpack_pair_rows convert n rows from / to the reference's bit
+ * planes (reference.py:191-224).  tq_ip_scan_topk_pair_rows and
+ * tq_attention_scores_pair_rows are tq_ip_scan_topk / tq_attention_scores_packed over
+ * them, with identical scores and ids (2 and 3 bits: every pair's two products come from
+ * one per-query table, so no multiply per row; 4 bits: the pair-layout kernels).
+ * Workspace as tq_ip_scan_topk's; 2- and 3-bit calls take at most 65535 queries.
+ */
+int tq_pack_pair_rows(const uint8_t* packed, int64_t n, int32_t d, int32_t bit_width, uint8_t* rows,
+                      void* stream);
+int tq_unpack_pair_rows(const uint8_t* rows, int64_t n, int32_t d, int32_t bit_width, uint8_t* packed,
+                        void* stream);
+int tq_ip_scan_topk_pair_rows(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                              const uint8_t* rows, const float* norms, int64_t N,
+                              const float* centroids, const float* rotation, int32_t bit_width,
+                              int32_t k, float* out_scores, int64_t* out_ids, void* workspace,
+                              size_t workspace_bytes, void* stream);
+int tq_attention_scores_pair_rows(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                  const uint8_t* rows, const float* key_norms, int64_t T,
+                                  const float* centroids, const float* rotation, int32_t bit_width,
+                                  float* scores, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/*
  * tq_ip_scan_topk_pairs without a workspace argument.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops that forbid hipMalloc).  The candidate lists live in a static device

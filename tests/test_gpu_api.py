@@ -190,7 +190,7 @@ def test_tqix_index_from_reference_core_file(golden, tmp_path):
     # fp32 ambiguity band (its quantize multiplies by 1/norm), and TQIX round-trips
     own = TurboQuantIndex(64, bit_width=3, rotation="core", seed=7)
     own.add(T(z["vectors"]))
-    got = O.unpack_codes(own._packed_codes.cpu().numpy(), 3, 64)
+    got = O.unpack_codes(own._bitplane_codes().cpu().numpy(), 3, 64)
     want = O.unpack_codes(open_tqix_codes(src), 3, 64)
     O.check_codes(got, want, z["vectors"], z["R_d64_s7"], z["bnd_b3_d64"])
     own.save_tqix(str(tmp_path / "own.tqix"))

@@ -421,7 +421,98 @@ def test_scan_topk_bit_exact(d, b):
         assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
 
 
-@pytest.mark.parametrize("b,layout", [(4, "pairs"), (4, "bitplane"), (3, "bitplane"), (2, "bitplane")])
+def pair_rows_np(codes, bits):
+    """Independent numpy packing of codes [N, d] into pair rows (include/turboquant_hip.h):
+    2 bits: byte b = c[4b] << 6 | c[4b+1] << 4 | c[4b+2] << 2 | c[4b+3]; 3 bits: per 32 dims
+    12 bytes, byte 4i + k = pair (4i + k)'s index c[2p] << 3 | c[2p+1] in bits 0-5 and bits
+    2i, 2i+1 of pair (12 + k)'s index in bits 6-7; 4 bits: byte p = c[2p] << 4 | c[2p+1]."""
+    c = codes.astype(np.uint32)
+    N, d = c.shape
+    if bits == 4:
+        return ((c[:, 0::2] << 4) | c[:, 1::2]).astype(np.uint8)
+    if bits == 2:
+        return ((c[:, 0::4] << 6) | (c[:, 1::4] << 4) | (c[:, 2::4] << 2) | c[:, 3::4]).astype(np.uint8)
+    idx = (c[:, 0::2] << 3) | c[:, 1::2]                     # [N, d/2] pair indices
+    out = np.zeros((N, d * 3 // 8), np.uint32)
+    for t in range(d // 32):
+        for i in range(3):
+            for k in range(4):
+                lo = idx[:, 16 * t + 4 * i + k]
+                hi = idx[:, 16 * t + 12 + k]
+                out[:, 12 * t + 4 * i + k] = lo | (((hi >> (2 * i)) & 3) << 6)
+    return out.astype(np.uint8)
+
+
+def k_pair_rows(packed, d, bits):
+    N = packed.shape[0]
+    out = torch.zeros(max(N, 1), d * bits // 8, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_pack_pair_rows(capi.p(T(packed)), capi.i64(N), capi.i32(d), capi.i32(bits),
+                                     capi.p(out), capi.stream()))
+    sync()
+    return out[:N]
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("d", [64, 128])
+def test_pair_rows_pack_roundtrip(bits, d):
+    rs = np.random.RandomState(60 + 7 * bits + d)
+    codes = rs.randint(0, 1 << bits, (333, d))
+    packed = O.pack_codes(codes, bits)
+    rows = k_pair_rows(packed, d, bits)
+    assert np.array_equal(rows.cpu().numpy(), pair_rows_np(codes, bits))
+    back = torch.empty(333, bits * d // 8, dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_unpack_pair_rows(capi.p(rows), capi.i64(333), capi.i32(d), capi.i32(bits),
+                                       capi.p(back), capi.stream()))
+    sync()
+    assert np.array_equal(back.cpu().numpy(), packed)
+    if bits == 3:  # a planted mistake in the numpy packing (pairs 12-15 dropped) fails
+        bad = codes.copy()
+        bad[:, 24:32] = 0
+        assert not np.array_equal(rows.cpu().numpy(), pair_rows_np(bad, bits))
+
+
+def k_scan_pair_rows(q, rows, norms, cen, R, bits, k, q_dt=capi.TQ_F32):
+    Q, d = q.shape
+    N = rows.shape[0]
+    os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
+    oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, bits, N, k), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_ip_scan_topk_pair_rows(capi.p(T(q)), q_dt, capi.i64(Q), capi.i32(d), capi.p(rows),
+                                             capi.p(T(norms)), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
+                                             capi.i32(bits), capi.i32(k), capi.p(os_), capi.p(oi),
+                                             capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    return os_.cpu().numpy(), oi.cpu().numpy()
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("d", [64, 128])
+def test_pair_rows_scan_bit_exact(bits, d):
+    # ragged N; one, several and many queries (one query per block row at 2-3 bits)
+    rs = np.random.RandomState(80 + 7 * bits + d)
+    N = 20000 + 37
+    R, cen, p, nm = _db(rs, N, d, bits)
+    rows = k_pair_rows(p, d, bits)
+    for Q, k in ((1, 10), (4, 1), (9, 32)):
+        q = rs.randn(Q, d).astype(np.float32)
+        s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k)
+        so, io = O.search_topk(q, p, nm, cen, R, bits, k)
+        assert np.array_equal(i, io), (Q, k)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    q = rs.randn(3, d).astype(np.float32)
+    out = torch.empty(3, 1500, dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(L().tq_scan_workspace_bytes(3, d, bits, 1500, 0), 1), dtype=torch.uint8, device=DEV)
+    capi.check(L().tq_attention_scores_pair_rows(capi.p(T(q)), capi.TQ_F32, capi.i64(3), capi.i32(d),
+                                                 capi.p(rows), capi.p(T(nm[:1500])), capi.i64(1500),
+                                                 capi.p(T(cen)), capi.p(T(R)), capi.i32(bits), capi.p(out),
+                                                 capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    sync()
+    want = O.lut_scores_f32(q, p[:1500], nm[:1500], cen, R, bits)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("b,layout", [(4, "pairs"), (4, "bitplane"), (3, "bitplane"), (2, "bitplane"),
+                                      (3, "pairs"), (2, "pairs")])
 def test_scan_q64_batch_vs_oracle(b, layout):
     # A config-2 query batch (64 normalized fp16 queries, k = 10) over N = 100,003 unit
     # rows: the multi-query scan (four queries per block) must return the oracle's ids
@@ -436,8 +527,10 @@ def test_scan_q64_batch_vs_oracle(b, layout):
     qf = rs.randn(64, d).astype(np.float32)
     qf /= np.linalg.norm(qf, axis=1, keepdims=True)
     q16 = qf.astype(np.float16)
-    if layout == "pairs":
+    if layout == "pairs" and b == 4:
         s, i = k_scan_pairs(q16, k_pack_pairs(p, d), nm, cen, R, 10, q_dt=capi.TQ_F16)
+    elif layout == "pairs":
+        s, i = k_scan_pair_rows(q16, k_pair_rows(p, d, b), nm, cen, R, b, 10, q_dt=capi.TQ_F16)
     else:
         s, i = k_scan(q16, p, nm, cen, R, b, 10, q_dt=capi.TQ_F16)
     so, io = O.search_topk(q16.astype(np.float32), p, nm, cen, R, b, 10)

@@ -462,6 +462,94 @@ at::Tensor attention_scores_prod(const at::Tensor& query, const at::Tensor& mse_
   return scores;
 }
 
+// Pair rows of 2-4 bit codes (d * bits / 8 bytes per row, d = 64 or 128): conversion
+// from / to bit-plane rows and the top-k scan over them.
+at::Tensor pack_pair_rows(const at::Tensor& packed, int64_t bit_width, int64_t dim) {
+  require_gpu(packed, "packed");
+  c10::DeviceGuard g(packed.device());
+  auto pk = packed.contiguous();
+  TORCH_CHECK(pk.dim() == 2 && pk.scalar_type() == at::kByte && pk.size(1) == packed_width(bit_width, dim),
+              "packed must be uint8 [n, bits * ceil(dim / 8)]");
+  auto rows = at::empty({pk.size(0), dim * bit_width / 8}, pk.options());
+  check_rc(tq_pack_pair_rows(pk.data_ptr<uint8_t>(), pk.size(0), (int32_t)dim, (int32_t)bit_width,
+                             rows.data_ptr<uint8_t>(), cur_stream(pk)));
+  return rows;
+}
+
+at::Tensor unpack_pair_rows(const at::Tensor& rows, int64_t bit_width, int64_t dim) {
+  require_gpu(rows, "rows");
+  c10::DeviceGuard g(rows.device());
+  auto r = rows.contiguous();
+  TORCH_CHECK(r.dim() == 2 && r.scalar_type() == at::kByte && r.size(1) * 8 == dim * bit_width,
+              "rows must be uint8 [n, dim * bits / 8]");
+  auto out = at::empty({r.size(0), packed_width(bit_width, dim)}, r.options());
+  check_rc(tq_unpack_pair_rows(r.data_ptr<uint8_t>(), r.size(0), (int32_t)dim, (int32_t)bit_width,
+                               out.data_ptr<uint8_t>(), cur_stream(r)));
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_pair_rows(const at::Tensor& queries,
+                                                          const at::Tensor& rows,
+                                                          const at::Tensor& norms,
+                                                          const at::Tensor& centroids,
+                                                          const at::Tensor& rotation,
+                                                          int64_t bit_width, int64_t k) {
+  require_gpu(queries, "queries");
+  TORCH_CHECK(queries.dim() == 2, "queries must be [Q, d]");
+  TORCH_CHECK(rows.dim() == 2 && rows.scalar_type() == at::kByte, "rows must be uint8 [N, d * bits / 8]");
+  c10::DeviceGuard g(queries.device());
+  const auto dev = queries.device();
+  auto q = floatc(queries, dev);
+  auto p = rows.to(dev).contiguous();
+  auto nm = f32c(norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t Q = q.size(0), d = q.size(1), N = p.size(0);
+  TORCH_CHECK(p.size(1) * 8 == d * bit_width, "rows must hold d * bits / 8 bytes");
+  TORCH_CHECK(nm.numel() == N, "norms must have N entries");
+  TORCH_CHECK(cen.numel() == (int64_t(1) << bit_width), "centroids must have 2^bits entries");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
+  auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
+  if (Q == 0) return {os, oi};
+  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
+  check_rc(tq_ip_scan_topk_pair_rows(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
+                                     p.data_ptr<uint8_t>(), nm.data_ptr<float>(), N,
+                                     cen.data_ptr<float>(), R.data_ptr<float>(), (int32_t)bit_width,
+                                     (int32_t)k, os.data_ptr<float>(), oi.data_ptr<int64_t>(),
+                                     ws.data_ptr(), ws.numel(), cur_stream(q)));
+  return {os, oi};
+}
+
+at::Tensor attention_scores_pair_rows(const at::Tensor& query, const at::Tensor& rows,
+                                      const at::Tensor& key_norms, const at::Tensor& centroids,
+                                      const at::Tensor& rotation, int64_t bit_width) {
+  require_gpu(query, "query");
+  TORCH_CHECK(query.dim() == 3, "query must be [batch, heads, head_dim]");
+  TORCH_CHECK(rows.dim() == 2 && rows.scalar_type() == at::kByte, "rows must be uint8 [T, d * bits / 8]");
+  c10::DeviceGuard g(query.device());
+  const auto dev = query.device();
+  auto q = f32c(query, dev);
+  auto pk = rows.to(dev).contiguous();
+  auto kn = f32c(key_norms, dev);
+  auto cen = f32c(centroids, dev);
+  auto R = f32c(rotation, dev);
+  const int64_t B = q.size(0), H = q.size(1), d = q.size(2), T = pk.size(0);
+  TORCH_CHECK(pk.size(1) * 8 == d * bit_width, "rows must hold d * bits / 8 bytes");
+  TORCH_CHECK(kn.numel() == T, "key_norms must have seq_len entries");
+  TORCH_CHECK(cen.numel() == (int64_t(1) << bit_width), "centroids must have 2^bits entries");
+  TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+  auto scores = at::empty({B, H, T}, q.options());
+  if (B * H == 0 || T == 0) return scores;
+  auto ws = workspace(tq_scan_workspace_bytes(B * H, (int32_t)d, (int32_t)bit_width, T, 0), dev);
+  check_rc(tq_attention_scores_pair_rows(q.data_ptr(), TQ_F32, B * H, (int32_t)d,
+                                         pk.data_ptr<uint8_t>(), kn.data_ptr<float>(), T,
+                                         cen.data_ptr<float>(), R.data_ptr<float>(),
+                                         (int32_t)bit_width, scores.data_ptr<float>(),
+                                         ws.data_ptr(), ws.numel(), cur_stream(q)));
+  return scores;
+}
+
 at::Tensor attention_scores_pairs(const at::Tensor& query, const at::Tensor& pairs,
                                   const at::Tensor& key_norms, const at::Tensor& centroids,
                                   const at::Tensor& rotation) {
@@ -951,6 +1039,12 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor rotation, int k) -> (Tensor, Tensor)");
   m.def("attention_scores_pairs(Tensor query, Tensor pairs, Tensor key_norms, Tensor centroids,"
         " Tensor rotation) -> Tensor");
+  m.def("pack_pair_rows(Tensor packed, int bit_width, int dim) -> Tensor");
+  m.def("unpack_pair_rows(Tensor rows, int bit_width, int dim) -> Tensor");
+  m.def("ip_scan_topk_pair_rows(Tensor queries, Tensor rows, Tensor norms, Tensor centroids,"
+        " Tensor rotation, int bit_width, int k) -> (Tensor, Tensor)");
+  m.def("attention_scores_pair_rows(Tensor query, Tensor rows, Tensor key_norms, Tensor centroids,"
+        " Tensor rotation, int bit_width) -> Tensor");
   // host-side tables (no tensor arguments: registered with catch-all kernels)
   m.def("core_rotation(int dim, int seed) -> Tensor", &core_rotation);
   m.def("core_codebook(int bits, int dim) -> (Tensor, Tensor)", &core_codebook);
@@ -1008,6 +1102,10 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("ip_scan_topk", &ip_scan_topk);
   m.impl("ip_scan_topk_pairs", &ip_scan_topk_pairs);
   m.impl("attention_scores_pairs", &attention_scores_pairs);
+  m.impl("pack_pair_rows", &pack_pair_rows);
+  m.impl("unpack_pair_rows", &unpack_pair_rows);
+  m.impl("ip_scan_topk_pair_rows", &ip_scan_topk_pair_rows);
+  m.impl("attention_scores_pair_rows", &attention_scores_pair_rows);
   m.impl("ip_scan_topk_prod", &ip_scan_topk_prod);
   m.impl("paged_store", &paged_store);
   m.impl("paged_gather", &paged_gather);

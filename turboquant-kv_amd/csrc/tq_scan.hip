@@ -674,6 +674,61 @@ __device__ __forceinline__ float pair_row(const uint32_t* wds, uint32_t copy8, c
   return acc;
 }
 
+// ------------------------------------------------------------------ 2- and 3-bit pair rows
+// Rows of 2- or 3-bit codes where each table index covers the two codes of a pair of dims
+// (2p, 2p + 1): index = code[2p] << BITS | code[2p + 1].  Bytes per row = the bit-plane
+// row's (d * BITS / 8).
+//   2 bits: byte b = the indices of pairs 2b (high nibble) and 2b + 1 (low nibble).
+//   3 bits: per 32 dims (16 pairs) 12 bytes = words X0, X1, X2: the low 6 bits of byte k of
+//           X_i hold pair 4i + k; pair 12 + k's index is spread over bits 6-7 of byte k of
+//           X0 (index bits 0-1), X1 (bits 2-3) and X2 (bits 4-5).
+// The block's table holds, per pair, every index's two products (fl(q_rot[2p] * c[hi]),
+// fl(q_rot[2p + 1] * c[lo])) -- the reference's per-dim LUT values
+// (csrc/core/turboquant_core.cpp:440-446) -- so a row costs one 8-byte read and two adds
+// (in dim order) per pair and no multiply.  Lanes reading one pair's table touch at most
+// 2^(2 BITS) distinct 8-byte entries: conflict-free at 2 bits, near it at 3.
+template <int BITS>
+constexpr int pmp_pair_bytes() { return (1 << (2 * BITS)) * 8; }
+
+// Pairs [P0, P0 + 16) from words X0..X2 (3 bits) or 16 pairs from two words (2 bits),
+// added in pair order.
+template <int BITS, int D>
+__device__ __forceinline__ float pmp_row(const uint32_t* w, const char* ctab) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+  if constexpr (BITS == 2) {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) {
+      decode_pairs<8>(w[i], 8 * i, [&](int p, uint32_t addr) {
+        const float2 e = *reinterpret_cast<const float2*>(ctab + p * pmp_pair_bytes<2>() + addr);
+        acc = acc + e.x;
+        acc = acc + e.y;
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) {
+      const uint32_t X[4] = {w[3 * t], w[3 * t + 1], w[3 * t + 2],
+                             ((w[3 * t] >> 6) & 0x03030303u) | ((w[3 * t + 1] >> 4) & 0x0C0C0C0Cu) |
+                                 ((w[3 * t + 2] >> 2) & 0x30303030u)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int p = 16 * t + 4 * i + k;
+          const uint32_t idx = __builtin_amdgcn_ubfe(X[i], 8 * k, 6);
+          const float2 e = *reinterpret_cast<const float2*>(ctab + p * pmp_pair_bytes<3>() + idx * 8);
+          acc = acc + e.x;
+          acc = acc + e.y;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  return acc;
+}
+
 // Bitonic sort of one (score, id) per lane over the 64 lanes, best first (score desc, id
 // asc).  Pads are (-inf, INT_MAX): every entry is better than a pad.
 __device__ __forceinline__ void wave_sort64(float& s, int& id) {
@@ -744,15 +799,19 @@ __device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count
   }
 }
 
-template <int D, bool TOPK>
+// BITS 4: the pair layout with the centroid-pair table and register products above; BITS 2,
+// 3: pair rows with the per-block table of products (pmp_row).
+template <int D, bool TOPK, int BITS = 4>
 __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
   static_assert(D == 64 || D == 128, "pair scan dims");
-  constexpr int RB = D / 2;   // bytes per row
-  constexpr int NW = RB / 4;  // 32-bit words per row
-  constexpr int NQ = D / 16;  // q_rot registers
-  static_assert(RB % kPairGroup == 0, "whole byte groups per row");
-  __shared__ __attribute__((aligned(16))) char ctab[kCtabBytes];
+  static_assert(BITS >= 2 && BITS <= 4, "pair rows of 2-4 bit codes");
+  constexpr int RB = D * BITS / 8;  // bytes per row
+  constexpr int NW = RB / 4;        // 32-bit words per row
+  constexpr int NQ = D / 16;        // q_rot registers
+  static_assert(BITS != 4 || RB % kPairGroup == 0, "whole byte groups per row");
+  constexpr int CT = BITS == 4 ? kCtabBytes : (D / 2) * pmp_pair_bytes<BITS>();
+  __shared__ __attribute__((aligned(16))) char ctab[CT];
   __shared__ float qs_s[D];
   __shared__ float qr_s[D];
   __shared__ float cen_s[16];
@@ -784,12 +843,23 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
     }
     qr_s[tid] = v;
   }
-  for (int e = tid; e < 256 * 16; e += kPsThreads) {  // entry b, copies 2c and 2c + 1
-    const int b = e >> 4, c = e & 15;
-    const float hi = cen_s[b >> 4], lo = cen_s[b & 15];
-    *reinterpret_cast<float4*>(ctab + b * 256 + c * 16) = make_float4(hi, lo, hi, lo);
+  if constexpr (BITS == 4) {
+    for (int e = tid; e < 256 * 16; e += kPsThreads) {  // entry b, copies 2c and 2c + 1
+      const int b = e >> 4, c = e & 15;
+      const float hi = cen_s[b >> 4], lo = cen_s[b & 15];
+      *reinterpret_cast<float4*>(ctab + b * 256 + c * 16) = make_float4(hi, lo, hi, lo);
+    }
   }
   __syncthreads();
+  if constexpr (BITS != 4) {  // products of pair p, index i (i = hi << BITS | lo)
+    constexpr int L = 1 << BITS;
+    for (int e = tid; e < (D / 2) * L * L; e += kPsThreads) {
+      const int pp = e / (L * L), i = e - pp * (L * L);
+      *reinterpret_cast<float2*>(ctab + e * 8) =
+          make_float2(qr_s[2 * pp] * cen_s[i >> BITS], qr_s[2 * pp + 1] * cen_s[i & (L - 1)]);
+    }
+    __syncthreads();
+  }
   float qv[NQ];
 #pragma unroll
   for (int m = 0; m < NQ; ++m) qv[m] = qr_s[16 * m + (lane & 15)];
@@ -827,15 +897,24 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
       const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows_rs, off, 16 * i, 0);
       b.w[4 * i + 0] = v.x; b.w[4 * i + 1] = v.y; b.w[4 * i + 2] = v.z; b.w[4 * i + 3] = v.w;
     }
+    if constexpr (RB % 16 == 8) {  // 3-bit rows of 64 dims: 24 bytes
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rows_rs, off, RB - 8, 0);
+      b.w[NW - 2] = v.x; b.w[NW - 1] = v.y;
+    }
     b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
   };
 
   auto score = [&](const RowBuf& rb) {
-    // The broadcasts of qv are loop-invariant: hoisted, each would hold a register of its
-    // own (128 for d = 128).  Redefining qv here keeps them inside the multiplies.
+    float acc;
+    if constexpr (BITS == 4) {
+      // The broadcasts of qv are loop-invariant: hoisted, each would hold a register of its
+      // own (128 for d = 128).  Redefining qv here keeps them inside the multiplies.
 #pragma unroll
-    for (int m = 0; m < NQ; ++m) asm volatile("" : "+v"(qv[m]));
-    const float acc = pair_row<NQ>(rb.w, copy8, ctab, qv, std::make_integer_sequence<int, RB / kPairGroup>{});
+      for (int m = 0; m < NQ; ++m) asm volatile("" : "+v"(qv[m]));
+      acc = pair_row<NQ>(rb.w, copy8, ctab, qv, std::make_integer_sequence<int, RB / kPairGroup>{});
+    } else {
+      acc = pmp_row<BITS, D>(rb.w, ctab);
+    }
     float sc = acc * rb.n * a.post_scale;
     // materialized here: sunk into a branch that uses it, the products would be split
     // from their broadcasts (a DPP move cannot move into divergent code)
@@ -1510,12 +1589,19 @@ int pair_scan_blocks(int64_t nrows) {
   return b < 1 ? 1 : b;
 }
 
-template <bool TOPK>
-int launch_pair_scan(const ScanArgs& a, dim3 grid, hipStream_t st) {
-  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK>), grid, dim3(kPsThreads), 0, st, a);
-  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK>), grid, dim3(kPsThreads), 0, st, a);
+template <bool TOPK, int BITS>
+int launch_pair_scan_b(const ScanArgs& a, dim3 grid, hipStream_t st) {
+  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK, BITS>), grid, dim3(kPsThreads), 0, st, a);
+  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK, BITS>), grid, dim3(kPsThreads), 0, st, a);
   TQ_LAUNCH_CHECK("pair_scan_kernel");
   return TQ_OK;
+}
+
+template <bool TOPK>
+int launch_pair_scan(const ScanArgs& a, dim3 grid, hipStream_t st, int bits = 4) {
+  if (bits == 2) return launch_pair_scan_b<TOPK, 2>(a, grid, st);
+  if (bits == 3) return launch_pair_scan_b<TOPK, 3>(a, grid, st);
+  return launch_pair_scan_b<TOPK, 4>(a, grid, st);
 }
 
 // *nblocks_out: the grid's row blocks (TOPK: the lists merge_kernel reads per query).
@@ -1524,6 +1610,8 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   const bool aligned = fast_aligned(a);
   int qb = queries_per_block(a);
   if (!aligned && qb > 2) qb = 2;
+  // 2- and 3-bit pair rows: one query per block row of the pair scan, at any query count
+  if (pairs && bits != 4) qb = 1;
   const int64_t rows_hint = a.seq_lens ? a.stream_rows : a.nrows;
   const bool pair1 = pairs && qb == 1;
   dim3 grid(pair1 ? (unsigned)pair_scan_blocks(rows_hint) : (unsigned)scan_blocks(rows_hint),
@@ -1534,9 +1622,9 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   if (per_block * (int64_t)(bits * a.bpp) >= ((int64_t)1 << 32))
     return fail(TQ_EINVAL, "too many rows per scan block");
   if (pairs) {
-    if (bits != 4 || !aligned || (a.bpp != 8 && a.bpp != 16))
-      return fail(TQ_EINVAL, "pair-layout scan needs 4-bit codes, dim 64 or 128 and a 16-byte aligned base");
-    if (pair1) return topk ? launch_pair_scan<true>(a, grid, st) : launch_pair_scan<false>(a, grid, st);
+    if (bits < 2 || bits > 4 || !aligned || (a.bpp != 8 && a.bpp != 16))
+      return fail(TQ_EINVAL, "pair-row scan needs 2-4 bit codes, dim 64 or 128 and a 16-byte aligned base");
+    if (pair1) return topk ? launch_pair_scan<true>(a, grid, st, bits) : launch_pair_scan<false>(a, grid, st, bits);
     return topk ? launch_scan_pairs<true>(a, qb, grid, st) : launch_scan_pairs<false>(a, qb, grid, st);
   }
   if (a.signs) {
@@ -1624,6 +1712,7 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.out_s = out_scores; a.out_i = out_ids;
   if (prod) set_prod(a, *prod);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
+  TQ_REQUIRE(!pairs || bit_width == 4 || nq <= 65535, "too many queries in one call");
   int nb = 0;
   const int rc = launch_scan(a, prod ? bit_width - 1 : bit_width, true, 1, st, pairs, &nb);
   if (rc != TQ_OK) return rc;
@@ -1658,6 +1747,7 @@ int attention_scores(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.k = 0; a.scores = scores;
   if (prod) set_prod(a, *prod);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
+  TQ_REQUIRE(!pairs || bit_width == 4 || nq <= 65535, "too many queries in one call");
   return launch_scan(a, prod ? bit_width - 1 : bit_width, false, 1, st, pairs);
 }
 
@@ -1839,6 +1929,144 @@ int tq_decode_attention_packed(const void* q, tq_dtype q_dtype, int32_t B, int32
                      seq_lens, hq, (int)q_dtype, out, t_max > 0 ? stats : nullptr, lse);
   TQ_LAUNCH_CHECK("combine_kernel");
   return TQ_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ pair rows <-> bit planes
+namespace tq {
+namespace {
+
+// Code of dim j in a bit-plane row (reference.py:191-224 layout).
+__device__ __forceinline__ uint32_t plane_code(const uint8_t* row, int bpp, int bits, int j) {
+  uint32_t c = 0;
+  for (int p = 0; p < bits; ++p) c |= ((row[p * bpp + (j >> 3)] >> (7 - (j & 7))) & 1u) << p;
+  return c;
+}
+
+// Code of dim j in a pair row of d dims (layout above pmp_row; 4 bits: byte j/2, high
+// nibble for even j).
+__device__ __forceinline__ uint32_t pair_row_code(const uint8_t* row, int bits, int j) {
+  if (bits == 4) return (j & 1) ? (row[j >> 1] & 15u) : (row[j >> 1] >> 4);
+  if (bits == 2) return (row[j >> 2] >> (6 - 2 * (j & 3))) & 3u;
+  const int pp = j >> 1, t = pp >> 4, q = pp & 15;
+  uint32_t idx;
+  if (q < 12) {
+    idx = row[12 * t + q] & 63u;
+  } else {
+    idx = 0;
+    for (int i = 0; i < 3; ++i) idx |= (uint32_t)((row[12 * t + 4 * i + (q - 12)] >> 6) & 3) << (2 * i);
+  }
+  return (j & 1) ? (idx & 7u) : (idx >> 3);
+}
+
+// One thread per output byte of the pair rows.
+__global__ void pack_pair_rows_kernel(const uint8_t* __restrict__ packed, int64_t n, int d, int bits,
+                                      uint8_t* __restrict__ rows) {
+  const int bpp = (d + 7) / 8, P = bits * bpp, RB = d * bits / 8;
+  const int64_t total = n * RB;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / RB;
+    const int b = (int)(e - r * RB);
+    const uint8_t* src = packed + r * P;
+    uint32_t v;
+    if (bits == 4) {
+      v = plane_code(src, bpp, 4, 2 * b) << 4 | plane_code(src, bpp, 4, 2 * b + 1);
+    } else if (bits == 2) {
+      v = 0;
+      for (int k = 0; k < 4; ++k) v |= plane_code(src, bpp, 2, 4 * b + k) << (6 - 2 * k);
+    } else {
+      const int t = b / 12, q = b - 12 * t, i = q >> 2, k = q & 3;
+      const int plo = 16 * t + q, phi = 16 * t + 12 + k;
+      const uint32_t ilo = plane_code(src, bpp, 3, 2 * plo) << 3 | plane_code(src, bpp, 3, 2 * plo + 1);
+      const uint32_t ihi = plane_code(src, bpp, 3, 2 * phi) << 3 | plane_code(src, bpp, 3, 2 * phi + 1);
+      v = ilo | ((ihi >> (2 * i)) & 3u) << 6;
+    }
+    rows[e] = (uint8_t)v;
+  }
+}
+
+// One thread per output byte of the bit-plane rows.
+__global__ void unpack_pair_rows_kernel(const uint8_t* __restrict__ rows, int64_t n, int d, int bits,
+                                        uint8_t* __restrict__ packed) {
+  const int bpp = (d + 7) / 8, P = bits * bpp, RB = d * bits / 8;
+  const int64_t total = n * P;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / P;
+    const int byte = (int)(e - r * P), pl = byte / bpp, o = byte - pl * bpp;
+    uint32_t out = 0;
+    for (int k = 0; k < 8 && 8 * o + k < d; ++k)
+      out |= ((pair_row_code(rows + r * RB, bits, 8 * o + k) >> pl) & 1u) << (7 - k);
+    packed[e] = (uint8_t)out;
+  }
+}
+
+int check_pair_rows(int64_t n, int32_t d, int32_t bits) {
+  TQ_REQUIRE(d == 64 || d == 128, "pair rows need dim 64 or 128, got %d", d);
+  TQ_REQUIRE(bits >= 2 && bits <= 4, "pair rows hold 2-4 bit codes, got %d", bits);
+  TQ_REQUIRE(n >= 0, "bad sizes");
+  return TQ_OK;
+}
+
+}  // namespace
+}  // namespace tq
+
+extern "C" {
+
+int tq_pack_pair_rows(const uint8_t* packed, int64_t n, int32_t d, int32_t bit_width, uint8_t* rows,
+                      void* stream) {
+  const int rc = check_pair_rows(n, d, bit_width);
+  if (rc != TQ_OK) return rc;
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(packed && rows, "null pointer argument");
+  const int64_t total = n * d * bit_width / 8;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(pack_pair_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     packed, n, (int)d, (int)bit_width, rows);
+  TQ_LAUNCH_CHECK("pack_pair_rows_kernel");
+  return TQ_OK;
+}
+
+int tq_unpack_pair_rows(const uint8_t* rows, int64_t n, int32_t d, int32_t bit_width, uint8_t* packed,
+                        void* stream) {
+  const int rc = check_pair_rows(n, d, bit_width);
+  if (rc != TQ_OK) return rc;
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(packed && rows, "null pointer argument");
+  const int64_t total = n * bit_width * ((d + 7) / 8);
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
+  hipLaunchKernelGGL(unpack_pair_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     rows, n, (int)d, (int)bit_width, packed);
+  TQ_LAUNCH_CHECK("unpack_pair_rows_kernel");
+  return TQ_OK;
+}
+
+int tq_ip_scan_topk_pair_rows(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                              const uint8_t* rows, const float* norms, int64_t N,
+                              const float* centroids, const float* rotation, int32_t bit_width,
+                              int32_t k, float* out_scores, int64_t* out_ids, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const int rc = check_pair_rows(N, d, bit_width);
+  if (rc != TQ_OK) return rc;
+  TQ_REQUIRE(N == 0 || (reinterpret_cast<uintptr_t>(rows) & 15u) == 0,
+             "pair rows must be 16-byte aligned");
+  return ip_scan_topk(queries, q_dtype, nq, d, rows, norms, N, centroids, rotation, bit_width, k,
+                      out_scores, out_ids, workspace, workspace_bytes, stream, true);
+}
+
+int tq_attention_scores_pair_rows(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                  const uint8_t* rows, const float* key_norms, int64_t T,
+                                  const float* centroids, const float* rotation, int32_t bit_width,
+                                  float* scores, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const int rc = check_pair_rows(T, d, bit_width);
+  if (rc != TQ_OK) return rc;
+  TQ_REQUIRE(T == 0 || (reinterpret_cast<uintptr_t>(rows) & 15u) == 0,
+             "pair rows must be 16-byte aligned");
+  return attention_scores(query, q_dtype, nq, d, rows, key_norms, T, centroids, rotation, bit_width,
+                          scores, workspace, workspace_bytes, stream, true);
 }
 
 }  // extern "C"

@@ -66,6 +66,31 @@ def attention_scores_pairs(query, pairs, key_norms, centroids, rotation):
     return _ops().attention_scores_pairs(query, pairs, key_norms, centroids, rotation)
 
 
+def pack_pair_rows(packed, bit_width, dim):
+    """Bit-plane rows [n, bits*ceil(d/8)] -> pair rows [n, d*bits/8] (2-4 bits, d 64/128):
+    one table index per pair of dims (layout in include/turboquant_hip.h)."""
+    _require_device(packed, "packed")
+    return _ops().pack_pair_rows(packed, bit_width, dim)
+
+
+def unpack_pair_rows(rows, bit_width, dim):
+    """Pair rows back to the reference's bit-plane rows (reference.py:191-224)."""
+    _require_device(rows, "rows")
+    return _ops().unpack_pair_rows(rows, bit_width, dim)
+
+
+def ip_scan_topk_pair_rows(queries, rows, norms, centroids, rotation, bit_width, k):
+    """ip_scan_topk over pair rows: identical scores and ids."""
+    _require_device(queries, "queries")
+    return _ops().ip_scan_topk_pair_rows(queries, rows, norms, centroids, rotation, bit_width, k)
+
+
+def attention_scores_pair_rows(query, rows, key_norms, centroids, rotation, bit_width):
+    """attention_scores_packed over pair rows: identical scores."""
+    _require_device(query, "query")
+    return _ops().attention_scores_pair_rows(query, rows, key_norms, centroids, rotation, bit_width)
+
+
 def ip_scan_topk_prod(queries, mse_packed, signs, res_norms, norms, centroids, rotation, qjl,
                       bit_width, k):
     """Top-k of <q, dequantize_prod(row)> (search.py:229-252) scored from the packed rows:

@@ -69,8 +69,9 @@ class TurboQuantIndex:
             self._code_bits = bit_width - 1
             self._S_matrix = make_qjl_matrix(dim, dim, seed)
             self._S_dev = self._S_matrix.to(self.device)
-        # 4-bit MSE rows of 64/128 dims live in the pair layout (same row width).
-        self._pairs = mode == "mse" and bit_width == 4 and dim in (64, 128)
+        # 2-4 bit MSE rows of 64/128 dims live as pair rows (same row width): one table
+        # read per pair of dims in the scan.
+        self._pairs = mode == "mse" and 2 <= bit_width <= 4 and dim in (64, 128)
         self._bnd = self._codebook[0].to(self.device)
         self._cen = self._codebook[1].to(self.device)
         self.n_vectors = 0
@@ -89,14 +90,13 @@ class TurboQuantIndex:
         """The database rows in the reference's bit-plane format [n, b*ceil(d/8)]."""
         if self._packed_buf is None or not self._pairs:
             return self._packed_codes
-        return ops.unpack_decode_layout(self._packed_buf.unsqueeze(0), self.dim, 4, False, 0,
-                                        self.n_vectors)[0]
+        return ops.unpack_pair_rows(self._packed_codes, self.bit_width, self.dim)
 
     def _store_codes(self, packed: torch.Tensor, pos: int) -> None:
         """Write bit-plane rows at rows pos.. of the database buffer."""
         if self._pairs:
-            ops.pack_decode_layout(packed.unsqueeze(0), self._packed_buf.unsqueeze(0), self.dim,
-                                   4, False, pos)
+            self._packed_buf[pos: pos + packed.shape[0]] = ops.pack_pair_rows(packed, self.bit_width,
+                                                                               self.dim)
         else:
             self._packed_buf[pos: pos + packed.shape[0]] = packed
 
@@ -179,13 +179,14 @@ class TurboQuantIndex:
         if self.mode == "mse":
             if k <= _SCAN_MAX_K:
                 if self._pairs:
-                    return ops.ip_scan_topk_pairs(q, self._packed_codes, self._norms, self._cen,
-                                                  self._rot_dev, k)
+                    return ops.ip_scan_topk_pair_rows(q, self._packed_codes, self._norms, self._cen,
+                                                      self._rot_dev, self.bit_width, k)
                 return ops.ip_scan_topk(q, self._packed_codes, self._norms, self._cen,
                                         self._rot_dev, self.bit_width, k)
             if self._pairs:
-                s = ops.attention_scores_pairs(q.float().unsqueeze(0), self._packed_codes,
-                                               self._norms, self._cen, self._rot_dev)[0]
+                s = ops.attention_scores_pair_rows(q.float().unsqueeze(0), self._packed_codes,
+                                                   self._norms, self._cen, self._rot_dev,
+                                                   self.bit_width)[0]
             else:
                 s = ops.attention_scores_packed(q.float().unsqueeze(0), self._packed_codes,
                                                 self._norms, self._cen, self._rot_dev,
