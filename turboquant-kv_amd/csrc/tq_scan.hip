@@ -686,45 +686,75 @@ __device__ __forceinline__ float pair_row(const uint32_t* wds, uint32_t copy8, c
 // fl(q_rot[2p + 1] * c[lo])) -- the reference's per-dim LUT values
 // (csrc/core/turboquant_core.cpp:440-446) -- so a row costs one 8-byte read and two adds
 // (in dim order) per pair and no multiply.  Lanes reading one pair's table touch at most
-// 2^(2 BITS) distinct 8-byte entries: conflict-free at 2 bits, near it at 3.
+// 2^(2 BITS) distinct 8-byte entries: conflict-free at 2 bits (128 bytes); at 3 bits the
+// 512 bytes wrap the 64 banks twice (indices i and i + 32 share banks), which measured
+// faster than splitting each entry over two 256-byte halves read as two b32.
 template <int BITS>
 constexpr int pmp_pair_bytes() { return (1 << (2 * BITS)) * 8; }
 
-// Pairs [P0, P0 + 16) from words X0..X2 (3 bits) or 16 pairs from two words (2 bits),
-// added in pair order.
+// The row's table reads in groups of 8 pairs, each group's reads issued before the previous
+// group's adds (two register buffers), so LDS latency overlaps the add chain; a schedule
+// barrier per group keeps the compiler from hoisting every read of the row (128 registers).
+// Products are added in pair order: the reference's per-dim order.
+template <int BITS>
+constexpr int pmp_group() { return BITS == 2 ? 8 : 4; }  // pairs per pipelined group
+
+template <int BITS, int D>
+__device__ __forceinline__ void pmp_fetch(const uint32_t* w, const char* ctab, int g,
+                                          float2 (&e)[pmp_group<BITS>()]) {
+  if constexpr (BITS == 2) {
+    // group g = word g: bytes k = 0..3, pairs 8g + 2k (high nibble), 8g + 2k + 1 (low)
+    const uint32_t wh = (w[g] >> 1) & 0x78787878u, wl = (w[g] << 3) & 0x78787878u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int p = 8 * g + 2 * k;
+      e[2 * k] = *reinterpret_cast<const float2*>(
+          ctab + p * pmp_pair_bytes<2>() + __builtin_amdgcn_perm(0u, wh, 0x0c0c0c00u | k));
+      e[2 * k + 1] = *reinterpret_cast<const float2*>(
+          ctab + (p + 1) * pmp_pair_bytes<2>() + __builtin_amdgcn_perm(0u, wl, 0x0c0c0c00u | k));
+    }
+  } else {
+    // group g = word i of 16-pair block t: pairs 16t + 4i + k (X3 rebuilt from the top bits
+    // of X0..X2)
+    const int t = g >> 2, i = g & 3;
+    const uint32_t* X = w + 3 * t;
+    const uint32_t wi = i < 3 ? X[i]
+                              : ((X[0] >> 6) & 0x03030303u) | ((X[1] >> 4) & 0x0C0C0C0Cu) |
+                                    ((X[2] >> 2) & 0x30303030u);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t idx = __builtin_amdgcn_ubfe(wi, 8 * k, 6);
+      e[k] = *reinterpret_cast<const float2*>(ctab + (16 * t + 4 * i + k) * pmp_pair_bytes<3>() + idx * 8);
+    }
+  }
+}
+
 template <int BITS, int D>
 __device__ __forceinline__ float pmp_row(const uint32_t* w, const char* ctab) {
 #pragma clang fp contract(off)
+  constexpr int GP = pmp_group<BITS>();
+  constexpr int NG = D / 2 / GP;  // groups per row (even)
   float acc = 0.f;
-  if constexpr (BITS == 2) {
+  float2 ea[GP], eb[GP];
+  pmp_fetch<BITS, D>(w, ctab, 0, ea);
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) {
-      decode_pairs<8>(w[i], 8 * i, [&](int p, uint32_t addr) {
-        const float2 e = *reinterpret_cast<const float2*>(ctab + p * pmp_pair_bytes<2>() + addr);
-        acc = acc + e.x;
-        acc = acc + e.y;
-      });
-      __builtin_amdgcn_sched_barrier(0);
+  for (int g = 0; g < NG; g += 2) {
+    pmp_fetch<BITS, D>(w, ctab, g + 1, eb);
+#pragma unroll
+    for (int q = 0; q < GP; ++q) {
+      acc = acc + ea[q].x;
+      acc = acc + ea[q].y;
     }
-  } else {
+    asm volatile("" : "+v"(acc));  // the adds stay in this group (pure ops float otherwise)
+    __builtin_amdgcn_sched_barrier(0);
+    if (g + 2 < NG) pmp_fetch<BITS, D>(w, ctab, g + 2, ea);
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t) {
-      const uint32_t X[4] = {w[3 * t], w[3 * t + 1], w[3 * t + 2],
-                             ((w[3 * t] >> 6) & 0x03030303u) | ((w[3 * t + 1] >> 4) & 0x0C0C0C0Cu) |
-                                 ((w[3 * t + 2] >> 2) & 0x30303030u)};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int p = 16 * t + 4 * i + k;
-          const uint32_t idx = __builtin_amdgcn_ubfe(X[i], 8 * k, 6);
-          const float2 e = *reinterpret_cast<const float2*>(ctab + p * pmp_pair_bytes<3>() + idx * 8);
-          acc = acc + e.x;
-          acc = acc + e.y;
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int q = 0; q < GP; ++q) {
+      acc = acc + eb[q].x;
+      acc = acc + eb[q].y;
     }
+    asm volatile("" : "+v"(acc));
+    __builtin_amdgcn_sched_barrier(0);
   }
   return acc;
 }
@@ -826,6 +856,45 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tid = threadIdx.x;
 
+  // ---- this wave's rows
+  int64_t nrows = a.nrows;
+  if (a.seq_lens) {
+    const int64_t sl = a.seq_lens[s / a.spb];
+    nrows = sl < a.stream_rows ? sl : a.stream_rows;
+  }
+  const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
+  const int64_t rbeg = (int64_t)blockIdx.x * per_block;
+  const int64_t rend = min(nrows, rbeg + per_block);
+  const uint8_t* base = a.packed + (size_t)s * a.stream_rows * RB;
+  const float* nbase = a.norms + (size_t)s * a.stream_rows;
+
+  struct RowBuf {
+    uint32_t w[NW];
+    float n;
+  };
+  const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
+  const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * RB, nbr * (uint32_t)RB);
+  const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
+  auto load_row = [&](int64_t r, RowBuf& b) {
+    const uint32_t rr = (uint32_t)(r - rbeg);
+    const int off = (int)(rr * (uint32_t)RB);
+#pragma unroll
+    for (int i = 0; i < RB / 16; ++i) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows_rs, off, 16 * i, 0);
+      b.w[4 * i + 0] = v.x; b.w[4 * i + 1] = v.y; b.w[4 * i + 2] = v.z; b.w[4 * i + 3] = v.w;
+    }
+    if constexpr (RB % 16 == 8) {  // 3-bit rows of 64 dims: 24 bytes
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rows_rs, off, RB - 8, 0);
+      b.w[NW - 2] = v.x; b.w[NW - 1] = v.y;
+    }
+    b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
+  };
+
+  constexpr int64_t kStride = kPsWaves * 64;
+  const int64_t first = rbeg + wave * 64;
+  int64_t row = first + lane;
+  const int nsteps = __builtin_amdgcn_readfirstlane(
+      first < rend ? (int)((rend - first + kStride - 1) / kStride) : 0);
   // ---- query rotation (build_tables' arithmetic) and the centroid-pair table
   if (tid < D) qs_s[tid] = load_as_f32(a.q, (int64_t)q0 * D + tid, a.q_dt);
   else if (tid < D + 16) cen_s[tid - D] = a.cen[tid - D];
@@ -865,44 +934,11 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
   for (int m = 0; m < NQ; ++m) qv[m] = qr_s[16 * m + (lane & 15)];
   const uint32_t copy8 = (uint32_t)(lane & 31) * 8;
 
-  int64_t nrows = a.nrows;
-  if (a.seq_lens) {
-    const int64_t sl = a.seq_lens[s / a.spb];
-    nrows = sl < a.stream_rows ? sl : a.stream_rows;
-  }
-  const int64_t per_block = ((nrows + gridDim.x - 1) / gridDim.x + 63) / 64 * 64;
-  const int64_t rbeg = (int64_t)blockIdx.x * per_block;
-  const int64_t rend = min(nrows, rbeg + per_block);
-  const uint8_t* base = a.packed + (size_t)s * a.stream_rows * RB;
-  const float* nbase = a.norms + (size_t)s * a.stream_rows;
-
   float th = -INFINITY;
   int thi = INT_MAX;
   int cnt = 0;
   float* cs = cand_s + wave * kCandCap;
   int* ci = cand_i + wave * kCandCap;
-
-  struct RowBuf {
-    uint32_t w[NW];
-    float n;
-  };
-  const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
-  const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * RB, nbr * (uint32_t)RB);
-  const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
-  auto load_row = [&](int64_t r, RowBuf& b) {
-    const uint32_t rr = (uint32_t)(r - rbeg);
-    const int off = (int)(rr * (uint32_t)RB);
-#pragma unroll
-    for (int i = 0; i < RB / 16; ++i) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows_rs, off, 16 * i, 0);
-      b.w[4 * i + 0] = v.x; b.w[4 * i + 1] = v.y; b.w[4 * i + 2] = v.z; b.w[4 * i + 3] = v.w;
-    }
-    if constexpr (RB % 16 == 8) {  // 3-bit rows of 64 dims: 24 bytes
-      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rows_rs, off, RB - 8, 0);
-      b.w[NW - 2] = v.x; b.w[NW - 1] = v.y;
-    }
-    b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
-  };
 
   auto score = [&](const RowBuf& rb) {
     float acc;
@@ -952,11 +988,6 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
     }
   };
 
-  constexpr int64_t kStride = kPsWaves * 64;
-  const int64_t first = rbeg + wave * 64;
-  int64_t row = first + lane;
-  const int nsteps = __builtin_amdgcn_readfirstlane(
-      first < rend ? (int)((rend - first + kStride - 1) / kStride) : 0);
   RowBuf ta, tb;
   if (nsteps > 0) load_row(row, ta);
   if (nsteps > 1) load_row(row + kStride, tb);
