@@ -39,9 +39,9 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (vector or MFMA)
 METRIC = "packed-KV decode-attn GB/s (% HBM peak); 10M×d128 4-bit IP scan queries/s"
 PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms
-# HBM bytes per launch of pair_scan_kernel<128,true> on the headline workload, from
+# HBM bytes per launch of pair_filter_kernel<128,false> on the headline workload, from
 # rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a copy kernel's readings (FETCH x2.0,
-# WRITE x1.0); commands and raw counts in profiles/pair_scan_kernel_b4_q1_N10M_d128.md.
+# WRITE x1.0); commands and raw counts in profiles/pair_filter_kernel_b4_q1_N10M_d128.md.
 SCAN_TRAFFIC_BYTES = 686.7e6
 
 
@@ -722,7 +722,7 @@ def main():
                    "N": 10_000_000, "d": 128, "bits": 4, "queries_per_step": 1, "k": 10},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": SCAN_TRAFFIC_BYTES,
-                     "kernel": "ip_scan_topk_pairs op (pair_scan_kernel<128,true> + merge_kernel)",
+                     "kernel": "ip_scan_topk_pairs op (pair_filter_kernel<128,false> + filter_merge_kernel)",
                      "bytes_per_launch": bytes_alg},
         "cpu_baseline": cpu,
         "decode_attn_GBps": {str(T): v[1] / v[0] / 1e6 for T, v in dec.items()},

@@ -32,6 +32,7 @@
 #include "tq_common.h"
 #include "tq_decode.h"
 
+#include <atomic>
 #include <climits>
 #include <mutex>
 #include <utility>
@@ -1368,6 +1369,650 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
     merge_query(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
 }
 
+// ------------------------------------------------------------------ filtered pair scan
+// One-query top-k over 4-bit pair-layout rows (d = 64 / 128) whose answer carries the
+// reference's exact scores (csrc/core/turboquant_core.cpp:455-494: per-dim products
+// q_rot[j] * c[code] rounded one by one, added in dim order, times the norm; strict '>'
+// with the lower index winning ties).
+//
+// Filter.  An approximate score per row on the matrix cores.  A code byte is a table
+// index; one 4-byte LDS read returns the fp16 centroid pair (c[hi], c[lo]), which is
+// exactly what v_mfma_f32_16x16x32_f16 takes as B operand (16 rows x 32 dims per MFMA).
+// The A operand holds the rotated query, scaled by a power of two and split into fp16 hi
+// + lo parts, in rows 0 and 1.  Per 64 rows that is 64 table reads, 16 MFMAs and a few
+// dozen VALU instructions, against 128 multiplies and 128 dependent adds per row for the
+// reference's arithmetic: the scan runs at the HBM streaming rate instead of the VALU
+// rate.
+//   Bound: |approx - exact| <= |n| * beta, beta = 2^-10 * ||q_rot||_1 * max|c|.  The fp16
+//   centroids are within 2^-11 relative, the hi + lo query within 2^-22, fp32 accumulation
+//   of 256 exact products within 256 * 2^-23 relative and the exact sum within 128 * 2^-24,
+//   all relative to sum_j |q_j c_j| <= ||q_rot||_1 * max|c| (about 2^-10.9 in all; the
+//   worst case measured on 12M random and adversarial rows was 2^-12.3).
+//   Each row gets lo = approx - B and hi = approx + B.  Every wave keeps (th, thi) = the
+//   k-th best (lo, id) over the rows it has seen -- k distinct rows score at least their
+//   lo, so the k-th best exact (score, id) is at least (th, thi) -- and lists a row only
+//   when (hi, id) reaches it; a row below it cannot be in the answer.  A list that stays
+//   full after pruning (near-ties, duplicate rows) is rescored exactly in place, which
+//   leaves at most k entries.  Waves share th through LDS.  Each block writes its pruned
+//   list (at most k + kFsExtra entries).
+// Merge (filter_merge_kernel): the k-th best (lo, id) over all block lists, the entries
+// whose (hi, id) reach it rescored exactly, and their top k.
+constexpr int kFsThreads = 256;   // 4 waves; two blocks per CU
+constexpr int kFsWaves = kFsThreads / 64;
+constexpr int kFsCap = 128;       // candidate slots per wave
+constexpr int kFsEager = 48;      // a list this long is pruned (and th published) at once
+constexpr int kHtabBytes = 256 * 256;  // byte value x 64 lane copies x fp16 centroid pair
+constexpr int kFsExtra = 4;       // a block list holds at most k + kFsExtra entries
+
+struct FilterArgs {
+  const uint8_t* rows;  // [n][D / 2] pair layout
+  const float* norms;   // [n]
+  int64_t n;
+  const void* q;        // [nq][D]
+  int q_dt;
+  const float* rot;     // [D][D]
+  const float* cen;     // [16]
+  int k;
+  int out;              // block list slots: k + kFsExtra
+  float* blo;           // [nq][nblocks][out] block lists (lo, hi, id)
+  float* bhi;
+  int32_t* bid;         // -1 past the list's length
+  float* qrot;          // [nq][D] q_rot, written by block 0 (for the merge's rescoring)
+  float* out_s;         // [nq][k]
+  int64_t* out_i;
+};
+
+typedef _Float16 fs_v8h __attribute__((ext_vector_type(8)));
+typedef float fs_v4f __attribute__((ext_vector_type(4)));
+
+// Exact score of one pair-layout row: the reference's arithmetic, as pair_scan_kernel.
+template <int D>
+__device__ __forceinline__ float exact_pair_score(const uint8_t* __restrict__ row, float n,
+                                                  const float* qr, const float* cen) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+  const u32x4* r4 = reinterpret_cast<const u32x4*>(row);
+#pragma unroll 1
+  for (int i = 0; i < D / 32; ++i) {
+    const u32x4 v = r4[i];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int p = 16 * i + 4 * wi + b;
+        const uint32_t byte = (w[wi] >> (8 * b)) & 0xFFu;
+        const float p0 = qr[2 * p] * cen[byte >> 4];
+        acc = acc + p0;
+        const float p1 = qr[2 * p + 1] * cen[byte & 15u];
+        acc = acc + p1;
+      }
+    }
+  }
+  return acc * n;
+}
+
+__device__ __forceinline__ bool fs_keep(float hi, int id, float th, int thi) {
+  return (hi > th) | ((hi == th) & (id <= thi));
+}
+
+// One wave's candidate list: LDS slots and the wave-uniform count and threshold.
+struct FsList {
+  float* lo;
+  float* hi;
+  int* id;
+  int cnt;
+  float th;
+  int thi;
+};
+
+__device__ __forceinline__ int lane_prefix(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// (th, thi) from the list's k-th best (lo, id) when it holds k entries or more (kept if
+// it beats the current one; found by ranking each entry against all of them, one
+// broadcast LDS read per entry), then the entries whose (hi, id) fall below it are dropped.
+__device__ __forceinline__ void fs_prune(FsList& L, int k) {
+  const int lane = threadIdx.x & 63;
+  float lo[2], hi[2];
+  int id[2];
+  bool v[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int e = lane + 64 * r;
+    v[r] = e < L.cnt;
+    lo[r] = v[r] ? L.lo[e] : -INFINITY;
+    hi[r] = v[r] ? L.hi[e] : -INFINITY;
+    id[r] = v[r] ? L.id[e] : INT_MAX;
+  }
+  if (L.cnt >= k) {
+    int r0 = 0, r1 = 0;
+    for (int f = 0; f < L.cnt; ++f) {
+      const float lf = L.lo[f];
+      const int idf = L.id[f];
+      r0 += better(lf, idf, lo[0], id[0]);
+      r1 += better(lf, idf, lo[1], id[1]);
+    }
+    const uint64_t b0 = __ballot(v[0] & (r0 == k - 1)), b1 = __ballot(v[1] & (r1 == k - 1));
+    const int src = b0 ? __ffsll((long long)b0) - 1 : __ffsll((long long)b1) - 1;
+    const float ts = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b0 ? lo[0] : lo[1]), src));
+    const int ti = __builtin_amdgcn_readlane(b0 ? id[0] : id[1], src);
+    if (better(ts, ti, L.th, L.thi)) { L.th = ts; L.thi = ti; }
+  }
+  const bool k0 = v[0] & fs_keep(hi[0], id[0], L.th, L.thi);
+  const bool k1 = v[1] & fs_keep(hi[1], id[1], L.th, L.thi);
+  const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
+  const int n0 = __popcll(m0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (k0) {
+    const int p = lane_prefix(m0);
+    L.lo[p] = lo[0]; L.hi[p] = hi[0]; L.id[p] = id[0];
+  }
+  if (k1) {
+    const int p = n0 + lane_prefix(m1);
+    L.lo[p] = lo[1]; L.hi[p] = hi[1]; L.id[p] = id[1];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  L.cnt = n0 + __popcll(m1);
+}
+
+// Rescore every entry with the reference's arithmetic (lo = hi = the exact score; NaN
+// scores are never listed), then prune: at most k entries remain.
+template <int D>
+__device__ __forceinline__ void fs_exact(FsList& L, int k, const uint8_t* __restrict__ rows,
+                                         const float* __restrict__ norms, const float* qr,
+                                         const float* cen) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll 1
+  for (int r = 0; r < 2; ++r) {
+    const int e = lane + 64 * r;
+    if (e < L.cnt) {
+      const int id = L.id[e];
+      const float s = exact_pair_score<D>(rows + (size_t)id * (D / 2), norms[id], qr, cen);
+      const bool nan = __builtin_isnan(s);
+      L.lo[e] = nan ? -INFINITY : s;
+      L.hi[e] = nan ? __builtin_nanf("") : s;  // fs_keep fails for NaN: dropped
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  fs_prune(L, k);
+}
+
+// Best of this wave's threshold and the ones the block's other waves published (a
+// published th alone is the weaker (th, INT_MAX): every row with hi == th passes it).
+__device__ __forceinline__ void fs_share(FsList& L, float* th_s, int wave) {
+  if ((threadIdx.x & 63) == 0) th_s[wave] = L.th;
+#pragma unroll
+  for (int w = 0; w < kFsWaves; ++w) {
+    const float t = th_s[w];
+    if (t > L.th) { L.th = t; L.thi = INT_MAX; }
+  }
+}
+
+// fp16 centroid pair of byte K of w: LDS entry (byte << 8) | lane * 4 (64 lane copies).
+template <int K>
+__device__ __forceinline__ uint32_t fs_hlook(uint32_t w, uint32_t lane4, const char* htab) {
+  const uint32_t addr = __builtin_amdgcn_perm(w, lane4, 0x0c0c0000u | ((4u + K) << 8));
+  return *reinterpret_cast<const uint32_t*>(htab + addr);
+}
+
+// Per query, one kFmThreads block after the filter: every block-list slot (a.out slots of
+// (lo, hi, id) per block, id -1 past the list's length) is loaded in one round into
+// registers, NR per thread.  tau = the k-th best of 64 group maxima of (lo, id) (groups of
+// 8 threads; k distinct rows, each scoring at least its lo) bounds the answer from below;
+// the entries whose (hi, id) reach it are rescored with the reference's arithmetic (q_rot
+// from the filter's block 0) and rank-sorted, with (-inf, -1) pads.  More than kMergeCap
+// of them (near-ties across blocks): slot r of every thread at a time, rescored and merged
+// into a running top k.
+constexpr int kFmThreads = 512;
+constexpr int kFmWaves = kFmThreads / 64;
+constexpr int kFmRegs = 40;  // list slots per thread: 512 blocks x (32 + 4) / 512 = 36
+
+template <int D, int NR>
+__global__ __launch_bounds__(kFmThreads) void filter_merge_kernel(FilterArgs a, int nslots) {
+#pragma clang fp contract(off)
+  __shared__ float qr[D];
+  __shared__ float cen[16];
+  __shared__ __attribute__((aligned(16))) float gs[64];
+  __shared__ __attribute__((aligned(16))) int gi[64];
+  __shared__ float ss[kMergeCap + kFmThreads];
+  __shared__ int si[kMergeCap + kFmThreads];
+  __shared__ int cnt_s, nvalid_s, taui_s;
+  __shared__ float tau_s;
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int k = a.k;
+  const size_t base = (size_t)q * nslots;
+  float* os = a.out_s + (size_t)q * k;
+  int64_t* oi = a.out_i + (size_t)q * k;
+  // q_rot and centroids first: their waits then do not wait for the slots behind them
+  float qv = 0.f;
+  if (tid < D) qv = a.qrot[(size_t)q * D + tid];
+  else if (tid < D + 16) qv = a.cen[tid - D];
+  float el[NR], eh[NR];
+  int ei[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int e = tid + kFmThreads * r;
+    const size_t ec = base + (size_t)(e < nslots ? e : nslots - 1);
+    const float lo = a.blo[ec], hi = a.bhi[ec];
+    const int id = a.bid[ec];
+    const bool ok = (e < nslots) & (id >= 0);
+    el[r] = ok ? lo : -INFINITY;
+    eh[r] = ok ? hi : -INFINITY;
+    ei[r] = ok ? id : INT_MAX;
+  }
+  if (tid < D) qr[tid] = qv;
+  else if (tid < D + 16) cen[tid - D] = qv;
+  float bs = -INFINITY;
+  int bi = INT_MAX;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const bool take = (ei[r] != INT_MAX) & ((bi == INT_MAX) | better(el[r], ei[r], bs, bi));
+    bs = take ? el[r] : bs;
+    bi = take ? ei[r] : bi;
+  }
+  best_step<0xB1, 0xF>(bs, bi);   // quad_perm [1,0,3,2]
+  best_step<0x4E, 0xF>(bs, bi);   // quad_perm [2,3,0,1]
+  best_step<0x141, 0xF>(bs, bi);  // row_half_mirror: 8-lane groups
+  if ((lane & 7) == 0) { gs[tid >> 3] = bs; gi[tid >> 3] = bi; }
+  if (tid == 0) { cnt_s = 0; nvalid_s = 0; tau_s = -INFINITY; taui_s = INT_MAX; }
+  __syncthreads();
+  if (wave == 0) {
+    const float s0 = gs[lane];
+    const int i0 = gi[lane];
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < 64; j += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(gs + j);
+      const int4 i4 = *reinterpret_cast<const int4*>(gi + j);
+      rank += (i4.x != INT_MAX) & better(s4.x, i4.x, s0, i0);
+      rank += (i4.y != INT_MAX) & better(s4.y, i4.y, s0, i0);
+      rank += (i4.z != INT_MAX) & better(s4.z, i4.z, s0, i0);
+      rank += (i4.w != INT_MAX) & better(s4.w, i4.w, s0, i0);
+    }
+    if ((i0 != INT_MAX) & (rank == k - 1)) { tau_s = s0; taui_s = i0; }
+  }
+  __syncthreads();
+  // survivors: (hi, id) at or above tau
+  const float tau = tau_s;
+  const int taui = taui_s;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if ((ei[r] != INT_MAX) & fs_keep(eh[r], ei[r], tau, taui)) {
+      const int p = atomicAdd(&cnt_s, 1);
+      if (p < kMergeCap) si[p] = ei[r];
+    }
+  }
+  __syncthreads();
+  const int m = cnt_s;
+  if (m <= kMergeCap) {
+    // rescored exactly; NaN scores are never listed
+    for (int e = tid; e < m; e += kFmThreads) {
+      const int id = si[e];
+      const float sc = exact_pair_score<D>(a.rows + (size_t)id * (D / 2), a.norms[id], qr, cen);
+      ss[e] = sc;
+      if (!__builtin_isnan(sc)) atomicAdd(&nvalid_s, 1);
+    }
+    __syncthreads();
+    for (int e = tid; e < m; e += kFmThreads) {
+      const float se = ss[e];
+      const int ie = si[e];
+      if (__builtin_isnan(se)) continue;
+      int rank = 0;
+      for (int f = 0; f < m; ++f) rank += better(ss[f], si[f], se, ie);
+      if (rank < k) { os[rank] = se; oi[rank] = ie; }
+    }
+    for (int e = nvalid_s + tid; e < k; e += kFmThreads) { os[e] = -INFINITY; oi[e] = -1; }
+    return;  // uniform
+  }
+  // more survivors than kMergeCap: slot r of every thread at a time, rescored and merged
+  // into a running top k in ss / si[0, k)
+  if (tid < k) { ss[tid] = -INFINITY; si[tid] = INT_MAX; }
+  __syncthreads();
+#pragma unroll 1
+  for (int r = 0; r < NR; ++r) {
+    bool svr = false;
+    int idr = INT_MAX;
+#pragma unroll
+    for (int u = 0; u < NR; ++u)
+      if (u == r) { svr = (ei[u] != INT_MAX) & fs_keep(eh[u], ei[u], tau, taui); idr = ei[u]; }
+    float sc = -INFINITY;
+    int id = INT_MAX;
+    if (svr) {
+      const float x = exact_pair_score<D>(a.rows + (size_t)idr * (D / 2), a.norms[idr], qr, cen);
+      if (!__builtin_isnan(x)) { sc = x; id = idr; }
+    }
+    ss[k + tid] = sc;
+    si[k + tid] = id;
+    __syncthreads();
+    float ns = -INFINITY;
+    int ni = INT_MAX, nrank = k;
+    for (int e = tid; e < k + kFmThreads; e += kFmThreads) {
+      const float se = ss[e];
+      const int ie = si[e];
+      int rank = 0;
+      for (int f = 0; f < k + kFmThreads; ++f) rank += better(ss[f], si[f], se, ie);
+      if ((ie != INT_MAX) & (rank < k)) { ns = se; ni = ie; nrank = rank; }
+    }
+    __syncthreads();
+    if (nrank < k) { ss[nrank] = ns; si[nrank] = ni; }
+    __syncthreads();
+  }
+  for (int e = tid; e < k; e += kFmThreads) {
+    os[e] = si[e] == INT_MAX ? -INFINITY : ss[e];
+    oi[e] = si[e] == INT_MAX ? -1 : si[e];
+  }
+}
+
+// BIG: rows or norms past 2^32 bytes -- a buffer resource per 64-row group (64-bit base);
+// otherwise one resource over the whole database and 32-bit offsets.
+template <int D, bool BIG>
+__global__ __launch_bounds__(kFsThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+pair_filter_kernel(FilterArgs a) {
+#pragma clang fp contract(off)
+  static_assert(D == 64 || D == 128, "pair filter dims");
+  constexpr int RB = D / 2;   // bytes per row
+  constexpr int KT = D / 32;  // MFMA k tiles per row
+  constexpr int LW = D / 32;  // 32-bit words per lane per 16-row tile (16 B at D=128, 8 B at 64)
+  __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
+  __shared__ float qs_s[D];
+  __shared__ float qr_s[D];
+  __shared__ float cen_s[16];
+  __shared__ float red_s[2 * kFsWaves];
+  __shared__ float th_s[kFsWaves];
+  __shared__ float lo_s[kFsWaves * kFsCap];
+  __shared__ float hi_s[kFsWaves * kFsCap];
+  __shared__ int id_s[kFsWaves * kFsCap];
+  __shared__ int cnt_s[kFsWaves];
+  __shared__ float wth_s[kFsWaves];
+  __shared__ int wthi_s[kFsWaves];
+
+  const int q = blockIdx.y;
+  // wave-uniform (readfirstlane) so row offsets and buffer resources live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
+  const uint32_t W = gridDim.x * kFsWaves;
+  const uint32_t gw = blockIdx.x * kFsWaves + wave;
+  const uint32_t n = (uint32_t)a.n;  // < 2^31 (ids are int32)
+  const uint32_t ngroups = (n + 63) / 64;
+  const int nsteps = gw < ngroups ? (int)((ngroups - 1 - gw) / W + 1) : 0;
+
+  // ---- query, centroids and this thread's rotation row first, so that waiting for them
+  // does not wait for the row prefetch behind them
+  // (the query as a raw dword through a bounded buffer: no dtype branch, so no wait, here)
+  float cload = 0.f;
+  float4 rrow[D / 4];
+  const int esz = a.q_dt == TQ_F32 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t qrs =
+      buf_rsrc(static_cast<const char*>(a.q) + (size_t)q * D * esz, (uint32_t)(D * esz));
+  const uint32_t qraw = __builtin_amdgcn_raw_buffer_load_b32(qrs, (tid * esz) & ~3, 0, 0);
+  if (tid < D) {
+    const float4* r4 = reinterpret_cast<const float4*>(a.rot + (size_t)tid * D);
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) rrow[i] = r4[i];
+  }
+  if (tid < 16) cload = a.cen[tid];
+
+  // Rows of step t: the 64-row group t * W + gw (grid stride: all waves sweep memory
+  // together).  Lane 16 g + i reads LW words of row 16 rt + i at byte 4 LW g, one load per
+  // 16-row tile rt: each load instruction covers 16 whole rows.  Loads past the last row
+  // return zeros (the resource's range check).
+  struct RowBuf {
+    uint32_t w[4 * LW];
+    float n;
+  };
+  const uint32_t loff = (lane & 15) * RB + (lane >> 4) * (4 * LW);
+  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * (uint32_t)RB);
+  const __amdgpu_buffer_rsrc_t norms_all = buf_rsrc(a.norms, BIG ? 0u : n * 4u);
+  auto load = [&](int t, RowBuf& b) {
+    const uint32_t g = (uint32_t)t * W + gw;
+    __amdgpu_buffer_rsrc_t rs = rows_all, ns = norms_all;
+    uint32_t roff = loff, noff = lane * 4u;
+    if constexpr (BIG) {
+      const int64_t r0 = (int64_t)g * 64;
+      const int64_t left = a.n - r0;
+      const uint32_t nr = (uint32_t)(left < 64 ? (left > 0 ? left : 0) : 64);
+      rs = buf_rsrc(a.rows + r0 * RB, nr * (uint32_t)RB);
+      ns = buf_rsrc(a.norms + r0, nr * 4u);
+    } else {
+      const uint32_t gl = g < ngroups ? g : ngroups;  // groups past the end: an empty range
+      roff += gl * (64u * RB);
+      noff += gl * 256u;
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      if constexpr (LW == 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        b.w[4 * rt + 0] = v.x; b.w[4 * rt + 1] = v.y; b.w[4 * rt + 2] = v.z; b.w[4 * rt + 3] = v.w;
+      } else {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        b.w[2 * rt + 0] = v.x; b.w[2 * rt + 1] = v.y;
+      }
+    }
+    b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ns, (int)noff, 0, kNT));
+  };
+  RowBuf ta, tb;
+  __builtin_amdgcn_sched_barrier(0);
+  load(0, ta);
+  // the loop issues each buffer's loads as one group (rows, then norm); the prologue keeps
+  // that order, so the per-register wait counts agree on both paths into the loop
+  __builtin_amdgcn_sched_barrier(0);
+  load(1, tb);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- query rotation (pair_scan_kernel's arithmetic), tables, bound
+  if (tid < D) {
+    const uint32_t h = (tid & 1) ? qraw >> 16 : qraw & 0xFFFFu;  // 2-byte types: this half
+    qs_s[tid] = a.q_dt == TQ_F32 ? __uint_as_float(qraw)
+              : a.q_dt == TQ_BF16 ? __uint_as_float(h << 16)
+                                  : __half2float(__ushort_as_half((unsigned short)h));
+  }
+  if (tid < 16) cen_s[tid] = cload;
+  if (tid < kFsWaves) th_s[tid] = -INFINITY;
+  __syncthreads();
+  float qv = 0.f;
+  if (tid < D) {
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) {
+      qv = qv + qs_s[4 * i] * rrow[i].x;
+      qv = qv + qs_s[4 * i + 1] * rrow[i].y;
+      qv = qv + qs_s[4 * i + 2] * rrow[i].z;
+      qv = qv + qs_s[4 * i + 3] * rrow[i].w;
+    }
+    qr_s[tid] = qv;
+  }
+  for (int e = tid; e < 256 * 16; e += kFsThreads) {  // entry b, copies 4c..4c+3
+    const int b = e >> 4, c = e & 15;
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    const uint32_t v = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)cen_s[b >> 4], (_Float16)cen_s[b & 15]});
+    *reinterpret_cast<u32x4*>(htab + b * 256 + c * 16) = (u32x4){v, v, v, v};
+  }
+  // max |q_rot| and ||q_rot||_1 (threads >= D contribute 0)
+  {
+    float am = fabsf(qv), l1 = fabsf(qv);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      am = fmaxf(am, __shfl_xor(am, off));
+      l1 = l1 + __shfl_xor(l1, off);
+    }
+    if (lane == 0) { red_s[wave] = am; red_s[kFsWaves + wave] = l1; }
+  }
+  __syncthreads();
+  float amax = 0.f, l1 = 0.f, cmax = 0.f;
+#pragma unroll
+  for (int w = 0; w < kFsWaves; ++w) { amax = fmaxf(amax, red_s[w]); l1 = l1 + red_s[kFsWaves + w]; }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) cmax = fmaxf(cmax, fabsf(cen_s[i]));
+  // scale: max |q_rot| * scale in [2^14, 2^15); a query whose scale would leave fp32's
+  // range gets beta = inf (every row is then rescored exactly).
+  int ex = 0;
+  const bool scalable = amax > 0.f && amax < INFINITY;
+  if (scalable) frexpf(amax, &ex);
+  const bool ok = scalable && ex > -100 && ex < 100;
+  const float scale = ok ? ldexpf(1.f, 15 - ex) : 1.f;
+  const float inv_scale = ok ? ldexpf(1.f, ex - 15) : 1.f;
+  const float beta = ok ? l1 * cmax * 0x1p-10f : (amax == 0.f ? 0.f : INFINITY);
+  fs_v8h qa[KT];
+  {
+    const int m = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = qr_s[(D == 128 ? 32 : 16) * g + 8 * kt + e] * scale;
+        const _Float16 h = (_Float16)x;
+        const _Float16 l = (_Float16)(x - (float)h);
+        qa[kt][e] = m == 0 ? h : (m == 1 ? l : (_Float16)0.f);
+      }
+    }
+  }
+  const uint32_t lane4 = (uint32_t)lane * 4;
+
+  // Approximate scores of the wave's 64 rows, lane = row: tile rt's rows are the columns of
+  // its MFMAs; rows 0 / 1 of the result (hi / lo query part) sit in lanes 0-15, and three
+  // row swaps bring tile rt's 16 scores to lanes 16 rt .. 16 rt + 15.
+  auto approx = [&](const RowBuf& rb) -> float {
+    float t[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      fs_v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const uint32_t x = rb.w[LW * rt + kt];
+        const u32x4 bw = {fs_hlook<0>(x, lane4, htab), fs_hlook<1>(x, lane4, htab),
+                          fs_hlook<2>(x, lane4, htab), fs_hlook<3>(x, lane4, htab)};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kt], __builtin_bit_cast(fs_v8h, bw), acc, 0, 0, 0);
+      }
+      t[rt] = acc[0] + acc[1];
+    }
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(t[0]), __float_as_uint(t[1]), false, false);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t[2]), __float_as_uint(t[3]), false, false);
+    const auto s = __builtin_amdgcn_permlane32_swap(p[0], r[0], false, false);
+    return __uint_as_float(s[0]);
+  };
+
+  FsList L{lo_s + wave * kFsCap, hi_s + wave * kFsCap, id_s + wave * kFsCap, 0, -INFINITY, INT_MAX};
+  // Per step the common case costs two multiplies, an fma and a compare: hi >= th can only
+  // hold for a row that beats th's float (NaN passes too); the rest -- row validity, the
+  // exact (hi, id) test, lo, non-finite scores -- runs only when some lane passes.
+  auto step = [&](const RowBuf& rb, int t) {
+    const float sa = approx(rb) * inv_scale * rb.n;
+    const float hq = __builtin_fmaf(fabsf(rb.n), beta, sa);
+    if (__ballot(!(hq < L.th)) == 0) return;
+    const uint32_t row = ((uint32_t)t * W + gw) * 64u + lane;
+    const bool valid = row < n;
+    const float B = fabsf(rb.n) * beta;
+    const bool fin = (fabsf(sa) < INFINITY) & (B < INFINITY);
+    const float lo = fin ? sa - B : -INFINITY;
+    const float hi = fin ? sa + B : INFINITY;
+    const int id = (int)row;
+    bool ins = valid & fs_keep(hi, id, L.th, L.thi);
+    uint64_t mask = __ballot(ins);
+    if (mask == 0) return;
+    int nnew = __popcll(mask);
+    if (L.cnt + nnew > kFsCap) {
+      fs_share(L, th_s, wave);
+      fs_prune(L, a.k);
+      ins = valid & fs_keep(hi, id, L.th, L.thi);
+      mask = __ballot(ins);
+      nnew = __popcll(mask);
+      if (L.cnt + nnew > kFsCap) {
+        fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);
+        ins = valid & fs_keep(hi, id, L.th, L.thi);
+        mask = __ballot(ins);
+        nnew = __popcll(mask);
+      }
+    }
+    if (ins) {
+      const int p = L.cnt + lane_prefix(mask);
+      L.lo[p] = lo; L.hi[p] = hi; L.id[p] = id;
+    }
+    L.cnt += nnew;
+    // raise th early -- from the first k rows, then whenever the list grows long -- and
+    // share it with the block's other waves: fewer inserts for all of them
+    if ((L.cnt >= kFsEager) | ((L.th == -INFINITY) & (L.cnt >= a.k))) {
+      fs_share(L, th_s, wave);
+      fs_prune(L, a.k);
+      fs_share(L, th_s, wave);
+    }
+  };
+
+  // Loads past the last step address an empty range (zeros, no memory access); issuing
+  // them unconditionally keeps every path's load order the same, so each step waits only
+  // for its own rows.  After the first step the list is pruned once, which sets the
+  // threshold from 64 rows instead of letting 128 rows in first.
+  // Loads past the last step address an empty range (zeros, no memory access); issuing
+  // them unconditionally keeps every path's load order the same, so each step waits only
+  // for its own rows.
+  for (int t = 0; t < nsteps; t += 2) {
+    step(ta, t);
+    load(t + 2, ta);
+    if (t + 1 >= nsteps) break;
+    step(tb, t + 1);
+    load(t + 3, tb);
+  }
+
+  // ---- block list: each wave pruned (at most kMaxK entries, exact if it had more), then
+  // wave 0 prunes the union with the best of the waves' and the call's thresholds.
+  fs_share(L, th_s, wave);
+  fs_prune(L, a.k);
+  if (L.cnt > kMaxK) fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);
+  if (lane == 0) { cnt_s[wave] = L.cnt; wth_s[wave] = L.th; wthi_s[wave] = L.thi; }
+  __syncthreads();
+  const size_t bslot = (size_t)q * gridDim.x + blockIdx.x;
+  if (wave == 0) {
+    int total = 0;
+    int off[kFsWaves];
+#pragma unroll
+    for (int w = 0; w < kFsWaves; ++w) {
+      off[w] = total;
+      total += cnt_s[w];
+      if (better(wth_s[w], wthi_s[w], L.th, L.thi)) { L.th = wth_s[w]; L.thi = wthi_s[w]; }
+    }
+    // gather the other waves' entries behind wave 0's (at most 4 x 32 = 128 in all)
+    float glo[2], ghi[2];
+    int gid[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = lane + 64 * r;
+      int slot = e;  // wave 0's entries stay where they are
+#pragma unroll
+      for (int u = 1; u < kFsWaves; ++u) slot = e >= off[u] ? u * kFsCap + (e - off[u]) : slot;
+      const bool v = e < total;
+      glo[r] = v ? lo_s[slot] : 0.f;
+      ghi[r] = v ? hi_s[slot] : 0.f;
+      gid[r] = v ? id_s[slot] : 0;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = lane + 64 * r;
+      if (e < total) { L.lo[e] = glo[r]; L.hi[e] = ghi[r]; L.id[e] = gid[r]; }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    L.cnt = total;
+    fs_prune(L, a.k);
+    if (L.cnt > a.out) fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);  // then at most k
+    // every slot: id -1 past the list's length
+    const size_t base = bslot * a.out;
+    for (int e = lane; e < a.out; e += 64) {
+      const bool v = e < L.cnt;
+      a.blo[base + e] = v ? L.lo[e] : -INFINITY;
+      a.bhi[base + e] = v ? L.hi[e] : -INFINITY;
+      a.bid[base + e] = v ? L.id[e] : -1;
+    }
+  }
+  if (blockIdx.x == 0 && tid < D) a.qrot[(size_t)q * D + tid] = qr_s[tid];  // for the merge
+}
+
+
 // ------------------------------------------------------------------ softmax stats
 // stats[q] = (max_t s, sum_t exp(s - max)) over the valid tokens of query q's stream.
 __global__ __launch_bounds__(kThreads) void softmax_stats_kernel(const float* __restrict__ scores,
@@ -1676,6 +2321,63 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   return fail(TQ_EINVAL, "bit_width must be 1-4, got %d", bits);
 }
 
+// Row blocks of the filtered pair scan: two 4-wave blocks per CU, fewer when there are
+// fewer 64-row groups than waves.
+int filter_blocks(int64_t nrows) {
+  const int64_t groups = (nrows + 63) / 64;
+  const int64_t want = (groups + kFsWaves - 1) / kFsWaves;
+  const int64_t cap = (int64_t)device_cu_count() * 2;
+  const int64_t b = want < cap ? want : cap;
+  return (int)(b < 1 ? 1 : b);
+}
+
+// Workspace of the filtered pair scan: block lists (lo, hi, id) of k + kFsExtra entries,
+// their counts, q_rot per query.
+size_t filter_workspace_bytes(int64_t nq, int d, int64_t N, int k) {
+  const size_t nb = (size_t)filter_blocks(N);
+  const size_t out = (size_t)k + kFsExtra;
+  return align_up((size_t)nq * nb * out * 4, 256) * 3 + align_up((size_t)nq * d * 4, 256);
+}
+
+template <int D>
+int launch_filter_d(const FilterArgs& f, int nb, int nq, bool big, hipStream_t st) {
+  const dim3 grid((unsigned)nb, (unsigned)nq);
+  if (big) hipLaunchKernelGGL((pair_filter_kernel<D, true>), grid, dim3(kFsThreads), 0, st, f);
+  else hipLaunchKernelGGL((pair_filter_kernel<D, false>), grid, dim3(kFsThreads), 0, st, f);
+  TQ_LAUNCH_CHECK("pair_filter_kernel");
+  const int nslots = nb * f.out;
+  const dim3 mg((unsigned)nq);
+  if (nslots <= 4 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<D, 4>), mg, dim3(kFmThreads), 0, st, f, nslots);
+  else if (nslots <= 16 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<D, 16>), mg, dim3(kFmThreads), 0, st, f, nslots);
+  else hipLaunchKernelGGL((filter_merge_kernel<D, kFmRegs>), mg, dim3(kFmThreads), 0, st, f, nslots);
+  TQ_LAUNCH_CHECK("filter_merge_kernel");
+  return TQ_OK;
+}
+
+int launch_filter(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, const uint8_t* pairs,
+                  const float* norms, int64_t N, const float* centroids, const float* rotation,
+                  int32_t k, float* out_scores, int64_t* out_ids, char* ws, hipStream_t st) {
+  TQ_REQUIRE(nq <= 65535, "too many queries in one call");
+  const int nb = filter_blocks(N);
+  const int out = k + kFsExtra;
+  TQ_REQUIRE(nb * out <= kFmRegs * kFmThreads, "too many block lists for the merge");
+  FilterArgs f{};
+  f.rows = pairs; f.norms = norms; f.n = N; f.q = queries; f.q_dt = q_dtype; f.rot = rotation;
+  f.cen = centroids; f.k = k; f.out = out;
+  f.blo = reinterpret_cast<float*>(ws);
+  ws += align_up((size_t)nq * nb * out * 4, 256);
+  f.bhi = reinterpret_cast<float*>(ws);
+  ws += align_up((size_t)nq * nb * out * 4, 256);
+  f.bid = reinterpret_cast<int32_t*>(ws);
+  ws += align_up((size_t)nq * nb * out * 4, 256);
+  f.qrot = reinterpret_cast<float*>(ws);
+  f.out_s = out_scores; f.out_i = out_ids;
+  // 32-bit offsets while rows and norms stay under 2^32 bytes
+  const bool big = N * (d / 2) >= ((int64_t)1 << 32) - 4096 || N * 4 >= ((int64_t)1 << 32) - 4096;
+  return d == 128 ? launch_filter_d<128>(f, nb, (int)nq, big, st)
+                  : launch_filter_d<64>(f, nb, (int)nq, big, st);
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -1689,6 +2391,10 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
   if (k > 0) {
     const size_t nb = (size_t)scan_blocks(N);
     bytes += align_up((size_t)nq * nb * k * 4, 256) * 2;
+    if (bit_width == 4 && (d == 64 || d == 128)) {  // the filtered pair scan's lists
+      const size_t fb = 256 + filter_workspace_bytes(nq, d, N, k);
+      if (fb > bytes) bytes = fb;
+    }
   }
   return bytes;
 }
@@ -1742,6 +2448,11 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.part_s = ps; a.part_i = pi; a.scores = nullptr;
   a.out_s = out_scores; a.out_i = out_ids;
   if (prod) set_prod(a, *prod);
+  // One query over 4-bit pair rows: the filtered scan (approximate scores on the matrix
+  // cores, the candidates rescored exactly).
+  if (pairs && bit_width == 4 && !prod && nq == 1 && (d == 64 || d == 128))
+    return launch_filter(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
+                         out_scores, out_ids, static_cast<char*>(workspace) + 256, st);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
   TQ_REQUIRE(!pairs || bit_width == 4 || nq <= 65535, "too many queries in one call");
   int nb = 0;
