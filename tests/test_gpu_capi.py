@@ -148,7 +148,7 @@ def k_scan_pairs(q, pairs, norms, cen, R, k, q_dt=capi.TQ_F32):
     os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
     oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
     ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, 4, N, k), 1), dtype=torch.uint8, device=DEV)
-    nt = T(norms) if N else torch.empty(0, dtype=torch.float32, device=DEV)
+    nt = norms if torch.is_tensor(norms) else (T(norms) if N else torch.empty(0, dtype=torch.float32, device=DEV))
     capi.check(L().tq_ip_scan_topk_pairs(capi.p(T(q)), q_dt, capi.i64(Q), capi.i32(d), capi.p(pairs),
                                          capi.p(nt), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
                                          capi.i32(k), capi.p(os_), capi.p(oi), capi.p(ws),
@@ -670,6 +670,133 @@ def test_pairs_scan_one_query_ties():
         so, io = O.search_topk(q, p, nm, cen, R, 4, k)
         assert np.array_equal(i, io), k
         assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+def _topk_no_nan(scores, k):
+    # the scan never lists a NaN score; the remaining rows in the oracle's order
+    sc = np.where(np.isnan(scores), -np.inf, scores)
+    keep = ~np.isnan(scores)
+    so, io = O.topk_desc(sc, sc.shape[1])
+    out_s = np.full((sc.shape[0], k), -np.inf, np.float32)
+    out_i = np.full((sc.shape[0], k), -1, np.int64)
+    for r in range(sc.shape[0]):
+        ids = [j for j in io[r] if keep[r, j]][:k]
+        out_i[r, :len(ids)] = ids
+        out_s[r, :len(ids)] = scores[r, ids]
+    return out_s, out_i
+
+
+def test_pairs_scan_one_query_special_norms():
+    # The one-query scan scores rows approximately first; rows whose norms are zero,
+    # negative, huge, tiny or infinite (inf * 0 = NaN rows are never listed) must still
+    # come out exactly as the reference's arithmetic orders them.
+    rs = np.random.RandomState(23)
+    d = 128
+    N = 150_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    nm = nm.copy()
+    idx = rs.permutation(N)
+    nm[idx[:2000]] = 0.0
+    nm[idx[2000:4000]] *= -1.0
+    nm[idx[4000:4010]] = 1e30
+    nm[idx[4010:4020]] = -1e30
+    nm[idx[4020:4030]] = 1e-38
+    nm[idx[4030:4036]] = np.inf
+    nm[idx[4036:4040]] = -np.inf
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(1, d).astype(np.float32)
+    want = O.lut_scores_f32(q, p, nm, cen, R, 4)
+    for k in (1, 10, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = _topk_no_nan(want, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+@pytest.mark.parametrize("qscale", [0.0, 1e-36, 1e-20, 1e20, 1e34])
+def test_pairs_scan_one_query_extreme_queries(qscale):
+    # Queries that are zero (every score ties at 0: the lowest ids win) or whose scale
+    # leaves the fp16 filter's range (every row is rescored exactly) or nearly does.
+    rs = np.random.RandomState(31)
+    d = 64
+    N = 40_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    pairs = k_pack_pairs(p, d)
+    q = (rs.randn(1, d) * qscale).astype(np.float32)
+    want = O.lut_scores_f32(q, p, nm, cen, R, 4)
+    for k in (3, 10):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = _topk_no_nan(want, k)
+        assert np.array_equal(i, io), (qscale, k)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), (qscale, k)
+
+
+def test_pairs_scan_one_query_ulp_ties():
+    # 600 copies of the best row whose norms differ from it by a few ulps: their
+    # approximate scores cannot tell them apart, their exact scores can.
+    rs = np.random.RandomState(41)
+    d = 128
+    N = 80_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    q = rs.randn(1, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q, p, nm, cen, R, 4)))
+    idx = rs.choice(N, 600, replace=False)
+    p[idx] = p[top]
+    steps = rs.randint(-3, 4, size=600).astype(np.int32)
+    nm[idx] = (nm[top].view(np.int32) + steps).view(np.float32)
+    pairs = k_pack_pairs(p, d)
+    for k in (5, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = O.search_topk(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+def test_pairs_scan_one_query_past_4gib():
+    # 67.1M rows of d = 128 (4.3 GB of codes): rows past byte 2^32 are addressed with
+    # 64-bit bases.  Random codes, norm 0 except 200 planted rows spread over the whole
+    # range (most past 2^32 bytes); the answer is the planted rows with positive scores,
+    # then zero-score rows by lowest id.  Only the planted rows go through the oracle.
+    rs = np.random.RandomState(53)
+    d = 128
+    N = (1 << 26) + 1017
+    R = O.dense_qr_rotation(d, 42)
+    _, cen = O.lloyd_max_codebook(4, d)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    pairs = torch.randint(0, 256, (N, d // 2), dtype=torch.uint8, device=DEV, generator=g)
+    norms = torch.zeros(N, dtype=torch.float32, device=DEV)
+    planted = np.sort(rs.choice(np.arange(1000, N), 200, replace=False))
+    planted[-1] = N - 1
+    codes = rs.randint(0, 16, size=(200, d)).astype(np.uint8)
+    pn = (rs.rand(200) * 2 + 0.5).astype(np.float32)
+    pt = torch.from_numpy((codes[:, 0::2] << 4) | codes[:, 1::2]).to(DEV)
+    it = torch.from_numpy(planted).to(DEV)
+    pairs[it] = pt
+    norms[it] = torch.from_numpy(pn).to(DEV)
+    q = rs.randn(1, d).astype(np.float32)
+    ps = O.lut_scores_f32(q, O.pack_codes(codes, 4), pn, cen, R, 4)[0]
+    pos = [(float(ps[j]), int(planted[j])) for j in range(200) if ps[j] > 0]
+    pos.sort(key=lambda t: (-t[0], t[1]))
+    assert len(pos) >= 32
+    zero_ids = [j for j in range(64) if j not in set(planted.tolist())]
+    for k in (10, 32):
+        s, i = k_scan_pairs(q, pairs, norms, cen, R, k)
+        want_i = [t[1] for t in pos][:k]
+        want_s = np.array([t[0] for t in pos][:k], np.float32)
+        assert np.array_equal(i[0], np.array(want_i)), k
+        assert np.array_equal(s[0].view(np.uint32), want_s.view(np.uint32)), k
+    # three positive rows left: then the zero-score rows (norm 0) by lowest id
+    keep3 = {t[1] for t in pos[:3]}
+    drop = [int(planted[j]) for j in range(200) if ps[j] > 0 and int(planted[j]) not in keep3]
+    norms[torch.tensor(drop, device=DEV)] = 0.0
+    s, i = k_scan_pairs(q, pairs, norms, cen, R, 10)
+    want_i = [t[1] for t in pos[:3]] + zero_ids[:7]
+    assert np.array_equal(i[0], np.array(want_i))
+    assert np.array_equal(s[0, :3].view(np.uint32), np.array([t[0] for t in pos[:3]], np.float32).view(np.uint32))
+    assert (s[0, 3:] == 0).all()
+    del pairs, norms
+    torch.cuda.empty_cache()
 
 
 # ------------------------------------------------------------------ decode attention

@@ -1391,18 +1391,19 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
 //   Each row gets lo = approx - B and hi = approx + B.  Every wave keeps (th, thi) = the
 //   k-th best (lo, id) over the rows it has seen -- k distinct rows score at least their
 //   lo, so the k-th best exact (score, id) is at least (th, thi) -- and lists a row only
-//   when (hi, id) reaches it; a row below it cannot be in the answer.  A list that stays
-//   full after pruning (near-ties, duplicate rows) is rescored exactly in place, which
-//   leaves at most k entries.  Waves share th through LDS.  Each block writes its pruned
-//   list (at most k + kFsExtra entries).
-// Merge (filter_merge_kernel): the k-th best (lo, id) over all block lists, the entries
-// whose (hi, id) reach it rescored exactly, and their top k.
-constexpr int kFsThreads = 256;   // 4 waves; two blocks per CU
+//   when (hi, id) reaches it; a row below it cannot be in the answer.  A listed row's code
+//   bytes and norm are copied from the registers they arrived in to LDS beside its list
+//   entry, so rescoring it exactly never reads memory again.  A list that stays full after
+//   pruning (near-ties, duplicate rows) is rescored exactly in place, which leaves at most
+//   k entries.  Waves share th through LDS.  At the end every wave rescores its list
+//   exactly (at most k entries remain), each entry is ranked against the block's other
+//   waves' entries, and the block writes its exact top k.
+// Merge (filter_merge_kernel): the top k of the block lists.
+constexpr int kFsThreads = 512;   // 8 waves; one block per CU
 constexpr int kFsWaves = kFsThreads / 64;
 constexpr int kFsCap = 128;       // candidate slots per wave
 constexpr int kFsEager = 48;      // a list this long is pruned (and th published) at once
 constexpr int kHtabBytes = 256 * 256;  // byte value x 64 lane copies x fp16 centroid pair
-constexpr int kFsExtra = 4;       // a block list holds at most k + kFsExtra entries
 
 struct FilterArgs {
   const uint8_t* rows;  // [n][D / 2] pair layout
@@ -1413,11 +1414,8 @@ struct FilterArgs {
   const float* rot;     // [D][D]
   const float* cen;     // [16]
   int k;
-  int out;              // block list slots: k + kFsExtra
-  float* blo;           // [nq][nblocks][out] block lists (lo, hi, id)
-  float* bhi;
-  int32_t* bid;         // -1 past the list's length
-  float* qrot;          // [nq][D] q_rot, written by block 0 (for the merge's rescoring)
+  float* bs;            // [nq][nblocks][k] block lists: exact scores, best first
+  int32_t* bi;          // ids; -1 past the list's length
   float* out_s;         // [nq][k]
   int64_t* out_i;
 };
@@ -1425,7 +1423,8 @@ struct FilterArgs {
 typedef _Float16 fs_v8h __attribute__((ext_vector_type(8)));
 typedef float fs_v4f __attribute__((ext_vector_type(4)));
 
-// Exact score of one pair-layout row: the reference's arithmetic, as pair_scan_kernel.
+// Exact score of one pair-layout row (byte p = codes 2p (high nibble) and 2p + 1): the
+// reference's arithmetic, as pair_scan_kernel.  `row` is 16-byte aligned (LDS here).
 template <int D>
 __device__ __forceinline__ float exact_pair_score(const uint8_t* __restrict__ row, float n,
                                                   const float* qr, const float* cen) {
@@ -1452,15 +1451,47 @@ __device__ __forceinline__ float exact_pair_score(const uint8_t* __restrict__ ro
   return acc * n;
 }
 
+// The same score with every table read of a 32-dim chunk issued before the chunk's
+// dependent adds (for the block end; the in-loop rescoring keeps exact_pair_score's
+// smaller register footprint).
+template <int D>
+__device__ __forceinline__ float exact_pair_score_pipelined(const uint32_t* row, float n,
+                                                            const float* qr, const float* cen) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+#pragma unroll 1
+  for (int c = 0; c < D / 32; ++c) {
+    float p[32];
+    const u32x4 v = reinterpret_cast<const u32x4*>(row)[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int pl = 4 * wi + b, pg = 16 * c + pl;
+        const uint32_t byte = (w[wi] >> (8 * b)) & 0xFFu;
+        p[2 * pl] = qr[2 * pg] * cen[byte >> 4];
+        p[2 * pl + 1] = qr[2 * pg + 1] * cen[byte & 15u];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc = acc + p[j];
+  }
+  return acc * n;
+}
+
 __device__ __forceinline__ bool fs_keep(float hi, int id, float th, int thi) {
   return (hi > th) | ((hi == th) & (id <= thi));
 }
 
-// One wave's candidate list: LDS slots and the wave-uniform count and threshold.
+// One wave's candidate list in LDS: (lo, hi, id, norm) per entry, the entry's row codes
+// (RW words) in rw, and the wave-uniform count and threshold.
 struct FsList {
   float* lo;
   float* hi;
   int* id;
+  float* nr;
+  uint32_t* rw;
   int cnt;
   float th;
   int thi;
@@ -1470,12 +1501,110 @@ __device__ __forceinline__ int lane_prefix(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Order-preserving 32-bit key of a non-NaN float (-0 and +0 get the same key).
+__device__ __forceinline__ uint32_t fs_fkey(float x) {
+  const uint32_t b = __float_as_uint(x + 0.0f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float fs_unkey(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// The k-th best (score desc, id asc) of the wave's valid entries, NV per lane (at least k
+// of them, no NaN scores, distinct ids >= 0).  The k-th largest score key comes from a
+// 32-step binary search on counts (a compare mask and a scalar popcount per entry
+// register and step); when several entries share that score, the needed smallest id among
+// them from a 31-step search.  About 2 NV VALU ops per step, against n per entry for
+// ranking every entry against every other.
+template <int NV>
+__device__ __forceinline__ void wave_kth(const float* s, const int* id, const bool* v, int k,
+                                         float& ts, int& ti) {
+  uint32_t u[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) u[j] = v[j] ? fs_fkey(s[j]) : 0u;  // every real key is > 0
+  uint32_t x = 0;
+#pragma unroll 4
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t t = x | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) c += __popcll(__ballot(u[j] >= t));
+    if (c >= k) x = t;
+  }
+  int cg = 0, ce = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    cg += __popcll(__ballot(u[j] > x));
+    ce += __popcll(__ballot(u[j] == x));
+  }
+  ts = fs_unkey(x);
+  if (ce == 1) {
+    int t = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const uint64_t m = __ballot(u[j] == x);
+      if (m) t = __builtin_amdgcn_readlane(id[j], __ffsll((long long)m) - 1);
+    }
+    ti = t;
+  } else {  // the (k - cg)-th smallest id among the ties: largest y with fewer below it
+    const int need = k - cg;
+    uint32_t y = 0;
+#pragma unroll 1
+    for (int bit = 30; bit >= 0; --bit) {
+      const uint32_t t = y | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) c += __popcll(__ballot((u[j] == x) & ((uint32_t)id[j] < t)));
+      if (c < need) y = t;
+    }
+    ti = (int)y;
+  }
+}
+
+__device__ __forceinline__ int rank1(const float* s, const int* id, int n, float s0, int i0);
+
+// Ranks of the m LDS entries (cs[c], ci[c]) among themselves (entries with ci == INT_MAX
+// hold nothing and rank nowhere), with NT threads: each entry is ranked by up to 8
+// threads against a slice of the others (16-byte aligned slices: cs / ci readable and
+// padded with (-inf, INT_MAX) up to m rounded up to 4), the slices' counts summed into
+// rk[c] (zero on entry) with LDS atomics.  The caller syncs before reading rk.
+template <int NT>
+__device__ __forceinline__ void block_rank(const float* cs, const int* ci, int m, int* rk, int tid) {
+  if (m <= 0) return;
+  const int P = m >= NT ? 1 : (NT / m < 8 ? NT / m : 8);
+  const int chunk = (((m + P - 1) / P) + 3) & ~3;
+  for (int t = tid; t < m * P; t += NT) {
+    const int c = t % m, part = t / m, lo = part * chunk;
+    const int n = m - lo < chunk ? m - lo : chunk;
+    if ((n > 0) & (ci[c] != INT_MAX)) {
+      const int r = rank1(cs + lo, ci + lo, n, cs[c], ci[c]);
+      if (r) atomicAdd(rk + c, r);
+    }
+  }
+}
+
+__device__ __forceinline__ int rank1(const float* s, const int* id, int n, float s0, int i0) {
+  int r0 = 0;
+#pragma unroll 4
+  for (int f = 0; f < n; f += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(s + f);
+    const int4 b = *reinterpret_cast<const int4*>(id + f);
+    r0 += (f + 0 < n) & better(a.x, b.x, s0, i0);
+    r0 += (f + 1 < n) & better(a.y, b.y, s0, i0);
+    r0 += (f + 2 < n) & better(a.z, b.z, s0, i0);
+    r0 += (f + 3 < n) & better(a.w, b.w, s0, i0);
+  }
+  return r0;
+}
+
 // (th, thi) from the list's k-th best (lo, id) when it holds k entries or more (kept if
-// it beats the current one; found by ranking each entry against all of them, one
-// broadcast LDS read per entry), then the entries whose (hi, id) fall below it are dropped.
+// it beats the current one), then the entries whose (hi, id) fall below it are dropped
+// (the rest, with their row codes, move down to close the gaps).
+template <int RW>
 __device__ __forceinline__ void fs_prune(FsList& L, int k) {
   const int lane = threadIdx.x & 63;
-  float lo[2], hi[2];
+  float lo[2], hi[2], nr[2];
   int id[2];
   bool v[2];
 #pragma unroll
@@ -1485,53 +1614,64 @@ __device__ __forceinline__ void fs_prune(FsList& L, int k) {
     lo[r] = v[r] ? L.lo[e] : -INFINITY;
     hi[r] = v[r] ? L.hi[e] : -INFINITY;
     id[r] = v[r] ? L.id[e] : INT_MAX;
+    nr[r] = v[r] ? L.nr[e] : 0.f;
   }
   if (L.cnt >= k) {
-    int r0 = 0, r1 = 0;
-    for (int f = 0; f < L.cnt; ++f) {
-      const float lf = L.lo[f];
-      const int idf = L.id[f];
-      r0 += better(lf, idf, lo[0], id[0]);
-      r1 += better(lf, idf, lo[1], id[1]);
-    }
-    const uint64_t b0 = __ballot(v[0] & (r0 == k - 1)), b1 = __ballot(v[1] & (r1 == k - 1));
-    const int src = b0 ? __ffsll((long long)b0) - 1 : __ffsll((long long)b1) - 1;
-    const float ts = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b0 ? lo[0] : lo[1]), src));
-    const int ti = __builtin_amdgcn_readlane(b0 ? id[0] : id[1], src);
+    float ts;
+    int ti;
+    wave_kth<2>(lo, id, v, k, ts, ti);
     if (better(ts, ti, L.th, L.thi)) { L.th = ts; L.thi = ti; }
   }
   const bool k0 = v[0] & fs_keep(hi[0], id[0], L.th, L.thi);
   const bool k1 = v[1] & fs_keep(hi[1], id[1], L.th, L.thi);
   const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
   const int n0 = __popcll(m0);
+  const int p0 = lane_prefix(m0), p1 = n0 + lane_prefix(m1);
+  // rows that move are read before any entry is written (a destination slot may hold a
+  // row that has yet to move)
+  const bool mv0 = k0 & (p0 != lane), mv1 = k1 & (p1 != lane + 64);
+  u32x4 w0[RW / 4], w1[RW / 4];
+  const u32x4* s0 = reinterpret_cast<const u32x4*>(L.rw + lane * RW);
+  const u32x4* s1 = reinterpret_cast<const u32x4*>(L.rw + (lane + 64) * RW);
+#pragma unroll
+  for (int j = 0; j < RW / 4; ++j) {
+    w0[j] = mv0 ? s0[j] : (u32x4){0u, 0u, 0u, 0u};
+    w1[j] = mv1 ? s1[j] : (u32x4){0u, 0u, 0u, 0u};
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   if (k0) {
-    const int p = lane_prefix(m0);
-    L.lo[p] = lo[0]; L.hi[p] = hi[0]; L.id[p] = id[0];
+    L.lo[p0] = lo[0]; L.hi[p0] = hi[0]; L.id[p0] = id[0]; L.nr[p0] = nr[0];
+    if (mv0) {
+      u32x4* d = reinterpret_cast<u32x4*>(L.rw + p0 * RW);
+#pragma unroll
+      for (int j = 0; j < RW / 4; ++j) d[j] = w0[j];
+    }
   }
   if (k1) {
-    const int p = n0 + lane_prefix(m1);
-    L.lo[p] = lo[1]; L.hi[p] = hi[1]; L.id[p] = id[1];
+    L.lo[p1] = lo[1]; L.hi[p1] = hi[1]; L.id[p1] = id[1]; L.nr[p1] = nr[1];
+    if (mv1) {
+      u32x4* d = reinterpret_cast<u32x4*>(L.rw + p1 * RW);
+#pragma unroll
+      for (int j = 0; j < RW / 4; ++j) d[j] = w1[j];
+    }
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   L.cnt = n0 + __popcll(m1);
 }
 
-// Rescore every entry with the reference's arithmetic (lo = hi = the exact score; NaN
-// scores are never listed), then prune: at most k entries remain.
+// Rescore every entry with the reference's arithmetic from its row codes in LDS (lo = hi
+// = the exact score; NaN scores are never listed), then prune: at most k entries remain.
 template <int D>
-__device__ __forceinline__ void fs_exact(FsList& L, int k, const uint8_t* __restrict__ rows,
-                                         const float* __restrict__ norms, const float* qr,
-                                         const float* cen) {
+__device__ __forceinline__ void fs_exact(FsList& L, int k, const float* qr, const float* cen) {
+  constexpr int RW = D / 8;
   const int lane = threadIdx.x & 63;
 #pragma unroll 1
   for (int r = 0; r < 2; ++r) {
     const int e = lane + 64 * r;
     if (e < L.cnt) {
-      const int id = L.id[e];
-      const float s = exact_pair_score<D>(rows + (size_t)id * (D / 2), norms[id], qr, cen);
+      const float s = exact_pair_score<D>(reinterpret_cast<const uint8_t*>(L.rw + e * RW), L.nr[e], qr, cen);
       const bool nan = __builtin_isnan(s);
       L.lo[e] = nan ? -INFINITY : s;
       L.hi[e] = nan ? __builtin_nanf("") : s;  // fs_keep fails for NaN: dropped
@@ -1539,7 +1679,7 @@ __device__ __forceinline__ void fs_exact(FsList& L, int k, const uint8_t* __rest
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  fs_prune(L, k);
+  fs_prune<RW>(L, k);
 }
 
 // Best of this wave's threshold and the ones the block's other waves published (a
@@ -1560,152 +1700,129 @@ __device__ __forceinline__ uint32_t fs_hlook(uint32_t w, uint32_t lane4, const c
   return *reinterpret_cast<const uint32_t*>(htab + addr);
 }
 
-// Per query, one kFmThreads block after the filter: every block-list slot (a.out slots of
-// (lo, hi, id) per block, id -1 past the list's length) is loaded in one round into
-// registers, NR per thread.  tau = the k-th best of 64 group maxima of (lo, id) (groups of
-// 8 threads; k distinct rows, each scoring at least its lo) bounds the answer from below;
-// the entries whose (hi, id) reach it are rescored with the reference's arithmetic (q_rot
-// from the filter's block 0) and rank-sorted, with (-inf, -1) pads.  More than kMergeCap
-// of them (near-ties across blocks): slot r of every thread at a time, rescored and merged
-// into a running top k.
+// Per query, one kFmThreads block after the filter: the block lists (k exact (score, id)
+// per block, best first, id -1 past a list's length) are loaded in one round into
+// registers, NR slots per thread.  tau = the best over the waves of the k-th best of the
+// wave's share of the block bests (ranked by register broadcast within the wave): k
+// distinct rows score at least tau, so every row of the answer does too.  The entries at
+// or above tau (tens on real data) are ranked among themselves by all threads, with
+// (-inf, -1) pads; more than kFmCap of them (ties across blocks) take k rounds of a
+// block-wide arg-best instead.
 constexpr int kFmThreads = 512;
 constexpr int kFmWaves = kFmThreads / 64;
-constexpr int kFmRegs = 40;  // list slots per thread: 512 blocks x (32 + 4) / 512 = 36
+constexpr int kFmRegs = 40;    // list slots per thread
+constexpr int kFmCap = 512;    // survivors ranked in LDS
 
-template <int D, int NR>
-__global__ __launch_bounds__(kFmThreads) void filter_merge_kernel(FilterArgs a, int nslots) {
-#pragma clang fp contract(off)
-  __shared__ float qr[D];
-  __shared__ float cen[16];
-  __shared__ __attribute__((aligned(16))) float gs[64];
-  __shared__ __attribute__((aligned(16))) int gi[64];
-  __shared__ float ss[kMergeCap + kFmThreads];
-  __shared__ int si[kMergeCap + kFmThreads];
-  __shared__ int cnt_s, nvalid_s, taui_s;
-  __shared__ float tau_s;
+template <int NR>
+__global__ __launch_bounds__(kFmThreads) void filter_merge_kernel(FilterArgs a, int nblocks) {
+  __shared__ __attribute__((aligned(16))) float ss[kFmCap + 4];
+  __shared__ __attribute__((aligned(16))) int si[kFmCap + 4];
+  __shared__ int rk[kFmCap];
+  __shared__ float wb_s[kFmWaves];
+  __shared__ int wb_i[kFmWaves];
+  __shared__ int cnt_s;
   const int q = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int k = a.k;
+  const int nslots = nblocks * k;
   const size_t base = (size_t)q * nslots;
   float* os = a.out_s + (size_t)q * k;
   int64_t* oi = a.out_i + (size_t)q * k;
-  // q_rot and centroids first: their waits then do not wait for the slots behind them
-  float qv = 0.f;
-  if (tid < D) qv = a.qrot[(size_t)q * D + tid];
-  else if (tid < D + 16) qv = a.cen[tid - D];
-  float el[NR], eh[NR];
+  float es[NR];
   int ei[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int e = tid + kFmThreads * r;
     const size_t ec = base + (size_t)(e < nslots ? e : nslots - 1);
-    const float lo = a.blo[ec], hi = a.bhi[ec];
-    const int id = a.bid[ec];
+    const float s = a.bs[ec];
+    const int id = a.bi[ec];
     const bool ok = (e < nslots) & (id >= 0);
-    el[r] = ok ? lo : -INFINITY;
-    eh[r] = ok ? hi : -INFINITY;
+    es[r] = ok ? s : -INFINITY;
     ei[r] = ok ? id : INT_MAX;
   }
-  if (tid < D) qr[tid] = qv;
-  else if (tid < D + 16) cen[tid - D] = qv;
+  // this wave's share of the block bests: blocks wave * per .. + per - 1, one per lane
+  const int per = (nblocks + kFmWaves - 1) / kFmWaves;
   float bs = -INFINITY;
   int bi = INT_MAX;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const bool take = (ei[r] != INT_MAX) & ((bi == INT_MAX) | better(el[r], ei[r], bs, bi));
-    bs = take ? el[r] : bs;
-    bi = take ? ei[r] : bi;
+  {
+    const int b = wave * per + lane;
+    const bool in = (lane < per) & (b < nblocks);
+    const size_t ec = base + (size_t)(in ? b : 0) * k;
+    const float x = a.bs[ec];
+    const int id = a.bi[ec];
+    if (in & (id >= 0)) { bs = x; bi = id; }
   }
-  best_step<0xB1, 0xF>(bs, bi);   // quad_perm [1,0,3,2]
-  best_step<0x4E, 0xF>(bs, bi);   // quad_perm [2,3,0,1]
-  best_step<0x141, 0xF>(bs, bi);  // row_half_mirror: 8-lane groups
-  if ((lane & 7) == 0) { gs[tid >> 3] = bs; gi[tid >> 3] = bi; }
-  if (tid == 0) { cnt_s = 0; nvalid_s = 0; tau_s = -INFINITY; taui_s = INT_MAX; }
-  __syncthreads();
-  if (wave == 0) {
-    const float s0 = gs[lane];
-    const int i0 = gi[lane];
-    int rank = 0;
-#pragma unroll 4
-    for (int j = 0; j < 64; j += 4) {
-      const float4 s4 = *reinterpret_cast<const float4*>(gs + j);
-      const int4 i4 = *reinterpret_cast<const int4*>(gi + j);
-      rank += (i4.x != INT_MAX) & better(s4.x, i4.x, s0, i0);
-      rank += (i4.y != INT_MAX) & better(s4.y, i4.y, s0, i0);
-      rank += (i4.z != INT_MAX) & better(s4.z, i4.z, s0, i0);
-      rank += (i4.w != INT_MAX) & better(s4.w, i4.w, s0, i0);
+  if (tid == 0) cnt_s = 0;
+  {  // rank of each lane's block best among the wave's (per <= 64 of them)
+    int r = 0;
+    for (int j = 0; j < per && j < 64; ++j) {
+      const float sj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), j));
+      const int ij = __builtin_amdgcn_readlane(bi, j);
+      r += (ij != INT_MAX) & better(sj, ij, bs, bi);
     }
-    if ((i0 != INT_MAX) & (rank == k - 1)) { tau_s = s0; taui_s = i0; }
+    const uint64_t hit = __ballot((bi != INT_MAX) & (r == k - 1));
+    float ts = -INFINITY;
+    int ti = INT_MAX;
+    if (hit) {
+      const int src = __ffsll((long long)hit) - 1;
+      ts = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bs), src));
+      ti = __builtin_amdgcn_readlane(bi, src);
+    }
+    if (lane == 0) { wb_s[wave] = ts; wb_i[wave] = ti; }
   }
   __syncthreads();
-  // survivors: (hi, id) at or above tau
-  const float tau = tau_s;
-  const int taui = taui_s;
+  float tau = -INFINITY;
+  int taui = INT_MAX;  // no wave holds k lists: every entry survives
+#pragma unroll
+  for (int w = 0; w < kFmWaves; ++w)
+    if ((wb_i[w] != INT_MAX) & ((taui == INT_MAX) | better(wb_s[w], wb_i[w], tau, taui))) { tau = wb_s[w]; taui = wb_i[w]; }
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    if ((ei[r] != INT_MAX) & fs_keep(eh[r], ei[r], tau, taui)) {
+    if ((ei[r] != INT_MAX) & fs_keep(es[r], ei[r], tau, taui)) {
       const int p = atomicAdd(&cnt_s, 1);
-      if (p < kMergeCap) si[p] = ei[r];
+      if (p < kFmCap) { ss[p] = es[r]; si[p] = ei[r]; rk[p] = 0; }
     }
   }
   __syncthreads();
   const int m = cnt_s;
-  if (m <= kMergeCap) {
-    // rescored exactly; NaN scores are never listed
-    for (int e = tid; e < m; e += kFmThreads) {
-      const int id = si[e];
-      const float sc = exact_pair_score<D>(a.rows + (size_t)id * (D / 2), a.norms[id], qr, cen);
-      ss[e] = sc;
-      if (!__builtin_isnan(sc)) atomicAdd(&nvalid_s, 1);
-    }
+  if (m <= kFmCap) {
+    if (tid < (((m + 3) & ~3) - m)) { ss[m + tid] = -INFINITY; si[m + tid] = INT_MAX; }
     __syncthreads();
-    for (int e = tid; e < m; e += kFmThreads) {
-      const float se = ss[e];
-      const int ie = si[e];
-      if (__builtin_isnan(se)) continue;
-      int rank = 0;
-      for (int f = 0; f < m; ++f) rank += better(ss[f], si[f], se, ie);
-      if (rank < k) { os[rank] = se; oi[rank] = ie; }
-    }
-    for (int e = nvalid_s + tid; e < k; e += kFmThreads) { os[e] = -INFINITY; oi[e] = -1; }
+    block_rank<kFmThreads>(ss, si, m, rk, tid);
+    __syncthreads();
+    for (int e = tid; e < m; e += kFmThreads)
+      if (rk[e] < k) { os[rk[e]] = ss[e]; oi[rk[e]] = si[e]; }
+    for (int e = m + tid; e < k; e += kFmThreads) { os[e] = -INFINITY; oi[e] = -1; }
     return;  // uniform
   }
-  // more survivors than kMergeCap: slot r of every thread at a time, rescored and merged
-  // into a running top k in ss / si[0, k)
-  if (tid < k) { ss[tid] = -INFINITY; si[tid] = INT_MAX; }
-  __syncthreads();
+  // k rounds: the best survivor not emitted yet (every entry strictly below the last one)
+  float last_s = INFINITY;
+  int last_i = -1;
 #pragma unroll 1
-  for (int r = 0; r < NR; ++r) {
-    bool svr = false;
-    int idr = INT_MAX;
+  for (int r = 0; r < k; ++r) {
+    float cs = -INFINITY;
+    int ci = INT_MAX;
 #pragma unroll
-    for (int u = 0; u < NR; ++u)
-      if (u == r) { svr = (ei[u] != INT_MAX) & fs_keep(eh[u], ei[u], tau, taui); idr = ei[u]; }
-    float sc = -INFINITY;
-    int id = INT_MAX;
-    if (svr) {
-      const float x = exact_pair_score<D>(a.rows + (size_t)idr * (D / 2), a.norms[idr], qr, cen);
-      if (!__builtin_isnan(x)) { sc = x; id = idr; }
+    for (int u = 0; u < NR; ++u) {
+      const bool c = (ei[u] != INT_MAX) & fs_keep(es[u], ei[u], tau, taui) &
+                     better(last_s, last_i, es[u], ei[u]);
+      if (c & ((ci == INT_MAX) | better(es[u], ei[u], cs, ci))) { cs = es[u]; ci = ei[u]; }
     }
-    ss[k + tid] = sc;
-    si[k + tid] = id;
+    wave_best(cs, ci);
     __syncthreads();
-    float ns = -INFINITY;
-    int ni = INT_MAX, nrank = k;
-    for (int e = tid; e < k + kFmThreads; e += kFmThreads) {
-      const float se = ss[e];
-      const int ie = si[e];
-      int rank = 0;
-      for (int f = 0; f < k + kFmThreads; ++f) rank += better(ss[f], si[f], se, ie);
-      if ((ie != INT_MAX) & (rank < k)) { ns = se; ni = ie; nrank = rank; }
+    if (lane == 0) { wb_s[wave] = cs; wb_i[wave] = ci; }
+    __syncthreads();
+    cs = wb_s[0];
+    ci = wb_i[0];
+#pragma unroll
+    for (int w = 1; w < kFmWaves; ++w)
+      if ((wb_i[w] != INT_MAX) & ((ci == INT_MAX) | better(wb_s[w], wb_i[w], cs, ci))) { cs = wb_s[w]; ci = wb_i[w]; }
+    last_s = cs;
+    last_i = ci;
+    if (tid == 0) {
+      os[r] = ci == INT_MAX ? -INFINITY : cs;
+      oi[r] = ci == INT_MAX ? -1 : ci;
     }
-    __syncthreads();
-    if (nrank < k) { ss[nrank] = ns; si[nrank] = ni; }
-    __syncthreads();
-  }
-  for (int e = tid; e < k; e += kFmThreads) {
-    os[e] = si[e] == INT_MAX ? -INFINITY : ss[e];
-    oi[e] = si[e] == INT_MAX ? -1 : si[e];
   }
 }
 
@@ -1719,18 +1836,21 @@ pair_filter_kernel(FilterArgs a) {
   constexpr int RB = D / 2;   // bytes per row
   constexpr int KT = D / 32;  // MFMA k tiles per row
   constexpr int LW = D / 32;  // 32-bit words per lane per 16-row tile (16 B at D=128, 8 B at 64)
+  constexpr int RW = D / 8;   // 32-bit words per row
   __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
   __shared__ float qs_s[D];
   __shared__ float qr_s[D];
   __shared__ float cen_s[16];
   __shared__ float red_s[2 * kFsWaves];
   __shared__ float th_s[kFsWaves];
-  __shared__ float lo_s[kFsWaves * kFsCap];
+  __shared__ int thi_s[kFsWaves];
+  __shared__ int ncand_s, nvalid_s;
+  __shared__ __attribute__((aligned(16))) float lo_s[kFsWaves * kFsCap];
   __shared__ float hi_s[kFsWaves * kFsCap];
-  __shared__ int id_s[kFsWaves * kFsCap];
+  __shared__ __attribute__((aligned(16))) int id_s[kFsWaves * kFsCap];
+  __shared__ float nr_s[kFsWaves * kFsCap];
+  __shared__ __attribute__((aligned(16))) uint32_t rw_s[kFsWaves * kFsCap * RW];  // row codes
   __shared__ int cnt_s[kFsWaves];
-  __shared__ float wth_s[kFsWaves];
-  __shared__ int wthi_s[kFsWaves];
 
   const int q = blockIdx.y;
   // wave-uniform (readfirstlane) so row offsets and buffer resources live in SGPRs
@@ -1896,7 +2016,8 @@ pair_filter_kernel(FilterArgs a) {
     return __uint_as_float(s[0]);
   };
 
-  FsList L{lo_s + wave * kFsCap, hi_s + wave * kFsCap, id_s + wave * kFsCap, 0, -INFINITY, INT_MAX};
+  FsList L{lo_s + wave * kFsCap, hi_s + wave * kFsCap, id_s + wave * kFsCap,
+           nr_s + wave * kFsCap, rw_s + wave * kFsCap * RW, 0, -INFINITY, INT_MAX};
   // Per step the common case costs two multiplies, an fma and a compare: hi >= th can only
   // hold for a row that beats th's float (NaN passes too); the rest -- row validity, the
   // exact (hi, id) test, lo, non-finite scores -- runs only when some lane passes.
@@ -1917,27 +2038,43 @@ pair_filter_kernel(FilterArgs a) {
     int nnew = __popcll(mask);
     if (L.cnt + nnew > kFsCap) {
       fs_share(L, th_s, wave);
-      fs_prune(L, a.k);
+      fs_prune<RW>(L, a.k);
       ins = valid & fs_keep(hi, id, L.th, L.thi);
       mask = __ballot(ins);
       nnew = __popcll(mask);
       if (L.cnt + nnew > kFsCap) {
-        fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);
+        fs_exact<D>(L, a.k, qr_s, cen_s);
         ins = valid & fs_keep(hi, id, L.th, L.thi);
         mask = __ballot(ins);
         nnew = __popcll(mask);
       }
+      if (mask == 0) return;
     }
     if (ins) {
       const int p = L.cnt + lane_prefix(mask);
-      L.lo[p] = lo; L.hi[p] = hi; L.id[p] = id;
+      L.lo[p] = lo; L.hi[p] = hi; L.id[p] = id; L.nr[p] = rb.n;
+    }
+    // the listed rows' codes, from the lanes that loaded them: in tile rt this lane holds
+    // LW words of row 16 rt + (lane & 15) at word LW (lane >> 4)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int r = 16 * rt + (lane & 15);
+      if ((mask >> r) & 1) {
+        const int p = L.cnt + __popcll(mask & ((1ull << r) - 1));
+        uint32_t* d = L.rw + p * RW + LW * (lane >> 4);
+        if constexpr (LW == 4) {
+          *reinterpret_cast<u32x4*>(d) = (u32x4){rb.w[4 * rt], rb.w[4 * rt + 1], rb.w[4 * rt + 2], rb.w[4 * rt + 3]};
+        } else {
+          *reinterpret_cast<u32x2*>(d) = (u32x2){rb.w[2 * rt], rb.w[2 * rt + 1]};
+        }
+      }
     }
     L.cnt += nnew;
     // raise th early -- from the first k rows, then whenever the list grows long -- and
     // share it with the block's other waves: fewer inserts for all of them
     if ((L.cnt >= kFsEager) | ((L.th == -INFINITY) & (L.cnt >= a.k))) {
       fs_share(L, th_s, wave);
-      fs_prune(L, a.k);
+      fs_prune<RW>(L, a.k);
       fs_share(L, th_s, wave);
     }
   };
@@ -1957,61 +2094,51 @@ pair_filter_kernel(FilterArgs a) {
     load(t + 3, tb);
   }
 
-  // ---- block list: each wave pruned (at most kMaxK entries, exact if it had more), then
-  // wave 0 prunes the union with the best of the waves' and the call's thresholds.
-  fs_share(L, th_s, wave);
-  fs_prune(L, a.k);
-  if (L.cnt > kMaxK) fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);
-  if (lane == 0) { cnt_s[wave] = L.cnt; wth_s[wave] = L.th; wthi_s[wave] = L.thi; }
+  // ---- block list.  (bt, bti) = the best of the waves' thresholds (each is the k-th best
+  // (lo, id) of some rows of its wave, so it bounds the block's answer from below).  The
+  // entries whose (hi, id) reach it (about 50 on random data) are gathered, rescored
+  // exactly one per thread from their row codes in LDS, and ranked among themselves; the
+  // block's top k go to its slots in rank order, with (-inf, -1) past the end.  The
+  // candidate arrays reuse the table's LDS, which no wave reads after its loop.
+  if (lane == 0) { th_s[wave] = L.th; thi_s[wave] = L.thi; }
+  if (tid == 0) { ncand_s = 0; nvalid_s = 0; }
   __syncthreads();
-  const size_t bslot = (size_t)q * gridDim.x + blockIdx.x;
-  if (wave == 0) {
-    int total = 0;
-    int off[kFsWaves];
+  float bt = th_s[0];
+  int bti = thi_s[0];
 #pragma unroll
-    for (int w = 0; w < kFsWaves; ++w) {
-      off[w] = total;
-      total += cnt_s[w];
-      if (better(wth_s[w], wthi_s[w], L.th, L.thi)) { L.th = wth_s[w]; L.thi = wthi_s[w]; }
-    }
-    // gather the other waves' entries behind wave 0's (at most 4 x 32 = 128 in all)
-    float glo[2], ghi[2];
-    int gid[2];
+  for (int w = 1; w < kFsWaves; ++w)
+    if (better(th_s[w], thi_s[w], bt, bti)) { bt = th_s[w]; bti = thi_s[w]; }
+  int* cslot = reinterpret_cast<int*>(htab);                                  // [kFsWaves * kFsCap]
+  float* cs = reinterpret_cast<float*>(htab + 4 * kFsWaves * kFsCap);        // exact scores
+  int* ci = reinterpret_cast<int*>(htab + 8 * kFsWaves * kFsCap);            // ids (INT_MAX: NaN)
+  int* rk = reinterpret_cast<int*>(htab + 12 * kFsWaves * kFsCap);           // ranks
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = lane + 64 * r;
-      int slot = e;  // wave 0's entries stay where they are
-#pragma unroll
-      for (int u = 1; u < kFsWaves; ++u) slot = e >= off[u] ? u * kFsCap + (e - off[u]) : slot;
-      const bool v = e < total;
-      glo[r] = v ? lo_s[slot] : 0.f;
-      ghi[r] = v ? hi_s[slot] : 0.f;
-      gid[r] = v ? id_s[slot] : 0;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = lane + 64 * r;
-      if (e < total) { L.lo[e] = glo[r]; L.hi[e] = ghi[r]; L.id[e] = gid[r]; }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    L.cnt = total;
-    fs_prune(L, a.k);
-    if (L.cnt > a.out) fs_exact<D>(L, a.k, a.rows, a.norms, qr_s, cen_s);  // then at most k
-    // every slot: id -1 past the list's length
-    const size_t base = bslot * a.out;
-    for (int e = lane; e < a.out; e += 64) {
-      const bool v = e < L.cnt;
-      a.blo[base + e] = v ? L.lo[e] : -INFINITY;
-      a.bhi[base + e] = v ? L.hi[e] : -INFINITY;
-      a.bid[base + e] = v ? L.id[e] : -1;
-    }
+  for (int r = 0; r < 2; ++r) {
+    const int e = lane + 64 * r;
+    if ((e < L.cnt) && fs_keep(L.hi[e], L.id[e], bt, bti)) cslot[atomicAdd(&ncand_s, 1)] = wave * kFsCap + e;
   }
-  if (blockIdx.x == 0 && tid < D) a.qrot[(size_t)q * D + tid] = qr_s[tid];  // for the merge
+  __syncthreads();
+  const int m = ncand_s;
+  for (int t = tid; t < m; t += kFsThreads) {
+    const int sl = cslot[t];
+    const float x = exact_pair_score_pipelined<D>(rw_s + sl * RW, nr_s[sl], qr_s, cen_s);
+    const bool ok = !__builtin_isnan(x);
+    cs[t] = ok ? x : -INFINITY;
+    ci[t] = ok ? id_s[sl] : INT_MAX;  // (-inf, INT_MAX) ranks below every listed row
+    rk[t] = 0;
+    if (ok) atomicAdd(&nvalid_s, 1);
+  }
+  for (int t = m + tid; t < ((m + 3) & ~3); t += kFsThreads) { cs[t] = -INFINITY; ci[t] = INT_MAX; }
+  __syncthreads();
+  block_rank<kFsThreads>(cs, ci, m, rk, tid);
+  __syncthreads();
+  const size_t base = ((size_t)q * gridDim.x + blockIdx.x) * a.k;
+  for (int t = tid; t < m; t += kFsThreads) {
+    const int id = ci[t], rank = rk[t];
+    if ((id != INT_MAX) & (rank < a.k)) { a.bs[base + rank] = cs[t]; a.bi[base + rank] = id; }
+  }
+  for (int e = nvalid_s + tid; e < a.k; e += kFsThreads) { a.bs[base + e] = -INFINITY; a.bi[base + e] = -1; }
 }
-
 
 // ------------------------------------------------------------------ softmax stats
 // stats[q] = (max_t s, sum_t exp(s - max)) over the valid tokens of query q's stream.
@@ -2321,22 +2448,21 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   return fail(TQ_EINVAL, "bit_width must be 1-4, got %d", bits);
 }
 
-// Row blocks of the filtered pair scan: two 4-wave blocks per CU, fewer when there are
+// Row blocks of the filtered pair scan: one 8-wave block per CU, fewer when there are
 // fewer 64-row groups than waves.
 int filter_blocks(int64_t nrows) {
   const int64_t groups = (nrows + 63) / 64;
   const int64_t want = (groups + kFsWaves - 1) / kFsWaves;
-  const int64_t cap = (int64_t)device_cu_count() * 2;
+  const int64_t cap = (int64_t)device_cu_count();
   const int64_t b = want < cap ? want : cap;
   return (int)(b < 1 ? 1 : b);
 }
 
-// Workspace of the filtered pair scan: block lists (lo, hi, id) of k + kFsExtra entries,
-// their counts, q_rot per query.
+// Workspace of the filtered pair scan: the block lists, k (score, id) per block and query.
 size_t filter_workspace_bytes(int64_t nq, int d, int64_t N, int k) {
+  (void)d;
   const size_t nb = (size_t)filter_blocks(N);
-  const size_t out = (size_t)k + kFsExtra;
-  return align_up((size_t)nq * nb * out * 4, 256) * 3 + align_up((size_t)nq * d * 4, 256);
+  return align_up((size_t)nq * nb * k * 4, 256) * 2;
 }
 
 template <int D>
@@ -2345,11 +2471,11 @@ int launch_filter_d(const FilterArgs& f, int nb, int nq, bool big, hipStream_t s
   if (big) hipLaunchKernelGGL((pair_filter_kernel<D, true>), grid, dim3(kFsThreads), 0, st, f);
   else hipLaunchKernelGGL((pair_filter_kernel<D, false>), grid, dim3(kFsThreads), 0, st, f);
   TQ_LAUNCH_CHECK("pair_filter_kernel");
-  const int nslots = nb * f.out;
+  const int nslots = nb * f.k;
   const dim3 mg((unsigned)nq);
-  if (nslots <= 4 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<D, 4>), mg, dim3(kFmThreads), 0, st, f, nslots);
-  else if (nslots <= 16 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<D, 16>), mg, dim3(kFmThreads), 0, st, f, nslots);
-  else hipLaunchKernelGGL((filter_merge_kernel<D, kFmRegs>), mg, dim3(kFmThreads), 0, st, f, nslots);
+  if (nslots <= 4 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<4>), mg, dim3(kFmThreads), 0, st, f, nb);
+  else if (nslots <= 16 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<16>), mg, dim3(kFmThreads), 0, st, f, nb);
+  else hipLaunchKernelGGL((filter_merge_kernel<kFmRegs>), mg, dim3(kFmThreads), 0, st, f, nb);
   TQ_LAUNCH_CHECK("filter_merge_kernel");
   return TQ_OK;
 }
@@ -2359,18 +2485,13 @@ int launch_filter(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, 
                   int32_t k, float* out_scores, int64_t* out_ids, char* ws, hipStream_t st) {
   TQ_REQUIRE(nq <= 65535, "too many queries in one call");
   const int nb = filter_blocks(N);
-  const int out = k + kFsExtra;
-  TQ_REQUIRE(nb * out <= kFmRegs * kFmThreads, "too many block lists for the merge");
+  TQ_REQUIRE(nb * k <= kFmRegs * kFmThreads && nb <= 64 * kFmWaves, "too many block lists for the merge");
   FilterArgs f{};
   f.rows = pairs; f.norms = norms; f.n = N; f.q = queries; f.q_dt = q_dtype; f.rot = rotation;
-  f.cen = centroids; f.k = k; f.out = out;
-  f.blo = reinterpret_cast<float*>(ws);
-  ws += align_up((size_t)nq * nb * out * 4, 256);
-  f.bhi = reinterpret_cast<float*>(ws);
-  ws += align_up((size_t)nq * nb * out * 4, 256);
-  f.bid = reinterpret_cast<int32_t*>(ws);
-  ws += align_up((size_t)nq * nb * out * 4, 256);
-  f.qrot = reinterpret_cast<float*>(ws);
+  f.cen = centroids; f.k = k;
+  f.bs = reinterpret_cast<float*>(ws);
+  ws += align_up((size_t)nq * nb * k * 4, 256);
+  f.bi = reinterpret_cast<int32_t*>(ws);
   f.out_s = out_scores; f.out_i = out_ids;
   // 32-bit offsets while rows and norms stay under 2^32 bytes
   const bool big = N * (d / 2) >= ((int64_t)1 << 32) - 4096 || N * 4 >= ((int64_t)1 << 32) - 4096;
