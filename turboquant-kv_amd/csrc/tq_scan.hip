@@ -1383,11 +1383,17 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
 // dozen VALU instructions, against 128 multiplies and 128 dependent adds per row for the
 // reference's arithmetic: the scan runs at the HBM streaming rate instead of the VALU
 // rate.
-//   Bound: |approx - exact| <= |n| * beta, beta = 2^-10 * ||q_rot||_1 * max|c|.  The fp16
-//   centroids are within 2^-11 relative, the hi + lo query within 2^-22, fp32 accumulation
-//   of 256 exact products within 256 * 2^-23 relative and the exact sum within 128 * 2^-24,
-//   all relative to sum_j |q_j c_j| <= ||q_rot||_1 * max|c| (about 2^-10.9 in all; the
-//   worst case measured on 12M random and adversarial rows was 2^-12.3).
+//   Bound: |approx - exact| <= |n| * beta with
+//     beta = ||q_rot||_1 * (e_c + 2^-14 max|c|) * (1 + 2^-10),  e_c = max_i |c_i - fp16(c_i)|.
+//   Terms, each times ||q_rot||_1: the fp16 centroids e_c (computed, not assumed: inf when a
+//   centroid overflows fp16, which turns the filter off); the hi + lo query split 2^-22
+//   max|c| (plus 128 * 2^-25 / scale, far below); fp32 accumulation of the 256 exact
+//   products of the MFMAs, 256 * 2^-23 max|c|; the reference's own sequential sum,
+//   128 * 2^-24 max|c|; the two final multiplies by n, 2^-23 max|c|: 2^-14.5 max|c| in all
+//   but e_c.  The (1 + 2^-10) covers the rounding of ||q_rot||_1 and of sa +- B (B >= 2^-14
+//   |sa| / (1 + 2^-10), so rounding sa + B moves it by less than 2^-10 B).  For the 4-bit
+//   Lloyd-Max tables e_c = 2^-12.1 max|c| (d = 128) and 2^-11.6 max|c| (d = 64); the worst
+//   |approx - exact| measured on 12M random and adversarial rows was 2^-12.3 ||q||_1 max|c|.
 //   Each row gets lo = approx - B and hi = approx + B.  Every wave keeps (th, thi) = the
 //   k-th best (lo, id) over the rows it has seen -- k distinct rows score at least their
 //   lo, so the k-th best exact (score, id) is at least (th, thi) -- and lists a row only
@@ -1777,10 +1783,15 @@ __global__ __launch_bounds__(kFmThreads) void filter_merge_kernel(FilterArgs a, 
   for (int w = 0; w < kFmWaves; ++w)
     if ((wb_i[w] != INT_MAX) & ((taui == INT_MAX) | better(wb_s[w], wb_i[w], tau, taui))) { tau = wb_s[w]; taui = wb_i[w]; }
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    if ((ei[r] != INT_MAX) & fs_keep(es[r], ei[r], tau, taui)) {
-      const int p = atomicAdd(&cnt_s, 1);
-      if (p < kFmCap) { ss[p] = es[r]; si[p] = ei[r]; rk[p] = 0; }
+  for (int r = 0; r < NR; ++r) {  // one LDS atomic per wave and register
+    const bool kp = (ei[r] != INT_MAX) & fs_keep(es[r], ei[r], tau, taui);
+    const uint64_t km = __ballot(kp);
+    if (km) {
+      int p0 = 0;
+      if (lane == 0) p0 = atomicAdd(&cnt_s, __popcll(km));
+      p0 = __builtin_amdgcn_readfirstlane(p0);
+      const int p = p0 + lane_prefix(km);
+      if (kp & (p < kFmCap)) { ss[p] = es[r]; si[p] = ei[r]; rk[p] = 0; }
     }
   }
   __syncthreads();
@@ -1968,6 +1979,9 @@ pair_filter_kernel(FilterArgs a) {
   for (int w = 0; w < kFsWaves; ++w) { amax = fmaxf(amax, red_s[w]); l1 = l1 + red_s[kFsWaves + w]; }
 #pragma unroll
   for (int i = 0; i < 16; ++i) cmax = fmaxf(cmax, fabsf(cen_s[i]));
+  float ec = 0.f;  // largest fp16 rounding error of a centroid (inf if one overflows fp16)
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ec = fmaxf(ec, fabsf(cen_s[i] - (float)(_Float16)cen_s[i]));
   // scale: max |q_rot| * scale in [2^14, 2^15); a query whose scale would leave fp32's
   // range gets beta = inf (every row is then rescored exactly).
   int ex = 0;
@@ -1976,7 +1990,7 @@ pair_filter_kernel(FilterArgs a) {
   const bool ok = scalable && ex > -100 && ex < 100;
   const float scale = ok ? ldexpf(1.f, 15 - ex) : 1.f;
   const float inv_scale = ok ? ldexpf(1.f, ex - 15) : 1.f;
-  const float beta = ok ? l1 * cmax * 0x1p-10f : (amax == 0.f ? 0.f : INFINITY);
+  const float beta = ok ? l1 * (ec + cmax * 0x1p-14f) * (1.f + 0x1p-10f) : (amax == 0.f ? 0.f : INFINITY);
   fs_v8h qa[KT];
   {
     const int m = lane & 15, g = lane >> 4;
@@ -2113,9 +2127,16 @@ pair_filter_kernel(FilterArgs a) {
   int* ci = reinterpret_cast<int*>(htab + 8 * kFsWaves * kFsCap);            // ids (INT_MAX: NaN)
   int* rk = reinterpret_cast<int*>(htab + 12 * kFsWaves * kFsCap);           // ranks
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
+  for (int r = 0; r < 2; ++r) {  // one LDS atomic per wave and half
     const int e = lane + 64 * r;
-    if ((e < L.cnt) && fs_keep(L.hi[e], L.id[e], bt, bti)) cslot[atomicAdd(&ncand_s, 1)] = wave * kFsCap + e;
+    const bool kp = (e < L.cnt) && fs_keep(L.hi[e], L.id[e], bt, bti);
+    const uint64_t km = __ballot(kp);
+    if (km) {
+      int p0 = 0;
+      if (lane == 0) p0 = atomicAdd(&ncand_s, __popcll(km));
+      p0 = __builtin_amdgcn_readfirstlane(p0);
+      if (kp) cslot[p0 + lane_prefix(km)] = wave * kFsCap + e;
+    }
   }
   __syncthreads();
   const int m = ncand_s;
@@ -2474,6 +2495,7 @@ int launch_filter_d(const FilterArgs& f, int nb, int nq, bool big, hipStream_t s
   const int nslots = nb * f.k;
   const dim3 mg((unsigned)nq);
   if (nslots <= 4 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<4>), mg, dim3(kFmThreads), 0, st, f, nb);
+  else if (nslots <= 8 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<8>), mg, dim3(kFmThreads), 0, st, f, nb);
   else if (nslots <= 16 * kFmThreads) hipLaunchKernelGGL((filter_merge_kernel<16>), mg, dim3(kFmThreads), 0, st, f, nb);
   else hipLaunchKernelGGL((filter_merge_kernel<kFmRegs>), mg, dim3(kFmThreads), 0, st, f, nb);
   TQ_LAUNCH_CHECK("filter_merge_kernel");
