@@ -354,7 +354,9 @@ int tq_paged_gather(const uint8_t* pool, const float* norm_pool, int64_t num_blo
  * (bt_stride = max_blocks_per_seq).  Head_dim 64, K 1-4 / V 1-2 bits, at most 4 query
  * heads per KV head, fp16/bf16 queries and a power-of-two block_size >= 4 run the fused
  * decode kernel reading the pools directly; other shapes gather the rows into the
- * workspace first.  Pools 16-byte aligned; num_blocks * hkv * block_size * P < 2^31.
+ * workspace first.  Pools 16-byte aligned; num_blocks * hkv * block_size < 2^32 rows (pools
+ * from 2 GiB on are read with 64-bit addresses, and a block id outside the pool reads the
+ * pool's last block instead of memory outside it).
  */
 size_t tq_decode_paged_workspace_bytes(tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
                                        int32_t d, int32_t kbits, int32_t vbits,
@@ -389,7 +391,8 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
  * tq_paged_store; negative or out-of-pool slots skipped), leaving the other tokens of
  * each tile as they are.  Workspace: tq_decode_dl_workspace_bytes(B, hq, hkv,
  * max_blocks_per_seq * block_size).  Pools 16-byte aligned; num_blocks * hkv * block_size
- * * 32 < 2^31.  Outputs as tq_decode_attention_dl's.
+ * < 2^32 rows (pools from 2 GiB on are read with 64-bit addresses; a block id outside the
+ * pool reads the pool's last block).  Outputs as tq_decode_attention_dl's.
  */
 int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
                                int32_t hkv, const int64_t* slot_mapping, uint8_t* vtile_pool,

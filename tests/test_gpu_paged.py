@@ -517,3 +517,116 @@ def test_decode_layout_prefill_chunks_with_several_splits_vs_f64():
     for got in (whole, chunked):
         assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
     assert not np.array_equal(whole, chunked)  # the plans really differ
+
+
+# ------------------------------------------------------------------ pools past 2 GiB
+def _high_tables(lens, bs, nb, width):
+    """Block tables using the pool's last blocks (past the 2 GiB mark of the key pool),
+    in descending order; entries past a sequence's blocks are -1."""
+    tab = np.full((len(lens), width), -1, np.int32)
+    nxt = nb - 1
+    for i, n in enumerate(lens):
+        for j in range((n + bs - 1) // bs):
+            tab[i, j] = nxt
+            nxt -= 1
+    return tab
+
+
+@pytest.mark.parametrize("layout", ["decode", "bitplane"])
+def test_paged_pools_past_2gib(layout):
+    # Key pools of 2.46 GB (76.8M rows of 32 B): the sequences' blocks sit past byte 2^31,
+    # which 32-bit buffer offsets cannot reach, so these calls take the 64-bit-address
+    # kernels.  Same sums as the contiguous kernels over the same rows, and the float64
+    # oracle within the bf16 tolerance.
+    from turboquant_kv import ops
+    rs = np.random.RandomState(77)
+    Hkv, G, bs = 2, 4, 64
+    Hq = G * Hkv
+    lens = [700, 1, 1500]
+    B = len(lens)
+    nb = 600_000
+    assert nb * Hkv * bs * 32 >= 2 ** 31
+    width = (max(lens) + bs - 1) // bs + 1
+    tab = _high_tables(lens, bs, nb, width)
+    assert int(tab[tab >= 0].min()) * Hkv * bs * 32 >= 2 ** 31
+    slots = np.array([tab[i, t // bs] * bs + t % bs for i, n in enumerate(lens) for t in range(n)],
+                     np.int64)
+    n = len(slots)
+    krows = rs.randint(0, 256, (n, Hkv, 32)).astype(np.uint8)
+    vrows = rs.randint(0, 256, (n, Hkv, 16)).astype(np.uint8)
+    kn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
+    vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
+    Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
+    _, ck = O.lloyd_max_codebook(4, 64)
+    _, cv = O.lloyd_max_codebook(2, 64)
+    q = torch.from_numpy(rs.randn(B, Hq, 64).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    scale = 0.125
+    Tc = width * bs
+    kc_ = np.zeros((B, Hkv, Tc, 32), np.uint8)
+    vc_ = np.zeros((B, Hkv, Tc, 16), np.uint8)
+    kn_, vn_ = np.zeros((B, Hkv, Tc), np.float32), np.zeros((B, Hkv, Tc), np.float32)
+    o = 0
+    for b, L_ in enumerate(lens):
+        kc_[b, :, :L_] = krows[o:o + L_].transpose(1, 0, 2)
+        vc_[b, :, :L_] = vrows[o:o + L_].transpose(1, 0, 2)
+        kn_[b, :, :L_], vn_[b, :, :L_] = kn[o:o + L_].T, vn[o:o + L_].T
+        o += L_
+    lens_t = T(np.asarray(lens, np.int32))
+    out = torch.empty_like(q)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
+    knp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
+    vnp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
+    if layout == "decode":
+        kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
+        vt = torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV)
+        pairs = torch.empty(n * Hkv, 1, 32, dtype=torch.uint8, device=DEV)
+        ops.pack_decode_layout(T(krows).view(n * Hkv, 1, 32), pairs, 64, 4, False, 0)
+        capi.check(L().tq_paged_store(capi.p(pairs), capi.p(T(kn)), capi.i64(n), capi.i32(Hkv),
+                                      capi.i32(32), capi.p(T(slots)), capi.p(kp), capi.p(knp),
+                                      capi.i64(nb), capi.i32(bs), capi.stream()))
+        capi.check(L().tq_paged_store_value_tiles(capi.p(T(vrows)), capi.p(T(vn)), capi.i64(n),
+                                                  capi.i32(Hkv), capi.p(T(slots)), capi.p(vt),
+                                                  capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.stream()))
+        ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
+        capi.check(L().tq_decode_attention_paged_dl(
+            capi.p(q), capi.TQ_BF16, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp),
+            capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(tab)),
+            capi.i32(width), capi.p(lens_t), capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)),
+            ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
+            capi.stream()))
+        sync()
+        got = out.float().cpu().numpy()
+        del kp, vt
+        kpairs = torch.empty(B * Hkv, Tc, 32, dtype=torch.uint8, device=DEV)
+        vblocks = torch.zeros(B * Hkv, Tc // 64, 1024, dtype=torch.uint8, device=DEV)
+        ops.pack_decode_layout(T(kc_).view(B * Hkv, Tc, 32), kpairs, 64, 4, False, 0)
+        ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 16), vblocks, 64, 2, True, 0)
+        ref, _ = ops.decode_attention_dl(q, kpairs.view(B, Hkv, Tc, 32), T(kn_),
+                                         vblocks.view(B, Hkv, Tc // 64, 1024), T(vn_), lens_t, T(ck),
+                                         T(cv), T(Rk), T(Rv), scale, return_lse=True)
+        ref = ref.float().cpu().numpy()
+    else:
+        kpool = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
+        vpool = torch.zeros(nb, Hkv, bs, 16, dtype=torch.uint8, device=DEV)
+        for rows, norms, pool, npool in ((krows, kn, kpool, knp), (vrows, vn, vpool, vnp)):
+            capi.check(L().tq_paged_store(capi.p(T(rows)), capi.p(T(norms)), capi.i64(n), capi.i32(Hkv),
+                                          capi.i32(rows.shape[2]), capi.p(T(slots)), capi.p(pool),
+                                          capi.p(npool), capi.i64(nb), capi.i32(bs), capi.stream()))
+        wsb = L().tq_decode_paged_workspace_bytes(capi.TQ_BF16, B, Hq, Hkv, 64, 4, 2, width, bs)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+        capi.check(L().tq_decode_attention_paged(
+            capi.p(q), capi.TQ_BF16, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(64),
+            capi.p(kpool), capi.p(knp), capi.p(vpool), capi.p(vnp), capi.i64(nb), capi.i32(bs),
+            capi.p(T(tab)), capi.i32(width), capi.p(lens_t), capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)),
+            capi.p(T(Rv)), capi.i32(4), capi.i32(2), ctypes.c_float(scale), capi.p(out), capi.p(lse),
+            capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+        sync()
+        got = out.float().cpu().numpy()
+        del kpool, vpool
+        ref, _ = k_decode(q, kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv, 4, 2, scale)
+    del knp, vnp
+    torch.cuda.empty_cache()
+    assert np.array_equal(got, ref)  # same arithmetic and split plan as the contiguous kernel
+    want = O.decode_attention_f64(q.float().cpu().numpy(), kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv,
+                                  4, 2, scale)
+    assert np.max(np.abs(got - want)) <= 1e-2 * np.max(np.abs(want))

@@ -36,6 +36,8 @@ struct PagedPools {
   int bt_stride;
   int bs_log2;
   uint32_t pool_rows;           // num_blocks * hkv * block_size
+  uint32_t num_blocks;
+  bool wide;                    // rows past 2 GiB: 64-bit addresses
 };
 
 // True when the fused kernel covers this call (head_dim 64, K 1-4 bits, V 1-2 bits,

@@ -76,6 +76,7 @@ struct DecodeArgs {
   int bt_stride;
   int bs_log2;           // log2(block_size), block_size >= 4
   uint32_t pool_rows;    // num_blocks * hkv * block_size
+  uint32_t num_blocks;   // wide pools (PG 2): block ids are clamped below it
 };
 
 // Raw buffer resource over `bytes` bytes at `p` (gfx9 dword 3); loads past the end
@@ -103,6 +104,25 @@ __device__ __forceinline__ void load_row(__amdgpu_buffer_rsrc_t rs, uint32_t off
   }
 }
 
+// The same from a global address (row bytes 16-byte aligned when NB is a multiple of 16,
+// else 8-byte aligned).
+template <int NB>
+__device__ __forceinline__ void load_row_at(const uint8_t* p, uint32_t (&w)[NB / 4]) {
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      const u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
+      w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB / 8; ++i) {
+      const u32x2 v = reinterpret_cast<const u32x2*>(p)[i];
+      w[2 * i] = v.x; w[2 * i + 1] = v.y;
+    }
+  }
+}
+
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
 }
@@ -116,8 +136,12 @@ __device__ __forceinline__ uint32_t quad_transpose(uint32_t x, uint32_t sel1, ui
   return perm(yp, y, sel2);
 }
 
-template <int KB, int VB, bool PAGED = false>
+// PG: 0 contiguous; 1 paged pools read through buffer resources over whole pools (32-bit
+// offsets: pools under 2 GiB); 2 paged pools of any size: rows at 64-bit addresses from
+// clamped block ids.
+template <int KB, int VB, int PG = 0>
 __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs a) {
+  constexpr bool PAGED = PG != 0, WIDE = PG == 2;
   constexpr int PK = KB * 8, PV = VB * 8;  // packed row bytes (d = 64)
   // Tables first; after the tile loop the same bytes hold the cross-quad reduction.
   __shared__ __attribute__((aligned(16))) char tabs[2 * kTabBytes];
@@ -219,20 +243,32 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
   auto load_tile = [&](int t0, Tile& x, uint32_t blk) {
     uint32_t tr, nr;
     if constexpr (PAGED) {
-      // the lane quad's four tokens share a block (block_size >= 4, t0 % 4 == 0)
+      // the lane quad's four tokens share a block (block_size >= 4, t0 % 4 == 0); wide
+      // pools: an id outside the pool (a corrupt table) reads the last block
+      if constexpr (WIDE) blk = blk < a.num_blocks ? blk : a.num_blocks - 1;
       tr = ((blk * (uint32_t)a.hkv + (uint32_t)g) << bsl) | ((uint32_t)(t0 + lane) & ((1u << bsl) - 1));
       nr = tr - (uint32_t)hn;
     } else {
       tr = (uint32_t)(t0 + lane);
       nr = (uint32_t)(t0 + 4 * quad);
     }
-    load_row<PK>(krs, tr * PK, x.k);
-    load_row<PV>(vrs, tr * PV, x.v);
-    const uint32_t no = nr * 4;
+    if constexpr (WIDE) {  // pool rows (< 2^32) at 64-bit byte addresses
+      load_row_at<PK>(a.kpacked + (size_t)tr * PK, x.k);
+      load_row_at<PV>(a.vpacked + (size_t)tr * PV, x.v);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x.kn[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(knrs, (int)no, 4 * r, 0));
-      x.vn[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vnrs, (int)no, 4 * r, 0));
+      for (int r = 0; r < 4; ++r) {
+        x.kn[r] = a.knorms[(size_t)nr + r];
+        x.vn[r] = a.vnorms[(size_t)nr + r];
+      }
+    } else {
+      load_row<PK>(krs, tr * PK, x.k);
+      load_row<PV>(vrs, tr * PV, x.v);
+      const uint32_t no = nr * 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x.kn[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(knrs, (int)no, 4 * r, 0));
+        x.vn[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vnrs, (int)no, 4 * r, 0));
+      }
     }
   };
 
@@ -491,6 +527,7 @@ struct DlArgs {
   int bt_stride;
   int bs_log2;
   uint32_t pool_rows;  // num_blocks * hkv * bs
+  uint32_t num_blocks;  // wide pools (PG 3, 4): block ids are clamped below it
 };
 
 __device__ __forceinline__ uint32_t byte_addr(uint32_t base_copy, uint32_t w, int byte) {
@@ -559,9 +596,12 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // 2 paged pools of block_size 16 or 32 (16-token value sub-blocks of 256 B: lane
 // 16 sl + c's word holds what word m of its 64-token tile row holds for sub-block m).
 // VB: value code width (2, 3 or 4; sub-blocks hold 2-bit values only).
+// PG: 0 contiguous; 1 / 2 paged pools (blocks >= 64 tokens / 16- or 32-token blocks) read
+// through buffer resources over whole pools (32-bit offsets: pools under 2 GiB); 3 / 4 the
+// same for pools of any size: rows at 64-bit addresses from clamped block ids.
 template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
-  constexpr bool PAGED = PG != 0, SUB16 = PG == 2;
+  constexpr bool PAGED = PG != 0, SUB16 = PG == 2 || PG == 4, WIDE = PG >= 3;
   static_assert(VB >= 2 && VB <= 4 && (!SUB16 || VB == 2), "value width");
   constexpr int VW = VB == 2 ? 4 : 2 * VB;  // value words per lane and tile
   constexpr uint32_t VTILE = 512u * VB;     // bytes per 64-token value tile
@@ -656,24 +696,46 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       return r;
     }
   };
+  // wide pools: an id outside the pool (a corrupt table) reads the last block, not memory
+  // outside the pool
+  const uint32_t blast = a.num_blocks - 1;
+  auto clampb = [&](uint32_t x) -> uint32_t { return x < a.num_blocks ? x : blast; };
   auto load_tile = [&](int t0, Tile& x, Blk blk) {
     // rg[g]: pool row of the first token of the tile's 16-token group g; vt: value tile
     uint32_t rg[4], vt = (uint32_t)t0 >> 6;
 #pragma unroll
     for (int g = 0; g < 4; ++g) rg[g] = (uint32_t)t0 + 16 * g;
-    if constexpr (PG == 1) {
+    if constexpr (PG == 1 || PG == 3) {
+      if constexpr (WIDE) blk = clampb(blk);
       const uint32_t sb = blk * (uint32_t)a.hkv + (uint32_t)kvh;
       const uint32_t in = (uint32_t)t0 & ((1u << bsl) - 1);
 #pragma unroll
       for (int g = 0; g < 4; ++g) rg[g] = ((sb << bsl) | in) + 16 * g;
       vt = (sb << (bsl - 6)) | (in >> 6);
     } else if constexpr (SUB16) {
-      const uint32_t bl[4] = {blk.x, blk.y, blk.z, blk.w};
+      uint32_t bl[4] = {blk.x, blk.y, blk.z, blk.w};
+      if constexpr (WIDE) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) bl[g] = clampb(bl[g]);
+      }
 #pragma unroll
       for (int g = 0; g < 4; ++g)
         rg[g] = ((bl[g] * (uint32_t)a.hkv + (uint32_t)kvh) << bsl) |
                 (((uint32_t)t0 + 16 * g) & ((1u << bsl) - 1));
     }
+    if constexpr (WIDE) {  // pool rows (< 2^32) at 64-bit byte addresses
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        x.k[g] = *reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl);
+      if constexpr (SUB16) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          x.v[m] = *reinterpret_cast<const uint32_t*>(a.vblocks + (size_t)(rg[m] >> 4) * 256 + lane * 4);
+      } else {
+        const u32x4 v0 = *reinterpret_cast<const u32x4*>(a.vblocks + (size_t)vt * VTILE + lane * 16);
+        x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+      }
+    } else {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
       x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 + 8 * sl), 0, 0);
@@ -693,13 +755,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
       }
     }
+    }
     // norms of the lane's four tokens (group gq): 16-byte aligned (t_cap % 64 == 0,
     // aligned base)
     uint32_t rq = rg[0] + 16 * gq;
     if constexpr (SUB16) rq = gq == 0 ? rg[0] : gq == 1 ? rg[1] : gq == 2 ? rg[2] : rg[3];
     const uint32_t no = (rq + 4 * sl) * 4;
-    const u32x4 kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
-    const u32x4 vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
+    u32x4 kn4, vn4;
+    if constexpr (WIDE) {
+      kn4 = *reinterpret_cast<const u32x4*>(a.knorms + (size_t)(rq + 4 * sl));
+      vn4 = *reinterpret_cast<const u32x4*>(a.vnorms + (size_t)(rq + 4 * sl));
+    } else {
+      kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
+      vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
+    }
     // (__builtin_bit_cast of a vector element would read element 0: convert by value)
     x.kn[0] = __uint_as_float(kn4.x); x.kn[1] = __uint_as_float(kn4.y);
     x.kn[2] = __uint_as_float(kn4.z); x.kn[3] = __uint_as_float(kn4.w);
@@ -1312,10 +1381,10 @@ SplitPlan plan_splits(int B, int hkv, int64_t t_max) {
   return {split, (int)((t_max + split - 1) / split)};
 }
 
-template <int KB, bool PAGED = false>
+template <int KB, int PG = 0>
 int launch_kb(int vb, dim3 grid, const DecodeArgs& a, hipStream_t st) {
-  if (vb == 1) hipLaunchKernelGGL((fused_decode_kernel<KB, 1, PAGED>), grid, dim3(kDecThreads), 0, st, a);
-  else hipLaunchKernelGGL((fused_decode_kernel<KB, 2, PAGED>), grid, dim3(kDecThreads), 0, st, a);
+  if (vb == 1) hipLaunchKernelGGL((fused_decode_kernel<KB, 1, PG>), grid, dim3(kDecThreads), 0, st, a);
+  else hipLaunchKernelGGL((fused_decode_kernel<KB, 2, PG>), grid, dim3(kDecThreads), 0, st, a);
   TQ_LAUNCH_CHECK("fused_decode_kernel");
   return TQ_OK;
 }
@@ -1366,11 +1435,21 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
   if (pg) {
     a.block_tables = pg->block_tables; a.bt_stride = pg->bt_stride; a.bs_log2 = pg->bs_log2;
     a.pool_rows = pg->pool_rows;
-    switch (c.kbits) {
-      case 1: rc = launch_kb<1, true>(c.vbits, grid, a, st); break;
-      case 2: rc = launch_kb<2, true>(c.vbits, grid, a, st); break;
-      case 3: rc = launch_kb<3, true>(c.vbits, grid, a, st); break;
-      default: rc = launch_kb<4, true>(c.vbits, grid, a, st); break;
+    a.num_blocks = pg->num_blocks;
+    if (!pg->wide) {
+      switch (c.kbits) {
+        case 1: rc = launch_kb<1, 1>(c.vbits, grid, a, st); break;
+        case 2: rc = launch_kb<2, 1>(c.vbits, grid, a, st); break;
+        case 3: rc = launch_kb<3, 1>(c.vbits, grid, a, st); break;
+        default: rc = launch_kb<4, 1>(c.vbits, grid, a, st); break;
+      }
+    } else {
+      switch (c.kbits) {
+        case 1: rc = launch_kb<1, 2>(c.vbits, grid, a, st); break;
+        case 2: rc = launch_kb<2, 2>(c.vbits, grid, a, st); break;
+        case 3: rc = launch_kb<3, 2>(c.vbits, grid, a, st); break;
+        default: rc = launch_kb<4, 2>(c.vbits, grid, a, st); break;
+      }
     }
   } else {
     switch (c.kbits) {
@@ -1488,6 +1567,10 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
         else launch_dl_kernel<0, 4>(q_dtype, (unsigned)grid, a, st);
       } else if (pg == 1) {
         launch_dl_kernel<1, 2>(q_dtype, (unsigned)grid, a, st);
+      } else if (pg == 3) {
+        launch_dl_kernel<3, 2>(q_dtype, (unsigned)grid, a, st);
+      } else if (pg == 4) {
+        launch_dl_kernel<4, 2>(q_dtype, (unsigned)grid, a, st);
       } else {
         launch_dl_kernel<2, 2>(q_dtype, (unsigned)grid, a, st);
       }
@@ -1593,7 +1676,9 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
   TQ_REQUIRE(num_blocks >= 0 && max_blocks_per_seq >= 0, "bad sizes");
   const int64_t t_cap = (int64_t)max_blocks_per_seq * block_size;
   const int64_t pool_rows = num_blocks * hkv * block_size;
-  TQ_REQUIRE(pool_rows * 32 < (int64_t)INT_MAX, "pools too large for 32-bit offsets");
+  TQ_REQUIRE(pool_rows < ((int64_t)1 << 32), "pools hold at most 2^32 rows per layer");
+  // pools from 2 GiB of key rows on: 64-bit addresses (the buffer path's offsets are 32-bit)
+  const bool wide = pool_rows * 32 >= (int64_t)INT_MAX;
   if (B == 0) return TQ_OK;
   TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
              "null pointer argument");
@@ -1614,8 +1699,9 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
   a.qscale = scale * 1.4426950408889634f;
   a.block_tables = block_tables; a.bt_stride = max_blocks_per_seq; a.bs_log2 = bsl;
   a.pool_rows = (uint32_t)pool_rows;
-  return run_dl(a, q_dtype, B, hq, hkv, 2, bsl >= 6 ? 1 : 2, p, workspace, out, lse,
-                as_stream(stream));
+  a.num_blocks = (uint32_t)std::max<int64_t>(num_blocks, 1);
+  const int pg = (bsl >= 6 ? 1 : 2) + (wide ? 2 : 0);
+  return run_dl(a, q_dtype, B, hq, hkv, 2, pg, p, workspace, out, lse, as_stream(stream));
 }
 
 int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,

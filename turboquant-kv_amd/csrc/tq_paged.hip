@@ -193,8 +193,9 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
   const int bpp = (d + 7) / 8;
   const int pk = kbits * bpp, pv = vbits * bpp;
   const int64_t pool_rows = num_blocks * hkv * block_size;
-  TQ_REQUIRE(pool_rows * (pk > pv ? pk : pv) < (int64_t)INT_MAX,
-             "pools too large for 32-bit offsets (%lld rows)", (long long)pool_rows);
+  TQ_REQUIRE(pool_rows < ((int64_t)1 << 32), "pools hold at most 2^32 rows per layer");
+  // pools from 2 GiB of rows on: 64-bit addresses (the buffer path's offsets are 32-bit)
+  const bool wide = pool_rows * (pk > pv ? pk : pv) >= (int64_t)INT_MAX;
   TQ_REQUIRE(((reinterpret_cast<uintptr_t>(kpool) | reinterpret_cast<uintptr_t>(vpool) |
                reinterpret_cast<uintptr_t>(knorm_pool) | reinterpret_cast<uintptr_t>(vnorm_pool)) &
               15u) == 0,
@@ -208,7 +209,8 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
                      t_max, seq_lens, kcentroids, vcentroids, krotation, vrotation,
                      kbits, vbits, scale, out, lse};
   if (t_max > 0 && bsl >= 2 && fused_decode_covers(fc)) {
-    const PagedPools pg{block_tables, max_blocks_per_seq, bsl, (uint32_t)pool_rows};
+    const PagedPools pg{block_tables, max_blocks_per_seq, bsl, (uint32_t)pool_rows,
+                        (uint32_t)std::max<int64_t>(num_blocks, 1), wide};
     return launch_fused_decode(fc, workspace, workspace_bytes, st, &pg);
   }
   // Other shapes: gather the batch's rows into contiguous buffers and run the general
