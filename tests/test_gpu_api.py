@@ -270,3 +270,32 @@ def test_cache_gqa_batched_decode_matches_composition():
     logits = kv.attention_scores(0, q.unsqueeze(2))
     ref = kv.attention_values(0, torch.softmax(logits, -1)).squeeze(2)
     assert (fused - ref).abs().max().item() <= 1e-4 * ref.abs().max().item()
+
+
+@pytest.mark.parametrize("bits,d,mode", [(4, 128, "mse"), (3, 200, "mse"), (4, 64, "prod")])
+def test_index_search_k_above_32_ties_and_order(bits, d, mode):
+    # k above the fused scan's 32 scores every row and selects with the core's heap order
+    # (score descending, lower index first on a tie): 200 duplicated rows tie exactly.
+    from turboquant_kv import TurboQuantIndex
+    rs = np.random.RandomState(bits * 7 + d)
+    db = rs.randn(6000, d).astype(np.float32)
+    db[rs.choice(6000, 200, replace=False)] = db[17]
+    idx = TurboQuantIndex.from_vectors(torch.from_numpy(db).to(DEV), bit_width=bits, mode=mode)
+    q = rs.randn(3, d).astype(np.float32)
+    q[0] = db[17]
+    for k in (64, 300):
+        s, i = idx.search(torch.from_numpy(q).to(DEV), k=k)
+        s, i = s.cpu().numpy(), i.cpu().numpy()
+        if mode == "mse":
+            want_s, want_i = O.search_topk(q, idx._bitplane_codes().cpu().numpy(), idx._norms.cpu().numpy(),
+                                           idx._cen.cpu().numpy(), idx._rot_dev.cpu().numpy(), bits, k)
+            assert np.array_equal(i, want_i), k
+            assert np.array_equal(s.view(np.uint32), want_s.view(np.uint32)), k
+        else:  # prod: the heap order over the scan's own scores
+            full = idx.search(torch.from_numpy(q).to(DEV), k=6000)[0].cpu().numpy()
+            assert (np.diff(s, axis=1) <= 0).all()
+            for r in range(3):
+                for a in range(k - 1):
+                    if s[r, a] == s[r, a + 1]:
+                        assert i[r, a] < i[r, a + 1]
+            assert np.array_equal(s, full[:, :k])

@@ -261,3 +261,32 @@ def test_huffman_window_table_decoder_equals_bit_walk():
             b = ops().huffman_decode(data, -1, long_w, long_l, long_s)
             assert torch.equal(a, b), (nbytes, nbits)
             assert not (a == 1).any() and not (a == 4).any()   # replaced / shadowed words
+
+
+def test_large_k_topk_keeps_the_lowest_index_among_ties():
+    # The k > 32 search path selects with torch.topk, whose order among ties is
+    # unspecified; the helper must return the reference core's heap order (score
+    # descending, lower index first on a tie) and never list NaN, over integer-valued
+    # scores full of ties, -inf and NaN, against the oracle's lexsort order.
+    from turboquant_kv.search import _topk_lowest_index
+    import tq_oracle as O
+    rs = np.random.RandomState(0)
+    for trial in range(300):
+        Q, N = rs.randint(1, 4), rs.randint(1, 300)
+        k = rs.randint(1, N + 1)
+        s = rs.randint(-5, 5, size=(Q, N)).astype(np.float32)
+        if trial % 3 == 0:
+            s[rs.rand(Q, N) < 0.2] = np.nan
+        if trial % 5 == 0:
+            s[rs.rand(Q, N) < 0.2] = -np.inf
+        v, i = _topk_lowest_index(torch.from_numpy(s), k)
+        sc = np.where(np.isnan(s), -np.inf, s)
+        want_s, want_i = O.topk_desc(sc, N)
+        for q in range(Q):
+            ids = [j for j in want_i[q] if not np.isnan(s[q, j])][:k]
+            ei = np.full(k, -1)
+            ei[:len(ids)] = ids
+            es = np.full(k, -np.inf, np.float32)
+            es[:len(ids)] = s[q, ids]
+            assert np.array_equal(i[q].numpy(), ei), (trial, q)
+            assert np.array_equal(v[q].numpy(), es), (trial, q)

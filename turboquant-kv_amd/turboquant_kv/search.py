@@ -44,6 +44,37 @@ MODE_PROD = 1
 _SCAN_MAX_K = 32  # the fused top-k kernel's per-call limit
 
 
+def _topk_lowest_index(s: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Top k of each row of s [Q, N] (k <= N) by score descending, equal scores in
+    increasing index order -- the order of the reference core's heap, which keeps the
+    earlier row on a tie (turboquant_core.cpp:487-512) -- and NaN scores never listed
+    ((-inf, -1) pads in their place, as the fused scan).  torch.topk alone leaves the order
+    of ties unspecified: its k-th value sets a threshold, every score above it is taken,
+    then the lowest-index entries at it, and the k winners are sorted stably."""
+    nan = torch.isnan(s)
+    sc = torch.where(nan, torch.full_like(s, float("-inf")), s)
+    kth = torch.topk(sc, k, dim=-1).values[:, -1:]
+    above = sc > kth
+    tie = (sc == kth) & ~nan
+    tie_nan = (sc == kth) & nan  # a NaN ranks below every real score, -inf included
+    need = k - above.sum(dim=-1, keepdim=True)
+    need_nan = need - tie.sum(dim=-1, keepdim=True)
+    take = (above | (tie & (torch.cumsum(tie.to(torch.int32), dim=-1) <= need)) |
+            (tie_nan & (torch.cumsum(tie_nan.to(torch.int32), dim=-1) <= need_nan)))
+    idx = take.nonzero()[:, 1].view(s.shape[0], k)  # row-major: ascending index per row
+    vals = sc.gather(1, idx)
+    vals, order = torch.sort(vals, dim=-1, descending=True, stable=True)
+    idx = idx.gather(1, order)
+    was_nan = nan.gather(1, idx)
+    if bool(was_nan.any()):  # NaN rows sit among the -inf ones: make them pads, last
+        vals = torch.where(was_nan, torch.full_like(vals, float("-inf")), vals)
+        idx = torch.where(was_nan, torch.full_like(idx, -1), idx)
+        key = was_nan.to(torch.int32)
+        key, order = torch.sort(key, dim=-1, stable=True)
+        vals, idx = vals.gather(1, order), idx.gather(1, order)
+    return vals, idx
+
+
 class TurboQuantIndex:
     def __init__(self, dim: int, bit_width: int = 3, mode: str = "mse", rotation: str = "dense_qr",
                  seed: int = 42, device="cuda"):
@@ -191,8 +222,7 @@ class TurboQuantIndex:
                 s = ops.attention_scores_packed(q.float().unsqueeze(0), self._packed_codes,
                                                 self._norms, self._cen, self._rot_dev,
                                                 self.bit_width)[0]
-            top = torch.topk(s, k, dim=-1)
-            return top.values, top.indices
+            return _topk_lowest_index(s, k)
         if self.bit_width <= 4:
             # Scored from the packed rows: <q, dequantize_prod(row)> rearranged as
             # n * (<R q, c[codes]> + sqrt(pi/2)/d * gamma * <S q, +-1>).
@@ -204,14 +234,12 @@ class TurboQuantIndex:
                                           self._qjl_signs, self._residual_norms, self._norms,
                                           self._cen, self._rot_dev, self._S_dev,
                                           self.bit_width)[0]
-            top = torch.topk(s, k, dim=-1)
-            return top.values, top.indices
+            return _topk_lowest_index(s, k)
         recon = _ops().dequantize_prod_packed(self._packed_codes, self._qjl_signs,
                                               self._residual_norms, self._norms, self._cen,
                                               self._rot_dev, self._S_dev, self.bit_width, self.dim)
         scores = q.float() @ recon.t()
-        top = torch.topk(scores, k, dim=-1)
-        return top.values, top.indices
+        return _topk_lowest_index(scores, k)
 
     # ------------------------------------------------------------------ persistence
     def save(self, path: str) -> None:
