@@ -618,6 +618,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   __shared__ float qs2_s[4];  // per-head query scales
   __shared__ float red_m[kDlWaves][4];
   __shared__ float red_l[kDlWaves][4];
+  __shared__ u32x2 kst_s[256];  // K table entries (hi, lo words) before replication
+  __shared__ u32x4 vst_s[256];  // V table entries
   char* const ktab = tabs + kDlTab;
   char* const vtab = tabs;
 
@@ -849,23 +851,22 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   __syncthreads();
   const float vsc = sc_s[0];
   const float ksc = sc_s[1];
-  // Tables: each thread writes 16-byte runs of identical copies.  K: entry i, copies 4q ..
-  // 4q + 3 of the hi parts (and of the lo parts with PREC_K).  V: entry i, copies 2q,
-  // 2q + 1 (or, EXACT_V, copy q: hi and lo halves).
-  for (int e = tid; e < 256 * 8; e += kDlThreads) {
-    const int i = e >> 3, q = e & 7;
+  // Tables: each entry's fp16 words are converted once (a thread per K entry, a thread
+  // per V entry) into a small staging table, then stored as 16-byte runs of identical
+  // copies, consecutive lanes writing consecutive runs (conflict-free LDS writes).
+  // K: entry i, copies 4q .. 4q + 3 of the hi parts (and of the lo parts with PREC_K).
+  // V: entry i, copies 2q, 2q + 1 (or, EXACT_V, copy q: hi and lo halves); VB 3, 4: pair
+  // entries (c[low code], c[high code]) * vsc as two fp16, copies 4q .. 4q + 3, lo halves
+  // 128 bytes further.
+  static_assert(kDlThreads == 512, "a thread per K entry and a thread per V entry");
+  if (tid < 256) {
+    const int i = tid;
     const float x0 = cen_s[i >> 4] * ksc, x1 = cen_s[i & 15] * ksc;
     const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-    const uint32_t wh = pack_h2(h0, h1);
-    *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + q * 16) = (u32x4){wh, wh, wh, wh};
-    if constexpr (PREC_K) {
-      const uint32_t wl = pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
-      *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + kDlKLo + q * 16) = (u32x4){wl, wl, wl, wl};
-    }
-  }
-  if constexpr (VB == 2) {
-    for (int e = tid; e < 256 * 16; e += kDlThreads) {
-      const int i = e >> 4, q = e & 15;
+    kst_s[i] = (u32x2){pack_h2(h0, h1), pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1))};
+  } else {
+    const int i = tid - 256;
+    if constexpr (VB == 2) {
       v4h vh, vl;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -874,23 +875,34 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         vl[t] = (_Float16)(x - (float)vh[t]);
       }
       const u32x2 h = __builtin_bit_cast(u32x2, vh), lo = __builtin_bit_cast(u32x2, vl);
-      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) =
-          EXACT_V ? (u32x4){h.x, h.y, lo.x, lo.y} : (u32x4){h.x, h.y, h.x, h.y};
-    }
-  } else {
-    // pair entries: (c[low code], c[high code]) * vsc as two fp16, copies 4q .. 4q + 3;
-    // lo halves 128 bytes further
-    constexpr int mask = (1 << VB) - 1;
-    for (int e = tid; e < 256 * 8; e += kDlThreads) {
-      const int i = e >> 3, q = e & 7;
+      vst_s[i] = EXACT_V ? (u32x4){h.x, h.y, lo.x, lo.y} : (u32x4){h.x, h.y, h.x, h.y};
+    } else {
+      constexpr int mask = (1 << VB) - 1;
       const float x0 = cen_s[16 + (i & mask)] * vsc, x1 = cen_s[16 + ((i >> VB) & mask)] * vsc;
       const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-      const uint32_t wh = pack_h2(h0, h1);
-      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) = (u32x4){wh, wh, wh, wh};
-      if constexpr (EXACT_V) {
-        const uint32_t wl = pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1));
-        *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + 128 + q * 16) = (u32x4){wl, wl, wl, wl};
-      }
+      vst_s[i] = (u32x4){pack_h2(h0, h1), pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1)), 0u, 0u};
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < 256 * 8; e += kDlThreads) {
+    const int i = e >> 3, q = e & 7;
+    const u32x2 w = kst_s[i];
+    *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + q * 16) = (u32x4){w.x, w.x, w.x, w.x};
+    if constexpr (PREC_K)
+      *reinterpret_cast<u32x4*>(ktab + i * kDlEntry + 128 + kDlKLo + q * 16) = (u32x4){w.y, w.y, w.y, w.y};
+  }
+  if constexpr (VB == 2) {
+    for (int e = tid; e < 256 * 16; e += kDlThreads) {
+      const int i = e >> 4, q = e & 15;
+      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) = vst_s[i];
+    }
+  } else {
+    for (int e = tid; e < 256 * 8; e += kDlThreads) {
+      const int i = e >> 3, q = e & 7;
+      const u32x4 w = vst_s[i];
+      *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + q * 16) = (u32x4){w.x, w.x, w.x, w.x};
+      if constexpr (EXACT_V)
+        *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + 128 + q * 16) = (u32x4){w.y, w.y, w.y, w.y};
     }
   }
   __syncthreads();
@@ -1146,6 +1158,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     process(tc, t + 2 * kStep);
   }
 
+  // The whole-sequence path's R_v column (threads of waves 0-3: dim = lane), requested
+  // now so that its latency runs under the reduction below.
+  float rv[kDim];
+  if ((a.out != nullptr) & (tid < 4 * kDim)) {
+#pragma unroll
+    for (int k = 0; k < kDim; ++k) rv[k] = a.vrot[k * kDim + (tid & 63)];
+  }
   // ---- reduction: l over the lanes of a head; outputs over the waves (LDS)
   l += __shfl_xor(l, 4);
   l += __shfl_xor(l, 8);
@@ -1198,8 +1217,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       const int m = tid >> 6, dim = tid & 63;
       if (m < a.G) {
         float r = 0.f;
-#pragma unroll 8
-        for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], a.vrot[k * kDim + dim], r);
+#pragma unroll
+        for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv[k], r);
         store_from_f32(a.out, (qh0 + m) * kDim + dim, r, a.q_dt);
       }
     }
