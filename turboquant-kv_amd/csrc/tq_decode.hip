@@ -702,6 +702,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // outside the pool
   const uint32_t blast = a.num_blocks - 1;
   auto clampb = [&](uint32_t x) -> uint32_t { return x < a.num_blocks ? x : blast; };
+  // Every tile load covers whole cache lines per instruction (512 B of key rows, 1 KB of a
+  // value tile, 256 B of norms) and is read once: non-temporal.
   auto load_tile = [&](int t0, Tile& x, Blk blk) {
     // rg[g]: pool row of the first token of the tile's 16-token group g; vt: value tile
     uint32_t rg[4], vt = (uint32_t)t0 >> 6;
@@ -728,32 +730,32 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if constexpr (WIDE) {  // pool rows (< 2^32) at 64-bit byte addresses
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        x.k[g] = *reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl);
+        x.k[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl));
       if constexpr (SUB16) {
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-          x.v[m] = *reinterpret_cast<const uint32_t*>(a.vblocks + (size_t)(rg[m] >> 4) * 256 + lane * 4);
+          x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(a.vblocks + (size_t)(rg[m] >> 4) * 256 + lane * 4));
       } else {
-        const u32x4 v0 = *reinterpret_cast<const u32x4*>(a.vblocks + (size_t)vt * VTILE + lane * 16);
+        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vblocks + (size_t)vt * VTILE + lane * 16));
         x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
       }
     } else {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 + 8 * sl), 0, 0);
+      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 + 8 * sl), 0, kNT);
     if constexpr (SUB16) {
       // value sub-block of group m = its first pool row / 16 (rows of a group are 16-aligned)
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)((rg[m] >> 4) * 256 + lane * 4), 0, 0);
+        x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)((rg[m] >> 4) * 256 + lane * 4), 0, kNT);
     } else {
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + lane * 16), 0, 0);
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + lane * 16), 0, kNT);
       x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
       if constexpr (VB == 3) {
-        const u32x2 v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, (int)(vt * VTILE + 1024 + lane * 8), 0, 0);
+        const u32x2 v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, (int)(vt * VTILE + 1024 + lane * 8), 0, kNT);
         x.v[4] = v1.x; x.v[5] = v1.y;
       } else if constexpr (VB == 4) {
-        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + 1024 + lane * 16), 0, 0);
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + 1024 + lane * 16), 0, kNT);
         x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
       }
     }
@@ -765,11 +767,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     const uint32_t no = (rq + 4 * sl) * 4;
     u32x4 kn4, vn4;
     if constexpr (WIDE) {
-      kn4 = *reinterpret_cast<const u32x4*>(a.knorms + (size_t)(rq + 4 * sl));
-      vn4 = *reinterpret_cast<const u32x4*>(a.vnorms + (size_t)(rq + 4 * sl));
+      kn4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.knorms + (size_t)(rq + 4 * sl)));
+      vn4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vnorms + (size_t)(rq + 4 * sl)));
     } else {
-      kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, 0);
-      vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, 0);
+      kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, kNT);
+      vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, kNT);
     }
     // (__builtin_bit_cast of a vector element would read element 0: convert by value)
     x.kn[0] = __uint_as_float(kn4.x); x.kn[1] = __uint_as_float(kn4.y);

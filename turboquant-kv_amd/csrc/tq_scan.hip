@@ -1891,8 +1891,9 @@ pair_filter_kernel(FilterArgs a) {
 
   // Rows of step t: the 64-row group t * W + gw (grid stride: all waves sweep memory
   // together).  Lane 16 g + i reads LW words of row 16 rt + i at byte 4 LW g, one load per
-  // 16-row tile rt: each load instruction covers 16 whole rows.  Loads past the last row
-  // return zeros (the resource's range check).
+  // 16-row tile rt: each load instruction covers 16 whole rows, so the loads are
+  // non-temporal (the rows stream through once; 10M x 128 went 130 -> 120 us per op).
+  // Loads past the last row return zeros (the resource's range check).
   struct RowBuf {
     uint32_t w[4 * LW];
     float n;
@@ -1918,10 +1919,10 @@ pair_filter_kernel(FilterArgs a) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       if constexpr (LW == 4) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, kNT);
         b.w[4 * rt + 0] = v.x; b.w[4 * rt + 1] = v.y; b.w[4 * rt + 2] = v.z; b.w[4 * rt + 3] = v.w;
       } else {
-        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, kNT);
         b.w[2 * rt + 0] = v.x; b.w[2 * rt + 1] = v.y;
       }
     }
