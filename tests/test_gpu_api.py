@@ -82,6 +82,33 @@ def test_torch_ops_reference_schemas(golden):
         ops.unpack_codes(packed, 3, 128)
 
 
+def test_reference_schemas_cpu_and_gpu_agree(golden):
+    """The same call on host tensors (CPU kernels) and on device tensors (gfx950 kernels):
+    pack/unpack and scores bit-identical, codes equal outside the decision band (the MFMA
+    contraction and the CPU kernel's sequential sum round differently), values within the
+    fp32 bound."""
+    ops = torch.ops.turboquant
+    m, rot = golden("quant_mse"), golden("rotation")
+    x, R = m["d64_x"][2:], rot["R_d64_s42"]  # rows of norm > 1e-10
+    bnd, cen = O.lloyd_max_codebook(3, 64)
+    tc = lambda a: torch.from_numpy(np.ascontiguousarray(a))
+    pc, nc = ops.rotate_and_quantize(tc(x), tc(R), tc(bnd), 3)
+    pg, ng = ops.rotate_and_quantize(T(x), T(R), T(bnd), 3)
+    O.check_codes(O.unpack_codes(pg.cpu().numpy(), 3, 64), O.unpack_codes(pc.numpy(), 3, 64), x, R, bnd)
+    assert np.allclose(nc.numpy(), ng.cpu().numpy(), rtol=4e-6, atol=0)
+    assert torch.equal(ops.unpack_codes(pc, 3, 64), ops.unpack_codes(pc.to(DEV), 3, 64).cpu())
+    codes = ops.unpack_codes(pc, 3, 64)
+    assert torch.equal(ops.pack_codes(codes, 3), ops.pack_codes(codes.to(DEV), 3).cpu())
+    q = np.random.RandomState(0).randn(2, 4, 64).astype(np.float32)
+    sc = ops.attention_scores_packed(tc(q), pc, nc, tc(cen), tc(R), 3)
+    sg = ops.attention_scores_packed(T(q), pc.to(DEV), nc.to(DEV), T(cen), T(R), 3)
+    assert np.array_equal(sc.numpy().view(np.uint32), sg.cpu().numpy().view(np.uint32))
+    w = torch.softmax(sc, -1)
+    oc = ops.attention_values_packed(w, pc, nc, tc(cen), tc(R), 3)
+    og = ops.attention_values_packed(w.to(DEV), pc.to(DEV), nc.to(DEV), T(cen), T(R), 3)
+    assert np.allclose(oc.numpy(), og.cpu().numpy(), rtol=1e-5, atol=1e-5 * oc.abs().max().item())
+
+
 def test_index_vs_reference(golden, tmp_path):
     from turboquant_kv import TurboQuantIndex
     ix, m = golden("index"), golden("quant_mse")

@@ -1,6 +1,7 @@
 """CPU tests of the product's host side: setup code bit-exact with the reference,
 the C ABI library exports what the header declares, the torch.ops schemas
-register, and CPU tensors are refused (no CPU kernels, no fallback)."""
+register, CPU tensors reach CPU kernels only for the five reference schemas (which the
+reference registers for the CPU key too) and are refused everywhere else (no fallback)."""
 
 import ctypes
 import os
@@ -92,8 +93,12 @@ def test_cpu_tensors_are_refused():
     from turboquant_kv._lib import ops
     with pytest.raises(RuntimeError, match="HIP device"):
         quantize_mse(torch.randn(4, 64), 4)
+    # the new ops have HIP kernels only: no CPU dispatch entry
     with pytest.raises((RuntimeError, NotImplementedError)):
-        ops().pack_codes(torch.zeros(2, 8, dtype=torch.uint8), 2)
+        ops().quantize_mse_packed(torch.randn(4, 64), torch.eye(64), torch.zeros(15), 4)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        ops().ip_scan_topk(torch.randn(1, 64), torch.zeros(8, 32, dtype=torch.uint8), torch.ones(8),
+                           torch.zeros(16), torch.eye(64), 4, 2)
 
 
 def test_index_file_format_header():

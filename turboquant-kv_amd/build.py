@@ -29,6 +29,9 @@ TORCH_LIB = os.path.join(LIBDIR, "libturboquant_torch.so")
 
 HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip", "tq_paged.hip", "tq_core_tables.hip",
                "tq_entropy.hip"]
+# host C++ of the torch.ops library: the HIP-device ops and the CPU-tensor kernels of the
+# reference schemas
+TORCH_SOURCES = ["torch_ops.cpp", "cpu_ops.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = [
@@ -74,19 +77,22 @@ def build(verbose: bool = False) -> None:
             cmd = [HIPCC, *DEVICE_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
             jobs.append(ex.submit(_run, cmd))
         inc, libs = _torch_paths()
-        torch_obj = os.path.join(OBJDIR, "torch_ops.o")
-        tcmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-x", "c++", "-D__HIP_PLATFORM_AMD__=1",
-                "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={_cxx11_abi()}"]
-        for i in inc + ["/opt/rocm/include"]:
-            tcmd += ["-isystem", i]
-        tcmd += ["-c", os.path.join(CSRC, "torch_ops.cpp"), "-o", torch_obj]
-        jobs.append(ex.submit(_run, tcmd))
+        torch_objs = []
+        for src in TORCH_SOURCES:
+            obj = os.path.join(OBJDIR, src.replace(".cpp", ".o"))
+            torch_objs.append(obj)
+            tcmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-x", "c++", "-D__HIP_PLATFORM_AMD__=1",
+                    "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={_cxx11_abi()}"]
+            for i in inc + ["/opt/rocm/include"]:
+                tcmd += ["-isystem", i]
+            tcmd += ["-c", os.path.join(CSRC, src), "-o", obj]
+            jobs.append(ex.submit(_run, tcmd))
         for j in jobs:
             out = j.result()
             if verbose and out.strip():
                 print(out)
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", HIP_LIB])
-    link = [HIPCC, "-shared", "-fPIC", torch_obj, "-o", TORCH_LIB, f"-L{LIBDIR}",
+    link = [HIPCC, "-shared", "-fPIC", *torch_objs, "-o", TORCH_LIB, f"-L{LIBDIR}",
             "-lturboquant_hip", "-Wl,-rpath,$ORIGIN"]
     for l in libs:
         link += [f"-L{l}", f"-Wl,-rpath,{l}"]

@@ -46,3 +46,10 @@ def require_device(t: torch.Tensor, name: str) -> None:
         raise RuntimeError(
             f"turboquant_kv: {name} must be a tensor on a HIP device; this MI355X build "
             "has no CPU kernels")
+
+
+def require_tensor(t: torch.Tensor, name: str) -> None:
+    """The five reference schemas run on HIP-device tensors (gfx950 kernels) and on CPU
+    tensors (their CPU kernels, as the reference registers): any tensor is accepted."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"turboquant_kv: {name} must be a torch.Tensor")

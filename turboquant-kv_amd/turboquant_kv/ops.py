@@ -2,7 +2,10 @@
 
 Unlike the reference's dispatch chain (Triton -> torch.ops -> Python, with every
 error swallowed, ops.py:51-56,159-179), each function here calls exactly one op
-and lets errors propagate.
+and lets errors propagate.  The five reference schemas (pack_codes, unpack_codes,
+rotate_and_quantize, attention_scores_packed, attention_values_packed) take tensors on
+a HIP device (gfx950 kernels) or in host memory (the CPU kernels the reference also
+registers, registration.cpp:106-112); every other op needs HIP-device tensors.
 """
 
 from __future__ import annotations
@@ -12,28 +15,29 @@ from typing import Tuple
 import torch
 
 from turboquant_kv._lib import ops as _ops, require_device as _require_device
+from turboquant_kv._lib import require_tensor as _require_tensor
 
 
 def pack_codes(codes: torch.Tensor, bit_width: int) -> torch.Tensor:
-    _require_device(codes, "codes")
+    _require_tensor(codes, "codes")
     return _ops().pack_codes(codes, bit_width)
 
 
 def unpack_codes(packed: torch.Tensor, bit_width: int, dim: int) -> torch.Tensor:
-    _require_device(packed, "packed")
+    _require_tensor(packed, "packed")
     return _ops().unpack_codes(packed, bit_width, dim)
 
 
 def rotate_and_quantize(vectors: torch.Tensor, rotation: torch.Tensor, boundaries: torch.Tensor,
                         bit_width: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """(packed, norms fp32) of fp32-upcast vectors (ops.py:74-104)."""
-    _require_device(vectors, "vectors")
+    _require_tensor(vectors, "vectors")
     return _ops().rotate_and_quantize(vectors, rotation, boundaries, bit_width)
 
 
 def attention_scores_packed(query, packed_keys, key_norms, centroids, rotation, bit_width):
     """scores[b, h, t] = n_t * (R q_bh) . c[code_t], no 1/sqrt(d) (ops.py:131-194)."""
-    _require_device(query, "query")
+    _require_tensor(query, "query")
     return _ops().attention_scores_packed(query, packed_keys, key_norms, centroids, rotation,
                                           bit_width)
 
@@ -42,7 +46,7 @@ def attention_values_packed(attn_weights, packed_values, value_norms, centroids,
                             bit_width):
     """out[b, h] = (sum_t w n_t c[code_t]) @ rotation_T; pass R itself to invert the
     rotation (ops.py:202-246)."""
-    _require_device(attn_weights, "attn_weights")
+    _require_tensor(attn_weights, "attn_weights")
     return _ops().attention_values_packed(attn_weights, packed_values, value_norms, centroids,
                                           rotation_T, bit_width)
 
