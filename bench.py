@@ -49,9 +49,19 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_op(fn, steps, warmup):
+def time_op(fn, steps, warmup, settle_s=0.0):
+    """Mean ms per call of `steps` calls after `warmup` untimed ones.  settle_s: before
+    the warm-up, keep calling fn for that long (untimed), so the GPU's clocks have settled
+    under this kernel's sustained load (a fresh box runs the first ~100 ms of a kernel up
+    to 20 % slower)."""
     import torch
 
+    if settle_s > 0:
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -126,7 +136,7 @@ def bench_scan(args, extra):
                                     "note": "same scan over the reference's bit-plane rows"}
     log(f"scan b=4 Q=1 (bit-plane rows): {t * 1e3:.1f} us/query, {bytes_alg / t / 1e6:.0f} GB/s")
     fn = lambda: ops.ip_scan_topk_pairs(q1, pairs, norms, cen, R, k)
-    ms = time_op(fn, args.steps, args.warmup)
+    ms = time_op(fn, args.steps, args.warmup, settle_s=0.3)
     res["headline"] = (ms, bytes_alg)
     log(f"scan b=4 Q=1 (pair layout): {ms * 1e3:.1f} us/query, {bytes_alg / ms / 1e6:.0f} GB/s")
     if not args.quick:
@@ -214,8 +224,8 @@ def bench_decode(args, extra):
         # steady state: the first tens of calls of a kernel on a fresh box run slow (clocks,
         # first-touch of the cache copies); 200 calls of the short contexts take < 10 ms
         steps = 200 if T < 32768 else 40
-        ms = time_op(fn, steps, 40)
-        ms_bp = time_op(fn_bitplane, steps, 40)
+        ms = time_op(fn, steps, 40, settle_s=0.3)
+        ms_bp = time_op(fn_bitplane, steps, 40, settle_s=0.1)
         bytes_alg = per + 2 * B * Hq * d * 2
         out[T] = (ms, bytes_alg)
         extra[f"decode_attn_T{T}"] = {"us_per_step": ms * 1e3, "GBps": bytes_alg / ms / 1e6,
@@ -242,7 +252,7 @@ def bench_decode(args, extra):
 
             pk, pkn, pv, pvn = (to_pool(t) for t in c[:4])
             ms_pg = time_op(lambda: ops.decode_attention_paged(q, pk, pkn, pv, pvn, tab, sl, ck, cv,
-                                                               Rk, Rv, kb, vb, 1.0 / 8.0), 20, 3)
+                                                               Rk, Rv, kb, vb, 1.0 / 8.0), 20, 3, settle_s=0.1)
             extra[f"decode_attn_T{T}"].update({"paged_bs16_us": ms_pg * 1e3,
                                                "paged_bs16_GBps": bytes_alg / ms_pg / 1e6})
             log(f"decode T={T} paged (block 16, shuffled): {ms_pg * 1e3:.1f} us, "
@@ -255,7 +265,7 @@ def bench_decode(args, extra):
             pvs = torch.empty(B * nbs, Hkv, 1, 4 * d, dtype=torch.uint8, device="cuda")
             pvs[perm] = sub.reshape(B * nbs, Hkv, 1, 4 * d)
             ms_p16 = time_op(lambda: ops.decode_attention_paged_dl(q, pkp, pkn, pvs, pvn, tab, sl, ck,
-                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3)
+                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3, settle_s=0.1)
             extra[f"decode_attn_T{T}"].update({"paged_dl_bs16_us": ms_p16 * 1e3,
                                                "paged_dl_bs16_GBps": bytes_alg / ms_p16 / 1e6})
             log(f"decode T={T} paged decode layout (block 16, shuffled): {ms_p16 * 1e3:.1f} us, "
@@ -272,7 +282,7 @@ def bench_decode(args, extra):
             pvt = torch.empty(B * nbs, Hkv, 1, 16 * d, dtype=torch.uint8, device="cuda")
             pvt[perm] = c[5].transpose(1, 2).reshape(B * nbs, Hkv, 1, 16 * d)
             ms_pdl = time_op(lambda: ops.decode_attention_paged_dl(q, pkp, pkn, pvt, pvn, tab, sl, ck,
-                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3)
+                                                                   cv, Rk, Rv, 1.0 / 8.0), 20, 3, settle_s=0.1)
             extra[f"decode_attn_T{T}"].update({"paged_dl_bs64_us": ms_pdl * 1e3,
                                                "paged_dl_bs64_GBps": bytes_alg / ms_pdl / 1e6})
             log(f"decode T={T} paged decode layout (block 64, shuffled): {ms_pdl * 1e3:.1f} us, "
