@@ -637,44 +637,39 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const int bg = (int)(W / (uint32_t)a.nsplit);
   const int b = bg / a.hkv;
   const int g = bg - b * a.hkv;
-  const int64_t T = min((int64_t)max(a.seq_lens[b], 0), a.t_cap);
+  // The sequence length is requested first, and nothing below is addressed through it
+  // until the prologue's loads (query, R_k, the first tiles) are all in flight: their
+  // latency and its own then overlap instead of following one another.
+  const int32_t slen = a.seq_lens[b];
   const int64_t t_begin = (int64_t)split * a.split_tokens;
-  const int64_t t_end = min(T, t_begin + a.split_tokens);
   const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.Gfull + a.hofs;
   const int tid = threadIdx.x;
-  if (t_begin >= t_end) {  // uniform
-    if (a.out != nullptr && T == 0 && tid < a.G * kDim) {  // empty sequence: zeros, lse -inf
-      store_from_f32(a.out, qh0 * kDim + tid, 0.f, a.q_dt);
-      if (a.lse && (tid & 63) == 0) a.lse[qh0 + (tid >> 6)] = -INFINITY;
-    }
-    return;
-  }
 
   const int wave = tid >> 6, lane = tid & 63;
   // Lane roles (see the score layout and the tile loads below).
   const int sl = lane >> 4, col = lane & 15;
   const int hh = lane & 3, gq = (lane >> 2) & 3;
-  // Contiguous: the buffers cover the stream's tokens below t_end.  Paged: they cover the
-  // whole pools, and a tile's block id comes through a buffer over the sequence's block
-  // table (entries past the blocks holding tokens below t_end read as block 0: loaded and
-  // masked; ids outside the pool address bytes outside the buffers, which read as zero).
+  // Contiguous: the buffers cover the stream's capacity (t_cap rows, all allocated).
+  // Paged: they cover the whole pools, and a tile's block id comes through a buffer over
+  // the sequence's block-table row (entries past the sequence's blocks name whatever
+  // block they hold: loaded and masked; ids outside the pool address bytes outside the
+  // buffers, which read as zero).  Tokens at or past t_end are masked by selects at their
+  // use, so what the loads return for them never matters.
   const size_t sbase = PAGED ? 0 : (size_t)bg * (size_t)a.t_cap;
-  const uint32_t nrows = PAGED ? a.pool_rows : (uint32_t)t_end;
+  const uint32_t nrows = PAGED ? a.pool_rows : (uint32_t)a.t_cap;
   const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, nrows * 32);
   const __amdgpu_buffer_rsrc_t vrs =
       make_rsrc(a.vblocks + sbase * (8 * VB),
-                PAGED ? nrows * (8 * VB) : (uint32_t)((t_end + 63) >> 6) * VTILE);
-  // Norms are read four tokens at a time: the range covers whole quads (inside the
-  // allocation, t_cap % 4 == 0); entries past t_end are masked.
-  const uint32_t nbytes = PAGED ? nrows * 4 : (uint32_t)((t_end + 3) >> 2) * 16;
+                PAGED ? nrows * (8 * VB) : (uint32_t)(a.t_cap >> 6) * VTILE);
+  // Norms are read four tokens at a time (t_cap % 4 == 0, pools of whole blocks).
+  const uint32_t nbytes = nrows * 4;
   const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
   const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
   const int bsl = PAGED ? a.bs_log2 : 0;
   const int kvh = g;  // the kv head (the tile loads below name their token groups g)
   const __amdgpu_buffer_rsrc_t btrs =
       make_rsrc(PAGED ? a.block_tables + (size_t)b * a.bt_stride : a.seq_lens,
-                PAGED ? (uint32_t)(((t_end + (1 << bsl) - 1) >> bsl) * 4) : 0u);
-  const int te = (int)t_end;
+                PAGED ? (uint32_t)a.bt_stride * 4u : 0u);
 
   struct Tile {
     u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
@@ -782,7 +777,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 
   constexpr int kStep = kDlWaves * 64;
   const int tf = (int)t_begin + wave * 64;
-  const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
   Tile ta, tb, tc;
 
   // ---- prologue.  Every global read is issued up front, in the order its data is needed
@@ -812,6 +806,19 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   load_tile(tf, ta, load_block(tf));
   load_tile(tf + kStep, tb, load_block(tf + kStep));
   bnx = load_block(tf + 2 * kStep);
+
+  // ---- the split's token range, now that the sequence length has had its latency
+  const int64_t T = min((int64_t)max(slen, 0), a.t_cap);
+  const int64_t t_end = min(T, t_begin + a.split_tokens);
+  if (t_begin >= t_end) {  // uniform
+    if (a.out != nullptr && T == 0 && tid < a.G * kDim) {  // empty sequence: zeros, lse -inf
+      store_from_f32(a.out, qh0 * kDim + tid, 0.f, a.q_dt);
+      if (a.lse && (tid & 63) == 0) a.lse[qh0 + (tid >> 6)] = -INFINITY;
+    }
+    return;
+  }
+  const int te = (int)t_end;
+  const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
   if (tid < 32) cen_s[tid] = cenv;
   if (tid < 4 * kDim) {
     const uint32_t bits = a.q_dt == TQ_F32 ? qraw : (qraw >> (8 * (qbyte & 2))) & 0xFFFFu;
@@ -1143,8 +1150,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   };
 
   // Tiles are loaded two ahead into three buffers used in turn: one tile of lookahead
-  // does not cover the HBM latency under full load.  Loads past te read zeros (buffer
-  // range check); the tile count is made wave-uniform explicitly.
+  // does not cover the HBM latency under full load (more lookahead measured slower: the
+  // extra tiles in flight delay the prologue's own reads).  Loads past te read data that
+  // is masked (or zeros past the buffers); the tile count is made wave-uniform explicitly.
   for (int it = 0; it < ntiles; it += 3) {
     const int t = tf + it * kStep;
     const Blk b1 = load_block(t + 3 * kStep);
