@@ -320,6 +320,19 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                            void* stream);
 
 /*
+ * The exact current token merged into a decode output (o, lse from
+ * tq_decode_attention_dl / tq_decode_attention_packed with the lse output) by
+ * log-sum-exp: replaces the HF cache's eager composition of that merge
+ * (turboquant_kv/hf_integration.py:372-390, which attends the token being decoded to its
+ * own unquantized key and value).  o, q, out [B, hq, d] in q_dtype; lse [B, hq] fp32 (natural
+ * log); k_new, v_new [B, hkv, d] in kv_dtype.  s = (q . k_new) * scale, m = max(lse, s),
+ * out = (o e^(lse - m) + v_new e^(s - m)) / (e^(lse - m) + e^(s - m)) in fp32.  out may be o.
+ */
+int tq_decode_merge_token(const void* o, const float* lse, const void* q, tq_dtype q_dtype,
+                          const void* k_new, const void* v_new, tq_dtype kv_dtype, int32_t B,
+                          int32_t hq, int32_t hkv, int32_t d, float scale, void* out, void* stream);
+
+/*
  * Paged KV storage (vLLM block tables).  The reference's vLLM backend keeps one
  * contiguous QuantizedKVCache per model with no block tables
  * (turboquant_kv/vllm_plugin/__init__.py:114-304, 350-412); these entry points give its

@@ -194,3 +194,33 @@ def test_vllm_attention_step_gqa():
     ref = c.attention_values(0, torch.softmax(logits, -1)).transpose(0, 1)
     assert (fused - ref).abs().max().item() <= 1e-4 * ref.abs().max().item()
     assert kv.get_seq_length(0) == 21 and kv.memory_bytes() > 0
+
+
+@pytest.mark.parametrize("dt,kvdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                      (torch.float16, torch.bfloat16)])
+def test_decode_merge_token_vs_float64(dt, kvdt):
+    """tq_decode_merge_token against the log-sum-exp merge of hf_integration.py:372-390 in
+    float64, including a row whose history is empty (lse = -inf: the output is v_new) and
+    queries that dominate either side."""
+    from turboquant_kv._lib import ops
+    g = torch.Generator(device="cuda").manual_seed(3)
+    B, Hq, Hkv, d, scale = 3, 8, 2, 64, 0.125
+    q = torch.randn(B, Hq, d, generator=g, device="cuda").to(dt)
+    o = torch.randn(B, Hq, d, generator=g, device="cuda").to(dt)
+    lse = torch.randn(B, Hq, generator=g, device="cuda") * 4
+    lse[0, 1] = -math.inf
+    k = (torch.randn(B, Hkv, d, generator=g, device="cuda") * 3).to(kvdt)
+    v = torch.randn(B, Hkv, d, generator=g, device="cuda").to(kvdt)
+    out = ops().decode_merge_token(o, lse, q, k, v, scale)
+    assert out.dtype == dt and out.shape == (B, Hq, d)
+    G = Hq // Hkv
+    kd = k.double().repeat_interleave(G, 1)
+    vd = v.double().repeat_interleave(G, 1)
+    s = (q.double() * kd).sum(-1) * scale
+    m = torch.maximum(lse.double(), s)
+    wh, wn = torch.exp(lse.double() - m), torch.exp(s - m)
+    want = (o.double() * wh[..., None] + vd * wn[..., None]) / (wh + wn)[..., None]
+    tol = 1e-5 if dt == torch.float32 else (1e-2 if dt == torch.bfloat16 else 2e-3)
+    err = (out.double() - want).abs().max().item()
+    assert err <= tol * want.abs().max().item(), err
+    assert torch.allclose(out[0, 1].double(), vd[0, 1], rtol=tol, atol=tol)

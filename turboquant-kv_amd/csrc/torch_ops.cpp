@@ -1012,6 +1012,34 @@ at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
                                              kcentroids, vcentroids, krotation, vrotation, scale));
 }
 
+// The exact current token merged into a decode output by log-sum-exp
+// (hf_integration.py:372-390): o [B, Hq, d] and lse [B, Hq] from a *_lse decode op, q
+// [B, Hq, d], k_new / v_new [B, Hkv, d]; returns [B, Hq, d] in q.dtype.
+at::Tensor decode_merge_token(const at::Tensor& o, const at::Tensor& lse, const at::Tensor& q,
+                              const at::Tensor& k_new, const at::Tensor& v_new, double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3 && o.dim() == 3 && k_new.dim() == 3 && v_new.dim() == 3,
+              "q / o must be [B, Hq, d] and k_new / v_new [B, Hkv, d]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  auto oo = o.to(dev, qq.scalar_type()).contiguous();
+  auto ls = f32c(lse, dev);
+  auto kn = floatc(k_new, dev);
+  auto vn = v_new.to(dev, kn.scalar_type()).contiguous();
+  const int64_t B = qq.size(0), Hq = qq.size(1), d = qq.size(2), Hkv = kn.size(1);
+  TORCH_CHECK(oo.sizes() == qq.sizes(), "o must match q's shape");
+  TORCH_CHECK(ls.numel() == B * Hq, "lse must be [B, Hq]");
+  TORCH_CHECK(kn.size(0) == B && kn.size(2) == d && vn.sizes() == kn.sizes(),
+              "k_new / v_new must be [B, Hkv, d]");
+  auto out = at::empty_like(qq);
+  check_rc(tq_decode_merge_token(oo.data_ptr(), ls.data_ptr<float>(), qq.data_ptr(),
+                                 to_tq(qq.scalar_type()), kn.data_ptr(), vn.data_ptr(),
+                                 to_tq(kn.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv,
+                                 (int32_t)d, (float)scale, out.data_ptr(), cur_stream(qq)));
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(turboquant, m) {
@@ -1081,6 +1109,8 @@ TORCH_LIBRARY(turboquant, m) {
   m.def("decode_attention_dl_lse(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, float scale) -> (Tensor, Tensor)");
+  m.def("decode_merge_token(Tensor o, Tensor lse, Tensor q, Tensor k_new, Tensor v_new,"
+        " float scale) -> Tensor");
   m.def("paged_store_value_tiles(Tensor rows, Tensor norms, Tensor slot_mapping,"
         " Tensor(a!) vtile_pool, Tensor(b!) vnorm_pool) -> ()");
   m.def("decode_attention_paged_dl(Tensor q, Tensor kpairs_pool, Tensor knorm_pool,"
@@ -1119,4 +1149,5 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("unpack_decode_layout", &unpack_decode_layout);
   m.impl("decode_attention_dl", &decode_attention_dl);
   m.impl("decode_attention_dl_lse", &decode_attention_dl_lse);
+  m.impl("decode_merge_token", &decode_merge_token);
 }

@@ -1570,6 +1570,37 @@ void launch_dl_kernel(tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStrea
     hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
 }
 
+// The exact current token merged into a decode output by log-sum-exp (the HF cache's
+// rule that the token being decoded attends to its own unquantized key and value,
+// hf_integration.py:372-390): one wave per query head h of batch row b, KV head
+// h / (hq / hkv).  s = (q . k_new) * scale; m = max(lse, s); out = (o e^(lse - m) +
+// v_new e^(s - m)) / (e^(lse - m) + e^(s - m)), in fp32, stored in the query's type.  `out`
+// may be `o` (each element is read and then written by the same lane).
+__global__ __launch_bounds__(64) void merge_token_kernel(const void* o, const float* __restrict__ lse,
+                                                         const void* __restrict__ q,
+                                                         const void* __restrict__ knew,
+                                                         const void* __restrict__ vnew, int hq,
+                                                         int hkv, int d, float scale, int q_dt,
+                                                         int kv_dt, void* out) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / hq;
+  const int h = (int)(row - b * hq);
+  const int64_t kvrow = b * hkv + h / (hq / hkv);
+  const int lane = threadIdx.x;
+  float dot = 0.f;
+  for (int j = lane; j < d; j += 64)
+    dot = fmaf(load_as_f32(q, row * d + j, q_dt), load_as_f32(knew, kvrow * d + j, kv_dt), dot);
+  dot = wave_sum(dot);
+  const float sn = dot * scale;
+  const float lh = lse[row];
+  const float m = fmaxf(lh, sn);
+  const float wh = expf(lh - m), wn = expf(sn - m), den = wh + wn;
+  for (int j = lane; j < d; j += 64) {
+    const float x = load_as_f32(o, row * d + j, q_dt) * wh + load_as_f32(vnew, kvrow * d + j, kv_dt) * wn;
+    store_from_f32(out, row * d + j, x / den, q_dt);
+  }
+}
+
 // The decode-layout kernel over every (stream, split), in launches of at most four query
 // heads per KV head, then (several splits) the log-sum-exp combine.  `a` carries
 // everything but the split plan, the head range and the outputs.
@@ -1731,6 +1762,23 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
   a.num_blocks = (uint32_t)std::max<int64_t>(num_blocks, 1);
   const int pg = (bsl >= 6 ? 1 : 2) + (wide ? 2 : 0);
   return run_dl(a, q_dtype, B, hq, hkv, 2, pg, p, workspace, out, lse, as_stream(stream));
+}
+
+int tq_decode_merge_token(const void* o, const float* lse, const void* q, tq_dtype q_dtype,
+                          const void* k_new, const void* v_new, tq_dtype kv_dtype, int32_t B,
+                          int32_t hq, int32_t hkv, int32_t d, float scale, void* out, void* stream) {
+  TQ_REQUIRE(valid_dtype(q_dtype) && valid_dtype(kv_dtype), "unknown dtype");
+  TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0,
+             "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
+  TQ_REQUIRE(d >= 1 && d <= 4096, "head_dim must be in [1, 4096], got %d", d);
+  const int64_t rows = (int64_t)B * hq;
+  TQ_REQUIRE(rows <= 0x7FFFFFFFll, "too many query heads in one call");
+  if (rows == 0) return TQ_OK;
+  TQ_REQUIRE(o && lse && q && k_new && v_new && out, "null pointer argument");
+  hipLaunchKernelGGL(merge_token_kernel, dim3((unsigned)rows), dim3(64), 0, as_stream(stream), o, lse, q,
+                     k_new, v_new, (int)hq, (int)hkv, (int)d, scale, (int)q_dtype, (int)kv_dtype, out);
+  TQ_LAUNCH_CHECK("merge_token_kernel");
+  return TQ_OK;
 }
 
 int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, int32_t d,

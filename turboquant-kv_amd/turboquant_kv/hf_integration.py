@@ -171,10 +171,10 @@ class TurboQuantLayer(_HFLayer):
                                           d, q.code_bits, vals, self.seq_len)
             else:
                 p[:, :, sl] = out[0].view(B, H, s, -1)
-            n[:, :, sl] = out[-1].float().view(B, H, s)
+            n[:, :, sl].copy_(out[-1].view(B, H, s))  # one cast-and-copy kernel
             if q.prod:
                 getattr(self, sg)[:, :, sl] = out[1].view(B, H, s, -1)
-                getattr(self, rs)[:, :, sl] = out[2].float().view(B, H, s)
+                getattr(self, rs)[:, :, sl].copy_(out[2].view(B, H, s))
         self.seq_len += s
 
     def dequantized(self, upto: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -296,6 +296,20 @@ def _sdpa_gqa(query, key, value, attention_mask, scaling):
     return out.transpose(1, 2).contiguous()
 
 
+_HIST_LENS: Dict[Any, torch.Tensor] = {}
+
+
+def _history_lengths(B: int, t_hist: int, device) -> torch.Tensor:
+    """[B] int32 tensor of t_hist, shared by every layer of a decode step (one fill per
+    step instead of one per layer)."""
+    key = (B, t_hist, str(device))
+    t = _HIST_LENS.get(key)
+    if t is None:
+        _HIST_LENS.clear()
+        t = _HIST_LENS[key] = torch.full((B,), t_hist, dtype=torch.int32, device=device)
+    return t
+
+
 def turboquant_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
                          **kwargs):
     """Attention function registered as "turboquant" with transformers."""
@@ -310,7 +324,7 @@ def turboquant_attention(module, query, key, value, attention_mask, scaling=None
     B, Hq, sq, d = query.shape
     if sq == 1 and attention_mask is None and t_hist > 0 and not layer.kq.prod:
         q = query[:, :, 0, :]
-        seq = torch.full((B,), t_hist, dtype=torch.int32, device=query.device)
+        seq = _history_lengths(B, t_hist, query.device)
         if layer.dl:
             o_h, lse_h = _ops().decode_attention_dl_lse(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
@@ -319,14 +333,10 @@ def turboquant_attention(module, query, key, value, attention_mask, scaling=None
             o_h, lse_h = _ops().decode_attention_packed_lse(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
                 layer.kq.R, layer.vq.R, layer.kq.bits, layer.vq.bits, float(scaling))
-        G = Hq // k_new.shape[1]
-        kn = k_new[:, :, 0, :].float().repeat_interleave(G, dim=1)        # (B, Hq, d)
-        vn = value[:, :, 0, :].float().repeat_interleave(G, dim=1)
-        s_new = (q.float() * kn).sum(-1) * scaling                          # (B, Hq)
-        m = torch.maximum(lse_h, s_new)
-        w_h = torch.exp(lse_h - m)
-        w_n = torch.exp(s_new - m)
-        out = (o_h.float() * w_h[..., None] + vn * w_n[..., None]) / (w_h + w_n)[..., None]
+        # the token being decoded attends to its own exact key and value: merged by
+        # log-sum-exp in one kernel (the eager composition of hf_integration.py:372-390)
+        out = _ops().decode_merge_token(o_h, lse_h, q, k_new[:, :, 0, :], value[:, :, 0, :],
+                                        float(scaling))
         return out.to(query.dtype).unsqueeze(1), None
     k_old, v_old = layer.dequantized(upto=t_hist)
     k_all = torch.cat([k_old, k_new.to(k_old.dtype)], dim=-2)
