@@ -1247,3 +1247,31 @@ def test_prod_scan_rejects_bad_bits():
             k_scan_prod(q, np.zeros((4, 8 * max(bits - 1, 1)), np.uint8), np.zeros((4, 8), np.uint8),
                         np.ones(4, np.float32), np.ones(4, np.float32), np.zeros(2, np.float32),
                         np.eye(64, dtype=np.float32), np.eye(64, dtype=np.float32), bits, 4)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantize_few_rows_equals_tiled_kernel(d, dt):
+    """A call of at most 16384 bf16/fp16 rows of d 64/128 (a decode step's append) runs one
+    wave per row; its codes and norms equal the tiled kernel's -- the same rows inside a
+    call of 20,000 rows -- bit for bit, and the oracle's outside the decision band."""
+    g = torch.Generator(device=DEV).manual_seed(d)
+    x = torch.randn(20000, d, generator=g, device=DEV) * 3
+    x[5] = 0.0
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    cdt = capi.TQ_BF16 if dt == "bf16" else capi.TQ_F16
+    xt = x.to(tdt).contiguous()
+    R = O.dense_qr_rotation(d, 42)
+    for bits in (1, 2, 3, 4):
+        bnd, _ = O.lloyd_max_codebook(bits, d)
+        big_p, big_n = k_quantize(xt, R, bnd, bits, cdt, cdt)
+        for n in (1, 37, 512):
+            p, nm = k_quantize(xt[:n].contiguous(), R, bnd, bits, cdt, cdt)
+            assert np.array_equal(p, big_p[:n]), (bits, n)
+            assert np.array_equal(nm.view(np.uint32), big_n[:n].view(np.uint32)), (bits, n)
+        # against the oracle: identical outside the decision band (inside it the reduced-
+        # precision sums flip often -- the tiled kernel these equal is the one pinned to
+        # reference.py's own bf16 codes by the golden test above)
+        xf = xt[:512].float().cpu().numpy()
+        O.check_codes(O.unpack_codes(p, bits, d), O.quantize_mse(xf, bits, R, bnd, dt)[2], xf, R,
+                      bnd, dt, max_rate=1.0)

@@ -665,6 +665,86 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(DequantArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- one row per wave (few rows)
+// quantize_kernel<false>'s arithmetic, bit for bit, for bf16/fp16 inputs of d = 64 / 128,
+// with one wave per row (lane j owns output dims j and j + 64): a decode step appends one
+// token per (sequence, KV head) -- a few hundred rows -- which 16-row tiles would spread
+// over a few dozen workgroups, each walking its tile through five barriers.  Here R (its
+// elements rounded to the input type, transposed: Rt[k][j]) sits in LDS; per row the norm
+// (fmaf over the lane's dims, then the wave sum: tile_norms' order), the unit vector
+// (rounded), y_j = sum_k fmaf(u_k, R[j][k]) for k ascending (contract_rows' order), the
+// code (count_below) and the bit planes from ballots (dim j at bit 7 - j % 8 of byte j / 8).
+constexpr int kQrThreads = 256;
+constexpr int64_t kQrMaxRows = 16384;  // above this the tiled kernel is as fast
+
+template <int D>
+__global__ __launch_bounds__(kQrThreads) void quantize_rows_kernel(QuantArgs a) {
+  constexpr int C = D / 64;  // output dims per lane
+  constexpr int BPP = D / 8;
+  __shared__ float rt_s[D][D + 1];  // padded: the transposing writes hit distinct banks
+  __shared__ float u_s[kQrThreads / 64][D];
+  __shared__ float bnd_s[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rdt = a.rdt;
+  const int nlev = 1 << a.bits;
+  if (threadIdx.x < nlev - 1) bnd_s[threadIdx.x] = round_to(a.bnd[threadIdx.x], rdt);
+  for (int e = threadIdx.x; e < D * D; e += kQrThreads) {  // coalesced read of R row j
+    const int j = e / D, k = e - j * D;
+    rt_s[k][j] = round_to(a.rot[e], rdt);
+  }
+  __syncthreads();
+  const float eps = round_to(1e-10f, rdt);
+  const int P = a.bits * BPP;
+  for (int64_t row = (int64_t)blockIdx.x * (kQrThreads / 64) + wave; row < a.n;
+       row += (int64_t)gridDim.x * (kQrThreads / 64)) {
+    float x[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) x[c] = load_as_f32(a.x, row * D + lane + 64 * c, a.in_dt);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) ss = fmaf(x[c], x[c], ss);
+    ss = wave_sum(ss);
+    const float nrm = round_to(sqrtf(ss), rdt);
+    if (lane == 0) a.norms[row] = nrm;
+    const float den = fmaxf(nrm, eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) u_s[wave][lane + 64 * c] = round_to(x[c] / den, rdt);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float acc[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < D; ++k) {
+      const float uk = u_s[wave][k];
+#pragma unroll
+      for (int c = 0; c < C; ++c) acc[c] = fmaf(uk, rt_s[k][lane + 64 * c], acc[c]);
+    }
+    uint32_t code[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) code[c] = (uint32_t)count_below(bnd_s, nlev, round_to(acc[c], rdt));
+    // lane L < P writes byte L of the row: plane L / BPP, dims 8 (L % BPP) .. + 7
+    uint8_t out = 0;
+#pragma unroll
+    for (int pl = 0; pl < 4; ++pl) {
+      if (pl < a.bits) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const uint64_t m = __ballot((code[c] >> pl) & 1u);
+          const int b = lane - pl * BPP - 8 * c;  // byte of this plane held in mask c
+          if (b >= 0 && b < 8)
+            out = (uint8_t)(__builtin_bitreverse32((uint32_t)(m >> (8 * b)) & 0xFFu) >> 24);
+        }
+      }
+    }
+    if (lane < P) a.packed[row * P + lane] = out;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // u_s is rewritten by the next row
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 int grid_for_tiles(int64_t n) {
   const int64_t tiles = (n + kRows - 1) / kRows;
   const int64_t cap = (int64_t)device_cu_count() * 6;
@@ -757,6 +837,16 @@ int tq_rotate_and_quantize(const void* vectors, tq_dtype in_dtype, tq_dtype roun
   if (use_mfma_quantize(vectors, in_dtype, round_dtype, d)) {
     launch_quantize_mfma<false>(a, as_stream(stream));
     TQ_LAUNCH_CHECK("quantize_mfma_kernel<mse>");
+    return TQ_OK;
+  }
+  if ((d == 64 || d == 128) && in_dtype != TQ_F32 && n <= kQrMaxRows) {  // few rows: a wave each
+    const int64_t waves_per_cu = d == 64 ? 16 : 8;  // LDS: 16 / 64 KB of R per workgroup
+    const int64_t cap = (int64_t)device_cu_count() * waves_per_cu / (kQrThreads / 64);
+    const int64_t want = (n + kQrThreads / 64 - 1) / (kQrThreads / 64);
+    const dim3 grid((unsigned)(want < cap ? want : cap));
+    if (d == 64) hipLaunchKernelGGL(quantize_rows_kernel<64>, grid, dim3(kQrThreads), 0, as_stream(stream), a);
+    else hipLaunchKernelGGL(quantize_rows_kernel<128>, grid, dim3(kQrThreads), 0, as_stream(stream), a);
+    TQ_LAUNCH_CHECK("quantize_rows_kernel");
     return TQ_OK;
   }
   hipLaunchKernelGGL(quantize_kernel<false>, dim3(grid_for_tiles(n)), dim3(kThreads), 0,
