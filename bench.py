@@ -407,15 +407,24 @@ def bench_prod_scan(args, extra):
         del x, a, s_, r_, n_
     q1 = queries(1, d, seed=4)
     bytes_alg = N * ((b - 1) * bpp + bpp + 8) + d * 2 + k * 12
-    ms = time_op(lambda: ops.ip_scan_topk_prod(q1, mp, sg, rn, nm, cen, R, S, b, k), 30, 3)
+    # bit-plane MSE halves first (the comparison line), then the pair rows TurboQuantIndex
+    # stores (same bytes per row, scores bit-identical)
+    ms_bp = time_op(lambda: ops.ip_scan_topk_prod(q1, mp, sg, rn, nm, cen, R, S, b, k), 30, 3,
+                    settle_s=0.1)
+    rows = ops.pack_pair_rows(mp, b - 1, d)
+    ms = time_op(lambda: ops.ip_scan_topk_prod_pair_rows(q1, rows, sg, rn, nm, cen, R, S, b, k), 30, 3,
+                 settle_s=0.2)
     gbs = bytes_alg / ms / 1e6
     extra["scan_prod_b4_Q1"] = {
         "us_per_query": ms * 1e3, "queries_per_s": 1e3 / ms, "GBps": gbs,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "bytes_per_launch": bytes_alg},
-        "kernel": "scan_kernel<3,16,1,true,false,false,true> + merge_kernel",
+        "kernel": "pair_scan_kernel<128,true,3,true> + merge_kernel (MSE half as pair rows)",
+        "bitplane_rows_us": ms_bp * 1e3,
         "workload": "ip_scan_topk_prod N=10,000,000 d=128 bits=4 (3+1) Q=1 fp16 query k=10"}
-    log(f"prod scan b=4 Q=1: {ms * 1e3:.1f} us/query, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.0%})")
+    log(f"prod scan b=4 Q=1: {ms * 1e3:.1f} us/query, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.0%}); "
+        f"bit-plane MSE rows {ms_bp * 1e3:.1f} us")
+    del rows
     if not args.quick:
         qf = q1.float()
 

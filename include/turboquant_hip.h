@@ -169,6 +169,27 @@ int tq_attention_scores_pairs(const void* query, tq_dtype q_dtype, int64_t nq, i
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Prod-mode scoring over pair rows: tq_ip_scan_topk_prod / tq_attention_scores_prod
+ * (same arguments, scores bit-identical) with the MSE half stored as pair rows
+ * (tq_pack_pair_rows of the bit_width - 1 bit codes; bit_width 3 or 4, d 64 or 128) beside
+ * the bit-plane sign rows and the residual norms.  Replaces the reference's prod search
+ * (turboquant_kv/search.py:229-252: dequantize every row, matmul); pair rows and sign rows
+ * 16-byte aligned.
+ */
+int tq_ip_scan_topk_prod_pair_rows(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                   const uint8_t* mse_rows, const uint8_t* signs,
+                                   const float* res_norms, const float* norms, int64_t N,
+                                   const float* centroids, const float* rotation, const float* qjl,
+                                   int32_t bit_width, int32_t k, float* out_scores, int64_t* out_ids,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+int tq_attention_scores_prod_pair_rows(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                       const uint8_t* mse_rows, const uint8_t* signs,
+                                       const float* res_norms, const float* key_norms, int64_t T,
+                                       const float* centroids, const float* rotation,
+                                       const float* qjl, int32_t bit_width, float* scores,
+                                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Pair rows: 2-, 3- or 4-bit codes arranged so one table index covers the codes of a pair
  * of dims (2p, 2p+1), same bytes per row as the bit-plane rows (d * bits / 8), d = 64 or
  * 128.  TurboQuantIndex keeps its MSE databases of those dims in this form.

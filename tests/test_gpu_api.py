@@ -158,7 +158,7 @@ def test_prod_index_search_scores_without_reconstruction():
         db = rs.randn(3000, d).astype(np.float32)
         idx = TurboQuantIndex.from_vectors(T(db), bit_width=b, mode="prod")
         q = rs.randn(6, d).astype(np.float32)
-        rows = [t.cpu().numpy() for t in (idx._packed_codes, idx._qjl_signs,
+        rows = [t.cpu().numpy() for t in (idx._bitplane_codes(), idx._qjl_signs,
                                           idx._residual_norms, idx._norms)]
         R, S = idx._rot_dev.cpu().numpy(), idx._S_dev.cpu().numpy()
         ref = O.prod_scores_f64(q, *rows, b, d, R, idx._cen.cpu().numpy(), S)
@@ -166,7 +166,7 @@ def test_prod_index_search_scores_without_reconstruction():
         # |q| n (1 + 2 gamma)
         tol = d * 2.0 ** -24 * np.linalg.norm(q, axis=1)[:, None] * rows[3][None, :] * (1 + 2 * rows[2][None, :])
         recon = torch.ops.turboquant.dequantize_prod_packed(
-            idx._packed_codes, idx._qjl_signs, idx._residual_norms, idx._norms, idx._cen,
+            idx._bitplane_codes(), idx._qjl_signs, idx._residual_norms, idx._norms, idx._cen,
             idx._rot_dev, idx._S_dev, b, d)
         composed = (T(q) @ recon.t()).cpu().numpy()
         assert np.all(np.abs(composed - ref) <= tol)

@@ -1275,3 +1275,30 @@ def test_quantize_few_rows_equals_tiled_kernel(d, dt):
         xf = xt[:512].float().cpu().numpy()
         O.check_codes(O.unpack_codes(p, bits, d), O.quantize_mse(xf, bits, R, bnd, dt)[2], xf, R,
                       bnd, dt, max_rate=1.0)
+
+
+@pytest.mark.parametrize("d,b", [(128, 4), (64, 4), (128, 3), (64, 3)])
+def test_prod_pair_rows_equal_bitplane_prod_scan(d, b):
+    """Prod scoring with the MSE half as pair rows is the bit-plane prod scan bit for bit:
+    top-k ids and scores (one query and several), and every score of the all-rows op."""
+    from turboquant_kv._lib import ops
+    g = torch.Generator(device=DEV).manual_seed(d + b)
+    N = 70_001
+    x = torch.randn(N, d, generator=g, device=DEV)
+    x[7] = 0.0
+    R = T(O.dense_qr_rotation(d, 42))
+    bnd, cen = O.lloyd_max_codebook(b - 1, d)
+    S = T(O.qjl_matrix(d, d, 42))
+    mp, sg, rn, nm = ops().quantize_prod_packed(x, R, T(bnd), T(cen), S, b)
+    rows = ops().pack_pair_rows(mp, b - 1, d)
+    for Q in (1, 5):
+        q = torch.randn(Q, d, generator=g, device=DEV).half()
+        s0, i0 = ops().ip_scan_topk_prod(q, mp, sg, rn, nm, T(cen), R, S, b, 10)
+        s1, i1 = ops().ip_scan_topk_prod_pair_rows(q, rows, sg, rn, nm, T(cen), R, S, b, 10)
+        assert torch.equal(i0, i1)
+        assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+    qa = torch.randn(2, 3, d, generator=g, device=DEV)
+    a0 = ops().attention_scores_prod(qa, mp[:5000], sg[:5000], rn[:5000], nm[:5000], T(cen), R, S, b)
+    a1 = ops().attention_scores_prod_pair_rows(qa, rows[:5000], sg[:5000], rn[:5000], nm[:5000],
+                                               T(cen), R, S, b)
+    assert torch.equal(a0.view(torch.int32), a1.view(torch.int32))

@@ -403,15 +403,16 @@ ProdRowsT prod_rows(const at::Tensor& mse_packed, const at::Tensor& signs,
 
 // <q, dequantize_prod(row)> for every row, top-k (search.py:229-252 without the
 // reconstruction).
-std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod(const at::Tensor& queries,
-                                                     const at::Tensor& mse_packed,
-                                                     const at::Tensor& signs,
-                                                     const at::Tensor& res_norms,
-                                                     const at::Tensor& norms,
-                                                     const at::Tensor& centroids,
-                                                     const at::Tensor& rotation,
-                                                     const at::Tensor& qjl, int64_t bit_width,
-                                                     int64_t k) {
+// pairs: the MSE half as pair rows (tq_ip_scan_topk_prod_pair_rows; same row width).
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod_impl(const at::Tensor& queries,
+                                                          const at::Tensor& mse_packed,
+                                                          const at::Tensor& signs,
+                                                          const at::Tensor& res_norms,
+                                                          const at::Tensor& norms,
+                                                          const at::Tensor& centroids,
+                                                          const at::Tensor& rotation,
+                                                          const at::Tensor& qjl, int64_t bit_width,
+                                                          int64_t k, bool pairs) {
   require_gpu(queries, "queries");
   TORCH_CHECK(queries.dim() == 2, "queries must be [Q, d]");
   c10::DeviceGuard g(queries.device());
@@ -424,22 +425,38 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod(const at::Tensor& queries,
   auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
   if (Q == 0) return {os, oi};
   auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
-  check_rc(tq_ip_scan_topk_prod(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
-                                r.mp.data_ptr<uint8_t>(), r.sg.data_ptr<uint8_t>(),
-                                r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), N,
-                                r.cen.data_ptr<float>(), r.R.data_ptr<float>(),
-                                r.S.data_ptr<float>(), (int32_t)bit_width, (int32_t)k,
-                                os.data_ptr<float>(), oi.data_ptr<int64_t>(), ws.data_ptr(),
-                                ws.numel(), cur_stream(q)));
+  check_rc((pairs ? tq_ip_scan_topk_prod_pair_rows : tq_ip_scan_topk_prod)(
+      q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d, r.mp.data_ptr<uint8_t>(),
+      r.sg.data_ptr<uint8_t>(), r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), N,
+      r.cen.data_ptr<float>(), r.R.data_ptr<float>(), r.S.data_ptr<float>(), (int32_t)bit_width,
+      (int32_t)k, os.data_ptr<float>(), oi.data_ptr<int64_t>(), ws.data_ptr(), ws.numel(),
+      cur_stream(q)));
   return {os, oi};
 }
 
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod(const at::Tensor& queries, const at::Tensor& mse_packed,
+                                                     const at::Tensor& signs, const at::Tensor& res_norms,
+                                                     const at::Tensor& norms, const at::Tensor& centroids,
+                                                     const at::Tensor& rotation, const at::Tensor& qjl,
+                                                     int64_t bit_width, int64_t k) {
+  return ip_scan_topk_prod_impl(queries, mse_packed, signs, res_norms, norms, centroids, rotation,
+                                qjl, bit_width, k, false);
+}
+
+std::tuple<at::Tensor, at::Tensor> ip_scan_topk_prod_pair_rows(
+    const at::Tensor& queries, const at::Tensor& mse_rows, const at::Tensor& signs,
+    const at::Tensor& res_norms, const at::Tensor& norms, const at::Tensor& centroids,
+    const at::Tensor& rotation, const at::Tensor& qjl, int64_t bit_width, int64_t k) {
+  return ip_scan_topk_prod_impl(queries, mse_rows, signs, res_norms, norms, centroids, rotation,
+                                qjl, bit_width, k, true);
+}
+
 // attention_scores_packed for prod-mode keys: query [B, H, d] -> [B, H, T] fp32.
-at::Tensor attention_scores_prod(const at::Tensor& query, const at::Tensor& mse_packed,
-                                 const at::Tensor& signs, const at::Tensor& res_norms,
-                                 const at::Tensor& key_norms, const at::Tensor& centroids,
-                                 const at::Tensor& rotation, const at::Tensor& qjl,
-                                 int64_t bit_width) {
+at::Tensor attention_scores_prod_impl(const at::Tensor& query, const at::Tensor& mse_packed,
+                                      const at::Tensor& signs, const at::Tensor& res_norms,
+                                      const at::Tensor& key_norms, const at::Tensor& centroids,
+                                      const at::Tensor& rotation, const at::Tensor& qjl,
+                                      int64_t bit_width, bool pairs) {
   require_gpu(query, "query");
   TORCH_CHECK(query.dim() == 3, "query must be [batch, heads, head_dim]");
   c10::DeviceGuard g(query.device());
@@ -452,14 +469,29 @@ at::Tensor attention_scores_prod(const at::Tensor& query, const at::Tensor& mse_
   auto scores = at::empty({B, H, T}, q.options());
   if (B * H == 0 || T == 0) return scores;
   auto ws = workspace(tq_scan_workspace_bytes(B * H, (int32_t)d, (int32_t)bit_width, T, 0), dev);
-  check_rc(tq_attention_scores_prod(q.data_ptr(), TQ_F32, B * H, (int32_t)d,
-                                    r.mp.data_ptr<uint8_t>(), r.sg.data_ptr<uint8_t>(),
-                                    r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), T,
-                                    r.cen.data_ptr<float>(), r.R.data_ptr<float>(),
-                                    r.S.data_ptr<float>(), (int32_t)bit_width,
-                                    scores.data_ptr<float>(), ws.data_ptr(), ws.numel(),
-                                    cur_stream(q)));
+  check_rc((pairs ? tq_attention_scores_prod_pair_rows : tq_attention_scores_prod)(
+      q.data_ptr(), TQ_F32, B * H, (int32_t)d, r.mp.data_ptr<uint8_t>(), r.sg.data_ptr<uint8_t>(),
+      r.rn.data_ptr<float>(), r.nm.data_ptr<float>(), T, r.cen.data_ptr<float>(),
+      r.R.data_ptr<float>(), r.S.data_ptr<float>(), (int32_t)bit_width, scores.data_ptr<float>(),
+      ws.data_ptr(), ws.numel(), cur_stream(q)));
   return scores;
+}
+
+at::Tensor attention_scores_prod(const at::Tensor& query, const at::Tensor& mse_packed,
+                                 const at::Tensor& signs, const at::Tensor& res_norms,
+                                 const at::Tensor& key_norms, const at::Tensor& centroids,
+                                 const at::Tensor& rotation, const at::Tensor& qjl, int64_t bit_width) {
+  return attention_scores_prod_impl(query, mse_packed, signs, res_norms, key_norms, centroids,
+                                    rotation, qjl, bit_width, false);
+}
+
+at::Tensor attention_scores_prod_pair_rows(const at::Tensor& query, const at::Tensor& mse_rows,
+                                           const at::Tensor& signs, const at::Tensor& res_norms,
+                                           const at::Tensor& key_norms, const at::Tensor& centroids,
+                                           const at::Tensor& rotation, const at::Tensor& qjl,
+                                           int64_t bit_width) {
+  return attention_scores_prod_impl(query, mse_rows, signs, res_norms, key_norms, centroids,
+                                    rotation, qjl, bit_width, true);
 }
 
 // Pair rows of 2-4 bit codes (d * bits / 8 bytes per row, d = 64 or 128): conversion
@@ -1092,6 +1124,12 @@ TORCH_LIBRARY(turboquant, m) {
         " -> (Tensor, Tensor)");
   m.def("attention_scores_prod(Tensor query, Tensor mse_packed, Tensor signs, Tensor res_norms,"
         " Tensor key_norms, Tensor centroids, Tensor rotation, Tensor qjl, int bit_width) -> Tensor");
+  m.def("ip_scan_topk_prod_pair_rows(Tensor queries, Tensor mse_rows, Tensor signs, Tensor res_norms,"
+        " Tensor norms, Tensor centroids, Tensor rotation, Tensor qjl, int bit_width, int k)"
+        " -> (Tensor, Tensor)");
+  m.def("attention_scores_prod_pair_rows(Tensor query, Tensor mse_rows, Tensor signs,"
+        " Tensor res_norms, Tensor key_norms, Tensor centroids, Tensor rotation, Tensor qjl,"
+        " int bit_width) -> Tensor");
   m.def("decode_attention_packed(Tensor q, Tensor kpacked, Tensor knorms, Tensor vpacked,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
         " Tensor krotation, Tensor vrotation, int kbits, int vbits, float scale) -> Tensor");
@@ -1143,6 +1181,8 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("paged_store_value_tiles", &paged_store_value_tiles);
   m.impl("decode_attention_paged_dl", &decode_attention_paged_dl);
   m.impl("attention_scores_prod", &attention_scores_prod);
+  m.impl("ip_scan_topk_prod_pair_rows", &ip_scan_topk_prod_pair_rows);
+  m.impl("attention_scores_prod_pair_rows", &attention_scores_prod_pair_rows);
   m.impl("decode_attention_packed", &decode_attention_packed);
   m.impl("decode_attention_packed_lse", &decode_attention_packed_lse);
   m.impl("pack_decode_layout", &pack_decode_layout);

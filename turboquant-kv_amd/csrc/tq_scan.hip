@@ -832,19 +832,27 @@ __device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count
 
 // BITS 4: the pair layout with the centroid-pair table and register products above; BITS 2,
 // 3: pair rows with the per-block table of products (pmp_row).
-template <int D, bool TOPK, int BITS = 4>
+// PROD (BITS 2, 3): prod rows -- the MSE half as pair rows, the sign row and the residual
+// norm gamma beside it -- scored as scan_kernel<BITS, ..., PROD> scores them, bit for bit:
+// the same MSE sum (per-dim LUT products in dim order), the QJL term as a sum of
+// build_tables' sign-nibble entries in group order, acc = fma(gamma, sacc, acc).
+template <int D, bool TOPK, int BITS = 4, bool PROD = false>
 __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
   static_assert(D == 64 || D == 128, "pair scan dims");
   static_assert(BITS >= 2 && BITS <= 4, "pair rows of 2-4 bit codes");
+  static_assert(!PROD || BITS <= 3, "prod pair rows: 2- or 3-bit MSE codes");
+  constexpr int SB = D / 8;  // sign bytes per row
   constexpr int RB = D * BITS / 8;  // bytes per row
   constexpr int NW = RB / 4;        // 32-bit words per row
   constexpr int NQ = D / 16;        // q_rot registers
   static_assert(BITS != 4 || RB % kPairGroup == 0, "whole byte groups per row");
   constexpr int CT = BITS == 4 ? kCtabBytes : (D / 2) * pmp_pair_bytes<BITS>();
   __shared__ __attribute__((aligned(16))) char ctab[CT];
+  __shared__ __attribute__((aligned(16))) char sgn_s[PROD ? D * 16 : 16];  // (D/4) x 16 entries
   __shared__ float qs_s[D];
   __shared__ float qr_s[D];
+  __shared__ float qss_s[PROD ? D : 1];
   __shared__ float cen_s[16];
   __shared__ float cand_s[TOPK ? kPsWaves * kCandCap : 1];
   __shared__ int cand_i[TOPK ? kPsWaves * kCandCap : 1];
@@ -872,10 +880,16 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
   struct RowBuf {
     uint32_t w[NW];
     float n;
+    uint32_t sw[PROD ? SB / 4 : 1];  // prod: sign row
+    float g;                          // prod: residual norm
   };
   const uint32_t nbr = (uint32_t)(rend > rbeg ? rend - rbeg : 0);
   const __amdgpu_buffer_rsrc_t rows_rs = buf_rsrc(base + rbeg * RB, nbr * (uint32_t)RB);
   const __amdgpu_buffer_rsrc_t norm_rs = buf_rsrc(nbase + rbeg, nbr * 4u);
+  const __amdgpu_buffer_rsrc_t sgn_rs =
+      buf_rsrc(PROD ? a.signs + ((size_t)s * a.stream_rows + rbeg) * SB : a.packed, PROD ? nbr * (uint32_t)SB : 0u);
+  const __amdgpu_buffer_rsrc_t gam_rs =
+      buf_rsrc(PROD ? a.gammas + (size_t)s * a.stream_rows + rbeg : a.norms, PROD ? nbr * 4u : 0u);
   auto load_row = [&](int64_t r, RowBuf& b) {
     const uint32_t rr = (uint32_t)(r - rbeg);
     const int off = (int)(rr * (uint32_t)RB);
@@ -889,6 +903,16 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
       b.w[NW - 2] = v.x; b.w[NW - 1] = v.y;
     }
     b.n = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(norm_rs, (int)(rr * 4u), 0, kNT));
+    if constexpr (PROD) {
+      if constexpr (SB == 16) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(sgn_rs, (int)(rr * 16u), 0, 0);
+        b.sw[0] = v.x; b.sw[1] = v.y; b.sw[2] = v.z; b.sw[3] = v.w;
+      } else {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(sgn_rs, (int)(rr * 8u), 0, 0);
+        b.sw[0] = v.x; b.sw[1] = v.y;
+      }
+      b.g = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(gam_rs, (int)(rr * 4u), 0, kNT));
+    }
   };
 
   constexpr int64_t kStride = kPsWaves * 64;
@@ -912,6 +936,18 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
       v = v + qs_s[k + 3] * r4.w;
     }
     qr_s[tid] = v;
+  } else if (PROD && tid >= 2 * D && tid < 3 * D) {  // S q, build_tables' arithmetic
+    const int j = tid - 2 * D;
+    const float* sr = a.qjl + (size_t)j * D;
+    float w = 0.f;
+    for (int k = 0; k < D; k += 4) {
+      const float4 s4 = *reinterpret_cast<const float4*>(sr + k);
+      w = fmaf(qs_s[k], s4.x, w);
+      w = fmaf(qs_s[k + 1], s4.y, w);
+      w = fmaf(qs_s[k + 2], s4.z, w);
+      w = fmaf(qs_s[k + 3], s4.w, w);
+    }
+    qss_s[j] = w;
   }
   if constexpr (BITS == 4) {
     for (int e = tid; e < 256 * 16; e += kPsThreads) {  // entry b, copies 2c and 2c + 1
@@ -927,6 +963,18 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
       const int pp = e / (L * L), i = e - pp * (L * L);
       *reinterpret_cast<float2*>(ctab + e * 8) =
           make_float2(qr_s[2 * pp] * cen_s[i >> BITS], qr_s[2 * pp + 1] * cen_s[i & (L - 1)]);
+    }
+    if constexpr (PROD) {  // sign-nibble entries (g, v), layout (g>>1)*128 + v*8 + (g&1)*4
+      for (int e = tid; e < D * 4; e += kPsThreads) {
+        const int g = e >> 4, v = e & 15;
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = qss_s[4 * g + i];
+          t += ((v >> (3 - i)) & 1) ? x : -x;
+        }
+        *reinterpret_cast<float*>(sgn_s + (g >> 1) * 128 + v * 8 + (g & 1) * 4) = t * a.qjl_scale;
+      }
     }
     __syncthreads();
   }
@@ -951,6 +999,15 @@ __global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
       acc = pair_row<NQ>(rb.w, copy8, ctab, qv, std::make_integer_sequence<int, RB / kPairGroup>{});
     } else {
       acc = pmp_row<BITS, D>(rb.w, ctab);
+    }
+    if constexpr (PROD) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int w = 0; w < SB / 4; ++w)
+        decode_pairs<8>(rb.sw[w], 8 * w, [&](int g, uint32_t addr) {
+          sacc += *reinterpret_cast<const float*>(sgn_s + (g >> 1) * 128 + (g & 1) * 4 + addr);
+        });
+      acc = fmaf(rb.g, sacc, acc);
     }
     float sc = acc * rb.n * a.post_scale;
     // materialized here: sunk into a branch that uses it, the products would be split
@@ -2414,16 +2471,21 @@ int pair_scan_blocks(int64_t nrows) {
   return b < 1 ? 1 : b;
 }
 
-template <bool TOPK, int BITS>
+template <bool TOPK, int BITS, bool PROD = false>
 int launch_pair_scan_b(const ScanArgs& a, dim3 grid, hipStream_t st) {
-  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK, BITS>), grid, dim3(kPsThreads), 0, st, a);
-  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK, BITS>), grid, dim3(kPsThreads), 0, st, a);
+  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK, BITS, PROD>), grid, dim3(kPsThreads), 0, st, a);
+  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK, BITS, PROD>), grid, dim3(kPsThreads), 0, st, a);
   TQ_LAUNCH_CHECK("pair_scan_kernel");
   return TQ_OK;
 }
 
 template <bool TOPK>
 int launch_pair_scan(const ScanArgs& a, dim3 grid, hipStream_t st, int bits = 4) {
+  if (a.signs) {  // prod rows: `bits` is the MSE half's width
+    if (bits == 2) return launch_pair_scan_b<TOPK, 2, true>(a, grid, st);
+    if (bits == 3) return launch_pair_scan_b<TOPK, 3, true>(a, grid, st);
+    return fail(TQ_EINVAL, "prod pair rows hold 2- or 3-bit MSE codes, got %d", bits);
+  }
   if (bits == 2) return launch_pair_scan_b<TOPK, 2>(a, grid, st);
   if (bits == 3) return launch_pair_scan_b<TOPK, 3>(a, grid, st);
   return launch_pair_scan_b<TOPK, 4>(a, grid, st);
@@ -2449,6 +2511,7 @@ int launch_scan(const ScanArgs& a, int bits, bool topk, int nstreams, hipStream_
   if (pairs) {
     if (bits < 2 || bits > 4 || !aligned || (a.bpp != 8 && a.bpp != 16))
       return fail(TQ_EINVAL, "pair-row scan needs 2-4 bit codes, dim 64 or 128 and a 16-byte aligned base");
+    if (a.signs && !pair1) return fail(TQ_EINVAL, "prod pair rows need 2- or 3-bit MSE codes");
     if (pair1) return topk ? launch_pair_scan<true>(a, grid, st, bits) : launch_pair_scan<false>(a, grid, st, bits);
     return topk ? launch_scan_pairs<true>(a, qb, grid, st) : launch_scan_pairs<false>(a, qb, grid, st);
   }
@@ -2598,7 +2661,7 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
     return launch_filter(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
                          out_scores, out_ids, static_cast<char*>(workspace) + 256, st);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  TQ_REQUIRE(!pairs || bit_width == 4 || nq <= 65535, "too many queries in one call");
+  TQ_REQUIRE(!pairs || (prod ? bit_width - 1 : bit_width) == 4 || nq <= 65535, "too many queries in one call");
   int nb = 0;
   const int rc = launch_scan(a, prod ? bit_width - 1 : bit_width, true, 1, st, pairs, &nb);
   if (rc != TQ_OK) return rc;
@@ -2633,7 +2696,7 @@ int attention_scores(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
   a.k = 0; a.scores = scores;
   if (prod) set_prod(a, *prod);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");
-  TQ_REQUIRE(!pairs || bit_width == 4 || nq <= 65535, "too many queries in one call");
+  TQ_REQUIRE(!pairs || (prod ? bit_width - 1 : bit_width) == 4 || nq <= 65535, "too many queries in one call");
   return launch_scan(a, prod ? bit_width - 1 : bit_width, false, 1, st, pairs);
 }
 
@@ -2940,6 +3003,40 @@ int tq_ip_scan_topk_pair_rows(const void* queries, tq_dtype q_dtype, int64_t nq,
              "pair rows must be 16-byte aligned");
   return ip_scan_topk(queries, q_dtype, nq, d, rows, norms, N, centroids, rotation, bit_width, k,
                       out_scores, out_ids, workspace, workspace_bytes, stream, true);
+}
+
+int tq_ip_scan_topk_prod_pair_rows(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                   const uint8_t* mse_rows, const uint8_t* signs,
+                                   const float* res_norms, const float* norms, int64_t N,
+                                   const float* centroids, const float* rotation, const float* qjl,
+                                   int32_t bit_width, int32_t k, float* out_scores, int64_t* out_ids,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(bit_width == 3 || bit_width == 4,
+             "prod pair rows hold 2- or 3-bit MSE codes (bit_width 3 or 4), got %d", bit_width);
+  const int rc = check_pair_rows(N, d, bit_width - 1);
+  if (rc != TQ_OK) return rc;
+  TQ_REQUIRE(N == 0 || ((reinterpret_cast<uintptr_t>(mse_rows) | reinterpret_cast<uintptr_t>(signs)) & 15u) == 0,
+             "pair rows and sign rows must be 16-byte aligned");
+  const ProdRows p{signs, res_norms, qjl};
+  return ip_scan_topk(queries, q_dtype, nq, d, mse_rows, norms, N, centroids, rotation, bit_width, k,
+                      out_scores, out_ids, workspace, workspace_bytes, stream, true, &p);
+}
+
+int tq_attention_scores_prod_pair_rows(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,
+                                       const uint8_t* mse_rows, const uint8_t* signs,
+                                       const float* res_norms, const float* key_norms, int64_t T,
+                                       const float* centroids, const float* rotation,
+                                       const float* qjl, int32_t bit_width, float* scores,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  TQ_REQUIRE(bit_width == 3 || bit_width == 4,
+             "prod pair rows hold 2- or 3-bit MSE codes (bit_width 3 or 4), got %d", bit_width);
+  const int rc = check_pair_rows(T, d, bit_width - 1);
+  if (rc != TQ_OK) return rc;
+  TQ_REQUIRE(T == 0 || ((reinterpret_cast<uintptr_t>(mse_rows) | reinterpret_cast<uintptr_t>(signs)) & 15u) == 0,
+             "pair rows and sign rows must be 16-byte aligned");
+  const ProdRows p{signs, res_norms, qjl};
+  return attention_scores(query, q_dtype, nq, d, mse_rows, key_norms, T, centroids, rotation,
+                          bit_width, scores, workspace, workspace_bytes, stream, true, &p);
 }
 
 int tq_attention_scores_pair_rows(const void* query, tq_dtype q_dtype, int64_t nq, int32_t d,

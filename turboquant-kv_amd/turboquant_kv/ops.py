@@ -113,6 +113,22 @@ def attention_scores_prod(query, mse_packed, signs, res_norms, key_norms, centro
                                         rotation, qjl, bit_width)
 
 
+def ip_scan_topk_prod_pair_rows(queries, mse_rows, signs, res_norms, norms, centroids, rotation,
+                                qjl, bit_width, k):
+    """ip_scan_topk_prod with the MSE half as pair rows (bit_width 3 or 4, d 64/128):
+    the same scores bit for bit."""
+    _require_device(queries, "queries")
+    return _ops().ip_scan_topk_prod_pair_rows(queries, mse_rows, signs, res_norms, norms, centroids,
+                                              rotation, qjl, bit_width, k)
+
+
+def attention_scores_prod_pair_rows(query, mse_rows, signs, res_norms, key_norms, centroids,
+                                    rotation, qjl, bit_width):
+    _require_device(query, "query")
+    return _ops().attention_scores_prod_pair_rows(query, mse_rows, signs, res_norms, key_norms,
+                                                  centroids, rotation, qjl, bit_width)
+
+
 def decode_attention_packed(q, kpacked, knorms, vpacked, vnorms, seq_lens, kcentroids,
                             vcentroids, krotation, vrotation, kbits, vbits, scale):
     """Fused GQA decode attention over packed K/V -> [B, Hq, d] in q.dtype."""

@@ -100,9 +100,9 @@ class TurboQuantIndex:
             self._code_bits = bit_width - 1
             self._S_matrix = make_qjl_matrix(dim, dim, seed)
             self._S_dev = self._S_matrix.to(self.device)
-        # 2-4 bit MSE rows of 64/128 dims live as pair rows (same row width): one table
-        # read per pair of dims in the scan.
-        self._pairs = mode == "mse" and 2 <= bit_width <= 4 and dim in (64, 128)
+        # 2-4 bit MSE rows of 64/128 dims, and the 2-3 bit MSE halves of prod rows, live as
+        # pair rows (same row width): one table read per pair of dims in the scan.
+        self._pairs = 2 <= self._code_bits <= (4 if mode == "mse" else 3) and dim in (64, 128)
         self._bnd = self._codebook[0].to(self.device)
         self._cen = self._codebook[1].to(self.device)
         self.n_vectors = 0
@@ -121,12 +121,12 @@ class TurboQuantIndex:
         """The database rows in the reference's bit-plane format [n, b*ceil(d/8)]."""
         if self._packed_buf is None or not self._pairs:
             return self._packed_codes
-        return ops.unpack_pair_rows(self._packed_codes, self.bit_width, self.dim)
+        return ops.unpack_pair_rows(self._packed_codes, self._code_bits, self.dim)
 
     def _store_codes(self, packed: torch.Tensor, pos: int) -> None:
         """Write bit-plane rows at rows pos.. of the database buffer."""
         if self._pairs:
-            self._packed_buf[pos: pos + packed.shape[0]] = ops.pack_pair_rows(packed, self.bit_width,
+            self._packed_buf[pos: pos + packed.shape[0]] = ops.pack_pair_rows(packed, self._code_bits,
                                                                                self.dim)
         else:
             self._packed_buf[pos: pos + packed.shape[0]] = packed
@@ -194,7 +194,7 @@ class TurboQuantIndex:
         else:
             mp, sg, rn, nm = _ops().quantize_prod_packed(x, self._rot_dev, self._bnd, self._cen,
                                                          self._S_dev, self.bit_width)
-            self._packed_buf[sl] = mp
+            self._store_codes(mp, self.n_vectors)
             self._sign_buf[sl] = sg
             self._res_buf[sl] = rn.float()
             self._norm_buf[sl] = nm.float()
@@ -226,16 +226,17 @@ class TurboQuantIndex:
         if self.bit_width <= 4:
             # Scored from the packed rows: <q, dequantize_prod(row)> rearranged as
             # n * (<R q, c[codes]> + sqrt(pi/2)/d * gamma * <S q, +-1>).
+            scan = ops.ip_scan_topk_prod_pair_rows if self._pairs else ops.ip_scan_topk_prod
+            scores_of = (ops.attention_scores_prod_pair_rows if self._pairs
+                         else ops.attention_scores_prod)
             if k <= _SCAN_MAX_K:
-                return ops.ip_scan_topk_prod(q, self._packed_codes, self._qjl_signs,
-                                             self._residual_norms, self._norms, self._cen,
-                                             self._rot_dev, self._S_dev, self.bit_width, k)
-            s = ops.attention_scores_prod(q.float().unsqueeze(0), self._packed_codes,
-                                          self._qjl_signs, self._residual_norms, self._norms,
-                                          self._cen, self._rot_dev, self._S_dev,
-                                          self.bit_width)[0]
+                return scan(q, self._packed_codes, self._qjl_signs, self._residual_norms,
+                            self._norms, self._cen, self._rot_dev, self._S_dev, self.bit_width, k)
+            s = scores_of(q.float().unsqueeze(0), self._packed_codes, self._qjl_signs,
+                          self._residual_norms, self._norms, self._cen, self._rot_dev, self._S_dev,
+                          self.bit_width)[0]
             return _topk_lowest_index(s, k)
-        recon = _ops().dequantize_prod_packed(self._packed_codes, self._qjl_signs,
+        recon = _ops().dequantize_prod_packed(self._bitplane_codes(), self._qjl_signs,
                                               self._residual_norms, self._norms, self._cen,
                                               self._rot_dev, self._S_dev, self.bit_width, self.dim)
         scores = q.float() @ recon.t()
