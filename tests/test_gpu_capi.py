@@ -1302,3 +1302,40 @@ def test_prod_pair_rows_equal_bitplane_prod_scan(d, b):
     a1 = ops().attention_scores_prod_pair_rows(qa, rows[:5000], sg[:5000], rn[:5000], nm[:5000],
                                                T(cen), R, S, b)
     assert torch.equal(a0.view(torch.int32), a1.view(torch.int32))
+
+
+@pytest.mark.parametrize("bits,d", [(3, 128), (2, 128), (2, 64)])
+def test_pair_rows_one_query_filter_cases(bits, d):
+    """One query over 2-/3-bit pair rows: ids and scores equal the oracle's bit for bit on
+    ragged N, fp16 unit queries, duplicated best rows (exact ties), special norms (zero,
+    negative, huge, tiny, infinite: NaN rows are never listed) and zero / huge / tiny
+    query scales."""
+    rs = np.random.RandomState(300 + 10 * bits + d)
+    N = 130_001
+    R, cen, p, nm = _db(rs, N, d, bits)
+    nm = nm.copy()
+    # ties: 500 copies of the best row for a fixed query
+    q0 = rs.randn(1, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q0, p, nm, cen, R, bits)))
+    idx = rs.permutation(N)
+    p[idx[:500]] = p[top]
+    nm[idx[:500]] = nm[top]
+    nm[idx[500:1500]] = 0.0
+    nm[idx[1500:2500]] *= -1.0
+    nm[idx[2500:2510]] = 1e30
+    nm[idx[2510:2520]] = 1e-38
+    nm[idx[2520:2526]] = np.inf
+    nm[idx[2526:2530]] = -np.inf
+    rows = k_pair_rows(p, d, bits)
+    qn = rs.randn(1, d).astype(np.float32)
+    qn /= np.linalg.norm(qn)
+    cases = [(q0, capi.TQ_F32), (qn.astype(np.float16), capi.TQ_F16)]
+    cases += [((rs.randn(1, d) * sc).astype(np.float32), capi.TQ_F32) for sc in (0.0, 1e-36, 1e34)]
+    for q, qdt in cases:
+        qf = q.astype(np.float32)
+        want = O.lut_scores_f32(qf, p, nm, cen, R, bits)
+        for k in (1, 10, 32):
+            s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k, q_dt=qdt)
+            so, io = _topk_no_nan(want, k)
+            assert np.array_equal(i, io), (k, qdt)
+            assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), (k, qdt)
