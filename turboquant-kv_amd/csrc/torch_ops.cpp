@@ -1044,6 +1044,54 @@ at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
                                              kcentroids, vcentroids, krotation, vrotation, scale));
 }
 
+// Appends s new tokens of every (batch row, KV head) to a decode-layout cache at token
+// position pos: keys [B, H, s, d] and values quantized as quantize_mse_packed does
+// (rounding in their own dtype), written into kp [B, H, t_cap, d/2] / vp [B, H, t_cap/64,
+// 8 vbits d] and their fp32 norms into kn / vn [B, H, t_cap] -- the HF cache's append
+// (hf_integration.py: quantize + pack + norm store for K and V) in one call.
+void cache_append_dl(const at::Tensor& key, const at::Tensor& value, at::Tensor& kp, at::Tensor& kn,
+                     at::Tensor& vp, at::Tensor& vn, int64_t pos, const at::Tensor& krotation,
+                     const at::Tensor& kboundaries, const at::Tensor& vrotation,
+                     const at::Tensor& vboundaries, int64_t kbits, int64_t vbits) {
+  require_gpu(key, "key");
+  TORCH_CHECK(key.dim() == 4 && value.sizes() == key.sizes(), "key / value must be [B, H, s, d]");
+  c10::DeviceGuard g(key.device());
+  const auto dev = key.device();
+  const int64_t B = key.size(0), H = key.size(1), n = key.size(2), d = key.size(3);
+  TORCH_CHECK(kp.dim() == 4 && vp.dim() == 4 && kp.size(0) == B && kp.size(1) == H &&
+                  vp.size(0) == B && vp.size(1) == H && kp.is_contiguous() && vp.is_contiguous(),
+              "kp / vp must be contiguous [B, H, ...] decode-layout caches");
+  TORCH_CHECK(kn.dim() == 3 && vn.dim() == 3 && kn.scalar_type() == at::kFloat &&
+                  vn.scalar_type() == at::kFloat && kn.size(0) == B && kn.size(1) == H &&
+                  vn.sizes() == kn.sizes(),
+              "kn / vn must be float32 [B, H, t_cap]");
+  TORCH_CHECK(pos >= 0 && pos + n <= kn.size(2), "tokens past the cache's capacity");
+  if (B * H * n == 0) return;
+  for (int values = 0; values < 2; ++values) {
+    const at::Tensor& t = values ? value : key;
+    at::Tensor& cache = values ? vp : kp;
+    at::Tensor& norm_cache = values ? vn : kn;
+    const int64_t bits = values ? vbits : kbits;
+    auto x = floatc(t.reshape({B * H * n, d}), dev);
+    const tq_dtype dt = to_tq(x.scalar_type());
+    auto R = f32c(values ? vrotation : krotation, dev);
+    auto bnd = f32c(values ? vboundaries : kboundaries, dev);
+    TORCH_CHECK(R.dim() == 2 && R.size(0) == d && R.size(1) == d, "rotation must be [d, d]");
+    TORCH_CHECK(bits >= 1 && bits <= 4 && bnd.numel() == (1 << bits) - 1,
+                "boundaries length must be 2^bit_width - 1");
+    auto packed = at::empty({B * H * n, packed_width(bits, d)}, x.options().dtype(at::kByte));
+    auto norms = at::empty({B * H * n}, x.options().dtype(at::kFloat));
+    check_rc(tq_rotate_and_quantize(x.data_ptr(), dt, dt, B * H * n, (int32_t)d, R.data_ptr<float>(),
+                                    bnd.data_ptr<float>(), (int32_t)bits, packed.data_ptr<uint8_t>(),
+                                    norms.data_ptr<float>(), cur_stream(x)));
+    const int64_t t_cap = values ? cache.size(2) * 64 : cache.size(2);
+    TORCH_CHECK(cache.size(3) == (values ? 8 * bits * d : d / 2), "cache width mismatch");
+    check_rc(tq_pack_decode_layout(packed.data_ptr<uint8_t>(), B * H, n, (int32_t)d, (int32_t)bits,
+                                   values, cache.data_ptr<uint8_t>(), t_cap, pos, cur_stream(x)));
+    norm_cache.narrow(2, pos, n).copy_(norms.view({B, H, n}));
+  }
+}
+
 // The exact current token merged into a decode output by log-sum-exp
 // (hf_integration.py:372-390): o [B, Hq, d] and lse [B, Hq] from a *_lse decode op, q
 // [B, Hq, d], k_new / v_new [B, Hkv, d]; returns [B, Hq, d] in q.dtype.
@@ -1149,6 +1197,9 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor krotation, Tensor vrotation, float scale) -> (Tensor, Tensor)");
   m.def("decode_merge_token(Tensor o, Tensor lse, Tensor q, Tensor k_new, Tensor v_new,"
         " float scale) -> Tensor");
+  m.def("cache_append_dl(Tensor key, Tensor value, Tensor(a!) kp, Tensor(b!) kn, Tensor(c!) vp,"
+        " Tensor(d!) vn, int pos, Tensor krotation, Tensor kboundaries, Tensor vrotation,"
+        " Tensor vboundaries, int kbits, int vbits) -> ()");
   m.def("paged_store_value_tiles(Tensor rows, Tensor norms, Tensor slot_mapping,"
         " Tensor(a!) vtile_pool, Tensor(b!) vnorm_pool) -> ()");
   m.def("decode_attention_paged_dl(Tensor q, Tensor kpairs_pool, Tensor knorm_pool,"
@@ -1190,4 +1241,5 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("decode_attention_dl", &decode_attention_dl);
   m.impl("decode_attention_dl_lse", &decode_attention_dl_lse);
   m.impl("decode_merge_token", &decode_merge_token);
+  m.impl("cache_append_dl", &cache_append_dl);
 }

@@ -161,6 +161,12 @@ class TurboQuantLayer(_HFLayer):
     def _append(self, key_states, value_states) -> None:
         B, H, s, d = key_states.shape
         self._grow(self.seq_len + s)
+        if self.dl and not self.kq.prod:  # K and V quantized, packed and stored in one op
+            _ops().cache_append_dl(key_states, value_states, self.kp, self.kn, self.vp, self.vn,
+                                   self.seq_len, self.kq.R, self.kq.bnd, self.vq.R, self.vq.bnd,
+                                   self.kq.bits, self.vq.bits)
+            self.seq_len += s
+            return
         sl = slice(self.seq_len, self.seq_len + s)
         for vals, (q, x, p, n, sg, rs) in enumerate(
                 ((self.kq, key_states, self.kp, self.kn, "ks", "kr"),
