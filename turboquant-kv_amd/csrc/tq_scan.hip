@@ -836,8 +836,11 @@ __device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count
 // norm gamma beside it -- scored as scan_kernel<BITS, ..., PROD> scores them, bit for bit:
 // the same MSE sum (per-dim LUT products in dim order), the QJL term as a sum of
 // build_tables' sign-nibble entries in group order, acc = fma(gamma, sacc, acc).
+// Occupancy: two blocks per CU (6 waves per SIMD, 80 VGPRs); the prod variant's sign rows
+// need more registers, and spilling them (7 VGPRs, 44.7 MB of scratch writes per 10M-row
+// scan) cost more than running one block per CU (190 -> 169 us at 10M x 128).
 template <int D, bool TOPK, int BITS = 4, bool PROD = false>
-__global__ __launch_bounds__(kPsThreads, 6) void pair_scan_kernel(ScanArgs a) {
+__global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(ScanArgs a) {
 #pragma clang fp contract(off)
   static_assert(D == 64 || D == 128, "pair scan dims");
   static_assert(BITS >= 2 && BITS <= 4, "pair rows of 2-4 bit codes");
