@@ -355,21 +355,35 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
   // matrix operands: bR[t] = R[col][k_t] (u R^T), bC[t] = R[k_t][col] (c R), bS[t] = S[col][k_t]
   // (RELOAD: one array, refilled before each contraction; zero outside d x d)
   constexpr bool kHold = !RELOAD;
-  float bR[KS], bC[kProd && kHold ? KS : 1], bS[kProd && kHold ? KS : 1];
-  auto load_op = [&](float (&bm)[KS], const float* __restrict__ M, bool transposed) {
+  // RELOAD: each contraction's operand comes in two halves of k-steps (the second loaded
+  // after the first half's MFMAs), so a wave holds KS / 2 operand registers: with 13-16
+  // waves per workgroup a wave has 128 VGPRs, and a whole operand spilled.  The MFMAs
+  // keep their k order, so the sums are unchanged.
+  constexpr int KH = RELOAD ? KS / 2 : KS;
+  static_assert(!RELOAD || KS % 2 == 0, "two halves of k-steps");
+  float bR[KH], bC[kProd && kHold ? KS : 1], bS[kProd && kHold ? KS : 1];
+  // (RELOAD: half h of the k-steps, t = h KH .. h KH + KH - 1)
+  auto load_op = [&](float (&bm)[KH], const float* __restrict__ M, bool transposed, int h = 0) {
     if constexpr (RELOAD) {
-      // Indices clamped into the d x d matrix (every load stays inside it), the padded
-      // entries then zeroed.  The clamped column and d pass through an empty asm so the
-      // 3 x KS address computations are redone per call, not hoisted out of the tile loop
-      // (held across it they would need hundreds of registers).
+      // Buffer loads of the d x d matrix: an offset past its end reads 0 (the hardware's
+      // range check), one inside it but outside row/column d is zeroed by the select.
+      // Element (r, c) of M sits at byte 4 (r d + c).  Per load one 32-bit offset: the
+      // lane part (its column, its k group g) in a register, the k-step's constant part
+      // as the instruction's immediate (M[col][k]) or added to it (M[k][col]).  The
+      // column and d pass through an empty asm so the offsets are formed per call, not
+      // hoisted out of the tile loop (held across it they would need KS registers each).
+      const __amdgpu_buffer_rsrc_t rs = buf_rsrc(M, (uint32_t)(d * d) * 4u);
       int cc = col < d ? col : d - 1, dd = d;
       asm volatile("" : "+v"(cc), "+v"(dd));
 #pragma unroll
-      for (int t = 0; t < KS; ++t) {
-        const int k = kof(t);
-        const int kc = k < dd ? k : dd - 1;
-        const float v = transposed ? M[kc * dd + cc] : M[cc * dd + kc];
-        bm[t] = (col < d && k < d) ? v : 0.f;
+      for (int i = 0; i < KH; ++i) {
+        const int t = h * KH + i, k = kof(t);
+        const int kc = t < KF ? 64 * (t >> 4) + (t & 15) : 64 * (D / 64) + 4 * (t - KF);  // k - lane part
+        const int kl = t < KF ? 16 * g : g;
+        uint32_t v;
+        if (transposed) v = __builtin_amdgcn_raw_buffer_load_b32(rs, ((kl + kc) * dd + cc) * 4, 0, 0);
+        else v = __builtin_amdgcn_raw_buffer_load_b32(rs, (cc * dd + kl) * 4, kc * 4, 0);
+        bm[i] = (col < d && k < d) ? __uint_as_float(v) : 0.f;
       }
     } else {
 #pragma unroll
@@ -379,7 +393,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       }
     }
   };
-  load_op(bR, a.rot, false);
+  if constexpr (kHold) load_op(bR, a.rot, false);
   if constexpr (kProd && kHold) {
     load_op(bC, a.rot, true);
     load_op(bS, a.qjl, false);
@@ -437,6 +451,25 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bounds the tile reads in flight
     }
   };
+  // RELOAD: the same product with the operand M (transposed or not) loaded half by half.
+  auto gemm_reload = [&](const float* T, const float* __restrict__ M, bool transposed,
+                         v4f_t (&acc)[RB]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = (v4f_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __builtin_amdgcn_sched_barrier(0);  // the second half's loads wait for the first's MFMAs
+      load_op(bR, M, transposed, h);
+#pragma unroll
+      for (int i = 0; i < KH; ++i) {
+        const int t = h * KH + i, k = kof(t);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(T[(16 * rb + c16) * LD + k], bR[i], acc[rb], 0, 0, 0);
+        if ((t & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
   // Bit planes of this thread's 16 codes in cs, stored for row r0 + trow.
   auto pack_cs = [&](int rows, int64_t r0, int bits, uint8_t* __restrict__ out) {
     const uint4 c = *reinterpret_cast<const uint4*>(&cs[trow * D + 16 * part]);
@@ -489,8 +522,8 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
     __syncthreads();
     // ---- y = u R^T, codes = #{bnd < y}
     v4f_t acc[RB];
-    if constexpr (RELOAD && kProd) load_op(bR, a.rot, false);  // replaced by S last tile
-    gemm(kProd ? tb : ta, bR, acc);
+    if constexpr (RELOAD) gemm_reload(kProd ? tb : ta, a.rot, false, acc);
+    else gemm(kProd ? tb : ta, bR, acc);
     if (kProd) __syncthreads();  // every wave is done reading tb before it takes c[codes]
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -511,8 +544,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       // ---- residual = u - c[codes] R (ta, u, is no operand of this product: each lane
       // rewrites its own elements)
       if constexpr (RELOAD) {
-        load_op(bR, a.rot, true);
-        gemm(tb, bR, acc);
+        gemm_reload(tb, a.rot, true, acc);
       } else {
         gemm(tb, bC, acc);
       }
@@ -534,8 +566,7 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       }
       // ---- signs of residual S^T
       if constexpr (RELOAD) {
-        load_op(bR, a.qjl, false);
-        gemm(ta, bR, acc);
+        gemm_reload(ta, a.qjl, false, acc);
       } else {
         gemm(ta, bS, acc);
       }
