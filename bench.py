@@ -292,6 +292,48 @@ def bench_decode(args, extra):
     return out
 
 
+def bench_prefill(args, extra):
+    """Causal prefill of a 4096-token prompt over decode-layout paged pools (block 16, the
+    vLLM default), Llama-3.2-1B attention shape (Hq 32, Hkv 8, d 64), K4/V2, one layer:
+    the tiled prefill kernel against the per-token decode launch it replaces."""
+    import torch
+    from turboquant_kv import _lib
+    from turboquant_kv.config import TurboQuantConfig
+    from turboquant_kv.vllm_plugin import PagedKVPools
+
+    ops = _lib.ops()
+    Hq, Hkv, d, bs, n = 32, 8, 64, 16, 4096
+    nb = n // bs + 8
+    pools = PagedKVPools(TurboQuantConfig(), 1, nb, bs, Hkv, d, "cuda", layout="decode")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    table = torch.randperm(nb, generator=g, device="cuda")[:n // bs].to(torch.int32)
+    pos = torch.arange(n, device="cuda")
+    slots = table.long()[pos // bs] * bs + pos % bs
+    k = torch.randn(n, Hkv, d, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(n, Hkv, d, generator=g, device="cuda").to(torch.bfloat16)
+    pools.write(0, k, v, slots)
+    q = torch.randn(n, Hq, d, generator=g, device="cuda").to(torch.bfloat16)
+    scale = 1.0 / 8.0
+    ms = time_op(lambda: pools.prefill(0, q, table, n, scale), 20, 3, settle_s=0.1)
+    st = pools.layers[0]
+    bt = table[None].expand(n, -1).contiguous()
+    lens = torch.arange(1, n + 1, dtype=torch.int32, device="cuda")
+    ms_tok = time_op(lambda: ops.decode_attention_paged_dl(q, st["kp"], st["kn"], st["vt"], st["vn"], bt,
+                                                           lens, pools.kcen, pools.vcen, pools.R_k,
+                                                           pools.R_v, scale), 5, 1)
+    flop = Hq * n * (n + 1) / 2 * 4 * d  # q.k and w.v over the visible (query, token) pairs
+    extra["prefill_paged_dl_4096_llama1b"] = {
+        "ms_per_layer": ms, "tokens_per_s": n / ms * 1e3, "TFLOPs": flop / ms / 1e9,
+        "kernel": "dl_prefill_kernel<true> (block 16)",
+        "per_token_decode_ms": ms_tok,
+        "note": "one layer, 4096 new tokens at positions 0..4095 (T = n), bf16 queries, fp32 out; "
+                "TFLOP/s counts 4 d flop per visible (query head, token) pair; the kernel runs "
+                "each fp16 MFMA product as hi/lo parts (3 MFMAs per term)"}
+    log(f"prefill 4096 tokens (paged decode layout, block 16): {ms:.3f} ms per layer, "
+        f"{n / ms * 1e3 / 1e6:.2f} M tokens/s, {flop / ms / 1e9:.1f} TFLOP/s; per-token decode "
+        f"launch {ms_tok:.3f} ms")
+
+
 def bench_quantize(args, extra):
     import torch
     from turboquant_kv import _lib
@@ -670,6 +712,8 @@ def main():
                     help="only the end-to-end greedy decode (configs[4])")
     ap.add_argument("--scan-only", action="store_true",
                     help="only the index scans (configs[1]: 4-, 3- and 2-bit), e.g. for a profiler run")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 4096-token paged prefill, e.g. for a profiler run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy 3 times (counter calibration)")
     args = ap.parse_args()
@@ -712,6 +756,11 @@ def main():
         bench_scan(args, extra)
         print(json.dumps(extra))
         return
+    if args.prefill_only:
+        extra = {}
+        bench_prefill(args, extra)
+        print(json.dumps(extra))
+        return
     extra = {}
     t0 = time.perf_counter()
     scan = bench_scan(args, extra)
@@ -719,6 +768,7 @@ def main():
     if not args.quick:
         bench_quantize(args, extra)
         bench_prod_scan(args, extra)
+        bench_prefill(args, extra)
         bench_formats(args, extra)
         bench_e2e(args, extra)
     cpu = None if args.no_cpu else cpu_baseline(scan["db4"])

@@ -443,6 +443,26 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
                                  void* stream);
 
 /*
+ * Causal prefill of one sequence over decode-layout paged pools (the pools of
+ * tq_decode_attention_paged_dl): its n new tokens q [n][hq][64] sit at positions
+ * T - n .. T - 1 and new token i attends to tokens 0 .. T - n + i, read through
+ * block_table [max_blocks] (T <= max_blocks * block_size).  out [n][hq][64] fp32,
+ * 16-byte aligned.  Replaces the reference backend's prefill attention over its
+ * dequantized cache (vllm_plugin/__init__.py:400 via cache.py:282-339), which has no
+ * block tables and no causal mask; one kernel streams each 64-token tile once per 16
+ * query rows instead of once per row.  Pools of any size (64-bit addresses; block ids
+ * clamped into the pool).  No workspace.
+ */
+int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, int64_t T, int32_t hq,
+                                  int32_t hkv, int32_t d, const uint8_t* kpairs_pool,
+                                  const float* knorm_pool, const uint8_t* vtile_pool,
+                                  const float* vnorm_pool, int64_t num_blocks, int32_t block_size,
+                                  const int32_t* block_table, int32_t max_blocks,
+                                  const float* kcentroids, const float* vcentroids,
+                                  const float* krotation, const float* vrotation, float scale,
+                                  float* out, void* stream);
+
+/*
  * Host-side tables of the reference's standalone C++ core, for TQIX v1 index files
  * (turboquant_core.cpp:559-618), which record only (dim, bit_width, seed): the reader
  * rebuilds the rotation and codebook the writer used.  No device work; outputs are host

@@ -468,33 +468,12 @@ def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
         before = [before[i] + n_new[i] for i in range(4)]
 
 
-def test_decode_layout_prefill_in_chunks_equals_one_launch():
-    # A prefill whose (token, kv head) streams exceed one launch's limit runs in chunks;
-    # the chunked result equals the single launch's bit for bit.
-    from turboquant_kv.vllm_plugin import PagedKVPools
-    from turboquant_kv.config import TurboQuantConfig
-    Hkv, Hq, d, bs, nb = 2, 8, 64, 16, 16
-    pools = PagedKVPools(TurboQuantConfig(), 1, nb, bs, Hkv, d, DEV, layout="decode")
-    g = torch.Generator(device=DEV).manual_seed(5)
-    n = 100
-    table = torch.randperm(nb, generator=g, device=DEV)[:8].to(torch.int32)
-    slots = (table.long()[torch.arange(n, device=DEV) // bs] * bs + torch.arange(n, device=DEV) % bs)
-    k = torch.randn(n, Hkv, d, generator=g, device=DEV)
-    v = torch.randn(n, Hkv, d, generator=g, device=DEV)
-    pools.write(0, k, v, slots)
-    q = torch.randn(n, Hq, d, generator=g, device=DEV)
-    whole = pools.prefill(0, q, table, n, 0.125)
-    pools.dl_max_streams = 64          # 32 rows per launch: four launches
-    chunked = pools.prefill(0, q, table, n, 0.125)
-    # at T = 100 both split plans have one split per stream: identical sums
-    assert torch.equal(whole, chunked)
-
-
-def test_decode_layout_prefill_chunks_with_several_splits_vs_f64():
-    # A longer prefill in launches of 32 rows: each launch's 64 streams are split over
-    # several workgroups (and merged by the combine kernel) while the single launch keeps
-    # one split per stream, so the sums differ in order; both must match the float64
-    # paged oracle.
+def test_decode_layout_prefill_kernel_vs_per_token_decode():
+    # PagedKVPools.prefill over decode-layout pools runs the tiled prefill kernel.  A whole
+    # 1200-token prompt (T = n, block size 16, shuffled blocks) against the per-token
+    # decode kernel over the same pools (fp32 queries: both paths fp32-accurate) and the
+    # float64 paged oracle.
+    from turboquant_kv import ops
     from turboquant_kv.vllm_plugin import PagedKVPools
     from turboquant_kv.config import TurboQuantConfig
     Hkv, Hq, d, bs, nb, n = 2, 8, 64, 16, 80, 1200
@@ -506,17 +485,89 @@ def test_decode_layout_prefill_chunks_with_several_splits_vs_f64():
     v = torch.randn(n, Hkv, d, generator=g, device=DEV)
     pools.write(0, k, v, slots)
     q = torch.randn(n, Hq, d, generator=g, device=DEV)
-    whole = pools.prefill(0, q, table, n, 0.125).cpu().numpy()
-    pools.dl_max_streams = 64
-    chunked = pools.prefill(0, q, table, n, 0.125).cpu().numpy()
+    got = pools.prefill(0, q, table, n, 0.125).cpu().numpy()
+    st = pools.layers[0]
+    per_token = ops.decode_attention_paged_dl(
+        q, st["kp"], st["kn"], st["vt"], st["vn"], table[None].expand(n, -1).contiguous(),
+        torch.arange(1, n + 1, dtype=torch.int32, device=DEV), pools.kcen, pools.vcen, pools.R_k,
+        pools.R_v, 0.125).cpu().numpy()
     P = _bitplane_pools(pools, table.cpu().numpy()[None], [n])
     want = O.paged_attention_f64(q.cpu().numpy(), P["k"], P["kn"], P["v"], P["vn"],
                                  table.cpu().numpy(), n, pools.kcen.cpu().numpy(),
                                  pools.vcen.cpu().numpy(), pools.R_k.cpu().numpy(),
                                  pools.R_v.cpu().numpy(), 4, 2, 0.125)
-    for got in (whole, chunked):
-        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
-    assert not np.array_equal(whole, chunked)  # the plans really differ
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+    assert np.max(np.abs(got - per_token)) <= 1e-5 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("bs,G,n,qdt", [(16, 4, 300, torch.bfloat16), (32, 7, 77, torch.float16),
+                                        (64, 1, 200, torch.float32), (128, 8, 129, torch.bfloat16),
+                                        (64, 4, 1, torch.float32)])
+def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
+    # tq_prefill_attention_paged_dl: sequence 1's last n tokens (positions T-n .. T-1, so
+    # T-n tokens of history) against the per-token decode-layout kernel (B = n rows, row i's
+    # context ending at its own position, fp32 queries) and the float64 decode oracle per
+    # row.  Query rows per KV head n*G are ragged against the kernel's 64-row tiles; the
+    # sequence's stale slots past T hold NaN norms and its block-table entries past T are
+    # -1 (clamped into the pool, masked): neither may reach the output.
+    from turboquant_kv import ops
+    rs = np.random.RandomState(bs * 31 + G + n)
+    Hkv = 2
+    Hq = G * Hkv
+    lens = [37, 1100 + bs, 5]
+    width = (max(lens) + bs - 1) // bs + 2
+    nb = sum((L + bs - 1) // bs for L in lens) + 4
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    Tq = lens[1]
+    row = tab[1].copy()
+    nblk = (Tq + bs - 1) // bs
+    for t in range(Tq, nblk * bs):
+        knp[int(row[nblk - 1]), :, t % bs] = float("nan")
+        vnp[int(row[nblk - 1]), :, t % bs] = float("nan")
+    row[nblk:] = -1
+    Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
+    _, ck = O.lloyd_max_codebook(4, 64)
+    _, cv = O.lloyd_max_codebook(2, 64)
+    q = torch.from_numpy(rs.randn(n, Hq, 64).astype(np.float32)).to(DEV).to(qdt)
+    scale = 0.125
+    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[qdt]
+    out = torch.empty(n, Hq, 64, dtype=torch.float32, device=DEV)
+    print(f"prefill capi bs={bs} G={G} n={n} T={Tq} {qdt}", flush=True)
+    capi.check(L().tq_prefill_attention_paged_dl(
+        capi.p(q), dt, capi.i32(n), capi.i64(Tq), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp),
+        capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(row)), capi.i32(width),
+        capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)), ctypes.c_float(scale), capi.p(out),
+        capi.stream()))
+    sync()
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    qf = q.float()
+    bt = T(row)[None].expand(n, -1).contiguous()
+    pos = torch.arange(Tq - n + 1, Tq + 1, dtype=torch.int32, device=DEV)
+    per_token = ops.decode_attention_paged_dl(qf, kp, knp, vt, vnp, bt, pos, T(ck), T(cv), T(Rk), T(Rv),
+                                              scale).cpu().numpy()
+    kr, kn_, vr, vn_ = seqs[1]
+    bc = lambda x: np.broadcast_to(x[None], (n,) + x.shape)
+    want = O.decode_attention_f64(qf.cpu().numpy(), bc(kr), bc(kn_), bc(vr), bc(vn_), pos.cpu().numpy(),
+                                  ck, cv, Rk, Rv, 4, 2, scale)
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+    assert np.max(np.abs(got - per_token)) <= 1e-5 * np.max(np.abs(want))
+
+
+def test_prefill_kernel_capi_refusals():
+    # bad shapes are refused before any launch
+    z = torch.zeros(64, dtype=torch.float32, device=DEV)
+    zb = torch.zeros(64, dtype=torch.uint8, device=DEV)
+    tab = torch.zeros(4, dtype=torch.int32, device=DEV)
+    args = lambda n, T_, bs, d=64, hq=8: (
+        capi.p(z), capi.TQ_F32, capi.i32(n), capi.i64(T_), capi.i32(hq), capi.i32(2), capi.i32(d),
+        capi.p(zb), capi.p(z), capi.p(zb), capi.p(z), capi.i64(1), capi.i32(bs), capi.p(tab), capi.i32(4),
+        capi.p(z), capi.p(z), capi.p(z), capi.p(z), ctypes.c_float(1.0), capi.p(z), capi.stream())
+    assert L().tq_prefill_attention_paged_dl(*args(1, 1, 16, d=128)) != 0      # head_dim 64 only
+    assert L().tq_prefill_attention_paged_dl(*args(1, 1, 24)) != 0             # block size
+    assert L().tq_prefill_attention_paged_dl(*args(5, 4, 16)) != 0            # n > T
+    assert L().tq_prefill_attention_paged_dl(*args(1, 65, 16)) != 0            # T past the table
+    assert L().tq_prefill_attention_paged_dl(*args(1, 1, 16, hq=7)) != 0       # GQA groups
 
 
 # ------------------------------------------------------------------ pools past 2 GiB

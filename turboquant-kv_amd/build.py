@@ -27,8 +27,8 @@ OBJDIR = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(LIBDIR, "libturboquant_hip.so")
 TORCH_LIB = os.path.join(LIBDIR, "libturboquant_torch.so")
 
-HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip", "tq_paged.hip", "tq_core_tables.hip",
-               "tq_entropy.hip"]
+HIP_SOURCES = ["tq_quantize.hip", "tq_scan.hip", "tq_decode.hip", "tq_paged.hip", "tq_prefill.hip",
+               "tq_core_tables.hip", "tq_entropy.hip"]
 # host C++ of the torch.ops library: the HIP-device ops and the CPU-tensor kernels of the
 # reference schemas
 TORCH_SOURCES = ["torch_ops.cpp", "cpu_ops.cpp"]

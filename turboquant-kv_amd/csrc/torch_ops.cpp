@@ -1034,6 +1034,50 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
   return {out, lse};
 }
 
+at::Tensor prefill_attention_paged_dl(
+    const at::Tensor& q, const at::Tensor& kpairs_pool, const at::Tensor& knorm_pool,
+    const at::Tensor& vtile_pool, const at::Tensor& vnorm_pool, const at::Tensor& block_table,
+    int64_t T, const at::Tensor& kcentroids, const at::Tensor& vcentroids,
+    const at::Tensor& krotation, const at::Tensor& vrotation, double scale) {
+  require_gpu(q, "q");
+  TORCH_CHECK(q.dim() == 3, "q must be [n, Hq, d]");
+  TORCH_CHECK(kpairs_pool.dim() == 4 && vtile_pool.dim() == 4,
+              "kpairs_pool must be [num_blocks, hkv, block_size, d/2] and vtile_pool "
+              "[num_blocks, hkv, block_size/64, 16d]");
+  c10::DeviceGuard g(q.device());
+  const auto dev = q.device();
+  auto qq = floatc(q, dev);
+  const int64_t n = qq.size(0), Hq = qq.size(1), d = qq.size(2);
+  const int64_t nb = kpairs_pool.size(0), Hkv = kpairs_pool.size(1), bs = kpairs_pool.size(2);
+  for (const at::Tensor* t : {&kpairs_pool, &vtile_pool, &knorm_pool, &vnorm_pool})
+    TORCH_CHECK(t->device() == dev && t->is_contiguous(), "pools must be contiguous on the query's device");
+  TORCH_CHECK(kpairs_pool.scalar_type() == at::kByte && vtile_pool.scalar_type() == at::kByte,
+              "pools must be uint8");
+  const int64_t tile_tokens = bs >= 64 ? 64 : 16;
+  TORCH_CHECK(kpairs_pool.size(3) == d / 2 && vtile_pool.size(0) == nb && vtile_pool.size(1) == Hkv &&
+                  vtile_pool.size(2) * tile_tokens == bs && vtile_pool.size(3) == tile_tokens * d / 4,
+              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, 16d] "
+              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 4d] (block_size 16, 32)");
+  TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
+                  knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
+              "norm pools must be float32 [num_blocks, hkv, block_size]");
+  auto bt = block_table.to(dev, at::kInt).contiguous().view(-1);
+  auto kc = f32c(kcentroids, dev);
+  auto vc = f32c(vcentroids, dev);
+  auto Rk = f32c(krotation, dev);
+  auto Rv = f32c(vrotation, dev);
+  TORCH_CHECK(kc.numel() == 16 && vc.numel() == 4, "decode layout: 4-bit keys, 2-bit values");
+  TORCH_CHECK(Rk.numel() == d * d && Rv.numel() == d * d, "rotations must be [d, d]");
+  auto out = at::empty({n, Hq, d}, qq.options().dtype(at::kFloat));
+  check_rc(tq_prefill_attention_paged_dl(
+      qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)n, T, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
+      kpairs_pool.data_ptr<uint8_t>(), knorm_pool.data_ptr<float>(), vtile_pool.data_ptr<uint8_t>(),
+      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, bt.data_ptr<int32_t>(), (int32_t)bt.numel(),
+      kc.data_ptr<float>(), vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(),
+      (float)scale, out.data_ptr<float>(), cur_stream(qq)));
+  return out;
+}
+
 at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
                                const at::Tensor& knorms, const at::Tensor& vblocks,
                                const at::Tensor& vnorms, const at::Tensor& seq_lens,
@@ -1206,6 +1250,10 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor vtile_pool, Tensor vnorm_pool, Tensor block_tables, Tensor seq_lens,"
         " Tensor kcentroids, Tensor vcentroids, Tensor krotation, Tensor vrotation,"
         " float scale) -> (Tensor, Tensor)");
+  m.def("prefill_attention_paged_dl(Tensor q, Tensor kpairs_pool, Tensor knorm_pool,"
+        " Tensor vtile_pool, Tensor vnorm_pool, Tensor block_table, int T,"
+        " Tensor kcentroids, Tensor vcentroids, Tensor krotation, Tensor vrotation,"
+        " float scale) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
@@ -1231,6 +1279,7 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("decode_attention_paged", &decode_attention_paged);
   m.impl("paged_store_value_tiles", &paged_store_value_tiles);
   m.impl("decode_attention_paged_dl", &decode_attention_paged_dl);
+  m.impl("prefill_attention_paged_dl", &prefill_attention_paged_dl);
   m.impl("attention_scores_prod", &attention_scores_prod);
   m.impl("ip_scan_topk_prod_pair_rows", &ip_scan_topk_prod_pair_rows);
   m.impl("attention_scores_prod_pair_rows", &attention_scores_prod_pair_rows);

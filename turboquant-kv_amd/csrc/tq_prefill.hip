@@ -1,0 +1,377 @@
+// tq_prefill.hip -- causal prefill attention over decode-layout paged pools on gfx950.
+//
+// Semantics: one sequence's n new tokens at positions T - n .. T - 1 attend causally to
+// its first T tokens: new token i sees tokens 0 .. T - n + i (the mask of vLLM's prefill;
+// the reference's backend attends over its dequantized cache, vllm_plugin/__init__.py:400
+// with cache.py:282-339 for the scores and values).  score = scale * n_k <R_k q, c_k[code]>,
+// softmax over the visible tokens, out = (sum_t w_t n_v,t c_v[code_t]) R_v.
+//
+// One workgroup of four waves per (64 query rows, KV head h); query row r of h is query
+// head h G + r % G of new token r / G.  Each wave owns 16 rows and streams the 64-token
+// tiles its last row can see, once for all 16 rows (the per-token decode launch reads the
+// history once per row), with an online softmax in the log2 domain.  Per tile and wave:
+//   S^T = K Qrot^T  v_mfma_f32_16x16x32_f16, one 16-token group b per MFMA chain.  A: lane
+//                   (c, g) = (lane % 16, lane / 16) holds token 16 b + c, dims 8 g .. 8 g + 7
+//                   and 32 + 8 g .. : one 4-byte read of its pair bytes each, four pair-
+//                   table lookups (c[hi], c[lo]) as fp16.  B: the rotated query (fp16 hi +
+//                   lo parts); c.q = ch qh + ch ql + cl qh, accumulated in fp32.  Lane
+//                   (c, g) gets tokens 16 b + 4 g + r of query row c.
+//   softmax         per query row over the four lanes c, c + 16, c + 32, c + 48.
+//   O^T += V^T P^T  A: value centroids of dim 16 nb + c for the 8 tokens lane (c, g) holds
+//                   weights of -- the decode layout's 16-byte value word of lane 16 g + c
+//                   carries exactly those tokens' 2-bit codes (byte nb of word m: tokens
+//                   16 m + 4 g .. + 3, dim 16 nb + c), so no data moves between lanes.  B:
+//                   weights times value norms, the layout S^T left them in (hi + lo).
+// Rotations in fp32 on v_mfma_f32_16x16x4f32: Qrot = q R_k^T (rows of R_k permuted so the
+// result lands in the B layout above), out = O R_v.  Each row's query and the centroid
+// tables are scaled by powers of two into [0.5, 1) before the fp16 split (exact), which
+// the fp32 results undo.  Accuracy: the dropped lo x lo terms are 2^-22 relative, so the
+// scores and weighted sums are fp32-accurate; outputs fp32.
+//
+// Pools: rows at 64-bit addresses from block ids clamped into the pool (any pool size; a
+// corrupt table reads the pool's last block, never memory outside it).  Tokens past a
+// row's limit are masked by selects, so stale rows and norms (even NaN) contribute 0.
+
+#include "tq_common.h"
+
+#include <climits>
+
+namespace tq {
+namespace {
+
+constexpr int kPfThreads = 256;
+constexpr int kPfRows = 64;  // query rows per workgroup, 16 per wave
+constexpr int kPfLd = 68;    // LDS row stride of the rotations in floats (16-byte rows)
+
+typedef float pf_v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 pf_v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t pf_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pf_u32x2 __attribute__((ext_vector_type(2)));
+
+struct PfArgs {
+  const void* q;  // [n][hq][64]
+  int q_dt;
+  int n, hq, hkv, G;
+  int64_t past;  // T - n
+  const uint8_t* kpairs;  // [num_blocks][hkv][bs][32]
+  const float* knorms;    // [num_blocks][hkv][bs]
+  const uint8_t* vtiles;  // [num_blocks][hkv][bs/64][1024] or [num_blocks][hkv][bs/16][256]
+  const float* vnorms;
+  const int32_t* block_table;  // the sequence's row
+  int max_blocks;
+  int bs_log2;
+  uint32_t num_blocks;
+  const float* kcen;  // 16
+  const float* vcen;  // 4
+  const float* krot;  // [64][64]
+  const float* vrot;
+  float qscale;  // softmax scale * log2(e)
+  float* out;    // [n][hq][64]
+};
+
+__device__ __forceinline__ pf_v8h pf_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  pf_u32x4 t = {a, b, c, d};
+  return __builtin_bit_cast(pf_v8h, t);
+}
+
+__device__ __forceinline__ uint32_t pf_pack(_Float16 lo, _Float16 hi) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, (h2_t){lo, hi});
+}
+
+// 2^-e with amax = m 2^e, m in [0.5, 1) (1 for 0, inf or NaN)
+__device__ __forceinline__ float pf_pow2_scale(float amax) {
+  int e = 0;
+  if (amax > 0.f && amax < INFINITY) frexpf(amax, &e);
+  return ldexpf(1.f, -e);
+}
+
+// SUB: value sub-blocks of 16 tokens (block_size 16 or 32), else 64-token value tiles.
+template <bool SUB>
+__global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float rk_s[64 * kPfLd];
+  __shared__ __attribute__((aligned(16))) float rv_s[64 * kPfLd];
+  __shared__ uint32_t tkh[256], tkl[256];    // key pair entries (c[hi nibble], c[lo nibble])
+  __shared__ pf_u32x2 tvh[256], tvl[256];    // value bytes: four 2-bit codes -> four fp16
+  __shared__ float sc_s[2];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const int hkv = a.hkv;
+  const int nG = a.n * a.G;
+  const int nrt = (nG + kPfRows - 1) / kPfRows;
+  const int h = (int)(blockIdx.x % (unsigned)hkv);
+  const int rt = nrt - 1 - (int)(blockIdx.x / (unsigned)hkv);  // longest rows first
+
+  // ---- rotations into LDS; centroid tables scaled by powers of two, fp16 hi + lo
+  for (int i = tid; i < 64 * 64; i += kPfThreads) {
+    rk_s[(i >> 6) * kPfLd + (i & 63)] = a.krot[i];
+    rv_s[(i >> 6) * kPfLd + (i & 63)] = a.vrot[i];
+  }
+  if (wave == 0) {
+    float km = lane < 16 ? fabsf(a.kcen[lane]) : 0.f;
+    float vm = lane < 4 ? fabsf(a.vcen[lane]) : 0.f;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      km = fmaxf(km, __shfl_xor(km, o, 64));
+      vm = fmaxf(vm, __shfl_xor(vm, o, 64));
+    }
+    if (lane == 0) {
+      sc_s[0] = pf_pow2_scale(km);
+      sc_s[1] = pf_pow2_scale(vm);
+    }
+  }
+  __syncthreads();
+  const float ksc = sc_s[0], vsc = sc_s[1];
+  {
+    const int e = tid;  // one entry per thread
+    const float c0 = a.kcen[e >> 4] * ksc, c1 = a.kcen[e & 15] * ksc;
+    const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
+    tkh[e] = pf_pack(h0, h1);
+    tkl[e] = pf_pack((_Float16)(c0 - (float)h0), (_Float16)(c1 - (float)h1));
+    _Float16 vh[4], vl[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float v = a.vcen[(e >> (2 * t)) & 3] * vsc;
+      vh[t] = (_Float16)v;
+      vl[t] = (_Float16)(v - (float)vh[t]);
+    }
+    tvh[e] = (pf_u32x2){pf_pack(vh[0], vh[1]), pf_pack(vh[2], vh[3])};
+    tvl[e] = (pf_u32x2){pf_pack(vl[0], vl[1]), pf_pack(vl[2], vl[3])};
+  }
+  __syncthreads();  // the last barrier: from here on every wave runs on its own
+
+  const int row0 = rt * kPfRows + wave * 16;
+  if (row0 >= nG) return;
+  const int row = row0 + c, rowc = row < nG ? row : nG - 1;
+  const int ti = rowc / a.G;
+  const int qh = h * a.G + (rowc - ti * a.G);
+  const int64_t qoff = ((int64_t)ti * a.hq + qh) * 64;
+  const int64_t lim = row < nG ? a.past + ti + 1 : 0;  // tokens this row sees
+  const int64_t limw = a.past + (min(row0 + 15, nG - 1) / a.G) + 1;
+  const int ntiles = (int)((limw + 63) >> 6);
+
+  // ---- Qrot = (q * qscale) R_k^T.  MFMA mb, k-step s4: A[m][k] = R_k[pi(16 mb + m)][4 s4 + k],
+  // B[k][c] = q_c[4 s4 + k]; lane (c, g) register r gets Qrot_c[pi(16 mb + 4 g + r)] with
+  // pi(16 mb + 4 g + r) = 32 (mb / 2) + 8 g + 4 (mb % 2) + r: dims 8 g + i and 32 + 8 g + i.
+  pf_v4f d[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) d[mb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s4 = 0; s4 < 16; ++s4) {
+    const float b = load_as_f32(a.q, qoff + 4 * s4 + g, a.q_dt) * a.qscale;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int dim = 32 * (mb >> 1) + 8 * (c >> 2) + 4 * (mb & 1) + (c & 3);
+      d[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(rk_s[dim * kPfLd + 4 * s4 + g], b, d[mb], 0, 0, 0);
+    }
+  }
+  float qm = 0.f;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qm = fmaxf(qm, fabsf(d[mb][r]));
+  qm = fmaxf(qm, __shfl_xor(qm, 16, 64));
+  qm = fmaxf(qm, __shfl_xor(qm, 32, 64));
+  const float qsc = pf_pow2_scale(qm);
+  const float kinv = 1.f / (qsc * ksc);  // a power of two
+  pf_v8h qhi[2], qlo[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = d[2 * s + (i >> 2)][i & 3] * qsc;
+      const _Float16 hv = (_Float16)v;
+      qhi[s][i] = hv;
+      qlo[s][i] = (_Float16)(v - (float)hv);
+    }
+
+  const int bsl = a.bs_log2;
+  const int64_t bsm = ((int64_t)1 << bsl) - 1;
+  float m = -INFINITY, l = 0.f;
+  pf_v4f o[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) o[nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int64_t t0 = (int64_t)kt * 64;
+    // pool row of token t0 + 16 b (a 16-token group never straddles a block)
+    int64_t base[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int64_t tb = t0 + 16 * b;
+      const int bi = (int)min<int64_t>(tb >> bsl, (int64_t)a.max_blocks - 1);
+      const uint32_t blk = min((uint32_t)a.block_table[bi], a.num_blocks - 1u);
+      base[b] = (((int64_t)blk * hkv + h) << bsl) + (tb & bsm);
+    }
+    uint32_t kw[4][2];
+    pf_v4f nk[4], nv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint8_t* kr = a.kpairs + (base[b] + c) * 32 + 4 * g;
+      kw[b][0] = *reinterpret_cast<const uint32_t*>(kr);
+      kw[b][1] = *reinterpret_cast<const uint32_t*>(kr + 16);
+      nk[b] = *reinterpret_cast<const pf_v4f*>(a.knorms + base[b] + 4 * g);
+      nv[b] = *reinterpret_cast<const pf_v4f*>(a.vnorms + base[b] + 4 * g);
+    }
+    uint32_t vw[4];
+    if constexpr (SUB) {
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm)
+        vw[mm] = *reinterpret_cast<const uint32_t*>(a.vtiles + base[mm] * 16 + 4 * lane);
+    } else {
+      const pf_u32x4 v = *reinterpret_cast<const pf_u32x4*>(a.vtiles + base[0] * 16 + 16 * lane);
+      vw[0] = v.x; vw[1] = v.y; vw[2] = v.z; vw[3] = v.w;
+    }
+
+    // ---- scores (log2 domain), masked past each row's limit
+    pf_v4f sv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint32_t w = kw[b][s];
+        const uint32_t i0 = w & 255u, i1 = (w >> 8) & 255u, i2 = (w >> 16) & 255u, i3 = w >> 24;
+        const pf_v8h ah = pf_h8(tkh[i0], tkh[i1], tkh[i2], tkh[i3]);
+        const pf_v8h al = pf_h8(tkl[i0], tkl[i1], tkl[i2], tkl[i3]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qhi[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[s], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t tok = t0 + 16 * b + 4 * g + r;
+        sv[b][r] = tok < lim ? acc[r] * kinv * nk[b][r] : -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[b][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float ms = mn == -INFINITY ? 0.f : mn;
+    const float alpha = exp2f(m - ms);
+    m = mn;
+    l *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) o[nb] *= alpha;
+    pf_v4f pv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = exp2f(sv[b][r] - ms);
+        l += p;
+        pv[b][r] = t0 + 16 * b + 4 * g + r < lim ? p * nv[b][r] : 0.f;
+      }
+
+    // ---- O^T += V^T P^T over the tile's two 32-token halves
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      pf_v8h bh, bl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = pv[2 * s + (i >> 2)][i & 3];
+        const _Float16 hv = (_Float16)v;
+        bh[i] = hv;
+        bl[i] = (_Float16)(v - (float)hv);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
+        const pf_u32x2 h0 = tvh[b0], h1 = tvh[b1], l0 = tvl[b0], l1 = tvl[b1];
+        const pf_v8h ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
+        const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o[nb], 0, 0, 0);
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o[nb], 0, 0, 0);
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o[nb], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- out = (O / l) R_v.  o[nb][r] of lane (c, g) = O_c[16 nb + 4 g + r]: the B operand
+  // of k-step (nb, r); A[m][k] = R_v[16 nb + 4 k + r][16 ob + m]; lane (c, g) register r
+  // gets out_c[16 ob + 4 g + r].
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const float inv = l > 0.f ? 1.f / (l * vsc) : 0.f;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) o[nb] *= inv;
+  float* dst = a.out + qoff;
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) {
+    pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rv_s[(16 * nb + 4 * g + r) * kPfLd + 16 * ob + c],
+                                                   o[nb][r], acc, 0, 0, 0);
+    if (row < nG) *reinterpret_cast<pf_v4f*>(dst + 16 * ob + 4 * g) = acc;
+  }
+}
+
+}  // namespace
+}  // namespace tq
+
+using namespace tq;
+
+extern "C" {
+
+int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, int64_t T, int32_t hq,
+                                  int32_t hkv, int32_t d, const uint8_t* kpairs_pool,
+                                  const float* knorm_pool, const uint8_t* vtile_pool,
+                                  const float* vnorm_pool, int64_t num_blocks, int32_t block_size,
+                                  const int32_t* block_table, int32_t max_blocks,
+                                  const float* kcentroids, const float* vcentroids,
+                                  const float* krotation, const float* vrotation, float scale,
+                                  float* out, void* stream) {
+  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  TQ_REQUIRE(d == 64, "decode layout covers head_dim 64, got %d", d);
+  TQ_REQUIRE(hkv >= 1 && hq >= hkv && hq % hkv == 0,
+             "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
+  int bsl = 0;
+  while (bsl < 30 && (1 << bsl) < block_size) ++bsl;
+  TQ_REQUIRE(block_size >= 16 && (1 << bsl) == block_size,
+             "decode-layout pools need a power-of-two block_size >= 16, got %d", block_size);
+  TQ_REQUIRE(n >= 0 && T >= n && max_blocks >= 0 && num_blocks >= 0, "bad sizes");
+  TQ_REQUIRE(T <= (int64_t)max_blocks * block_size,
+             "context of %lld tokens exceeds the block table (%d blocks of %d)", (long long)T,
+             max_blocks, block_size);
+  const int64_t rows = (int64_t)n * (hq / hkv);
+  TQ_REQUIRE(rows <= INT_MAX - kPfRows, "too many query rows in one call");
+  const int64_t grid = (rows + kPfRows - 1) / kPfRows * hkv;
+  TQ_REQUIRE(grid <= INT_MAX, "too many query rows in one call");
+  TQ_REQUIRE(num_blocks <= (int64_t)UINT_MAX, "too many blocks");
+  if (n == 0) return TQ_OK;
+  TQ_REQUIRE(num_blocks >= 1, "empty pools");
+  TQ_REQUIRE(q && out && block_table && kpairs_pool && knorm_pool && vtile_pool && vnorm_pool &&
+                 kcentroids && vcentroids && krotation && vrotation,
+             "null pointer argument");
+  TQ_REQUIRE(((reinterpret_cast<uintptr_t>(kpairs_pool) | reinterpret_cast<uintptr_t>(vtile_pool) |
+               reinterpret_cast<uintptr_t>(knorm_pool) | reinterpret_cast<uintptr_t>(vnorm_pool) |
+               reinterpret_cast<uintptr_t>(out)) & 15u) == 0,
+             "pools and output must be 16-byte aligned");
+  PfArgs a{};
+  a.q = q; a.q_dt = (int)q_dtype; a.n = n; a.hq = hq; a.hkv = hkv; a.G = hq / hkv;
+  a.past = T - n;
+  a.kpairs = kpairs_pool; a.knorms = knorm_pool; a.vtiles = vtile_pool; a.vnorms = vnorm_pool;
+  a.block_table = block_table; a.max_blocks = max_blocks; a.bs_log2 = bsl;
+  a.num_blocks = (uint32_t)num_blocks;
+  a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
+  a.qscale = scale * 1.4426950408889634f;
+  a.out = out;
+  if (bsl >= 6)
+    hipLaunchKernelGGL(dl_prefill_kernel<false>, dim3((unsigned)grid), dim3(kPfThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(dl_prefill_kernel<true>, dim3((unsigned)grid), dim3(kPfThreads), 0, as_stream(stream), a);
+  TQ_LAUNCH_CHECK("dl_prefill_kernel");
+  return TQ_OK;
+}
+
+}  // extern "C"

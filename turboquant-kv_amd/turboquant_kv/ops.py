@@ -225,3 +225,15 @@ def decode_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool
                                                 block_tables, seq_lens, kcentroids, vcentroids,
                                                 krotation, vrotation, float(scale))
     return (out, lse) if return_lse else out
+
+
+def prefill_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool, block_table, T,
+                               kcentroids, vcentroids, krotation, vrotation, scale):
+    """Causal prefill of one sequence over decode-layout paged pools: its n new tokens
+    q [n, Hq, 64] sit at positions T-n .. T-1 and new token i attends to tokens
+    0 .. T-n+i, read through block_table [max_blocks].  -> [n, Hq, 64] fp32.  One kernel
+    streams each 64-token tile once per 16 query rows."""
+    _require_device(q, "q")
+    return _ops().prefill_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool,
+                                             block_table, int(T), kcentroids, vcentroids,
+                                             krotation, vrotation, float(scale))

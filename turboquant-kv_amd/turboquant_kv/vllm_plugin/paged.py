@@ -82,9 +82,6 @@ def gather_value_tiles(vt_pool: torch.Tensor, block_table: torch.Tensor, T: int)
 class PagedKVPools:
     """A model's paged packed KV storage: per layer, K/V block pools and norms."""
 
-    # (row, kv head) streams per decode-layout launch: the kernel's grid.y limit
-    dl_max_streams: int = 65535
-
     def __init__(self, config: TurboQuantConfig, num_layers: int, num_blocks: int, block_size: int,
                  num_kv_heads: int, head_dim: int, device="cuda", layout: str = "bitplane"):
         if config.mode not in ("mse", "prod"):
@@ -245,15 +242,10 @@ class PagedKVPools:
         G = Hq // H
         st = self.layers[layer]
         if "kp" in st:
-            # one decode row per new token, its context ending at its own position; rows in
-            # chunks of at most 65535 (row, kv head) streams (the kernel's grid limit)
-            qf = q.to(self.device).float()
-            lens = torch.arange(T - n + 1, T + 1, dtype=torch.int32, device=self.device)
-            step = max(1, self.dl_max_streams // H)
-            bt = block_table.to(self.device, torch.int32).view(1, -1).expand(min(n, step), -1).contiguous()
-            outs = [self._decode_dl(st, qf[i:i + step], bt[:min(step, n - i)], lens[i:i + step], scale)
-                    for i in range(0, n, step)]
-            return outs[0] if len(outs) == 1 else torch.cat(outs)
+            # one kernel: each 64-token tile of the history read once per 16 query rows
+            return ops.prefill_attention_paged_dl(q.to(self.device), st["kp"], st["kn"], st["vt"],
+                                                  st["vn"], block_table.to(self.device), T, self.kcen,
+                                                  self.vcen, self.R_k, self.R_v, float(scale))
         qf = q.to(self.device).float()
         pos = torch.arange(T - n, T, device=self.device)
         mask = torch.arange(T, device=self.device)[None, :] > pos[:, None]       # [n, T]
