@@ -496,8 +496,9 @@ def test_decode_layout_prefill_kernel_vs_per_token_decode():
                                  table.cpu().numpy(), n, pools.kcen.cpu().numpy(),
                                  pools.vcen.cpu().numpy(), pools.R_k.cpu().numpy(),
                                  pools.R_v.cpu().numpy(), 4, 2, 0.125)
+    # both kernels fp32-accurate, their sums in different orders
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
-    assert np.max(np.abs(got - per_token)) <= 1e-5 * np.max(np.abs(want))
+    assert np.max(np.abs(got - per_token)) <= 4e-5 * np.max(np.abs(want))
 
 
 @pytest.mark.parametrize("bs,G,n,qdt", [(16, 4, 300, torch.bfloat16), (32, 7, 77, torch.float16),
@@ -550,8 +551,13 @@ def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
     bc = lambda x: np.broadcast_to(x[None], (n,) + x.shape)
     want = O.decode_attention_f64(qf.cpu().numpy(), bc(kr), bc(kn_), bc(vr), bc(vn_), pos.cpu().numpy(),
                                   ck, cv, Rk, Rv, 4, 2, scale)
-    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
-    assert np.max(np.abs(got - per_token)) <= 1e-5 * np.max(np.abs(want))
+    # fp32 / fp16 queries: hi + lo operand parts, fp32-accurate; bf16 queries: one fp16
+    # product per term (outputs consumed in bf16, whose rounding is 2^-9)
+    # (outputs average many values, so their maximum sits far below the summed terms':
+    # both bars are relative to the float64 output's maximum)
+    tol_f64, tol_tok = (1e-4, 1e-4) if qdt != torch.bfloat16 else (5e-3, 5e-3)
+    assert np.max(np.abs(got - want)) <= tol_f64 * np.max(np.abs(want))
+    assert np.max(np.abs(got - per_token)) <= tol_tok * np.max(np.abs(want))
 
 
 def test_prefill_kernel_capi_refusals():

@@ -25,8 +25,10 @@
 // Rotations in fp32 on v_mfma_f32_16x16x4f32: Qrot = q R_k^T (rows of R_k permuted so the
 // result lands in the B layout above), out = O R_v.  Each row's query and the centroid
 // tables are scaled by powers of two into [0.5, 1) before the fp16 split (exact), which
-// the fp32 results undo.  Accuracy: the dropped lo x lo terms are 2^-22 relative, so the
-// scores and weighted sums are fp32-accurate; outputs fp32.
+// the fp32 results undo.  Accuracy: fp32 and fp16 queries take hi + lo parts (the dropped
+// lo x lo terms are 2^-22 relative: fp32-accurate scores and sums); bf16 queries one fp16
+// product per term (2^-11 relative per operand, below the bf16 rounding of their outputs).
+// Outputs fp32.
 //
 // Pools: rows at 64-bit addresses from block ids clamped into the pool (any pool size; a
 // corrupt table reads the pool's last block, never memory outside it).  Tokens past a
@@ -35,6 +37,7 @@
 #include "tq_common.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace tq {
 namespace {
@@ -87,7 +90,10 @@ __device__ __forceinline__ float pf_pow2_scale(float amax) {
 }
 
 // SUB: value sub-blocks of 16 tokens (block_size 16 or 32), else 64-token value tiles.
-template <bool SUB>
+// PREC: fp16 hi + lo parts of every operand (three products per term, fp32-accurate);
+// otherwise one fp16 product per term (about 2^-11 relative per operand), for bf16 queries
+// whose outputs are consumed in bf16 (2^-9).
+template <bool SUB, bool PREC>
 __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float rk_s[64 * kPfLd];
@@ -194,8 +200,13 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) o[nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
 
-  for (int kt = 0; kt < ntiles; ++kt) {
+  // Tiles every row of the wave sees whole need no mask (all but the last one or two).
+  const int64_t limlo = a.past + row0 / a.G + 1;
+  auto tile = [&](auto masked_tag, int kt) {
+    constexpr bool MASK = decltype(masked_tag)::value;
     const int64_t t0 = (int64_t)kt * 64;
+    // tokens of this tile the lane's row sees (rows past the end: none)
+    const int rel = MASK ? (int)max<int64_t>(0, min<int64_t>(lim - t0, 64)) : 64;
     // pool row of token t0 + 16 b (a 16-token group never straddles a block)
     int64_t base[4];
 #pragma unroll
@@ -235,15 +246,17 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
         const uint32_t w = kw[b][s];
         const uint32_t i0 = w & 255u, i1 = (w >> 8) & 255u, i2 = (w >> 16) & 255u, i3 = w >> 24;
         const pf_v8h ah = pf_h8(tkh[i0], tkh[i1], tkh[i2], tkh[i3]);
-        const pf_v8h al = pf_h8(tkl[i0], tkl[i1], tkl[i2], tkl[i3]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qhi[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[s], acc, 0, 0, 0);
+        if constexpr (PREC) {
+          const pf_v8h al = pf_h8(tkl[i0], tkl[i1], tkl[i2], tkl[i3]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[s], acc, 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t tok = t0 + 16 * b + 4 * g + r;
-        sv[b][r] = tok < lim ? acc[r] * kinv * nk[b][r] : -INFINITY;
+        const float x = acc[r] * kinv * nk[b][r];
+        sv[b][r] = (!MASK || 16 * b + 4 * g + r < rel) ? x : -INFINITY;
       }
     }
     float mx = -INFINITY;
@@ -255,7 +268,9 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mn = fmaxf(m, mx);
     const float ms = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp2f(m - ms);
+    // 2^x on the hardware's exp2 (results below 2^-126 flush to 0: weights that small
+    // against the running maximum's 1 do not change an fp32 sum)
+    const float alpha = __builtin_amdgcn_exp2f(m - ms);
     m = mn;
     l *= alpha;
 #pragma unroll
@@ -265,9 +280,10 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
     for (int b = 0; b < 4; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(sv[b][r] - ms);
+        const float p = __builtin_amdgcn_exp2f(sv[b][r] - ms);
         l += p;
-        pv[b][r] = t0 + 16 * b + 4 * g + r < lim ? p * nv[b][r] : 0.f;
+        // masked tokens' norms may be stale (even NaN): selected away, not multiplied
+        pv[b][r] = (!MASK || 16 * b + 4 * g + r < rel) ? p * nv[b][r] : 0.f;
       }
 
     // ---- O^T += V^T P^T over the tile's two 32-token halves
@@ -279,19 +295,26 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
         const float v = pv[2 * s + (i >> 2)][i & 3];
         const _Float16 hv = (_Float16)v;
         bh[i] = hv;
-        bl[i] = (_Float16)(v - (float)hv);
+        if constexpr (PREC) bl[i] = (_Float16)(v - (float)hv);
       }
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
-        const pf_u32x2 h0 = tvh[b0], h1 = tvh[b1], l0 = tvl[b0], l1 = tvl[b1];
+        const pf_u32x2 h0 = tvh[b0], h1 = tvh[b1];
         const pf_v8h ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
-        const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
         o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o[nb], 0, 0, 0);
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o[nb], 0, 0, 0);
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o[nb], 0, 0, 0);
+        if constexpr (PREC) {
+          const pf_u32x2 l0 = tvl[b0], l1 = tvl[b1];
+          const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
+          o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o[nb], 0, 0, 0);
+          o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o[nb], 0, 0, 0);
+        }
       }
     }
+  };
+  for (int kt = 0; kt < ntiles; ++kt) {
+    if ((int64_t)kt * 64 + 64 <= limlo) tile(std::false_type{}, kt);
+    else tile(std::true_type{}, kt);
   }
 
   // ---- out = (O / l) R_v.  o[nb][r] of lane (c, g) = O_c[16 nb + 4 g + r]: the B operand
@@ -366,10 +389,17 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
   a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
   a.qscale = scale * 1.4426950408889634f;
   a.out = out;
-  if (bsl >= 6)
-    hipLaunchKernelGGL(dl_prefill_kernel<false>, dim3((unsigned)grid), dim3(kPfThreads), 0, as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(dl_prefill_kernel<true>, dim3((unsigned)grid), dim3(kPfThreads), 0, as_stream(stream), a);
+  // bf16 queries: one product per term (their outputs are consumed in bf16)
+  const bool prec = q_dtype != TQ_BF16;
+  const dim3 gr((unsigned)grid), bl(kPfThreads);
+  hipStream_t st = as_stream(stream);
+  if (bsl >= 6) {
+    if (prec) hipLaunchKernelGGL((dl_prefill_kernel<false, true>), gr, bl, 0, st, a);
+    else hipLaunchKernelGGL((dl_prefill_kernel<false, false>), gr, bl, 0, st, a);
+  } else {
+    if (prec) hipLaunchKernelGGL((dl_prefill_kernel<true, true>), gr, bl, 0, st, a);
+    else hipLaunchKernelGGL((dl_prefill_kernel<true, false>), gr, bl, 0, st, a);
+  }
   TQ_LAUNCH_CHECK("dl_prefill_kernel");
   return TQ_OK;
 }
