@@ -98,8 +98,13 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float rk_s[64 * kPfLd];
   __shared__ __attribute__((aligned(16))) float rv_s[64 * kPfLd];
-  __shared__ uint32_t tkh[256], tkl[256];    // key pair entries (c[hi nibble], c[lo nibble])
-  __shared__ pf_u32x2 tvh[256], tvl[256];    // value bytes: four 2-bit codes -> four fp16
+  // Tables, KC / VC copies of each entry (lane L reads copy L % KC, L % VC, so a wave's
+  // random lookups spread over the banks instead of piling onto a 1 KB table's):
+  //   tk[p][i KC + j]  key byte i -> (c[i >> 4], c[i & 15]) as two fp16, part p (hi, lo)
+  //   tv[p][i VC + j]  value byte i -> its four 2-bit codes' centroids as four fp16
+  constexpr int KC = PREC ? 4 : 8, VC = PREC ? 2 : 4, NP = PREC ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint32_t tk[NP][256 * KC];
+  __shared__ __attribute__((aligned(16))) pf_u32x2 tv[NP][256 * VC];
   __shared__ float sc_s[2];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -134,8 +139,8 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
     const int e = tid;  // one entry per thread
     const float c0 = a.kcen[e >> 4] * ksc, c1 = a.kcen[e & 15] * ksc;
     const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
-    tkh[e] = pf_pack(h0, h1);
-    tkl[e] = pf_pack((_Float16)(c0 - (float)h0), (_Float16)(c1 - (float)h1));
+    const uint32_t kh = pf_pack(h0, h1);
+    const uint32_t kl = pf_pack((_Float16)(c0 - (float)h0), (_Float16)(c1 - (float)h1));
     _Float16 vh[4], vl[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -143,9 +148,20 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
       vh[t] = (_Float16)v;
       vl[t] = (_Float16)(v - (float)vh[t]);
     }
-    tvh[e] = (pf_u32x2){pf_pack(vh[0], vh[1]), pf_pack(vh[2], vh[3])};
-    tvl[e] = (pf_u32x2){pf_pack(vl[0], vl[1]), pf_pack(vl[2], vl[3])};
+    const uint32_t v0 = pf_pack(vh[0], vh[1]), v1 = pf_pack(vh[2], vh[3]);
+    const uint32_t w0 = pf_pack(vl[0], vl[1]), w1 = pf_pack(vl[2], vl[3]);
+#pragma unroll
+    for (int j = 0; j < KC; j += 4) {
+      *reinterpret_cast<pf_u32x4*>(&tk[0][e * KC + j]) = (pf_u32x4){kh, kh, kh, kh};
+      if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tk[NP - 1][e * KC + j]) = (pf_u32x4){kl, kl, kl, kl};
+    }
+#pragma unroll
+    for (int j = 0; j < VC; j += 2) {
+      *reinterpret_cast<pf_u32x4*>(&tv[0][e * VC + j]) = (pf_u32x4){v0, v1, v0, v1};
+      if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tv[NP - 1][e * VC + j]) = (pf_u32x4){w0, w1, w0, w1};
+    }
   }
+  const int kcp = lane & (KC - 1), vcp = lane & (VC - 1);
   __syncthreads();  // the last barrier: from here on every wave runs on its own
 
   const int row0 = rt * kPfRows + wave * 16;
@@ -245,10 +261,12 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
       for (int s = 0; s < 2; ++s) {
         const uint32_t w = kw[b][s];
         const uint32_t i0 = w & 255u, i1 = (w >> 8) & 255u, i2 = (w >> 16) & 255u, i3 = w >> 24;
-        const pf_v8h ah = pf_h8(tkh[i0], tkh[i1], tkh[i2], tkh[i3]);
+        const pf_v8h ah = pf_h8(tk[0][i0 * KC + kcp], tk[0][i1 * KC + kcp], tk[0][i2 * KC + kcp],
+                                tk[0][i3 * KC + kcp]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qhi[s], acc, 0, 0, 0);
         if constexpr (PREC) {
-          const pf_v8h al = pf_h8(tkl[i0], tkl[i1], tkl[i2], tkl[i3]);
+          const pf_v8h al = pf_h8(tk[NP - 1][i0 * KC + kcp], tk[NP - 1][i1 * KC + kcp],
+                                  tk[NP - 1][i2 * KC + kcp], tk[NP - 1][i3 * KC + kcp]);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[s], acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[s], acc, 0, 0, 0);
         }
@@ -300,11 +318,11 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
-        const pf_u32x2 h0 = tvh[b0], h1 = tvh[b1];
+        const pf_u32x2 h0 = tv[0][b0 * VC + vcp], h1 = tv[0][b1 * VC + vcp];
         const pf_v8h ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
         o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o[nb], 0, 0, 0);
         if constexpr (PREC) {
-          const pf_u32x2 l0 = tvl[b0], l1 = tvl[b1];
+          const pf_u32x2 l0 = tv[NP - 1][b0 * VC + vcp], l1 = tv[NP - 1][b1 * VC + vcp];
           const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
           o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o[nb], 0, 0, 0);
           o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o[nb], 0, 0, 0);
