@@ -326,3 +326,24 @@ def test_index_search_k_above_32_ties_and_order(bits, d, mode):
                     if s[r, a] == s[r, a + 1]:
                         assert i[r, a] < i[r, a + 1]
             assert np.array_equal(s, full[:, :k])
+
+
+def test_index_search_many_queries_in_chunks(monkeypatch):
+    # A batch larger than one launch's query chunk runs as consecutive launches: the same
+    # results as the oracle, for the fused top-k and for k above 32 (whose [Q, N] score
+    # matrix is chunked by bytes).
+    from turboquant_kv import TurboQuantIndex
+    from turboquant_kv import search as S
+    monkeypatch.setattr(S, "_SEARCH_CHUNK", 96)
+    monkeypatch.setattr(S, "_SCORE_BYTES", 4 * 3000 * 40)
+    rs = np.random.RandomState(5)
+    db = rs.randn(3000, 128).astype(np.float32)
+    idx = TurboQuantIndex.from_vectors(torch.from_numpy(db).to(DEV), bit_width=4)
+    q = rs.randn(250, 128).astype(np.float32)
+    for k in (10, 40):
+        s, i = idx.search(torch.from_numpy(q).to(DEV), k=k)
+        want_s, want_i = O.search_topk(q, idx._bitplane_codes().cpu().numpy(), idx._norms.cpu().numpy(),
+                                       idx._cen.cpu().numpy(), idx._rot_dev.cpu().numpy(), 4, k)
+        assert s.shape == (250, k) and i.shape == (250, k)
+        assert np.array_equal(i.cpu().numpy(), want_i), k
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), want_s.view(np.uint32)), k

@@ -42,6 +42,12 @@ HEADER_SIZE = struct.calcsize(HEADER_FORMAT)
 MODE_MSE = 0
 MODE_PROD = 1
 _SCAN_MAX_K = 32  # the fused top-k kernel's per-call limit
+# Queries per scan launch: the scans' candidate lists grow with the query count (and a
+# launch takes at most 65,535 queries); larger batches run as consecutive launches.
+_SEARCH_CHUNK = 4096
+# k above _SCAN_MAX_K scores every row into a [Q, N] fp32 matrix: at most this many
+# score bytes per launch
+_SCORE_BYTES = 1 << 30
 
 
 def _topk_lowest_index(s: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -201,12 +207,21 @@ class TurboQuantIndex:
         self.n_vectors += n
 
     def search(self, queries: torch.Tensor, k: int = 10) -> Tuple[torch.Tensor, torch.Tensor]:
-        """Top-k inner products: (scores (Q, k'), indices (Q, k')) with k' = min(k, n_vectors)."""
+        """Top-k inner products: (scores (Q, k'), indices (Q, k')) with k' = min(k, n_vectors).
+        Any number of queries: large batches run in consecutive launches."""
         if queries.dim() == 1:
             queries = queries.unsqueeze(0)
         assert self.n_vectors > 0, "Index is empty"
         q = queries.to(self.device)
         k = min(k, self.n_vectors)
+        step = (_SEARCH_CHUNK if k <= _SCAN_MAX_K and (self.mode == "mse" or self.bit_width <= 4)
+                else max(1, min(_SEARCH_CHUNK, _SCORE_BYTES // (4 * self.n_vectors))))
+        if q.shape[0] <= step:
+            return self._search(q, k)
+        parts = [self._search(q[i:i + step], k) for i in range(0, q.shape[0], step)]
+        return torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
+
+    def _search(self, q: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
         if self.mode == "mse":
             if k <= _SCAN_MAX_K:
                 if self._pairs:
