@@ -44,7 +44,6 @@ namespace {
 
 constexpr int kPfThreads = 256;
 constexpr int kPfRows = 64;  // query rows per workgroup, 16 per wave
-constexpr int kPfLd = 68;    // LDS row stride of the rotations in floats (16-byte rows)
 
 typedef float pf_v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 pf_v8h __attribute__((ext_vector_type(8)));
@@ -94,10 +93,8 @@ __device__ __forceinline__ float pf_pow2_scale(float amax) {
 // otherwise one fp16 product per term (about 2^-11 relative per operand), for bf16 queries
 // whose outputs are consumed in bf16 (2^-9).
 template <bool SUB, bool PREC>
-__global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
+__global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float rk_s[64 * kPfLd];
-  __shared__ __attribute__((aligned(16))) float rv_s[64 * kPfLd];
   // Tables, KC / VC copies of each entry (lane L reads copy L % KC, L % VC, so a wave's
   // random lookups spread over the banks instead of piling onto a 1 KB table's):
   //   tk[p][i KC + j]  key byte i -> (c[i >> 4], c[i & 15]) as two fp16, part p (hi, lo)
@@ -115,11 +112,7 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
   const int h = (int)(blockIdx.x % (unsigned)hkv);
   const int rt = nrt - 1 - (int)(blockIdx.x / (unsigned)hkv);  // longest rows first
 
-  // ---- rotations into LDS; centroid tables scaled by powers of two, fp16 hi + lo
-  for (int i = tid; i < 64 * 64; i += kPfThreads) {
-    rk_s[(i >> 6) * kPfLd + (i & 63)] = a.krot[i];
-    rv_s[(i >> 6) * kPfLd + (i & 63)] = a.vrot[i];
-  }
+  // ---- centroid tables scaled by powers of two, fp16 hi (+ lo)
   if (wave == 0) {
     float km = lane < 16 ? fabsf(a.kcen[lane]) : 0.f;
     float vm = lane < 4 ? fabsf(a.vcen[lane]) : 0.f;
@@ -174,19 +167,52 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
   const int64_t limw = a.past + (min(row0 + 15, nG - 1) / a.G) + 1;
   const int ntiles = (int)((limw + 63) >> 6);
 
-  // ---- Qrot = (q * qscale) R_k^T.  MFMA mb, k-step s4: A[m][k] = R_k[pi(16 mb + m)][4 s4 + k],
-  // B[k][c] = q_c[4 s4 + k]; lane (c, g) register r gets Qrot_c[pi(16 mb + 4 g + r)] with
+  // ---- Qrot = (q * qscale) R_k^T.  MFMA mb, k-step s: lane (c, g) supplies A[c][g] =
+  // R_k[pi(16 mb + c)][16 g + s] and B[g][c] = q_c[16 g + s] (the contraction runs over the
+  // input dims in the order 16 g + s, so each lane reads 16 consecutive floats of a row);
+  // register r of lane (c, g) gets Qrot_c[pi(16 mb + 4 g + r)] with
   // pi(16 mb + 4 g + r) = 32 (mb / 2) + 8 g + 4 (mb % 2) + r: dims 8 g + i and 32 + 8 g + i.
   pf_v4f d[4];
+  {
+    float qv[16];
+    if (a.q_dt == TQ_F32) {
+      const pf_v4f* src = reinterpret_cast<const pf_v4f*>(static_cast<const float*>(a.q) + qoff + 16 * g);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) d[mb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const pf_v4f v = src[j4];
+        qv[4 * j4] = v.x; qv[4 * j4 + 1] = v.y; qv[4 * j4 + 2] = v.z; qv[4 * j4 + 3] = v.w;
+      }
+    } else {
+      const pf_u32x4* src = reinterpret_cast<const pf_u32x4*>(static_cast<const uint16_t*>(a.q) + qoff + 16 * g);
+      const bool bf = a.q_dt == TQ_BF16;
 #pragma unroll
-  for (int s4 = 0; s4 < 16; ++s4) {
-    const float b = load_as_f32(a.q, qoff + 4 * s4 + g, a.q_dt) * a.qscale;
+      for (int j8 = 0; j8 < 2; ++j8) {
+        const pf_u32x4 v = src[j8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t hb = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          qv[8 * j8 + e] = bf ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+        }
+      }
+    }
+    float rk[4][16];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       const int dim = 32 * (mb >> 1) + 8 * (c >> 2) + 4 * (mb & 1) + (c & 3);
-      d[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(rk_s[dim * kPfLd + 4 * s4 + g], b, d[mb], 0, 0, 0);
+      const pf_v4f* src = reinterpret_cast<const pf_v4f*>(a.krot + dim * 64 + 16 * g);
+#pragma unroll
+      for (int j4 = 0; j4 < 4; ++j4) {
+        const pf_v4f v = src[j4];
+        rk[mb][4 * j4] = v.x; rk[mb][4 * j4 + 1] = v.y; rk[mb][4 * j4 + 2] = v.z; rk[mb][4 * j4 + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) d[mb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s16 = 0; s16 < 16; ++s16) {
+      const float b = qv[s16] * a.qscale;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) d[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(rk[mb][s16], b, d[mb], 0, 0, 0);
     }
   }
   float qm = 0.f;
@@ -344,6 +370,14 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) o[nb] *= inv;
   float* dst = a.out + qoff;
+  // this lane's R_v entries, all requested before the first product
+  float rv[4][16];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rv[ob][4 * nb + r] = a.vrot[(16 * nb + 4 * g + r) * 64 + 16 * ob + c];
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
     pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
@@ -351,8 +385,7 @@ __global__ __launch_bounds__(kPfThreads, 3) void dl_prefill_kernel(PfArgs a) {
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rv_s[(16 * nb + 4 * g + r) * kPfLd + 16 * ob + c],
-                                                   o[nb][r], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[ob][4 * nb + r], o[nb][r], acc, 0, 0, 0);
     if (row < nG) *reinterpret_cast<pf_v4f*>(dst + 16 * ob + 4 * g) = acc;
   }
 }
