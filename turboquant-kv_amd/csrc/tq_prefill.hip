@@ -43,7 +43,7 @@ namespace tq {
 namespace {
 
 constexpr int kPfThreads = 256;
-constexpr int kPfRows = 64;  // query rows per workgroup, 16 per wave
+constexpr int kPfRows = 64;  // query rows per workgroup and row group, 16 per wave
 
 typedef float pf_v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 pf_v8h __attribute__((ext_vector_type(8)));
@@ -93,13 +93,14 @@ __device__ __forceinline__ float pf_pow2_scale(float amax) {
 // otherwise one fp16 product per term (about 2^-11 relative per operand), for bf16 queries
 // whose outputs are consumed in bf16 (2^-9).
 template <bool SUB, bool PREC>
-__global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(PfArgs a) {
+__global__ __launch_bounds__(kPfThreads, PREC ? 3 : 2) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
   // Tables, KC / VC copies of each entry (lane L reads copy L % KC, L % VC, so a wave's
   // random lookups spread over the banks instead of piling onto a 1 KB table's):
   //   tk[p][i KC + j]  key byte i -> (c[i >> 4], c[i & 15]) as two fp16, part p (hi, lo)
   //   tv[p][i VC + j]  value byte i -> its four 2-bit codes' centroids as four fp16
   constexpr int KC = PREC ? 4 : 8, VC = PREC ? 2 : 4, NP = PREC ? 2 : 1;
+  constexpr int NGR = PREC ? 1 : 2;  // 16-row groups per wave (sharing each tile's operands)
   __shared__ __attribute__((aligned(16))) uint32_t tk[NP][256 * KC];
   __shared__ __attribute__((aligned(16))) pf_u32x2 tv[NP][256 * VC];
   __shared__ float sc_s[2];
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
   const int c = lane & 15, g = lane >> 4;
   const int hkv = a.hkv;
   const int nG = a.n * a.G;
-  const int nrt = (nG + kPfRows - 1) / kPfRows;
+  const int nrt = (nG + kPfRows * NGR - 1) / (kPfRows * NGR);
   const int h = (int)(blockIdx.x % (unsigned)hkv);
   const int rt = nrt - 1 - (int)(blockIdx.x / (unsigned)hkv);  // longest rows first
 
@@ -157,14 +158,21 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
   const int kcp = lane & (KC - 1), vcp = lane & (VC - 1);
   __syncthreads();  // the last barrier: from here on every wave runs on its own
 
-  const int row0 = rt * kPfRows + wave * 16;
+  // rows of this wave: group j holds rows row0 + 16 j + c
+  const int row0 = rt * (kPfRows * NGR) + wave * (16 * NGR);
   if (row0 >= nG) return;
-  const int row = row0 + c, rowc = row < nG ? row : nG - 1;
-  const int ti = rowc / a.G;
-  const int qh = h * a.G + (rowc - ti * a.G);
-  const int64_t qoff = ((int64_t)ti * a.hq + qh) * 64;
-  const int64_t lim = row < nG ? a.past + ti + 1 : 0;  // tokens this row sees
-  const int64_t limw = a.past + (min(row0 + 15, nG - 1) / a.G) + 1;
+  int row[NGR];
+  int64_t qoff[NGR], lim[NGR];
+#pragma unroll
+  for (int j = 0; j < NGR; ++j) {
+    row[j] = row0 + 16 * j + c;
+    const int rowc = row[j] < nG ? row[j] : nG - 1;
+    const int ti = rowc / a.G;
+    const int qh = h * a.G + (rowc - ti * a.G);
+    qoff[j] = ((int64_t)ti * a.hq + qh) * 64;
+    lim[j] = row[j] < nG ? a.past + ti + 1 : 0;  // tokens this row sees
+  }
+  const int64_t limw = a.past + (min(row0 + 16 * NGR - 1, nG - 1) / a.G) + 1;
   const int ntiles = (int)((limw + 63) >> 6);
 
   // ---- Qrot = (q * qscale) R_k^T.  MFMA mb, k-step s: lane (c, g) supplies A[c][g] =
@@ -172,29 +180,9 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
   // input dims in the order 16 g + s, so each lane reads 16 consecutive floats of a row);
   // register r of lane (c, g) gets Qrot_c[pi(16 mb + 4 g + r)] with
   // pi(16 mb + 4 g + r) = 32 (mb / 2) + 8 g + 4 (mb % 2) + r: dims 8 g + i and 32 + 8 g + i.
-  pf_v4f d[4];
+  pf_v8h qhi[NGR][2], qlo[NGR][2];
+  float kinv[NGR];
   {
-    float qv[16];
-    if (a.q_dt == TQ_F32) {
-      const pf_v4f* src = reinterpret_cast<const pf_v4f*>(static_cast<const float*>(a.q) + qoff + 16 * g);
-#pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const pf_v4f v = src[j4];
-        qv[4 * j4] = v.x; qv[4 * j4 + 1] = v.y; qv[4 * j4 + 2] = v.z; qv[4 * j4 + 3] = v.w;
-      }
-    } else {
-      const pf_u32x4* src = reinterpret_cast<const pf_u32x4*>(static_cast<const uint16_t*>(a.q) + qoff + 16 * g);
-      const bool bf = a.q_dt == TQ_BF16;
-#pragma unroll
-      for (int j8 = 0; j8 < 2; ++j8) {
-        const pf_u32x4 v = src[j8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t hb = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-          qv[8 * j8 + e] = bf ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
-        }
-      }
-    }
     float rk[4][16];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -207,48 +195,79 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
       }
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) d[mb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NGR; ++j) {
+      float qv[16];
+      if (a.q_dt == TQ_F32) {
+        const pf_v4f* src = reinterpret_cast<const pf_v4f*>(static_cast<const float*>(a.q) + qoff[j] + 16 * g);
 #pragma unroll
-    for (int s16 = 0; s16 < 16; ++s16) {
-      const float b = qv[s16] * a.qscale;
+        for (int j4 = 0; j4 < 4; ++j4) {
+          const pf_v4f v = src[j4];
+          qv[4 * j4] = v.x; qv[4 * j4 + 1] = v.y; qv[4 * j4 + 2] = v.z; qv[4 * j4 + 3] = v.w;
+        }
+      } else {
+        const pf_u32x4* src = reinterpret_cast<const pf_u32x4*>(static_cast<const uint16_t*>(a.q) + qoff[j] + 16 * g);
+        const bool bf = a.q_dt == TQ_BF16;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) d[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(rk[mb][s16], b, d[mb], 0, 0, 0);
+        for (int j8 = 0; j8 < 2; ++j8) {
+          const pf_u32x4 v = src[j8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t hb = (v[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+            qv[8 * j8 + e] = bf ? __uint_as_float(hb << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+          }
+        }
+      }
+      pf_v4f d[4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) d[mb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s16 = 0; s16 < 16; ++s16) {
+        const float b = qv[s16] * a.qscale;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) d[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(rk[mb][s16], b, d[mb], 0, 0, 0);
+      }
+      float qm = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qm = fmaxf(qm, fabsf(d[mb][r]));
+      qm = fmaxf(qm, __shfl_xor(qm, 16, 64));
+      qm = fmaxf(qm, __shfl_xor(qm, 32, 64));
+      const float qsc = pf_pow2_scale(qm);
+      kinv[j] = 1.f / (qsc * ksc);  // a power of two
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = d[2 * s + (i >> 2)][i & 3] * qsc;
+          const _Float16 hv = (_Float16)v;
+          qhi[j][s][i] = hv;
+          qlo[j][s][i] = (_Float16)(v - (float)hv);
+        }
     }
   }
-  float qm = 0.f;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qm = fmaxf(qm, fabsf(d[mb][r]));
-  qm = fmaxf(qm, __shfl_xor(qm, 16, 64));
-  qm = fmaxf(qm, __shfl_xor(qm, 32, 64));
-  const float qsc = pf_pow2_scale(qm);
-  const float kinv = 1.f / (qsc * ksc);  // a power of two
-  pf_v8h qhi[2], qlo[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float v = d[2 * s + (i >> 2)][i & 3] * qsc;
-      const _Float16 hv = (_Float16)v;
-      qhi[s][i] = hv;
-      qlo[s][i] = (_Float16)(v - (float)hv);
-    }
 
   const int bsl = a.bs_log2;
   const int64_t bsm = ((int64_t)1 << bsl) - 1;
-  float m = -INFINITY, l = 0.f;
-  pf_v4f o[4];
+  float m[NGR], l[NGR];
+  pf_v4f o[NGR][4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) o[nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NGR; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) o[j][nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+  }
 
   // Tiles every row of the wave sees whole need no mask (all but the last one or two).
   const int64_t limlo = a.past + row0 / a.G + 1;
   auto tile = [&](auto masked_tag, int kt) {
     constexpr bool MASK = decltype(masked_tag)::value;
     const int64_t t0 = (int64_t)kt * 64;
-    // tokens of this tile the lane's row sees (rows past the end: none)
-    const int rel = MASK ? (int)max<int64_t>(0, min<int64_t>(lim - t0, 64)) : 64;
+    // tokens of this tile each of the lane's rows sees (rows past the end: none)
+    int rel[NGR];
+#pragma unroll
+    for (int j = 0; j < NGR; ++j) rel[j] = MASK ? (int)max<int64_t>(0, min<int64_t>(lim[j] - t0, 64)) : 64;
     // pool row of token t0 + 16 b (a 16-token group never straddles a block)
     int64_t base[4];
 #pragma unroll
@@ -278,80 +297,93 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
       vw[0] = v.x; vw[1] = v.y; vw[2] = v.z; vw[3] = v.w;
     }
 
-    // ---- scores (log2 domain), masked past each row's limit
-    pf_v4f sv[4];
+    // ---- scores (log2 domain), masked past each row's limit; one key operand per (b, s)
+    // serves every row group
+    pf_v4f sv[NGR][4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+      pf_v4f acc[NGR];
+#pragma unroll
+      for (int j = 0; j < NGR; ++j) acc[j] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const uint32_t w = kw[b][s];
         const uint32_t i0 = w & 255u, i1 = (w >> 8) & 255u, i2 = (w >> 16) & 255u, i3 = w >> 24;
         const pf_v8h ah = pf_h8(tk[0][i0 * KC + kcp], tk[0][i1 * KC + kcp], tk[0][i2 * KC + kcp],
                                 tk[0][i3 * KC + kcp]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qhi[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NGR; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qhi[j][s], acc[j], 0, 0, 0);
         if constexpr (PREC) {
           const pf_v8h al = pf_h8(tk[NP - 1][i0 * KC + kcp], tk[NP - 1][i1 * KC + kcp],
                                   tk[NP - 1][i2 * KC + kcp], tk[NP - 1][i3 * KC + kcp]);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[s], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[s], acc, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < NGR; ++j) {
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[j][s], acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qhi[j][s], acc[j], 0, 0, 0);
+          }
         }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = acc[r] * kinv * nk[b][r];
-        sv[b][r] = (!MASK || 16 * b + 4 * g + r < rel) ? x : -INFINITY;
-      }
+      for (int j = 0; j < NGR; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = acc[j][r] * kinv[j] * nk[b][r];
+          sv[j][b][r] = (!MASK || 16 * b + 4 * g + r < rel[j]) ? x : -INFINITY;
+        }
     }
-    float mx = -INFINITY;
+    pf_v8h bh[NGR][2], bl[NGR][2];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int j = 0; j < NGR; ++j) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[b][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx);
-    const float ms = mn == -INFINITY ? 0.f : mn;
-    // 2^x on the hardware's exp2 (results below 2^-126 flush to 0: weights that small
-    // against the running maximum's 1 do not change an fp32 sum)
-    const float alpha = __builtin_amdgcn_exp2f(m - ms);
-    m = mn;
-    l *= alpha;
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) o[nb] *= alpha;
-    pf_v4f pv[4];
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][b][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m[j], mx);
+      const float ms = mn == -INFINITY ? 0.f : mn;
+      // 2^x on the hardware's exp2 (results below 2^-126 flush to 0: weights that small
+      // against the running maximum's 1 do not change an fp32 sum)
+      const float alpha = __builtin_amdgcn_exp2f(m[j] - ms);
+      m[j] = mn;
+      l[j] *= alpha;
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+      for (int nb = 0; nb < 4; ++nb) o[j][nb] *= alpha;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sv[b][r] - ms);
-        l += p;
-        // masked tokens' norms may be stale (even NaN): selected away, not multiplied
-        pv[b][r] = (!MASK || 16 * b + 4 * g + r < rel) ? p * nv[b][r] : 0.f;
-      }
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(sv[j][b][r] - ms);
+          l[j] += p;
+          // masked tokens' norms may be stale (even NaN): selected away, not multiplied
+          const float v = (!MASK || 16 * b + 4 * g + r < rel[j]) ? p * nv[b][r] : 0.f;
+          const _Float16 hv = (_Float16)v;
+          bh[j][b >> 1][4 * (b & 1) + r] = hv;
+          if constexpr (PREC) bl[j][b >> 1][4 * (b & 1) + r] = (_Float16)(v - (float)hv);
+        }
+    }
 
-    // ---- O^T += V^T P^T over the tile's two 32-token halves
+    // ---- O^T += V^T P^T over the tile's two 32-token halves; one value operand per
+    // (s, nb) serves every row group
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      pf_v8h bh, bl;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = pv[2 * s + (i >> 2)][i & 3];
-        const _Float16 hv = (_Float16)v;
-        bh[i] = hv;
-        if constexpr (PREC) bl[i] = (_Float16)(v - (float)hv);
-      }
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
         const pf_u32x2 h0 = tv[0][b0 * VC + vcp], h1 = tv[0][b1 * VC + vcp];
         const pf_v8h ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, o[nb], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NGR; ++j)
+          o[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j][s], o[j][nb], 0, 0, 0);
         if constexpr (PREC) {
           const pf_u32x2 l0 = tv[NP - 1][b0 * VC + vcp], l1 = tv[NP - 1][b1 * VC + vcp];
           const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
-          o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, o[nb], 0, 0, 0);
-          o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, o[nb], 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < NGR; ++j) {
+            o[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j][s], o[j][nb], 0, 0, 0);
+            o[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j][s], o[j][nb], 0, 0, 0);
+          }
         }
       }
     }
@@ -361,15 +393,9 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
     else tile(std::true_type{}, kt);
   }
 
-  // ---- out = (O / l) R_v.  o[nb][r] of lane (c, g) = O_c[16 nb + 4 g + r]: the B operand
-  // of k-step (nb, r); A[m][k] = R_v[16 nb + 4 k + r][16 ob + m]; lane (c, g) register r
-  // gets out_c[16 ob + 4 g + r].
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  const float inv = l > 0.f ? 1.f / (l * vsc) : 0.f;
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) o[nb] *= inv;
-  float* dst = a.out + qoff;
+  // ---- out = (O / l) R_v.  o[j][nb][r] of lane (c, g) = O_c[16 nb + 4 g + r]: the B
+  // operand of k-step (nb, r); A[m][k] = R_v[16 nb + 4 k + r][16 ob + m]; lane (c, g)
+  // register r gets out_c[16 ob + 4 g + r].
   // this lane's R_v entries, all requested before the first product
   float rv[4][16];
 #pragma unroll
@@ -379,14 +405,22 @@ __global__ __launch_bounds__(kPfThreads, PREC ? 3 : 4) void dl_prefill_kernel(Pf
 #pragma unroll
       for (int r = 0; r < 4; ++r) rv[ob][4 * nb + r] = a.vrot[(16 * nb + 4 * g + r) * 64 + 16 * ob + c];
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
-    pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NGR; ++j) {
+    float lt = l[j];
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    const float inv = lt > 0.f ? 1.f / (lt * vsc) : 0.f;
+    float* dst = a.out + qoff[j];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int ob = 0; ob < 4; ++ob) {
+      pf_v4f acc = (pf_v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[ob][4 * nb + r], o[nb][r], acc, 0, 0, 0);
-    if (row < nG) *reinterpret_cast<pf_v4f*>(dst + 16 * ob + 4 * g) = acc;
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[ob][4 * nb + r], o[j][nb][r] * inv, acc, 0, 0, 0);
+      if (row[j] < nG) *reinterpret_cast<pf_v4f*>(dst + 16 * ob + 4 * g) = acc;
+    }
   }
 }
 
@@ -419,7 +453,11 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
              max_blocks, block_size);
   const int64_t rows = (int64_t)n * (hq / hkv);
   TQ_REQUIRE(rows <= INT_MAX - kPfRows, "too many query rows in one call");
-  const int64_t grid = (rows + kPfRows - 1) / kPfRows * hkv;
+  // bf16 queries: one product per term (their outputs are consumed in bf16), two 16-row
+  // groups per wave
+  const bool prec = q_dtype != TQ_BF16;
+  const int wg_rows = prec ? kPfRows : 2 * kPfRows;
+  const int64_t grid = (rows + wg_rows - 1) / wg_rows * hkv;
   TQ_REQUIRE(grid <= INT_MAX, "too many query rows in one call");
   TQ_REQUIRE(num_blocks <= (int64_t)UINT_MAX, "too many blocks");
   if (n == 0) return TQ_OK;
@@ -440,8 +478,6 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
   a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
   a.qscale = scale * 1.4426950408889634f;
   a.out = out;
-  // bf16 queries: one product per term (their outputs are consumed in bf16)
-  const bool prec = q_dtype != TQ_BF16;
   const dim3 gr((unsigned)grid), bl(kPfThreads);
   hipStream_t st = as_stream(stream);
   if (bsl >= 6) {
