@@ -93,14 +93,14 @@ __device__ __forceinline__ float pf_pow2_scale(float amax) {
 // otherwise one fp16 product per term (about 2^-11 relative per operand), for bf16 queries
 // whose outputs are consumed in bf16 (2^-9).
 template <bool SUB, bool PREC>
-__global__ __launch_bounds__(kPfThreads, PREC ? 3 : 2) void dl_prefill_kernel(PfArgs a) {
+__global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
   // Tables, KC / VC copies of each entry (lane L reads copy L % KC, L % VC, so a wave's
   // random lookups spread over the banks instead of piling onto a 1 KB table's):
   //   tk[p][i KC + j]  key byte i -> (c[i >> 4], c[i & 15]) as two fp16, part p (hi, lo)
   //   tv[p][i VC + j]  value byte i -> its four 2-bit codes' centroids as four fp16
   constexpr int KC = PREC ? 4 : 8, VC = PREC ? 2 : 4, NP = PREC ? 2 : 1;
-  constexpr int NGR = PREC ? 1 : 2;  // 16-row groups per wave (sharing each tile's operands)
+  constexpr int NGR = PREC ? 2 : 3;  // 16-row groups per wave (sharing each tile's operands)
   __shared__ __attribute__((aligned(16))) uint32_t tk[NP][256 * KC];
   __shared__ __attribute__((aligned(16))) pf_u32x2 tv[NP][256 * VC];
   __shared__ float sc_s[2];
@@ -456,7 +456,7 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
   // bf16 queries: one product per term (their outputs are consumed in bf16), two 16-row
   // groups per wave
   const bool prec = q_dtype != TQ_BF16;
-  const int wg_rows = prec ? kPfRows : 2 * kPfRows;
+  const int wg_rows = prec ? 2 * kPfRows : 3 * kPfRows;
   const int64_t grid = (rows + wg_rows - 1) / wg_rows * hkv;
   TQ_REQUIRE(grid <= INT_MAX, "too many query rows in one call");
   TQ_REQUIRE(num_blocks <= (int64_t)UINT_MAX, "too many blocks");
