@@ -449,8 +449,8 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
  * block_table [max_blocks] (T <= max_blocks * block_size).  out [n][hq][64] fp32,
  * 16-byte aligned.  Replaces the reference backend's prefill attention over its
  * dequantized cache (vllm_plugin/__init__.py:400 via cache.py:282-339), which has no
- * block tables and no causal mask; one kernel streams each 64-token tile once per 16
- * query rows instead of once per row.  Pools of any size (64-bit addresses; block ids
+ * block tables and no causal mask; one kernel streams each 64-token tile once per 48
+ * query rows (32 for fp32 / fp16 queries) instead of once per row.  Pools of any size (64-bit addresses; block ids
  * clamped into the pool).  No workspace.
  */
 int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, int64_t T, int32_t hq,

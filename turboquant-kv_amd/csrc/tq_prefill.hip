@@ -6,10 +6,12 @@
 // with cache.py:282-339 for the scores and values).  score = scale * n_k <R_k q, c_k[code]>,
 // softmax over the visible tokens, out = (sum_t w_t n_v,t c_v[code_t]) R_v.
 //
-// One workgroup of four waves per (64 query rows, KV head h); query row r of h is query
-// head h G + r % G of new token r / G.  Each wave owns 16 rows and streams the 64-token
-// tiles its last row can see, once for all 16 rows (the per-token decode launch reads the
-// history once per row), with an online softmax in the log2 domain.  Per tile and wave:
+// One workgroup of four waves per (64 NGR query rows, KV head h); query row r of h is
+// query head h G + r % G of new token r / G.  Each wave owns NGR groups of 16 rows (three
+// for bf16 queries, two otherwise) and streams the 64-token tiles its last row can see,
+// once for all of them (the per-token decode launch reads the history once per row); each
+// tile's key and value operands are looked up once and feed every group's MFMAs.  Online
+// softmax in the log2 domain.  Per tile, wave and row group:
 //   S^T = K Qrot^T  v_mfma_f32_16x16x32_f16, one 16-token group b per MFMA chain.  A: lane
 //                   (c, g) = (lane % 16, lane / 16) holds token 16 b + c, dims 8 g .. 8 g + 7
 //                   and 32 + 8 g .. : one 4-byte read of its pair bytes each, four pair-

@@ -232,7 +232,7 @@ def prefill_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_poo
     """Causal prefill of one sequence over decode-layout paged pools: its n new tokens
     q [n, Hq, 64] sit at positions T-n .. T-1 and new token i attends to tokens
     0 .. T-n+i, read through block_table [max_blocks].  -> [n, Hq, 64] fp32.  One kernel
-    streams each 64-token tile once per 16 query rows."""
+    streams each 64-token tile once per 48 query rows (32 for fp32 / fp16 queries)."""
     _require_device(q, "q")
     return _ops().prefill_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool,
                                              block_table, int(T), kcentroids, vcentroids,

@@ -242,7 +242,7 @@ class PagedKVPools:
         G = Hq // H
         st = self.layers[layer]
         if "kp" in st:
-            # one kernel: each 64-token tile of the history read once per 16 query rows
+            # one kernel: each 64-token tile of the history read once per 48 query rows
             return ops.prefill_attention_paged_dl(q.to(self.device), st["kp"], st["kn"], st["vt"],
                                                   st["vn"], block_table.to(self.device), T, self.kcen,
                                                   self.vcen, self.R_k, self.R_v, float(scale))
