@@ -329,7 +329,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
       for (int j = 0; j < NGR; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float x = acc[j][r] * kinv[j] * nk[b][r];
+          // score / kinv (kinv a power of two: scaling it out is exact)
+          const float x = acc[j][r] * nk[b][r];
           sv[j][b][r] = (!MASK || 16 * b + 4 * g + r < rel[j]) ? x : -INFINITY;
         }
     }
@@ -343,20 +344,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sv[j][b][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mn = fmaxf(m[j], mx);
+      const float mn = fmaxf(m[j], mx * kinv[j]);
       const float ms = mn == -INFINITY ? 0.f : mn;
       // 2^x on the hardware's exp2 (results below 2^-126 flush to 0: weights that small
-      // against the running maximum's 1 do not change an fp32 sum)
-      const float alpha = __builtin_amdgcn_exp2f(m[j] - ms);
-      m[j] = mn;
-      l[j] *= alpha;
+      // against the running maximum's 1 do not change an fp32 sum).  The accumulators are
+      // rescaled only when some row's maximum moved (a few tiles per row).
+      if (__any(mn != m[j])) {
+        const float alpha = __builtin_amdgcn_exp2f(m[j] - ms);
+        l[j] *= alpha;
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) o[j][nb] *= alpha;
+        for (int nb = 0; nb < 4; ++nb) o[j][nb] *= alpha;
+      }
+      m[j] = mn;
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(sv[j][b][r] - ms);
+          const float p = __builtin_amdgcn_exp2f(fmaf(sv[j][b][r], kinv[j], -ms));
           l[j] += p;
           // masked tokens' norms may be stale (even NaN): selected away, not multiplied
           const float v = (!MASK || 16 * b + 4 * g + r < rel[j]) ? p * nv[b][r] : 0.f;
