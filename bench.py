@@ -324,7 +324,8 @@ def bench_prefill(args, extra):
     flop = Hq * n * (n + 1) / 2 * 4 * d  # q.k and w.v over the visible (query, token) pairs
     extra["prefill_paged_dl_4096_llama1b"] = {
         "ms_per_layer": ms, "tokens_per_s": n / ms * 1e3, "TFLOPs": flop / ms / 1e9,
-        "kernel": "dl_prefill_kernel<true> (block 16)",
+        "fp16_dense_peak_frac": flop / ms / 1e9 / 2500.0,
+        "kernel": "dl_prefill_kernel<true,false> (block 16, bf16 queries)",
         "per_token_decode_ms": ms_tok,
         "note": "one layer, 4096 new tokens at positions 0..4095 (T = n), bf16 queries, fp32 out; "
                 "TFLOP/s counts 4 d flop per visible (query head, token) pair; the kernel runs "
