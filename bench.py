@@ -145,7 +145,8 @@ def bench_scan(args, extra):
             t = time_op(lambda: ops.ip_scan_topk_pairs(qq, pairs, norms, cen, R, k), steps, 1)
             extra[f"scan_b4_Q{Q}"] = {"ms_per_batch": t, "queries_per_s": Q / t * 1e3}
             log(f"scan b=4 Q={Q}: {t:.2f} ms/batch, {Q / t * 1e3:.0f} q/s")
-    res["db4"] = (packed, norms, R, cen)  # bit-plane rows: the CPU reference's input
+    # bit-plane rows (the CPU reference's input) and the pair rows the headline op reads
+    res["db4"] = (packed, norms, R, cen, pairs)
     if not args.quick:
         for bits in (3, 2):
             # TurboQuantIndex keeps 2/3-bit d=128 rows as pair rows (same bytes per row):
@@ -328,8 +329,9 @@ def bench_prefill(args, extra):
         "kernel": "dl_prefill_kernel<true,false> (block 16, bf16 queries)",
         "per_token_decode_ms": ms_tok,
         "note": "one layer, 4096 new tokens at positions 0..4095 (T = n), bf16 queries, fp32 out; "
-                "TFLOP/s counts 4 d flop per visible (query head, token) pair; the kernel runs "
-                "each fp16 MFMA product as hi/lo parts (3 MFMAs per term)"}
+                "TFLOP/s counts 4 d flop per visible (query head, token) pair; with bf16 queries "
+                "the kernel runs one fp16 MFMA product per term (fp32/fp16 queries take hi/lo "
+                "parts, 3 MFMAs per term) and three 16-row query groups per wave"}
     log(f"prefill 4096 tokens (paged decode layout, block 16): {ms:.3f} ms per layer, "
         f"{n / ms * 1e3 / 1e6:.2f} M tokens/s, {flop / ms / 1e9:.1f} TFLOP/s; per-token decode "
         f"launch {ms_tok:.3f} ms")
@@ -610,6 +612,7 @@ def bench_cpu_configs(args, extra):
         log("cpu legs skipped: oracle/libtq_oracle_cpu.so is not built")
         return
     kind = "reference" if cpu_libs.have_ref() else "port"
+    which = "ref" if cpu_libs.have_ref() else "port"
     gen = torch.Generator().manual_seed(0)
     x = torch.randn(65536, 128, generator=gen)
     qs = torch.randn(256, 128, generator=gen)
@@ -621,7 +624,7 @@ def bench_cpu_configs(args, extra):
     packed, norms = cpu_libs.rotate_and_quantize(xn, Rn, bn, 4)
     tq = time.perf_counter() - t0
     t0 = time.perf_counter()
-    s_cpu, i_cpu = cpu_libs.search_packed(qn, packed, norms, Rn, cn, 4, 10, kind)
+    s_cpu, i_cpu = cpu_libs.search_packed(qn, packed, norms, Rn, cn, 4, 10, which)
     ts = time.perf_counter() - t0
     # the same work on the GPU: quantize, then the 256-query scan over bit-plane rows
     xg, Rg, bg, cg, qg = (t.cuda() for t in (x, R, bnd, cen, qs))
@@ -668,34 +671,55 @@ def rs_normal(n, d, seed=0):
 
 
 def cpu_baseline(db, budget_s=12.0):
-    """The reference's C++ search_packed over the same 10M-row database, one query per
-    OpenMP thread, enough rounds of queries for about `budget_s` seconds."""
+    """The reference's C++ search_packed (turboquant_core.cpp:407-514, compiled from the
+    reference's own source into oracle/_ref; "kind": "reference") -- or, where that build
+    is absent, this repo's C restatement of it ("kind": "port") -- over the same 10M-row
+    database, one query per OpenMP thread, enough rounds of queries for about `budget_s`
+    seconds.  The same queries then run one at a time through the headline GPU op, and
+    the fraction whose top-k ids and scores equal the CPU's bit for bit is reported: the
+    full-size parity check of the timed path."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import cpu_libs
+    from turboquant_kv import _lib
 
-    packed, norms, R, cen = db
+    packed, norms, R, cen, pairs = db
     if not (cpu_libs.have_ref() or cpu_libs.have_port()):
         return None
-    kind = "reference" if cpu_libs.have_ref() else "port"
+    which = "ref" if cpu_libs.have_ref() else "port"
+    kind = "reference" if which == "ref" else "port"
     cores = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     p = packed.cpu().numpy()
     nm = norms.cpu().numpy()
     Rn, cn = R.cpu().numpy(), cen.cpu().numpy()
-    qn = queries(cores * 64, 128, seed=3).float().cpu().numpy()
+    qh = queries(cores * 64, 128, seed=3)
+    qn = qh.float().cpu().numpy()
     t0 = time.perf_counter()
-    cpu_libs.search_packed(qn[:cores], p, nm, Rn, cn, 4, 10, kind)  # one query per thread
+    cpu_libs.search_packed(qn[:cores], p, nm, Rn, cn, 4, 10, which)  # one query per thread
     t1 = time.perf_counter() - t0
     rounds = max(1, min(64, int(budget_s / max(t1, 1e-3))))
     nq = cores * rounds
     t0 = time.perf_counter()
-    cpu_libs.search_packed(qn[:nq], p, nm, Rn, cn, 4, 10, kind)
+    s_cpu, i_cpu = cpu_libs.search_packed(qn[:nq], p, nm, Rn, cn, 4, 10, which)
     dt = time.perf_counter() - t0
+    ops = _lib.ops()
+    same = 0
+    for j in range(nq):
+        s_g, i_g = ops.ip_scan_topk_pairs(qh[j:j + 1], pairs, norms, cen, R, 10)
+        same += int(np.array_equal(i_g.cpu().numpy()[0], i_cpu[j])
+                    and np.array_equal(s_g.cpu().numpy()[0].view(np.uint32),
+                                       s_cpu[j].view(np.uint32)))
+    log(f"cpu baseline ({kind}, {cores} threads): {nq / dt:.1f} q/s; GPU top-k bit-exact on "
+        f"{same} of {nq} queries")
+    name = ("turboquant_core.cpp search_packed compiled from the reference's source"
+            if which == "ref" else "C restatement of turboquant_core.cpp search_packed")
     return {"value": nq / dt, "unit": "queries/s", "cores": cores, "kind": kind,
+            "code": name,
             "sample": f"{nq} queries over all {p.shape[0]} rows of the same 4-bit database "
-                      f"({dt:.1f} s, one query per OpenMP thread, k=10)"}
+                      f"({dt:.1f} s, one query per OpenMP thread, k=10)",
+            "cpu_gpu_topk_bit_exact": same / nq, "cpu_gpu_topk_queries_compared": nq}
 
 
 def main():

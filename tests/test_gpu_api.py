@@ -47,6 +47,37 @@ def test_quantize_mse_api_vs_reference(golden):
     assert np.array_equal(norms.float().cpu().numpy(), O.bf16_bits_to_f32(m["bf16_d64_b4_norms_u16"]))
 
 
+def test_quantize_with_rht_rotation_vs_reference_matrix(golden):
+    """rotation="rht": the product builds its RHT matrix on this host with torch.linalg.qr,
+    whose float32 bits differ between hosts (up to ~30 ulp against the fixture host).  The
+    codes are bit-exact with the oracle under the matrix the product built (outside the
+    fp32 decision band), and equal the reference's codes under the reference-written matrix
+    except where the matrices' difference can move a coordinate across a boundary."""
+    from turboquant_kv import TurboQuantMSE
+    from turboquant_kv.reference import lloyd_max_codebook
+    rot = golden("rotation")
+    m = golden("quant_mse")
+    for d in (64, 128):
+        x = m["d128_x"][:, :d].copy() if d == 64 else m["d128_x"]
+        R_ref = rot[f"RHT_d{d}_s42"]
+        for b in (2, 4):
+            tq = TurboQuantMSE(d, b, seed=42, rotation="rht", device=DEV)
+            R_own = tq.rotation.cpu().numpy()
+            dev = float(np.abs(R_own.astype(np.float64) - R_ref).max())
+            assert dev <= d * 2.0 ** -24
+            packed, norms = tq.quantize(T(x))
+            codes = O.unpack_codes(packed.cpu().numpy(), b, d)
+            bnd = lloyd_max_codebook(b, d)[0].numpy()
+            _, n_o, c_own = O.quantize_mse(x, b, R_own, bnd)
+            O.check_codes(codes, c_own, x, R_own, bnd)
+            assert np.allclose(norms.cpu().numpy(), n_o, rtol=1e-6, atol=0)
+            # against the reference's matrix: |y - y_ref| <= sum_k |u_k| |dR_jk|, and
+            # |R_jk| = 1/sqrt(d), so the band widens by sqrt(d) * dev relative
+            _, _, c_ref = O.quantize_mse(x, b, R_ref, bnd)
+            amb = O.code_margin(x, R_ref, bnd, rel=2.0 ** -20 + np.sqrt(d) * dev)
+            assert not ((codes != c_ref) & ~amb).any()
+
+
 def test_quantize_prod_api_roundtrip(golden):
     from turboquant_kv import quantize_prod, dequantize_prod
     pr = golden("quant_prod")

@@ -164,9 +164,10 @@ def test_decode_paged_vs_contiguous_and_f64(d, kb, vb, G, bs, qdt):
     assert np.max(np.abs(got - want)) <= tol * np.max(np.abs(want))
 
 
-def _step_meta(blocks, before, n_new, bs):
+def _step_meta(blocks, before, n_new, bs, host_copies=False):
     """One vLLM-ordered batch: sequences with n_new > 1 are prefills (listed first), the
-    rest decode one token.  blocks[i] = sequence i's physical blocks for all its tokens."""
+    rest decode one token.  blocks[i] = sequence i's physical blocks for all its tokens.
+    host_copies: the metadata also carries host lists of query_start_loc and seq_lens."""
     from turboquant_kv.vllm_plugin import TurboQuantAttentionMetadata
     order = sorted(range(len(n_new)), key=lambda i: n_new[i] == 1)
     width = max(len(b) for b in blocks)
@@ -181,8 +182,10 @@ def _step_meta(blocks, before, n_new, bs):
         slot_mapping=torch.tensor(slots, dtype=torch.long, device=DEV),
         seq_lens=torch.tensor(lens, dtype=torch.int32, device=DEV),
         block_tables=torch.from_numpy(tab).to(DEV),
-        query_start_loc=torch.tensor(qsl, dtype=torch.int32),
-        num_prefills=sum(1 for i in order if n_new[i] > 1))
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32, device=DEV),
+        num_prefills=sum(1 for i in order if n_new[i] > 1),
+        query_start_loc_cpu=list(qsl) if host_copies else None,
+        seq_lens_cpu=list(lens) if host_copies else None)
     return md, order, lens, tab
 
 
@@ -441,7 +444,7 @@ def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
     before = [0, 0, 0, 0]
     scale = 0.125
     for step, n_new in enumerate(steps):
-        md, order, lens, tab = _step_meta(blocks, before, n_new, bs)
+        md, order, lens, tab = _step_meta(blocks, before, n_new, bs, host_copies=step == 0)
         n_tok = sum(n_new)
         q = torch.randn(n_tok, Hq, d, device=DEV, dtype=torch.bfloat16)
         k = torch.randn(n_tok, Hkv, d, device=DEV, dtype=torch.bfloat16)

@@ -33,7 +33,21 @@ def test_product_codebook_rotation_qjl_bits(golden):
             assert np.array_equal(make_rotation_matrix(d, s).numpy(), rot[f"R_d{d}_s{s}"])
             assert np.array_equal(make_qjl_matrix(d, d, s).numpy(), qj[f"S_d{d}_s{s}"])
     for d in (64, 128):
-        assert np.array_equal(make_rht_rotation(d, 42).numpy(), rot[f"RHT_d{d}_s42"])
+        # The RHT matrix is re-orthogonalized by torch.linalg.qr (reference.py:174), whose
+        # float32 LAPACK bits depend on the host's kernels: the fixture host and an MI355X
+        # box differ by up to ~30 ulp (4e-7 at d = 64).  Pinned here at the scale of float32
+        # Householder QR's backward error, d * 2^-24 entrywise, with the same signs and
+        # orthogonality; tests/test_gpu_api.py checks the codes quantized with it.
+        got, want = make_rht_rotation(d, 42).numpy(), rot[f"RHT_d{d}_s42"]
+        assert got.dtype == np.float32 and got.shape == (d, d)
+        assert np.array_equal(np.sign(got), np.sign(want))
+        tol = d * 2.0 ** -24
+        assert np.abs(got.astype(np.float64) - want).max() <= tol
+        g64 = got.astype(np.float64)
+        assert np.abs(g64 @ g64.T - np.eye(d)).max() <= 2 * tol
+        # before the QR every entry is +-1/sqrt(d) (d a power of two: H D is already
+        # orthogonal), and the QR only fixes rounding
+        assert np.abs(np.abs(g64) - 1 / np.sqrt(d)).max() <= tol
     with pytest.raises(ValueError):
         make_rotation_matrix(8, 1, "nope")
 

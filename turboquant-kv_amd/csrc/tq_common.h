@@ -122,6 +122,39 @@ __device__ __forceinline__ int count_below(const float* bnd, int nlev, float y) 
   return lo;
 }
 
+// ---------------------------------------------------------------- MFMA operand fence
+// Explicit wait states between VALU fp32 -> fp16 conversions and the MFMAs that read
+// their results as an A/B operand.  On gfx950 an MFMA issued directly after the
+// v_cvt_pk_f16_f32 that wrote its operand has read stale registers.  The asm below
+// redefines the operand registers, so every MFMA that reads them is ordered after it
+// whatever the scheduler does, and its two s_nop 7 put 16 wait states between the last
+// conversion that wrote them and that MFMA.  (A copy the register allocator might insert
+// after it is a plain move, whose VALU -> MFMA hazard the compiler tracks itself.)  The asm
+// is not volatile: it has no side effects, so memory operations (the table lookups) may
+// still be scheduled across it; its outputs are used, so it is never dropped.
+template <typename A>
+__device__ __forceinline__ void mfma_operand_fence(A& a) {
+  asm("s_nop 7\n\ts_nop 7" : "+v"(a));
+}
+template <typename A, typename B>
+__device__ __forceinline__ void mfma_operand_fence(A& a, B& b) {
+  asm("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
+template <typename A, typename B, typename C, typename D>
+__device__ __forceinline__ void mfma_operand_fence(A& a, B& b, C& c, D& d) {
+  asm("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+template <typename A>
+__device__ __forceinline__ void mfma_operand_fence6(A& a, A& b, A& c, A& d, A& e, A& f) {
+  asm("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f));
+}
+template <typename A>
+__device__ __forceinline__ void mfma_operand_fence8(A& a, A& b, A& c, A& d, A& e, A& f, A& g,
+                                                    A& h) {
+  asm("s_nop 7\n\ts_nop 7"
+               : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h));
+}
+
 inline bool valid_dtype(int dt) { return dt == TQ_F32 || dt == TQ_F16 || dt == TQ_BF16; }
 inline size_t dtype_size(int dt) { return dt == TQ_F32 ? 4 : 2; }
 

@@ -359,6 +359,7 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
       wa[r] = (_Float16)(p * cur.vn[r]);
     }
     l += psum;
+    tq::mfma_operand_fence(wa);  // VALU conversions -> MFMA operand: explicit wait states
 
     // ---- p.V
     uint32_t Tw[2 * VB];
@@ -1081,22 +1082,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     }
     l += psum;
     // The weights are written by VALU conversions and read by the MFMAs below as the A
-    // operand.  Pinning them here (the empty asm materializes them) and the schedule
-    // barriers keep the table lookups (at least 16 instructions) between the two: issued
-    // right after a v_cvt_pk_f16_f32, an MFMA has read stale operand registers on gfx950.
-    {
-      u32x2 w2 = __builtin_bit_cast(u32x2, wh);
-      uint32_t w2x = w2.x, w2y = w2.y;
-      asm volatile("" : "+v"(w2x), "+v"(w2y));
-      wh = as_v4h(w2x, w2y);
-      if constexpr (EXACT_V) {
-        u32x2 l2 = __builtin_bit_cast(u32x2, wl);
-        uint32_t l2x = l2.x, l2y = l2.y;
-        asm volatile("" : "+v"(l2x), "+v"(l2y));
-        wl = as_v4h(l2x, l2y);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    // operand: explicit wait states between the two (tq::mfma_operand_fence).
+    if constexpr (EXACT_V) tq::mfma_operand_fence(wh, wl);
+    else tq::mfma_operand_fence(wh);
 
     // ---- p.V: one 16x16x32 MFMA per (token half G, dim group dg): A rows = heads (rows
     // 4-15 unused), k = 8 sl + j: tokens of block 8G + sl (j < 4) and 8G + 4 + sl (j >= 4),

@@ -370,6 +370,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
         }
     }
 
+    // The weights are written by VALU conversions and read by the MFMAs below as the B
+    // operand: explicit wait states between the two (tq::mfma_operand_fence).
+    if constexpr (NGR == 3 && !PREC) {
+      tq::mfma_operand_fence6(bh[0][0], bh[0][1], bh[1][0], bh[1][1], bh[2][0], bh[2][1]);
+    } else if constexpr (NGR == 2 && PREC) {
+      tq::mfma_operand_fence8(bh[0][0], bh[0][1], bh[1][0], bh[1][1], bl[0][0], bl[0][1],
+                              bl[1][0], bl[1][1]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NGR; ++j) {
+        if constexpr (PREC) tq::mfma_operand_fence(bh[j][0], bh[j][1], bl[j][0], bl[j][1]);
+        else tq::mfma_operand_fence(bh[j][0], bh[j][1]);
+      }
+    }
+
     // ---- O^T += V^T P^T over the tile's two 32-token halves; one value operand per
     // (s, nb) serves every row group
 #pragma unroll
@@ -459,8 +474,8 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
              max_blocks, block_size);
   const int64_t rows = (int64_t)n * (hq / hkv);
   TQ_REQUIRE(rows <= INT_MAX - kPfRows, "too many query rows in one call");
-  // bf16 queries: one product per term (their outputs are consumed in bf16), two 16-row
-  // groups per wave
+  // bf16 queries: one product per term (their outputs are consumed in bf16), three 16-row
+  // groups per wave; fp32 / fp16 queries: hi + lo parts, two groups per wave
   const bool prec = q_dtype != TQ_BF16;
   const int wg_rows = prec ? 2 * kPfRows : 3 * kPfRows;
   const int64_t grid = (rows + wg_rows - 1) / wg_rows * hkv;

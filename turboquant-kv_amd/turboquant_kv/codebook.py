@@ -98,7 +98,10 @@ def make_rht_rotation(dim: int, seed: int = 42) -> torch.Tensor:
     random +-1 diagonal from torch's CPU generator, normalized Sylvester Hadamard
     matrix of the next power of two, H @ D cropped to (dim, dim), re-orthogonalized
     by QR with the same sign fix.  torch's QR result depends on its thread count,
-    so it runs single-threaded here: the matrix is the same in every process."""
+    so it runs single-threaded here: the matrix is the same in every process on one
+    host.  Across hosts it is not bit-stable, in the reference as here: the float32
+    LAPACK kernels behind torch.linalg.qr differ by CPU, and two hosts' matrices differ
+    by an ulp or two per entry (both orthogonal to 1e-6)."""
     nthreads = torch.get_num_threads()
     torch.set_num_threads(1)
     try:

@@ -52,6 +52,9 @@ class TurboQuantAttentionMetadata:
       block_tables     [num_seqs, max_blocks] int32
       query_start_loc  [num_seqs + 1]: first token of each sequence in the batch
       num_prefills     number of leading prefill sequences
+      query_start_loc_cpu, seq_lens_cpu  optional host copies of the two (vLLM keeps
+                       them beside the device tensors); a step with prefill sequences
+                       reads them instead of copying the device tensors back
     """
 
     slot_mapping: torch.Tensor
@@ -60,6 +63,8 @@ class TurboQuantAttentionMetadata:
     query_start_loc: torch.Tensor
     num_prefills: int
     layer_id: int = 0
+    query_start_loc_cpu: Optional[List[int]] = None
+    seq_lens_cpu: Optional[List[int]] = None
 
 
 def gather_value_tiles(vt_pool: torch.Tensor, block_table: torch.Tensor, T: int) -> torch.Tensor:
@@ -310,20 +315,29 @@ class PagedKVPools:
         layer = md.layer_id
         self.write(layer, key, value, md.slot_mapping)
         out = output if output is not None else torch.empty_like(query)
-        qsl = md.query_start_loc.tolist()
-        lens = md.seq_lens.tolist()
-        for i in range(md.num_prefills):
-            a, b = qsl[i], qsl[i + 1]
-            if b > a:
-                out[a:b] = self.prefill(layer, query[a:b], md.block_tables[i], int(lens[i]),
-                                        scale).to(out.dtype)
-        d0 = qsl[md.num_prefills]
-        if len(qsl) - 1 > md.num_prefills:
-            nd = len(qsl) - 1 - md.num_prefills
-            out[d0:d0 + nd] = self.decode(layer, query[d0:d0 + nd],
-                                          md.block_tables[md.num_prefills:],
-                                          md.seq_lens[md.num_prefills:].to(self.device, torch.int32),
-                                          scale).to(out.dtype)
+        npf = md.num_prefills
+        if npf > 0:
+            # prefill needs each sequence's token range and context length on the host: the
+            # metadata's host copies, else one copy of just the prefill sequences' entries
+            if md.query_start_loc_cpu is not None and md.seq_lens_cpu is not None:
+                qsl, lens = md.query_start_loc_cpu, md.seq_lens_cpu
+            else:
+                both = torch.cat([md.query_start_loc[:npf + 1].to(torch.int64),
+                                  md.seq_lens[:npf].to(torch.int64)]).tolist()
+                qsl, lens = both[:npf + 1], both[npf + 1:]
+            for i in range(npf):
+                a, b = qsl[i], qsl[i + 1]
+                if b > a:
+                    out[a:b] = self.prefill(layer, query[a:b], md.block_tables[i], int(lens[i]),
+                                            scale).to(out.dtype)
+        # decode sequences hold one token each and come last: their count and position
+        # follow from the shapes, with no host copy of the device metadata
+        nd = md.block_tables.shape[0] - npf
+        if nd > 0:
+            d0 = query.shape[0] - nd
+            out[d0:] = self.decode(layer, query[d0:], md.block_tables[npf:],
+                                   md.seq_lens[npf:].to(self.device, torch.int32),
+                                   scale).to(out.dtype)
         return out
 
     def memory_bytes(self) -> int:
