@@ -155,9 +155,16 @@ int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d
  * bit-plane row rearranged, written by tq_pack_decode_layout (values = 0, one stream,
  * t_cap = N).  Identical scores and ids; each code is one masked nibble, so a lookup
  * costs one address instruction instead of two.  d must be 64 or 128 and `pairs`
- * 16-byte aligned.  Workspace: tq_scan_workspace_bytes(nq, d, 4, N, k) / (nq, d, 4, 0, 0).
+ * 16-byte aligned.  Workspace: tq_scan_pairs_workspace_bytes(nq, d, N, k) for the top-k
+ * scan, tq_scan_workspace_bytes(nq, d, 4, 0, 0) for the scores.  With two or more queries
+ * and that workspace the top-k runs the multi-query filtered scan (64 queries share each
+ * table lookup on the matrix cores; candidates rescored with the reference's arithmetic,
+ * so ids and scores are the exact scan's); a workspace of only
+ * tq_scan_workspace_bytes(nq, d, 4, N, k) runs the exact multi-query scan.
  * TurboQuantIndex keeps 4-bit MSE databases of those dims in this layout.
+ * Replaces: the scan of turboquant_core.cpp:407-514 (search_packed) for query batches.
  */
+size_t tq_scan_pairs_workspace_bytes(int64_t nq, int32_t d, int64_t N, int32_t k);
 int tq_ip_scan_topk_pairs(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
                           const uint8_t* pairs, const float* norms, int64_t N,
                           const float* centroids, const float* rotation, int32_t k,

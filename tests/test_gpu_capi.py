@@ -142,12 +142,16 @@ def k_pack_pairs(packed, d):
     return out[:N]
 
 
-def k_scan_pairs(q, pairs, norms, cen, R, k, q_dt=capi.TQ_F32):
+def k_scan_pairs(q, pairs, norms, cen, R, k, q_dt=capi.TQ_F32, exact=False):
+    """tq_ip_scan_topk_pairs; with two or more queries the full workspace runs the
+    multi-query filtered scan, exact=True the exact multi-query scan (smaller workspace)."""
     Q, d = q.shape
     N = pairs.shape[0]
     os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
     oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
-    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, 4, N, k), 1), dtype=torch.uint8, device=DEV)
+    wsb = (L().tq_scan_workspace_bytes(Q, d, 4, N, k) if exact
+           else L().tq_scan_pairs_workspace_bytes(Q, d, N, k))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
     nt = norms if torch.is_tensor(norms) else (T(norms) if N else torch.empty(0, dtype=torch.float32, device=DEV))
     capi.check(L().tq_ip_scan_topk_pairs(capi.p(T(q)), q_dt, capi.i64(Q), capi.i32(d), capi.p(pairs),
                                          capi.p(nt), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
@@ -795,6 +799,184 @@ def test_pairs_scan_one_query_past_4gib():
     assert np.array_equal(i[0], np.array(want_i))
     assert np.array_equal(s[0, :3].view(np.uint32), np.array([t[0] for t in pos[:3]], np.float32).view(np.uint32))
     assert (s[0, 3:] == 0).all()
+    del pairs, norms
+    torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------------ multi-query filtered scan
+def _cpu_search(q, p, nm, cen, R, k):
+    """The C restatement of the reference core's search (oracle/tq_cpu.c, OpenMP) over
+    bit-plane rows, for batches the numpy oracle is too slow for.  tests/test_oracle.py
+    holds it bit-exact with the reference's compiled core and with the numpy oracle,
+    including the oracle's order of exactly tied scores (lower index first; the core's own
+    heap leaves the order of tied scores unspecified)."""
+    import cpu_libs
+    return cpu_libs.search_packed(q, p, nm, R, cen, 4, k, "port")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_mq_scan_vs_oracle_and_exact_path(d):
+    # Batches of 2, 64 and 130 queries (one, one and three 64-query tiles, the last two
+    # partly filled) over ~100k unit rows: ids and scores bit-identical to the oracle and
+    # to the exact multi-query scan, for k = 1, 10, 32, fp32 and fp16 queries.
+    rs = np.random.RandomState(90 + d)
+    N = 100_003 if d == 128 else 60_001
+    R, cen, p, nm = _db(rs, N, d, 4)
+    nm = nm / np.float32(np.sqrt(d))  # unit-scale rows
+    pairs = k_pack_pairs(p, d)
+    for Q in (2, 64, 130):
+        q = rs.randn(Q, d).astype(np.float32)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+        s32, i32 = _cpu_search(q, p, nm, cen, R, 32)
+        if Q == 2:
+            so, io = O.search_topk(q, p, nm, cen, R, 4, 32)
+            assert np.array_equal(io, i32) and np.array_equal(so.view(np.uint32), s32.view(np.uint32))
+        for k in (1, 10, 32):
+            s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+            assert np.array_equal(i, i32[:, :k]), (Q, k)
+            assert np.array_equal(s.view(np.uint32), s32[:, :k].view(np.uint32)), (Q, k)
+            se, ie = k_scan_pairs(q, pairs, nm, cen, R, k, exact=True)
+            assert np.array_equal(ie, i) and np.array_equal(se.view(np.uint32), s.view(np.uint32))
+        q16 = q.astype(np.float16)
+        s, i = k_scan_pairs(q16, pairs, nm, cen, R, 10, capi.TQ_F16)
+        so, io = _cpu_search(q16.astype(np.float32), p, nm, cen, R, 10)
+        assert np.array_equal(i, io) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+def test_mq_scan_q1024_with_ties():
+    # configs[1]'s largest batch: 1024 normalized fp16 queries over 100,003 rows in which 40
+    # rows appear 25 times each (exact ties across and within blocks), k = 10 and 32:
+    # bit-identical to the reference core's search.
+    rs = np.random.RandomState(1024)
+    d, N = 128, 100_003
+    R, cen, p, nm = _db(rs, N, d, 4)
+    nm = nm / np.float32(np.sqrt(d))
+    src = rs.choice(N, 40, replace=False)
+    for j, r in enumerate(src):
+        dst = rs.choice(N, 24, replace=False)
+        p[dst] = p[r]
+        nm[dst] = nm[r]
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(1024, d).astype(np.float32)
+    q = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float16)
+    # the tied rows are the answer of some queries: queries 0-39 point at them
+    q[:40] = (O.dequantize_mse(p[src], np.ones(40, np.float32), 4, d, R, cen)).astype(np.float16)
+    qf = q.astype(np.float32)
+    s32, i32 = _cpu_search(qf, p, nm, cen, R, 32)
+    for k in (10, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k, capi.TQ_F16)
+        assert np.array_equal(i, i32[:, :k]), k
+        assert np.array_equal(s.view(np.uint32), s32[:, :k].view(np.uint32)), k
+
+
+def test_mq_scan_overflowing_lists_take_the_exact_fallback():
+    # 3000 copies of query 0's best row: its lists overflow (the query is answered by the
+    # exact scan), the other queries of the tile stay on the filter; all bit-exact.
+    rs = np.random.RandomState(77)
+    d = 128
+    R, cen, p, nm = _db(rs, 30000, d, 4)
+    q = rs.randn(5, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q[:1], p, nm, cen, R, 4)[0]))
+    idx = rs.choice(30000, 3000, replace=False)
+    p[idx] = p[top]
+    nm[idx] = nm[top]
+    pairs = k_pack_pairs(p, d)
+    for k in (4, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = O.search_topk(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+def test_mq_scan_special_norms():
+    # zero, negative, huge, tiny and infinite norms (inf * 0 = NaN rows never listed)
+    rs = np.random.RandomState(29)
+    d = 128
+    N = 150_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    nm = nm.copy()
+    idx = rs.permutation(N)
+    nm[idx[:2000]] = 0.0
+    nm[idx[2000:4000]] *= -1.0
+    nm[idx[4000:4010]] = 1e30
+    nm[idx[4010:4020]] = -1e30
+    nm[idx[4020:4030]] = 1e-38
+    nm[idx[4030:4036]] = np.inf
+    nm[idx[4036:4040]] = -np.inf
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(6, d).astype(np.float32)
+    want = O.lut_scores_f32(q, p, nm, cen, R, 4)
+    for k in (1, 10, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = _topk_no_nan(want, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+@pytest.mark.parametrize("qscale", [0.0, 1e-36, 1e-20, 1e20, 1e34])
+def test_mq_scan_extreme_query_in_tile(qscale):
+    # One query of the tile is zero or far outside the fp16 filter's range: the tile's
+    # bound turns the filter off and every query is answered by the exact scan.
+    rs = np.random.RandomState(37)
+    d = 64
+    N = 40_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    pairs = k_pack_pairs(p, d)
+    q = rs.randn(4, d).astype(np.float32)
+    q[2] *= np.float32(qscale)
+    want = O.lut_scores_f32(q, p, nm, cen, R, 4)
+    for k in (3, 10):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = _topk_no_nan(want, k)
+        assert np.array_equal(i, io), (qscale, k)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), (qscale, k)
+
+
+def test_mq_scan_ulp_ties():
+    # 600 copies of query 0's best row with norms a few ulps apart: the approximate scores
+    # cannot order them, the exact rescoring does.
+    rs = np.random.RandomState(43)
+    d = 128
+    N = 80_000
+    R, cen, p, nm = _db(rs, N, d, 4)
+    q = rs.randn(3, d).astype(np.float32)
+    top = int(np.argmax(O.lut_scores_f32(q[:1], p, nm, cen, R, 4)[0]))
+    idx = rs.choice(N, 600, replace=False)
+    p[idx] = p[top]
+    steps = rs.randint(-3, 4, size=600).astype(np.int32)
+    nm[idx] = (nm[top].view(np.int32) + steps).view(np.float32)
+    pairs = k_pack_pairs(p, d)
+    for k in (5, 32):
+        s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+        so, io = O.search_topk(q, p, nm, cen, R, 4, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+def test_mq_scan_past_4gib_equals_exact_path():
+    # 67.1M random rows of d = 128 (4.3 GB of codes, 64-bit row bases in the filter): the
+    # filtered batch equals the exact multi-query scan bit for bit, and the answer rows'
+    # scores equal the oracle's arithmetic on them.
+    rs = np.random.RandomState(59)
+    d = 128
+    N = (1 << 26) + 1017
+    R = O.dense_qr_rotation(d, 42)
+    _, cen = O.lloyd_max_codebook(4, d)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7)
+    pairs = torch.randint(0, 256, (N, d // 2), dtype=torch.uint8, device=DEV, generator=g)
+    norms = (torch.rand(N, device=DEV, generator=g) + 0.5).float()
+    q = rs.randn(3, d).astype(np.float32)
+    s, i = k_scan_pairs(q, pairs, norms, cen, R, 10)
+    se, ie = k_scan_pairs(q, pairs, norms, cen, R, 10, exact=True)
+    assert np.array_equal(i, ie) and np.array_equal(s.view(np.uint32), se.view(np.uint32))
+    for r in range(3):
+        rows = pairs[torch.from_numpy(i[r]).to(DEV)].cpu().numpy()
+        codes = np.empty((10, d), np.uint8)
+        codes[:, 0::2], codes[:, 1::2] = rows >> 4, rows & 15
+        want = O.lut_scores_f32(q[r:r + 1], O.pack_codes(codes, 4), norms[torch.from_numpy(i[r]).to(DEV)].cpu().numpy(),
+                                cen, R, 4)[0]
+        assert np.array_equal(s[r].view(np.uint32), want.view(np.uint32))
     del pairs, norms
     torch.cuda.empty_cache()
 

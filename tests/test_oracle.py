@@ -311,6 +311,28 @@ def test_c_search_bit_exact_with_oracle(golden, which):
         assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32))
 
 
+def test_c_search_port_tie_order_equals_oracle():
+    # Exactly tied scores (duplicated rows) and k past the ties: the C restatement lists
+    # them as the oracle does, score descending then lower index first.
+    rs = np.random.RandomState(8)
+    d, b, N = 64, 4, 3000
+    R = O.dense_qr_rotation(d, 42)
+    bnd, cen = O.lloyd_max_codebook(b, d)
+    x = rs.randn(N, d).astype(np.float32)
+    p, n, _ = O.quantize_mse(x, b, R, bnd)
+    q = rs.randn(3, d).astype(np.float32)
+    top = np.argsort(-O.lut_scores_f32(q, p, n, cen, R, b), axis=1)[:, :3]
+    for r in range(3):
+        for j in range(3):
+            dst = rs.choice(N, 7, replace=False)
+            p[dst], n[dst] = p[top[r, j]], n[top[r, j]]
+    for k in (5, 16, 32):
+        s0, i0 = O.search_topk(q, p, n, cen, R, b, k)
+        s1, i1 = cpu_libs.search_packed(q, p, n, R, cen, b, k, "port")
+        assert np.array_equal(i0, i1), k
+        assert np.array_equal(s0.view(np.uint32), s1.view(np.uint32)), k
+
+
 def test_cache_fixture_matches_oracle(golden):
     c, rot = golden("cache"), golden("rotation")
     R, Rv = rot["R_d64_s42"], rot["R_d64_s43"]

@@ -361,7 +361,7 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk_pairs(const at::Tensor& queries,
   auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
   auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
   if (Q == 0) return {os, oi};
-  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, 4, N, (int32_t)k), dev);
+  auto ws = workspace(tq_scan_pairs_workspace_bytes(Q, (int32_t)d, N, (int32_t)k), dev);
   check_rc(tq_ip_scan_topk_pairs(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
                                  p.data_ptr<uint8_t>(), nm.data_ptr<float>(), N,
                                  cen.data_ptr<float>(), R.data_ptr<float>(), (int32_t)k,

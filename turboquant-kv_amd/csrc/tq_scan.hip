@@ -76,6 +76,7 @@ struct ScanArgs {
   float* scores;            // ALL:  [nq_total][stream_rows]
   float* out_s;             // [nq_total][k] (TOPK: written by merge_kernel)
   int64_t* out_i;
+  const int32_t* qflag;     // optional [qps]: a block whose queries are all 0 here returns
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -337,6 +338,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   }
   const int q0 = s * a.qps + qb * QB;            // first global query of this block
   const int nq = min(QB, a.qps - qb * QB);       // valid queries in this block
+  if (a.qflag) {  // only flagged queries are scanned (uniform)
+    int any = 0;
+    for (int j = 0; j < nq; ++j) any |= a.qflag[qb * QB + j];
+    if (!any) return;
+  }
   const int P = BITS * a.bpp;
 
   build_tables<NLEV, DP, QB, PROD>(a, q0, nq, lut_s, sgn_s);
@@ -1422,7 +1428,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
                                                          const int32_t* __restrict__ part_i,
                                                          int nblocks, int k,
                                                          float* __restrict__ out_s,
-                                                         int64_t* __restrict__ out_i) {
+                                                         int64_t* __restrict__ out_i,
+                                                         const int32_t* __restrict__ qflag) {
+  if (qflag && !qflag[blockIdx.x]) return;  // only flagged queries (uniform)
   if (nblocks * k <= kThreads * kMergeRegs)  // uniform
     merge_query_regs(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
   else
@@ -2222,6 +2230,600 @@ pair_filter_kernel(FilterArgs a) {
   for (int e = nvalid_s + tid; e < a.k; e += kFsThreads) { a.bs[base + e] = -INFINITY; a.bi[base + e] = -1; }
 }
 
+// ------------------------------------------------------------------ multi-query filtered pair scan
+// Top-k over 4-bit pair-layout rows (d = 64 / 128) for batches of queries, with the
+// reference's exact scores and tie order (csrc/core/turboquant_core.cpp:407-514), as the
+// one-query filter above; here 64 queries share every table lookup.
+//
+// A wave takes 64 queries x 64 rows per step on v_mfma_f32_16x16x32_f16: A = 16 queries'
+// rotated vectors (one tile-wide power-of-two scale, rounded to fp16) per M tile, B = 16
+// rows' fp16 centroid pairs per N tile from one LDS lookup per code byte -- the lookups
+// of a row serve all 64 queries.  Lane (n, g) of N tile rt gets queries 16 mt + 4 g + r of
+// row 16 rt + n.  Bound (per tile, with l1 = max over its queries of ||q_rot||_1, e_c the
+// largest fp16 rounding error of a centroid, s the scale):
+//   |approx - exact| <= |n| beta + 2^-100,
+//   beta = (l1 (e_c (1 + 2^-11) + max|c| (2^-11 + 2^-15)) + d (max|c| + e_c) 2^-25 / s) (1 + 2^-9).
+// Terms: fp16 rounding of the scaled query (2^-11 relative, or 2^-25 absolute below fp16's
+// normal range, the last term), the centroids' fp16 errors, fp32 accumulation of the d
+// exact products (d 2^-24 <= 2^-17 relative) and the reference's own sequential sum and
+// final multiply (2^-17 + 2^-24); the (1 + 2^-9) covers rounding l1, beta, |n| beta and the
+// fma that adds it (each under 2^-12 of the bound); the absolute 2^-100 covers n / s
+// underflowing in m = n / s (an error below |acc| 2^-150 <= 2^-125).
+// Pipeline (one call):
+//   mq_prep_kernel    per 64-query tile: q_rot with the reference's arithmetic (kept for
+//                     the exact rescoring), the fp16 A operands, 1/s and beta.
+//   mq_sample_kernel  lo = approx - bound of 4096 evenly spaced 64-row groups; each lane
+//                     keeps, per query, the maximum over its 16 rows (a bucket).
+//   mq_select_kernel  per query: tau = the k-th largest bucket maximum.  Buckets are
+//                     disjoint row sets, so k distinct rows score at least tau; a row
+//                     whose upper bound hi = approx + bound is below tau is not in the
+//                     answer.
+//   mq_filter_kernel  every row: hi against tau per (query, row); the rows that reach it
+//                     (a few hundred per query at 10M rows) are listed per (block, query)
+//                     with (hi, lo, id).
+//   mq_merge_kernel   per query: tau' = the k-th best lo of the list, the entries whose hi
+//                     reaches it are rescored exactly (rows re-read from memory) and
+//                     ranked; the answer is the exact scan's, ties included.  A list that
+//                     overflowed (ties, duplicated rows, degenerate queries) flags the query
+//                     instead, and the exact multi-query scan then runs for flagged queries
+//                     only (its blocks for unflagged queries return at once).
+constexpr int kMqQ = 64;                 // queries per tile
+constexpr int kMqThreads = 512;          // 8 waves; one block per CU
+constexpr int kMqWaves = kMqThreads / 64;
+constexpr int kMqCap = 64;               // listed rows per (block, query)
+constexpr int kMqSampleGroups = 4096;    // 64-row groups sampled for tau
+constexpr int kMqGroupsPerWave = 4;      // sampled groups per wave (16 rows per bucket)
+constexpr int kMqSelVals = 64;           // bucket maxima per thread in mq_select_kernel
+constexpr int kMqSelThreads = 256;
+constexpr int kMqMaxBuckets = kMqSelVals * kMqSelThreads;
+constexpr int kMqMergeCap = 6144;        // listed entries a query's merge holds in LDS
+constexpr int kMqTilesPerRound = 8;      // query tiles per filter launch
+constexpr int kMqFallbackBlocks = 128;   // row blocks of the exact fallback scan
+static_assert((kMqSampleGroups / (kMqWaves * kMqGroupsPerWave)) * kMqWaves * 16 <= kMqMaxBuckets,
+              "bucket count");
+
+struct MqArgs {
+  const uint8_t* rows;  // [n][D / 2] pair layout
+  const float* norms;   // [n]
+  int64_t n;
+  const void* q;        // [nq][D]
+  int q_dt;
+  int nq;
+  const float* rot;     // [D][D]
+  const float* cen;     // [16]
+  int k;
+  float* qrot;          // [nq][D] rotated queries (reference arithmetic)
+  uint32_t* qa;         // per tile [KT][4][64 lanes][4 words]: fp16 A operands
+  float* tparam;        // per tile {1 / s, beta}
+  float* buckets;       // [round queries][nbk]
+  float* tau;           // [nq]
+  int nbk;              // buckets per query
+  int sstride;          // sampled group stride
+  int nsgroups;         // sampled groups
+  int nb;               // filter blocks
+  int tile0;            // first tile of the round
+  int* cnt;             // [round tiles][nb][64] listed rows per (block, query)
+  float* chi;           // [round tiles][nb][64][kMqCap]
+  float* clo;
+  int* cid;
+  int* flag;            // [nq] 1: the exact fallback answers this query
+  float* out_s;         // [nq][k]
+  int64_t* out_i;
+};
+
+// Rows of one 64-row group for the MFMA B operands: lane 16 g + i holds LW words of row
+// 16 rt + i at byte 4 LW g of the row, per 16-row tile rt, and the norm of row `lane`.
+// Rows past n read as zeros (the buffer's range check).
+template <int D, bool BIG>
+struct MqRows {
+  static constexpr int RB = D / 2;
+  static constexpr int LW = D / 32;
+  uint32_t w[4 * LW];
+  float n;
+  __device__ __forceinline__ void load(const MqArgs& a, uint32_t g, uint32_t ngroups,
+                                       __amdgpu_buffer_rsrc_t rows_all,
+                                       __amdgpu_buffer_rsrc_t norms_all, int lane, int cpol) {
+    __amdgpu_buffer_rsrc_t rs = rows_all, ns = norms_all;
+    uint32_t roff = (lane & 15) * RB + (lane >> 4) * (4 * LW), noff = lane * 4u;
+    if constexpr (BIG) {
+      const int64_t r0 = (int64_t)g * 64;
+      const int64_t left = a.n - r0;
+      const uint32_t nr = (uint32_t)(left < 64 ? (left > 0 ? left : 0) : 64);
+      rs = buf_rsrc(a.rows + r0 * RB, nr * (uint32_t)RB);
+      ns = buf_rsrc(a.norms + r0, nr * 4u);
+    } else {
+      const uint32_t gl = g < ngroups ? g : ngroups;
+      roff += gl * (64u * RB);
+      noff += gl * 256u;
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      if constexpr (LW == 4) {
+        const u32x4 v = cpol ? __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        w[4 * rt + 0] = v.x; w[4 * rt + 1] = v.y; w[4 * rt + 2] = v.z; w[4 * rt + 3] = v.w;
+      } else {
+        const u32x2 v = cpol ? __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, 0);
+        w[2 * rt + 0] = v.x; w[2 * rt + 1] = v.y;
+      }
+    }
+    n = __uint_as_float(cpol ? __builtin_amdgcn_raw_buffer_load_b32(ns, (int)noff, 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b32(ns, (int)noff, 0, 0));
+  }
+};
+
+// The 64 KB fp16 centroid-pair table (entry (byte << 8) | lane * 4: (c[byte >> 4],
+// c[byte & 15]) in 64 lane copies), as pair_filter_kernel builds it.
+__device__ __forceinline__ void mq_fill_htab(char* htab, const float* cen_s, int tid, int nthreads) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  for (int e = tid; e < 256 * 16; e += nthreads) {
+    const int b = e >> 4, c = e & 15;
+    const uint32_t v = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)cen_s[b >> 4], (_Float16)cen_s[b & 15]});
+    *reinterpret_cast<u32x4*>(htab + b * 256 + c * 16) = (u32x4){v, v, v, v};
+  }
+}
+
+// Approximate scores (in units of the scaled query) of 16 rows x 64 queries: N tile rt of
+// the group in `rb`.  acc[mt][r] = query 16 mt + 4 (lane >> 4) + r, row 16 rt + (lane & 15).
+template <int D, bool BIG>
+__device__ __forceinline__ void mq_tile_scores(const MqRows<D, BIG>& rb, int rt, const fs_v8h (&qa)[4][D / 32],
+                                               uint32_t lane4, const char* htab, fs_v4f (&acc)[4]) {
+  constexpr int KT = D / 32, LW = D / 32;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) acc[mt] = (fs_v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const uint32_t x = rb.w[LW * rt + kt];
+    const u32x4 bw = {fs_hlook<0>(x, lane4, htab), fs_hlook<1>(x, lane4, htab),
+                      fs_hlook<2>(x, lane4, htab), fs_hlook<3>(x, lane4, htab)};
+    const fs_v8h b = __builtin_bit_cast(fs_v8h, bw);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[mt][kt], b, acc[mt], 0, 0, 0);
+  }
+}
+
+// Per 64-query tile: q_rot (reference arithmetic: q_rot[j] = sum over i in order of
+// q[i] * R[j][i], each product rounded), the scale, beta and the fp16 A operands.
+template <int D>
+__global__ __launch_bounds__(256) void mq_prep_kernel(MqArgs a) {
+#pragma clang fp contract(off)
+  constexpr int KT = D / 32;
+  __shared__ float qs[kMqQ][D + 1];
+  __shared__ float qr[kMqQ][D + 1];
+  __shared__ float red[2][kMqQ];
+  __shared__ float cen_s[16];
+  const int tile = blockIdx.x, tid = threadIdx.x;
+  const int q0 = tile * kMqQ;
+  const int nvalid = min(kMqQ, a.nq - q0);
+  for (int e = tid; e < kMqQ * D; e += 256) {
+    const int qi = e / D, j = e % D;
+    qs[qi][j] = qi < nvalid ? load_as_f32(a.q, (int64_t)(q0 + qi) * D + j, a.q_dt) : 0.f;
+  }
+  if (tid < 16) cen_s[tid] = a.cen[tid];
+  __syncthreads();
+  {
+    const int j = tid % D, qg = tid / D;
+    constexpr int QSTEP = 256 / D;
+    float4 rrow[D / 4];
+    const float4* r4 = reinterpret_cast<const float4*>(a.rot + (size_t)j * D);
+#pragma unroll
+    for (int i = 0; i < D / 4; ++i) rrow[i] = r4[i];
+    for (int qi = qg; qi < kMqQ; qi += QSTEP) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < D / 4; ++i) {
+        v = v + qs[qi][4 * i] * rrow[i].x;
+        v = v + qs[qi][4 * i + 1] * rrow[i].y;
+        v = v + qs[qi][4 * i + 2] * rrow[i].z;
+        v = v + qs[qi][4 * i + 3] * rrow[i].w;
+      }
+      qr[qi][j] = v;
+      if (qi < nvalid) a.qrot[(size_t)(q0 + qi) * D + j] = v;
+    }
+  }
+  __syncthreads();
+  if (tid < kMqQ) {
+    float am = 0.f, l1 = 0.f;
+    for (int j = 0; j < D; ++j) {
+      const float x = fabsf(qr[tid][j]);
+      am = fmaxf(am, x);
+      l1 = l1 + x;
+    }
+    const bool v = tid < nvalid;
+    red[0][tid] = v ? am : 0.f;
+    red[1][tid] = v ? l1 : 0.f;
+    // a NaN anywhere in a valid query turns the filter off for the tile
+    if (v && !(l1 < INFINITY)) red[1][tid] = INFINITY;
+  }
+  __syncthreads();
+  float amax = 0.f, l1 = 0.f;
+  for (int i = 0; i < kMqQ; ++i) { amax = fmaxf(amax, red[0][i]); l1 = fmaxf(l1, red[1][i]); }
+  float cmax = 0.f, ec = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    cmax = fmaxf(cmax, fabsf(cen_s[i]));
+    ec = fmaxf(ec, fabsf(cen_s[i] - (float)(_Float16)cen_s[i]));
+  }
+  int ex = 0;
+  const bool scalable = amax > 0.f && amax < INFINITY;
+  if (scalable) frexpf(amax, &ex);
+  const bool ok = scalable && ex > -60 && ex < 60 && l1 < INFINITY && ec < INFINITY;
+  const float scale = ok ? ldexpf(1.f, 15 - ex) : 0.f;
+  const float inv_s = ok ? ldexpf(1.f, ex - 15) : 0.f;
+  float beta = INFINITY;
+  if (ok) {
+    beta = (l1 * (ec * (1.f + 0x1p-11f) + cmax * (0x1p-11f + 0x1p-15f)) +
+            (float)D * (cmax + ec) * 0x1p-25f * inv_s) * (1.f + 0x1p-9f);
+    if (!(beta < INFINITY)) beta = INFINITY;
+  }
+  if (tid == 0) {
+    a.tparam[2 * tile] = inv_s;
+    a.tparam[2 * tile + 1] = beta;
+  }
+  // A operand of (kt, mt), lane (m, g): query 16 mt + m, dims (D == 128 ? 32 : 16) g + 8 kt + e
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  for (int it = tid; it < KT * 4 * 64; it += 256) {
+    const int lane = it & 63, mt = (it >> 6) & 3, kt = it >> 8;
+    const int qi = 16 * mt + (lane & 15), g = lane >> 4;
+    const int dim0 = (D == 128 ? 32 : 16) * g + 8 * kt;
+    uint32_t wv[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const _Float16 h0 = (_Float16)(qr[qi][dim0 + 2 * w] * scale);
+      const _Float16 h1 = (_Float16)(qr[qi][dim0 + 2 * w + 1] * scale);
+      wv[w] = __builtin_bit_cast(uint32_t, (h2_t){h0, h1});
+    }
+    *reinterpret_cast<u32x4*>(a.qa + (((size_t)tile * KT + kt) * 4 + mt) * 256 + lane * 4) =
+        (u32x4){wv[0], wv[1], wv[2], wv[3]};
+  }
+}
+
+// The tile's A operands, 1/s and beta for this lane.
+template <int D>
+__device__ __forceinline__ void mq_load_tile(const MqArgs& a, int tile, int lane, fs_v8h (&qa)[4][D / 32],
+                                             float& inv_s, float& beta) {
+  constexpr int KT = D / 32;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(a.qa + (((size_t)tile * KT + kt) * 4 + mt) * 256 + lane * 4);
+      qa[mt][kt] = __builtin_bit_cast(fs_v8h, v);
+    }
+  inv_s = a.tparam[2 * tile];
+  beta = a.tparam[2 * tile + 1];
+}
+
+// Buckets: wave (block b, wave w) takes sampled groups (8 b + w) * 4 + u; lane (n, g) keeps
+// per query 16 mt + 4 g + r the largest lo over its rows 16 rt + n of those groups.
+template <int D, bool BIG>
+__global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+mq_sample_kernel(MqArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
+  __shared__ float cen_s[16];
+  const int rtile = blockIdx.y, tile = a.tile0 + rtile;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t n = (uint32_t)a.n;
+  const uint32_t ngroups = (n + 63) / 64;
+  fs_v8h qa[4][D / 32];
+  float inv_s, beta;
+  mq_load_tile<D>(a, tile, lane, qa, inv_s, beta);
+  if (tid < 16) cen_s[tid] = a.cen[tid];
+  __syncthreads();
+  mq_fill_htab(htab, cen_s, tid, kMqThreads);
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * (uint32_t)(D / 2));
+  const __amdgpu_buffer_rsrc_t norms_all = buf_rsrc(a.norms, BIG ? 0u : n * 4u);
+  const uint32_t lane4 = (uint32_t)lane * 4;
+  float bmax[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bmax[mt][r] = -INFINITY;
+  const int sw = blockIdx.x * kMqWaves + wave;
+#pragma unroll 1
+  for (int u = 0; u < kMqGroupsPerWave; ++u) {
+    const int s = sw * kMqGroupsPerWave + u;
+    if (s >= a.nsgroups) break;
+    const uint32_t g = (uint32_t)s * (uint32_t)a.sstride;
+    MqRows<D, BIG> rb;
+    rb.load(a, g, ngroups, rows_all, norms_all, lane, 0);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      fs_v4f acc[4];
+      mq_tile_scores<D, BIG>(rb, rt, qa, lane4, htab, acc);
+      const float nr = __shfl(rb.n, 16 * rt + (lane & 15));
+      const bool valid = g * 64u + 16u * rt + (uint32_t)(lane & 15) < n;
+      const float m = inv_s * nr;
+      const float L = valid ? -__builtin_fmaf(fabsf(nr), beta, 0x1p-100f) : -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bmax[mt][r] = fmaxf(bmax[mt][r], __builtin_fmaf(acc[mt][r], m, L));
+    }
+  }
+  const int bidx = sw * 16 + (lane & 15);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ql = 16 * mt + 4 * (lane >> 4) + r;
+      const float v = bmax[mt][r];
+      // +inf (an overflowed approximation) hides the bucket's other rows: no bound from it
+      a.buckets[(size_t)(rtile * kMqQ + ql) * a.nbk + bidx] = v < INFINITY ? v : -INFINITY;
+    }
+}
+
+// tau[q] = the k-th largest of the query's nbk bucket maxima (-inf when fewer than k are
+// above -inf): a 32-step binary search on order-preserving keys.
+__global__ __launch_bounds__(kMqSelThreads) void mq_select_kernel(MqArgs a) {
+  __shared__ int part[kMqSelThreads / 64];
+  __shared__ int tot;
+  const int ql = blockIdx.x;
+  const int q = a.tile0 * kMqQ + ql;
+  if (q >= a.nq) return;  // uniform
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* src = a.buckets + (size_t)ql * a.nbk;
+  uint32_t u[kMqSelVals];
+#pragma unroll
+  for (int j = 0; j < kMqSelVals; ++j) {
+    const int e = j * kMqSelThreads + tid;
+    u[j] = 0u;  // below every real key
+    if (e < a.nbk) {
+      const float v = src[e];
+      u[j] = v > -INFINITY ? fs_fkey(v) : 0u;
+    }
+  }
+  uint32_t x = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t t = x | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < kMqSelVals; ++j) c += (u[j] >= t);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+    if (lane == 0) part[wave] = c;
+    __syncthreads();
+    if (tid == 0) {
+      int s = 0;
+#pragma unroll
+      for (int w = 0; w < kMqSelThreads / 64; ++w) s += part[w];
+      tot = s;
+    }
+    __syncthreads();
+    if (tot >= a.k) x = t;
+    __syncthreads();
+  }
+  if (tid == 0) a.tau[q] = x ? fs_unkey(x) : -INFINITY;
+}
+
+// Every row against tau per query; rows whose upper bound reaches it are listed.
+template <int D, bool BIG>
+__global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+mq_filter_kernel(MqArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
+  __shared__ float cen_s[16];
+  __shared__ int cnt_s[kMqQ];
+  const int rtile = blockIdx.y, tile = a.tile0 + rtile;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t W = gridDim.x * kMqWaves;
+  const uint32_t gw = blockIdx.x * kMqWaves + wave;
+  const uint32_t n = (uint32_t)a.n;
+  const uint32_t ngroups = (n + 63) / 64;
+  const int nsteps = gw < ngroups ? (int)((ngroups - 1 - gw) / W + 1) : 0;
+  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * (uint32_t)(D / 2));
+  const __amdgpu_buffer_rsrc_t norms_all = buf_rsrc(a.norms, BIG ? 0u : n * 4u);
+  MqRows<D, BIG> ta, tb;
+  ta.load(a, gw, ngroups, rows_all, norms_all, lane, 1);
+  tb.load(a, gw + W, ngroups, rows_all, norms_all, lane, 1);
+
+  fs_v8h qa[4][D / 32];
+  float inv_s, beta;
+  mq_load_tile<D>(a, tile, lane, qa, inv_s, beta);
+  float th[4][4];
+  uint32_t qv = 0;  // bit 4 mt + r: query 16 mt + 4 (lane >> 4) + r is a real query
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int q = tile * kMqQ + 16 * mt + 4 * (lane >> 4) + r;
+      const bool v = q < a.nq;
+      th[mt][r] = v ? a.tau[q] : INFINITY;
+      qv |= (uint32_t)v << (4 * mt + r);
+    }
+  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < kMqQ) cnt_s[tid] = 0;
+  __syncthreads();
+  mq_fill_htab(htab, cen_s, tid, kMqThreads);
+  __syncthreads();
+  const uint32_t lane4 = (uint32_t)lane * 4;
+  const size_t lbase = ((size_t)rtile * a.nb + blockIdx.x) * kMqQ;
+
+  auto step = [&](const MqRows<D, BIG>& rb, int t) {
+    const uint32_t g = (uint32_t)t * W + gw;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      fs_v4f acc[4];
+      mq_tile_scores<D, BIG>(rb, rt, qa, lane4, htab, acc);
+      const float nr = __shfl(rb.n, 16 * rt + (lane & 15));
+      const uint32_t row = g * 64u + 16u * rt + (uint32_t)(lane & 15);
+      const bool valid = row < n;
+      const float m = inv_s * nr;
+      const float H = valid ? __builtin_fmaf(fabsf(nr), beta, 0x1p-100f) : -INFINITY;
+      bool any = false;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) any |= !(__builtin_fmaf(acc[mt][r], m, H) < th[mt][r]);
+      if (__ballot(any) == 0) continue;
+      // a row reaches some query's tau (NaN bounds reach every tau): list it there
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float hi = __builtin_fmaf(acc[mt][r], m, H);
+          const bool p = !(hi < th[mt][r]) & valid & ((qv >> (4 * mt + r)) & 1u);
+          if (__ballot(p) == 0) continue;
+          if (p) {
+            const int ql = 16 * mt + 4 * (lane >> 4) + r;
+            const int slot = atomicAdd(&cnt_s[ql], 1);
+            if (slot < kMqCap) {
+              const size_t e = (lbase + ql) * kMqCap + slot;
+              a.chi[e] = hi;
+              a.clo[e] = __builtin_fmaf(acc[mt][r], m, -H);
+              a.cid[e] = (int)row;
+            }
+          }
+        }
+    }
+  };
+  for (int t = 0; t < nsteps; t += 2) {
+    step(ta, t);
+    ta.load(a, (uint32_t)(t + 2) * W + gw, ngroups, rows_all, norms_all, lane, 1);
+    if (t + 1 >= nsteps) break;
+    step(tb, t + 1);
+    tb.load(a, (uint32_t)(t + 3) * W + gw, ngroups, rows_all, norms_all, lane, 1);
+  }
+  __syncthreads();
+  if (tid < kMqQ) a.cnt[lbase + tid] = cnt_s[tid];
+}
+
+// Per query: the listed rows of every block, tau' = their k-th best lo, the rows whose hi
+// reaches it rescored exactly and ranked.  More than kMqCap rows listed by one block, or
+// more than kMqMergeCap in all, flags the query for the exact fallback instead.
+template <int D>
+__global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
+  __shared__ __attribute__((aligned(16))) float ehi[kMqMergeCap];
+  __shared__ __attribute__((aligned(16))) float elo[kMqMergeCap];
+  __shared__ __attribute__((aligned(16))) int eid[kMqMergeCap];
+  __shared__ int off_s[kMqThreads + 1];
+  __shared__ int part[kMqWaves];
+  __shared__ int bad_s, m2_s, nvalid_s, tot_s;
+  __shared__ float qr_s[D];
+  __shared__ float cen_s[16];
+  const int ql = blockIdx.x % kMqQ, rtile = blockIdx.x / kMqQ;
+  const int q = (a.tile0 + rtile) * kMqQ + ql;
+  if (q >= a.nq) return;  // uniform
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nb = a.nb, k = a.k;
+  // listed counts per block and their prefix sums (nb <= kMqThreads)
+  int c = 0;
+  if (tid < nb) c = a.cnt[((size_t)rtile * nb + tid) * kMqQ + ql];
+  if (tid == 0) bad_s = 0;
+  __syncthreads();
+  if (c > kMqCap) bad_s = 1;
+  int incl = c;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) part[wave] = incl;
+  __syncthreads();
+  int wofs = 0;
+  for (int w = 0; w < wave; ++w) wofs += part[w];
+  off_s[tid] = wofs + incl - c;
+  if (tid == kMqThreads - 1) off_s[kMqThreads] = wofs + incl;
+  __syncthreads();
+  const int M = off_s[kMqThreads];
+  if (bad_s || M > kMqMergeCap) {
+    if (tid == 0) a.flag[q] = 1;
+    return;  // uniform
+  }
+  if (tid == 0) a.flag[q] = 0;
+  // gather the lists
+  for (int e = tid; e < nb * kMqCap; e += kMqThreads) {
+    const int b = e / kMqCap, j = e % kMqCap;
+    const int cb = off_s[b + 1] - off_s[b];
+    if (j < cb) {
+      const size_t src = (((size_t)rtile * nb + b) * kMqQ + ql) * kMqCap + j;
+      const int dst = off_s[b] + j;
+      const float lo = a.clo[src];
+      ehi[dst] = a.chi[src];
+      elo[dst] = lo == lo ? lo : -INFINITY;
+      eid[dst] = a.cid[src];
+    }
+  }
+  if (tid < D) qr_s[tid] = a.qrot[(size_t)q * D + tid];
+  if (tid < 16) cen_s[tid] = a.cen[tid];
+  __syncthreads();
+  // tau' = max(tau, k-th best lo): a 32-step binary search on keys, 12 entries per thread
+  constexpr int EPT = (kMqMergeCap + kMqThreads - 1) / kMqThreads;
+  uint32_t u[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = j * kMqThreads + tid;
+    u[j] = (e < M && elo[e] > -INFINITY) ? fs_fkey(elo[e]) : 0u;
+  }
+  uint32_t x = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t t = x | (1u << bit);
+    int cc = 0;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) cc += (u[j] >= t);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) cc += __shfl_xor(cc, off);
+    if (lane == 0) part[wave] = cc;
+    __syncthreads();
+    if (tid == 0) {
+      int s = 0;
+#pragma unroll
+      for (int w = 0; w < kMqWaves; ++w) s += part[w];
+      tot_s = s;
+    }
+    __syncthreads();
+    if (tot_s >= k) x = t;
+    __syncthreads();
+  }
+  const float tk = x ? fs_unkey(x) : -INFINITY;
+  const float tau2 = fmaxf(a.tau[q], tk);
+  // survivors: entries whose hi reaches tau'; their ids move to the front of eid (every
+  // entry is read before any is overwritten; order does not matter, the ranking orders them)
+  if (tid == 0) { m2_s = 0; nvalid_s = 0; }
+  int my[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = j * kMqThreads + tid;
+    my[j] = (e < M && !(ehi[e] < tau2)) ? eid[e] : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < EPT; ++j)
+    if (my[j] >= 0) eid[atomicAdd(&m2_s, 1)] = my[j];
+  __syncthreads();
+  const int m2 = m2_s;
+  // exact rescoring of the survivors: the row's codes and norm from memory
+  constexpr int RB = D / 2;
+  for (int s = tid; s < m2; s += kMqThreads) {
+    const int id = eid[s];
+    const float sc = exact_pair_score<D>(a.rows + (size_t)id * RB, a.norms[id], qr_s, cen_s);
+    const bool ok = !__builtin_isnan(sc);
+    ehi[s] = ok ? sc : -INFINITY;
+    if (!ok) eid[s] = INT_MAX;  // ranks below every listed row
+    else atomicAdd(&nvalid_s, 1);
+  }
+  for (int s = m2 + tid; s < ((m2 + 3) & ~3); s += kMqThreads) { ehi[s] = -INFINITY; eid[s] = INT_MAX; }
+  int* rk = reinterpret_cast<int*>(elo);
+  for (int s = tid; s < m2; s += kMqThreads) rk[s] = 0;
+  __syncthreads();
+  block_rank<kMqThreads>(ehi, eid, m2, rk, tid);
+  __syncthreads();
+  float* os = a.out_s + (size_t)q * k;
+  int64_t* oi = a.out_i + (size_t)q * k;
+  for (int s = tid; s < m2; s += kMqThreads) {
+    const int id = eid[s], rank = rk[s];
+    if ((id != INT_MAX) & (rank < k)) { os[rank] = ehi[s]; oi[rank] = id; }
+  }
+  for (int e = nvalid_s + tid; e < k; e += kMqThreads) { os[e] = -INFINITY; oi[e] = -1; }
+}
+
 // ------------------------------------------------------------------ softmax stats
 // stats[q] = (max_t s, sum_t exp(s - max)) over the valid tokens of query q's stream.
 __global__ __launch_bounds__(kThreads) void softmax_stats_kernel(const float* __restrict__ scores,
@@ -2588,6 +3190,133 @@ int launch_filter(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, 
                   : launch_filter_d<64>(f, nb, (int)nq, big, st);
 }
 
+// ------------------------------------------------------------------ multi-query filtered scan: host
+// Workspace layout of the multi-query filtered pair scan.  Per call: rotated queries, A
+// operands, tile parameters, tau and flags for every query; per round of at most
+// kMqTilesPerRound tiles (reused round after round): bucket maxima, listed rows and the
+// exact fallback's block lists.
+struct MqLayout {
+  int ntiles, tiles_round, nbk, nsgroups, sstride, nb, fbx;
+  size_t qrot, qa, tparam, tau, flag, buckets, cnt, chi, clo, cid, fps, fpi, total;
+};
+
+MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
+  MqLayout L{};
+  const int KT = d / 32;
+  L.ntiles = (int)((nq + kMqQ - 1) / kMqQ);
+  L.tiles_round = L.ntiles < kMqTilesPerRound ? L.ntiles : kMqTilesPerRound;
+  const int64_t ngroups = (N + 63) / 64;
+  L.nsgroups = (int)(ngroups < kMqSampleGroups ? ngroups : kMqSampleGroups);
+  if (L.nsgroups < 1) L.nsgroups = 1;
+  L.sstride = (int)(ngroups / L.nsgroups);
+  if (L.sstride < 1) L.sstride = 1;
+  const int sblocks = (L.nsgroups + kMqWaves * kMqGroupsPerWave - 1) / (kMqWaves * kMqGroupsPerWave);
+  L.nbk = sblocks * kMqWaves * 16;
+  L.nb = filter_blocks(N);
+  L.fbx = scan_blocks(N) < kMqFallbackBlocks ? scan_blocks(N) : kMqFallbackBlocks;
+  const size_t rq = (size_t)L.tiles_round * kMqQ;
+  size_t o = 256;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes, 256); return at; };
+  L.qrot = take((size_t)nq * d * 4);
+  L.qa = take((size_t)L.ntiles * KT * 4 * 64 * 16);
+  L.tparam = take((size_t)L.ntiles * 2 * 4);
+  L.tau = take((size_t)nq * 4);
+  L.flag = take((size_t)nq * 4);
+  L.buckets = take(rq * L.nbk * 4);
+  L.cnt = take((size_t)L.tiles_round * L.nb * kMqQ * 4);
+  const size_t slots = (size_t)L.tiles_round * L.nb * kMqQ * kMqCap;
+  L.chi = take(slots * 4);
+  L.clo = take(slots * 4);
+  L.cid = take(slots * 4);
+  L.fps = take(rq * L.fbx * k * 4);
+  L.fpi = take(rq * L.fbx * k * 4);
+  L.total = o;
+  return L;
+}
+
+// The multi-query filter applies to 4-bit pair rows of d 64 / 128 with at least two queries.
+bool mq_applies(int64_t nq, int d, int64_t N) {
+  return nq >= 2 && N > 0 && (d == 64 || d == 128);
+}
+
+template <int D>
+int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size_t qbytes,
+                char* ws, bool big, hipStream_t st) {
+  hipLaunchKernelGGL((mq_prep_kernel<D>), dim3((unsigned)L.ntiles), dim3(256), 0, st, base);
+  TQ_LAUNCH_CHECK("mq_prep_kernel");
+  const int sblocks = L.nbk / (kMqWaves * 16);
+  for (int t0 = 0; t0 < L.ntiles; t0 += L.tiles_round) {
+    MqArgs a = base;
+    a.tile0 = t0;
+    const int nt = L.ntiles - t0 < L.tiles_round ? L.ntiles - t0 : L.tiles_round;
+    const dim3 sg((unsigned)sblocks, (unsigned)nt), fg((unsigned)L.nb, (unsigned)nt);
+    if (big) {
+      hipLaunchKernelGGL((mq_sample_kernel<D, true>), sg, dim3(kMqThreads), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((mq_sample_kernel<D, false>), sg, dim3(kMqThreads), 0, st, a);
+    }
+    TQ_LAUNCH_CHECK("mq_sample_kernel");
+    hipLaunchKernelGGL(mq_select_kernel, dim3((unsigned)(nt * kMqQ)), dim3(kMqSelThreads), 0, st, a);
+    TQ_LAUNCH_CHECK("mq_select_kernel");
+    if (big) {
+      hipLaunchKernelGGL((mq_filter_kernel<D, true>), fg, dim3(kMqThreads), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((mq_filter_kernel<D, false>), fg, dim3(kMqThreads), 0, st, a);
+    }
+    TQ_LAUNCH_CHECK("mq_filter_kernel");
+    hipLaunchKernelGGL((mq_merge_kernel<D>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
+    TQ_LAUNCH_CHECK("mq_merge_kernel");
+    // The exact scan for the round's flagged queries (blocks of unflagged ones return).
+    const int q0 = t0 * kMqQ;
+    const int rq = (int)(a.nq - q0 < nt * kMqQ ? a.nq - q0 : nt * kMqQ);
+    ScanArgs s{};
+    s.packed = a.rows; s.norms = a.norms; s.stream_rows = a.n; s.nrows = a.n; s.seq_lens = nullptr;
+    s.spb = 1; s.bpp = D / 8; s.q = static_cast<const char*>(queries) + (size_t)q0 * qbytes;
+    s.q_dt = a.q_dt; s.d = D; s.rot = a.rot; s.cen = a.cen; s.qps = rq; s.post_scale = 1.f;
+    s.k = a.k;
+    s.part_s = reinterpret_cast<float*>(ws + L.fps);
+    s.part_i = reinterpret_cast<int32_t*>(ws + L.fpi);
+    s.scores = nullptr;
+    s.out_s = a.out_s + (size_t)q0 * a.k;
+    s.out_i = a.out_i + (size_t)q0 * a.k;
+    s.qflag = a.flag + q0;
+    const dim3 xg((unsigned)L.fbx, (unsigned)((rq + 3) / 4), 1u);
+    const int rc = launch_scan_pairs<true>(s, 4, xg, st);
+    if (rc != TQ_OK) return rc;
+    hipLaunchKernelGGL(merge_kernel, dim3((unsigned)rq), dim3(kThreads), 0, st, s.part_s, s.part_i,
+                       L.fbx, a.k, s.out_s, s.out_i, (const int32_t*)s.qflag);
+    TQ_LAUNCH_CHECK("merge_kernel");
+  }
+  return TQ_OK;
+}
+
+int launch_mq(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, const uint8_t* pairs,
+              const float* norms, int64_t N, const float* centroids, const float* rotation,
+              int32_t k, float* out_scores, int64_t* out_ids, char* ws, hipStream_t st) {
+  const MqLayout L = mq_layout(nq, d, N, k);
+  TQ_REQUIRE(L.nb <= kMqThreads, "too many filter blocks");
+  MqArgs a{};
+  a.rows = pairs; a.norms = norms; a.n = N; a.q = queries; a.q_dt = q_dtype; a.nq = (int)nq;
+  a.rot = rotation; a.cen = centroids; a.k = k;
+  a.qrot = reinterpret_cast<float*>(ws + L.qrot);
+  a.qa = reinterpret_cast<uint32_t*>(ws + L.qa);
+  a.tparam = reinterpret_cast<float*>(ws + L.tparam);
+  a.tau = reinterpret_cast<float*>(ws + L.tau);
+  a.flag = reinterpret_cast<int*>(ws + L.flag);
+  a.buckets = reinterpret_cast<float*>(ws + L.buckets);
+  a.cnt = reinterpret_cast<int*>(ws + L.cnt);
+  a.chi = reinterpret_cast<float*>(ws + L.chi);
+  a.clo = reinterpret_cast<float*>(ws + L.clo);
+  a.cid = reinterpret_cast<int*>(ws + L.cid);
+  a.nbk = L.nbk; a.sstride = L.sstride; a.nsgroups = L.nsgroups; a.nb = L.nb;
+  a.out_s = out_scores; a.out_i = out_ids;
+  const size_t qbytes = (size_t)d * dtype_size(q_dtype);
+  // 32-bit offsets while rows and norms stay under 2^32 bytes
+  const bool big = N * (d / 2) >= ((int64_t)1 << 32) - 4096 || N * 4 >= ((int64_t)1 << 32) - 4096;
+  return d == 128 ? launch_mq_d<128>(a, L, queries, qbytes, ws, big, st)
+                  : launch_mq_d<64>(a, L, queries, qbytes, ws, big, st);
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -2605,6 +3334,15 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
       const size_t fb = 256 + filter_workspace_bytes(nq, d, N, k);
       if (fb > bytes) bytes = fb;
     }
+  }
+  return bytes;
+}
+
+size_t tq_scan_pairs_workspace_bytes(int64_t nq, int32_t d, int64_t N, int32_t k) {
+  size_t bytes = tq_scan_workspace_bytes(nq, d, 4, N, k);
+  if (k >= 1 && k <= kMaxK && mq_applies(nq, d, N)) {
+    const size_t mq = mq_layout(nq, d, N, k).total;
+    if (mq > bytes) bytes = mq;
   }
   return bytes;
 }
@@ -2645,6 +3383,13 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, N, k);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t st = as_stream(stream);
+  // Several queries over 4-bit pair rows: the multi-query filtered scan, when the
+  // workspace holds its buffers (tq_scan_pairs_workspace_bytes); the exact multi-query
+  // scan below otherwise.
+  if (pairs && bit_width == 4 && !prod && mq_applies(nq, d, N) && nq <= INT_MAX &&
+      workspace_bytes >= mq_layout(nq, d, N, k).total)
+    return launch_mq(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
+                     out_scores, out_ids, static_cast<char*>(workspace), st);
   char* ws = static_cast<char*>(workspace) + 256;
   // The lists are laid out for scan_blocks(N) blocks; a launch uses at most that many.
   const int nb_max = scan_blocks(N);
@@ -2669,7 +3414,7 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   const int rc = launch_scan(a, prod ? bit_width - 1 : bit_width, true, 1, st, pairs, &nb);
   if (rc != TQ_OK) return rc;
   hipLaunchKernelGGL(merge_kernel, dim3((unsigned)nq), dim3(kThreads), 0, st, ps, pi, nb, k,
-                     out_scores, out_ids);
+                     out_scores, out_ids, (const int32_t*)nullptr);
   TQ_LAUNCH_CHECK("merge_kernel");
   return TQ_OK;
 }
