@@ -136,18 +136,30 @@ def bench_scan(args, extra):
                                     "note": "same scan over the reference's bit-plane rows"}
     log(f"scan b=4 Q=1 (bit-plane rows): {t * 1e3:.1f} us/query, {bytes_alg / t / 1e6:.0f} GB/s")
     fn = lambda: ops.ip_scan_topk_pairs(q1, pairs, norms, cen, R, k)
-    ms = time_op(fn, args.steps, args.warmup, settle_s=0.3)
-    res["headline"] = (ms, bytes_alg)
-    log(f"scan b=4 Q=1 (pair layout): {ms * 1e3:.1f} us/query, {bytes_alg / ms / 1e6:.0f} GB/s")
+    if not getattr(args, "batch_only", False):
+        ms = time_op(fn, args.steps, args.warmup, settle_s=0.3)
+        res["headline"] = (ms, bytes_alg)
+        log(f"scan b=4 Q=1 (pair layout): {ms * 1e3:.1f} us/query, {bytes_alg / ms / 1e6:.0f} GB/s")
     if not args.quick:
-        for Q, steps in ((64, 3), (1024, 1)):
+        for Q, steps in ((64, 20), (1024, 5)):
             qq = queries(Q, d, seed=2)
-            t = time_op(lambda: ops.ip_scan_topk_pairs(qq, pairs, norms, cen, R, k), steps, 1)
-            extra[f"scan_b4_Q{Q}"] = {"ms_per_batch": t, "queries_per_s": Q / t * 1e3}
-            log(f"scan b=4 Q={Q}: {t:.2f} ms/batch, {Q / t * 1e3:.0f} q/s")
+            t = time_op(lambda: ops.ip_scan_topk_pairs(qq, pairs, norms, cen, R, k), steps, 2,
+                        settle_s=0.1)
+            # the multi-query filtered scan: one pass over the rows per 64-query tile, 2 d
+            # flops per (query, row) of fp16 MFMA work in its filter
+            tiles = (Q + 63) // 64
+            flop = tiles * 64 * N * d * 2.0
+            extra[f"scan_b4_Q{Q}"] = {
+                "ms_per_batch": t, "queries_per_s": Q / t * 1e3,
+                "row_passes": tiles, "GBps_rows_read": tiles * N * (4 * 16 + 4) / t / 1e6,
+                "filter_TFLOPs": flop / t / 1e9, "fp16_dense_peak_frac": flop / t / 1e9 / 2500.0,
+                "kernels": "mq_prep + mq_sample + mq_select + mq_filter + mq_merge (+ exact scan "
+                           "for flagged queries: none here)"}
+            log(f"scan b=4 Q={Q}: {t:.3f} ms/batch, {Q / t * 1e3:.0f} q/s, filter "
+                f"{flop / t / 1e9:.0f} TFLOP/s, rows read at {tiles * N * 68 / t / 1e6:.0f} GB/s")
     # bit-plane rows (the CPU reference's input) and the pair rows the headline op reads
     res["db4"] = (packed, norms, R, cen, pairs)
-    if not args.quick:
+    if not args.quick and not getattr(args, "batch_only", False):
         for bits in (3, 2):
             # TurboQuantIndex keeps 2/3-bit d=128 rows as pair rows (same bytes per row):
             # one table read of two precomputed products per pair of dims
@@ -737,6 +749,8 @@ def main():
                     help="only the end-to-end greedy decode (configs[4])")
     ap.add_argument("--scan-only", action="store_true",
                     help="only the index scans (configs[1]: 4-, 3- and 2-bit), e.g. for a profiler run")
+    ap.add_argument("--batch-only", action="store_true",
+                    help="only the 4-bit Q=64 / Q=1024 query batches of configs[1], e.g. for a profiler run")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 4096-token paged prefill, e.g. for a profiler run")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -774,6 +788,11 @@ def main():
     if args.e2e_only:
         extra = {}
         bench_e2e(args, extra)
+        print(json.dumps(extra))
+        return
+    if args.batch_only:
+        extra = {}
+        bench_scan(args, extra)
         print(json.dumps(extra))
         return
     if args.scan_only:

@@ -505,6 +505,9 @@ struct DlArgs {
   const float* vnorms;
   int64_t t_cap;
   const int32_t* seq_lens;
+  // optional [B]: tokens before seq_starts[b] are masked (left-padded batches); the
+  // tiles holding them are still read
+  const int32_t* seq_starts;
   const float* kcen;  // 16
   const float* vcen;  // 2^VB
   const float* krot;
@@ -642,6 +645,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // until the prologue's loads (query, R_k, the first tiles) are all in flight: their
   // latency and its own then overlap instead of following one another.
   const int32_t slen = a.seq_lens[b];
+  const int32_t sstart = a.seq_starts ? a.seq_starts[b] : 0;
   const int64_t t_begin = (int64_t)split * a.split_tokens;
   const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.Gfull + a.hofs;
   const int tid = threadIdx.x;
@@ -819,6 +823,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     return;
   }
   const int te = (int)t_end;
+  const int ts = (int)min((int64_t)max(sstart, 0), T);  // first unmasked token
   const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
   if (tid < 32) cen_s[tid] = cenv;
   if (tid < 4 * kDim) {
@@ -1052,9 +1057,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     // copy of the norms merged from a branch was miscompiled -- registers of the live
     // norms reused before their last read).
     const int nvalid = te - (t0 + 16 * gq + 4 * sl);
+    const int nlow = ts - (t0 + 16 * gq + 4 * sl);  // registers below it are masked
     float s[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = r < nvalid ? skk[r] * cur.kn[r] : -INFINITY;
+    for (int r = 0; r < 4; ++r) s[r] = (r < nvalid) & (r >= nlow) ? skk[r] * cur.kn[r] : -INFINITY;
     const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     if (__any(lm > M)) {
       float m2 = lm;
@@ -1076,7 +1082,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     for (int r = 0; r < 4; ++r) {
       const float p = __builtin_amdgcn_exp2f(s[r] - M);
       psum += p;
-      const float w = r < nvalid ? p * cur.vn[r] : 0.f;
+      const float w = (r < nvalid) & (r >= nlow) ? p * cur.vn[r] : 0.f;
       wh[r] = (_Float16)w;
       if constexpr (EXACT_V) wl[r] = (_Float16)(w - (float)wh[r]);
     }
@@ -1647,14 +1653,15 @@ size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t 
   return 256 + align_up(rows * p.nsplit * kDim * 4, 256) + align_up(rows * p.nsplit * 8, 256);
 }
 
-int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
-                           int32_t d, const uint8_t* kpairs, const float* knorms,
-                           const uint8_t* vblocks, const float* vnorms, int64_t t_cap,
-                           const int32_t* seq_lens, const float* kcentroids,
-                           const float* vcentroids, const float* krotation,
-                           const float* vrotation, int32_t kbits, int32_t vbits, float scale,
-                           void* out, float* lse, void* workspace, size_t workspace_bytes,
-                           void* stream) {
+int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
+                                  int32_t hkv, int32_t d, const uint8_t* kpairs,
+                                  const float* knorms, const uint8_t* vblocks,
+                                  const float* vnorms, int64_t t_cap, const int32_t* seq_lens,
+                                  const int32_t* seq_starts, const float* kcentroids,
+                                  const float* vcentroids, const float* krotation,
+                                  const float* vrotation, int32_t kbits, int32_t vbits,
+                                  float scale, void* out, float* lse, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
   if (d != kDim || kbits != 4 || vbits < 2 || vbits > 4)
     return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-4 bit "
@@ -1678,9 +1685,24 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
   const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
   DlArgs a{};
   a.q = q; a.kpairs = kpairs; a.knorms = knorms; a.vblocks = vblocks; a.vnorms = vnorms;
-  a.t_cap = t_cap; a.seq_lens = seq_lens; a.kcen = kcentroids; a.vcen = vcentroids;
-  a.krot = krotation; a.vrot = vrotation; a.qscale = scale * 1.4426950408889634f;
+  a.t_cap = t_cap; a.seq_lens = seq_lens; a.seq_starts = seq_starts; a.kcen = kcentroids;
+  a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
+  a.qscale = scale * 1.4426950408889634f;
   return run_dl(a, q_dtype, B, hq, hkv, vbits, 0, p, workspace, out, lse, as_stream(stream));
+}
+
+int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
+                           int32_t d, const uint8_t* kpairs, const float* knorms,
+                           const uint8_t* vblocks, const float* vnorms, int64_t t_cap,
+                           const int32_t* seq_lens, const float* kcentroids,
+                           const float* vcentroids, const float* krotation,
+                           const float* vrotation, int32_t kbits, int32_t vbits, float scale,
+                           void* out, float* lse, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return tq_decode_attention_dl_window(q, q_dtype, B, hq, hkv, d, kpairs, knorms, vblocks, vnorms,
+                                       t_cap, seq_lens, nullptr, kcentroids, vcentroids, krotation,
+                                       vrotation, kbits, vbits, scale, out, lse, workspace,
+                                       workspace_bytes, stream);
 }
 
 int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,

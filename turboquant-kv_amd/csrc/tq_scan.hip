@@ -1554,6 +1554,26 @@ __device__ __forceinline__ float exact_pair_score_pipelined(const uint32_t* row,
   return acc * n;
 }
 
+// exact_pair_score for a row held in registers (word w = bytes 4w .. 4w + 3).
+template <int D>
+__device__ __forceinline__ float exact_pair_score_regs(const uint32_t (&rw)[D / 8], float n,
+                                                       const float* qr, const float* cen) {
+#pragma clang fp contract(off)
+  float acc = 0.f;
+#pragma unroll
+  for (int w = 0; w < D / 8; ++w)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int p = 4 * w + b;
+      const uint32_t byte = (rw[w] >> (8 * b)) & 0xFFu;
+      const float p0 = qr[2 * p] * cen[byte >> 4];
+      acc = acc + p0;
+      const float p1 = qr[2 * p + 1] * cen[byte & 15u];
+      acc = acc + p1;
+    }
+  return acc * n;
+}
+
 __device__ __forceinline__ bool fs_keep(float hi, int id, float th, int thi) {
   return (hi > th) | ((hi == th) & (id <= thi));
 }
@@ -2250,17 +2270,16 @@ pair_filter_kernel(FilterArgs a) {
 // fma that adds it (each under 2^-12 of the bound); the absolute 2^-100 covers n / s
 // underflowing in m = n / s (an error below |acc| 2^-150 <= 2^-125).
 // Pipeline (one call):
-//   mq_prep_kernel    per 64-query tile: q_rot with the reference's arithmetic (kept for
-//                     the exact rescoring), the fp16 A operands, 1/s and beta.
-//   mq_sample_kernel  lo = approx - bound of 4096 evenly spaced 64-row groups; each lane
-//                     keeps, per query, the maximum over its 16 rows (a bucket).
-//   mq_select_kernel  per query: tau = the k-th largest bucket maximum.  Buckets are
-//                     disjoint row sets, so k distinct rows score at least tau; a row
+//   mq_rotate_kernel  q_rot with the reference's arithmetic (kept for the exact rescoring).
+//   mq_tile_kernel    per 64-query tile: the fp16 A operands, 1/s and beta.
+//   mq_sample_kernel  lo = approx - bound of 4096 evenly spaced 64-row groups; per query,
+//                     the maximum over each block's 16 groups (a bucket of 1024 rows).
+//   mq_filter_kernel  prologue: per query, tau = the k-th largest bucket maximum.  Buckets
+//                     are disjoint row sets, so k distinct rows score at least tau; a row
 //                     whose upper bound hi = approx + bound is below tau is not in the
-//                     answer.
-//   mq_filter_kernel  every row: hi against tau per (query, row); the rows that reach it
-//                     (a few hundred per query at 10M rows) are listed per (block, query)
-//                     with (hi, lo, id).
+//                     answer.  Then every row: hi against tau per (query, row); the rows
+//                     that reach it (a few hundred per query at 10M rows) are listed per
+//                     (block, query) with (hi, lo, id).
 //   mq_merge_kernel   per query: tau' = the k-th best lo of the list, the entries whose hi
 //                     reaches it are rescored exactly (rows re-read from memory) and
 //                     ranked; the answer is the exact scan's, ties included.  A list that
@@ -2272,15 +2291,12 @@ constexpr int kMqThreads = 512;          // 8 waves; one block per CU
 constexpr int kMqWaves = kMqThreads / 64;
 constexpr int kMqCap = 64;               // listed rows per (block, query)
 constexpr int kMqSampleGroups = 4096;    // 64-row groups sampled for tau
-constexpr int kMqGroupsPerWave = 4;      // sampled groups per wave (16 rows per bucket)
-constexpr int kMqSelVals = 64;           // bucket maxima per thread in mq_select_kernel
-constexpr int kMqSelThreads = 256;
-constexpr int kMqMaxBuckets = kMqSelVals * kMqSelThreads;
+constexpr int kMqGroupsPerWave = 2;      // sampled groups per wave (one bucket per wave)
+constexpr int kMqMaxBuckets = 256;       // bucket maxima per query (one per sample block)
 constexpr int kMqMergeCap = 6144;        // listed entries a query's merge holds in LDS
 constexpr int kMqTilesPerRound = 8;      // query tiles per filter launch
 constexpr int kMqFallbackBlocks = 128;   // row blocks of the exact fallback scan
-static_assert((kMqSampleGroups / (kMqWaves * kMqGroupsPerWave)) * kMqWaves * 16 <= kMqMaxBuckets,
-              "bucket count");
+static_assert(kMqSampleGroups / (kMqWaves * kMqGroupsPerWave) <= kMqMaxBuckets, "bucket count");
 
 struct MqArgs {
   const uint8_t* rows;  // [n][D / 2] pair layout
@@ -2353,6 +2369,15 @@ struct MqRows {
   }
 };
 
+// Maximum over each 16-lane row of the wave (DPP: quad swaps, then half-row and row mirrors).
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 // The 64 KB fp16 centroid-pair table (entry (byte << 8) | lane * 4: (c[byte >> 4],
 // c[byte & 15]) in 64 lane copies), as pair_filter_kernel builds it.
 __device__ __forceinline__ void mq_fill_htab(char* htab, const float* cen_s, int tid, int nthreads) {
@@ -2364,77 +2389,117 @@ __device__ __forceinline__ void mq_fill_htab(char* htab, const float* cen_s, int
   }
 }
 
-// Approximate scores (in units of the scaled query) of 16 rows x 64 queries: N tile rt of
-// the group in `rb`.  acc[mt][r] = query 16 mt + 4 (lane >> 4) + r, row 16 rt + (lane & 15).
+// B operands of N tile rt of the group in `rb`: per k tile, the fp16 centroid pairs of the
+// lane's four code bytes (one LDS lookup each).
 template <int D, bool BIG>
-__device__ __forceinline__ void mq_tile_scores(const MqRows<D, BIG>& rb, int rt, const fs_v8h (&qa)[4][D / 32],
-                                               uint32_t lane4, const char* htab, fs_v4f (&acc)[4]) {
+__device__ __forceinline__ void mq_fetch_b(const MqRows<D, BIG>& rb, int rt, uint32_t lane4,
+                                           const char* htab, u32x4 (&bw)[D / 32]) {
   constexpr int KT = D / 32, LW = D / 32;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const uint32_t x = rb.w[LW * rt + kt];
+    bw[kt] = (u32x4){fs_hlook<0>(x, lane4, htab), fs_hlook<1>(x, lane4, htab),
+                     fs_hlook<2>(x, lane4, htab), fs_hlook<3>(x, lane4, htab)};
+  }
+}
+
+// Approximate scores (in units of the scaled query) of 16 rows x 64 queries from one N
+// tile's B operands: acc[mt][r] = query 16 mt + 4 (lane >> 4) + r, row 16 rt + (lane & 15).
+template <int D>
+__device__ __forceinline__ void mq_mfma(const u32x4 (&bw)[D / 32], const fs_v8h (&qa)[4][D / 32],
+                                        fs_v4f (&acc)[4]) {
+  constexpr int KT = D / 32;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) acc[mt] = (fs_v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
-    const uint32_t x = rb.w[LW * rt + kt];
-    const u32x4 bw = {fs_hlook<0>(x, lane4, htab), fs_hlook<1>(x, lane4, htab),
-                      fs_hlook<2>(x, lane4, htab), fs_hlook<3>(x, lane4, htab)};
-    const fs_v8h b = __builtin_bit_cast(fs_v8h, bw);
+    const fs_v8h b = __builtin_bit_cast(fs_v8h, bw[kt]);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[mt][kt], b, acc[mt], 0, 0, 0);
   }
 }
 
-// Per 64-query tile: q_rot (reference arithmetic: q_rot[j] = sum over i in order of
-// q[i] * R[j][i], each product rounded), the scale, beta and the fp16 A operands.
+template <int D, bool BIG>
+__device__ __forceinline__ void mq_tile_scores(const MqRows<D, BIG>& rb, int rt, const fs_v8h (&qa)[4][D / 32],
+                                               uint32_t lane4, const char* htab, fs_v4f (&acc)[4]) {
+  u32x4 bw[D / 32];
+  mq_fetch_b<D, BIG>(rb, rt, lane4, htab, bw);
+  mq_mfma<D>(bw, qa, acc);
+}
+
+// q_rot of four queries per block (reference arithmetic: q_rot[j] = sum over i in order
+// of q[i] * R[j][i], each product rounded; csrc/core/turboquant_core.cpp:429-437).
+// Thread j holds row j of R; the queries are read from LDS as 16-byte broadcasts.
+constexpr int kMqRotQ = 4;
 template <int D>
-__global__ __launch_bounds__(256) void mq_prep_kernel(MqArgs a) {
+__global__ __launch_bounds__(D) void mq_rotate_kernel(MqArgs a) {
 #pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float qs[kMqRotQ][D];
+  const int j = threadIdx.x;
+  const int q0 = blockIdx.x * kMqRotQ;
+  const int nv = min(kMqRotQ, a.nq - q0);
+  float4 rrow[D / 4];
+  const float4* r4 = reinterpret_cast<const float4*>(a.rot + (size_t)j * D);
+#pragma unroll
+  for (int i = 0; i < D / 4; ++i) rrow[i] = r4[i];
+#pragma unroll
+  for (int qi = 0; qi < kMqRotQ; ++qi)
+    qs[qi][j] = qi < nv ? load_as_f32(a.q, (int64_t)(q0 + qi) * D + j, a.q_dt) : 0.f;
+  __syncthreads();
+  float v[kMqRotQ];
+#pragma unroll
+  for (int qi = 0; qi < kMqRotQ; ++qi) v[qi] = 0.f;
+#pragma unroll
+  for (int i = 0; i < D / 4; ++i) {
+#pragma unroll
+    for (int qi = 0; qi < kMqRotQ; ++qi) {
+      const float4 x = *reinterpret_cast<const float4*>(&qs[qi][4 * i]);
+      v[qi] = v[qi] + x.x * rrow[i].x;
+      v[qi] = v[qi] + x.y * rrow[i].y;
+      v[qi] = v[qi] + x.z * rrow[i].z;
+      v[qi] = v[qi] + x.w * rrow[i].w;
+    }
+  }
+#pragma unroll
+  for (int qi = 0; qi < kMqRotQ; ++qi)
+    if (qi < nv) a.qrot[(size_t)(q0 + qi) * D + j] = v[qi];
+}
+
+// Per 64-query tile: the scale, beta and the fp16 A operands from the rotated queries.
+template <int D>
+__global__ __launch_bounds__(kMqThreads) void mq_tile_kernel(MqArgs a) {
   constexpr int KT = D / 32;
-  __shared__ float qs[kMqQ][D + 1];
   __shared__ float qr[kMqQ][D + 1];
   __shared__ float red[2][kMqQ];
   __shared__ float cen_s[16];
-  const int tile = blockIdx.x, tid = threadIdx.x;
+  const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const int q0 = tile * kMqQ;
   const int nvalid = min(kMqQ, a.nq - q0);
-  for (int e = tid; e < kMqQ * D; e += 256) {
+  for (int e = tid; e < kMqQ * D; e += kMqThreads) {
     const int qi = e / D, j = e % D;
-    qs[qi][j] = qi < nvalid ? load_as_f32(a.q, (int64_t)(q0 + qi) * D + j, a.q_dt) : 0.f;
+    qr[qi][j] = qi < nvalid ? a.qrot[(size_t)(q0 + qi) * D + j] : 0.f;
   }
   if (tid < 16) cen_s[tid] = a.cen[tid];
   __syncthreads();
-  {
-    const int j = tid % D, qg = tid / D;
-    constexpr int QSTEP = 256 / D;
-    float4 rrow[D / 4];
-    const float4* r4 = reinterpret_cast<const float4*>(a.rot + (size_t)j * D);
-#pragma unroll
-    for (int i = 0; i < D / 4; ++i) rrow[i] = r4[i];
-    for (int qi = qg; qi < kMqQ; qi += QSTEP) {
-      float v = 0.f;
-#pragma unroll
-      for (int i = 0; i < D / 4; ++i) {
-        v = v + qs[qi][4 * i] * rrow[i].x;
-        v = v + qs[qi][4 * i + 1] * rrow[i].y;
-        v = v + qs[qi][4 * i + 2] * rrow[i].z;
-        v = v + qs[qi][4 * i + 3] * rrow[i].w;
-      }
-      qr[qi][j] = v;
-      if (qi < nvalid) a.qrot[(size_t)(q0 + qi) * D + j] = v;
-    }
-  }
-  __syncthreads();
-  if (tid < kMqQ) {
+  {  // max |q_rot| and ||q_rot||_1 per query: 8 threads per query
+    const int qi = tid >> 3, part = tid & 7;
     float am = 0.f, l1 = 0.f;
-    for (int j = 0; j < D; ++j) {
-      const float x = fabsf(qr[tid][j]);
+    for (int j = part; j < D; j += 8) {
+      const float x = fabsf(qr[qi][j]);
       am = fmaxf(am, x);
       l1 = l1 + x;
     }
-    const bool v = tid < nvalid;
-    red[0][tid] = v ? am : 0.f;
-    red[1][tid] = v ? l1 : 0.f;
-    // a NaN anywhere in a valid query turns the filter off for the tile
-    if (v && !(l1 < INFINITY)) red[1][tid] = INFINITY;
+#pragma unroll
+    for (int off = 4; off >= 1; off >>= 1) {
+      am = fmaxf(am, __shfl_xor(am, off));
+      l1 = l1 + __shfl_xor(l1, off);
+    }
+    if (part == 0) {
+      const bool v = qi < nvalid;
+      red[0][qi] = v ? am : 0.f;
+      // a NaN anywhere in a valid query turns the filter off for the tile
+      red[1][qi] = v ? (l1 < INFINITY ? l1 : INFINITY) : 0.f;
+    }
   }
   __syncthreads();
   float amax = 0.f, l1 = 0.f;
@@ -2463,9 +2528,9 @@ __global__ __launch_bounds__(256) void mq_prep_kernel(MqArgs a) {
   }
   // A operand of (kt, mt), lane (m, g): query 16 mt + m, dims (D == 128 ? 32 : 16) g + 8 kt + e
   typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-  for (int it = tid; it < KT * 4 * 64; it += 256) {
-    const int lane = it & 63, mt = (it >> 6) & 3, kt = it >> 8;
-    const int qi = 16 * mt + (lane & 15), g = lane >> 4;
+  for (int it = tid; it < KT * 4 * 64; it += kMqThreads) {
+    const int l = it & 63, mt = (it >> 6) & 3, kt = it >> 8;
+    const int qi = 16 * mt + (l & 15), g = l >> 4;
     const int dim0 = (D == 128 ? 32 : 16) * g + 8 * kt;
     uint32_t wv[4];
 #pragma unroll
@@ -2474,9 +2539,10 @@ __global__ __launch_bounds__(256) void mq_prep_kernel(MqArgs a) {
       const _Float16 h1 = (_Float16)(qr[qi][dim0 + 2 * w + 1] * scale);
       wv[w] = __builtin_bit_cast(uint32_t, (h2_t){h0, h1});
     }
-    *reinterpret_cast<u32x4*>(a.qa + (((size_t)tile * KT + kt) * 4 + mt) * 256 + lane * 4) =
+    *reinterpret_cast<u32x4*>(a.qa + (((size_t)tile * KT + kt) * 4 + mt) * 256 + l * 4) =
         (u32x4){wv[0], wv[1], wv[2], wv[3]};
   }
+  (void)lane;
 }
 
 // The tile's A operands, 1/s and beta for this lane.
@@ -2503,6 +2569,7 @@ mq_sample_kernel(MqArgs a) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
   __shared__ float cen_s[16];
+  __shared__ float wmax_s[kMqWaves][kMqQ];
   const int rtile = blockIdx.y, tile = a.tile0 + rtile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2524,13 +2591,20 @@ mq_sample_kernel(MqArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) bmax[mt][r] = -INFINITY;
   const int sw = blockIdx.x * kMqWaves + wave;
-#pragma unroll 1
+  // every group's loads first (a sampled group past nsgroups reads the empty range past
+  // the last row: zeros, and its rows are not valid)
+  MqRows<D, BIG> rbs[kMqGroupsPerWave];
+  uint32_t gs[kMqGroupsPerWave];
+#pragma unroll
   for (int u = 0; u < kMqGroupsPerWave; ++u) {
     const int s = sw * kMqGroupsPerWave + u;
-    if (s >= a.nsgroups) break;
-    const uint32_t g = (uint32_t)s * (uint32_t)a.sstride;
-    MqRows<D, BIG> rb;
-    rb.load(a, g, ngroups, rows_all, norms_all, lane, 0);
+    gs[u] = s < a.nsgroups ? (uint32_t)s * (uint32_t)a.sstride : ngroups;
+    rbs[u].load(a, gs[u], ngroups, rows_all, norms_all, lane, 0);
+  }
+#pragma unroll
+  for (int u = 0; u < kMqGroupsPerWave; ++u) {
+    const uint32_t g = gs[u];
+    const MqRows<D, BIG>& rb = rbs[u];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       fs_v4f acc[4];
@@ -2545,60 +2619,54 @@ mq_sample_kernel(MqArgs a) {
         for (int r = 0; r < 4; ++r) bmax[mt][r] = fmaxf(bmax[mt][r], __builtin_fmaf(acc[mt][r], m, L));
     }
   }
-  const int bidx = sw * 16 + (lane & 15);
+  // The block's rows make one bucket per query: the maximum over the 16 lanes of the
+  // query's row group, then over the waves.  +inf (an overflowed approximation) hides the
+  // other rows of its lane: no bound from that lane.
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      const float v = row_max16(bmax[mt][r] < INFINITY ? bmax[mt][r] : -INFINITY);
       const int ql = 16 * mt + 4 * (lane >> 4) + r;
-      const float v = bmax[mt][r];
-      // +inf (an overflowed approximation) hides the bucket's other rows: no bound from it
-      a.buckets[(size_t)(rtile * kMqQ + ql) * a.nbk + bidx] = v < INFINITY ? v : -INFINITY;
+      if ((lane & 15) == 0) wmax_s[wave][ql] = v;
     }
+  __syncthreads();
+  if (tid < kMqQ) {
+    float v = wmax_s[0][tid];
+#pragma unroll
+    for (int w = 1; w < kMqWaves; ++w) v = fmaxf(v, wmax_s[w][tid]);
+    a.buckets[(size_t)(rtile * kMqQ + tid) * a.nbk + blockIdx.x] = v;
+  }
 }
 
-// tau[q] = the k-th largest of the query's nbk bucket maxima (-inf when fewer than k are
-// above -inf): a 32-step binary search on order-preserving keys.
-__global__ __launch_bounds__(kMqSelThreads) void mq_select_kernel(MqArgs a) {
-  __shared__ int part[kMqSelThreads / 64];
-  __shared__ int tot;
-  const int ql = blockIdx.x;
-  const int q = a.tile0 * kMqQ + ql;
-  if (q >= a.nq) return;  // uniform
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* src = a.buckets + (size_t)ql * a.nbk;
-  uint32_t u[kMqSelVals];
+// tau of each of the tile's 64 queries (eight threads per query): the k-th largest of its
+// nbk bucket maxima, -inf when fewer than k are above -inf -- a 32-step binary search on
+// order-preserving keys.  Buckets are disjoint row sets, so k distinct rows score at
+// least tau.
+__device__ __forceinline__ void mq_tau(const MqArgs& a, int rtile, int tid, float* tau_s) {
+  constexpr int PER = kMqMaxBuckets / 8;
+  const int ql = tid >> 3, part = tid & 7;
+  const float* src = a.buckets + (size_t)(rtile * kMqQ + ql) * a.nbk;
+  float vals[PER];
 #pragma unroll
-  for (int j = 0; j < kMqSelVals; ++j) {
-    const int e = j * kMqSelThreads + tid;
-    u[j] = 0u;  // below every real key
-    if (e < a.nbk) {
-      const float v = src[e];
-      u[j] = v > -INFINITY ? fs_fkey(v) : 0u;
-    }
-  }
+  for (int j = 0; j < PER; ++j) vals[j] = src[min(8 * j + part, a.nbk - 1)];
+  uint32_t u[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    u[j] = ((8 * j + part < a.nbk) & (vals[j] > -INFINITY)) ? fs_fkey(vals[j]) : 0u;
   uint32_t x = 0;
 #pragma unroll 1
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t t = x | (1u << bit);
     int c = 0;
 #pragma unroll
-    for (int j = 0; j < kMqSelVals; ++j) c += (u[j] >= t);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
-    if (lane == 0) part[wave] = c;
-    __syncthreads();
-    if (tid == 0) {
-      int s = 0;
-#pragma unroll
-      for (int w = 0; w < kMqSelThreads / 64; ++w) s += part[w];
-      tot = s;
-    }
-    __syncthreads();
-    if (tot >= a.k) x = t;
-    __syncthreads();
+    for (int j = 0; j < PER; ++j) c += (u[j] >= t);
+    c += __shfl_xor(c, 1);
+    c += __shfl_xor(c, 2);
+    c += __shfl_xor(c, 4);
+    if (c >= a.k) x = t;
   }
-  if (tid == 0) a.tau[q] = x ? fs_unkey(x) : -INFINITY;
+  if (part == 0) tau_s[ql] = x ? fs_unkey(x) : -INFINITY;
 }
 
 // Every row against tau per query; rows whose upper bound reaches it are listed.
@@ -2609,6 +2677,7 @@ mq_filter_kernel(MqArgs a) {
   __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
   __shared__ float cen_s[16];
   __shared__ int cnt_s[kMqQ];
+  __shared__ float tau_s[kMqQ];
   const int rtile = blockIdx.y, tile = a.tile0 + rtile;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2626,31 +2695,39 @@ mq_filter_kernel(MqArgs a) {
   fs_v8h qa[4][D / 32];
   float inv_s, beta;
   mq_load_tile<D>(a, tile, lane, qa, inv_s, beta);
+  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < kMqQ) cnt_s[tid] = 0;
+  mq_tau(a, rtile, tid, tau_s);
+  __syncthreads();
+  if (blockIdx.x == 0 && tid < kMqQ && tile * kMqQ + tid < a.nq) a.tau[tile * kMqQ + tid] = tau_s[tid];
   float th[4][4];
   uint32_t qv = 0;  // bit 4 mt + r: query 16 mt + 4 (lane >> 4) + r is a real query
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int q = tile * kMqQ + 16 * mt + 4 * (lane >> 4) + r;
-      const bool v = q < a.nq;
-      th[mt][r] = v ? a.tau[q] : INFINITY;
+      const int ql = 16 * mt + 4 * (lane >> 4) + r;
+      const bool v = tile * kMqQ + ql < a.nq;
+      th[mt][r] = v ? tau_s[ql] : INFINITY;
       qv |= (uint32_t)v << (4 * mt + r);
     }
-  if (tid < 16) cen_s[tid] = a.cen[tid];
-  if (tid < kMqQ) cnt_s[tid] = 0;
-  __syncthreads();
   mq_fill_htab(htab, cen_s, tid, kMqThreads);
   __syncthreads();
   const uint32_t lane4 = (uint32_t)lane * 4;
   const size_t lbase = ((size_t)rtile * a.nb + blockIdx.x) * kMqQ;
 
+  // Per row tile: the MFMAs, then hi = acc * m + H of (query 16 mt + 4 (lane >> 4) + r, row
+  // 16 rt + (lane & 15)) against the queries' tau.  The next tile's table lookups are issued
+  // before this tile's tests, so their latency runs under the tests and the branch.
   auto step = [&](const MqRows<D, BIG>& rb, int t) {
     const uint32_t g = (uint32_t)t * W + gw;
+    u32x4 bw[2][D / 32];
+    mq_fetch_b<D, BIG>(rb, 0, lane4, htab, bw[0]);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       fs_v4f acc[4];
-      mq_tile_scores<D, BIG>(rb, rt, qa, lane4, htab, acc);
+      mq_mfma<D>(bw[rt & 1], qa, acc);
+      if (rt < 3) mq_fetch_b<D, BIG>(rb, rt + 1, lane4, htab, bw[(rt + 1) & 1]);
       const float nr = __shfl(rb.n, 16 * rt + (lane & 15));
       const uint32_t row = g * 64u + 16u * rt + (uint32_t)(lane & 15);
       const bool valid = row < n;
@@ -2737,51 +2814,53 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
     return;  // uniform
   }
   if (tid == 0) a.flag[q] = 0;
-  // gather the lists
-  for (int e = tid; e < nb * kMqCap; e += kMqThreads) {
-    const int b = e / kMqCap, j = e % kMqCap;
-    const int cb = off_s[b + 1] - off_s[b];
-    if (j < cb) {
-      const size_t src = (((size_t)rtile * nb + b) * kMqQ + ql) * kMqCap + j;
-      const int dst = off_s[b] + j;
-      const float lo = a.clo[src];
-      ehi[dst] = a.chi[src];
-      elo[dst] = lo == lo ? lo : -INFINITY;
-      eid[dst] = a.cid[src];
+  // gather the lists: entry e of the concatenation is slot e - off_s[b] of block b, found by
+  // a binary search over the prefix sums (every load of the gather in flight at once)
+  for (int e = tid; e < M; e += kMqThreads) {
+    int lo = 0, hi = nb;  // off_s[lo] <= e < off_s[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off_s[mid] <= e) lo = mid; else hi = mid;
     }
+    const size_t src = (((size_t)rtile * nb + lo) * kMqQ + ql) * kMqCap + (e - off_s[lo]);
+    const float l = a.clo[src];
+    ehi[e] = a.chi[src];
+    elo[e] = l == l ? l : -INFINITY;
+    eid[e] = a.cid[src];
   }
   if (tid < D) qr_s[tid] = a.qrot[(size_t)q * D + tid];
   if (tid < 16) cen_s[tid] = a.cen[tid];
   __syncthreads();
-  // tau' = max(tau, k-th best lo): a 32-step binary search on keys, 12 entries per thread
+  // tau' = max(tau, k-th best lo): wave 0 alone, a 32-step binary search on keys (the first
+  // 1024 entries in registers, the rest read from LDS).  Up to one entry per thread every
+  // entry is rescored anyway: no search.
   constexpr int EPT = (kMqMergeCap + kMqThreads - 1) / kMqThreads;
-  uint32_t u[EPT];
+  constexpr int RK = 16;
+  if (tid == 0) tot_s = 0;
+  if (wave == 0 && M > kMqThreads) {
+    uint32_t u[RK];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = j * kMqThreads + tid;
-    u[j] = (e < M && elo[e] > -INFINITY) ? fs_fkey(elo[e]) : 0u;
-  }
-  uint32_t x = 0;
-#pragma unroll 1
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t t = x | (1u << bit);
-    int cc = 0;
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) cc += (u[j] >= t);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) cc += __shfl_xor(cc, off);
-    if (lane == 0) part[wave] = cc;
-    __syncthreads();
-    if (tid == 0) {
-      int s = 0;
-#pragma unroll
-      for (int w = 0; w < kMqWaves; ++w) s += part[w];
-      tot_s = s;
+    for (int j = 0; j < RK; ++j) {
+      const int e = j * 64 + lane;
+      u[j] = (e < M && elo[e] > -INFINITY) ? fs_fkey(elo[e]) : 0u;
     }
-    __syncthreads();
-    if (tot_s >= k) x = t;
-    __syncthreads();
+    uint32_t x = 0;
+#pragma unroll 1
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t t = x | (1u << bit);
+      int cc = 0;  // wave-uniform: popcounts of compare masks
+#pragma unroll
+      for (int j = 0; j < RK; ++j) cc += __popcll(__ballot(u[j] >= t));
+      for (int e0 = RK * 64; e0 < M; e0 += 64) {
+        const int e = e0 + lane;
+        cc += __popcll(__ballot((e < M) && (elo[e] > -INFINITY) && (fs_fkey(elo[e]) >= t)));
+      }
+      if (cc >= k) x = t;
+    }
+    if (lane == 0) tot_s = (int)x;
   }
+  __syncthreads();
+  const uint32_t x = (uint32_t)tot_s;
   const float tk = x ? fs_unkey(x) : -INFINITY;
   const float tau2 = fmaxf(a.tau[q], tk);
   // survivors: entries whose hi reaches tau'; their ids move to the front of eid (every
@@ -2803,7 +2882,16 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   constexpr int RB = D / 2;
   for (int s = tid; s < m2; s += kMqThreads) {
     const int id = eid[s];
-    const float sc = exact_pair_score<D>(a.rows + (size_t)id * RB, a.norms[id], qr_s, cen_s);
+    // the row's bytes and norm requested together, then scored from registers
+    uint32_t rw[D / 8];
+    const u32x4* r4 = reinterpret_cast<const u32x4*>(a.rows + (size_t)id * RB);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const u32x4 v = r4[i];
+      rw[4 * i] = v.x; rw[4 * i + 1] = v.y; rw[4 * i + 2] = v.z; rw[4 * i + 3] = v.w;
+    }
+    const float nrm = a.norms[id];
+    const float sc = exact_pair_score_regs<D>(rw, nrm, qr_s, cen_s);
     const bool ok = !__builtin_isnan(sc);
     ehi[s] = ok ? sc : -INFINITY;
     if (!ok) eid[s] = INT_MAX;  // ranks below every listed row
@@ -3211,7 +3299,7 @@ MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
   L.sstride = (int)(ngroups / L.nsgroups);
   if (L.sstride < 1) L.sstride = 1;
   const int sblocks = (L.nsgroups + kMqWaves * kMqGroupsPerWave - 1) / (kMqWaves * kMqGroupsPerWave);
-  L.nbk = sblocks * kMqWaves * 16;
+  L.nbk = sblocks;
   L.nb = filter_blocks(N);
   L.fbx = scan_blocks(N) < kMqFallbackBlocks ? scan_blocks(N) : kMqFallbackBlocks;
   const size_t rq = (size_t)L.tiles_round * kMqQ;
@@ -3242,9 +3330,12 @@ bool mq_applies(int64_t nq, int d, int64_t N) {
 template <int D>
 int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size_t qbytes,
                 char* ws, bool big, hipStream_t st) {
-  hipLaunchKernelGGL((mq_prep_kernel<D>), dim3((unsigned)L.ntiles), dim3(256), 0, st, base);
-  TQ_LAUNCH_CHECK("mq_prep_kernel");
-  const int sblocks = L.nbk / (kMqWaves * 16);
+  hipLaunchKernelGGL((mq_rotate_kernel<D>), dim3((unsigned)((base.nq + kMqRotQ - 1) / kMqRotQ)),
+                     dim3(D), 0, st, base);
+  TQ_LAUNCH_CHECK("mq_rotate_kernel");
+  hipLaunchKernelGGL((mq_tile_kernel<D>), dim3((unsigned)L.ntiles), dim3(kMqThreads), 0, st, base);
+  TQ_LAUNCH_CHECK("mq_tile_kernel");
+  const int sblocks = L.nbk;
   for (int t0 = 0; t0 < L.ntiles; t0 += L.tiles_round) {
     MqArgs a = base;
     a.tile0 = t0;
@@ -3256,8 +3347,6 @@ int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size
       hipLaunchKernelGGL((mq_sample_kernel<D, false>), sg, dim3(kMqThreads), 0, st, a);
     }
     TQ_LAUNCH_CHECK("mq_sample_kernel");
-    hipLaunchKernelGGL(mq_select_kernel, dim3((unsigned)(nt * kMqQ)), dim3(kMqSelThreads), 0, st, a);
-    TQ_LAUNCH_CHECK("mq_select_kernel");
     if (big) {
       hipLaunchKernelGGL((mq_filter_kernel<D, true>), fg, dim3(kMqThreads), 0, st, a);
     } else {
