@@ -200,7 +200,8 @@ def k_unpack_dl(cache, t_cap, t0, n, values, vbits=2):
     return out.cpu().numpy()
 
 
-def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale, vbits=2):
+def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale, vbits=2,
+                seq_starts=None):
     B, Hq, d = q_t.shape
     Hkv, Tc = kn.shape[1], kn.shape[2]
     out = torch.empty_like(q_t)
@@ -208,11 +209,16 @@ def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale, vb
     ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
     dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
     sl = T(np.asarray(seq_lens, np.int32))
-    capi.check(L().tq_decode_attention_dl(
-        capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache),
-        capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)), capi.i64(Tc), capi.p(sl), capi.p(T(kc)),
-        capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(vbits), ctypes.c_float(scale),
-        capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
+    common = (capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache),
+              capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)), capi.i64(Tc), capi.p(sl))
+    rest = (capi.p(T(kc)), capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(vbits),
+            ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
+            capi.stream())
+    if seq_starts is None:
+        capi.check(L().tq_decode_attention_dl(*common, *rest))
+    else:
+        capi.check(L().tq_decode_attention_dl_window(*common, capi.p(T(np.asarray(seq_starts, np.int32))),
+                                                     *rest))
     sync()
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
@@ -1210,6 +1216,57 @@ def test_decode_layout_vbits_and_groups_vs_f64(vb, G):
         # held to the bf16 output tolerance; fp32 / fp16 queries use hi + lo parts
         lse_tol = 1e-2 if dt == torch.bfloat16 else 1e-5
         assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= lse_tol
+
+
+@pytest.mark.parametrize("vb", [2, 3])
+def test_decode_layout_window_vs_f64(vb):
+    # Windows [start, len) of each sequence (left-padded batches): tokens before start are
+    # masked; starts inside a 64-token tile, on a tile edge, at 0, at len - 1 and at len
+    # (an empty window: zeros and lse -inf).  Against float64 attention over the window's
+    # rows alone.
+    rs = np.random.RandomState(700 + vb)
+    d, Hkv, G, Tc = 64, 2, 4, 2112
+    seq = [700, 1500, 64, 2100, 3, 513, 90]
+    starts = [0, 37, 63, 1290, 2, 513, 64]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    n = B * Hkv * Tc
+    K = rs.randn(n, d).astype(np.float32)
+    V = rs.randn(n, d).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, Tc, -1), Tc, 0, 0)
+    vc = k_pack_dl(vp.reshape(B * Hkv, Tc, -1), Tc, 0, 1, vbits=vb)
+    kp, vp = kp.reshape(B, Hkv, Tc, -1), vp.reshape(B, Hkv, Tc, -1)
+    kn, vn = kn.reshape(B, Hkv, Tc), vn.reshape(B, Hkv, Tc)
+    # stale norms before each window must not reach the output
+    for b in range(B):
+        kn[b, :, :starts[b]] = np.nan
+        vn[b, :, :starts[b]] = np.nan
+    q = (rs.randn(B, Hq, d) * 3.0).astype(np.float32)
+    for dt, tol in ((torch.float32, 1e-4), (torch.bfloat16, 1e-2)):
+        qt = torch.from_numpy(q).to(DEV).to(dt)
+        qf = qt.float().cpu().numpy()
+        got, lse = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb,
+                               seq_starts=starts)
+        for b in range(B):
+            s0, t = starts[b], seq[b]
+            if s0 >= t:
+                assert np.all(got[b] == 0) and np.isneginf(lse[b]).all()
+                continue
+            want = O.decode_attention_f64(qf[b:b + 1], kp[b:b + 1, :, s0:t], kn[b:b + 1, :, s0:t],
+                                          vp[b:b + 1, :, s0:t], vn[b:b + 1, :, s0:t], [t - s0], ck, cv,
+                                          Rk, Rv, 4, vb, 0.125)[0]
+            err = np.max(np.abs(got[b] - want)) / np.max(np.abs(want))
+            assert err <= tol, (dt, b, err)
+    # starts of 0 equal the plain entry point bit for bit
+    qt = torch.from_numpy(q).to(DEV).to(torch.bfloat16)
+    kn0, vn0 = np.nan_to_num(kn), np.nan_to_num(vn)
+    a, la = k_decode_dl(qt, kc, kn0, vc, vn0, seq, ck, cv, Rk, Rv, 0.125, vbits=vb, seq_starts=[0] * B)
+    b_, lb = k_decode_dl(qt, kc, kn0, vc, vn0, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+    assert np.array_equal(a, b_) and np.array_equal(la, lb)
 
 
 @pytest.mark.parametrize("vb,T", [(2, 2048), (3, 1024)])

@@ -99,6 +99,64 @@ def test_hf_fused_decode_logits_match_reference_semantics():
     assert out.shape == (4, 46)
 
 
+def test_hf_fused_decode_left_padded_generate():
+    # generate() on a left-padded batch (prompts of 300, 211, 40 and 299 tokens): every
+    # decode step carries an attention mask.  The fused steps (decode-layout kernel over
+    # each sequence's window after its padding + the exact new token) against the
+    # reference's rule run by the general path (dequantized history + SDPA with the mask):
+    # per-step logits within 1e-3 of the maximum, the same greedy tokens.
+    from turboquant_kv import TurboQuantCache
+    from turboquant_kv.hf_integration import enable_fused_attention
+    model = _tiny_llama_gqa4()
+    g = torch.Generator(DEV).manual_seed(3)
+    lens = [300, 211, 40, 299]
+    L_ = max(lens)
+    ids = torch.randint(1, 1000, (4, L_), device=DEV, generator=g)
+    mask = torch.zeros(4, L_, dtype=torch.long, device=DEV)
+    for b, n in enumerate(lens):
+        ids[b, :L_ - n] = 0
+        mask[b, L_ - n:] = 1
+
+    def run(fused):
+        if fused:
+            enable_fused_attention(model)
+        else:
+            model.set_attn_implementation("sdpa")
+        cache = TurboQuantCache(key_bits=4, value_bits=3, fused_attention=fused)
+        with torch.no_grad():
+            out = model.generate(input_ids=ids, attention_mask=mask, past_key_values=cache,
+                                 max_new_tokens=5, do_sample=False, output_scores=True,
+                                 return_dict_in_generate=True, pad_token_id=0)
+        return out.sequences, torch.stack([s.float() for s in out.scores]), cache
+
+    seq_ref, sc_ref, _ = run(False)
+    seq_got, sc_got, cache = run(True)
+    assert cache.layers[0].dl
+    err = ((sc_got - sc_ref).abs().amax(-1) / sc_ref.abs().amax(-1)).max().item()
+    assert err <= 1e-3, err
+    assert torch.equal(seq_got, seq_ref)
+
+
+def test_hf_window_starts_from_masks():
+    # The mask -> window reading: left padding gives the first attended position; a hole in
+    # the middle, a masked current token or a fully masked row give None (general path).
+    from turboquant_kv.hf_integration import _window_starts
+    m = torch.ones(3, 1, 1, 9, dtype=torch.bool, device=DEV)
+    m[1, ..., :4] = False
+    m[2, ..., :8] = False
+    assert _window_starts(m, 3, 8).tolist() == [0, 4, 8]
+    f = torch.zeros(3, 1, 1, 9, device=DEV)
+    f[1, ..., :4] = float("-inf")
+    assert _window_starts(f, 3, 8).tolist() == [0, 4, 0]
+    h = m.clone()
+    h[0, ..., 5] = False
+    assert _window_starts(h, 3, 8) is None
+    c = m.clone()
+    c[0, ..., 8] = False
+    assert _window_starts(c, 3, 8) is None
+    assert _window_starts(m, 3, 9) is None  # a mask of another length
+
+
 @pytest.mark.parametrize("vb,G", [(3, 4), (2, 4), (4, 2), (3, 8)])
 def test_hf_fused_decode_step_vs_f64(vb, G):
     # One decode step of a bf16 layer: the attention function's output against float64

@@ -900,7 +900,7 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
     const at::Tensor& q, const at::Tensor& kpairs, const at::Tensor& knorms,
     const at::Tensor& vblocks, const at::Tensor& vnorms, const at::Tensor& seq_lens,
     const at::Tensor& kcentroids, const at::Tensor& vcentroids, const at::Tensor& krotation,
-    const at::Tensor& vrotation, double scale) {
+    const at::Tensor& vrotation, double scale, const c10::optional<at::Tensor>& seq_starts) {
   require_gpu(q, "q");
   TORCH_CHECK(q.dim() == 3, "q must be [B, Hq, d]");
   TORCH_CHECK(kpairs.dim() == 4 && vblocks.dim() == 4,
@@ -929,6 +929,11 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
               "norms must be float32 [B, Hkv, T]");
   auto sl = seq_lens.to(dev, at::kInt).contiguous();
   TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
+  at::Tensor ss;
+  if (seq_starts.has_value() && seq_starts->defined()) {
+    ss = seq_starts->to(dev, at::kInt).contiguous();
+    TORCH_CHECK(ss.numel() == B, "seq_starts must have B entries");
+  }
   auto kc = f32c(kcentroids, dev);
   auto vc = f32c(vcentroids, dev);
   auto Rk = f32c(krotation, dev);
@@ -939,10 +944,11 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
   if (B == 0) return {out, lse};
   auto ws = workspace(tq_decode_dl_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)Hkv, Tc), dev);
-  check_rc(tq_decode_attention_dl(
+  check_rc(tq_decode_attention_dl_window(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
       kpairs.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vblocks.data_ptr<uint8_t>(),
-      vnorms.data_ptr<float>(), Tc, sl.data_ptr<int32_t>(), kc.data_ptr<float>(),
+      vnorms.data_ptr<float>(), Tc, sl.data_ptr<int32_t>(),
+      ss.defined() ? ss.data_ptr<int32_t>() : nullptr, kc.data_ptr<float>(),
       vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), 4, (int32_t)vbits,
       (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(), ws.numel(),
       cur_stream(qq)));
@@ -1085,7 +1091,8 @@ at::Tensor decode_attention_dl(const at::Tensor& q, const at::Tensor& kpairs,
                                const at::Tensor& krotation, const at::Tensor& vrotation,
                                double scale) {
   return std::get<0>(decode_attention_dl_lse(q, kpairs, knorms, vblocks, vnorms, seq_lens,
-                                             kcentroids, vcentroids, krotation, vrotation, scale));
+                                             kcentroids, vcentroids, krotation, vrotation, scale,
+                                             c10::nullopt));
 }
 
 // Appends s new tokens of every (batch row, KV head) to a decode-layout cache at token
@@ -1238,7 +1245,8 @@ TORCH_LIBRARY(turboquant, m) {
         " Tensor krotation, Tensor vrotation, float scale) -> Tensor");
   m.def("decode_attention_dl_lse(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
         " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
-        " Tensor krotation, Tensor vrotation, float scale) -> (Tensor, Tensor)");
+        " Tensor krotation, Tensor vrotation, float scale, Tensor? seq_starts=None)"
+        " -> (Tensor, Tensor)");
   m.def("decode_merge_token(Tensor o, Tensor lse, Tensor q, Tensor k_new, Tensor v_new,"
         " float scale) -> Tensor");
   m.def("cache_append_dl(Tensor key, Tensor value, Tensor(a!) kp, Tensor(b!) kn, Tensor(c!) vp,"

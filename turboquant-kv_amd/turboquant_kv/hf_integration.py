@@ -316,6 +316,33 @@ def _history_lengths(B: int, t_hist: int, device) -> torch.Tensor:
     return t
 
 
+_WINDOW: Dict[Any, Optional[torch.Tensor]] = {}
+
+
+def _window_starts(mask: torch.Tensor, B: int, t_hist: int) -> Optional[torch.Tensor]:
+    """Left-padding starts of a decode step from its attention mask [B, 1, 1, t_hist + 1]
+    (bool, True = attend, as transformers' sdpa_mask builds it; or additive float, 0 =
+    attend): per sequence the first attended position, when every position from it through
+    the current token is attended -- the form generate() gives left-padded batches.  None
+    for any other mask (the caller takes the general path).  One host read per mask: every
+    layer of a step shares the step's mask tensor."""
+    key = (id(mask), mask.data_ptr(), tuple(mask.shape), t_hist)
+    if key in _WINDOW:
+        return _WINDOW[key]
+    _WINDOW.clear()
+    m = mask[:, 0, -1, :] if mask.dim() == 4 else mask.reshape(mask.shape[0], -1)
+    vis = m if m.dtype == torch.bool else (m == 0)
+    res = None
+    if vis.shape[-1] == t_hist + 1:
+        vis = vis.expand(B, -1)
+        first = vis.int().argmax(-1)  # the first attended position (0 when none is)
+        ok = ((vis.sum(-1) == vis.shape[-1] - first) & vis[:, -1]).all()
+        if bool(ok):
+            res = first.to(torch.int32)
+    _WINDOW[key] = res
+    return res
+
+
 def turboquant_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
                          **kwargs):
     """Attention function registered as "turboquant" with transformers."""
@@ -328,13 +355,19 @@ def turboquant_attention(module, query, key, value, attention_mask, scaling=None
     t_hist = key._tq_hist
     k_new = key.as_subclass(torch.Tensor)
     B, Hq, sq, d = query.shape
-    if sq == 1 and attention_mask is None and t_hist > 0 and not layer.kq.prod:
+    # a padded batch's mask (left padding, as generate() pads) becomes per-sequence window
+    # starts of the decode-layout kernel; any other mask takes the general path
+    starts = None
+    if sq == 1 and attention_mask is not None and t_hist > 0 and layer.dl and not layer.kq.prod:
+        starts = _window_starts(attention_mask, B, t_hist)
+    if sq == 1 and (attention_mask is None or starts is not None) and t_hist > 0 \
+            and not layer.kq.prod:
         q = query[:, :, 0, :]
         seq = _history_lengths(B, t_hist, query.device)
         if layer.dl:
             o_h, lse_h = _ops().decode_attention_dl_lse(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
-                layer.kq.R, layer.vq.R, float(scaling))
+                layer.kq.R, layer.vq.R, float(scaling), starts)
         else:
             o_h, lse_h = _ops().decode_attention_packed_lse(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
