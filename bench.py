@@ -577,7 +577,9 @@ def bench_e2e(args, extra):
                                            L.kq.R, L.vq.R, 0.125)
 
     ms = time_op(one, 32, 4)
-    kb = B * 8 * T * (32 + 24 + 8) + 2 * B * 32 * 64 * 2
+    nsz = layers[0].kn.element_size()  # bf16 norms in a bf16 model's cache (as the reference)
+    kb = B * 8 * T * (32 + 24 + 2 * nsz) + 2 * B * 32 * 64 * 2
+    res["decode_kernel_bytes_per_token_head"] = 32 + 24 + 2 * nsz
     res["decode_kernel_us_per_layer"] = ms * 1e3
     res["decode_kernel_GBps"] = kb / ms / 1e6
     res["decode_kernel_hbm_frac"] = kb / ms / 1e6 / HBM_PEAK_GBS
@@ -749,6 +751,8 @@ def main():
                     help="only the end-to-end greedy decode (configs[4])")
     ap.add_argument("--scan-only", action="store_true",
                     help="only the index scans (configs[1]: 4-, 3- and 2-bit), e.g. for a profiler run")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode attention legs (configs[3] at 4K, 16K and 32K)")
     ap.add_argument("--batch-only", action="store_true",
                     help="only the 4-bit Q=64 / Q=1024 query batches of configs[1], e.g. for a profiler run")
     ap.add_argument("--prefill-only", action="store_true",
@@ -788,6 +792,12 @@ def main():
     if args.e2e_only:
         extra = {}
         bench_e2e(args, extra)
+        print(json.dumps(extra))
+        return
+    if args.decode_only:
+        extra = {}
+        dec = bench_decode(args, extra)
+        extra["decode_attn_hbm_frac"] = {str(T): v[1] / v[0] / 1e6 / HBM_PEAK_GBS for T, v in dec.items()}
         print(json.dumps(extra))
         return
     if args.batch_only:

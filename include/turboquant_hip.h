@@ -350,13 +350,17 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
  * tq_decode_attention_dl over a window [seq_starts[b], seq_lens[b]) of each sequence: tokens
  * before seq_starts[b] are masked (a left-padded batch, whose 2-D attention mask hides the
  * first seq_starts[b] positions).  seq_starts may be null (every window starts at 0).
+ * knorms / vnorms hold norm_dtype values: TQ_F32, or TQ_BF16 / TQ_F16 for a 16-bit model's
+ * cache, which keeps its norms in the model's dtype as the reference's HF cache does
+ * (turboquant_kv/hf_integration.py:512-525 counts them so).
  * Replaces: the masked decode step of turboquant_kv/hf_integration.py:319-421 (dequantized
  * history + SDPA with the attention mask).
  */
 int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
                                   int32_t hkv, int32_t d, const uint8_t* kpairs,
-                                  const float* knorms, const uint8_t* vblocks,
-                                  const float* vnorms, int64_t t_cap, const int32_t* seq_lens,
+                                  const void* knorms, const uint8_t* vblocks,
+                                  const void* vnorms, tq_dtype norm_dtype, int64_t t_cap,
+                                  const int32_t* seq_lens,
                                   const int32_t* seq_starts, const float* kcentroids,
                                   const float* vcentroids, const float* krotation,
                                   const float* vrotation, int32_t kbits, int32_t vbits,

@@ -200,25 +200,33 @@ def k_unpack_dl(cache, t_cap, t0, n, values, vbits=2):
     return out.cpu().numpy()
 
 
+_DT = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}
+
+
 def k_decode_dl(q_t, kcache, kn, vcache, vn, seq_lens, kc, vc, Rk, Rv, scale, vbits=2,
-                seq_starts=None):
+                seq_starts=None, norm_dtype=None):
+    """tq_decode_attention_dl; with seq_starts or norm_dtype (the norms cast to that torch
+    dtype) tq_decode_attention_dl_window."""
     B, Hq, d = q_t.shape
     Hkv, Tc = kn.shape[1], kn.shape[2]
     out = torch.empty_like(q_t)
     lse = torch.empty(B, Hq, dtype=torch.float32, device=DEV)
     ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
-    dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[q_t.dtype]
+    dt = _DT[q_t.dtype]
     sl = T(np.asarray(seq_lens, np.int32))
-    common = (capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache),
-              capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)), capi.i64(Tc), capi.p(sl))
     rest = (capi.p(T(kc)), capi.p(T(vc)), capi.p(T(Rk)), capi.p(T(Rv)), capi.i32(4), capi.i32(vbits),
             ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
             capi.stream())
-    if seq_starts is None:
-        capi.check(L().tq_decode_attention_dl(*common, *rest))
+    head = (capi.p(q_t), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(d), capi.p(kcache))
+    if seq_starts is None and norm_dtype is None:
+        capi.check(L().tq_decode_attention_dl(*head, capi.p(T(kn)), capi.p(vcache), capi.p(T(vn)),
+                                              capi.i64(Tc), capi.p(sl), *rest))
     else:
-        capi.check(L().tq_decode_attention_dl_window(*common, capi.p(T(np.asarray(seq_starts, np.int32))),
-                                                     *rest))
+        nd = norm_dtype or torch.float32
+        knt, vnt = T(kn, nd), T(vn, nd)
+        st = capi.p(None) if seq_starts is None else capi.p(T(np.asarray(seq_starts, np.int32)))
+        capi.check(L().tq_decode_attention_dl_window(*head, capi.p(knt), capi.p(vcache), capi.p(vnt),
+                                                     _DT[nd], capi.i64(Tc), capi.p(sl), st, *rest))
     sync()
     return out.float().cpu().numpy(), lse.cpu().numpy()
 
@@ -1267,6 +1275,38 @@ def test_decode_layout_window_vs_f64(vb):
     a, la = k_decode_dl(qt, kc, kn0, vc, vn0, seq, ck, cv, Rk, Rv, 0.125, vbits=vb, seq_starts=[0] * B)
     b_, lb = k_decode_dl(qt, kc, kn0, vc, vn0, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
     assert np.array_equal(a, b_) and np.array_equal(la, lb)
+
+
+@pytest.mark.parametrize("nd", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("vb", [2, 3, 4])
+def test_decode_layout_16bit_norms(nd, vb):
+    # A 16-bit model's cache keeps its norms in that dtype (the reference's quantize returns
+    # them so): the kernel reads them as 16-bit values.  With norms that are exactly
+    # representable in nd, the output equals the fp32-norm call's up to the compiler's
+    # contraction choices (an fp16 norm can enter a mixed-precision fma directly): within
+    # 1e-5 of the output's maximum, lse within 1e-6.
+    rs = np.random.RandomState(800 + vb)
+    d, Hkv, G, Tc = 64, 2, 4, 1088
+    seq = [1000, 5, 64, 1088]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    _, ck = O.lloyd_max_codebook(4, d)
+    _, cv = O.lloyd_max_codebook(vb, d)
+    kp = rs.randint(0, 256, (B * Hkv, Tc, 32)).astype(np.uint8)
+    vp = rs.randint(0, 256, (B * Hkv, Tc, 8 * vb)).astype(np.uint8)
+    kc = k_pack_dl(kp, Tc, 0, 0)  # any bytes are valid bit-plane rows
+    vc = k_pack_dl(vp, Tc, 0, 1, vbits=vb)
+    to16 = lambda x: torch.from_numpy(x).to(nd).float().numpy()
+    kn = to16(rs.uniform(0.3, 3.0, (B, Hkv, Tc)).astype(np.float32))
+    vn = to16(rs.uniform(0.3, 3.0, (B, Hkv, Tc)).astype(np.float32))
+    for qdt in (torch.float32, torch.bfloat16):
+        qt = torch.from_numpy(rs.randn(B, Hq, d).astype(np.float32)).to(DEV).to(qdt)
+        a, la = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+        b_, lb = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb, norm_dtype=nd)
+        assert np.max(np.abs(a - b_)) <= 1e-5 * np.max(np.abs(a)), qdt
+        ok = np.isfinite(la)
+        assert np.array_equal(ok, np.isfinite(lb))
+        assert np.max(np.abs(la[ok] - lb[ok])) <= 1e-6 * max(1.0, np.max(np.abs(la[ok]))), qdt
 
 
 @pytest.mark.parametrize("vb,T", [(2, 2048), (3, 1024)])

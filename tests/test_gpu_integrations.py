@@ -42,7 +42,7 @@ def test_hf_update_returns_dequantized_history_plus_exact_new():
     rows = layer.rows(False, 5).reshape(-1, 32).cpu().numpy()   # bit-plane rows
     got = O.unpack_codes(rows, 4, 64)
     O.check_codes(got, codes, x, R, bnd)
-    deq = O.dequantize_mse(rows, layer.kn[:, :, :5].reshape(-1).cpu().numpy(), 4, 64, R, cen)
+    deq = O.dequantize_mse(rows, layer.kn[:, :, :5].reshape(-1).float().cpu().numpy(), 4, 64, R, cen)
     assert np.allclose(K[:, :, :5].reshape(-1, 64).cpu().numpy(), deq, rtol=1e-5, atol=1e-5)
     assert cache.get_seq_length(0) == 6 and cache.memory_bytes() == 2 * 2 * 6 * (32 + 16 + 8)
 
@@ -183,13 +183,16 @@ def test_hf_fused_decode_step_vs_f64(vb, G):
     got = got.float().cpu().numpy()[:, 0]                       # [B, Hq, d]
     layer = cache.layers[0]
     assert layer.dl
+    # a bf16 model's cache keeps bf16 norms, counted as the reference counts them
+    assert layer.kn.dtype == torch.bfloat16 and layer.vn.dtype == torch.bfloat16
+    assert cache.memory_bytes() == B * Hkv * (T + 1) * (32 + 8 * vb + 2 * 2)
     Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
     _, ck = O.lloyd_max_codebook(4, d)
     _, cv = O.lloyd_max_codebook(vb, d)
     kr = layer.rows(False, T).cpu().numpy()
     vr = layer.rows(True, T).cpu().numpy()
-    kn = layer.kn[:, :, :T].cpu().numpy()
-    vn = layer.vn[:, :, :T].cpu().numpy()
+    kn = layer.kn[:, :, :T].float().cpu().numpy()
+    vn = layer.vn[:, :, :T].float().cpu().numpy()
     qf = q.float().cpu().numpy()[:, :, 0].astype(np.float64)
     k1f = k1.float().cpu().numpy()[:, :, 0].astype(np.float64)
     v1f = v1.float().cpu().numpy()[:, :, 0].astype(np.float64)

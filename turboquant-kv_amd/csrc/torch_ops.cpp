@@ -924,9 +924,11 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
                   vblocks.size(1) == Hkv && vblocks.size(2) * 64 == Tc &&
                   vblocks.size(3) == 8 * vbits * d && vbits >= 2 && vbits <= 4,
               "decode-layout K/V shape mismatch");
-  TORCH_CHECK(knorms.scalar_type() == at::kFloat && vnorms.scalar_type() == at::kFloat &&
-                  knorms.numel() == B * Hkv * Tc && vnorms.numel() == B * Hkv * Tc,
-              "norms must be float32 [B, Hkv, T]");
+  const auto ndt = knorms.scalar_type();
+  TORCH_CHECK((ndt == at::kFloat || ndt == at::kBFloat16 || ndt == at::kHalf) &&
+                  vnorms.scalar_type() == ndt && knorms.numel() == B * Hkv * Tc &&
+                  vnorms.numel() == B * Hkv * Tc,
+              "norms must be [B, Hkv, T], both float32, bfloat16 or float16");
   auto sl = seq_lens.to(dev, at::kInt).contiguous();
   TORCH_CHECK(sl.numel() == B, "seq_lens must have B entries");
   at::Tensor ss;
@@ -946,8 +948,8 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   auto ws = workspace(tq_decode_dl_workspace_bytes((int32_t)B, (int32_t)Hq, (int32_t)Hkv, Tc), dev);
   check_rc(tq_decode_attention_dl_window(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
-      kpairs.data_ptr<uint8_t>(), knorms.data_ptr<float>(), vblocks.data_ptr<uint8_t>(),
-      vnorms.data_ptr<float>(), Tc, sl.data_ptr<int32_t>(),
+      kpairs.data_ptr<uint8_t>(), knorms.data_ptr(), vblocks.data_ptr<uint8_t>(),
+      vnorms.data_ptr(), to_tq(ndt), Tc, sl.data_ptr<int32_t>(),
       ss.defined() ? ss.data_ptr<int32_t>() : nullptr, kc.data_ptr<float>(),
       vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(), 4, (int32_t)vbits,
       (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(), ws.numel(),
@@ -1112,10 +1114,11 @@ void cache_append_dl(const at::Tensor& key, const at::Tensor& value, at::Tensor&
   TORCH_CHECK(kp.dim() == 4 && vp.dim() == 4 && kp.size(0) == B && kp.size(1) == H &&
                   vp.size(0) == B && vp.size(1) == H && kp.is_contiguous() && vp.is_contiguous(),
               "kp / vp must be contiguous [B, H, ...] decode-layout caches");
-  TORCH_CHECK(kn.dim() == 3 && vn.dim() == 3 && kn.scalar_type() == at::kFloat &&
-                  vn.scalar_type() == at::kFloat && kn.size(0) == B && kn.size(1) == H &&
+  TORCH_CHECK(kn.dim() == 3 && vn.dim() == 3 &&
+                  (kn.scalar_type() == at::kFloat || kn.scalar_type() == key.scalar_type()) &&
+                  vn.scalar_type() == kn.scalar_type() && kn.size(0) == B && kn.size(1) == H &&
                   vn.sizes() == kn.sizes(),
-              "kn / vn must be float32 [B, H, t_cap]");
+              "kn / vn must be [B, H, t_cap], float32 or the key's dtype");
   TORCH_CHECK(pos >= 0 && pos + n <= kn.size(2), "tokens past the cache's capacity");
   if (B * H * n == 0) return;
   for (int values = 0; values < 2; ++values) {

@@ -500,7 +500,7 @@ struct DlArgs {
   int q_dt;
   int hq, hkv, G;
   const uint8_t* kpairs;   // [B*hkv][t_cap][32]
-  const float* knorms;     // [B*hkv][t_cap]
+  const float* knorms;     // [B*hkv][t_cap] (ND != 0: 16-bit values, read through a cast)
   const uint8_t* vblocks;  // [B*hkv][t_cap/4][64]
   const float* vnorms;
   int64_t t_cap;
@@ -603,10 +603,13 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // PG: 0 contiguous; 1 / 2 paged pools (blocks >= 64 tokens / 16- or 32-token blocks) read
 // through buffer resources over whole pools (32-bit offsets: pools under 2 GiB); 3 / 4 the
 // same for pools of any size: rows at 64-bit addresses from clamped block ids.
-template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2>
+// ND: the norms' dtype -- 0 fp32, TQ_F16 or TQ_BF16 (contiguous caches only: a bf16 model's
+// cache keeps its norms in bf16, as the reference's quantize returns them).
+template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   constexpr bool PAGED = PG != 0, SUB16 = PG == 2 || PG == 4, WIDE = PG >= 3;
   static_assert(VB >= 2 && VB <= 4 && (!SUB16 || VB == 2), "value width");
+  static_assert(ND == 0 || PG == 0, "16-bit norms: contiguous caches");
   constexpr int VW = VB == 2 ? 4 : 2 * VB;  // value words per lane and tile
   constexpr uint32_t VTILE = 512u * VB;     // bytes per 64-token value tile
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
@@ -667,9 +670,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       make_rsrc(a.vblocks + sbase * (8 * VB),
                 PAGED ? nrows * (8 * VB) : (uint32_t)(a.t_cap >> 6) * VTILE);
   // Norms are read four tokens at a time (t_cap % 4 == 0, pools of whole blocks).
-  const uint32_t nbytes = nrows * 4;
-  const __amdgpu_buffer_rsrc_t knrs = make_rsrc(a.knorms + sbase, nbytes);
-  const __amdgpu_buffer_rsrc_t vnrs = make_rsrc(a.vnorms + sbase, nbytes);
+  constexpr uint32_t NSZ = ND ? 2 : 4;  // bytes per norm
+  const uint32_t nbytes = nrows * NSZ;
+  const __amdgpu_buffer_rsrc_t knrs =
+      make_rsrc(reinterpret_cast<const char*>(a.knorms) + sbase * NSZ, nbytes);
+  const __amdgpu_buffer_rsrc_t vnrs =
+      make_rsrc(reinterpret_cast<const char*>(a.vnorms) + sbase * NSZ, nbytes);
   const int bsl = PAGED ? a.bs_log2 : 0;
   const int kvh = g;  // the kv head (the tile loads below name their token groups g)
   const __amdgpu_buffer_rsrc_t btrs =
@@ -764,11 +770,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     // aligned base)
     uint32_t rq = rg[0] + 16 * gq;
     if constexpr (SUB16) rq = gq == 0 ? rg[0] : gq == 1 ? rg[1] : gq == 2 ? rg[2] : rg[3];
-    const uint32_t no = (rq + 4 * sl) * 4;
+    const uint32_t no = (rq + 4 * sl) * NSZ;
     u32x4 kn4, vn4;
     if constexpr (WIDE) {
       kn4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.knorms + (size_t)(rq + 4 * sl)));
       vn4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vnorms + (size_t)(rq + 4 * sl)));
+    } else if constexpr (ND != 0) {  // four 16-bit norms, widened to fp32 bit patterns
+      const u32x2 k2 = __builtin_amdgcn_raw_buffer_load_b64(knrs, (int)no, 0, kNT);
+      const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(vnrs, (int)no, 0, kNT);
+      auto wide = [](uint32_t h) -> uint32_t {
+        return ND == TQ_BF16 ? h << 16
+                             : __float_as_uint(__half2float(__ushort_as_half((unsigned short)h)));
+      };
+      kn4 = (u32x4){wide(k2.x & 0xFFFFu), wide(k2.x >> 16), wide(k2.y & 0xFFFFu), wide(k2.y >> 16)};
+      vn4 = (u32x4){wide(v2.x & 0xFFFFu), wide(v2.x >> 16), wide(v2.y & 0xFFFFu), wide(v2.y >> 16)};
     } else {
       kn4 = __builtin_amdgcn_raw_buffer_load_b128(knrs, (int)no, 0, kNT);
       vn4 = __builtin_amdgcn_raw_buffer_load_b128(vnrs, (int)no, 0, kNT);
@@ -1060,7 +1075,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     const int nlow = ts - (t0 + 16 * gq + 4 * sl);  // registers below it are masked
     float s[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = (r < nvalid) & (r >= nlow) ? skk[r] * cur.kn[r] : -INFINITY;
+    for (int r = 0; r < 4; ++r) s[r] = ((r < nvalid) & (r >= nlow)) ? skk[r] * cur.kn[r] : -INFINITY;
     const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     if (__any(lm > M)) {
       float m2 = lm;
@@ -1082,7 +1097,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     for (int r = 0; r < 4; ++r) {
       const float p = __builtin_amdgcn_exp2f(s[r] - M);
       psum += p;
-      const float w = (r < nvalid) & (r >= nlow) ? p * cur.vn[r] : 0.f;
+      const float w = ((r < nvalid) & (r >= nlow)) ? p * cur.vn[r] : 0.f;
       wh[r] = (_Float16)w;
       if constexpr (EXACT_V) wl[r] = (_Float16)(w - (float)wh[r]);
     }
@@ -1554,14 +1569,21 @@ SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
   return {split, (int)((t_cap + split - 1) / split)};
 }
 
-template <int PG, int VB>
+template <int PG, int VB, int ND = 0>
 void launch_dl_kernel(tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
   if (q_dtype == TQ_F32)
-    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else if (q_dtype == TQ_F16)
-    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
+}
+
+template <int ND>
+void launch_dl_contiguous(int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
+  if (vbits == 2) launch_dl_kernel<0, 2, ND>(q_dtype, grid, a, st);
+  else if (vbits == 3) launch_dl_kernel<0, 3, ND>(q_dtype, grid, a, st);
+  else launch_dl_kernel<0, 4, ND>(q_dtype, grid, a, st);
 }
 
 // The exact current token merged into a decode output by log-sum-exp (the HF cache's
@@ -1599,7 +1621,8 @@ __global__ __launch_bounds__(64) void merge_token_kernel(const void* o, const fl
 // heads per KV head, then (several splits) the log-sum-exp combine.  `a` carries
 // everything but the split plan, the head range and the outputs.
 int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg,
-           const SplitPlan& p, void* workspace, void* out, float* lse, hipStream_t st) {
+           const SplitPlan& p, void* workspace, void* out, float* lse, hipStream_t st,
+           int norm_dt = TQ_F32) {
   const size_t rows = (size_t)B * hq;
   char* ws = static_cast<char*>(workspace) + 256;
   float* part = reinterpret_cast<float*>(ws);
@@ -1616,9 +1639,9 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
       a.hofs = h0;
       a.G = std::min(4, a.Gfull - h0);
       if (pg == 0) {
-        if (vbits == 2) launch_dl_kernel<0, 2>(q_dtype, (unsigned)grid, a, st);
-        else if (vbits == 3) launch_dl_kernel<0, 3>(q_dtype, (unsigned)grid, a, st);
-        else launch_dl_kernel<0, 4>(q_dtype, (unsigned)grid, a, st);
+        if (norm_dt == TQ_BF16) launch_dl_contiguous<TQ_BF16>(vbits, q_dtype, (unsigned)grid, a, st);
+        else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16>(vbits, q_dtype, (unsigned)grid, a, st);
+        else launch_dl_contiguous<0>(vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 1) {
         launch_dl_kernel<1, 2>(q_dtype, (unsigned)grid, a, st);
       } else if (pg == 3) {
@@ -1655,14 +1678,15 @@ size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t 
 
 int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
                                   int32_t hkv, int32_t d, const uint8_t* kpairs,
-                                  const float* knorms, const uint8_t* vblocks,
-                                  const float* vnorms, int64_t t_cap, const int32_t* seq_lens,
+                                  const void* knorms, const uint8_t* vblocks,
+                                  const void* vnorms, tq_dtype norm_dtype, int64_t t_cap,
+                                  const int32_t* seq_lens,
                                   const int32_t* seq_starts, const float* kcentroids,
                                   const float* vcentroids, const float* krotation,
                                   const float* vrotation, int32_t kbits, int32_t vbits,
                                   float scale, void* out, float* lse, void* workspace,
                                   size_t workspace_bytes, void* stream) {
-  TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
+  TQ_REQUIRE(valid_dtype(q_dtype) && valid_dtype(norm_dtype), "unknown dtype");
   if (d != kDim || kbits != 4 || vbits < 2 || vbits > 4)
     return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-4 bit "
                                  "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
@@ -1684,11 +1708,12 @@ int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, in
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   const SplitPlan p = t_cap > 0 ? plan_dl_splits(B, hkv, t_cap) : SplitPlan{kDlMinSplit, 1};
   DlArgs a{};
-  a.q = q; a.kpairs = kpairs; a.knorms = knorms; a.vblocks = vblocks; a.vnorms = vnorms;
-  a.t_cap = t_cap; a.seq_lens = seq_lens; a.seq_starts = seq_starts; a.kcen = kcentroids;
-  a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
-  a.qscale = scale * 1.4426950408889634f;
-  return run_dl(a, q_dtype, B, hq, hkv, vbits, 0, p, workspace, out, lse, as_stream(stream));
+  a.q = q; a.kpairs = kpairs; a.knorms = static_cast<const float*>(knorms); a.vblocks = vblocks;
+  a.vnorms = static_cast<const float*>(vnorms); a.t_cap = t_cap; a.seq_lens = seq_lens;
+  a.seq_starts = seq_starts; a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation;
+  a.vrot = vrotation; a.qscale = scale * 1.4426950408889634f;
+  return run_dl(a, q_dtype, B, hq, hkv, vbits, 0, p, workspace, out, lse, as_stream(stream),
+                (int)norm_dtype);
 }
 
 int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
@@ -1700,7 +1725,7 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
                            void* out, float* lse, void* workspace, size_t workspace_bytes,
                            void* stream) {
   return tq_decode_attention_dl_window(q, q_dtype, B, hq, hkv, d, kpairs, knorms, vblocks, vnorms,
-                                       t_cap, seq_lens, nullptr, kcentroids, vcentroids, krotation,
+                                       TQ_F32, t_cap, seq_lens, nullptr, kcentroids, vcentroids, krotation,
                                        vrotation, kbits, vbits, scale, out, lse, workspace,
                                        workspace_bytes, stream);
 }

@@ -121,6 +121,12 @@ class TurboQuantLayer(_HFLayer):
             # decode layout: mse, 4-bit keys, 2-4 bit values, head_dim 64
             self.dl = (not self.kq.prod and self.kq.code_bits == 4 and
                        2 <= self.vq.code_bits <= 4 and d == 64)
+            # norms in the model's dtype for 16-bit models, as the reference's cache keeps
+            # them (quantize returns them in the input dtype; hf_integration.py:512-525
+            # counts them so); the decode-layout kernel reads 16-bit norms directly.  Other
+            # layouts keep fp32 norms for their kernels.
+            self.norm_dtype = (self.dtype if self.dl and self.dtype in (torch.bfloat16, torch.float16)
+                               else torch.float32)
         self.is_initialized = True
 
     def _grow(self, need: int) -> None:
@@ -149,8 +155,8 @@ class TurboQuantLayer(_HFLayer):
         else:
             self.kp = grown(getattr(self, "kp", None), self.kq.code_bits * bpp, dtype=torch.uint8)
             self.vp = grown(getattr(self, "vp", None), self.vq.code_bits * bpp, dtype=torch.uint8)
-        self.kn = grown(getattr(self, "kn", None), dtype=torch.float32)
-        self.vn = grown(getattr(self, "vn", None), dtype=torch.float32)
+        self.kn = grown(getattr(self, "kn", None), dtype=self.norm_dtype)
+        self.vn = grown(getattr(self, "vn", None), dtype=self.norm_dtype)
         if prod:
             self.ks = grown(getattr(self, "ks", None), bpp, dtype=torch.uint8)
             self.vs = grown(getattr(self, "vs", None), bpp, dtype=torch.uint8)
@@ -266,7 +272,8 @@ class TurboQuantLayer(_HFLayer):
             return 0
         B, H, T = self.batch, self.num_heads, self.seq_len
         bpp = (self.head_dim + 7) // 8
-        per = (self.kq.code_bits + self.vq.code_bits) * bpp + 8
+        nsz = torch.finfo(self.norm_dtype).bits // 8
+        per = (self.kq.code_bits + self.vq.code_bits) * bpp + 2 * nsz
         if self.kq.prod:
             per += 2 * bpp + 8
         return B * H * T * per
