@@ -153,10 +153,18 @@ def bench_scan(args, extra):
                 "ms_per_batch": t, "queries_per_s": Q / t * 1e3,
                 "row_passes": tiles, "GBps_rows_read": tiles * N * (4 * 16 + 4) / t / 1e6,
                 "filter_TFLOPs": flop / t / 1e9, "fp16_dense_peak_frac": flop / t / 1e9 / 2500.0,
-                "kernels": "mq_prep + mq_sample + mq_select + mq_filter + mq_merge (+ exact scan "
-                           "for flagged queries: none here)"}
+                "kernels": "mq_rotate + mq_tile + mq_sample + mq_filter + mq_merge (+ exact "
+                           "scan for flagged queries: none here)"}
             log(f"scan b=4 Q={Q}: {t:.3f} ms/batch, {Q / t * 1e3:.0f} q/s, filter "
                 f"{flop / t / 1e9:.0f} TFLOP/s, rows read at {tiles * N * 68 / t / 1e6:.0f} GB/s")
+        # k = 100 (bench_realworld.py's recall@100 searches): the same fused kernels, one
+        # query included (above k = 32 a single query takes the multi-query filter too)
+        for Q, steps in ((1, 20), (64, 20), (1024, 5)):
+            qq = queries(Q, d, seed=3)
+            t = time_op(lambda: ops.ip_scan_topk_pairs(qq, pairs, norms, cen, R, 100), steps, 2,
+                        settle_s=0.1)
+            extra[f"scan_b4_Q{Q}_k100"] = {"ms_per_batch": t, "queries_per_s": Q / t * 1e3}
+            log(f"scan b=4 Q={Q} k=100: {t:.3f} ms/batch, {Q / t * 1e3:.0f} q/s")
     # bit-plane rows (the CPU reference's input) and the pair rows the headline op reads
     res["db4"] = (packed, norms, R, cen, pairs)
     if not args.quick and not getattr(args, "batch_only", False):

@@ -140,7 +140,7 @@ int tq_attention_values_packed(const float* attn_weights, int64_t nq, int64_t T,
  *   top k by score descending; equal scores keep the lower index first.
  *   queries [nq, d] of q_dtype (fp16/bf16 are upcast to fp32 before rotation),
  *   packed [N, b*ceil(d/8)], norms [N] fp32, out_scores [nq, k] fp32,
- *   out_ids [nq, k] int64.  k > N pads with (-inf, -1).  2 <= b <= 4, d <= 256, k <= 32.
+ *   out_ids [nq, k] int64.  k > N pads with (-inf, -1).  1 <= b <= 4, d <= 256, k <= 128.
  */
 size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N, int32_t k);
 int tq_ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,

@@ -332,8 +332,9 @@ def test_cache_gqa_batched_decode_matches_composition():
 
 @pytest.mark.parametrize("bits,d,mode", [(4, 128, "mse"), (3, 200, "mse"), (4, 64, "prod")])
 def test_index_search_k_above_32_ties_and_order(bits, d, mode):
-    # k above the fused scan's 32 scores every row and selects with the core's heap order
-    # (score descending, lower index first on a tie): 200 duplicated rows tie exactly.
+    # k up to 128 runs the fused top-k scans, k above scores every row and selects; both
+    # give the core's heap order (score descending, lower index first on a tie): 200
+    # duplicated rows tie exactly.
     from turboquant_kv import TurboQuantIndex
     rs = np.random.RandomState(bits * 7 + d)
     db = rs.randn(6000, d).astype(np.float32)
@@ -341,7 +342,7 @@ def test_index_search_k_above_32_ties_and_order(bits, d, mode):
     idx = TurboQuantIndex.from_vectors(torch.from_numpy(db).to(DEV), bit_width=bits, mode=mode)
     q = rs.randn(3, d).astype(np.float32)
     q[0] = db[17]
-    for k in (64, 300):
+    for k in (64, 100, 128, 300):
         s, i = idx.search(torch.from_numpy(q).to(DEV), k=k)
         s, i = s.cpu().numpy(), i.cpu().numpy()
         if mode == "mse":

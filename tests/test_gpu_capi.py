@@ -995,6 +995,89 @@ def test_mq_scan_past_4gib_equals_exact_path():
     torch.cuda.empty_cache()
 
 
+# ------------------------------------------------------------------ top-k above 32
+def _plant_ties(rs, p, nm, nsrc, copies):
+    """Copy each of nsrc random rows (codes and norm) over `copies` other rows: exact ties."""
+    N = p.shape[0]
+    src = rs.choice(N, nsrc, replace=False)
+    for r in src:
+        dst = rs.choice(N, copies, replace=False)
+        p[dst] = p[r]
+        nm[dst] = nm[r]
+    return src
+
+
+@pytest.mark.parametrize("d,b", [(64, 1), (128, 2), (200, 3), (128, 4), (64, 4)])
+def test_scan_large_k_bit_exact_with_ties(d, b):
+    # k = 33, 100 and 128 over bit-plane rows (the exact scan's lists sized for k, the
+    # long-list block merge, the large-k merge), one and several queries, 40 rows appearing
+    # six times each (query 0 points at one of them), and a table of 77 rows (k > N pads
+    # with (-inf, -1)): bit-identical to the oracle, tie order included.
+    rs = np.random.RandomState(700 + d + b)
+    N = 20_011
+    R, cen, p, nm = _db(rs, N, d, b)
+    nm = nm.copy()
+    src = _plant_ties(rs, p, nm, 40, 5)
+    for Q in (1, 5):
+        q = rs.randn(Q, d).astype(np.float32)
+        q[0] = O.dequantize_mse(p[src[:1]], np.ones(1, np.float32), b, d, R, cen)[0]
+        so, io = O.search_topk(q, p, nm, cen, R, b, 128)
+        for k in (33, 100, 128):
+            s, i = k_scan(q, p, nm, cen, R, b, k)
+            assert np.array_equal(i, io[:, :k]), (Q, k)
+            assert np.array_equal(s.view(np.uint32), so[:, :k].view(np.uint32)), (Q, k)
+        s, i = k_scan(q, p[:77], nm[:77], cen, R, b, 100)
+        so, io = O.search_topk(q, p[:77], nm[:77], cen, R, b, 100)
+        assert np.array_equal(i, io) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits,d", [(2, 64), (3, 128)])
+def test_pair_rows_scan_large_k_with_ties(bits, d):
+    # 2-/3-bit pair rows (one query per block row of the pair scan: twelve wave lists of up
+    # to k entries merged by binary search), k = 64, 100, 128, with exact ties.
+    rs = np.random.RandomState(710 + bits + d)
+    N = 30_007
+    R, cen, p, nm = _db(rs, N, d, bits)
+    nm = nm.copy()
+    src = _plant_ties(rs, p, nm, 40, 5)
+    rows = k_pair_rows(p, d, bits)
+    for Q in (1, 3):
+        q = rs.randn(Q, d).astype(np.float32)
+        q[0] = O.dequantize_mse(p[src[:1]], np.ones(1, np.float32), bits, d, R, cen)[0]
+        so, io = O.search_topk(q, p, nm, cen, R, bits, 128)
+        for k in (64, 100, 128):
+            s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k)
+            assert np.array_equal(i, io[:, :k]), (Q, k)
+            assert np.array_equal(s.view(np.uint32), so[:, :k].view(np.uint32)), (Q, k)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_pairs_scan_large_k_with_ties(d):
+    # 4-bit pair rows, k = 64, 100 and 128: the multi-query filtered scan (a single query
+    # included: above k = 32 it takes one query too), the exact multi-query scan and the
+    # one-query pair scan, over 300k unit rows in which 60 rows appear eight times each
+    # (queries 0-9 point at them): bit-identical to the C restatement of the reference core.
+    rs = np.random.RandomState(128 + d)
+    N = 300_007
+    R, cen, p, nm = _db(rs, N, d, 4)
+    nm = nm / np.float32(np.sqrt(d))
+    src = _plant_ties(rs, p, nm, 60, 7)
+    pairs = k_pack_pairs(p, d)
+    for Q in (1, 64, 130):
+        q = rs.randn(Q, d).astype(np.float32)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+        t = min(Q, 10)
+        q[:t] = O.dequantize_mse(p[src[:t]], np.ones(t, np.float32), 4, d, R, cen)
+        s128, i128 = _cpu_search(q, p, nm, cen, R, 128)
+        for k in (64, 100, 128):
+            s, i = k_scan_pairs(q, pairs, nm, cen, R, k)
+            assert np.array_equal(i, i128[:, :k]), (Q, k)
+            assert np.array_equal(s.view(np.uint32), s128[:, :k].view(np.uint32)), (Q, k)
+        se, ie = k_scan_pairs(q, pairs, nm, cen, R, 100, exact=True)
+        assert np.array_equal(ie, i128[:, :100]), Q
+        assert np.array_equal(se.view(np.uint32), s128[:, :100].view(np.uint32)), Q
+
+
 # ------------------------------------------------------------------ decode attention
 @pytest.mark.parametrize("d,kb,vb", [(64, 4, 2), (128, 3, 4), (64, 2, 3)])
 def test_decode_attention_vs_f64(d, kb, vb):
@@ -1451,7 +1534,7 @@ def _check_prod_topk(s, i, ref, tol, k):
 def test_prod_scan_topk_vs_f64(d, b):
     rs = np.random.RandomState(5 * d + b)
     R, S, cen, mp, sg, g, nm = _prod_db(rs, 12000, d, b)
-    for Q, k in ((1, 10), (4, 1), (7, 32)):
+    for Q, k in ((1, 10), (4, 1), (7, 32), (1, 100), (3, 128)):
         q = rs.randn(Q, d).astype(np.float32)
         s, i = k_scan_prod(q, mp, sg, g, nm, cen, R, S, b, k)
         ref = O.prod_scores_f64(q, mp, sg, g, nm, b, d, R, cen, S)
@@ -1572,10 +1655,11 @@ def test_prod_pair_rows_equal_bitplane_prod_scan(d, b):
     rows = ops().pack_pair_rows(mp, b - 1, d)
     for Q in (1, 5):
         q = torch.randn(Q, d, generator=g, device=DEV).half()
-        s0, i0 = ops().ip_scan_topk_prod(q, mp, sg, rn, nm, T(cen), R, S, b, 10)
-        s1, i1 = ops().ip_scan_topk_prod_pair_rows(q, rows, sg, rn, nm, T(cen), R, S, b, 10)
-        assert torch.equal(i0, i1)
-        assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+        for k in (10, 100):
+            s0, i0 = ops().ip_scan_topk_prod(q, mp, sg, rn, nm, T(cen), R, S, b, k)
+            s1, i1 = ops().ip_scan_topk_prod_pair_rows(q, rows, sg, rn, nm, T(cen), R, S, b, k)
+            assert torch.equal(i0, i1), (Q, k)
+            assert torch.equal(s0.view(torch.int32), s1.view(torch.int32)), (Q, k)
     qa = torch.randn(2, 3, d, generator=g, device=DEV)
     a0 = ops().attention_scores_prod(qa, mp[:5000], sg[:5000], rn[:5000], nm[:5000], T(cen), R, S, b)
     a1 = ops().attention_scores_prod_pair_rows(qa, rows[:5000], sg[:5000], rn[:5000], nm[:5000],

@@ -78,8 +78,8 @@ def test_capi_rejects_bad_arguments_without_launching():
     rc = lib.tq_rotate_and_quantize(z, 0, 0, capi.i64(4), capi.i32(300), z, z, capi.i32(4), z, z, z)
     assert rc == 1 and b"dim" in lib.tq_last_error()
     rc = lib.tq_ip_scan_topk(z, 0, capi.i64(1), capi.i32(64), z, z, capi.i64(10), z, z,
-                             capi.i32(4), capi.i32(100), z, z, z, ctypes.c_size_t(0), z)
-    assert rc == 1 and b"k must be" in lib.tq_last_error()
+                             capi.i32(4), capi.i32(129), z, z, z, ctypes.c_size_t(0), z)
+    assert rc == 1 and b"k must be in [1, 128]" in lib.tq_last_error()
     rc = lib.tq_decode_attention_packed(z, 0, capi.i32(1), capi.i32(6), capi.i32(4), capi.i32(64),
                                         z, z, z, z, capi.i64(8), z, z, z, z, z, capi.i32(4),
                                         capi.i32(2), ctypes.c_float(1.0), z, z, z, ctypes.c_size_t(0), z)

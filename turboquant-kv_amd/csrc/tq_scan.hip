@@ -42,8 +42,12 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxK = 32;
-constexpr int kCandCap = 64 + kMaxK;  // per (wave, query) candidate slots
+constexpr int kMaxK = 128;           // top-k of the fused scans
+constexpr int kSmallK = 32;          // the one-query filter and the small-list paths
+// Candidate slots per (wave, query) of the exact scans' top-k lists, in dynamic LDS: room
+// for the k kept entries plus one 64-row step of new ones.
+__host__ __device__ constexpr int cand_cap(int k) { return k <= kSmallK ? 96 : 192; }
+constexpr int kCandRegs = cand_cap(kMaxK) / 64;  // list entries per lane in wave_compact
 constexpr int kValTokens = 256;       // tokens staged per values chunk
 constexpr int kSplitTokens = 1024;    // tokens per values split (decode / values op)
 
@@ -71,6 +75,7 @@ struct ScanArgs {
   int qps;                  // queries per stream
   float post_scale;         // multiplies norm * sum (decode: softmax scale)
   int k;
+  int ccap;                 // TOPK: cand_cap(k), the dynamic LDS lists' slots
   float* part_s;            // TOPK: [nq_total][gridDim.x][k]
   int32_t* part_i;
   float* scores;            // ALL:  [nq_total][stream_rows]
@@ -177,27 +182,34 @@ __device__ __forceinline__ bool better(float sa, int ia, float sb, int ib) {
   return (sa > sb) | ((sa == sb) & (ia < ib));
 }
 
-// Reduce a wave's candidate list (cs/ci, `count` entries, count <= 128) to its best
-// min(count, k) entries in sorted order.  Wave-uniform arguments.
-__device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int k, float& th,
-                                             int& thi) {
+// Reduce a wave's candidate list (cs/ci, `count` entries, count <= 64 R) to its best
+// min(count, k) entries in sorted order: every entry counts the entries better than it
+// and moves to that rank.  Wave-uniform arguments.
+template <int R>
+__device__ __forceinline__ void wave_compact_r(float* cs, int* ci, int& count, int k, float& th,
+                                               int& thi) {
   const int lane = threadIdx.x & 63;
-  const bool v0 = lane < count, v1 = lane + 64 < count;
-  float s0 = 0.f, s1 = 0.f;
-  int i0 = 0, i1 = 0;
-  if (v0) { s0 = cs[lane]; i0 = ci[lane]; }
-  if (v1) { s1 = cs[lane + 64]; i1 = ci[lane + 64]; }
-  int r0 = 0, r1 = 0;
+  float s[R];
+  int id[R], rk[R];
+  bool v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    v[r] = lane + 64 * r < count;
+    s[r] = v[r] ? cs[lane + 64 * r] : 0.f;
+    id[r] = v[r] ? ci[lane + 64 * r] : 0;
+    rk[r] = 0;
+  }
   for (int e = 0; e < count; ++e) {
     const float se = cs[e];
     const int ie = ci[e];
-    r0 += better(se, ie, s0, i0);
-    r1 += better(se, ie, s1, i1);
+#pragma unroll
+    for (int r = 0; r < R; ++r) rk[r] += better(se, ie, s[r], id[r]);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-  if (v0 && r0 < k) { cs[r0] = s0; ci[r0] = i0; }
-  if (v1 && r1 < k) { cs[r1] = s1; ci[r1] = i1; }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (v[r] && rk[r] < k) { cs[rk[r]] = s[r]; ci[rk[r]] = id[r]; }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   count = count < k ? count : k;
@@ -205,6 +217,24 @@ __device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int
     th = cs[k - 1];
     thi = ci[k - 1];
   }
+}
+
+// wave_compact_r for lists of up to cand_cap(kMaxK) entries.
+__device__ __forceinline__ void wave_compact(float* cs, int* ci, int& count, int k, float& th,
+                                             int& thi) {
+  if (count <= 128) wave_compact_r<2>(cs, ci, count, k, th, thi);  // uniform
+  else wave_compact_r<kCandRegs>(cs, ci, count, k, th, thi);
+}
+
+// Rank of (s, id) among the n entries of a best-first list: the entries better than it,
+// by binary search (ids are distinct, so no entry of another list equals it).
+__device__ __forceinline__ int sorted_rank(const float* ls, const int* li, int n, float s, int id) {
+  int lo = 0, hi = n;  // entries [0, lo) are better, [hi, n) are not
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (better(ls[mid], li[mid], s, id)) lo = mid + 1; else hi = mid;
+  }
+  return lo;
 }
 
 // The block's query tables in LDS.  q_rot[j] = sum_k q[k] * R[j][k] with k ascending and
@@ -324,13 +354,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) char lut_s[QB * QSTRIDE];
   constexpr int SW = GENERIC ? 8 : BPP / 4;         // sign-row words (prod mode)
   __shared__ __attribute__((aligned(16))) char sgn_s[PROD ? QB * DP * 16 : 16];
-  __shared__ float cand_s[TOPK ? kWaves * QB * kCandCap : 1];
-  __shared__ int cand_i[TOPK ? kWaves * QB * kCandCap : 1];
+  // TOPK: kWaves * QB lists of a.ccap (score, id) slots in dynamic LDS
+  extern __shared__ __attribute__((aligned(16))) char dyn_s[];
+  const int ccap = TOPK ? a.ccap : 0;
+  float* cand_s = reinterpret_cast<float*>(dyn_s);
+  int* cand_i = reinterpret_cast<int*>(dyn_s) + kWaves * QB * ccap;
   __shared__ int cnt_s[TOPK ? kWaves * QB : 1];
 
   const int s = blockIdx.z;
   const int qb = blockIdx.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   int64_t nrows = a.nrows;
   if (a.seq_lens) {
     const int64_t sl = a.seq_lens[s / a.spb];
@@ -359,8 +392,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
   int cnt[QB];
 #pragma unroll
   for (int qi = 0; qi < QB; ++qi) { th[qi] = -INFINITY; thi[qi] = INT_MAX; cnt[qi] = 0; }
-  float* my_cs = cand_s + wave * QB * kCandCap;
-  int* my_ci = cand_i + wave * QB * kCandCap;
+  float* my_cs = cand_s + wave * QB * ccap;
+  int* my_ci = cand_i + wave * QB * ccap;
 
   int64_t row = rbeg + wave * 64 + lane;
   // Loads are unconditional (rows past the end re-read the last row and are masked
@@ -532,9 +565,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
         uint64_t mask = __ballot(pred);
         int nnew = __popcll(mask);
         if (nnew == 0) continue;
-        float* cs = my_cs + qi * kCandCap;
-        int* ci = my_ci + qi * kCandCap;
-        if (cnt[qi] + nnew > kCandCap) {
+        float* cs = my_cs + qi * ccap;
+        int* ci = my_ci + qi * ccap;
+        if (cnt[qi] + nnew > ccap) {
           wave_compact(cs, ci, cnt[qi], a.k, th[qi], thi[qi]);
           pred = valid & better(sc, id, th[qi], thi[qi]);
           mask = __ballot(pred);
@@ -585,12 +618,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int qi = 0; qi < QB; ++qi) {
       if (qi >= nq) break;
-      if (cnt[qi] > a.k) wave_compact(my_cs + qi * kCandCap, my_ci + qi * kCandCap, cnt[qi], a.k,
-                                      th[qi], thi[qi]);
+      // every wave list leaves sorted (best first) with at most k entries
+      if (cnt[qi] > 1) wave_compact(my_cs + qi * ccap, my_ci + qi * ccap, cnt[qi], a.k, th[qi], thi[qi]);
       if (lane == 0) cnt_s[wave * QB + qi] = cnt[qi];
     }
     __syncthreads();
-    // Merge the 4 wave lists of query qi (<= 4k <= 128 entries): wave qi % 4.
+    // Merge the 4 wave lists of query qi (<= 4k entries): wave qi % 4.
     for (int qi = wave; qi < nq; qi += kWaves) {
       int total = 0;
       int off[kWaves];
@@ -602,21 +635,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int t = 1; t < kWaves; ++t) w += (e >= off[t]);
         const int slot = e - off[w];
-        sc = cand_s[(w * QB + qi) * kCandCap + slot];
-        id = cand_i[(w * QB + qi) * kCandCap + slot];
+        sc = cand_s[(w * QB + qi) * ccap + slot];
+        id = cand_i[(w * QB + qi) * ccap + slot];
       };
       float* ps = a.part_s + ((size_t)(q0 + qi) * gridDim.x + blockIdx.x) * a.k;
       int32_t* pi = a.part_i + ((size_t)(q0 + qi) * gridDim.x + blockIdx.x) * a.k;
-      for (int e = lane; e < 2 * 64; e += 64) {
-        if (e < total) {
-          float se; int ie;
-          fetch(e, se, ie);
-          int rank = 0;
-          for (int f = 0; f < total; ++f) {
-            float sf; int jf;
-            fetch(f, sf, jf);
-            rank += better(sf, jf, se, ie);
+      if (total <= 128) {  // uniform
+        for (int e = lane; e < 2 * 64; e += 64) {
+          if (e < total) {
+            float se; int ie;
+            fetch(e, se, ie);
+            int rank = 0;
+            for (int f = 0; f < total; ++f) {
+              float sf; int jf;
+              fetch(f, sf, jf);
+              rank += better(sf, jf, se, ie);
+            }
+            if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
           }
+        }
+      } else {
+        // long lists: an entry's rank is its slot in its own sorted list plus, per other
+        // wave's list, the entries better than it (binary search)
+        for (int e = lane; e < total; e += 64) {
+          int w = 0;
+#pragma unroll
+          for (int t = 1; t < kWaves; ++t) w += (e >= off[t]);
+          const int slot = e - off[w];
+          const float se = cand_s[(w * QB + qi) * ccap + slot];
+          const int ie = cand_i[(w * QB + qi) * ccap + slot];
+          int rank = slot;
+#pragma unroll
+          for (int t = 0; t < kWaves; ++t)
+            if (t != w)
+              rank += sorted_rank(cand_s + (t * QB + qi) * ccap, cand_i + (t * QB + qi) * ccap,
+                                  cnt_s[t * QB + qi], se, ie);
           if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
         }
       }
@@ -809,10 +862,15 @@ __device__ __forceinline__ void wave_sort128(float (&s)[2], int (&id)[2]) {
   }
 }
 
-// Reduce a wave's candidate list (count <= 128 entries) to its best min(count, k) in
-// sorted order; th/thi become the k-th best once there are k.  Wave-uniform arguments.
+// Reduce a wave's candidate list to its best min(count, k) in sorted order; th/thi become
+// the k-th best once there are k.  Up to 128 entries: a bitonic sort in registers; longer
+// lists (k above 64): wave_compact_r's ranking.  Wave-uniform arguments.
 __device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count, int k, float& th,
                                                   int& thi) {
+  if (count > 128) {  // uniform
+    wave_compact_r<kCandRegs>(cs, ci, count, k, th, thi);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   float s[2];
   int id[2];
@@ -827,12 +885,14 @@ __device__ __forceinline__ void wave_compact_sort(float* cs, int* ci, int& count
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   if (lane < k && lane < count) { cs[lane] = s[0]; ci[lane] = id[0]; }
+  if (lane + 64 < k && lane + 64 < count) { cs[lane + 64] = s[1]; ci[lane + 64] = id[1]; }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   count = count < k ? count : k;
   if (count == k) {
-    th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s[0]), k - 1));
-    thi = __builtin_amdgcn_readlane(id[0], k - 1);
+    const bool hi = k > 64;  // uniform: entry k - 1 is in register hi, lane (k - 1) & 63
+    th = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hi ? s[1] : s[0]), (k - 1) & 63));
+    thi = __builtin_amdgcn_readlane(hi ? id[1] : id[0], (k - 1) & 63);
   }
 }
 
@@ -863,15 +923,18 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
   __shared__ float qr_s[D];
   __shared__ float qss_s[PROD ? D : 1];
   __shared__ float cen_s[16];
-  __shared__ float cand_s[TOPK ? kPsWaves * kCandCap : 1];
-  __shared__ int cand_i[TOPK ? kPsWaves * kCandCap : 1];
+  // TOPK: kPsWaves lists of a.ccap (score, id) slots in dynamic LDS
+  extern __shared__ __attribute__((aligned(16))) char dyn_s[];
+  const int ccap = TOPK ? a.ccap : 0;
+  float* cand_s = reinterpret_cast<float*>(dyn_s);
+  int* cand_i = reinterpret_cast<int*>(dyn_s) + kPsWaves * ccap;
   __shared__ int cnt_s[TOPK ? kPsWaves : 1];
   __shared__ float bnd_s;
   __shared__ int bnd_i;
 
   const int s = blockIdx.z;
   const int q0 = s * a.qps + blockIdx.y;  // this block's query
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int tid = threadIdx.x;
 
   // ---- this wave's rows
@@ -995,8 +1058,8 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
   float th = -INFINITY;
   int thi = INT_MAX;
   int cnt = 0;
-  float* cs = cand_s + wave * kCandCap;
-  int* ci = cand_i + wave * kCandCap;
+  float* cs = cand_s + wave * ccap;
+  int* ci = cand_i + wave * ccap;
 
   auto score = [&](const RowBuf& rb) {
     float acc;
@@ -1034,7 +1097,7 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
       uint64_t mask = __ballot(pred);
       int nnew = __popcll(mask);
       if (nnew == 0) return;
-      if (cnt + nnew > kCandCap) {
+      if (cnt + nnew > ccap) {
         const float bs = th;
         const int bi = thi;
         wave_compact_sort(cs, ci, cnt, a.k, th, thi);
@@ -1090,12 +1153,13 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
           const int e = lane + 64 * r;
           const int w = e / kTake, j = e - w * kTake;
           const bool ok = w < kPsWaves && j < cnt_s[w < kPsWaves ? w : 0];
-          sv[r] = ok ? cand_s[w * kCandCap + j] : -INFINITY;
-          iv[r] = ok ? cand_i[w * kCandCap + j] : INT_MAX;
+          sv[r] = ok ? cand_s[w * ccap + j] : -INFINITY;
+          iv[r] = ok ? cand_i[w * ccap + j] : INT_MAX;
         }
         wave_sort128(sv, iv);
-        const float bs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[0]), a.k - 1));
-        const int bi = __builtin_amdgcn_readlane(iv[0], a.k - 1);
+        const bool hi = a.k > 64;  // uniform: entry k - 1 in register hi
+        const float bs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hi ? sv[1] : sv[0]), (a.k - 1) & 63));
+        const int bi = __builtin_amdgcn_readlane(hi ? iv[1] : iv[0], (a.k - 1) & 63);
         if (lane == 0) { bnd_s = bs; bnd_i = bi; }  // (-inf, INT_MAX): fewer than k rows
       }
       __syncthreads();
@@ -1119,51 +1183,55 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
   }
 
   if constexpr (TOPK) {
-    if (cnt > a.k) wave_compact_sort(cs, ci, cnt, a.k, th, thi);
+    // every wave list leaves sorted (best first) with at most k entries
+    if (cnt > 1) wave_compact_sort(cs, ci, cnt, a.k, th, thi);
     if (lane == 0) cnt_s[wave] = cnt;
     __syncthreads();
-    // wave 0: the block's best k of the wave lists (<= k entries each)
-    if (wave == 0) {
-      int total = 0;
-      int off[kPsWaves];
+    int total = 0;
+    int off[kPsWaves];
 #pragma unroll
-      for (int w = 0; w < kPsWaves; ++w) { off[w] = total; total += cnt_s[w]; }
-      auto fetch = [&](int e, float& sc, int& id) {
-        int w = 0;
-#pragma unroll
-        for (int t = 1; t < kPsWaves; ++t) w += (e >= off[t]);
-        const int slot = e - off[w];
-        sc = cand_s[w * kCandCap + slot];
-        id = cand_i[w * kCandCap + slot];
-      };
-      float* ps = a.part_s + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
-      int32_t* pi = a.part_i + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
-      if (total <= 128) {
+    for (int w = 0; w < kPsWaves; ++w) { off[w] = total; total += cnt_s[w]; }
+    float* ps = a.part_s + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
+    int32_t* pi = a.part_i + ((size_t)q0 * gridDim.x + blockIdx.x) * a.k;
+    if (total <= 128) {  // uniform; wave 0 sorts the union
+      if (wave == 0) {
         float sv[2];
         int iv[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int e = lane + 64 * r;
-          if (e < total) fetch(e, sv[r], iv[r]);
-          else { sv[r] = -INFINITY; iv[r] = INT_MAX; }
+          int w = 0;
+#pragma unroll
+          for (int t = 1; t < kPsWaves; ++t) w += (e >= off[t]);
+          const bool ok = e < total;
+          sv[r] = ok ? cand_s[w * ccap + e - off[w]] : -INFINITY;
+          iv[r] = ok ? cand_i[w * ccap + e - off[w]] : INT_MAX;
         }
         wave_sort128(sv, iv);
         if (lane < a.k) {
           ps[lane] = lane < total ? sv[0] : -INFINITY;
           pi[lane] = lane < total ? iv[0] : -1;
         }
-      } else {  // k > 10: rank every entry of the union
-        for (int e = lane; e < total; e += 64) {
-          float se; int ie;
-          fetch(e, se, ie);
-          int rank = 0;
-          for (int f = 0; f < total; ++f) {
-            float sf; int jf;
-            fetch(f, sf, jf);
-            rank += better(sf, jf, se, ie);
-          }
-          if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
+        if (lane + 64 < a.k) {
+          ps[lane + 64] = lane + 64 < total ? sv[1] : -INFINITY;
+          pi[lane + 64] = lane + 64 < total ? iv[1] : -1;
         }
+      }
+    } else {
+      // an entry's rank: its slot in its own sorted list plus, per other wave's list, the
+      // entries better than it (binary search); total > 128 >= k, so no pads
+      for (int e = threadIdx.x; e < total; e += kPsThreads) {
+        int w = 0;
+#pragma unroll
+        for (int t = 1; t < kPsWaves; ++t) w += (e >= off[t]);
+        const int slot = e - off[w];
+        const float se = cand_s[w * ccap + slot];
+        const int ie = cand_i[w * ccap + slot];
+        int rank = slot;
+#pragma unroll
+        for (int t = 0; t < kPsWaves; ++t)
+          if (t != w) rank += sorted_rank(cand_s + t * ccap, cand_i + t * ccap, cnt_s[t], se, ie);
+        if (rank < a.k) { ps[rank] = se; pi[rank] = ie; }
       }
     }
   }
@@ -1424,6 +1492,10 @@ __device__ void merge_query_regs(const float* __restrict__ part_s, const int32_t
   merge_query(part_s, part_i, nblocks, k, q, out_s, out_i);
 }
 
+__device__ void merge_query_big(const float* __restrict__ part_s, const int32_t* __restrict__ part_i,
+                                int nblocks, int k, int q, float* __restrict__ out_s,
+                                int64_t* __restrict__ out_i);
+
 __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict__ part_s,
                                                          const int32_t* __restrict__ part_i,
                                                          int nblocks, int k,
@@ -1431,7 +1503,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(const float* __restrict
                                                          int64_t* __restrict__ out_i,
                                                          const int32_t* __restrict__ qflag) {
   if (qflag && !qflag[blockIdx.x]) return;  // only flagged queries (uniform)
-  if (nblocks * k <= kThreads * kMergeRegs)  // uniform
+  if (k > kSmallK)  // uniform
+    merge_query_big(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
+  else if (nblocks * k <= kThreads * kMergeRegs)  // uniform
     merge_query_regs(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
   else
     merge_query(part_s, part_i, nblocks, k, blockIdx.x, out_s, out_i);
@@ -1690,6 +1764,119 @@ __device__ __forceinline__ int rank1(const float* s, const int* id, int n, float
     r0 += (f + 3 < n) & better(a.w, b.w, s0, i0);
   }
   return r0;
+}
+
+// merge_query for k above kSmallK, where 64 group maxima no longer bound the k-th best.
+// Per query, for all kThreads threads of a block:
+//   1. tau = the k-th largest score among the leading ceil(k / nblocks) entries of every
+//      block list (a 32-step binary search on order-preserving keys): those are k distinct
+//      rows, so the k-th best score overall is at least tau.
+//   2. Per list, the entries scoring at least tau (a prefix: the lists are best first, pads
+//      (-inf, -1) last) are counted by binary search and gathered into LDS.
+//   3. The survivors are ranked (score desc, id asc) and the best k written.
+// More than kBigMergeCap survivors (many rows tied at tau) fall back to merge_query.
+constexpr int kBigMergeCap = 2048;
+__device__ void merge_query_big(const float* __restrict__ part_s, const int32_t* __restrict__ part_i,
+                                int nblocks, int k, int q, float* __restrict__ out_s,
+                                int64_t* __restrict__ out_i) {
+  constexpr int CR = (kThreads * kMaxBlocksPerLane + kMaxK + kThreads - 1) / kThreads;  // candidates / thread
+  __shared__ __attribute__((aligned(16))) float bss[kBigMergeCap + 4];
+  __shared__ __attribute__((aligned(16))) int bsi[kBigMergeCap + 4];
+  __shared__ int brk[kBigMergeCap];
+  __shared__ int bcnt[33];
+  __shared__ int bpart[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* ps = part_s + (size_t)q * nblocks * k;
+  const int32_t* pi = part_i + (size_t)q * nblocks * k;
+  const int depth = (k + nblocks - 1) / nblocks;
+  const int ncand = nblocks * depth;
+  // 1. candidate keys (0: a pad, below every real key), all loads in flight together
+  uint32_t u[CR];
+#pragma unroll
+  for (int j = 0; j < CR; ++j) {
+    const int c = tid + j * kThreads;
+    const int cc = c < ncand ? c : ncand - 1;
+    const int b = cc / depth, pos = cc - b * depth;
+    const int id = pi[(size_t)b * k + pos];
+    const float sc = ps[(size_t)b * k + pos];
+    u[j] = (c < ncand) & (id >= 0) ? fs_fkey(sc) : 0u;
+  }
+  if (tid < 33) bcnt[tid] = 0;
+  __syncthreads();
+  uint32_t x = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t t = x | (1u << bit);
+    int c = 0;  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < CR; ++j) c += __popcll(__ballot(u[j] >= t));
+    if (lane == 0 && c) atomicAdd(&bcnt[bit], c);
+    __syncthreads();
+    if (bcnt[bit] >= k) x = t;
+  }
+  const float tau = x ? fs_unkey(x) : -INFINITY;
+  // 2. survivors per list: the prefix whose entries are real and score >= tau
+  int cnt[kMaxBlocksPerLane];
+  int mine = 0;
+#pragma unroll
+  for (int r = 0; r < kMaxBlocksPerLane; ++r) {
+    const int b = tid + r * kThreads;
+    int lo = 0;
+    if (b < nblocks) {
+      const float* ls = ps + (size_t)b * k;
+      const int32_t* li = pi + (size_t)b * k;
+      if ((li[0] >= 0) & (ls[0] >= tau)) {
+        int hi = k;  // entries [0, lo) pass, [hi, k) do not
+        lo = 1;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((li[mid] >= 0) & (ls[mid] >= tau)) lo = mid + 1; else hi = mid;
+        }
+      }
+    }
+    cnt[r] = lo;
+    mine += lo;
+  }
+  // block exclusive prefix sum of the per-thread counts
+  int incl = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  if (lane == 63) bpart[wave] = incl;
+  __syncthreads();
+  int base = incl - mine;
+  int S = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    base += w < wave ? bpart[w] : 0;
+    S += bpart[w];
+  }
+  if (S > kBigMergeCap) {  // uniform
+    merge_query(part_s, part_i, nblocks, k, q, out_s, out_i);
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < kMaxBlocksPerLane; ++r) {
+    const int b = tid + r * kThreads;
+    for (int e = 0; e < cnt[r]; ++e) {
+      bss[base + e] = ps[(size_t)b * k + e];
+      bsi[base + e] = pi[(size_t)b * k + e];
+    }
+    base += cnt[r];
+  }
+  for (int e = S + tid; e < ((S + 3) & ~3); e += kThreads) { bss[e] = -INFINITY; bsi[e] = INT_MAX; }
+  for (int e = tid; e < S; e += kThreads) brk[e] = 0;
+  __syncthreads();
+  // 3. ranks, then the best k
+  block_rank<kThreads>(bss, bsi, S, brk, tid);
+  __syncthreads();
+  float* os = out_s + (size_t)q * k;
+  int64_t* oi = out_i + (size_t)q * k;
+  for (int e = tid; e < S; e += kThreads)
+    if (brk[e] < k) { os[brk[e]] = bss[e]; oi[brk[e]] = bsi[e]; }
+  for (int e = S + tid; e < k; e += kThreads) { os[e] = -INFINITY; oi[e] = -1; }
 }
 
 // (th, thi) from the list's k-th best (lo, id) when it holds k entries or more (kept if
@@ -2294,6 +2481,7 @@ constexpr int kMqSampleGroups = 4096;    // 64-row groups sampled for tau
 constexpr int kMqGroupsPerWave = 2;      // sampled groups per wave (one bucket per wave)
 constexpr int kMqMaxBuckets = 256;       // bucket maxima per query (one per sample block)
 constexpr int kMqMergeCap = 6144;        // listed entries a query's merge holds in LDS
+constexpr int kMqMergeCapBig = 12288;    // the same for k above kSmallK (147 KB of LDS)
 constexpr int kMqTilesPerRound = 8;      // query tiles per filter launch
 constexpr int kMqFallbackBlocks = 128;   // row blocks of the exact fallback scan
 static_assert(kMqSampleGroups / (kMqWaves * kMqGroupsPerWave) <= kMqMaxBuckets, "bucket count");
@@ -2773,15 +2961,16 @@ mq_filter_kernel(MqArgs a) {
 
 // Per query: the listed rows of every block, tau' = their k-th best lo, the rows whose hi
 // reaches it rescored exactly and ranked.  More than kMqCap rows listed by one block, or
-// more than kMqMergeCap in all, flags the query for the exact fallback instead.
-template <int D>
+// more than MCAP in all, flags the query for the exact fallback instead.
+template <int D, int MCAP>
 __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
-  __shared__ __attribute__((aligned(16))) float ehi[kMqMergeCap];
-  __shared__ __attribute__((aligned(16))) float elo[kMqMergeCap];
-  __shared__ __attribute__((aligned(16))) int eid[kMqMergeCap];
+  __shared__ __attribute__((aligned(16))) float ehi[MCAP];
+  __shared__ __attribute__((aligned(16))) float elo[MCAP];
+  __shared__ __attribute__((aligned(16))) int eid[MCAP];
   __shared__ int off_s[kMqThreads + 1];
   __shared__ int part[kMqWaves];
-  __shared__ int bad_s, m2_s, nvalid_s, tot_s;
+  __shared__ int tcnt[32];
+  __shared__ int bad_s, m2_s, nvalid_s;
   __shared__ float qr_s[D];
   __shared__ float cen_s[16];
   const int ql = blockIdx.x % kMqQ, rtile = blockIdx.x / kMqQ;
@@ -2809,7 +2998,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   if (tid == kMqThreads - 1) off_s[kMqThreads] = wofs + incl;
   __syncthreads();
   const int M = off_s[kMqThreads];
-  if (bad_s || M > kMqMergeCap) {
+  if (bad_s || M > MCAP) {
     if (tid == 0) a.flag[q] = 1;
     return;  // uniform
   }
@@ -2831,41 +3020,38 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   if (tid < D) qr_s[tid] = a.qrot[(size_t)q * D + tid];
   if (tid < 16) cen_s[tid] = a.cen[tid];
   __syncthreads();
-  // tau' = max(tau, k-th best lo): wave 0 alone, a 32-step binary search on keys (the first
-  // 1024 entries in registers, the rest read from LDS).  Up to one entry per thread every
-  // entry is rescored anyway: no search.
-  constexpr int EPT = (kMqMergeCap + kMqThreads - 1) / kMqThreads;
-  constexpr int RK = 16;
-  if (tid == 0) tot_s = 0;
-  if (wave == 0 && M > kMqThreads) {
-    uint32_t u[RK];
+  // tau' = max(tau, k-th best lo): a 32-step binary search on keys, every thread holding
+  // its EPT entries' keys (per step a compare mask and a popcount per register, one LDS
+  // add per wave).  Up to one entry per thread every entry is rescored anyway: no search.
+  constexpr int EPT = (MCAP + kMqThreads - 1) / kMqThreads;
+  if (tid < 32) tcnt[tid] = 0;
+  uint32_t x = 0;
+  if (M > kMqThreads) {  // uniform
+    uint32_t u[EPT];
 #pragma unroll
-    for (int j = 0; j < RK; ++j) {
-      const int e = j * 64 + lane;
+    for (int j = 0; j < EPT; ++j) {
+      const int e = j * kMqThreads + tid;
       u[j] = (e < M && elo[e] > -INFINITY) ? fs_fkey(elo[e]) : 0u;
     }
-    uint32_t x = 0;
+    __syncthreads();
 #pragma unroll 1
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t t = x | (1u << bit);
-      int cc = 0;  // wave-uniform: popcounts of compare masks
+      int cc = 0;  // wave-uniform
 #pragma unroll
-      for (int j = 0; j < RK; ++j) cc += __popcll(__ballot(u[j] >= t));
-      for (int e0 = RK * 64; e0 < M; e0 += 64) {
-        const int e = e0 + lane;
-        cc += __popcll(__ballot((e < M) && (elo[e] > -INFINITY) && (fs_fkey(elo[e]) >= t)));
-      }
-      if (cc >= k) x = t;
+      for (int j = 0; j < EPT; ++j)
+        if (j * kMqThreads < M) cc += __popcll(__ballot(u[j] >= t));
+      if (lane == 0 && cc) atomicAdd(&tcnt[bit], cc);
+      __syncthreads();
+      if (tcnt[bit] >= k) x = t;
     }
-    if (lane == 0) tot_s = (int)x;
   }
-  __syncthreads();
-  const uint32_t x = (uint32_t)tot_s;
   const float tk = x ? fs_unkey(x) : -INFINITY;
   const float tau2 = fmaxf(a.tau[q], tk);
   // survivors: entries whose hi reaches tau'; their ids move to the front of eid (every
   // entry is read before any is overwritten; order does not matter, the ranking orders them)
   if (tid == 0) { m2_s = 0; nvalid_s = 0; }
+  __syncthreads();
   int my[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
@@ -3112,8 +3298,11 @@ template <int BITS, int BPP, int QB, bool TOPK, bool GENERIC, bool PAIRS = false
 int launch_scan_t(const ScanArgs& a, dim3 grid, hipStream_t st) {
   static_assert(QB * 8 * (GENERIC ? 32 : BPP) * ((1 << BITS) * 4 + (PROD ? 16 : 0)) <= 48 * 1024,
                 "table too large");
-  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC, PAIRS, PROD>), grid, dim3(kThreads), 0,
-                     st, a);
+  ScanArgs b = a;
+  b.ccap = TOPK ? cand_cap(a.k) : 0;
+  const size_t lds = TOPK ? (size_t)kWaves * QB * b.ccap * 8 : 0;  // the top-k lists
+  hipLaunchKernelGGL((scan_kernel<BITS, BPP, QB, TOPK, GENERIC, PAIRS, PROD>), grid, dim3(kThreads), lds,
+                     st, b);
   TQ_LAUNCH_CHECK("scan_kernel");
   return TQ_OK;
 }
@@ -3166,8 +3355,11 @@ int pair_scan_blocks(int64_t nrows) {
 
 template <bool TOPK, int BITS, bool PROD = false>
 int launch_pair_scan_b(const ScanArgs& a, dim3 grid, hipStream_t st) {
-  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK, BITS, PROD>), grid, dim3(kPsThreads), 0, st, a);
-  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK, BITS, PROD>), grid, dim3(kPsThreads), 0, st, a);
+  ScanArgs b = a;
+  b.ccap = TOPK ? cand_cap(a.k) : 0;
+  const size_t lds = TOPK ? (size_t)kPsWaves * b.ccap * 8 : 0;  // the top-k lists
+  if (a.bpp == 16) hipLaunchKernelGGL((pair_scan_kernel<128, TOPK, BITS, PROD>), grid, dim3(kPsThreads), lds, st, b);
+  else hipLaunchKernelGGL((pair_scan_kernel<64, TOPK, BITS, PROD>), grid, dim3(kPsThreads), lds, st, b);
   TQ_LAUNCH_CHECK("pair_scan_kernel");
   return TQ_OK;
 }
@@ -3322,9 +3514,10 @@ MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
   return L;
 }
 
-// The multi-query filter applies to 4-bit pair rows of d 64 / 128 with at least two queries.
-bool mq_applies(int64_t nq, int d, int64_t N) {
-  return nq >= 2 && N > 0 && (d == 64 || d == 128);
+// The multi-query filter applies to 4-bit pair rows of d 64 / 128 with at least two
+// queries, or one query with k above the one-query filter's kSmallK.
+bool mq_applies(int64_t nq, int d, int64_t N, int k) {
+  return (nq >= 2 || (nq == 1 && k > kSmallK)) && N > 0 && (d == 64 || d == 128);
 }
 
 template <int D>
@@ -3353,7 +3546,10 @@ int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size
       hipLaunchKernelGGL((mq_filter_kernel<D, false>), fg, dim3(kMqThreads), 0, st, a);
     }
     TQ_LAUNCH_CHECK("mq_filter_kernel");
-    hipLaunchKernelGGL((mq_merge_kernel<D>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
+    if (a.k > kSmallK)
+      hipLaunchKernelGGL((mq_merge_kernel<D, kMqMergeCapBig>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((mq_merge_kernel<D, kMqMergeCap>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
     TQ_LAUNCH_CHECK("mq_merge_kernel");
     // The exact scan for the round's flagged queries (blocks of unflagged ones return).
     const int q0 = t0 * kMqQ;
@@ -3429,7 +3625,7 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
 
 size_t tq_scan_pairs_workspace_bytes(int64_t nq, int32_t d, int64_t N, int32_t k) {
   size_t bytes = tq_scan_workspace_bytes(nq, d, 4, N, k);
-  if (k >= 1 && k <= kMaxK && mq_applies(nq, d, N)) {
+  if (k >= 1 && k <= kMaxK && mq_applies(nq, d, N, k)) {
     const size_t mq = mq_layout(nq, d, N, k).total;
     if (mq > bytes) bytes = mq;
   }
@@ -3475,7 +3671,7 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   // Several queries over 4-bit pair rows: the multi-query filtered scan, when the
   // workspace holds its buffers (tq_scan_pairs_workspace_bytes); the exact multi-query
   // scan below otherwise.
-  if (pairs && bit_width == 4 && !prod && mq_applies(nq, d, N) && nq <= INT_MAX &&
+  if (pairs && bit_width == 4 && !prod && mq_applies(nq, d, N, k) && nq <= INT_MAX &&
       workspace_bytes >= mq_layout(nq, d, N, k).total)
     return launch_mq(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
                      out_scores, out_ids, static_cast<char*>(workspace), st);
@@ -3494,7 +3690,7 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   if (prod) set_prod(a, *prod);
   // One query over 4-bit pair rows: the filtered scan (approximate scores on the matrix
   // cores, the candidates rescored exactly).
-  if (pairs && bit_width == 4 && !prod && nq == 1 && (d == 64 || d == 128))
+  if (pairs && bit_width == 4 && !prod && nq == 1 && (d == 64 || d == 128) && k <= kSmallK)
     return launch_filter(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
                          out_scores, out_ids, static_cast<char*>(workspace) + 256, st);
   TQ_REQUIRE(nq <= 65535 * 4, "too many queries in one call");

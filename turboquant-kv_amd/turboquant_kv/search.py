@@ -41,9 +41,10 @@ HEADER_FORMAT = "<BII"  # bit_width u8, dim u32, n_vectors u32
 HEADER_SIZE = struct.calcsize(HEADER_FORMAT)
 MODE_MSE = 0
 MODE_PROD = 1
-_SCAN_MAX_K = 32  # the fused top-k kernel's per-call limit
-# Queries per scan launch: the scans' candidate lists grow with the query count (and a
-# launch takes at most 65,535 queries); larger batches run as consecutive launches.
+_SCAN_MAX_K = 128  # the fused top-k kernels' per-call limit
+# Queries per scan launch at k <= 32 (k above: proportionally fewer): the scans' per-block
+# candidate lists grow with queries x k (and a launch takes at most 65,535 queries);
+# larger batches run as consecutive launches.
 _SEARCH_CHUNK = 4096
 # k above _SCAN_MAX_K scores every row into a [Q, N] fp32 matrix: at most this many
 # score bytes per launch
@@ -214,14 +215,22 @@ class TurboQuantIndex:
         assert self.n_vectors > 0, "Index is empty"
         q = queries.to(self.device)
         k = min(k, self.n_vectors)
-        step = (_SEARCH_CHUNK if k <= _SCAN_MAX_K and (self.mode == "mse" or self.bit_width <= 4)
+        fused = k <= _SCAN_MAX_K and (self.mode == "mse" or self.bit_width <= 4)
+        step = (max(1, _SEARCH_CHUNK * 32 // max(k, 32)) if fused
                 else max(1, min(_SEARCH_CHUNK, _SCORE_BYTES // (4 * self.n_vectors))))
+        recon = None
+        if self.mode == "prod" and self.bit_width > 4:  # built once for every chunk
+            recon = _ops().dequantize_prod_packed(self._bitplane_codes(), self._qjl_signs,
+                                                  self._residual_norms, self._norms, self._cen,
+                                                  self._rot_dev, self._S_dev, self.bit_width,
+                                                  self.dim)
         if q.shape[0] <= step:
-            return self._search(q, k)
-        parts = [self._search(q[i:i + step], k) for i in range(0, q.shape[0], step)]
+            return self._search(q, k, recon)
+        parts = [self._search(q[i:i + step], k, recon) for i in range(0, q.shape[0], step)]
         return torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
 
-    def _search(self, q: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    def _search(self, q: torch.Tensor, k: int,
+                recon: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         if self.mode == "mse":
             if k <= _SCAN_MAX_K:
                 if self._pairs:
@@ -251,9 +260,11 @@ class TurboQuantIndex:
                           self._residual_norms, self._norms, self._cen, self._rot_dev, self._S_dev,
                           self.bit_width)[0]
             return _topk_lowest_index(s, k)
-        recon = _ops().dequantize_prod_packed(self._bitplane_codes(), self._qjl_signs,
-                                              self._residual_norms, self._norms, self._cen,
-                                              self._rot_dev, self._S_dev, self.bit_width, self.dim)
+        if recon is None:
+            recon = _ops().dequantize_prod_packed(self._bitplane_codes(), self._qjl_signs,
+                                                  self._residual_norms, self._norms, self._cen,
+                                                  self._rot_dev, self._S_dev, self.bit_width,
+                                                  self.dim)
         scores = q.float() @ recon.t()
         return _topk_lowest_index(scores, k)
 
