@@ -309,6 +309,30 @@ def bench_decode(args, extra):
             log(f"decode T={T} paged decode layout (block 64, shuffled): {ms_pdl * 1e3:.1f} us, "
                 f"{bytes_alg / ms_pdl / 1e6:.0f} GB/s")
             del pkp, pkn, pvt, pvn
+            # configs[4]'s K4/V3 cache in vLLM's default block-16 pools, blocks shuffled:
+            # random codes and norms (the kernel's time does not depend on their values)
+            bs, vb3 = 16, 3
+            nbs = T // bs
+            perm = torch.randperm(B * nbs, generator=g, device="cuda")
+            tab = perm.view(B, nbs).to(torch.int32)
+            pkp = torch.randint(0, 256, (B * nbs, Hkv, bs, d // 2), dtype=torch.uint8, device="cuda",
+                                generator=g)
+            pv3 = torch.randint(0, 256, (B * nbs, Hkv, bs // 16, 128 * vb3), dtype=torch.uint8,
+                                device="cuda", generator=g)
+            pkn = torch.rand(B * nbs, Hkv, bs, generator=g, device="cuda") + 0.5
+            pvn = torch.rand(B * nbs, Hkv, bs, generator=g, device="cuda") + 0.5
+            cv3 = lloyd_max_codebook(vb3, d)[1].cuda()
+            ms_v3 = time_op(lambda: ops.decode_attention_paged_dl(q, pkp, pkn, pv3, pvn, tab, sl, ck,
+                                                                  cv3, Rk, Rv, 1.0 / 8.0), 20, 3, settle_s=0.1)
+            bytes_v3 = B * Hkv * T * (d // 2 + 8 * vb3 + 4 + 4) + 2 * B * Hq * d * 2
+            extra["decode_attn_T32768_paged_K4V3_bs16"] = {
+                "us_per_step": ms_v3 * 1e3, "GBps": bytes_v3 / ms_v3 / 1e6,
+                "hbm_frac": bytes_v3 / ms_v3 / 1e6 / HBM_PEAK_GBS, "tokens_per_s": B / ms_v3 * 1e3,
+                "layout": "decode-layout pools, block 16 (16-token value sub-blocks of 384 B)",
+                "bytes_per_token_head": d // 2 + 8 * vb3 + 8}
+            log(f"decode T={T} paged K4/V3 decode layout (block 16, shuffled): {ms_v3 * 1e3:.1f} us, "
+                f"{bytes_v3 / ms_v3 / 1e6:.0f} GB/s")
+            del pkp, pkn, pv3, pvn
         del caches
     return out
 

@@ -433,41 +433,48 @@ int tq_decode_attention_paged(const void* q, tq_dtype q_dtype, int32_t B, int32_
                               size_t workspace_bytes, void* stream);
 
 /*
- * Paged pools in the decode layout (4-bit keys, 2-bit values, head_dim 64, any number of
- * query heads per KV head): the same kernel as tq_decode_attention_dl with block lookups
- * per 64-token tile (one for block
- * sizes >= 64, one per 16-token group below), for power-of-two block sizes >= 16.
- * Replaces, like tq_decode_attention_paged, the reference backend's forward
- * (turboquant_kv/vllm_plugin/__init__.py:209-304).
+ * Paged pools in the decode layout (4-bit keys, vbits = 2-4 bit values, head_dim 64, any
+ * number of query heads per KV head): the same kernel as tq_decode_attention_dl with block
+ * lookups per 64-token tile (one for block sizes >= 64, one per 16-token group below), for
+ * power-of-two block sizes >= 16.  Replaces, like tq_decode_attention_paged, the reference
+ * backend's forward (turboquant_kv/vllm_plugin/__init__.py:209-304).
  *   kpairs_pool [num_blocks][hkv][block_size][32]   key pair bytes (tq_pack_decode_layout,
  *                                                   values = 0) stored with tq_paged_store
- *   vtile_pool  block_size >= 64: [num_blocks][hkv][block_size/64][1024] value tiles
- *               (byte layout above); block_size 16, 32: [num_blocks][hkv][block_size/16]
- *               [256] sub-blocks, token t of one at byte 4*(16*sl + c) + dg, bits 2*(t%4),
- *               sl = t/4, dim 16*dg + c (bytes 16L + 4m + dg of a 64-token tile row are
- *               byte 4L + dg of its sub-block m)
+ *   vtile_pool  block_size >= 64: [num_blocks][hkv][block_size/64][512 * vbits] value
+ *               tiles (the byte layout of tq_pack_decode_layout's value tiles);
+ *               block_size 16, 32: [num_blocks][hkv][block_size/16][128 * vbits] sub-blocks,
+ *               each holding what its 16-token group m of a 64-token tile contributes.
+ *               With tt the token's offset in its sub-block, sl = tt/4, r = tt%4, dim
+ *               16*dg + c, L = 16*sl + c:
+ *                 vbits 2  byte 4L + dg, bits 2r (tile byte 16L + 4m + dg)
+ *                 vbits 4  byte 8L + 2dg + r/2, bits 4(r%2) (the two bytes that group m
+ *                          fills of tile word 4(m/2) + dg)
+ *                 vbits 3  dims below 48: byte 4L + 2dg + r/2 (dg 0, 1) or 256 + 2L + r/2
+ *                          (dg 2), bits 3(r%2); dims 48-63: code bit b is bit
+ *                          q = 3(r%2) + b of the pair index, stored at bit 6 + q%2 of the
+ *                          byte of share q/2 (the tile layout's spread of dim group 3)
  *   knorm_pool, vnorm_pool [num_blocks][hkv][block_size]
- * tq_paged_store_value_tiles writes new tokens' 2-bit value rows [n_tokens][hkv][16]
- * (bit planes) and norms [n_tokens][hkv] into their slots (slot_mapping as in
- * tq_paged_store; negative or out-of-pool slots skipped), leaving the other tokens of
- * each tile as they are.  Workspace: tq_decode_dl_workspace_bytes(B, hq, hkv,
- * max_blocks_per_seq * block_size).  Pools 16-byte aligned; num_blocks * hkv * block_size
- * < 2^32 rows (pools from 2 GiB on are read with 64-bit addresses; a block id outside the
- * pool reads the pool's last block).  Outputs as tq_decode_attention_dl's.
+ * tq_paged_store_value_tiles writes new tokens' vbits-bit value rows
+ * [n_tokens][hkv][8 * vbits] (bit planes) and norms [n_tokens][hkv] into their slots
+ * (slot_mapping as in tq_paged_store; negative or out-of-pool slots skipped), leaving the
+ * other tokens of each tile as they are.  Workspace: tq_decode_dl_workspace_bytes(B, hq,
+ * hkv, max_blocks_per_seq * block_size).  Pools 16-byte aligned; num_blocks * hkv *
+ * block_size < 2^32 rows (pools from 2 GiB on are read with 64-bit addresses; a block id
+ * outside the pool reads the pool's last block).  Outputs as tq_decode_attention_dl's.
  */
 int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
                                int32_t hkv, const int64_t* slot_mapping, uint8_t* vtile_pool,
                                float* vnorm_pool, int64_t num_blocks, int32_t block_size,
-                               void* stream);
+                               int32_t vbits, void* stream);
 int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
                                  int32_t d, const uint8_t* kpairs_pool, const float* knorm_pool,
                                  const uint8_t* vtile_pool, const float* vnorm_pool,
-                                 int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
-                                 int32_t max_blocks_per_seq, const int32_t* seq_lens,
-                                 const float* kcentroids, const float* vcentroids,
-                                 const float* krotation, const float* vrotation, float scale,
-                                 void* out, float* lse, void* workspace, size_t workspace_bytes,
-                                 void* stream);
+                                 int64_t num_blocks, int32_t block_size, int32_t vbits,
+                                 const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                 const int32_t* seq_lens, const float* kcentroids,
+                                 const float* vcentroids, const float* krotation,
+                                 const float* vrotation, float scale, void* out, float* lse,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Causal prefill of one sequence over decode-layout paged pools (the pools of
@@ -484,7 +491,7 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
                                   int32_t hkv, int32_t d, const uint8_t* kpairs_pool,
                                   const float* knorm_pool, const uint8_t* vtile_pool,
                                   const float* vnorm_pool, int64_t num_blocks, int32_t block_size,
-                                  const int32_t* block_table, int32_t max_blocks,
+                                  int32_t vbits, const int32_t* block_table, int32_t max_blocks,
                                   const float* kcentroids, const float* vcentroids,
                                   const float* krotation, const float* vrotation, float scale,
                                   float* out, void* stream);

@@ -197,7 +197,7 @@ def _bitplane_pools(pools, tab, lens):
     if "kp" not in st:
         return P
     nb, H, bs = st["kn"].shape
-    out = {"k": np.zeros((nb, H, bs, 32), np.uint8), "v": np.zeros((nb, H, bs, 16), np.uint8),
+    out = {"k": np.zeros((nb, H, bs, 32), np.uint8), "v": np.zeros((nb, H, bs, 8 * pools.vbits), np.uint8),
            "kn": np.zeros((nb, H, bs), np.float32), "vn": np.zeros((nb, H, bs), np.float32)}
     for j, n in enumerate(lens):
         bt = torch.from_numpy(tab[j]).to(DEV)
@@ -214,6 +214,8 @@ def _bitplane_pools(pools, tab, lens):
                                                    ("mse", 4, 2, 64, 4, "auto"),
                                                    ("mse", 4, 2, 64, 8, "auto"),
                                                    ("mse", 4, 2, 64, 7, "auto"),
+                                                   ("mse", 4, 3, 64, 4, "auto"),
+                                                   ("mse", 4, 4, 64, 2, "auto"),
                                                    ("mse", 3, 2, 128, 2, "auto"),
                                                    ("prod", 4, 3, 64, 2, "auto")])
 def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G, layout):
@@ -229,7 +231,7 @@ def test_vllm_paged_step_vs_f64(mode, kb, vb, d, G, layout):
                                   num_gpu_blocks=nb, pool_layout=layout)
     kv = TurboQuantPagedKVCache(cfg, num_layers=1, num_heads=Hkv, head_dim=d, device=DEV)
     pools = kv.pools()
-    assert pools.layout == ("decode" if (mode, kb, vb, d, layout) == ("mse", 4, 2, 64, "auto")
+    assert pools.layout == ("decode" if (mode, kb, d, layout) == ("mse", 4, 64, "auto")
                             else "bitplane")
     scale = 1.0 / math.sqrt(d)
     steps = [[40, 17, 70, 5], [30, 1, 1, 1]]   # new tokens per sequence in each step
@@ -301,8 +303,8 @@ def test_vllm_paged_protected_layer_and_padding():
 
 
 # ------------------------------------------------------------------ decode-layout pools
-def _dl_pools(rs, lens, bs, nb, width, Hkv):
-    """Random 4-bit key / 2-bit value bit-plane rows of every token, stored into
+def _dl_pools(rs, lens, bs, nb, width, Hkv, vb=2):
+    """Random 4-bit key / vb-bit value bit-plane rows of every token, stored into
     decode-layout block pools through the C ABI (values in two shuffled calls, so tiles are
     filled piecewise).  Returns the pools and each sequence's contiguous rows and norms."""
     from turboquant_kv import ops
@@ -311,13 +313,13 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv):
                      np.int64)
     n = len(slots)
     krows = rs.randint(0, 256, (n, Hkv, 32)).astype(np.uint8)
-    vrows = rs.randint(0, 256, (n, Hkv, 16)).astype(np.uint8)
+    vrows = rs.randint(0, 256, (n, Hkv, 8 * vb)).astype(np.uint8)
     kn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
     knp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
-    vt = (torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV) if bs >= 64 else
-          torch.zeros(nb, Hkv, bs // 16, 256, dtype=torch.uint8, device=DEV))
+    vt = (torch.zeros(nb, Hkv, bs // 64, 512 * vb, dtype=torch.uint8, device=DEV) if bs >= 64 else
+          torch.zeros(nb, Hkv, bs // 16, 128 * vb, dtype=torch.uint8, device=DEV))
     vnp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
     pairs = torch.empty(n * Hkv, 1, 32, dtype=torch.uint8, device=DEV)
     ops.pack_decode_layout(T(krows).view(n * Hkv, 1, 32), pairs, 64, 4, False, 0)
@@ -331,7 +333,7 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv):
         npart = np.concatenate([vn[part], vn[:1]])
         capi.check(L().tq_paged_store_value_tiles(capi.p(T(rp)), capi.p(T(npart)), capi.i64(len(sp)),
                                                   capi.i32(Hkv), capi.p(T(sp)), capi.p(vt), capi.p(vnp),
-                                                  capi.i64(nb), capi.i32(bs), capi.stream()))
+                                                  capi.i64(nb), capi.i32(bs), capi.i32(vb), capi.stream()))
     sync()
     seqs, o = [], 0
     for L_ in lens:
@@ -341,15 +343,18 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv):
     return tab, kp, knp, vt, vnp, seqs
 
 
+@pytest.mark.parametrize("vb", [2, 3, 4])
 @pytest.mark.parametrize("bs", [16, 32, 64, 128])
-def test_paged_dl_store_round_trip(bs):
+def test_paged_dl_store_round_trip(bs, vb):
+    # every bit of every token's value code lands where the decode kernel reads it: the
+    # pools gathered back into the contiguous decode layout unpack to the stored rows
     from turboquant_kv import ops
     from turboquant_kv.vllm_plugin.paged import gather_value_tiles
-    rs = np.random.RandomState(bs)
+    rs = np.random.RandomState(bs + vb)
     Hkv, lens = 2, [130, 64, 1, 0]
     width = (max(lens) + bs - 1) // bs + 1
     nb = sum((n + bs - 1) // bs for n in lens) + 3
-    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv, vb)
     for b, n in enumerate(lens):
         if n == 0:
             continue
@@ -360,17 +365,24 @@ def test_paged_dl_store_round_trip(bs):
         _, vnn = ops.paged_gather(kp, vnp, bt, one(n), n)
         kr, knr, vr, vnr = seqs[b]
         assert np.array_equal(ops.unpack_decode_layout(pr[0], 64, 4, False, 0, n).cpu().numpy(), kr)
-        assert np.array_equal(ops.unpack_decode_layout(tiles, 64, 2, True, 0, n).cpu().numpy(), vr)
+        assert np.array_equal(ops.unpack_decode_layout(tiles, 64, vb, True, 0, n).cpu().numpy(), vr)
         assert np.array_equal(pn[0].cpu().numpy(), knr) and np.array_equal(vnn[0].cpu().numpy(), vnr)
 
 
-@pytest.mark.parametrize("bs,G,qdt", [(64, 4, torch.bfloat16), (128, 2, torch.float16),
-                                      (64, 1, torch.float32), (16, 4, torch.bfloat16),
-                                      (32, 2, torch.float16), (16, 1, torch.float32),
-                                      (16, 8, torch.bfloat16), (64, 6, torch.float32)])
-def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
+@pytest.mark.parametrize("bs,G,qdt,vb", [(64, 4, torch.bfloat16, 2), (128, 2, torch.float16, 2),
+                                         (64, 1, torch.float32, 2), (16, 4, torch.bfloat16, 2),
+                                         (32, 2, torch.float16, 2), (16, 1, torch.float32, 2),
+                                         (16, 8, torch.bfloat16, 2), (64, 6, torch.float32, 2),
+                                         (16, 4, torch.bfloat16, 3), (64, 4, torch.bfloat16, 3),
+                                         (32, 6, torch.float32, 3), (128, 1, torch.float16, 3),
+                                         (16, 2, torch.float16, 4), (64, 8, torch.float32, 4),
+                                         (32, 4, torch.bfloat16, 4)])
+def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt, vb):
+    # The paged decode-layout kernel (16-token sub-blocks below block size 64, 64-token
+    # tiles from 64 on) equals the contiguous kernel over the same tokens bit for bit, and
+    # the float64 oracle within the query type's tolerance.
     from turboquant_kv import ops
-    rs = np.random.RandomState(bs + G)
+    rs = np.random.RandomState(bs + G + 100 * vb)
     Hkv = 2
     Hq = G * Hkv
     lens = [0, 3, 700, 1500, 64]
@@ -378,11 +390,11 @@ def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     width = (max(lens) + bs - 1) // bs + 1
     width = -(-width * bs // 64) * 64 // bs   # the contiguous reference needs t_cap % 64 == 0
     nb = sum((n + bs - 1) // bs for n in lens) + 4
-    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv, vb)
     tab[0, 0] = 7   # a block id past sequence 0's (empty) context: never read
     Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
     _, ck = O.lloyd_max_codebook(4, 64)
-    _, cv = O.lloyd_max_codebook(2, 64)
+    _, cv = O.lloyd_max_codebook(vb, 64)
     q = torch.from_numpy(rs.randn(B, Hq, 64).astype(np.float32)).to(DEV).to(qdt)
     scale = 0.125
     dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[qdt]
@@ -392,7 +404,7 @@ def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
     capi.check(L().tq_decode_attention_paged_dl(
         capi.p(q), dt, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp), capi.p(knp),
-        capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(tab)), capi.i32(width),
+        capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.i32(vb), capi.p(T(tab)), capi.i32(width),
         capi.p(T(np.asarray(lens, np.int32))), capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)),
         ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
         capi.stream()))
@@ -400,37 +412,39 @@ def test_decode_paged_dl_vs_contiguous_and_f64(bs, G, qdt):
     got, got_lse = out.float().cpu().numpy(), lse.cpu().numpy()
     # the same tokens in contiguous decode-layout caches of the same capacity
     kc_ = np.zeros((B, Hkv, Tc, 32), np.uint8)
-    vc_ = np.zeros((B, Hkv, Tc, 16), np.uint8)
+    vc_ = np.zeros((B, Hkv, Tc, 8 * vb), np.uint8)
     kn_, vn_ = np.zeros((B, Hkv, Tc), np.float32), np.zeros((B, Hkv, Tc), np.float32)
     for b, n in enumerate(lens):
         kc_[b, :, :n], kn_[b, :, :n], vc_[b, :, :n], vn_[b, :, :n] = seqs[b]
     kpairs = torch.empty(B * Hkv, Tc, 32, dtype=torch.uint8, device=DEV)
-    vblocks = torch.zeros(B * Hkv, Tc // 64, 1024, dtype=torch.uint8, device=DEV)
+    vblocks = torch.zeros(B * Hkv, Tc // 64, 512 * vb, dtype=torch.uint8, device=DEV)
     ops.pack_decode_layout(T(kc_).view(B * Hkv, Tc, 32), kpairs, 64, 4, False, 0)
-    ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 16), vblocks, 64, 2, True, 0)
+    ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 8 * vb), vblocks, 64, vb, True, 0)
     ref, ref_lse = ops.decode_attention_dl(q, kpairs.view(B, Hkv, Tc, 32), T(kn_),
-                                           vblocks.view(B, Hkv, Tc // 64, 1024), T(vn_),
+                                           vblocks.view(B, Hkv, Tc // 64, 512 * vb), T(vn_),
                                            T(np.asarray(lens, np.int32)), T(ck), T(cv), T(Rk), T(Rv),
                                            scale, return_lse=True)
     # same kernel, same split plan: identical sums
     assert np.array_equal(got, ref.float().cpu().numpy())
     assert np.array_equal(got_lse, ref_lse.cpu().numpy())
     want = O.decode_attention_f64(q.float().cpu().numpy(), kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv,
-                                  4, 2, scale)
+                                  4, vb, scale)
     assert np.all(got[0] == 0) and np.all(np.isneginf(got_lse[0]))
     tol = 1e-2 if qdt != torch.float32 else 1e-4
     assert np.max(np.abs(got - want)) <= tol * np.max(np.abs(want))
 
 
+@pytest.mark.parametrize("vb", [2, 3, 4])
 @pytest.mark.parametrize("bs", [64, 16])
-def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
+def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs, vb):
     # The vLLM step (chunked prefill + decodes) on decode-layout pools: the stored codes
-    # equal the bit-plane pools' and outputs match the float64 paged oracle.
+    # equal the bit-plane pools' and outputs match the float64 paged oracle (K4/V3 is
+    # configs[4]'s cache).
     from turboquant_kv.vllm_plugin import PagedKVPools
     from turboquant_kv.config import TurboQuantConfig
-    rs = np.random.RandomState(11)
+    rs = np.random.RandomState(11 + vb)
     Hkv, Hq, d, nb = 2, 8, 64, 24 * 64 // bs
-    cfg = TurboQuantConfig(key_bits=4, value_bits=2)
+    cfg = TurboQuantConfig(key_bits=4, value_bits=vb)
     bp = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV)
     dl = PagedKVPools(cfg, 1, nb, bs, Hkv, d, DEV, layout="decode")
     steps = [[100, 17, 200, 5], [70, 1, 1, 1]]
@@ -463,7 +477,7 @@ def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
                 assert torch.equal(r_bp, r_dl) and torch.equal(n_bp, n_dl), (step, j, kind)
             a, b = qsl[j], qsl[j + 1]
             want = O.paged_attention_f64(q[a:b].float().cpu().numpy(), P["k"], P["kn"], P["v"], P["vn"],
-                                         tab[j], lens[j], kc, vc, Rk, Rv, 4, 2, scale)
+                                         tab[j], lens[j], kc, vc, Rk, Rv, 4, vb, scale)
             got = out_dl[a:b].float().cpu().numpy()
             assert np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want)), (step, j)
             ref = out_bp[a:b].float().cpu().numpy()
@@ -471,7 +485,8 @@ def test_vllm_paged_step_decode_layout_vs_bitplane_and_f64(bs):
         before = [before[i] + n_new[i] for i in range(4)]
 
 
-def test_decode_layout_prefill_kernel_vs_per_token_decode():
+@pytest.mark.parametrize("vb", [2, 3, 4])
+def test_decode_layout_prefill_kernel_vs_per_token_decode(vb):
     # PagedKVPools.prefill over decode-layout pools runs the tiled prefill kernel.  A whole
     # 1200-token prompt (T = n, block size 16, shuffled blocks) against the per-token
     # decode kernel over the same pools (fp32 queries: both paths fp32-accurate) and the
@@ -480,7 +495,7 @@ def test_decode_layout_prefill_kernel_vs_per_token_decode():
     from turboquant_kv.vllm_plugin import PagedKVPools
     from turboquant_kv.config import TurboQuantConfig
     Hkv, Hq, d, bs, nb, n = 2, 8, 64, 16, 80, 1200
-    pools = PagedKVPools(TurboQuantConfig(), 1, nb, bs, Hkv, d, DEV, layout="decode")
+    pools = PagedKVPools(TurboQuantConfig(value_bits=vb), 1, nb, bs, Hkv, d, DEV, layout="decode")
     g = torch.Generator(device=DEV).manual_seed(6)
     table = torch.randperm(nb, generator=g, device=DEV)[:(n + bs - 1) // bs].to(torch.int32)
     slots = (table.long()[torch.arange(n, device=DEV) // bs] * bs + torch.arange(n, device=DEV) % bs)
@@ -498,16 +513,18 @@ def test_decode_layout_prefill_kernel_vs_per_token_decode():
     want = O.paged_attention_f64(q.cpu().numpy(), P["k"], P["kn"], P["v"], P["vn"],
                                  table.cpu().numpy(), n, pools.kcen.cpu().numpy(),
                                  pools.vcen.cpu().numpy(), pools.R_k.cpu().numpy(),
-                                 pools.R_v.cpu().numpy(), 4, 2, 0.125)
+                                 pools.R_v.cpu().numpy(), 4, vb, 0.125)
     # both kernels fp32-accurate, their sums in different orders
     assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
     assert np.max(np.abs(got - per_token)) <= 4e-5 * np.max(np.abs(want))
 
 
-@pytest.mark.parametrize("bs,G,n,qdt", [(16, 4, 300, torch.bfloat16), (32, 7, 77, torch.float16),
-                                        (64, 1, 200, torch.float32), (128, 8, 129, torch.bfloat16),
-                                        (64, 4, 1, torch.float32)])
-def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
+@pytest.mark.parametrize("bs,G,n,qdt,vb", [(16, 4, 300, torch.bfloat16, 2), (32, 7, 77, torch.float16, 2),
+                                           (64, 1, 200, torch.float32, 2), (128, 8, 129, torch.bfloat16, 2),
+                                           (64, 4, 1, torch.float32, 2), (16, 4, 300, torch.bfloat16, 3),
+                                           (64, 2, 200, torch.float32, 3), (32, 7, 77, torch.float16, 4),
+                                           (128, 4, 129, torch.bfloat16, 4), (16, 1, 65, torch.float32, 4)])
+def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt, vb):
     # tq_prefill_attention_paged_dl: sequence 1's last n tokens (positions T-n .. T-1, so
     # T-n tokens of history) against the per-token decode-layout kernel (B = n rows, row i's
     # context ending at its own position, fp32 queries) and the float64 decode oracle per
@@ -515,13 +532,13 @@ def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
     # sequence's stale slots past T hold NaN norms and its block-table entries past T are
     # -1 (clamped into the pool, masked): neither may reach the output.
     from turboquant_kv import ops
-    rs = np.random.RandomState(bs * 31 + G + n)
+    rs = np.random.RandomState(bs * 31 + G + n + 1000 * vb)
     Hkv = 2
     Hq = G * Hkv
     lens = [37, 1100 + bs, 5]
     width = (max(lens) + bs - 1) // bs + 2
     nb = sum((L + bs - 1) // bs for L in lens) + 4
-    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv)
+    tab, kp, knp, vt, vnp, seqs = _dl_pools(rs, lens, bs, nb, width, Hkv, vb)
     Tq = lens[1]
     row = tab[1].copy()
     nblk = (Tq + bs - 1) // bs
@@ -531,15 +548,16 @@ def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
     row[nblk:] = -1
     Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
     _, ck = O.lloyd_max_codebook(4, 64)
-    _, cv = O.lloyd_max_codebook(2, 64)
+    _, cv = O.lloyd_max_codebook(vb, 64)
     q = torch.from_numpy(rs.randn(n, Hq, 64).astype(np.float32)).to(DEV).to(qdt)
     scale = 0.125
     dt = {torch.float32: capi.TQ_F32, torch.bfloat16: capi.TQ_BF16, torch.float16: capi.TQ_F16}[qdt]
     out = torch.empty(n, Hq, 64, dtype=torch.float32, device=DEV)
-    print(f"prefill capi bs={bs} G={G} n={n} T={Tq} {qdt}", flush=True)
+    print(f"prefill capi bs={bs} G={G} n={n} T={Tq} {qdt} vb={vb}", flush=True)
     capi.check(L().tq_prefill_attention_paged_dl(
         capi.p(q), dt, capi.i32(n), capi.i64(Tq), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp),
-        capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(row)), capi.i32(width),
+        capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.i32(vb), capi.p(T(row)),
+        capi.i32(width),
         capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)), ctypes.c_float(scale), capi.p(out),
         capi.stream()))
     sync()
@@ -553,7 +571,7 @@ def test_prefill_kernel_capi_vs_per_token_decode_and_f64(bs, G, n, qdt):
     kr, kn_, vr, vn_ = seqs[1]
     bc = lambda x: np.broadcast_to(x[None], (n,) + x.shape)
     want = O.decode_attention_f64(qf.cpu().numpy(), bc(kr), bc(kn_), bc(vr), bc(vn_), pos.cpu().numpy(),
-                                  ck, cv, Rk, Rv, 4, 2, scale)
+                                  ck, cv, Rk, Rv, 4, vb, scale)
     # fp32 / fp16 queries: hi + lo operand parts, fp32-accurate; bf16 queries: one fp16
     # product per term (outputs consumed in bf16, whose rounding is 2^-9)
     # (outputs average many values, so their maximum sits far below the summed terms':
@@ -568,15 +586,16 @@ def test_prefill_kernel_capi_refusals():
     z = torch.zeros(64, dtype=torch.float32, device=DEV)
     zb = torch.zeros(64, dtype=torch.uint8, device=DEV)
     tab = torch.zeros(4, dtype=torch.int32, device=DEV)
-    args = lambda n, T_, bs, d=64, hq=8: (
+    args = lambda n, T_, bs, d=64, hq=8, vb=2: (
         capi.p(z), capi.TQ_F32, capi.i32(n), capi.i64(T_), capi.i32(hq), capi.i32(2), capi.i32(d),
-        capi.p(zb), capi.p(z), capi.p(zb), capi.p(z), capi.i64(1), capi.i32(bs), capi.p(tab), capi.i32(4),
-        capi.p(z), capi.p(z), capi.p(z), capi.p(z), ctypes.c_float(1.0), capi.p(z), capi.stream())
+        capi.p(zb), capi.p(z), capi.p(zb), capi.p(z), capi.i64(1), capi.i32(bs), capi.i32(vb), capi.p(tab),
+        capi.i32(4), capi.p(z), capi.p(z), capi.p(z), capi.p(z), ctypes.c_float(1.0), capi.p(z), capi.stream())
     assert L().tq_prefill_attention_paged_dl(*args(1, 1, 16, d=128)) != 0      # head_dim 64 only
     assert L().tq_prefill_attention_paged_dl(*args(1, 1, 24)) != 0             # block size
     assert L().tq_prefill_attention_paged_dl(*args(5, 4, 16)) != 0            # n > T
     assert L().tq_prefill_attention_paged_dl(*args(1, 65, 16)) != 0            # T past the table
     assert L().tq_prefill_attention_paged_dl(*args(1, 1, 16, hq=7)) != 0       # GQA groups
+    assert L().tq_prefill_attention_paged_dl(*args(1, 1, 16, vb=5)) != 0       # value width
 
 
 # ------------------------------------------------------------------ pools past 2 GiB
@@ -592,19 +611,21 @@ def _high_tables(lens, bs, nb, width):
     return tab
 
 
-@pytest.mark.parametrize("layout", ["decode", "bitplane"])
-def test_paged_pools_past_2gib(layout):
+@pytest.mark.parametrize("layout,vb,bs", [("decode", 2, 64), ("decode", 3, 64), ("decode", 4, 16),
+                                          ("bitplane", 2, 64)])
+def test_paged_pools_past_2gib(layout, vb, bs):
     # Key pools of 2.46 GB (76.8M rows of 32 B): the sequences' blocks sit past byte 2^31,
     # which 32-bit buffer offsets cannot reach, so these calls take the 64-bit-address
-    # kernels.  Same sums as the contiguous kernels over the same rows, and the float64
-    # oracle within the bf16 tolerance.
+    # kernels (64-token value tiles, and 16-token sub-blocks at block size 16).  Same sums
+    # as the contiguous kernels over the same rows, and the float64 oracle within the bf16
+    # tolerance.
     from turboquant_kv import ops
-    rs = np.random.RandomState(77)
-    Hkv, G, bs = 2, 4, 64
+    rs = np.random.RandomState(77 + vb + bs)
+    Hkv, G = 2, 4
     Hq = G * Hkv
     lens = [700, 1, 1500]
     B = len(lens)
-    nb = 600_000
+    nb = 600_000 * 64 // bs
     assert nb * Hkv * bs * 32 >= 2 ** 31
     width = (max(lens) + bs - 1) // bs + 1
     tab = _high_tables(lens, bs, nb, width)
@@ -613,17 +634,17 @@ def test_paged_pools_past_2gib(layout):
                      np.int64)
     n = len(slots)
     krows = rs.randint(0, 256, (n, Hkv, 32)).astype(np.uint8)
-    vrows = rs.randint(0, 256, (n, Hkv, 16)).astype(np.uint8)
+    vrows = rs.randint(0, 256, (n, Hkv, 8 * vb)).astype(np.uint8)
     kn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     Rk, Rv = O.dense_qr_rotation(64, 42), O.dense_qr_rotation(64, 43)
     _, ck = O.lloyd_max_codebook(4, 64)
-    _, cv = O.lloyd_max_codebook(2, 64)
+    _, cv = O.lloyd_max_codebook(vb, 64)
     q = torch.from_numpy(rs.randn(B, Hq, 64).astype(np.float32)).to(DEV).to(torch.bfloat16)
     scale = 0.125
-    Tc = width * bs
+    Tc = -(-width * bs // 64) * 64   # the contiguous reference needs t_cap % 64 == 0
     kc_ = np.zeros((B, Hkv, Tc, 32), np.uint8)
-    vc_ = np.zeros((B, Hkv, Tc, 16), np.uint8)
+    vc_ = np.zeros((B, Hkv, Tc, 8 * vb), np.uint8)
     kn_, vn_ = np.zeros((B, Hkv, Tc), np.float32), np.zeros((B, Hkv, Tc), np.float32)
     o = 0
     for b, L_ in enumerate(lens):
@@ -638,7 +659,8 @@ def test_paged_pools_past_2gib(layout):
     vnp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
     if layout == "decode":
         kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
-        vt = torch.zeros(nb, Hkv, bs // 64, 1024, dtype=torch.uint8, device=DEV)
+        vt = (torch.zeros(nb, Hkv, bs // 64, 512 * vb, dtype=torch.uint8, device=DEV) if bs >= 64 else
+              torch.zeros(nb, Hkv, bs // 16, 128 * vb, dtype=torch.uint8, device=DEV))
         pairs = torch.empty(n * Hkv, 1, 32, dtype=torch.uint8, device=DEV)
         ops.pack_decode_layout(T(krows).view(n * Hkv, 1, 32), pairs, 64, 4, False, 0)
         capi.check(L().tq_paged_store(capi.p(pairs), capi.p(T(kn)), capi.i64(n), capi.i32(Hkv),
@@ -646,11 +668,14 @@ def test_paged_pools_past_2gib(layout):
                                       capi.i64(nb), capi.i32(bs), capi.stream()))
         capi.check(L().tq_paged_store_value_tiles(capi.p(T(vrows)), capi.p(T(vn)), capi.i64(n),
                                                   capi.i32(Hkv), capi.p(T(slots)), capi.p(vt),
-                                                  capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.stream()))
-        ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, Tc), dtype=torch.uint8, device=DEV)
+                                                  capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.i32(vb),
+                                                  capi.stream()))
+        ws = torch.empty(L().tq_decode_dl_workspace_bytes(B, Hq, Hkv, width * bs), dtype=torch.uint8,
+                         device=DEV)
+        print(f"paged decode past 2 GiB vb={vb} bs={bs}", flush=True)
         capi.check(L().tq_decode_attention_paged_dl(
             capi.p(q), capi.TQ_BF16, capi.i32(B), capi.i32(Hq), capi.i32(Hkv), capi.i32(64), capi.p(kp),
-            capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.p(T(tab)),
+            capi.p(knp), capi.p(vt), capi.p(vnp), capi.i64(nb), capi.i32(bs), capi.i32(vb), capi.p(T(tab)),
             capi.i32(width), capi.p(lens_t), capi.p(T(ck)), capi.p(T(cv)), capi.p(T(Rk)), capi.p(T(Rv)),
             ctypes.c_float(scale), capi.p(out), capi.p(lse), capi.p(ws), ctypes.c_size_t(ws.numel()),
             capi.stream()))
@@ -658,11 +683,11 @@ def test_paged_pools_past_2gib(layout):
         got = out.float().cpu().numpy()
         del kp, vt
         kpairs = torch.empty(B * Hkv, Tc, 32, dtype=torch.uint8, device=DEV)
-        vblocks = torch.zeros(B * Hkv, Tc // 64, 1024, dtype=torch.uint8, device=DEV)
+        vblocks = torch.zeros(B * Hkv, Tc // 64, 512 * vb, dtype=torch.uint8, device=DEV)
         ops.pack_decode_layout(T(kc_).view(B * Hkv, Tc, 32), kpairs, 64, 4, False, 0)
-        ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 16), vblocks, 64, 2, True, 0)
+        ops.pack_decode_layout(T(vc_).view(B * Hkv, Tc, 8 * vb), vblocks, 64, vb, True, 0)
         ref, _ = ops.decode_attention_dl(q, kpairs.view(B, Hkv, Tc, 32), T(kn_),
-                                         vblocks.view(B, Hkv, Tc // 64, 1024), T(vn_), lens_t, T(ck),
+                                         vblocks.view(B, Hkv, Tc // 64, 512 * vb), T(vn_), lens_t, T(ck),
                                          T(cv), T(Rk), T(Rv), scale, return_lse=True)
         ref = ref.float().cpu().numpy()
     else:
@@ -688,5 +713,5 @@ def test_paged_pools_past_2gib(layout):
     torch.cuda.empty_cache()
     assert np.array_equal(got, ref)  # same arithmetic and split plan as the contiguous kernel
     want = O.decode_attention_f64(q.float().cpu().numpy(), kc_, kn_, vc_, vn_, lens, ck, cv, Rk, Rv,
-                                  4, 2, scale)
+                                  4, vb, scale)
     assert np.max(np.abs(got - want)) <= 1e-2 * np.max(np.abs(want))

@@ -957,24 +957,37 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_dl_lse(
   return {out, lse};
 }
 
-// 2-bit value rows [n, hkv, 16] + norms [n, hkv] into the value tiles
-// vtile_pool [num_blocks, hkv, block_size/64, 1024] (+ vnorm_pool [num_blocks, hkv, block_size]).
+// Value widths of decode-layout value pools: tile_bytes = 64-token tiles of 512 * VB bytes
+// (block_size >= 64) or 16-token sub-blocks of 128 * VB (block_size 16, 32); 0 if neither.
+int value_tile_bits(int64_t tile_bytes, bool tiles64) {
+  const int64_t unit = tiles64 ? 512 : 128;
+  if (tile_bytes % unit != 0) return 0;
+  const int64_t vb = tile_bytes / unit;
+  return vb >= 2 && vb <= 4 ? (int)vb : 0;
+}
+
+// VB-bit value rows [n, hkv, 8 VB] + norms [n, hkv] into the value tiles
+// vtile_pool [num_blocks, hkv, block_size/64, 512 VB] (block_size >= 64) or
+// [num_blocks, hkv, block_size/16, 128 VB] (+ vnorm_pool [num_blocks, hkv, block_size]).
 void paged_store_value_tiles(const at::Tensor& rows, const at::Tensor& norms,
                              const at::Tensor& slot_mapping, at::Tensor& vtile_pool,
                              at::Tensor& vnorm_pool) {
   require_gpu(vtile_pool, "vtile_pool");
+  // 64-token tiles are 1024-2048 bytes, 16-token sub-blocks 256-512: the width tells them apart
+  const bool tiles64 = vtile_pool.dim() == 4 && vtile_pool.size(3) >= 1024;
+  const int vb = vtile_pool.dim() == 4 ? value_tile_bits(vtile_pool.size(3), tiles64) : 0;
   TORCH_CHECK(vtile_pool.dim() == 4 && vtile_pool.scalar_type() == at::kByte &&
-                  vtile_pool.is_contiguous() && (vtile_pool.size(3) == 1024 || vtile_pool.size(3) == 256),
-              "vtile_pool must be contiguous uint8 [num_blocks, hkv, block_size/64, 1024] "
-              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 256] (block_size 16, 32)");
+                  vtile_pool.is_contiguous() && vb != 0,
+              "vtile_pool must be contiguous uint8 [num_blocks, hkv, block_size/64, 512 VB] "
+              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 128 VB] (block_size 16, 32)");
   c10::DeviceGuard g(vtile_pool.device());
   const auto dev = vtile_pool.device();
   const int64_t nb = vtile_pool.size(0), hkv = vtile_pool.size(1);
-  const int64_t bs = vtile_pool.size(2) * (vtile_pool.size(3) == 1024 ? 64 : 16);
-  TORCH_CHECK((vtile_pool.size(3) == 1024) == (bs >= 64), "value tile shape does not match block_size");
+  const int64_t bs = vtile_pool.size(2) * (tiles64 ? 64 : 16);
+  TORCH_CHECK(tiles64 == (bs >= 64), "value tile shape does not match block_size");
   TORCH_CHECK(rows.dim() == 3 && rows.scalar_type() == at::kByte && rows.size(1) == hkv &&
-                  rows.size(2) == 16,
-              "rows must be uint8 [n, hkv, 16] (2-bit codes of d = 64)");
+                  rows.size(2) == 8 * vb,
+              "rows must be uint8 [n, hkv, 8 * value bits] (bit planes of d = 64)");
   const int64_t n = rows.size(0);
   auto r = rows.to(dev).contiguous();
   auto nm = f32c(norms, dev);
@@ -986,7 +999,7 @@ void paged_store_value_tiles(const at::Tensor& rows, const at::Tensor& norms,
               "vnorm_pool must be contiguous float32 [num_blocks, hkv, block_size]");
   check_rc(tq_paged_store_value_tiles(r.data_ptr<uint8_t>(), nm.data_ptr<float>(), n, (int32_t)hkv,
                                       sm.data_ptr<int64_t>(), vtile_pool.data_ptr<uint8_t>(),
-                                      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs,
+                                      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, (int32_t)vb,
                                       cur_stream(vtile_pool)));
 }
 
@@ -1010,10 +1023,12 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
   TORCH_CHECK(kpairs_pool.scalar_type() == at::kByte && vtile_pool.scalar_type() == at::kByte,
               "pools must be uint8");
   const int64_t tile_tokens = bs >= 64 ? 64 : 16;
+  const int vb = d == 64 ? value_tile_bits(vtile_pool.size(3), bs >= 64) : 0;
   TORCH_CHECK(kpairs_pool.size(3) == d / 2 && vtile_pool.size(0) == nb && vtile_pool.size(1) == Hkv &&
-                  vtile_pool.size(2) * tile_tokens == bs && vtile_pool.size(3) == tile_tokens * d / 4,
-              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, 16d] "
-              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 4d] (block_size 16, 32)");
+                  vtile_pool.size(2) * tile_tokens == bs && vb != 0,
+              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, "
+              "512 VB] (block_size >= 64) or [num_blocks, hkv, block_size/16, 128 VB] (block_size "
+              "16, 32), VB = 2-4 value bits, head_dim 64");
   TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
                   knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
               "norm pools must be float32 [num_blocks, hkv, block_size]");
@@ -1025,7 +1040,9 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
   auto vc = f32c(vcentroids, dev);
   auto Rk = f32c(krotation, dev);
   auto Rv = f32c(vrotation, dev);
-  TORCH_CHECK(kc.numel() == 16 && vc.numel() == 4, "decode layout: 4-bit keys, 2-bit values");
+  TORCH_CHECK(kc.numel() == 16 && vc.numel() == (1 << vb),
+              "decode layout: 4-bit keys (16 centroids) and 2^VB value centroids for the pool's "
+              "VB-bit value tiles");
   auto out = at::empty({B, Hq, d}, qq.options());
   auto lse = at::empty({B, Hq}, qq.options().dtype(at::kFloat));
   if (B == 0) return {out, lse};
@@ -1035,7 +1052,7 @@ std::tuple<at::Tensor, at::Tensor> decode_attention_paged_dl(
   check_rc(tq_decode_attention_paged_dl(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)B, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
       kpairs_pool.data_ptr<uint8_t>(), knorm_pool.data_ptr<float>(), vtile_pool.data_ptr<uint8_t>(),
-      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, bt.data_ptr<int32_t>(), (int32_t)bt.size(1),
+      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, (int32_t)vb, bt.data_ptr<int32_t>(), (int32_t)bt.size(1),
       sl.data_ptr<int32_t>(), kc.data_ptr<float>(), vc.data_ptr<float>(), Rk.data_ptr<float>(),
       Rv.data_ptr<float>(), (float)scale, out.data_ptr(), lse.data_ptr<float>(), ws.data_ptr(),
       ws.numel(), cur_stream(qq)));
@@ -1062,10 +1079,12 @@ at::Tensor prefill_attention_paged_dl(
   TORCH_CHECK(kpairs_pool.scalar_type() == at::kByte && vtile_pool.scalar_type() == at::kByte,
               "pools must be uint8");
   const int64_t tile_tokens = bs >= 64 ? 64 : 16;
+  const int vb = d == 64 ? value_tile_bits(vtile_pool.size(3), bs >= 64) : 0;
   TORCH_CHECK(kpairs_pool.size(3) == d / 2 && vtile_pool.size(0) == nb && vtile_pool.size(1) == Hkv &&
-                  vtile_pool.size(2) * tile_tokens == bs && vtile_pool.size(3) == tile_tokens * d / 4,
-              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, 16d] "
-              "(block_size >= 64) or [num_blocks, hkv, block_size/16, 4d] (block_size 16, 32)");
+                  vtile_pool.size(2) * tile_tokens == bs && vb != 0,
+              "decode-layout pool shapes mismatch: value tiles [num_blocks, hkv, block_size/64, "
+              "512 VB] (block_size >= 64) or [num_blocks, hkv, block_size/16, 128 VB] (block_size "
+              "16, 32), VB = 2-4 value bits, head_dim 64");
   TORCH_CHECK(knorm_pool.scalar_type() == at::kFloat && vnorm_pool.scalar_type() == at::kFloat &&
                   knorm_pool.numel() == nb * Hkv * bs && vnorm_pool.numel() == nb * Hkv * bs,
               "norm pools must be float32 [num_blocks, hkv, block_size]");
@@ -1074,13 +1093,15 @@ at::Tensor prefill_attention_paged_dl(
   auto vc = f32c(vcentroids, dev);
   auto Rk = f32c(krotation, dev);
   auto Rv = f32c(vrotation, dev);
-  TORCH_CHECK(kc.numel() == 16 && vc.numel() == 4, "decode layout: 4-bit keys, 2-bit values");
+  TORCH_CHECK(kc.numel() == 16 && vc.numel() == (1 << vb),
+              "decode layout: 4-bit keys (16 centroids) and 2^VB value centroids for the pool's "
+              "VB-bit value tiles");
   TORCH_CHECK(Rk.numel() == d * d && Rv.numel() == d * d, "rotations must be [d, d]");
   auto out = at::empty({n, Hq, d}, qq.options().dtype(at::kFloat));
   check_rc(tq_prefill_attention_paged_dl(
       qq.data_ptr(), to_tq(qq.scalar_type()), (int32_t)n, T, (int32_t)Hq, (int32_t)Hkv, (int32_t)d,
       kpairs_pool.data_ptr<uint8_t>(), knorm_pool.data_ptr<float>(), vtile_pool.data_ptr<uint8_t>(),
-      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, bt.data_ptr<int32_t>(), (int32_t)bt.numel(),
+      vnorm_pool.data_ptr<float>(), nb, (int32_t)bs, (int32_t)vb, bt.data_ptr<int32_t>(), (int32_t)bt.numel(),
       kc.data_ptr<float>(), vc.data_ptr<float>(), Rk.data_ptr<float>(), Rv.data_ptr<float>(),
       (float)scale, out.data_ptr<float>(), cur_stream(qq)));
   return out;

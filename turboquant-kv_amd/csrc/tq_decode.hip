@@ -597,9 +597,12 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // term, about 2^-11 relative per operand -- finer than the bf16 arithmetic the reference
 // scores bf16 inputs in.
 // PG: 0 contiguous caches; 1 paged pools of block_size >= 64 (64-token value tiles);
-// 2 paged pools of block_size 16 or 32 (16-token value sub-blocks of 256 B: lane
-// 16 sl + c's word holds what word m of its 64-token tile row holds for sub-block m).
-// VB: value code width (2, 3 or 4; sub-blocks hold 2-bit values only).
+// 2 paged pools of block_size 16 or 32 (16-token value sub-blocks of 128 VB bytes, each
+// the share of its token group m of the tile words: VB 2, lane L's word = tile word m;
+// VB 4, lane L's 8 bytes at 8 L = the two bytes of each tile word 4 (m / 2) + dg that
+// group m fills (dg = 0..3, two bytes each); VB 3, the two bytes of tile words
+// 3 (m / 2) + 0, 1 at 4 L and of word 3 (m / 2) + 2 at 256 + 2 L).
+// VB: value code width (2, 3 or 4).
 // PG: 0 contiguous; 1 / 2 paged pools (blocks >= 64 tokens / 16- or 32-token blocks) read
 // through buffer resources over whole pools (32-bit offsets: pools under 2 GiB); 3 / 4 the
 // same for pools of any size: rows at 64-bit addresses from clamped block ids.
@@ -608,9 +611,12 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   constexpr bool PAGED = PG != 0, SUB16 = PG == 2 || PG == 4, WIDE = PG >= 3;
-  static_assert(VB >= 2 && VB <= 4 && (!SUB16 || VB == 2), "value width");
+  static_assert(VB >= 2 && VB <= 4, "value width");
   static_assert(ND == 0 || PG == 0, "16-bit norms: contiguous caches");
-  constexpr int VW = VB == 2 ? 4 : 2 * VB;  // value words per lane and tile
+  // value words per lane and tile as loaded (16-token sub-blocks of 3-bit values: the four
+  // groups' 4-byte and 2-byte shares, reassembled into tile words at their use)
+  constexpr int VW = VB == 2 ? 4 : SUB16 ? 8 : 2 * VB;
+  constexpr uint32_t SBB = 128u * VB;       // bytes per 16-token value sub-block
   constexpr uint32_t VTILE = 512u * VB;     // bytes per 64-token value tile
   // V table at 0: index = block byte; 32 copies of 4 fp16 centroids, or (EXACT_V) 16
   // copies of 4 hi + 4 lo halves (VB 3, 4: a pair byte's two fp16 centroids, 32 copies
@@ -739,11 +745,29 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         x.k[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl));
       if constexpr (SUB16) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(a.vblocks + (size_t)(rg[m] >> 4) * 256 + lane * 4));
+        for (int m = 0; m < 4; ++m) {
+          const uint8_t* sb = a.vblocks + (size_t)(rg[m] >> 4) * SBB;
+          if constexpr (VB == 2) {
+            x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
+          } else if constexpr (VB == 4) {
+            const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sb + lane * 8));
+            x.v[2 * m] = w.x; x.v[2 * m + 1] = w.y;
+          } else {
+            x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
+            x.v[4 + m] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(sb + 256 + lane * 2));
+          }
+        }
       } else {
-        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vblocks + (size_t)vt * VTILE + lane * 16));
+        const uint8_t* tb = a.vblocks + (size_t)vt * VTILE;
+        const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb + lane * 16));
         x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+        if constexpr (VB == 3) {
+          const u32x2 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(tb + 1024 + lane * 8));
+          x.v[4] = v1.x; x.v[5] = v1.y;
+        } else if constexpr (VB == 4) {
+          const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb + 1024 + lane * 16));
+          x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
+        }
       }
     } else {
 #pragma unroll
@@ -752,8 +776,18 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if constexpr (SUB16) {
       // value sub-block of group m = its first pool row / 16 (rows of a group are 16-aligned)
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-        x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, (int)((rg[m] >> 4) * 256 + lane * 4), 0, kNT);
+      for (int m = 0; m < 4; ++m) {
+        const int so = (int)((rg[m] >> 4) * SBB);
+        if constexpr (VB == 2) {
+          x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
+        } else if constexpr (VB == 4) {
+          const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vrs, so + lane * 8, 0, kNT);
+          x.v[2 * m] = w.x; x.v[2 * m + 1] = w.y;
+        } else {
+          x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
+          x.v[4 + m] = __builtin_amdgcn_raw_buffer_load_b16(vrs, so + 256 + lane * 2, 0, kNT);
+        }
+      }
     } else {
       const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + lane * 16), 0, kNT);
       x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
@@ -968,13 +1002,26 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
   const uint32_t vcopy = VB != 2 ? (uint32_t)(lane & 31) * 4
                           : EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
+  // VB 3, 4: tile word i of half G (16-token sub-blocks: bytes 0-1 from group 2G's share,
+  // bytes 2-3 from group 2G + 1's)
+  auto tword = [&](const Tile& x, int G, int i) -> uint32_t {
+    if constexpr (!SUB16) {
+      return x.v[(VB == 4 ? 4 : 3) * G + i];
+    } else if constexpr (VB == 4) {
+      return __builtin_amdgcn_perm(x.v[2 * (2 * G + 1) + (i >> 1)], x.v[2 * (2 * G) + (i >> 1)],
+                                   (i & 1) ? 0x07060302u : 0x05040100u);
+    } else {
+      return i == 2 ? __builtin_amdgcn_perm(x.v[4 + 2 * G + 1], x.v[4 + 2 * G], 0x05040100u)
+                    : __builtin_amdgcn_perm(x.v[2 * G + 1], x.v[2 * G], i ? 0x07060302u : 0x05040100u);
+    }
+  };
   // VB 3, 4: the word whose four bytes index the pair entries of half G, dim group dg
   auto vword = [&](const Tile& x, int G, int dg) -> uint32_t {
     if constexpr (VB == 4) {
-      return x.v[4 * G + dg];
+      return tword(x, G, dg);
     } else {
-      if (dg < 3) return x.v[3 * G + dg];
-      const uint32_t x0 = x.v[3 * G], x1 = x.v[3 * G + 1], x2 = x.v[3 * G + 2];
+      if (dg < 3) return tword(x, G, dg);
+      const uint32_t x0 = tword(x, G, 0), x1 = tword(x, G, 1), x2 = tword(x, G, 2);
       return ((x0 >> 6) & 0x03030303u) | ((x1 >> 4) & 0x0C0C0C0Cu) | ((x2 >> 2) & 0x30303030u);
     }
   };
@@ -1511,17 +1558,24 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
 namespace tq {
 namespace {
 
-// New tokens' 2-bit value codes (bit-plane rows [n][hkv][16], d = 64) into the value
-// tiles of a paged pool, one thread per (token, head, dim).  Token t of a 64-token tile
-// sits at byte 16 (16 sl + c) + 4 m + dg, bits 2 (t % 4), with 4 m + sl = (t % 64) / 4,
-// dim = 16 dg + c (the decode layout); below block_size 64, token t of a 16-token
-// sub-block sits at byte 4 (16 sl + c) + dg, sl = (t % 16) / 4.  Tokens of one tile share bytes, so each field is cleared
-// and set with 32-bit atomics (disjoint bits: concurrent tokens do not interfere); slots
-// outside the pool are skipped.
+// New tokens' VB-bit value codes (bit-plane rows [n][hkv][8 VB], d = 64: plane p at bytes
+// 8p .. 8p + 7) into the value tiles of a paged pool, one thread per (token, head, dim).
+// With tt the token's offset in its 64-token tile (block_size >= 64) or 16-token sub-block
+// (below), sl = (tt % 16) / 4, r = tt % 4, m = tt / 16, L = 16 sl + dim % 16, dg = dim / 16,
+// the code goes where the decode kernel reads it:
+//   VB 2  tile byte 16 L + 4 m + dg, sub-block byte 4 L + dg; bits 2 r
+//   VB 4  byte 2 (m % 2) + r / 2 of tile word 4 (m / 2) + dg, sub-block byte
+//         8 L + 2 dg + r / 2; bits 4 (r % 2)
+//   VB 3  dims below 48: byte 2 (m % 2) + r / 2 of tile word 3 (m / 2) + dg (sub-block
+//         byte 4 L + 2 dg + r / 2 for dg 0, 1, 256 + 2 L + r / 2 for dg 2), bits 3 (r % 2);
+//         dims 48-63: code bit b is bit q = 3 (r % 2) + b of the pair index, at bit
+//         6 + q % 2 of the same byte position of word (or sub-block share) q / 2
+// Tokens of one tile share bytes, so each field is cleared and set with 32-bit atomics
+// (disjoint bits: concurrent tokens do not interfere); slots outside the pool are skipped.
 __global__ __launch_bounds__(256) void paged_vtile_store_kernel(
     const uint8_t* __restrict__ rows, const float* __restrict__ norms, int64_t n, int hkv,
     const int64_t* __restrict__ slot_mapping, uint32_t* __restrict__ vpool,
-    float* __restrict__ vnorm_pool, int64_t num_slots, int bs_log2) {
+    float* __restrict__ vnorm_pool, int64_t num_slots, int bs_log2, int vb) {
   const int64_t total = n * hkv * kDim;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int j = (int)(e & (kDim - 1));
@@ -1532,23 +1586,40 @@ __global__ __launch_bounds__(256) void paged_vtile_store_kernel(
     if (slot < 0 || slot >= num_slots) continue;
     const int64_t blk = slot >> bs_log2;
     const int off = (int)(slot & ((1 << bs_log2) - 1));
-    const uint8_t* row = rows + th * 16;  // plane 0: bytes 0-7, plane 1: bytes 8-15
-    const uint32_t code = ((row[j >> 3] >> (7 - (j & 7))) & 1u) | (((row[8 + (j >> 3)] >> (7 - (j & 7))) & 1u) << 1);
-    const int tt = off & 63, q4 = tt >> 2;
-    uint32_t* w;
-    int shift;
-    if (bs_log2 >= 6) {  // 64-token tiles of 1024 B
-      const int byte = 16 * (16 * (q4 & 3) + (j & 15)) + 4 * (q4 >> 2) + (j >> 4);
-      shift = 8 * (byte & 3) + 2 * (tt & 3);
-      const int64_t tile = ((blk * hkv + h) << (bs_log2 - 6)) + (off >> 6);
-      w = vpool + tile * 256 + (byte >> 2);
-    } else {  // 16-token sub-blocks of 256 B: byte 4 (16 sl + c) + dg
-      shift = 8 * (j >> 4) + 2 * (tt & 3);
-      const int64_t sub = (((blk * hkv + h) << bs_log2) + off) >> 4;
-      w = vpool + sub * 64 + 16 * (q4 & 3) + (j & 15);
+    const uint8_t* row = rows + th * 8 * vb;
+    uint32_t code = 0;
+    for (int p = 0; p < vb; ++p) code |= ((row[8 * p + (j >> 3)] >> (7 - (j & 7))) & 1u) << p;
+    const bool tiles = bs_log2 >= 6;
+    const int tt = off & (tiles ? 63 : 15);
+    const int sl = (tt >> 2) & 3, r = tt & 3, m = tt >> 4, c = j & 15, L = 16 * sl + c;
+    // byte base of the token's tile (64-token tiles of 512 VB bytes) or sub-block (128 VB)
+    const int64_t base = tiles ? ((((blk * hkv + h) << (bs_log2 - 6)) + (off >> 6)) * 512 * vb)
+                               : (((((blk * hkv + h) << bs_log2) + off) >> 4) * 128 * vb);
+    auto put = [&](int byte, int bit, uint32_t mask, uint32_t val) {
+      const int64_t at = base + byte;  // base is a multiple of 4
+      uint32_t* w = vpool + (at >> 2);
+      const int sh = 8 * (int)(at & 3) + bit;
+      atomicAnd(w, ~(mask << sh));
+      atomicOr(w, val << sh);
+    };
+    // byte of tile word / sub-block share i (dim group or word index) for this token
+    auto byte_of = [&](int i) -> int {
+      if (tiles) return vt_byte_off(vb, L, (vb == 4 ? 4 : 3) * (m >> 1) + i, 2 * (m & 1) + (r >> 1));
+      if (vb == 4) return 8 * L + 2 * i + (r >> 1);
+      return i < 2 ? 4 * L + 2 * i + (r >> 1) : 256 + 2 * L + (r >> 1);
+    };
+    if (vb == 2) {
+      put(tiles ? 16 * L + 4 * m + (j >> 4) : 4 * L + (j >> 4), 2 * r, 3u, code);
+    } else if (vb == 4) {
+      put(byte_of(j >> 4), 4 * (r & 1), 15u, code);
+    } else if (j < 48) {
+      put(byte_of(j >> 4), 3 * (r & 1), 7u, code);
+    } else {
+      for (int b = 0; b < 3; ++b) {
+        const int q = 3 * (r & 1) + b;
+        put(byte_of(q >> 1), 6 + (q & 1), 1u, (code >> b) & 1u);
+      }
     }
-    atomicAnd(w, ~(3u << shift));
-    atomicOr(w, code << shift);
     if (j == 0) vnorm_pool[((blk * hkv + h) << bs_log2) + off] = norms[th];
   }
 }
@@ -1584,6 +1655,13 @@ void launch_dl_contiguous(int vbits, tq_dtype q_dtype, unsigned grid, const DlAr
   if (vbits == 2) launch_dl_kernel<0, 2, ND>(q_dtype, grid, a, st);
   else if (vbits == 3) launch_dl_kernel<0, 3, ND>(q_dtype, grid, a, st);
   else launch_dl_kernel<0, 4, ND>(q_dtype, grid, a, st);
+}
+
+template <int PG>
+void launch_dl_paged(int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
+  if (vbits == 2) launch_dl_kernel<PG, 2>(q_dtype, grid, a, st);
+  else if (vbits == 3) launch_dl_kernel<PG, 3>(q_dtype, grid, a, st);
+  else launch_dl_kernel<PG, 4>(q_dtype, grid, a, st);
 }
 
 // The exact current token merged into a decode output by log-sum-exp (the HF cache's
@@ -1643,13 +1721,13 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
         else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16>(vbits, q_dtype, (unsigned)grid, a, st);
         else launch_dl_contiguous<0>(vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 1) {
-        launch_dl_kernel<1, 2>(q_dtype, (unsigned)grid, a, st);
+        launch_dl_paged<1>(vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 3) {
-        launch_dl_kernel<3, 2>(q_dtype, (unsigned)grid, a, st);
+        launch_dl_paged<3>(vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 4) {
-        launch_dl_kernel<4, 2>(q_dtype, (unsigned)grid, a, st);
+        launch_dl_paged<4>(vbits, q_dtype, (unsigned)grid, a, st);
       } else {
-        launch_dl_kernel<2, 2>(q_dtype, (unsigned)grid, a, st);
+        launch_dl_paged<2>(vbits, q_dtype, (unsigned)grid, a, st);
       }
       TQ_LAUNCH_CHECK("dl_decode_kernel");
     }
@@ -1733,8 +1811,9 @@ int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t h
 int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t n_tokens,
                                int32_t hkv, const int64_t* slot_mapping, uint8_t* vpool,
                                float* vnorm_pool, int64_t num_blocks, int32_t block_size,
-                               void* stream) {
+                               int32_t vbits, void* stream) {
   TQ_REQUIRE(n_tokens >= 0 && hkv >= 1 && num_blocks >= 0, "bad sizes");
+  TQ_REQUIRE(vbits >= 2 && vbits <= 4, "value tiles hold 2-4 bit codes, got %d", vbits);
   int bsl = 0;
   while ((1 << bsl) < block_size) ++bsl;
   TQ_REQUIRE(block_size >= 16 && (1 << bsl) == block_size,
@@ -1746,7 +1825,7 @@ int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t 
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
   hipLaunchKernelGGL(paged_vtile_store_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
                      rows, norms, n_tokens, (int)hkv, slot_mapping, reinterpret_cast<uint32_t*>(vpool),
-                     vnorm_pool, num_blocks << bsl, bsl);
+                     vnorm_pool, num_blocks << bsl, bsl, (int)vbits);
   TQ_LAUNCH_CHECK("paged_vtile_store_kernel");
   return TQ_OK;
 }
@@ -1754,14 +1833,15 @@ int tq_paged_store_value_tiles(const uint8_t* rows, const float* norms, int64_t 
 int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
                                  int32_t d, const uint8_t* kpairs_pool, const float* knorm_pool,
                                  const uint8_t* vtile_pool, const float* vnorm_pool,
-                                 int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
-                                 int32_t max_blocks_per_seq, const int32_t* seq_lens,
-                                 const float* kcentroids, const float* vcentroids,
-                                 const float* krotation, const float* vrotation, float scale,
-                                 void* out, float* lse, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 int64_t num_blocks, int32_t block_size, int32_t vbits,
+                                 const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                 const int32_t* seq_lens, const float* kcentroids,
+                                 const float* vcentroids, const float* krotation,
+                                 const float* vrotation, float scale, void* out, float* lse,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
   TQ_REQUIRE(d == kDim, "decode layout covers head_dim 64, got %d", d);
+  TQ_REQUIRE(vbits >= 2 && vbits <= 4, "value tiles hold 2-4 bit codes, got %d", vbits);
   TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0,
              "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
   int bsl = 0;
@@ -1796,7 +1876,7 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
   a.pool_rows = (uint32_t)pool_rows;
   a.num_blocks = (uint32_t)std::max<int64_t>(num_blocks, 1);
   const int pg = (bsl >= 6 ? 1 : 2) + (wide ? 2 : 0);
-  return run_dl(a, q_dtype, B, hq, hkv, 2, pg, p, workspace, out, lse, as_stream(stream));
+  return run_dl(a, q_dtype, B, hq, hkv, vbits, pg, p, workspace, out, lse, as_stream(stream));
 }
 
 int tq_decode_merge_token(const void* o, const float* lse, const void* q, tq_dtype q_dtype,

@@ -20,10 +20,13 @@
 //                   (c, g) gets tokens 16 b + 4 g + r of query row c.
 //   softmax         per query row over the four lanes c, c + 16, c + 32, c + 48.
 //   O^T += V^T P^T  A: value centroids of dim 16 nb + c for the 8 tokens lane (c, g) holds
-//                   weights of -- the decode layout's 16-byte value word of lane 16 g + c
-//                   carries exactly those tokens' 2-bit codes (byte nb of word m: tokens
-//                   16 m + 4 g .. + 3, dim 16 nb + c), so no data moves between lanes.  B:
-//                   weights times value norms, the layout S^T left them in (hi + lo).
+//                   weights of -- the decode layout's value words of lane 16 g + c carry
+//                   exactly those tokens' codes, so no data moves between lanes: 2-bit
+//                   values, byte nb of words 2 s and 2 s + 1 (tokens 16 m + 4 g .. + 3,
+//                   one lookup of four centroids each); 3- and 4-bit values, the four bytes
+//                   of tile word (4 s + nb), or the dim-group word of half s (3 bits), one
+//                   lookup of a (c[low code], c[high code]) pair each.  B: weights times
+//                   value norms, the layout S^T left them in (hi + lo).
 // Rotations in fp32 on v_mfma_f32_16x16x4f32: Qrot = q R_k^T (rows of R_k permuted so the
 // result lands in the B layout above), out = O R_v.  Each row's query and the centroid
 // tables are scaled by powers of two into [0.5, 1) before the fp16 split (exact), which
@@ -59,14 +62,14 @@ struct PfArgs {
   int64_t past;  // T - n
   const uint8_t* kpairs;  // [num_blocks][hkv][bs][32]
   const float* knorms;    // [num_blocks][hkv][bs]
-  const uint8_t* vtiles;  // [num_blocks][hkv][bs/64][1024] or [num_blocks][hkv][bs/16][256]
+  const uint8_t* vtiles;  // [num_blocks][hkv][bs/64][512 VB] or [num_blocks][hkv][bs/16][128 VB]
   const float* vnorms;
   const int32_t* block_table;  // the sequence's row
   int max_blocks;
   int bs_log2;
   uint32_t num_blocks;
   const float* kcen;  // 16
-  const float* vcen;  // 4
+  const float* vcen;  // 2^VB
   const float* krot;  // [64][64]
   const float* vrot;
   float qscale;  // softmax scale * log2(e)
@@ -94,17 +97,23 @@ __device__ __forceinline__ float pf_pow2_scale(float amax) {
 // PREC: fp16 hi + lo parts of every operand (three products per term, fp32-accurate);
 // otherwise one fp16 product per term (about 2^-11 relative per operand), for bf16 queries
 // whose outputs are consumed in bf16 (2^-9).
-template <bool SUB, bool PREC>
+// VB: value code width (2, 3 or 4); tiles and sub-blocks as the decode kernel reads them.
+template <bool SUB, bool PREC, int VB>
 __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
 #pragma clang fp contract(off)
   // Tables, KC / VC copies of each entry (lane L reads copy L % KC, L % VC, so a wave's
   // random lookups spread over the banks instead of piling onto a 1 KB table's):
   //   tk[p][i KC + j]  key byte i -> (c[i >> 4], c[i & 15]) as two fp16, part p (hi, lo)
-  //   tv[p][i VC + j]  value byte i -> its four 2-bit codes' centroids as four fp16
+  //   tv[p][i VC + j]  VB 2: value byte i -> its four 2-bit codes' centroids as four fp16;
+  //                    VB 3, 4: (in tw, 2 VC copies) byte i -> (c[low code], c[high code])
+  //                    as two fp16 (3 bits: the top two bits of i ignored)
   constexpr int KC = PREC ? 4 : 8, VC = PREC ? 2 : 4, NP = PREC ? 2 : 1;
+  constexpr int WC = 2 * VC;  // copies of a VB 3 / 4 pair entry (the same 8 KB)
   constexpr int NGR = PREC ? 2 : 3;  // 16-row groups per wave (sharing each tile's operands)
+  static_assert(VB >= 2 && VB <= 4, "value width");
   __shared__ __attribute__((aligned(16))) uint32_t tk[NP][256 * KC];
-  __shared__ __attribute__((aligned(16))) pf_u32x2 tv[NP][256 * VC];
+  __shared__ __attribute__((aligned(16))) pf_u32x2 tv[VB == 2 ? NP : 1][VB == 2 ? 256 * VC : 1];
+  __shared__ __attribute__((aligned(16))) uint32_t tw[VB == 2 ? 1 : NP][VB == 2 ? 1 : 256 * WC];
   __shared__ float sc_s[2];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
   // ---- centroid tables scaled by powers of two, fp16 hi (+ lo)
   if (wave == 0) {
     float km = lane < 16 ? fabsf(a.kcen[lane]) : 0.f;
-    float vm = lane < 4 ? fabsf(a.vcen[lane]) : 0.f;
+    float vm = lane < (1 << VB) ? fabsf(a.vcen[lane]) : 0.f;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
       km = fmaxf(km, __shfl_xor(km, o, 64));
@@ -137,27 +146,40 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
     const _Float16 h0 = (_Float16)c0, h1 = (_Float16)c1;
     const uint32_t kh = pf_pack(h0, h1);
     const uint32_t kl = pf_pack((_Float16)(c0 - (float)h0), (_Float16)(c1 - (float)h1));
-    _Float16 vh[4], vl[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float v = a.vcen[(e >> (2 * t)) & 3] * vsc;
-      vh[t] = (_Float16)v;
-      vl[t] = (_Float16)(v - (float)vh[t]);
-    }
-    const uint32_t v0 = pf_pack(vh[0], vh[1]), v1 = pf_pack(vh[2], vh[3]);
-    const uint32_t w0 = pf_pack(vl[0], vl[1]), w1 = pf_pack(vl[2], vl[3]);
 #pragma unroll
     for (int j = 0; j < KC; j += 4) {
       *reinterpret_cast<pf_u32x4*>(&tk[0][e * KC + j]) = (pf_u32x4){kh, kh, kh, kh};
       if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tk[NP - 1][e * KC + j]) = (pf_u32x4){kl, kl, kl, kl};
     }
+    if constexpr (VB == 2) {
+      _Float16 vh[4], vl[4];
 #pragma unroll
-    for (int j = 0; j < VC; j += 2) {
-      *reinterpret_cast<pf_u32x4*>(&tv[0][e * VC + j]) = (pf_u32x4){v0, v1, v0, v1};
-      if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tv[NP - 1][e * VC + j]) = (pf_u32x4){w0, w1, w0, w1};
+      for (int t = 0; t < 4; ++t) {
+        const float v = a.vcen[(e >> (2 * t)) & 3] * vsc;
+        vh[t] = (_Float16)v;
+        vl[t] = (_Float16)(v - (float)vh[t]);
+      }
+      const uint32_t v0 = pf_pack(vh[0], vh[1]), v1 = pf_pack(vh[2], vh[3]);
+      const uint32_t w0 = pf_pack(vl[0], vl[1]), w1 = pf_pack(vl[2], vl[3]);
+#pragma unroll
+      for (int j = 0; j < VC; j += 2) {
+        *reinterpret_cast<pf_u32x4*>(&tv[0][e * VC + j]) = (pf_u32x4){v0, v1, v0, v1};
+        if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tv[NP - 1][e * VC + j]) = (pf_u32x4){w0, w1, w0, w1};
+      }
+    } else {
+      constexpr int mask = (1 << VB) - 1;
+      const float x0 = a.vcen[e & mask] * vsc, x1 = a.vcen[(e >> VB) & mask] * vsc;
+      const _Float16 y0 = (_Float16)x0, y1 = (_Float16)x1;
+      const uint32_t vhw = pf_pack(y0, y1);
+      const uint32_t vlw = pf_pack((_Float16)(x0 - (float)y0), (_Float16)(x1 - (float)y1));
+#pragma unroll
+      for (int j = 0; j < WC; j += 4) {
+        *reinterpret_cast<pf_u32x4*>(&tw[0][e * WC + j]) = (pf_u32x4){vhw, vhw, vhw, vhw};
+        if constexpr (PREC) *reinterpret_cast<pf_u32x4*>(&tw[NP - 1][e * WC + j]) = (pf_u32x4){vlw, vlw, vlw, vlw};
+      }
     }
   }
-  const int kcp = lane & (KC - 1), vcp = lane & (VC - 1);
+  const int kcp = lane & (KC - 1), vcp = lane & (VC - 1), wcp = lane & (WC - 1);
   __syncthreads();  // the last barrier: from here on every wave runs on its own
 
   // rows of this wave: group j holds rows row0 + 16 j + c
@@ -289,15 +311,59 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
       nk[b] = *reinterpret_cast<const pf_v4f*>(a.knorms + base[b] + 4 * g);
       nv[b] = *reinterpret_cast<const pf_v4f*>(a.vnorms + base[b] + 4 * g);
     }
-    uint32_t vw[4];
+    // value words (8 VB bytes per pool row; a sub-block starts at its group's first row):
+    // VB 2 tile words 0-3; VB 3 / 4 tiles: words 0-3, then 4-5 / 4-7; sub-blocks of VB 3 /
+    // 4: each group's shares, reassembled by vword below
+    constexpr int NV = VB == 2 ? 4 : (SUB ? 8 : 2 * VB);
+    uint32_t vw[NV];
     if constexpr (SUB) {
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm)
-        vw[mm] = *reinterpret_cast<const uint32_t*>(a.vtiles + base[mm] * 16 + 4 * lane);
+      for (int mm = 0; mm < 4; ++mm) {
+        const uint8_t* sb = a.vtiles + base[mm] * (8 * VB);
+        if constexpr (VB == 2) {
+          vw[mm] = *reinterpret_cast<const uint32_t*>(sb + 4 * lane);
+        } else if constexpr (VB == 4) {
+          const pf_u32x2 w = *reinterpret_cast<const pf_u32x2*>(sb + 8 * lane);
+          vw[2 * mm] = w.x; vw[2 * mm + 1] = w.y;
+        } else {
+          vw[mm] = *reinterpret_cast<const uint32_t*>(sb + 4 * lane);
+          vw[4 + mm] = *reinterpret_cast<const uint16_t*>(sb + 256 + 2 * lane);
+        }
+      }
     } else {
-      const pf_u32x4 v = *reinterpret_cast<const pf_u32x4*>(a.vtiles + base[0] * 16 + 16 * lane);
+      const uint8_t* tb = a.vtiles + base[0] * (8 * VB);
+      const pf_u32x4 v = *reinterpret_cast<const pf_u32x4*>(tb + 16 * lane);
       vw[0] = v.x; vw[1] = v.y; vw[2] = v.z; vw[3] = v.w;
+      if constexpr (VB == 3) {
+        const pf_u32x2 v1 = *reinterpret_cast<const pf_u32x2*>(tb + 1024 + 8 * lane);
+        vw[4] = v1.x; vw[5] = v1.y;
+      } else if constexpr (VB == 4) {
+        const pf_u32x4 v1 = *reinterpret_cast<const pf_u32x4*>(tb + 1024 + 16 * lane);
+        vw[4] = v1.x; vw[5] = v1.y; vw[6] = v1.z; vw[7] = v1.w;
+      }
     }
+    // VB 3 / 4: tile word i of half s (sub-blocks: bytes 0-1 from group 2 s's share, 2-3
+    // from group 2 s + 1's), then the word whose bytes index the pair entries of dim group nb
+    auto tword = [&](int s, int i) -> uint32_t {
+      if constexpr (!SUB) {
+        return vw[(VB == 4 ? 4 : 3) * s + i];
+      } else if constexpr (VB == 4) {
+        return __builtin_amdgcn_perm(vw[2 * (2 * s + 1) + (i >> 1)], vw[2 * (2 * s) + (i >> 1)],
+                                     (i & 1) ? 0x07060302u : 0x05040100u);
+      } else {
+        return i == 2 ? __builtin_amdgcn_perm(vw[4 + 2 * s + 1], vw[4 + 2 * s], 0x05040100u)
+                      : __builtin_amdgcn_perm(vw[2 * s + 1], vw[2 * s], i ? 0x07060302u : 0x05040100u);
+      }
+    };
+    auto vword = [&](int s, int nb) -> uint32_t {
+      if constexpr (VB == 4) {
+        return tword(s, nb);
+      } else {
+        if (nb < 3) return tword(s, nb);
+        const uint32_t x0 = tword(s, 0), x1 = tword(s, 1), x2 = tword(s, 2);
+        return ((x0 >> 6) & 0x03030303u) | ((x1 >> 4) & 0x0C0C0C0Cu) | ((x2 >> 2) & 0x30303030u);
+      }
+    };
 
     // ---- scores (log2 domain), masked past each row's limit; one key operand per (b, s)
     // serves every row group
@@ -391,15 +457,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
-        const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
-        const pf_u32x2 h0 = tv[0][b0 * VC + vcp], h1 = tv[0][b1 * VC + vcp];
-        const pf_v8h ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
+        pf_v8h ah, al{};
+        if constexpr (VB == 2) {
+          const uint32_t b0 = (vw[2 * s] >> (8 * nb)) & 255u, b1 = (vw[2 * s + 1] >> (8 * nb)) & 255u;
+          const pf_u32x2 h0 = tv[0][b0 * VC + vcp], h1 = tv[0][b1 * VC + vcp];
+          ah = pf_h8(h0.x, h0.y, h1.x, h1.y);
+          if constexpr (PREC) {
+            const pf_u32x2 l0 = tv[NP - 1][b0 * VC + vcp], l1 = tv[NP - 1][b1 * VC + vcp];
+            al = pf_h8(l0.x, l0.y, l1.x, l1.y);
+          }
+        } else {
+          const uint32_t w = vword(s, nb);
+          const uint32_t i0 = w & 255u, i1 = (w >> 8) & 255u, i2 = (w >> 16) & 255u, i3 = w >> 24;
+          ah = pf_h8(tw[0][i0 * WC + wcp], tw[0][i1 * WC + wcp], tw[0][i2 * WC + wcp], tw[0][i3 * WC + wcp]);
+          if constexpr (PREC)
+            al = pf_h8(tw[NP - 1][i0 * WC + wcp], tw[NP - 1][i1 * WC + wcp], tw[NP - 1][i2 * WC + wcp],
+                       tw[NP - 1][i3 * WC + wcp]);
+        }
 #pragma unroll
         for (int j = 0; j < NGR; ++j)
           o[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j][s], o[j][nb], 0, 0, 0);
         if constexpr (PREC) {
-          const pf_u32x2 l0 = tv[NP - 1][b0 * VC + vcp], l1 = tv[NP - 1][b1 * VC + vcp];
-          const pf_v8h al = pf_h8(l0.x, l0.y, l1.x, l1.y);
 #pragma unroll
           for (int j = 0; j < NGR; ++j) {
             o[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j][s], o[j][nb], 0, 0, 0);
@@ -445,6 +523,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
   }
 }
 
+template <bool SUB, bool PREC>
+void launch_prefill(int vbits, dim3 grid, const PfArgs& a, hipStream_t st) {
+  if (vbits == 2) hipLaunchKernelGGL((dl_prefill_kernel<SUB, PREC, 2>), grid, dim3(kPfThreads), 0, st, a);
+  else if (vbits == 3) hipLaunchKernelGGL((dl_prefill_kernel<SUB, PREC, 3>), grid, dim3(kPfThreads), 0, st, a);
+  else hipLaunchKernelGGL((dl_prefill_kernel<SUB, PREC, 4>), grid, dim3(kPfThreads), 0, st, a);
+}
+
 }  // namespace
 }  // namespace tq
 
@@ -456,12 +541,13 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
                                   int32_t hkv, int32_t d, const uint8_t* kpairs_pool,
                                   const float* knorm_pool, const uint8_t* vtile_pool,
                                   const float* vnorm_pool, int64_t num_blocks, int32_t block_size,
-                                  const int32_t* block_table, int32_t max_blocks,
+                                  int32_t vbits, const int32_t* block_table, int32_t max_blocks,
                                   const float* kcentroids, const float* vcentroids,
                                   const float* krotation, const float* vrotation, float scale,
                                   float* out, void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype), "unknown dtype");
   TQ_REQUIRE(d == 64, "decode layout covers head_dim 64, got %d", d);
+  TQ_REQUIRE(vbits >= 2 && vbits <= 4, "value tiles hold 2-4 bit codes, got %d", vbits);
   TQ_REQUIRE(hkv >= 1 && hq >= hkv && hq % hkv == 0,
              "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
   int bsl = 0;
@@ -499,14 +585,14 @@ int tq_prefill_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t n, in
   a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation; a.vrot = vrotation;
   a.qscale = scale * 1.4426950408889634f;
   a.out = out;
-  const dim3 gr((unsigned)grid), bl(kPfThreads);
+  const dim3 gr((unsigned)grid);
   hipStream_t st = as_stream(stream);
   if (bsl >= 6) {
-    if (prec) hipLaunchKernelGGL((dl_prefill_kernel<false, true>), gr, bl, 0, st, a);
-    else hipLaunchKernelGGL((dl_prefill_kernel<false, false>), gr, bl, 0, st, a);
+    if (prec) launch_prefill<false, true>(vbits, gr, a, st);
+    else launch_prefill<false, false>(vbits, gr, a, st);
   } else {
-    if (prec) hipLaunchKernelGGL((dl_prefill_kernel<true, true>), gr, bl, 0, st, a);
-    else hipLaunchKernelGGL((dl_prefill_kernel<true, false>), gr, bl, 0, st, a);
+    if (prec) launch_prefill<true, true>(vbits, gr, a, st);
+    else launch_prefill<true, false>(vbits, gr, a, st);
   }
   TQ_LAUNCH_CHECK("dl_prefill_kernel");
   return TQ_OK;

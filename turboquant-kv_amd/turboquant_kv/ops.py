@@ -206,11 +206,12 @@ def decode_attention_paged(q, kpool, knorm_pool, vpool, vnorm_pool, block_tables
 
 
 def paged_store_value_tiles(rows, norms, slot_mapping, vtile_pool, vnorm_pool):
-    """Write 2-bit value rows [n, hkv, 16] (bit planes of d = 64) and norms [n, hkv] into
-    the value tiles vtile_pool -- [num_blocks, hkv, block_size/64, 1024] for block sizes
-    >= 64, [num_blocks, hkv, block_size/16, 256] for 16 and 32 -- (+ norms [num_blocks,
-    hkv, block_size]) at the flat slots slot_mapping [n]; other tokens of a tile keep their
-    bits, slots outside the pool are skipped."""
+    """Write vb-bit value rows [n, hkv, 8 vb] (bit planes of d = 64, vb = 2-4) and norms
+    [n, hkv] into the value tiles vtile_pool -- [num_blocks, hkv, block_size/64, 512 vb] for
+    block sizes >= 64, [num_blocks, hkv, block_size/16, 128 vb] for 16 and 32; vb is read
+    from the pool's width -- (+ norms [num_blocks, hkv, block_size]) at the flat slots
+    slot_mapping [n]; other tokens of a tile keep their bits, slots outside the pool are
+    skipped."""
     _require_device(vtile_pool, "vtile_pool")
     _ops().paged_store_value_tiles(rows, norms, slot_mapping, vtile_pool, vnorm_pool)
 
@@ -219,7 +220,8 @@ def decode_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool
                               seq_lens, kcentroids, vcentroids, krotation, vrotation, scale,
                               return_lse=False):
     """decode_attention_dl over paged pools in the decode layout (block_size a power of two
-    >= 16): batch row b attends to its first seq_lens[b] tokens through block_tables."""
+    >= 16, 2-4 bit value tiles as paged_store_value_tiles writes them): batch row b attends
+    to its first seq_lens[b] tokens through block_tables."""
     _require_device(q, "q")
     out, lse = _ops().decode_attention_paged_dl(q, kpairs_pool, knorm_pool, vtile_pool, vnorm_pool,
                                                 block_tables, seq_lens, kcentroids, vcentroids,

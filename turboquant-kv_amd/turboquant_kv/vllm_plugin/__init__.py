@@ -63,7 +63,7 @@ class TurboQuantKVCacheConfig:
     protected_layers: int = 0
     seed: int = 42
     # block pool layout: "bitplane", "decode" (the MFMA decode kernel's layout: mse, 4-bit
-    # keys, 2-bit values, head_dim 64, power-of-two block_size >= 16) or "auto" (decode
+    # keys, 2-4 bit values, head_dim 64, power-of-two block_size >= 16) or "auto" (decode
     # where it applies)
     pool_layout: str = "auto"
 

@@ -18,13 +18,13 @@ Keys use `seed`, values `seed + 1`, prod mode the (bits-1)-bit codebook and the 
 matrices of seed + 12345 / seed + 1 + 12345 -- the QuantizedKVCache conventions
 (cache.py:56-76).  Protected layers keep fp16 rows in pools of the same block layout.
 
-layout="decode" (mse mode, 4-bit keys, 2-bit values, head_dim 64, block_size a power of
-two >= 16) keeps the quantized layers in the decode layout instead: key pair bytes
-[num_blocks, H, block_size, 32] and value tiles -- [num_blocks, H, block_size/64, 1024]
-(64-token tiles) for block sizes >= 64, [num_blocks, H, block_size/16, 256] (16-token
+layout="decode" (mse mode, 4-bit keys, 2-, 3- or 4-bit values, head_dim 64, block_size a
+power of two >= 16) keeps the quantized layers in the decode layout instead: key pair bytes
+[num_blocks, H, block_size, 32] and value tiles -- [num_blocks, H, block_size/64, 512 vb]
+(64-token tiles) for block sizes >= 64, [num_blocks, H, block_size/16, 128 vb] (16-token
 sub-blocks) below -- read by the MFMA decode kernel through the block tables
-(`decode_attention_paged_dl`); a prefill sequence runs as that decode with one row per new
-token whose context ends at its own position (the causal mask).
+(`decode_attention_paged_dl`); a prefill sequence runs the causal prefill kernel over the
+same pools (`prefill_attention_paged_dl`).
 """
 
 from __future__ import annotations
@@ -69,19 +69,29 @@ class TurboQuantAttentionMetadata:
 
 def gather_value_tiles(vt_pool: torch.Tensor, block_table: torch.Tensor, T: int) -> torch.Tensor:
     """Value tiles of tokens 0..T-1 of one sequence from a decode-layout pool, in the
-    contiguous decode layout [H, ceil(T/64), 1024] (unpack_decode_layout's input)."""
+    contiguous decode layout [H, ceil(T/64), 512 vb] (unpack_decode_layout's input)."""
     nb, H, per_block, width = vt_pool.shape
     dev = vt_pool.device
-    n = (T + 63) // 64 if width == 1024 else (T + 15) // 16
+    tiles64 = width >= 1024
+    vb = width // (512 if tiles64 else 128)
+    n = (T + 63) // 64 if tiles64 else (T + 15) // 16
     tiles, _ = ops.paged_gather(vt_pool, None, block_table.view(1, -1),
                                 torch.tensor([n], dtype=torch.int32, device=dev), n)
-    if width == 1024:
+    if tiles64:
         return tiles[0]
-    # 16-token sub-blocks: sub-block m of a tile holds word m of each lane's 16 bytes
+    # 16-token sub-blocks: sub-block m of a tile holds group m's share of the tile words
     nt = (T + 63) // 64
-    sub = torch.zeros(H, nt * 4, 256, dtype=torch.uint8, device=dev)
+    sub = torch.zeros(H, nt * 4, width, dtype=torch.uint8, device=dev)
     sub[:, :n] = tiles[0]
-    return sub.view(H, nt, 4, 64, 4).permute(0, 1, 3, 2, 4).reshape(H, nt, 1024)
+    if vb == 2:  # word m of each lane
+        return sub.view(H, nt, 4, 64, 4).permute(0, 1, 3, 2, 4).reshape(H, nt, 1024)
+    if vb == 4:  # bytes 2 (m % 2) .. + 1 of tile word 4 (m / 2) + dg: lane L's 8 bytes
+        w = sub.view(H, nt, 2, 2, 64, 4, 2)              # [G, m % 2, L, dg, byte]
+        return w.permute(0, 1, 2, 4, 5, 3, 6).reshape(H, nt, 2048)
+    a = sub[..., :256].reshape(H, nt, 2, 2, 64, 2, 2)      # words 3G + 0, 1: [G, m % 2, L, i, byte]
+    b = sub[..., 256:].reshape(H, nt, 2, 2, 64, 1, 2)      # word 3G + 2
+    w = torch.cat([a, b], dim=5).permute(0, 1, 4, 2, 5, 3, 6).reshape(H, nt, 64, 6, 4)
+    return torch.cat([w[:, :, :, :4].reshape(H, nt, 1024), w[:, :, :, 4:].reshape(H, nt, 512)], dim=2)
 
 
 class PagedKVPools:
@@ -94,7 +104,7 @@ class PagedKVPools:
         if layout not in ("bitplane", "decode"):
             raise ValueError(f"Unknown layout: {layout}")
         if layout == "decode" and not self.decode_layout_supported(config, head_dim, block_size):
-            raise ValueError("layout='decode' needs mse mode, 4-bit keys, 2-bit values, "
+            raise ValueError("layout='decode' needs mse mode, 4-bit keys, 2-4 bit values, "
                              "head_dim 64 and a power-of-two block_size >= 16")
         self.layout = layout
         self.config = config
@@ -129,8 +139,8 @@ class PagedKVPools:
             if layout == "decode":
                 self.layers.append({"kp": torch.zeros(nb, H, bs, head_dim // 2, **u8),
                                     "kn": torch.zeros(nb, H, bs, **f32),
-                                    "vt": (torch.zeros(nb, H, bs // 64, 1024, **u8) if bs >= 64
-                                           else torch.zeros(nb, H, bs // 16, 256, **u8)),
+                                    "vt": (torch.zeros(nb, H, bs // 64, 512 * vb, **u8) if bs >= 64
+                                           else torch.zeros(nb, H, bs // 16, 128 * vb, **u8)),
                                     "vn": torch.zeros(nb, H, bs, **f32)})
                 continue
             st = {"k": torch.zeros(nb, H, bs, kb * bpp, **u8), "kn": torch.zeros(nb, H, bs, **f32),
@@ -142,7 +152,7 @@ class PagedKVPools:
 
     @staticmethod
     def decode_layout_supported(config: TurboQuantConfig, head_dim: int, block_size: int) -> bool:
-        return (config.mode == "mse" and config.key_bits == 4 and config.value_bits == 2
+        return (config.mode == "mse" and config.key_bits == 4 and 2 <= config.value_bits <= 4
                 and head_dim == 64 and block_size >= 16 and block_size & (block_size - 1) == 0)
 
     # ------------------------------------------------------------------ writes
@@ -208,7 +218,7 @@ class PagedKVPools:
                 return ops.unpack_decode_layout(pairs[0], d, 4, False, 0, T), norms[0]
             tiles = gather_value_tiles(st["vt"], block_table, T)
             _, norms = ops.paged_gather(st["kp"], st["vn"], block_table.view(1, -1), one(T), T)
-            return ops.unpack_decode_layout(tiles, d, 2, True, 0, T), norms[0]
+            return ops.unpack_decode_layout(tiles, d, self.vbits, True, 0, T), norms[0]
         norm_key = {"k": "kn", "v": "vn", "ks": "kr", "vs": "vr"}[key]
         rows, norms = ops.paged_gather(st[key], st[norm_key], block_table.view(1, -1),
                                        torch.tensor([T], dtype=torch.int32, device=self.device), T)
