@@ -333,6 +333,31 @@ def bench_decode(args, extra):
             log(f"decode T={T} paged K4/V3 decode layout (block 16, shuffled): {ms_v3 * 1e3:.1f} us, "
                 f"{bytes_v3 / ms_v3 / 1e6:.0f} GB/s")
             del pkp, pkn, pv3, pvn
+            # head_dim 128 (the Llama-3-8B / Qwen-7B head shape), contiguous decode layout,
+            # K4/V2 and K4/V3: random codes and norms (the kernel's time does not depend on them)
+            d2 = 128
+            Rk2 = make_rotation_matrix(d2, 42).cuda()
+            Rv2 = make_rotation_matrix(d2, 43).cuda()
+            ck2 = lloyd_max_codebook(4, d2)[1].cuda()
+            q2 = torch.randn(B, Hq, d2, generator=g, device="cuda").to(torch.bfloat16)
+            kp2 = torch.randint(0, 256, (B, Hkv, T, d2 // 2), dtype=torch.uint8, device="cuda", generator=g)
+            kn2 = torch.rand(B, Hkv, T, generator=g, device="cuda") + 0.5
+            vn2 = torch.rand(B, Hkv, T, generator=g, device="cuda") + 0.5
+            for vbh in (2, 3):
+                vt2 = torch.randint(0, 256, (B, Hkv, T // 64, 8 * vbh * d2), dtype=torch.uint8,
+                                    device="cuda", generator=g)
+                cv2 = lloyd_max_codebook(vbh, d2)[1].cuda()
+                ms_h = time_op(lambda: ops.decode_attention_dl(q2, kp2, kn2, vt2, vn2, sl, ck2, cv2, Rk2,
+                                                               Rv2, 1.0 / math.sqrt(d2)), 20, 3, settle_s=0.1)
+                bytes_h = B * Hkv * T * (d2 // 2 + vbh * d2 // 8 + 8) + 2 * B * Hq * d2 * 2
+                extra[f"decode_attn_T{T}_d128_K4V{vbh}"] = {
+                    "us_per_step": ms_h * 1e3, "GBps": bytes_h / ms_h / 1e6,
+                    "hbm_frac": bytes_h / ms_h / 1e6 / HBM_PEAK_GBS, "tokens_per_s": B / ms_h * 1e3,
+                    "config": f"B {B}, Hq {Hq}, Hkv {Hkv}, head_dim 128, bf16 queries, fp32 norms"}
+                log(f"decode T={T} head_dim 128 K4/V{vbh}: {ms_h * 1e3:.1f} us, "
+                    f"{bytes_h / ms_h / 1e6:.0f} GB/s")
+                del vt2
+            del kp2, kn2, vn2
         del caches
     return out
 

@@ -315,12 +315,16 @@ def test_cache_reference_behaviours():
     assert prodc.attention_values(0, w).shape == (2, 1, 64)
 
 
-def test_cache_gqa_batched_decode_matches_composition():
+@pytest.mark.parametrize("d,vb", [(64, 2), (128, 2), (128, 3)])
+def test_cache_gqa_batched_decode_matches_composition(d, vb):
+    # the fused decode (decode layout: head_dim 64 and 128) against scores, softmax and
+    # values composed from the cache's own ops
     from turboquant_kv import QuantizedKVCache, TurboQuantConfig
     torch.manual_seed(1)
-    B, Hq, H, d, T_ = 2, 8, 2, 64, 700
-    kv = QuantizedKVCache(TurboQuantConfig(key_bits=4, value_bits=2), 1, 1024, H, d, device=DEV,
+    B, Hq, H, T_ = 2, 8, 2, 700
+    kv = QuantizedKVCache(TurboQuantConfig(key_bits=4, value_bits=vb), 1, 1024, H, d, device=DEV,
                           batch_size=B)
+    assert kv._dl
     kv.append(0, torch.randn(B, H, 500, d, device=DEV), torch.randn(B, H, 500, d, device=DEV))
     kv.append(0, torch.randn(B, H, T_ - 500, d, device=DEV), torch.randn(B, H, T_ - 500, d, device=DEV))
     q = torch.randn(B, Hq, d, device=DEV)

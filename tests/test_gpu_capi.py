@@ -174,10 +174,9 @@ def k_scores_pairs(q, pairs, norms, cen, R):
     return out.cpu().numpy()
 
 
-def k_pack_dl(packed, t_cap, pos, values, cache=None, vbits=2):
+def k_pack_dl(packed, t_cap, pos, values, cache=None, vbits=2, d=64):
     """Bit-plane rows [S, n, P] -> decode-layout cache (created zeroed when None)."""
     S, n, _ = packed.shape
-    d = 64
     bits = vbits if values else 4
     if cache is None:
         shape = (S, t_cap // 64, 8 * vbits * d) if values else (S, t_cap, d // 2)
@@ -189,12 +188,12 @@ def k_pack_dl(packed, t_cap, pos, values, cache=None, vbits=2):
     return cache
 
 
-def k_unpack_dl(cache, t_cap, t0, n, values, vbits=2):
+def k_unpack_dl(cache, t_cap, t0, n, values, vbits=2, d=64):
     S = cache.shape[0]
     bits = vbits if values else 4
-    out = torch.empty(S, n, bits * 8, dtype=torch.uint8, device=DEV)
+    out = torch.empty(S, n, bits * (d // 8), dtype=torch.uint8, device=DEV)
     capi.check(L().tq_unpack_decode_layout(capi.p(cache), capi.i64(S), capi.i64(t_cap), capi.i64(t0),
-                                           capi.i64(n), capi.i32(64), capi.i32(bits), capi.i32(values),
+                                           capi.i64(n), capi.i32(d), capi.i32(bits), capi.i32(values),
                                            capi.p(out), capi.stream()))
     sync()
     return out.cpu().numpy()
@@ -1213,7 +1212,7 @@ def test_decode_layout_attention_vs_f64(G):
 
 
 def dl_value_tiles_np(codes, vb):
-    """Independent numpy packing of 3/4-bit value codes [S, t_cap, 64] into decode-layout
+    """Independent numpy packing of 2/3/4-bit value codes [S, t_cap, 64] into decode-layout
     tiles [S, t_cap/64, 512*vb]: lane L = 16 sl + c owns words 0-3 at byte 16 L and the
     rest at 1024 + (8 vb - 16) L; byte k = 2 (m % 2) + t // 2 of word w holds the pair
     (tokens t = 2p, 2p + 1 of block 4m + sl, dim j): vb 4: w = 4 (m // 2) + j // 16, codes
@@ -1222,6 +1221,10 @@ def dl_value_tiles_np(codes, vb):
     3 (m // 2) + 0, 1, 2."""
     S, tc, d = codes.shape
     nt = tc // 64
+    if vb == 2:  # byte 16 (16 sl + c) + 4 m + dg: dim 16 dg + c of four tokens at bits 2 t
+        v = codes.reshape(S, nt, 4, 4, 4, 4, 16).astype(np.uint32)  # [S, tile, m, sl, t, dg, c]
+        packed = v[:, :, :, :, 0] | (v[:, :, :, :, 1] << 2) | (v[:, :, :, :, 2] << 4) | (v[:, :, :, :, 3] << 6)
+        return packed.transpose(0, 1, 3, 5, 2, 4).reshape(S, nt, 1024).astype(np.uint8)
     x = codes.reshape(S, nt, 4, 4, 4, d).astype(np.uint32)  # [S, tile, m, sl, t, j]
     out = np.zeros((S, nt, 512 * vb), np.uint32)
 
@@ -1432,6 +1435,108 @@ def test_decode_layout_config_shape_vs_f64(vb, T):
                                             Rk, Rv, 4, vb, 0.125)
     head = lambda x: np.max(np.max(np.abs(x - want), axis=-1) / np.max(np.abs(want), axis=-1))
     assert head(got) <= 0.5 * head(ref), (head(got), head(ref))
+
+
+@pytest.mark.parametrize("vb", [2, 3, 4])
+def test_decode_layout_d128_pack_roundtrip(vb):
+    # head_dim 128: key rows of 64 pair bytes; value tiles of two 64-dim halves, each the
+    # 64-dim tile of its dims (the independent numpy packing per half), from appends in
+    # uneven pieces
+    rs = np.random.RandomState(80 + vb)
+    S, t_cap, d = 2, 192, 128
+    codes = rs.randint(0, 1 << vb, (S, t_cap, d))
+    vp = np.stack([O.pack_codes(codes[s], vb) for s in range(S)])
+    vc = None
+    for pos, n in ((0, 3), (3, 61), (64, 65), (129, 63)):
+        vc = k_pack_dl(np.ascontiguousarray(vp[:, pos:pos + n]), t_cap, pos, 1, vc, vbits=vb, d=d)
+    tiles = vc.cpu().numpy().reshape(S, t_cap // 64, 2, 512 * vb)
+    for h in range(2):
+        assert np.array_equal(tiles[:, :, h].reshape(S, t_cap // 64, -1),
+                              dl_value_tiles_np(codes[:, :, 64 * h:64 * h + 64], vb)), h
+    assert np.array_equal(k_unpack_dl(vc, t_cap, 0, t_cap, 1, vbits=vb, d=d), vp)
+    assert np.array_equal(k_unpack_dl(vc, t_cap, 7, 100, 1, vbits=vb, d=d), vp[:, 7:107])
+    kcodes = rs.randint(0, 16, (S, t_cap, d))
+    kpk = np.stack([O.pack_codes(kcodes[s], 4) for s in range(S)])
+    kc = k_pack_dl(kpk, t_cap, 0, 0, d=d)
+    pairs = kc.cpu().numpy()
+    assert np.array_equal(pairs, ((kcodes[:, :, 0::2] << 4) | kcodes[:, :, 1::2]).astype(np.uint8))
+    assert np.array_equal(k_unpack_dl(kc, t_cap, 0, t_cap, 0, d=d), kpk)
+
+
+@pytest.mark.parametrize("vb,G", [(2, 4), (3, 4), (4, 4), (2, 1), (3, 6)])
+def test_decode_layout_d128_vs_f64(vb, G):
+    # head_dim 128 (two 64-dim halves per operand): Hq 32 / Hkv 8 at G = 4, ragged lengths
+    # (several splits for the long rows), fp32 / bf16 / fp16 queries against the float64
+    # decode oracle, output and log-sum-exp.
+    rs = np.random.RandomState(900 + 10 * vb + G)
+    d, Hkv, Tc = 128, 8 if G == 4 else 2, 2112
+    seq = [0, 1, 65, 700, 2100]
+    B, Hq = len(seq), Hkv * G
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    n = B * Hkv * Tc
+    K = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    V = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    K[:, rs.choice(d, 4, replace=False)] *= 20.0
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, Tc, -1), Tc, 0, 0, d=d)
+    vc = k_pack_dl(vp.reshape(B * Hkv, Tc, -1), Tc, 0, 1, vbits=vb, d=d)
+    kp, vp = kp.reshape(B, Hkv, Tc, -1), vp.reshape(B, Hkv, Tc, -1)
+    kn, vn = kn.reshape(B, Hkv, Tc), vn.reshape(B, Hkv, Tc)
+    q = (rs.randn(B, Hq, d) * 3.0).astype(np.float32)
+    print(f"decode d=128 vb={vb} G={G}", flush=True)
+    for dt, tol in ((torch.float32, 1e-4), (torch.bfloat16, 1e-2), (torch.float16, 3e-3)):
+        qt = torch.from_numpy(q).to(DEV).to(dt)
+        qf = qt.float().cpu().numpy()
+        want, want_lse = O.decode_attention_f64(qf, kp, kn, vp, vn, seq, ck, cv, Rk, Rv, 4, vb,
+                                                0.125, return_lse=True)
+        got, lse = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+        assert np.all(got[0] == 0) and np.isneginf(lse[0]).all()
+        for bi in range(1, B):
+            err = np.max(np.abs(got[bi] - want[bi])) / np.max(np.abs(want[bi]))
+            assert err <= tol, (dt, seq[bi], err)
+        ok = np.isfinite(want_lse)
+        # the scores' rounding error follows the products q_j k_j, not the score (outlier
+        # channels make them large where a score is near 0): the log-sum-exp is held to the
+        # tolerance relative to its batch row's largest magnitude
+        scale = np.maximum(1.0, np.max(np.where(ok, np.abs(want_lse), 0.0), axis=1, keepdims=True))
+        lse_tol = 1e-2 if dt == torch.bfloat16 else 1e-5
+        rel = np.abs(np.where(ok, lse - want_lse, 0.0)) / scale
+        assert np.max(rel) <= lse_tol, (dt, np.max(rel))
+
+
+@pytest.mark.parametrize("vb", [2, 3])
+def test_decode_layout_d128_config_shape_vs_f64(vb):
+    # B = 32, Hq = 32, Hkv = 8, head_dim 128, T = 1024 (one split per stream: the kernel
+    # applies R_v and writes the output itself), bf16 queries and K/V with outlier channels
+    rs = np.random.RandomState(17 + vb)
+    B, Hq, Hkv, d, T_ = 32, 32, 8, 128, 1024
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    K = rs.randn(B, Hkv, T_, d).astype(np.float32)
+    V = rs.randn(B, Hkv, T_, d).astype(np.float32)
+    for h in range(Hkv):
+        ch = rs.choice(d, 4, replace=False)
+        K[:, h, :, ch] *= 20.0
+        V[:, h, :, ch] *= 20.0
+    K = torch.from_numpy(K).to(torch.bfloat16).float().numpy().reshape(-1, d)
+    V = torch.from_numpy(V).to(torch.bfloat16).float().numpy().reshape(-1, d)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, T_, -1), T_, 0, 0, d=d)
+    vc = k_pack_dl(vp.reshape(B * Hkv, T_, -1), T_, 0, 1, vbits=vb, d=d)
+    kp, vp = kp.reshape(B, Hkv, T_, -1), vp.reshape(B, Hkv, T_, -1)
+    kn, vn = kn.reshape(B, Hkv, T_), vn.reshape(B, Hkv, T_)
+    qt = torch.from_numpy(rs.randn(B, Hq, d).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    seq = [T_] * B
+    want = O.decode_attention_f64(qt.float().cpu().numpy(), kp, kn, vp, vn, seq, ck, cv, Rk, Rv,
+                                  4, vb, 0.125)
+    got, _ = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb)
+    err = max(np.max(np.abs(got[b] - want[b])) / np.max(np.abs(want[b])) for b in range(B))
+    assert err <= 1e-2, err
 
 
 def test_scan_many_exact_ties_take_fallback():

@@ -428,9 +428,10 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
   }
 }
 
-// One 64-thread block per query row: log-sum-exp merge of the splits, o = o_rot / L,
-// out = o @ R_v; lse (natural log) = (max + log2 L) * ln 2.
-__global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restrict__ part,
+// One D-thread block per query row (D = head_dim, 64 or 128): log-sum-exp merge of the
+// splits, o = o_rot / L, out = o @ R_v; lse (natural log) = (max + log2 L) * ln 2.
+template <int D = kDim>
+__global__ __launch_bounds__(D) void fused_combine_kernel(const float* __restrict__ part,
                                                            const float2* __restrict__ stats,
                                                            int nsplit, int64_t split_tokens,
                                                            const int32_t* __restrict__ seq_lens,
@@ -438,14 +439,14 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
                                                            const float* __restrict__ vrot,
                                                            int out_dt, void* __restrict__ out,
                                                            float* __restrict__ lse) {
-  __shared__ float o_s[kDim];
+  __shared__ float o_s[D];
   const int64_t row = blockIdx.x;
   const int b = (int)(row / hq);
   const int j = threadIdx.x;
   // column j of R_v, requested first: its loads overlap the split merge below
-  float rcol[kDim];
+  float rcol[D];
 #pragma unroll
-  for (int k = 0; k < kDim; ++k) rcol[k] = vrot[k * kDim + j];
+  for (int k = 0; k < D; ++k) rcol[k] = vrot[k * D + j];
   const int64_t T = min((int64_t)max(seq_lens[b], 0), t_max);
   const int ns = (int)((T + split_tokens - 1) / split_tokens);
   float M = -INFINITY;
@@ -455,21 +456,23 @@ __global__ __launch_bounds__(64) void fused_combine_kernel(const float* __restri
     const float2 st = stats[row * nsplit + s];
     const float f = st.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st.x - M);
     L += st.y * f;
-    o += part[(row * nsplit + s) * kDim + j] * f;
+    o += part[(row * nsplit + s) * D + j] * f;
   }
   const bool any = ns > 0 && L > 0.f;
   o_s[j] = any ? o / L : 0.f;
   __syncthreads();
   float r = 0.f;
 #pragma unroll
-  for (int k = 0; k < kDim; ++k) r = fmaf(o_s[k], rcol[k], r);
-  store_from_f32(out, row * kDim + j, r, out_dt);
+  for (int k = 0; k < D; ++k) r = fmaf(o_s[k], rcol[k], r);
+  store_from_f32(out, row * D + j, r, out_dt);
   if (lse && j == 0) lse[row] = any ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
 }
 
 // ------------------------------------------------------------------ decode layout
 // The decode layout holds the same codes as the bit-plane rows, arranged for the
-// decode kernel (4-bit keys; 2-, 3- or 4-bit values; head_dim 64):
+// decode kernel (4-bit keys; 2-, 3- or 4-bit values; head_dim 64 -- head_dim 128 as two
+// 64-dim halves: key bytes 32 h .., value tile half h at byte h * 512 VB, each laid out
+// as below for dims 64 h ..):
 //   keys    per token d/2 bytes; byte p = (code[2p] << 4) | code[2p+1]
 //   values  64-token tiles of 512 * VB bytes.  Lane L = 16 sl + c of a wave reads the
 //           words its p.V operands need: words 0-3 at byte 16 L, words 4.. at byte
@@ -494,6 +497,7 @@ constexpr int kDlTab = 256 * kDlEntry;         // 64 KB per table
 constexpr int kDlKLo = 1152;
 constexpr int kDlTabs = 2 * kDlTab + 5 * kDlEntry;
 constexpr int kDlMinSplit = kDlWaves * 64;     // one tile per wave
+constexpr int kDlMaxDim = 128;                 // head_dim of the largest (contiguous) layout
 
 struct DlArgs {
   const void* q;
@@ -608,11 +612,18 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // same for pools of any size: rows at 64-bit addresses from clamped block ids.
 // ND: the norms' dtype -- 0 fp32, TQ_F16 or TQ_BF16 (contiguous caches only: a bf16 model's
 // cache keeps its norms in bf16, as the reference's quantize returns them).
-template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0>
+// NH: 64-dim halves of the head (1: head_dim 64; 2: head_dim 128, contiguous caches).  A
+// 128-dim key row is 64 pair bytes, half h at bytes 32 h ..; a 128-dim value tile is two
+// 64-dim tiles, half h (dims 64 h ..) at byte h * 512 VB.  Each half runs the 64-dim
+// operand layouts below; q.K chains both halves' products into one score, p.V keeps one
+// accumulator set per half.
+template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0, int NH = 1>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   constexpr bool PAGED = PG != 0, SUB16 = PG == 2 || PG == 4, WIDE = PG >= 3;
+  constexpr int D = 64 * NH;  // head_dim
   static_assert(VB >= 2 && VB <= 4, "value width");
   static_assert(ND == 0 || PG == 0, "16-bit norms: contiguous caches");
+  static_assert(NH == 1 || (NH == 2 && PG == 0), "head_dim 128: contiguous caches");
   // value words per lane and tile as loaded (16-token sub-blocks of 3-bit values: the four
   // groups' 4-byte and 2-byte shares, reassembled into tile words at their use)
   constexpr int VW = VB == 2 ? 4 : SUB16 ? 8 : 2 * VB;
@@ -624,8 +635,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
   // at kDlKLo).  After the tile loop the bytes hold the reduction.
   __shared__ __attribute__((aligned(16))) char tabs[kDlTabs];
-  __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4][2][kDim];  // q * qs2: hi, lo
-  __shared__ float qs_s[4][kDim];
+  __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4][2][D];  // q * qs2: hi, lo
+  __shared__ float qs_s[4][D];
+  __shared__ float hmax_s[NH == 2 ? kDlWaves : 1];  // head_dim 128: per-wave |q_rot| maxima
   __shared__ float cen_s[32];  // 16 key centroids, then the value centroids
   __shared__ float sc_s[2];  // value and key centroid scales
   __shared__ float qs2_s[4];  // per-head query scales
@@ -671,10 +683,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // use, so what the loads return for them never matters.
   const size_t sbase = PAGED ? 0 : (size_t)bg * (size_t)a.t_cap;
   const uint32_t nrows = PAGED ? a.pool_rows : (uint32_t)a.t_cap;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32, nrows * 32);
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.kpairs + sbase * 32 * NH, nrows * 32 * NH);
   const __amdgpu_buffer_rsrc_t vrs =
-      make_rsrc(a.vblocks + sbase * (8 * VB),
-                PAGED ? nrows * (8 * VB) : (uint32_t)(a.t_cap >> 6) * VTILE);
+      make_rsrc(a.vblocks + sbase * (8 * VB * NH),
+                PAGED ? nrows * (8 * VB) : (uint32_t)(a.t_cap >> 6) * VTILE * NH);
   // Norms are read four tokens at a time (t_cap % 4 == 0, pools of whole blocks).
   constexpr uint32_t NSZ = ND ? 2 : 4;  // bytes per norm
   const uint32_t nbytes = nrows * NSZ;
@@ -689,8 +701,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
                 PAGED ? (uint32_t)a.bt_stride * 4u : 0u);
 
   struct Tile {
-    u32x2 k[4];      // group g: key bytes 8 sl .. 8 sl + 7 of token 16 g + col
-    uint32_t v[VW];  // the lane's value tile words (layout above)
+    u32x2 k[NH][4];      // half h, group g: key bytes 32 h + 8 sl .. + 7 of token 16 g + col
+    uint32_t v[NH][VW];  // the lane's value tile words of each half (layout above)
     float kn[4], vn[4];  // tokens 16 gq + 4 sl + r
   };
   // Paged: block id of the tile at t0 (one per tile, the same in every lane; SUB16: one
@@ -742,61 +754,67 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if constexpr (WIDE) {  // pool rows (< 2^32) at 64-bit byte addresses
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        x.k[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl));
+        x.k[0][g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(a.kpairs + (size_t)(rg[g] + col) * 32 + 8 * sl));
       if constexpr (SUB16) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
           const uint8_t* sb = a.vblocks + (size_t)(rg[m] >> 4) * SBB;
           if constexpr (VB == 2) {
-            x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
+            x.v[0][m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
           } else if constexpr (VB == 4) {
             const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(sb + lane * 8));
-            x.v[2 * m] = w.x; x.v[2 * m + 1] = w.y;
+            x.v[0][2 * m] = w.x; x.v[0][2 * m + 1] = w.y;
           } else {
-            x.v[m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
-            x.v[4 + m] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(sb + 256 + lane * 2));
+            x.v[0][m] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(sb + lane * 4));
+            x.v[0][4 + m] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(sb + 256 + lane * 2));
           }
         }
       } else {
         const uint8_t* tb = a.vblocks + (size_t)vt * VTILE;
         const u32x4 v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb + lane * 16));
-        x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
+        x.v[0][0] = v0.x; x.v[0][1] = v0.y; x.v[0][2] = v0.z; x.v[0][3] = v0.w;
         if constexpr (VB == 3) {
           const u32x2 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(tb + 1024 + lane * 8));
-          x.v[4] = v1.x; x.v[5] = v1.y;
+          x.v[0][4] = v1.x; x.v[0][5] = v1.y;
         } else if constexpr (VB == 4) {
           const u32x4 v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb + 1024 + lane * 16));
-          x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
+          x.v[0][4] = v1.x; x.v[0][5] = v1.y; x.v[0][6] = v1.z; x.v[0][7] = v1.w;
         }
       }
     } else {
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      x.k[g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 + 8 * sl), 0, kNT);
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        x.k[h][g] = __builtin_amdgcn_raw_buffer_load_b64(krs, (int)((rg[g] + col) * 32 * NH + 32 * h + 8 * sl), 0, kNT);
     if constexpr (SUB16) {
       // value sub-block of group m = its first pool row / 16 (rows of a group are 16-aligned)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int so = (int)((rg[m] >> 4) * SBB);
         if constexpr (VB == 2) {
-          x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
+          x.v[0][m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
         } else if constexpr (VB == 4) {
           const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(vrs, so + lane * 8, 0, kNT);
-          x.v[2 * m] = w.x; x.v[2 * m + 1] = w.y;
+          x.v[0][2 * m] = w.x; x.v[0][2 * m + 1] = w.y;
         } else {
-          x.v[m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
-          x.v[4 + m] = __builtin_amdgcn_raw_buffer_load_b16(vrs, so + 256 + lane * 2, 0, kNT);
+          x.v[0][m] = __builtin_amdgcn_raw_buffer_load_b32(vrs, so + lane * 4, 0, kNT);
+          x.v[0][4 + m] = __builtin_amdgcn_raw_buffer_load_b16(vrs, so + 256 + lane * 2, 0, kNT);
         }
       }
     } else {
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + lane * 16), 0, kNT);
-      x.v[0] = v0.x; x.v[1] = v0.y; x.v[2] = v0.z; x.v[3] = v0.w;
-      if constexpr (VB == 3) {
-        const u32x2 v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, (int)(vt * VTILE + 1024 + lane * 8), 0, kNT);
-        x.v[4] = v1.x; x.v[5] = v1.y;
-      } else if constexpr (VB == 4) {
-        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(vt * VTILE + 1024 + lane * 16), 0, kNT);
-        x.v[4] = v1.x; x.v[5] = v1.y; x.v[6] = v1.z; x.v[7] = v1.w;
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const int tb = (int)((vt * NH + h) * VTILE);
+        const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(vrs, tb + lane * 16, 0, kNT);
+        x.v[h][0] = v0.x; x.v[h][1] = v0.y; x.v[h][2] = v0.z; x.v[h][3] = v0.w;
+        if constexpr (VB == 3) {
+          const u32x2 v1 = __builtin_amdgcn_raw_buffer_load_b64(vrs, tb + 1024 + lane * 8, 0, kNT);
+          x.v[h][4] = v1.x; x.v[h][5] = v1.y;
+        } else if constexpr (VB == 4) {
+          const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(vrs, tb + 1024 + lane * 16, 0, kNT);
+          x.v[h][4] = v1.x; x.v[h][5] = v1.y; x.v[h][6] = v1.z; x.v[h][7] = v1.w;
+        }
       }
     }
     }
@@ -844,17 +862,21 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // the query element as the aligned 32-bit word that holds it (one load whatever the
   // dtype, converted after the barrier: a dtype branch here made the compiler wait for it
   // before issuing the loads below)
-  const int qh = tid >> 6;
-  const int64_t qe = (qh0 + (qh < a.G ? qh : 0)) * kDim + (tid & 63);
+  // thread tid < 4 D: head qh = tid / D, dim qj = tid % D
+  const int qh = tid / D, qj = tid % D;
+  const int64_t qe = (qh0 + (qh < a.G ? qh : 0)) * D + qj;
   const int64_t qbyte = qe * (a.q_dt == TQ_F32 ? 4 : 2);
   uint32_t qraw = 0;
-  if (tid < 4 * kDim)
+  if (tid < 4 * D)
     qraw = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(a.q) + (qbyte & ~int64_t(3)));
-  float4 rrow[kDim / 4];  // row `lane` of R_k (waves 0-3)
-  if (tid < 4 * kDim) {
-    const float4* r4 = reinterpret_cast<const float4*>(a.krot + (tid & 63) * kDim);
+  // row qj of R_k (head_dim 64: waves 0-3, held from here; 128: read in the product below)
+  float4 rrow[NH == 1 ? kDim / 4 : 1];
+  if constexpr (NH == 1) {
+    if (tid < 4 * kDim) {
+      const float4* r4 = reinterpret_cast<const float4*>(a.krot + (tid & 63) * kDim);
 #pragma unroll
-    for (int k = 0; k < kDim / 4; ++k) rrow[k] = r4[k];
+      for (int k = 0; k < kDim / 4; ++k) rrow[k] = r4[k];
+    }
   }
   Blk bnx{};  // paged: block id(s) of the next tile to load
   load_tile(tf, ta, load_block(tf));
@@ -865,9 +887,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const int64_t T = min((int64_t)max(slen, 0), a.t_cap);
   const int64_t t_end = min(T, t_begin + a.split_tokens);
   if (t_begin >= t_end) {  // uniform
-    if (a.out != nullptr && T == 0 && tid < a.G * kDim) {  // empty sequence: zeros, lse -inf
-      store_from_f32(a.out, qh0 * kDim + tid, 0.f, a.q_dt);
-      if (a.lse && (tid & 63) == 0) a.lse[qh0 + (tid >> 6)] = -INFINITY;
+    if (a.out != nullptr && T == 0 && tid < a.G * D) {  // empty sequence: zeros, lse -inf
+      store_from_f32(a.out, qh0 * D + tid, 0.f, a.q_dt);
+      if (a.lse && qj == 0) a.lse[qh0 + qh] = -INFINITY;
     }
     return;
   }
@@ -875,15 +897,49 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const int ts = (int)min((int64_t)max(sstart, 0), T);  // first unmasked token
   const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
   if (tid < 32) cen_s[tid] = cenv;
-  if (tid < 4 * kDim) {
+  if (tid < 4 * D) {
     const uint32_t bits = a.q_dt == TQ_F32 ? qraw : (qraw >> (8 * (qbyte & 2))) & 0xFFFFu;
     const float qv = a.q_dt == TQ_F32 ? __uint_as_float(bits)
                      : a.q_dt == TQ_BF16 ? __uint_as_float(bits << 16)
                                          : __half2float(__ushort_as_half((unsigned short)bits));
-    qs_s[qh][tid & 63] = qh < a.G ? qv : 0.f;
+    qs_s[qh][qj] = qh < a.G ? qv : 0.f;
   }
   __syncthreads();
-  if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane
+  if constexpr (NH == 2) {  // head_dim 128: every wave rotates (head wave / 2, dims 64 (wave % 2) ..)
+    const int h = qh, j = qj;
+    const float4* r4 = reinterpret_cast<const float4*>(a.krot + j * D);
+    float v = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < D / 4; ++k) {
+      const float4 r = r4[k];
+      v = fmaf(r.x, qs_s[h][4 * k], v);
+      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
+      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
+      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
+    }
+    v *= a.qscale;
+    const float wm = wave_max(fabsf(v));
+    if (lane == 0) hmax_s[wave] = wm;
+    if (tid < 32) {  // the centroid scales (the key and value centroids are in cen_s)
+      const float c = fabsf(cen_s[tid & 15]);
+      const float vcv = (tid & 15) < (1 << VB) ? fabsf(cen_s[16 + (tid & 15)]) : 0.f;
+      float km = c, vm = vcv;
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) {
+        km = fmaxf(km, __shfl_xor(km, o));
+        vm = fmaxf(vm, __shfl_xor(vm, o));
+      }
+      if (tid == 0) { sc_s[0] = pow2_scale(vm); sc_s[1] = pow2_scale(km); }
+    }
+    __syncthreads();
+    // fp16 hi + lo parts, the head's largest element scaled into [0.5, 1) (both halves)
+    const float s2 = pow2_scale(fmaxf(hmax_s[2 * h], hmax_s[2 * h + 1]));
+    const float x = v * s2;
+    const _Float16 xh = (_Float16)x;
+    qhl_s[h][0][j] = xh;
+    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
+    if (j == 0) qs2_s[h] = s2;
+  } else if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane
     const int h = tid >> 6, j = tid & 63;
     float v = 0.f;
 #pragma unroll
@@ -978,23 +1034,35 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // (multiplies the centroid hi parts); bqh[c]: hi columns only (centroid lo parts).
   // Without PREC_K each token group g has its own columns instead: col 4g + h = head h
   // (hi halves), so one accumulator collects all four groups already in the score layout
-  // below.  bcol[c][g]: the lane's hi halves if col / 4 == g, else zero.
-  v8h bq[2], bqh[2], bcol[2][4];
+  // below.  bcol[c][g]: the lane's hi halves if col / 4 == g, else zero.  Head_dim 128: the
+  // same per half h (dims 64 h + ..); without PREC_K the hi halves bhi[h][c] are kept and
+  // the per-group columns selected at their use.
+  v8h bq[NH][2], bqh[NH][2], bcol[NH == 1 ? 2 : 1][4], bhi[NH][2];
+  const v8h vz = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int h = 0; h < NH; ++h)
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const int d0 = 16 * sl + 8 * c;
-    const v8h z = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+    const int d0 = 64 * h + 16 * sl + 8 * c;
+    const v8h z = vz;
     if constexpr (PREC_K) {
       const v8h hi = col < 4 ? *reinterpret_cast<const v8h*>(&qhl_s[col][0][d0]) : z;
       const v8h lo = (col >= 4 && col < 8) ? *reinterpret_cast<const v8h*>(&qhl_s[col - 4][1][d0]) : z;
-      bq[c] = col < 4 ? hi : lo;
-      bqh[c] = hi;
+      bq[h][c] = col < 4 ? hi : lo;
+      bqh[h][c] = hi;
     } else {
       const v8h hi = *reinterpret_cast<const v8h*>(&qhl_s[col & 3][0][d0]);
+      bhi[h][c] = hi;
+      if constexpr (NH == 1) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) bcol[c][g] = (col >> 2) == g ? hi : z;
+        for (int g = 0; g < 4; ++g) bcol[c][g] = (col >> 2) == g ? hi : z;
+      }
     }
   }
+  auto bcol_of = [&](int h, int c, int g) -> v8h {
+    if constexpr (NH == 1) return bcol[c][g];
+    else return (col >> 2) == g ? bhi[h][c] : vz;
+  };
   // Score layout after q.K: lane 16 sl + 4 g + h holds tokens 16 g + 4 sl + r (register r)
   // of head h; g = token group of the 16x16x32 MFMA whose rows hold them.
   const float kinv = 1.f / (ksc * qs2_s[hh]);  // a power of two: exact
@@ -1004,24 +1072,26 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
                           : EXACT_V ? (uint32_t)(lane & 15) * 16 : (uint32_t)(lane & 31) * 8;
   // VB 3, 4: tile word i of half G (16-token sub-blocks: bytes 0-1 from group 2G's share,
   // bytes 2-3 from group 2G + 1's)
-  auto tword = [&](const Tile& x, int G, int i) -> uint32_t {
+  auto tword = [&](const Tile& x, int hd, int G, int i) -> uint32_t {
+    const uint32_t* v = x.v[hd];
     if constexpr (!SUB16) {
-      return x.v[(VB == 4 ? 4 : 3) * G + i];
+      return v[(VB == 4 ? 4 : 3) * G + i];
     } else if constexpr (VB == 4) {
-      return __builtin_amdgcn_perm(x.v[2 * (2 * G + 1) + (i >> 1)], x.v[2 * (2 * G) + (i >> 1)],
+      return __builtin_amdgcn_perm(v[2 * (2 * G + 1) + (i >> 1)], v[2 * (2 * G) + (i >> 1)],
                                    (i & 1) ? 0x07060302u : 0x05040100u);
     } else {
-      return i == 2 ? __builtin_amdgcn_perm(x.v[4 + 2 * G + 1], x.v[4 + 2 * G], 0x05040100u)
-                    : __builtin_amdgcn_perm(x.v[2 * G + 1], x.v[2 * G], i ? 0x07060302u : 0x05040100u);
+      return i == 2 ? __builtin_amdgcn_perm(v[4 + 2 * G + 1], v[4 + 2 * G], 0x05040100u)
+                    : __builtin_amdgcn_perm(v[2 * G + 1], v[2 * G], i ? 0x07060302u : 0x05040100u);
     }
   };
-  // VB 3, 4: the word whose four bytes index the pair entries of half G, dim group dg
-  auto vword = [&](const Tile& x, int G, int dg) -> uint32_t {
+  // VB 3, 4: the word whose four bytes index the pair entries of token half G, dim group
+  // dg (of head half hd)
+  auto vword = [&](const Tile& x, int hd, int G, int dg) -> uint32_t {
     if constexpr (VB == 4) {
-      return tword(x, G, dg);
+      return tword(x, hd, G, dg);
     } else {
-      if (dg < 3) return tword(x, G, dg);
-      const uint32_t x0 = tword(x, G, 0), x1 = tword(x, G, 1), x2 = tword(x, G, 2);
+      if (dg < 3) return tword(x, hd, G, dg);
+      const uint32_t x0 = tword(x, hd, G, 0), x1 = tword(x, hd, G, 1), x2 = tword(x, hd, G, 2);
       return ((x0 >> 6) & 0x03030303u) | ((x1 >> 4) & 0x0C0C0C0Cu) | ((x2 >> 2) & 0x30303030u);
     }
   };
@@ -1030,9 +1100,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   };
 
   float M = -INFINITY, l = 0.f;
-  v4f acc[4];  // dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 16 dg + lane
+  // half h, dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 64 h + 16 dg + lane
+  v4f acc[NH][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < NH; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[h][i] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   // One 64-token tile of this wave: x holds its data, loaded one tile ahead.
   auto process = [&](const Tile& cur, int t0) {
@@ -1046,10 +1119,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       // one product per term; chunk c accumulates in its own chain
       v4f d2[2] = {(v4f){0.f, 0.f, 0.f, 0.f}, (v4f){0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
+      for (int hd = 0; hd < NH; ++hd)
+#pragma unroll
       for (int g = 0; g < 4; ++g) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const uint32_t w = c ? cur.k[g].y : cur.k[g].x;
+          const uint32_t w = c ? cur.k[hd][g].y : cur.k[hd][g].x;
           uint32_t ad[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) ad[j] = byte_addr(kcopy, w, j);
@@ -1057,7 +1132,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
                                 *reinterpret_cast<const uint32_t*>(tabs + ad[1]),
                                 *reinterpret_cast<const uint32_t*>(tabs + ad[2]),
                                 *reinterpret_cast<const uint32_t*>(tabs + ad[3]));
-          d2[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bcol[c][g], d2[c], 0, 0, 0);
+          d2[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bcol_of(hd, c, g), d2[c], 0, 0, 0);
         }
       }
       skk = (d2[0] + d2[1]) * kinv;
@@ -1067,8 +1142,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     for (int g = 0; g < 4; ++g) {
       dk[g] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const uint32_t w = c ? cur.k[g].y : cur.k[g].x;
+      for (int hc = 0; hc < 2 * NH; ++hc) {
+        const int hd = hc >> 1, c = hc & 1;
+        const uint32_t w = c ? cur.k[hd][g].y : cur.k[hd][g].x;
         uint32_t ad[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) ad[j] = byte_addr(kcopy, w, j);
@@ -1080,8 +1156,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
                               *reinterpret_cast<const uint32_t*>(tabs + ad[1] + kDlKLo),
                               *reinterpret_cast<const uint32_t*>(tabs + ad[2] + kDlKLo),
                               *reinterpret_cast<const uint32_t*>(tabs + ad[3] + kDlKLo));
-        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[c], dk[g], 0, 0, 0);
-        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[c], dk[g], 0, 0, 0);
+        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[hd][c], dk[g], 0, 0, 0);
+        dk[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[hd][c], dk[g], 0, 0, 0);
       }
     }
     // Lane 16 sl + 4 g + h takes group g's column h (lane 16 sl + h) plus column 4 + h
@@ -1098,21 +1174,25 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 
     // The value-centroid lookups depend only on the tile's bytes: issued here, their LDS
     // latency runs under the softmax arithmetic.  (p.V below describes the operands.)
+    // (head half hd's operands; head_dim 128: half 1's after half 0's products)
+    auto value_ops = [&](int hd, v8h (&bv)[8]) {
+      if constexpr (VB == 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
+          const int G = i >> 2, dg = i & 3;
+          bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[hd][2 * G], dg)),
+                        *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[hd][2 * G + 1], dg)));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; bytes: blocks 8G + sl, 8G + 4 + sl
+          const uint32_t w = vword(cur, hd, i >> 2, i & 3);
+          bv[i] = as_v8h(vpair(w, 0), vpair(w, 1), vpair(w, 2), vpair(w, 3));
+        }
+      }
+    };
     v8h bv[8];
-    if constexpr (!EXACT_V && VB == 2) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; value words m = 2G, 2G + 1
-        const int G = i >> 2, dg = i & 3;
-        bv[i] = cat_h(*reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg)),
-                      *reinterpret_cast<const v4h*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg)));
-      }
-    } else if constexpr (!EXACT_V) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {  // i = 4 G + dg; bytes: blocks 8G + sl, 8G + 4 + sl
-        const uint32_t w = vword(cur, i >> 2, i & 3);
-        bv[i] = as_v8h(vpair(w, 0), vpair(w, 1), vpair(w, 2), vpair(w, 3));
-      }
-    }
+    if constexpr (!EXACT_V) value_ops(0, bv);
 
     // ---- online softmax (register r = token t0 + 16 gq + 4 sl + r, head hh)
     // Tokens at or past te are masked with selects at their use (branch-free: a masked
@@ -1135,7 +1215,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       l *= f;
       const v4f fv = {__shfl(f, 0), __shfl(f, 1), __shfl(f, 2), __shfl(f, 3)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= fv;
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[h][i] *= fv;
       M = mn;
     }
     v4h wh, wl;
@@ -1168,20 +1250,27 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     if constexpr (!EXACT_V) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        acc[i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[i >> 2], bv[i], acc[i & 3], 0, 0, 0);
+        acc[0][i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[i >> 2], bv[i], acc[0][i & 3], 0, 0, 0);
+      if constexpr (NH == 2) {
+        value_ops(1, bv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          acc[1][i & 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[i >> 2], bv[i], acc[1][i & 3], 0, 0, 0);
+      }
     } else {
 #pragma unroll
-      for (int G = 0; G < 2; ++G) {
+      for (int hG = 0; hG < 2 * NH; ++hG) {
+        const int hd = hG >> 1, G = hG & 1;
         v8h bh[4], bl[4];
 #pragma unroll
         for (int dg = 0; dg < 4; ++dg) {
           if constexpr (VB == 2) {
-            const u32x4 e0 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G], dg));
-            const u32x4 e1 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[2 * G + 1], dg));
+            const u32x4 e0 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[hd][2 * G], dg));
+            const u32x4 e1 = *reinterpret_cast<const u32x4*>(tabs + byte_addr(vcopy, cur.v[hd][2 * G + 1], dg));
             bh[dg] = as_v8h(e0.x, e0.y, e1.x, e1.y);
             bl[dg] = as_v8h(e0.z, e0.w, e1.z, e1.w);
           } else {
-            const uint32_t w = vword(cur, G, dg);
+            const uint32_t w = vword(cur, hd, G, dg);
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -1193,13 +1282,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
             bl[dg] = as_v8h(lo[0], lo[1], lo[2], lo[3]);
           }
         }
-        if (G == 0) __builtin_amdgcn_sched_barrier(0);
+        if (hG == 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bh[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[hd][dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bh[dg], acc[hd][dg], 0, 0, 0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(awl[G], bh[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[hd][dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(awl[G], bh[dg], acc[hd][dg], 0, 0, 0);
 #pragma unroll
-        for (int dg = 0; dg < 4; ++dg) acc[dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bl[dg], acc[dg], 0, 0, 0);
+        for (int dg = 0; dg < 4; ++dg) acc[hd][dg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[G], bl[dg], acc[hd][dg], 0, 0, 0);
       }
     }
 
@@ -1225,11 +1314,14 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   }
 
   // The whole-sequence path's R_v column (threads of waves 0-3: dim = lane), requested
-  // now so that its latency runs under the reduction below.
-  float rv[kDim];
-  if ((a.out != nullptr) & (tid < 4 * kDim)) {
+  // now so that its latency runs under the reduction below (head_dim 128: read in the
+  // product at the end).
+  float rv[NH == 1 ? kDim : 1];
+  if constexpr (NH == 1) {
+    if ((a.out != nullptr) & (tid < 4 * kDim)) {
 #pragma unroll
-    for (int k = 0; k < kDim; ++k) rv[k] = a.vrot[k * kDim + (tid & 63)];
+      for (int k = 0; k < kDim; ++k) rv[k] = a.vrot[k * kDim + (tid & 63)];
+    }
   }
   // ---- reduction: l over the lanes of a head; outputs over the waves (LDS)
   l += __shfl_xor(l, 4);
@@ -1254,21 +1346,23 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   float* red = reinterpret_cast<float*>(tabs);  // [wave][head m][dim]
   if (lane < 16) {
 #pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
     for (int dg = 0; dg < 4; ++dg)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) red[(wave * 4 + m) * kDim + 16 * dg + lane] = acc[dg][m] * fw[m];
+      for (int m = 0; m < 4; ++m) red[(wave * 4 + m) * D + 64 * h + 16 * dg + lane] = acc[h][dg][m] * fw[m];
   }
   __syncthreads();
-  if (tid < 4 * kDim) {
-    const int m = tid >> 6, dim = tid & 63;
+  if (tid < 4 * D) {
+    const int m = tid / D, dim = tid % D;
     float sum = 0.f;
-    for (int w = 0; w < kDlWaves; ++w) sum += red[(w * 4 + m) * kDim + dim];
+    for (int w = 0; w < kDlWaves; ++w) sum += red[(w * 4 + m) * D + dim];
     float L = 0.f;
     for (int w = 0; w < kDlWaves; ++w)
       if (red_m[w][m] != -INFINITY) L += red_l[w][m] * __builtin_amdgcn_exp2f(red_m[w][m] - mx[m]);
     if (a.out == nullptr) {  // several splits: partials for the combine kernel
       if (m < a.G) {
-        a.part[((qh0 + m) * a.nsplit + split) * kDim + dim] = sum / vsc;
+        a.part[((qh0 + m) * a.nsplit + split) * D + dim] = sum / vsc;
         if (dim == 0) a.stats[(qh0 + m) * a.nsplit + split] = make_float2(mx[m], L);
       }
     } else {  // the whole sequence: out = (o / L) @ R_v here
@@ -1279,13 +1373,18 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   }
   if (a.out != nullptr) {
     __syncthreads();
-    if (tid < 4 * kDim) {
-      const int m = tid >> 6, dim = tid & 63;
+    if (tid < 4 * D) {
+      const int m = tid / D, dim = tid % D;
       if (m < a.G) {
         float r = 0.f;
+        if constexpr (NH == 1) {
 #pragma unroll
-        for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv[k], r);
-        store_from_f32(a.out, (qh0 + m) * kDim + dim, r, a.q_dt);
+          for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv[k], r);
+        } else {
+#pragma unroll 8
+          for (int k = 0; k < D; ++k) r = fmaf(qs_s[m][k], a.vrot[k * D + dim], r);
+        }
+        store_from_f32(a.out, (qh0 + m) * D + dim, r, a.q_dt);
       }
     }
   }
@@ -1351,19 +1450,21 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
           (uint8_t)((code(s, t, 2 * pidx) << 4) | code(s, t, 2 * pidx + 1));
     }
   } else if (bits == 2) {
-    // value tiles of 64 tokens (d = 64): byte 16 L + 4 m + dg of tile T, L = 16 sl + c,
-    // holds dim 16 dg + c of tokens 64 T + 4 (4 m + sl) + t, 2 bits each (t = 0..3)
+    // value tiles of 64 tokens, a 1024-byte half per 64 dims (d = 64 or 128): byte
+    // 16 L + 4 m + dg of half h of tile T, L = 16 sl + c, holds dim 64 h + 16 dg + c of
+    // tokens 64 T + 4 (4 m + sl) + t, 2 bits each (t = 0..3)
+    const int tbytes = 1024 * (d / 64);
     const int64_t c0 = pos >> 6, c1 = (pos + n + 63) >> 6;
     const int64_t nt = c1 - c0;
-    const int64_t total = n_streams * nt * 1024;
+    const int64_t total = n_streams * nt * tbytes;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-      const int byte = (int)(e & 1023);
-      const int64_t r = e >> 10, s = r / nt, tile = c0 + (r - s * nt);
+      const int tb = (int)(e % tbytes), byte = tb & 1023;
+      const int64_t r = e / tbytes, s = r / nt, tile = c0 + (r - s * nt);
       const int L = byte >> 4, m = (byte >> 2) & 3, dg = byte & 3;
       const int sl = L >> 4, c = L & 15;
-      const int j = 16 * dg + c;
-      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * 1024 + byte;
+      const int j = 64 * (tb >> 10) + 16 * dg + c;
+      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * tbytes + tb;
       uint32_t v = *dst;
       for (int tt = 0; tt < 4; ++tt) {
         const int64_t t = tile * 64 + 4 * (4 * m + sl) + tt - pos;
@@ -1373,15 +1474,16 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
       *dst = (uint8_t)v;
     }
   } else {
-    // 3- and 4-bit value tiles of 512 * bits bytes: each byte's bits gathered one by one
-    const int tb = 512 * bits, nb = 8 * bits - 16;
+    // 3- and 4-bit value tiles of 512 * bits bytes per 64-dim half: each byte's bits
+    // gathered one by one
+    const int tb = 512 * bits, nb = 8 * bits - 16, tbytes = tb * (d / 64);
     const int64_t c0 = pos >> 6, c1 = (pos + n + 63) >> 6;
     const int64_t nt = c1 - c0;
-    const int64_t total = n_streams * nt * tb;
+    const int64_t total = n_streams * nt * tbytes;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-      const int off = (int)(e % tb);
-      const int64_t r = e / tb, s = r / nt, tile = c0 + (r - s * nt);
+      const int toff = (int)(e % tbytes), half = toff / tb, off = toff - half * tb;
+      const int64_t r = e / tbytes, s = r / nt, tile = c0 + (r - s * nt);
       int L, w, k;
       if (off < 1024) {
         L = off >> 4; w = (off >> 2) & 3; k = off & 3;
@@ -1391,14 +1493,14 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
         const int rr = o - L * nb;
         w = 4 + (rr >> 2); k = rr & 3;
       }
-      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * tb + off;
+      uint8_t* dst = cache + (s * (t_cap >> 6) + tile) * tbytes + toff;
       uint32_t v = *dst;
       for (int b = 0; b < 8; ++b) {
         int tt, j, cbit;
         vt_bit_source(bits, L, w, k, b, tt, j, cbit);
         const int64_t t = tile * 64 + tt - pos;
         if (t < 0 || t >= n) continue;
-        v = (v & ~(1u << b)) | (((code(s, t, j) >> cbit) & 1u) << b);
+        v = (v & ~(1u << b)) | (((code(s, t, 64 * half + j) >> cbit) & 1u) << b);
       }
       *dst = (uint8_t)v;
     }
@@ -1426,15 +1528,18 @@ __global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_st
         const uint8_t pb = cache[(s * t_cap + t) * (d / 2) + (j >> 1)];
         c = (j & 1) ? (pb & 15u) : (pb >> 4);
       } else if (bits == 2) {
+        // tile of 64 tokens and d dims: 64-dim halves of 1024 bytes, dims 64 h + .. in half h
         const int blk = (int)((t >> 2) & 15);  // block within the 64-token tile = 4 m + sl
-        const int64_t at = (s * (t_cap >> 6) + (t >> 6)) * 1024 + ((blk & 3) * 16 + (j & 15)) * 16 +
-                           (blk >> 2) * 4 + (j >> 4);
+        const int jh = j & 63;
+        const int64_t at = (s * (t_cap >> 6) + (t >> 6)) * (1024 * (d / 64)) + (j >> 6) * 1024 +
+                           ((blk & 3) * 16 + (jh & 15)) * 16 + (blk >> 2) * 4 + (jh >> 4);
         c = (cache[at] >> (2 * (t & 3))) & 3u;
       } else {
         const int tt = (int)(t & 63), blk = tt >> 2, m = blk >> 2, sl = blk & 3;
         const int G = m >> 1, kb = 2 * (m & 1) + ((tt >> 1) & 1), eo = tt & 1;
-        const int L = 16 * sl + (j & 15), dg = j >> 4;
-        const uint8_t* tile = cache + (s * (t_cap >> 6) + (t >> 6)) * (512 * bits);
+        const int L = 16 * sl + (j & 15), dg = (j & 63) >> 4;
+        const uint8_t* tile = cache + (s * (t_cap >> 6) + (t >> 6)) * (512 * bits * (d / 64)) +
+                              (j >> 6) * (512 * bits);
         if (bits == 4) {
           c = (tile[vt_byte_off(4, L, 4 * G + dg, kb)] >> (4 * eo)) & 15u;
         } else if (dg < 3) {
@@ -1545,7 +1650,7 @@ int launch_fused_decode(const FusedDecodeCall& c, void* workspace, size_t worksp
     }
   }
   if (rc != TQ_OK) return rc;
-  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, a.part,
+  hipLaunchKernelGGL(fused_combine_kernel<kDim>, dim3((unsigned)rows), dim3(kDim), 0, st, a.part,
                      a.stats, p.nsplit, p.split_tokens, c.seq_lens, c.t_max, c.hq, c.vrot,
                      c.q_dt, c.out, c.lse);
   TQ_LAUNCH_CHECK("fused_combine_kernel");
@@ -1640,21 +1745,29 @@ SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
   return {split, (int)((t_cap + split - 1) / split)};
 }
 
-template <int PG, int VB, int ND = 0>
+template <int PG, int VB, int ND = 0, int NH = 1>
 void launch_dl_kernel(tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
   if (q_dtype == TQ_F32)
-    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else if (q_dtype == TQ_F16)
-    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB, ND>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
 }
 
-template <int ND>
+template <int ND, int NH>
 void launch_dl_contiguous(int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
-  if (vbits == 2) launch_dl_kernel<0, 2, ND>(q_dtype, grid, a, st);
-  else if (vbits == 3) launch_dl_kernel<0, 3, ND>(q_dtype, grid, a, st);
-  else launch_dl_kernel<0, 4, ND>(q_dtype, grid, a, st);
+  if (vbits == 2) launch_dl_kernel<0, 2, ND, NH>(q_dtype, grid, a, st);
+  else if (vbits == 3) launch_dl_kernel<0, 3, ND, NH>(q_dtype, grid, a, st);
+  else launch_dl_kernel<0, 4, ND, NH>(q_dtype, grid, a, st);
+}
+
+template <int NH>
+void launch_dl_norms(int norm_dt, int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a,
+                     hipStream_t st) {
+  if (norm_dt == TQ_BF16) launch_dl_contiguous<TQ_BF16, NH>(vbits, q_dtype, grid, a, st);
+  else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16, NH>(vbits, q_dtype, grid, a, st);
+  else launch_dl_contiguous<0, NH>(vbits, q_dtype, grid, a, st);
 }
 
 template <int PG>
@@ -1697,14 +1810,15 @@ __global__ __launch_bounds__(64) void merge_token_kernel(const void* o, const fl
 
 // The decode-layout kernel over every (stream, split), in launches of at most four query
 // heads per KV head, then (several splits) the log-sum-exp combine.  `a` carries
-// everything but the split plan, the head range and the outputs.
+// everything but the split plan, the head range and the outputs.  d: head_dim (64, or 128
+// for contiguous caches).
 int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg,
            const SplitPlan& p, void* workspace, void* out, float* lse, hipStream_t st,
-           int norm_dt = TQ_F32) {
+           int norm_dt = TQ_F32, int d = kDim) {
   const size_t rows = (size_t)B * hq;
   char* ws = static_cast<char*>(workspace) + 256;
   float* part = reinterpret_cast<float*>(ws);
-  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDim * 4, 256));
+  float2* stats = reinterpret_cast<float2*>(ws + align_up(rows * p.nsplit * kDlMaxDim * 4, 256));
   const bool single = p.nsplit == 1;
   if (a.t_cap > 0) {
     a.q_dt = (int)q_dtype; a.hq = hq; a.hkv = hkv;
@@ -1717,9 +1831,8 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
       a.hofs = h0;
       a.G = std::min(4, a.Gfull - h0);
       if (pg == 0) {
-        if (norm_dt == TQ_BF16) launch_dl_contiguous<TQ_BF16>(vbits, q_dtype, (unsigned)grid, a, st);
-        else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16>(vbits, q_dtype, (unsigned)grid, a, st);
-        else launch_dl_contiguous<0>(vbits, q_dtype, (unsigned)grid, a, st);
+        if (d == 128) launch_dl_norms<2>(norm_dt, vbits, q_dtype, (unsigned)grid, a, st);
+        else launch_dl_norms<1>(norm_dt, vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 1) {
         launch_dl_paged<1>(vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 3) {
@@ -1733,9 +1846,14 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
     }
     if (single) return TQ_OK;
   }
-  hipLaunchKernelGGL(fused_combine_kernel, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
-                     p.nsplit, p.split_tokens, a.seq_lens, a.t_cap, hq, a.vrot, (int)q_dtype, out,
-                     lse);
+  if (d == 128)
+    hipLaunchKernelGGL(fused_combine_kernel<128>, dim3((unsigned)rows), dim3(128), 0, st, part, stats,
+                       p.nsplit, p.split_tokens, a.seq_lens, a.t_cap, hq, a.vrot, (int)q_dtype, out,
+                       lse);
+  else
+    hipLaunchKernelGGL(fused_combine_kernel<kDim>, dim3((unsigned)rows), dim3(kDim), 0, st, part, stats,
+                       p.nsplit, p.split_tokens, a.seq_lens, a.t_cap, hq, a.vrot, (int)q_dtype, out,
+                       lse);
   TQ_LAUNCH_CHECK("fused_combine_kernel");
   return TQ_OK;
 }
@@ -1751,7 +1869,8 @@ size_t tq_decode_dl_workspace_bytes(int32_t B, int32_t hq, int32_t hkv, int64_t 
   if (B <= 0 || hq <= 0 || hkv <= 0 || t_cap <= 0) return 256;
   const SplitPlan p = plan_dl_splits(B, hkv, t_cap);
   const size_t rows = (size_t)B * hq;
-  return 256 + align_up(rows * p.nsplit * kDim * 4, 256) + align_up(rows * p.nsplit * 8, 256);
+  // partial outputs sized for head_dim up to 128
+  return 256 + align_up(rows * p.nsplit * kDlMaxDim * 4, 256) + align_up(rows * p.nsplit * 8, 256);
 }
 
 int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq,
@@ -1765,14 +1884,14 @@ int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, in
                                   float scale, void* out, float* lse, void* workspace,
                                   size_t workspace_bytes, void* stream) {
   TQ_REQUIRE(valid_dtype(q_dtype) && valid_dtype(norm_dtype), "unknown dtype");
-  if (d != kDim || kbits != 4 || vbits < 2 || vbits > 4)
-    return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 with 4-bit keys and 2-4 bit "
-                                 "values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
+  if ((d != 64 && d != 128) || kbits != 4 || vbits < 2 || vbits > 4)
+    return fail(TQ_EUNSUPPORTED, "decode layout covers head_dim 64 and 128 with 4-bit keys and "
+                                 "2-4 bit values, got d=%d kbits=%d vbits=%d", d, kbits, vbits);
   TQ_REQUIRE(B >= 0 && hkv >= 1 && hq >= hkv && hq % hkv == 0,
              "num_heads (%d) must be a multiple of num_kv_heads (%d)", hq, hkv);
   TQ_REQUIRE(t_cap >= 0 && t_cap % 64 == 0, "capacity must be a multiple of 64, got %lld",
              (long long)t_cap);
-  TQ_REQUIRE(t_cap * 32 < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
+  TQ_REQUIRE(t_cap * (d / 2) < (int64_t)INT_MAX, "capacity too large for 32-bit offsets");
   if (B == 0) return TQ_OK;
   TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
              "null pointer argument");
@@ -1791,7 +1910,7 @@ int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, in
   a.seq_starts = seq_starts; a.kcen = kcentroids; a.vcen = vcentroids; a.krot = krotation;
   a.vrot = vrotation; a.qscale = scale * 1.4426950408889634f;
   return run_dl(a, q_dtype, B, hq, hkv, vbits, 0, p, workspace, out, lse, as_stream(stream),
-                (int)norm_dtype);
+                (int)norm_dtype, d);
 }
 
 int tq_decode_attention_dl(const void* q, tq_dtype q_dtype, int32_t B, int32_t hq, int32_t hkv,
@@ -1904,11 +2023,12 @@ int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, i
   TQ_REQUIRE(values ? (bit_width >= 2 && bit_width <= 4) : bit_width == 4,
              "decode layout holds 4-bit keys and 2-4 bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && pos >= 0 && pos + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
-             "value tiles need dim 64 and a capacity that is a multiple of 64");
+  TQ_REQUIRE(!values || (t_cap % 64 == 0 && (d == 64 || d == 128)),
+             "value tiles need dim 64 or 128 and a capacity that is a multiple of 64");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
-  const int64_t per = values ? (((pos + n + 63) >> 6) - (pos >> 6)) * 512 * bit_width : n * (d / 2);
+  const int64_t per = values ? (((pos + n + 63) >> 6) - (pos >> 6)) * 512 * bit_width * (d / 64)
+                             : n * (d / 2);
   const int64_t total = n_streams * per;
   const int64_t blocks = std::min<int64_t>((total + 255) / 256, (int64_t)device_cu_count() * 16);
   hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
@@ -1925,8 +2045,8 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
   TQ_REQUIRE(values ? (bit_width >= 2 && bit_width <= 4) : bit_width == 4,
              "decode layout holds 4-bit keys and 2-4 bit values");
   TQ_REQUIRE(n_streams >= 0 && n >= 0 && t0 >= 0 && t0 + n <= t_cap, "bad token range");
-  TQ_REQUIRE(!values || (t_cap % 64 == 0 && d == 64),
-             "value tiles need dim 64 and a capacity that is a multiple of 64");
+  TQ_REQUIRE(!values || (t_cap % 64 == 0 && (d == 64 || d == 128)),
+             "value tiles need dim 64 or 128 and a capacity that is a multiple of 64");
   if (n_streams == 0 || n == 0) return TQ_OK;
   TQ_REQUIRE(packed && cache, "null pointer argument");
   const int64_t total = n_streams * n * bit_width * ((d + 7) / 8);

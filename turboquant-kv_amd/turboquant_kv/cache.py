@@ -11,8 +11,8 @@ attention_values_packed kernels); `decode_attention` runs the fused GQA decode
 kernel.  Query heads may be a multiple of the KV heads (head h reads KV head
 h // (Hq / H), as HF's repeat_kv does); the reference only handles equal counts.
 
-For 4-bit keys and 2-bit values at head_dim 64 (MSE mode) the codes are kept in the
-decode layout (same bytes per token, arranged for the decode kernel: key bytes hold two
+For 4-bit keys and 2-4 bit values at head_dim 64 or 128 (MSE mode) the codes are kept in
+the decode layout (same bytes per token, arranged for the decode kernel: key bytes hold two
 4-bit codes, value bytes hold one dim of four consecutive tokens); the reference keeps
 its packed storage private (cache.py:81-130), so only `_key_packed` / `_val_packed`,
 which return the bit-plane rows, see the difference.
@@ -81,8 +81,8 @@ class QuantizedKVCache:
         self._vbnd, self._vcen = vcb[0].to(dev), vcb[1].to(dev)
 
         bpp = (head_dim + 7) // 8
-        # 4-bit keys and 2-4 bit values of head_dim 64 are kept in the decode layout
-        self._dl = (not self._is_prod and kb == 4 and 2 <= vb <= 4 and head_dim == 64)
+        # 4-bit keys and 2-4 bit values of head_dim 64 or 128 are kept in the decode layout
+        self._dl = (not self._is_prod and kb == 4 and 2 <= vb <= 4 and head_dim in (64, 128))
         # decode-layout value tiles hold 64 tokens: capacity rounded up to a multiple of 64
         self._t_cap = (max_seq_len + 63) // 64 * 64 if self._dl else max_seq_len
         B, H, T = batch_size, num_heads, self._t_cap

@@ -4,10 +4,10 @@ Targets the layer-based Cache of transformers 5.x: each transformer layer gets a
 `TurboQuantLayer` holding packed device storage + fp32 norms [B, H_kv, capacity] that
 grows geometrically; every `update` quantizes all (batch, head, token) rows of the new
 states in one kernel launch (the reference loops over batch items and heads in Python,
-hf_integration.py:370-415).  MSE caches with 4-bit keys, 2-4 bit values and head_dim 64
-(the default K4/V2 and the K4/V3 of the end-to-end config) keep their codes in the decode
-layout -- key pair bytes [B, H_kv, capacity, 32], 64-token value tiles [B, H_kv,
-capacity/64, 512*value_bits] -- that the fused decode kernel streams; other shapes keep
+hf_integration.py:370-415).  MSE caches with 4-bit keys, 2-4 bit values and head_dim 64 or
+128 (the default K4/V2 and the K4/V3 of the end-to-end config) keep their codes in the
+decode layout -- key pair bytes [B, H_kv, capacity, d/2], 64-token value tiles [B, H_kv,
+capacity/64, 8*value_bits*d] -- that the fused decode kernel streams; other shapes keep
 the reference's bit-plane rows [B, H_kv, capacity, P].
 
 Semantics kept from the reference (hf_integration.py:319-421):
@@ -118,9 +118,9 @@ class TurboQuantLayer(_HFLayer):
             self.kq = _Quantizer(d, cfg.key_bits, cfg.seed, cfg, self.device)
             self.vq = _Quantizer(d, cfg.value_bits, cfg.seed + 1, cfg, self.device)
             self.keys = self.values = None
-            # decode layout: mse, 4-bit keys, 2-4 bit values, head_dim 64
+            # decode layout: mse, 4-bit keys, 2-4 bit values, head_dim 64 or 128
             self.dl = (not self.kq.prod and self.kq.code_bits == 4 and
-                       2 <= self.vq.code_bits <= 4 and d == 64)
+                       2 <= self.vq.code_bits <= 4 and d in (64, 128))
             # norms in the model's dtype for 16-bit models, as the reference's cache keeps
             # them (quantize returns them in the input dtype; hf_integration.py:512-525
             # counts them so); the decode-layout kernel reads 16-bit norms directly.  Other

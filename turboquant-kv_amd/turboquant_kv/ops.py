@@ -167,7 +167,7 @@ def unpack_decode_layout(cache: torch.Tensor, dim: int, bit_width: int, values: 
 def decode_attention_dl(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids, vcentroids,
                         krotation, vrotation, scale, return_lse: bool = False):
     """decode_attention_packed over a decode-layout cache (4-bit keys, 2-4 bit values --
-    the width of the value tiles names it --, head_dim 64, any number of query heads per
+    the width of the value tiles names it --, head_dim 64 or 128, any number of query heads per
     KV head): [B, Hq, d] in q.dtype (and the [B, Hq] log-sum-exp with return_lse)."""
     _require_device(q, "q")
     if return_lse:
