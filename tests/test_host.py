@@ -66,7 +66,7 @@ def test_capi_exports_every_declared_symbol():
     for s in syms:
         assert hasattr(lib, s), s
     lib.tq_abi_version.restype = ctypes.c_int
-    assert lib.tq_abi_version() == 3
+    assert lib.tq_abi_version() == 4
 
 
 @pytest.mark.skipif(not _built(), reason="native library not built")

@@ -852,7 +852,7 @@ extern "C" {
 
 const char* tq_last_error(void) { return tq::last_error().c_str(); }
 
-int tq_abi_version(void) { return 3; }
+int tq_abi_version(void) { return 4; }
 
 int tq_rotate_and_quantize(const void* vectors, tq_dtype in_dtype, tq_dtype round_dtype, int64_t n,
                            int32_t d, const float* rotation, const float* boundaries,
