@@ -639,7 +639,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   __shared__ float qs_s[4][D];
   __shared__ float hmax_s[NH == 2 ? kDlWaves : 1];  // head_dim 128: per-wave |q_rot| maxima
   __shared__ float cen_s[32];  // 16 key centroids, then the value centroids
-  __shared__ float sc_s[2];  // value and key centroid scales
+  __shared__ __attribute__((aligned(16))) float rv_s[NH == 1 ? kDim * kDim : 1];  // R_v (one split)
   __shared__ float qs2_s[4];  // per-head query scales
   __shared__ float red_m[kDlWaves][4];
   __shared__ float red_l[kDlWaves][4];
@@ -853,14 +853,16 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 
   // ---- prologue.  Every global read is issued up front, in the order its data is needed
   // (loads complete in issue order, so waiting for one never waits for a later one): the
-  // centroids and the query, this thread's row of R_k, then the first two tiles, whose
-  // latency runs under the rotation and the table fill.  (R_v stays in global memory for
-  // the epilogue: staged in LDS it took the workgroup to 151 KB, measured 5 % slower.)
+  // centroids, the query, R_k and (one split per stream) R_v, the matrices read coalesced.
+  // A barrier then holds the first tiles' loads back until every wave has issued those: a
+  // wave's tile loads queued ahead of another wave's query load would delay it.  Then:
+  // centroids, query and R_k into LDS | staged table entries and the rotated query |
+  // the tables' copies and R_v into LDS.
   float cenv = 0.f;
   if (tid < 16) cenv = a.kcen[tid];
   else if (tid < 16 + (1 << VB)) cenv = a.vcen[tid - 16];
   // the query element as the aligned 32-bit word that holds it (one load whatever the
-  // dtype, converted after the barrier: a dtype branch here made the compiler wait for it
+  // dtype, converted after the tables: a dtype branch here made the compiler wait for it
   // before issuing the loads below)
   // thread tid < 4 D: head qh = tid / D, dim qj = tid % D
   const int qh = tid / D, qj = tid % D;
@@ -869,15 +871,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   uint32_t qraw = 0;
   if (tid < 4 * D)
     qraw = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(a.q) + (qbyte & ~int64_t(3)));
-  // row qj of R_k (head_dim 64: waves 0-3, held from here; 128: read in the product below)
-  float4 rrow[NH == 1 ? kDim / 4 : 1];
+  // Head_dim 64: R_k and (one split per stream, for the epilogue) R_v, read coalesced:
+  // thread tid holds floats 8 tid .. 8 tid + 7 of each (row tid / 8, float4 columns
+  // 2 (tid % 8) and 2 (tid % 8) + 1).  R_k goes through rv_s for the rotation, R_v after it.
+  // (Head_dim 128: R_k is read in the product below, R_v in the epilogue.)
+  v4f rk0 = (v4f){0.f, 0.f, 0.f, 0.f}, rk1 = rk0, rv0 = rk0, rv1 = rk0;
   if constexpr (NH == 1) {
-    if (tid < 4 * kDim) {
-      const float4* r4 = reinterpret_cast<const float4*>(a.krot + (tid & 63) * kDim);
-#pragma unroll
-      for (int k = 0; k < kDim / 4; ++k) rrow[k] = r4[k];
-    }
+    const v4f* k4 = reinterpret_cast<const v4f*>(a.krot) + 2 * tid;
+    const v4f* r4 = reinterpret_cast<const v4f*>(a.vrot) + 2 * tid;
+    rk0 = k4[0];
+    rk1 = k4[1];
+    rv0 = r4[0];
+    rv1 = r4[1];
   }
+  __builtin_amdgcn_s_barrier();
   Blk bnx{};  // paged: block id(s) of the next tile to load
   load_tile(tf, ta, load_block(tf));
   load_tile(tf + kStep, tb, load_block(tf + kStep));
@@ -904,73 +911,25 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
                                          : __half2float(__ushort_as_half((unsigned short)bits));
     qs_s[qh][qj] = qh < a.G ? qv : 0.f;
   }
-  __syncthreads();
-  if constexpr (NH == 2) {  // head_dim 128: every wave rotates (head wave / 2, dims 64 (wave % 2) ..)
-    const int h = qh, j = qj;
-    const float4* r4 = reinterpret_cast<const float4*>(a.krot + j * D);
-    float v = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < D / 4; ++k) {
-      const float4 r = r4[k];
-      v = fmaf(r.x, qs_s[h][4 * k], v);
-      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
-      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
-      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
-    }
-    v *= a.qscale;
-    const float wm = wave_max(fabsf(v));
-    if (lane == 0) hmax_s[wave] = wm;
-    if (tid < 32) {  // the centroid scales (the key and value centroids are in cen_s)
-      const float c = fabsf(cen_s[tid & 15]);
-      const float vcv = (tid & 15) < (1 << VB) ? fabsf(cen_s[16 + (tid & 15)]) : 0.f;
-      float km = c, vm = vcv;
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) {
-        km = fmaxf(km, __shfl_xor(km, o));
-        vm = fmaxf(vm, __shfl_xor(vm, o));
-      }
-      if (tid == 0) { sc_s[0] = pow2_scale(vm); sc_s[1] = pow2_scale(km); }
-    }
-    __syncthreads();
-    // fp16 hi + lo parts, the head's largest element scaled into [0.5, 1) (both halves)
-    const float s2 = pow2_scale(fmaxf(hmax_s[2 * h], hmax_s[2 * h + 1]));
-    const float x = v * s2;
-    const _Float16 xh = (_Float16)x;
-    qhl_s[h][0][j] = xh;
-    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
-    if (j == 0) qs2_s[h] = s2;
-  } else if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane
-    const int h = tid >> 6, j = tid & 63;
-    float v = 0.f;
-#pragma unroll
-    for (int k = 0; k < kDim / 4; ++k) {
-      const float4 r = rrow[k];
-      v = fmaf(r.x, qs_s[h][4 * k], v);
-      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
-      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
-      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
-    }
-    v *= a.qscale;
-    // fp16 hi + lo parts of the rotated query, scaled by a power of two that brings the
-    // head's largest element into [0.5, 1) (lo parts stay normal numbers)
-    const float s2 = pow2_scale(wave_max(fabsf(v)));
-    const float x = v * s2;
-    const _Float16 xh = (_Float16)x;
-    qhl_s[h][0][j] = xh;
-    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
-    if (j == 0) qs2_s[h] = s2;
-  } else if (tid < 4 * kDim + 64) {  // wave 4: value centroid scale
-    const int l = tid & 63;
-    const float vm = wave_max(l < (1 << VB) ? fabsf(cen_s[16 + l]) : 0.f);
-    if (l == 0) sc_s[0] = pow2_scale(vm);
-  } else if (tid < 4 * kDim + 128) {  // wave 5: key centroid scale
-    const int l = tid & 63;
-    const float km = wave_max(l < 16 ? fabsf(cen_s[l]) : 0.f);
-    if (l == 0) sc_s[1] = pow2_scale(km);
+  if constexpr (NH == 1) {
+    // R_k row r, float4 column c at slot 16 r + ((c + r) & 15): the rotation's lane r then
+    // reads its row with 16 lanes' 16-byte reads on distinct banks
+    const int r = tid >> 3, c = 2 * (tid & 7);
+    v4f* rk = reinterpret_cast<v4f*>(rv_s);
+    rk[16 * r + ((c + r) & 15)] = rk0;
+    rk[16 * r + ((c + 1 + r) & 15)] = rk1;
   }
   __syncthreads();
-  const float vsc = sc_s[0];
-  const float ksc = sc_s[1];
+  // centroid scales: the powers of two that bring each codebook's largest |c| into
+  // [0.5, 1) (the same in every lane)
+  float km = fabsf(cen_s[lane & 15]);
+  float vm = (lane & 15) < (1 << VB) ? fabsf(cen_s[16 + (lane & 15)]) : 0.f;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) {
+    km = fmaxf(km, __shfl_xor(km, o));
+    vm = fmaxf(vm, __shfl_xor(vm, o));
+  }
+  const float ksc = pow2_scale(km), vsc = pow2_scale(vm);
   // Tables: each entry's fp16 words are converted once (a thread per K entry, a thread
   // per V entry) into a small staging table, then stored as 16-byte runs of identical
   // copies, consecutive lanes writing consecutive runs (conflict-free LDS writes).
@@ -1003,6 +962,52 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       vst_s[i] = (u32x4){pack_h2(h0, h1), pack_h2((_Float16)(x0 - (float)h0), (_Float16)(x1 - (float)h1)), 0u, 0u};
     }
   }
+  // the rotated query (the staged entries above are in flight to LDS meanwhile)
+  if constexpr (NH == 2) {  // head_dim 128: every wave rotates (head wave / 2, dims 64 (wave % 2) ..)
+    const int h = qh, j = qj;
+    const float4* r4 = reinterpret_cast<const float4*>(a.krot + j * D);
+    float v = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < D / 4; ++k) {
+      const float4 r = r4[k];
+      v = fmaf(r.x, qs_s[h][4 * k], v);
+      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
+      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
+      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
+    }
+    v *= a.qscale;
+    const float wm = wave_max(fabsf(v));
+    if (lane == 0) hmax_s[wave] = wm;
+    __syncthreads();
+    // fp16 hi + lo parts, the head's largest element scaled into [0.5, 1) (both halves)
+    const float s2 = pow2_scale(fmaxf(hmax_s[2 * h], hmax_s[2 * h + 1]));
+    const float x = v * s2;
+    const _Float16 xh = (_Float16)x;
+    qhl_s[h][0][j] = xh;
+    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
+    if (j == 0) qs2_s[h] = s2;
+  } else if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane (row j of R_k)
+    const int h = tid >> 6, j = tid & 63;
+    const v4f* rk = reinterpret_cast<const v4f*>(rv_s);
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kDim / 4; ++k) {
+      const v4f r = rk[16 * j + ((k + j) & 15)];
+      v = fmaf(r.x, qs_s[h][4 * k], v);
+      v = fmaf(r.y, qs_s[h][4 * k + 1], v);
+      v = fmaf(r.z, qs_s[h][4 * k + 2], v);
+      v = fmaf(r.w, qs_s[h][4 * k + 3], v);
+    }
+    v *= a.qscale;
+    // fp16 hi + lo parts of the rotated query, scaled by a power of two that brings the
+    // head's largest element into [0.5, 1) (lo parts stay normal numbers)
+    const float s2 = pow2_scale(wave_max(fabsf(v)));
+    const float x = v * s2;
+    const _Float16 xh = (_Float16)x;
+    qhl_s[h][0][j] = xh;
+    qhl_s[h][1][j] = (_Float16)(x - (float)xh);
+    if (j == 0) qs2_s[h] = s2;
+  }
   __syncthreads();
   for (int e = tid; e < 256 * 8; e += kDlThreads) {
     const int i = e >> 3, q = e & 7;
@@ -1024,6 +1029,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       if constexpr (EXACT_V)
         *reinterpret_cast<u32x4*>(vtab + i * kDlEntry + 128 + q * 16) = (u32x4){w.y, w.y, w.y, w.y};
     }
+  }
+  if constexpr (NH == 1) {  // R_k has been read: rv_s takes R_v
+    reinterpret_cast<v4f*>(rv_s)[2 * tid] = rv0;
+    reinterpret_cast<v4f*>(rv_s)[2 * tid + 1] = rv1;
   }
   __syncthreads();
 
@@ -1298,31 +1307,43 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // does not cover the HBM latency under full load (more lookahead measured slower: the
   // extra tiles in flight delay the prologue's own reads).  Loads past te read data that
   // is masked (or zeros past the buffers); the tile count is made wave-uniform explicitly.
-  for (int it = 0; it < ntiles; it += 3) {
-    const int t = tf + it * kStep;
-    const Blk b1 = load_block(t + 3 * kStep);
-    load_tile(t + 2 * kStep, tc, bnx);
-    process(ta, t);
-    if (it + 1 >= ntiles) break;
-    const Blk b2 = load_block(t + 4 * kStep);
-    load_tile(t + 3 * kStep, ta, b1);
-    process(tb, t + kStep);
-    if (it + 2 >= ntiles) break;
-    bnx = load_block(t + 5 * kStep);
-    load_tile(t + 4 * kStep, tb, b2);
-    process(tc, t + 2 * kStep);
-  }
-
-  // The whole-sequence path's R_v column (threads of waves 0-3: dim = lane), requested
-  // now so that its latency runs under the reduction below (head_dim 128: read in the
-  // product at the end).
-  float rv[NH == 1 ? kDim : 1];
+  // Head_dim 64: whole groups of three tiles, then the last one or two (in ta, tb).  The
+  // loop has no exit inside a group: an exit there joins the back edge, and every
+  // iteration then starts by waiting for all loads in flight, the lookahead tile's
+  // included.  (Head_dim 128 keeps the exits: two more copies of its tile code spill.)
   if constexpr (NH == 1) {
-    if ((a.out != nullptr) & (tid < 4 * kDim)) {
-#pragma unroll
-      for (int k = 0; k < kDim; ++k) rv[k] = a.vrot[k * kDim + (tid & 63)];
+    int it = 0;
+    for (; it + 3 <= ntiles; it += 3) {
+      const int t = tf + it * kStep;
+      const Blk b1 = load_block(t + 3 * kStep);
+      load_tile(t + 2 * kStep, tc, bnx);
+      process(ta, t);
+      const Blk b2 = load_block(t + 4 * kStep);
+      load_tile(t + 3 * kStep, ta, b1);
+      process(tb, t + kStep);
+      bnx = load_block(t + 5 * kStep);
+      load_tile(t + 4 * kStep, tb, b2);
+      process(tc, t + 2 * kStep);
+    }
+    if (it < ntiles) process(ta, tf + it * kStep);
+    if (it + 1 < ntiles) process(tb, tf + (it + 1) * kStep);
+  } else {
+    for (int it = 0; it < ntiles; it += 3) {
+      const int t = tf + it * kStep;
+      const Blk b1 = load_block(t + 3 * kStep);
+      load_tile(t + 2 * kStep, tc, bnx);
+      process(ta, t);
+      if (it + 1 >= ntiles) break;
+      const Blk b2 = load_block(t + 4 * kStep);
+      load_tile(t + 3 * kStep, ta, b1);
+      process(tb, t + kStep);
+      if (it + 2 >= ntiles) break;
+      bnx = load_block(t + 5 * kStep);
+      load_tile(t + 4 * kStep, tb, b2);
+      process(tc, t + 2 * kStep);
     }
   }
+
   // ---- reduction: l over the lanes of a head; outputs over the waves (LDS)
   l += __shfl_xor(l, 4);
   l += __shfl_xor(l, 8);
@@ -1379,7 +1400,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         float r = 0.f;
         if constexpr (NH == 1) {
 #pragma unroll
-          for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv[k], r);
+          for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv_s[k * kDim + dim], r);
         } else {
 #pragma unroll 8
           for (int k = 0; k < D; ++k) r = fmaf(qs_s[m][k], a.vrot[k * D + dim], r);
@@ -1896,7 +1917,8 @@ int tq_decode_attention_dl_window(const void* q, tq_dtype q_dtype, int32_t B, in
   TQ_REQUIRE(q && out && seq_lens && kcentroids && vcentroids && krotation && vrotation,
              "null pointer argument");
   TQ_REQUIRE(t_cap == 0 || (kpairs && knorms && vblocks && vnorms), "null pointer argument");
-  TQ_REQUIRE((reinterpret_cast<uintptr_t>(krotation) & 15u) == 0, "rotation must be 16-byte aligned");
+  TQ_REQUIRE(((reinterpret_cast<uintptr_t>(krotation) | reinterpret_cast<uintptr_t>(vrotation)) & 15u) == 0,
+             "rotations must be 16-byte aligned");
   TQ_REQUIRE(t_cap == 0 || ((reinterpret_cast<uintptr_t>(kpairs) | reinterpret_cast<uintptr_t>(vblocks) |
                              reinterpret_cast<uintptr_t>(knorms) | reinterpret_cast<uintptr_t>(vnorms)) &
                             15u) == 0,
@@ -1978,7 +2000,8 @@ int tq_decode_attention_paged_dl(const void* q, tq_dtype q_dtype, int32_t B, int
              "null pointer argument");
   TQ_REQUIRE(t_cap == 0 || (kpairs_pool && knorm_pool && vtile_pool && vnorm_pool && block_tables),
              "null pointer argument");
-  TQ_REQUIRE((reinterpret_cast<uintptr_t>(krotation) & 15u) == 0, "rotation must be 16-byte aligned");
+  TQ_REQUIRE(((reinterpret_cast<uintptr_t>(krotation) | reinterpret_cast<uintptr_t>(vrotation)) & 15u) == 0,
+             "rotations must be 16-byte aligned");
   TQ_REQUIRE(t_cap == 0 || ((reinterpret_cast<uintptr_t>(kpairs_pool) | reinterpret_cast<uintptr_t>(vtile_pool) |
                              reinterpret_cast<uintptr_t>(knorm_pool) | reinterpret_cast<uintptr_t>(vnorm_pool)) &
                             15u) == 0,
