@@ -167,26 +167,38 @@ def bench_scan(args, extra):
             log(f"scan b=4 Q={Q} k=100: {t:.3f} ms/batch, {Q / t * 1e3:.0f} q/s")
     # bit-plane rows (the CPU reference's input) and the pair rows the headline op reads
     res["db4"] = (packed, norms, R, cen, pairs)
-    if not args.quick and not getattr(args, "batch_only", False):
+    if not args.quick:
         for bits in (3, 2):
-            # TurboQuantIndex keeps 2/3-bit d=128 rows as pair rows (same bytes per row):
-            # one table read of two precomputed products per pair of dims
+            # TurboQuantIndex keeps 2/3-bit d=128 rows as pair rows (same bytes per row)
             p3, n3, R3, c3, _ = make_db(N, d, bits)
             rows = ops.pack_pair_rows(p3, bits, d)
-            t_bp = time_op(lambda: ops.ip_scan_topk(q1, p3, n3, c3, R3, bits, k), 20, 3)
-            t = time_op(lambda: ops.ip_scan_topk_pair_rows(q1, rows, n3, c3, R3, bits, k), 30, 3)
             ba = N * (bits * 16 + 4)
-            extra[f"scan_b{bits}_Q1"] = {"us_per_query": t * 1e3, "queries_per_s": 1e3 / t,
-                                         "GBps": ba / t / 1e6, "hbm_frac": ba / t / 1e6 / HBM_PEAK_GBS,
-                                         "layout": "pair rows (TurboQuantIndex storage)",
-                                         "bitplane_rows_us": t_bp * 1e3}
-            log(f"scan b={bits} Q=1: {t * 1e3:.1f} us, {ba / t / 1e6:.0f} GB/s "
-                f"(bit-plane rows {t_bp * 1e3:.1f} us)")
-            if bits == 3:
-                qq = queries(64, d, seed=2)
-                t64 = time_op(lambda: ops.ip_scan_topk_pair_rows(qq, rows, n3, c3, R3, bits, k), 3, 1)
-                extra["scan_b3_Q64"] = {"ms_per_batch": t64, "queries_per_s": 64 / t64 * 1e3,
-                                        "layout": "pair rows"}
+            if not getattr(args, "batch_only", False):
+                # one query: the pair-row scan (one table read of two precomputed products
+                # per pair of dims)
+                t_bp = time_op(lambda: ops.ip_scan_topk(q1, p3, n3, c3, R3, bits, k), 20, 3)
+                t = time_op(lambda: ops.ip_scan_topk_pair_rows(q1, rows, n3, c3, R3, bits, k), 30, 3)
+                extra[f"scan_b{bits}_Q1"] = {"us_per_query": t * 1e3, "queries_per_s": 1e3 / t,
+                                             "GBps": ba / t / 1e6, "hbm_frac": ba / t / 1e6 / HBM_PEAK_GBS,
+                                             "layout": "pair rows (TurboQuantIndex storage)",
+                                             "bitplane_rows_us": t_bp * 1e3}
+                log(f"scan b={bits} Q=1: {t * 1e3:.1f} us, {ba / t / 1e6:.0f} GB/s "
+                    f"(bit-plane rows {t_bp * 1e3:.1f} us)")
+            for Q, steps in ((64, 20), (1024, 5)):
+                # batches: the multi-query filtered scan over the pair rows (fp16 centroid
+                # pairs from a 2^(2 bits)-entry table as the B operands)
+                qq = queries(Q, d, seed=2)
+                t = time_op(lambda: ops.ip_scan_topk_pair_rows(qq, rows, n3, c3, R3, bits, k), steps, 2,
+                            settle_s=0.1)
+                tiles = (Q + 63) // 64
+                flop = tiles * 64 * N * d * 2.0
+                extra[f"scan_b{bits}_Q{Q}"] = {
+                    "ms_per_batch": t, "queries_per_s": Q / t * 1e3, "row_passes": tiles,
+                    "GBps_rows_read": tiles * ba / t / 1e6, "filter_TFLOPs": flop / t / 1e9,
+                    "fp16_dense_peak_frac": flop / t / 1e9 / 2500.0, "layout": "pair rows",
+                    "kernels": "mq_rotate + mq_tile + mq_sample + mq_filter + mq_merge"}
+                log(f"scan b={bits} Q={Q}: {t:.3f} ms/batch, {Q / t * 1e3:.0f} q/s, filter "
+                    f"{flop / t / 1e9:.0f} TFLOP/s")
             del p3, n3, rows
     return res
 

@@ -211,8 +211,15 @@ int tq_attention_scores_prod_pair_rows(const void* query, tq_dtype q_dtype, int6
  * tq_attention_scores_pair_rows are tq_ip_scan_topk / tq_attention_scores_packed over
  * them, with identical scores and ids (2 and 3 bits: every pair's two products come from
  * one per-query table, so no multiply per row; 4 bits: the pair-layout kernels).
- * Workspace as tq_ip_scan_topk's; 2- and 3-bit calls take at most 65535 queries.
+ * Workspace as tq_ip_scan_topk's (2- and 3-bit calls then take at most 65535 queries), or
+ * tq_scan_pair_rows_workspace_bytes(nq, d, bits, N, k): with two or more queries the top-k
+ * then runs the multi-query filtered scan, as over the pair layout (fp16 centroid pairs
+ * from a 2^(2 bits)-entry table as the matrix cores' B operands, candidates rescored with
+ * the reference's arithmetic: the exact scan's ids and scores).  No counterpart in the
+ * reference for the size function (its search allocates nothing on a device).
  */
+size_t tq_scan_pair_rows_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N,
+                                         int32_t k);
 int tq_pack_pair_rows(const uint8_t* packed, int64_t n, int32_t d, int32_t bit_width, uint8_t* rows,
                       void* stream);
 int tq_unpack_pair_rows(const uint8_t* rows, int64_t n, int32_t d, int32_t bit_width, uint8_t* packed,

@@ -31,6 +31,9 @@ def lib():
         _lib.tq_scan_pairs_workspace_bytes.restype = ctypes.c_size_t
         _lib.tq_scan_pairs_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int64,
                                                        ctypes.c_int32]
+        _lib.tq_scan_pair_rows_workspace_bytes.restype = ctypes.c_size_t
+        _lib.tq_scan_pair_rows_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                                           ctypes.c_int64, ctypes.c_int32]
         _lib.tq_decode_workspace_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                                    ctypes.c_int64]
         _lib.tq_decode_paged_workspace_bytes.restype = ctypes.c_size_t

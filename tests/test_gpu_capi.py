@@ -488,14 +488,19 @@ def test_pair_rows_pack_roundtrip(bits, d):
         assert not np.array_equal(rows.cpu().numpy(), pair_rows_np(bad, bits))
 
 
-def k_scan_pair_rows(q, rows, norms, cen, R, bits, k, q_dt=capi.TQ_F32):
+def k_scan_pair_rows(q, rows, norms, cen, R, bits, k, q_dt=capi.TQ_F32, exact=False):
+    """tq_ip_scan_topk_pair_rows; with two or more queries the full workspace runs the
+    multi-query filtered scan, exact=True the exact scans (smaller workspace)."""
     Q, d = q.shape
     N = rows.shape[0]
     os_ = torch.empty(Q, k, dtype=torch.float32, device=DEV)
     oi = torch.empty(Q, k, dtype=torch.int64, device=DEV)
-    ws = torch.empty(max(L().tq_scan_workspace_bytes(Q, d, bits, N, k), 1), dtype=torch.uint8, device=DEV)
+    wsb = (L().tq_scan_workspace_bytes(Q, d, bits, N, k) if exact
+           else L().tq_scan_pair_rows_workspace_bytes(Q, d, bits, N, k))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    nt = norms if torch.is_tensor(norms) else T(norms)
     capi.check(L().tq_ip_scan_topk_pair_rows(capi.p(T(q)), q_dt, capi.i64(Q), capi.i32(d), capi.p(rows),
-                                             capi.p(T(norms)), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
+                                             capi.p(nt), capi.i64(N), capi.p(T(cen)), capi.p(T(R)),
                                              capi.i32(bits), capi.i32(k), capi.p(os_), capi.p(oi),
                                              capi.p(ws), ctypes.c_size_t(ws.numel()), capi.stream()))
     sync()
@@ -512,10 +517,11 @@ def test_pair_rows_scan_bit_exact(bits, d):
     rows = k_pair_rows(p, d, bits)
     for Q, k in ((1, 10), (4, 1), (9, 32)):
         q = rs.randn(Q, d).astype(np.float32)
-        s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k)
         so, io = O.search_topk(q, p, nm, cen, R, bits, k)
-        assert np.array_equal(i, io), (Q, k)
-        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+        for exact in (False, True):  # the multi-query filter (Q > 1) and the exact scan
+            s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k, exact=exact)
+            assert np.array_equal(i, io), (Q, k, exact)
+            assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), (Q, k, exact)
     q = rs.randn(3, d).astype(np.float32)
     out = torch.empty(3, 1500, dtype=torch.float32, device=DEV)
     ws = torch.empty(max(L().tq_scan_workspace_bytes(3, d, bits, 1500, 0), 1), dtype=torch.uint8, device=DEV)
@@ -992,6 +998,118 @@ def test_mq_scan_past_4gib_equals_exact_path():
         assert np.array_equal(s[r].view(np.uint32), want.view(np.uint32))
     del pairs, norms
     torch.cuda.empty_cache()
+
+
+def _cpu_search_bits(q, p, nm, cen, R, bits, k):
+    import cpu_libs
+    return cpu_libs.search_packed(q, p, nm, R, cen, bits, k, "port")
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+@pytest.mark.parametrize("d", [64, 128])
+def test_mq_pair_rows_vs_oracle_and_exact_path(bits, d):
+    # 2- and 3-bit pair rows: batches of 2, 64 and 130 queries over ~100k unit rows (ragged
+    # N), fp32 and fp16 queries, k = 1, 10, 32 and 100: the multi-query filtered scan's ids
+    # and scores bit-identical to the oracle (C restatement of the reference core) and to
+    # the exact pair-row scan.
+    rs = np.random.RandomState(300 + 10 * bits + d)
+    N = 100_003 if d == 128 else 60_001
+    R, cen, p, nm = _db(rs, N, d, bits)
+    nm = nm / np.float32(np.sqrt(d))
+    rows = k_pair_rows(p, d, bits)
+    for Q in (2, 64, 130):
+        q = rs.randn(Q, d).astype(np.float32)
+        q /= np.linalg.norm(q, axis=1, keepdims=True)
+        s100, i100 = _cpu_search_bits(q, p, nm, cen, R, bits, 100)
+        if Q == 2:
+            so, io = O.search_topk(q, p, nm, cen, R, bits, 100)
+            assert np.array_equal(io, i100) and np.array_equal(so.view(np.uint32), s100.view(np.uint32))
+        for k in (1, 10, 32, 100):
+            s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k)
+            assert np.array_equal(i, i100[:, :k]), (Q, k)
+            assert np.array_equal(s.view(np.uint32), s100[:, :k].view(np.uint32)), (Q, k)
+            if k == 10:
+                se, ie = k_scan_pair_rows(q, rows, nm, cen, R, bits, k, exact=True)
+                assert np.array_equal(ie, i) and np.array_equal(se.view(np.uint32), s.view(np.uint32))
+        q16 = q.astype(np.float16)
+        s, i = k_scan_pair_rows(q16, rows, nm, cen, R, bits, 10, q_dt=capi.TQ_F16)
+        so, io = _cpu_search_bits(q16.astype(np.float32), p, nm, cen, R, bits, 10)
+        assert np.array_equal(i, io) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_mq_pair_rows_q1024_with_ties(bits):
+    # configs[1]'s 1024-query batch at 3 and 2 bits: normalized fp16 queries over 100,003
+    # rows in which 40 rows appear 25 times each (queries 0-39 point at them), k = 10 and
+    # 32: bit-identical to the reference core's search.
+    rs = np.random.RandomState(1024 + bits)
+    d, N = 128, 100_003
+    R, cen, p, nm = _db(rs, N, d, bits)
+    nm = nm / np.float32(np.sqrt(d))
+    src = rs.choice(N, 40, replace=False)
+    for r in src:
+        dst = rs.choice(N, 24, replace=False)
+        p[dst] = p[r]
+        nm[dst] = nm[r]
+    rows = k_pair_rows(p, d, bits)
+    q = rs.randn(1024, d).astype(np.float32)
+    q = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float16)
+    q[:40] = (O.dequantize_mse(p[src], np.ones(40, np.float32), bits, d, R, cen)).astype(np.float16)
+    s32, i32 = _cpu_search_bits(q.astype(np.float32), p, nm, cen, R, bits, 32)
+    for k in (10, 32):
+        s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k, q_dt=capi.TQ_F16)
+        assert np.array_equal(i, i32[:, :k]), k
+        assert np.array_equal(s.view(np.uint32), s32[:, :k].view(np.uint32)), k
+
+
+@pytest.mark.parametrize("bits,d", [(2, 128), (3, 64)])
+def test_mq_pair_rows_fallback_special_norms_and_ulp_ties(bits, d):
+    # Query 0's best row copied over 3000 rows (its lists overflow: the exact pair-row scan
+    # answers it, flagged alone), 600 more copies of query 1's best row with norms a few
+    # ulps apart, and zero, negative, huge, tiny and infinite norms: all bit-exact.
+    rs = np.random.RandomState(88 + bits)
+    N = 80_000
+    R, cen, p, nm = _db(rs, N, d, bits)
+    nm = nm.copy()
+    q = rs.randn(5, d).astype(np.float32)
+    sc = O.lut_scores_f32(q[:2], p, nm, cen, R, bits)
+    top0, top1 = int(np.argmax(sc[0])), int(np.argmax(sc[1]))
+    perm = rs.permutation(np.setdiff1d(np.arange(N), [top0, top1]))
+    a, b = perm[:3000], perm[3000:3600]
+    p[a] = p[top0]
+    nm[a] = nm[top0]
+    p[b] = p[top1]
+    nm[b] = (nm[top1].view(np.int32) + rs.randint(-3, 4, size=600).astype(np.int32)).view(np.float32)
+    sp = perm[3600:]
+    nm[sp[:2000]] = 0.0
+    nm[sp[2000:4000]] *= -1.0
+    nm[sp[4000:4010]] = 1e30
+    nm[sp[4010:4020]] = -1e30
+    nm[sp[4020:4030]] = 1e-38
+    nm[sp[4030:4036]] = np.inf
+    nm[sp[4036:4040]] = -np.inf
+    rows = k_pair_rows(p, d, bits)
+    want = O.lut_scores_f32(q, p, nm, cen, R, bits)
+    for k in (4, 32):
+        s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, k)
+        so, io = _topk_no_nan(want, k)
+        assert np.array_equal(i, io), k
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32)), k
+
+
+@pytest.mark.parametrize("qscale", [0.0, 1e-36, 1e20])
+def test_mq_pair_rows_extreme_query_in_tile(qscale):
+    # a zero or out-of-range query turns the tile's filter off: the exact scan answers all
+    rs = np.random.RandomState(41)
+    d, bits, N = 128, 3, 30_000
+    R, cen, p, nm = _db(rs, N, d, bits)
+    rows = k_pair_rows(p, d, bits)
+    q = rs.randn(4, d).astype(np.float32)
+    q[1] *= np.float32(qscale)
+    want = O.lut_scores_f32(q, p, nm, cen, R, bits)
+    s, i = k_scan_pair_rows(q, rows, nm, cen, R, bits, 10)
+    so, io = _topk_no_nan(want, 10)
+    assert np.array_equal(i, io) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
 
 
 # ------------------------------------------------------------------ top-k above 32

@@ -544,7 +544,7 @@ std::tuple<at::Tensor, at::Tensor> ip_scan_topk_pair_rows(const at::Tensor& quer
   auto os = at::empty({Q, k}, q.options().dtype(at::kFloat));
   auto oi = at::empty({Q, k}, q.options().dtype(at::kLong));
   if (Q == 0) return {os, oi};
-  auto ws = workspace(tq_scan_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
+  auto ws = workspace(tq_scan_pair_rows_workspace_bytes(Q, (int32_t)d, (int32_t)bit_width, N, (int32_t)k), dev);
   check_rc(tq_ip_scan_topk_pair_rows(q.data_ptr(), to_tq(q.scalar_type()), Q, (int32_t)d,
                                      p.data_ptr<uint8_t>(), nm.data_ptr<float>(), N,
                                      cen.data_ptr<float>(), R.data_ptr<float>(), (int32_t)bit_width,

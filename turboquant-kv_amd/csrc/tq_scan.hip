@@ -934,6 +934,7 @@ __global__ __launch_bounds__(kPsThreads, PROD ? 4 : 6) void pair_scan_kernel(Sca
 
   const int s = blockIdx.z;
   const int q0 = s * a.qps + blockIdx.y;  // this block's query
+  if (a.qflag && !a.qflag[blockIdx.y]) return;  // only flagged queries are scanned (uniform)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int tid = threadIdx.x;
 
@@ -1648,6 +1649,53 @@ __device__ __forceinline__ float exact_pair_score_regs(const uint32_t (&rw)[D / 
   return acc * n;
 }
 
+// The same for a pair row of BITS-bit codes (layouts above pmp_row): products
+// q_rot[j] * c[code_j] added in dim order, then times the norm.
+template <int D, int BITS>
+__device__ __forceinline__ float exact_row_score_regs(const uint32_t (&rw)[D * BITS / 32], float n,
+                                                      const float* qr, const float* cen) {
+#pragma clang fp contract(off)
+  if constexpr (BITS == 4) {
+    return exact_pair_score_regs<D>(rw, n, qr, cen);
+  } else if constexpr (BITS == 2) {
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < D / 16; ++w)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (rw[w] >> (8 * b)) & 0xFFu;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float p = qr[16 * w + 4 * b + c] * cen[(byte >> (6 - 2 * c)) & 3u];
+          acc = acc + p;
+        }
+      }
+    return acc * n;
+  } else {
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) {
+      const uint32_t* X = rw + 3 * t;
+      const uint32_t x3 = ((X[0] >> 6) & 0x03030303u) | ((X[1] >> 4) & 0x0C0C0C0Cu) |
+                          ((X[2] >> 2) & 0x30303030u);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t wi = i < 3 ? X[i] : x3;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int p = 16 * t + 4 * i + k;
+          const uint32_t idx = (wi >> (8 * k)) & 63u;
+          const float p0 = qr[2 * p] * cen[idx >> 3];
+          acc = acc + p0;
+          const float p1 = qr[2 * p + 1] * cen[idx & 7u];
+          acc = acc + p1;
+        }
+      }
+    }
+    return acc * n;
+  }
+}
+
 __device__ __forceinline__ bool fs_keep(float hi, int id, float th, int thi) {
   return (hi > th) | ((hi == th) & (id <= thi));
 }
@@ -1799,7 +1847,7 @@ __device__ void merge_query_big(const float* __restrict__ part_s, const int32_t*
     const int b = cc / depth, pos = cc - b * depth;
     const int id = pi[(size_t)b * k + pos];
     const float sc = ps[(size_t)b * k + pos];
-    u[j] = (c < ncand) & (id >= 0) ? fs_fkey(sc) : 0u;
+    u[j] = ((c < ncand) & (id >= 0)) ? fs_fkey(sc) : 0u;
   }
   if (tid < 33) bcnt[tid] = 0;
   __syncthreads();
@@ -2487,14 +2535,14 @@ constexpr int kMqFallbackBlocks = 128;   // row blocks of the exact fallback sca
 static_assert(kMqSampleGroups / (kMqWaves * kMqGroupsPerWave) <= kMqMaxBuckets, "bucket count");
 
 struct MqArgs {
-  const uint8_t* rows;  // [n][D / 2] pair layout
+  const uint8_t* rows;  // [n][D * BITS / 8] pair rows (4 bits: the pair layout)
   const float* norms;   // [n]
   int64_t n;
   const void* q;        // [nq][D]
   int q_dt;
   int nq;
   const float* rot;     // [D][D]
-  const float* cen;     // [16]
+  const float* cen;     // [2^BITS]
   int k;
   float* qrot;          // [nq][D] rotated queries (reference arithmetic)
   uint32_t* qa;         // per tile [KT][4][64 lanes][4 words]: fp16 A operands
@@ -2515,20 +2563,27 @@ struct MqArgs {
   int64_t* out_i;
 };
 
-// Rows of one 64-row group for the MFMA B operands: lane 16 g + i holds LW words of row
-// 16 rt + i at byte 4 LW g of the row, per 16-row tile rt, and the norm of row `lane`.
+// Rows of one 64-row group for the MFMA B operands: lane 16 g + i holds NW words of row
+// 16 rt + i per 16-row tile rt, and the norm of row `lane`.  The words hold the dims of
+// lane group g's A operands (dims (D / 4) g ..):
+//   4 bits: D / 32 words at byte 4 NW g;
+//   3 bits: the 12-byte block of 32 dims holding them, at byte 12 g (D 128) or 12 (g / 2)
+//           (D 64: the odd group's pairs 12-15 are rebuilt from all three words);
+//   2 bits: D / 64 words at byte 4 NW g.
 // Rows past n read as zeros (the buffer's range check).
-template <int D, bool BIG>
+template <int D, int BITS, bool BIG>
 struct MqRows {
-  static constexpr int RB = D / 2;
-  static constexpr int LW = D / 32;
-  uint32_t w[4 * LW];
+  static constexpr int RB = D * BITS / 8;
+  static constexpr int NW = BITS == 4 ? D / 32 : BITS == 3 ? 3 : D / 64;
+  uint32_t w[4 * NW];
   float n;
   __device__ __forceinline__ void load(const MqArgs& a, uint32_t g, uint32_t ngroups,
                                        __amdgpu_buffer_rsrc_t rows_all,
                                        __amdgpu_buffer_rsrc_t norms_all, int lane, int cpol) {
     __amdgpu_buffer_rsrc_t rs = rows_all, ns = norms_all;
-    uint32_t roff = (lane & 15) * RB + (lane >> 4) * (4 * LW), noff = lane * 4u;
+    const uint32_t lg = (uint32_t)lane >> 4;
+    const uint32_t gofs = BITS == 3 ? 12u * (D == 128 ? lg : lg >> 1) : 4u * NW * lg;
+    uint32_t roff = (lane & 15) * RB + gofs, noff = lane * 4u;
     if constexpr (BIG) {
       const int64_t r0 = (int64_t)g * 64;
       const int64_t left = a.n - r0;
@@ -2542,14 +2597,23 @@ struct MqRows {
     }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
-      if constexpr (LW == 4) {
-        const u32x4 v = cpol ? __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, kNT)
-                             : __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(roff + 16 * RB * rt), 0, 0);
+      const int o = (int)(roff + 16 * RB * rt);
+      if constexpr (NW == 4) {
+        const u32x4 v = cpol ? __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
         w[4 * rt + 0] = v.x; w[4 * rt + 1] = v.y; w[4 * rt + 2] = v.z; w[4 * rt + 3] = v.w;
-      } else {
-        const u32x2 v = cpol ? __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, kNT)
-                             : __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(roff + 16 * RB * rt), 0, 0);
+      } else if constexpr (NW == 3) {
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 v = cpol ? __builtin_amdgcn_raw_buffer_load_b96(rs, o, 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b96(rs, o, 0, 0);
+        w[3 * rt + 0] = v.x; w[3 * rt + 1] = v.y; w[3 * rt + 2] = v.z;
+      } else if constexpr (NW == 2) {
+        const u32x2 v = cpol ? __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, kNT)
+                             : __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0);
         w[2 * rt + 0] = v.x; w[2 * rt + 1] = v.y;
+      } else {
+        w[rt] = cpol ? __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, kNT)
+                     : __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0);
       }
     }
     n = __uint_as_float(cpol ? __builtin_amdgcn_raw_buffer_load_b32(ns, (int)noff, 0, kNT)
@@ -2566,26 +2630,59 @@ __device__ __forceinline__ float row_max16(float v) {
   return v;
 }
 
-// The 64 KB fp16 centroid-pair table (entry (byte << 8) | lane * 4: (c[byte >> 4],
-// c[byte & 15]) in 64 lane copies), as pair_filter_kernel builds it.
+// The fp16 centroid-pair table: entry (p << 8) | lane * 4 holds (c[p >> BITS],
+// c[p & (2^BITS - 1)]) in 64 lane copies for each pair index p of two BITS-bit codes (the
+// first dim's code in the high bits): 64 KB for 4 bits, as pair_filter_kernel builds it,
+// 16 KB for 3 bits, 4 KB for 2 bits.
+template <int BITS>
 __device__ __forceinline__ void mq_fill_htab(char* htab, const float* cen_s, int tid, int nthreads) {
   typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-  for (int e = tid; e < 256 * 16; e += nthreads) {
+  constexpr int M = (1 << BITS) - 1;
+  for (int e = tid; e < (1 << (2 * BITS)) * 16; e += nthreads) {
     const int b = e >> 4, c = e & 15;
-    const uint32_t v = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)cen_s[b >> 4], (_Float16)cen_s[b & 15]});
+    const uint32_t v = __builtin_bit_cast(uint32_t, (h2_t){(_Float16)cen_s[b >> BITS], (_Float16)cen_s[b & M]});
     *reinterpret_cast<u32x4*>(htab + b * 256 + c * 16) = (u32x4){v, v, v, v};
   }
 }
 
+// Pair indices of k tile kt of N tile rt (dims 8 kt .. 8 kt + 7 of the lane group's
+// share), one per byte in dim order.
+template <int D, int BITS, bool BIG>
+__device__ __forceinline__ uint32_t mq_pair_indices(const MqRows<D, BITS, BIG>& rb, int rt, int kt,
+                                                    uint32_t lane) {
+  constexpr int NW = MqRows<D, BITS, BIG>::NW;
+  const uint32_t* w = rb.w + NW * rt;
+  if constexpr (BITS == 4) {
+    return w[kt];  // a byte per pair of dims
+  } else if constexpr (BITS == 3) {
+    // word i of the block: pairs 4 i .. 4 i + 3, six bits each; word 3 from the top bits
+    const uint32_t x3 = ((w[0] >> 6) & 0x03030303u) | ((w[1] >> 4) & 0x0C0C0C0Cu) |
+                        ((w[2] >> 2) & 0x30303030u);
+    if constexpr (D == 128) {
+      return kt < 3 ? w[kt] & 0x3F3F3F3Fu : x3;
+    } else {  // lane group g: words 2 (g % 2) + kt
+      const bool odd = (lane >> 4) & 1u;
+      return odd ? (kt ? x3 : w[2] & 0x3F3F3F3Fu) : w[kt] & 0x3F3F3F3Fu;
+    }
+  } else {
+    // bytes 2 kt, 2 kt + 1 of the lane's words, each two 4-bit pair indices (high nibble
+    // first): [b0 >> 4, b0 & 15, b1 >> 4, b1 & 15]
+    const uint32_t x = w[D == 128 ? kt >> 1 : 0];
+    const int h = D == 128 ? kt & 1 : kt;
+    const uint32_t t = __builtin_amdgcn_perm(x, x, h ? 0x03030202u : 0x01010000u);
+    return ((t >> 4) & 0x000F000Fu) | (t & 0x0F000F00u);
+  }
+}
+
 // B operands of N tile rt of the group in `rb`: per k tile, the fp16 centroid pairs of the
-// lane's four code bytes (one LDS lookup each).
-template <int D, bool BIG>
-__device__ __forceinline__ void mq_fetch_b(const MqRows<D, BIG>& rb, int rt, uint32_t lane4,
+// lane's four pair indices (one LDS lookup each).
+template <int D, int BITS, bool BIG>
+__device__ __forceinline__ void mq_fetch_b(const MqRows<D, BITS, BIG>& rb, int rt, uint32_t lane4,
                                            const char* htab, u32x4 (&bw)[D / 32]) {
-  constexpr int KT = D / 32, LW = D / 32;
+  constexpr int KT = D / 32;
 #pragma unroll
   for (int kt = 0; kt < KT; ++kt) {
-    const uint32_t x = rb.w[LW * rt + kt];
+    const uint32_t x = mq_pair_indices<D, BITS, BIG>(rb, rt, kt, lane4 >> 2);
     bw[kt] = (u32x4){fs_hlook<0>(x, lane4, htab), fs_hlook<1>(x, lane4, htab),
                      fs_hlook<2>(x, lane4, htab), fs_hlook<3>(x, lane4, htab)};
   }
@@ -2607,11 +2704,12 @@ __device__ __forceinline__ void mq_mfma(const u32x4 (&bw)[D / 32], const fs_v8h 
   }
 }
 
-template <int D, bool BIG>
-__device__ __forceinline__ void mq_tile_scores(const MqRows<D, BIG>& rb, int rt, const fs_v8h (&qa)[4][D / 32],
-                                               uint32_t lane4, const char* htab, fs_v4f (&acc)[4]) {
+template <int D, int BITS, bool BIG>
+__device__ __forceinline__ void mq_tile_scores(const MqRows<D, BITS, BIG>& rb, int rt,
+                                               const fs_v8h (&qa)[4][D / 32], uint32_t lane4,
+                                               const char* htab, fs_v4f (&acc)[4]) {
   u32x4 bw[D / 32];
-  mq_fetch_b<D, BIG>(rb, rt, lane4, htab, bw);
+  mq_fetch_b<D, BITS, BIG>(rb, rt, lane4, htab, bw);
   mq_mfma<D>(bw, qa, acc);
 }
 
@@ -2654,8 +2752,9 @@ __global__ __launch_bounds__(D) void mq_rotate_kernel(MqArgs a) {
 }
 
 // Per 64-query tile: the scale, beta and the fp16 A operands from the rotated queries.
-template <int D>
+template <int D, int BITS>
 __global__ __launch_bounds__(kMqThreads) void mq_tile_kernel(MqArgs a) {
+  constexpr int NC = 1 << BITS;  // centroids
   constexpr int KT = D / 32;
   __shared__ float qr[kMqQ][D + 1];
   __shared__ float red[2][kMqQ];
@@ -2667,7 +2766,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_tile_kernel(MqArgs a) {
     const int qi = e / D, j = e % D;
     qr[qi][j] = qi < nvalid ? a.qrot[(size_t)(q0 + qi) * D + j] : 0.f;
   }
-  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < NC) cen_s[tid] = a.cen[tid];
   __syncthreads();
   {  // max |q_rot| and ||q_rot||_1 per query: 8 threads per query
     const int qi = tid >> 3, part = tid & 7;
@@ -2694,7 +2793,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_tile_kernel(MqArgs a) {
   for (int i = 0; i < kMqQ; ++i) { amax = fmaxf(amax, red[0][i]); l1 = fmaxf(l1, red[1][i]); }
   float cmax = 0.f, ec = 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < NC; ++i) {
     cmax = fmaxf(cmax, fabsf(cen_s[i]));
     ec = fmaxf(ec, fabsf(cen_s[i] - (float)(_Float16)cen_s[i]));
   }
@@ -2751,12 +2850,13 @@ __device__ __forceinline__ void mq_load_tile(const MqArgs& a, int tile, int lane
 
 // Buckets: wave (block b, wave w) takes sampled groups (8 b + w) * 4 + u; lane (n, g) keeps
 // per query 16 mt + 4 g + r the largest lo over its rows 16 rt + n of those groups.
-template <int D, bool BIG>
+template <int D, int BITS, bool BIG>
 __global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 mq_sample_kernel(MqArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
+  __shared__ __attribute__((aligned(16))) char htab[256 << (2 * BITS)];
   __shared__ float cen_s[16];
+  constexpr uint32_t RB = D * BITS / 8;
   __shared__ float wmax_s[kMqWaves][kMqQ];
   const int rtile = blockIdx.y, tile = a.tile0 + rtile;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -2766,11 +2866,11 @@ mq_sample_kernel(MqArgs a) {
   fs_v8h qa[4][D / 32];
   float inv_s, beta;
   mq_load_tile<D>(a, tile, lane, qa, inv_s, beta);
-  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < (1 << BITS)) cen_s[tid] = a.cen[tid];
   __syncthreads();
-  mq_fill_htab(htab, cen_s, tid, kMqThreads);
+  mq_fill_htab<BITS>(htab, cen_s, tid, kMqThreads);
   __syncthreads();
-  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * (uint32_t)(D / 2));
+  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * RB);
   const __amdgpu_buffer_rsrc_t norms_all = buf_rsrc(a.norms, BIG ? 0u : n * 4u);
   const uint32_t lane4 = (uint32_t)lane * 4;
   float bmax[4][4];
@@ -2781,7 +2881,7 @@ mq_sample_kernel(MqArgs a) {
   const int sw = blockIdx.x * kMqWaves + wave;
   // every group's loads first (a sampled group past nsgroups reads the empty range past
   // the last row: zeros, and its rows are not valid)
-  MqRows<D, BIG> rbs[kMqGroupsPerWave];
+  MqRows<D, BITS, BIG> rbs[kMqGroupsPerWave];
   uint32_t gs[kMqGroupsPerWave];
 #pragma unroll
   for (int u = 0; u < kMqGroupsPerWave; ++u) {
@@ -2792,11 +2892,11 @@ mq_sample_kernel(MqArgs a) {
 #pragma unroll
   for (int u = 0; u < kMqGroupsPerWave; ++u) {
     const uint32_t g = gs[u];
-    const MqRows<D, BIG>& rb = rbs[u];
+    const MqRows<D, BITS, BIG>& rb = rbs[u];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       fs_v4f acc[4];
-      mq_tile_scores<D, BIG>(rb, rt, qa, lane4, htab, acc);
+      mq_tile_scores<D, BITS, BIG>(rb, rt, qa, lane4, htab, acc);
       const float nr = __shfl(rb.n, 16 * rt + (lane & 15));
       const bool valid = g * 64u + 16u * rt + (uint32_t)(lane & 15) < n;
       const float m = inv_s * nr;
@@ -2858,12 +2958,13 @@ __device__ __forceinline__ void mq_tau(const MqArgs& a, int rtile, int tid, floa
 }
 
 // Every row against tau per query; rows whose upper bound reaches it are listed.
-template <int D, bool BIG>
+template <int D, int BITS, bool BIG>
 __global__ __launch_bounds__(kMqThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 mq_filter_kernel(MqArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) char htab[kHtabBytes];
+  __shared__ __attribute__((aligned(16))) char htab[256 << (2 * BITS)];
   __shared__ float cen_s[16];
+  constexpr uint32_t RB = D * BITS / 8;
   __shared__ int cnt_s[kMqQ];
   __shared__ float tau_s[kMqQ];
   const int rtile = blockIdx.y, tile = a.tile0 + rtile;
@@ -2874,16 +2975,16 @@ mq_filter_kernel(MqArgs a) {
   const uint32_t n = (uint32_t)a.n;
   const uint32_t ngroups = (n + 63) / 64;
   const int nsteps = gw < ngroups ? (int)((ngroups - 1 - gw) / W + 1) : 0;
-  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * (uint32_t)(D / 2));
+  const __amdgpu_buffer_rsrc_t rows_all = buf_rsrc(a.rows, BIG ? 0u : n * RB);
   const __amdgpu_buffer_rsrc_t norms_all = buf_rsrc(a.norms, BIG ? 0u : n * 4u);
-  MqRows<D, BIG> ta, tb;
+  MqRows<D, BITS, BIG> ta, tb;
   ta.load(a, gw, ngroups, rows_all, norms_all, lane, 1);
   tb.load(a, gw + W, ngroups, rows_all, norms_all, lane, 1);
 
   fs_v8h qa[4][D / 32];
   float inv_s, beta;
   mq_load_tile<D>(a, tile, lane, qa, inv_s, beta);
-  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < (1 << BITS)) cen_s[tid] = a.cen[tid];
   if (tid < kMqQ) cnt_s[tid] = 0;
   mq_tau(a, rtile, tid, tau_s);
   __syncthreads();
@@ -2899,7 +3000,7 @@ mq_filter_kernel(MqArgs a) {
       th[mt][r] = v ? tau_s[ql] : INFINITY;
       qv |= (uint32_t)v << (4 * mt + r);
     }
-  mq_fill_htab(htab, cen_s, tid, kMqThreads);
+  mq_fill_htab<BITS>(htab, cen_s, tid, kMqThreads);
   __syncthreads();
   const uint32_t lane4 = (uint32_t)lane * 4;
   const size_t lbase = ((size_t)rtile * a.nb + blockIdx.x) * kMqQ;
@@ -2907,15 +3008,15 @@ mq_filter_kernel(MqArgs a) {
   // Per row tile: the MFMAs, then hi = acc * m + H of (query 16 mt + 4 (lane >> 4) + r, row
   // 16 rt + (lane & 15)) against the queries' tau.  The next tile's table lookups are issued
   // before this tile's tests, so their latency runs under the tests and the branch.
-  auto step = [&](const MqRows<D, BIG>& rb, int t) {
+  auto step = [&](const MqRows<D, BITS, BIG>& rb, int t) {
     const uint32_t g = (uint32_t)t * W + gw;
     u32x4 bw[2][D / 32];
-    mq_fetch_b<D, BIG>(rb, 0, lane4, htab, bw[0]);
+    mq_fetch_b<D, BITS, BIG>(rb, 0, lane4, htab, bw[0]);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       fs_v4f acc[4];
       mq_mfma<D>(bw[rt & 1], qa, acc);
-      if (rt < 3) mq_fetch_b<D, BIG>(rb, rt + 1, lane4, htab, bw[(rt + 1) & 1]);
+      if (rt < 3) mq_fetch_b<D, BITS, BIG>(rb, rt + 1, lane4, htab, bw[(rt + 1) & 1]);
       const float nr = __shfl(rb.n, 16 * rt + (lane & 15));
       const uint32_t row = g * 64u + 16u * rt + (uint32_t)(lane & 15);
       const bool valid = row < n;
@@ -2962,7 +3063,7 @@ mq_filter_kernel(MqArgs a) {
 // Per query: the listed rows of every block, tau' = their k-th best lo, the rows whose hi
 // reaches it rescored exactly and ranked.  More than kMqCap rows listed by one block, or
 // more than MCAP in all, flags the query for the exact fallback instead.
-template <int D, int MCAP>
+template <int D, int BITS, int MCAP>
 __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   __shared__ __attribute__((aligned(16))) float ehi[MCAP];
   __shared__ __attribute__((aligned(16))) float elo[MCAP];
@@ -3018,7 +3119,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
     eid[e] = a.cid[src];
   }
   if (tid < D) qr_s[tid] = a.qrot[(size_t)q * D + tid];
-  if (tid < 16) cen_s[tid] = a.cen[tid];
+  if (tid < (1 << BITS)) cen_s[tid] = a.cen[tid];
   __syncthreads();
   // tau' = max(tau, k-th best lo): a 32-step binary search on keys, every thread holding
   // its EPT entries' keys (per step a compare mask and a popcount per register, one LDS
@@ -3065,19 +3166,20 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   __syncthreads();
   const int m2 = m2_s;
   // exact rescoring of the survivors: the row's codes and norm from memory
-  constexpr int RB = D / 2;
+  constexpr int RB = D * BITS / 8;
   for (int s = tid; s < m2; s += kMqThreads) {
     const int id = eid[s];
-    // the row's bytes and norm requested together, then scored from registers
-    uint32_t rw[D / 8];
-    const u32x4* r4 = reinterpret_cast<const u32x4*>(a.rows + (size_t)id * RB);
+    // the row's bytes (8-byte aligned) and norm requested together, then scored from
+    // registers
+    uint32_t rw[RB / 4];
+    const u32x2* r2 = reinterpret_cast<const u32x2*>(a.rows + (size_t)id * RB);
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
-      const u32x4 v = r4[i];
-      rw[4 * i] = v.x; rw[4 * i + 1] = v.y; rw[4 * i + 2] = v.z; rw[4 * i + 3] = v.w;
+    for (int i = 0; i < RB / 8; ++i) {
+      const u32x2 v = r2[i];
+      rw[2 * i] = v.x; rw[2 * i + 1] = v.y;
     }
     const float nrm = a.norms[id];
-    const float sc = exact_pair_score_regs<D>(rw, nrm, qr_s, cen_s);
+    const float sc = exact_row_score_regs<D, BITS>(rw, nrm, qr_s, cen_s);
     const bool ok = !__builtin_isnan(sc);
     ehi[s] = ok ? sc : -INFINITY;
     if (!ok) eid[s] = INT_MAX;  // ranks below every listed row
@@ -3480,7 +3582,9 @@ struct MqLayout {
   size_t qrot, qa, tparam, tau, flag, buckets, cnt, chi, clo, cid, fps, fpi, total;
 };
 
-MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
+int pair_scan_blocks(int64_t nrows);
+
+MqLayout mq_layout(int64_t nq, int d, int64_t N, int k, int bits) {
   MqLayout L{};
   const int KT = d / 32;
   L.ntiles = (int)((nq + kMqQ - 1) / kMqQ);
@@ -3493,7 +3597,9 @@ MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
   const int sblocks = (L.nsgroups + kMqWaves * kMqGroupsPerWave - 1) / (kMqWaves * kMqGroupsPerWave);
   L.nbk = sblocks;
   L.nb = filter_blocks(N);
-  L.fbx = scan_blocks(N) < kMqFallbackBlocks ? scan_blocks(N) : kMqFallbackBlocks;
+  // row blocks of the exact fallback: the 4-bit multi-query scan, or the pair-row scan
+  const int fb = bits == 4 ? scan_blocks(N) : pair_scan_blocks(N);
+  L.fbx = fb < kMqFallbackBlocks ? fb : kMqFallbackBlocks;
   const size_t rq = (size_t)L.tiles_round * kMqQ;
   size_t o = 256;
   auto take = [&](size_t bytes) { const size_t at = o; o = align_up(o + bytes, 256); return at; };
@@ -3514,19 +3620,20 @@ MqLayout mq_layout(int64_t nq, int d, int64_t N, int k) {
   return L;
 }
 
-// The multi-query filter applies to 4-bit pair rows of d 64 / 128 with at least two
-// queries, or one query with k above the one-query filter's kSmallK.
-bool mq_applies(int64_t nq, int d, int64_t N, int k) {
-  return (nq >= 2 || (nq == 1 && k > kSmallK)) && N > 0 && (d == 64 || d == 128);
+// The multi-query filter applies to pair rows of d 64 / 128 with at least two queries; for
+// 4-bit rows also to one query with k above the one-query filter's kSmallK.
+bool mq_applies(int64_t nq, int d, int64_t N, int k, int bits) {
+  return (nq >= 2 || (bits == 4 && nq == 1 && k > kSmallK)) && N > 0 && (d == 64 || d == 128) &&
+         bits >= 2 && bits <= 4;
 }
 
-template <int D>
+template <int D, int BITS>
 int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size_t qbytes,
                 char* ws, bool big, hipStream_t st) {
   hipLaunchKernelGGL((mq_rotate_kernel<D>), dim3((unsigned)((base.nq + kMqRotQ - 1) / kMqRotQ)),
                      dim3(D), 0, st, base);
   TQ_LAUNCH_CHECK("mq_rotate_kernel");
-  hipLaunchKernelGGL((mq_tile_kernel<D>), dim3((unsigned)L.ntiles), dim3(kMqThreads), 0, st, base);
+  hipLaunchKernelGGL((mq_tile_kernel<D, BITS>), dim3((unsigned)L.ntiles), dim3(kMqThreads), 0, st, base);
   TQ_LAUNCH_CHECK("mq_tile_kernel");
   const int sblocks = L.nbk;
   for (int t0 = 0; t0 < L.ntiles; t0 += L.tiles_round) {
@@ -3535,21 +3642,21 @@ int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size
     const int nt = L.ntiles - t0 < L.tiles_round ? L.ntiles - t0 : L.tiles_round;
     const dim3 sg((unsigned)sblocks, (unsigned)nt), fg((unsigned)L.nb, (unsigned)nt);
     if (big) {
-      hipLaunchKernelGGL((mq_sample_kernel<D, true>), sg, dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_sample_kernel<D, BITS, true>), sg, dim3(kMqThreads), 0, st, a);
     } else {
-      hipLaunchKernelGGL((mq_sample_kernel<D, false>), sg, dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_sample_kernel<D, BITS, false>), sg, dim3(kMqThreads), 0, st, a);
     }
     TQ_LAUNCH_CHECK("mq_sample_kernel");
     if (big) {
-      hipLaunchKernelGGL((mq_filter_kernel<D, true>), fg, dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_filter_kernel<D, BITS, true>), fg, dim3(kMqThreads), 0, st, a);
     } else {
-      hipLaunchKernelGGL((mq_filter_kernel<D, false>), fg, dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_filter_kernel<D, BITS, false>), fg, dim3(kMqThreads), 0, st, a);
     }
     TQ_LAUNCH_CHECK("mq_filter_kernel");
     if (a.k > kSmallK)
-      hipLaunchKernelGGL((mq_merge_kernel<D, kMqMergeCapBig>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_merge_kernel<D, BITS, kMqMergeCapBig>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
     else
-      hipLaunchKernelGGL((mq_merge_kernel<D, kMqMergeCap>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
+      hipLaunchKernelGGL((mq_merge_kernel<D, BITS, kMqMergeCap>), dim3((unsigned)(nt * kMqQ)), dim3(kMqThreads), 0, st, a);
     TQ_LAUNCH_CHECK("mq_merge_kernel");
     // The exact scan for the round's flagged queries (blocks of unflagged ones return).
     const int q0 = t0 * kMqQ;
@@ -3565,8 +3672,12 @@ int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size
     s.out_s = a.out_s + (size_t)q0 * a.k;
     s.out_i = a.out_i + (size_t)q0 * a.k;
     s.qflag = a.flag + q0;
-    const dim3 xg((unsigned)L.fbx, (unsigned)((rq + 3) / 4), 1u);
-    const int rc = launch_scan_pairs<true>(s, 4, xg, st);
+    int rc;
+    if constexpr (BITS == 4) {
+      rc = launch_scan_pairs<true>(s, 4, dim3((unsigned)L.fbx, (unsigned)((rq + 3) / 4), 1u), st);
+    } else {  // the pair-row scan: one query per block row
+      rc = launch_pair_scan<true>(s, dim3((unsigned)L.fbx, (unsigned)rq, 1u), st, BITS);
+    }
     if (rc != TQ_OK) return rc;
     hipLaunchKernelGGL(merge_kernel, dim3((unsigned)rq), dim3(kThreads), 0, st, s.part_s, s.part_i,
                        L.fbx, a.k, s.out_s, s.out_i, (const int32_t*)s.qflag);
@@ -3577,8 +3688,8 @@ int launch_mq_d(const MqArgs& base, const MqLayout& L, const void* queries, size
 
 int launch_mq(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, const uint8_t* pairs,
               const float* norms, int64_t N, const float* centroids, const float* rotation,
-              int32_t k, float* out_scores, int64_t* out_ids, char* ws, hipStream_t st) {
-  const MqLayout L = mq_layout(nq, d, N, k);
+              int32_t bits, int32_t k, float* out_scores, int64_t* out_ids, char* ws, hipStream_t st) {
+  const MqLayout L = mq_layout(nq, d, N, k, bits);
   TQ_REQUIRE(L.nb <= kMqThreads, "too many filter blocks");
   MqArgs a{};
   a.rows = pairs; a.norms = norms; a.n = N; a.q = queries; a.q_dt = q_dtype; a.nq = (int)nq;
@@ -3597,9 +3708,15 @@ int launch_mq(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d, cons
   a.out_s = out_scores; a.out_i = out_ids;
   const size_t qbytes = (size_t)d * dtype_size(q_dtype);
   // 32-bit offsets while rows and norms stay under 2^32 bytes
-  const bool big = N * (d / 2) >= ((int64_t)1 << 32) - 4096 || N * 4 >= ((int64_t)1 << 32) - 4096;
-  return d == 128 ? launch_mq_d<128>(a, L, queries, qbytes, ws, big, st)
-                  : launch_mq_d<64>(a, L, queries, qbytes, ws, big, st);
+  const bool big = N * (d * bits / 8) >= ((int64_t)1 << 32) - 4096 || N * 4 >= ((int64_t)1 << 32) - 4096;
+  if (d == 128) {
+    if (bits == 2) return launch_mq_d<128, 2>(a, L, queries, qbytes, ws, big, st);
+    if (bits == 3) return launch_mq_d<128, 3>(a, L, queries, qbytes, ws, big, st);
+    return launch_mq_d<128, 4>(a, L, queries, qbytes, ws, big, st);
+  }
+  if (bits == 2) return launch_mq_d<64, 2>(a, L, queries, qbytes, ws, big, st);
+  if (bits == 3) return launch_mq_d<64, 3>(a, L, queries, qbytes, ws, big, st);
+  return launch_mq_d<64, 4>(a, L, queries, qbytes, ws, big, st);
 }
 
 }  // namespace
@@ -3623,13 +3740,18 @@ size_t tq_scan_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t
   return bytes;
 }
 
-size_t tq_scan_pairs_workspace_bytes(int64_t nq, int32_t d, int64_t N, int32_t k) {
-  size_t bytes = tq_scan_workspace_bytes(nq, d, 4, N, k);
-  if (k >= 1 && k <= kMaxK && mq_applies(nq, d, N, k)) {
-    const size_t mq = mq_layout(nq, d, N, k).total;
+size_t tq_scan_pair_rows_workspace_bytes(int64_t nq, int32_t d, int32_t bit_width, int64_t N,
+                                         int32_t k) {
+  size_t bytes = tq_scan_workspace_bytes(nq, d, bit_width, N, k);
+  if (k >= 1 && k <= kMaxK && mq_applies(nq, d, N, k, bit_width)) {
+    const size_t mq = mq_layout(nq, d, N, k, bit_width).total;
     if (mq > bytes) bytes = mq;
   }
   return bytes;
+}
+
+size_t tq_scan_pairs_workspace_bytes(int64_t nq, int32_t d, int64_t N, int32_t k) {
+  return tq_scan_pair_rows_workspace_bytes(nq, d, 4, N, k);
 }
 
 }  // extern "C"
@@ -3668,12 +3790,11 @@ int ip_scan_topk(const void* queries, tq_dtype q_dtype, int64_t nq, int32_t d,
   const size_t need = tq_scan_workspace_bytes(nq, d, bit_width, N, k);
   TQ_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need %zu bytes", need);
   hipStream_t st = as_stream(stream);
-  // Several queries over 4-bit pair rows: the multi-query filtered scan, when the
-  // workspace holds its buffers (tq_scan_pairs_workspace_bytes); the exact multi-query
-  // scan below otherwise.
-  if (pairs && bit_width == 4 && !prod && mq_applies(nq, d, N, k) && nq <= INT_MAX &&
-      workspace_bytes >= mq_layout(nq, d, N, k).total)
-    return launch_mq(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, k,
+  // Several queries over pair rows: the multi-query filtered scan, when the workspace
+  // holds its buffers (tq_scan_pair_rows_workspace_bytes); the exact scans below otherwise.
+  if (pairs && !prod && mq_applies(nq, d, N, k, bit_width) && nq <= INT_MAX &&
+      workspace_bytes >= mq_layout(nq, d, N, k, bit_width).total)
+    return launch_mq(queries, q_dtype, nq, d, packed, norms, N, centroids, rotation, bit_width, k,
                      out_scores, out_ids, static_cast<char*>(workspace), st);
   char* ws = static_cast<char*>(workspace) + 256;
   // The lists are laid out for scan_blocks(N) blocks; a launch uses at most that many.
