@@ -702,9 +702,13 @@ def bench_cpu_configs(args, extra):
     R = make_rotation_matrix(128, 42)
     bnd, cen = lloyd_max_codebook(4, 128)
     xn, Rn, bn, cn, qn = (t.numpy() for t in (x, R, bnd, cen, qs))
-    cpu_libs.rotate_and_quantize(xn[:1024], Rn, bn, 4)  # warm the thread pool
+    # quantize: the reference's rotate_and_quantize_cpu (quant_cpu.cpp:44-118) compiled from
+    # its source into oracle/_ref where that build exists, else the C restatement of it
+    qref = cpu_libs.have_ref_cpu()
+    quantize = cpu_libs.ref_cpu_rotate_and_quantize if qref else cpu_libs.rotate_and_quantize
+    quantize(xn[:1024], Rn, bn, 4)  # warm the thread pool
     t0 = time.perf_counter()
-    packed, norms = cpu_libs.rotate_and_quantize(xn, Rn, bn, 4)
+    packed, norms = quantize(xn, Rn, bn, 4)
     tq = time.perf_counter() - t0
     t0 = time.perf_counter()
     s_cpu, i_cpu = cpu_libs.search_packed(qn, packed, norms, Rn, cn, 4, 10, which)
@@ -716,9 +720,17 @@ def bench_cpu_configs(args, extra):
     tgs = time_op(lambda: ops.ip_scan_topk(qg, pg, ng, cg, Rg, 4, 10), 20, 3)
     _, i_gpu = ops.ip_scan_topk(qg, pg, ng, cg, Rg, 4, 10)
     same = float((i_gpu.cpu().numpy() == i_cpu).mean())
+    tqt, tst, pk_t, ids_t, thr = torch_cpu_config0(x, R, bnd, cen, qs)
+    extra["cpu_config0_torch"] = {
+        "quantize_vectors_per_s": 65536 / tqt, "search_queries_per_s": 256 / tst, "threads": thr,
+        "kind": "port", "packed_byte_agreement_with_c_path": float((pk_t == packed).mean()),
+        "topk_id_agreement_with_c_path": float((ids_t == i_cpu).mean()),
+        "note": "torch-CPU composition of reference.py's algorithm: norm, divide, rotate, "
+                "searchsorted, bit-plane pack; search by unpack, centroid gather, matmul, topk"}
     extra["cpu_config0"] = {
         "quantize_vectors_per_s": 65536 / tq, "search_queries_per_s": 256 / ts, "cores": cores,
-        "quantize": "port (C/OpenMP restatement of quant_cpu.cpp:44-118)",
+        "quantize": ("reference (quant_cpu.cpp rotate_and_quantize_cpu, compiled from its source)"
+                     if qref else "port (C/OpenMP restatement of quant_cpu.cpp:44-118)"),
         "search": f"{kind} (turboquant_core.cpp search_packed, one query per OpenMP thread)",
         "sample": "the whole config: 65,536 x 128 fp32 vectors, 256 queries, k = 10",
         "gpu_quantize_vectors_per_s": 65536 / tgq * 1e3, "gpu_search_queries_per_s": 256 / tgs * 1e3,
@@ -746,6 +758,41 @@ def bench_cpu_configs(args, extra):
                   "clipped to 255), prod 3+1 bit",
         "note": "numpy restatement of reference.py:392-469 (BLAS matmuls)"}
     log(f"config 2 prod quantize CPU ({threads} threads): {n / tp / 1e6:.2f} M vec/s")
+
+
+def torch_cpu_config0(x, R, bnd, cen, qs, bits=4, k=10):
+    """configs[0] through torch CPU ops in the steps of reference.py (quantize_mse:
+    normalize by max(||x||, 1e-10), rotate, searchsorted, pack bit planes MSB first; search:
+    unpack, centroids times norms, q_rot @ rows^T, topk).  Returns (quantize seconds,
+    search seconds, packed codes, top-k ids, threads)."""
+    import torch
+    thr = torch.get_num_threads()
+    n, d = x.shape
+    w8 = torch.tensor([128, 64, 32, 16, 8, 4, 2, 1], dtype=torch.uint8)
+
+    def quantize(v):
+        nrm = torch.linalg.vector_norm(v, dim=1)
+        u = v / nrm.clamp_min(1e-10)[:, None]
+        codes = torch.searchsorted(bnd, (u @ R.T).contiguous())
+        planes = [(((codes >> p) & 1).to(torch.uint8).view(v.shape[0], d // 8, 8) * w8).sum(-1, dtype=torch.uint8)
+                  for p in range(bits)]
+        return torch.cat(planes, dim=1), nrm
+
+    def search(q, packed, nrm):
+        planes = packed.view(-1, bits, d // 8)
+        bitsv = ((planes[..., None] >> torch.arange(7, -1, -1, dtype=torch.uint8)) & 1).view(-1, bits, d)
+        codes = (bitsv.to(torch.int64) << torch.arange(bits).view(1, bits, 1)).sum(1)
+        rows = cen[codes] * nrm[:, None]
+        return torch.topk((q @ R.T) @ rows.T, k, dim=1)
+
+    quantize(x[:1024])
+    t0 = time.perf_counter()
+    packed, nrm = quantize(x)
+    tq = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    _, ids = search(qs, packed, nrm)
+    ts = time.perf_counter() - t0
+    return tq, ts, packed.numpy(), ids.numpy(), thr
 
 
 def rs_normal(n, d, seed=0):

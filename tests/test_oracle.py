@@ -110,6 +110,73 @@ def test_pack_matches_reference_core():
         assert np.array_equal(cpu_libs.ref_pack_codes(codes, bits), O.pack_codes(codes, bits))
 
 
+# ------------------------------------------------------------------ the reference's CPU kernels
+# csrc/cpu/quant_cpu.cpp compiled from the reference's source against the installed torch
+# (oracle/_ref/libquant_cpu_ref.so, through oracle/ref_quant_cpu_shim.cpp).
+_REF_CPU = pytest.mark.skipif(not cpu_libs.have_ref_cpu(), reason="reference CPU kernels not built here")
+
+
+@_REF_CPU
+def test_quantize_port_bit_exact_with_reference_cpu_kernel():
+    # rotate_and_quantize_cpu (quant_cpu.cpp:44-118): the C restatement timed as the config-0
+    # CPU baseline returns its codes and norms bit for bit; the numpy oracle's codes agree
+    # outside their ambiguity band.  Heavy-tailed rows, a zero row and a 1e-12-scaled row.
+    rs = np.random.RandomState(21)
+    for d, b in ((64, 2), (128, 4), (200, 3), (128, 1)):
+        R = O.dense_qr_rotation(d, 42)
+        bnd, _ = O.lloyd_max_codebook(b, d)
+        x = (rs.randn(700, d) * rs.lognormal(size=(1, d))).astype(np.float32)
+        x[3] = 0.0
+        x[5] *= np.float32(1e-12)
+        pr, nr = cpu_libs.ref_cpu_rotate_and_quantize(x, R, bnd, b)
+        pp, npo = cpu_libs.rotate_and_quantize(x, R, bnd, b)
+        assert np.array_equal(pp, pr), (d, b)
+        assert np.array_equal(npo.view(np.uint32), nr.view(np.uint32)), (d, b)
+        _, n, codes = O.quantize_mse(x, b, R, bnd)
+        refc = O.unpack_codes(pr, b, d)
+        # rows of norm <= 1e-10: the CPU kernel multiplies them by 0 (quant_cpu.cpp:83, the
+        # code of 0 everywhere) where reference.py divides by max(n, 1e-10) (the oracle)
+        tiny = nr <= np.float32(1e-10)
+        assert tiny[3] and tiny[5] and tiny.sum() == 2
+        assert (refc[tiny] == np.searchsorted(bnd, np.float32(0.0), side="left")).all()
+        O.check_codes(codes[~tiny], refc[~tiny], x[~tiny], R, bnd)
+        # norms: d squares summed in another order (numpy's pairwise sum vs the kernel's loop)
+        assert np.allclose(n, nr, rtol=d * 2.0 ** -24, atol=0)
+
+
+@_REF_CPU
+def test_scores_oracle_bit_exact_with_reference_cpu_kernel():
+    # attention_scores_packed_cpu (quant_cpu.cpp:125-197) against the oracle's exact-fp32
+    # LUT scores (the arithmetic the GPU scans are held to), batch x heads queries
+    rs = np.random.RandomState(22)
+    for d, b in ((64, 3), (128, 4), (200, 2)):
+        R = O.dense_qr_rotation(d, 42)
+        bnd, cen = O.lloyd_max_codebook(b, d)
+        packed, norms, _ = O.quantize_mse(rs.randn(900, d).astype(np.float32), b, R, bnd)
+        q = rs.randn(2, 3, d).astype(np.float32)
+        got = cpu_libs.ref_cpu_attention_scores(q, packed, norms, cen, R, b)
+        want = O.lut_scores_f32(q.reshape(6, d), packed, norms, cen, R, b).reshape(2, 3, -1)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (d, b)
+
+
+@_REF_CPU
+def test_values_oracle_matches_reference_cpu_kernel():
+    # attention_values_packed_cpu (quant_cpu.cpp:199-266), fp32, against the oracle's
+    # float64 closed form with M = R (what the reference's `rotation_T` argument is given)
+    rs = np.random.RandomState(23)
+    for d, b in ((64, 2), (128, 3), (200, 4)):
+        R = O.dense_qr_rotation(d, 43)
+        bnd, cen = O.lloyd_max_codebook(b, d)
+        packed, norms, _ = O.quantize_mse(rs.randn(500, d).astype(np.float32), b, R, bnd)
+        w = rs.rand(2, 2, 500).astype(np.float32)
+        w /= w.sum(-1, keepdims=True)
+        got = cpu_libs.ref_cpu_attention_values(w, packed, norms, cen, R, b, d)
+        want = O.values_f64(w.reshape(4, 500), packed, norms, cen, R, b).reshape(2, 2, d)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max()), (d, b)
+        wrong = O.values_f64(w.reshape(4, 500), packed, norms, cen, R.T.copy(), b).reshape(2, 2, d)
+        assert np.abs(got - wrong).max() > 0.1 * np.abs(want).max()
+
+
 # ------------------------------------------------------------------ quantize
 def test_searchsorted_tie_goes_low():
     bnd = np.array([-1.0, 0.0, 1.0], np.float32)
