@@ -335,6 +335,24 @@ int tq_unpack_decode_layout(const uint8_t* cache, int64_t n_streams, int64_t t_c
                             uint8_t* packed, void* stream);
 
 /*
+ * One decode step's cache append in one launch: token `pos` of every stream (key and
+ * value [n_streams][d], bf16 or fp16, d = 64 or 128) quantized (4-bit keys, vbits-bit
+ * values; the codebook boundaries and rotations of tq_rotate_and_quantize) and written
+ * into the decode layout above: kpairs [n_streams][t_cap][d/2], vtiles
+ * [n_streams][t_cap/64][512*vbits*(d/64)] (only this token's bits change), and the norms
+ * knorms / vnorms [n_streams][t_cap] in norm_dtype (TQ_F32, TQ_BF16 or TQ_F16).  Codes
+ * and norms equal tq_rotate_and_quantize (rounding in the input type) followed by
+ * tq_pack_decode_layout, bit for bit.
+ * Replaces: the quantize-and-store of one new token in TurboQuantCache.update
+ * (hf_integration.py:319-345 with cache.py:148-210's quantize_mse of keys and values).
+ */
+int tq_cache_append_dl(const void* key, const void* value, tq_dtype in_dtype, int64_t n_streams,
+                       int32_t d, const float* krotation, const float* kboundaries,
+                       const float* vrotation, const float* vboundaries, int32_t vbits,
+                       uint8_t* kpairs, void* knorms, uint8_t* vtiles, void* vnorms,
+                       tq_dtype norm_dtype, int64_t t_cap, int64_t pos, void* stream);
+
+/*
  * tq_decode_attention_packed over a decode-layout cache (same semantics and output):
  * head_dim 64, 4-bit keys, 2-4 bit values (vbits), any number of query heads per KV head
  * (launched four at a time), t_cap a multiple of 64.  kpairs [B, hkv, t_cap, 32],

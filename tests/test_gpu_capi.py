@@ -1263,6 +1263,70 @@ def test_fused_decode_ragged_vs_f64(kb, vb, G):
             assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= 1e-4
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("vb", [2, 3, 4])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_cache_append_dl_equals_quantize_then_pack(d, vb, dt):
+    # tq_cache_append_dl (one token per stream, one launch) against tq_rotate_and_quantize
+    # (rounding in the input type) followed by tq_pack_decode_layout, bit for bit: caches
+    # that start as random bytes (the other tokens' bits must survive), positions on both
+    # sides of tile boundaries, fp32 and 16-bit norm caches, outlier channels.
+    tdt, cdt = (torch.bfloat16, capi.TQ_BF16) if dt == "bf16" else (torch.float16, capi.TQ_F16)
+    rs = np.random.RandomState(500 + 10 * vb + d)
+    S, t_cap = 37, 192
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, _ = O.lloyd_max_codebook(4, d)
+    bv, _ = O.lloyd_max_codebook(vb, d)
+    scales = np.ones(d, np.float32)
+    scales[rs.choice(d, 4, replace=False)] = 20.0
+    g = torch.Generator(device=DEV)
+    g.manual_seed(vb * 1000 + d)
+    kp0 = torch.randint(0, 256, (S, t_cap, d // 2), dtype=torch.uint8, device=DEV, generator=g)
+    vp0 = torch.randint(0, 256, (S, t_cap // 64, 8 * vb * d), dtype=torch.uint8, device=DEV, generator=g)
+    for ndt, ncode in ((torch.float32, capi.TQ_F32), (tdt, cdt)):
+        kn0 = torch.randn(S, t_cap, device=DEV, generator=g).to(ndt)
+        vn0 = torch.randn(S, t_cap, device=DEV, generator=g).to(ndt)
+        fused = [kp0.clone(), kn0.clone(), vp0.clone(), vn0.clone()]
+        ref = [kp0.clone(), kn0.clone(), vp0.clone(), vn0.clone()]
+        for pos in (0, 1, 62, 63, 64, 65, 127, 128, 191):
+            k = torch.from_numpy(rs.randn(S, d).astype(np.float32) * scales).to(DEV).to(tdt)
+            v = torch.from_numpy(rs.randn(S, d).astype(np.float32) * scales).to(DEV).to(tdt)
+            if pos == 65:
+                k[3] = 0  # a zero row: norm 0, the code of 0 everywhere
+            capi.check(L().tq_cache_append_dl(
+                capi.p(k), capi.p(v), cdt, capi.i64(S), capi.i32(d), capi.p(T(Rk)), capi.p(T(bk)),
+                capi.p(T(Rv)), capi.p(T(bv)), capi.i32(vb), capi.p(fused[0]), capi.p(fused[1]),
+                capi.p(fused[2]), capi.p(fused[3]), ncode, capi.i64(t_cap), capi.i64(pos), capi.stream()))
+            kq, kn = k_quantize(k, Rk, bk, 4, cdt, cdt)
+            vq, vn = k_quantize(v, Rv, bv, vb, cdt, cdt)
+            k_pack_dl(kq.reshape(S, 1, -1), t_cap, pos, 0, cache=ref[0], d=d)
+            k_pack_dl(vq.reshape(S, 1, -1), t_cap, pos, 1, cache=ref[2], vbits=vb, d=d)
+            ref[1][:, pos] = torch.from_numpy(kn).to(DEV).to(ndt)
+            ref[3][:, pos] = torch.from_numpy(vn).to(DEV).to(ndt)
+        sync()
+        for name, a, b in zip(("kpairs", "knorms", "vtiles", "vnorms"), fused, ref):
+            ai = a.view(torch.uint8) if a.dtype == torch.uint8 else a.view(torch.int16 if a.element_size() == 2 else torch.int32)
+            bi = b.view(torch.uint8) if b.dtype == torch.uint8 else b.view(torch.int16 if b.element_size() == 2 else torch.int32)
+            assert torch.equal(ai, bi), (name, ndt)
+        # untouched positions keep their bytes
+        keep = [t for t in range(t_cap) if t not in (0, 1, 62, 63, 64, 65, 127, 128, 191)]
+        assert torch.equal(fused[0][:, keep], kp0[:, keep])
+
+
+def test_cache_append_dl_refusals():
+    k = torch.zeros(4, 64, dtype=torch.float32, device=DEV)
+    buf = torch.zeros(4096, dtype=torch.uint8, device=DEV)
+    R = T(O.dense_qr_rotation(64, 42))
+    bk, _ = O.lloyd_max_codebook(4, 64)
+    args = lambda dt, d, vb, t_cap, pos: (capi.p(k), capi.p(k), dt, capi.i64(4), capi.i32(d), capi.p(R), capi.p(T(bk)),
+                                          capi.p(R), capi.p(T(bk)), capi.i32(vb), capi.p(buf), capi.p(buf),
+                                          capi.p(buf), capi.p(buf), capi.TQ_F32, capi.i64(t_cap), capi.i64(pos),
+                                          capi.stream())
+    for bad in ((capi.TQ_F32, 64, 2, 64, 0), (capi.TQ_BF16, 96, 2, 64, 0), (capi.TQ_BF16, 64, 5, 64, 0),
+                (capi.TQ_BF16, 64, 2, 60, 0), (capi.TQ_BF16, 64, 2, 64, 64)):
+        assert L().tq_cache_append_dl(*args(*bad)) != 0, bad
+
+
 def test_decode_layout_pack_roundtrip():
     # Appends in uneven pieces (partial value blocks are merged with their earlier tokens);
     # the layout bytes are checked against an independent numpy packing of the codes and

@@ -1142,6 +1142,29 @@ void cache_append_dl(const at::Tensor& key, const at::Tensor& value, at::Tensor&
               "kn / vn must be [B, H, t_cap], float32 or the key's dtype");
   TORCH_CHECK(pos >= 0 && pos + n <= kn.size(2), "tokens past the cache's capacity");
   if (B * H * n == 0) return;
+  const auto kdt = key.scalar_type();
+  if (n == 1 && kbits == 4 && vbits >= 2 && vbits <= 4 && (d == 64 || d == 128) &&
+      (kdt == at::kBFloat16 || kdt == at::kHalf) && value.scalar_type() == kdt &&
+      kn.is_contiguous() && vn.is_contiguous()) {
+    // one token per stream (a decode step): quantized and stored in one launch
+    auto k1 = key.to(dev).reshape({B * H, d}).contiguous();
+    auto v1 = value.to(dev).reshape({B * H, d}).contiguous();
+    auto Rk = f32c(krotation, dev), Rv = f32c(vrotation, dev);
+    auto bk = f32c(kboundaries, dev), bv = f32c(vboundaries, dev);
+    TORCH_CHECK(Rk.dim() == 2 && Rk.size(0) == d && Rk.size(1) == d && Rv.sizes() == Rk.sizes(),
+                "rotations must be [d, d]");
+    TORCH_CHECK(bk.numel() == 15 && bv.numel() == (1 << vbits) - 1,
+                "boundaries length must be 2^bit_width - 1");
+    TORCH_CHECK(kp.size(3) == d / 2 && vp.size(3) == 8 * vbits * d, "cache width mismatch");
+    const int64_t t_cap = kp.size(2);
+    TORCH_CHECK(vp.size(2) * 64 == t_cap && kn.size(2) == t_cap, "cache capacities differ");
+    check_rc(tq_cache_append_dl(k1.data_ptr(), v1.data_ptr(), to_tq(kdt), B * H, (int32_t)d,
+                                Rk.data_ptr<float>(), bk.data_ptr<float>(), Rv.data_ptr<float>(),
+                                bv.data_ptr<float>(), (int32_t)vbits, kp.data_ptr<uint8_t>(),
+                                kn.data_ptr(), vp.data_ptr<uint8_t>(), vn.data_ptr(),
+                                to_tq(kn.scalar_type()), t_cap, pos, cur_stream(k1)));
+    return;
+  }
   for (int values = 0; values < 2; ++values) {
     const at::Tensor& t = values ? value : key;
     at::Tensor& cache = values ? vp : kp;

@@ -1528,6 +1528,154 @@ __global__ void dl_pack_kernel(const uint8_t* __restrict__ packed, int64_t n_str
   }
 }
 
+// One new token per stream quantized and written straight into the decode layout (key
+// pair bytes, the token's bits of its value tile, both norms): a decode step's cache
+// append in one launch instead of a quantize and a layout pass for each of K and V.
+// Arithmetic of quantize_rows_kernel (bf16 / fp16 inputs, rounded in that type), so codes
+// and norms equal tq_rotate_and_quantize followed by tq_pack_decode_layout bit for bit.
+// One wave per (stream, K or V) row; R_k and R_v, rounded and transposed, in LDS.  A
+// stream's token is the only writer of its bits in this launch: every value-tile byte is
+// read, merged and written by one lane (3-bit tiles: the lane of dims 16 i + c also
+// places dim 48 + c's bits that share its bytes).
+struct AppendArgs {
+  const void* key;    // [n_streams][D]
+  const void* value;  // [n_streams][D]
+  int in_dt;          // TQ_BF16 or TQ_F16 (also the rounding type)
+  int64_t n_streams;
+  const float* krot;  // [D][D]
+  const float* kbnd;  // 15
+  const float* vrot;
+  const float* vbnd;  // 2^VB - 1
+  uint8_t* kpairs;    // [n_streams][t_cap][D / 2]
+  void* knorms;       // [n_streams][t_cap], norm_dt
+  uint8_t* vtiles;    // [n_streams][t_cap / 64][512 VB (D / 64)]
+  void* vnorms;
+  int norm_dt;
+  int64_t t_cap, pos;
+};
+
+constexpr int kApThreads = 256;
+
+template <int D, int VB>
+__global__ __launch_bounds__(kApThreads) void dl_append_kernel(AppendArgs a) {
+  constexpr int C = D / 64;  // dims per lane (lane + 64 c: half c of the head)
+  __shared__ float rk_s[D][D + 1];
+  __shared__ float rv_s[D][D + 1];
+  __shared__ float u_s[kApThreads / 64][D];
+  __shared__ float bk_s[16], bv_s[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rdt = a.in_dt;
+  if (threadIdx.x < 15) bk_s[threadIdx.x] = round_to(a.kbnd[threadIdx.x], rdt);
+  if (threadIdx.x < (1 << VB) - 1) bv_s[threadIdx.x] = round_to(a.vbnd[threadIdx.x], rdt);
+  for (int e = threadIdx.x; e < D * D; e += kApThreads) {  // coalesced reads of R rows
+    const int j = e / D, k = e - j * D;
+    rk_s[k][j] = round_to(a.krot[e], rdt);
+    rv_s[k][j] = round_to(a.vrot[e], rdt);
+  }
+  __syncthreads();
+  const float eps = round_to(1e-10f, rdt);
+  const int64_t tile = a.pos >> 6;
+  const int tt = (int)(a.pos & 63);  // the token within its tile
+  for (int64_t row = (int64_t)blockIdx.x * (kApThreads / 64) + wave; row < 2 * a.n_streams;
+       row += (int64_t)gridDim.x * (kApThreads / 64)) {
+    const bool val = row >= a.n_streams;  // uniform
+    const int64_t s = val ? row - a.n_streams : row;
+    float x[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) x[c] = load_as_f32(val ? a.value : a.key, s * D + lane + 64 * c, a.in_dt);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) ss = fmaf(x[c], x[c], ss);
+    ss = wave_sum(ss);
+    const float nrm = round_to(sqrtf(ss), rdt);
+    const float den = fmaxf(nrm, eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) u_s[wave][lane + 64 * c] = round_to(x[c] / den, rdt);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float acc[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[c] = 0.f;
+    if (!val) {
+#pragma unroll 8
+      for (int k = 0; k < D; ++k) {
+        const float uk = u_s[wave][k];
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[c] = fmaf(uk, rk_s[k][lane + 64 * c], acc[c]);
+      }
+    } else {
+#pragma unroll 8
+      for (int k = 0; k < D; ++k) {
+        const float uk = u_s[wave][k];
+#pragma unroll
+        for (int c = 0; c < C; ++c) acc[c] = fmaf(uk, rv_s[k][lane + 64 * c], acc[c]);
+      }
+    }
+    uint32_t code[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      code[c] = (uint32_t)count_below(val ? bv_s : bk_s, val ? 1 << VB : 16, round_to(acc[c], rdt));
+    const int64_t slot = s * a.t_cap + a.pos;
+    if (lane == 0) store_from_f32(val ? a.vnorms : a.knorms, slot, nrm, a.norm_dt);
+    if (!val) {
+      // key pair bytes: byte p of half c = code[2p] << 4 | code[2p + 1]
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const uint32_t nx = (uint32_t)__shfl_down((int)code[c], 1);
+        if ((lane & 1) == 0) a.kpairs[slot * (D / 2) + 32 * c + (lane >> 1)] = (uint8_t)((code[c] << 4) | nx);
+      }
+    } else {
+      // value tile layout (above dl_pack_kernel / vt_bit_source): token tt's codes
+      const int sl = (tt >> 2) & 3, m = tt >> 4;
+      uint8_t* tb = a.vtiles + (s * (a.t_cap >> 6) + tile) * (int64_t)(512 * VB * C);
+      uint32_t code48[C];
+#pragma unroll
+      for (int c = 0; c < C; ++c) code48[c] = (uint32_t)__shfl((int)code[c], 48 + (lane & 15));
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        uint8_t* hb = tb + c * (512 * VB);  // half c (dims 64 c ..)
+        const int j = lane, cc = j & 15;
+        const int L = 16 * sl + cc;
+        int off;
+        uint32_t mask, bits;
+        if constexpr (VB == 2) {
+          const int t2 = tt & 3;
+          off = 16 * L + 4 * m + (j >> 4);
+          mask = 3u << (2 * t2);
+          bits = code[c] << (2 * t2);
+        } else {
+          const int e = tt & 1, k = 2 * (m & 1) + ((tt >> 1) & 1), G = m >> 1;
+          if constexpr (VB == 4) {
+            off = vt_byte_off(4, L, 4 * G + (j >> 4), k);
+            mask = 15u << (4 * e);
+            bits = code[c] << (4 * e);
+          } else {
+            // dims 16 i + c (i < 3): bits 3e .. 3e + 2 of word 3G + i; the same byte's bits
+            // 6 and 7 hold bits q - 3e of dim 48 + c's code, q = 2i, 2i + 1
+            const int i = j >> 4;
+            off = vt_byte_off(3, L, 3 * G + (i < 3 ? i : 0), k);
+            mask = 7u << (3 * e);
+            bits = code[c] << (3 * e);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int cb = 2 * i + h - 3 * e;
+              if (cb >= 0 && cb < 3) {
+                mask |= 1u << (6 + h);
+                bits |= ((code48[c] >> cb) & 1u) << (6 + h);
+              }
+            }
+          }
+        }
+        if (VB != 3 || j < 48) hb[off] = (uint8_t)((hb[off] & ~mask) | bits);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // u_s is rewritten by the next row
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
 // Decode layout -> bit-plane rows of tokens [t0, t0 + n): one thread per output byte.
 __global__ void dl_unpack_kernel(const uint8_t* __restrict__ cache, int64_t n_streams,
                                  int64_t t_cap, int64_t t0, int64_t n, int d, int bits, int values,
@@ -2057,6 +2205,40 @@ int tq_pack_decode_layout(const uint8_t* packed, int64_t n_streams, int64_t n, i
   hipLaunchKernelGGL(dl_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), packed,
                      n_streams, n, d, bit_width, values, cache, t_cap, pos);
   TQ_LAUNCH_CHECK("dl_pack_kernel");
+  return TQ_OK;
+}
+
+int tq_cache_append_dl(const void* key, const void* value, tq_dtype in_dtype, int64_t n_streams,
+                       int32_t d, const float* krotation, const float* kboundaries,
+                       const float* vrotation, const float* vboundaries, int32_t vbits,
+                       uint8_t* kpairs, void* knorms, uint8_t* vtiles, void* vnorms,
+                       tq_dtype norm_dtype, int64_t t_cap, int64_t pos, void* stream) {
+  TQ_REQUIRE(in_dtype == TQ_BF16 || in_dtype == TQ_F16, "keys and values must be bf16 or fp16");
+  TQ_REQUIRE(d == 64 || d == 128, "dim must be 64 or 128, got %d", d);
+  TQ_REQUIRE(vbits >= 2 && vbits <= 4, "value bits must be 2-4, got %d", vbits);
+  TQ_REQUIRE(norm_dtype == TQ_F32 || norm_dtype == TQ_BF16 || norm_dtype == TQ_F16, "unknown norm dtype");
+  TQ_REQUIRE(n_streams >= 0 && t_cap >= 0 && t_cap % 64 == 0 && pos >= 0 && pos < t_cap,
+             "bad position or capacity");
+  if (n_streams == 0) return TQ_OK;
+  TQ_REQUIRE(key && value && krotation && kboundaries && vrotation && vboundaries && kpairs &&
+                 knorms && vtiles && vnorms,
+             "null pointer argument");
+  AppendArgs a{key, value, (int)in_dtype, n_streams, krotation, kboundaries, vrotation, vboundaries,
+               kpairs, knorms, vtiles, vnorms, (int)norm_dtype, t_cap, pos};
+  const int64_t want = (2 * n_streams + kApThreads / 64 - 1) / (kApThreads / 64);
+  const int64_t cap = (int64_t)device_cu_count() * (d == 64 ? 4 : 1);  // LDS: 33 / 132 KB of R
+  const dim3 grid((unsigned)std::min(want, cap));
+  hipStream_t st = as_stream(stream);
+  if (d == 64) {
+    if (vbits == 2) hipLaunchKernelGGL((dl_append_kernel<64, 2>), grid, dim3(kApThreads), 0, st, a);
+    else if (vbits == 3) hipLaunchKernelGGL((dl_append_kernel<64, 3>), grid, dim3(kApThreads), 0, st, a);
+    else hipLaunchKernelGGL((dl_append_kernel<64, 4>), grid, dim3(kApThreads), 0, st, a);
+  } else {
+    if (vbits == 2) hipLaunchKernelGGL((dl_append_kernel<128, 2>), grid, dim3(kApThreads), 0, st, a);
+    else if (vbits == 3) hipLaunchKernelGGL((dl_append_kernel<128, 3>), grid, dim3(kApThreads), 0, st, a);
+    else hipLaunchKernelGGL((dl_append_kernel<128, 4>), grid, dim3(kApThreads), 0, st, a);
+  }
+  TQ_LAUNCH_CHECK("dl_append_kernel");
   return TQ_OK;
 }
 
