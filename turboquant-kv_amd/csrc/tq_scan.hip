@@ -2196,20 +2196,24 @@ pair_filter_kernel(FilterArgs a) {
   const uint32_t ngroups = (n + 63) / 64;
   const int nsteps = gw < ngroups ? (int)((ngroups - 1 - gw) / W + 1) : 0;
 
-  // ---- query, centroids and this thread's rotation row first, so that waiting for them
-  // does not wait for the row prefetch behind them
+  // ---- query, centroids and the rotation first, so that waiting for them does not wait
+  // for the row prefetch behind them
   // (the query as a raw dword through a bounded buffer: no dtype branch, so no wait, here)
   float cload = 0.f;
-  float4 rrow[D / 4];
   const int esz = a.q_dt == TQ_F32 ? 4 : 2;
   const __amdgpu_buffer_rsrc_t qrs =
       buf_rsrc(static_cast<const char*>(a.q) + (size_t)q * D * esz, (uint32_t)(D * esz));
   const uint32_t qraw = __builtin_amdgcn_raw_buffer_load_b32(qrs, (tid * esz) & ~3, 0, 0);
-  if (tid < D) {
-    const float4* r4 = reinterpret_cast<const float4*>(a.rot + (size_t)tid * D);
+  // R read coalesced (load i: float4 i * kFsThreads + tid), staged in the table's LDS
+  // before the table is built: row r, float4 column c at slot (D/4) r + ((c + r) mod (D/4)),
+  // so the rotation's thread r reads its row with 16 lanes per pass on distinct banks
+  // (row-per-thread global reads touched 64 cache lines per load instruction)
+  constexpr int RC = D / 4;                     // float4 per row
+  constexpr int RV = D * RC / kFsThreads;       // float4 per thread
+  static_assert(D * D * 4 <= kHtabBytes, "R fits in the table's LDS");
+  fs_v4f rv[RV];
 #pragma unroll
-    for (int i = 0; i < D / 4; ++i) rrow[i] = r4[i];
-  }
+  for (int i = 0; i < RV; ++i) rv[i] = reinterpret_cast<const fs_v4f*>(a.rot)[i * kFsThreads + tid];
   if (tid < 16) cload = a.cen[tid];
 
   // Rows of step t: the 64-row group t * W + gw (grid stride: all waves sweep memory
@@ -2269,18 +2273,29 @@ pair_filter_kernel(FilterArgs a) {
   }
   if (tid < 16) cen_s[tid] = cload;
   if (tid < kFsWaves) th_s[tid] = -INFINITY;
+  {
+    fs_v4f* rs_l = reinterpret_cast<fs_v4f*>(htab);
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+      const int f = i * kFsThreads + tid, r = f / RC, c = f % RC;
+      rs_l[RC * r + ((c + r) & (RC - 1))] = rv[i];
+    }
+  }
   __syncthreads();
   float qv = 0.f;
   if (tid < D) {
+    const fs_v4f* rs_l = reinterpret_cast<const fs_v4f*>(htab);
 #pragma unroll
     for (int i = 0; i < D / 4; ++i) {
-      qv = qv + qs_s[4 * i] * rrow[i].x;
-      qv = qv + qs_s[4 * i + 1] * rrow[i].y;
-      qv = qv + qs_s[4 * i + 2] * rrow[i].z;
-      qv = qv + qs_s[4 * i + 3] * rrow[i].w;
+      const fs_v4f r = rs_l[RC * tid + ((i + tid) & (RC - 1))];
+      qv = qv + qs_s[4 * i] * r.x;
+      qv = qv + qs_s[4 * i + 1] * r.y;
+      qv = qv + qs_s[4 * i + 2] * r.z;
+      qv = qv + qs_s[4 * i + 3] * r.w;
     }
     qr_s[tid] = qv;
   }
+  __syncthreads();  // R read: the table takes its LDS
   for (int e = tid; e < 256 * 16; e += kFsThreads) {  // entry b, copies 4c..4c+3
     const int b = e >> 4, c = e & 15;
     typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
