@@ -1494,6 +1494,60 @@ def test_decode_layout_vbits_and_groups_vs_f64(vb, G):
         assert np.max(np.abs(lse[ok] - want_lse[ok]) / np.maximum(1.0, np.abs(want_lse[ok]))) <= lse_tol
 
 
+@pytest.mark.parametrize("vb", [2, 3, 4])
+@pytest.mark.parametrize("case", ["516x4", "515x8"])
+def test_decode_layout_two_streams_per_workgroup_vs_f64(vb, case):
+    # At least two streams per CU (B * hkv >= 512 on the 256-CU MI355X) the kernel runs two
+    # streams per workgroup, four waves each: 516 streams (G = 4) and an odd 515 (G = 8:
+    # two launches of four heads; the last workgroup's second stream does not exist), with
+    # ragged and empty sequences, window starts, fp32 and bf16 norms, fp32 / bf16 queries.
+    rs = np.random.RandomState(900 + vb + (0 if case == "516x4" else 50))
+    d = 64
+    if case == "516x4":
+        B, Hkv, G, Tc = 129, 4, 4, 192
+    else:
+        B, Hkv, G, Tc = 515, 1, 8, 128
+    Hq = Hkv * G
+    seq = rs.randint(0, Tc + 1, size=B)
+    seq[:6] = [0, 1, 63, 64, 65, Tc]
+    starts = np.minimum(rs.randint(0, 40, size=B), seq)
+    starts[:6] = 0
+    Rk, Rv = O.dense_qr_rotation(d, 42), O.dense_qr_rotation(d, 43)
+    bk, ck = O.lloyd_max_codebook(4, d)
+    bv, cv = O.lloyd_max_codebook(vb, d)
+    n = B * Hkv * Tc
+    K = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    V = rs.randn(n, d).astype(np.float32) * rs.uniform(0.2, 3.0, (n, 1)).astype(np.float32)
+    kp, kn, _ = O.quantize_mse(K, 4, Rk, bk)
+    vp, vn, _ = O.quantize_mse(V, vb, Rv, bv)
+    kc = k_pack_dl(kp.reshape(B * Hkv, Tc, -1), Tc, 0, 0)
+    vc = k_pack_dl(vp.reshape(B * Hkv, Tc, -1), Tc, 0, 1, vbits=vb)
+    kp, vp = kp.reshape(B, Hkv, Tc, -1), vp.reshape(B, Hkv, Tc, -1)
+    kn, vn = kn.reshape(B, Hkv, Tc), vn.reshape(B, Hkv, Tc)
+    q = (rs.randn(B, Hq, d) * 3.0).astype(np.float32)
+    for dt, tol, nd in ((torch.float32, 1e-4, None), (torch.bfloat16, 1e-2, torch.bfloat16)):
+        qt = torch.from_numpy(q).to(DEV).to(dt)
+        qf = qt.float().cpu().numpy()
+        knr = T(kn, nd).float().cpu().numpy() if nd is not None else kn
+        vnr = T(vn, nd).float().cpu().numpy() if nd is not None else vn
+        for st in (None, starts):
+            got, lse = k_decode_dl(qt, kc, kn, vc, vn, seq, ck, cv, Rk, Rv, 0.125, vbits=vb,
+                                   seq_starts=st, norm_dtype=nd)
+            lo = np.zeros(B, np.int64) if st is None else st
+            for bi in range(B):
+                if seq[bi] - lo[bi] <= 0:
+                    assert np.all(got[bi] == 0) and np.isneginf(lse[bi]).all(), (dt, bi)
+                    continue
+                rows = slice(int(lo[bi]), int(seq[bi]))
+                want, want_lse = O.decode_attention_f64(
+                    qf[bi:bi + 1], kp[bi:bi + 1, :, rows], knr[bi:bi + 1, :, rows], vp[bi:bi + 1, :, rows],
+                    vnr[bi:bi + 1, :, rows], [seq[bi] - lo[bi]], ck, cv, Rk, Rv, 4, vb, 0.125, return_lse=True)
+                err = np.max(np.abs(got[bi] - want[0])) / np.max(np.abs(want[0]))
+                assert err <= tol, (dt, case, bi, err)
+                lse_tol = 1e-2 if dt == torch.bfloat16 else 1e-5
+                assert np.max(np.abs(lse[bi] - want_lse[0]) / np.maximum(1.0, np.abs(want_lse[0]))) <= lse_tol
+
+
 @pytest.mark.parametrize("vb", [2, 3])
 def test_decode_layout_window_vs_f64(vb):
     # Windows [start, len) of each sequence (left-padded batches): tokens before start are

@@ -536,6 +536,7 @@ struct DlArgs {
   int bs_log2;
   uint32_t pool_rows;  // num_blocks * hkv * bs
   uint32_t num_blocks;  // wide pools (PG 3, 4): block ids are clamped below it
+  int nstreams;         // B * hkv (two streams per workgroup: the last one may be missing)
 };
 
 __device__ __forceinline__ uint32_t byte_addr(uint32_t base_copy, uint32_t w, int byte) {
@@ -617,11 +618,13 @@ __device__ __forceinline__ float pow2_scale(float amax) {
 // 64-dim tiles, half h (dims 64 h ..) at byte h * 512 VB.  Each half runs the 64-dim
 // operand layouts below; q.K chains both halves' products into one score, p.V keeps one
 // accumulator set per half.
-template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0, int NH = 1>
+template <bool EXACT_V, bool PREC_K, int PG = 0, int VB = 2, int ND = 0, int NH = 1, int SPW = 1>
 __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   constexpr bool PAGED = PG != 0, SUB16 = PG == 2 || PG == 4, WIDE = PG >= 3;
   constexpr int D = 64 * NH;  // head_dim
+  constexpr int WPS = kDlWaves / SPW;  // waves per stream
   static_assert(VB >= 2 && VB <= 4, "value width");
+  static_assert(SPW == 1 || (SPW == 2 && NH == 1 && PG == 0), "two streams: contiguous head_dim 64");
   static_assert(ND == 0 || PG == 0, "16-bit norms: contiguous caches");
   static_assert(NH == 1 || (NH == 2 && PG == 0), "head_dim 128: contiguous caches");
   // value words per lane and tile as loaded (16-token sub-blocks of 3-bit values: the four
@@ -635,12 +638,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // fp16 hi parts (c[high nibble], c[low nibble]) * ks, and 32 of the lo parts (layout
   // at kDlKLo).  After the tile loop the bytes hold the reduction.
   __shared__ __attribute__((aligned(16))) char tabs[kDlTabs];
-  __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4][2][D];  // q * qs2: hi, lo
-  __shared__ float qs_s[4][D];
+  __shared__ __attribute__((aligned(16))) _Float16 qhl_s[4 * SPW][2][D];  // q * qs2: hi, lo
+  __shared__ float qs_s[4 * SPW][D];
   __shared__ float hmax_s[NH == 2 ? kDlWaves : 1];  // head_dim 128: per-wave |q_rot| maxima
   __shared__ float cen_s[32];  // 16 key centroids, then the value centroids
   __shared__ __attribute__((aligned(16))) float rv_s[NH == 1 ? kDim * kDim : 1];  // R_v (one split)
-  __shared__ float qs2_s[4];  // per-head query scales
+  __shared__ float qs2_s[4 * SPW];  // per-head query scales
   __shared__ float red_m[kDlWaves][4];
   __shared__ float red_l[kDlWaves][4];
   __shared__ u32x2 kst_s[256];  // K table entries (hi, lo words) before replication
@@ -658,20 +661,25 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     const uint32_t N = gridDim.x;
     if ((N & 7u) == 0) W = (W & 7u) * (N >> 3) + (W >> 3);
   }
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  // SPW 2: waves 0-3 take stream 2W, waves 4-7 stream 2W + 1 (one split; the last
+  // workgroup's second stream may not exist: then its waves take no tiles and write nothing)
+  const int sw = SPW == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / WPS);
   const int split = (int)(W % (uint32_t)a.nsplit);
-  const int bg = (int)(W / (uint32_t)a.nsplit);
+  const int bg0 = (int)(W / (uint32_t)a.nsplit) * SPW + sw;
+  const bool live = SPW == 1 || bg0 < a.nstreams;
+  const int bg = live ? bg0 : 0;
   const int b = bg / a.hkv;
   const int g = bg - b * a.hkv;
   // The sequence length is requested first, and nothing below is addressed through it
   // until the prologue's loads (query, R_k, the first tiles) are all in flight: their
   // latency and its own then overlap instead of following one another.
-  const int32_t slen = a.seq_lens[b];
+  const int32_t slen = live ? a.seq_lens[b] : 0;
   const int32_t sstart = a.seq_starts ? a.seq_starts[b] : 0;
   const int64_t t_begin = (int64_t)split * a.split_tokens;
   const int64_t qh0 = (int64_t)b * a.hq + (int64_t)g * a.Gfull + a.hofs;
-  const int tid = threadIdx.x;
 
-  const int wave = tid >> 6, lane = tid & 63;
   // Lane roles (see the score layout and the tile loads below).
   const int sl = lane >> 4, col = lane & 15;
   const int hh = lane & 3, gq = (lane >> 2) & 3;
@@ -847,8 +855,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     x.vn[2] = __uint_as_float(vn4.z); x.vn[3] = __uint_as_float(vn4.w);
   };
 
-  constexpr int kStep = kDlWaves * 64;
-  const int tf = (int)t_begin + wave * 64;
+  constexpr int kStep = WPS * 64;
+  const int tf = (int)t_begin + (wave % WPS) * 64;
   Tile ta, tb, tc;
 
   // ---- prologue.  Every global read is issued up front, in the order its data is needed
@@ -864,12 +872,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // the query element as the aligned 32-bit word that holds it (one load whatever the
   // dtype, converted after the tables: a dtype branch here made the compiler wait for it
   // before issuing the loads below)
-  // thread tid < 4 D: head qh = tid / D, dim qj = tid % D
+  // thread tid < 4 SPW D: head qh = tid / D (head qh % 4 of the thread's stream), dim
+  // qj = tid % D
   const int qh = tid / D, qj = tid % D;
-  const int64_t qe = (qh0 + (qh < a.G ? qh : 0)) * D + qj;
+  const int64_t qe = (qh0 + ((qh & 3) < a.G ? (qh & 3) : 0)) * D + qj;
   const int64_t qbyte = qe * (a.q_dt == TQ_F32 ? 4 : 2);
   uint32_t qraw = 0;
-  if (tid < 4 * D)
+  if (tid < 4 * SPW * D)
     qraw = *reinterpret_cast<const uint32_t*>(static_cast<const char*>(a.q) + (qbyte & ~int64_t(3)));
   // Head_dim 64: R_k and (one split per stream, for the epilogue) R_v, read coalesced:
   // thread tid holds floats 8 tid .. 8 tid + 7 of each (row tid / 8, float4 columns
@@ -893,7 +902,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // ---- the split's token range, now that the sequence length has had its latency
   const int64_t T = min((int64_t)max(slen, 0), a.t_cap);
   const int64_t t_end = min(T, t_begin + a.split_tokens);
-  if (t_begin >= t_end) {  // uniform
+  // (SPW 2: one split; an empty stream's waves take no tiles and its epilogue writes zeros
+  // and lse -inf)
+  if (SPW == 1 && t_begin >= t_end) {  // uniform
     if (a.out != nullptr && T == 0 && tid < a.G * D) {  // empty sequence: zeros, lse -inf
       store_from_f32(a.out, qh0 * D + tid, 0.f, a.q_dt);
       if (a.lse && qj == 0) a.lse[qh0 + qh] = -INFINITY;
@@ -904,12 +915,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   const int ts = (int)min((int64_t)max(sstart, 0), T);  // first unmasked token
   const int ntiles = __builtin_amdgcn_readfirstlane(tf < te ? (te - tf + kStep - 1) / kStep : 0);
   if (tid < 32) cen_s[tid] = cenv;
-  if (tid < 4 * D) {
+  if (tid < 4 * SPW * D) {
     const uint32_t bits = a.q_dt == TQ_F32 ? qraw : (qraw >> (8 * (qbyte & 2))) & 0xFFFFu;
     const float qv = a.q_dt == TQ_F32 ? __uint_as_float(bits)
                      : a.q_dt == TQ_BF16 ? __uint_as_float(bits << 16)
                                          : __half2float(__ushort_as_half((unsigned short)bits));
-    qs_s[qh][qj] = qh < a.G ? qv : 0.f;
+    qs_s[qh][qj] = (qh & 3) < a.G ? qv : 0.f;
   }
   if constexpr (NH == 1) {
     // R_k row r, float4 column c at slot 16 r + ((c + r) & 15): the rotation's lane r then
@@ -986,7 +997,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     qhl_s[h][0][j] = xh;
     qhl_s[h][1][j] = (_Float16)(x - (float)xh);
     if (j == 0) qs2_s[h] = s2;
-  } else if (tid < 4 * kDim) {  // waves 0-3: head h = wave, dim j = lane (row j of R_k)
+  } else if (tid < 4 * SPW * kDim) {  // waves 0-3 (SPW 2: 0-7): head h = wave, dim j = lane (row j of R_k)
     const int h = tid >> 6, j = tid & 63;
     const v4f* rk = reinterpret_cast<const v4f*>(rv_s);
     float v = 0.f;
@@ -1055,12 +1066,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     const int d0 = 64 * h + 16 * sl + 8 * c;
     const v8h z = vz;
     if constexpr (PREC_K) {
-      const v8h hi = col < 4 ? *reinterpret_cast<const v8h*>(&qhl_s[col][0][d0]) : z;
-      const v8h lo = (col >= 4 && col < 8) ? *reinterpret_cast<const v8h*>(&qhl_s[col - 4][1][d0]) : z;
+      const v8h hi = col < 4 ? *reinterpret_cast<const v8h*>(&qhl_s[4 * sw + col][0][d0]) : z;
+      const v8h lo = (col >= 4 && col < 8) ? *reinterpret_cast<const v8h*>(&qhl_s[4 * sw + col - 4][1][d0]) : z;
       bq[h][c] = col < 4 ? hi : lo;
       bqh[h][c] = hi;
     } else {
-      const v8h hi = *reinterpret_cast<const v8h*>(&qhl_s[col & 3][0][d0]);
+      const v8h hi = *reinterpret_cast<const v8h*>(&qhl_s[4 * sw + (col & 3)][0][d0]);
       bhi[h][c] = hi;
       if constexpr (NH == 1) {
 #pragma unroll
@@ -1074,7 +1085,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   };
   // Score layout after q.K: lane 16 sl + 4 g + h holds tokens 16 g + 4 sl + r (register r)
   // of head h; g = token group of the 16x16x32 MFMA whose rows hold them.
-  const float kinv = 1.f / (ksc * qs2_s[hh]);  // a power of two: exact
+  const float kinv = 1.f / (ksc * qs2_s[4 * sw + hh]);  // a power of two: exact
   // byte 0: copy offset; byte 2 of kcopy: the K table's 64 KB base
   const uint32_t kcopy = (uint32_t)kDlTab | (128u + (uint32_t)(lane & 31) * 4);
   const uint32_t vcopy = VB != 2 ? (uint32_t)(lane & 31) * 4
@@ -1355,11 +1366,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   }
   __syncthreads();  // also: every wave is done with the tables
   float mx[4], fw[4];
+  const int w0 = WPS * sw;  // the stream's first wave
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    float v = red_m[0][m];
+    float v = red_m[w0][m];
 #pragma unroll
-    for (int w = 1; w < kDlWaves; ++w) v = fmaxf(v, red_m[w][m]);
+    for (int w = 1; w < WPS; ++w) v = fmaxf(v, red_m[w0 + w][m]);
     mx[m] = v;
     const float mw = red_m[wave][m];
     fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]);
@@ -1374,12 +1386,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       for (int m = 0; m < 4; ++m) red[(wave * 4 + m) * D + 64 * h + 16 * dg + lane] = acc[h][dg][m] * fw[m];
   }
   __syncthreads();
-  if (tid < 4 * D) {
-    const int m = tid / D, dim = tid % D;
+  // thread tid < 4 SPW D: head m of its own wave's stream (tid / (4 D) = sw)
+  if (tid < 4 * SPW * D) {
+    const int m = (tid / D) & 3, dim = tid % D;
     float sum = 0.f;
-    for (int w = 0; w < kDlWaves; ++w) sum += red[(w * 4 + m) * D + dim];
+    for (int w = w0; w < w0 + WPS; ++w) sum += red[(w * 4 + m) * D + dim];
     float L = 0.f;
-    for (int w = 0; w < kDlWaves; ++w)
+    for (int w = w0; w < w0 + WPS; ++w)
       if (red_m[w][m] != -INFINITY) L += red_l[w][m] * __builtin_amdgcn_exp2f(red_m[w][m] - mx[m]);
     if (a.out == nullptr) {  // several splits: partials for the combine kernel
       if (m < a.G) {
@@ -1387,23 +1400,23 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
         if (dim == 0) a.stats[(qh0 + m) * a.nsplit + split] = make_float2(mx[m], L);
       }
     } else {  // the whole sequence: out = (o / L) @ R_v here
-      qs_s[m][dim] = L > 0.f ? sum / (vsc * L) : 0.f;
+      qs_s[4 * sw + m][dim] = L > 0.f ? sum / (vsc * L) : 0.f;
     }
-    if (a.out != nullptr && m < a.G && dim == 0 && a.lse)
+    if (live && a.out != nullptr && m < a.G && dim == 0 && a.lse)
       a.lse[qh0 + m] = L > 0.f ? (mx[m] + log2f(L)) * 0.69314718055994531f : -INFINITY;
   }
   if (a.out != nullptr) {
     __syncthreads();
-    if (tid < 4 * D) {
-      const int m = tid / D, dim = tid % D;
-      if (m < a.G) {
+    if (tid < 4 * SPW * D) {
+      const int m = (tid / D) & 3, dim = tid % D;
+      if (live && m < a.G) {
         float r = 0.f;
         if constexpr (NH == 1) {
 #pragma unroll
-          for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[m][k], rv_s[k * kDim + dim], r);
+          for (int k = 0; k < kDim; ++k) r = fmaf(qs_s[4 * sw + m][k], rv_s[k * kDim + dim], r);
         } else {
 #pragma unroll 8
-          for (int k = 0; k < D; ++k) r = fmaf(qs_s[m][k], a.vrot[k * D + dim], r);
+          for (int k = 0; k < D; ++k) r = fmaf(qs_s[4 * sw + m][k], a.vrot[k * D + dim], r);
         }
         store_from_f32(a.out, (qh0 + m) * D + dim, r, a.q_dt);
       }
@@ -1914,29 +1927,29 @@ SplitPlan plan_dl_splits(int B, int hkv, int64_t t_cap) {
   return {split, (int)((t_cap + split - 1) / split)};
 }
 
-template <int PG, int VB, int ND = 0, int NH = 1>
+template <int PG, int VB, int ND = 0, int NH = 1, int SPW = 1>
 void launch_dl_kernel(tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
   if (q_dtype == TQ_F32)
-    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<true, true, PG, VB, ND, NH, SPW>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else if (q_dtype == TQ_F16)
-    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, true, PG, VB, ND, NH, SPW>), dim3(grid), dim3(kDlThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB, ND, NH>), dim3(grid), dim3(kDlThreads), 0, st, a);
+    hipLaunchKernelGGL((dl_decode_kernel<false, false, PG, VB, ND, NH, SPW>), dim3(grid), dim3(kDlThreads), 0, st, a);
 }
 
-template <int ND, int NH>
+template <int ND, int NH, int SPW>
 void launch_dl_contiguous(int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a, hipStream_t st) {
-  if (vbits == 2) launch_dl_kernel<0, 2, ND, NH>(q_dtype, grid, a, st);
-  else if (vbits == 3) launch_dl_kernel<0, 3, ND, NH>(q_dtype, grid, a, st);
-  else launch_dl_kernel<0, 4, ND, NH>(q_dtype, grid, a, st);
+  if (vbits == 2) launch_dl_kernel<0, 2, ND, NH, SPW>(q_dtype, grid, a, st);
+  else if (vbits == 3) launch_dl_kernel<0, 3, ND, NH, SPW>(q_dtype, grid, a, st);
+  else launch_dl_kernel<0, 4, ND, NH, SPW>(q_dtype, grid, a, st);
 }
 
-template <int NH>
+template <int NH, int SPW = 1>
 void launch_dl_norms(int norm_dt, int vbits, tq_dtype q_dtype, unsigned grid, const DlArgs& a,
                      hipStream_t st) {
-  if (norm_dt == TQ_BF16) launch_dl_contiguous<TQ_BF16, NH>(vbits, q_dtype, grid, a, st);
-  else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16, NH>(vbits, q_dtype, grid, a, st);
-  else launch_dl_contiguous<0, NH>(vbits, q_dtype, grid, a, st);
+  if (norm_dt == TQ_BF16) launch_dl_contiguous<TQ_BF16, NH, SPW>(vbits, q_dtype, grid, a, st);
+  else if (norm_dt == TQ_F16) launch_dl_contiguous<TQ_F16, NH, SPW>(vbits, q_dtype, grid, a, st);
+  else launch_dl_contiguous<0, NH, SPW>(vbits, q_dtype, grid, a, st);
 }
 
 template <int PG>
@@ -1994,13 +2007,22 @@ int run_dl(DlArgs a, tq_dtype q_dtype, int B, int hq, int hkv, int vbits, int pg
     a.split_tokens = p.split_tokens; a.nsplit = p.nsplit; a.part = part; a.stats = stats;
     a.out = single ? out : nullptr; a.lse = single ? lse : nullptr;
     a.Gfull = hq / hkv;
-    const uint64_t grid = (uint64_t)p.nsplit * (uint64_t)B * (uint64_t)hkv;
+    a.nstreams = B * hkv;
+    // At least two streams per CU (one split each): two streams per workgroup, four waves
+    // each, so the tables, R_k and R_v are built once for both and every stream is
+    // resident at once (one workgroup per CU: a second round of workgroups would pay the
+    // prologue again).
+    const bool two = pg == 0 && d == kDim && p.nsplit == 1 &&
+                     (int64_t)B * hkv >= 2 * (int64_t)device_cu_count();
+    const uint64_t grid = two ? ((uint64_t)B * hkv + 1) / 2
+                              : (uint64_t)p.nsplit * (uint64_t)B * (uint64_t)hkv;
     TQ_REQUIRE(grid <= 0xFFFFFFFFull, "too many (stream, split) workgroups");
     for (int h0 = 0; h0 < a.Gfull; h0 += 4) {
       a.hofs = h0;
       a.G = std::min(4, a.Gfull - h0);
       if (pg == 0) {
         if (d == 128) launch_dl_norms<2>(norm_dt, vbits, q_dtype, (unsigned)grid, a, st);
+        else if (two) launch_dl_norms<1, 2>(norm_dt, vbits, q_dtype, (unsigned)grid, a, st);
         else launch_dl_norms<1>(norm_dt, vbits, q_dtype, (unsigned)grid, a, st);
       } else if (pg == 1) {
         launch_dl_paged<1>(vbits, q_dtype, (unsigned)grid, a, st);
