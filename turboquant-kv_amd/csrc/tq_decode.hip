@@ -1580,10 +1580,26 @@ __global__ __launch_bounds__(kApThreads) void dl_append_kernel(AppendArgs a) {
   const int rdt = a.in_dt;
   if (threadIdx.x < 15) bk_s[threadIdx.x] = round_to(a.kbnd[threadIdx.x], rdt);
   if (threadIdx.x < (1 << VB) - 1) bv_s[threadIdx.x] = round_to(a.vbnd[threadIdx.x], rdt);
-  for (int e = threadIdx.x; e < D * D; e += kApThreads) {  // coalesced reads of R rows
-    const int j = e / D, k = e - j * D;
-    rk_s[k][j] = round_to(a.krot[e], rdt);
-    rv_s[k][j] = round_to(a.vrot[e], rdt);
+  // R_k and R_v: float4 f = i * kApThreads + tid (coalesced), four at a time in flight,
+  // stored rounded and transposed (row j = 4 f / D: the 64 lanes' writes hit 64 banks)
+  constexpr int NF = D * D / 4 / kApThreads;  // float4 per thread and matrix
+#pragma unroll
+  for (int c0 = 0; c0 < NF; c0 += 4) {
+    v4f rk4[4], rv4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rk4[i] = reinterpret_cast<const v4f*>(a.krot)[(c0 + i) * kApThreads + threadIdx.x];
+      rv4[i] = reinterpret_cast<const v4f*>(a.vrot)[(c0 + i) * kApThreads + threadIdx.x];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = (c0 + i) * kApThreads + threadIdx.x, j = 4 * f / D, k = 4 * f % D;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        rk_s[k + e][j] = round_to(rk4[i][e], rdt);
+        rv_s[k + e][j] = round_to(rv4[i][e], rdt);
+      }
+    }
   }
   __syncthreads();
   const float eps = round_to(1e-10f, rdt);
@@ -1596,6 +1612,22 @@ __global__ __launch_bounds__(kApThreads) void dl_append_kernel(AppendArgs a) {
     float x[C];
 #pragma unroll
     for (int c = 0; c < C; ++c) x[c] = load_as_f32(val ? a.value : a.key, s * D + lane + 64 * c, a.in_dt);
+    // value rows: this lane's byte of the token's value tile per half (layout above
+    // dl_pack_kernel / vt_bit_source), its old contents requested with the row
+    const int sl = (tt >> 2) & 3, m = tt >> 4, j = lane, cc = j & 15, L = 16 * sl + cc;
+    int off;
+    if constexpr (VB == 2) {
+      off = 16 * L + 4 * m + (j >> 4);
+    } else {
+      const int k = 2 * (m & 1) + ((tt >> 1) & 1), G = m >> 1;
+      off = VB == 4 ? vt_byte_off(4, L, 4 * G + (j >> 4), k)
+                    : vt_byte_off(3, L, 3 * G + ((j >> 4) < 3 ? (j >> 4) : 0), k);
+    }
+    uint8_t* tb = a.vtiles + (s * (a.t_cap >> 6) + tile) * (int64_t)(512 * VB * C);
+    const bool vlane = val && (VB != 3 || j < 48);
+    uint32_t old[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) old[c] = vlane ? tb[c * (512 * VB) + off] : 0u;
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < C; ++c) ss = fmaf(x[c], x[c], ss);
@@ -1639,35 +1671,26 @@ __global__ __launch_bounds__(kApThreads) void dl_append_kernel(AppendArgs a) {
         if ((lane & 1) == 0) a.kpairs[slot * (D / 2) + 32 * c + (lane >> 1)] = (uint8_t)((code[c] << 4) | nx);
       }
     } else {
-      // value tile layout (above dl_pack_kernel / vt_bit_source): token tt's codes
-      const int sl = (tt >> 2) & 3, m = tt >> 4;
-      uint8_t* tb = a.vtiles + (s * (a.t_cap >> 6) + tile) * (int64_t)(512 * VB * C);
+      // token tt's bit fields of the tile bytes
       uint32_t code48[C];
 #pragma unroll
       for (int c = 0; c < C; ++c) code48[c] = (uint32_t)__shfl((int)code[c], 48 + (lane & 15));
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        uint8_t* hb = tb + c * (512 * VB);  // half c (dims 64 c ..)
-        const int j = lane, cc = j & 15;
-        const int L = 16 * sl + cc;
-        int off;
         uint32_t mask, bits;
         if constexpr (VB == 2) {
           const int t2 = tt & 3;
-          off = 16 * L + 4 * m + (j >> 4);
           mask = 3u << (2 * t2);
           bits = code[c] << (2 * t2);
         } else {
-          const int e = tt & 1, k = 2 * (m & 1) + ((tt >> 1) & 1), G = m >> 1;
+          const int e = tt & 1;
           if constexpr (VB == 4) {
-            off = vt_byte_off(4, L, 4 * G + (j >> 4), k);
             mask = 15u << (4 * e);
             bits = code[c] << (4 * e);
           } else {
             // dims 16 i + c (i < 3): bits 3e .. 3e + 2 of word 3G + i; the same byte's bits
             // 6 and 7 hold bits q - 3e of dim 48 + c's code, q = 2i, 2i + 1
             const int i = j >> 4;
-            off = vt_byte_off(3, L, 3 * G + (i < 3 ? i : 0), k);
             mask = 7u << (3 * e);
             bits = code[c] << (3 * e);
 #pragma unroll
@@ -1680,7 +1703,7 @@ __global__ __launch_bounds__(kApThreads) void dl_append_kernel(AppendArgs a) {
             }
           }
         }
-        if (VB != 3 || j < 48) hb[off] = (uint8_t)((hb[off] & ~mask) | bits);
+        if (vlane) tb[c * (512 * VB) + off] = (uint8_t)((old[c] & ~mask) | bits);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
