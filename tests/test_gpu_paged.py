@@ -143,9 +143,16 @@ def test_decode_paged_vs_contiguous_and_f64(d, kb, vb, G, bs, qdt):
     vpool = rs.randint(0, 256, (nb, Hkv, bs, vb * bpp)).astype(np.uint8)
     knp = rs.uniform(0.5, 2.0, (nb, Hkv, bs)).astype(np.float32)
     vnp = rs.uniform(0.5, 2.0, (nb, Hkv, bs)).astype(np.float32)
+    # stale slots past each sequence's end in its last block hold NaN norms: masked
+    # tokens must not reach the output
+    for b, n in enumerate(lens):
+        if n % bs:
+            knp[tab[b, (n - 1) // bs], :, n % bs:] = np.nan
+            vnp[tab[b, (n - 1) // bs], :, n % bs:] = np.nan
     q = torch.from_numpy(rs.randn(B, Hq, d).astype(np.float32)).to(DEV).to(qdt)
     scale = 1.0 / math.sqrt(d)
     got, lse = k_decode_paged(q, kpool, knp, vpool, vnp, tab, lens, ck, cv, Rk, Rv, kb, vb, scale)
+    assert np.all(np.isfinite(got))
     # the same tokens laid out contiguously, through the contiguous decode entry point
     Tm = width * bs
     kc_, kn_, vc_, vn_ = (np.zeros((B, Hkv, Tm) + p.shape[3:], p.dtype) for p in (kpool, knp, vpool, vnp))
@@ -303,10 +310,11 @@ def test_vllm_paged_protected_layer_and_padding():
 
 
 # ------------------------------------------------------------------ decode-layout pools
-def _dl_pools(rs, lens, bs, nb, width, Hkv, vb=2):
+def _dl_pools(rs, lens, bs, nb, width, Hkv, vb=2, vmul=None):
     """Random 4-bit key / vb-bit value bit-plane rows of every token, stored into
     decode-layout block pools through the C ABI (values in two shuffled calls, so tiles are
-    filled piecewise).  Returns the pools and each sequence's contiguous rows and norms."""
+    filled piecewise).  vmul(positions) scales the value norms per token.  Returns the
+    pools and each sequence's contiguous rows and norms."""
     from turboquant_kv import ops
     tab = _tables(rs, lens, bs, nb, width)
     slots = np.array([tab[i, t // bs] * bs + t % bs for i, n in enumerate(lens) for t in range(n)],
@@ -316,6 +324,9 @@ def _dl_pools(rs, lens, bs, nb, width, Hkv, vb=2):
     vrows = rs.randint(0, 256, (n, Hkv, 8 * vb)).astype(np.uint8)
     kn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
     vn = rs.uniform(0.5, 2.0, (n, Hkv)).astype(np.float32)
+    if vmul is not None:
+        pos = np.concatenate([np.arange(L_) for L_ in lens])
+        vn = (vn * vmul(pos)[:, None]).astype(np.float32)
     kp = torch.zeros(nb, Hkv, bs, 32, dtype=torch.uint8, device=DEV)
     knp = torch.zeros(nb, Hkv, bs, dtype=torch.float32, device=DEV)
     vt = (torch.zeros(nb, Hkv, bs // 64, 512 * vb, dtype=torch.uint8, device=DEV) if bs >= 64 else

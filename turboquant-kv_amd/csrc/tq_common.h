@@ -113,6 +113,54 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// fp16 hi + lo parts of x (hi + lo = x to about 2^-22).  x is pinned as an fp32 value
+// first: when x is a product, the compiler may otherwise fold the multiply into each
+// conversion separately (one part rounded once from the exact product, the other via its
+// fp32 rounding), and in the rare case where the two roundings differ the parts describe
+// numbers one fp16 ulp apart.
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+  asm("" : "+v"(x));
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+
+// ---------------------------------------------------------------- value-norm scale
+// The attention kernels hand the weights p |v| (p <= 1: softmax weights against the
+// running maximum) to the matrix cores as fp16, whose range (2^-24 .. 65504) is far
+// narrower than the norms' fp32.  A wave keeps a power of two S = 2^e such that every
+// |v| S it has seen is at most 2^14, so the weights stay finite for any finite norm and
+// keep fp16's full precision for small ones.  A tile that breaks the bound lowers e (the
+// accumulators are rescaled by 2^(e' - e), exactly) and the wave's result is multiplied
+// by 2^-e at the end.  Scaling by a power of two commutes with rounding, so weights that
+// were normal fp16 numbers without it give the same bits with it.  Wave-uniform.
+struct VnScale {
+  static constexpr float kBound = 16384.f;  // |v| S at most 2^14
+  int e = 126;  // the first tile with a norm above 2^-112 sets it
+  float s = 0x1p126f;
+  // vmax: this lane's largest |v| over the tile's live tokens (0 for none)
+  __device__ __forceinline__ bool needs(float vmax) const { return __any(vmax * s > kBound); }
+  // the same test on this lane's largest |v| S
+  __device__ __forceinline__ bool over(float vsmax) const { return __any(vsmax > kBound); }
+  // Lowers e so that the wave's largest |v| lands in [2^13, 2^14); returns the factor for
+  // the accumulators.  vmax as above, on every lane.
+  __device__ __forceinline__ float rescale(float vmax) {
+    const float wm = wave_max(vmax);
+    const int en = __builtin_amdgcn_readfirstlane(14 - __builtin_amdgcn_frexp_expf(wm));
+    const float f = __builtin_amdgcn_ldexpf(1.f, en - e);
+    e = en;
+    s = __builtin_amdgcn_ldexpf(1.f, en);
+    return f;
+  }
+  __device__ __forceinline__ float inv() const { return __builtin_amdgcn_ldexpf(1.f, -e); }
+  // Sets e so that the wave's largest |v| (vmax on every lane) lands in
+  // [2^(top-1), 2^top) (e at most 126: a wave of zero norms keeps 2^top).
+  __device__ __forceinline__ void fit(float vmax, int top) {
+    const float wm = wave_max(vmax);
+    e = min(126, __builtin_amdgcn_readfirstlane(top - __builtin_amdgcn_frexp_expf(wm)));
+    s = __builtin_amdgcn_ldexpf(1.f, e);
+  }
+};
+
 // #{ bnd[i] < y } for sorted bnd of length 2^bits - 1 (torch.searchsorted, right=False).
 __device__ __forceinline__ int count_below(const float* bnd, int nlev, float y) {
   int lo = 0;

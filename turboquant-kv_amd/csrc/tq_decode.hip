@@ -274,6 +274,7 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
 
   float M = -INFINITY;  // running max of this lane's head (same in all lanes of the head)
   float l = 0.f;        // this lane's share of sum 2^(s - M)
+  tq::VnScale vs;       // value norms scaled into fp16 range
   v4f acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
@@ -328,15 +329,25 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       s[r] = skk[r] * cur.kn[r];
-      vn[r] = cur.vn[r];
+      // contiguous caches: norms past t_end read as zero; paged pools: a stale norm (even
+      // NaN) is masked with a select, not a branch (a masked copy of the norms merged
+      // from a branch has been miscompiled: registers of the live norms reused before
+      // their last read)
+      vn[r] = (!PAGED || t0 + 4 * quad + r < te) ? cur.vn[r] : 0.f;
     }
     if (t0 + 64 > te) {
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (t0 + 4 * quad + r >= te) { s[r] = -INFINITY; vn[r] = 0.f; }
+        if (t0 + 4 * quad + r >= te) s[r] = -INFINITY;
     }
     const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    if (__any(lm > M)) {
+    // value norms times the wave's scale (masked tokens 0: a stale pool norm may be NaN)
+    float vns[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vns[r] = vn[r] * vs.s;
+    const float vm = fmaxf(fmaxf(fabsf(vns[0]), fabsf(vns[1])), fmaxf(fabsf(vns[2]), fabsf(vns[3])));
+    // one branch for both rare events: a running maximum moved, the value scale must drop
+    if (__any((lm > M) | (vm > tq::VnScale::kBound))) {
       float m2 = lm;
       m2 = fmaxf(m2, __shfl_xor(m2, 4));
       m2 = fmaxf(m2, __shfl_xor(m2, 8));
@@ -345,7 +356,13 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
       const float mn = fmaxf(M, m2);
       const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
       l *= f;
-      const v4f fv = {__shfl(f, 0), __shfl(f, 1), __shfl(f, 2), __shfl(f, 3)};
+      float fs = 1.f;  // the value scale's factor
+      if (vs.over(vm)) {
+        fs = vs.rescale(fmaxf(fmaxf(fabsf(vn[0]), fabsf(vn[1])), fmaxf(fabsf(vn[2]), fabsf(vn[3]))));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vns[r] = vn[r] * vs.s;
+      }
+      const v4f fv = {__shfl(f, 0) * fs, __shfl(f, 1) * fs, __shfl(f, 2) * fs, __shfl(f, 3) * fs};
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] *= fv;
       M = mn;
@@ -356,7 +373,7 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
     for (int r = 0; r < 4; ++r) {
       const float p = __builtin_amdgcn_exp2f(s[r] - M);
       psum += p;
-      wa[r] = (_Float16)(p * cur.vn[r]);
+      wa[r] = (_Float16)(p * vns[r]);
     }
     l += psum;
     tq::mfma_operand_fence(wa);  // VALU conversions -> MFMA operand: explicit wait states
@@ -402,7 +419,8 @@ __global__ __launch_bounds__(kDecThreads, 2) void fused_decode_kernel(DecodeArgs
   for (int m = 0; m < 4; ++m) {
     mx[m] = fmaxf(fmaxf(red_m[0][m], red_m[1][m]), fmaxf(red_m[2][m], red_m[3][m]));
     const float mw = red_m[wave][m];
-    fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]);
+    // this wave's share in true scale: its value-norm scale divided out
+    fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]) * vs.inv();
   }
   float* red = reinterpret_cast<float*>(tabs);  // [wave*16 + quad][i][j][m]
   const v4f fwv = {fw[0], fw[1], fw[2], fw[3]};
@@ -1120,6 +1138,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   };
 
   float M = -INFINITY, l = 0.f;
+  tq::VnScale vs;  // value norms scaled into fp16 range
   // half h, dim group dg: lanes 0-15 hold heads 0-3 (registers), dim 64 h + 16 dg + lane
   v4f acc[NH][4];
 #pragma unroll
@@ -1224,7 +1243,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[r] = ((r < nvalid) & (r >= nlow)) ? skk[r] * cur.kn[r] : -INFINITY;
     const float lm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    if (__any(lm > M)) {
+    // the live tokens' value norms times the wave's scale (masked ones 0)
+    float vns[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vns[r] = ((r < nvalid) & (r >= nlow)) ? cur.vn[r] * vs.s : 0.f;
+    const float vm = fmaxf(fmaxf(fabsf(vns[0]), fabsf(vns[1])), fmaxf(fabsf(vns[2]), fabsf(vns[3])));
+    // one branch for both rare events: a running maximum moved, the value scale must drop
+    if (__any((lm > M) | (vm > tq::VnScale::kBound))) {
       float m2 = lm;
       m2 = fmaxf(m2, __shfl_xor(m2, 4));
       m2 = fmaxf(m2, __shfl_xor(m2, 8));
@@ -1233,22 +1258,39 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
       const float mn = fmaxf(M, m2);
       const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mn);
       l *= f;
-      const v4f fv = {__shfl(f, 0), __shfl(f, 1), __shfl(f, 2), __shfl(f, 3)};
+      float fs = 1.f;  // the value scale's factor
+      if (vs.over(vm)) {
+        float um = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) um = fmaxf(um, ((r < nvalid) & (r >= nlow)) ? fabsf(cur.vn[r]) : 0.f);
+        fs = vs.rescale(um);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vns[r] = ((r < nvalid) & (r >= nlow)) ? cur.vn[r] * vs.s : 0.f;
+      }
+      const v4f fv = {__shfl(f, 0) * fs, __shfl(f, 1) * fs, __shfl(f, 2) * fs, __shfl(f, 3) * fs};
 #pragma unroll
       for (int h = 0; h < NH; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[h][i] *= fv;
       M = mn;
     }
+    // masked tokens: s = -inf, p = 0 (M clamped: M is -inf while every token so far was masked)
+    const float Mp = fmaxf(M, -0x1.fffffep127f);
     v4h wh, wl;
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float p = __builtin_amdgcn_exp2f(s[r] - M);
+      const float p = __builtin_amdgcn_exp2f(s[r] - Mp);
       psum += p;
-      const float w = ((r < nvalid) & (r >= nlow)) ? p * cur.vn[r] : 0.f;
-      wh[r] = (_Float16)w;
-      if constexpr (EXACT_V) wl[r] = (_Float16)(w - (float)wh[r]);
+      const float w = p * vns[r];
+      if constexpr (EXACT_V) {
+        _Float16 h, lo;
+        tq::split_f16(w, h, lo);
+        wh[r] = h;
+        wl[r] = lo;
+      } else {
+        wh[r] = (_Float16)w;
+      }
     }
     l += psum;
     // The weights are written by VALU conversions and read by the MFMAs below as the A
@@ -1374,7 +1416,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     for (int w = 1; w < WPS; ++w) v = fmaxf(v, red_m[w0 + w][m]);
     mx[m] = v;
     const float mw = red_m[wave][m];
-    fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]);
+    // this wave's share in true scale: its value-norm scale divided out
+    fw[m] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx[m]) * vs.inv();
   }
   float* red = reinterpret_cast<float*>(tabs);  // [wave][head m][dim]
   if (lane < 16) {

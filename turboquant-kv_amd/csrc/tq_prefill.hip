@@ -275,13 +275,36 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
   const int64_t bsm = ((int64_t)1 << bsl) - 1;
   float m[NGR], l[NGR];
   pf_v4f o[NGR][4];
+
+  // pool row of token t0 + 16 b (a 16-token group never straddles a block)
+  auto tile_rows = [&](int64_t t0, int64_t* base) {
 #pragma unroll
-  for (int j = 0; j < NGR; ++j) {
-    m[j] = -INFINITY;
-    l[j] = 0.f;
+    for (int b = 0; b < 4; ++b) {
+      const int64_t tb = t0 + 16 * b;
+      const int bi = (int)min<int64_t>(tb >> bsl, (int64_t)a.max_blocks - 1);
+      const uint32_t blk = min((uint32_t)a.block_table[bi], a.num_blocks - 1u);
+      base[b] = (((int64_t)blk * hkv + h) << bsl) + (tb & bsm);
+    }
+  };
+  // this lane's largest |v| over tile kt's tokens that some row of the wave sees
+  auto tile_vmax = [&](int kt) -> float {
+    int64_t base[4];
+    tile_rows((int64_t)kt * 64, base);
+    float vm = 0.f;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) o[j][nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
-  }
+    for (int b = 0; b < 4; ++b) {
+      const pf_v4f x = *reinterpret_cast<const pf_v4f*>(a.vnorms + base[b] + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vm = fmaxf(vm, (int64_t)kt * 64 + 16 * b + 4 * g + r < limw ? fabsf(x[r]) : 0.f);
+    }
+    return vm;
+  };
+  // The value-norm scale comes from tile 0 (its largest |v| lands in [2^11, 2^12), so
+  // later norms up to 16 times larger still give finite fp16 weights); a wave whose
+  // accumulators end non-finite runs its tiles again with the scale of all its tiles.
+  tq::VnScale vs;
+  vs.fit(tile_vmax(0), 12);
 
   // Tiles every row of the wave sees whole need no mask (all but the last one or two).
   const int64_t limlo = a.past + row0 / a.G + 1;
@@ -292,15 +315,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
     int rel[NGR];
 #pragma unroll
     for (int j = 0; j < NGR; ++j) rel[j] = MASK ? (int)max<int64_t>(0, min<int64_t>(lim[j] - t0, 64)) : 64;
-    // pool row of token t0 + 16 b (a 16-token group never straddles a block)
     int64_t base[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int64_t tb = t0 + 16 * b;
-      const int bi = (int)min<int64_t>(tb >> bsl, (int64_t)a.max_blocks - 1);
-      const uint32_t blk = min((uint32_t)a.block_table[bi], a.num_blocks - 1u);
-      base[b] = (((int64_t)blk * hkv + h) << bsl) + (tb & bsm);
-    }
+    tile_rows(t0, base);
     uint32_t kw[4][2];
     pf_v4f nk[4], nv[4];
 #pragma unroll
@@ -400,6 +416,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
           sv[j][b][r] = (!MASK || 16 * b + 4 * g + r < rel[j]) ? x : -INFINITY;
         }
     }
+    // value norms times the wave's scale (masked tokens are selected away below)
+    float nvs[4][4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) nvs[b][r] = nv[b][r] * vs.s;
     pf_v8h bh[NGR][2], bl[NGR][2];
 #pragma unroll
     for (int j = 0; j < NGR; ++j) {
@@ -429,10 +451,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
           const float p = __builtin_amdgcn_exp2f(fmaf(sv[j][b][r], kinv[j], -ms));
           l[j] += p;
           // masked tokens' norms may be stale (even NaN): selected away, not multiplied
-          const float v = (!MASK || 16 * b + 4 * g + r < rel[j]) ? p * nv[b][r] : 0.f;
-          const _Float16 hv = (_Float16)v;
-          bh[j][b >> 1][4 * (b & 1) + r] = hv;
-          if constexpr (PREC) bl[j][b >> 1][4 * (b & 1) + r] = (_Float16)(v - (float)hv);
+          const float v = (!MASK || 16 * b + 4 * g + r < rel[j]) ? p * nvs[b][r] : 0.f;
+          if constexpr (PREC) {
+            _Float16 hv, lv;
+            tq::split_f16(v, hv, lv);
+            bh[j][b >> 1][4 * (b & 1) + r] = hv;
+            bl[j][b >> 1][4 * (b & 1) + r] = lv;
+          } else {
+            bh[j][b >> 1][4 * (b & 1) + r] = (_Float16)v;
+          }
         }
     }
 
@@ -487,9 +514,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
       }
     }
   };
-  for (int kt = 0; kt < ntiles; ++kt) {
-    if ((int64_t)kt * 64 + 64 <= limlo) tile(std::false_type{}, kt);
-    else tile(std::true_type{}, kt);
+  for (int pass = 0;; ++pass) {
+#pragma unroll
+    for (int j = 0; j < NGR; ++j) {
+      m[j] = -INFINITY;
+      l[j] = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) o[j][nb] = (pf_v4f){0.f, 0.f, 0.f, 0.f};
+    }
+    for (int kt = 0; kt < ntiles; ++kt) {
+      if ((int64_t)kt * 64 + 64 <= limlo) tile(std::false_type{}, kt);
+      else tile(std::true_type{}, kt);
+    }
+    if (pass == 1) break;
+    bool bad = false;  // an fp16 weight overflowed (or the inputs hold inf / NaN)
+#pragma unroll
+    for (int j = 0; j < NGR; ++j)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= !(fabsf(o[j][nb][r]) <= 0x1.fffffep127f);
+    if (!__any(bad)) break;
+    float vm = 0.f;
+    for (int kt = 0; kt < ntiles; ++kt) vm = fmaxf(vm, tile_vmax(kt));
+    vs.fit(vm, 12);
   }
 
   // ---- out = (O / l) R_v.  o[j][nb][r] of lane (c, g) = O_c[16 nb + 4 g + r]: the B
@@ -508,7 +556,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void dl_prefill_kernel(PfArgs a) {
     float lt = l[j];
     lt += __shfl_xor(lt, 16, 64);
     lt += __shfl_xor(lt, 32, 64);
-    const float inv = lt > 0.f ? 1.f / (lt * vsc) : 0.f;
+    const float inv = lt > 0.f ? 1.f / (lt * vsc) * vs.inv() : 0.f;
     float* dst = a.out + qoff[j];
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) {
