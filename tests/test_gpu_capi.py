@@ -822,6 +822,53 @@ def test_pairs_scan_one_query_past_4gib():
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("bits", [2, 3])
+def test_pair_rows_one_query_past_4gib(bits):
+    # One query over 2-/3-bit pair rows of d = 128 past 2^32 bytes (4.3 GB of codes): rows
+    # there are addressed with 64-bit bases.  Random codes, norm 0 except
+    # 200 planted rows spread over the whole range; the answer is the planted rows with
+    # positive scores (only they go through the oracle), then zero-score rows by lowest id.
+    rs = np.random.RandomState(57 + bits)
+    d = 128
+    rb = d * bits // 8
+    N = (1 << 32) // rb + 1017
+    R = O.dense_qr_rotation(d, 42)
+    _, cen = O.lloyd_max_codebook(bits, d)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7 + bits)
+    rows = torch.randint(0, 256, (N, rb), dtype=torch.uint8, device=DEV, generator=g)
+    norms = torch.zeros(N, dtype=torch.float32, device=DEV)
+    planted = np.sort(rs.choice(np.arange(1000, N), 200, replace=False))
+    planted[-1] = N - 1
+    codes = rs.randint(0, 1 << bits, size=(200, d)).astype(np.uint8)
+    packed = O.pack_codes(codes, bits)
+    pn = (rs.rand(200) * 2 + 0.5).astype(np.float32)
+    it = torch.from_numpy(planted).to(DEV)
+    rows[it] = k_pair_rows(packed, d, bits)
+    norms[it] = torch.from_numpy(pn).to(DEV)
+    q = rs.randn(1, d).astype(np.float32)
+    ps = O.lut_scores_f32(q, packed, pn, cen, R, bits)[0]
+    pos = [(float(ps[j]), int(planted[j])) for j in range(200) if ps[j] > 0]
+    pos.sort(key=lambda t: (-t[0], t[1]))
+    assert len(pos) >= 32
+    print(f"pair rows past 4 GiB: {bits} bits, {N} rows", flush=True)
+    for k in (10, 32):
+        s, i = k_scan_pair_rows(q, rows, norms, cen, R, bits, k)
+        want_i = [t[1] for t in pos][:k]
+        want_s = np.array([t[0] for t in pos][:k], np.float32)
+        assert np.array_equal(i[0], np.array(want_i)), k
+        assert np.array_equal(s[0].view(np.uint32), want_s.view(np.uint32)), k
+    keep3 = {t[1] for t in pos[:3]}
+    drop = [int(planted[j]) for j in range(200) if ps[j] > 0 and int(planted[j]) not in keep3]
+    norms[torch.tensor(drop, device=DEV)] = 0.0
+    s, i = k_scan_pair_rows(q, rows, norms, cen, R, bits, 10)
+    zero_ids = [j for j in range(64) if j not in set(planted.tolist())]
+    assert np.array_equal(i[0], np.array([t[1] for t in pos[:3]] + zero_ids[:7]))
+    assert (s[0, 3:] == 0).all()
+    del rows, norms
+    torch.cuda.empty_cache()
+
+
 # ------------------------------------------------------------------ multi-query filtered scan
 def _cpu_search(q, p, nm, cen, R, k):
     """The C restatement of the reference core's search (oracle/tq_cpu.c, OpenMP) over
@@ -2008,7 +2055,7 @@ def test_prod_pair_rows_equal_bitplane_prod_scan(d, b):
     assert torch.equal(a0.view(torch.int32), a1.view(torch.int32))
 
 
-@pytest.mark.parametrize("bits,d", [(3, 128), (2, 128), (2, 64)])
+@pytest.mark.parametrize("bits,d", [(3, 128), (3, 64), (2, 128), (2, 64)])
 def test_pair_rows_one_query_filter_cases(bits, d):
     """One query over 2-/3-bit pair rows: ids and scores equal the oracle's bit for bit on
     ragged N, fp16 unit queries, duplicated best rows (exact ties), special norms (zero,
