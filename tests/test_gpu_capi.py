@@ -275,6 +275,47 @@ def test_quantize_zero_tiny_and_empty_rows():
     k_quantize(T(np.zeros((0, d), np.float32)), R, bnd, b)  # no launch, no error
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_quantize_unaligned_outputs_equal_aligned(d):
+    # Outputs aligned to whole bit planes take one 16-byte (d 64: 8-byte) store per plane
+    # through LDS; outputs at other offsets take 2-byte stores.  Both give the same bytes
+    # (MSE codes, prod codes and sign bits), on a ragged row count (a partial last tile).
+    rs = np.random.RandomState(90 + d)
+    n = 1000 + 37
+    x = rs.randn(n, d).astype(np.float32)
+    R = O.dense_qr_rotation(d, 42)
+    S = O.qjl_matrix(d, d, 43)
+    bpp = d // 8
+    for bits in (2, 3, 4):
+        bnd, _ = O.lloyd_max_codebook(bits, d)
+        want, wn = k_quantize(T(x), R, bnd, bits)
+        buf = torch.zeros(n * bits * bpp + 16, dtype=torch.uint8, device=DEV)
+        out = buf[2:2 + n * bits * bpp]
+        norms = torch.empty(n, dtype=torch.float32, device=DEV)
+        capi.check(L().tq_rotate_and_quantize(capi.p(T(x)), capi.TQ_F32, capi.TQ_F32, capi.i64(n),
+                                              capi.i32(d), capi.p(T(R)), capi.p(T(bnd)), capi.i32(bits),
+                                              capi.p(out), capi.p(norms), capi.stream()))
+        sync()
+        assert np.array_equal(out.cpu().numpy().reshape(n, -1), want), bits
+        assert np.array_equal(norms.cpu().numpy(), wn), bits
+    for bits in (3, 4):
+        bnd, cen = O.lloyd_max_codebook(bits - 1, d)
+        mp, sg, rn, nm = k_prod(x, R, bnd, cen, S, bits)
+        b1 = torch.zeros(n * (bits - 1) * bpp + 16, dtype=torch.uint8, device=DEV)
+        b2 = torch.zeros(n * bpp + 16, dtype=torch.uint8, device=DEV)
+        mpo, sgo = b1[2:2 + n * (bits - 1) * bpp], b2[6:6 + n * bpp]
+        rno = torch.empty(n, dtype=torch.float32, device=DEV)
+        nmo = torch.empty(n, dtype=torch.float32, device=DEV)
+        capi.check(L().tq_quantize_prod(capi.p(T(x)), capi.TQ_F32, capi.TQ_F32, capi.i64(n), capi.i32(d),
+                                        capi.p(T(R)), capi.p(T(bnd)), capi.p(T(cen)), capi.p(T(S)),
+                                        capi.i32(bits), capi.p(mpo), capi.p(sgo), capi.p(rno), capi.p(nmo),
+                                        capi.stream()))
+        sync()
+        assert np.array_equal(mpo.cpu().numpy().reshape(n, -1), mp), bits
+        assert np.array_equal(sgo.cpu().numpy().reshape(n, -1), sg), bits
+        assert np.array_equal(rno.cpu().numpy(), rn) and np.array_equal(nmo.cpu().numpy(), nm), bits
+
+
 def test_quantize_prod_vs_reference(golden):
     pr, rot, qj = golden("quant_prod"), golden("rotation"), golden("qjl")
     for name, d in (("d128", 128), ("d200", 200)):

@@ -470,10 +470,34 @@ __global__ __launch_bounds__(qm_threads<D>()) void quantize_mfma_kernel(QuantArg
       }
     }
   };
-  // Bit planes of this thread's 16 codes in cs, stored for row r0 + trow.
+  // Bit planes of row r0 + trow's codes in cs, stored to `out`.  Whole planes (an output
+  // aligned to them): each thread's 16-bit share of every plane goes over the row's own
+  // codes in LDS (only the row's threads read those, all from one wave, and each holds
+  // its codes in registers by then), and the threads part < bits copy plane `part` out
+  // with one 16-byte (D 64: 8-byte) store.  Otherwise 2-byte stores (RELOAD: bytes).
   auto pack_cs = [&](int rows, int64_t r0, int bits, uint8_t* __restrict__ out) {
     const uint4 c = *reinterpret_cast<const uint4*>(&cs[trow * D + 16 * part]);
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    if constexpr (!RELOAD) {
+      if ((reinterpret_cast<uintptr_t>(out) & (BPP - 1)) == 0) {
+        uint8_t* srow = &cs[trow * D];  // bits * BPP <= D bytes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        for (int p = 0; p < bits; ++p)
+          *reinterpret_cast<uint16_t*>(srow + p * BPP + 2 * part) = (uint16_t)qm_plane16(w, p);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (trow < rows && part < bits) {
+          uint8_t* dst = out + (r0 + trow) * (int64_t)(bits * BPP) + part * BPP;
+          if constexpr (D == 128) {
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(srow + part * BPP);
+          } else {
+            *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(srow + part * BPP);
+          }
+        }
+        return;
+      }
+    }
     if (trow < rows) {
       if constexpr (RELOAD) {  // odd plane widths: byte stores, dims below d only
         const int bpp = (d + 7) >> 3;
