@@ -129,20 +129,20 @@ __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
 // running maximum) to the matrix cores as fp16, whose range (2^-24 .. 65504) is far
 // narrower than the norms' fp32.  A wave keeps a power of two S = 2^e such that every
 // |v| S it has seen is at most 2^14, so the weights stay finite for any finite norm and
-// keep fp16's full precision for small ones.  A tile that breaks the bound lowers e (the
-// accumulators are rescaled by 2^(e' - e), exactly) and the wave's result is multiplied
-// by 2^-e at the end.  Scaling by a power of two commutes with rounding, so weights that
-// were normal fp16 numbers without it give the same bits with it.  Wave-uniform.
+// keep fp16's full precision for small ones.  Decode: a tile that breaks the bound lowers
+// e (the accumulators are rescaled by 2^(e' - e), exactly); prefill: e comes from the
+// wave's first tile (fit) and a wave that overflows runs again with the scale of all its
+// tiles.  The wave's result is multiplied by 2^-e at the end.  Scaling by a power of two
+// commutes with rounding, so weights that were normal fp16 numbers without it give the
+// same bits with it.  Wave-uniform.
 struct VnScale {
   static constexpr float kBound = 16384.f;  // |v| S at most 2^14
   int e = 126;  // the first tile with a norm above 2^-112 sets it
   float s = 0x1p126f;
-  // vmax: this lane's largest |v| over the tile's live tokens (0 for none)
-  __device__ __forceinline__ bool needs(float vmax) const { return __any(vmax * s > kBound); }
-  // the same test on this lane's largest |v| S
+  // vsmax: this lane's largest |v| S over the tile's live tokens (0 for none)
   __device__ __forceinline__ bool over(float vsmax) const { return __any(vsmax > kBound); }
   // Lowers e so that the wave's largest |v| lands in [2^13, 2^14); returns the factor for
-  // the accumulators.  vmax as above, on every lane.
+  // the accumulators.  vmax: this lane's largest |v| over the tile's live tokens.
   __device__ __forceinline__ float rescale(float vmax) {
     const float wm = wave_max(vmax);
     const int en = __builtin_amdgcn_readfirstlane(14 - __builtin_amdgcn_frexp_expf(wm));
