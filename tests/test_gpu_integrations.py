@@ -285,3 +285,32 @@ def test_decode_merge_token_vs_float64(dt, kvdt):
     err = (out.double() - want).abs().max().item()
     assert err <= tol * want.abs().max().item(), err
     assert torch.allclose(out[0, 1].double(), vd[0, 1], rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_decode_attention_dl_merged_equals_two_ops(dt):
+    """decode_attention_dl_merged (the HF decode step's one op) equals
+    decode_attention_dl_lse followed by decode_merge_token bit for bit, with and without
+    window starts."""
+    from turboquant_kv._lib import ops
+    rs = np.random.RandomState(8)
+    g = torch.Generator(device="cuda").manual_seed(8)
+    B, Hq, Hkv, d, Tc, vb, scale = 3, 8, 2, 64, 256, 3, 0.125
+    kp = torch.randint(0, 256, (B, Hkv, Tc, d // 2), dtype=torch.uint8, device="cuda", generator=g)
+    vp = torch.randint(0, 256, (B, Hkv, Tc // 64, 8 * vb * d), dtype=torch.uint8, device="cuda",
+                       generator=g)
+    kn = torch.rand(B, Hkv, Tc, device="cuda", generator=g) + 0.5
+    vn = torch.rand(B, Hkv, Tc, device="cuda", generator=g) + 0.5
+    R = torch.from_numpy(O.dense_qr_rotation(d, 42)).cuda()
+    _, kc = O.lloyd_max_codebook(4, d)
+    _, vc = O.lloyd_max_codebook(vb, d)
+    kc, vc = torch.from_numpy(kc).cuda(), torch.from_numpy(vc).cuda()
+    seq = torch.tensor([200, 1, 256], dtype=torch.int32, device="cuda")
+    q = torch.randn(B, Hq, d, generator=g, device="cuda").to(dt)
+    kv_new = [torch.randn(B, Hkv, d, generator=g, device="cuda").to(dt) for _ in range(2)]
+    for starts in (None, torch.tensor([3, 0, 70], dtype=torch.int32, device="cuda")):
+        o, lse = ops().decode_attention_dl_lse(q, kp, kn, vp, vn, seq, kc, vc, R, R, scale, starts)
+        want = ops().decode_merge_token(o, lse, q, kv_new[0], kv_new[1], scale)
+        got = ops().decode_attention_dl_merged(q, kp, kn, vp, vn, seq, kc, vc, R, R, scale, starts,
+                                               kv_new[0], kv_new[1])
+        assert got.dtype == want.dtype and torch.equal(got, want)

@@ -1218,6 +1218,20 @@ at::Tensor decode_merge_token(const at::Tensor& o, const at::Tensor& lse, const 
   return out;
 }
 
+// One decode step of a decode-layout cache in one op: attention over the cached history
+// (decode_attention_dl_lse) merged with the token being decoded, which attends to its own
+// exact key and value (decode_merge_token) -- the same two launches, one dispatch.
+at::Tensor decode_attention_dl_merged(
+    const at::Tensor& q, const at::Tensor& kpairs, const at::Tensor& knorms,
+    const at::Tensor& vblocks, const at::Tensor& vnorms, const at::Tensor& seq_lens,
+    const at::Tensor& kcentroids, const at::Tensor& vcentroids, const at::Tensor& krotation,
+    const at::Tensor& vrotation, double scale, const c10::optional<at::Tensor>& seq_starts,
+    const at::Tensor& k_new, const at::Tensor& v_new) {
+  auto ol = decode_attention_dl_lse(q, kpairs, knorms, vblocks, vnorms, seq_lens, kcentroids,
+                                    vcentroids, krotation, vrotation, scale, seq_starts);
+  return decode_merge_token(std::get<0>(ol), std::get<1>(ol), q, k_new, v_new, scale);
+}
+
 }  // namespace
 
 TORCH_LIBRARY(turboquant, m) {
@@ -1296,6 +1310,10 @@ TORCH_LIBRARY(turboquant, m) {
         " -> (Tensor, Tensor)");
   m.def("decode_merge_token(Tensor o, Tensor lse, Tensor q, Tensor k_new, Tensor v_new,"
         " float scale) -> Tensor");
+  m.def("decode_attention_dl_merged(Tensor q, Tensor kpairs, Tensor knorms, Tensor vblocks,"
+        " Tensor vnorms, Tensor seq_lens, Tensor kcentroids, Tensor vcentroids,"
+        " Tensor krotation, Tensor vrotation, float scale, Tensor? seq_starts, Tensor k_new,"
+        " Tensor v_new) -> Tensor");
   m.def("cache_append_dl(Tensor key, Tensor value, Tensor(a!) kp, Tensor(b!) kn, Tensor(c!) vp,"
         " Tensor(d!) vn, int pos, Tensor krotation, Tensor kboundaries, Tensor vrotation,"
         " Tensor vboundaries, int kbits, int vbits) -> ()");
@@ -1345,5 +1363,6 @@ TORCH_LIBRARY_IMPL(turboquant, CUDA, m) {
   m.impl("decode_attention_dl", &decode_attention_dl);
   m.impl("decode_attention_dl_lse", &decode_attention_dl_lse);
   m.impl("decode_merge_token", &decode_merge_token);
+  m.impl("decode_attention_dl_merged", &decode_attention_dl_merged);
   m.impl("cache_append_dl", &cache_append_dl);
 }

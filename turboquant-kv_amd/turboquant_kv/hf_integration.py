@@ -371,18 +371,20 @@ def turboquant_attention(module, query, key, value, attention_mask, scaling=None
             and not layer.kq.prod:
         q = query[:, :, 0, :]
         seq = _history_lengths(B, t_hist, query.device)
+        # the token being decoded attends to its own exact key and value: merged with the
+        # history by log-sum-exp in one kernel (the eager composition of
+        # hf_integration.py:372-390); the decode layout takes both in one op
         if layer.dl:
-            o_h, lse_h = _ops().decode_attention_dl_lse(
+            out = _ops().decode_attention_dl_merged(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
-                layer.kq.R, layer.vq.R, float(scaling), starts)
+                layer.kq.R, layer.vq.R, float(scaling), starts, k_new[:, :, 0, :],
+                value[:, :, 0, :])
         else:
             o_h, lse_h = _ops().decode_attention_packed_lse(
                 q, layer.kp, layer.kn, layer.vp, layer.vn, seq, layer.kq.cen, layer.vq.cen,
                 layer.kq.R, layer.vq.R, layer.kq.bits, layer.vq.bits, float(scaling))
-        # the token being decoded attends to its own exact key and value: merged by
-        # log-sum-exp in one kernel (the eager composition of hf_integration.py:372-390)
-        out = _ops().decode_merge_token(o_h, lse_h, q, k_new[:, :, 0, :], value[:, :, 0, :],
-                                        float(scaling))
+            out = _ops().decode_merge_token(o_h, lse_h, q, k_new[:, :, 0, :], value[:, :, 0, :],
+                                            float(scaling))
         return out.to(query.dtype).unsqueeze(1), None
     k_old, v_old = layer.dequantized(upto=t_hist)
     k_all = torch.cat([k_old, k_new.to(k_old.dtype)], dim=-2)
