@@ -1363,7 +1363,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
   // Head_dim 64: whole groups of three tiles, then the last one or two (in ta, tb).  The
   // loop has no exit inside a group: an exit there joins the back edge, and every
   // iteration then starts by waiting for all loads in flight, the lookahead tile's
-  // included.  (Head_dim 128 keeps the exits: two more copies of its tile code spill.)
+  // included.  (Head_dim 128 keeps the exits: two more copies of its tile code spill.
+  // With 3- and 4-bit values its three buffers spill too (9 / 28 VGPRs): those take two
+  // buffers, one tile ahead -- a 128-dim tile carries twice the bytes of a 64-dim one, and
+  // K4/V3 at T = 32K measured 176-177 against 181-182 us; 2-bit values keep three, 155-156
+  // against 157-158 us.)
   if constexpr (NH == 1) {
     int it = 0;
     for (; it + 3 <= ntiles; it += 3) {
@@ -1380,6 +1384,15 @@ __global__ __launch_bounds__(kDlThreads, 1) void dl_decode_kernel(DlArgs a) {
     }
     if (it < ntiles) process(ta, tf + it * kStep);
     if (it + 1 < ntiles) process(tb, tf + (it + 1) * kStep);
+  } else if constexpr (VB != 2) {
+    for (int it = 0; it < ntiles; it += 2) {
+      const int t = tf + it * kStep;
+      process(ta, t);
+      if (it + 1 >= ntiles) break;
+      load_tile(t + 2 * kStep, ta, bnx);
+      process(tb, t + kStep);
+      load_tile(t + 3 * kStep, tb, bnx);
+    }
   } else {
     for (int it = 0; it < ntiles; it += 3) {
       const int t = tf + it * kStep;
