@@ -1600,31 +1600,31 @@ __device__ __forceinline__ float exact_pair_score(const uint8_t* __restrict__ ro
   return acc * n;
 }
 
-// The same score with every table read of a 32-dim chunk issued before the chunk's
-// dependent adds (for the block end; the in-loop rescoring keeps exact_pair_score's
-// smaller register footprint).
+// exact_pair_score from a product table: ptab[16 j + i] = qr[j] * cen[i] (the same fp32
+// products), so each dim costs one table read (the row's nibbles pre-shifted to byte
+// offsets, the dim's 64-byte stride in the read's immediate offset) and the add, in the
+// same order.  `row` and `ptab` in LDS, `row` 16-byte aligned.
 template <int D>
-__device__ __forceinline__ float exact_pair_score_pipelined(const uint32_t* row, float n,
-                                                            const float* qr, const float* cen) {
+__device__ __forceinline__ float exact_pair_score_ptab(const uint32_t* row, float n,
+                                                       const float* ptab) {
 #pragma clang fp contract(off)
+  const char* pt = reinterpret_cast<const char*>(ptab);
   float acc = 0.f;
-#pragma unroll 1
+#pragma unroll
   for (int c = 0; c < D / 32; ++c) {
-    float p[32];
     const u32x4 v = reinterpret_cast<const u32x4*>(row)[c];
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi) {
+      const uint32_t h4 = (w[wi] >> 2) & 0x3C3C3C3Cu;  // byte b: 4 * (high nibble)
+      const uint32_t l4 = (w[wi] << 2) & 0x3C3C3C3Cu;  // byte b: 4 * (low nibble)
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int pl = 4 * wi + b, pg = 16 * c + pl;
-        const uint32_t byte = (w[wi] >> (8 * b)) & 0xFFu;
-        p[2 * pl] = qr[2 * pg] * cen[byte >> 4];
-        p[2 * pl + 1] = qr[2 * pg + 1] * cen[byte & 15u];
+        const int pg = 16 * c + 4 * wi + b;
+        acc = acc + *reinterpret_cast<const float*>(pt + 128 * pg + ((h4 >> (8 * b)) & 0xFFu));
+        acc = acc + *reinterpret_cast<const float*>(pt + 128 * pg + 64 + ((l4 >> (8 * b)) & 0xFFu));
       }
     }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) acc = acc + p[j];
   }
   return acc * n;
 }
@@ -2465,6 +2465,10 @@ pair_filter_kernel(FilterArgs a) {
   float* cs = reinterpret_cast<float*>(htab + 4 * kFsWaves * kFsCap);        // exact scores
   int* ci = reinterpret_cast<int*>(htab + 8 * kFsWaves * kFsCap);            // ids (INT_MAX: NaN)
   int* rk = reinterpret_cast<int*>(htab + 12 * kFsWaves * kFsCap);           // ranks
+  // exact products for the rescoring: ptab[16 j + i] = qr[j] * cen[i] (D x 16 floats)
+  float* ptab = reinterpret_cast<float*>(htab + 16 * kFsWaves * kFsCap);
+  static_assert(16 * kFsWaves * kFsCap + D * 16 * 4 <= kHtabBytes, "product table fits");
+  for (int e = tid; e < D * 16; e += kFsThreads) ptab[e] = qr_s[e >> 4] * cen_s[e & 15];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {  // one LDS atomic per wave and half
     const int e = lane + 64 * r;
@@ -2481,7 +2485,7 @@ pair_filter_kernel(FilterArgs a) {
   const int m = ncand_s;
   for (int t = tid; t < m; t += kFsThreads) {
     const int sl = cslot[t];
-    const float x = exact_pair_score_pipelined<D>(rw_s + sl * RW, nr_s[sl], qr_s, cen_s);
+    const float x = exact_pair_score_ptab<D>(rw_s + sl * RW, nr_s[sl], ptab);
     const bool ok = !__builtin_isnan(x);
     cs[t] = ok ? x : -INFINITY;
     ci[t] = ok ? id_s[sl] : INT_MAX;  // (-inf, INT_MAX) ranks below every listed row
