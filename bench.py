@@ -42,7 +42,7 @@ PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms (BASELINE.md
 # HBM bytes per launch of pair_filter_kernel<128,false> on the headline workload, from
 # rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a copy kernel's readings (FETCH x2.0,
 # WRITE x1.0); commands and raw counts in profiles/pair_filter_kernel_b4_q1_N10M_d128.md.
-SCAN_TRAFFIC_BYTES = 680.9e6
+SCAN_TRAFFIC_BYTES = 681.0e6
 
 
 def log(msg):
