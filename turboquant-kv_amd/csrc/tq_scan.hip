@@ -1814,6 +1814,61 @@ __device__ __forceinline__ int rank1(const float* s, const int* id, int n, float
   return r0;
 }
 
+// The entries of (cs, ci)[0, m) that can be among the k best, ranked among themselves (ci
+// == INT_MAX: no entry).  When more than S = max(64, 2k rounded up to 64) are given, the
+// first S -- in no particular order of score -- are ranked among themselves first, and only
+// the entries reaching their k-th best (k distinct entries do, so every entry of the answer
+// does; about k m / S of them) move to the front and are ranked: S^2 + (k m / S)^2
+// comparisons instead of m^2.  Returns the number of entries ranked (the front of cs / ci);
+// rk[c] = the rank of entry c among them.  cs / ci are padded with (-inf, INT_MAX) from m
+// up to m rounded to 4 and have room for that; EPT >= capacity / NT.  shf: one float,
+// shi: two ints of LDS.  Every thread of the block calls it; it ends with a barrier.
+template <int NT, int EPT>
+__device__ __forceinline__ int rank_best(float* cs, int* ci, int m, int k, int* rk, int tid,
+                                         float* shf, int* shi) {
+  const int S = min(m, max(64, (2 * k + 63) & ~63));
+  int mr = m;
+  if (S < m) {  // uniform
+    for (int c = tid; c < S; c += NT) rk[c] = 0;
+    if (tid == 0) { shf[0] = -INFINITY; shi[0] = INT_MAX; shi[1] = 0; }
+    __syncthreads();
+    block_rank<NT>(cs, ci, S, rk, tid);
+    __syncthreads();
+    for (int c = tid; c < S; c += NT)
+      if ((ci[c] != INT_MAX) & (rk[c] == k - 1)) { shf[0] = cs[c]; shi[0] = ci[c]; }
+    __syncthreads();
+    const float ts = shf[0];
+    const int ti = shi[0];
+    if (ti != INT_MAX) {  // uniform: the sample holds k entries
+      float vs[EPT];
+      int vi[EPT];
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {  // every entry is read before any is written
+        const int e = j * NT + tid;
+        const bool kp = (e < m) && (ci[e] != INT_MAX) && !better(ts, ti, cs[e], ci[e]);
+        vs[j] = kp ? cs[e] : 0.f;
+        vi[j] = kp ? ci[e] : INT_MAX;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        if (vi[j] != INT_MAX) {
+          const int p = atomicAdd(&shi[1], 1);
+          cs[p] = vs[j];
+          ci[p] = vi[j];
+        }
+      __syncthreads();
+      mr = shi[1];
+      for (int c = mr + tid; c < ((mr + 3) & ~3); c += NT) { cs[c] = -INFINITY; ci[c] = INT_MAX; }
+    }
+  }
+  for (int c = tid; c < mr; c += NT) rk[c] = 0;
+  __syncthreads();
+  block_rank<NT>(cs, ci, mr, rk, tid);
+  __syncthreads();
+  return mr;
+}
+
 // merge_query for k above kSmallK, where 64 group maxima no longer bound the k-th best.
 // Per query, for all kThreads threads of a block:
 //   1. tau = the k-th largest score among the leading ceil(k / nblocks) entries of every
@@ -2178,7 +2233,8 @@ pair_filter_kernel(FilterArgs a) {
   __shared__ float red_s[2 * kFsWaves];
   __shared__ float th_s[kFsWaves];
   __shared__ int thi_s[kFsWaves];
-  __shared__ int ncand_s, nvalid_s;
+  __shared__ int ncand_s, nvalid_s, rbi_s[2];
+  __shared__ float rbf_s;
   __shared__ __attribute__((aligned(16))) float lo_s[kFsWaves * kFsCap];
   __shared__ float hi_s[kFsWaves * kFsCap];
   __shared__ __attribute__((aligned(16))) int id_s[kFsWaves * kFsCap];
@@ -2493,11 +2549,10 @@ pair_filter_kernel(FilterArgs a) {
     if (ok) atomicAdd(&nvalid_s, 1);
   }
   for (int t = m + tid; t < ((m + 3) & ~3); t += kFsThreads) { cs[t] = -INFINITY; ci[t] = INT_MAX; }
-  __syncthreads();
-  block_rank<kFsThreads>(cs, ci, m, rk, tid);
-  __syncthreads();
+  const int mr = rank_best<kFsThreads, (kFsWaves * kFsCap + kFsThreads - 1) / kFsThreads>(
+      cs, ci, m, a.k, rk, tid, &rbf_s, rbi_s);
   const size_t base = ((size_t)q * gridDim.x + blockIdx.x) * a.k;
-  for (int t = tid; t < m; t += kFsThreads) {
+  for (int t = tid; t < mr; t += kFsThreads) {
     const int id = ci[t], rank = rk[t];
     if ((id != INT_MAX) & (rank < a.k)) { a.bs[base + rank] = cs[t]; a.bi[base + rank] = id; }
   }
@@ -3090,7 +3145,7 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   __shared__ int off_s[kMqThreads + 1];
   __shared__ int part[kMqWaves];
   __shared__ int tcnt[32];
-  __shared__ int bad_s, m2_s, nvalid_s, m3_s, ti_s;
+  __shared__ int bad_s, m2_s, nvalid_s, shi_s[2];
   __shared__ float ts_s;
   __shared__ float qr_s[D];
   __shared__ float cen_s[16];
@@ -3207,52 +3262,8 @@ __global__ __launch_bounds__(kMqThreads) void mq_merge_kernel(MqArgs a) {
   }
   for (int s = m2 + tid; s < ((m2 + 3) & ~3); s += kMqThreads) { ehi[s] = -INFINITY; eid[s] = INT_MAX; }
   int* rk = reinterpret_cast<int*>(elo);
-  // Only entries that can be among the k best are ranked.  T = the k-th best of a sample
-  // (the first S entries, in no particular order of score; S >= 2k) is reached by k
-  // distinct entries, so every entry of the answer reaches it: ranking the sample costs
-  // S^2 comparisons instead of m2^2 (hundreds of survivors took 12-19 us to rank), and
-  // about k m2 / S entries reach T.
-  const int S = min(m2, max(64, (2 * k + 63) & ~63));
-  int m3 = m2;
-  if (S < m2) {  // uniform
-    for (int s = tid; s < S; s += kMqThreads) rk[s] = 0;
-    if (tid == 0) { ts_s = -INFINITY; ti_s = INT_MAX; m3_s = 0; }
-    __syncthreads();
-    block_rank<kMqThreads>(ehi, eid, S, rk, tid);
-    __syncthreads();
-    for (int s = tid; s < S; s += kMqThreads)
-      if ((eid[s] != INT_MAX) & (rk[s] == k - 1)) { ts_s = ehi[s]; ti_s = eid[s]; }
-    __syncthreads();
-    const float ts = ts_s;
-    const int ti = ti_s;
-    if (ti != INT_MAX) {  // uniform: the sample holds k valid entries
-      // the entries not ranked below T move to the front (all read before any is written)
-      float vs[EPT];
-      int vi[EPT];
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) {
-        const int e = j * kMqThreads + tid;
-        const bool kp = (e < m2) && (eid[e] != INT_MAX) && !better(ts, ti, ehi[e], eid[e]);
-        vs[j] = kp ? ehi[e] : 0.f;
-        vi[j] = kp ? eid[e] : INT_MAX;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < EPT; ++j)
-        if (vi[j] != INT_MAX) {
-          const int pp = atomicAdd(&m3_s, 1);
-          ehi[pp] = vs[j];
-          eid[pp] = vi[j];
-        }
-      __syncthreads();
-      m3 = m3_s;
-      for (int s = m3 + tid; s < ((m3 + 3) & ~3); s += kMqThreads) { ehi[s] = -INFINITY; eid[s] = INT_MAX; }
-    }
-  }
-  for (int s = tid; s < m3; s += kMqThreads) rk[s] = 0;
-  __syncthreads();
-  block_rank<kMqThreads>(ehi, eid, m3, rk, tid);
-  __syncthreads();
+  // only the survivors that can be among the k best are ranked
+  const int m3 = rank_best<kMqThreads, EPT>(ehi, eid, m2, k, rk, tid, &ts_s, shi_s);
   float* os = a.out_s + (size_t)q * k;
   int64_t* oi = a.out_i + (size_t)q * k;
   for (int s = tid; s < m3; s += kMqThreads) {
