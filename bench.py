@@ -38,7 +38,7 @@ sys.path.insert(0, os.path.join(ROOT, "turboquant-kv_amd"))
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (vector or MFMA)
 METRIC = "packed-KV decode-attn GB/s (% HBM peak); 10M×d128 4-bit IP scan queries/s"
-PUBLISHED_QPS = 1000.0 / 2.70  # H100 Triton scan, 1 query, 2.70 ms
+PUBLISHED_QPS = 1000.0 / 2.70  # the reference's published H100 Triton scan: 1 query, 2.70 ms
 # HBM bytes per launch of pair_filter_kernel<128,false> on the headline workload, from
 # rocprofv3 FETCH_SIZE + WRITE_SIZE passes scaled by a copy kernel's readings (FETCH x2.0,
 # WRITE x1.0); commands and raw counts in profiles/pair_filter_kernel_b4_q1_N10M_d128.md.
@@ -670,7 +670,7 @@ def bench_e2e(args, extra):
 
 
 def bench_cpu_configs(args, extra):
-    """CPU legs of BASELINE.md section 3 beside the GPU numbers of the same work:
+    """CPU legs (the reference's CPU-runnable configurations) beside the GPU numbers of the same work:
     configs[0] in full -- TurboQuantMSE 4-bit on 65,536 N(0,1) fp32 vectors (torch CPU
     generator, seed 0), d = 128, R = make_rotation_matrix(128, 42), then 256 queries (the
     generator's next draws), k = 10 -- quantized by this repo's C/OpenMP restatement of
@@ -887,7 +887,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(the path is single-GPU; there is no sharded run)", file=sys.stderr)
         sys.exit(2)
     import torch
     from turboquant_kv import _lib

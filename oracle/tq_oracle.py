@@ -220,7 +220,7 @@ def boundary_distance(x, R, bnd):
 
 
 def check_codes(got, want, x, R, bnd, dtype: str = "f32", max_rate: float = 2e-5):
-    """Parity of quantize codes (SURVEY Appendix B.1 policy): codes outside the ambiguity
+    """Parity of quantize codes (the summation-order policy): codes outside the ambiguity
     band must be identical; inside it they may differ, but no more often than `max_rate`
     per coordinate (about 10x the flip rate two fp32 summation orders give near the
     boundaries, ~1-2e-6).  Returns a summary dict; raises AssertionError otherwise."""
